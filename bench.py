@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Benchmark of the dense-contraction hot path on one MI355X.
+
+Headline (the `value`): float16 `mm` 8192x8192x8192 (config C5 "square") in
+TFLOP/s through the C ABI (tvk_gemm), inputs resident in HBM, N(0,1) from a
+fixed seed. One step = one tvk_gemm call over the whole problem. K timed steps
+are bracketed by torch.cuda.synchronize(); the dominant kernel's average
+duration comes from HIP events recorded on the stream the kernel runs on.
+
+Secondary figures (same JSON line, under "extra"): the C2 MLP GEMM chain
+forward+backward step in ms, the C5 skinny 16x4096x14336 GEMM in GB/s with
+B rotated over buffers larger than the 256 MB Infinity Cache, and C1 fp32
+1024^3 mm.
+
+cpu_baseline: the oracle's restatement of the reference SIMD tile
+(oracle/gemm_oracle.c, kind "port") timed on the host cores on a bounded
+sample of the same workload (whole rows of the 8192^3 product).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+PEAK_F16_TFLOPS = 2516.6   # MI355X dense fp16/bf16 MFMA, AMD spec sheet
+PEAK_F32_TFLOPS = 157.3    # MI355X fp32 matrix
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-extra", action="store_true", help="headline only")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return p.parse_args()
+
+
+def timed(fn, steps, warmup, stream):
+    """Runs fn warmup times, then times `steps` calls with events on `stream`.
+
+    Returns (ms per step from events, ms per step from the host clock)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return start.elapsed_time(end) / steps, (t1 - t0) * 1e3 / steps
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} (WORLD_SIZE={world}) is not supported. "
+              "The path shards by splitting N or M across GPUs with no exchange; see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from torchvulkan_amd import _abi
+
+    _abi.load()  # fails loudly when the HIP library is not built
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    props = _abi.DeviceProps()
+    _abi.check(_abi.load().tvk_device_properties(0, props))
+
+    # ---- headline: fp16 8192^3 --------------------------------------------
+    n = 8192
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn((n, n), generator=g).to(torch.float16).to(dev)
+    b = torch.randn((n, n), generator=g).to(torch.float16).to(dev)
+    c = torch.empty((n, n), dtype=torch.float16, device=dev)
+    plan = _abi.gemm_plan(a, b, c)
+    desc = _abi.make_gemm_desc(a, b, c, stream=stream.cuda_stream)
+    lib = _abi.load()
+    import ctypes as C
+    dref = C.byref(desc)
+
+    def step():
+        st = lib.tvk_gemm(dref)
+        if st:
+            _abi.check(st)
+
+    ms, host_ms = timed(step, args.steps, args.warmup, stream)
+    flops = 2.0 * n * n * n
+    tflops = flops / (ms * 1e-3) / 1e12
+    roofline = {
+        "kernel": plan,
+        "bound": "mfma",
+        "achieved": round(tflops, 2),
+        "peak": PEAK_F16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(tflops / PEAK_F16_TFLOPS, 4),
+        "traffic": None,
+        "algorithmic_unit": "2*M*N*K flops per launch",
+        "avg_kernel_ms": round(ms, 5),
+    }
+
+    extra = {}
+    if not args.no_extra:
+        extra = run_extra(torch, _abi, dev, stream, max(5, args.steps // 5), max(2, args.warmup // 2))
+    del a, b, c
+    torch.cuda.empty_cache()
+
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    line = {
+        "metric": "fp16 GEMM TFLOP/s & % MFMA peak; fwd+bwd step ms (MLP/LLM/ResNet shapes)",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "host_ms_per_step": round(host_ms, 5),
+        "pct_mfma_peak": round(100.0 * tflops / PEAK_F16_TFLOPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "C5 square: fp16 mm 8192x8192x8192, N(0,1) seed 0, row-major operands, via tvk_gemm",
+                   "M": n, "N": n, "K": n, "kernel": plan},
+        "device": {"name": props.name.decode(), "arch": props.arch.decode(), "compute_units": props.compute_units,
+                   "clock_mhz": props.clock_khz / 1000.0},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+def run_extra(torch, _abi, dev, stream, steps, warmup):
+    out = {}
+    # ---- C2 MLP chain fwd+bwd (GEMMs only, fp16) ----------------------------
+    dims = [784, 4096, 4096, 4096, 10]
+    g = torch.Generator().manual_seed(1)
+    B = 256
+    xs = [torch.rand((B, dims[0]), generator=g).to(torch.float16).to(dev)]
+    ws, bs = [], []
+    for i in range(4):
+        bound = dims[i] ** -0.5
+        ws.append(((torch.rand((dims[i + 1], dims[i]), generator=g) * 2 - 1) * bound).to(torch.float16).to(dev))
+        bs.append(((torch.rand((dims[i + 1],), generator=g) * 2 - 1) * bound).to(torch.float16).to(dev))
+    for i in range(4):
+        xs.append(torch.empty((B, dims[i + 1]), dtype=torch.float16, device=dev))
+    dys = [torch.randn((B, d), generator=g).to(torch.float16).to(dev) for d in dims[1:]]
+    dxs = [torch.empty((B, d), dtype=torch.float16, device=dev) for d in dims[:-1]]
+    dws = [torch.empty_like(w) for w in ws]
+    s = stream.cuda_stream
+    descs = []
+    for i in range(4):  # forward: x_{i+1} = x_i W_i^T + b_i
+        descs.append(_abi.make_gemm_desc(xs[i], ws[i].t(), xs[i + 1], bias=bs[i], beta=1.0, stream=s))
+    for i in reversed(range(4)):  # backward: dW_i = dY_i^T x_i ; dX_i = dY_i W_i (not for the input layer)
+        descs.append(_abi.make_gemm_desc(dys[i].t(), xs[i], dws[i], stream=s))
+        if i > 0:
+            descs.append(_abi.make_gemm_desc(dys[i], ws[i], dxs[i], stream=s))
+    lib = _abi.load()
+    import ctypes as C
+    refs = [C.byref(d) for d in descs]
+
+    def mlp_step():
+        for r in refs:
+            st = lib.tvk_gemm(r)
+            if st:
+                _abi.check(st)
+
+    ms, _ = timed(mlp_step, steps, warmup, stream)
+    fl = 0
+    for d in descs:
+        fl += 2 * d.M * d.N * d.K
+    out["c2_mlp_gemm_fwd_bwd_ms"] = round(ms, 4)
+    out["c2_mlp_gemm_tflops"] = round(fl / (ms * 1e-3) / 1e12, 2)
+
+    # ---- C5 skinny 16x4096x14336 fp16, B rotated past the Infinity Cache ----
+    M, K, N = 16, 4096, 14336
+    a = torch.randn((M, K), generator=g).to(torch.float16).to(dev)
+    bufs = [torch.randn((K, N), generator=g).to(torch.float16).to(dev) for _ in range(3)]
+    c = torch.empty((M, N), dtype=torch.float16, device=dev)
+    sd = [_abi.make_gemm_desc(a, bb, c, stream=s) for bb in bufs]
+    srefs = [C.byref(d) for d in sd]
+    idx = [0]
+
+    def skinny_step():
+        r = srefs[idx[0] % 3]
+        idx[0] += 1
+        st = lib.tvk_gemm(r)
+        if st:
+            _abi.check(st)
+
+    ms, _ = timed(skinny_step, steps * 3, warmup, stream)
+    byts = 2 * (M * K + K * N + M * N)
+    out["c5_skinny_kernel"] = _abi.gemm_plan(a, bufs[0], c)
+    out["c5_skinny_us"] = round(ms * 1e3, 2)
+    out["c5_skinny_GBps"] = round(byts / (ms * 1e-3) / 1e9, 1)
+    out["c5_skinny_pct_hbm"] = round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)
+    del bufs
+
+    # ---- C1 fp32 1024^3 ----------------------------------------------------
+    a = torch.randn((1024, 1024), generator=g).to(dev)
+    b = torch.randn((1024, 1024), generator=g).to(dev)
+    c = torch.empty((1024, 1024), device=dev)
+    d1 = _abi.make_gemm_desc(a, b, c, stream=s)
+    r1 = C.byref(d1)
+
+    def c1_step():
+        st = lib.tvk_gemm(r1)
+        if st:
+            _abi.check(st)
+
+    ms, _ = timed(c1_step, steps, warmup, stream)
+    out["c1_fp32_mm_1024_us"] = round(ms * 1e3, 2)
+    out["c1_fp32_tflops"] = round(2 * 1024 ** 3 / (ms * 1e-3) / 1e12, 2)
+    out["c1_kernel"] = _abi.gemm_plan(a, b, c)
+    return out
+
+
+def cpu_baseline():
+    """Times the oracle (the reference SIMD tile's algorithm restated in C) on
+    a bounded sample of the headline workload: 32 whole rows of the fp16
+    8192^3 product, on the host's cores."""
+    import numpy as np
+    from oracle import oracle as orc
+
+    orc.load()
+    n, rows = 8192, 32
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((rows, n)).astype(np.float16).view(np.uint16)
+    b = rng.standard_normal((n, n)).astype(np.float16).view(np.uint16)
+    threads = max(1, min(16, os.cpu_count() or 1))
+    t0 = time.perf_counter()
+    orc.gemm(a, b, orc.F16, threads=threads)
+    dt = time.perf_counter() - t0
+    tfl = 2.0 * rows * n * n / dt / 1e12
+    return {
+        "value": round(tfl, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{rows} of 8192 rows of the fp16 8192^3 mm (oracle/gemm_oracle.c, sequential-k fp32 FMA), {dt:.2f} s",
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,171 @@
+/*
+ * tvk_hip.h - the C ABI of the MI355X (gfx950) dense-contraction library.
+ *
+ * This is the thin boundary that replaces, for the dense-contraction path only,
+ * the reference's Vulkan runtime layer (device/queue setup, VMA memory, shader
+ * manager and autotuner under src/vulkan/) and its matmul/conv shaders
+ * (src/shaders/ops/matmul_*.slang, conv_*.slang, winograd_*.slang).
+ *
+ * Rules of the ABI:
+ *   - extern "C", plain pointers, sizes and enums; no C++ or torch types cross it.
+ *   - every entry point returns a tvk_status; tvk_last_error() gives the
+ *     thread-local message of the last failure.
+ *   - the library never owns caller tensors: pointers are borrowed for the call.
+ *   - compute entry points are asynchronous on `stream` (a hipStream_t); a NULL
+ *     stream means the library's own stream for the current device.
+ *   - strides are in ELEMENTS, not bytes, and may be zero (broadcast) or any
+ *     positive value; element offsets must fit in int64.
+ */
+#ifndef TVK_HIP_H
+#define TVK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. UNSUPPORTED means "this call cannot run on the device; the
+ * caller should take its CPU fallback" - the role TORCHVULKAN_FALLBACK plays in
+ * the reference (src/api/fallback.h:7-11). */
+typedef enum {
+    TVK_OK = 0,
+    TVK_ERR_UNSUPPORTED = 1,
+    TVK_ERR_OOM = 2,
+    TVK_ERR_INVALID = 3,
+    TVK_ERR_DEVICE = 4
+} tvk_status;
+
+typedef enum {
+    TVK_F32 = 0,
+    TVK_F16 = 1,
+    TVK_BF16 = 2
+} tvk_dtype;
+
+/* Epilogue activation, the reference's MatmulActivation
+ * (src/api/ops/matmul.cpp:13-18): NONE=0, RELU=1, GELU=2 (erf form). */
+typedef enum {
+    TVK_ACT_NONE = 0,
+    TVK_ACT_RELU = 1,
+    TVK_ACT_GELU = 2
+} tvk_activation;
+
+/* ------------------------------------------------------------------------- */
+/* Errors                                                                     */
+/* ------------------------------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). Replaces the
+ * TORCH_CHECK strings the reference raises from inside its runtime. */
+const char* tvk_last_error(void);
+
+/* ------------------------------------------------------------------------- */
+/* Runtime: devices and streams                                               */
+/* Replaces VulkanContext::Instance()/getDeviceCount()/CurrentDevice()        */
+/* (src/vulkan/vulkan_context.h:9-55, src/api/backend.cpp:11-30).             */
+/* ------------------------------------------------------------------------- */
+
+tvk_status tvk_device_count(int* count);
+tvk_status tvk_set_device(int device);
+tvk_status tvk_get_device(int* device);
+/* The library's stream for `device` (created on first use, default priority). */
+tvk_status tvk_get_stream(int device, void** stream);
+/* Blocks until all work on the library stream of `device` is done.
+ * Replaces DeviceContext::flush() behind torchvulkan.synchronize
+ * (src/api/backend.cpp:32-35). */
+tvk_status tvk_synchronize(int device);
+
+typedef struct {
+    char name[256];
+    char arch[64];           /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    size_t total_memory;
+    int compute_units;
+    int clock_khz;           /* peak shader clock reported by the runtime */
+    int wavefront_size;
+    size_t lds_per_block;
+    int pci_bus_id;
+    int has_fp64, has_fp16, has_bf16;
+} tvk_device_props;
+
+/* Replaces _device_properties (src/api/backend.cpp:104-124). */
+tvk_status tvk_device_properties(int device, tvk_device_props* out);
+
+/* ------------------------------------------------------------------------- */
+/* Memory: a hipMalloc-backed caching allocator, stream-ordered on the        */
+/* library stream. Replaces VulkanAllocator + DeviceContext buffer pools      */
+/* (src/vulkan/allocator.cpp:59-200, src/vulkan/cache.cpp:78-89).             */
+/* ------------------------------------------------------------------------- */
+
+/* Allocates `bytes` (rounded up to a size class) on `device`. bytes==0 gives
+ * *out==NULL and TVK_OK. Over the budget set by tvk_set_memory_limit this
+ * returns TVK_ERR_OOM, the reference's TORCHVULKAN_STRICT_ALLOCATION
+ * behaviour (src/vulkan/allocator.cpp:171-200). */
+tvk_status tvk_malloc(int device, size_t bytes, void** out);
+/* Returns a block to its size-class cache. NULL is a no-op. Freeing a pointer
+ * the allocator did not hand out is TVK_ERR_INVALID. */
+tvk_status tvk_free(void* ptr);
+/* Releases every cached (unused) block of `device` back to HIP
+ * (torchvulkan.empty_cache, src/api/backend.cpp:52-54). */
+tvk_status tvk_empty_cache(int device);
+/* Device of a pointer the allocator handed out, or -1
+ * (getDeviceFromPtr, src/api/hook.cpp:58-62). */
+tvk_status tvk_pointer_device(const void* ptr, int* device);
+/* 0 = no limit. */
+tvk_status tvk_set_memory_limit(int device, size_t bytes);
+
+tvk_status tvk_memory_allocated(int device, size_t* bytes);
+tvk_status tvk_max_memory_allocated(int device, size_t* bytes);
+tvk_status tvk_memory_reserved(int device, size_t* bytes);
+tvk_status tvk_reset_peak_memory_stats(int device);
+/* (free, total) as hipMemGetInfo reports them (src/api/backend.cpp:82-85). */
+tvk_status tvk_mem_get_info(int device, size_t* free_bytes, size_t* total_bytes);
+
+/* Stream-ordered copies. h2d/d2h block until done when `blocking` != 0. */
+tvk_status tvk_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream, int blocking);
+tvk_status tvk_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream, int blocking);
+tvk_status tvk_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Compute: batched strided GEMM with fused epilogue                          */
+/* ------------------------------------------------------------------------- */
+
+/* One batched GEMM:
+ *   C[b,m,n] = act( alpha * sum_k A[b,m,k] * B[b,k,n] + beta * bias[b,m,n] )
+ * with every operand addressed as base + b*s[0] + row*s[1] + col*s[2]
+ * (elements). The bias term is applied only when bias != NULL and beta != 0,
+ * the reference's has_bias rule (src/api/ops/matmul.cpp:259,394). alpha and
+ * beta are rounded to float32, the accumulate type the reference pushes them
+ * in (src/vulkan/builders.h:119-140, src/api/ops/matmul.cpp:238-239).
+ * Accumulation is float32 for every dtype; the result is rounded once to
+ * `dtype` (round to nearest even). K == 0 gives act(beta*bias) or zeros
+ * (src/api/ops/matmul.cpp:284-288).
+ *
+ * Replaces the dispatch in dispatch_matmul_shader
+ * (src/api/ops/matmul.cpp:584-597) of matmul_simd_main
+ * (src/shaders/ops/matmul_simd.slang:23-44) and matmul_coop_main
+ * (src/shaders/ops/matmul_coop.slang:443-452), with the same 4-stride operand
+ * model as TensorStrides (src/shaders/helpers/gemm.slang:3-9). */
+typedef struct {
+    int32_t dtype;          /* tvk_dtype of A, B, bias and C */
+    int32_t activation;     /* tvk_activation */
+    int64_t batch, M, N, K;
+    const void* a; int64_t a_stride[3];
+    const void* b; int64_t b_stride[3];
+    const void* bias; int64_t bias_stride[3];   /* NULL: no bias */
+    void* c; int64_t c_stride[3];
+    double alpha, beta;
+    void* stream;           /* hipStream_t or NULL */
+} tvk_gemm_desc;
+
+tvk_status tvk_gemm(const tvk_gemm_desc* desc);
+
+/* Name of the kernel tvk_gemm would launch for `desc` (no launch). Used by
+ * tests and the benchmark to state which path ran; replaces the tuner's
+ * choice record (src/vulkan/autotuner.cpp:56-84). */
+tvk_status tvk_gemm_plan(const tvk_gemm_desc* desc, char* name, size_t name_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TVK_HIP_H */

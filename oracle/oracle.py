@@ -1,0 +1,167 @@
+"""Python driver of the CPU oracle (test infrastructure only).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, and only as the checker: the product path never calls it.
+
+Arrays are numpy arrays; float16 and bfloat16 operands travel as their raw
+16-bit patterns (dtype uint16) together with a dtype code, so the oracle sees
+exactly the bits the device sees. See gemm_oracle.c for the reference lines
+each function restates.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "build" / "liboracle.so"
+
+F32, F16, BF16 = 0, 1, 2
+ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
+
+_lib = None
+_P64 = C.POINTER(C.c_int64)
+
+
+def build() -> Path:
+    """Compiles the oracle with its Makefile (gcc), output under oracle/build/."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        lib = C.CDLL(str(LIB))
+        lib.oracle_f32_to_f16.argtypes = [C.c_float]
+        lib.oracle_f32_to_f16.restype = C.c_uint16
+        lib.oracle_f16_to_f32.argtypes = [C.c_uint16]
+        lib.oracle_f16_to_f32.restype = C.c_float
+        lib.oracle_f32_to_bf16.argtypes = [C.c_float]
+        lib.oracle_f32_to_bf16.restype = C.c_uint16
+        lib.oracle_bf16_to_f32.argtypes = [C.c_uint16]
+        lib.oracle_bf16_to_f32.restype = C.c_float
+        lib.oracle_gelu.argtypes = [C.c_float]
+        lib.oracle_gelu.restype = C.c_float
+        lib.oracle_gemm_rows.argtypes = [
+            C.c_int, C.c_int, C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
+            C.c_void_p, _P64, C.c_void_p, _P64, C.c_void_p, _P64, C.c_void_p, _P64,
+            C.c_double, C.c_double, C.POINTER(C.c_float),
+        ]
+        lib.oracle_gemm_rows.restype = C.c_int
+        _lib = lib
+    return _lib
+
+
+# ---------------------------------------------------------------------------
+# element conversions (vectorised through the C functions)
+# ---------------------------------------------------------------------------
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    f = np.vectorize(load().oracle_f32_to_f16, otypes=[np.uint16])
+    return f(np.asarray(x, dtype=np.float32))
+
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    f = np.vectorize(load().oracle_f16_to_f32, otypes=[np.float32])
+    return f(np.asarray(h, dtype=np.uint16))
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    f = np.vectorize(load().oracle_f32_to_bf16, otypes=[np.uint16])
+    return f(np.asarray(x, dtype=np.float32))
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def to_f32(bits_or_f32: np.ndarray, dtype: int) -> np.ndarray:
+    if dtype == F32:
+        return np.asarray(bits_or_f32, dtype=np.float32)
+    if dtype == F16:
+        return np.asarray(bits_or_f32, dtype=np.uint16).view(np.float16).astype(np.float32)
+    return bf16_bits_to_f32(bits_or_f32)
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+
+def _estrides3(x: np.ndarray) -> tuple[int, int, int]:
+    es = x.itemsize
+    st = [s // es for s in x.strides]
+    if x.ndim == 2:
+        return (0, st[0], st[1])
+    if x.ndim == 3:
+        return (st[0], st[1], st[2])
+    raise ValueError("expected 2-D or 3-D")
+
+
+def gemm(a: np.ndarray, b: np.ndarray, dtype: int, bias: np.ndarray | None = None, alpha: float = 1.0,
+         beta: float = 0.0, act: int = ACT_NONE, fma: bool = True, threads: int | None = None) -> np.ndarray:
+    """C = act(alpha*A@B + beta*bias) in the reference SIMD tile's order.
+
+    a: [M,K] or [B,M,K]; b: [K,N] or [B,K,N] (any strides, including
+    broadcast); bias broadcasts to C. Returns a contiguous array of the same
+    element storage (float32, or uint16 bit patterns for float16/bfloat16).
+    """
+    lib = load()
+    batched = a.ndim == 3 or b.ndim == 3
+    if batched:
+        nb = max(a.shape[0] if a.ndim == 3 else 1, b.shape[0] if b.ndim == 3 else 1)
+        if a.ndim == 2:
+            a = np.broadcast_to(a, (nb,) + a.shape)
+        if b.ndim == 2:
+            b = np.broadcast_to(b, (nb,) + b.shape)
+    else:
+        nb = 1
+    M, K = a.shape[-2], a.shape[-1]
+    K2, N = b.shape[-2], b.shape[-1]
+    if K != K2:
+        raise ValueError(f"shapes cannot be multiplied ({M}x{K} and {K2}x{N})")
+    store = np.float32 if dtype == F32 else np.uint16
+    out_shape = (nb, M, N) if batched else (M, N)
+    c = np.zeros(out_shape, dtype=store)
+    if c.size == 0:
+        return c
+    sa = (C.c_int64 * 3)(*_estrides3(a))
+    sb = (C.c_int64 * 3)(*_estrides3(b))
+    sc = (C.c_int64 * 3)(*_estrides3(c))
+    bias_e = None
+    sbias = (C.c_int64 * 3)(0, 0, 0)
+    if bias is not None:
+        bias_e = np.broadcast_to(np.asarray(bias, dtype=store), out_shape)
+        sbias = (C.c_int64 * 3)(*_estrides3(bias_e))
+    a_p = a.ctypes.data if a.size else None
+    b_p = b.ctypes.data if b.size else None
+    bias_p = bias_e.ctypes.data if bias_e is not None else None
+
+    threads = threads or max(1, min(16, os.cpu_count() or 1))
+    jobs = []
+    rows_per = max(1, -(-M // max(1, threads)))
+    for bi in range(nb):
+        for m0 in range(0, M, rows_per):
+            jobs.append((bi, m0, min(M, m0 + rows_per)))
+
+    def run(job):
+        bi, m0, m1 = job
+        scratch = (C.c_float * max(1, N))()
+        rc = lib.oracle_gemm_rows(dtype, act, 1 if fma else 0, bi, m0, m1, N, K, a_p, sa, b_p, sb, bias_p, sbias,
+                                  c.ctypes.data, sc, float(alpha), float(beta), scratch)
+        if rc != 0:
+            raise ValueError("oracle_gemm_rows rejected its arguments")
+
+    if len(jobs) == 1:
+        run(jobs[0])
+    else:
+        with cf.ThreadPoolExecutor(max_workers=threads) as ex:
+            list(ex.map(run, jobs))
+    return c

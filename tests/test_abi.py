@@ -1,0 +1,87 @@
+"""CPU checks of the C ABI: the library loads, exports every entry point that
+include/tvk_hip.h declares, and rejects bad descriptors with the documented
+status codes. No compute is launched (there is no GPU here)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from torchvulkan_amd import _abi
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_entry_points() -> set[str]:
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(tvk_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _abi.load()
+    names = declared_entry_points()
+    assert "tvk_gemm" in names and "tvk_malloc" in names
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    assert set(_abi._ALL_ENTRY_POINTS) <= names
+
+
+def test_device_count_without_gpu_is_not_an_error():
+    assert _abi.device_count() >= 0
+
+
+def test_gemm_rejects_null_desc():
+    lib = _abi.load()
+    assert lib.tvk_gemm(None) == _abi.TVK_ERR_INVALID
+    assert b"desc is NULL" in lib.tvk_last_error()
+
+
+def _desc(**kw):
+    d = _abi.GemmDesc()
+    d.dtype, d.batch, d.M, d.N, d.K = _abi.TVK_F16, 1, 4, 4, 4
+    d.a, d.b, d.c = 16, 16, 16   # never dereferenced by validation
+    d.a_stride = _abi.I64x3(0, 4, 1)
+    d.b_stride = _abi.I64x3(0, 4, 1)
+    d.c_stride = _abi.I64x3(0, 4, 1)
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("dtype", 7, _abi.TVK_ERR_UNSUPPORTED),
+    ("activation", 9, _abi.TVK_ERR_INVALID),
+    ("M", -1, _abi.TVK_ERR_INVALID),
+    ("K", 1 << 40, _abi.TVK_ERR_UNSUPPORTED),
+    ("c", None, _abi.TVK_ERR_INVALID),
+])
+def test_gemm_validation_codes(field, value, status):
+    lib = _abi.load()
+    d = _desc(**{field: value})
+    assert lib.tvk_gemm(C.byref(d)) == status
+    assert lib.tvk_last_error()
+
+
+@pytest.mark.parametrize("a_stride,b_stride,dtype,M,N,K,want", [
+    ((0, 8192, 1), (0, 8192, 1), _abi.TVK_F16, 8192, 8192, 8192, "gemm16_mfma_256x256"),
+    ((0, 4096, 1), (0, 1, 4096), _abi.TVK_F16, 256, 4096, 4096, "gemm16_mfma_128x128"),
+    ((0, 3, 5), (0, 4, 1), _abi.TVK_F16, 8, 4, 4, "gemm_generic"),
+    ((0, 1024, 1), (0, 1024, 1), _abi.TVK_F32, 1024, 1024, 1024, "gemm32_seq_128x128"),
+    ((0, 4, 1), (0, 4, 1), _abi.TVK_BF16, 4, 4, 0, "gemm_k0_fill"),
+])
+def test_gemm_plan_without_gpu(a_stride, b_stride, dtype, M, N, K, want):
+    lib = _abi.load()
+    d = _desc(a_stride=_abi.I64x3(*a_stride), b_stride=_abi.I64x3(*b_stride), dtype=dtype, M=M, N=N, K=K)
+    buf = C.create_string_buffer(64)
+    assert lib.tvk_gemm_plan(C.byref(d), buf, 64) == _abi.TVK_OK
+    assert buf.value.decode() == want
+
+
+def test_free_rejects_foreign_pointer():
+    lib = _abi.load()
+    assert lib.tvk_free(C.c_void_p(0x1234)) == _abi.TVK_ERR_INVALID
+    assert lib.tvk_free(None) == _abi.TVK_OK

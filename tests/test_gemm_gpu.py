@@ -1,0 +1,268 @@
+"""GEMM parity on the GPU, through the C ABI (tvk_gemm), against the oracle.
+
+Cases follow the configs of the path: C1 fp32 mm 1024^3 (+relu, sum), the
+MLP addmm chain and its backward GEMMs (C2), the transformer linears and
+head-strided bmm (C3), and the sweep (C5): square 8192^3, skinny
+16x4096x14336, ragged 1000x777x3000, baddbmm 64x512x512x128 with alpha=0.5,
+beta=1, and transposed / sliced views. Edge cases follow the reference's
+rules (src/api/ops/matmul.cpp:259,284-288): empty outputs, K == 0, beta == 0
+with a NaN bias. Tolerances are in tests/gemm_cases.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests.gemm_cases import (TOL, assert_close, decode, oracle_mm, randint, randn, to_np)
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+F16_TYPES = [torch.float16, torch.bfloat16]
+ALL_TYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+def run(abi, a, b, out_shape, dtype, bias=None, alpha=1.0, beta=0.0, act=0):
+    """Runs tvk_gemm on device copies of host views a/b (strides kept)."""
+    da = a.to(DEV) if a.is_contiguous() else _device_view(a)
+    db = b.to(DEV) if b.is_contiguous() else _device_view(b)
+    dbias = None if bias is None else bias.to(DEV)
+    c = torch.empty(out_shape, dtype=dtype, device=DEV)
+    abi.gemm(da, db, c, bias=dbias, alpha=alpha, beta=beta, activation=act)
+    torch.cuda.synchronize()
+    return decode(to_np(c), dtype), abi.gemm_plan(da, db, c, bias=dbias, alpha=alpha, beta=beta, activation=act)
+
+
+def _device_view(t: torch.Tensor) -> torch.Tensor:
+    """Device tensor with the same strides as the host view (copies its storage)."""
+    base = t.as_strided((t.untyped_storage().nbytes() // t.element_size(),), (1,), 0)
+    dbase = base.to(DEV)
+    return dbase.as_strided(t.shape, t.stride(), t.storage_offset())
+
+
+# ---------------------------------------------------------------------------
+# bit-exact cases
+# ---------------------------------------------------------------------------
+
+def test_c1_fp32_mm_1024_bit_exact(gpu):
+    a = randn((1024, 1024), torch.float32, 0)
+    b = randn((1024, 1024), torch.float32, 1)
+    got, plan = run(gpu, a, b, (1024, 1024), torch.float32)
+    ref = oracle_mm(a, b, torch.float32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"{plan}: not bit-exact"
+    # the config's tail: relu then sum (ops the reference runs on its CPU fallback)
+    assert np.maximum(got, 0).astype(np.float64).sum() == np.maximum(ref, 0).astype(np.float64).sum()
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("shape", [(256, 256, 256), (300, 520, 136), (64, 80, 24)])
+def test_integer_exact_all_layouts(gpu, dtype, ta, tb, shape):
+    # integer operands: every summation order gives identical bits
+    M, N, K = shape
+    a = randint((K, M) if ta else (M, K), dtype, 10)
+    b = randint((N, K) if tb else (K, N), dtype, 11)
+    a = a.t() if ta else a
+    b = b.t() if tb else b
+    got, plan = run(gpu, a, b, (M, N), dtype)
+    ref = oracle_mm(a, b, dtype)
+    assert np.array_equal(got, ref), plan
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+def test_integer_exact_ragged_unaligned(gpu, dtype):
+    # K rows of 777 halves are not 16-byte aligned: the element-wise load path
+    a = randint((100, 77), dtype, 12)
+    b = randint((77, 300), dtype, 13)
+    got, plan = run(gpu, a, b, (100, 300), dtype)
+    assert "mfma" in plan
+    assert np.array_equal(got, oracle_mm(a, b, dtype)), plan
+
+
+# ---------------------------------------------------------------------------
+# C2: MLP addmm chain (fp16 / fp32 accumulate), forward and backward
+# ---------------------------------------------------------------------------
+
+MLP = [784, 4096, 4096, 4096, 10]
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("layer", range(4))
+def test_c2_mlp_forward_addmm(gpu, dtype, layer):
+    fin, fout = MLP[layer], MLP[layer + 1]
+    bound = 1.0 / np.sqrt(fin)
+    g = torch.Generator().manual_seed(20 + layer)
+    x = torch.rand((256, fin), generator=g).to(dtype)
+    w = ((torch.rand((fout, fin), generator=g) * 2 - 1) * bound).to(dtype)
+    bias = ((torch.rand((fout,), generator=g) * 2 - 1) * bound).to(dtype)
+    got, plan = run(gpu, x, w.t(), (256, fout), dtype, bias=bias, beta=1.0)
+    ref = oracle_mm(x, w.t(), dtype, bias=bias, beta=1.0)
+    assert_close(got, ref, dtype, plan)
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+def test_c2_mlp_backward_gemms(gpu, dtype):
+    g = torch.Generator().manual_seed(30)
+    dy = torch.randn((256, 4096), generator=g).to(dtype)
+    w = (torch.randn((4096, 4096), generator=g) * 0.02).to(dtype)
+    x = torch.rand((256, 784), generator=g).to(dtype)
+    dy1 = torch.randn((256, 4096), generator=g).to(dtype)
+    # dX = dY . W   (W is [out, in] row-major: B is n-contiguous)
+    got, plan = run(gpu, dy, w, (256, 4096), dtype)
+    assert_close(got, oracle_mm(dy, w, dtype), dtype, "dX " + plan)
+    # dW = dY^T . X (dY^T is an m-contiguous transposed view)
+    got, plan = run(gpu, dy1.t(), x, (4096, 784), dtype)
+    assert_close(got, oracle_mm(dy1.t(), x, dtype), dtype, "dW " + plan)
+
+
+# ---------------------------------------------------------------------------
+# C3: transformer linears and head-strided bmm
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("fin,fout", [(512, 512), (512, 256), (512, 3072), (1536, 512), (512, 96)])
+def test_c3_linear(gpu, dtype, fin, fout):
+    x = randn((8192, fin), dtype, 40)
+    w = randn((fout, fin), dtype, 41, std=0.02)
+    got, plan = run(gpu, x, w.t(), (8192, fout), dtype)
+    assert_close(got, oracle_mm(x, w.t(), dtype), dtype, plan)
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+def test_c3_head_strided_bmm(gpu, dtype):
+    # one sequence of the batch: q/k/v as [heads, seq, head_dim] views of [seq, heads*head_dim]
+    q = randn((256, 8 * 64), dtype, 50)
+    k = randn((256, 8 * 64), dtype, 51)
+    qh = q.view(256, 8, 64).transpose(0, 1)            # [8, 256, 64] strides (64, 512, 1)
+    kt = k.view(256, 8, 64).transpose(0, 1).transpose(1, 2)  # [8, 64, 256] strides (64, 1, 512)
+    got, plan = run(gpu, qh, kt, (8, 256, 256), dtype)
+    assert_close(got, oracle_mm(qh, kt, dtype), dtype, "QK^T " + plan)
+    p = randn((8, 256, 256), dtype, 52, std=0.1)
+    v = randn((256, 8 * 64), dtype, 53)
+    vh = v.view(256, 8, 64).transpose(0, 1)            # [8, 256, 64]
+    got, plan = run(gpu, p, vh, (8, 256, 64), dtype)
+    assert_close(got, oracle_mm(p, vh, dtype), dtype, "PV " + plan)
+
+
+# ---------------------------------------------------------------------------
+# C5: sweep
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", ALL_TYPES)
+def test_c5_ragged(gpu, dtype):
+    a = randn((1000, 777), dtype, 60)
+    b = randn((777, 3000), dtype, 61)
+    got, plan = run(gpu, a, b, (1000, 3000), dtype)
+    ref = oracle_mm(a, b, dtype)
+    if dtype == torch.float32:
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), plan
+    assert_close(got, ref, dtype, plan)
+
+
+@pytest.mark.parametrize("dtype", ALL_TYPES)
+def test_c5_baddbmm(gpu, dtype):
+    inp = randn((64, 512, 512), dtype, 70)
+    b1 = randn((64, 512, 128), dtype, 71)
+    b2 = randn((64, 128, 512), dtype, 72)
+    got, plan = run(gpu, b1, b2, (64, 512, 512), dtype, bias=inp, alpha=0.5, beta=1.0)
+    ref = oracle_mm(b1, b2, dtype, bias=inp, alpha=0.5, beta=1.0)
+    if dtype == torch.float32:
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), plan
+    assert_close(got, ref, dtype, plan)
+
+
+@pytest.mark.parametrize("dtype", ALL_TYPES)
+def test_c5_skinny(gpu, dtype):
+    a = randn((16, 4096), dtype, 80)
+    b = randn((4096, 14336), dtype, 81)
+    got, plan = run(gpu, a, b, (16, 14336), dtype)
+    assert_close(got, oracle_mm(a, b, dtype), dtype, plan)
+
+
+@pytest.mark.parametrize("dtype", ALL_TYPES)
+def test_c5_square_8192(gpu, dtype):
+    # Full-size run. The oracle checks one seeded row in every 256-row band,
+    # so every output tile is crossed by a checked row; a row-sum property
+    # then covers all of C: sum_j C[i,j] == (A @ (B @ 1))[i] within the
+    # spread the per-element rounding allows.
+    a = randn((8192, 8192), dtype, 90)
+    b = randn((8192, 8192), dtype, 91)
+    got, plan = run(gpu, a, b, (8192, 8192), dtype)
+    rng = np.random.default_rng(0)
+    rows = np.arange(0, 8192, 256) + rng.integers(0, 256, 32)
+    ref = oracle_mm(a[torch.from_numpy(rows)], b, dtype)
+    if dtype == torch.float32:
+        assert np.array_equal(got[rows].view(np.uint32), ref.view(np.uint32)), plan
+    assert_close(got[rows], ref, dtype, plan)
+    bsum = decode(to_np(b), dtype).astype(np.float64).sum(axis=1)
+    rs = decode(to_np(a), dtype).astype(np.float64) @ bsum
+    g64 = got.astype(np.float64)
+    ulp = np.spacing(np.abs(got).astype(np.float16 if dtype == torch.float16 else np.float32)).astype(np.float64)
+    if dtype == torch.bfloat16:
+        ulp = np.abs(g64) * 2.0 ** -7
+    var = (ulp ** 2).sum(axis=1) / 12 + ((1e-5 * (np.abs(g64) + 1)) ** 2).sum(axis=1) / 3
+    assert np.all(np.abs(g64.sum(axis=1) - rs) <= 8 * np.sqrt(var) + 1e-9), plan
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+def test_c5_transposed_and_sliced_views(gpu, dtype):
+    big = randn((1100, 900), dtype, 100)
+    a = big[50:1050:1, 100:877]               # [1000, 777] rows of stride 900
+    b = randn((3000, 800), dtype, 101)[:, :777].t()   # [777, 3000] k-contiguous, sliced
+    got, plan = run(gpu, a, b, (1000, 3000), dtype)
+    assert_close(got, oracle_mm(a, b, dtype), dtype, plan)
+
+
+# ---------------------------------------------------------------------------
+# epilogue and edge cases
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", ALL_TYPES)
+@pytest.mark.parametrize("act", [orc.ACT_RELU, orc.ACT_GELU])
+def test_activation_epilogue(gpu, dtype, act):
+    a = randn((300, 200), dtype, 110)
+    b = randn((200, 260), dtype, 111)
+    bias = randn((260,), dtype, 112)
+    got, plan = run(gpu, a, b, (300, 260), dtype, bias=bias, alpha=0.5, beta=2.0, act=act)
+    assert_close(got, oracle_mm(a, b, dtype, bias=bias, alpha=0.5, beta=2.0, act=act), dtype, plan)
+
+
+@pytest.mark.parametrize("dtype", ALL_TYPES)
+def test_beta_zero_ignores_nan_bias(gpu, dtype):
+    a = randn((64, 32), dtype, 120)
+    b = randn((32, 48), dtype, 121)
+    bias = torch.full((64, 48), float("nan"), dtype=dtype)
+    got, _ = run(gpu, a, b, (64, 48), dtype, bias=bias, beta=0.0)
+    assert not np.isnan(got).any()
+    assert_close(got, oracle_mm(a, b, dtype), dtype)
+
+
+@pytest.mark.parametrize("dtype", ALL_TYPES)
+def test_k_zero(gpu, dtype):
+    a = torch.empty((5, 0), dtype=dtype)
+    b = torch.empty((0, 7), dtype=dtype)
+    bias = randn((7,), dtype, 130)
+    got, plan = run(gpu, a, b, (5, 7), dtype, bias=bias, beta=3.0)
+    assert plan == "gemm_k0_fill"
+    assert_close(got, oracle_mm(a, b, dtype, bias=bias, beta=3.0), dtype)
+    got, _ = run(gpu, a, b, (5, 7), dtype)
+    assert np.array_equal(got, np.zeros((5, 7), np.float32))
+
+
+def test_empty_output_is_a_no_op(gpu):
+    a = torch.empty((0, 8), dtype=torch.float16)
+    b = randn((8, 4), torch.float16, 140)
+    got, plan = run(gpu, a, b, (0, 4), torch.float16)
+    assert got.shape == (0, 4) and plan == "none"
+
+
+def test_fully_strided_operands_generic_path(gpu):
+    # neither stride of A is 1: only the generic kernel accepts it
+    big = randn((64, 96), torch.float16, 150)
+    a = big[::2, ::3]          # [32, 32], strides (192, 3)
+    b = randn((32, 40), torch.float16, 151)
+    got, plan = run(gpu, a, b, (32, 40), torch.float16)
+    assert plan == "gemm_generic"
+    assert_close(got, oracle_mm(a, b, torch.float16), torch.float16, plan)

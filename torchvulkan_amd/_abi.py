@@ -1,0 +1,198 @@
+"""ctypes binding of the C ABI declared in include/tvk_hip.h.
+
+This is the binding a Python caller of the boundary uses (tests, the
+benchmark and the smoke check call the library through it). It never falls
+back to anything: if ``libtvk_hip.so`` is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+_LIB_PATH = Path(__file__).resolve().parent / "libtvk_hip.so"
+
+TVK_OK, TVK_ERR_UNSUPPORTED, TVK_ERR_OOM, TVK_ERR_INVALID, TVK_ERR_DEVICE = range(5)
+TVK_F32, TVK_F16, TVK_BF16 = range(3)
+TVK_ACT_NONE, TVK_ACT_RELU, TVK_ACT_GELU = range(3)
+
+STATUS_NAMES = {0: "OK", 1: "UNSUPPORTED", 2: "OOM", 3: "INVALID", 4: "DEVICE"}
+
+
+class TvkError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"tvk status {STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+class TvkUnsupported(TvkError):
+    """The call cannot run on the device (the caller takes its CPU fallback)."""
+
+
+class TvkOutOfMemory(TvkError):
+    pass
+
+
+I64x3 = C.c_int64 * 3
+
+
+class GemmDesc(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int32),
+        ("activation", C.c_int32),
+        ("batch", C.c_int64),
+        ("M", C.c_int64),
+        ("N", C.c_int64),
+        ("K", C.c_int64),
+        ("a", C.c_void_p), ("a_stride", I64x3),
+        ("b", C.c_void_p), ("b_stride", I64x3),
+        ("bias", C.c_void_p), ("bias_stride", I64x3),
+        ("c", C.c_void_p), ("c_stride", I64x3),
+        ("alpha", C.c_double),
+        ("beta", C.c_double),
+        ("stream", C.c_void_p),
+    ]
+
+
+class DeviceProps(C.Structure):
+    _fields_ = [
+        ("name", C.c_char * 256),
+        ("arch", C.c_char * 64),
+        ("total_memory", C.c_size_t),
+        ("compute_units", C.c_int),
+        ("clock_khz", C.c_int),
+        ("wavefront_size", C.c_int),
+        ("lds_per_block", C.c_size_t),
+        ("pci_bus_id", C.c_int),
+        ("has_fp64", C.c_int),
+        ("has_fp16", C.c_int),
+        ("has_bf16", C.c_int),
+    ]
+
+
+_lib = None
+
+
+def lib_path() -> Path:
+    return _LIB_PATH
+
+
+def load() -> C.CDLL:
+    """Loads libtvk_hip.so (raises OSError when it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            raise OSError(f"{_LIB_PATH} is not built; run python -m torchvulkan_amd.build")
+        lib = C.CDLL(str(_LIB_PATH))
+        lib.tvk_last_error.restype = C.c_char_p
+        lib.tvk_gemm.argtypes = [C.POINTER(GemmDesc)]
+        lib.tvk_gemm_plan.argtypes = [C.POINTER(GemmDesc), C.c_char_p, C.c_size_t]
+        lib.tvk_malloc.argtypes = [C.c_int, C.c_size_t, C.POINTER(C.c_void_p)]
+        lib.tvk_free.argtypes = [C.c_void_p]
+        lib.tvk_pointer_device.argtypes = [C.c_void_p, C.POINTER(C.c_int)]
+        lib.tvk_memcpy_h2d.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_int]
+        lib.tvk_memcpy_d2h.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_int]
+        lib.tvk_memcpy_d2d.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+        lib.tvk_get_stream.argtypes = [C.c_int, C.POINTER(C.c_void_p)]
+        for fn in ("tvk_memory_allocated", "tvk_max_memory_allocated", "tvk_memory_reserved"):
+            getattr(lib, fn).argtypes = [C.c_int, C.POINTER(C.c_size_t)]
+        lib.tvk_set_memory_limit.argtypes = [C.c_int, C.c_size_t]
+        lib.tvk_mem_get_info.argtypes = [C.c_int, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+        lib.tvk_device_properties.argtypes = [C.c_int, C.POINTER(DeviceProps)]
+        for fn in _ALL_ENTRY_POINTS:
+            getattr(lib, fn).restype = C.c_int if fn != "tvk_last_error" else C.c_char_p
+        _lib = lib
+    return _lib
+
+
+_ALL_ENTRY_POINTS = (
+    "tvk_last_error", "tvk_device_count", "tvk_set_device", "tvk_get_device", "tvk_get_stream",
+    "tvk_synchronize", "tvk_device_properties", "tvk_malloc", "tvk_free", "tvk_empty_cache",
+    "tvk_pointer_device", "tvk_set_memory_limit", "tvk_memory_allocated", "tvk_max_memory_allocated",
+    "tvk_memory_reserved", "tvk_reset_peak_memory_stats", "tvk_mem_get_info", "tvk_memcpy_h2d",
+    "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan",
+)
+
+
+def check(status: int) -> None:
+    if status == TVK_OK:
+        return
+    msg = load().tvk_last_error().decode(errors="replace")
+    if status == TVK_ERR_UNSUPPORTED:
+        raise TvkUnsupported(status, msg)
+    if status == TVK_ERR_OOM:
+        raise TvkOutOfMemory(status, msg)
+    raise TvkError(status, msg)
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    check(load().tvk_device_count(C.byref(n)))
+    return n.value
+
+
+# ---------------------------------------------------------------------------
+# torch-tensor helpers (torch supplies device memory and the stream)
+# ---------------------------------------------------------------------------
+
+def _dtype_code(dtype) -> int:
+    import torch
+
+    codes = {torch.float32: TVK_F32, torch.float16: TVK_F16, torch.bfloat16: TVK_BF16}
+    if dtype not in codes:
+        raise TvkUnsupported(TVK_ERR_UNSUPPORTED, f"dtype {dtype} is not on the dense-contraction path")
+    return codes[dtype]
+
+
+def _strides3(t) -> tuple[int, int, int]:
+    if t.dim() == 2:
+        return (0, t.stride(0), t.stride(1))
+    if t.dim() == 3:
+        return (t.stride(0), t.stride(1), t.stride(2))
+    raise ValueError("expected a 2-D or 3-D tensor")
+
+
+def make_gemm_desc(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, stream=None) -> GemmDesc:
+    """Describes C = act(alpha*A@B + beta*bias) over 2-D or batched 3-D tensors.
+
+    `bias` may be any tensor that broadcasts to C's shape (it is expanded with
+    stride-0 views, as the reference's prepare_matmul_operands does).
+    """
+    batch = c.shape[0] if c.dim() == 3 else 1
+    M, N = c.shape[-2], c.shape[-1]
+    K = a.shape[-1]
+    d = GemmDesc()
+    d.dtype = _dtype_code(c.dtype)
+    d.activation = activation
+    d.batch, d.M, d.N, d.K = batch, M, N, K
+    d.a = a.data_ptr() if a.numel() else None
+    d.a_stride = I64x3(*_strides3(a))
+    d.b = b.data_ptr() if b.numel() else None
+    d.b_stride = I64x3(*_strides3(b))
+    if bias is not None:
+        bias_e = bias.expand(c.shape)
+        d.bias = bias_e.data_ptr()
+        d.bias_stride = I64x3(*_strides3(bias_e))
+    d.c = c.data_ptr() if c.numel() else None
+    d.c_stride = I64x3(*_strides3(c))
+    d.alpha = float(alpha)
+    d.beta = float(beta)
+    d.stream = stream
+    return d
+
+
+def gemm(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, stream=None) -> None:
+    """Runs tvk_gemm on torch device tensors; `stream` defaults to torch's current stream."""
+    import torch
+
+    if stream is None and c.is_cuda:
+        stream = torch.cuda.current_stream(c.device).cuda_stream
+    d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, stream)
+    check(load().tvk_gemm(C.byref(d)))
+
+
+def gemm_plan(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE) -> str:
+    d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, None)
+    buf = C.create_string_buffer(128)
+    check(load().tvk_gemm_plan(C.byref(d), buf, 128))
+    return buf.value.decode()

@@ -1,0 +1,79 @@
+"""Build recipe for the gfx950 dense-contraction library.
+
+Compiles every HIP source of the C ABI (``csrc/*.hip``) for gfx950 with hipcc
+and links them into ``torchvulkan_amd/libtvk_hip.so``, in-tree, so the built
+library travels with the source tree. The PrivateUse1 backend extension
+(``csrc/backend/*.cpp``) is built by :func:`build_backend` against the
+installed torch headers and links to the same library.
+
+Run ``python -m torchvulkan_amd.build`` (or ``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libtvk_hip.so"
+INCLUDE = PKG.parent / "include"
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# Packed FP32 instructions are disabled for every device pass; the host pass
+# warns that it does not know the feature, which is harmless.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in proc.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out)
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD / (src.stem + ".o")
+    _run([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
+    return obj
+
+
+def build_library(jobs: int | None = None) -> Path:
+    """Compile csrc/*.hip for gfx950 and link libtvk_hip.so (always rebuilds)."""
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2) - 1), 16)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, sources))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def main() -> None:
+    lib = build_library()
+    print(f"built {lib}")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,606 @@
+// Dense GEMM kernels for gfx950 (MI355X) and the tvk_gemm dispatcher.
+//
+// Reference semantics followed (file:line under the reference tree):
+//   - operand model: base + batch*s0 + row*s1 + col*s2, TensorStrides
+//     (src/shaders/helpers/gemm.slang:3-9, src/api/ops/matmul.cpp:156-160)
+//   - epilogue: v = acc*alpha; if has_bias: v += bias*beta; v = act(v); one
+//     rounding to the storage type (src/shaders/helpers/gemm_simd.slang:67-99,
+//     src/shaders/ops/matmul_coop.slang:383-408, src/shaders/core/dtype.slang:255-282)
+//   - has_bias = bias defined && beta != 0 (src/api/ops/matmul.cpp:259,394)
+//   - K == 0: act(beta*bias) or zeros (src/api/ops/matmul.cpp:284-288,402-406)
+//
+// Kernels:
+//   gemm16_mfma  float16/bfloat16, 256x256 or 128x128 block tiles, 4 waves,
+//                v_mfma_f32_32x32x16_{f16,bf16}, both operands staged through
+//                LDS in a k-contiguous padded layout, double buffered. An operand
+//                whose contiguous dimension is M or N (a transposed view) is
+//                transposed in registers on its way into LDS, so no copy is made.
+//   gemm32_seq   float32 with the reference SIMD tile's summation order:
+//                every output accumulates fmaf(a_k, b_k, acc) for k = 0..K-1
+//                in sequence (src/shaders/helpers/gemm_simd.slang:219-239).
+//   gemm_generic any strides / dtype, one thread per output, same order.
+#include "tvk_common.h"
+
+#include <algorithm>
+#include <cstring>
+#include <cstdio>
+
+namespace tvk {
+namespace {
+
+struct GemmArgs {
+    const void* a;
+    const void* b;
+    const void* bias;
+    void* c;
+    int64_t sa[3], sb[3], sbias[3], sc[3];
+    int M, N, K;
+    int batch;
+    float alpha, beta;
+    int has_bias;
+    int act;
+    int tiles_m, tiles_n;
+};
+
+// ----------------------------------------------------------------------------
+// epilogue (shared by all kernels)
+// ----------------------------------------------------------------------------
+
+__device__ inline float gelu_erf(float v) {
+    return 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
+}
+
+// v = acc*alpha; v = v + bias*beta; act(v). Contraction is off so the two
+// products round separately, as the reference's ext_mul/ext_add chain does.
+template <int DT>
+__device__ inline float epilogue_value(const GemmArgs& p, int b, int row, int col, float acc) {
+#pragma clang fp contract(off)
+    float v = acc * p.alpha;
+    if (p.has_bias) {
+        typedef typename elem<DT>::T T;
+        const T* bias = reinterpret_cast<const T*>(p.bias);
+        float bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2]]);
+        float t = bv * p.beta;
+        v = v + t;
+    }
+    if (p.act == TVK_ACT_RELU) v = v > 0.0f ? v : (v != v ? v : 0.0f);
+    else if (p.act == TVK_ACT_GELU) v = gelu_erf(v);
+    return v;
+}
+
+template <int DT>
+__device__ inline void store_out(const GemmArgs& p, int b, int row, int col, float acc) {
+    typedef typename elem<DT>::T T;
+    T* c = reinterpret_cast<T*>(p.c);
+    float v = epilogue_value<DT>(p, b, row, col, acc);
+    c[(int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2]] = elem<DT>::from_f32(v);
+}
+
+// ----------------------------------------------------------------------------
+// K == 0 and generic kernels
+// ----------------------------------------------------------------------------
+
+template <int DT>
+__global__ void gemm_k0_kernel(GemmArgs p) {
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t total = (int64_t)p.batch * p.M * p.N;
+    if (idx >= total) return;
+    int col = (int)(idx % p.N);
+    int row = (int)((idx / p.N) % p.M);
+    int b = (int)(idx / ((int64_t)p.N * p.M));
+    store_out<DT>(p, b, row, col, 0.0f);
+}
+
+// One output per thread, sequential k, fmaf accumulate: the reference SIMD
+// tile's per-output order, for operands no tiled kernel accepts.
+template <int DT>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
+    typedef typename elem<DT>::T T;
+    int col = blockIdx.x * 16 + (threadIdx.x % 16);
+    int row = blockIdx.y * 16 + (threadIdx.x / 16);
+    int b = blockIdx.z;
+    if (row >= p.M || col >= p.N) return;
+    const T* a = reinterpret_cast<const T*>(p.a) + (int64_t)b * p.sa[0] + (int64_t)row * p.sa[1];
+    const T* bm = reinterpret_cast<const T*>(p.b) + (int64_t)b * p.sb[0] + (int64_t)col * p.sb[2];
+    float acc = 0.0f;
+    for (int k = 0; k < p.K; ++k)
+        acc = fmaf(elem<DT>::to_f32(a[(int64_t)k * p.sa[2]]), elem<DT>::to_f32(bm[(int64_t)k * p.sb[1]]), acc);
+    store_out<DT>(p, b, row, col, acc);
+}
+
+// ----------------------------------------------------------------------------
+// float32, sequential-k order: 128x128 block, 256 threads, 8x8 per thread
+// ----------------------------------------------------------------------------
+
+constexpr int S_BM = 128, S_BN = 128, S_BK = 16;
+
+__global__ __launch_bounds__(256) void gemm32_seq_kernel(GemmArgs p) {
+#pragma clang fp contract(off)
+    __shared__ float As[2][S_BK][S_BM + 4];
+    __shared__ float Bs[2][S_BK][S_BN + 4];
+    const int tid = threadIdx.x;
+    const int tm = blockIdx.x / p.tiles_n, tn = blockIdx.x % p.tiles_n;
+    const int b = blockIdx.y;
+    const int m0 = tm * S_BM, n0 = tn * S_BN;
+    const float* A = reinterpret_cast<const float*>(p.a) + (int64_t)b * p.sa[0];
+    const float* B = reinterpret_cast<const float*>(p.b) + (int64_t)b * p.sb[0];
+
+    // loader mapping: 2048 elements of each tile, 8 per thread.
+    // A tile element (m, k): thread covers k-fastest when A is k-contiguous.
+    const bool a_kfast = p.sa[2] == 1;
+    const bool b_nfast = p.sb[2] == 1;
+    float ra[8], rb[8];
+
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            int e = tid + i * 256;
+            int m, k;
+            if (a_kfast) { k = e % S_BK; m = e / S_BK; }
+            else { m = e % S_BM; k = e / S_BM; }
+            int gm = m0 + m, gk = k0 + k;
+            ra[i] = (gm < p.M && gk < p.K) ? A[(int64_t)gm * p.sa[1] + (int64_t)gk * p.sa[2]] : 0.0f;
+            int n, kb;
+            if (b_nfast) { n = e % S_BN; kb = e / S_BN; }
+            else { kb = e % S_BK; n = e / S_BK; }
+            int gn = n0 + n, gkb = k0 + kb;
+            rb[i] = (gn < p.N && gkb < p.K) ? B[(int64_t)gkb * p.sb[1] + (int64_t)gn * p.sb[2]] : 0.0f;
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            int e = tid + i * 256;
+            int m, k;
+            if (a_kfast) { k = e % S_BK; m = e / S_BK; }
+            else { m = e % S_BM; k = e / S_BM; }
+            As[buf][k][m] = ra[i];
+            int n, kb;
+            if (b_nfast) { n = e % S_BN; kb = e / S_BN; }
+            else { kb = e % S_BK; n = e / S_BK; }
+            Bs[buf][kb][n] = rb[i];
+        }
+    };
+
+    const int tx = tid % 16, ty = tid / 16;
+    float acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+
+    const int nk = (p.K + S_BK - 1) / S_BK;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load((kt + 1) * S_BK);
+#pragma unroll
+        for (int k = 0; k < S_BK; ++k) {
+            // rows ty*4..+3 and 64+ty*4..+3; cols tx*4..+3 and 64+tx*4..+3
+            float4 a0 = *reinterpret_cast<const float4*>(&As[buf][k][ty * 4]);
+            float4 a1 = *reinterpret_cast<const float4*>(&As[buf][k][64 + ty * 4]);
+            float4 b0 = *reinterpret_cast<const float4*>(&Bs[buf][k][tx * 4]);
+            float4 b1 = *reinterpret_cast<const float4*>(&Bs[buf][k][64 + tx * 4]);
+            float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+        }
+        if (kt + 1 < nk) store(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        int row = m0 + (i < 4 ? ty * 4 + i : 64 + ty * 4 + i - 4);
+        if (row >= p.M) continue;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            int col = n0 + (j < 4 ? tx * 4 + j : 64 + tx * 4 + j - 4);
+            if (col < p.N) store_out<TVK_F32>(p, b, row, col, acc[i][j]);
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// float16 / bfloat16 MFMA kernel
+// ----------------------------------------------------------------------------
+
+constexpr int H_BK = 64;          // k per LDS stage
+constexpr int H_LDK = H_BK + 8;   // padded LDS row (halfs): 144 B, conflict-free b128 reads
+
+template <int DT>
+__device__ inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    if constexpr (DT == TVK_F16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Out-of-range buffer offset: the hardware returns zeros for it.
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ inline u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ inline uint32_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
+// Eight consecutive elements of one operand along its contiguous dimension.
+// VEC: one 16-byte load (alignment and extent are multiples of 8 elements);
+// otherwise eight 2-byte loads, each range-checked.
+template <bool VEC>
+__device__ inline u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, bool row_ok, int64_t elem_off, int64_t step, int valid) {
+    if constexpr (VEC) {
+        return buf_load16(r, (row_ok && valid > 0) ? (uint32_t)(elem_off * 2) : kOOB);
+    } else {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            h[e] = buf_load2(r, (row_ok && e < valid) ? (uint32_t)((elem_off + e * step) * 2) : kOOB);
+        u32x4 v;
+        v.x = h[0] | (h[1] << 16);
+        v.y = h[2] | (h[3] << 16);
+        v.z = h[4] | (h[5] << 16);
+        v.w = h[6] | (h[7] << 16);
+        return v;
+    }
+}
+
+// Loader of one operand tile of R rows (rows = M for A, N for B) x 64 k into
+// LDS laid out [R][H_LDK] with k contiguous.
+//   KMAJ: the operand's k stride is 1: thread t loads 16 B chunks (8 k) of rows
+//         t/8 + 32*i, chunk t%8.
+//   else: the operand's row stride is 1 (M or N contiguous): thread t loads,
+//         for k = 4*(t%16) + 0..3, eight consecutive rows starting at
+//         8*(t/16 + 16*u), and transposes the 4x8 block into 8 rows of 4 k.
+template <int R, bool KMAJ, bool VEC>
+struct TileLoader {
+    static constexpr int NREG = R / 32;   // 16-byte registers per thread per stage
+    u32x4 reg[NREG];
+
+    __device__ inline void load(__amdgpu_buffer_rsrc_t rsrc, int64_t s_row, int64_t s_k, int row0, int rows, int k0, int K, int tid) {
+        if constexpr (KMAJ) {
+            const int kc = (tid % 8) * 8;
+#pragma unroll
+            for (int i = 0; i < NREG; ++i) {
+                int r = tid / 8 + 32 * i;
+                int gr = row0 + r, gk = k0 + kc;
+                int valid = K - gk;
+                reg[i] = load_chunk<VEC>(rsrc, gr < rows, (int64_t)gr * s_row + (int64_t)gk * s_k, s_k, valid);
+            }
+        } else {
+            const int kq = (tid % 16) * 4;
+#pragma unroll
+            for (int u = 0; u < NREG / 4; ++u) {
+                int rc = 8 * (tid / 16 + 16 * u);
+                int gr = row0 + rc;
+                int valid = rows - gr;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    int gk = k0 + kq + q;
+                    reg[u * 4 + q] = load_chunk<VEC>(rsrc, gk < K, (int64_t)gk * s_k + (int64_t)gr * s_row, s_row, valid);
+                }
+            }
+        }
+    }
+
+    __device__ inline void store(uint16_t* lds, int tid) {
+        if constexpr (KMAJ) {
+            const int kc = (tid % 8) * 8;
+#pragma unroll
+            for (int i = 0; i < NREG; ++i) {
+                int r = tid / 8 + 32 * i;
+                *reinterpret_cast<u32x4*>(lds + r * H_LDK + kc) = reg[i];
+            }
+        } else {
+            const int kq = (tid % 16) * 4;
+#pragma unroll
+            for (int u = 0; u < NREG / 4; ++u) {
+                int rc = 8 * (tid / 16 + 16 * u);
+                const u32x4 r0 = reg[u * 4 + 0], r1 = reg[u * 4 + 1], r2 = reg[u * 4 + 2], r3 = reg[u * 4 + 3];
+                const uint32_t w0[4] = {r0.x, r0.y, r0.z, r0.w};
+                const uint32_t w1[4] = {r1.x, r1.y, r1.z, r1.w};
+                const uint32_t w2[4] = {r2.x, r2.y, r2.z, r2.w};
+                const uint32_t w3[4] = {r3.x, r3.y, r3.z, r3.w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    // element 2d (low halves) and 2d+1 (high halves) of each k row
+                    u32x2 lo, hi;
+                    lo.x = __builtin_amdgcn_perm(w1[d], w0[d], 0x05040100u);
+                    lo.y = __builtin_amdgcn_perm(w3[d], w2[d], 0x05040100u);
+                    hi.x = __builtin_amdgcn_perm(w1[d], w0[d], 0x07060302u);
+                    hi.y = __builtin_amdgcn_perm(w3[d], w2[d], 0x07060302u);
+                    *reinterpret_cast<u32x2*>(lds + (rc + 2 * d) * H_LDK + kq) = lo;
+                    *reinterpret_cast<u32x2*>(lds + (rc + 2 * d + 1) * H_LDK + kq) = hi;
+                }
+            }
+        }
+    }
+};
+
+// Maps a block index to its (tile_m, tile_n) so that the blocks one XCD runs
+// at a time cover a compact patch of C: blocks are dealt to the 8 XCDs round
+// robin, so consecutive ids on one XCD are made consecutive in a grouped
+// (GROUP_M rows at a time) column-major walk over the tiles.
+__device__ inline void tile_of(int bid, int nblocks, int tiles_m, int tiles_n, int& tm, int& tn) {
+    int lid = bid;
+    if (nblocks % 8 == 0) lid = (bid % 8) * (nblocks / 8) + bid / 8;
+    const int GM = 8;
+    int per_group = GM * tiles_n;
+    int g = lid / per_group;
+    int first_m = g * GM;
+    int gm = min(tiles_m - first_m, GM);
+    int in = lid % per_group;
+    tm = first_m + in % gm;
+    tn = in / gm;
+}
+
+template <int DT, bool AK, bool BK, int BM, int BN, bool VEC>
+__global__ __launch_bounds__(256) void gemm16_mfma_kernel(GemmArgs p) {
+    constexpr int WM = BM / 2, WN = BN / 2;    // wave tile
+    constexpr int FM = WM / 32, FN = WN / 32;  // 32x32 fragments per wave
+    __shared__ uint16_t lds[2][(BM + BN) * H_LDK];
+
+    const int tid = threadIdx.x;
+    const int lane = tid % 64, wave = tid / 64;
+    const int wm = wave / 2, wn = wave % 2;
+    const int b = blockIdx.y;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    // operand buffers of this batch: A rows are M, B rows are N
+    const uint16_t* A = reinterpret_cast<const uint16_t*>(p.a) + (int64_t)b * p.sa[0];
+    const uint16_t* B = reinterpret_cast<const uint16_t*>(p.b) + (int64_t)b * p.sb[0];
+    const int64_t a_bytes = 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1);
+    const int64_t b_bytes = 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1);
+    __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)min(a_bytes, (int64_t)0x7fffffff), 0x00020000);
+    __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)B, 0, (int)min(b_bytes, (int64_t)0x7fffffff), 0x00020000);
+
+    TileLoader<BM, AK, VEC> la;
+    TileLoader<BN, BK, VEC> lb;
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // A: row stride sa[1] (over M), k stride sa[2]; B: "row" = N with stride sb[2], k stride sb[1]
+    const int nk = (p.K + H_BK - 1) / H_BK;
+    la.load(ra, p.sa[1], p.sa[2], m0, p.M, 0, p.K, tid);
+    lb.load(rb, p.sb[2], p.sb[1], n0, p.N, 0, p.K, tid);
+    la.store(lds[0], tid);
+    lb.store(lds[0] + BM * H_LDK, tid);
+    __syncthreads();
+
+    const int frag_row = lane % 32;
+    const int frag_k = (lane / 32) * 8;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) {
+            la.load(ra, p.sa[1], p.sa[2], m0, p.M, (kt + 1) * H_BK, p.K, tid);
+            lb.load(rb, p.sb[2], p.sb[1], n0, p.N, (kt + 1) * H_BK, p.K, tid);
+        }
+        const uint16_t* As = lds[buf];
+        const uint16_t* Bs = lds[buf] + BM * H_LDK;
+#pragma unroll
+        for (int kk = 0; kk < H_BK; kk += 16) {
+            u32x4 af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                af[i] = *reinterpret_cast<const u32x4*>(As + (wm * WM + i * 32 + frag_row) * H_LDK + kk + frag_k);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                bf[j] = *reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 32 + frag_row) * H_LDK + kk + frag_k);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) acc[i][j] = mfma32<DT>(af[i], bf[j], acc[i][j]);
+        }
+        if (kt + 1 < nk) {
+            la.store(lds[buf ^ 1], tid);
+            lb.store(lds[buf ^ 1] + BM * H_LDK, tid);
+        }
+        __syncthreads();
+    }
+
+    // accumulator layout of v_mfma_f32_32x32x16: lane holds column lane%32,
+    // register r holds row (r/4)*8 + (lane/32)*4 + r%4
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int col = n0 + wn * WN + j * 32 + lane % 32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * WM + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4);
+                if (row < p.M && col < p.N) store_out<DT>(p, b, row, col, acc[i][j][r]);
+            }
+        }
+}
+
+// ----------------------------------------------------------------------------
+// host dispatch
+// ----------------------------------------------------------------------------
+
+enum class Kern { K0, GENERIC, SEQ32, MFMA256, MFMA128 };
+
+struct Plan {
+    Kern kern;
+    bool ak = true, bk = true, vec = true;
+    const char* name;
+};
+
+bool fits_i32(int64_t v) { return v >= 0 && v <= 0x7fffffff; }
+
+int64_t operand_extent_bytes(int64_t rows, int64_t s_row, int64_t cols, int64_t s_col, size_t es) {
+    return (int64_t)es * ((rows - 1) * s_row + (cols - 1) * s_col + 1);
+}
+
+Plan make_plan(const tvk_gemm_desc& d) {
+    Plan pl{Kern::GENERIC, true, true, true, "gemm_generic"};
+    if (d.K == 0) return Plan{Kern::K0, true, true, true, "gemm_k0_fill"};
+    const size_t es = dtype_size(d.dtype);
+    if (d.dtype == TVK_F32) {
+        pl.kern = Kern::SEQ32;
+        pl.name = "gemm32_seq_128x128";
+        return pl;
+    }
+    // which dimension of each operand is contiguous (size-1 dims have any stride)
+    const bool a_k = d.a_stride[2] == 1 || d.K == 1;
+    const bool a_m = d.a_stride[1] == 1 || d.M == 1;
+    const bool b_k = d.b_stride[1] == 1 || d.K == 1;
+    const bool b_n = d.b_stride[2] == 1 || d.N == 1;
+    if (!(a_k || a_m) || !(b_k || b_n)) return pl;
+    if (operand_extent_bytes(d.M, d.a_stride[1], d.K, d.a_stride[2], es) >= 0x7fffffff ||
+        operand_extent_bytes(d.N, d.b_stride[2], d.K, d.b_stride[1], es) >= 0x7fffffff)
+        return pl;
+    pl.ak = a_k;
+    pl.bk = b_k;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    bool vec = al16(d.a) && al16(d.b);
+    if (d.batch > 1) vec = vec && d.a_stride[0] % 8 == 0 && d.b_stride[0] % 8 == 0;
+    if (pl.ak) vec = vec && d.K % 8 == 0 && (d.M == 1 || d.a_stride[1] % 8 == 0);
+    else vec = vec && d.M % 8 == 0 && (d.K == 1 || d.a_stride[2] % 8 == 0);
+    if (pl.bk) vec = vec && d.K % 8 == 0 && (d.N == 1 || d.b_stride[2] % 8 == 0);
+    else vec = vec && d.N % 8 == 0 && (d.K == 1 || d.b_stride[1] % 8 == 0);
+    pl.vec = vec;
+    const int64_t t256 = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
+    if (d.M >= 256 && d.N >= 256 && t256 >= 192) {
+        pl.kern = Kern::MFMA256;
+        pl.name = "gemm16_mfma_256x256";
+    } else {
+        pl.kern = Kern::MFMA128;
+        pl.name = "gemm16_mfma_128x128";
+    }
+    return pl;
+}
+
+template <int DT, int BM, int BN>
+void launch_mfma(const Plan& pl, GemmArgs& p, dim3 grid, hipStream_t s) {
+#define TVK_L(AK, BK, VEC) hipLaunchKernelGGL((gemm16_mfma_kernel<DT, AK, BK, BM, BN, VEC>), grid, dim3(256), 0, s, p)
+    if (pl.vec) {
+        if (pl.ak && pl.bk) TVK_L(true, true, true);
+        else if (pl.ak) TVK_L(true, false, true);
+        else if (pl.bk) TVK_L(false, true, true);
+        else TVK_L(false, false, true);
+    } else {
+        if (pl.ak && pl.bk) TVK_L(true, true, false);
+        else if (pl.ak) TVK_L(true, false, false);
+        else if (pl.bk) TVK_L(false, true, false);
+        else TVK_L(false, false, false);
+    }
+#undef TVK_L
+}
+
+template <int DT>
+tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
+    GemmArgs p;
+    memset(&p, 0, sizeof(p));
+    p.a = d.a; p.b = d.b; p.bias = d.bias; p.c = d.c;
+    for (int i = 0; i < 3; ++i) {
+        p.sa[i] = d.a_stride[i]; p.sb[i] = d.b_stride[i]; p.sbias[i] = d.bias_stride[i]; p.sc[i] = d.c_stride[i];
+    }
+    p.M = (int)d.M; p.N = (int)d.N; p.K = (int)d.K;
+    p.alpha = (float)d.alpha;
+    p.beta = (float)d.beta;
+    p.has_bias = (d.bias != nullptr && d.beta != 0.0) ? 1 : 0;
+    p.act = d.activation;
+
+    const int64_t max_y = 65535;
+    for (int64_t b0 = 0; b0 < d.batch; b0 += max_y) {
+        const int nb = (int)std::min<int64_t>(max_y, d.batch - b0);
+        GemmArgs q = p;
+        q.batch = nb;
+        const size_t es = dtype_size(d.dtype);
+        q.a = (const char*)d.a + (size_t)(b0 * d.a_stride[0]) * es;
+        q.b = (const char*)d.b + (size_t)(b0 * d.b_stride[0]) * es;
+        if (q.has_bias) q.bias = (const char*)d.bias + (size_t)(b0 * d.bias_stride[0]) * es;
+        q.c = (char*)d.c + (size_t)(b0 * d.c_stride[0]) * es;
+        switch (pl.kern) {
+        case Kern::K0: {
+            int64_t total = (int64_t)nb * d.M * d.N;
+            hipLaunchKernelGGL(gemm_k0_kernel<DT>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, q);
+            break;
+        }
+        case Kern::GENERIC:
+            hipLaunchKernelGGL(gemm_generic_kernel<DT>, dim3((unsigned)((d.N + 15) / 16), (unsigned)((d.M + 15) / 16), nb), dim3(256), 0, s, q);
+            break;
+        case Kern::SEQ32:
+            if constexpr (DT == TVK_F32) {
+                q.tiles_m = (int)((d.M + S_BM - 1) / S_BM);
+                q.tiles_n = (int)((d.N + S_BN - 1) / S_BN);
+                hipLaunchKernelGGL(gemm32_seq_kernel, dim3(q.tiles_m * q.tiles_n, nb), dim3(256), 0, s, q);
+            }
+            break;
+        case Kern::MFMA256:
+        case Kern::MFMA128:
+            if constexpr (DT != TVK_F32) {
+                const int T = pl.kern == Kern::MFMA256 ? 256 : 128;
+                q.tiles_m = (int)((d.M + T - 1) / T);
+                q.tiles_n = (int)((d.N + T - 1) / T);
+                dim3 grid(q.tiles_m * q.tiles_n, nb);
+                if (T == 256) launch_mfma<DT, 256, 256>(pl, q, grid, s);
+                else launch_mfma<DT, 128, 128>(pl, q, grid, s);
+            }
+            break;
+        }
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_gemm: launch failed: ") + hipGetErrorString(e));
+    return TVK_OK;
+}
+
+tvk_status validate(const tvk_gemm_desc* d) {
+    if (!d) return fail(TVK_ERR_INVALID, "tvk_gemm: desc is NULL");
+    if (d->dtype != TVK_F32 && d->dtype != TVK_F16 && d->dtype != TVK_BF16)
+        return fail(TVK_ERR_UNSUPPORTED, "tvk_gemm: unsupported dtype " + std::to_string(d->dtype));
+    if (d->activation < TVK_ACT_NONE || d->activation > TVK_ACT_GELU)
+        return fail(TVK_ERR_INVALID, "tvk_gemm: invalid activation " + std::to_string(d->activation));
+    if (d->batch < 0 || d->M < 0 || d->N < 0 || d->K < 0) return fail(TVK_ERR_INVALID, "tvk_gemm: negative size");
+    if (!fits_i32(d->M) || !fits_i32(d->N) || !fits_i32(d->K) || !fits_i32(d->batch))
+        return fail(TVK_ERR_UNSUPPORTED, "tvk_gemm: a dimension exceeds 2^31-1");
+    for (int i = 0; i < 3; ++i)
+        if (d->a_stride[i] < 0 || d->b_stride[i] < 0 || d->c_stride[i] < 0 || d->bias_stride[i] < 0)
+            return fail(TVK_ERR_UNSUPPORTED, "tvk_gemm: negative strides are not supported");
+    if (d->batch == 0 || d->M == 0 || d->N == 0) return TVK_OK;
+    if (!d->c) return fail(TVK_ERR_INVALID, "tvk_gemm: c is NULL");
+    if (d->K > 0 && (!d->a || !d->b)) return fail(TVK_ERR_INVALID, "tvk_gemm: a or b is NULL");
+    return TVK_OK;
+}
+
+}  // namespace
+}  // namespace tvk
+
+using namespace tvk;
+
+extern "C" tvk_status tvk_gemm_plan(const tvk_gemm_desc* desc, char* name, size_t name_len) {
+    tvk_status st = validate(desc);
+    if (st != TVK_OK) return st;
+    if (!name || name_len == 0) return fail(TVK_ERR_INVALID, "tvk_gemm_plan: name buffer is empty");
+    const char* n = (desc->batch == 0 || desc->M == 0 || desc->N == 0) ? "none" : make_plan(*desc).name;
+    snprintf(name, name_len, "%s", n);
+    return TVK_OK;
+}
+
+extern "C" tvk_status tvk_gemm(const tvk_gemm_desc* desc) {
+    tvk_status st = validate(desc);
+    if (st != TVK_OK) return st;
+    const tvk_gemm_desc& d = *desc;
+    if (d.batch == 0 || d.M == 0 || d.N == 0) return TVK_OK;
+    Plan pl = make_plan(d);
+    hipStream_t s = resolve_stream(d.stream);
+    switch (d.dtype) {
+    case TVK_F32: return run<TVK_F32>(d, pl, s);
+    case TVK_F16: return run<TVK_F16>(d, pl, s);
+    default: return run<TVK_BF16>(d, pl, s);
+    }
+}

@@ -1,0 +1,298 @@
+// Runtime half of the C ABI: devices, one library stream per device, a
+// hipMalloc-backed caching allocator and stream-ordered copies.
+//
+// Replaces, for the dense-contraction path, the reference's Vulkan runtime:
+// VulkanContext device enumeration (src/vulkan/vulkan_context.cpp:251-357),
+// DeviceContext memory counters (src/vulkan/device_context.h:64-68), the
+// VulkanAllocator (src/vulkan/allocator.cpp:59-200) and its LRU buffer pools
+// (src/vulkan/cache.cpp:78-89). The reference records work and flushes it with
+// one blocking submit; here every call is enqueued on an in-order HIP stream,
+// so hazards between kernels are ordered by the stream itself.
+#include "tvk_common.h"
+
+#include <map>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+#include <cstring>
+
+namespace tvk {
+
+static thread_local std::string g_last_error;
+void set_error(const std::string& msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceState {
+    hipStream_t stream = nullptr;
+    // size class -> cached free blocks
+    std::map<size_t, std::vector<void*>> free_blocks;
+    size_t allocated = 0;   // bytes in live blocks (size-class rounded)
+    size_t peak = 0;
+    size_t reserved = 0;    // bytes obtained from hipMalloc and not yet released
+    size_t limit = 0;       // 0 = none
+};
+
+struct Block {
+    size_t size;
+    int device;
+};
+
+std::mutex g_mu;
+DeviceState g_dev[kMaxDevices];
+std::unordered_map<void*, Block> g_live;
+
+// Size classes: 512 B granules below 1 MiB, 2 MiB granules above, so cached
+// blocks are reused across nearby request sizes without unbounded waste.
+size_t size_class(size_t bytes) {
+    if (bytes < (1u << 20)) return (bytes + 511) & ~size_t(511);
+    const size_t g = size_t(2) << 20;
+    return (bytes + g - 1) / g * g;
+}
+
+bool valid_device(int d) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return false;
+    return d >= 0 && d < n && d < kMaxDevices;
+}
+
+// Releases all cached blocks of one device (caller holds g_mu).
+void release_cached_locked(int device) {
+    DeviceState& st = g_dev[device];
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(device);
+    if (st.stream) (void)hipStreamSynchronize(st.stream);
+    for (auto& kv : st.free_blocks) {
+        for (void* p : kv.second) {
+            (void)hipFree(p);
+            st.reserved -= kv.first;
+        }
+    }
+    st.free_blocks.clear();
+    (void)hipSetDevice(prev);
+}
+
+}  // namespace
+
+hipStream_t device_stream(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState& st = g_dev[device];
+    if (!st.stream) {
+        int prev = 0;
+        (void)hipGetDevice(&prev);
+        (void)hipSetDevice(device);
+        // default priority: the library never creates prioritised streams
+        (void)hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking);
+        (void)hipSetDevice(prev);
+    }
+    return st.stream;
+}
+
+}  // namespace tvk
+
+using namespace tvk;
+
+extern "C" {
+
+const char* tvk_last_error(void) { return g_last_error.c_str(); }
+
+tvk_status tvk_device_count(int* count) {
+    if (!count) return fail(TVK_ERR_INVALID, "tvk_device_count: count is NULL");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) n = 0;  // no runtime/GPU: zero devices, not an error
+    *count = n;
+    clear_error();
+    return TVK_OK;
+}
+
+tvk_status tvk_set_device(int device) {
+    if (!valid_device(device)) return fail(TVK_ERR_INVALID, "tvk_set_device: invalid device index " + std::to_string(device));
+    TVK_HIP_CHECK(hipSetDevice(device));
+    return TVK_OK;
+}
+
+tvk_status tvk_get_device(int* device) {
+    if (!device) return fail(TVK_ERR_INVALID, "tvk_get_device: device is NULL");
+    TVK_HIP_CHECK(hipGetDevice(device));
+    return TVK_OK;
+}
+
+tvk_status tvk_get_stream(int device, void** stream) {
+    if (!stream) return fail(TVK_ERR_INVALID, "tvk_get_stream: stream is NULL");
+    if (!valid_device(device)) return fail(TVK_ERR_INVALID, "tvk_get_stream: invalid device index " + std::to_string(device));
+    hipStream_t s = device_stream(device);
+    if (!s) return fail(TVK_ERR_DEVICE, "tvk_get_stream: could not create the device stream");
+    *stream = s;
+    return TVK_OK;
+}
+
+tvk_status tvk_synchronize(int device) {
+    if (!valid_device(device)) return fail(TVK_ERR_INVALID, "tvk_synchronize: invalid device index " + std::to_string(device));
+    int prev = 0;
+    TVK_HIP_CHECK(hipGetDevice(&prev));
+    TVK_HIP_CHECK(hipSetDevice(device));
+    hipError_t e = hipStreamSynchronize(device_stream(device));
+    (void)hipSetDevice(prev);
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_synchronize: ") + hipGetErrorString(e));
+    return TVK_OK;
+}
+
+tvk_status tvk_device_properties(int device, tvk_device_props* out) {
+    if (!out) return fail(TVK_ERR_INVALID, "tvk_device_properties: out is NULL");
+    if (!valid_device(device)) return fail(TVK_ERR_INVALID, "tvk_device_properties: invalid device index " + std::to_string(device));
+    hipDeviceProp_t p;
+    TVK_HIP_CHECK(hipGetDeviceProperties(&p, device));
+    memset(out, 0, sizeof(*out));
+    strncpy(out->name, p.name, sizeof(out->name) - 1);
+    strncpy(out->arch, p.gcnArchName, sizeof(out->arch) - 1);
+    out->total_memory = p.totalGlobalMem;
+    out->compute_units = p.multiProcessorCount;
+    out->clock_khz = p.clockRate;
+    out->wavefront_size = p.warpSize;
+    out->lds_per_block = p.sharedMemPerBlock;
+    out->pci_bus_id = p.pciBusID;
+    out->has_fp64 = 1;
+    out->has_fp16 = 1;
+    out->has_bf16 = 1;
+    return TVK_OK;
+}
+
+tvk_status tvk_malloc(int device, size_t bytes, void** out) {
+    if (!out) return fail(TVK_ERR_INVALID, "tvk_malloc: out is NULL");
+    *out = nullptr;
+    if (!valid_device(device)) return fail(TVK_ERR_INVALID, "tvk_malloc: invalid device index " + std::to_string(device));
+    if (bytes == 0) return TVK_OK;
+    const size_t sz = size_class(bytes);
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState& st = g_dev[device];
+    if (st.limit && st.allocated + sz > st.limit)
+        return fail(TVK_ERR_OOM, "tvk_malloc: allocating " + std::to_string(bytes) + " bytes would exceed the memory limit of " +
+                                     std::to_string(st.limit) + " bytes (" + std::to_string(st.allocated) + " in use)");
+    void* p = nullptr;
+    auto it = st.free_blocks.find(sz);
+    if (it != st.free_blocks.end() && !it->second.empty()) {
+        p = it->second.back();
+        it->second.pop_back();
+    } else {
+        int prev = 0;
+        (void)hipGetDevice(&prev);
+        (void)hipSetDevice(device);
+        hipError_t e = hipMalloc(&p, sz);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            // give the cache back and retry once
+            release_cached_locked(device);
+            (void)hipSetDevice(device);
+            e = hipMalloc(&p, sz);
+        }
+        (void)hipSetDevice(prev);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(TVK_ERR_OOM, "tvk_malloc: out of device memory allocating " + std::to_string(bytes) + " bytes");
+        }
+        st.reserved += sz;
+    }
+    g_live[p] = Block{sz, device};
+    st.allocated += sz;
+    if (st.allocated > st.peak) st.peak = st.allocated;
+    *out = p;
+    return TVK_OK;
+}
+
+tvk_status tvk_free(void* ptr) {
+    if (!ptr) return TVK_OK;
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_live.find(ptr);
+    if (it == g_live.end()) return fail(TVK_ERR_INVALID, "tvk_free: pointer was not allocated by tvk_malloc");
+    DeviceState& st = g_dev[it->second.device];
+    st.allocated -= it->second.size;
+    st.free_blocks[it->second.size].push_back(ptr);
+    g_live.erase(it);
+    return TVK_OK;
+}
+
+tvk_status tvk_empty_cache(int device) {
+    if (!valid_device(device)) return fail(TVK_ERR_INVALID, "tvk_empty_cache: invalid device index " + std::to_string(device));
+    std::lock_guard<std::mutex> lk(g_mu);
+    release_cached_locked(device);
+    return TVK_OK;
+}
+
+tvk_status tvk_pointer_device(const void* ptr, int* device) {
+    if (!device) return fail(TVK_ERR_INVALID, "tvk_pointer_device: device is NULL");
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_live.find(const_cast<void*>(ptr));
+    *device = it == g_live.end() ? -1 : it->second.device;
+    return TVK_OK;
+}
+
+tvk_status tvk_set_memory_limit(int device, size_t bytes) {
+    if (device < 0 || device >= kMaxDevices) return fail(TVK_ERR_INVALID, "tvk_set_memory_limit: invalid device index");
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_dev[device].limit = bytes;
+    return TVK_OK;
+}
+
+#define TVK_STAT_GETTER(fn, field)                                                          \
+    tvk_status fn(int device, size_t* bytes) {                                              \
+        if (!bytes) return fail(TVK_ERR_INVALID, #fn ": bytes is NULL");                    \
+        if (device < 0 || device >= kMaxDevices) return fail(TVK_ERR_INVALID, #fn ": invalid device index"); \
+        std::lock_guard<std::mutex> lk(g_mu);                                               \
+        *bytes = g_dev[device].field;                                                       \
+        return TVK_OK;                                                                      \
+    }
+TVK_STAT_GETTER(tvk_memory_allocated, allocated)
+TVK_STAT_GETTER(tvk_max_memory_allocated, peak)
+TVK_STAT_GETTER(tvk_memory_reserved, reserved)
+
+tvk_status tvk_reset_peak_memory_stats(int device) {
+    if (device < 0 || device >= kMaxDevices) return fail(TVK_ERR_INVALID, "tvk_reset_peak_memory_stats: invalid device index");
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_dev[device].peak = g_dev[device].allocated;
+    return TVK_OK;
+}
+
+tvk_status tvk_mem_get_info(int device, size_t* free_bytes, size_t* total_bytes) {
+    if (!free_bytes || !total_bytes) return fail(TVK_ERR_INVALID, "tvk_mem_get_info: NULL output");
+    if (!valid_device(device)) return fail(TVK_ERR_INVALID, "tvk_mem_get_info: invalid device index " + std::to_string(device));
+    int prev = 0;
+    TVK_HIP_CHECK(hipGetDevice(&prev));
+    TVK_HIP_CHECK(hipSetDevice(device));
+    hipError_t e = hipMemGetInfo(free_bytes, total_bytes);
+    (void)hipSetDevice(prev);
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_mem_get_info: ") + hipGetErrorString(e));
+    return TVK_OK;
+}
+
+tvk_status tvk_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream, int blocking) {
+    if (bytes == 0) return TVK_OK;
+    if (!dst || !src) return fail(TVK_ERR_INVALID, "tvk_memcpy_h2d: NULL pointer");
+    hipStream_t s = resolve_stream(stream);
+    TVK_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+    if (blocking) TVK_HIP_CHECK(hipStreamSynchronize(s));
+    return TVK_OK;
+}
+
+tvk_status tvk_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream, int blocking) {
+    if (bytes == 0) return TVK_OK;
+    if (!dst || !src) return fail(TVK_ERR_INVALID, "tvk_memcpy_d2h: NULL pointer");
+    hipStream_t s = resolve_stream(stream);
+    TVK_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+    if (blocking) TVK_HIP_CHECK(hipStreamSynchronize(s));
+    return TVK_OK;
+}
+
+tvk_status tvk_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return TVK_OK;
+    if (!dst || !src) return fail(TVK_ERR_INVALID, "tvk_memcpy_d2d: NULL pointer");
+    TVK_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, resolve_stream(stream)));
+    return TVK_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,85 @@
+// Shared definitions of the gfx950 dense-contraction library: status/error
+// plumbing, element types and the float32 <-> float16/bfloat16 conversions the
+// kernels and the host agree on.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/tvk_hip.h"
+
+namespace tvk {
+
+// Thread-local last error (tvk_last_error).
+void set_error(const std::string& msg);
+void clear_error();
+
+inline tvk_status fail(tvk_status code, const std::string& msg) {
+    set_error(msg);
+    return code;
+}
+
+#define TVK_HIP_CHECK(expr)                                                      \
+    do {                                                                         \
+        hipError_t _e = (expr);                                                  \
+        if (_e != hipSuccess)                                                    \
+            return ::tvk::fail(TVK_ERR_DEVICE, std::string(#expr " failed: ") +  \
+                                                   hipGetErrorString(_e));       \
+    } while (0)
+
+// Library stream of a device (created lazily); defined in runtime.hip.
+hipStream_t device_stream(int device);
+inline hipStream_t resolve_stream(void* s) {
+    if (s) return reinterpret_cast<hipStream_t>(s);
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    return device_stream(dev);
+}
+
+inline size_t dtype_size(int32_t dt) { return dt == TVK_F32 ? 4 : 2; }
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Element storage as raw 16-bit patterns for the 16-bit types.
+struct bf16_raw { uint16_t bits; };
+
+// float32 -> bfloat16, round to nearest even; NaN stays a quiet NaN. This is
+// the same rounding c10::BFloat16's float constructor performs.
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7fffu + lsb;
+    return (uint16_t)(u >> 16);
+}
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t b) {
+    return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+// Element type traits used by the kernels: load as float, store from float.
+template <int DT> struct elem;
+template <> struct elem<TVK_F32> {
+    typedef float T;
+    __device__ static inline float to_f32(T v) { return v; }
+    __device__ static inline T from_f32(float v) { return v; }
+};
+template <> struct elem<TVK_F16> {
+    typedef half_t T;
+    __device__ static inline float to_f32(T v) { return (float)v; }
+    __device__ static inline T from_f32(float v) { return (half_t)v; }  // v_cvt_f16_f32: RNE
+};
+template <> struct elem<TVK_BF16> {
+    typedef uint16_t T;
+    __device__ static inline float to_f32(T v) { return bf16_bits_to_f32(v); }
+    __device__ static inline T from_f32(float v) { return f32_to_bf16_bits(v); }
+};
+
+}  // namespace tvk
