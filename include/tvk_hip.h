@@ -137,7 +137,10 @@ tvk_status tvk_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream
  * beta are rounded to float32, the accumulate type the reference pushes them
  * in (src/vulkan/builders.h:119-140, src/api/ops/matmul.cpp:238-239).
  * Accumulation is float32 for every dtype; the result is rounded once to
- * `dtype` (round to nearest even). K == 0 gives act(beta*bias) or zeros
+ * `dtype` (round to nearest even). float32 always accumulates in the
+ * reference SIMD tile's order (fmaf over k in sequence per output,
+ * src/shaders/helpers/gemm_simd.slang:219-239); float16/bfloat16 use MFMA
+ * tiles whose order within 16 k is the hardware's, unless TVK_GEMM_EXACT. K == 0 gives act(beta*bias) or zeros
  * (src/api/ops/matmul.cpp:284-288).
  *
  * Replaces the dispatch in dispatch_matmul_shader
@@ -145,9 +148,18 @@ tvk_status tvk_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream
  * (src/shaders/ops/matmul_simd.slang:23-44) and matmul_coop_main
  * (src/shaders/ops/matmul_coop.slang:443-452), with the same 4-stride operand
  * model as TensorStrides (src/shaders/helpers/gemm.slang:3-9). */
+/* tvk_gemm_desc.flags */
+#define TVK_GEMM_EXACT 1u   /* every dtype in the reference SIMD tile's order:
+                               float32 operands, fmaf over k = 0..K-1 in
+                               sequence per output (bit-identical to that
+                               order); float16/bfloat16 then run at the float32
+                               matrix rate instead of their own */
+
 typedef struct {
     int32_t dtype;          /* tvk_dtype of A, B, bias and C */
     int32_t activation;     /* tvk_activation */
+    uint32_t flags;         /* TVK_GEMM_* */
+    int32_t reserved;       /* must be 0 */
     int64_t batch, M, N, K;
     const void* a; int64_t a_stride[3];
     const void* b; int64_t b_stride[3];

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from tests.gemm_cases import (TOL, assert_close, decode, oracle_mm, randint, randn, to_np)
+from tests.gemm_cases import (TOL, assert_bit_exact, assert_close, decode, oracle_mm, randint, randn, to_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -24,15 +24,16 @@ F16_TYPES = [torch.float16, torch.bfloat16]
 ALL_TYPES = [torch.float32, torch.float16, torch.bfloat16]
 
 
-def run(abi, a, b, out_shape, dtype, bias=None, alpha=1.0, beta=0.0, act=0):
+def run(abi, a, b, out_shape, dtype, bias=None, alpha=1.0, beta=0.0, act=0, exact=False):
     """Runs tvk_gemm on device copies of host views a/b (strides kept)."""
     da = a.to(DEV) if a.is_contiguous() else _device_view(a)
     db = b.to(DEV) if b.is_contiguous() else _device_view(b)
     dbias = None if bias is None else bias.to(DEV)
     c = torch.empty(out_shape, dtype=dtype, device=DEV)
-    abi.gemm(da, db, c, bias=dbias, alpha=alpha, beta=beta, activation=act)
+    abi.gemm(da, db, c, bias=dbias, alpha=alpha, beta=beta, activation=act, exact=exact)
     torch.cuda.synchronize()
-    return decode(to_np(c), dtype), abi.gemm_plan(da, db, c, bias=dbias, alpha=alpha, beta=beta, activation=act)
+    plan = abi.gemm_plan(da, db, c, bias=dbias, alpha=alpha, beta=beta, activation=act, exact=exact)
+    return decode(to_np(c), dtype), plan
 
 
 def _device_view(t: torch.Tensor) -> torch.Tensor:
@@ -51,7 +52,8 @@ def test_c1_fp32_mm_1024_bit_exact(gpu):
     b = randn((1024, 1024), torch.float32, 1)
     got, plan = run(gpu, a, b, (1024, 1024), torch.float32)
     ref = oracle_mm(a, b, torch.float32)
-    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"{plan}: not bit-exact"
+    assert plan.startswith("gemm_seq_mfma")
+    assert_bit_exact(got, ref, plan)
     # the config's tail: relu then sum (ops the reference runs on its CPU fallback)
     assert np.maximum(got, 0).astype(np.float64).sum() == np.maximum(ref, 0).astype(np.float64).sum()
 
@@ -157,7 +159,7 @@ def test_c5_ragged(gpu, dtype):
     got, plan = run(gpu, a, b, (1000, 3000), dtype)
     ref = oracle_mm(a, b, dtype)
     if dtype == torch.float32:
-        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), plan
+        assert_bit_exact(got, ref, plan)
     assert_close(got, ref, dtype, plan)
 
 
@@ -169,7 +171,7 @@ def test_c5_baddbmm(gpu, dtype):
     got, plan = run(gpu, b1, b2, (64, 512, 512), dtype, bias=inp, alpha=0.5, beta=1.0)
     ref = oracle_mm(b1, b2, dtype, bias=inp, alpha=0.5, beta=1.0)
     if dtype == torch.float32:
-        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), plan
+        assert_bit_exact(got, ref, plan)
     assert_close(got, ref, dtype, plan)
 
 
@@ -194,7 +196,7 @@ def test_c5_square_8192(gpu, dtype):
     rows = np.arange(0, 8192, 256) + rng.integers(0, 256, 32)
     ref = oracle_mm(a[torch.from_numpy(rows)], b, dtype)
     if dtype == torch.float32:
-        assert np.array_equal(got[rows].view(np.uint32), ref.view(np.uint32)), plan
+        assert_bit_exact(got[rows], ref, plan)
     assert_close(got[rows], ref, dtype, plan)
     bsum = decode(to_np(b), dtype).astype(np.float64).sum(axis=1)
     rs = decode(to_np(a), dtype).astype(np.float64) @ bsum
@@ -266,3 +268,35 @@ def test_fully_strided_operands_generic_path(gpu):
     got, plan = run(gpu, a, b, (32, 40), torch.float16)
     assert plan == "gemm_generic"
     assert_close(got, oracle_mm(a, b, torch.float16), torch.float16, plan)
+
+
+# ---------------------------------------------------------------------------
+# TVK_GEMM_EXACT: every dtype in the reference SIMD tile's order, bit for bit
+# ---------------------------------------------------------------------------
+
+def _exact_cases(dtype):
+    g = torch.Generator().manual_seed(160)
+    x = torch.rand((256, 784), generator=g).to(dtype)
+    w = ((torch.rand((4096, 784), generator=g) * 2 - 1) / 28.0).to(dtype)
+    bias = ((torch.rand((4096,), generator=g) * 2 - 1) / 28.0).to(dtype)
+    yield "mlp_fwd_addmm", x, w.t(), (256, 4096), dict(bias=bias, beta=1.0)
+    dy = torch.randn((256, 1024), generator=g).to(dtype)
+    yield "mlp_dW_transposed", dy.t(), x, (1024, 784), {}
+    yield "ragged", randn((1000, 777), dtype, 161), randn((777, 300), dtype, 162), (1000, 300), {}
+    q = randn((256, 512), dtype, 163)
+    k = randn((256, 512), dtype, 164)
+    yield ("head_strided_qk", q.view(256, 8, 64).transpose(0, 1),
+           k.view(256, 8, 64).transpose(0, 1).transpose(1, 2), (8, 256, 256), {})
+    inp = randn((8, 512, 512), dtype, 165)
+    yield ("baddbmm", randn((8, 512, 128), dtype, 166), randn((8, 128, 512), dtype, 167), (8, 512, 512),
+           dict(bias=inp, alpha=0.5, beta=1.0))
+    yield "gelu", randn((300, 200), dtype, 168), randn((200, 260), dtype, 169), (300, 260), dict(act=orc.ACT_RELU)
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+def test_exact_mode_bit_identical(gpu, dtype):
+    for name, a, b, shape, kw in _exact_cases(dtype):
+        got, plan = run(gpu, a, b, shape, dtype, exact=True, **kw)
+        assert plan.startswith("gemm_seq_mfma"), plan
+        ref = oracle_mm(a, b, dtype, **kw)
+        assert_bit_exact(got, ref, f"{name} {plan}")

@@ -15,6 +15,7 @@ _LIB_PATH = Path(__file__).resolve().parent / "libtvk_hip.so"
 TVK_OK, TVK_ERR_UNSUPPORTED, TVK_ERR_OOM, TVK_ERR_INVALID, TVK_ERR_DEVICE = range(5)
 TVK_F32, TVK_F16, TVK_BF16 = range(3)
 TVK_ACT_NONE, TVK_ACT_RELU, TVK_ACT_GELU = range(3)
+TVK_GEMM_EXACT = 1
 
 STATUS_NAMES = {0: "OK", 1: "UNSUPPORTED", 2: "OOM", 3: "INVALID", 4: "DEVICE"}
 
@@ -40,6 +41,8 @@ class GemmDesc(C.Structure):
     _fields_ = [
         ("dtype", C.c_int32),
         ("activation", C.c_int32),
+        ("flags", C.c_uint32),
+        ("reserved", C.c_int32),
         ("batch", C.c_int64),
         ("M", C.c_int64),
         ("N", C.c_int64),
@@ -152,7 +155,7 @@ def _strides3(t) -> tuple[int, int, int]:
     raise ValueError("expected a 2-D or 3-D tensor")
 
 
-def make_gemm_desc(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, stream=None) -> GemmDesc:
+def make_gemm_desc(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, stream=None, exact=False) -> GemmDesc:
     """Describes C = act(alpha*A@B + beta*bias) over 2-D or batched 3-D tensors.
 
     `bias` may be any tensor that broadcasts to C's shape (it is expanded with
@@ -164,6 +167,7 @@ def make_gemm_desc(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_N
     d = GemmDesc()
     d.dtype = _dtype_code(c.dtype)
     d.activation = activation
+    d.flags = TVK_GEMM_EXACT if exact else 0
     d.batch, d.M, d.N, d.K = batch, M, N, K
     d.a = a.data_ptr() if a.numel() else None
     d.a_stride = I64x3(*_strides3(a))
@@ -181,18 +185,18 @@ def make_gemm_desc(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_N
     return d
 
 
-def gemm(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, stream=None) -> None:
+def gemm(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, stream=None, exact=False) -> None:
     """Runs tvk_gemm on torch device tensors; `stream` defaults to torch's current stream."""
     import torch
 
     if stream is None and c.is_cuda:
         stream = torch.cuda.current_stream(c.device).cuda_stream
-    d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, stream)
+    d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, stream, exact)
     check(load().tvk_gemm(C.byref(d)))
 
 
-def gemm_plan(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE) -> str:
-    d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, None)
+def gemm_plan(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, exact=False) -> str:
+    d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, None, exact)
     buf = C.create_string_buffer(128)
     check(load().tvk_gemm_plan(C.byref(d), buf, 128))
     return buf.value.decode()

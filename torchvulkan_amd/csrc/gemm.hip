@@ -15,9 +15,11 @@
 //                LDS in a k-contiguous padded layout, double buffered. An operand
 //                whose contiguous dimension is M or N (a transposed view) is
 //                transposed in registers on its way into LDS, so no copy is made.
-//   gemm32_seq   float32 with the reference SIMD tile's summation order:
-//                every output accumulates fmaf(a_k, b_k, acc) for k = 0..K-1
-//                in sequence (src/shaders/helpers/gemm_simd.slang:219-239).
+//   gemm_seq_mfma  float32 (and every dtype under TVK_GEMM_EXACT) in the
+//                reference SIMD tile's summation order: every output
+//                accumulates fmaf(a_k, b_k, acc) for k = 0..K-1 in sequence
+//                (src/shaders/helpers/gemm_simd.slang:219-239), issued as
+//                v_mfma_f32_32x32x1f32 rank-1 updates (one rounding each).
 //   gemm_generic any strides / dtype, one thread per output, same order.
 #include "tvk_common.h"
 
@@ -106,103 +108,6 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
     for (int k = 0; k < p.K; ++k)
         acc = fmaf(elem<DT>::to_f32(a[(int64_t)k * p.sa[2]]), elem<DT>::to_f32(bm[(int64_t)k * p.sb[1]]), acc);
     store_out<DT>(p, b, row, col, acc);
-}
-
-// ----------------------------------------------------------------------------
-// float32, sequential-k order: 128x128 block, 256 threads, 8x8 per thread
-// ----------------------------------------------------------------------------
-
-constexpr int S_BM = 128, S_BN = 128, S_BK = 16;
-
-__global__ __launch_bounds__(256) void gemm32_seq_kernel(GemmArgs p) {
-#pragma clang fp contract(off)
-    __shared__ float As[2][S_BK][S_BM + 4];
-    __shared__ float Bs[2][S_BK][S_BN + 4];
-    const int tid = threadIdx.x;
-    const int tm = blockIdx.x / p.tiles_n, tn = blockIdx.x % p.tiles_n;
-    const int b = blockIdx.y;
-    const int m0 = tm * S_BM, n0 = tn * S_BN;
-    const float* A = reinterpret_cast<const float*>(p.a) + (int64_t)b * p.sa[0];
-    const float* B = reinterpret_cast<const float*>(p.b) + (int64_t)b * p.sb[0];
-
-    // loader mapping: 2048 elements of each tile, 8 per thread.
-    // A tile element (m, k): thread covers k-fastest when A is k-contiguous.
-    const bool a_kfast = p.sa[2] == 1;
-    const bool b_nfast = p.sb[2] == 1;
-    float ra[8], rb[8];
-
-    auto load = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            int e = tid + i * 256;
-            int m, k;
-            if (a_kfast) { k = e % S_BK; m = e / S_BK; }
-            else { m = e % S_BM; k = e / S_BM; }
-            int gm = m0 + m, gk = k0 + k;
-            ra[i] = (gm < p.M && gk < p.K) ? A[(int64_t)gm * p.sa[1] + (int64_t)gk * p.sa[2]] : 0.0f;
-            int n, kb;
-            if (b_nfast) { n = e % S_BN; kb = e / S_BN; }
-            else { kb = e % S_BK; n = e / S_BK; }
-            int gn = n0 + n, gkb = k0 + kb;
-            rb[i] = (gn < p.N && gkb < p.K) ? B[(int64_t)gkb * p.sb[1] + (int64_t)gn * p.sb[2]] : 0.0f;
-        }
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            int e = tid + i * 256;
-            int m, k;
-            if (a_kfast) { k = e % S_BK; m = e / S_BK; }
-            else { m = e % S_BM; k = e / S_BM; }
-            As[buf][k][m] = ra[i];
-            int n, kb;
-            if (b_nfast) { n = e % S_BN; kb = e / S_BN; }
-            else { kb = e % S_BK; n = e / S_BK; }
-            Bs[buf][kb][n] = rb[i];
-        }
-    };
-
-    const int tx = tid % 16, ty = tid / 16;
-    float acc[8][8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
-
-    const int nk = (p.K + S_BK - 1) / S_BK;
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) load((kt + 1) * S_BK);
-#pragma unroll
-        for (int k = 0; k < S_BK; ++k) {
-            // rows ty*4..+3 and 64+ty*4..+3; cols tx*4..+3 and 64+tx*4..+3
-            float4 a0 = *reinterpret_cast<const float4*>(&As[buf][k][ty * 4]);
-            float4 a1 = *reinterpret_cast<const float4*>(&As[buf][k][64 + ty * 4]);
-            float4 b0 = *reinterpret_cast<const float4*>(&Bs[buf][k][tx * 4]);
-            float4 b1 = *reinterpret_cast<const float4*>(&Bs[buf][k][64 + tx * 4]);
-            float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-            float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
-        }
-        if (kt + 1 < nk) store(buf ^ 1);
-        __syncthreads();
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        int row = m0 + (i < 4 ? ty * 4 + i : 64 + ty * 4 + i - 4);
-        if (row >= p.M) continue;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            int col = n0 + (j < 4 ? tx * 4 + j : 64 + tx * 4 + j - 4);
-            if (col < p.N) store_out<TVK_F32>(p, b, row, col, acc[i][j]);
-        }
-    }
 }
 
 // ----------------------------------------------------------------------------
@@ -428,10 +333,207 @@ __global__ __launch_bounds__(256) void gemm16_mfma_kernel(GemmArgs p) {
 }
 
 // ----------------------------------------------------------------------------
+// sequential-k kernel on v_mfma_f32_32x32x1f32 (all dtypes; exact mode)
+// ----------------------------------------------------------------------------
+//
+// v_mfma_f32_32x32x1f32 is two 32x32 outer products with k = 1: lane l gives
+// A[row l%32] and B[col l%32] of block l/32, and every output gets one fused
+// multiply-add with a single rounding. Feeding the same A to both blocks makes
+// one instruction a 32x64 rank-1 update, and issuing them for k = 0, 1, 2, ...
+// reproduces acc = fmaf(a_k, b_k, acc) in sequence for every output: the
+// reference SIMD tile's order, at the float32 matrix-core rate. Operands of
+// any input dtype are widened to float32 (exactly) on their way into LDS.
+
+constexpr int Q_BK = 16;   // k per LDS stage
+
+__device__ inline f32x32 mfma_x1(float a, float b, f32x32 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
+}
+
+// Widens the elements of a 16-byte chunk to float32.
+template <int DT>
+__device__ inline void widen_chunk(u32x4 v, float* out) {
+    if constexpr (DT == TVK_F32) {
+        out[0] = __builtin_bit_cast(float, v.x); out[1] = __builtin_bit_cast(float, v.y);
+        out[2] = __builtin_bit_cast(float, v.z); out[3] = __builtin_bit_cast(float, v.w);
+    } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (DT == TVK_F16) {
+                out[2 * i] = (float)__builtin_bit_cast(half_t, (uint16_t)(w[i] & 0xffffu));
+                out[2 * i + 1] = (float)__builtin_bit_cast(half_t, (uint16_t)(w[i] >> 16));
+            } else {
+                out[2 * i] = __builtin_bit_cast(float, w[i] << 16);
+                out[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
+            }
+        }
+    }
+}
+
+// One operand tile in its own global layout: OUTER rows x INNER contiguous
+// elements, staged as float32 in LDS with the same layout ([OUTER][INNER+4]).
+template <int DT, int OUTER, int INNER, bool VEC>
+struct SeqLoader {
+    static constexpr int ES = DT == TVK_F32 ? 4 : 2;
+    static constexpr int CE = 16 / ES;                    // elements per chunk
+    static constexpr int CPR = INNER / CE;                // chunks per row
+    static constexpr int NCH = OUTER * CPR;               // chunks per tile
+    static constexpr int PER = (NCH + 255) / 256;
+    static constexpr int LD = INNER + 4;
+    u32x4 reg[PER];
+
+    __device__ inline void load(__amdgpu_buffer_rsrc_t r, int64_t s_outer, int64_t s_inner, int outer0, int outer_n,
+                                int inner0, int inner_n, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int id = tid + 256 * i;
+            const int ro = id / CPR, ci = (id % CPR) * CE;
+            const int go = outer0 + ro, gi = inner0 + ci;
+            const bool ok = (id < NCH) && go < outer_n;
+            const int valid = inner_n - gi;
+            const int64_t off = (int64_t)go * s_outer + (int64_t)gi * s_inner;
+            if constexpr (VEC) {
+                reg[i] = buf_load16(r, (ok && valid > 0) ? (uint32_t)(off * ES) : kOOB);
+            } else {
+                uint32_t e[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < CE; ++j) {
+                    const uint32_t o = (ok && j < valid) ? (uint32_t)((off + j * s_inner) * ES) : kOOB;
+                    if constexpr (ES == 4) e[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)o, 0, 0);
+                    else e[j] = buf_load2(r, o);
+                }
+                if constexpr (ES == 4) reg[i] = u32x4{e[0], e[1], e[2], e[3]};
+                else reg[i] = u32x4{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
+            }
+        }
+    }
+
+    __device__ inline void store(float* lds, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int id = tid + 256 * i;
+            if (id >= NCH) break;
+            const int ro = id / CPR, ci = (id % CPR) * CE;
+            float f[8];
+            widen_chunk<DT>(reg[i], f);
+#pragma unroll
+            for (int j = 0; j < CE; j += 4)
+                *reinterpret_cast<f32x4*>(lds + ro * LD + ci + j) = f32x4{f[j], f[j + 1], f[j + 2], f[j + 3]};
+        }
+    }
+};
+
+template <int DT, bool AK, bool BK, int BM, int BN, bool VEC>
+__global__ __launch_bounds__(256) void gemm_seq_mfma_kernel(GemmArgs p) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 64;
+    // A k-major: [BM][Q_BK]; A m-major: [Q_BK][BM]. Same for B with N.
+    typedef SeqLoader<DT, AK ? BM : Q_BK, AK ? Q_BK : BM, VEC> LA;
+    typedef SeqLoader<DT, BK ? BN : Q_BK, BK ? Q_BK : BN, VEC> LB;
+    constexpr int A_FL = (AK ? BM : Q_BK) * LA::LD;
+    constexpr int B_FL = (BK ? BN : Q_BK) * LB::LD;
+    __shared__ float lds[2][A_FL + B_FL];
+
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int wm = wave / 2, wn = wave % 2;
+    const int b = blockIdx.y;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    constexpr int ES = DT == TVK_F32 ? 4 : 2;
+    const char* A = reinterpret_cast<const char*>(p.a) + (int64_t)b * p.sa[0] * ES;
+    const char* B = reinterpret_cast<const char*>(p.b) + (int64_t)b * p.sb[0] * ES;
+    const int64_t a_bytes = ES * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1);
+    const int64_t b_bytes = ES * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1);
+    __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)min(a_bytes, (int64_t)0x7fffffff), 0x00020000);
+    __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)B, 0, (int)min(b_bytes, (int64_t)0x7fffffff), 0x00020000);
+
+    LA la;
+    LB lb;
+    auto load = [&](int k0) {
+        if constexpr (AK) la.load(ra, p.sa[1], p.sa[2], m0, p.M, k0, p.K, tid);
+        else la.load(ra, p.sa[2], p.sa[1], k0, p.K, m0, p.M, tid);
+        if constexpr (BK) lb.load(rb, p.sb[2], p.sb[1], n0, p.N, k0, p.K, tid);
+        else lb.load(rb, p.sb[1], p.sb[2], k0, p.K, n0, p.N, tid);
+    };
+
+    f32x32 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 32; ++r) acc[i][j][r] = 0.0f;
+
+    const int nk = (p.K + Q_BK - 1) / Q_BK;
+    load(0);
+    la.store(lds[0], tid);
+    lb.store(lds[0] + A_FL, tid);
+    __syncthreads();
+    const int arow = wm * WM + lane % 32;   // + 32*i
+    const int bcol = wn * WN + lane;        // + 64*j
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load((kt + 1) * Q_BK);
+        const float* As = lds[buf];
+        const float* Bs = lds[buf] + A_FL;
+#pragma unroll
+        for (int k4 = 0; k4 < Q_BK; k4 += 4) {
+            float av[FM][4], bv[FN][4];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                if constexpr (AK) {
+                    f32x4 v = *reinterpret_cast<const f32x4*>(As + (arow + 32 * i) * LA::LD + k4);
+                    av[i][0] = v.x; av[i][1] = v.y; av[i][2] = v.z; av[i][3] = v.w;
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) av[i][q] = As[(k4 + q) * LA::LD + arow + 32 * i];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                if constexpr (BK) {
+                    f32x4 v = *reinterpret_cast<const f32x4*>(Bs + (bcol + 64 * j) * LB::LD + k4);
+                    bv[j][0] = v.x; bv[j][1] = v.y; bv[j][2] = v.z; bv[j][3] = v.w;
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) bv[j][q] = Bs[(k4 + q) * LB::LD + bcol + 64 * j];
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) acc[i][j] = mfma_x1(av[i][q], bv[j][q], acc[i][j]);
+        }
+        if (kt + 1 < nk) {
+            la.store(lds[buf ^ 1], tid);
+            lb.store(lds[buf ^ 1] + A_FL, tid);
+        }
+        __syncthreads();
+    }
+
+    // output of block r/16: row (rr/4)*8 + (lane/32)*4 + rr%4, column (r/16)*32 + lane%32
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 32; ++r) {
+                const int rr = r % 16;
+                const int row = m0 + wm * WM + 32 * i + (rr / 4) * 8 + (lane / 32) * 4 + rr % 4;
+                const int col = n0 + wn * WN + 64 * j + (r / 16) * 32 + lane % 32;
+                if (row < p.M && col < p.N) store_out<DT>(p, b, row, col, acc[i][j][r]);
+            }
+}
+
+// ----------------------------------------------------------------------------
 // host dispatch
 // ----------------------------------------------------------------------------
 
-enum class Kern { K0, GENERIC, SEQ32, MFMA256, MFMA128 };
+enum class Kern { K0, GENERIC, SEQ256, SEQ128, MFMA256, MFMA128 };
 
 struct Plan {
     Kern kern;
@@ -449,11 +551,6 @@ Plan make_plan(const tvk_gemm_desc& d) {
     Plan pl{Kern::GENERIC, true, true, true, "gemm_generic"};
     if (d.K == 0) return Plan{Kern::K0, true, true, true, "gemm_k0_fill"};
     const size_t es = dtype_size(d.dtype);
-    if (d.dtype == TVK_F32) {
-        pl.kern = Kern::SEQ32;
-        pl.name = "gemm32_seq_128x128";
-        return pl;
-    }
     // which dimension of each operand is contiguous (size-1 dims have any stride)
     const bool a_k = d.a_stride[2] == 1 || d.K == 1;
     const bool a_m = d.a_stride[1] == 1 || d.M == 1;
@@ -465,40 +562,51 @@ Plan make_plan(const tvk_gemm_desc& d) {
         return pl;
     pl.ak = a_k;
     pl.bk = b_k;
+    // 16-byte chunks need 16-byte aligned rows and whole chunks along the contiguous dimension
+    const int64_t ce = 16 / (int64_t)es;
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     bool vec = al16(d.a) && al16(d.b);
-    if (d.batch > 1) vec = vec && d.a_stride[0] % 8 == 0 && d.b_stride[0] % 8 == 0;
-    if (pl.ak) vec = vec && d.K % 8 == 0 && (d.M == 1 || d.a_stride[1] % 8 == 0);
-    else vec = vec && d.M % 8 == 0 && (d.K == 1 || d.a_stride[2] % 8 == 0);
-    if (pl.bk) vec = vec && d.K % 8 == 0 && (d.N == 1 || d.b_stride[2] % 8 == 0);
-    else vec = vec && d.N % 8 == 0 && (d.K == 1 || d.b_stride[1] % 8 == 0);
+    if (d.batch > 1) vec = vec && d.a_stride[0] % ce == 0 && d.b_stride[0] % ce == 0;
+    if (pl.ak) vec = vec && d.K % ce == 0 && (d.M == 1 || d.a_stride[1] % ce == 0);
+    else vec = vec && d.M % ce == 0 && (d.K == 1 || d.a_stride[2] % ce == 0);
+    if (pl.bk) vec = vec && d.K % ce == 0 && (d.N == 1 || d.b_stride[2] % ce == 0);
+    else vec = vec && d.N % ce == 0 && (d.K == 1 || d.b_stride[1] % ce == 0);
     pl.vec = vec;
     const int64_t t256 = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
-    if (d.M >= 256 && d.N >= 256 && t256 >= 192) {
-        pl.kern = Kern::MFMA256;
-        pl.name = "gemm16_mfma_256x256";
+    const bool big = d.M >= 256 && d.N >= 256 && t256 >= 192;
+    if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
+        pl.kern = big ? Kern::SEQ256 : Kern::SEQ128;
+        pl.name = big ? "gemm_seq_mfma_256x256" : "gemm_seq_mfma_128x128";
     } else {
-        pl.kern = Kern::MFMA128;
-        pl.name = "gemm16_mfma_128x128";
+        pl.kern = big ? Kern::MFMA256 : Kern::MFMA128;
+        pl.name = big ? "gemm16_mfma_256x256" : "gemm16_mfma_128x128";
     }
     return pl;
 }
 
+#define TVK_LAYOUT_SWITCH(PL, KERNEL, ...)                                                  \
+    do {                                                                                    \
+        if ((PL).vec) {                                                                     \
+            if ((PL).ak && (PL).bk) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, true, true, BM, BN, true>), grid, dim3(256), 0, s, p);   \
+            else if ((PL).ak) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, true, false, BM, BN, true>), grid, dim3(256), 0, s, p);        \
+            else if ((PL).bk) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, false, true, BM, BN, true>), grid, dim3(256), 0, s, p);        \
+            else hipLaunchKernelGGL((KERNEL<__VA_ARGS__, false, false, BM, BN, true>), grid, dim3(256), 0, s, p);                    \
+        } else {                                                                            \
+            if ((PL).ak && (PL).bk) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, true, true, BM, BN, false>), grid, dim3(256), 0, s, p);  \
+            else if ((PL).ak) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, true, false, BM, BN, false>), grid, dim3(256), 0, s, p);       \
+            else if ((PL).bk) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, false, true, BM, BN, false>), grid, dim3(256), 0, s, p);       \
+            else hipLaunchKernelGGL((KERNEL<__VA_ARGS__, false, false, BM, BN, false>), grid, dim3(256), 0, s, p);                   \
+        }                                                                                   \
+    } while (0)
+
 template <int DT, int BM, int BN>
 void launch_mfma(const Plan& pl, GemmArgs& p, dim3 grid, hipStream_t s) {
-#define TVK_L(AK, BK, VEC) hipLaunchKernelGGL((gemm16_mfma_kernel<DT, AK, BK, BM, BN, VEC>), grid, dim3(256), 0, s, p)
-    if (pl.vec) {
-        if (pl.ak && pl.bk) TVK_L(true, true, true);
-        else if (pl.ak) TVK_L(true, false, true);
-        else if (pl.bk) TVK_L(false, true, true);
-        else TVK_L(false, false, true);
-    } else {
-        if (pl.ak && pl.bk) TVK_L(true, true, false);
-        else if (pl.ak) TVK_L(true, false, false);
-        else if (pl.bk) TVK_L(false, true, false);
-        else TVK_L(false, false, false);
-    }
-#undef TVK_L
+    TVK_LAYOUT_SWITCH(pl, gemm16_mfma_kernel, DT);
+}
+
+template <int DT, int BM, int BN>
+void launch_seq(const Plan& pl, GemmArgs& p, dim3 grid, hipStream_t s) {
+    TVK_LAYOUT_SWITCH(pl, gemm_seq_mfma_kernel, DT);
 }
 
 template <int DT>
@@ -534,13 +642,16 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
         case Kern::GENERIC:
             hipLaunchKernelGGL(gemm_generic_kernel<DT>, dim3((unsigned)((d.N + 15) / 16), (unsigned)((d.M + 15) / 16), nb), dim3(256), 0, s, q);
             break;
-        case Kern::SEQ32:
-            if constexpr (DT == TVK_F32) {
-                q.tiles_m = (int)((d.M + S_BM - 1) / S_BM);
-                q.tiles_n = (int)((d.N + S_BN - 1) / S_BN);
-                hipLaunchKernelGGL(gemm32_seq_kernel, dim3(q.tiles_m * q.tiles_n, nb), dim3(256), 0, s, q);
-            }
+        case Kern::SEQ256:
+        case Kern::SEQ128: {
+            const int T = pl.kern == Kern::SEQ256 ? 256 : 128;
+            q.tiles_m = (int)((d.M + T - 1) / T);
+            q.tiles_n = (int)((d.N + T - 1) / T);
+            dim3 grid(q.tiles_m * q.tiles_n, nb);
+            if (T == 256) launch_seq<DT, 256, 256>(pl, q, grid, s);
+            else launch_seq<DT, 128, 128>(pl, q, grid, s);
             break;
+        }
         case Kern::MFMA256:
         case Kern::MFMA128:
             if constexpr (DT != TVK_F32) {
@@ -563,6 +674,8 @@ tvk_status validate(const tvk_gemm_desc* d) {
     if (!d) return fail(TVK_ERR_INVALID, "tvk_gemm: desc is NULL");
     if (d->dtype != TVK_F32 && d->dtype != TVK_F16 && d->dtype != TVK_BF16)
         return fail(TVK_ERR_UNSUPPORTED, "tvk_gemm: unsupported dtype " + std::to_string(d->dtype));
+    if ((d->flags & ~TVK_GEMM_EXACT) != 0 || d->reserved != 0)
+        return fail(TVK_ERR_INVALID, "tvk_gemm: unknown flags or nonzero reserved field");
     if (d->activation < TVK_ACT_NONE || d->activation > TVK_ACT_GELU)
         return fail(TVK_ERR_INVALID, "tvk_gemm: invalid activation " + std::to_string(d->activation));
     if (d->batch < 0 || d->M < 0 || d->N < 0 || d->K < 0) return fail(TVK_ERR_INVALID, "tvk_gemm: negative size");
