@@ -11,8 +11,10 @@
  *   - every entry point returns a tvk_status; tvk_last_error() gives the
  *     thread-local message of the last failure.
  *   - the library never owns caller tensors: pointers are borrowed for the call.
- *   - compute entry points are asynchronous on `stream` (a hipStream_t); a NULL
- *     stream means the library's own stream for the current device.
+ *   - compute and copy entry points are asynchronous on `stream` (a
+ *     hipStream_t); a NULL stream is HIP's default stream. tvk_get_stream
+ *     gives the library's own per-device stream, the one tvk_synchronize
+ *     waits for and the caching allocator's blocks are ordered on.
  *   - strides are in ELEMENTS, not bytes, and may be zero (broadcast) or any
  *     positive value; element offsets must fit in int64.
  */

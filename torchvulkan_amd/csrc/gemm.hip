@@ -49,24 +49,23 @@ struct GemmArgs {
 // ----------------------------------------------------------------------------
 
 __device__ inline float gelu_erf(float v) {
+#pragma clang fp contract(off)
     return 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
 }
 
 // v = acc*alpha; v = v + bias*beta; act(v). Contraction is off so the two
 // products round separately, as the reference's ext_mul/ext_add chain does.
-template <int DT>
-__device__ inline float epilogue_value(const GemmArgs& p, int b, int row, int col, float acc) {
+// Out of line, with scalar arguments only: the tiled kernels call it from an
+// unrolled epilogue and must keep their accumulators in registers.
+__device__ __noinline__ float epilogue_math(float acc, float alpha, int has_bias, float bv, float beta, int act) {
 #pragma clang fp contract(off)
-    float v = acc * p.alpha;
-    if (p.has_bias) {
-        typedef typename elem<DT>::T T;
-        const T* bias = reinterpret_cast<const T*>(p.bias);
-        float bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2]]);
-        float t = bv * p.beta;
+    float v = acc * alpha;
+    if (has_bias) {
+        float t = bv * beta;
         v = v + t;
     }
-    if (p.act == TVK_ACT_RELU) v = v > 0.0f ? v : (v != v ? v : 0.0f);
-    else if (p.act == TVK_ACT_GELU) v = gelu_erf(v);
+    if (act == TVK_ACT_RELU) v = v > 0.0f ? v : (v != v ? v : 0.0f);
+    else if (act == TVK_ACT_GELU) v = gelu_erf(v);
     return v;
 }
 
@@ -74,8 +73,31 @@ template <int DT>
 __device__ inline void store_out(const GemmArgs& p, int b, int row, int col, float acc) {
     typedef typename elem<DT>::T T;
     T* c = reinterpret_cast<T*>(p.c);
-    float v = epilogue_value<DT>(p, b, row, col, acc);
+    float v;
+    if (!p.has_bias && p.act == TVK_ACT_NONE) {
+#pragma clang fp contract(off)
+        v = acc * p.alpha;
+    } else {
+        float bv = 0.0f;
+        if (p.has_bias) {
+            const T* bias = reinterpret_cast<const T*>(p.bias);
+            bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2]]);
+        }
+        v = epilogue_math(acc, p.alpha, p.has_bias, bv, p.beta, p.act);
+    }
     c[(int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2]] = elem<DT>::from_f32(v);
+}
+
+// Epilogue of 16 accumulators of one lane that share a column and sit at
+// rows row0 + (r/4)*8 + r%4 (the 32x32 MFMA accumulator layout).
+template <int DT>
+__device__ inline void store_frag16(const GemmArgs& p, int b, int row0, int col, const f32x16& v) {
+    if (col >= p.N) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = row0 + (r / 4) * 8 + (r % 4);
+        if (row < p.M) store_out<DT>(p, b, row, col, v[r]);
+    }
 }
 
 // ----------------------------------------------------------------------------
@@ -288,27 +310,36 @@ __global__ __launch_bounds__(256) void gemm16_mfma_kernel(GemmArgs p) {
 
     const int frag_row = lane % 32;
     const int frag_k = (lane / 32) * 8;
+    const int a_off = (wm * WM + frag_row) * H_LDK + frag_k;
+    const int b_off = BM * H_LDK + (wn * WN + frag_row) * H_LDK + frag_k;
+    u32x4 af[2][FM], bf[2][FN];
+    auto read_frags = [&](const uint16_t* base, int kk, int slot) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[slot][i] = *reinterpret_cast<const u32x4*>(base + a_off + i * 32 * H_LDK + kk);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bf[slot][j] = *reinterpret_cast<const u32x4*>(base + b_off + j * 32 * H_LDK + kk);
+    };
     for (int kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
         if (kt + 1 < nk) {
             la.load(ra, p.sa[1], p.sa[2], m0, p.M, (kt + 1) * H_BK, p.K, tid);
             lb.load(rb, p.sb[2], p.sb[1], n0, p.N, (kt + 1) * H_BK, p.K, tid);
         }
-        const uint16_t* As = lds[buf];
-        const uint16_t* Bs = lds[buf] + BM * H_LDK;
+        const uint16_t* base = lds[buf];
+        read_frags(base, 0, 0);
 #pragma unroll
-        for (int kk = 0; kk < H_BK; kk += 16) {
-            u32x4 af[FM], bf[FN];
+        for (int kk = 0; kk < H_BK / 16; ++kk) {
+            const int cur = kk & 1;
+            // the fragments of step kk+1 are requested before the MFMAs of
+            // step kk are issued; the fences keep the scheduler from sinking
+            // the LDS reads back next to their use
+            if (kk + 1 < H_BK / 16) read_frags(base, (kk + 1) * 16, cur ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < FM; ++i)
-                af[i] = *reinterpret_cast<const u32x4*>(As + (wm * WM + i * 32 + frag_row) * H_LDK + kk + frag_k);
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
-                bf[j] = *reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 32 + frag_row) * H_LDK + kk + frag_k);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j) acc[i][j] = mfma32<DT>(af[i], bf[j], acc[i][j]);
+                for (int j = 0; j < FN; ++j) acc[i][j] = mfma32<DT>(af[cur][i], bf[cur][j], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (kt + 1 < nk) {
             la.store(lds[buf ^ 1], tid);
@@ -322,14 +353,8 @@ __global__ __launch_bounds__(256) void gemm16_mfma_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int col = n0 + wn * WN + j * 32 + lane % 32;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * WM + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4);
-                if (row < p.M && col < p.N) store_out<DT>(p, b, row, col, acc[i][j][r]);
-            }
-        }
+        for (int j = 0; j < FN; ++j)
+            store_frag16<DT>(p, b, m0 + wm * WM + i * 32 + (lane / 32) * 4, n0 + wn * WN + j * 32 + lane % 32, acc[i][j]);
 }
 
 // ----------------------------------------------------------------------------
@@ -354,8 +379,10 @@ __device__ inline f32x32 mfma_x1(float a, float b, f32x32 c) {
 template <int DT>
 __device__ inline void widen_chunk(u32x4 v, float* out) {
     if constexpr (DT == TVK_F32) {
-        out[0] = __builtin_bit_cast(float, v.x); out[1] = __builtin_bit_cast(float, v.y);
-        out[2] = __builtin_bit_cast(float, v.z); out[3] = __builtin_bit_cast(float, v.w);
+        // bit-cast the whole vector: clang 22 miscompiles a bit-cast of one
+        // ext_vector element (it reads element 0 for every element)
+        const f32x4 fv = __builtin_bit_cast(f32x4, v);
+        out[0] = fv.x; out[1] = fv.y; out[2] = fv.z; out[3] = fv.w;
     } else {
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -519,14 +546,12 @@ __global__ __launch_bounds__(256) void gemm_seq_mfma_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 32; ++r) {
-                const int rr = r % 16;
-                const int row = m0 + wm * WM + 32 * i + (rr / 4) * 8 + (lane / 32) * 4 + rr % 4;
-                const int col = n0 + wn * WN + 64 * j + (r / 16) * 32 + lane % 32;
-                if (row < p.M && col < p.N) store_out<DT>(p, b, row, col, acc[i][j][r]);
-            }
+        for (int j = 0; j < FN; ++j) {
+            const int row0 = m0 + wm * WM + 32 * i + (lane / 32) * 4;
+            const int col0 = n0 + wn * WN + 64 * j + lane % 32;
+            store_frag16<DT>(p, b, row0, col0, acc[i][j].lo);
+            store_frag16<DT>(p, b, row0, col0 + 32, acc[i][j].hi);
+        }
 }
 
 // ----------------------------------------------------------------------------

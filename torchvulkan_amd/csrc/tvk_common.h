@@ -30,12 +30,8 @@ inline tvk_status fail(tvk_status code, const std::string& msg) {
 
 // Library stream of a device (created lazily); defined in runtime.hip.
 hipStream_t device_stream(int device);
-inline hipStream_t resolve_stream(void* s) {
-    if (s) return reinterpret_cast<hipStream_t>(s);
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    return device_stream(dev);
-}
+// A NULL stream handle is HIP's default (null) stream, as in every HIP library.
+inline hipStream_t resolve_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline size_t dtype_size(int32_t dt) { return dt == TVK_F32 ? 4 : 2; }
 
