@@ -26,6 +26,7 @@
 #include <algorithm>
 #include <cstring>
 #include <cstdio>
+#include <cstdlib>
 
 namespace tvk {
 namespace {
@@ -185,9 +186,10 @@ __device__ inline u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, bool row_ok, int64_
 //   else: the operand's row stride is 1 (M or N contiguous): thread t loads,
 //         for k = 4*(t%16) + 0..3, eight consecutive rows starting at
 //         8*(t/16 + 16*u), and transposes the 4x8 block into 8 rows of 4 k.
-template <int R, bool KMAJ, bool VEC>
+template <int R, bool KMAJ, bool VEC, int NT>
 struct TileLoader {
-    static constexpr int NREG = R / 32;   // 16-byte registers per thread per stage
+    static constexpr int NREG = R * 8 / NT;   // 16-byte registers per thread per stage
+    static_assert(KMAJ || NREG % 4 == 0, "transposing loader works on 4 k rows");
     u32x4 reg[NREG];
 
     __device__ inline void load(__amdgpu_buffer_rsrc_t rsrc, int64_t s_row, int64_t s_k, int row0, int rows, int k0, int K, int tid) {
@@ -195,7 +197,7 @@ struct TileLoader {
             const int kc = (tid % 8) * 8;
 #pragma unroll
             for (int i = 0; i < NREG; ++i) {
-                int r = tid / 8 + 32 * i;
+                int r = tid / 8 + (NT / 8) * i;
                 int gr = row0 + r, gk = k0 + kc;
                 int valid = K - gk;
                 reg[i] = load_chunk<VEC>(rsrc, gr < rows, (int64_t)gr * s_row + (int64_t)gk * s_k, s_k, valid);
@@ -204,7 +206,7 @@ struct TileLoader {
             const int kq = (tid % 16) * 4;
 #pragma unroll
             for (int u = 0; u < NREG / 4; ++u) {
-                int rc = 8 * (tid / 16 + 16 * u);
+                int rc = 8 * (tid / 16 + (NT / 16) * u);
                 int gr = row0 + rc;
                 int valid = rows - gr;
 #pragma unroll
@@ -221,14 +223,14 @@ struct TileLoader {
             const int kc = (tid % 8) * 8;
 #pragma unroll
             for (int i = 0; i < NREG; ++i) {
-                int r = tid / 8 + 32 * i;
+                int r = tid / 8 + (NT / 8) * i;
                 *reinterpret_cast<u32x4*>(lds + r * H_LDK + kc) = reg[i];
             }
         } else {
             const int kq = (tid % 16) * 4;
 #pragma unroll
             for (int u = 0; u < NREG / 4; ++u) {
-                int rc = 8 * (tid / 16 + 16 * u);
+                int rc = 8 * (tid / 16 + (NT / 16) * u);
                 const u32x4 r0 = reg[u * 4 + 0], r1 = reg[u * 4 + 1], r2 = reg[u * 4 + 2], r3 = reg[u * 4 + 3];
                 const uint32_t w0[4] = {r0.x, r0.y, r0.z, r0.w};
                 const uint32_t w1[4] = {r1.x, r1.y, r1.z, r1.w};
@@ -267,15 +269,17 @@ __device__ inline void tile_of(int bid, int nblocks, int tiles_m, int tiles_n, i
     tn = in / gm;
 }
 
-template <int DT, bool AK, bool BK, int BM, int BN, bool VEC>
-__global__ __launch_bounds__(256) void gemm16_mfma_kernel(GemmArgs p) {
-    constexpr int WM = BM / 2, WN = BN / 2;    // wave tile
+// WGN: waves along N (2 or 4); 2 waves along M. NT = 128 * WGN threads.
+template <int DT, bool AK, bool BK, int BM, int BN, bool VEC, int WGN>
+__global__ __launch_bounds__(128 * WGN) void gemm16_mfma_kernel(GemmArgs p) {
+    constexpr int NT = 128 * WGN;
+    constexpr int WM = BM / 2, WN = BN / WGN;  // wave tile
     constexpr int FM = WM / 32, FN = WN / 32;  // 32x32 fragments per wave
     __shared__ uint16_t lds[2][(BM + BN) * H_LDK];
 
     const int tid = threadIdx.x;
     const int lane = tid % 64, wave = tid / 64;
-    const int wm = wave / 2, wn = wave % 2;
+    const int wm = wave / WGN, wn = wave % WGN;
     const int b = blockIdx.y;
     int tm, tn;
     tile_of(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, tm, tn);
@@ -289,8 +293,8 @@ __global__ __launch_bounds__(256) void gemm16_mfma_kernel(GemmArgs p) {
     __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)min(a_bytes, (int64_t)0x7fffffff), 0x00020000);
     __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)B, 0, (int)min(b_bytes, (int64_t)0x7fffffff), 0x00020000);
 
-    TileLoader<BM, AK, VEC> la;
-    TileLoader<BN, BK, VEC> lb;
+    TileLoader<BM, AK, VEC, NT> la;
+    TileLoader<BN, BK, VEC, NT> lb;
 
     f32x16 acc[FM][FN];
 #pragma unroll
@@ -319,31 +323,55 @@ __global__ __launch_bounds__(256) void gemm16_mfma_kernel(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) bf[slot][j] = *reinterpret_cast<const u32x4*>(base + b_off + j * 32 * H_LDK + kk);
     };
+    // One LDS stage per iteration, four MFMA steps of 16 k each. The global
+    // loads of the next stage are interleaved with the MFMAs of step 0 and
+    // their LDS stores (into the other buffer) with the MFMAs of step 3, so
+    // the matrix pipe stays busy while the memory instructions issue. On the
+    // last iteration the loads fall outside K and read zeros (buffer range
+    // check), which keeps the loop body free of branches.
+    constexpr int NMF = FM * FN;
     for (int kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
-        if (kt + 1 < nk) {
-            la.load(ra, p.sa[1], p.sa[2], m0, p.M, (kt + 1) * H_BK, p.K, tid);
-            lb.load(rb, p.sb[2], p.sb[1], n0, p.N, (kt + 1) * H_BK, p.K, tid);
-        }
         const uint16_t* base = lds[buf];
         read_frags(base, 0, 0);
 #pragma unroll
         for (int kk = 0; kk < H_BK / 16; ++kk) {
             const int cur = kk & 1;
-            // the fragments of step kk+1 are requested before the MFMAs of
-            // step kk are issued; the fences keep the scheduler from sinking
-            // the LDS reads back next to their use
             if (kk + 1 < H_BK / 16) read_frags(base, (kk + 1) * 16, cur ^ 1);
-            __builtin_amdgcn_sched_barrier(0);
+            if (kk == 0) {
+                la.load(ra, p.sa[1], p.sa[2], m0, p.M, (kt + 1) * H_BK, p.K, tid);
+                lb.load(rb, p.sb[2], p.sb[1], n0, p.N, (kt + 1) * H_BK, p.K, tid);
+            }
+            if (kk == H_BK / 16 - 1) {
+                la.store(lds[buf ^ 1], tid);
+                lb.store(lds[buf ^ 1] + BM * H_LDK, tid);
+            }
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j) acc[i][j] = mfma32<DT>(af[cur][i], bf[cur][j], acc[i][j]);
+            if (kk + 1 < H_BK / 16) {
+                // next step's fragment reads first, then the MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
+            }
+            if (kk == 0) {
+                // one global load between consecutive MFMAs
+#pragma unroll
+                for (int q = 0; q < NMF; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+            } else if (kk == H_BK / 16 - 1) {
+                // LDS stores of the next stage between the MFMAs
+#pragma unroll
+                for (int q = 0; q < NMF; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
+                }
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x008, NMF, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
-        }
-        if (kt + 1 < nk) {
-            la.store(lds[buf ^ 1], tid);
-            lb.store(lds[buf ^ 1] + BM * H_LDK, tid);
         }
         __syncthreads();
     }
@@ -558,7 +586,7 @@ __global__ __launch_bounds__(256) void gemm_seq_mfma_kernel(GemmArgs p) {
 // host dispatch
 // ----------------------------------------------------------------------------
 
-enum class Kern { K0, GENERIC, SEQ256, SEQ128, MFMA256, MFMA128 };
+enum class Kern { K0, GENERIC, SEQ256, SEQ128, MFMA256, MFMA256W8, MFMA128 };
 
 struct Plan {
     Kern kern;
@@ -602,36 +630,40 @@ Plan make_plan(const tvk_gemm_desc& d) {
     if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
         pl.kern = big ? Kern::SEQ256 : Kern::SEQ128;
         pl.name = big ? "gemm_seq_mfma_256x256" : "gemm_seq_mfma_128x128";
+    } else if (big) {
+        static const bool w8 = getenv("TVK_GEMM_W4") == nullptr;
+        pl.kern = w8 ? Kern::MFMA256W8 : Kern::MFMA256;
+        pl.name = w8 ? "gemm16_mfma_256x256_w8" : "gemm16_mfma_256x256";
     } else {
-        pl.kern = big ? Kern::MFMA256 : Kern::MFMA128;
-        pl.name = big ? "gemm16_mfma_256x256" : "gemm16_mfma_128x128";
+        pl.kern = Kern::MFMA128;
+        pl.name = "gemm16_mfma_128x128";
     }
     return pl;
 }
 
-#define TVK_LAYOUT_SWITCH(PL, KERNEL, ...)                                                  \
+#define TVK_LAYOUT_SWITCH(PL, NTHR, KERNEL, ...)                                            \
     do {                                                                                    \
         if ((PL).vec) {                                                                     \
-            if ((PL).ak && (PL).bk) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, true, true, BM, BN, true>), grid, dim3(256), 0, s, p);   \
-            else if ((PL).ak) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, true, false, BM, BN, true>), grid, dim3(256), 0, s, p);        \
-            else if ((PL).bk) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, false, true, BM, BN, true>), grid, dim3(256), 0, s, p);        \
-            else hipLaunchKernelGGL((KERNEL<__VA_ARGS__, false, false, BM, BN, true>), grid, dim3(256), 0, s, p);                    \
+            if ((PL).ak && (PL).bk) hipLaunchKernelGGL((KERNEL<DT, true, true, BM, BN, true __VA_ARGS__>), grid, dim3(NTHR), 0, s, p);   \
+            else if ((PL).ak) hipLaunchKernelGGL((KERNEL<DT, true, false, BM, BN, true __VA_ARGS__>), grid, dim3(NTHR), 0, s, p);        \
+            else if ((PL).bk) hipLaunchKernelGGL((KERNEL<DT, false, true, BM, BN, true __VA_ARGS__>), grid, dim3(NTHR), 0, s, p);        \
+            else hipLaunchKernelGGL((KERNEL<DT, false, false, BM, BN, true __VA_ARGS__>), grid, dim3(NTHR), 0, s, p);                    \
         } else {                                                                            \
-            if ((PL).ak && (PL).bk) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, true, true, BM, BN, false>), grid, dim3(256), 0, s, p);  \
-            else if ((PL).ak) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, true, false, BM, BN, false>), grid, dim3(256), 0, s, p);       \
-            else if ((PL).bk) hipLaunchKernelGGL((KERNEL<__VA_ARGS__, false, true, BM, BN, false>), grid, dim3(256), 0, s, p);       \
-            else hipLaunchKernelGGL((KERNEL<__VA_ARGS__, false, false, BM, BN, false>), grid, dim3(256), 0, s, p);                   \
+            if ((PL).ak && (PL).bk) hipLaunchKernelGGL((KERNEL<DT, true, true, BM, BN, false __VA_ARGS__>), grid, dim3(NTHR), 0, s, p);  \
+            else if ((PL).ak) hipLaunchKernelGGL((KERNEL<DT, true, false, BM, BN, false __VA_ARGS__>), grid, dim3(NTHR), 0, s, p);       \
+            else if ((PL).bk) hipLaunchKernelGGL((KERNEL<DT, false, true, BM, BN, false __VA_ARGS__>), grid, dim3(NTHR), 0, s, p);       \
+            else hipLaunchKernelGGL((KERNEL<DT, false, false, BM, BN, false __VA_ARGS__>), grid, dim3(NTHR), 0, s, p);                   \
         }                                                                                   \
     } while (0)
 
-template <int DT, int BM, int BN>
+template <int DT, int BM, int BN, int WGN>
 void launch_mfma(const Plan& pl, GemmArgs& p, dim3 grid, hipStream_t s) {
-    TVK_LAYOUT_SWITCH(pl, gemm16_mfma_kernel, DT);
+    TVK_LAYOUT_SWITCH(pl, 128 * WGN, gemm16_mfma_kernel, , WGN);
 }
 
 template <int DT, int BM, int BN>
 void launch_seq(const Plan& pl, GemmArgs& p, dim3 grid, hipStream_t s) {
-    TVK_LAYOUT_SWITCH(pl, gemm_seq_mfma_kernel, DT);
+    TVK_LAYOUT_SWITCH(pl, 256, gemm_seq_mfma_kernel);
 }
 
 template <int DT>
@@ -678,14 +710,16 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
             break;
         }
         case Kern::MFMA256:
+        case Kern::MFMA256W8:
         case Kern::MFMA128:
             if constexpr (DT != TVK_F32) {
-                const int T = pl.kern == Kern::MFMA256 ? 256 : 128;
+                const int T = pl.kern == Kern::MFMA128 ? 128 : 256;
                 q.tiles_m = (int)((d.M + T - 1) / T);
                 q.tiles_n = (int)((d.N + T - 1) / T);
                 dim3 grid(q.tiles_m * q.tiles_n, nb);
-                if (T == 256) launch_mfma<DT, 256, 256>(pl, q, grid, s);
-                else launch_mfma<DT, 128, 128>(pl, q, grid, s);
+                if (pl.kern == Kern::MFMA256W8) launch_mfma<DT, 256, 256, 4>(pl, q, grid, s);
+                else if (pl.kern == Kern::MFMA256) launch_mfma<DT, 256, 256, 2>(pl, q, grid, s);
+                else launch_mfma<DT, 128, 128, 2>(pl, q, grid, s);
             }
             break;
         }
