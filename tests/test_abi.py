@@ -69,6 +69,8 @@ def test_gemm_validation_codes(field, value, status):
 @pytest.mark.parametrize("a_stride,b_stride,dtype,M,N,K,want", [
     ((0, 8192, 1), (0, 8192, 1), _abi.TVK_F16, 8192, 8192, 8192, "gemm16_mfma_256x256_w8"),
     ((0, 4096, 1), (0, 1, 4096), _abi.TVK_F16, 256, 4096, 4096, "gemm16_mfma_128x128"),
+    ((0, 4096, 1), (0, 14336, 1), _abi.TVK_F16, 16, 14336, 4096, "gemm16_skinny_bn"),
+    ((0, 4096, 1), (0, 1, 4096), _abi.TVK_BF16, 8, 4096, 4096, "gemm16_skinny_bk"),
     ((0, 3, 5), (0, 4, 1), _abi.TVK_F16, 8, 4, 4, "gemm_generic"),
     ((0, 1024, 1), (0, 1024, 1), _abi.TVK_F32, 1024, 1024, 1024, "gemm_seq_mfma_128x128"),
     ((0, 4, 1), (0, 4, 1), _abi.TVK_BF16, 4, 4, 0, "gemm_k0_fill"),

@@ -300,3 +300,44 @@ def test_exact_mode_bit_identical(gpu, dtype):
         assert plan.startswith("gemm_seq_mfma"), plan
         ref = oracle_mm(a, b, dtype, **kw)
         assert_bit_exact(got, ref, f"{name} {plan}")
+
+
+# ---------------------------------------------------------------------------
+# M <= 16: the HBM-streaming kernel (split K, last-arrival reduction)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("M,N,K,bt,aligned", [
+    (16, 14336, 4096, False, True),   # C5 skinny, B row-major
+    (16, 14336, 4096, True, True),    # B as a transposed weight view (k-contiguous)
+    (1, 4096, 4096, True, True),      # one token through a linear
+    (7, 1000, 2000, False, True),     # ragged rows / last strip
+    (5, 777, 999, False, False),      # K and N not multiples of 8: element loads
+    (16, 256, 64, True, True),        # K too small to split
+])
+def test_skinny_shapes(gpu, dtype, M, N, K, bt, aligned):
+    a = randn((M, K), dtype, 200)
+    b = randn((N, K), dtype, 201).t() if bt else randn((K, N), dtype, 201)
+    bias = randn((N,), dtype, 202)
+    got, plan = run(gpu, a, b, (M, N), dtype, bias=bias, alpha=0.5, beta=1.0)
+    assert plan.startswith("gemm16_skinny"), plan
+    assert_close(got, oracle_mm(a, b, dtype, bias=bias, alpha=0.5, beta=1.0), dtype, plan)
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+def test_skinny_batched_and_repeated(gpu, dtype):
+    # batched decode-like bmm; two calls in a row reuse the arrival counters
+    a = randn((6, 4, 512), dtype, 210)
+    b = randn((6, 512, 640), dtype, 211)
+    for _ in range(2):
+        got, plan = run(gpu, a, b, (6, 4, 640), dtype)
+        assert plan.startswith("gemm16_skinny"), plan
+        assert_close(got, oracle_mm(a, b, dtype), dtype, plan)
+
+
+def test_skinny_exact_mode_uses_sequential_kernel(gpu):
+    a = randn((16, 1024), torch.float16, 220)
+    b = randn((1024, 2048), torch.float16, 221)
+    got, plan = run(gpu, a, b, (16, 2048), torch.float16, exact=True)
+    assert plan.startswith("gemm_seq_mfma"), plan
+    assert_bit_exact(got, oracle_mm(a, b, torch.float16), plan)

@@ -21,7 +21,7 @@
 //                (src/shaders/helpers/gemm_simd.slang:219-239), issued as
 //                v_mfma_f32_32x32x1f32 rank-1 updates (one rounding each).
 //   gemm_generic any strides / dtype, one thread per output, same order.
-#include "tvk_common.h"
+#include "gemm_common.h"
 
 #include <algorithm>
 #include <cstring>
@@ -30,76 +30,6 @@
 
 namespace tvk {
 namespace {
-
-struct GemmArgs {
-    const void* a;
-    const void* b;
-    const void* bias;
-    void* c;
-    int64_t sa[3], sb[3], sbias[3], sc[3];
-    int M, N, K;
-    int batch;
-    float alpha, beta;
-    int has_bias;
-    int act;
-    int tiles_m, tiles_n;
-};
-
-// ----------------------------------------------------------------------------
-// epilogue (shared by all kernels)
-// ----------------------------------------------------------------------------
-
-__device__ inline float gelu_erf(float v) {
-#pragma clang fp contract(off)
-    return 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
-}
-
-// v = acc*alpha; v = v + bias*beta; act(v). Contraction is off so the two
-// products round separately, as the reference's ext_mul/ext_add chain does.
-// Out of line, with scalar arguments only: the tiled kernels call it from an
-// unrolled epilogue and must keep their accumulators in registers.
-__device__ __noinline__ float epilogue_math(float acc, float alpha, int has_bias, float bv, float beta, int act) {
-#pragma clang fp contract(off)
-    float v = acc * alpha;
-    if (has_bias) {
-        float t = bv * beta;
-        v = v + t;
-    }
-    if (act == TVK_ACT_RELU) v = v > 0.0f ? v : (v != v ? v : 0.0f);
-    else if (act == TVK_ACT_GELU) v = gelu_erf(v);
-    return v;
-}
-
-template <int DT>
-__device__ inline void store_out(const GemmArgs& p, int b, int row, int col, float acc) {
-    typedef typename elem<DT>::T T;
-    T* c = reinterpret_cast<T*>(p.c);
-    float v;
-    if (!p.has_bias && p.act == TVK_ACT_NONE) {
-#pragma clang fp contract(off)
-        v = acc * p.alpha;
-    } else {
-        float bv = 0.0f;
-        if (p.has_bias) {
-            const T* bias = reinterpret_cast<const T*>(p.bias);
-            bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2]]);
-        }
-        v = epilogue_math(acc, p.alpha, p.has_bias, bv, p.beta, p.act);
-    }
-    c[(int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2]] = elem<DT>::from_f32(v);
-}
-
-// Epilogue of 16 accumulators of one lane that share a column and sit at
-// rows row0 + (r/4)*8 + r%4 (the 32x32 MFMA accumulator layout).
-template <int DT>
-__device__ inline void store_frag16(const GemmArgs& p, int b, int row0, int col, const f32x16& v) {
-    if (col >= p.N) return;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = row0 + (r / 4) * 8 + (r % 4);
-        if (row < p.M) store_out<DT>(p, b, row, col, v[r]);
-    }
-}
 
 // ----------------------------------------------------------------------------
 // K == 0 and generic kernels
@@ -146,37 +76,6 @@ __device__ inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
     else
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-// Out-of-range buffer offset: the hardware returns zeros for it.
-constexpr uint32_t kOOB = 0x80000000u;
-
-__device__ inline u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-}
-__device__ inline uint32_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
-}
-
-// Eight consecutive elements of one operand along its contiguous dimension.
-// VEC: one 16-byte load (alignment and extent are multiples of 8 elements);
-// otherwise eight 2-byte loads, each range-checked.
-template <bool VEC>
-__device__ inline u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, bool row_ok, int64_t elem_off, int64_t step, int valid) {
-    if constexpr (VEC) {
-        return buf_load16(r, (row_ok && valid > 0) ? (uint32_t)(elem_off * 2) : kOOB);
-    } else {
-        uint32_t h[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            h[e] = buf_load2(r, (row_ok && e < valid) ? (uint32_t)((elem_off + e * step) * 2) : kOOB);
-        u32x4 v;
-        v.x = h[0] | (h[1] << 16);
-        v.y = h[2] | (h[3] << 16);
-        v.z = h[4] | (h[5] << 16);
-        v.w = h[6] | (h[7] << 16);
-        return v;
-    }
 }
 
 // Loader of one operand tile of R rows (rows = M for A, N for B) x 64 k into
@@ -586,7 +485,7 @@ __global__ __launch_bounds__(256) void gemm_seq_mfma_kernel(GemmArgs p) {
 // host dispatch
 // ----------------------------------------------------------------------------
 
-enum class Kern { K0, GENERIC, SEQ256, SEQ128, MFMA256, MFMA256W8, MFMA128 };
+enum class Kern { K0, GENERIC, SEQ256, SEQ128, MFMA256, MFMA256W8, MFMA128, SKINNY };
 
 struct Plan {
     Kern kern;
@@ -625,6 +524,17 @@ Plan make_plan(const tvk_gemm_desc& d) {
     if (pl.bk) vec = vec && d.K % ce == 0 && (d.N == 1 || d.b_stride[2] % ce == 0);
     else vec = vec && d.N % ce == 0 && (d.K == 1 || d.b_stride[1] % ce == 0);
     pl.vec = vec;
+    if (d.dtype != TVK_F32 && !(d.flags & TVK_GEMM_EXACT) && skinny_applies(d.M, d.N, d.K, d.batch)) {
+        // the streaming kernel loads A by rows of k: 16-byte loads need A k-contiguous too
+        bool v = al16(d.a) && al16(d.b) && a_k && d.K % 8 == 0 && (d.M == 1 || d.a_stride[1] % 8 == 0);
+        if (d.batch > 1) v = v && d.a_stride[0] % 8 == 0 && d.b_stride[0] % 8 == 0;
+        if (b_k) v = v && (d.N == 1 || d.b_stride[2] % 8 == 0);
+        else v = v && d.N % 8 == 0 && (d.K == 1 || d.b_stride[1] % 8 == 0);
+        pl.kern = Kern::SKINNY;
+        pl.vec = v;
+        pl.name = skinny_name(b_k);
+        return pl;
+    }
     const int64_t t256 = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
     const bool big = d.M >= 256 && d.N >= 256 && t256 >= 192;
     if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
@@ -709,6 +619,13 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
             else launch_seq<DT, 128, 128>(pl, q, grid, s);
             break;
         }
+        case Kern::SKINNY:
+            if constexpr (DT != TVK_F32) {
+                hipError_t e = launch_skinny(DT, q, pl.bk, pl.vec, s);
+                if (e != hipSuccess) return fail(e == hipErrorOutOfMemory ? TVK_ERR_OOM : TVK_ERR_DEVICE,
+                                                  std::string("tvk_gemm: skinny launch failed: ") + hipGetErrorString(e));
+            }
+            break;
         case Kern::MFMA256:
         case Kern::MFMA256W8:
         case Kern::MFMA128:

@@ -1,0 +1,123 @@
+// Pieces shared by the GEMM translation units: kernel arguments, the fused
+// epilogue and buffer-resource loads with hardware range checking.
+#pragma once
+
+#include "tvk_common.h"
+
+namespace tvk {
+
+struct GemmArgs {
+    const void* a;
+    const void* b;
+    const void* bias;
+    void* c;
+    int64_t sa[3], sb[3], sbias[3], sc[3];
+    int M, N, K;
+    int batch;
+    float alpha, beta;
+    int has_bias;
+    int act;
+    int tiles_m, tiles_n;
+};
+
+// ----------------------------------------------------------------------------
+// epilogue (shared by all kernels)
+// ----------------------------------------------------------------------------
+
+__device__ inline float gelu_erf(float v) {
+#pragma clang fp contract(off)
+    return 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
+}
+
+// v = acc*alpha; v = v + bias*beta; act(v). Contraction is off so the two
+// products round separately, as the reference's ext_mul/ext_add chain does.
+// Out of line, with scalar arguments only: the tiled kernels call it from an
+// unrolled epilogue and must keep their accumulators in registers.
+static __device__ __noinline__ float epilogue_math(float acc, float alpha, int has_bias, float bv, float beta, int act) {
+#pragma clang fp contract(off)
+    float v = acc * alpha;
+    if (has_bias) {
+        float t = bv * beta;
+        v = v + t;
+    }
+    if (act == TVK_ACT_RELU) v = v > 0.0f ? v : (v != v ? v : 0.0f);
+    else if (act == TVK_ACT_GELU) v = gelu_erf(v);
+    return v;
+}
+
+template <int DT>
+__device__ inline void store_out(const GemmArgs& p, int b, int row, int col, float acc) {
+    typedef typename elem<DT>::T T;
+    T* c = reinterpret_cast<T*>(p.c);
+    float v;
+    if (!p.has_bias && p.act == TVK_ACT_NONE) {
+#pragma clang fp contract(off)
+        v = acc * p.alpha;
+    } else {
+        float bv = 0.0f;
+        if (p.has_bias) {
+            const T* bias = reinterpret_cast<const T*>(p.bias);
+            bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2]]);
+        }
+        v = epilogue_math(acc, p.alpha, p.has_bias, bv, p.beta, p.act);
+    }
+    c[(int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2]] = elem<DT>::from_f32(v);
+}
+
+// Epilogue of 16 accumulators of one lane that share a column and sit at
+// rows row0 + (r/4)*8 + r%4 (the 32x32 MFMA accumulator layout).
+template <int DT>
+__device__ inline void store_frag16(const GemmArgs& p, int b, int row0, int col, const f32x16& v) {
+    if (col >= p.N) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = row0 + (r / 4) * 8 + (r % 4);
+        if (row < p.M) store_out<DT>(p, b, row, col, v[r]);
+    }
+}
+
+
+// Out-of-range buffer offset: the hardware returns zeros for it.
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ inline u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ inline uint32_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
+// Eight consecutive elements of one operand along its contiguous dimension.
+// VEC: one 16-byte load (alignment and extent are multiples of 8 elements);
+// otherwise eight 2-byte loads, each range-checked.
+template <bool VEC>
+__device__ inline u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, bool row_ok, int64_t elem_off, int64_t step, int valid) {
+    if constexpr (VEC) {
+        return buf_load16(r, (row_ok && valid > 0) ? (uint32_t)(elem_off * 2) : kOOB);
+    } else {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            h[e] = buf_load2(r, (row_ok && e < valid) ? (uint32_t)((elem_off + e * step) * 2) : kOOB);
+        u32x4 v;
+        v.x = h[0] | (h[1] << 16);
+        v.y = h[2] | (h[3] << 16);
+        v.z = h[4] | (h[5] << 16);
+        v.w = h[6] | (h[7] << 16);
+        return v;
+    }
+}
+
+// Library-owned scratch of a device (defined in runtime.hip). Both grow on
+// demand; the counters are zero between calls (every kernel that increments
+// one resets it before it exits).
+void* device_workspace(int device, size_t bytes);
+uint32_t* device_counters(int device, size_t count);
+
+// M <= 16 streaming kernel (gemm_skinny.hip). b_kmajor: B's k stride is 1.
+// vec: 16-byte loads are legal for A and B. Returns hipSuccess or the launch error.
+hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, hipStream_t s);
+const char* skinny_name(bool b_kmajor);
+bool skinny_applies(int64_t M, int64_t N, int64_t K, int64_t batch);
+
+}  // namespace tvk

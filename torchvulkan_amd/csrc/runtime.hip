@@ -15,6 +15,7 @@
 #include <unordered_map>
 #include <vector>
 #include <cstring>
+#include <algorithm>
 
 namespace tvk {
 
@@ -28,6 +29,10 @@ constexpr int kMaxDevices = 64;
 
 struct DeviceState {
     hipStream_t stream = nullptr;
+    void* workspace = nullptr;      // library scratch (split-k partials)
+    size_t workspace_bytes = 0;
+    uint32_t* counters = nullptr;   // zeroed arrival counters
+    size_t counter_count = 0;
     // size class -> cached free blocks
     std::map<size_t, std::vector<void*>> free_blocks;
     size_t allocated = 0;   // bytes in live blocks (size-class rounded)
@@ -77,6 +82,58 @@ void release_cached_locked(int device) {
 }
 
 }  // namespace
+
+// Grows the device's scratch area. Growing waits for the whole device first,
+// since kernels still queued on any stream may be using the old area.
+void* device_workspace(int device, size_t bytes) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState& st = g_dev[device];
+    if (bytes > st.workspace_bytes) {
+        int prev = 0;
+        (void)hipGetDevice(&prev);
+        (void)hipSetDevice(device);
+        if (st.workspace) {
+            (void)hipDeviceSynchronize();
+            (void)hipFree(st.workspace);
+        }
+        size_t sz = std::max(bytes, size_t(16) << 20);
+        if (hipMalloc(&st.workspace, sz) != hipSuccess) {
+            (void)hipGetLastError();
+            st.workspace = nullptr;
+            sz = 0;
+        }
+        st.workspace_bytes = sz;
+        (void)hipSetDevice(prev);
+    }
+    return st.workspace;
+}
+
+uint32_t* device_counters(int device, size_t count) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState& st = g_dev[device];
+    if (count > st.counter_count) {
+        int prev = 0;
+        (void)hipGetDevice(&prev);
+        (void)hipSetDevice(device);
+        if (st.counters) {
+            (void)hipDeviceSynchronize();
+            (void)hipFree(st.counters);
+        }
+        size_t n = std::max(count, size_t(65536));
+        if (hipMalloc(&st.counters, n * sizeof(uint32_t)) != hipSuccess ||
+            hipMemset(st.counters, 0, n * sizeof(uint32_t)) != hipSuccess ||
+            hipDeviceSynchronize() != hipSuccess) {
+            (void)hipGetLastError();
+            st.counters = nullptr;
+            n = 0;
+        }
+        st.counter_count = n;
+        (void)hipSetDevice(prev);
+    }
+    return st.counters;
+}
 
 hipStream_t device_stream(int device) {
     if (device < 0 || device >= kMaxDevices) return nullptr;
