@@ -178,6 +178,45 @@ tvk_status tvk_gemm(const tvk_gemm_desc* desc);
  * choice record (src/vulkan/autotuner.cpp:56-84). */
 tvk_status tvk_gemm_plan(const tvk_gemm_desc* desc, char* name, size_t name_len);
 
+/* ------------------------------------------------------------------------- */
+/* Compute: 2-D convolution as implicit GEMM                                  */
+/* ------------------------------------------------------------------------- */
+
+/* One 2-D convolution problem. Tensors are contiguous NCHW, weights
+ * [c_out][c_in/groups][kh][kw] (the reference makes every operand contiguous
+ * before its conv kernels, src/api/ops/conv.cpp:1101-1103,1145-1147). The
+ * same descriptor serves the three directions; which pointers are read and
+ * which one is written depends on the entry point:
+ *   fwd:   y = conv(x, weight) + bias        (reads x, weight, bias; writes y)
+ *   dgrad: x = conv_transpose(y, weight)     (reads y, weight; writes x)
+ *   wgrad: weight = correlate(x, y)          (reads x, y; writes weight)
+ * h_out/w_out must equal floor((h + 2p - d(k-1) - 1)/s) + 1.
+ * Accumulation is float32; float32 (and every dtype under TVK_GEMM_EXACT)
+ * accumulates each output over k in order, fused multiply-add per term. */
+typedef struct {
+    int32_t dtype;
+    uint32_t flags;          /* TVK_GEMM_EXACT */
+    int64_t n, c_in, h, w;
+    int64_t c_out, kh, kw;
+    int64_t stride[2], padding[2], dilation[2];
+    int64_t groups;
+    int64_t h_out, w_out;
+    void* x;
+    void* weight;
+    const void* bias;        /* fwd only; NULL: none */
+    void* y;
+    void* stream;
+} tvk_conv_desc;
+
+/* Replaces implicit_forward (src/api/ops/conv.cpp:1014-1022) and its
+ * conv_simd/conv_coop/winograd kernels. */
+tvk_status tvk_conv2d_fwd(const tvk_conv_desc* desc);
+/* Replaces implicit_grad_input (src/api/ops/conv.cpp:1024-1032), including
+ * the transposed-convolution forward that reuses it (conv.cpp:1105). */
+tvk_status tvk_conv2d_dgrad(const tvk_conv_desc* desc);
+/* Replaces implicit_grad_weight (src/api/ops/conv.cpp:1034-1060). */
+tvk_status tvk_conv2d_wgrad(const tvk_conv_desc* desc);
+
 #ifdef __cplusplus
 }
 #endif

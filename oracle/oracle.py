@@ -165,3 +165,108 @@ def gemm(a: np.ndarray, b: np.ndarray, dtype: int, bias: np.ndarray | None = Non
         with cf.ThreadPoolExecutor(max_workers=threads) as ex:
             list(ex.map(run, jobs))
     return c
+
+
+# ---------------------------------------------------------------------------
+# 2-D convolution (conv_oracle.c)
+# ---------------------------------------------------------------------------
+
+class ConvGeom(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in (
+        "n", "cin", "h", "w", "cout", "kh", "kw", "sh", "sw", "ph", "pw", "dh", "dw", "groups", "ho", "wo")]
+
+
+def conv_out_size(size: int, k: int, s: int, p: int, d: int) -> int:
+    return (size + 2 * p - d * (k - 1) - 1) // s + 1
+
+
+def make_geom(x_shape, w_shape, stride=(1, 1), padding=(0, 0), dilation=(1, 1), groups=1, out_hw=None) -> ConvGeom:
+    n, cin, h, w = x_shape
+    cout, _, kh, kw = w_shape
+    if out_hw is None:
+        out_hw = (conv_out_size(h, kh, stride[0], padding[0], dilation[0]),
+                  conv_out_size(w, kw, stride[1], padding[1], dilation[1]))
+    return ConvGeom(n, cin, h, w, cout, kh, kw, stride[0], stride[1], padding[0], padding[1],
+                    dilation[0], dilation[1], groups, out_hw[0], out_hw[1])
+
+
+def _conv_lib():
+    lib = load()
+    if not getattr(lib, "_conv_ready", False):
+        P = C.POINTER(ConvGeom)
+        lib.oracle_conv_fwd.argtypes = [C.c_int, P, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        lib.oracle_conv_dgrad.argtypes = [C.c_int, P, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]
+        lib.oracle_conv_wgrad.argtypes = [C.c_int, P, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+        lib.oracle_winograd_fwd.argtypes = [C.c_int, P, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        for f in ("oracle_conv_fwd", "oracle_conv_dgrad", "oracle_conv_wgrad", "oracle_winograd_fwd"):
+            getattr(lib, f).restype = C.c_int
+        lib._conv_ready = True
+    return lib
+
+
+def _parallel(total: int, fn, threads: int | None):
+    threads = threads or max(1, min(16, os.cpu_count() or 1))
+    per = max(1, -(-total // threads))
+    ranges = [(b, min(total, b + per)) for b in range(0, total, per)]
+
+    def run(r):
+        if fn(*r) != 0:
+            raise ValueError("conv oracle rejected its arguments")
+
+    if len(ranges) <= 1:
+        for r in ranges:
+            run(r)
+    else:
+        with cf.ThreadPoolExecutor(max_workers=threads) as ex:
+            list(ex.map(run, ranges))
+
+
+def _c(x):
+    return np.ascontiguousarray(x)
+
+
+def conv2d(x, w, dtype: int, bias=None, stride=(1, 1), padding=(0, 0), dilation=(1, 1), groups=1,
+           threads=None) -> np.ndarray:
+    """Forward implicit-GEMM convolution in the reference's k order (c, kh, kw)."""
+    lib = _conv_lib()
+    x, w = _c(x), _c(w)
+    g = make_geom(x.shape, w.shape, stride, padding, dilation, groups)
+    y = np.zeros((g.n, g.cout, g.ho, g.wo), dtype=x.dtype)
+    b = None if bias is None else _c(bias)
+    _parallel(g.n, lambda s, e: lib.oracle_conv_fwd(dtype, C.byref(g), s, e, x.ctypes.data, w.ctypes.data,
+                                                    None if b is None else b.ctypes.data, y.ctypes.data), threads)
+    return y
+
+
+def conv2d_dgrad(dy, w, x_shape, dtype: int, stride=(1, 1), padding=(0, 0), dilation=(1, 1), groups=1,
+                 threads=None) -> np.ndarray:
+    lib = _conv_lib()
+    dy, w = _c(dy), _c(w)
+    g = make_geom(x_shape, w.shape, stride, padding, dilation, groups, out_hw=dy.shape[2:])
+    dx = np.zeros(tuple(x_shape), dtype=dy.dtype)
+    _parallel(g.n, lambda s, e: lib.oracle_conv_dgrad(dtype, C.byref(g), s, e, dy.ctypes.data, w.ctypes.data,
+                                                      dx.ctypes.data), threads)
+    return dx
+
+
+def conv2d_wgrad(x, dy, w_shape, dtype: int, stride=(1, 1), padding=(0, 0), dilation=(1, 1), groups=1,
+                 acc64=True, threads=None) -> np.ndarray:
+    lib = _conv_lib()
+    x, dy = _c(x), _c(dy)
+    g = make_geom(x.shape, w_shape, stride, padding, dilation, groups, out_hw=dy.shape[2:])
+    dw = np.zeros(tuple(w_shape), dtype=x.dtype)
+    _parallel(g.cout, lambda s, e: lib.oracle_conv_wgrad(dtype, C.byref(g), s, e, x.ctypes.data, dy.ctypes.data,
+                                                         dw.ctypes.data, 1 if acc64 else 0), threads)
+    return dw
+
+
+def winograd_conv2d(x, w, dtype: int, bias=None, padding=(1, 1), threads=None) -> np.ndarray:
+    """The reference's Winograd F(2x2,3x3) forward, intermediates rounded to dtype."""
+    lib = _conv_lib()
+    x, w = _c(x), _c(w)
+    g = make_geom(x.shape, w.shape, (1, 1), padding, (1, 1), 1)
+    y = np.zeros((g.n, g.cout, g.ho, g.wo), dtype=x.dtype)
+    b = None if bias is None else _c(bias)
+    _parallel(g.n, lambda s, e: lib.oracle_winograd_fwd(dtype, C.byref(g), s, e, x.ctypes.data, w.ctypes.data,
+                                                        None if b is None else b.ctypes.data, y.ctypes.data), threads)
+    return y

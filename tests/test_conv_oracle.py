@@ -1,0 +1,80 @@
+"""Pins the convolution oracle (oracle/conv_oracle.c) against torch CPU in
+float64: integer-valued operands make every summation order exact, so the
+index maps (padding, stride, dilation, groups, 1x1, transposed gradients) are
+held to equality; random operands check the Winograd restatement against the
+direct convolution it must approximate."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+GEOMS = [
+    # x shape, w shape, stride, padding, dilation, groups
+    ((2, 3, 9, 9), (4, 3, 3, 3), (1, 1), (1, 1), (1, 1), 1),
+    ((2, 4, 10, 7), (6, 4, 3, 3), (2, 2), (1, 1), (1, 1), 1),
+    ((1, 4, 9, 11), (6, 2, 3, 3), (2, 1), (1, 2), (1, 2), 2),
+    ((3, 8, 6, 6), (4, 8, 1, 1), (2, 2), (0, 0), (1, 1), 1),
+    ((1, 2, 5, 5), (2, 2, 5, 3), (1, 3), (2, 0), (1, 1), 1),
+]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    orc.build()
+
+
+def _ints(shape, seed, lo=-3, hi=4):
+    return np.random.default_rng(seed).integers(lo, hi, shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("geom", GEOMS)
+def test_forward_exact(geom):
+    xs, ws, s, p, d, g = geom
+    x, w, b = _ints(xs, 1), _ints(ws, 2), _ints((ws[0],), 3)
+    got = orc.conv2d(x, w, orc.F32, bias=b, stride=s, padding=p, dilation=d, groups=g)
+    want = torch.nn.functional.conv2d(torch.from_numpy(x).double(), torch.from_numpy(w).double(),
+                                      torch.from_numpy(b).double(), s, p, d, g).numpy()
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("geom", GEOMS)
+def test_gradients_exact(geom):
+    xs, ws, s, p, d, g = geom
+    x = torch.from_numpy(_ints(xs, 4)).double().requires_grad_()
+    w = torch.from_numpy(_ints(ws, 5)).double().requires_grad_()
+    y = torch.nn.functional.conv2d(x, w, None, s, p, d, g)
+    dy = torch.from_numpy(_ints(tuple(y.shape), 6)).double()
+    y.backward(dy)
+    dx = orc.conv2d_dgrad(dy.float().numpy(), w.detach().float().numpy(), xs, orc.F32, s, p, d, g)
+    dw = orc.conv2d_wgrad(x.detach().float().numpy(), dy.float().numpy(), ws, orc.F32, s, p, d, g)
+    dw32 = orc.conv2d_wgrad(x.detach().float().numpy(), dy.float().numpy(), ws, orc.F32, s, p, d, g, acc64=False)
+    assert np.array_equal(dx, x.grad.numpy().astype(np.float32))
+    assert np.array_equal(dw, w.grad.numpy().astype(np.float32))
+    assert np.array_equal(dw32, w.grad.numpy().astype(np.float32))
+
+
+def test_fp16_storage_rounds_once():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((2, 8, 8, 8)).astype(np.float16)
+    w = (rng.standard_normal((8, 8, 3, 3)) * 0.1).astype(np.float16)
+    got = orc.conv2d(x.view(np.uint16), w.view(np.uint16), orc.F16, padding=(1, 1)).view(np.float16)
+    want = torch.nn.functional.conv2d(torch.from_numpy(x).double(), torch.from_numpy(w).double(), padding=1).numpy()
+    # one rounding of a float32 accumulation: within half an fp16 ulp plus the fp32 sum error
+    assert np.all(np.abs(got.astype(np.float64) - want) <= np.abs(want) * 2.0 ** -11 + 1e-4)
+
+
+@pytest.mark.parametrize("dtype,tol", [(orc.F32, 1e-5), (orc.F16, 5e-3)])
+def test_winograd_restatement_close_to_direct(dtype, tol):
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((2, 16, 9, 10)).astype(np.float32)
+    w = (rng.standard_normal((16, 16, 3, 3)) * np.sqrt(2 / 144)).astype(np.float32)
+    b = rng.standard_normal(16).astype(np.float32)
+    if dtype == orc.F16:
+        x, w, b = (v.astype(np.float16).view(np.uint16) for v in (x, w, b))
+    wino = orc.to_f32(orc.winograd_conv2d(x, w, dtype, bias=b, padding=(1, 1)), dtype)
+    direct = orc.to_f32(orc.conv2d(x, w, dtype, bias=b, padding=(1, 1)), dtype)
+    assert np.all(np.abs(wino - direct) <= tol * (np.abs(direct) + 1))
+    if dtype == orc.F16:
+        # the rounded intermediates do change the result (the check has teeth)
+        assert not np.array_equal(wino, direct)

@@ -57,6 +57,23 @@ class GemmDesc(C.Structure):
     ]
 
 
+class ConvDesc(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int32),
+        ("flags", C.c_uint32),
+        ("n", C.c_int64), ("c_in", C.c_int64), ("h", C.c_int64), ("w", C.c_int64),
+        ("c_out", C.c_int64), ("kh", C.c_int64), ("kw", C.c_int64),
+        ("stride", C.c_int64 * 2), ("padding", C.c_int64 * 2), ("dilation", C.c_int64 * 2),
+        ("groups", C.c_int64),
+        ("h_out", C.c_int64), ("w_out", C.c_int64),
+        ("x", C.c_void_p),
+        ("weight", C.c_void_p),
+        ("bias", C.c_void_p),
+        ("y", C.c_void_p),
+        ("stream", C.c_void_p),
+    ]
+
+
 class DeviceProps(C.Structure):
     _fields_ = [
         ("name", C.c_char * 256),
@@ -102,6 +119,8 @@ def load() -> C.CDLL:
         lib.tvk_set_memory_limit.argtypes = [C.c_int, C.c_size_t]
         lib.tvk_mem_get_info.argtypes = [C.c_int, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
         lib.tvk_device_properties.argtypes = [C.c_int, C.POINTER(DeviceProps)]
+        for fn in ("tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad"):
+            getattr(lib, fn).argtypes = [C.POINTER(ConvDesc)]
         for fn in _ALL_ENTRY_POINTS:
             getattr(lib, fn).restype = C.c_int if fn != "tvk_last_error" else C.c_char_p
         _lib = lib
@@ -114,6 +133,7 @@ _ALL_ENTRY_POINTS = (
     "tvk_pointer_device", "tvk_set_memory_limit", "tvk_memory_allocated", "tvk_max_memory_allocated",
     "tvk_memory_reserved", "tvk_reset_peak_memory_stats", "tvk_mem_get_info", "tvk_memcpy_h2d",
     "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan",
+    "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad",
 )
 
 
@@ -200,3 +220,69 @@ def gemm_plan(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, 
     buf = C.create_string_buffer(128)
     check(load().tvk_gemm_plan(C.byref(d), buf, 128))
     return buf.value.decode()
+
+
+def _pair(v):
+    return (v, v) if isinstance(v, int) else tuple(v)
+
+
+def make_conv_desc(x_shape, w_shape, dtype, stride=1, padding=0, dilation=1, groups=1, x=None, weight=None, bias=None,
+                   y=None, stream=None, exact=False) -> ConvDesc:
+    """Describes a 2-D convolution over contiguous NCHW tensors (pointers from torch tensors or None)."""
+    stride, padding, dilation = _pair(stride), _pair(padding), _pair(dilation)
+    n, cin, h, w = x_shape
+    cout, _, kh, kw = w_shape
+    ho = (h + 2 * padding[0] - dilation[0] * (kh - 1) - 1) // stride[0] + 1
+    wo = (w + 2 * padding[1] - dilation[1] * (kw - 1) - 1) // stride[1] + 1
+    d = ConvDesc()
+    d.dtype = _dtype_code(dtype)
+    d.flags = TVK_GEMM_EXACT if exact else 0
+    d.n, d.c_in, d.h, d.w, d.c_out, d.kh, d.kw = n, cin, h, w, cout, kh, kw
+    d.stride = (C.c_int64 * 2)(*stride)
+    d.padding = (C.c_int64 * 2)(*padding)
+    d.dilation = (C.c_int64 * 2)(*dilation)
+    d.groups = groups
+    d.h_out, d.w_out = ho, wo
+    ptr = lambda t: None if t is None or t.numel() == 0 else t.data_ptr()
+    d.x, d.weight, d.bias, d.y = ptr(x), ptr(weight), ptr(bias), ptr(y)
+    d.stream = stream
+    return d
+
+
+def _conv_call(fn, d):
+    check(getattr(load(), fn)(C.byref(d)))
+
+
+def conv2d_fwd(x, weight, bias=None, stride=1, padding=0, dilation=1, groups=1, exact=False):
+    """y = conv2d(x, weight) + bias through tvk_conv2d_fwd (torch device tensors, contiguous NCHW)."""
+    import torch
+
+    d = make_conv_desc(x.shape, weight.shape, x.dtype, stride, padding, dilation, groups, exact=exact)
+    y = torch.empty((d.n, d.c_out, d.h_out, d.w_out), dtype=x.dtype, device=x.device)
+    d.x, d.weight, d.y = x.data_ptr(), weight.data_ptr(), y.data_ptr()
+    d.bias = None if bias is None else bias.data_ptr()
+    d.stream = torch.cuda.current_stream(x.device).cuda_stream
+    _conv_call("tvk_conv2d_fwd", d)
+    return y
+
+
+def conv2d_dgrad(dy, weight, x_shape, stride=1, padding=0, dilation=1, groups=1, exact=False):
+    import torch
+
+    d = make_conv_desc(x_shape, weight.shape, dy.dtype, stride, padding, dilation, groups, exact=exact)
+    dx = torch.empty(tuple(x_shape), dtype=dy.dtype, device=dy.device)
+    d.x, d.weight, d.y = dx.data_ptr(), weight.data_ptr(), dy.data_ptr()
+    d.stream = torch.cuda.current_stream(dy.device).cuda_stream
+    _conv_call("tvk_conv2d_dgrad", d)
+    return dx
+
+
+def conv2d_wgrad(x, dy, w_shape, stride=1, padding=0, dilation=1, groups=1, exact=False):
+    import torch
+
+    d = make_conv_desc(x.shape, w_shape, x.dtype, stride, padding, dilation, groups, exact=exact)
+    dw = torch.empty(tuple(w_shape), dtype=x.dtype, device=x.device)
+    d.x, d.weight, d.y = x.data_ptr(), dw.data_ptr(), dy.data_ptr()
+    d.stream = torch.cuda.current_stream(x.device).cuda_stream
+    _conv_call("tvk_conv2d_wgrad", d)
+    return dw
