@@ -70,9 +70,58 @@ def build_library(jobs: int | None = None) -> Path:
     return LIB
 
 
+BACKEND_SRC = CSRC / "backend"
+BACKEND = PKG / "_C.so"
+
+
+def _torch_flags() -> tuple[list[str], list[str]]:
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension as ce
+
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cflags = [
+        "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-variable", "-Wno-unused-function",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_API_INCLUDE_EXTENSION_H", "-DTORCH_EXTENSION_NAME=_C",
+        *[f"-I{p}" for p in ce.include_paths()], f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}",
+    ]
+    libdir = ce.library_paths()[0]
+    ldflags = [
+        f"-L{libdir}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+        f"-L{PKG}", "-ltvk_hip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{libdir}",
+    ]
+    return cflags, ldflags
+
+
+def build_backend(jobs: int | None = None) -> Path:
+    """Compile the PrivateUse1 backend (csrc/backend/*.cpp) with g++ into torchvulkan_amd/_C.so."""
+    if not LIB.exists():
+        raise RuntimeError("build libtvk_hip.so first")
+    BUILD.mkdir(exist_ok=True)
+    cflags, ldflags = _torch_flags()
+    sources = sorted(BACKEND_SRC.glob("*.cpp"))
+    cxx = os.environ.get("CXX", "g++")
+
+    def comp(src: Path) -> Path:
+        obj = BUILD / ("backend_" + src.stem + ".o")
+        _run([cxx, *cflags, "-c", str(src), "-o", str(obj)])
+        return obj
+
+    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2) - 1), 16)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(comp, sources))
+    tmp = BACKEND.with_suffix(".so.tmp")
+    _run([cxx, "-shared", *map(str, objs), "-o", str(tmp), *ldflags])
+    os.replace(tmp, BACKEND)
+    return BACKEND
+
+
 def main() -> None:
     lib = build_library()
     print(f"built {lib}")
+    ext = build_backend()
+    print(f"built {ext}")
 
 
 if __name__ == "__main__":

@@ -1,0 +1,391 @@
+// PrivateUse1 device plumbing: allocator, device guard, hooks, the boxed CPU
+// fallback, tensor creation / views / copies, and the `_C` Python module.
+//
+// Mirrors the reference's registration layer: allocator (src/vulkan/allocator.cpp),
+// guard (src/api/guard.cpp:19-100), hooks (src/api/hook.cpp:53-83), fallback
+// (src/api/fallback.cpp:5-13), tensor basics (src/api/tensor/allocation.cpp:238-247,
+// transfer.cpp:392-397, views.cpp:151-158) and the pybind module
+// (src/api/backend.cpp:9-130). Device memory comes from tvk_malloc; copies run
+// on the library stream.
+#include "common.h"
+
+#include <ATen/EmptyTensor.h>
+#include <ATen/detail/PrivateUse1HooksInterface.h>
+#include <ATen/native/CPUFallback.h>
+#include <ATen/native/Resize.h>
+#include <ATen/ops/_reshape_alias_native.h>
+#include <ATen/ops/as_strided_native.h>
+#include <ATen/ops/set_native.h>
+#include <ATen/ops/view_native.h>
+#include <c10/core/Allocator.h>
+#include <c10/core/impl/DeviceGuardImplInterface.h>
+
+#include <atomic>
+#include <chrono>
+#include <cstdlib>
+#include <cstring>
+#include <unordered_map>
+
+namespace tvkb {
+
+bool strict_mode() {
+    const char* v = std::getenv("TORCHVULKAN_STRICT");
+    return v && std::strcmp(v, "0") != 0 && v[0] != '\0';
+}
+
+void check_status(tvk_status st, const char* what) {
+    if (st == TVK_OK) return;
+    std::string msg = std::string("torchvulkan [ERROR]: ") + tvk_last_error();
+    if (msg.size() == 21) msg += what;
+    if (st == TVK_ERR_OOM) TORCH_CHECK_WITH(OutOfMemoryError, false, msg);
+    TORCH_CHECK(false, msg);
+}
+
+void* stream_of(c10::DeviceIndex index) {
+    void* s = nullptr;
+    check_status(tvk_get_stream(index < 0 ? 0 : index, &s), "tvk_get_stream");
+    return s;
+}
+
+int32_t tvk_dtype_of(c10::ScalarType t, bool& ok) {
+    ok = true;
+    switch (t) {
+    case at::kFloat: return TVK_F32;
+    case at::kHalf: return TVK_F16;
+    case at::kBFloat16: return TVK_BF16;
+    default: ok = false; return -1;
+    }
+}
+
+void view_extent(const at::Tensor& t, int64_t& lo, int64_t& n) {
+    lo = t.storage_offset();
+    int64_t hi = lo;
+    for (int64_t d = 0; d < t.dim(); ++d) {
+        TORCH_CHECK(t.stride(d) >= 0, "torchvulkan [ERROR]: negative strides are not supported");
+        if (t.size(d) == 0) { n = 0; return; }
+        hi += (t.size(d) - 1) * t.stride(d);
+    }
+    n = hi - lo + 1;
+}
+
+at::Tensor to_host(const at::Tensor& t) {
+    at::Tensor out = at::empty(t.sizes(), t.options().device(at::kCPU));
+    if (t.numel() == 0) return out;
+    int64_t lo = 0, n = 0;
+    view_extent(t, lo, n);
+    const int64_t es = t.element_size();
+    at::Tensor buf = at::empty({n}, t.options().device(at::kCPU));
+    const char* src = static_cast<const char*>(t.storage().data()) + lo * es;
+    check_status(tvk_memcpy_d2h(buf.data_ptr(), src, (size_t)(n * es), stream_of(t), 1), "copy to host");
+    std::vector<int64_t> strides(t.strides().begin(), t.strides().end());
+    out.copy_(buf.as_strided(t.sizes(), strides, 0));
+    return out;
+}
+
+void from_host(const at::Tensor& host, const at::Tensor& dst) {
+    if (dst.numel() == 0) return;
+    at::Tensor src = host.to(dst.scalar_type()).contiguous();
+    void* s = stream_of(dst);
+    if (dst.is_contiguous()) {
+        check_status(tvk_memcpy_h2d(dst.data_ptr(), src.data_ptr(), (size_t)(src.numel() * src.element_size()), s, 1),
+                     "copy to device");
+        return;
+    }
+    // strided destination: read its storage extent, write the view on the host, write the extent back
+    int64_t lo = 0, n = 0;
+    view_extent(dst, lo, n);
+    const int64_t es = dst.element_size();
+    at::Tensor buf = at::empty({n}, dst.options().device(at::kCPU));
+    char* base = static_cast<char*>(dst.storage().mutable_data()) + lo * es;
+    check_status(tvk_memcpy_d2h(buf.data_ptr(), base, (size_t)(n * es), s, 1), "copy to host");
+    std::vector<int64_t> strides(dst.strides().begin(), dst.strides().end());
+    buf.as_strided(dst.sizes(), strides, 0).copy_(src);
+    check_status(tvk_memcpy_h2d(base, buf.data_ptr(), (size_t)(n * es), s, 1), "copy to device");
+}
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// allocator
+// ---------------------------------------------------------------------------
+
+thread_local c10::DeviceIndex g_current = 0;
+
+void free_fn(void* p) {
+    if (p) (void)tvk_free(p);
+}
+
+struct TvkAllocator final : c10::Allocator {
+    c10::DataPtr allocate(size_t nbytes) override {
+        const c10::DeviceIndex dev = g_current;
+        void* p = nullptr;
+        if (nbytes) check_status(tvk_malloc(dev, nbytes, &p), "tvk_malloc");
+        return {p, p, &free_fn, c10::Device(c10::DeviceType::PrivateUse1, dev)};
+    }
+    c10::DeleterFnPtr raw_deleter() const override { return &free_fn; }
+    void copy_data(void* dest, const void* src, std::size_t count) const override {
+        check_status(tvk_memcpy_d2d(dest, src, count, stream_of(g_current)), "tvk_memcpy_d2d");
+    }
+};
+
+TvkAllocator g_allocator;
+
+// ---------------------------------------------------------------------------
+// device guard: one stream per device; events are host timestamps taken after
+// synchronizing the stream, as the reference's guard does (guard.cpp:44-61)
+// ---------------------------------------------------------------------------
+
+struct HostEvent {
+    bool recorded = false;
+    std::chrono::steady_clock::time_point time;
+};
+
+struct TvkGuardImpl final : c10::impl::DeviceGuardImplInterface {
+    c10::DeviceType type() const override { return c10::DeviceType::PrivateUse1; }
+    c10::Device exchangeDevice(c10::Device d) const override {
+        c10::Device old = getDevice();
+        setDevice(d);
+        return old;
+    }
+    c10::Device getDevice() const override { return c10::Device(c10::DeviceType::PrivateUse1, g_current); }
+    void setDevice(c10::Device d) const override {
+        TORCH_CHECK(d.type() == c10::DeviceType::PrivateUse1, "torchvulkan [ERROR]: expected a vulkan device");
+        if (d.index() >= 0) {
+            check_status(tvk_set_device(d.index()), "tvk_set_device");
+            g_current = d.index();
+        }
+    }
+    void uncheckedSetDevice(c10::Device d) const noexcept override {
+        if (d.index() >= 0 && tvk_set_device(d.index()) == TVK_OK) g_current = d.index();
+    }
+    c10::Stream getStream(c10::Device d) const noexcept override {
+        return c10::Stream(c10::Stream::DEFAULT, d.has_index() ? d : getDevice());
+    }
+    c10::Stream getDefaultStream(c10::Device d) const override {
+        return c10::Stream(c10::Stream::DEFAULT, d.has_index() ? d : getDevice());
+    }
+    c10::Stream exchangeStream(c10::Stream s) const noexcept override { return s; }
+    c10::DeviceIndex deviceCount() const noexcept override {
+        int n = 0;
+        (void)tvk_device_count(&n);
+        return static_cast<c10::DeviceIndex>(n);
+    }
+    bool queryStream(const c10::Stream& s) const override {
+        synchronizeStream(s);
+        return true;
+    }
+    void synchronizeStream(const c10::Stream& s) const override { synchronizeDevice(s.device_index()); }
+    void synchronizeDevice(const c10::DeviceIndex index) const override {
+        check_status(tvk_synchronize(index < 0 ? g_current : index), "tvk_synchronize");
+    }
+    void destroyEvent(void* event, const c10::DeviceIndex) const noexcept override { delete static_cast<HostEvent*>(event); }
+    void record(void** event, const c10::Stream& stream, const c10::DeviceIndex, const c10::EventFlag) const override {
+        if (*event == nullptr) *event = new HostEvent();
+        synchronizeStream(stream);
+        auto* e = static_cast<HostEvent*>(*event);
+        e->recorded = true;
+        e->time = std::chrono::steady_clock::now();
+    }
+    void block(void*, const c10::Stream&) const override {}
+    bool queryEvent(void*) const override { return true; }
+    void synchronizeEvent(void*) const override {}
+    double elapsedTime(void* a, void* b, const c10::DeviceIndex) const override {
+        auto* s = static_cast<HostEvent*>(a);
+        auto* e = static_cast<HostEvent*>(b);
+        TORCH_CHECK(s && e && s->recorded && e->recorded, "Both events must be recorded before calculating elapsed time.");
+        return std::chrono::duration<double, std::milli>(e->time - s->time).count();
+    }
+};
+
+C10_REGISTER_GUARD_IMPL(PrivateUse1, TvkGuardImpl);
+
+// ---------------------------------------------------------------------------
+// hooks
+// ---------------------------------------------------------------------------
+
+struct TvkHooks final : at::PrivateUse1HooksInterface {
+    bool isBuilt() const override { return true; }
+    bool isAvailable() const override {
+        int n = 0;
+        return tvk_device_count(&n) == TVK_OK && n > 0;
+    }
+    const at::Generator& getDefaultGenerator(c10::DeviceIndex) const override {
+        // random numbers on this path are drawn on the host (the CPU fallback)
+        return at::detail::getDefaultCPUGenerator();
+    }
+    at::Device getDeviceFromPtr(void* data) const override {
+        int dev = -1;
+        (void)tvk_pointer_device(data, &dev);
+        TORCH_CHECK(dev >= 0, "torchvulkan [ERROR]: pointer was not allocated by the vulkan allocator");
+        return at::Device(at::DeviceType::PrivateUse1, static_cast<c10::DeviceIndex>(dev));
+    }
+    bool isPinnedPtr(const void*) const override { return false; }
+    at::Allocator* getPinnedMemoryAllocator() const override { return at::getCPUAllocator(); }
+    bool hasPrimaryContext(c10::DeviceIndex) const override { return true; }
+    void resizePrivateUse1Bytes(const c10::Storage& storage, size_t newsize) const override {
+        c10::StorageImpl* impl = storage.unsafeGetStorageImpl();
+        const size_t old = impl->nbytes();
+        if (newsize == old) return;
+        c10::DataPtr fresh = g_allocator.allocate(newsize);
+        const size_t keep = std::min(old, newsize);
+        if (keep) check_status(tvk_memcpy_d2d(fresh.get(), impl->data(), keep, stream_of(g_current)), "resize copy");
+        impl->set_data_ptr_noswap(std::move(fresh));
+        impl->set_nbytes(newsize);
+    }
+};
+
+struct HooksRegistrar {
+    HooksRegistrar() {
+        at::RegisterPrivateUse1HooksInterface(new TvkHooks());
+        c10::SetAllocator(c10::DeviceType::PrivateUse1, &g_allocator);
+    }
+} g_hooks_registrar;
+
+// ---------------------------------------------------------------------------
+// boxed CPU fallback (src/api/fallback.cpp:5-13)
+// ---------------------------------------------------------------------------
+
+void cpu_fallback(const c10::OperatorHandle& op, torch::jit::Stack* stack) {
+    TVKB_FALLBACK("Silent fallback detected for operation: ", op.schema().operator_name(), ".");
+    at::native::cpu_fallback(op, stack);
+}
+
+// ---------------------------------------------------------------------------
+// tensor basics
+// ---------------------------------------------------------------------------
+
+at::Tensor empty_memory_format(c10::IntArrayRef size, std::optional<at::ScalarType> dtype, std::optional<at::Layout> layout,
+                               std::optional<at::Device> device, std::optional<bool> pin_memory,
+                               std::optional<at::MemoryFormat> memory_format) {
+    const c10::DeviceGuard guard(device.value_or(c10::Device(c10::DeviceType::PrivateUse1, g_current)));
+    constexpr c10::DispatchKeySet ks(c10::DispatchKey::PrivateUse1);
+    return at::detail::empty_generic(size, &g_allocator, ks, c10::dtype_or_default(dtype), memory_format);
+}
+
+at::Tensor empty_strided(c10::IntArrayRef size, c10::IntArrayRef stride, std::optional<at::ScalarType> dtype,
+                         std::optional<at::Layout> layout, std::optional<at::Device> device, std::optional<bool> pin_memory) {
+    const c10::DeviceGuard guard(device.value_or(c10::Device(c10::DeviceType::PrivateUse1, g_current)));
+    constexpr c10::DispatchKeySet ks(c10::DispatchKey::PrivateUse1);
+    return at::detail::empty_strided_generic(size, stride, &g_allocator, ks, c10::dtype_or_default(dtype));
+}
+
+at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool non_blocking) {
+    TORCH_CHECK(self.sizes() == dst.sizes() || self.numel() == dst.numel(), "torchvulkan [ERROR]: _copy_from size mismatch");
+    if (dst.numel() == 0) return dst;
+    if (self.is_privateuseone() && dst.is_privateuseone() && self.scalar_type() == dst.scalar_type() &&
+        self.is_contiguous() && dst.is_contiguous() && self.sizes() == dst.sizes()) {
+        check_status(tvk_memcpy_d2d(dst.data_ptr(), self.data_ptr(), (size_t)(self.numel() * self.element_size()),
+                                    stream_of(dst)),
+                     "tvk_memcpy_d2d");
+        return dst;
+    }
+    at::Tensor host = self.is_privateuseone() ? to_host(self) : self;
+    if (dst.is_privateuseone()) {
+        from_host(host.reshape(dst.sizes()), dst);
+    } else {
+        dst.copy_(host.reshape(dst.sizes()));
+    }
+    return dst;
+}
+
+at::Tensor copy_from_and_resize(const at::Tensor& self, const at::Tensor& dst) {
+    at::native::resize_output(dst, self.sizes());
+    return copy_from(self, dst, false);
+}
+
+at::Scalar local_scalar_dense(const at::Tensor& self) { return to_host(self).item(); }
+
+const at::Tensor& resize_(const at::Tensor& self, c10::IntArrayRef size, std::optional<at::MemoryFormat> memory_format) {
+    at::TensorImpl* impl = self.unsafeGetTensorImpl();
+    impl->set_sizes_contiguous(size);
+    const size_t itemsize = impl->dtype().itemsize();
+    const size_t need = at::detail::computeStorageNbytesContiguous(size, itemsize, impl->storage_offset());
+    if (need > impl->storage().nbytes()) {
+        at::detail::getPrivateUse1Hooks().resizePrivateUse1Bytes(impl->storage(), need);
+    }
+    if (memory_format.has_value() && *memory_format != at::MemoryFormat::Preserve) {
+        impl->empty_tensor_restride(*memory_format);
+    }
+    return self;
+}
+
+}  // namespace
+}  // namespace tvkb
+
+TORCH_LIBRARY_IMPL(_, PrivateUse1, m) {
+    m.fallback(torch::CppFunction::makeFromBoxedFunction<&tvkb::cpu_fallback>());
+}
+
+TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+    m.impl("empty.memory_format", &tvkb::empty_memory_format);
+    m.impl("empty_strided", &tvkb::empty_strided);
+    m.impl("as_strided", &at::native::as_strided_tensorimpl);
+    m.impl("view", &at::native::view);
+    m.impl("_reshape_alias", &at::native::_reshape_alias);
+    m.impl("resize_", &tvkb::resize_);
+    m.impl("set_.source_Storage", &at::native::set_);
+    m.impl("set_.source_Storage_storage_offset", &at::native::set_storage_cpu_);
+    m.impl("_copy_from", &tvkb::copy_from);
+    m.impl("_copy_from_and_resize", &tvkb::copy_from_and_resize);
+    m.impl("_local_scalar_dense", &tvkb::local_scalar_dense);
+}
+
+// ---------------------------------------------------------------------------
+// Python module (the reference's _C, src/api/backend.cpp:9-130)
+// ---------------------------------------------------------------------------
+
+namespace {
+size_t stat(tvk_status (*fn)(int, size_t*), int64_t dev) {
+    size_t v = 0;
+    tvkb::check_status(fn((int)dev, &v), "memory statistics");
+    return v;
+}
+}  // namespace
+
+PYBIND11_MODULE(_C, m) {
+    m.doc() = "torchvulkan_amd backend: the vulkan (PrivateUse1) device on MI355X";
+    m.def("is_available", []() {
+        int n = 0;
+        return tvk_device_count(&n) == TVK_OK && n > 0;
+    });
+    m.def("device_count", []() -> int64_t {
+        int n = 0;
+        (void)tvk_device_count(&n);
+        return n;
+    });
+    m.def("current_device", []() -> int64_t { return tvkb::g_current; });
+    m.def("set_device", [](int64_t d) {
+        tvkb::check_status(tvk_set_device((int)d), "set_device");
+        tvkb::g_current = static_cast<c10::DeviceIndex>(d);
+    });
+    m.def("synchronize", [](int64_t d) { tvkb::check_status(tvk_synchronize((int)d), "synchronize"); },
+          py::call_guard<py::gil_scoped_release>());
+    m.def("empty_cache", [](int64_t d) { tvkb::check_status(tvk_empty_cache((int)d), "empty_cache"); },
+          py::call_guard<py::gil_scoped_release>());
+    m.def("_memory_allocated", [](int64_t d) { return stat(tvk_memory_allocated, d); });
+    m.def("_max_memory_allocated", [](int64_t d) { return stat(tvk_max_memory_allocated, d); });
+    m.def("_memory_reserved", [](int64_t d) { return stat(tvk_memory_reserved, d); });
+    m.def("_reset_peak_memory_stats", [](int64_t d) { tvkb::check_status(tvk_reset_peak_memory_stats((int)d), "reset_peak"); });
+    m.def("_set_memory_limit", [](int64_t d, size_t bytes) { tvkb::check_status(tvk_set_memory_limit((int)d, bytes), "limit"); });
+    m.def("_mem_get_info", [](int64_t d) {
+        size_t f = 0, t = 0;
+        tvkb::check_status(tvk_mem_get_info((int)d, &f, &t), "mem_get_info");
+        return std::make_pair(f, t);
+    });
+    m.def("_device_properties", [](int64_t d) {
+        tvk_device_props p;
+        tvkb::check_status(tvk_device_properties((int)d, &p), "device_properties");
+        py::dict info;
+        info["name"] = std::string(p.name);
+        info["arch"] = std::string(p.arch);
+        info["total_memory"] = p.total_memory;
+        info["compute_units"] = p.compute_units;
+        info["clock_khz"] = p.clock_khz;
+        info["subgroup_size"] = p.wavefront_size;
+        info["has_fp64"] = (bool)p.has_fp64;
+        info["has_fp16"] = (bool)p.has_fp16;
+        info["has_bf16"] = (bool)p.has_bf16;
+        return info;
+    });
+    m.def("_strict", []() { return tvkb::strict_mode(); });
+}

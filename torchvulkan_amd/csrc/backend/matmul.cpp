@@ -1,0 +1,283 @@
+// aten::mm / bmm / addmm / baddbmm / _addmm_activation (+ .out) for the
+// vulkan (PrivateUse1) device, computed by tvk_gemm.
+//
+// Follows src/api/ops/matmul.cpp: operand preparation and broadcasting
+// (prepare_matmul_operands :27-78, get_matmul_shape :108-140,
+// finish_matmul_output :142-149), the has_bias rule (:259), the empty / K == 0
+// cases (:284-288), the CPU-identical error checks (check_matrix_product
+// :600-606, bmm's meta checks :624-630, baddbmm's dtype check :662-663) and
+// the registrations (:751-763). Operands are handed to the kernel as strided
+// views: transposed and sliced operands are not copied.
+#include "common.h"
+
+#include <ATen/native/Resize.h>
+
+namespace tvkb {
+namespace {
+
+enum Activation { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
+
+struct Shape {
+    at::Tensor self, other;
+    bool self_unsqueezed = false, other_unsqueezed = false;
+    int64_t M = 0, K = 0, N = 0, B = 1;
+    std::vector<int64_t> batch_shape, out_shape;
+};
+
+Shape matmul_shape(const at::Tensor& self_, const at::Tensor& other_) {
+    Shape s;
+    s.self = self_;
+    s.other = other_;
+    if (s.self.dim() < 2) { s.self = s.self.unsqueeze(0); s.self_unsqueezed = true; }
+    if (s.other.dim() < 2) { s.other = s.other.unsqueeze(1); s.other_unsqueezed = true; }
+    TORCH_CHECK(s.self.scalar_type() == s.other.scalar_type(), "expected m1 and m2 to have the same dtype, but got: ",
+                s.self.dtype().name(), " != ", s.other.dtype().name());
+    TORCH_CHECK(s.self.size(-1) == s.other.size(-2), "mat1 and mat2 shapes cannot be multiplied (", s.self.size(-2), "x",
+                s.self.size(-1), " and ", s.other.size(-2), "x", s.other.size(-1), ")");
+    s.M = s.self.size(-2);
+    s.K = s.self.size(-1);
+    s.N = s.other.size(-1);
+    s.batch_shape = at::infer_size(s.self.sizes().slice(0, s.self.dim() - 2), s.other.sizes().slice(0, s.other.dim() - 2));
+    for (int64_t v : s.batch_shape) s.B *= v;
+    s.out_shape = s.batch_shape;
+    s.out_shape.push_back(s.M);
+    s.out_shape.push_back(s.N);
+    return s;
+}
+
+at::Tensor finish(const at::Tensor& out, const Shape& s) {
+    at::Tensor r = out.reshape(s.out_shape);
+    if (s.self_unsqueezed && s.other_unsqueezed) return r.squeeze(-1).squeeze(-1);
+    if (s.self_unsqueezed) return r.squeeze(-2);
+    if (s.other_unsqueezed) return r.squeeze(-1);
+    return r;
+}
+
+at::Tensor apply_activation(const at::Tensor& t, Activation act) {
+    if (act == ACT_RELU) return at::relu(t);
+    if (act == ACT_GELU) return at::gelu(t);
+    return t;
+}
+
+// 3-D view [B, rows, cols] of an operand expanded to the batch shape, without
+// a copy when the expanded batch dims collapse into one stride.
+at::Tensor batched_view(const at::Tensor& t, const std::vector<int64_t>& batch_shape, int64_t rows, int64_t cols, int64_t B) {
+    std::vector<int64_t> shape(batch_shape);
+    shape.push_back(rows);
+    shape.push_back(cols);
+    at::Tensor e = t.expand(shape);
+    if (e.dim() == 2) return e.unsqueeze(0);
+    // the flattened batch index b has offset b * s when every non-1 batch dim
+    // has stride s * (product of the batch dims after it); broadcast dims
+    // (stride 0 throughout) collapse too
+    int64_t s = -1, prod = 1;
+    bool ok = true;
+    for (int64_t d = (int64_t)batch_shape.size() - 1; d >= 0; --d) {
+        if (batch_shape[d] == 1) continue;
+        const int64_t st = e.stride(d);
+        if (s < 0) {
+            s = st;
+        } else if (st != s * prod) {
+            ok = false;
+        }
+        prod *= batch_shape[d];
+    }
+    if (s < 0) s = 0;
+    if (ok) return e.as_strided({B, rows, cols}, {s, e.stride(-2), e.stride(-1)});
+    return e.reshape({B, rows, cols});  // materialises a contiguous copy
+}
+
+at::Tensor dispatch_matmul(const at::Tensor& self_, const at::Tensor& other_, const at::Tensor& bias_, const at::Scalar& alpha,
+                           const at::Scalar& beta, Activation act, const std::function<at::Tensor()>& fallback) {
+    const bool has_bias = bias_.defined() && beta.toDouble() != 0.0;
+    Shape s = matmul_shape(self_, other_);
+    const c10::ScalarType dtype = at::result_type(s.self, s.other);
+    bool ok = false;
+    const int32_t tdt = tvk_dtype_of(dtype, ok);
+    if (!ok) {
+        TVKB_FALLBACK("A ", dtype, " matmul can't run on the Vulkan device. Falling back to CPU.");
+        return fallback();
+    }
+    TORCH_CHECK(act != ACT_GELU || at::isFloatingType(dtype), "torchvulkan [ERROR]: gelu is only defined for floating point matmuls, not ", dtype);
+
+    at::Tensor a = batched_view(s.self.to(dtype), s.batch_shape, s.M, s.K, s.B);
+    at::Tensor b = batched_view(s.other.to(dtype), s.batch_shape, s.K, s.N, s.B);
+    at::Tensor out = at::empty({s.B, s.M, s.N}, a.options());
+    if (s.M == 0 || s.N == 0 || s.B == 0) return finish(out, s);
+    at::Tensor bias;
+    if (has_bias) bias = batched_view(bias_.to(a.options()), s.batch_shape, s.M, s.N, s.B);
+    if (s.K == 0) {
+        at::Tensor r = has_bias ? (bias * beta) : out.zero_();
+        return finish(apply_activation(r, act), s);
+    }
+    for (const at::Tensor* t : {&a, &b, &bias}) {
+        if (!t->defined()) continue;
+        for (int64_t d = 0; d < 3; ++d)
+            if (t->stride(d) < 0) {
+                TVKB_FALLBACK("A matmul operand with negative strides. Falling back to CPU.");
+                return fallback();
+            }
+    }
+
+    tvk_gemm_desc d;
+    std::memset(&d, 0, sizeof(d));
+    d.dtype = tdt;
+    d.activation = act;
+    d.flags = 0;
+    if (const char* e = std::getenv("TORCHVULKAN_EXACT")) {
+        if (e[0] && std::strcmp(e, "0") != 0) d.flags = TVK_GEMM_EXACT;
+    }
+    d.batch = s.B; d.M = s.M; d.N = s.N; d.K = s.K;
+    d.a = a.data_ptr();
+    d.b = b.data_ptr();
+    d.c = out.data_ptr();
+    for (int i = 0; i < 3; ++i) {
+        d.a_stride[i] = a.stride(i);
+        d.b_stride[i] = b.stride(i);
+        d.c_stride[i] = out.stride(i);
+    }
+    if (has_bias) {
+        d.bias = bias.data_ptr();
+        for (int i = 0; i < 3; ++i) d.bias_stride[i] = bias.stride(i);
+    }
+    d.alpha = alpha.toDouble();
+    d.beta = has_bias ? beta.toDouble() : 0.0;
+    d.stream = stream_of(out);
+    const tvk_status st = tvk_gemm(&d);
+    if (st == TVK_ERR_UNSUPPORTED) {
+        TVKB_FALLBACK(tvk_last_error(), ". Falling back to CPU.");
+        return fallback();
+    }
+    check_status(st, "tvk_gemm");
+    return finish(out, s);
+}
+
+// The CPU's checks, with the CPU's messages (torch's mm / addmm meta
+// functions; the reference's check_matrix_product, matmul.cpp:600-606, keeps
+// the same rule: the device rejects exactly what the CPU rejects).
+void check_matrix_product(const char* name, const at::Tensor& mat1, const at::Tensor& mat2) {
+    if (std::strcmp(name, "mm") == 0) {
+        TORCH_CHECK(mat1.dim() == 2, "self must be a matrix");
+        TORCH_CHECK(mat2.dim() == 2, "mat2 must be a matrix");
+    } else {
+        TORCH_CHECK(mat1.dim() == 2, "mat1 must be a matrix, got ", mat1.dim(), "-D tensor");
+        TORCH_CHECK(mat2.dim() == 2, "mat2 must be a matrix, got ", mat2.dim(), "-D tensor");
+    }
+    TORCH_CHECK(mat1.size(1) == mat2.size(0), "mat1 and mat2 shapes cannot be multiplied (", mat1.size(0), "x",
+                mat1.size(1), " and ", mat2.size(0), "x", mat2.size(1), ")");
+}
+
+at::Tensor mm_vk(const at::Tensor& self, const at::Tensor& other) {
+    check_matrix_product("mm", self, other);
+    return dispatch_matmul(self, other, {}, 1, 0, ACT_NONE,
+                           [&]() { return at::mm(self.cpu(), other.cpu()).to(self.device()); });
+}
+
+at::Tensor bmm_vk(const at::Tensor& self, const at::Tensor& other) {
+    TORCH_CHECK(self.dim() == 3, "batch1 must be a 3D tensor");
+    TORCH_CHECK(other.dim() == 3, "batch2 must be a 3D tensor");
+    TORCH_CHECK(self.device() == other.device(), "Expected all tensors to be on the same device, but found at least two devices, ",
+                self.device(), " and ", other.device(), "!");
+    TORCH_CHECK(self.scalar_type() == other.scalar_type(), "expected scalar type ", self.scalar_type(), " but found ",
+                other.scalar_type());
+    TORCH_CHECK(other.size(0) == self.size(0) && other.size(1) == self.size(2),
+                "Expected size for first two dimensions of batch2 tensor to be: [", self.size(0), ", ", self.size(2),
+                "] but got: [", other.size(0), ", ", other.size(1), "].");
+    return dispatch_matmul(self, other, {}, 1, 0, ACT_NONE,
+                           [&]() { return at::bmm(self.cpu(), other.cpu()).to(self.device()); });
+}
+
+at::Tensor addmm_vk(const at::Tensor& input, const at::Tensor& mat1, const at::Tensor& mat2, const at::Scalar& beta,
+                 const at::Scalar& alpha) {
+    for (const at::Tensor* t : {&mat1, &mat2})
+        TORCH_CHECK(t->device() == input.device(), "Expected all tensors to be on the same device, but found at least two devices, ",
+                    input.device(), " and ", t->device(), "!");
+    check_matrix_product("addmm", mat1, mat2);
+    return dispatch_matmul(mat1, mat2, input, alpha, beta, ACT_NONE, [&]() {
+        return at::addmm(input.cpu(), mat1.cpu(), mat2.cpu(), beta, alpha).to(mat1.device());
+    });
+}
+
+at::Tensor baddbmm_vk(const at::Tensor& input, const at::Tensor& b1, const at::Tensor& b2, const at::Scalar& beta,
+                   const at::Scalar& alpha) {
+    TORCH_CHECK(input.scalar_type() == b1.scalar_type() && b1.scalar_type() == b2.scalar_type(),
+                "Input dtypes must be the same, got: input ", input.dtype().name(), ", batch1: ", b1.dtype().name(),
+                ", batch2: ", b2.dtype().name());
+    return dispatch_matmul(b1, b2, input, alpha, beta, ACT_NONE, [&]() {
+        return at::baddbmm(input.cpu(), b1.cpu(), b2.cpu(), beta, alpha).to(b1.device());
+    });
+}
+
+at::Tensor addmm_activation_vk(const at::Tensor& input, const at::Tensor& mat1, const at::Tensor& mat2, const at::Scalar& beta,
+                            const at::Scalar& alpha, bool use_gelu) {
+    return dispatch_matmul(mat1, mat2, input, alpha, beta, use_gelu ? ACT_GELU : ACT_RELU, [&]() {
+        return at::_addmm_activation(input.cpu(), mat1.cpu(), mat2.cpu(), beta, alpha, use_gelu).to(mat1.device());
+    });
+}
+
+// resize-and-copy into an out= tensor (src/api/ops/helpers.h:363-378)
+at::Tensor& fill_out(at::Tensor& out, const at::Tensor& res) {
+    TORCH_CHECK(!res.is_privateuseone() || out.is_privateuseone(), "Expected out tensor to have device ", res.device(),
+                ", but got ", out.device(), " instead");
+    TORCH_CHECK(at::canCast(res.scalar_type(), out.scalar_type()), "result type ", res.scalar_type(),
+                " can't be cast to the desired output type ", out.scalar_type());
+    if (res.is_same(out)) return out;
+    if (at::native::resize_output(out, res.sizes()) && res.is_non_overlapping_and_dense() && out.strides() != res.strides())
+        out.as_strided_(res.sizes(), res.strides());
+    out.copy_(res);
+    return out;
+}
+
+at::Tensor& mm_out_vk(const at::Tensor& self, const at::Tensor& other, at::Tensor& out) { return fill_out(out, mm_vk(self, other)); }
+at::Tensor& bmm_out_vk(const at::Tensor& self, const at::Tensor& other, at::Tensor& out) {
+    TORCH_CHECK(out.device() == self.device(), "Expected out tensor to have device ", self.device(), ", but got ",
+                out.device(), " instead");
+    return fill_out(out, bmm_vk(self, other));
+}
+at::Tensor& addmm_out_vk(const at::Tensor& input, const at::Tensor& m1, const at::Tensor& m2, const at::Scalar& beta,
+                      const at::Scalar& alpha, at::Tensor& out) {
+    return fill_out(out, addmm_vk(input, m1, m2, beta, alpha));
+}
+at::Tensor& baddbmm_out_vk(const at::Tensor& input, const at::Tensor& b1, const at::Tensor& b2, const at::Scalar& beta,
+                        const at::Scalar& alpha, at::Tensor& out) {
+    return fill_out(out, baddbmm_vk(input, b1, b2, beta, alpha));
+}
+at::Tensor& addmm_activation_out_vk(const at::Tensor& input, const at::Tensor& m1, const at::Tensor& m2, const at::Scalar& beta,
+                                 const at::Scalar& alpha, bool use_gelu, at::Tensor& out) {
+    return fill_out(out, addmm_activation_vk(input, m1, m2, beta, alpha, use_gelu));
+}
+
+// addbmm: sum_b b1[b] @ b2[b] as one mm on permuted operands
+// (src/api/decompositions.cpp:1114-1139)
+at::Tensor addbmm_vk(const at::Tensor& input, const at::Tensor& b1, const at::Tensor& b2, const at::Scalar& beta,
+                  const at::Scalar& alpha) {
+    TORCH_CHECK(b1.dim() == 3, "batch1 must be a 3D tensor");
+    TORCH_CHECK(b2.dim() == 3, "batch2 must be a 3D tensor");
+    TORCH_CHECK(b1.size(0) == b2.size(0), "batch1 and batch2 must have same number of batches, got ", b1.size(0), " and ",
+                b2.size(0));
+    TORCH_CHECK(b1.size(2) == b2.size(1), "Incompatible matrix sizes for bmm (", b1.size(1), "x", b1.size(2), " and ",
+                b2.size(1), "x", b2.size(2), ")");
+    const int64_t B = b1.size(0), M = b1.size(1), K = b1.size(2), N = b2.size(2);
+    at::Tensor a = b1.permute({1, 0, 2}).reshape({M, B * K});
+    at::Tensor b = b2.reshape({B * K, N});
+    return dispatch_matmul(a, b, input, alpha, beta, ACT_NONE, [&]() {
+        return at::addbmm(input.cpu(), b1.cpu(), b2.cpu(), beta, alpha).to(b1.device());
+    });
+}
+
+}  // namespace
+}  // namespace tvkb
+
+TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+    m.impl("mm", &tvkb::mm_vk);
+    m.impl("mm.out", &tvkb::mm_out_vk);
+    m.impl("bmm", &tvkb::bmm_vk);
+    m.impl("bmm.out", &tvkb::bmm_out_vk);
+    m.impl("addmm", &tvkb::addmm_vk);
+    m.impl("addmm.out", &tvkb::addmm_out_vk);
+    m.impl("baddbmm", &tvkb::baddbmm_vk);
+    m.impl("baddbmm.out", &tvkb::baddbmm_out_vk);
+    m.impl("_addmm_activation", &tvkb::addmm_activation_vk);
+    m.impl("_addmm_activation.out", &tvkb::addmm_activation_out_vk);
+    m.impl("addbmm", &tvkb::addbmm_vk);
+}
