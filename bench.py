@@ -38,7 +38,47 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-extra", action="store_true", help="headline only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--profile-kernel", choices=["gemm", "skinny", "copy"],
+                   help="launch only this kernel --steps times and exit (for rocprofv3 counter passes); "
+                        "'copy' is torch's copy of a 1 GiB buffer, the calibration for FETCH_SIZE/WRITE_SIZE")
     return p.parse_args()
+
+
+def profile_kernel(which, steps):
+    """Launches one kernel `steps` times with nothing else on the GPU but the
+    inputs' initialisation, so that per-dispatch counters read cleanly."""
+    import ctypes as C
+
+    import torch
+    from torchvulkan_amd import _abi
+
+    lib = _abi.load()
+    dev = torch.device("cuda:0")
+    s = torch.cuda.current_stream(dev).cuda_stream
+    if which == "copy":
+        x = torch.ones((1 << 29,), dtype=torch.float16, device=dev)   # 1 GiB
+        y = torch.empty_like(x)
+        for _ in range(steps):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(f"copy: {steps} x {x.numel() * 2} bytes read + written", flush=True)
+        return
+    if which == "gemm":
+        n = 8192
+        a = torch.randn((n, n), device=dev).to(torch.float16)
+        b = torch.randn((n, n), device=dev).to(torch.float16)
+        c = torch.empty((n, n), dtype=torch.float16, device=dev)
+        descs = [_abi.make_gemm_desc(a, b, c, stream=s)]
+    else:
+        M, K, N = 16, 4096, 14336
+        a = torch.randn((M, K), device=dev).to(torch.float16)
+        bufs = [torch.randn((K, N), device=dev).to(torch.float16) for _ in range(3)]
+        c = torch.empty((M, N), dtype=torch.float16, device=dev)
+        descs = [_abi.make_gemm_desc(a, bb, c, stream=s) for bb in bufs]
+    for i in range(steps):
+        _abi.check(lib.tvk_gemm(C.byref(descs[i % len(descs)])))
+    torch.cuda.synchronize()
+    print(f"{which}: {steps} launches of {_abi.gemm_plan(a, (bufs[0] if which == 'skinny' else b), c)}", flush=True)
 
 
 def timed(fn, steps, warmup, stream):
@@ -69,6 +109,10 @@ def main():
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} (WORLD_SIZE={world}) is not supported. "
               "The path shards by splitting N or M across GPUs with no exchange; see DESIGN.md.", file=sys.stderr)
         sys.exit(2)
+
+    if args.profile_kernel:
+        profile_kernel(args.profile_kernel, args.steps)
+        return
 
     import torch
     from torchvulkan_amd import _abi
@@ -215,6 +259,77 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c5_skinny_GBps"] = round(byts / (ms * 1e-3) / 1e9, 1)
     out["c5_skinny_pct_hbm"] = round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)
     del bufs
+
+    # ---- C4 ResNet convs: fwd + dgrad + wgrad of each layer, fp16, batch 128 -
+    layers = [(3, 64, 3, 1, 1, 32), (64, 64, 3, 1, 1, 32), (64, 128, 3, 2, 1, 32), (128, 256, 3, 2, 1, 16),
+              (64, 128, 1, 2, 0, 32), (128, 256, 1, 2, 0, 16)]
+    conv_calls = []
+    conv_flops = 0
+    keep = []
+    for cin, cout, k, st, pd, hw in layers:
+        x = torch.randn((128, cin, hw, hw), generator=g).to(torch.float16).to(dev)
+        w = (torch.randn((cout, cin, k, k), generator=g) * (2.0 / (cin * k * k)) ** 0.5).to(torch.float16).to(dev)
+        ho = (hw + 2 * pd - k) // st + 1
+        y = torch.empty((128, cout, ho, ho), dtype=torch.float16, device=dev)
+        dy = torch.randn((128, cout, ho, ho), generator=g).to(torch.float16).to(dev)
+        dx = torch.empty_like(x)
+        dw = torch.empty_like(w)
+        keep += [x, w, y, dy, dx, dw]
+        base = dict(stride=st, padding=pd, stream=s)
+        conv_calls.append(("tvk_conv2d_fwd", _abi.make_conv_desc(x.shape, w.shape, torch.float16, x=x, weight=w, y=y, **base)))
+        conv_calls.append(("tvk_conv2d_dgrad", _abi.make_conv_desc(x.shape, w.shape, torch.float16, x=dx, weight=w, y=dy, **base)))
+        conv_calls.append(("tvk_conv2d_wgrad", _abi.make_conv_desc(x.shape, w.shape, torch.float16, x=x, weight=dw, y=dy, **base)))
+        conv_flops += 3 * 2 * 128 * cout * ho * ho * cin * k * k
+    conv_refs = [(getattr(lib, fn), C.byref(d)) for fn, d in conv_calls]
+
+    def conv_step():
+        for fn, r in conv_refs:
+            st_ = fn(r)
+            if st_:
+                _abi.check(st_)
+
+    ms, _ = timed(conv_step, steps, warmup, stream)
+    out["c4_resnet_conv_fwd_bwd_ms"] = round(ms, 4)
+    out["c4_resnet_conv_tflops"] = round(conv_flops / (ms * 1e-3) / 1e12, 2)
+    del keep, conv_refs, conv_calls
+
+    # ---- C3 transformer layer GEMMs (fp16, tokens 8192): fwd + bwd ----------
+    T = 8192
+    shapes = [(512, 512), (512, 256), (512, 256), (512, 512), (512, 3072), (1536, 512)]  # q, k, v, out, gate_up, down
+    llm_descs = []
+    keep = []
+    llm_flops = 0
+    for fin, fout in shapes:
+        x = torch.randn((T, fin), generator=g).to(torch.float16).to(dev)
+        w = (torch.randn((fout, fin), generator=g) * 0.02).to(torch.float16).to(dev)
+        y = torch.empty((T, fout), dtype=torch.float16, device=dev)
+        dy = torch.randn((T, fout), generator=g).to(torch.float16).to(dev)
+        dx = torch.empty_like(x)
+        dw = torch.empty_like(w)
+        keep += [x, w, y, dy, dx, dw]
+        llm_descs += [_abi.make_gemm_desc(x, w.t(), y, stream=s), _abi.make_gemm_desc(dy, w, dx, stream=s),
+                      _abi.make_gemm_desc(dy.t(), x, dw, stream=s)]
+        llm_flops += 3 * 2 * T * fin * fout
+    # attention products per layer: 256 (batch x heads) of [256,64]x[64,256] and [256,256]x[256,64]
+    q = torch.randn((256, 256, 64), generator=g).to(torch.float16).to(dev)
+    kk = torch.randn((256, 256, 64), generator=g).to(torch.float16).to(dev)
+    sc = torch.empty((256, 256, 256), dtype=torch.float16, device=dev)
+    pv = torch.empty((256, 256, 64), dtype=torch.float16, device=dev)
+    keep += [q, kk, sc, pv]
+    llm_descs += [_abi.make_gemm_desc(q, kk.transpose(1, 2), sc, stream=s), _abi.make_gemm_desc(sc, kk, pv, stream=s)]
+    llm_flops += 2 * 2 * 256 * 256 * 256 * 64
+    llm_refs = [C.byref(d) for d in llm_descs]
+
+    def llm_step():
+        for r in llm_refs:
+            st_ = lib.tvk_gemm(r)
+            if st_:
+                _abi.check(st_)
+
+    ms, _ = timed(llm_step, steps, warmup, stream)
+    out["c3_llm_layer_gemm_fwd_bwd_ms"] = round(ms, 4)
+    out["c3_llm_layer_gemm_tflops"] = round(llm_flops / (ms * 1e-3) / 1e12, 2)
+    del keep, llm_refs, llm_descs
 
     # ---- C1 fp32 1024^3 ----------------------------------------------------
     a = torch.randn((1024, 1024), generator=g).to(dev)
