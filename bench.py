@@ -30,6 +30,14 @@ PEAK_F16_TFLOPS = 2516.6   # MI355X dense fp16/bf16 MFMA, AMD spec sheet
 PEAK_F32_TFLOPS = 157.3    # MI355X fp32 matrix
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
+# HBM bytes per launch of the headline kernel, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
+# (KiB per dispatch) scaled by what the same counters read for a 1 GiB copy (x2.0 and x1.0):
+# profiles/gemm_fp16_8192_counters.md. Counters need their own profiler runs, so the figure is
+# recorded here per kernel plan rather than measured inside the timed region.
+MEASURED_TRAFFIC = {
+    "gemm16_mfma_256x256_w8": {"bytes": 1.746e9, "fetch_kib": 786764, "write_kib": 131161},
+}
+
 
 def parse():
     p = argparse.ArgumentParser()
@@ -155,8 +163,10 @@ def main():
         "peak": PEAK_F16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(tflops / PEAK_F16_TFLOPS, 4),
-        "traffic": None,
+        "traffic": MEASURED_TRAFFIC.get(plan, {}).get("bytes"),
+        "traffic_source": "profiles/gemm_fp16_8192_counters.md" if plan in MEASURED_TRAFFIC else None,
         "algorithmic_unit": "2*M*N*K flops per launch",
+        "algorithmic_bytes": 3 * n * n * 2,
         "avg_kernel_ms": round(ms, 5),
     }
 
