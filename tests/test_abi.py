@@ -67,7 +67,10 @@ def test_gemm_validation_codes(field, value, status):
 
 
 @pytest.mark.parametrize("a_stride,b_stride,dtype,M,N,K,want", [
-    ((0, 8192, 1), (0, 8192, 1), _abi.TVK_F16, 8192, 8192, 8192, "gemm16_mfma_256x256_w8"),
+    ((0, 8192, 1), (0, 8192, 1), _abi.TVK_F16, 8192, 8192, 8192, "gemm16_dma_256x256"),
+    ((0, 1, 8192), (0, 1, 8192), _abi.TVK_BF16, 8192, 8192, 4096, "gemm16_dma_256x256"),
+    ((0, 8200, 1), (0, 8192, 1), _abi.TVK_F16, 8192, 8192, 8200, "gemm16_mfma_256x256_w8"),   # K % 32 != 0
+    ((0, 8193, 1), (0, 8192, 1), _abi.TVK_F16, 8192, 8192, 8192, "gemm16_mfma_256x256_w8"),   # rows not 16 B aligned
     ((0, 4096, 1), (0, 1, 4096), _abi.TVK_F16, 256, 4096, 4096, "gemm16_mfma_128x128"),
     ((0, 4096, 1), (0, 14336, 1), _abi.TVK_F16, 16, 14336, 4096, "gemm16_skinny_bn"),
     ((0, 4096, 1), (0, 1, 4096), _abi.TVK_BF16, 8, 4096, 4096, "gemm16_skinny_bk"),

@@ -84,6 +84,75 @@ def test_integer_exact_ragged_unaligned(gpu, dtype):
 
 
 # ---------------------------------------------------------------------------
+# the 256x256 LDS-ring kernel (gemm16_dma_256x256): integer operands keep the
+# fp32 accumulator exact, so the result is the exact sum rounded once to T, in
+# any summation order; float64 numpy plus one torch rounding is the reference
+# ---------------------------------------------------------------------------
+
+def _exact_ref(a, b, dtype):
+    r = a.double().numpy() @ b.double().numpy()
+    return decode(to_np(torch.from_numpy(r).to(dtype)), dtype)
+
+
+DMA_SHAPES = [
+    (4096, 3072, 96),    # K shorter than the four-stage ring
+    (4000, 3000, 32),    # one stage; ragged M and N
+    (2560, 5120, 1024),
+]
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("shape", DMA_SHAPES)
+def test_dma_kernel_integer_exact(gpu, dtype, ta, tb, shape):
+    M, N, K = shape
+    lo, hi = (-4, 5) if K <= 128 else (-2, 3)
+    a = randint((K, M) if ta else (M, K), dtype, 14, lo, hi)
+    b = randint((N, K) if tb else (K, N), dtype, 15, lo, hi)
+    a = a.t() if ta else a
+    b = b.t() if tb else b
+    got, plan = run(gpu, a, b, (M, N), dtype)
+    assert plan == "gemm16_dma_256x256"
+    assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+def test_dma_kernel_column_edge_inside_a_chunk(gpu, dtype):
+    # N = 3001 of rows strided 3008: the last 16-byte chunk of a B row would
+    # straddle N, so the ring kernel declines and another kernel runs
+    K = 64
+    a = randint((4096, K), dtype, 16)
+    wide = randint((K, 3008), dtype, 17)
+    b = wide[:, :3001]
+    got, plan = run(gpu, a, b, (4096, 3001), dtype)
+    assert plan != "gemm16_dma_256x256"
+    assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+def test_dma_kernel_batched(gpu, dtype):
+    a = randint((3, 1024, 64), dtype, 18)
+    b = randint((3, 64, 4096), dtype, 19)
+    got, plan = run(gpu, a, b, (3, 1024, 4096), dtype)
+    assert plan == "gemm16_dma_256x256"
+    assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("act", [orc.ACT_NONE, orc.ACT_RELU, orc.ACT_GELU])
+def test_dma_kernel_epilogue_sampled_rows(gpu, dtype, act):
+    M, N, K = 4096, 3072, 256
+    a = randn((M, K), dtype, 20)
+    b = randn((N, K), dtype, 21).t()
+    bias = randn((N,), dtype, 22)
+    got, plan = run(gpu, a, b, (M, N), dtype, bias=bias, alpha=0.5, beta=2.0, act=act)
+    assert plan == "gemm16_dma_256x256"
+    rows = np.r_[0:3, 255:258, 1000:1003, M - 3:M]
+    ref = oracle_mm(a[rows], b, dtype, bias=bias, alpha=0.5, beta=2.0, act=act)
+    assert_close(got[rows], ref, dtype, plan)
+
+
+# ---------------------------------------------------------------------------
 # C2: MLP addmm chain (fp16 / fp32 accumulate), forward and backward
 # ---------------------------------------------------------------------------
 

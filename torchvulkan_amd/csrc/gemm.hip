@@ -151,23 +151,6 @@ struct TileLoader {
     }
 };
 
-// Maps a block index to its (tile_m, tile_n) so that the blocks one XCD runs
-// at a time cover a compact patch of C: blocks are dealt to the 8 XCDs round
-// robin, so consecutive ids on one XCD are made consecutive in a grouped
-// (GROUP_M rows at a time) column-major walk over the tiles.
-__device__ inline void tile_of(int bid, int nblocks, int tiles_m, int tiles_n, int& tm, int& tn) {
-    int lid = bid;
-    if (nblocks % 8 == 0) lid = (bid % 8) * (nblocks / 8) + bid / 8;
-    const int GM = 8;
-    int per_group = GM * tiles_n;
-    int g = lid / per_group;
-    int first_m = g * GM;
-    int gm = min(tiles_m - first_m, GM);
-    int in = lid % per_group;
-    tm = first_m + in % gm;
-    tn = in / gm;
-}
-
 // WGN: waves along N (2 or 4); 2 waves along M. NT = 128 * WGN threads.
 template <int DT, bool AK, bool BK, int BM, int BN, bool VEC, int WGN>
 __global__ __launch_bounds__(128 * WGN) void gemm16_mfma_kernel(GemmArgs p) {
@@ -485,7 +468,7 @@ __global__ __launch_bounds__(256) void gemm_seq_mfma_kernel(GemmArgs p) {
 // host dispatch
 // ----------------------------------------------------------------------------
 
-enum class Kern { K0, GENERIC, SEQ256, SEQ128, MFMA256, MFMA256W8, MFMA128, SKINNY };
+enum class Kern { K0, GENERIC, SEQ256, SEQ128, MFMA256, MFMA256W8, MFMA128, SKINNY, DMA256 };
 
 struct Plan {
     Kern kern;
@@ -497,6 +480,22 @@ bool fits_i32(int64_t v) { return v >= 0 && v <= 0x7fffffff; }
 
 int64_t operand_extent_bytes(int64_t rows, int64_t s_row, int64_t cols, int64_t s_col, size_t es) {
     return (int64_t)es * ((rows - 1) * s_row + (cols - 1) * s_col + 1);
+}
+
+GemmArgs make_args(const tvk_gemm_desc& d) {
+    GemmArgs p;
+    memset(&p, 0, sizeof(p));
+    p.a = d.a; p.b = d.b; p.bias = d.bias; p.c = d.c;
+    for (int i = 0; i < 3; ++i) {
+        p.sa[i] = d.a_stride[i]; p.sb[i] = d.b_stride[i]; p.sbias[i] = d.bias_stride[i]; p.sc[i] = d.c_stride[i];
+    }
+    p.M = (int)d.M; p.N = (int)d.N; p.K = (int)d.K;
+    p.batch = (int)d.batch;
+    p.alpha = (float)d.alpha;
+    p.beta = (float)d.beta;
+    p.has_bias = (d.bias != nullptr && d.beta != 0.0) ? 1 : 0;
+    p.act = d.activation;
+    return p;
 }
 
 Plan make_plan(const tvk_gemm_desc& d) {
@@ -540,6 +539,9 @@ Plan make_plan(const tvk_gemm_desc& d) {
     if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
         pl.kern = big ? Kern::SEQ256 : Kern::SEQ128;
         pl.name = big ? "gemm_seq_mfma_256x256" : "gemm_seq_mfma_128x128";
+    } else if (big && dma_applies(make_args(d), a_k, b_k)) {
+        pl.kern = Kern::DMA256;
+        pl.name = "gemm16_dma_256x256";
     } else if (big) {
         static const bool w8 = getenv("TVK_GEMM_W4") == nullptr;
         pl.kern = w8 ? Kern::MFMA256W8 : Kern::MFMA256;
@@ -578,17 +580,7 @@ void launch_seq(const Plan& pl, GemmArgs& p, dim3 grid, hipStream_t s) {
 
 template <int DT>
 tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
-    GemmArgs p;
-    memset(&p, 0, sizeof(p));
-    p.a = d.a; p.b = d.b; p.bias = d.bias; p.c = d.c;
-    for (int i = 0; i < 3; ++i) {
-        p.sa[i] = d.a_stride[i]; p.sb[i] = d.b_stride[i]; p.sbias[i] = d.bias_stride[i]; p.sc[i] = d.c_stride[i];
-    }
-    p.M = (int)d.M; p.N = (int)d.N; p.K = (int)d.K;
-    p.alpha = (float)d.alpha;
-    p.beta = (float)d.beta;
-    p.has_bias = (d.bias != nullptr && d.beta != 0.0) ? 1 : 0;
-    p.act = d.activation;
+    const GemmArgs p = make_args(d);
 
     const int64_t max_y = 65535;
     for (int64_t b0 = 0; b0 < d.batch; b0 += max_y) {
@@ -624,6 +616,12 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
                 hipError_t e = launch_skinny(DT, q, pl.bk, pl.vec, s);
                 if (e != hipSuccess) return fail(e == hipErrorOutOfMemory ? TVK_ERR_OOM : TVK_ERR_DEVICE,
                                                   std::string("tvk_gemm: skinny launch failed: ") + hipGetErrorString(e));
+            }
+            break;
+        case Kern::DMA256:
+            if constexpr (DT != TVK_F32) {
+                hipError_t e = launch_dma(DT, q, pl.ak, pl.bk, s);
+                if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_gemm: launch failed: ") + hipGetErrorString(e));
             }
             break;
         case Kern::MFMA256:

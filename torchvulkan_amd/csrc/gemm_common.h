@@ -77,6 +77,23 @@ __device__ inline void store_frag16(const GemmArgs& p, int b, int row0, int col,
 }
 
 
+// Maps a block index to its (tile_m, tile_n) so that the blocks one XCD runs
+// at a time cover a compact patch of C: blocks are dealt to the 8 XCDs round
+// robin, so consecutive ids on one XCD are made consecutive in a grouped
+// (GROUP_M rows at a time) column-major walk over the tiles.
+__device__ inline void tile_of(int bid, int nblocks, int tiles_m, int tiles_n, int& tm, int& tn) {
+    int lid = bid;
+    if (nblocks % 8 == 0) lid = (bid % 8) * (nblocks / 8) + bid / 8;
+    const int GM = 8;
+    int per_group = GM * tiles_n;
+    int g = lid / per_group;
+    int first_m = g * GM;
+    int gm = min(tiles_m - first_m, GM);
+    int in = lid % per_group;
+    tm = first_m + in % gm;
+    tn = in / gm;
+}
+
 // Out-of-range buffer offset: the hardware returns zeros for it.
 constexpr uint32_t kOOB = 0x80000000u;
 
@@ -113,6 +130,12 @@ __device__ inline u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, bool row_ok, int64_
 // one resets it before it exits).
 void* device_workspace(int device, size_t bytes);
 uint32_t* device_counters(int device, size_t count);
+
+// 256x256-tile kernel with operands fetched straight into LDS (gemm_dma.hip).
+// dma_applies: the operands meet its alignment and K granularity; launch_dma
+// returns hipSuccess or the launch error.
+bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor);
+hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s);
 
 // M <= 16 streaming kernel (gemm_skinny.hip). b_kmajor: B's k stride is 1.
 // vec: 16-byte loads are legal for A and B. Returns hipSuccess or the launch error.

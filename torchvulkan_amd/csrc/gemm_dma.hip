@@ -1,0 +1,269 @@
+// float16/bfloat16 GEMM for large problems on gfx950: 256x256 workgroup tiles,
+// 8 waves (two per SIMD), v_mfma_f32_16x16x32, operands fetched from global
+// memory straight into LDS by buffer loads (no register staging) through a
+// ring of four 32-k stages.
+//
+// Reference semantics: the same operand model and epilogue as the other
+// tvk_gemm kernels (src/shaders/helpers/gemm.slang:3-9,
+// src/shaders/helpers/gemm_simd.slang:67-99); only the summation order inside
+// a 32-k step differs (the MFMA's), as with the reference's coop-matrix path
+// (src/shaders/ops/matmul_coop.slang:172-222).
+//
+// LDS layouts (per stage, per operand, 16 KB):
+//   k-contiguous operand ("KM"): 256 rows x 32 k, 64 B per row. Row r's 16-byte
+//     chunk c sits at slot c ^ swz_km(r), so the 16 rows one fragment read
+//     touches fall on distinct banks.
+//   m/n-contiguous operand ("MN"): 32 k-rows x 256 columns, 512 B per row,
+//     chunk slot c ^ swz_mn(k). Fragments are read with ds_read_b64_tr_b16,
+//     which transposes 4 k-rows x 16 columns across each 16-lane group.
+// Each buffer load writes one contiguous 1 KB block of LDS (lane l's 16 bytes
+// at offset 16*l), so every block is 16 KM rows or 2 MN rows.
+//
+// Pipeline, per 32-k stage kt (each wave: 32 MFMAs of 16x16x32 on a 128x64
+// wave tile): the MFMAs use fragments already in registers; between them the
+// wave reads the next stage's fragments and issues its share of the loads of
+// stage kt+4 into the slot stage kt occupied (free: every wave read it before
+// the previous barrier). One barrier per stage, after waiting until stage kt+2
+// has landed. The loads are issued from inline assembly: a compiler-visible
+// LDS-DMA would make every later LDS read wait for all of them.
+#include "gemm_common.h"
+
+#include <type_traits>
+
+namespace tvk {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define TVK_LDS __attribute__((address_space(3)))
+
+constexpr int D_BM = 256, D_BN = 256, D_BK = 32, D_NS = 4;
+constexpr int D_NW = 8, D_NT = 64 * D_NW;        // 2 waves along M x 4 along N
+constexpr int D_WTM = 128, D_WTN = 64;           // wave tile
+constexpr int D_FM = D_WTM / 16, D_FN = D_WTN / 16;
+constexpr int D_OPB = 256 * D_BK * 2;            // bytes per operand per stage
+constexpr int D_STB = 2 * D_OPB;                 // bytes per stage
+constexpr int D_DPW = D_OPB / 1024 / D_NW;       // loads per wave per operand per stage
+constexpr int D_DPS = 2 * D_DPW;                 // loads per wave per stage
+
+// Buffer resource over [p, p + bytes): loads past the end return zeros.
+__device__ inline i32x4 dma_rsrc(const void* p, int64_t bytes) {
+    const uint64_t a = (uint64_t)p;
+    return i32x4{(int)(uint32_t)a, (int)((a >> 32) & 0xffff), (int)min(bytes, (int64_t)0x7fffffff), 0x00020000};
+}
+
+// 16 bytes per lane from r + voff into LDS at lds_addr + 16 * lane (lds_addr
+// is wave-uniform; it travels in M0).
+__device__ inline void dma16(i32x4 r, uint32_t lds_addr, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(lds_addr), "v"(voff), "s"(r) : "memory");
+}
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+__device__ inline int swz_km(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+__device__ inline int swz_mn(int kr) { return (kr & 3) * 2; }
+
+// Per-lane source offsets (bytes, at k = 0) of one operand's loads. Rows or
+// columns outside the matrix start at kOOB, so with the k advance added they
+// stay past the buffer's end and load zeros.
+template <bool KM>
+struct DmaSrc {
+    uint32_t off[D_DPW];
+    uint32_t kstep;   // bytes per stage along k
+    __device__ inline void init(int64_t s_row, int64_t s_k, int row0, int rows, int wave, int lane) {
+#pragma unroll
+        for (int i = 0; i < D_DPW; ++i) {
+            const int blk = wave * D_DPW + i;
+            if constexpr (KM) {
+                const int row = blk * 16 + lane / 4;
+                const int c = (lane % 4) ^ swz_km(row);
+                const int gr = row0 + row;
+                off[i] = gr < rows ? (uint32_t)(((int64_t)gr * s_row + c * 8) * 2) : kOOB;
+            } else {
+                const int kr = blk * 2 + lane / 32;
+                const int c = (lane % 32) ^ swz_mn(kr);
+                const int gc = row0 + c * 8;
+                off[i] = gc < rows ? (uint32_t)(((int64_t)kr * s_k + gc) * 2) : kOOB;
+            }
+        }
+        kstep = KM ? (uint32_t)(D_BK * 2) : (uint32_t)(D_BK * s_k * 2);
+    }
+};
+
+// One 16x16x32 operand fragment: lane l holds row (or column) l % 16 and
+// k = (l / 16) * 8 .. + 7 of the stage.
+template <bool KM>
+__device__ inline u32x4 read_frag(uint32_t base, int row_base, int lane) {
+    if constexpr (KM) {
+        const int row = row_base + lane % 16;
+        const int chunk = lane / 16;
+        return *(const TVK_LDS u32x4*)(uintptr_t)(base + row * (2 * D_BK) + ((chunk ^ swz_km(row)) * 16));
+    } else {
+        // source lane s of group g points at k-row 8g + 4rr + s/4, columns 4(s%4)..+3;
+        // the transpose hands lane s the four k values of column s
+        const int g = lane / 16, s = lane % 16;
+        const int col = row_base + (s % 4) * 4;
+        const int chunk = col / 8, within = (col % 8) * 2;
+        u32x4 out;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int kr = g * 8 + rr * 4 + s / 4;
+            TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(base + kr * 512 + ((chunk ^ swz_mn(kr)) * 16) + within);
+            const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+            out[rr * 2] = w.x;
+            out[rr * 2 + 1] = w.y;
+        }
+        return out;
+    }
+}
+
+template <int DT>
+__device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (DT == TVK_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <int DT, bool AK, bool BK>
+__global__ __launch_bounds__(D_NT) void gemm16_dma_kernel(GemmArgs p) {
+    __shared__ __attribute__((aligned(1024))) char lds_raw[D_NS * D_STB];
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds_raw);
+    const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int wm = wave / 4, wn = wave % 4;
+    const int b = blockIdx.y;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * D_BM, n0 = tn * D_BN;
+
+    // A: (m, k) at m*sa[1] + k*sa[2]; B: (k, n) at k*sb[1] + n*sb[2]
+    const char* A = reinterpret_cast<const char*>(p.a) + (int64_t)b * p.sa[0] * 2;
+    const char* B = reinterpret_cast<const char*>(p.b) + (int64_t)b * p.sb[0] * 2;
+    const i32x4 ra = dma_rsrc(A, 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1));
+    const i32x4 rb = dma_rsrc(B, 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1));
+    DmaSrc<AK> da;
+    DmaSrc<BK> db;
+    da.init(p.sa[1], p.sa[2], m0, p.M, wave, lane);
+    db.init(p.sb[2], p.sb[1], n0, p.N, wave, lane);
+    auto dma_one = [&](int kt, int q) {   // q-th load (of D_DPS) of this wave for stage kt
+        const uint32_t slot = lds0 + (uint32_t)((kt % D_NS) * D_STB);
+        if (q < D_DPW) dma16(ra, slot + (uint32_t)((wave * D_DPW + q) * 1024), da.off[q] + (uint32_t)kt * da.kstep);
+        else dma16(rb, slot + D_OPB + (uint32_t)((wave * D_DPW + q - D_DPW) * 1024), db.off[q - D_DPW] + (uint32_t)kt * db.kstep);
+    };
+
+    f32x4 acc[D_FM][D_FN];
+#pragma unroll
+    for (int i = 0; i < D_FM; ++i)
+#pragma unroll
+        for (int j = 0; j < D_FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    u32x4 fa[2][D_FM], fb[2][D_FN];
+    const int nk = p.K / D_BK;
+    // prologue: stages 0..3 in flight; stage 0's fragments in registers once it
+    // has landed, stage 1 landed before the loop reads it
+#pragma unroll
+    for (int s = 0; s < D_NS; ++s)
+#pragma unroll
+        for (int q = 0; q < D_DPS; ++q) dma_one(s, q);
+    wait_vmcnt<D_DPS * (D_NS - 1)>();
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < D_FM; ++i) fa[0][i] = read_frag<AK>(lds0, wm * D_WTM + i * 16, lane);
+#pragma unroll
+    for (int j = 0; j < D_FN; ++j) fb[0][j] = read_frag<BK>(lds0 + D_OPB, wn * D_WTN + j * 16, lane);
+    wait_vmcnt<D_DPS * (D_NS - 2)>();
+    __syncthreads();
+
+    // Stage kt: MFMAs from register set `cur`; in between, one fragment read
+    // of stage kt+1 (into set cur^1) after each even MFMA and one load of
+    // stage kt+4 after each odd one, in this exact order (sched_barrier).
+    auto body = [&](int kt, auto cur_c) {
+        constexpr int cur = decltype(cur_c)::value;
+        const uint32_t st_next = lds0 + (uint32_t)(((kt + 1) % D_NS) * D_STB);
+#pragma unroll
+        for (int q = 0; q < D_FM * D_FN; ++q) {
+            const int i = q / D_FN, j = q % D_FN;
+            acc[i][j] = mfma16<DT>(fa[cur][i], fb[cur][j], acc[i][j]);
+            if (q % 2 == 0) {
+                const int r = q / 2;
+                if (r < D_FM) fa[cur ^ 1][r] = read_frag<AK>(st_next, wm * D_WTM + r * 16, lane);
+                else if (r < D_FM + D_FN) fb[cur ^ 1][r - D_FM] = read_frag<BK>(st_next + D_OPB, wn * D_WTN + (r - D_FM) * 16, lane);
+            } else if (q / 2 < D_DPS) {
+                dma_one(kt + D_NS, q / 2);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // stage kt+2 landed for this wave; after the barrier, for all waves
+        wait_vmcnt<D_DPS * (D_NS - 2)>();
+        __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        body(kt, std::integral_constant<int, 0>{});
+        body(kt + 1, std::integral_constant<int, 1>{});
+    }
+    if (kt < nk) body(kt, std::integral_constant<int, 0>{});
+    // loads of stages past the end are still in flight: drain them before
+    // the workgroup's LDS can be handed to another
+    wait_vmcnt<0>();
+
+    // accumulator layout of v_mfma_f32_16x16x32: lane l holds column l % 16,
+    // register r holds row (l / 16) * 4 + r
+#pragma unroll
+    for (int i = 0; i < D_FM; ++i)
+#pragma unroll
+        for (int j = 0; j < D_FN; ++j) {
+            const int col = n0 + wn * D_WTN + j * 16 + lane % 16;
+            if (col >= p.N) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm * D_WTM + i * 16 + (lane / 16) * 4 + r;
+                if (row < p.M) store_out<DT>(p, b, row, col, acc[i][j][r]);
+            }
+        }
+}
+
+}  // namespace
+
+bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor) {
+    if (p.K < D_BK || p.K % D_BK != 0) return false;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!al16(p.a) || !al16(p.b)) return false;
+    if (p.batch > 1 && (p.sa[0] % 8 != 0 || p.sb[0] % 8 != 0)) return false;
+    // every 16-byte chunk starts 16-byte aligned: the stride between the rows
+    // of the contiguous dimension is a multiple of 8 elements
+    const int64_t a_rows = a_kmajor ? p.sa[1] : p.sa[2];
+    const int64_t b_rows = b_kmajor ? p.sb[2] : p.sb[1];
+    if ((a_kmajor ? p.M : p.K) > 1 && a_rows % 8 != 0) return false;
+    if ((b_kmajor ? p.N : p.K) > 1 && b_rows % 8 != 0) return false;
+    // an m/n-contiguous operand whose last chunk straddled M or N would lose
+    // the valid part of that chunk on the last k-row: the range check ends
+    // the buffer at the last element, and extending it would read memory the
+    // tensor may not own
+    if (!a_kmajor && p.M % 8 != 0) return false;
+    if (!b_kmajor && p.N % 8 != 0) return false;
+    return true;
+}
+
+hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s) {
+    p.tiles_m = (p.M + D_BM - 1) / D_BM;
+    p.tiles_n = (p.N + D_BN - 1) / D_BN;
+    const dim3 grid(p.tiles_m * p.tiles_n, p.batch);
+#define TVK_DMA_LAUNCH(DT)                                                                                     \
+    do {                                                                                                       \
+        if (a_kmajor && b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, true>), grid, dim3(D_NT), 0, s, p);   \
+        else if (a_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, false>), grid, dim3(D_NT), 0, s, p);         \
+        else if (b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, true>), grid, dim3(D_NT), 0, s, p);         \
+        else hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, false>), grid, dim3(D_NT), 0, s, p);                      \
+    } while (0)
+    if (dtype == TVK_F16) TVK_DMA_LAUNCH(TVK_F16);
+    else TVK_DMA_LAUNCH(TVK_BF16);
+#undef TVK_DMA_LAUNCH
+    return hipGetLastError();
+}
+
+}  // namespace tvk
