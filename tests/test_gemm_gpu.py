@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from tests.gemm_cases import (TOL, assert_bit_exact, assert_close, decode, oracle_mm, randint, randn, to_np)
+from tests.gemm_cases import (TOL, gen, assert_bit_exact, assert_close, decode, oracle_mm, randint, randn, to_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -149,6 +149,49 @@ def test_dma_kernel_epilogue_sampled_rows(gpu, dtype, act):
     assert plan == "gemm16_dma_256x256"
     rows = np.r_[0:3, 255:258, 1000:1003, M - 3:M]
     ref = oracle_mm(a[rows], b, dtype, bias=bias, alpha=0.5, beta=2.0, act=act)
+    assert_close(got[rows], ref, dtype, plan)
+
+
+# ---------------------------------------------------------------------------
+# split-K (few output tiles, long K): float32 partials summed in split order
+# ---------------------------------------------------------------------------
+
+SPLIT_CASES = [
+    # (M, N, K, ta, tb, batch): dW = dY^T X of a transformer layer, a batch-256
+    # MLP layer, K not a multiple of the chunk, and a batched case
+    (512, 512, 8192, True, False, 1),
+    (256, 4096, 4096, False, True, 1),
+    (384, 320, 5000, False, False, 1),
+    (256, 256, 4096, False, False, 2),
+]
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_split_k_integer_exact(gpu, dtype, case):
+    M, N, K, ta, tb, batch = case
+    lead = (batch,) if batch > 1 else ()
+    a = randint(lead + ((K, M) if ta else (M, K)), dtype, 23, -2, 3)
+    b = randint(lead + ((N, K) if tb else (K, N)), dtype, 24, -2, 3)
+    a = a.transpose(-1, -2) if ta else a
+    b = b.transpose(-1, -2) if tb else b
+    got, plan = run(gpu, a, b, lead + (M, N), dtype)
+    assert plan == "gemm16_mfma_128x128_splitk"
+    assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("act", [orc.ACT_NONE, orc.ACT_RELU, orc.ACT_GELU])
+def test_split_k_epilogue_sampled_rows(gpu, dtype, act):
+    # C2 forward layer: addmm(bias, x, W^T) with the fused activation
+    M, N, K = 256, 4096, 4096
+    a = torch.rand((M, K), generator=gen(25)).to(dtype)
+    b = ((torch.rand((N, K), generator=gen(26)) * 2 - 1) * K ** -0.5).to(dtype).t()
+    bias = ((torch.rand((N,), generator=gen(27)) * 2 - 1) * K ** -0.5).to(dtype)
+    got, plan = run(gpu, a, b, (M, N), dtype, bias=bias, alpha=1.0, beta=1.0, act=act)
+    assert plan == "gemm16_mfma_128x128_splitk"
+    rows = np.r_[0:4, 127:130, M - 4:M]
+    ref = oracle_mm(a[rows], b, dtype, bias=bias, alpha=1.0, beta=1.0, act=act)
     assert_close(got[rows], ref, dtype, plan)
 
 

@@ -167,11 +167,18 @@ __global__ __launch_bounds__(128 * WGN) void gemm16_mfma_kernel(GemmArgs p) {
     tile_of(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
 
-    // operand buffers of this batch: A rows are M, B rows are N
+    // operand buffers of this batch (and of this k split): A rows are M, B rows are N
     const uint16_t* A = reinterpret_cast<const uint16_t*>(p.a) + (int64_t)b * p.sa[0];
     const uint16_t* B = reinterpret_cast<const uint16_t*>(p.b) + (int64_t)b * p.sb[0];
-    const int64_t a_bytes = 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1);
-    const int64_t b_bytes = 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1);
+    int K = p.K;
+    if (p.split > 1) {
+        const int kb = blockIdx.z * p.k_chunk;
+        A += (int64_t)kb * p.sa[2];
+        B += (int64_t)kb * p.sb[1];
+        K = min(p.k_chunk, p.K - kb);
+    }
+    const int64_t a_bytes = 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(K - 1) * p.sa[2] + 1);
+    const int64_t b_bytes = 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(K - 1) * p.sb[1] + 1);
     __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)min(a_bytes, (int64_t)0x7fffffff), 0x00020000);
     __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)B, 0, (int)min(b_bytes, (int64_t)0x7fffffff), 0x00020000);
 
@@ -187,9 +194,9 @@ __global__ __launch_bounds__(128 * WGN) void gemm16_mfma_kernel(GemmArgs p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     // A: row stride sa[1] (over M), k stride sa[2]; B: "row" = N with stride sb[2], k stride sb[1]
-    const int nk = (p.K + H_BK - 1) / H_BK;
-    la.load(ra, p.sa[1], p.sa[2], m0, p.M, 0, p.K, tid);
-    lb.load(rb, p.sb[2], p.sb[1], n0, p.N, 0, p.K, tid);
+    const int nk = (K + H_BK - 1) / H_BK;
+    la.load(ra, p.sa[1], p.sa[2], m0, p.M, 0, K, tid);
+    lb.load(rb, p.sb[2], p.sb[1], n0, p.N, 0, K, tid);
     la.store(lds[0], tid);
     lb.store(lds[0] + BM * H_LDK, tid);
     __syncthreads();
@@ -221,8 +228,8 @@ __global__ __launch_bounds__(128 * WGN) void gemm16_mfma_kernel(GemmArgs p) {
             const int cur = kk & 1;
             if (kk + 1 < H_BK / 16) read_frags(base, (kk + 1) * 16, cur ^ 1);
             if (kk == 0) {
-                la.load(ra, p.sa[1], p.sa[2], m0, p.M, (kt + 1) * H_BK, p.K, tid);
-                lb.load(rb, p.sb[2], p.sb[1], n0, p.N, (kt + 1) * H_BK, p.K, tid);
+                la.load(ra, p.sa[1], p.sa[2], m0, p.M, (kt + 1) * H_BK, K, tid);
+                lb.load(rb, p.sb[2], p.sb[1], n0, p.N, (kt + 1) * H_BK, K, tid);
             }
             if (kk == H_BK / 16 - 1) {
                 la.store(lds[buf ^ 1], tid);
@@ -260,11 +267,42 @@ __global__ __launch_bounds__(128 * WGN) void gemm16_mfma_kernel(GemmArgs p) {
 
     // accumulator layout of v_mfma_f32_32x32x16: lane holds column lane%32,
     // register r holds row (r/4)*8 + (lane/32)*4 + r%4
+    if (p.split > 1) {
+        float* part = p.part + ((int64_t)blockIdx.z * p.batch + b) * p.M * p.N;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int row0 = m0 + wm * WM + i * 32 + (lane / 32) * 4, col = n0 + wn * WN + j * 32 + lane % 32;
+                if (col >= p.N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = row0 + (r / 4) * 8 + (r % 4);
+                    if (row < p.M) part[(int64_t)row * p.N + col] = acc[i][j][r];
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
             store_frag16<DT>(p, b, m0 + wm * WM + i * 32 + (lane / 32) * 4, n0 + wn * WN + j * 32 + lane % 32, acc[i][j]);
+}
+
+// Sums the split-K partials of one output in split order, then applies the
+// epilogue and rounds once to the output type.
+template <int DT>
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmArgs p) {
+    const int64_t mn = (int64_t)p.M * p.N;
+    const int64_t total = (int64_t)p.batch * mn;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+        const int b = (int)(idx / mn);
+        const int64_t e = idx - (int64_t)b * mn;
+        float v = p.part[idx];
+        for (int z = 1; z < p.split; ++z) v += p.part[(int64_t)z * total + idx];
+        store_out<DT>(p, b, (int)(e / p.N), (int)(e % p.N), v);
+    }
 }
 
 // ----------------------------------------------------------------------------
@@ -474,6 +512,7 @@ struct Plan {
     Kern kern;
     bool ak = true, bk = true, vec = true;
     const char* name;
+    int split = 1, k_chunk = 0;   // MFMA128 split-K
 };
 
 bool fits_i32(int64_t v) { return v >= 0 && v <= 0x7fffffff; }
@@ -549,6 +588,21 @@ Plan make_plan(const tvk_gemm_desc& d) {
     } else {
         pl.kern = Kern::MFMA128;
         pl.name = "gemm16_mfma_128x128";
+        // Few output tiles and a long K (weight gradients, batch-256 layers):
+        // split K so about one workgroup per CU runs, partials in float32.
+        const int64_t t128 = ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
+        if (t128 < 192 && d.K >= 1024) {
+            int64_t split = std::min<int64_t>({(256 + t128 - 1) / t128, d.K / 256, 32});
+            if (split >= 2) {
+                const int64_t chunk = ((d.K + split - 1) / split + 63) / 64 * 64;
+                split = (d.K + chunk - 1) / chunk;
+                if (split >= 2 && split * d.batch * d.M * d.N * 4 <= (int64_t(512) << 20)) {
+                    pl.split = (int)split;
+                    pl.k_chunk = (int)chunk;
+                    pl.name = "gemm16_mfma_128x128_splitk";
+                }
+            }
+        }
     }
     return pl;
 }
@@ -634,7 +688,19 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
                 dim3 grid(q.tiles_m * q.tiles_n, nb);
                 if (pl.kern == Kern::MFMA256W8) launch_mfma<DT, 256, 256, 4>(pl, q, grid, s);
                 else if (pl.kern == Kern::MFMA256) launch_mfma<DT, 256, 256, 2>(pl, q, grid, s);
-                else launch_mfma<DT, 128, 128, 2>(pl, q, grid, s);
+                else if (pl.split > 1) {
+                    int dev = 0;
+                    (void)hipGetDevice(&dev);
+                    q.part = static_cast<float*>(device_workspace(dev, (size_t)pl.split * nb * d.M * d.N * 4));
+                    if (!q.part) return fail(TVK_ERR_OOM, "tvk_gemm: no workspace for split-K partials");
+                    q.split = pl.split;
+                    q.k_chunk = pl.k_chunk;
+                    grid.z = pl.split;
+                    launch_mfma<DT, 128, 128, 2>(pl, q, grid, s);
+                    const int64_t total = (int64_t)nb * d.M * d.N;
+                    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+                    hipLaunchKernelGGL(gemm_split_reduce_kernel<DT>, dim3(blocks), dim3(256), 0, s, q);
+                } else launch_mfma<DT, 128, 128, 2>(pl, q, grid, s);
             }
             break;
         }

@@ -18,6 +18,12 @@ struct GemmArgs {
     int has_bias;
     int act;
     int tiles_m, tiles_n;
+    // split-K (split > 1): blockIdx.z takes k in [z*k_chunk, (z+1)*k_chunk) and
+    // writes float32 partials to part[z][batch][M][N]; a second kernel sums
+    // them in z order and applies the epilogue
+    float* part;
+    int k_chunk;
+    int split;
 };
 
 // ----------------------------------------------------------------------------
