@@ -415,7 +415,9 @@ def test_exact_mode_bit_identical(gpu, dtype):
 
 
 # ---------------------------------------------------------------------------
-# M <= 16: the HBM-streaming kernel (split K, last-arrival reduction)
+# M <= 16: the HBM-streaming kernels (gemm16_skinny_ring for B n-contiguous
+# with aligned rows, split K with an ordered float32 reduction; the LDS
+# transpose kernel otherwise)
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", F16_TYPES)
@@ -423,7 +425,9 @@ def test_exact_mode_bit_identical(gpu, dtype):
     (16, 14336, 4096, False, True),   # C5 skinny, B row-major
     (16, 14336, 4096, True, True),    # B as a transposed weight view (k-contiguous)
     (1, 4096, 4096, True, True),      # one token through a linear
-    (7, 1000, 2000, False, True),     # ragged rows / last strip
+    (7, 1000, 2000, False, True),     # ragged rows / last strip (K % 32 != 0: not the ring)
+    (9, 4000, 1024, False, True),     # ring, 8-way split, partial last strip
+    (3, 32768, 96, False, True),      # ring without a split: direct epilogue
     (5, 777, 999, False, False),      # K and N not multiples of 8: element loads
     (16, 256, 64, True, True),        # K too small to split
 ])
@@ -445,6 +449,17 @@ def test_skinny_batched_and_repeated(gpu, dtype):
         got, plan = run(gpu, a, b, (6, 4, 640), dtype)
         assert plan.startswith("gemm16_skinny"), plan
         assert_close(got, oracle_mm(a, b, dtype), dtype, plan)
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+def test_skinny_ring_integer_exact(gpu, dtype):
+    # integer operands: partials of every split are exact, so the split sum is
+    # the exact sum rounded once
+    a = randint((16, 4096), dtype, 230, -2, 3)
+    b = randint((4096, 14336), dtype, 231, -2, 3)
+    got, plan = run(gpu, a, b, (16, 14336), dtype)
+    assert plan == "gemm16_skinny_ring_splitk"
+    assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
 
 
 def test_skinny_exact_mode_uses_sequential_kernel(gpu):

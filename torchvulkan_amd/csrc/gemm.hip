@@ -290,21 +290,6 @@ __global__ __launch_bounds__(128 * WGN) void gemm16_mfma_kernel(GemmArgs p) {
             store_frag16<DT>(p, b, m0 + wm * WM + i * 32 + (lane / 32) * 4, n0 + wn * WN + j * 32 + lane % 32, acc[i][j]);
 }
 
-// Sums the split-K partials of one output in split order, then applies the
-// epilogue and rounds once to the output type.
-template <int DT>
-__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmArgs p) {
-    const int64_t mn = (int64_t)p.M * p.N;
-    const int64_t total = (int64_t)p.batch * mn;
-    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
-        const int b = (int)(idx / mn);
-        const int64_t e = idx - (int64_t)b * mn;
-        float v = p.part[idx];
-        for (int z = 1; z < p.split; ++z) v += p.part[(int64_t)z * total + idx];
-        store_out<DT>(p, b, (int)(e / p.N), (int)(e % p.N), v);
-    }
-}
-
 // ----------------------------------------------------------------------------
 // sequential-k kernel on v_mfma_f32_32x32x1f32 (all dtypes; exact mode)
 // ----------------------------------------------------------------------------
@@ -570,7 +555,7 @@ Plan make_plan(const tvk_gemm_desc& d) {
         else v = v && d.N % 8 == 0 && (d.K == 1 || d.b_stride[1] % 8 == 0);
         pl.kern = Kern::SKINNY;
         pl.vec = v;
-        pl.name = skinny_name(b_k);
+        pl.name = skinny_name(make_args(d), b_k, v);
         return pl;
     }
     const int64_t t256 = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;

@@ -100,6 +100,24 @@ __device__ inline void tile_of(int bid, int nblocks, int tiles_m, int tiles_n, i
     tn = in / gm;
 }
 
+namespace {
+// Sums the split-K partials of one output in split order, then applies the
+// epilogue and rounds once to the output type.
+template <int DT>
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmArgs p) {
+    const int64_t mn = (int64_t)p.M * p.N;
+    const int64_t total = (int64_t)p.batch * mn;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+        const int b = (int)(idx / mn);
+        const int64_t e = idx - (int64_t)b * mn;
+        float v = p.part[idx];
+        for (int z = 1; z < p.split; ++z) v += p.part[(int64_t)z * total + idx];
+        store_out<DT>(p, b, (int)(e / p.N), (int)(e % p.N), v);
+    }
+}
+
+}  // namespace
+
 // Out-of-range buffer offset: the hardware returns zeros for it.
 constexpr uint32_t kOOB = 0x80000000u;
 
@@ -146,7 +164,7 @@ hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, hipS
 // M <= 16 streaming kernel (gemm_skinny.hip). b_kmajor: B's k stride is 1.
 // vec: 16-byte loads are legal for A and B. Returns hipSuccess or the launch error.
 hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, hipStream_t s);
-const char* skinny_name(bool b_kmajor);
+const char* skinny_name(const GemmArgs& p, bool b_kmajor, bool vec);
 bool skinny_applies(int64_t M, int64_t N, int64_t K, int64_t batch);
 
 }  // namespace tvk

@@ -12,8 +12,19 @@
 // ([K][N]) is written to a wave-private LDS tile as it arrives and read back
 // along k.
 //
+// B n-contiguous with 16-byte aligned rows ([K][N], the C5 layout) takes a
+// second kernel, gemm16_skinny_ring: workgroups of 8 waves own 128 columns
+// (256 bytes of each row of B) and a K range; B and A arrive by buffer loads
+// straight into a 4-stage LDS ring (no register staging), each wave reads its
+// 16 columns back along k with ds_read_b64_tr_b16 and issues one
+// v_mfma_f32_16x16x32 per 32 k. The K range is split between workgroups
+// until about one workgroup per CU runs; float32 partials are then summed in
+// split order by a second kernel that applies the epilogue.
+//
 // Epilogue semantics are the reference's (src/shaders/helpers/gemm_simd.slang:67-99).
 #include "gemm_common.h"
+
+#include <algorithm>
 
 namespace tvk {
 namespace {
@@ -152,15 +163,164 @@ __global__ __launch_bounds__(64 * SK_NW) void gemm_skinny_kernel(GemmArgs p) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// gemm16_skinny_ring
+// ---------------------------------------------------------------------------
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define TVK_LDS __attribute__((address_space(3)))
+
+constexpr int SR_NB = 128;                 // columns per workgroup
+constexpr int SR_NW = 8;                   // waves, 16 columns each
+constexpr int SR_NS = 4;                   // ring stages of 32 k
+constexpr int SR_ROW = SR_NB * 2;          // bytes of one k-row of the B tile
+constexpr int SR_BST = 32 * SR_ROW;        // B bytes per stage: 8 loads of 1 KB, one per wave
+constexpr int SR_STB = SR_BST + 1024;      // + A: 16 rows x 32 k, one load (wave 0)
+
+__device__ inline i32x4 sr_rsrc(const void* ptr, int64_t bytes) {
+    const uint64_t a = (uint64_t)ptr;
+    return i32x4{(int)(uint32_t)a, (int)((a >> 32) & 0xffff), (int)min(bytes, (int64_t)0x7fffffff), 0x00020000};
+}
+
+// 16 bytes per lane into LDS at lds_addr + 16 * lane (lds_addr wave-uniform,
+// carried in M0). Issued from asm so the compiler does not order every later
+// LDS read behind it; the waits are explicit.
+__device__ inline void sr_dma16(i32x4 r, uint32_t lds_addr, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(lds_addr), "v"(voff), "s"(r) : "memory");
+}
+template <int N>
+__device__ inline void sr_wait() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory"); }
+
+__device__ inline int sr_swz(int kr) { return (kr & 3) * 2; }
+
+// grid (strips, splits, batch); requires A k-contiguous, B n-contiguous, rows
+// of both 16-byte aligned, N % 8 == 0 and k_chunk % 32 == 0.
+template <int DT>
+__global__ __launch_bounds__(64 * SR_NW) void gemm_skinny_ring_kernel(GemmArgs p) {
+    __shared__ __attribute__((aligned(1024))) char lds_raw[SR_NS * SR_STB];
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds_raw);
+    const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int n0 = blockIdx.x * SR_NB, z = blockIdx.y, b = blockIdx.z;
+    const int kb = p.split > 1 ? z * p.k_chunk : 0;
+    const int klen = p.split > 1 ? p.k_chunk : p.K;
+    const int nk = klen / 32;
+
+    const char* A = reinterpret_cast<const char*>(p.a) + (int64_t)b * p.sa[0] * 2;
+    const char* B = reinterpret_cast<const char*>(p.b) + (int64_t)b * p.sb[0] * 2;
+    const i32x4 ra = sr_rsrc(A, 2 * ((int64_t)(p.M - 1) * p.sa[1] + p.K));
+    const i32x4 rb = sr_rsrc(B, 2 * ((int64_t)(p.K - 1) * p.sb[1] + p.N));
+    // wave w loads B block w (k-rows 4w..4w+3 of the stage); wave 0 also loads A
+    const int kr = wave * 4 + lane / 16;
+    const int bc = (lane % 16) ^ sr_swz(kr);
+    const int gc = n0 + bc * 8;
+    const uint32_t b_off = gc < p.N ? (uint32_t)(((int64_t)(kb + kr) * p.sb[1] + gc) * 2) : kOOB;
+    const uint32_t b_step = (uint32_t)(32 * p.sb[1] * 2);
+    const int ar = lane / 4;
+    const uint32_t a_off = ar < p.M ? (uint32_t)(((int64_t)ar * p.sa[1] + kb + (lane % 4) * 8) * 2) : kOOB;
+    auto issue = [&](int s) {
+        if (s >= nk) return;
+        const uint32_t slot = lds0 + (uint32_t)((s % SR_NS) * SR_STB);
+        sr_dma16(rb, slot + (uint32_t)(wave * 1024), b_off + (uint32_t)s * b_step);
+        if (wave == 0) sr_dma16(ra, slot + SR_BST, a_off + (uint32_t)s * 64);
+    };
+
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < SR_NS - 1; ++s) issue(s);
+    // this wave's B fragment: 16 columns, lane s of group g gets k 8g..8g+7 of column s
+    const int g = lane / 16, sl = lane % 16;
+    const int col = wave * 16 + (sl % 4) * 4;
+    const int chunk = col / 8, within = (col % 8) * 2;
+    for (int kt = 0; kt < nk; ++kt) {
+        // stage kt landed; the two stages issued after it may be in flight
+        if (nk - 1 - kt >= SR_NS - 2) {
+            if (wave == 0) sr_wait<2 * (SR_NS - 2)>();
+            else sr_wait<SR_NS - 2>();
+        } else {
+            sr_wait<0>();
+        }
+        __syncthreads();
+        issue(kt + SR_NS - 1);
+        const uint32_t st = lds0 + (uint32_t)((kt % SR_NS) * SR_STB);
+        const u32x4 af = *(const TVK_LDS u32x4*)(uintptr_t)(st + SR_BST + (lane % 16) * 64 + (lane / 16) * 16);
+        u32x4 bf;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int r = g * 8 + rr * 4 + sl / 4;
+            TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(st + r * SR_ROW + ((chunk ^ sr_swz(r)) * 16) + within);
+            const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+            bf[rr * 2] = w.x;
+            bf[rr * 2 + 1] = w.y;
+        }
+        acc = mfma16<DT>(af, bf, acc);
+    }
+    sr_wait<0>();
+
+    // lane l holds column l % 16 of the wave's 16, rows (l / 16) * 4 + r
+    const int n = n0 + wave * 16 + lane % 16;
+    if (n >= p.N) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int m = (lane / 16) * 4 + r;
+        if (m >= p.M) continue;
+        if (p.split > 1) p.part[(((int64_t)z * p.batch + b) * p.M + m) * p.N + n] = acc[r];
+        else store_out<DT>(p, b, m, n, acc[r]);
+    }
+}
+
+// Splits of K for the ring kernel: powers of two while the grid stays within
+// about one workgroup per CU and every split keeps at least 4 stages.
+int ring_splits(const GemmArgs& p) {
+    const int64_t wgs = (int64_t)((p.N + SR_NB - 1) / SR_NB) * p.batch;
+    int split = 1;
+    while (wgs * split * 2 <= 256 && p.K % (64 * split) == 0 && p.K / (2 * split) >= 128) split *= 2;
+    return split;
+}
+
+bool ring_applies(const GemmArgs& p, bool b_kmajor, bool vec) {
+    if (b_kmajor || !vec) return false;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!al16(p.a) || !al16(p.b) || p.sa[2] != 1 || p.sb[2] != 1) return false;
+    if (p.K % 32 != 0 || p.N % 8 != 0 || (p.M > 1 && p.sa[1] % 8 != 0) || (p.K > 1 && p.sb[1] % 8 != 0)) return false;
+    if (p.batch > 1 && (p.sa[0] % 8 != 0 || p.sb[0] % 8 != 0)) return false;
+    return true;
+}
 }  // namespace
 
 bool skinny_applies(int64_t M, int64_t N, int64_t K, int64_t batch) {
     return M >= 1 && M <= 16 && N >= 64 && K >= 64 && batch <= 65535;
 }
 
-const char* skinny_name(bool b_kmajor) { return b_kmajor ? "gemm16_skinny_bk" : "gemm16_skinny_bn"; }
+const char* skinny_name(const GemmArgs& p, bool b_kmajor, bool vec) {
+    if (ring_applies(p, b_kmajor, vec)) return ring_splits(p) > 1 ? "gemm16_skinny_ring_splitk" : "gemm16_skinny_ring";
+    return b_kmajor ? "gemm16_skinny_bk" : "gemm16_skinny_bn";
+}
 
 hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, hipStream_t s) {
+    if (ring_applies(p, b_kmajor, vec)) {
+        GemmArgs q = p;
+        q.split = ring_splits(p);
+        q.k_chunk = p.K / q.split;
+        if (q.split > 1) {
+            int dev = 0;
+            (void)hipGetDevice(&dev);
+            q.part = static_cast<float*>(device_workspace(dev, (size_t)q.split * p.batch * p.M * p.N * 4));
+            if (!q.part) return hipErrorOutOfMemory;
+        }
+        const dim3 grid((p.N + SR_NB - 1) / SR_NB, q.split, p.batch);
+        if (dtype == TVK_F16) hipLaunchKernelGGL(gemm_skinny_ring_kernel<TVK_F16>, grid, dim3(64 * SR_NW), 0, s, q);
+        else hipLaunchKernelGGL(gemm_skinny_ring_kernel<TVK_BF16>, grid, dim3(64 * SR_NW), 0, s, q);
+        if (q.split > 1) {
+            const int64_t total = (int64_t)p.batch * p.M * p.N;
+            const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+            if (dtype == TVK_F16) hipLaunchKernelGGL(gemm_split_reduce_kernel<TVK_F16>, dim3(blocks), dim3(256), 0, s, q);
+            else hipLaunchKernelGGL(gemm_split_reduce_kernel<TVK_BF16>, dim3(blocks), dim3(256), 0, s, q);
+        }
+        return hipGetLastError();
+    }
     const int strips = (p.N + SK_CW - 1) / SK_CW;
     dim3 grid(strips, 1, p.batch);
 #define TVK_SK(D, BKM, V) hipLaunchKernelGGL((gemm_skinny_kernel<D, BKM, V>), grid, dim3(64 * SK_NW), 0, s, p)
