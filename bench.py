@@ -35,7 +35,7 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 # profiles/gemm_fp16_8192_counters.md. Counters need their own profiler runs, so the figure is
 # recorded here per kernel plan rather than measured inside the timed region.
 MEASURED_TRAFFIC = {
-    "gemm16_mfma_256x256_w8": {"bytes": 1.746e9, "fetch_kib": 786764, "write_kib": 131161},
+    "gemm16_dma_256x256": {"bytes": 1.768e9, "fetch_kib": 796263, "write_kib": 133943},
 }
 
 
