@@ -117,6 +117,29 @@ def test_geometry_edge_cases(gpu, dtype, case):
                           case.pop("s"), case.pop("p"), case.pop("hw"), seed=20, **case)
 
 
+# channels-last ring kernels (channel counts in multiples of 32): odd sizes
+# with strides 2 and 3 (sub-pixel grad-input phases of different sizes, and
+# phases no tap reaches), dilation, a rectangular and a 4x4 kernel, a single
+# image, and output planes whose pixel count is not a multiple of 32 (grad
+# weight then takes the element-gather kernel)
+RING_CASES = [
+    dict(n=2, cin=32, cout=64, k=3, s=2, p=1, hw=15),
+    dict(n=3, cin=64, cout=32, k=3, s=1, p=2, hw=12, dil=2),
+    dict(n=2, cin=32, cout=96, k=(1, 3), s=1, p=1, hw=8),
+    dict(n=1, cin=128, cout=256, k=3, s=3, p=0, hw=17),
+    dict(n=2, cin=32, cout=32, k=4, s=2, p=1, hw=16),
+    dict(n=1, cin=64, cout=128, k=1, s=2, p=0, hw=9),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", RING_CASES)
+def test_ring_geometry(gpu, dtype, case):
+    case = dict(case)
+    _check_all_directions(gpu, dtype, case.pop("n"), case.pop("cin"), case.pop("cout"), case.pop("k"),
+                          case.pop("s"), case.pop("p"), case.pop("hw"), seed=40, **case)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_exact_mode_bit_identical(gpu, dtype):
     _check_all_directions(gpu, dtype, 4, 16, 32, 3, 2, 1, 12, seed=30, exact=True)

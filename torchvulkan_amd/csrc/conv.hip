@@ -30,6 +30,7 @@ namespace tvk {
 namespace {
 
 enum { FWD = 0, DGRAD = 1, WGRAD = 2 };
+static_assert(FWD == 0 && DGRAD == 1 && WGRAD == 2, "mode numbers shared with conv_nhwc.hip");
 
 struct ConvArgs {
     const void* x;
@@ -537,6 +538,8 @@ tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
         if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
         return TVK_OK;
     }
+    // channels-last implicit GEMM on the LDS ring (conv_nhwc.hip) where it applies
+    if (conv_ring_applies(d, MODE)) return conv_ring_run(d, MODE, who);
     const bool seq = (d.flags & TVK_GEMM_EXACT) != 0;
     if (MODE == WGRAD) {
         // split the long reduction so the grid covers the device: about 512

@@ -1,0 +1,555 @@
+// 2-D convolution on gfx950 as a channels-last implicit GEMM over the
+// direct-to-LDS ring of gemm_dma.hip: float16/bfloat16, groups == 1, channel
+// counts in multiples of 32 (the layers of the path's ResNet config; other
+// convolutions keep the element-gather kernels of conv.hip).
+//
+// Reference semantics (file:line under the reference tree): the same sums as
+// conv.hip's kernels (src/shaders/helpers/conv.slang:198-511,
+// src/api/ops/conv.cpp:1014-1060) with a different k order inside the
+// reduction (tap-major, channel-minor), which the fp16/bf16 tolerance allows;
+// the strided grad-input runs as stride^2 sub-pixel phases, each a dense GEMM
+// over the taps that reach it, as the reference's subpixel_split does
+// (src/api/ops/conv.cpp:364-382, src/shaders/helpers/conv.slang:135-172,364-432).
+//
+// Layouts. The activation that is gathered goes to NHWC in the library
+// workspace first (one transpose pass), so that 8 consecutive channels are one
+// 16-byte load; the weight is permuted to tap-major order.
+//   forward     C[p][co] = sum_{t,c} x_nhwc[pix(p) + off(t)][c] * Wf[co][t][c]
+//               p = output pixel (n, oh, ow); y is written NCHW
+//   grad input  C[p][c]  = sum_{t,co} dy_nhwc[pix(p) + off(t)][co] * Wd[c][t][co]
+//               p = input pixel of one sub-pixel phase; dx is written NCHW
+//   grad weight C[(t,c)][co] = sum_p x_nhwc[pix(p) + off(t)][c] * dy[n][co][o(p)]
+//               K = output pixels, split into float32 partials reduced in split
+//               order into dW[co][c][t]
+// Tiles are 256 rows (pixels, or (tap, channel) for grad weight) x BN columns
+// (output channels) with BN = 64, 128 or 256, a 4-stage ring of 32-k stages,
+// v_mfma_f32_16x16x32 on 64-column wave tiles.
+#include "tvk_common.h"
+#include "gemm_common.h"
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <type_traits>
+
+namespace tvk {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define TVK_LDS __attribute__((address_space(3)))
+
+constexpr int V_BM = 256, V_BK = 32, V_NS = 4;
+constexpr int V_MAXTAPS = 16;
+
+struct ConvRing {
+    const void* act;     // gathered activation, NHWC (x, or dy for grad input)
+    const void* wt;      // permuted weight [N][T][Cs] (forward / grad input)
+    const void* dyc;     // grad weight: dy, NCHW
+    const void* bias;    // forward
+    void* out;           // y / dx NCHW (forward, grad input); dW (grad weight, no split)
+    float* part;         // grad weight partials [split][M][N]
+    // gather geometry: the activation is [n][Hs][Ws][Cs]
+    int Hs, Ws, Cs;
+    // rows: pixels of an [n][Hp][Wp] grid (forward / grad input)
+    int Hp, Wp;
+    int M, N, K;         // GEMM sizes
+    int ntap;            // taps in this launch (a sub-pixel phase may use a subset)
+    int wt_taps;         // taps per row of the permuted weight
+    int tap_h[V_MAXTAPS], tap_w[V_MAXTAPS], tap_k[V_MAXTAPS];   // row offsets and weight tap of each k tap
+    int pix_sh, pix_sw, pix_bh, pix_bw;   // row pixel (i, j) -> source origin (i*sh + bh, j*sw + bw)
+    // output placement (forward / grad input): pixel (i, j) -> (i*osh + orh, j*osw + orw) of [n][N][Ho][Wo]
+    int Ho, Wo, osh, osw, orh, orw;
+    // grad weight: output pixels per image, width; k per split; taps for the dW order
+    int HWo, Wd, kh_kw, k_chunk, split;
+    int has_bias;
+    int act_bytes, wt_bytes, dyc_bytes;
+};
+
+__device__ inline i32x4 v_rsrc(const void* p, int64_t bytes) {
+    const uint64_t a = (uint64_t)p;
+    return i32x4{(int)(uint32_t)a, (int)((a >> 32) & 0xffff), (int)min(bytes, (int64_t)0x7fffffff), 0x00020000};
+}
+__device__ inline void v_dma16(i32x4 r, uint32_t lds_addr, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(lds_addr), "v"(voff), "s"(r) : "memory");
+}
+template <int N>
+__device__ inline void v_wait() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory"); }
+
+__device__ inline int swz_km(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+__device__ inline int swz_mn(int kr) { return (kr & 3) * 2; }
+
+template <int DT>
+__device__ inline f32x4 vmfma(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (DT == TVK_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// 16x16x32 fragment of a k-contiguous tile (rows of 64 bytes, XOR chunk swizzle)
+__device__ inline u32x4 frag_km(uint32_t base, int row_base, int lane) {
+    const int row = row_base + lane % 16;
+    return *(const TVK_LDS u32x4*)(uintptr_t)(base + row * 64 + (((lane / 16) ^ swz_km(row)) * 16));
+}
+// 16x16x32 fragment of an m-contiguous tile (k-rows of 512 bytes): transposed reads
+__device__ inline u32x4 frag_mn(uint32_t base, int col_base, int lane) {
+    const int g = lane / 16, s = lane % 16;
+    const int col = col_base + (s % 4) * 4;
+    const int chunk = col / 8, within = (col % 8) * 2;
+    u32x4 out;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+        const int kr = g * 8 + rr * 4 + s / 4;
+        TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(base + kr * 512 + ((chunk ^ swz_mn(kr)) * 16) + within);
+        const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+        out[rr * 2] = w.x;
+        out[rr * 2 + 1] = w.y;
+    }
+    return out;
+}
+
+// MODE 0: rows are pixels (forward, grad input); MODE 1: grad weight.
+template <int DT, int MODE, int BN>
+__global__ __launch_bounds__(BN == 64 ? 256 : 512) void conv_ring_kernel(ConvRing p) {
+    constexpr int NW = BN == 64 ? 4 : 8;
+    constexpr int WN = BN / 64, WMW = NW / WN;       // waves along N and M
+    constexpr int WTM = V_BM / WMW;                  // wave tile rows (64 x 64 column tile)
+    constexpr int FM = WTM / 16, FN = 4;
+    constexpr int OPA = V_BM * V_BK * 2;             // 16 KB
+    constexpr int OPB = BN * V_BK * 2;
+    constexpr int STB = OPA + OPB;
+    constexpr int DA = (OPA / 1024) / NW, DB = (OPB / 1024) / NW, DS = DA + DB;
+    static_assert(DB >= 1 && DA >= 1, "every wave loads both operands");
+    constexpr int LROW = V_BM + 8;                   // epilogue tile row (halfs)
+    constexpr int LDS_BYTES = V_NS * STB > BN * LROW * 2 ? V_NS * STB : BN * LROW * 2;
+    __shared__ __attribute__((aligned(1024))) char lds_raw[LDS_BYTES];
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds_raw);
+    const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int wm = wave / WN, wn = wave % WN;
+    const int m0 = blockIdx.x * V_BM, n0 = blockIdx.y * BN;
+    const int z = blockIdx.z;
+    const int kb = MODE == 1 ? z * p.k_chunk : 0;
+    const int klen = MODE == 1 ? min(p.k_chunk, p.K - kb) : p.K;
+    const int nk = klen / V_BK;
+
+    const i32x4 ra = v_rsrc(p.act, p.act_bytes);
+    const i32x4 rb = v_rsrc(MODE == 1 ? p.dyc : p.wt, MODE == 1 ? p.dyc_bytes : p.wt_bytes);
+
+    // ---- per-lane, per-load constants ----
+    // A (MODE 0): KM tile, 16 rows per block; row -> pixel (img, i, j) -> source origin
+    // A (MODE 1): MN tile, 2 k-rows per block; column chunk -> (tap, channel)
+    int a_base[DA], a_h[DA], a_w[DA], a_c[DA];
+    bool a_ok[DA];
+#pragma unroll
+    for (int q = 0; q < DA; ++q) {
+        const int blk = wave * DA + q;
+        if constexpr (MODE == 0) {
+            const int row = blk * 16 + lane / 4;
+            const int pix = m0 + row;
+            a_ok[q] = pix < p.M;
+            const int hw = p.Hp * p.Wp;
+            const int img = pix / hw, r = pix - img * hw;
+            const int i = r / p.Wp, j = r - i * p.Wp;
+            a_base[q] = img * p.Hs * p.Ws;
+            a_h[q] = i * p.pix_sh + p.pix_bh;
+            a_w[q] = j * p.pix_sw + p.pix_bw;
+            a_c[q] = ((lane % 4) ^ swz_km(row)) * 8;
+        } else {
+            const int kr = blk * 2 + lane / 32;
+            const int m = m0 + (((lane % 32) ^ swz_mn(kr)) * 8);
+            a_ok[q] = m < p.M;
+            const int t = m / p.Cs, c = m - t * p.Cs;
+            a_base[q] = kr;                       // k-row of the stage
+            a_h[q] = p.tap_h[min(t, V_MAXTAPS - 1)];
+            a_w[q] = p.tap_w[min(t, V_MAXTAPS - 1)];
+            a_c[q] = c;
+        }
+    }
+    // B: KM tile, 16 rows (output channels) per block
+    int b_row[DB], b_c[DB];
+    bool b_ok[DB];
+#pragma unroll
+    for (int q = 0; q < DB; ++q) {
+        const int blk = wave * DB + q;
+        const int row = blk * 16 + lane / 4;
+        b_row[q] = n0 + row;
+        b_ok[q] = n0 + row < p.N;
+        b_c[q] = ((lane % 4) ^ swz_km(row)) * 8;
+    }
+
+    auto issue = [&](int s) {
+        if (s >= nk) return;
+        const uint32_t slot = lds0 + (uint32_t)((s % V_NS) * STB);
+        const int k0 = kb + s * V_BK;
+        if constexpr (MODE == 0) {
+            const int t = k0 / p.Cs, c0 = k0 - t * p.Cs;
+            const int th = p.tap_h[t], tw = p.tap_w[t], tk = p.tap_k[t];
+#pragma unroll
+            for (int q = 0; q < DA; ++q) {
+                const int ih = a_h[q] + th, iw = a_w[q] + tw;
+                const bool ok = a_ok[q] && (unsigned)ih < (unsigned)p.Hs && (unsigned)iw < (unsigned)p.Ws;
+                const uint32_t off = ok ? (uint32_t)(((a_base[q] + ih * p.Ws + iw) * p.Cs + c0 + a_c[q]) * 2) : kOOB;
+                v_dma16(ra, slot + (uint32_t)((wave * DA + q) * 1024), off);
+            }
+#pragma unroll
+            for (int q = 0; q < DB; ++q) {
+                const uint32_t off = b_ok[q] ? (uint32_t)(((b_row[q] * p.wt_taps + tk) * p.Cs + c0 + b_c[q]) * 2) : kOOB;
+                v_dma16(rb, slot + OPA + (uint32_t)((wave * DB + q) * 1024), off);
+            }
+        } else {
+            // the stage's 32 output pixels lie in one image (HWo % 32 == 0)
+            const int img = k0 / p.HWo, o0 = k0 - img * p.HWo;
+#pragma unroll
+            for (int q = 0; q < DA; ++q) {
+                const int o = o0 + a_base[q];
+                const int oh = o / p.Wd, ow = o - oh * p.Wd;
+                const int ih = oh * p.pix_sh + a_h[q], iw = ow * p.pix_sw + a_w[q];
+                const bool ok = a_ok[q] && (unsigned)ih < (unsigned)p.Hs && (unsigned)iw < (unsigned)p.Ws;
+                const uint32_t off = ok ? (uint32_t)((((img * p.Hs + ih) * p.Ws + iw) * p.Cs + a_c[q]) * 2) : kOOB;
+                v_dma16(ra, slot + (uint32_t)((wave * DA + q) * 1024), off);
+            }
+#pragma unroll
+            for (int q = 0; q < DB; ++q) {
+                const uint32_t off = b_ok[q] ? (uint32_t)((((int64_t)img * p.N + b_row[q]) * p.HWo + o0 + b_c[q]) * 2) : kOOB;
+                v_dma16(rb, slot + OPA + (uint32_t)((wave * DB + q) * 1024), off);
+            }
+        }
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto read_a = [&](uint32_t st, int i) {
+        if constexpr (MODE == 0) return frag_km(st, wm * WTM + i * 16, lane);
+        else return frag_mn(st, wm * WTM + i * 16, lane);
+    };
+    u32x4 fa[2][FM], fb[2][FN];
+    if (nk > 0) {
+#pragma unroll
+        for (int s = 0; s < V_NS; ++s) issue(s);
+        // stage 0 landed
+        if (nk >= V_NS) v_wait<DS * (V_NS - 1)>(); else v_wait<0>();
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < FM; ++i) fa[0][i] = read_a(lds0, i);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) fb[0][j] = frag_km(lds0 + OPA, wn * 64 + j * 16, lane);
+        if (nk >= V_NS) v_wait<DS * (V_NS - 2)>(); else v_wait<0>();
+        __syncthreads();
+
+        auto body = [&](int kt, auto cur_c) {
+            constexpr int cur = decltype(cur_c)::value;
+            // (on the last stage the reads fetch a slot no stage filled: unused)
+            const uint32_t st_next = lds0 + (uint32_t)(((kt + 1) % V_NS) * STB);
+#pragma unroll
+            for (int q = 0; q < FM * FN; ++q) {
+                const int i = q / FN, j = q % FN;
+                acc[i][j] = vmfma<DT>(fa[cur][i], fb[cur][j], acc[i][j]);
+                if (q % 2 == 0) {
+                    const int r = q / 2;
+                    if (r < FM) fa[cur ^ 1][r] = read_a(st_next, r);
+                    else if (r < FM + FN) fb[cur ^ 1][r - FM] = frag_km(st_next + OPA, wn * 64 + (r - FM) * 16, lane);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            issue(kt + V_NS);
+            // stage kt+2 landed (or, near the end, everything issued)
+            if (kt + V_NS < nk) v_wait<DS * (V_NS - 2)>(); else v_wait<0>();
+            __syncthreads();
+        };
+        int kt = 0;
+        for (; kt + 1 < nk; kt += 2) {
+            body(kt, std::integral_constant<int, 0>{});
+            body(kt + 1, std::integral_constant<int, 1>{});
+        }
+        if (kt < nk) body(kt, std::integral_constant<int, 0>{});
+        v_wait<0>();
+        __syncthreads();
+    }
+
+    typedef typename elem<DT>::T T;
+    if constexpr (MODE == 1) {
+        // (tap, channel) rows x output-channel columns: partials, or dW[co][c][t]
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int col = n0 + wn * 64 + j * 16 + lane % 16;
+                if (col >= p.N) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = m0 + wm * WTM + i * 16 + (lane / 16) * 4 + r;
+                    if (row >= p.M) continue;
+                    if (p.split > 1) {
+                        p.part[((int64_t)z * p.M + row) * p.N + col] = acc[i][j][r];
+                    } else {
+                        const int t = row / p.Cs, c = row - t * p.Cs;
+                        reinterpret_cast<T*>(p.out)[((int64_t)col * p.Cs + c) * p.kh_kw + t] = elem<DT>::from_f32(acc[i][j][r]);
+                    }
+                }
+            }
+        return;
+    }
+
+    // pixels x channels -> NCHW through LDS: the tile is written as [channel][pixel]
+    // (rows of 256 pixels + 8 halfs of padding), then each thread stores 8 pixels
+    // of one channel at a time
+    uint16_t* tile = reinterpret_cast<uint16_t*>(lds_raw);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int ch = wn * 64 + j * 16 + lane % 16;
+            const int px = wm * WTM + i * 16 + (lane / 16) * 4;
+            float bv = 0.0f;
+            if (p.has_bias && n0 + ch < p.N) bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[n0 + ch]);
+            uint16_t h[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[i][j][r];
+                if (p.has_bias) {
+#pragma clang fp contract(off)
+                    v = v + bv;
+                }
+                h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
+            }
+            *reinterpret_cast<u32x2*>(tile + ch * LROW + px) = u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+        }
+    __syncthreads();
+    T* out = reinterpret_cast<T*>(p.out);
+    const int hw = p.Hp * p.Wp;
+    const bool dense = p.osh == 1 && p.osw == 1 && p.Hp == p.Ho && p.Wp == p.Wo && hw % 8 == 0;
+    constexpr int NT = 64 * NW;
+    for (int idx = tid; idx < BN * (V_BM / 8); idx += NT) {
+        const int ch = idx / (V_BM / 8), pc = idx % (V_BM / 8);
+        const int co = n0 + ch;
+        const int pix = m0 + pc * 8;
+        if (co >= p.N || pix >= p.M) continue;
+        const uint16_t* src = tile + ch * LROW + pc * 8;
+        if (dense && pix + 8 <= p.M) {
+            // 8 pixels of one image row run (hw % 8 == 0): one 16-byte store
+            const int img = pix / hw, o = pix - img * hw;
+            *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + co) * hw + o) = *reinterpret_cast<const u32x4*>(src);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int q = pix + e;
+                if (q >= p.M) break;
+                const int img = q / hw, r = q - img * hw;
+                const int i = r / p.Wp, j = r - i * p.Wp;
+                const int oh = i * p.osh + p.orh, ow = j * p.osw + p.orw;
+                out[(((int64_t)img * p.N + co) * p.Ho + oh) * p.Wo + ow] = __builtin_bit_cast(T, src[e]);
+            }
+        }
+    }
+}
+
+// NCHW -> NHWC, one image plane block of 64 channels x 64 pixels per workgroup
+template <typename T>
+__global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const T* src, T* dst, int C, int HW) {
+    __shared__ T tile[64][65];
+    const int img = blockIdx.z, c0 = blockIdx.y * 64, p0 = blockIdx.x * 64;
+    const T* s = src + (int64_t)img * C * HW;
+    T* d = dst + (int64_t)img * C * HW;
+    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+        const int c = e / 64, q = e % 64;
+        if (c0 + c < C && p0 + q < HW) tile[c][q] = s[(int64_t)(c0 + c) * HW + p0 + q];
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+        const int q = e / 64, c = e % 64;
+        if (c0 + c < C && p0 + q < HW) d[(int64_t)(p0 + q) * C + c0 + c] = tile[c][q];
+    }
+}
+
+// w[co][c][t] -> out[co][t][c] (forward) or out[c][t][co] (grad input)
+template <typename T, bool FORWARD>
+__global__ __launch_bounds__(256) void weight_permute_kernel(const T* w, T* out, int Cout, int Cin, int taps) {
+    const int64_t total = (int64_t)Cout * Cin * taps;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        const int t = (int)(e % taps);
+        const int c = (int)((e / taps) % Cin);
+        const int co = (int)(e / ((int64_t)taps * Cin));
+        const int64_t o = FORWARD ? ((int64_t)co * taps + t) * Cin + c : ((int64_t)c * taps + t) * Cout + co;
+        out[o] = w[e];
+    }
+}
+
+// grad weight: sums partials [split][(t,c)][co] in split order into dW[co][c][t]
+template <int DT>
+__global__ __launch_bounds__(256) void wgrad_ring_reduce_kernel(const float* part, void* out, int M, int N, int Cs, int taps, int split) {
+    typedef typename elem<DT>::T T;
+    const int64_t total = (int64_t)M * N;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        float v = part[e];
+        for (int s = 1; s < split; ++s) v += part[(int64_t)s * total + e];
+        const int row = (int)(e / N), co = (int)(e % N);
+        const int t = row / Cs, c = row - t * Cs;
+        reinterpret_cast<T*>(out)[((int64_t)co * Cs + c) * taps + t] = elem<DT>::from_f32(v);
+    }
+}
+
+template <int DT, int MODE>
+void launch_ring(const ConvRing& p, int gx, int gz, hipStream_t s) {
+    const int bn = p.N <= 64 ? 64 : p.N <= 128 ? 128 : 256;
+    const dim3 grid(gx, (p.N + bn - 1) / bn, gz);
+    if (bn == 64) hipLaunchKernelGGL((conv_ring_kernel<DT, MODE, 64>), grid, dim3(256), 0, s, p);
+    else if (bn == 128) hipLaunchKernelGGL((conv_ring_kernel<DT, MODE, 128>), grid, dim3(512), 0, s, p);
+    else hipLaunchKernelGGL((conv_ring_kernel<DT, MODE, 256>), grid, dim3(512), 0, s, p);
+}
+
+template <typename T>
+void launch_nhwc(const void* src, void* dst, int n, int C, int HW, hipStream_t s) {
+    const dim3 grid((HW + 63) / 64, (C + 63) / 64, n);
+    hipLaunchKernelGGL(nchw_to_nhwc_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(src), static_cast<T*>(dst), C, HW);
+}
+
+}  // namespace
+
+// mode: 0 forward, 1 grad input, 2 grad weight
+bool conv_ring_applies(const tvk_conv_desc& d, int mode) {
+    if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return false;
+    if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1) return false;
+    if (d.c_in % 32 != 0 || d.c_out % 32 != 0) return false;
+    if (d.kh * d.kw > V_MAXTAPS) return false;
+    if (d.n <= 0) return false;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!al16(d.x) || !al16(d.weight) || !al16(d.y)) return false;
+    if (mode == 1 && (d.stride[0] > 4 || d.stride[1] > 4)) return false;
+    if (mode == 2 && (d.h_out * d.w_out) % 32 != 0) return false;
+    // 32-bit element offsets inside the kernels
+    const int64_t big = std::max({d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h_out * d.w_out, d.c_out * d.c_in * d.kh * d.kw});
+    return big < (int64_t(1) << 30);
+}
+
+tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
+    const int n = (int)d.n, cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
+    const int Ho = (int)d.h_out, Wo = (int)d.w_out, kh = (int)d.kh, kw = (int)d.kw, T = kh * kw;
+    const int sh = (int)d.stride[0], sw = (int)d.stride[1], ph = (int)d.padding[0], pw = (int)d.padding[1];
+    const int dh = (int)d.dilation[0], dw = (int)d.dilation[1];
+    const size_t es = 2;
+    hipStream_t s = resolve_stream(d.stream);
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+
+    ConvRing p;
+    memset(&p, 0, sizeof(p));
+    auto align = [](size_t v) { return (v + 255) / 256 * 256; };
+    const bool f16 = d.dtype == TVK_F16;
+    if (mode == 0 || mode == 1) {
+        // gathered activation: x (forward) or dy (grad input), to NHWC
+        const int Cs = mode == 0 ? cin : cout, Hs = mode == 0 ? H : Ho, Ws = mode == 0 ? W : Wo;
+        const int Cn = mode == 0 ? cout : cin;   // GEMM columns
+        const size_t act_b = align((size_t)n * Cs * Hs * Ws * es), wt_b = align((size_t)Cn * T * Cs * es);
+        char* ws = static_cast<char*>(device_workspace(dev, act_b + wt_b));
+        if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the channels-last copies");
+        const void* src = mode == 0 ? d.x : d.y;
+        launch_nhwc<uint16_t>(src, ws, n, Cs, Hs * Ws, s);
+        const int64_t wn = (int64_t)cout * cin * T;
+        const unsigned wblocks = (unsigned)std::min<int64_t>((wn + 255) / 256, 2048);
+        if (mode == 0) hipLaunchKernelGGL((weight_permute_kernel<uint16_t, true>), dim3(wblocks), dim3(256), 0, s, static_cast<const uint16_t*>(d.weight), reinterpret_cast<uint16_t*>(ws + act_b), cout, cin, T);
+        else hipLaunchKernelGGL((weight_permute_kernel<uint16_t, false>), dim3(wblocks), dim3(256), 0, s, static_cast<const uint16_t*>(d.weight), reinterpret_cast<uint16_t*>(ws + act_b), cout, cin, T);
+        p.act = ws;
+        p.wt = ws + act_b;
+        p.Hs = Hs; p.Ws = Ws; p.Cs = Cs;
+        p.N = Cn;
+        p.act_bytes = (int)((size_t)n * Cs * Hs * Ws * es);
+        p.wt_bytes = (int)((size_t)Cn * T * Cs * es);
+        p.wt_taps = T;
+        p.out = mode == 0 ? d.y : d.x;
+        p.Ho = mode == 0 ? Ho : H;
+        p.Wo = mode == 0 ? Wo : W;
+        if (mode == 0) {
+            p.ntap = T;
+            for (int t = 0; t < T; ++t) { p.tap_h[t] = (t / kw) * dh; p.tap_w[t] = (t % kw) * dw; p.tap_k[t] = t; }
+            p.Hp = Ho; p.Wp = Wo;
+            p.pix_sh = sh; p.pix_sw = sw; p.pix_bh = -ph; p.pix_bw = -pw;
+            p.osh = 1; p.osw = 1; p.orh = 0; p.orw = 0;
+            p.bias = d.bias;
+            p.has_bias = d.bias ? 1 : 0;
+            p.M = n * Ho * Wo;
+            p.K = T * Cs;
+            const int gx = (p.M + V_BM - 1) / V_BM;
+            if (f16) launch_ring<TVK_F16, 0>(p, gx, 1, s);
+            else launch_ring<TVK_BF16, 0>(p, gx, 1, s);
+        } else {
+            // sub-pixel phases: input pixels (sh*i + ry, sw*j + rx) only meet taps
+            // with (ry + ph - kh*dh) % sh == 0 (and likewise along w)
+            for (int ry = 0; ry < sh; ++ry)
+                for (int rx = 0; rx < sw; ++rx) {
+                    const int Hp = (H - ry + sh - 1) / sh, Wp = (W - rx + sw - 1) / sw;
+                    if (Hp <= 0 || Wp <= 0) continue;
+                    ConvRing q = p;
+                    q.ntap = 0;
+                    for (int a = 0; a < kh; ++a) {
+                        const int nh = ry + ph - a * dh;
+                        if (((nh % sh) + sh) % sh != 0) continue;
+                        for (int b = 0; b < kw; ++b) {
+                            const int nw = rx + pw - b * dw;
+                            if (((nw % sw) + sw) % sw != 0) continue;
+                            q.tap_h[q.ntap] = nh / sh;
+                            q.tap_w[q.ntap] = nw / sw;
+                            q.tap_k[q.ntap] = a * kw + b;
+                            ++q.ntap;
+                        }
+                    }
+                    q.Hp = Hp; q.Wp = Wp;
+                    q.pix_sh = 1; q.pix_sw = 1; q.pix_bh = 0; q.pix_bw = 0;
+                    q.osh = sh; q.osw = sw; q.orh = ry; q.orw = rx;
+                    q.M = n * Hp * Wp;
+                    q.K = q.ntap * cout;
+                    // (a phase no tap reaches has K = 0: the kernel writes its zeros)
+                    const int gx = (q.M + V_BM - 1) / V_BM;
+                    if (f16) launch_ring<TVK_F16, 0>(q, gx, 1, s);
+                    else launch_ring<TVK_BF16, 0>(q, gx, 1, s);
+                }
+        }
+    } else {
+        // grad weight: x to NHWC; dy read NCHW; K = output pixels split into partials
+        const size_t act_b = align((size_t)n * cin * H * W * es);
+        p.M = T * cin;
+        p.N = cout;
+        p.K = n * Ho * Wo;
+        const int bn = cout <= 64 ? 64 : cout <= 128 ? 128 : 256;
+        const int64_t tiles = (int64_t)((p.M + V_BM - 1) / V_BM) * ((p.N + bn - 1) / bn);
+        int64_t split = std::max<int64_t>(1, std::min<int64_t>(512 / tiles, p.K / (8 * V_BK)));
+        int64_t chunk = ((p.K + split - 1) / split + V_BK - 1) / V_BK * V_BK;
+        split = (p.K + chunk - 1) / chunk;
+        const size_t part_b = split > 1 ? (size_t)split * p.M * p.N * 4 : 0;
+        char* ws = static_cast<char*>(device_workspace(dev, act_b + part_b));
+        if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the channels-last copy");
+        launch_nhwc<uint16_t>(d.x, ws, n, cin, H * W, s);
+        p.act = ws;
+        p.dyc = d.y;
+        p.part = split > 1 ? reinterpret_cast<float*>(ws + act_b) : nullptr;
+        p.out = d.weight;
+        p.Hs = H; p.Ws = W; p.Cs = cin;
+        p.ntap = T;
+        p.wt_taps = T;
+        for (int t = 0; t < T; ++t) { p.tap_h[t] = (t / kw) * dh - ph; p.tap_w[t] = (t % kw) * dw - pw; p.tap_k[t] = t; }
+        p.pix_sh = sh; p.pix_sw = sw;
+        p.HWo = Ho * Wo; p.Wd = Wo; p.kh_kw = T;
+        p.k_chunk = (int)chunk; p.split = (int)split;
+        p.act_bytes = (int)((size_t)n * cin * H * W * es);
+        p.dyc_bytes = (int)((size_t)n * cout * Ho * Wo * es);
+        const int gx = (p.M + V_BM - 1) / V_BM;
+        if (f16) launch_ring<TVK_F16, 1>(p, gx, (int)split, s);
+        else launch_ring<TVK_BF16, 1>(p, gx, (int)split, s);
+        if (split > 1) {
+            const int64_t total = (int64_t)p.M * p.N;
+            const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
+            if (f16) hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_F16>, dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
+            else hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_BF16>, dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
+        }
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
+    return TVK_OK;
+}
+
+}  // namespace tvk

@@ -161,6 +161,11 @@ uint32_t* device_counters(int device, size_t count);
 bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor);
 hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s);
 
+// Channels-last convolution on the LDS ring (conv_nhwc.hip); mode 0 forward,
+// 1 grad input, 2 grad weight.
+bool conv_ring_applies(const tvk_conv_desc& d, int mode);
+tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who);
+
 // M <= 16 streaming kernel (gemm_skinny.hip). b_kmajor: B's k stride is 1.
 // vec: 16-byte loads are legal for A and B. Returns hipSuccess or the launch error.
 hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, hipStream_t s);
