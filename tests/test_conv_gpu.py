@@ -129,6 +129,12 @@ RING_CASES = [
     dict(n=1, cin=128, cout=256, k=3, s=3, p=0, hw=17),
     dict(n=2, cin=32, cout=32, k=4, s=2, p=1, hw=16),
     dict(n=1, cin=64, cout=128, k=1, s=2, p=0, hw=9),
+    # the gathered side needs whole 32-channel stages; the other channel count
+    # is a column count and may be anything (3-channel stem grad input, 10
+    # output channels, 40 input channels in 8-channel grad-weight chunks)
+    dict(n=2, cin=3, cout=64, k=3, s=1, p=1, hw=16),
+    dict(n=2, cin=32, cout=10, k=3, s=1, p=1, hw=8),
+    dict(n=2, cin=40, cout=32, k=3, s=2, p=1, hw=12),
 ]
 
 

@@ -437,14 +437,21 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(uint16_t* out, int64_t h
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < halfs; i += (int64_t)gridDim.x * 256) out[i] = 0;
 }
 
-// Sums the grad-weight partials over the splits in split order and rounds once.
+// Sums the grad-weight partials over the splits and rounds once. Few outputs
+// with many splits (the 3-channel stem: 1728 outputs of 512 partials) would
+// leave a thread per output summing serially, so each output gets one wave:
+// lane l sums splits l, l+64, ... in order, then the 64 lane sums are added
+// by a fixed butterfly, so the result does not depend on timing.
 template <int DT>
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* part, void* out, int64_t count, int split) {
     typedef typename elem<DT>::T T;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
-        float v = part[i];
-        for (int s = 1; s < split; ++s) v += part[(int64_t)s * count + i];
-        reinterpret_cast<T*>(out)[i] = elem<DT>::from_f32(v);
+    const int lane = threadIdx.x % 64;
+    for (int64_t i = (int64_t)blockIdx.x * 4 + threadIdx.x / 64; i < count; i += (int64_t)gridDim.x * 4) {
+        float v = 0.0f;
+        for (int s = lane; s < split; s += 64) v += part[(int64_t)s * count + i];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+        if (lane == 0) reinterpret_cast<T*>(out)[i] = elem<DT>::from_f32(v);
     }
 }
 
@@ -567,7 +574,7 @@ tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
     }
     if (MODE == WGRAD && p.split > 1) {
         const int64_t count = (int64_t)p.cout * p.cx * p.taps;
-        const unsigned blocks = (unsigned)std::min<int64_t>((count + 255) / 256, 4096);
+        const unsigned blocks = (unsigned)std::min<int64_t>((count + 3) / 4, 8192);
         switch (d.dtype) {
         case TVK_F32: hipLaunchKernelGGL(wgrad_reduce_kernel<TVK_F32>, dim3(blocks), dim3(256), 0, s, p.part, out, count, p.split); break;
         case TVK_F16: hipLaunchKernelGGL(wgrad_reduce_kernel<TVK_F16>, dim3(blocks), dim3(256), 0, s, p.part, out, count, p.split); break;

@@ -28,6 +28,7 @@
 #include "gemm_common.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <string>
 #include <type_traits>
@@ -349,21 +350,40 @@ __global__ __launch_bounds__(BN == 64 ? 256 : 512) void conv_ring_kernel(ConvRin
     }
 }
 
-// NCHW -> NHWC, one image plane block of 64 channels x 64 pixels per workgroup
-template <typename T>
-__global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const T* src, T* dst, int C, int HW) {
-    __shared__ T tile[64][65];
+// NCHW -> NHWC for 16-bit elements, one block of 64 channels x 64 pixels per
+// workgroup: 16-byte loads along the pixels of a channel, 16-byte stores along
+// the channels of a pixel (when the counts allow; element accesses otherwise)
+__global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint16_t* src, uint16_t* dst, int C, int HW) {
+    __shared__ uint16_t tile[64][72];
     const int img = blockIdx.z, c0 = blockIdx.y * 64, p0 = blockIdx.x * 64;
-    const T* s = src + (int64_t)img * C * HW;
-    T* d = dst + (int64_t)img * C * HW;
-    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
-        const int c = e / 64, q = e % 64;
-        if (c0 + c < C && p0 + q < HW) tile[c][q] = s[(int64_t)(c0 + c) * HW + p0 + q];
+    const uint16_t* s = src + (int64_t)img * C * HW;
+    uint16_t* d = dst + (int64_t)img * C * HW;
+    const bool vec = HW % 8 == 0 && C % 8 == 0;
+#pragma unroll
+    for (int e = threadIdx.x; e < 64 * 8; e += 256) {
+        const int c = e / 8, q = (e % 8) * 8;
+        if (c0 + c >= C) continue;
+        if (vec && p0 + q + 8 <= HW) {
+            *reinterpret_cast<u32x4*>(&tile[c][q]) = *reinterpret_cast<const u32x4*>(s + (int64_t)(c0 + c) * HW + p0 + q);
+        } else {
+            for (int k = 0; k < 8; ++k)
+                if (p0 + q + k < HW) tile[c][q + k] = s[(int64_t)(c0 + c) * HW + p0 + q + k];
+        }
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
-        const int q = e / 64, c = e % 64;
-        if (c0 + c < C && p0 + q < HW) d[(int64_t)(p0 + q) * C + c0 + c] = tile[c][q];
+#pragma unroll
+    for (int e = threadIdx.x; e < 64 * 8; e += 256) {
+        const int q = e / 8, c = (e % 8) * 8;
+        if (p0 + q >= HW) continue;
+        if (vec && c0 + c + 8 <= C) {
+            uint32_t w[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) w[k] = (uint32_t)tile[c + 2 * k][q] | ((uint32_t)tile[c + 2 * k + 1][q] << 16);
+            *reinterpret_cast<u32x4*>(d + (int64_t)(p0 + q) * C + c0 + c) = u32x4{w[0], w[1], w[2], w[3]};
+        } else {
+            for (int k = 0; k < 8; ++k)
+                if (c0 + c + k < C) d[(int64_t)(p0 + q) * C + c0 + c + k] = tile[c + k][q];
+        }
     }
 }
 
@@ -403,10 +423,9 @@ void launch_ring(const ConvRing& p, int gx, int gz, hipStream_t s) {
     else hipLaunchKernelGGL((conv_ring_kernel<DT, MODE, 256>), grid, dim3(512), 0, s, p);
 }
 
-template <typename T>
 void launch_nhwc(const void* src, void* dst, int n, int C, int HW, hipStream_t s) {
     const dim3 grid((HW + 63) / 64, (C + 63) / 64, n);
-    hipLaunchKernelGGL(nchw_to_nhwc_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(src), static_cast<T*>(dst), C, HW);
+    hipLaunchKernelGGL(nchw_to_nhwc_kernel, grid, dim3(256), 0, s, static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), C, HW);
 }
 
 }  // namespace
@@ -415,7 +434,12 @@ void launch_nhwc(const void* src, void* dst, int n, int C, int HW, hipStream_t s
 bool conv_ring_applies(const tvk_conv_desc& d, int mode) {
     if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return false;
     if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1) return false;
-    if (d.c_in % 32 != 0 || d.c_out % 32 != 0) return false;
+    // the gathered channels make the k stages (whole 32-channel stages; grad
+    // weight gathers 8-channel chunks of the (tap, channel) rows); the other
+    // channel count is a GEMM column count and may be anything
+    if (mode == 0 && d.c_in % 32 != 0) return false;
+    if (mode == 1 && d.c_out % 32 != 0) return false;
+    if (mode == 2 && d.c_in % 8 != 0) return false;
     if (d.kh * d.kw > V_MAXTAPS) return false;
     if (d.n <= 0) return false;
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
@@ -449,7 +473,7 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
         char* ws = static_cast<char*>(device_workspace(dev, act_b + wt_b));
         if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the channels-last copies");
         const void* src = mode == 0 ? d.x : d.y;
-        launch_nhwc<uint16_t>(src, ws, n, Cs, Hs * Ws, s);
+        launch_nhwc(src, ws, n, Cs, Hs * Ws, s);
         const int64_t wn = (int64_t)cout * cin * T;
         const unsigned wblocks = (unsigned)std::min<int64_t>((wn + 255) / 256, 2048);
         if (mode == 0) hipLaunchKernelGGL((weight_permute_kernel<uint16_t, true>), dim3(wblocks), dim3(256), 0, s, static_cast<const uint16_t*>(d.weight), reinterpret_cast<uint16_t*>(ws + act_b), cout, cin, T);
@@ -517,13 +541,20 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
         p.K = n * Ho * Wo;
         const int bn = cout <= 64 ? 64 : cout <= 128 ? 128 : 256;
         const int64_t tiles = (int64_t)((p.M + V_BM - 1) / V_BM) * ((p.N + bn - 1) / bn);
-        int64_t split = std::max<int64_t>(1, std::min<int64_t>(512 / tiles, p.K / (8 * V_BK)));
+        // split K: more splits fill the device (about 256 workgroups) but each
+        // adds M*N float32 partials written and read back. Minimise
+        //   split*M*N*8 B / (5 TB/s) + 2*M*N*K / (1 PFLOP/s * min(1, tiles*split/256))
+        const double part_us = (double)p.M * p.N * 8 / 5e6;
+        const double full_us = 2.0 * p.M * p.N * p.K / 1e9;
+        int64_t split = (int64_t)std::sqrt(full_us * 256.0 / (double)tiles / std::max(part_us, 1e-6));
+        split = std::min<int64_t>(split, std::max<int64_t>(1, 256 / tiles));
+        split = std::max<int64_t>(1, std::min<int64_t>(split, p.K / (8 * V_BK)));
         int64_t chunk = ((p.K + split - 1) / split + V_BK - 1) / V_BK * V_BK;
         split = (p.K + chunk - 1) / chunk;
         const size_t part_b = split > 1 ? (size_t)split * p.M * p.N * 4 : 0;
         char* ws = static_cast<char*>(device_workspace(dev, act_b + part_b));
         if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the channels-last copy");
-        launch_nhwc<uint16_t>(d.x, ws, n, cin, H * W, s);
+        launch_nhwc(d.x, ws, n, cin, H * W, s);
         p.act = ws;
         p.dyc = d.y;
         p.part = split > 1 ? reinterpret_cast<float*>(ws + act_b) : nullptr;
