@@ -40,7 +40,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 #define TVK_LDS __attribute__((address_space(3)))
 
-constexpr int V_BM = 256, V_BK = 32, V_NS = 4;
+constexpr int V_BK = 32, V_NS = 4;
 constexpr int V_MAXTAPS = 16;
 
 struct ConvRing {
@@ -65,6 +65,13 @@ struct ConvRing {
     int HWo, Wd, kh_kw, k_chunk, split;
     int has_bias;
     int act_bytes, wt_bytes, dyc_bytes;
+};
+
+// One launch covers up to 4 problems in grid z: the sub-pixel phases of a
+// stride-2 grad input (forward and grad weight use ph[0])
+constexpr int V_MAXPH = 4;
+struct ConvRingSet {
+    ConvRing ph[V_MAXPH];
 };
 
 __device__ inline i32x4 v_rsrc(const void* p, int64_t bytes) {
@@ -111,14 +118,20 @@ __device__ inline u32x4 frag_mn(uint32_t base, int col_base, int lane) {
     return out;
 }
 
-// MODE 0: rows are pixels (forward, grad input); MODE 1: grad weight.
-template <int DT, int MODE, int BN>
-__global__ __launch_bounds__(BN == 64 ? 256 : 512) void conv_ring_kernel(ConvRing p) {
-    constexpr int NW = BN == 64 ? 4 : 8;
+// waves of a BM x BN tile: 64x64 wave tiles, except 256x256 (8 waves of 128x64)
+constexpr int ring_waves(int bm, int bn) { return bm == 256 ? (bn == 64 ? 4 : 8) : 2 * (bn / 64); }
+
+// MODE 0: rows are pixels (forward, grad input; grid z = sub-pixel phase);
+// MODE 1: grad weight (grid z = k split).
+template <int DT, int MODE, int BM, int BN>
+__global__ __launch_bounds__(64 * ring_waves(BM, BN)) void conv_ring_kernel(ConvRingSet set) {
+    static_assert(MODE == 0 || BM == 256, "grad weight uses 256-row tiles");
+    constexpr int V_BM = BM;
+    constexpr int NW = ring_waves(BM, BN);
     constexpr int WN = BN / 64, WMW = NW / WN;       // waves along N and M
-    constexpr int WTM = V_BM / WMW;                  // wave tile rows (64 x 64 column tile)
+    constexpr int WTM = V_BM / WMW;                  // wave tile rows (x 64 columns)
     constexpr int FM = WTM / 16, FN = 4;
-    constexpr int OPA = V_BM * V_BK * 2;             // 16 KB
+    constexpr int OPA = V_BM * V_BK * 2;
     constexpr int OPB = BN * V_BK * 2;
     constexpr int STB = OPA + OPB;
     constexpr int DA = (OPA / 1024) / NW, DB = (OPB / 1024) / NW, DS = DA + DB;
@@ -129,7 +142,9 @@ __global__ __launch_bounds__(BN == 64 ? 256 : 512) void conv_ring_kernel(ConvRin
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds_raw);
     const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const int wm = wave / WN, wn = wave % WN;
+    const ConvRing& p = set.ph[MODE == 0 ? blockIdx.z : 0];
     const int m0 = blockIdx.x * V_BM, n0 = blockIdx.y * BN;
+    if (m0 >= p.M) return;   // this phase has fewer row tiles than the grid
     const int z = blockIdx.z;
     const int kb = MODE == 1 ? z * p.k_chunk : 0;
     const int klen = MODE == 1 ? min(p.k_chunk, p.K - kb) : p.K;
@@ -400,27 +415,55 @@ __global__ __launch_bounds__(256) void weight_permute_kernel(const T* w, T* out,
     }
 }
 
-// grad weight: sums partials [split][(t,c)][co] in split order into dW[co][c][t]
-template <int DT>
+// grad weight: sums partials [split][(t,c)][co] into dW[co][c][t]. WAVE: one
+// wave per output (lane l sums splits l, l+64, ... in order, then a fixed
+// butterfly), for few outputs with many splits; else one thread per output
+// summing in split order.
+template <int DT, bool WAVE>
 __global__ __launch_bounds__(256) void wgrad_ring_reduce_kernel(const float* part, void* out, int M, int N, int Cs, int taps, int split) {
     typedef typename elem<DT>::T T;
     const int64_t total = (int64_t)M * N;
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-        float v = part[e];
-        for (int s = 1; s < split; ++s) v += part[(int64_t)s * total + e];
+    const int per = WAVE ? 4 : 256;
+    const int lane = threadIdx.x % 64;
+    for (int64_t e = (int64_t)blockIdx.x * per + (WAVE ? threadIdx.x / 64 : threadIdx.x); e < total; e += (int64_t)gridDim.x * per) {
+        float v;
+        if constexpr (WAVE) {
+            v = 0.0f;
+            for (int s = lane; s < split; s += 64) v += part[(int64_t)s * total + e];
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+            if (lane != 0) continue;
+        } else {
+            v = part[e];
+            for (int s = 1; s < split; ++s) v += part[(int64_t)s * total + e];
+        }
         const int row = (int)(e / N), co = (int)(e % N);
         const int t = row / Cs, c = row - t * Cs;
         reinterpret_cast<T*>(out)[((int64_t)co * Cs + c) * taps + t] = elem<DT>::from_f32(v);
     }
 }
 
+// Launches MODE 0 over set.ph[0..nph) (grid z = phase) or MODE 1 over `splits`
+// k splits. 128-row tiles when 256-row tiles would leave the device under-filled.
 template <int DT, int MODE>
-void launch_ring(const ConvRing& p, int gx, int gz, hipStream_t s) {
-    const int bn = p.N <= 64 ? 64 : p.N <= 128 ? 128 : 256;
-    const dim3 grid(gx, (p.N + bn - 1) / bn, gz);
-    if (bn == 64) hipLaunchKernelGGL((conv_ring_kernel<DT, MODE, 64>), grid, dim3(256), 0, s, p);
-    else if (bn == 128) hipLaunchKernelGGL((conv_ring_kernel<DT, MODE, 128>), grid, dim3(512), 0, s, p);
-    else hipLaunchKernelGGL((conv_ring_kernel<DT, MODE, 256>), grid, dim3(512), 0, s, p);
+void launch_ring(const ConvRingSet& set, int nph, int splits, hipStream_t s) {
+    const ConvRing& p0 = set.ph[0];
+    const int bn = p0.N <= 64 ? 64 : p0.N <= 128 ? 128 : 256;
+    int max_m = 0;
+    for (int i = 0; i < nph; ++i) max_m = std::max(max_m, set.ph[i].M);
+    const int ny = (p0.N + bn - 1) / bn;
+    const int64_t t256 = (int64_t)((max_m + 255) / 256) * ny * (MODE == 0 ? nph : splits);
+    const int bm = (MODE == 0 && t256 < 192) ? 128 : 256;
+    const dim3 grid((max_m + bm - 1) / bm, ny, MODE == 0 ? nph : splits);
+#define TVK_RING(BM_, BN_) hipLaunchKernelGGL((conv_ring_kernel<DT, MODE, BM_, BN_>), grid, dim3(64 * ring_waves(BM_, BN_)), 0, s, set)
+    if constexpr (MODE == 0) {
+        if (bm == 128) {
+            if (bn == 64) TVK_RING(128, 64); else if (bn == 128) TVK_RING(128, 128); else TVK_RING(128, 256);
+            return;
+        }
+    }
+    if (bn == 64) TVK_RING(256, 64); else if (bn == 128) TVK_RING(256, 128); else TVK_RING(256, 256);
+#undef TVK_RING
 }
 
 void launch_nhwc(const void* src, void* dst, int n, int C, int HW, hipStream_t s) {
@@ -498,12 +541,22 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
             p.has_bias = d.bias ? 1 : 0;
             p.M = n * Ho * Wo;
             p.K = T * Cs;
-            const int gx = (p.M + V_BM - 1) / V_BM;
-            if (f16) launch_ring<TVK_F16, 0>(p, gx, 1, s);
-            else launch_ring<TVK_BF16, 0>(p, gx, 1, s);
+            ConvRingSet set;
+            set.ph[0] = p;
+            if (f16) launch_ring<TVK_F16, 0>(set, 1, 1, s);
+            else launch_ring<TVK_BF16, 0>(set, 1, 1, s);
         } else {
             // sub-pixel phases: input pixels (sh*i + ry, sw*j + rx) only meet taps
-            // with (ry + ph - kh*dh) % sh == 0 (and likewise along w)
+            // with (ry + ph - kh*dh) % sh == 0 (and likewise along w); up to 4
+            // phases share a launch
+            ConvRingSet set;
+            int nph = 0;
+            auto flush = [&]() {
+                if (nph == 0) return;
+                if (f16) launch_ring<TVK_F16, 0>(set, nph, 1, s);
+                else launch_ring<TVK_BF16, 0>(set, nph, 1, s);
+                nph = 0;
+            };
             for (int ry = 0; ry < sh; ++ry)
                 for (int rx = 0; rx < sw; ++rx) {
                     const int Hp = (H - ry + sh - 1) / sh, Wp = (W - rx + sw - 1) / sw;
@@ -528,10 +581,10 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
                     q.M = n * Hp * Wp;
                     q.K = q.ntap * cout;
                     // (a phase no tap reaches has K = 0: the kernel writes its zeros)
-                    const int gx = (q.M + V_BM - 1) / V_BM;
-                    if (f16) launch_ring<TVK_F16, 0>(q, gx, 1, s);
-                    else launch_ring<TVK_BF16, 0>(q, gx, 1, s);
+                    set.ph[nph++] = q;
+                    if (nph == V_MAXPH) flush();
                 }
+            flush();
         }
     } else {
         // grad weight: x to NHWC; dy read NCHW; K = output pixels split into partials
@@ -540,7 +593,7 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
         p.N = cout;
         p.K = n * Ho * Wo;
         const int bn = cout <= 64 ? 64 : cout <= 128 ? 128 : 256;
-        const int64_t tiles = (int64_t)((p.M + V_BM - 1) / V_BM) * ((p.N + bn - 1) / bn);
+        const int64_t tiles = (int64_t)((p.M + 255) / 256) * ((p.N + bn - 1) / bn);
         // split K: more splits fill the device (about 256 workgroups) but each
         // adds M*N float32 partials written and read back. Minimise
         //   split*M*N*8 B / (5 TB/s) + 2*M*N*K / (1 PFLOP/s * min(1, tiles*split/256))
@@ -568,14 +621,21 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
         p.k_chunk = (int)chunk; p.split = (int)split;
         p.act_bytes = (int)((size_t)n * cin * H * W * es);
         p.dyc_bytes = (int)((size_t)n * cout * Ho * Wo * es);
-        const int gx = (p.M + V_BM - 1) / V_BM;
-        if (f16) launch_ring<TVK_F16, 1>(p, gx, (int)split, s);
-        else launch_ring<TVK_BF16, 1>(p, gx, (int)split, s);
+        ConvRingSet set;
+        set.ph[0] = p;
+        if (f16) launch_ring<TVK_F16, 1>(set, 1, (int)split, s);
+        else launch_ring<TVK_BF16, 1>(set, 1, (int)split, s);
         if (split > 1) {
             const int64_t total = (int64_t)p.M * p.N;
-            const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
-            if (f16) hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_F16>, dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
-            else hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_BF16>, dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
+            if (total < 256 * 1024 && split >= 8) {
+                const unsigned blocks = (unsigned)std::min<int64_t>((total + 3) / 4, 16384);
+                if (f16) hipLaunchKernelGGL((wgrad_ring_reduce_kernel<TVK_F16, true>), dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
+                else hipLaunchKernelGGL((wgrad_ring_reduce_kernel<TVK_BF16, true>), dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
+            } else {
+                const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
+                if (f16) hipLaunchKernelGGL((wgrad_ring_reduce_kernel<TVK_F16, false>), dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
+                else hipLaunchKernelGGL((wgrad_ring_reduce_kernel<TVK_BF16, false>), dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
+            }
         }
     }
     hipError_t e = hipGetLastError();
