@@ -341,6 +341,42 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c3_llm_layer_gemm_tflops"] = round(llm_flops / (ms * 1e-3) / 1e12, 2)
     del keep, llm_refs, llm_descs
 
+    # ---- C5 ragged [1000,777]x[777,3000] and baddbmm in[64,512,512] + 0.5*bmm ----
+    a = torch.randn((1000, 777), generator=g).to(torch.float16).to(dev)
+    b = torch.randn((777, 3000), generator=g).to(torch.float16).to(dev)
+    c = torch.empty((1000, 3000), dtype=torch.float16, device=dev)
+    dr = _abi.make_gemm_desc(a, b, c, stream=s)
+    rr = C.byref(dr)
+
+    def ragged_step():
+        st_ = lib.tvk_gemm(rr)
+        if st_:
+            _abi.check(st_)
+
+    ms, _ = timed(ragged_step, steps * 4, warmup, stream)
+    out["c5_ragged_kernel"] = _abi.gemm_plan(a, b, c)
+    out["c5_ragged_us"] = round(ms * 1e3, 2)
+    out["c5_ragged_tflops"] = round(2 * 1000 * 777 * 3000 / (ms * 1e-3) / 1e12, 2)
+    x1 = torch.randn((64, 512, 128), generator=g).to(torch.float16).to(dev)
+    x2 = torch.randn((64, 128, 512), generator=g).to(torch.float16).to(dev)
+    inp = torch.randn((64, 512, 512), generator=g).to(torch.float16).to(dev)
+    cb = torch.empty((64, 512, 512), dtype=torch.float16, device=dev)
+    db_ = _abi.make_gemm_desc(x1, x2, cb, bias=inp, alpha=0.5, beta=1.0, stream=s)
+    rb_ = C.byref(db_)
+
+    def baddbmm_step():
+        st_ = lib.tvk_gemm(rb_)
+        if st_:
+            _abi.check(st_)
+
+    ms, _ = timed(baddbmm_step, steps * 4, warmup, stream)
+    byts = 2 * (64 * 512 * 128 * 2 + 2 * 64 * 512 * 512)   # A, B, C-in, C-out
+    out["c5_baddbmm_kernel"] = _abi.gemm_plan(x1, x2, cb, bias=inp, alpha=0.5, beta=1.0)
+    out["c5_baddbmm_us"] = round(ms * 1e3, 2)
+    out["c5_baddbmm_GBps"] = round(byts / (ms * 1e-3) / 1e9, 1)
+    out["c5_baddbmm_pct_hbm"] = round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)
+    del a, b, c, x1, x2, inp, cb
+
     # ---- C1 fp32 1024^3 ----------------------------------------------------
     a = torch.randn((1024, 1024), generator=g).to(dev)
     b = torch.randn((1024, 1024), generator=g).to(dev)
