@@ -153,6 +153,31 @@ def test_dma_kernel_epilogue_sampled_rows(gpu, dtype, act):
 
 
 # ---------------------------------------------------------------------------
+# operands whose rows miss the 16-byte layout are copied once into an aligned,
+# zero-padded layout (workspace) before the vectorized kernels run
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("case", [
+    ((1000, 777), False, (777, 3000), False, None),    # C5 ragged: A rows of 777
+    ((777, 1000), True, (777, 3001), False, None),     # A m-contiguous view, B rows of 3001
+    ((3000, 777), False, (3000, 777), True, None),     # B = W^T with K = 777
+    ((600, 333), False, (333, 700), False, 3),         # batched, both repacked
+])
+def test_repacked_operands_integer_exact(gpu, dtype, case):
+    ashape, ta, bshape, tb, batch = case
+    lead = (batch,) if batch else ()
+    a = randint(lead + ashape, dtype, 26, -2, 3)
+    b = randint(lead + bshape, dtype, 27, -2, 3)
+    a = a.transpose(-1, -2) if ta else a
+    b = b.transpose(-1, -2) if tb else b
+    M, N = a.shape[-2], b.shape[-1]
+    got, plan = run(gpu, a, b, lead + (M, N), dtype)
+    assert "mfma" in plan or "dma" in plan, plan
+    assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
+
+
+# ---------------------------------------------------------------------------
 # split-K (few output tiles, long K): float32 partials summed in split order
 # ---------------------------------------------------------------------------
 

@@ -177,8 +177,15 @@ __global__ __launch_bounds__(128 * WGN) void gemm16_mfma_kernel(GemmArgs p) {
         B += (int64_t)kb * p.sb[1];
         K = min(p.k_chunk, p.K - kb);
     }
-    const int64_t a_bytes = 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(K - 1) * p.sa[2] + 1);
-    const int64_t b_bytes = 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(K - 1) * p.sb[1] + 1);
+    // With 16-byte loads the contiguous dimension is padded to 8 elements in
+    // memory (it is a multiple of 8, or the operand was repacked with zero
+    // padding): the range covers the padding so that the last chunk of the
+    // last row loads whole
+    auto pad8 = [](int v) { return (v + 7) / 8 * 8; };
+    const int ea_m = VEC && !AK ? pad8(p.M) : p.M, ea_k = VEC && AK ? pad8(K) : K;
+    const int eb_n = VEC && !BK ? pad8(p.N) : p.N, eb_k = VEC && BK ? pad8(K) : K;
+    const int64_t a_bytes = 2 * ((int64_t)(ea_m - 1) * p.sa[1] + (int64_t)(ea_k - 1) * p.sa[2] + 1);
+    const int64_t b_bytes = 2 * ((int64_t)(eb_n - 1) * p.sb[2] + (int64_t)(eb_k - 1) * p.sb[1] + 1);
     __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)min(a_bytes, (int64_t)0x7fffffff), 0x00020000);
     __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)B, 0, (int)min(b_bytes, (int64_t)0x7fffffff), 0x00020000);
 
@@ -488,6 +495,31 @@ __global__ __launch_bounds__(256) void gemm_seq_mfma_kernel(GemmArgs p) {
 }
 
 // ----------------------------------------------------------------------------
+// operand repack: dst[b][r][c] = src(b, r, c) for c < C, 0 for C <= c < Cp
+// (c is the operand's contiguous dimension; rows are Cp elements apart)
+// ----------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void repack16_kernel(const uint16_t* src, uint16_t* dst, int64_t s0, int64_t sr, int64_t sc,
+                                                        int batch, int R, int C, int Cp) {
+    const int64_t chunks = (int64_t)batch * R * (Cp / 8);
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < chunks; q += (int64_t)gridDim.x * 256) {
+        const int c0 = (int)(q % (Cp / 8)) * 8;
+        const int64_t br = q / (Cp / 8);
+        const int r = (int)(br % R), b = (int)(br / R);
+        const uint16_t* sp = src + (int64_t)b * s0 + (int64_t)r * sr;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = c0 + 2 * e;
+            const uint32_t lo = c < C ? sp[(int64_t)c * sc] : 0u;
+            const uint32_t hi = c + 1 < C ? sp[(int64_t)(c + 1) * sc] : 0u;
+            w[e] = lo | (hi << 16);
+        }
+        *reinterpret_cast<u32x4*>(dst + ((int64_t)b * R + r) * Cp + c0) = u32x4{w[0], w[1], w[2], w[3]};
+    }
+}
+
+// ----------------------------------------------------------------------------
 // host dispatch
 // ----------------------------------------------------------------------------
 
@@ -498,6 +530,9 @@ struct Plan {
     bool ak = true, bk = true, vec = true;
     const char* name;
     int split = 1, k_chunk = 0;   // MFMA128 split-K
+    // operands copied to an aligned workspace layout first (contiguous
+    // dimension padded with zeros to a multiple of 8 elements)
+    bool repack_a = false, repack_b = false;
 };
 
 bool fits_i32(int64_t v) { return v >= 0 && v <= 0x7fffffff; }
@@ -521,6 +556,14 @@ GemmArgs make_args(const tvk_gemm_desc& d) {
     p.act = d.activation;
     return p;
 }
+
+// Leading dimension of a repacked operand: its contiguous dimension padded to 8.
+int64_t pad8(int64_t v) { return (v + 7) / 8 * 8; }
+
+// Arguments as the kernels see them once the planned repacks are done (the
+// pointers of repacked operands only matter for alignment: workspace offsets
+// are 256-byte aligned).
+GemmArgs repacked_args(const tvk_gemm_desc& d, const struct Plan& pl);
 
 Plan make_plan(const tvk_gemm_desc& d) {
     Plan pl{Kern::GENERIC, true, true, true, "gemm_generic"};
@@ -547,6 +590,25 @@ Plan make_plan(const tvk_gemm_desc& d) {
     if (pl.bk) vec = vec && d.K % ce == 0 && (d.N == 1 || d.b_stride[2] % ce == 0);
     else vec = vec && d.N % ce == 0 && (d.K == 1 || d.b_stride[1] % ce == 0);
     pl.vec = vec;
+    // A sizeable fp16/bf16 product whose operands miss the 16-byte layout
+    // (rows not 8-element multiples, as [1000,777] or a sliced view) is worth
+    // one copy of the offending operands into an aligned layout
+    if (!vec && d.dtype != TVK_F32 && !(d.flags & TVK_GEMM_EXACT) && !skinny_applies(d.M, d.N, d.K, d.batch) &&
+        (double)d.M * d.N * d.K * d.batch >= double(1 << 28)) {
+        auto ok_a = [&]() {
+            bool v = al16(d.a) && (d.batch == 1 || d.a_stride[0] % ce == 0);
+            if (pl.ak) return v && d.K % ce == 0 && (d.M == 1 || d.a_stride[1] % ce == 0);
+            return v && d.M % ce == 0 && (d.K == 1 || d.a_stride[2] % ce == 0);
+        };
+        auto ok_b = [&]() {
+            bool v = al16(d.b) && (d.batch == 1 || d.b_stride[0] % ce == 0);
+            if (pl.bk) return v && d.K % ce == 0 && (d.N == 1 || d.b_stride[2] % ce == 0);
+            return v && d.N % ce == 0 && (d.K == 1 || d.b_stride[1] % ce == 0);
+        };
+        pl.repack_a = !ok_a();
+        pl.repack_b = !ok_b();
+        pl.vec = true;
+    }
     if (d.dtype != TVK_F32 && !(d.flags & TVK_GEMM_EXACT) && skinny_applies(d.M, d.N, d.K, d.batch)) {
         // the streaming kernel loads A by rows of k: 16-byte loads need A k-contiguous too
         bool v = al16(d.a) && al16(d.b) && a_k && d.K % 8 == 0 && (d.M == 1 || d.a_stride[1] % 8 == 0);
@@ -563,7 +625,7 @@ Plan make_plan(const tvk_gemm_desc& d) {
     if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
         pl.kern = big ? Kern::SEQ256 : Kern::SEQ128;
         pl.name = big ? "gemm_seq_mfma_256x256" : "gemm_seq_mfma_128x128";
-    } else if (big && dma_applies(make_args(d), a_k, b_k)) {
+    } else if (big && pl.vec && dma_applies(repacked_args(d, pl), a_k, b_k)) {
         pl.kern = Kern::DMA256;
         pl.name = "gemm16_dma_256x256";
     } else if (big) {
@@ -590,6 +652,22 @@ Plan make_plan(const tvk_gemm_desc& d) {
         }
     }
     return pl;
+}
+
+GemmArgs repacked_args(const tvk_gemm_desc& d, const Plan& pl) {
+    GemmArgs p = make_args(d);
+    static const char aligned_dummy[16] __attribute__((aligned(256))) = {0};
+    if (pl.repack_a) {
+        p.a = aligned_dummy;
+        if (pl.ak) { const int64_t ld = pad8(d.K); p.sa[0] = d.M * ld; p.sa[1] = ld; p.sa[2] = 1; }
+        else { const int64_t ld = pad8(d.M); p.sa[0] = d.K * ld; p.sa[1] = 1; p.sa[2] = ld; }
+    }
+    if (pl.repack_b) {
+        p.b = aligned_dummy;
+        if (pl.bk) { const int64_t ld = pad8(d.K); p.sb[0] = d.N * ld; p.sb[1] = 1; p.sb[2] = ld; }
+        else { const int64_t ld = pad8(d.N); p.sb[0] = d.K * ld; p.sb[1] = ld; p.sb[2] = 1; }
+    }
+    return p;
 }
 
 #define TVK_LAYOUT_SWITCH(PL, NTHR, KERNEL, ...)                                            \
@@ -631,6 +709,44 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
         q.b = (const char*)d.b + (size_t)(b0 * d.b_stride[0]) * es;
         if (q.has_bias) q.bias = (const char*)d.bias + (size_t)(b0 * d.bias_stride[0]) * es;
         q.c = (char*)d.c + (size_t)(b0 * d.c_stride[0]) * es;
+        // workspace: repacked operands, then split-K partials
+        auto al256 = [](size_t v) { return (v + 255) / 256 * 256; };
+        const int64_t a_rows = pl.ak ? d.M : d.K, a_ld = pad8(pl.ak ? d.K : d.M);
+        const int64_t b_rows = pl.bk ? d.N : d.K, b_ld = pad8(pl.bk ? d.K : d.N);
+        const size_t rep_a = pl.repack_a ? al256((size_t)nb * a_rows * a_ld * 2) : 0;
+        const size_t rep_b = pl.repack_b ? al256((size_t)nb * b_rows * b_ld * 2) : 0;
+        const size_t part_b = (pl.kern == Kern::MFMA128 && pl.split > 1) ? (size_t)pl.split * nb * d.M * d.N * 4 : 0;
+        char* ws = nullptr;
+        if (rep_a + rep_b + part_b > 0) {
+            int dev = 0;
+            (void)hipGetDevice(&dev);
+            ws = static_cast<char*>(device_workspace(dev, rep_a + rep_b + part_b));
+            if (!ws) return fail(TVK_ERR_OOM, "tvk_gemm: no workspace for repacked operands or split-K partials");
+        }
+        if constexpr (DT != TVK_F32) {
+            auto repack = [&](const void* src, int64_t s0, int64_t sr, int64_t sc, int64_t rows, int64_t cols, int64_t ld, char* dst) {
+                const int64_t chunks = (int64_t)nb * rows * (ld / 8);
+                const unsigned blocks = (unsigned)std::min<int64_t>((chunks + 255) / 256, 16384);
+                hipLaunchKernelGGL(repack16_kernel, dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(src),
+                                   reinterpret_cast<uint16_t*>(dst), s0, sr, sc, nb, (int)rows, (int)cols, (int)ld);
+            };
+            if (pl.repack_a) {
+                if (pl.ak) repack(q.a, d.a_stride[0], d.a_stride[1], d.a_stride[2], d.M, d.K, a_ld, ws);
+                else repack(q.a, d.a_stride[0], d.a_stride[2], d.a_stride[1], d.K, d.M, a_ld, ws);
+                q.a = ws;
+                q.sa[0] = a_rows * a_ld;
+                q.sa[1] = pl.ak ? a_ld : 1;
+                q.sa[2] = pl.ak ? 1 : a_ld;
+            }
+            if (pl.repack_b) {
+                if (pl.bk) repack(q.b, d.b_stride[0], d.b_stride[2], d.b_stride[1], d.N, d.K, b_ld, ws + rep_a);
+                else repack(q.b, d.b_stride[0], d.b_stride[1], d.b_stride[2], d.K, d.N, b_ld, ws + rep_a);
+                q.b = ws + rep_a;
+                q.sb[0] = b_rows * b_ld;
+                q.sb[1] = pl.bk ? 1 : b_ld;
+                q.sb[2] = pl.bk ? b_ld : 1;
+            }
+        }
         switch (pl.kern) {
         case Kern::K0: {
             int64_t total = (int64_t)nb * d.M * d.N;
@@ -674,10 +790,7 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
                 if (pl.kern == Kern::MFMA256W8) launch_mfma<DT, 256, 256, 4>(pl, q, grid, s);
                 else if (pl.kern == Kern::MFMA256) launch_mfma<DT, 256, 256, 2>(pl, q, grid, s);
                 else if (pl.split > 1) {
-                    int dev = 0;
-                    (void)hipGetDevice(&dev);
-                    q.part = static_cast<float*>(device_workspace(dev, (size_t)pl.split * nb * d.M * d.N * 4));
-                    if (!q.part) return fail(TVK_ERR_OOM, "tvk_gemm: no workspace for split-K partials");
+                    q.part = reinterpret_cast<float*>(ws + rep_a + rep_b);
                     q.split = pl.split;
                     q.k_chunk = pl.k_chunk;
                     grid.z = pl.split;

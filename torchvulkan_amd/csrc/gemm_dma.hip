@@ -211,20 +211,100 @@ __global__ __launch_bounds__(D_NT) void gemm16_dma_kernel(GemmArgs p) {
     // the workgroup's LDS can be handed to another
     wait_vmcnt<0>();
 
-    // accumulator layout of v_mfma_f32_16x16x32: lane l holds column l % 16,
-    // register r holds row (l / 16) * 4 + r
+    __syncthreads();   // every wave is done with the ring: it now holds the output tile
+
+    // Output through LDS, 64 rows at a time. The waves write their float32
+    // accumulators (layout of v_mfma_f32_16x16x32: lane l holds column l % 16,
+    // register r row (l / 16) * 4 + r); then each thread finishes 8 consecutive
+    // columns of one row (alpha, bias, activation, one rounding) and stores
+    // them with a single 16-byte store where the output rows allow it.
+    typedef typename elem<DT>::T T;
+    constexpr int E_LD = D_BN + 4;   // floats per LDS row
+    float* et = reinterpret_cast<float*>(lds_raw);
+    T* Cb = reinterpret_cast<T*>(p.c) + (int64_t)b * p.sc[0];
+    const T* Bb = p.has_bias ? reinterpret_cast<const T*>(p.bias) + (int64_t)b * p.sbias[0] : nullptr;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    const bool vec_c = p.sc[2] == 1 && p.sc[1] % 8 == 0 && al16(Cb);
+    const bool vec_b = p.has_bias && p.sbias[2] == 1 && p.sbias[1] % 8 == 0 && al16(Bb);
+    const bool plain = !p.has_bias && p.act == TVK_ACT_NONE;
+    // thread tid finishes chunk q = tid + j * D_NT (j < 4) of each 64-row pass:
+    // row q / 32, columns 8 * (q % 32); the bias chunks of all four passes are
+    // requested up front so their latency overlaps
+    static_assert(64 * (D_BN / 8) == 4 * D_NT, "four chunks per thread per pass");
+    u32x4 bpre[4][4];
+    if (vec_b) {
 #pragma unroll
-    for (int i = 0; i < D_FM; ++i)
+        for (int pass = 0; pass < 4; ++pass)
 #pragma unroll
-        for (int j = 0; j < D_FN; ++j) {
-            const int col = n0 + wn * D_WTN + j * 16 + lane % 16;
-            if (col >= p.N) continue;
+            for (int j = 0; j < 4; ++j) {
+                const int q = tid + j * D_NT;
+                const int row = m0 + pass * 64 + q / (D_BN / 8), col = n0 + (q % (D_BN / 8)) * 8;
+                bpre[pass][j] = u32x4{0, 0, 0, 0};
+                if (row < p.M && col + 8 <= p.N)
+                    bpre[pass][j] = *reinterpret_cast<const u32x4*>(Bb + (int64_t)row * p.sbias[1] + col);
+            }
+    }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = m0 + wm * D_WTM + i * 16 + (lane / 16) * 4 + r;
-                if (row < p.M) store_out<DT>(p, b, row, col, acc[i][j][r]);
+    for (int pass = 0; pass < 4; ++pass) {
+        if (wm == pass / 2) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const int i = (pass % 2) * 4 + ii;
+#pragma unroll
+                for (int j = 0; j < D_FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        et[(ii * 16 + (lane / 16) * 4 + r) * E_LD + wn * D_WTN + j * 16 + lane % 16] = acc[i][j][r];
             }
         }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int q = tid + j * D_NT;
+            const int rl = q / (D_BN / 8), cc = (q % (D_BN / 8)) * 8;
+            const int row = m0 + pass * 64 + rl, col = n0 + cc;
+            if (row >= p.M || col >= p.N) continue;
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(et + rl * E_LD + cc);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(et + rl * E_LD + cc + 4);
+            const float a8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            const bool full = col + 8 <= p.N;
+            float bv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (p.has_bias) {
+                if (vec_b && full) {
+                    const u32x4 w = bpre[pass][j];
+                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        bv[2 * e] = elem<DT>::to_f32(__builtin_bit_cast(T, (uint16_t)(ww[e] & 0xffffu)));
+                        bv[2 * e + 1] = elem<DT>::to_f32(__builtin_bit_cast(T, (uint16_t)(ww[e] >> 16)));
+                    }
+                } else {
+                    const T* bp = Bb + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2];
+                    for (int e = 0; e < 8 && col + e < p.N; ++e) bv[e] = elem<DT>::to_f32(bp[(int64_t)e * p.sbias[2]]);
+                }
+            }
+            uint16_t h[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float v;
+                if (plain) {
+#pragma clang fp contract(off)
+                    v = a8[e] * p.alpha;
+                } else {
+                    v = epilogue_math(a8[e], p.alpha, p.has_bias, bv[e], p.beta, p.act);
+                }
+                h[e] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
+            }
+            T* cp = Cb + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2];
+            if (vec_c && full) {
+                *reinterpret_cast<u32x4*>(cp) = u32x4{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
+                                                      (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16)};
+            } else {
+                for (int e = 0; e < 8 && col + e < p.N; ++e) cp[(int64_t)e * p.sc[2]] = __builtin_bit_cast(T, h[e]);
+            }
+        }
+        __syncthreads();
+    }
 }
 
 }  // namespace
