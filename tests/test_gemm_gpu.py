@@ -117,6 +117,32 @@ def test_dma_kernel_integer_exact(gpu, dtype, ta, tb, shape):
 
 
 @pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("shape", [(1000, 1024, 96), (8192, 512, 512), (4000, 136, 64)])
+def test_dma_kernel_128_tiles_integer_exact(gpu, dtype, ta, tb, shape):
+    # mid-size products take the same ring on 128x128 tiles
+    M, N, K = shape
+    a = randint((K, M) if ta else (M, K), dtype, 28, -2, 3)
+    b = randint((N, K) if tb else (K, N), dtype, 29, -2, 3)
+    a = a.t() if ta else a
+    b = b.t() if tb else b
+    got, plan = run(gpu, a, b, (M, N), dtype)
+    assert plan == "gemm16_dma_128x128"
+    assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+def test_dma_kernel_128_tiles_batched_epilogue(gpu, dtype):
+    # baddbmm-like: batched, C-in through the fused epilogue, alpha and beta
+    a = randn((4, 512, 512), dtype, 30)
+    b = randn((4, 512, 384), dtype, 31)
+    inp = randn((4, 512, 384), dtype, 32)
+    got, plan = run(gpu, a, b, (4, 512, 384), dtype, bias=inp, alpha=0.5, beta=1.0)
+    assert plan == "gemm16_dma_128x128"
+    assert_close(got, oracle_mm(a, b, dtype, bias=inp, alpha=0.5, beta=1.0), dtype, plan)
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
 def test_dma_kernel_column_edge_inside_a_chunk(gpu, dtype):
     # N = 3001 of rows strided 3008: the last 16-byte chunk of a B row would
     # straddle N, so the ring kernel declines and another kernel runs

@@ -523,7 +523,7 @@ __global__ __launch_bounds__(256) void repack16_kernel(const uint16_t* src, uint
 // host dispatch
 // ----------------------------------------------------------------------------
 
-enum class Kern { K0, GENERIC, SEQ256, SEQ128, MFMA256, MFMA256W8, MFMA128, SKINNY, DMA256 };
+enum class Kern { K0, GENERIC, SEQ256, SEQ128, MFMA256, MFMA256W8, MFMA128, SKINNY, DMA256, DMA128 };
 
 struct Plan {
     Kern kern;
@@ -635,9 +635,16 @@ Plan make_plan(const tvk_gemm_desc& d) {
     } else {
         pl.kern = Kern::MFMA128;
         pl.name = "gemm16_mfma_128x128";
+        const int64_t t128 = ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
+        // enough 128x128 tiles (or a short K, which split-K cannot help):
+        // the LDS-ring kernel on 128x128 tiles
+        if (pl.vec && (t128 >= 192 || d.K < 1024) && t128 >= 32 && dma_applies(repacked_args(d, pl), a_k, b_k)) {
+            pl.kern = Kern::DMA128;
+            pl.name = "gemm16_dma_128x128";
+            return pl;
+        }
         // Few output tiles and a long K (weight gradients, batch-256 layers):
         // split K so about one workgroup per CU runs, partials in float32.
-        const int64_t t128 = ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
         if (t128 < 192 && d.K >= 1024) {
             int64_t split = std::min<int64_t>({(256 + t128 - 1) / t128, d.K / 256, 32});
             if (split >= 2) {
@@ -774,8 +781,9 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
             }
             break;
         case Kern::DMA256:
+        case Kern::DMA128:
             if constexpr (DT != TVK_F32) {
-                hipError_t e = launch_dma(DT, q, pl.ak, pl.bk, s);
+                hipError_t e = launch_dma(DT, q, pl.ak, pl.bk, pl.kern == Kern::DMA256 ? 256 : 128, s);
                 if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_gemm: launch failed: ") + hipGetErrorString(e));
             }
             break;

@@ -155,11 +155,12 @@ __device__ inline u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, bool row_ok, int64_
 void* device_workspace(int device, size_t bytes);
 uint32_t* device_counters(int device, size_t count);
 
-// 256x256-tile kernel with operands fetched straight into LDS (gemm_dma.hip).
+// Tile kernel with operands fetched straight into LDS (gemm_dma.hip).
 // dma_applies: the operands meet its alignment and K granularity; launch_dma
 // returns hipSuccess or the launch error.
 bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor);
-hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s);
+// tile: 256 (256x256) or 128 (128x128)
+hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, int tile, hipStream_t s);
 
 // Channels-last convolution on the LDS ring (conv_nhwc.hip); mode 0 forward,
 // 1 grad input, 2 grad weight.

@@ -37,14 +37,26 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 #define TVK_LDS __attribute__((address_space(3)))
 
-constexpr int D_BM = 256, D_BN = 256, D_BK = 32, D_NS = 4;
-constexpr int D_NW = 8, D_NT = 64 * D_NW;        // 2 waves along M x 4 along N
-constexpr int D_WTM = 128, D_WTN = 64;           // wave tile
-constexpr int D_FM = D_WTM / 16, D_FN = D_WTN / 16;
-constexpr int D_OPB = 256 * D_BK * 2;            // bytes per operand per stage
-constexpr int D_STB = 2 * D_OPB;                 // bytes per stage
-constexpr int D_DPW = D_OPB / 1024 / D_NW;       // loads per wave per operand per stage
-constexpr int D_DPS = 2 * D_DPW;                 // loads per wave per stage
+constexpr int D_BK = 32, D_NS = 4;
+
+// Tile configurations: 256x256 runs 8 waves of 128x64; the others 64x64 wave
+// tiles (128x128: 4 waves, 256x128 and 128x256: 8 waves).
+template <int BM_, int BN_>
+struct DCfg {
+    static constexpr int BM = BM_, BN = BN_;
+    static constexpr bool BIG = BM == 256 && BN == 256;
+    static constexpr int NW = BIG ? 8 : (BM / 64) * (BN / 64);
+    static constexpr int NT = 64 * NW;
+    static constexpr int WN = BIG ? 4 : BN / 64;           // waves along N
+    static constexpr int WMW = NW / WN;                     // waves along M
+    static constexpr int WTM = BM / WMW, WTN = BN / WN;     // wave tile
+    static constexpr int FM = WTM / 16, FN = WTN / 16;
+    static constexpr int OPA = BM * D_BK * 2, OPB = BN * D_BK * 2;   // bytes per operand per stage
+    static constexpr int STB = OPA + OPB;
+    static constexpr int DA = OPA / 1024 / NW, DB = OPB / 1024 / NW; // loads per wave per stage
+    static constexpr int DS = DA + DB;
+    static_assert(DA >= 1 && DB >= 1 && WTN == 64, "tile configuration");
+};
 
 // Buffer resource over [p, p + bytes): loads past the end return zeros.
 __device__ inline i32x4 dma_rsrc(const void* p, int64_t bytes) {
@@ -70,22 +82,25 @@ __device__ inline int swz_mn(int kr) { return (kr & 3) * 2; }
 // Per-lane source offsets (bytes, at k = 0) of one operand's loads. Rows or
 // columns outside the matrix start at kOOB, so with the k advance added they
 // stay past the buffer's end and load zeros.
-template <bool KM>
+// D loads per wave; W = the tile's extent along this operand's rows (m or n):
+// an MN tile has k-rows of 2W bytes, 1024 / (2W) of them per 1 KB load.
+template <bool KM, int D, int W>
 struct DmaSrc {
-    uint32_t off[D_DPW];
+    uint32_t off[D];
     uint32_t kstep;   // bytes per stage along k
     __device__ inline void init(int64_t s_row, int64_t s_k, int row0, int rows, int wave, int lane) {
+        constexpr int CPR = 2 * W / 16;   // 16-byte chunks per MN k-row
 #pragma unroll
-        for (int i = 0; i < D_DPW; ++i) {
-            const int blk = wave * D_DPW + i;
+        for (int i = 0; i < D; ++i) {
+            const int blk = wave * D + i;
             if constexpr (KM) {
                 const int row = blk * 16 + lane / 4;
                 const int c = (lane % 4) ^ swz_km(row);
                 const int gr = row0 + row;
                 off[i] = gr < rows ? (uint32_t)(((int64_t)gr * s_row + c * 8) * 2) : kOOB;
             } else {
-                const int kr = blk * 2 + lane / 32;
-                const int c = (lane % 32) ^ swz_mn(kr);
+                const int kr = blk * (64 / CPR) + lane / CPR;
+                const int c = (lane % CPR) ^ swz_mn(kr);
                 const int gc = row0 + c * 8;
                 off[i] = gc < rows ? (uint32_t)(((int64_t)kr * s_k + gc) * 2) : kOOB;
             }
@@ -96,7 +111,7 @@ struct DmaSrc {
 
 // One 16x16x32 operand fragment: lane l holds row (or column) l % 16 and
 // k = (l / 16) * 8 .. + 7 of the stage.
-template <bool KM>
+template <bool KM, int W>
 __device__ inline u32x4 read_frag(uint32_t base, int row_base, int lane) {
     if constexpr (KM) {
         const int row = row_base + lane % 16;
@@ -112,7 +127,7 @@ __device__ inline u32x4 read_frag(uint32_t base, int row_base, int lane) {
 #pragma unroll
         for (int rr = 0; rr < 2; ++rr) {
             const int kr = g * 8 + rr * 4 + s / 4;
-            TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(base + kr * 512 + ((chunk ^ swz_mn(kr)) * 16) + within);
+            TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(base + kr * (2 * W) + ((chunk ^ swz_mn(kr)) * 16) + within);
             const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
             out[rr * 2] = w.x;
             out[rr * 2 + 1] = w.y;
@@ -129,12 +144,18 @@ __device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-template <int DT, bool AK, bool BK>
-__global__ __launch_bounds__(D_NT) void gemm16_dma_kernel(GemmArgs p) {
+constexpr int dma_threads(int bm, int bn) { return 64 * ((bm == 256 && bn == 256) ? 8 : (bm / 64) * (bn / 64)); }
+
+template <int DT, bool AK, bool BK, int BM, int BN>
+__global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArgs p) {
+    typedef DCfg<BM, BN> G;
+    constexpr int D_BM = BM, D_BN = BN, D_NT = G::NT, D_FM = G::FM, D_FN = G::FN, D_WTM = G::WTM, D_WTN = G::WTN;
+    constexpr int D_OPB = G::OPA, D_STB = G::STB, D_DPS = G::DS;
+    static_assert(dma_threads(BM, BN) == G::NT, "thread count");
     __shared__ __attribute__((aligned(1024))) char lds_raw[D_NS * D_STB];
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds_raw);
     const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
-    const int wm = wave / 4, wn = wave % 4;
+    const int wm = wave / G::WN, wn = wave % G::WN;
     const int b = blockIdx.y;
     int tm, tn;
     tile_of(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, tm, tn);
@@ -145,14 +166,14 @@ __global__ __launch_bounds__(D_NT) void gemm16_dma_kernel(GemmArgs p) {
     const char* B = reinterpret_cast<const char*>(p.b) + (int64_t)b * p.sb[0] * 2;
     const i32x4 ra = dma_rsrc(A, 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1));
     const i32x4 rb = dma_rsrc(B, 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1));
-    DmaSrc<AK> da;
-    DmaSrc<BK> db;
+    DmaSrc<AK, G::DA, BM> da;
+    DmaSrc<BK, G::DB, BN> db;
     da.init(p.sa[1], p.sa[2], m0, p.M, wave, lane);
     db.init(p.sb[2], p.sb[1], n0, p.N, wave, lane);
     auto dma_one = [&](int kt, int q) {   // q-th load (of D_DPS) of this wave for stage kt
         const uint32_t slot = lds0 + (uint32_t)((kt % D_NS) * D_STB);
-        if (q < D_DPW) dma16(ra, slot + (uint32_t)((wave * D_DPW + q) * 1024), da.off[q] + (uint32_t)kt * da.kstep);
-        else dma16(rb, slot + D_OPB + (uint32_t)((wave * D_DPW + q - D_DPW) * 1024), db.off[q - D_DPW] + (uint32_t)kt * db.kstep);
+        if (q < G::DA) dma16(ra, slot + (uint32_t)((wave * G::DA + q) * 1024), da.off[q] + (uint32_t)kt * da.kstep);
+        else dma16(rb, slot + D_OPB + (uint32_t)((wave * G::DB + q - G::DA) * 1024), db.off[q - G::DA] + (uint32_t)kt * db.kstep);
     };
 
     f32x4 acc[D_FM][D_FN];
@@ -172,9 +193,9 @@ __global__ __launch_bounds__(D_NT) void gemm16_dma_kernel(GemmArgs p) {
     wait_vmcnt<D_DPS * (D_NS - 1)>();
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < D_FM; ++i) fa[0][i] = read_frag<AK>(lds0, wm * D_WTM + i * 16, lane);
+    for (int i = 0; i < D_FM; ++i) fa[0][i] = read_frag<AK, BM>(lds0, wm * D_WTM + i * 16, lane);
 #pragma unroll
-    for (int j = 0; j < D_FN; ++j) fb[0][j] = read_frag<BK>(lds0 + D_OPB, wn * D_WTN + j * 16, lane);
+    for (int j = 0; j < D_FN; ++j) fb[0][j] = read_frag<BK, BN>(lds0 + D_OPB, wn * D_WTN + j * 16, lane);
     wait_vmcnt<D_DPS * (D_NS - 2)>();
     __syncthreads();
 
@@ -190,8 +211,8 @@ __global__ __launch_bounds__(D_NT) void gemm16_dma_kernel(GemmArgs p) {
             acc[i][j] = mfma16<DT>(fa[cur][i], fb[cur][j], acc[i][j]);
             if (q % 2 == 0) {
                 const int r = q / 2;
-                if (r < D_FM) fa[cur ^ 1][r] = read_frag<AK>(st_next, wm * D_WTM + r * 16, lane);
-                else if (r < D_FM + D_FN) fb[cur ^ 1][r - D_FM] = read_frag<BK>(st_next + D_OPB, wn * D_WTN + (r - D_FM) * 16, lane);
+                if (r < D_FM) fa[cur ^ 1][r] = read_frag<AK, BM>(st_next, wm * D_WTM + r * 16, lane);
+                else if (r < D_FM + D_FN) fb[cur ^ 1][r - D_FM] = read_frag<BK, BN>(st_next + D_OPB, wn * D_WTN + (r - D_FM) * 16, lane);
             } else if (q / 2 < D_DPS) {
                 dma_one(kt + D_NS, q / 2);
             }
@@ -230,13 +251,15 @@ __global__ __launch_bounds__(D_NT) void gemm16_dma_kernel(GemmArgs p) {
     // thread tid finishes chunk q = tid + j * D_NT (j < 4) of each 64-row pass:
     // row q / 32, columns 8 * (q % 32); the bias chunks of all four passes are
     // requested up front so their latency overlaps
-    static_assert(64 * (D_BN / 8) == 4 * D_NT, "four chunks per thread per pass");
-    u32x4 bpre[4][4];
+    constexpr int NPASS = D_BM / 64, CPT = 64 * (D_BN / 8) / D_NT;   // passes; chunks per thread per pass
+    static_assert(CPT * D_NT == 64 * (D_BN / 8), "whole chunks per thread");
+    static_assert(64 * (D_BN + 4) * 4 <= D_NS * D_STB, "epilogue tile fits the ring");
+    u32x4 bpre[NPASS][CPT];
     if (vec_b) {
 #pragma unroll
-        for (int pass = 0; pass < 4; ++pass)
+        for (int pass = 0; pass < NPASS; ++pass)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < CPT; ++j) {
                 const int q = tid + j * D_NT;
                 const int row = m0 + pass * 64 + q / (D_BN / 8), col = n0 + (q % (D_BN / 8)) * 8;
                 bpre[pass][j] = u32x4{0, 0, 0, 0};
@@ -245,11 +268,11 @@ __global__ __launch_bounds__(D_NT) void gemm16_dma_kernel(GemmArgs p) {
             }
     }
 #pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
-        if (wm == pass / 2) {
+    for (int pass = 0; pass < NPASS; ++pass) {
+        if (wm == pass * 64 / D_WTM) {
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-                const int i = (pass % 2) * 4 + ii;
+                const int i = (pass * 64 % D_WTM) / 16 + ii;
 #pragma unroll
                 for (int j = 0; j < D_FN; ++j)
 #pragma unroll
@@ -259,7 +282,7 @@ __global__ __launch_bounds__(D_NT) void gemm16_dma_kernel(GemmArgs p) {
         }
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < CPT; ++j) {
             const int q = tid + j * D_NT;
             const int rl = q / (D_BN / 8), cc = (q % (D_BN / 8)) * 8;
             const int row = m0 + pass * 64 + rl, col = n0 + cc;
@@ -329,20 +352,25 @@ bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor) {
     return true;
 }
 
-hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s) {
-    p.tiles_m = (p.M + D_BM - 1) / D_BM;
-    p.tiles_n = (p.N + D_BN - 1) / D_BN;
-    const dim3 grid(p.tiles_m * p.tiles_n, p.batch);
-#define TVK_DMA_LAUNCH(DT)                                                                                     \
-    do {                                                                                                       \
-        if (a_kmajor && b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, true>), grid, dim3(D_NT), 0, s, p);   \
-        else if (a_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, false>), grid, dim3(D_NT), 0, s, p);         \
-        else if (b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, true>), grid, dim3(D_NT), 0, s, p);         \
-        else hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, false>), grid, dim3(D_NT), 0, s, p);                      \
-    } while (0)
-    if (dtype == TVK_F16) TVK_DMA_LAUNCH(TVK_F16);
-    else TVK_DMA_LAUNCH(TVK_BF16);
-#undef TVK_DMA_LAUNCH
+template <int DT, int BM, int BN>
+void launch_dma_tile(GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s) {
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + BN - 1) / BN;
+    const dim3 grid(p.tiles_m * p.tiles_n, p.batch), block(DCfg<BM, BN>::NT);
+    if (a_kmajor && b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, true, BM, BN>), grid, block, 0, s, p);
+    else if (a_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, false, BM, BN>), grid, block, 0, s, p);
+    else if (b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, true, BM, BN>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, false, BM, BN>), grid, block, 0, s, p);
+}
+
+hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, int tile, hipStream_t s) {
+    if (dtype == TVK_F16) {
+        if (tile == 256) launch_dma_tile<TVK_F16, 256, 256>(p, a_kmajor, b_kmajor, s);
+        else launch_dma_tile<TVK_F16, 128, 128>(p, a_kmajor, b_kmajor, s);
+    } else {
+        if (tile == 256) launch_dma_tile<TVK_BF16, 256, 256>(p, a_kmajor, b_kmajor, s);
+        else launch_dma_tile<TVK_BF16, 128, 128>(p, a_kmajor, b_kmajor, s);
+    }
     return hipGetLastError();
 }
 
