@@ -102,7 +102,7 @@ def load() -> C.CDLL:
     global _lib
     if _lib is None:
         if not _LIB_PATH.exists():
-            raise OSError(f"{_LIB_PATH} is not built; run python -m torchvulkan_amd.build")
+            raise OSError(f"{_LIB_PATH} is not built; run python torchvulkan_amd/build.py")
         lib = C.CDLL(str(_LIB_PATH))
         lib.tvk_last_error.restype = C.c_char_p
         lib.tvk_gemm.argtypes = [C.POINTER(GemmDesc)]

@@ -6,7 +6,8 @@ library travels with the source tree. The PrivateUse1 backend extension
 (``csrc/backend/*.cpp``) is built by :func:`build_backend` against the
 installed torch headers and links to the same library.
 
-Run ``python -m torchvulkan_amd.build`` (or ``__graft_entry__.build()``).
+Run ``python torchvulkan_amd/build.py`` (or ``__graft_entry__.build()``); the
+package itself cannot be imported before its extension exists.
 """
 from __future__ import annotations
 
