@@ -39,10 +39,19 @@ typedef enum {
     TVK_ERR_DEVICE = 4
 } tvk_status;
 
+/* Element types. tvk_gemm and tvk_conv2d_* take F32, F16 and BF16; tvk_copy
+ * takes every one of them. BOOL is one byte holding 0 or 1. */
 typedef enum {
     TVK_F32 = 0,
     TVK_F16 = 1,
-    TVK_BF16 = 2
+    TVK_BF16 = 2,
+    TVK_F64 = 3,
+    TVK_I64 = 4,
+    TVK_I32 = 5,
+    TVK_I16 = 6,
+    TVK_I8 = 7,
+    TVK_U8 = 8,
+    TVK_BOOL = 9
 } tvk_dtype;
 
 /* Epilogue activation, the reference's MatmulActivation
@@ -126,6 +135,69 @@ tvk_status tvk_mem_get_info(int device, size_t* free_bytes, size_t* total_bytes)
 tvk_status tvk_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream, int blocking);
 tvk_status tvk_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream, int blocking);
 tvk_status tvk_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Copy and cast: one strided element-wise copy with dtype conversion         */
+/* ------------------------------------------------------------------------- */
+
+#define TVK_COPY_MAX_DIMS 16
+
+/* dst[i] = convert(src[i]) for every index i of `sizes`, with each tensor at
+ * base + sum_d i_d * stride_d (elements). src strides may be 0 (an expanded
+ * source); dst must not have two indices on one element, and src and dst must
+ * not partly overlap (the caller checks both, as the reference's
+ * TensorIterator does with set_check_mem_overlap, transfer.cpp:18-22).
+ *
+ * Conversion is the reference's castValue (src/shaders/core/cast.slang:49-52,
+ * src/shaders/core/dtype.slang:122-282): the source widens to int64 (signed
+ * integers), uint64 (U8), float (F16, BF16, F32) or double (F64); the
+ * destination is built from that wide value in one conversion:
+ *   - to an integer type: C conversion (truncation toward zero from a float,
+ *     two's-complement wrap from an integer; a float outside the target's
+ *     range or NaN is undefined there, as in SPIR-V, and saturates here);
+ *   - to F32/F64: round to nearest even;
+ *   - to F16: one round to nearest even from the wide value (from F64 too);
+ *   - to BF16: BFloat16(float(v)), so F64 rounds to float first.
+ * With BOOL on either side the value is (src != 0) ? 1 : 0 (IS_BOOL_CAST,
+ * src/shaders/ops/cast.slang:29-33).
+ *
+ * Replaces dispatch_copy_shader (src/api/tensor/transfer.cpp:16-56) and
+ * dispatch_cast_shader (src/api/tensor/cast.cpp:8-56). Dimensions are merged
+ * where both tensors allow it; more than TVK_COPY_MAX_DIMS dimensions left
+ * after merging is TVK_ERR_UNSUPPORTED. Offsets are 64-bit: no 32-bit limit. */
+typedef struct {
+    int32_t src_dtype;      /* tvk_dtype */
+    int32_t dst_dtype;      /* tvk_dtype */
+    int32_t ndim;           /* 0 .. TVK_COPY_MAX_DIMS (0: one element) */
+    int32_t reserved;       /* must be 0 */
+    int64_t sizes[TVK_COPY_MAX_DIMS];
+    const void* src; int64_t src_strides[TVK_COPY_MAX_DIMS];
+    void* dst; int64_t dst_strides[TVK_COPY_MAX_DIMS];
+    void* stream;           /* hipStream_t or NULL */
+} tvk_copy_desc;
+
+tvk_status tvk_copy(const tvk_copy_desc* desc);
+
+/* Name of the kernel tvk_copy would launch for `desc` ("memcpy", "cast_contig",
+ * "transpose", "strided", or "none" for an empty copy); no launch. */
+tvk_status tvk_copy_plan(const tvk_copy_desc* desc, char* name, size_t name_len);
+
+/* Fills every element of a strided destination with one element value.
+ * `pattern` holds the element's bytes (little-endian, low `elem_size` bytes):
+ * the caller converts the scalar to the element type, as the reference does
+ * on the host before its fill shader (src/api/ops/fill.cpp:11-131). A zero
+ * stride over an extent > 1 is TVK_ERR_INVALID. Replaces the fill_ and zero_
+ * dispatch (fill.cpp:131-133); fill_.Tensor reads its value on the host too. */
+typedef struct {
+    int32_t elem_size;      /* 1, 2, 4 or 8 */
+    int32_t ndim;           /* 0 .. TVK_COPY_MAX_DIMS */
+    int64_t sizes[TVK_COPY_MAX_DIMS];
+    void* dst; int64_t dst_strides[TVK_COPY_MAX_DIMS];
+    uint64_t pattern;
+    void* stream;
+} tvk_fill_desc;
+
+tvk_status tvk_fill(const tvk_fill_desc* desc);
 
 /* ------------------------------------------------------------------------- */
 /* Compute: batched strided GEMM with fused epilogue                          */

@@ -21,7 +21,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "build" / "liboracle.so"
 
-F32, F16, BF16 = 0, 1, 2
+F32, F16, BF16, F64, I64, I32, I16, I8, U8, BOOL = range(10)
 ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
 
 _lib = None
@@ -56,6 +56,10 @@ def load() -> C.CDLL:
             C.c_double, C.c_double, C.POINTER(C.c_float),
         ]
         lib.oracle_gemm_rows.restype = C.c_int
+        lib.oracle_cast.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int64]
+        lib.oracle_cast.restype = C.c_int
+        lib.oracle_f64_to_f16.argtypes = [C.c_double]
+        lib.oracle_f64_to_f16.restype = C.c_uint16
         _lib = lib
     return _lib
 
@@ -89,6 +93,24 @@ def to_f32(bits_or_f32: np.ndarray, dtype: int) -> np.ndarray:
     if dtype == F16:
         return np.asarray(bits_or_f32, dtype=np.uint16).view(np.float16).astype(np.float32)
     return bf16_bits_to_f32(bits_or_f32)
+
+
+# ---------------------------------------------------------------------------
+# element conversion of tvk_copy (copy_oracle.c)
+# ---------------------------------------------------------------------------
+
+# numpy storage of each code; float16/bfloat16 travel as raw uint16 patterns
+STORAGE = {F32: np.float32, F16: np.uint16, BF16: np.uint16, F64: np.float64, I64: np.int64, I32: np.int32,
+           I16: np.int16, I8: np.int8, U8: np.uint8, BOOL: np.uint8}
+
+
+def cast(src: np.ndarray, sdt: int, ddt: int) -> np.ndarray:
+    """castValue<sdt, ddt> of every element (the reference's cast rules); any shape, returns a dense array."""
+    s = np.ascontiguousarray(src, dtype=STORAGE[sdt])
+    d = np.zeros(s.shape, dtype=STORAGE[ddt])
+    if s.size and load().oracle_cast(sdt, s.ctypes.data, ddt, d.ctypes.data, s.size) != 0:
+        raise ValueError("oracle_cast rejected its dtypes")
+    return d
 
 
 # ---------------------------------------------------------------------------

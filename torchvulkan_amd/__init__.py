@@ -141,6 +141,12 @@ def manual_seed_all(seed) -> None:
     torch.manual_seed(seed)
 
 
+def _is_in_bad_fork() -> bool:
+    """torch.manual_seed asks every device module this before seeding it; the
+    host generator this device draws from has no fork state of its own."""
+    return False
+
+
 def seed() -> None:
     torch.seed()
 

@@ -13,7 +13,9 @@ from pathlib import Path
 _LIB_PATH = Path(__file__).resolve().parent / "libtvk_hip.so"
 
 TVK_OK, TVK_ERR_UNSUPPORTED, TVK_ERR_OOM, TVK_ERR_INVALID, TVK_ERR_DEVICE = range(5)
-TVK_F32, TVK_F16, TVK_BF16 = range(3)
+(TVK_F32, TVK_F16, TVK_BF16, TVK_F64, TVK_I64, TVK_I32, TVK_I16, TVK_I8, TVK_U8,
+ TVK_BOOL) = range(10)
+TVK_COPY_MAX_DIMS = 16
 TVK_ACT_NONE, TVK_ACT_RELU, TVK_ACT_GELU = range(3)
 TVK_GEMM_EXACT = 1
 
@@ -74,6 +76,33 @@ class ConvDesc(C.Structure):
     ]
 
 
+I64xD = C.c_int64 * TVK_COPY_MAX_DIMS
+
+
+class CopyDesc(C.Structure):
+    _fields_ = [
+        ("src_dtype", C.c_int32),
+        ("dst_dtype", C.c_int32),
+        ("ndim", C.c_int32),
+        ("reserved", C.c_int32),
+        ("sizes", I64xD),
+        ("src", C.c_void_p), ("src_strides", I64xD),
+        ("dst", C.c_void_p), ("dst_strides", I64xD),
+        ("stream", C.c_void_p),
+    ]
+
+
+class FillDesc(C.Structure):
+    _fields_ = [
+        ("elem_size", C.c_int32),
+        ("ndim", C.c_int32),
+        ("sizes", I64xD),
+        ("dst", C.c_void_p), ("dst_strides", I64xD),
+        ("pattern", C.c_uint64),
+        ("stream", C.c_void_p),
+    ]
+
+
 class DeviceProps(C.Structure):
     _fields_ = [
         ("name", C.c_char * 256),
@@ -121,6 +150,9 @@ def load() -> C.CDLL:
         lib.tvk_device_properties.argtypes = [C.c_int, C.POINTER(DeviceProps)]
         for fn in ("tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad"):
             getattr(lib, fn).argtypes = [C.POINTER(ConvDesc)]
+        lib.tvk_copy.argtypes = [C.POINTER(CopyDesc)]
+        lib.tvk_copy_plan.argtypes = [C.POINTER(CopyDesc), C.c_char_p, C.c_size_t]
+        lib.tvk_fill.argtypes = [C.POINTER(FillDesc)]
         for fn in _ALL_ENTRY_POINTS:
             getattr(lib, fn).restype = C.c_int if fn != "tvk_last_error" else C.c_char_p
         _lib = lib
@@ -133,7 +165,8 @@ _ALL_ENTRY_POINTS = (
     "tvk_pointer_device", "tvk_set_memory_limit", "tvk_memory_allocated", "tvk_max_memory_allocated",
     "tvk_memory_reserved", "tvk_reset_peak_memory_stats", "tvk_mem_get_info", "tvk_memcpy_h2d",
     "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan",
-    "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad",
+    "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad", "tvk_copy", "tvk_copy_plan",
+    "tvk_fill",
 )
 
 
@@ -165,6 +198,72 @@ def _dtype_code(dtype) -> int:
     if dtype not in codes:
         raise TvkUnsupported(TVK_ERR_UNSUPPORTED, f"dtype {dtype} is not on the dense-contraction path")
     return codes[dtype]
+
+
+def copy_dtype_code(dtype) -> int:
+    """tvk_dtype of a torch dtype tvk_copy handles (TvkUnsupported for the others)."""
+    import torch
+
+    codes = {torch.float32: TVK_F32, torch.float16: TVK_F16, torch.bfloat16: TVK_BF16, torch.float64: TVK_F64,
+             torch.int64: TVK_I64, torch.int32: TVK_I32, torch.int16: TVK_I16, torch.int8: TVK_I8,
+             torch.uint8: TVK_U8, torch.bool: TVK_BOOL}
+    if dtype not in codes:
+        raise TvkUnsupported(TVK_ERR_UNSUPPORTED, f"dtype {dtype} has no device copy")
+    return codes[dtype]
+
+
+def make_copy_desc(src, dst, stream=None) -> CopyDesc:
+    """Describes dst.copy_(src) for device tensors; src is broadcast to dst's shape."""
+    src = src.expand(dst.shape)
+    if dst.dim() > TVK_COPY_MAX_DIMS:
+        raise TvkUnsupported(TVK_ERR_UNSUPPORTED, f"{dst.dim()} dimensions")
+    d = CopyDesc()
+    d.src_dtype = copy_dtype_code(src.dtype)
+    d.dst_dtype = copy_dtype_code(dst.dtype)
+    d.ndim = dst.dim()
+    d.reserved = 0
+    d.sizes = I64xD(*dst.shape)
+    d.src = src.data_ptr() if src.numel() else None
+    d.src_strides = I64xD(*src.stride())
+    d.dst = dst.data_ptr() if dst.numel() else None
+    d.dst_strides = I64xD(*dst.stride())
+    d.stream = stream
+    return d
+
+
+def copy(src, dst, stream=None) -> None:
+    """dst.copy_(src) through tvk_copy (torch device tensors; torch's current stream by default)."""
+    import torch
+
+    if stream is None and dst.is_cuda:
+        stream = torch.cuda.current_stream(dst.device).cuda_stream
+    d = make_copy_desc(src, dst, stream)
+    check(load().tvk_copy(C.byref(d)))
+
+
+def copy_plan(src, dst) -> str:
+    d = make_copy_desc(src, dst)
+    buf = C.create_string_buffer(64)
+    check(load().tvk_copy_plan(C.byref(d), buf, 64))
+    return buf.value.decode()
+
+
+def fill(dst, value, stream=None) -> None:
+    """Fills a torch device tensor through tvk_fill; the element bytes come from a one-element CPU tensor."""
+    import torch
+
+    if stream is None and dst.is_cuda:
+        stream = torch.cuda.current_stream(dst.device).cuda_stream
+    one = torch.empty(1, dtype=dst.dtype).fill_(value)
+    d = FillDesc()
+    d.elem_size = dst.element_size()
+    d.ndim = dst.dim()
+    d.sizes = I64xD(*dst.shape)
+    d.dst = dst.data_ptr() if dst.numel() else None
+    d.dst_strides = I64xD(*dst.stride())
+    d.pattern = int.from_bytes(one.view(torch.uint8).numpy().tobytes(), "little")
+    d.stream = stream
+    check(load().tvk_fill(C.byref(d)))
 
 
 def _strides3(t) -> tuple[int, int, int]:

@@ -42,5 +42,13 @@ at::Tensor to_host(const at::Tensor& t);
 void from_host(const at::Tensor& host, const at::Tensor& dst);
 
 int32_t tvk_dtype_of(c10::ScalarType t, bool& ok);
+// tvk_dtype of every dtype tvk_copy handles.
+int32_t copy_dtype_of(c10::ScalarType t, bool& ok);
+// Both dtypes have a device copy, the dimension count fits, and neither side is
+// a lazily conjugated or negated view.
+bool device_copyable(const at::Tensor& src, const at::Tensor& dst);
+// dst.copy_(src) on the device (both device tensors on dst's device; src
+// broadcast to dst's shape), ordered on dst's stream.
+void device_copy(const at::Tensor& src, const at::Tensor& dst);
 
 }  // namespace tvkb

@@ -10,6 +10,8 @@
 #include "common.h"
 
 #include <ATen/EmptyTensor.h>
+#include <ATen/ExpandUtils.h>
+#include <ATen/MemoryOverlap.h>
 #include <ATen/detail/PrivateUse1HooksInterface.h>
 #include <ATen/native/CPUFallback.h>
 #include <ATen/native/Resize.h>
@@ -68,9 +70,58 @@ void view_extent(const at::Tensor& t, int64_t& lo, int64_t& n) {
     n = hi - lo + 1;
 }
 
-at::Tensor to_host(const at::Tensor& t) {
+int32_t copy_dtype_of(c10::ScalarType t, bool& ok) {
+    ok = true;
+    switch (t) {
+    case at::kFloat: return TVK_F32;
+    case at::kHalf: return TVK_F16;
+    case at::kBFloat16: return TVK_BF16;
+    case at::kDouble: return TVK_F64;
+    case at::kLong: return TVK_I64;
+    case at::kInt: return TVK_I32;
+    case at::kShort: return TVK_I16;
+    case at::kChar: return TVK_I8;
+    case at::kByte: return TVK_U8;
+    case at::kBool: return TVK_BOOL;
+    default: ok = false; return -1;
+    }
+}
+
+bool device_copyable(const at::Tensor& src, const at::Tensor& dst) {
+    bool a = false, b = false;
+    copy_dtype_of(src.scalar_type(), a);
+    copy_dtype_of(dst.scalar_type(), b);
+    return a && b && dst.dim() <= TVK_COPY_MAX_DIMS && !src.is_conj() && !src.is_neg() && !dst.is_conj() &&
+           !dst.is_neg();
+}
+
+void device_copy(const at::Tensor& src, const at::Tensor& dst) {
+    if (dst.numel() == 0) return;
+    const at::Tensor s = src.sizes() == dst.sizes() ? src : src.expand(dst.sizes());
+    tvk_copy_desc d;
+    std::memset(&d, 0, sizeof(d));
+    bool ok = false;
+    d.src_dtype = copy_dtype_of(s.scalar_type(), ok);
+    d.dst_dtype = copy_dtype_of(dst.scalar_type(), ok);
+    d.ndim = (int32_t)dst.dim();
+    for (int64_t k = 0; k < dst.dim(); ++k) {
+        d.sizes[k] = dst.size(k);
+        d.src_strides[k] = s.stride(k);
+        d.dst_strides[k] = dst.stride(k);
+    }
+    d.src = s.data_ptr();
+    d.dst = dst.data_ptr();
+    d.stream = stream_of(dst);
+    check_status(tvk_copy(&d), "tvk_copy");
+}
+
+namespace {
+
+// The byte-extent route for dtypes the device copy does not take (complex,
+// float8, unsigned 16-64 bit): the whole storage extent of the view crosses
+// PCIe and the host applies the strides.
+at::Tensor to_host_extent(const at::Tensor& t) {
     at::Tensor out = at::empty(t.sizes(), t.options().device(at::kCPU));
-    if (t.numel() == 0) return out;
     int64_t lo = 0, n = 0;
     view_extent(t, lo, n);
     const int64_t es = t.element_size();
@@ -82,25 +133,73 @@ at::Tensor to_host(const at::Tensor& t) {
     return out;
 }
 
-void from_host(const at::Tensor& host, const at::Tensor& dst) {
-    if (dst.numel() == 0) return;
-    at::Tensor src = host.to(dst.scalar_type()).contiguous();
-    void* s = stream_of(dst);
-    if (dst.is_contiguous()) {
-        check_status(tvk_memcpy_h2d(dst.data_ptr(), src.data_ptr(), (size_t)(src.numel() * src.element_size()), s, 1),
-                     "copy to device");
-        return;
-    }
-    // strided destination: read its storage extent, write the view on the host, write the extent back
+void from_host_extent(const at::Tensor& src, const at::Tensor& dst) {
     int64_t lo = 0, n = 0;
     view_extent(dst, lo, n);
     const int64_t es = dst.element_size();
+    void* s = stream_of(dst);
     at::Tensor buf = at::empty({n}, dst.options().device(at::kCPU));
     char* base = static_cast<char*>(dst.storage().mutable_data()) + lo * es;
     check_status(tvk_memcpy_d2h(buf.data_ptr(), base, (size_t)(n * es), s, 1), "copy to host");
     std::vector<int64_t> strides(dst.strides().begin(), dst.strides().end());
     buf.as_strided(dst.sizes(), strides, 0).copy_(src);
     check_status(tvk_memcpy_h2d(base, buf.data_ptr(), (size_t)(n * es), s, 1), "copy to device");
+}
+
+}  // namespace
+
+// Device -> host, after copy_vulkan_to_host (src/api/tensor/transfer.cpp:78-127):
+// expanded dimensions are narrowed to their one distinct slice first; a
+// strided view is gathered on the device into a dense buffer, which is the
+// only thing that crosses PCIe.
+at::Tensor to_host(const at::Tensor& t) {
+    at::Tensor out = at::empty(t.sizes(), t.options().device(at::kCPU));
+    if (t.numel() == 0) return out;
+    bool ok = false;
+    copy_dtype_of(t.scalar_type(), ok);
+    if (!ok || t.dim() > TVK_COPY_MAX_DIMS) return to_host_extent(t);
+    at::Tensor distinct = t;
+    bool expanded = false;
+    for (int64_t d = 0; d < t.dim(); ++d)
+        if (t.stride(d) == 0 && t.size(d) > 1) {
+            distinct = distinct.narrow(d, 0, 1);
+            expanded = true;
+        }
+    at::Tensor dense = distinct;
+    if (!distinct.is_contiguous()) {
+        dense = at::empty(distinct.sizes(), distinct.options().memory_format(at::MemoryFormat::Contiguous));
+        device_copy(distinct, dense);
+    }
+    at::Tensor host = expanded ? at::empty(distinct.sizes(), out.options()) : out;
+    check_status(tvk_memcpy_d2h(host.data_ptr(), dense.data_ptr(), (size_t)(dense.numel() * dense.element_size()),
+                                stream_of(t), 1),
+                 "copy to host");
+    if (expanded) out.copy_(host.expand(t.sizes()));
+    return out;
+}
+
+// Host -> device, after copy_host_to_vulkan (src/api/tensor/transfer.cpp:58-76):
+// the host converts to the destination dtype and packs densely; a strided
+// destination is written from a dense device staging buffer by tvk_copy.
+void from_host(const at::Tensor& host, const at::Tensor& dst) {
+    if (dst.numel() == 0) return;
+    at::Tensor src = host.to(dst.scalar_type());
+    if (src.sizes() != dst.sizes()) src = src.expand(dst.sizes());
+    src = src.contiguous();
+    void* s = stream_of(dst);
+    if (dst.is_contiguous()) {
+        check_status(tvk_memcpy_h2d(dst.data_ptr(), src.data_ptr(), (size_t)(src.numel() * src.element_size()), s, 1),
+                     "copy to device");
+        return;
+    }
+    if (!device_copyable(dst, dst)) {
+        from_host_extent(src, dst);
+        return;
+    }
+    at::Tensor staging = at::empty(dst.sizes(), dst.options().memory_format(at::MemoryFormat::Contiguous));
+    check_status(tvk_memcpy_h2d(staging.data_ptr(), src.data_ptr(), (size_t)(src.numel() * src.element_size()), s, 1),
+                 "copy to device");
+    device_copy(staging, dst);
 }
 
 namespace {
@@ -269,23 +368,101 @@ at::Tensor empty_strided(c10::IntArrayRef size, c10::IntArrayRef stride, std::op
     return at::detail::empty_strided_generic(size, stride, &g_allocator, ks, c10::dtype_or_default(dtype));
 }
 
+// _copy_from: torch routes copy_ here whenever one side is a vulkan tensor
+// (torchvulkan::copy_vulkan, src/api/tensor/transfer.cpp:292-397). Device to
+// device copies, casts and layout changes run on the device (tvk_copy);
+// crossing to or from the host moves only dense bytes.
 at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool non_blocking) {
-    TORCH_CHECK(self.sizes() == dst.sizes() || self.numel() == dst.numel(), "torchvulkan [ERROR]: _copy_from size mismatch");
     if (dst.numel() == 0) return dst;
-    if (self.is_privateuseone() && dst.is_privateuseone() && self.scalar_type() == dst.scalar_type() &&
-        self.is_contiguous() && dst.is_contiguous() && self.sizes() == dst.sizes()) {
-        check_status(tvk_memcpy_d2d(dst.data_ptr(), self.data_ptr(), (size_t)(self.numel() * self.element_size()),
-                                    stream_of(dst)),
-                     "tvk_memcpy_d2d");
+    // as at::native::copy_, a copy onto its own memory is a no-op
+    if (self.is_alias_of(dst) && self.storage_offset() == dst.storage_offset() && self.sizes().equals(dst.sizes()) &&
+        self.strides().equals(dst.strides()) && self.scalar_type() == dst.scalar_type() &&
+        self.is_conj() == dst.is_conj() && self.is_neg() == dst.is_neg())
+        return dst;
+    at::Tensor src = self;
+    if (src.sizes() != dst.sizes()) {
+        if (at::is_expandable_to(src.sizes(), dst.sizes())) src = src.expand(dst.sizes());
+        else {
+            TORCH_CHECK(src.numel() == dst.numel(), "torchvulkan [ERROR]: _copy_from size mismatch");
+            src = src.reshape(dst.sizes());
+        }
+    }
+    if (src.is_privateuseone() && dst.is_privateuseone()) {
+        if (device_copyable(src, dst)) {
+            at::assert_no_internal_overlap(dst);
+            at::assert_no_partial_overlap(dst, src);
+            if (src.device() != dst.device()) {
+                // another device's memory: stage through a dense buffer on the destination
+                at::Tensor dense = src.contiguous();
+                at::Tensor staged = at::empty(dense.sizes(), dense.options().device(dst.device()));
+                check_status(tvk_synchronize(src.device().index()), "tvk_synchronize");
+                check_status(tvk_memcpy_d2d(staged.data_ptr(), dense.data_ptr(),
+                                            (size_t)(dense.numel() * dense.element_size()), stream_of(dst)),
+                             "tvk_memcpy_d2d");
+                device_copy(staged, dst);
+            } else {
+                device_copy(src, dst);
+            }
+            return dst;
+        }
+        TVKB_FALLBACK("A copy from ", src.scalar_type(), " to ", dst.scalar_type(), " can't run on the device. Falling back to CPU.");
+        from_host(to_host(src), dst);
         return dst;
     }
-    at::Tensor host = self.is_privateuseone() ? to_host(self) : self;
     if (dst.is_privateuseone()) {
-        from_host(host.reshape(dst.sizes()), dst);
-    } else {
-        dst.copy_(host.reshape(dst.sizes()));
+        from_host(src, dst);
+        return dst;
     }
+    // device -> host: a cast the device can do is done before the transfer
+    if (src.scalar_type() != dst.scalar_type() && device_copyable(src, dst)) {
+        at::Tensor cast = at::empty(src.sizes(), src.options().dtype(dst.scalar_type()).memory_format(at::MemoryFormat::Contiguous));
+        device_copy(src, cast);
+        src = cast;
+    }
+    dst.copy_(to_host(src));
     return dst;
+}
+
+// fill_.Scalar / zero_ / fill_.Tensor (src/api/ops/fill.cpp:11-133): the host
+// converts the scalar to the element type, the device writes its bytes. The
+// conversion is a CPU fill of one element (for a one-element tensor) or of two
+// (otherwise), so the value and the overflow error are those of the CPU's fill
+// of the same tensor: CPU fill_ converts a lone element without the overflow
+// check it applies to larger tensors.
+at::Tensor& fill_scalar(at::Tensor& self, const at::Scalar& value) {
+    if (self.numel() == 0) return self;
+    bool ok = false;
+    copy_dtype_of(self.scalar_type(), ok);
+    at::Tensor one = at::empty({self.numel() == 1 ? 1 : 2}, self.options().device(at::kCPU)).fill_(value);
+    if (!ok || self.dim() > TVK_COPY_MAX_DIMS || self.is_conj() || self.is_neg()) {
+        TVKB_FALLBACK("Can't fill a ", self.scalar_type(), " tensor of this shape on the device. Falling back to CPU.");
+        from_host(one.narrow(0, 0, 1).expand(self.sizes()), self);
+        return self;
+    }
+    at::Tensor t = self;
+    for (int64_t d = 0; d < t.dim(); ++d)
+        if (t.stride(d) == 0 && t.size(d) > 1) t = t.narrow(d, 0, 1);   // one write per distinct element
+    tvk_fill_desc fd;
+    std::memset(&fd, 0, sizeof(fd));
+    fd.elem_size = (int32_t)t.element_size();
+    fd.ndim = (int32_t)t.dim();
+    for (int64_t k = 0; k < t.dim(); ++k) {
+        fd.sizes[k] = t.size(k);
+        fd.dst_strides[k] = t.stride(k);
+    }
+    fd.dst = t.data_ptr();
+    std::memcpy(&fd.pattern, one.data_ptr(), (size_t)one.element_size());   // element 0
+    fd.stream = stream_of(t);
+    check_status(tvk_fill(&fd), "tvk_fill");
+    return self;
+}
+
+at::Tensor& zero_(at::Tensor& self) { return fill_scalar(self, 0); }
+
+at::Tensor& fill_tensor(at::Tensor& self, const at::Tensor& value) {
+    TORCH_CHECK(value.dim() == 0, "fill_ only supports 0-dimension value tensor but got tensor with ", value.dim(),
+                " dimensions.");
+    return fill_scalar(self, value.item());
 }
 
 at::Tensor copy_from_and_resize(const at::Tensor& self, const at::Tensor& dst) {
@@ -327,6 +504,9 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
     m.impl("set_.source_Storage_storage_offset", &at::native::set_storage_cpu_);
     m.impl("_copy_from", &tvkb::copy_from);
     m.impl("_copy_from_and_resize", &tvkb::copy_from_and_resize);
+    m.impl("fill_.Scalar", &tvkb::fill_scalar);
+    m.impl("fill_.Tensor", &tvkb::fill_tensor);
+    m.impl("zero_", &tvkb::zero_);
     m.impl("_local_scalar_dense", &tvkb::local_scalar_dense);
 }
 

@@ -1,0 +1,742 @@
+// Strided element-wise copy with dtype conversion (tvk_copy): the copy and
+// cast kernels on both sides of every contraction (operand .to() and
+// .contiguous(), .out copies, conv's NCHW .contiguous()).
+//
+// Reference semantics: dispatch_copy_shader (src/api/tensor/transfer.cpp:16-56)
+// walks a TensorIterator-coalesced index space and copies T -> T;
+// dispatch_cast_shader (src/api/tensor/cast.cpp:8-56) does the same through
+// castValue (src/shaders/core/cast.slang:49-52): the source widens to int64,
+// uint64, float or double and the destination is built from that one wide
+// value (src/shaders/core/dtype.slang:122-282); with a bool on either side the
+// value is (src != 0) ? 1 : 0 (src/shaders/ops/cast.slang:29-33).
+//
+// The host plan merges dimensions the way TensorIterator coalesces them
+// (innermost first, by destination strides), then picks one of three kernels:
+//   cast_contig: both sides dense: 8 elements per thread, vector loads/stores;
+//   transpose:   destination contiguous along a dimension the source is not,
+//                source contiguous along another: 64x64 tiles through LDS, so
+//                both the loads and the stores are coalesced (W.t().contiguous(),
+//                NCHW <-> NHWC);
+//   strided:     anything else: one element per thread, offsets from the
+//                linear index by multiply-high division.
+// Same-dtype dense copies are a hipMemcpyAsync. Same-dtype copies move raw bits
+// (integer lanes of the element's size), so NaN payloads are kept.
+#include "tvk_common.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+
+namespace tvk {
+namespace {
+
+constexpr int kMaxDims = TVK_COPY_MAX_DIMS;
+constexpr int DYN = -1;   // dtype taken from the kernel arguments
+
+// ---------------------------------------------------------------------------
+// element conversion
+// ---------------------------------------------------------------------------
+
+enum { FAM_I = 0, FAM_U = 1, FAM_F = 2, FAM_D = 3 };
+
+__host__ __device__ constexpr int family(int dt) {
+    return dt == TVK_F64 ? FAM_D
+         : (dt == TVK_F32 || dt == TVK_F16 || dt == TVK_BF16) ? FAM_F
+         : (dt == TVK_U8 || dt == TVK_BOOL) ? FAM_U
+         : FAM_I;
+}
+
+struct Wide {
+    int64_t i;
+    uint64_t u;
+    float f;
+    double d;
+};
+
+__device__ __forceinline__ Wide load_wide(const char* p, int dt) {
+    Wide w{0, 0, 0.0f, 0.0};
+    switch (dt) {
+        case TVK_F32: w.f = *reinterpret_cast<const float*>(p); break;
+        case TVK_F16: w.f = (float)*reinterpret_cast<const _Float16*>(p); break;
+        case TVK_BF16: w.f = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p)); break;
+        case TVK_F64: w.d = *reinterpret_cast<const double*>(p); break;
+        case TVK_I64: w.i = *reinterpret_cast<const int64_t*>(p); break;
+        case TVK_I32: w.i = *reinterpret_cast<const int32_t*>(p); break;
+        case TVK_I16: w.i = *reinterpret_cast<const int16_t*>(p); break;
+        case TVK_I8: w.i = *reinterpret_cast<const int8_t*>(p); break;
+        default: w.u = *reinterpret_cast<const uint8_t*>(p); break;   // U8, BOOL
+    }
+    return w;
+}
+
+__device__ __forceinline__ bool nonzero(const Wide& w, int fam) {
+    switch (fam) {
+        case FAM_I: return w.i != 0;
+        case FAM_U: return w.u != 0;
+        case FAM_F: return w.f != 0.0f;   // NaN != 0
+        default: return w.d != 0.0;
+    }
+}
+
+__device__ __forceinline__ float wide_to_f32(const Wide& w, int fam) {
+    switch (fam) {
+        case FAM_I: return (float)w.i;
+        case FAM_U: return (float)w.u;
+        case FAM_F: return w.f;
+        default: return (float)w.d;
+    }
+}
+
+__device__ __forceinline__ double wide_to_f64(const Wide& w, int fam) {
+    switch (fam) {
+        case FAM_I: return (double)w.i;
+        case FAM_U: return (double)w.u;
+        case FAM_F: return (double)w.f;
+        default: return w.d;
+    }
+}
+
+// float64 -> float16 in one rounding (the reference's half(double)): round to
+// odd into float32 (24 bits >= 11 + 2), then round to nearest even into
+// float16, which gives the correctly rounded result (Boldo and Melquiond,
+// "When double rounding is odd", 2005).
+__device__ __forceinline__ _Float16 f64_to_f16(double d) {
+    float f = (float)d;
+    if (f != f || (double)f == d) return (_Float16)f;
+    uint32_t bits = __builtin_bit_cast(uint32_t, f);
+    if (fabs((double)f) > fabs(d)) bits -= 1;   // the magnitude went up: one step back toward zero
+    bits |= 1u;                                 // inexact: odd last bit
+    return (_Float16)__builtin_bit_cast(float, bits);
+}
+
+__device__ __forceinline__ _Float16 wide_to_f16(const Wide& w, int fam) {
+    if (fam == FAM_D) return f64_to_f16(w.d);
+    // integers: exact in float32 up to 2^24, and every larger magnitude is
+    // past float16's range either way, so one rounding results
+    return (_Float16)wide_to_f32(w, fam);
+}
+
+// Float to integer, saturating at the target's range, NaN -> 0 (out of range
+// is undefined in the reference; in range this is truncation toward zero).
+template <typename I>
+__device__ __forceinline__ I float_to_int(double v) {
+    constexpr double lo = (double)std::numeric_limits<I>::min();   // -2^(bits-1), exact in double
+    if (v != v) return 0;
+    if (v <= lo) return std::numeric_limits<I>::min();
+    if (v >= -lo) return std::numeric_limits<I>::max();
+    return (I)v;
+}
+
+template <typename I>
+__device__ __forceinline__ I wide_to_int(const Wide& w, int fam) {
+    switch (fam) {
+        case FAM_I: return (I)w.i;
+        case FAM_U: return (I)w.u;
+        case FAM_F: return float_to_int<I>((double)w.f);
+        default: return float_to_int<I>(w.d);
+    }
+}
+
+__device__ __forceinline__ uint8_t wide_to_u8(const Wide& w, int fam) {
+    switch (fam) {
+        case FAM_I: return (uint8_t)w.i;
+        case FAM_U: return (uint8_t)w.u;
+        default: {
+            const double v = fam == FAM_F ? (double)w.f : w.d;
+            if (!(v > 0.0)) return 0;
+            if (v >= 255.0) return 255;
+            return (uint8_t)v;
+        }
+    }
+}
+
+__device__ __forceinline__ void store_narrow(char* p, int dt, const Wide& w, int fam) {
+    switch (dt) {
+        case TVK_F32: *reinterpret_cast<float*>(p) = wide_to_f32(w, fam); break;
+        case TVK_F16: *reinterpret_cast<_Float16*>(p) = wide_to_f16(w, fam); break;
+        case TVK_BF16: *reinterpret_cast<uint16_t*>(p) = f32_to_bf16_bits(wide_to_f32(w, fam)); break;
+        case TVK_F64: *reinterpret_cast<double*>(p) = wide_to_f64(w, fam); break;
+        case TVK_I64: *reinterpret_cast<int64_t*>(p) = wide_to_int<int64_t>(w, fam); break;
+        case TVK_I32: *reinterpret_cast<int32_t*>(p) = wide_to_int<int32_t>(w, fam); break;
+        case TVK_I16: *reinterpret_cast<int16_t*>(p) = wide_to_int<int16_t>(w, fam); break;
+        case TVK_I8: *reinterpret_cast<int8_t*>(p) = wide_to_int<int8_t>(w, fam); break;
+        case TVK_U8: *reinterpret_cast<uint8_t*>(p) = wide_to_u8(w, fam); break;
+        default: *reinterpret_cast<uint8_t*>(p) = nonzero(w, fam) ? 1 : 0; break;   // BOOL
+    }
+}
+
+// dst = castValue<Src, Dst>(src). With compile-time dtypes every switch folds.
+__device__ __forceinline__ void convert(const char* sp, int sdt, char* dp, int ddt) {
+    Wide w = load_wide(sp, sdt);
+    int fam = family(sdt);
+    if (sdt == TVK_BOOL || ddt == TVK_BOOL) {
+        w.i = nonzero(w, fam) ? 1 : 0;
+        fam = FAM_I;
+    }
+    store_narrow(dp, ddt, w, fam);
+}
+
+template <int SDT, int DDT>
+struct Dts {
+    int s, d;
+    __device__ __forceinline__ Dts(int rs, int rd) : s(SDT == DYN ? rs : SDT), d(DDT == DYN ? rd : DDT) {}
+};
+
+// ---------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------
+
+struct Shape {
+    int nd;
+    int64_t size[kMaxDims], ss[kMaxDims], ds[kMaxDims];   // innermost first, elements
+};
+
+// Division by a runtime constant: q = (hi32(n * m) + n) >> s (exact for every
+// 32-bit n; the sum is taken in 64 bits).
+struct Div32 {
+    uint32_t d, m, s;
+};
+
+Div32 make_div(uint32_t d) {
+    Div32 r{d, 0, 0};
+    uint32_t s = 0;
+    while (s < 32 && (uint64_t(1) << s) < d) ++s;
+    r.s = s;
+    r.m = (uint32_t)(((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1);
+    return r;
+}
+
+__device__ __forceinline__ uint32_t div32(uint32_t n, const Div32& v) {
+    const uint32_t t = __umulhi(n, v.m);
+    return (uint32_t)(((uint64_t)t + n) >> v.s);
+}
+
+struct StridedArgs {
+    const char* src;
+    char* dst;
+    int sdt, ddt;
+    int ss_bytes, ds_bytes;   // element sizes
+    int nd;
+    int64_t numel;
+    Div32 div[kMaxDims];
+    int64_t ss[kMaxDims], ds[kMaxDims];
+    int64_t size[kMaxDims];
+};
+
+// One element per thread; dimension 0 is the destination's innermost, so
+// neighbouring threads write neighbouring elements where dst allows it.
+template <int SDT, int DDT, bool IDX32>
+__global__ __launch_bounds__(256) void copy_strided_kernel(StridedArgs p) {
+    const Dts<SDT, DDT> t(p.sdt, p.ddt);
+    const int64_t step = (int64_t)gridDim.x * 256;
+    for (int64_t li = (int64_t)blockIdx.x * 256 + threadIdx.x; li < p.numel; li += step) {
+        int64_t so = 0, dof = 0;
+        if constexpr (IDX32) {
+            uint32_t rem = (uint32_t)li;
+#pragma unroll 1
+            for (int k = 0; k < p.nd - 1; ++k) {
+                const uint32_t q = div32(rem, p.div[k]);
+                const uint32_t c = rem - q * p.div[k].d;
+                so += (int64_t)c * p.ss[k];
+                dof += (int64_t)c * p.ds[k];
+                rem = q;
+            }
+            so += (int64_t)rem * p.ss[p.nd - 1];
+            dof += (int64_t)rem * p.ds[p.nd - 1];
+        } else {
+            int64_t rem = li;
+#pragma unroll 1
+            for (int k = 0; k < p.nd - 1; ++k) {
+                const int64_t q = rem / p.size[k];
+                const int64_t c = rem - q * p.size[k];
+                so += c * p.ss[k];
+                dof += c * p.ds[k];
+                rem = q;
+            }
+            so += rem * p.ss[p.nd - 1];
+            dof += rem * p.ds[p.nd - 1];
+        }
+        convert(p.src + so * p.ss_bytes, t.s, p.dst + dof * p.ds_bytes, t.d);
+    }
+}
+
+// Dense to dense, 8 elements per thread. VEC: both bases aligned to 8
+// elements, so each group of 8 is one set of aligned vector accesses.
+template <int SDT, int DDT, int SB, int DB, bool VEC>
+__global__ __launch_bounds__(256) void cast_contig_kernel(const char* src, char* dst, int64_t n, int sdt, int ddt) {
+    const Dts<SDT, DDT> t(sdt, ddt);
+    const int64_t groups = (n + 7) / 8;
+    const int64_t step = (int64_t)gridDim.x * 256;
+    for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < groups; g += step) {
+        const int64_t e0 = g * 8;
+        if (VEC && e0 + 8 <= n) {
+            struct alignas(SB * 8) SV { char b[SB * 8]; };
+            struct alignas(DB * 8) DV { char b[DB * 8]; };
+            const SV sv = *reinterpret_cast<const SV*>(src + e0 * SB);
+            DV dv;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) convert(sv.b + e * SB, t.s, dv.b + e * DB, t.d);
+            *reinterpret_cast<DV*>(dst + e0 * DB) = dv;
+        } else {
+            const int64_t e1 = e0 + 8 < n ? e0 + 8 : n;
+            for (int64_t e = e0; e < e1; ++e) convert(src + e * SB, t.s, dst + e * DB, t.d);
+        }
+    }
+}
+
+// Runtime element sizes (dtypes outside the templated float set).
+__global__ __launch_bounds__(256) void cast_contig_dyn_kernel(const char* src, char* dst, int64_t n, int sdt, int ddt,
+                                                             int sb, int db) {
+    const int64_t step = (int64_t)gridDim.x * 256;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += step)
+        convert(src + e * sb, sdt, dst + e * db, ddt);
+}
+
+constexpr int TT = 64;   // transpose tile edge
+
+struct TransposeArgs {
+    const char* src;
+    char* dst;
+    int sdt, ddt;
+    int sb, db;               // element sizes
+    int64_t n0, nj;           // extents of the two tiled dimensions
+    int64_t ss0, dsj;         // src stride along 0, dst stride along j (the other two are 1)
+    int64_t tiles0, tilesj;
+    int nb;                   // other dimensions
+    int64_t bsize[kMaxDims], bss[kMaxDims], bds[kMaxDims];
+};
+
+// Writes the low `db` bytes of w (one converted element) to p.
+template <typename Word>
+__device__ __forceinline__ void store_elem(char* p, const Word& w, int db) {
+    switch (db) {
+        case 1: *reinterpret_cast<uint8_t*>(p) = (uint8_t)w; break;
+        case 2: *reinterpret_cast<uint16_t*>(p) = (uint16_t)w; break;
+        case 4: *reinterpret_cast<uint32_t*>(p) = (uint32_t)w; break;
+        default: *reinterpret_cast<uint64_t*>(p) = (uint64_t)w; break;
+    }
+}
+
+// dst is contiguous along dimension 0, src along dimension j. A 64x64 tile is
+// read along j (coalesced in src), converted, parked in LDS, and written
+// along 0 (coalesced in dst). Word = the LDS type holding one converted element.
+template <int SDT, int DDT, typename Word>
+__global__ __launch_bounds__(256) void copy_transpose_kernel(TransposeArgs p) {
+    const Dts<SDT, DDT> t(p.sdt, p.ddt);
+    const int db = DDT == DYN ? p.db : (int)dtype_size(DDT);
+    __shared__ Word tile[TT][TT + 1];
+    int64_t bid = blockIdx.x;
+    const int64_t t0 = bid % p.tiles0;
+    bid /= p.tiles0;
+    const int64_t tj = bid % p.tilesj;
+    int64_t rest = bid / p.tilesj;
+    int64_t so = 0, dof = 0;
+    for (int k = 0; k < p.nb; ++k) {
+        const int64_t c = rest % p.bsize[k];
+        rest /= p.bsize[k];
+        so += c * p.bss[k];
+        dof += c * p.bds[k];
+    }
+    const int64_t a0 = t0 * TT, b0 = tj * TT;
+    const int lane = threadIdx.x % TT, row = threadIdx.x / TT;
+#pragma unroll 4
+    for (int r = row; r < TT; r += 256 / TT) {
+        const int64_t a = a0 + r, b = b0 + lane;   // read along j
+        Word w = 0;
+        if (a < p.n0 && b < p.nj) convert(p.src + (so + a * p.ss0 + b) * p.sb, t.s, reinterpret_cast<char*>(&w), t.d);
+        tile[r][lane] = w;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int r = row; r < TT; r += 256 / TT) {
+        const int64_t b = b0 + r, a = a0 + lane;   // write along 0
+        if (a < p.n0 && b < p.nj) {
+            store_elem(p.dst + (dof + a + b * p.dsj) * db, tile[lane][r], db);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host plan
+// ---------------------------------------------------------------------------
+
+enum PlanKind { PK_NONE = 0, PK_MEMCPY, PK_CAST_CONTIG, PK_TRANSPOSE, PK_STRIDED };
+
+struct Plan {
+    PlanKind kind;
+    Shape sh;
+    int64_t numel;
+    int j;   // transpose: the source's contiguous dimension
+};
+
+bool valid_dtype(int dt) { return dt >= TVK_F32 && dt <= TVK_BOOL; }
+
+tvk_status make_plan(const tvk_copy_desc* d, Plan& pl, const char* who) {
+    if (!d) return fail(TVK_ERR_INVALID, std::string(who) + ": desc is NULL");
+    if (!valid_dtype(d->src_dtype) || !valid_dtype(d->dst_dtype))
+        return fail(TVK_ERR_UNSUPPORTED, std::string(who) + ": unsupported dtype");
+    if (d->reserved != 0) return fail(TVK_ERR_INVALID, std::string(who) + ": nonzero reserved field");
+    if (d->ndim < 0 || d->ndim > kMaxDims)
+        return fail(TVK_ERR_UNSUPPORTED, std::string(who) + ": ndim " + std::to_string(d->ndim) + " is outside 0.." +
+                                             std::to_string(kMaxDims));
+    pl = Plan{};
+    int64_t numel = 1;
+    for (int k = 0; k < d->ndim; ++k) {
+        if (d->sizes[k] < 0) return fail(TVK_ERR_INVALID, std::string(who) + ": negative size");
+        if (d->src_strides[k] < 0 || d->dst_strides[k] < 0)
+            return fail(TVK_ERR_UNSUPPORTED, std::string(who) + ": negative strides are not supported");
+        numel *= d->sizes[k];
+    }
+    pl.numel = numel;
+    if (numel == 0) {
+        pl.kind = PK_NONE;
+        return TVK_OK;
+    }
+    if (!d->src || !d->dst) return fail(TVK_ERR_INVALID, std::string(who) + ": src or dst is NULL");
+    // dimensions of extent > 1, innermost (smallest dst stride) first; ties by src stride
+    int idx[kMaxDims];
+    int n = 0;
+    for (int k = 0; k < d->ndim; ++k)
+        if (d->sizes[k] > 1) {
+            if (d->dst_strides[k] == 0)
+                return fail(TVK_ERR_INVALID, std::string(who) + ": dst has a zero stride over extent " +
+                                                 std::to_string(d->sizes[k]) + " (overlapping elements)");
+            idx[n++] = k;
+        }
+    std::stable_sort(idx, idx + n, [&](int x, int y) {
+        if (d->dst_strides[x] != d->dst_strides[y]) return d->dst_strides[x] < d->dst_strides[y];
+        return d->src_strides[x] < d->src_strides[y];
+    });
+    Shape& sh = pl.sh;
+    sh.nd = 0;
+    for (int q = 0; q < n; ++q) {
+        const int k = idx[q];
+        const int64_t sz = d->sizes[k], ss = d->src_strides[k], ds = d->dst_strides[k];
+        if (sh.nd > 0) {
+            const int l = sh.nd - 1;
+            if (ds == sh.ds[l] * sh.size[l] && ss == sh.ss[l] * sh.size[l]) {
+                sh.size[l] *= sz;
+                continue;
+            }
+        }
+        sh.size[sh.nd] = sz;
+        sh.ss[sh.nd] = ss;
+        sh.ds[sh.nd] = ds;
+        ++sh.nd;
+    }
+    if (sh.nd == 0) {   // one element
+        sh.nd = 1;
+        sh.size[0] = 1;
+        sh.ss[0] = 1;
+        sh.ds[0] = 1;
+    }
+    const bool same = d->src_dtype == d->dst_dtype && d->src_dtype != TVK_BOOL;
+    if (sh.nd == 1 && sh.ss[0] == 1 && sh.ds[0] == 1) {
+        pl.kind = same ? PK_MEMCPY : PK_CAST_CONTIG;
+        return TVK_OK;
+    }
+    pl.kind = PK_STRIDED;
+    if (sh.ds[0] == 1 && sh.ss[0] != 1 && sh.size[0] >= 8) {
+        for (int k = 1; k < sh.nd; ++k)
+            if (sh.ss[k] == 1 && sh.size[k] >= 8) {
+                pl.kind = PK_TRANSPOSE;
+                pl.j = k;
+                break;
+            }
+    }
+    return TVK_OK;
+}
+
+const char* plan_name(PlanKind k) {
+    switch (k) {
+        case PK_NONE: return "none";
+        case PK_MEMCPY: return "memcpy";
+        case PK_CAST_CONTIG: return "cast_contig";
+        case PK_TRANSPOSE: return "transpose";
+        default: return "strided";
+    }
+}
+
+unsigned grid_for(int64_t items) {
+    const int64_t blocks = (items + 255) / 256;
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(blocks, 65536));
+}
+
+// the raw-bits stand-in of a same-dtype copy: an integer type of the element's size
+int raw_dtype(int dt) {
+    switch (dtype_size(dt)) {
+        case 8: return TVK_I64;
+        case 4: return TVK_I32;
+        case 2: return TVK_I16;
+        default: return TVK_U8;
+    }
+}
+
+template <int S, int D>
+void launch_cast_contig_t(const char* s, char* d, int64_t n, hipStream_t st) {
+    constexpr int SB = S == TVK_F64 ? 8 : S == TVK_F32 ? 4 : 2;
+    constexpr int DB = D == TVK_F64 ? 8 : D == TVK_F32 ? 4 : 2;
+    const bool vec = reinterpret_cast<uintptr_t>(s) % (SB * 8) == 0 && reinterpret_cast<uintptr_t>(d) % (DB * 8) == 0;
+    const unsigned g = grid_for((n + 7) / 8);
+    if (vec) hipLaunchKernelGGL((cast_contig_kernel<S, D, SB, DB, true>), dim3(g), dim3(256), 0, st, s, d, n, S, D);
+    else hipLaunchKernelGGL((cast_contig_kernel<S, D, SB, DB, false>), dim3(g), dim3(256), 0, st, s, d, n, S, D);
+}
+
+template <int S>
+bool launch_cast_contig_s(int ddt, const char* s, char* d, int64_t n, hipStream_t st) {
+    switch (ddt) {
+        case TVK_F32: launch_cast_contig_t<S, TVK_F32>(s, d, n, st); return true;
+        case TVK_F16: launch_cast_contig_t<S, TVK_F16>(s, d, n, st); return true;
+        case TVK_BF16: launch_cast_contig_t<S, TVK_BF16>(s, d, n, st); return true;
+        case TVK_F64: launch_cast_contig_t<S, TVK_F64>(s, d, n, st); return true;
+        default: return false;
+    }
+}
+
+void launch_cast_contig(int sdt, int ddt, const char* s, char* d, int64_t n, hipStream_t st) {
+    bool done = false;
+    switch (sdt) {
+        case TVK_F32: done = launch_cast_contig_s<TVK_F32>(ddt, s, d, n, st); break;
+        case TVK_F16: done = launch_cast_contig_s<TVK_F16>(ddt, s, d, n, st); break;
+        case TVK_BF16: done = launch_cast_contig_s<TVK_BF16>(ddt, s, d, n, st); break;
+        case TVK_F64: done = launch_cast_contig_s<TVK_F64>(ddt, s, d, n, st); break;
+        default: break;
+    }
+    if (!done)
+        hipLaunchKernelGGL(cast_contig_dyn_kernel, dim3(grid_for(n)), dim3(256), 0, st, s, d, n, sdt, ddt,
+                           (int)dtype_size(sdt), (int)dtype_size(ddt));
+}
+
+void launch_strided(const Plan& pl, int sdt, int ddt, const void* src, void* dst, hipStream_t st) {
+    StridedArgs a{};
+    a.src = static_cast<const char*>(src);
+    a.dst = static_cast<char*>(dst);
+    const bool same = sdt == ddt && sdt != TVK_BOOL;
+    a.sdt = same ? raw_dtype(sdt) : sdt;
+    a.ddt = same ? raw_dtype(ddt) : ddt;
+    a.ss_bytes = (int)dtype_size(sdt);
+    a.ds_bytes = (int)dtype_size(ddt);
+    a.nd = pl.sh.nd;
+    a.numel = pl.numel;
+    bool idx32 = pl.numel <= 0xffffffffLL;
+    for (int k = 0; k < a.nd; ++k) {
+        a.size[k] = pl.sh.size[k];
+        a.ss[k] = pl.sh.ss[k];
+        a.ds[k] = pl.sh.ds[k];
+        if (idx32) a.div[k] = make_div((uint32_t)pl.sh.size[k]);
+    }
+    const dim3 g(grid_for(pl.numel)), b(256);
+#define TVK_STRIDED(S, D)                                                                            \
+    do {                                                                                            \
+        if (idx32) hipLaunchKernelGGL((copy_strided_kernel<S, D, true>), g, b, 0, st, a);          \
+        else hipLaunchKernelGGL((copy_strided_kernel<S, D, false>), g, b, 0, st, a);               \
+    } while (0)
+    if (same) {
+        switch (a.sdt) {
+            case TVK_I64: TVK_STRIDED(TVK_I64, TVK_I64); break;
+            case TVK_I32: TVK_STRIDED(TVK_I32, TVK_I32); break;
+            case TVK_I16: TVK_STRIDED(TVK_I16, TVK_I16); break;
+            default: TVK_STRIDED(TVK_U8, TVK_U8); break;
+        }
+    } else {
+        TVK_STRIDED(DYN, DYN);
+    }
+#undef TVK_STRIDED
+}
+
+void launch_transpose(const Plan& pl, int sdt, int ddt, const void* src, void* dst, hipStream_t st) {
+    TransposeArgs a{};
+    a.src = static_cast<const char*>(src);
+    a.dst = static_cast<char*>(dst);
+    const bool same = sdt == ddt && sdt != TVK_BOOL;
+    a.sdt = same ? raw_dtype(sdt) : sdt;
+    a.ddt = same ? raw_dtype(ddt) : ddt;
+    a.sb = (int)dtype_size(sdt);
+    a.db = (int)dtype_size(ddt);
+    const Shape& sh = pl.sh;
+    a.n0 = sh.size[0];
+    a.nj = sh.size[pl.j];
+    a.ss0 = sh.ss[0];
+    a.dsj = sh.ds[pl.j];
+    a.tiles0 = (a.n0 + TT - 1) / TT;
+    a.tilesj = (a.nj + TT - 1) / TT;
+    a.nb = 0;
+    int64_t blocks = a.tiles0 * a.tilesj;
+    for (int k = 1; k < sh.nd; ++k) {
+        if (k == pl.j) continue;
+        a.bsize[a.nb] = sh.size[k];
+        a.bss[a.nb] = sh.ss[k];
+        a.bds[a.nb] = sh.ds[k];
+        ++a.nb;
+        blocks *= sh.size[k];
+    }
+    const dim3 g((unsigned)blocks), b(256);
+#define TVK_TR(S, D, W) hipLaunchKernelGGL((copy_transpose_kernel<S, D, W>), g, b, 0, st, a)
+    if (same) {
+        switch (a.sdt) {
+            case TVK_I64: TVK_TR(TVK_I64, TVK_I64, uint64_t); break;
+            case TVK_I32: TVK_TR(TVK_I32, TVK_I32, uint32_t); break;
+            case TVK_I16: TVK_TR(TVK_I16, TVK_I16, uint32_t); break;
+            default: TVK_TR(TVK_U8, TVK_U8, uint32_t); break;
+        }
+    } else if (sdt == TVK_F32 && ddt == TVK_F16) TVK_TR(TVK_F32, TVK_F16, uint32_t);
+    else if (sdt == TVK_F32 && ddt == TVK_BF16) TVK_TR(TVK_F32, TVK_BF16, uint32_t);
+    else if (sdt == TVK_F16 && ddt == TVK_F32) TVK_TR(TVK_F16, TVK_F32, uint32_t);
+    else if (sdt == TVK_BF16 && ddt == TVK_F32) TVK_TR(TVK_BF16, TVK_F32, uint32_t);
+    else TVK_TR(DYN, DYN, uint64_t);
+#undef TVK_TR
+}
+
+// ---------------------------------------------------------------------------
+// fill
+// ---------------------------------------------------------------------------
+
+// Dense fill: 16-byte stores of the repeated pattern; the elements before the
+// first 16-byte boundary and after the last are stored one by one.
+template <typename E>
+__global__ __launch_bounds__(256) void fill_contig_kernel(E* dst, int64_t n, int64_t head, E v) {
+    constexpr int PER = 16 / sizeof(E);
+    const int64_t step = (int64_t)gridDim.x * 256;
+    const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (tid < head && tid < n) dst[tid] = v;
+    const int64_t body = (n - head) / PER;
+    struct alignas(16) V16 { E e[PER]; };
+    V16 vv;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) vv.e[i] = v;
+    V16* vd = reinterpret_cast<V16*>(dst + head);
+    for (int64_t i = tid; i < body; i += step) vd[i] = vv;
+    const int64_t tail0 = head + body * PER;
+    if (tail0 + tid < n) dst[tail0 + tid] = v;
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void fill_strided_kernel(char* dst, int nd, int64_t numel, StridedArgs p, E v) {
+    const int64_t step = (int64_t)gridDim.x * 256;
+    for (int64_t li = (int64_t)blockIdx.x * 256 + threadIdx.x; li < numel; li += step) {
+        int64_t rem = li, off = 0;
+#pragma unroll 1
+        for (int k = 0; k < nd - 1; ++k) {
+            const int64_t q = rem / p.size[k];
+            off += (rem - q * p.size[k]) * p.ds[k];
+            rem = q;
+        }
+        off += rem * p.ds[nd - 1];
+        reinterpret_cast<E*>(dst)[off] = v;
+    }
+}
+
+template <typename E>
+void launch_fill(const Plan& pl, void* dst, uint64_t pattern, hipStream_t st) {
+    E v;
+    std::memcpy(&v, &pattern, sizeof(E));
+    if (pl.sh.nd == 1 && pl.sh.ds[0] == 1) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(dst);
+        int64_t head = (int64_t)(((16 - a % 16) % 16) / sizeof(E));
+        if (a % sizeof(E) != 0) head = pl.numel;   // misaligned elements: the head covers everything
+        if (head > pl.numel) head = pl.numel;
+        const int64_t threads = std::max<int64_t>((pl.numel - head) / (16 / sizeof(E)), std::max<int64_t>(head, 16));
+        if (head > 256 * 65536LL) {
+            // element-wise: one element per thread in a grid-stride loop
+            StridedArgs p{};
+            p.size[0] = pl.numel;
+            p.ds[0] = 1;
+            hipLaunchKernelGGL(fill_strided_kernel<E>, dim3(grid_for(pl.numel)), dim3(256), 0, st,
+                               static_cast<char*>(dst), 1, pl.numel, p, v);
+            return;
+        }
+        hipLaunchKernelGGL(fill_contig_kernel<E>, dim3(grid_for(threads)), dim3(256), 0, st, static_cast<E*>(dst), pl.numel,
+                           head, v);
+        return;
+    }
+    StridedArgs p{};
+    for (int k = 0; k < pl.sh.nd; ++k) {
+        p.size[k] = pl.sh.size[k];
+        p.ds[k] = pl.sh.ds[k];
+    }
+    hipLaunchKernelGGL(fill_strided_kernel<E>, dim3(grid_for(pl.numel)), dim3(256), 0, st, static_cast<char*>(dst),
+                       pl.sh.nd, pl.numel, p, v);
+}
+
+}  // namespace
+}  // namespace tvk
+
+using namespace tvk;
+
+extern "C" tvk_status tvk_fill(const tvk_fill_desc* desc) {
+    if (!desc) return fail(TVK_ERR_INVALID, "tvk_fill: desc is NULL");
+    const int es = desc->elem_size;
+    if (es != 1 && es != 2 && es != 4 && es != 8)
+        return fail(TVK_ERR_INVALID, "tvk_fill: elem_size must be 1, 2, 4 or 8");
+    // the destination's dimensions merge as a same-dtype copy's would
+    tvk_copy_desc c;
+    std::memset(&c, 0, sizeof(c));
+    c.src_dtype = c.dst_dtype = es == 8 ? TVK_I64 : es == 4 ? TVK_I32 : es == 2 ? TVK_I16 : TVK_U8;
+    c.ndim = desc->ndim;
+    for (int k = 0; k < desc->ndim && k < kMaxDims; ++k) {
+        c.sizes[k] = desc->sizes[k];
+        c.dst_strides[k] = desc->dst_strides[k];
+        c.src_strides[k] = desc->dst_strides[k];
+    }
+    c.src = desc->dst;
+    c.dst = desc->dst;
+    Plan pl;
+    tvk_status st = make_plan(&c, pl, "tvk_fill");
+    if (st != TVK_OK) return st;
+    if (pl.kind == PK_NONE) return TVK_OK;
+    const hipStream_t s = resolve_stream(desc->stream);
+    switch (es) {
+        case 1: launch_fill<uint8_t>(pl, desc->dst, desc->pattern, s); break;
+        case 2: launch_fill<uint16_t>(pl, desc->dst, desc->pattern, s); break;
+        case 4: launch_fill<uint32_t>(pl, desc->dst, desc->pattern, s); break;
+        default: launch_fill<uint64_t>(pl, desc->dst, desc->pattern, s); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_fill: launch failed: ") + hipGetErrorString(e));
+    return TVK_OK;
+}
+
+extern "C" tvk_status tvk_copy_plan(const tvk_copy_desc* desc, char* name, size_t name_len) {
+    Plan pl;
+    tvk_status st = make_plan(desc, pl, "tvk_copy_plan");
+    if (st != TVK_OK) return st;
+    if (!name || name_len == 0) return fail(TVK_ERR_INVALID, "tvk_copy_plan: name buffer is empty");
+    std::strncpy(name, plan_name(pl.kind), name_len - 1);
+    name[name_len - 1] = '\0';
+    return TVK_OK;
+}
+
+extern "C" tvk_status tvk_copy(const tvk_copy_desc* desc) {
+    Plan pl;
+    tvk_status st = make_plan(desc, pl, "tvk_copy");
+    if (st != TVK_OK) return st;
+    if (pl.kind == PK_NONE) return TVK_OK;
+    // grid x of the transpose kernel is one block per tile and batch index
+    if (pl.kind == PK_TRANSPOSE) {
+        const Shape& sh = pl.sh;
+        int64_t blocks = ((sh.size[0] + TT - 1) / TT) * ((sh.size[pl.j] + TT - 1) / TT);
+        for (int k = 1; k < sh.nd; ++k)
+            if (k != pl.j) blocks *= sh.size[k];
+        if (blocks > 0x7fffffffLL) pl.kind = PK_STRIDED;
+    }
+    const hipStream_t s = resolve_stream(desc->stream);
+    const int sdt = desc->src_dtype, ddt = desc->dst_dtype;
+    switch (pl.kind) {
+        case PK_MEMCPY:
+            TVK_HIP_CHECK(hipMemcpyAsync(desc->dst, desc->src, (size_t)pl.numel * dtype_size(sdt), hipMemcpyDeviceToDevice, s));
+            return TVK_OK;
+        case PK_CAST_CONTIG:
+            launch_cast_contig(sdt, ddt, static_cast<const char*>(desc->src), static_cast<char*>(desc->dst), pl.numel, s);
+            break;
+        case PK_TRANSPOSE:
+            launch_transpose(pl, sdt, ddt, desc->src, desc->dst, s);
+            break;
+        default:
+            launch_strided(pl, sdt, ddt, desc->src, desc->dst, s);
+            break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_copy: launch failed: ") + hipGetErrorString(e));
+    return TVK_OK;
+}

@@ -33,7 +33,14 @@ hipStream_t device_stream(int device);
 // A NULL stream handle is HIP's default (null) stream, as in every HIP library.
 inline hipStream_t resolve_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-inline size_t dtype_size(int32_t dt) { return dt == TVK_F32 ? 4 : 2; }
+__host__ __device__ constexpr size_t dtype_size(int32_t dt) {
+    switch (dt) {
+        case TVK_F64: case TVK_I64: return 8;
+        case TVK_F32: case TVK_I32: return 4;
+        case TVK_F16: case TVK_BF16: case TVK_I16: return 2;
+        default: return 1;   // I8, U8, BOOL
+    }
+}
 
 typedef _Float16 half_t;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
