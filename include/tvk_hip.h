@@ -200,6 +200,66 @@ typedef struct {
 tvk_status tvk_fill(const tvk_fill_desc* desc);
 
 /* ------------------------------------------------------------------------- */
+/* Reductions and element-wise arithmetic on both sides of the contractions   */
+/* ------------------------------------------------------------------------- */
+
+/* dst = sum of src over the dimensions whose bit is set in reduce_mask.
+ * dst is indexed by the same dimensions as src: its strides for summed
+ * dimensions are ignored (keepdim or squeezed views are both expressible).
+ * Element types: src F32/F16/BF16/F64/I64/I32/I16/I8/U8/BOOL; dst F32, F16,
+ * BF16, F64 or I64. The accumulator is the reference's
+ * reduce_accumulate_dtype (src/api/ops/helpers.h:476-480): float32 when dst
+ * is F16/BF16, else dst's own type; each source element is converted to it
+ * first (sum_accumulated, src/api/ops/reduce.cpp:265-273), the total is
+ * rounded once to dst. An empty sum is 0. The order of the additions is fixed
+ * (the same bits on every run); it is not the reference shader's order, which
+ * its driver decides. Replaces sum / sum.dim_IntList
+ * (src/api/ops/reduce.cpp:276-291,750-751). */
+typedef struct {
+    int32_t src_dtype;
+    int32_t dst_dtype;
+    int32_t ndim;           /* 0 .. TVK_COPY_MAX_DIMS */
+    uint32_t reduce_mask;   /* bit d: sum over dimension d */
+    int64_t sizes[TVK_COPY_MAX_DIMS];
+    const void* src; int64_t src_strides[TVK_COPY_MAX_DIMS];
+    void* dst; int64_t dst_strides[TVK_COPY_MAX_DIMS];
+    void* stream;
+} tvk_reduce_desc;
+
+tvk_status tvk_reduce_sum(const tvk_reduce_desc* desc);
+
+typedef enum {
+    TVK_BIN_ADD = 0,        /* out = a + alpha*b */
+    TVK_BIN_SUB = 1,        /* out = a - alpha*b */
+    TVK_BIN_MUL = 2         /* out = a * b (alpha unused) */
+} tvk_binary_op;
+
+/* Element-wise out = op(a, b) over `sizes`, every operand strided (zero
+ * strides broadcast a and b). One dtype for all three: F32, F16, BF16, F64,
+ * I64, I32, I16, I8, U8. As the reference's binary shader
+ * (src/shaders/ops/binary.slang:39-55): alpha is converted to the dtype;
+ * with alpha != 1, add/sub compute T(a op T(alpha*b)), otherwise T(a op b);
+ * every operation rounds to the dtype (float16/bfloat16 compute in float32
+ * and round after each operation, dtype.slang:911-913), float32 products are
+ * not fused into the add. out may alias a or b exactly (in-place ops), not
+ * partly. Replaces add/sub/mul (.Tensor, _.Tensor, .out;
+ * src/api/ops/binary.cpp:269-300,1090-1118). */
+typedef struct {
+    int32_t op;             /* tvk_binary_op */
+    int32_t dtype;
+    int32_t ndim;           /* 0 .. TVK_COPY_MAX_DIMS */
+    int32_t reserved;       /* must be 0 */
+    int64_t sizes[TVK_COPY_MAX_DIMS];
+    const void* a; int64_t a_strides[TVK_COPY_MAX_DIMS];
+    const void* b; int64_t b_strides[TVK_COPY_MAX_DIMS];
+    void* out; int64_t out_strides[TVK_COPY_MAX_DIMS];
+    double alpha;
+    void* stream;
+} tvk_binary_desc;
+
+tvk_status tvk_binary(const tvk_binary_desc* desc);
+
+/* ------------------------------------------------------------------------- */
 /* Compute: batched strided GEMM with fused epilogue                          */
 /* ------------------------------------------------------------------------- */
 

@@ -114,6 +114,63 @@ def cast(src: np.ndarray, sdt: int, ddt: int) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# element-wise add / sub / mul of tvk_binary
+# ---------------------------------------------------------------------------
+
+BIN_ADD, BIN_SUB, BIN_MUL = 0, 1, 2
+_NP_INT = {I64: np.int64, I32: np.int32, I16: np.int16, I8: np.int8, U8: np.uint8}
+
+
+def _round_to(x32: np.ndarray, dt: int) -> np.ndarray:
+    """float32 values rounded to dt, returned as float32 values."""
+    if dt == F32:
+        return x32.astype(np.float32)
+    if dt == F16:
+        return x32.astype(np.float32).astype(np.float16).astype(np.float32)
+    return bf16_bits_to_f32(f32_to_bf16_bits(x32))
+
+
+def binary(a: np.ndarray, b: np.ndarray, dt: int, op: int, alpha: float = 1.0) -> np.ndarray:
+    """AddOp / SubOp / MulOp of the reference's binary shader in dtype dt
+    (src/shaders/ops/binary.slang:39-55): alpha converted to dt; with
+    alpha != 1, T(a op T(alpha*b)); float16/bfloat16 compute each operation
+    in float32 and round back (src/shaders/core/dtype.slang:911-913); float32
+    and float64 round every operation (no fused multiply-add); integers wrap.
+    a, b: storage arrays (uint16 patterns for float16/bfloat16), broadcast."""
+    a, b = np.broadcast_arrays(np.asarray(a, dtype=STORAGE[dt]), np.asarray(b, dtype=STORAGE[dt]))
+    has_alpha = op != BIN_MUL and alpha != 1.0
+    if dt in _NP_INT:
+        t = _NP_INT[dt]
+        with np.errstate(over="ignore"):
+            a64, b64 = a.astype(np.int64).astype(np.uint64), b.astype(np.int64).astype(np.uint64)
+            al = np.uint64(np.int64(int(alpha)).astype(np.uint64))
+            if op == BIN_MUL:
+                r = a64 * b64
+            else:
+                tb = al * b64 if has_alpha else b64
+                r = a64 + tb if op == BIN_ADD else a64 - tb
+        return r.astype(np.int64).astype(t)
+    if dt == F64:
+        a64, b64, al = a.astype(np.float64), b.astype(np.float64), np.float64(alpha)
+        if op == BIN_MUL:
+            return a64 * b64
+        t = al * b64 if has_alpha else b64
+        return a64 + t if op == BIN_ADD else a64 - t
+    fa, fb = to_f32(a, dt), to_f32(b, dt)
+    al = _round_to(np.array([alpha], dtype=np.float32), dt)[0]
+    if op == BIN_MUL:
+        r = _round_to(fa * fb, dt)
+    else:
+        t = _round_to(al * fb, dt) if has_alpha else fb
+        r = _round_to(fa + t if op == BIN_ADD else fa - t, dt)
+    if dt == F32:
+        return r
+    if dt == F16:
+        return r.astype(np.float16).view(np.uint16)
+    return f32_to_bf16_bits(r)
+
+
+# ---------------------------------------------------------------------------
 # GEMM
 # ---------------------------------------------------------------------------
 

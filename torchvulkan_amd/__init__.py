@@ -133,12 +133,13 @@ def is_bf16_supported() -> bool:
 
 def manual_seed(seed) -> None:
     """Random numbers for vulkan tensors are drawn on the host (the CPU fallback
-    runs the random ops), so seeding seeds the host generator."""
-    torch.manual_seed(seed)
+    runs the random ops), so seeding seeds the host generator. torch.manual_seed
+    calls manual_seed_all of this module in turn, so neither calls back into it."""
+    torch.default_generator.manual_seed(int(seed))
 
 
 def manual_seed_all(seed) -> None:
-    torch.manual_seed(seed)
+    torch.default_generator.manual_seed(int(seed))
 
 
 def _is_in_bad_fork() -> bool:

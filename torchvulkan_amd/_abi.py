@@ -103,6 +103,37 @@ class FillDesc(C.Structure):
     ]
 
 
+class ReduceDesc(C.Structure):
+    _fields_ = [
+        ("src_dtype", C.c_int32),
+        ("dst_dtype", C.c_int32),
+        ("ndim", C.c_int32),
+        ("reduce_mask", C.c_uint32),
+        ("sizes", I64xD),
+        ("src", C.c_void_p), ("src_strides", I64xD),
+        ("dst", C.c_void_p), ("dst_strides", I64xD),
+        ("stream", C.c_void_p),
+    ]
+
+
+TVK_BIN_ADD, TVK_BIN_SUB, TVK_BIN_MUL = range(3)
+
+
+class BinaryDesc(C.Structure):
+    _fields_ = [
+        ("op", C.c_int32),
+        ("dtype", C.c_int32),
+        ("ndim", C.c_int32),
+        ("reserved", C.c_int32),
+        ("sizes", I64xD),
+        ("a", C.c_void_p), ("a_strides", I64xD),
+        ("b", C.c_void_p), ("b_strides", I64xD),
+        ("out", C.c_void_p), ("out_strides", I64xD),
+        ("alpha", C.c_double),
+        ("stream", C.c_void_p),
+    ]
+
+
 class DeviceProps(C.Structure):
     _fields_ = [
         ("name", C.c_char * 256),
@@ -153,6 +184,8 @@ def load() -> C.CDLL:
         lib.tvk_copy.argtypes = [C.POINTER(CopyDesc)]
         lib.tvk_copy_plan.argtypes = [C.POINTER(CopyDesc), C.c_char_p, C.c_size_t]
         lib.tvk_fill.argtypes = [C.POINTER(FillDesc)]
+        lib.tvk_reduce_sum.argtypes = [C.POINTER(ReduceDesc)]
+        lib.tvk_binary.argtypes = [C.POINTER(BinaryDesc)]
         for fn in _ALL_ENTRY_POINTS:
             getattr(lib, fn).restype = C.c_int if fn != "tvk_last_error" else C.c_char_p
         _lib = lib
@@ -166,7 +199,7 @@ _ALL_ENTRY_POINTS = (
     "tvk_memory_reserved", "tvk_reset_peak_memory_stats", "tvk_mem_get_info", "tvk_memcpy_h2d",
     "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan",
     "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad", "tvk_copy", "tvk_copy_plan",
-    "tvk_fill",
+    "tvk_fill", "tvk_reduce_sum", "tvk_binary",
 )
 
 
@@ -264,6 +297,57 @@ def fill(dst, value, stream=None) -> None:
     d.pattern = int.from_bytes(one.view(torch.uint8).numpy().tobytes(), "little")
     d.stream = stream
     check(load().tvk_fill(C.byref(d)))
+
+
+def _stream_of(t, stream):
+    import torch
+
+    if stream is None and t.is_cuda:
+        stream = torch.cuda.current_stream(t.device).cuda_stream
+    return stream
+
+
+def reduce_sum(src, dims, keepdim=False, out_dtype=None, stream=None):
+    """torch.sum(src, dims, keepdim, dtype=out_dtype) through tvk_reduce_sum (device tensors)."""
+    import torch
+
+    nd = src.dim()
+    dims = [d % nd for d in dims] if dims else list(range(nd))
+    out_dtype = out_dtype or src.dtype
+    shape = [1 if d in dims else src.shape[d] for d in range(nd)] if keepdim else \
+        [src.shape[d] for d in range(nd) if d not in dims]
+    out = torch.empty(shape, dtype=out_dtype, device=src.device)
+    d = ReduceDesc()
+    d.src_dtype = copy_dtype_code(src.dtype)
+    d.dst_dtype = copy_dtype_code(out_dtype)
+    d.ndim = nd
+    d.reduce_mask = sum(1 << k for k in dims)
+    d.sizes = I64xD(*src.shape)
+    d.src = src.data_ptr() if src.numel() else None
+    d.src_strides = I64xD(*src.stride())
+    view = out.view([1 if k in dims else src.shape[k] for k in range(nd)]) if out.numel() else out
+    d.dst = out.data_ptr() if out.numel() else None
+    d.dst_strides = I64xD(*[0 if k in dims else (view.stride(k) if out.numel() else 0) for k in range(nd)])
+    d.stream = _stream_of(src, stream)
+    check(load().tvk_reduce_sum(C.byref(d)))
+    return out
+
+
+def binary(a, b, out, op, alpha=1.0, stream=None) -> None:
+    """out = op(a, b) through tvk_binary; a and b broadcast to out's shape (one dtype for all three)."""
+    a, b = a.expand(out.shape), b.expand(out.shape)
+    d = BinaryDesc()
+    d.op = op
+    d.dtype = copy_dtype_code(out.dtype)
+    d.ndim = out.dim()
+    d.reserved = 0
+    d.sizes = I64xD(*out.shape)
+    d.a, d.a_strides = a.data_ptr(), I64xD(*a.stride())
+    d.b, d.b_strides = b.data_ptr(), I64xD(*b.stride())
+    d.out, d.out_strides = out.data_ptr(), I64xD(*out.stride())
+    d.alpha = float(alpha)
+    d.stream = _stream_of(out, stream)
+    check(load().tvk_binary(C.byref(d)))
 
 
 def _strides3(t) -> tuple[int, int, int]:

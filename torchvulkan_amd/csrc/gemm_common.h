@@ -149,11 +149,6 @@ __device__ inline u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, bool row_ok, int64_
     }
 }
 
-// Library-owned scratch of a device (defined in runtime.hip). Both grow on
-// demand; the counters are zero between calls (every kernel that increments
-// one resets it before it exits).
-void* device_workspace(int device, size_t bytes);
-uint32_t* device_counters(int device, size_t count);
 
 // Tile kernel with operands fetched straight into LDS (gemm_dma.hip).
 // dma_applies: the operands meet its alignment and K granularity; launch_dma

@@ -30,6 +30,12 @@ inline tvk_status fail(tvk_status code, const std::string& msg) {
 
 // Library stream of a device (created lazily); defined in runtime.hip.
 hipStream_t device_stream(int device);
+// Library-owned scratch of a device (defined in runtime.hip). Both grow on
+// demand; the counters are zero between calls (every kernel that increments
+// one resets it before it exits).
+void* device_workspace(int device, size_t bytes);
+uint32_t* device_counters(int device, size_t count);
+
 // A NULL stream handle is HIP's default (null) stream, as in every HIP library.
 inline hipStream_t resolve_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
