@@ -377,6 +377,9 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c5_baddbmm_pct_hbm"] = round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)
     del a, b, c, x1, x2, inp, cb
 
+    # ---- copies, casts, sums and adds on both sides of the contractions ----
+    out.update(run_memory_ops(torch, _abi, dev, stream, steps, warmup, g))
+
     # ---- C1 fp32 1024^3 ----------------------------------------------------
     a = torch.randn((1024, 1024), generator=g).to(dev)
     b = torch.randn((1024, 1024), generator=g).to(dev)
@@ -394,6 +397,66 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c1_fp32_tflops"] = round(2 * 1024 ** 3 / (ms * 1e-3) / 1e12, 2)
     out["c1_kernel"] = _abi.gemm_plan(a, b, c)
     return out
+
+
+def run_memory_ops(torch, _abi, dev, stream, steps, warmup, g):
+    """HBM-bound kernels next to the GEMMs: GB/s of algorithmic bytes (each
+    operand read once, the result written once) and the fraction of 8 TB/s.
+    Sizes are far above the 256 MB Infinity Cache where they can be."""
+    import ctypes as C
+
+    lib = _abi.load()
+    s = stream.cuda_stream
+    res = {}
+
+    def measure(name, call, nbytes):
+        ms, _ = timed(call, steps * 2, warmup, stream)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "GBps": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 2)}
+
+    def copy_call(src, dst):
+        d = _abi.make_copy_desc(src, dst, stream=s)
+        r = C.byref(d)
+        return (lambda: _abi.check(lib.tvk_copy(r))), d
+
+    n = 16384
+    w = torch.randn((n, n), generator=g).to(torch.float16).to(dev)               # 512 MiB
+    wt = torch.empty((n, n), dtype=torch.float16, device=dev)
+    f, keep = copy_call(w.t(), wt)
+    measure("copy_transpose_f16_16384sq", f, 2 * w.numel() * 2)
+    x32 = torch.randn((1 << 27,), generator=g).to(dev)                            # 512 MiB
+    x16 = torch.empty((1 << 27,), dtype=torch.float16, device=dev)
+    f, keep2 = copy_call(x32, x16)
+    measure("cast_f32_to_f16_128M", f, x32.numel() * 6)
+    a = torch.randn((256, 64, 56, 56), generator=g).to(torch.float16).to(dev)    # 98 MiB each way
+    cl = torch.empty_like(a, memory_format=torch.channels_last)
+    f, keep3 = copy_call(a, cl)
+    measure("nchw_to_nhwc_f16_256x64x56x56", f, 2 * a.numel() * 2)
+    del w, wt, x32, keep, keep2, keep3
+
+    dy = torch.randn((65536, 3072), generator=g).to(torch.float16).to(dev)       # 384 MiB
+    bgrad = torch.empty((3072,), dtype=torch.float16, device=dev)
+    rd = _abi.ReduceDesc()
+    rd.src_dtype, rd.dst_dtype, rd.ndim, rd.reduce_mask = _abi.TVK_F16, _abi.TVK_F16, 2, 1
+    rd.sizes = _abi.I64xD(*dy.shape)
+    rd.src, rd.src_strides = dy.data_ptr(), _abi.I64xD(*dy.stride())
+    rd.dst, rd.dst_strides = bgrad.data_ptr(), _abi.I64xD(0, 1)
+    rd.stream = s
+    rr = C.byref(rd)
+    measure("sum_dim0_f16_65536x3072", lambda: _abi.check(lib.tvk_reduce_sum(rr)), dy.numel() * 2)
+    p_ = torch.randn((1 << 27,), generator=g).to(torch.float16).to(dev)
+    bd = _abi.BinaryDesc()
+    bd.op, bd.dtype, bd.ndim, bd.reserved = _abi.TVK_BIN_ADD, _abi.TVK_F16, 1, 0
+    bd.sizes = _abi.I64xD(p_.numel())
+    bd.a, bd.a_strides = p_.data_ptr(), _abi.I64xD(1)
+    bd.b, bd.b_strides = x16.data_ptr(), _abi.I64xD(1)
+    bd.out, bd.out_strides = p_.data_ptr(), _abi.I64xD(1)
+    bd.alpha, bd.stream = -0.01, s
+    br = C.byref(bd)
+    measure("add_inplace_alpha_f16_128M", lambda: _abi.check(lib.tvk_binary(br)), p_.numel() * 6)
+    del dy, p_, x16
+    torch.cuda.empty_cache()
+    return {"memory_ops": res}
 
 
 def cpu_baseline():

@@ -211,3 +211,29 @@ def test_fill(gpu, dtype, value):
     ref = torch.zeros((30, 40), dtype=dtype)
     ref[::3, 1::2] = value
     assert torch.equal(storage_view(m.cpu()), storage_view(ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.float64, torch.uint8, torch.bfloat16])
+def test_transpose_aligned_vector_path(gpu, dtype):
+    # 16-byte aligned rows on both sides: the vectorized tile kernel, including chunks cut by the matrix edge
+    g = torch.Generator().manual_seed(30)
+    big = (torch.randn((200, 144), generator=g) * 50).to(dtype).to(DEV)
+    for cols in (144, 132, 129):
+        src = big[:, :cols]
+        dst = torch.empty((cols, 200), dtype=dtype, device=DEV)
+        check_like_torch(src.t(), dst, "transpose")
+    x = torch.randn((4, 32, 8, 16), generator=g).to(dtype).to(DEV)
+    cl = torch.empty_like(x, memory_format=torch.channels_last)
+    check_like_torch(x, cl, "transpose")
+    back = torch.empty_like(x)
+    check_like_torch(cl, back, "transpose")
+
+
+@pytest.mark.parametrize("sdt,ddt", [(orc.F32, orc.F16), (orc.F16, orc.F32), (orc.BF16, orc.F32), (orc.F32, orc.BF16)])
+def test_transpose_cast_vector_path(gpu, sdt, ddt):
+    src_cpu = source_values(sdt, 96 * 256, 40 + sdt).view(96, 256)
+    src = src_cpu.to(DEV)
+    dst = torch.empty((256, 96), dtype=TORCH_OF[ddt], device=DEV)
+    assert run_copy(src.t(), dst) == "transpose"
+    want = orc.cast(storage_np(src_cpu.t()), sdt, ddt)
+    assert_bits_equal(storage_np(dst).reshape(-1), want.reshape(-1), ddt, "vector transpose cast")

@@ -157,8 +157,8 @@ def test_dma_kernel_column_edge_inside_a_chunk(gpu, dtype):
 
 @pytest.mark.parametrize("dtype", F16_TYPES)
 def test_dma_kernel_batched(gpu, dtype):
-    a = randint((3, 1024, 64), dtype, 18)
-    b = randint((3, 64, 4096), dtype, 19)
+    a = randint((3, 1024, 320), dtype, 18)
+    b = randint((3, 320, 4096), dtype, 19)
     got, plan = run(gpu, a, b, (3, 1024, 4096), dtype)
     assert plan == "gemm16_dma_256x256"
     assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
@@ -167,7 +167,7 @@ def test_dma_kernel_batched(gpu, dtype):
 @pytest.mark.parametrize("dtype", F16_TYPES)
 @pytest.mark.parametrize("act", [orc.ACT_NONE, orc.ACT_RELU, orc.ACT_GELU])
 def test_dma_kernel_epilogue_sampled_rows(gpu, dtype, act):
-    M, N, K = 4096, 3072, 256
+    M, N, K = 4096, 3072, 320
     a = randn((M, K), dtype, 20)
     b = randn((N, K), dtype, 21).t()
     bias = randn((N,), dtype, 22)

@@ -186,6 +186,80 @@ __global__ __launch_bounds__(256) void copy_transpose_kernel(TransposeArgs p) {
     }
 }
 
+// The same tile with 16-byte accesses on both sides: a thread loads
+// VS = 16/sb consecutive source elements along j and stores VD = 16/db
+// consecutive destination elements along 0. Chunks that cross the end of the
+// matrix fall back to one element at a time. LDS holds one converted element
+// per Word at [a][b] with a row pitch of TT+1 words, so both phases touch 64
+// distinct banks per wave. Requires 16-byte aligned chunk starts (bases and
+// the strides ss0*sb, dsj*db multiples of 16).
+template <int SDT, int DDT, typename Word>
+__global__ __launch_bounds__(256) void copy_transpose_vec_kernel(TransposeArgs p) {
+    constexpr int SB = (int)dtype_size(SDT), DB = (int)dtype_size(DDT);
+    constexpr int VS = 16 / SB, VD = 16 / DB;
+    constexpr int CS = TT / VS, CD = TT / VD;   // chunks per tile row, load / store side
+    __shared__ Word tile[TT][TT + 1];
+    int64_t bid = blockIdx.x;
+    const int64_t t0 = bid % p.tiles0;
+    bid /= p.tiles0;
+    const int64_t tj = bid % p.tilesj;
+    int64_t rest = bid / p.tilesj;
+    int64_t so = 0, dof = 0;
+    for (int k = 0; k < p.nb; ++k) {
+        const int64_t c = rest % p.bsize[k];
+        rest /= p.bsize[k];
+        so += c * p.bss[k];
+        dof += c * p.bds[k];
+    }
+    const int64_t a0 = t0 * TT, b0 = tj * TT;
+    const int tid = threadIdx.x;
+    // load: thread -> (row a, chunk of VS along b); consecutive threads on consecutive chunks
+#pragma unroll
+    for (int q = tid; q < TT * CS; q += 256) {
+        const int r = q / CS, cb = (q % CS) * VS;
+        const int64_t a = a0 + r, b = b0 + cb;
+        Word w[VS];
+        if (a < p.n0 && b + VS <= p.nj) {
+            struct alignas(16) V16 { char c[16]; };
+            const V16 v = *reinterpret_cast<const V16*>(p.src + (so + a * p.ss0 + b) * SB);
+#pragma unroll
+            for (int e = 0; e < VS; ++e) {
+                w[e] = 0;
+                convert(v.c + e * SB, SDT, reinterpret_cast<char*>(&w[e]), DDT);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < VS; ++e) {
+                w[e] = 0;
+                if (a < p.n0 && b + e < p.nj) convert(p.src + (so + a * p.ss0 + b + e) * SB, SDT, reinterpret_cast<char*>(&w[e]), DDT);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < VS; ++e) tile[r][cb + e] = w[e];
+    }
+    __syncthreads();
+    // store: thread -> (column b, chunk of VD along a); consecutive threads on consecutive chunks
+#pragma unroll
+    for (int q = tid; q < TT * CD; q += 256) {
+        const int r = q / CD, ca = (q % CD) * VD;
+        const int64_t b = b0 + r, a = a0 + ca;
+        if (b >= p.nj || a >= p.n0) continue;
+        char* dst = p.dst + (dof + a + b * p.dsj) * DB;
+        if (a + VD <= p.n0) {
+            struct alignas(16) V16 { char c[16]; };
+            V16 v;
+#pragma unroll
+            for (int e = 0; e < VD; ++e) {
+                const Word w = tile[ca + e][r];
+                __builtin_memcpy(v.c + e * DB, &w, DB);
+            }
+            *reinterpret_cast<V16*>(dst) = v;
+        } else {
+            for (int e = 0; a + e < p.n0; ++e) store_elem(dst + e * DB, tile[ca + e][r], DB);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // host plan
 // ---------------------------------------------------------------------------
@@ -401,6 +475,30 @@ void launch_transpose(const Plan& pl, int sdt, int ddt, const void* src, void* d
         blocks *= sh.size[k];
     }
     const dim3 g((unsigned)blocks), b(256);
+    // 16-byte chunk starts on both sides: aligned bases and row strides
+    auto a16 = [](uintptr_t v) { return v % 16 == 0; };
+    const bool vec = a16(reinterpret_cast<uintptr_t>(src)) && a16(reinterpret_cast<uintptr_t>(dst)) &&
+                     (a.ss0 * a.sb) % 16 == 0 && (a.dsj * a.db) % 16 == 0 && [&]() {
+                         for (int k = 0; k < a.nb; ++k)
+                             if ((a.bss[k] * a.sb) % 16 != 0 || (a.bds[k] * a.db) % 16 != 0) return false;
+                         return true;
+                     }();
+    if (vec) {
+#define TVK_TRV(S, D, W) hipLaunchKernelGGL((copy_transpose_vec_kernel<S, D, W>), g, b, 0, st, a)
+        if (same) {
+            switch (a.sdt) {
+                case TVK_I64: TVK_TRV(TVK_I64, TVK_I64, uint64_t); return;
+                case TVK_I32: TVK_TRV(TVK_I32, TVK_I32, uint32_t); return;
+                case TVK_I16: TVK_TRV(TVK_I16, TVK_I16, uint32_t); return;
+                default: TVK_TRV(TVK_U8, TVK_U8, uint32_t); return;
+            }
+        }
+        if (sdt == TVK_F32 && ddt == TVK_F16) { TVK_TRV(TVK_F32, TVK_F16, uint32_t); return; }
+        if (sdt == TVK_F32 && ddt == TVK_BF16) { TVK_TRV(TVK_F32, TVK_BF16, uint32_t); return; }
+        if (sdt == TVK_F16 && ddt == TVK_F32) { TVK_TRV(TVK_F16, TVK_F32, uint32_t); return; }
+        if (sdt == TVK_BF16 && ddt == TVK_F32) { TVK_TRV(TVK_BF16, TVK_F32, uint32_t); return; }
+#undef TVK_TRV
+    }
 #define TVK_TR(S, D, W) hipLaunchKernelGGL((copy_transpose_kernel<S, D, W>), g, b, 0, st, a)
     if (same) {
         switch (a.sdt) {

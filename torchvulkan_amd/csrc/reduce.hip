@@ -138,10 +138,10 @@ __device__ __forceinline__ int64_t red_offset(const RedArgs& p, int64_t r) {
 }
 
 // the result of output o (chunk z of `splits`) goes to the final output or
-// to the partial buffer laid out [o][z]
+// to the partial buffer laid out [z][o]
 template <typename Acc>
 __device__ __forceinline__ void put(const RedArgs& p, int64_t o, int64_t dof, int z, Acc v) {
-    if (p.ddt < 0) reinterpret_cast<Acc*>(p.dst)[o * p.splits + z] = v;
+    if (p.ddt < 0) reinterpret_cast<Acc*>(p.dst)[(int64_t)z * p.nout + o] = v;
     else store_acc<Acc>(p.dst + dof * p.db, p.ddt, v);
 }
 
@@ -184,14 +184,61 @@ __global__ __launch_bounds__(256) void reduce_col_kernel(RedArgs p) {
     }
 }
 
-// dst[o] = sum over z of part[o][z], in z order
+// Column mode with V = 16/sb consecutive outputs per thread along the
+// source's contiguous kept dimension: one 16-byte load per row and four rows
+// in flight per thread. Each output still adds its rows in order.
+template <typename Acc, int SDT>
+__global__ __launch_bounds__(256) void reduce_colv_kernel(RedArgs p) {
+    constexpr int SB = (int)dtype_size(SDT), V = 16 / SB;
+    struct alignas(16) V16 { char c[16]; };
+    const int z = blockIdx.y;
+    const int64_t r0 = (int64_t)z * p.chunk;
+    const int64_t r1 = r0 + p.chunk < p.nred ? r0 + p.chunk : p.nred;
+    const int64_t nvec = p.nout / V;
+    for (int64_t ov = (int64_t)blockIdx.x * 256 + threadIdx.x; ov < nvec; ov += (int64_t)gridDim.x * 256) {
+        const int64_t o = ov * V;
+        int64_t so, dof;
+        kept_offsets(p, o, so, dof);
+        Acc acc[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc[e] = 0;
+        int64_t r = r0;
+        for (; r + 4 <= r1; r += 4) {
+            V16 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const V16*>(p.src + (so + red_offset(p, r + u)) * SB);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int e = 0; e < V; ++e) acc[e] += load_acc<Acc>(v[u].c + e * SB, SDT);
+        }
+        for (; r < r1; ++r) {
+            const V16 v = *reinterpret_cast<const V16*>(p.src + (so + red_offset(p, r)) * SB);
+#pragma unroll
+            for (int e = 0; e < V; ++e) acc[e] += load_acc<Acc>(v.c + e * SB, SDT);
+        }
+#pragma unroll
+        for (int e = 0; e < V; ++e) put<Acc>(p, o + e, dof + e * p.kds[0], z, acc[e]);
+    }
+}
+
+// dst[o] = sum over z of part[z][o], in z order; neighbouring threads read
+// neighbouring partials, eight chunks in flight per thread
 template <typename Acc>
 __global__ __launch_bounds__(256) void reduce_fold_kernel(const Acc* part, RedArgs p) {
     for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < p.nout; o += (int64_t)gridDim.x * 256) {
         int64_t so, dof;
         kept_offsets(p, o, so, dof);
-        Acc v = part[o * p.splits];
-        for (int z = 1; z < p.splits; ++z) v += part[o * p.splits + z];
+        Acc v = part[o];
+        int z = 1;
+        for (; z + 8 <= p.splits; z += 8) {
+            Acc w[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[u] = part[(int64_t)(z + u) * p.nout + o];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += w[u];
+        }
+        for (; z < p.splits; ++z) v += part[(int64_t)z * p.nout + o];
         store_acc<Acc>(p.dst + dof * p.db, p.ddt, v);
     }
 }
@@ -209,13 +256,29 @@ unsigned blocks_for(int64_t n, int64_t per) {
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + per - 1) / per, 65535));
 }
 
+// column mode can take V = 16/sb outputs per thread: the source dtype is a
+// float one, the kept dimension 0 is the source's contiguous one with a
+// multiple of V elements, and every chunk start is 16-byte aligned
+bool colv_applies(const RedArgs& p) {
+    if (p.sdt != TVK_F32 && p.sdt != TVK_F16 && p.sdt != TVK_BF16) return false;
+    const int v = 16 / p.sb;
+    if (p.nk == 0 || p.kss[0] != 1 || p.ksize[0] % v != 0 || reinterpret_cast<uintptr_t>(p.src) % 16 != 0) return false;
+    for (int k = 1; k < p.nk; ++k)
+        if ((p.kss[k] * p.sb) % 16 != 0) return false;
+    for (int k = 0; k < p.nr; ++k)
+        if ((p.rss[k] * p.sb) % 16 != 0) return false;
+    return true;
+}
+
 template <typename Acc>
 tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
+    const bool colv = !row && colv_applies(p);
+    const int64_t per_thread = colv ? 16 / p.sb : 1;
     // split K when the outputs alone would leave the device short of blocks
-    const int64_t out_blocks = row ? p.nout : (p.nout + 255) / 256;
+    const int64_t out_blocks = row ? p.nout : (p.nout / per_thread + 255) / 256;
     int64_t splits = 1;
     if (out_blocks < 1024 && p.nred > 1) {
-        const int64_t min_chunk = row ? 4096 : 64;
+        const int64_t min_chunk = row ? 4096 : 256;
         splits = std::min<int64_t>((1024 + out_blocks - 1) / out_blocks, (p.nred + min_chunk - 1) / min_chunk);
         splits = std::max<int64_t>(1, std::min<int64_t>(splits, 65535));
     }
@@ -231,13 +294,17 @@ tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
         p.dst = reinterpret_cast<char*>(part);
         p.ddt = -1;
     }
-    const dim3 grid(row ? blocks_for(p.nout, 1) : blocks_for(p.nout, 256), (unsigned)splits);
+    const dim3 grid(row ? blocks_for(p.nout, 1) : blocks_for(p.nout / per_thread, 256), (unsigned)splits);
 #define TVK_RED(S)                                                                      \
     do {                                                                                \
         if (row) hipLaunchKernelGGL((reduce_row_kernel<Acc, S>), grid, dim3(256), 0, st, p); \
         else hipLaunchKernelGGL((reduce_col_kernel<Acc, S>), grid, dim3(256), 0, st, p);     \
     } while (0)
-    switch (p.sdt) {
+    if (colv) {
+        if (p.sdt == TVK_F32) hipLaunchKernelGGL((reduce_colv_kernel<Acc, TVK_F32>), grid, dim3(256), 0, st, p);
+        else if (p.sdt == TVK_F16) hipLaunchKernelGGL((reduce_colv_kernel<Acc, TVK_F16>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((reduce_colv_kernel<Acc, TVK_BF16>), grid, dim3(256), 0, st, p);
+    } else switch (p.sdt) {
         case TVK_F32: TVK_RED(TVK_F32); break;
         case TVK_F16: TVK_RED(TVK_F16); break;
         case TVK_BF16: TVK_RED(TVK_BF16); break;
