@@ -260,6 +260,42 @@ typedef struct {
 tvk_status tvk_binary(const tvk_binary_desc* desc);
 
 /* ------------------------------------------------------------------------- */
+/* Fused scaled dot-product attention (forward)                               */
+/* ------------------------------------------------------------------------- */
+
+/* out[b,h,i,:] = sum_j softmax_j(s[b,h,i,:]) * v[b,h/group,j,:] with
+ *   s[b,h,i,j] = scale * (q[b,h,i,:] . k[b,h/group,j,:]) + bias[b,h,i,j],
+ * s = -inf where `causal` and j > i (top-left aligned) or j >= len_kv;
+ * group = heads_q / heads_kv (grouped-query attention). A row with every
+ * key masked gives out = 0 and lse = +inf; otherwise
+ * lse[b,h,i] = max_j s + log(sum_j exp(s - max_j s)) (natural log, float32).
+ * Scores and the softmax are float32; the probabilities are rounded to the
+ * dtype before the product with v, as the reference's cooperative-matrix
+ * kernel stages them in the dtype (src/shaders/ops/attention_coop.slang;
+ * row semantics from chunked_forward, src/api/ops/attention.cpp:115-139).
+ * Supported: F16 and BF16; head_dim == head_dim_v in {64, 128}; q, k, v with
+ * unit stride along the head dimension and 16-byte aligned rows; bias in the
+ * dtype, any strides (zero strides broadcast). Other cases return
+ * TVK_ERR_UNSUPPORTED (the caller runs its decomposed path). Replaces
+ * fused_forward (src/api/ops/attention.cpp:434-500) behind
+ * _scaled_dot_product_fused_attention_overrideable (:697-719). */
+typedef struct {
+    int32_t dtype;
+    int32_t causal;
+    int64_t batch, heads_q, heads_kv, len_q, len_kv, head_dim, head_dim_v;
+    const void* q; int64_t q_stride[4];       /* [batch][head][row][dim], elements */
+    const void* k; int64_t k_stride[4];
+    const void* v; int64_t v_stride[4];
+    const void* bias; int64_t bias_stride[4]; /* NULL: none */
+    void* out; int64_t out_stride[4];
+    float* lse; int64_t lse_stride[3];        /* [batch][head][row] */
+    double scale;
+    void* stream;
+} tvk_attention_desc;
+
+tvk_status tvk_attention_fwd(const tvk_attention_desc* desc);
+
+/* ------------------------------------------------------------------------- */
 /* Compute: batched strided GEMM with fused epilogue                          */
 /* ------------------------------------------------------------------------- */
 

@@ -171,6 +171,42 @@ def binary(a: np.ndarray, b: np.ndarray, dt: int, op: int, alpha: float = 1.0) -
 
 
 # ---------------------------------------------------------------------------
+# scaled dot-product attention (float64 restatement)
+# ---------------------------------------------------------------------------
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, bias: np.ndarray | None = None, causal: bool = False,
+              scale: float | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """(out, lse) of the reference's attention rows in float64
+    (chunked_forward, src/api/ops/attention.cpp:115-139; scores per
+    chunk_scores, :101-113): s = scale*q.k (+ bias), -inf where causal and
+    key j > query i; a row with every key masked gives out 0 and lse +inf.
+    q [B,Hq,L,D], k [B,Hk,S,D], v [B,Hk,S,Dv] as float64 values; query head
+    h reads key/value head h // (Hq/Hk)."""
+    q, k, v = (np.asarray(t, dtype=np.float64) for t in (q, k, v))
+    B, Hq, L, D = q.shape
+    Hk, S = k.shape[1], k.shape[2]
+    g = Hq // Hk
+    scale = D ** -0.5 if scale is None else scale
+    kk = np.repeat(k, g, axis=1)
+    vv = np.repeat(v, g, axis=1)
+    s = np.einsum("bhld,bhsd->bhls", q, kk) * scale
+    if bias is not None:
+        s = s + np.broadcast_to(np.asarray(bias, dtype=np.float64), s.shape)
+    if causal:
+        s = np.where(np.arange(S)[None, :] > np.arange(L)[:, None], -np.inf, s)
+    mx = s.max(axis=-1, keepdims=True)
+    safe = np.where(np.isneginf(mx), 0.0, mx)
+    with np.errstate(invalid="ignore"):
+        p = np.exp(s - safe)
+    tot = p.sum(axis=-1, keepdims=True)
+    empty = tot == 0.0
+    out = np.einsum("bhls,bhsd->bhld", p, vv) / np.where(empty, 1.0, tot)
+    with np.errstate(divide="ignore"):
+        lse = np.where(empty, np.inf, safe + np.log(np.where(empty, 1.0, tot)))[..., 0]
+    return out, lse
+
+
+# ---------------------------------------------------------------------------
 # GEMM
 # ---------------------------------------------------------------------------
 

@@ -1,0 +1,111 @@
+"""tvk_attention_fwd on the GPU through the C ABI against the float64
+attention oracle, at the north_star tolerance for float16/bfloat16
+(5e-3*(|ref|+1) on out; lse within 1e-3*(|lse|+1)), and
+F.scaled_dot_product_attention on the vulkan device (forward and backward)
+against torch's CPU math attention in float64."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import oracle as orc
+from torchvulkan_amd import _abi
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def rand(shape, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+def f64(t):
+    return t.detach().cpu().double().numpy()
+
+
+def check(q, k, v, bias=None, causal=False, scale=None, what=""):
+    out, lse = _abi.attention_fwd(q.to(DEV), k.to(DEV), v.to(DEV), None if bias is None else bias.to(DEV), causal, scale)
+    torch.cuda.synchronize()
+    ro, rl = orc.attention(f64(q), f64(k), f64(v), None if bias is None else f64(bias), causal, scale)
+    go, gl = f64(out), out.new_zeros(0) if False else lse.cpu().double().numpy()
+    err = np.abs(go - ro) / (5e-3 * (np.abs(ro) + 1))
+    assert err.max() <= 1.0, f"{what}: out off by {err.max():.2f}x tolerance"
+    fin = np.isfinite(rl)
+    assert (np.isinf(gl) == ~fin).all(), f"{what}: +inf lse rows differ"
+    lerr = np.abs(gl[fin] - rl[fin]) / (1e-3 * (np.abs(rl[fin]) + 1))
+    assert lerr.size == 0 or lerr.max() <= 1.0, f"{what}: lse off by {lerr.max():.2f}x tolerance"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_transformer_shape(gpu, dtype, causal):
+    # the C3 attention at a reduced batch: 8 query heads over 2 kv heads, head_dim 64, seq 256
+    q, k, v = rand((2, 8, 256, 64), dtype, 1), rand((2, 2, 256, 64), dtype, 2), rand((2, 2, 256, 64), dtype, 3)
+    check(q, k, v, causal=causal, what=f"{dtype} causal={causal}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_ragged_lengths_and_head_dim_128(gpu, dtype):
+    q, k, v = rand((1, 4, 100, 128), dtype, 4), rand((1, 4, 301, 128), dtype, 5), rand((1, 4, 301, 128), dtype, 6)
+    check(q, k, v, what="L 100 S 301 D 128")
+    check(q, k, v, causal=True, what="causal L 100 S 301")
+    q2 = rand((1, 2, 300, 64), dtype, 7)
+    k2, v2 = rand((1, 2, 70, 64), dtype, 8), rand((1, 2, 70, 64), dtype, 9)
+    check(q2, k2, v2, causal=True, scale=0.2, what="causal L 300 > S 70")
+
+
+def test_bias_broadcast_and_masked_rows(gpu):
+    dtype = torch.float16
+    q, k, v = rand((2, 4, 64, 64), dtype, 10), rand((2, 4, 96, 64), dtype, 11), rand((2, 4, 96, 64), dtype, 12)
+    bias = rand((1, 4, 64, 96), dtype, 13)
+    check(q, k, v, bias=bias, what="bias broadcast over batch")
+    mask = torch.zeros((2, 1, 64, 96), dtype=dtype)
+    mask[:, :, 5] = float("-inf")            # row 5 attends to nothing: out 0, lse +inf
+    mask[:, :, 9, 1:] = float("-inf")        # row 9 attends to key 0 only
+    check(q, k, v, bias=mask, what="masked rows")
+
+
+def test_head_strided_views(gpu):
+    # q, k, v as [B, L, H, D] underneath (the projection output split into heads)
+    dtype = torch.float16
+    x = rand((2, 128, 8, 64), dtype, 14).to(DEV)
+    kv = rand((2, 128, 2, 64), dtype, 15).to(DEV)
+    q, k, v = x.transpose(1, 2), kv.transpose(1, 2), (kv * 0.5).transpose(1, 2)
+    check(q.cpu(), k.cpu(), v.cpu(), what="dense reference")
+    out, lse = _abi.attention_fwd(q, k, v, None, True)
+    torch.cuda.synchronize()
+    ro, _ = orc.attention(f64(q), f64(k), f64(v), None, True)
+    assert (np.abs(f64(out) - ro) <= 5e-3 * (np.abs(ro) + 1)).all()
+
+
+def test_rejects_unsupported(gpu):
+    q = torch.zeros((1, 1, 8, 48), dtype=torch.float16, device=DEV)
+    with pytest.raises(_abi.TvkUnsupported):
+        _abi.attention_fwd(q, q, q)
+    q32 = torch.zeros((1, 1, 8, 64), device=DEV)
+    with pytest.raises(_abi.TvkUnsupported):
+        _abi.attention_fwd(q32, q32, q32)
+
+
+def test_sdpa_on_vulkan_device(gpu):
+    import torchvulkan_amd  # noqa: F401
+
+    V = "vulkan"
+    dtype = torch.float16
+    q, k, v = rand((2, 8, 128, 64), dtype, 20), rand((2, 2, 128, 64), dtype, 21), rand((2, 2, 128, 64), dtype, 22)
+    qv, kv_, vv = (t.to(V).requires_grad_() for t in (q, k, v))
+    out = F.scaled_dot_product_attention(qv, kv_, vv, is_causal=True, enable_gqa=True)
+    q64, k64, v64 = (t.double().requires_grad_() for t in (q, k, v))
+    ref = F.scaled_dot_product_attention(q64, k64, v64, is_causal=True, enable_gqa=True)
+    assert out.shape == ref.shape and out.dtype == dtype
+    assert ((out.detach().cpu().double() - ref.detach()).abs() <= 5e-3 * (ref.detach().abs() + 1)).all()
+    g = rand(out.shape, dtype, 23)
+    out.backward(g.to(V))
+    ref.backward(g.double())
+    for got, want, name in ((qv.grad, q64.grad, "dq"), (kv_.grad, k64.grad, "dk"), (vv.grad, v64.grad, "dv")):
+        assert got.shape == want.shape, name
+        assert ((got.cpu().double() - want).abs() <= 1e-2 * (want.abs() + 1)).all(), name

@@ -1,0 +1,60 @@
+"""Pins the attention oracle (oracle.attention, the reference's chunked_forward
+rows in float64) against torch's CPU math attention in float64, and against
+closed forms: equal scores average v, a dominant key selects its value row,
+fully masked rows give 0 / +inf, grouped-query heads read their kv head."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from oracle import oracle as orc
+
+
+def rnd(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape)
+
+
+def torch_ref(q, k, v, bias=None, causal=False, scale=None):
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x))
+    g = q.shape[1] // k.shape[1]
+    kk, vv = t(k).repeat_interleave(g, 1), t(v).repeat_interleave(g, 1)
+    mask = None if bias is None else t(np.broadcast_to(bias, q.shape[:3] + (k.shape[2],)))
+    return F.scaled_dot_product_attention(t(q), kk, vv, attn_mask=mask, is_causal=causal, scale=scale).numpy()
+
+
+def test_matches_torch_math_float64():
+    q, k, v = rnd((2, 8, 37, 16), 0), rnd((2, 2, 53, 16), 1), rnd((2, 2, 53, 24), 2)
+    bias = rnd((1, 8, 37, 53), 3)
+    for causal, b in ((False, None), (True, None), (False, bias)):
+        out, lse = orc.attention(q, k, v, b, causal)
+        np.testing.assert_allclose(out, torch_ref(q, k, v, b, causal), rtol=1e-12, atol=1e-12)
+    # lse against a direct logsumexp of the scores
+    out, lse = orc.attention(q, k, v, None, False, scale=0.3)
+    s = np.einsum("bhld,bhsd->bhls", q, np.repeat(k, 4, axis=1)) * 0.3
+    np.testing.assert_allclose(lse, np.log(np.exp(s).sum(-1)), rtol=1e-12)
+
+
+def test_closed_forms():
+    v = rnd((1, 1, 10, 4), 4)
+    q = np.zeros((1, 1, 3, 8))
+    k = rnd((1, 1, 10, 8), 5)
+    out, lse = orc.attention(q, k, v)                           # all scores 0: the mean of v
+    np.testing.assert_allclose(out[0, 0], np.repeat(v[0, 0].mean(0, keepdims=True), 3, 0), rtol=1e-12)
+    np.testing.assert_allclose(lse, np.log(10.0))
+    bias = np.full((1, 1, 3, 10), -np.inf)
+    bias[0, 0, 1, 7] = 0.0                                    # row 1 sees only key 7; rows 0, 2 see nothing
+    out, lse = orc.attention(q, k, v, bias)
+    np.testing.assert_allclose(out[0, 0, 1], v[0, 0, 7], rtol=1e-12)
+    assert (out[0, 0, [0, 2]] == 0).all() and np.isinf(lse[0, 0, [0, 2]]).all() and lse[0, 0, 1] == 0.0
+    out, _ = orc.attention(np.ones((1, 1, 4, 8)), np.ones((1, 1, 4, 8)), v[:, :, :4], causal=True)
+    np.testing.assert_allclose(out[0, 0, 0], v[0, 0, 0], rtol=1e-12)   # causal row 0 sees key 0 only
+    np.testing.assert_allclose(out[0, 0, 3], v[0, 0, :4].mean(0), rtol=1e-12)
+
+
+def test_grouped_heads_read_their_kv_head():
+    q, k, v = rnd((1, 4, 5, 8), 6), rnd((1, 2, 7, 8), 7), rnd((1, 2, 7, 8), 8)
+    out, _ = orc.attention(q, k, v)
+    for h in range(4):
+        o1, _ = orc.attention(q[:, h:h + 1], k[:, h // 2:h // 2 + 1], v[:, h // 2:h // 2 + 1])
+        np.testing.assert_allclose(out[:, h:h + 1], o1, rtol=1e-12)

@@ -134,6 +134,26 @@ class BinaryDesc(C.Structure):
     ]
 
 
+I64x4 = C.c_int64 * 4
+
+
+class AttentionDesc(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int32),
+        ("causal", C.c_int32),
+        ("batch", C.c_int64), ("heads_q", C.c_int64), ("heads_kv", C.c_int64), ("len_q", C.c_int64),
+        ("len_kv", C.c_int64), ("head_dim", C.c_int64), ("head_dim_v", C.c_int64),
+        ("q", C.c_void_p), ("q_stride", I64x4),
+        ("k", C.c_void_p), ("k_stride", I64x4),
+        ("v", C.c_void_p), ("v_stride", I64x4),
+        ("bias", C.c_void_p), ("bias_stride", I64x4),
+        ("out", C.c_void_p), ("out_stride", I64x4),
+        ("lse", C.c_void_p), ("lse_stride", I64x3),
+        ("scale", C.c_double),
+        ("stream", C.c_void_p),
+    ]
+
+
 class DeviceProps(C.Structure):
     _fields_ = [
         ("name", C.c_char * 256),
@@ -186,6 +206,7 @@ def load() -> C.CDLL:
         lib.tvk_fill.argtypes = [C.POINTER(FillDesc)]
         lib.tvk_reduce_sum.argtypes = [C.POINTER(ReduceDesc)]
         lib.tvk_binary.argtypes = [C.POINTER(BinaryDesc)]
+        lib.tvk_attention_fwd.argtypes = [C.POINTER(AttentionDesc)]
         for fn in _ALL_ENTRY_POINTS:
             getattr(lib, fn).restype = C.c_int if fn != "tvk_last_error" else C.c_char_p
         _lib = lib
@@ -199,7 +220,7 @@ _ALL_ENTRY_POINTS = (
     "tvk_memory_reserved", "tvk_reset_peak_memory_stats", "tvk_mem_get_info", "tvk_memcpy_h2d",
     "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan",
     "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad", "tvk_copy", "tvk_copy_plan",
-    "tvk_fill", "tvk_reduce_sum", "tvk_binary",
+    "tvk_fill", "tvk_reduce_sum", "tvk_binary", "tvk_attention_fwd",
 )
 
 
@@ -348,6 +369,38 @@ def binary(a, b, out, op, alpha=1.0, stream=None) -> None:
     d.alpha = float(alpha)
     d.stream = _stream_of(out, stream)
     check(load().tvk_binary(C.byref(d)))
+
+
+def make_attention_desc(q, k, v, out, lse, bias=None, causal=False, scale=None, stream=None) -> AttentionDesc:
+    """Describes tvk_attention_fwd over [B, H, L, D] device tensors (bias broadcast to [B, Hq, L, S])."""
+    d = AttentionDesc()
+    d.dtype = _dtype_code(q.dtype)
+    d.causal = 1 if causal else 0
+    d.batch, d.heads_q, d.len_q, d.head_dim = q.shape
+    d.heads_kv, d.len_kv = k.shape[1], k.shape[2]
+    d.head_dim_v = v.shape[3]
+    d.q, d.q_stride = q.data_ptr(), I64x4(*q.stride())
+    d.k, d.k_stride = k.data_ptr(), I64x4(*k.stride())
+    d.v, d.v_stride = v.data_ptr(), I64x4(*v.stride())
+    if bias is not None:
+        be = bias.expand(q.shape[0], q.shape[1], q.shape[2], k.shape[2])
+        d.bias, d.bias_stride = be.data_ptr(), I64x4(*be.stride())
+    d.out, d.out_stride = out.data_ptr(), I64x4(*out.stride())
+    d.lse, d.lse_stride = lse.data_ptr(), I64x3(*lse.stride())
+    d.scale = float(scale if scale is not None else q.shape[3] ** -0.5)
+    d.stream = stream
+    return d
+
+
+def attention_fwd(q, k, v, bias=None, causal=False, scale=None, stream=None):
+    """(out, lse) of tvk_attention_fwd; out is a new [B, Hq, L, Dv] tensor, lse float32 [B, Hq, L]."""
+    import torch
+
+    out = torch.empty((q.shape[0], q.shape[1], q.shape[2], v.shape[3]), dtype=q.dtype, device=q.device)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
+    d = make_attention_desc(q, k, v, out, lse, bias, causal, scale, _stream_of(q, stream))
+    check(load().tvk_attention_fwd(C.byref(d)))
+    return out, lse
 
 
 def _strides3(t) -> tuple[int, int, int]:
