@@ -341,6 +341,27 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c3_llm_layer_gemm_tflops"] = round(llm_flops / (ms * 1e-3) / 1e12, 2)
     del keep, llm_refs, llm_descs
 
+    # ---- C3 attention: fused forward, batch 32, 8 query / 2 kv heads, seq 256, head_dim 64, causal
+    qa = torch.randn((32, 8, 256, 64), generator=g).to(torch.float16).to(dev)
+    ka = torch.randn((32, 2, 256, 64), generator=g).to(torch.float16).to(dev)
+    va = torch.randn((32, 2, 256, 64), generator=g).to(torch.float16).to(dev)
+    oa = torch.empty_like(qa)
+    la = torch.empty((32, 8, 256), dtype=torch.float32, device=dev)
+    ad = _abi.make_attention_desc(qa, ka, va, oa, la, causal=True, stream=s)
+    ar = C.byref(ad)
+
+    def attn_step():
+        st_ = lib.tvk_attention_fwd(ar)
+        if st_:
+            _abi.check(st_)
+
+    ms, _ = timed(attn_step, steps * 4, warmup, stream)
+    # causal: the unmasked half of the L x S scores (i >= j), two products of 2*D flops each
+    att_flops = 32 * 8 * (256 * 257 // 2) * 64 * 2 * 2
+    out["c3_attention_fwd_us"] = round(ms * 1e3, 2)
+    out["c3_attention_fwd_tflops"] = round(att_flops / (ms * 1e-3) / 1e12, 2)
+    del qa, ka, va, oa, la
+
     # ---- C5 ragged [1000,777]x[777,3000] and baddbmm in[64,512,512] + 0.5*bmm ----
     a = torch.randn((1000, 777), generator=g).to(torch.float16).to(dev)
     b = torch.randn((777, 3000), generator=g).to(torch.float16).to(dev)
