@@ -295,6 +295,33 @@ typedef struct {
 
 tvk_status tvk_attention_fwd(const tvk_attention_desc* desc);
 
+/* Gradients of tvk_attention_fwd: dq, dk, dv (same dtype and head layouts as
+ * q, k, v) from dout and the forward's out and lse (`fwd` describes q, k, v,
+ * bias, out, lse, scale and causal exactly as for the forward call). With
+ * P = exp(s - lse) and delta_i = sum_d dout[i,d]*out[i,d] (float32):
+ *   dv[j] = sum_i P[i,j] dout[i],  dS = P * (dout.v^T - delta),
+ *   dq[i] = scale * sum_j dS[i,j] k[j],  dk[j] = scale * sum_i dS[i,j] q[i],
+ * summed over the query heads of each kv head (the reference's
+ * chunked_backward, src/api/ops/attention.cpp:141-199; the fused passes
+ * BACKWARD_Q and BACKWARD_KV, :640-665). P and dS are formed in float32 and
+ * rounded to the dtype before their products, as the reference's
+ * scoreGradients stages them (src/shaders/ops/attention_coop.slang:283-305);
+ * accumulation is float32, and every output element
+ * is written by one workgroup (no atomics: the same bits every run). The
+ * gradient of the bias is not produced (the reference computes it on its
+ * chunked path). Same support as the forward; dout, dq, dk, dv with unit
+ * stride along the head dimension and 16-byte aligned rows. Uses B*Hq*L
+ * floats of the library workspace for delta. */
+typedef struct {
+    tvk_attention_desc fwd;
+    const void* dout; int64_t dout_stride[4];
+    void* dq; int64_t dq_stride[4];
+    void* dk; int64_t dk_stride[4];
+    void* dv; int64_t dv_stride[4];
+} tvk_attention_bwd_desc;
+
+tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc);
+
 /* ------------------------------------------------------------------------- */
 /* Compute: batched strided GEMM with fused epilogue                          */
 /* ------------------------------------------------------------------------- */

@@ -206,6 +206,44 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, bias: np.ndarray | No
     return out, lse
 
 
+def attention_bwd(q, k, v, dout, bias=None, causal=False, scale=None, out=None, round_to=None):
+    """(dq, dk, dv) of attention() in float64, as the reference's
+    chunked_backward (src/api/ops/attention.cpp:141-199): P = exp(s - lse),
+    delta = rowsum(dout*out), dS = P*(dout.v^T - delta), dq = scale*dS.k,
+    dk = scale*dS^T.q and dv = P^T.dout summed over each kv head's query
+    heads. `out` is the forward output as stored (rounded to its dtype); the
+    reference forms delta from that tensor (:156). Without it, the exact
+    float64 output is used. round_to (F16/BF16): P and dS are formed in
+    float32 and rounded to that dtype before their products, as the
+    reference's cooperative-matrix backward stages them
+    (src/shaders/ops/attention_coop.slang:283-305)."""
+    q, k, v, dout = (np.asarray(t, dtype=np.float64) for t in (q, k, v, dout))
+    B, Hq, L, D = q.shape
+    Hk, S = k.shape[1], k.shape[2]
+    g = Hq // Hk
+    scale = D ** -0.5 if scale is None else scale
+    exact_out, lse = attention(q, k, v, bias, causal, scale)
+    out = exact_out if out is None else np.asarray(out, dtype=np.float64)
+    kk, vv = np.repeat(k, g, axis=1), np.repeat(v, g, axis=1)
+    s = np.einsum("bhld,bhsd->bhls", q, kk) * scale
+    if bias is not None:
+        s = s + np.broadcast_to(np.asarray(bias, dtype=np.float64), s.shape)
+    if causal:
+        s = np.where(np.arange(S)[None, :] > np.arange(L)[:, None], -np.inf, s)
+    with np.errstate(invalid="ignore"):
+        p = np.where(np.isinf(lse)[..., None], 0.0, np.exp(s - lse[..., None]))
+    delta = (dout * out).sum(-1, keepdims=True)
+    dp = np.einsum("bhld,bhsd->bhls", dout, vv)
+    ds = p * (dp - delta)
+    if round_to is not None:
+        rt = lambda x: to_f32(cast(x.astype(np.float32), F32, round_to), round_to).astype(np.float64)
+        p, ds = rt(p), rt(ds)
+    dq = np.einsum("bhls,bhsd->bhld", ds, kk) * scale
+    dk = np.einsum("bhls,bhld->bhsd", ds, q).reshape(B, Hk, g, S, D).sum(2) * scale
+    dv = np.einsum("bhls,bhld->bhsd", p, dout).reshape(B, Hk, g, S, v.shape[3]).sum(2)
+    return dq, dk, dv
+
+
 # ---------------------------------------------------------------------------
 # GEMM
 # ---------------------------------------------------------------------------

@@ -58,3 +58,38 @@ def test_grouped_heads_read_their_kv_head():
     for h in range(4):
         o1, _ = orc.attention(q[:, h:h + 1], k[:, h // 2:h // 2 + 1], v[:, h // 2:h // 2 + 1])
         np.testing.assert_allclose(out[:, h:h + 1], o1, rtol=1e-12)
+
+
+def test_backward_matches_torch_autograd_float64():
+    q, k, v = rnd((2, 4, 19, 8), 10), rnd((2, 2, 23, 8), 11), rnd((2, 2, 23, 8), 12)
+    dout = rnd((2, 4, 19, 8), 13)
+    bias = rnd((1, 4, 19, 23), 14)
+    for causal, b in ((False, None), (True, None), (False, bias)):
+        dq, dk, dv = orc.attention_bwd(q, k, v, dout, b, causal)
+        tq, tk, tv = (torch.from_numpy(x).requires_grad_() for x in (q, k, v))
+        mask = None if b is None else torch.from_numpy(np.broadcast_to(b, (2, 4, 19, 23)).copy())
+        o = F.scaled_dot_product_attention(tq, tk.repeat_interleave(2, 1), tv.repeat_interleave(2, 1), attn_mask=mask,
+                                           is_causal=causal)
+        o.backward(torch.from_numpy(dout))
+        for got, want in ((dq, tq.grad), (dk, tk.grad), (dv, tv.grad)):
+            np.testing.assert_allclose(got, want.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_backward_rounding_option_changes_only_the_staged_values():
+    # round_to rounds P and dS to the dtype: on inputs where both are exact in float16
+    # (P in {0, 1} through a dominant key, dS small dyadic values) the rounded and exact results agree
+    q = np.zeros((1, 1, 2, 8))
+    k = np.zeros((1, 1, 2, 8))
+    v = rnd((1, 1, 2, 8), 20)
+    dout = np.full((1, 1, 2, 8), 0.5)
+    bias = np.array([[[[0.0, -np.inf], [0.0, -np.inf]]]])
+    exact = orc.attention_bwd(q, k, v, dout, bias)
+    rounded = orc.attention_bwd(q, k, v, dout, bias, round_to=orc.F16)
+    for a, b in zip(exact, rounded):
+        np.testing.assert_allclose(a, b, rtol=0, atol=1e-12)
+    # and on random inputs it differs by about the dtype's rounding
+    q, k, v, dout = rnd((1, 2, 16, 8), 21), rnd((1, 2, 16, 8), 22), rnd((1, 2, 16, 8), 23), rnd((1, 2, 16, 8), 24)
+    e = orc.attention_bwd(q, k, v, dout)
+    r = orc.attention_bwd(q, k, v, dout, round_to=orc.BF16)
+    d = max(np.abs(a - b).max() for a, b in zip(e, r))
+    assert 0 < d < 0.05

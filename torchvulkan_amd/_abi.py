@@ -154,6 +154,16 @@ class AttentionDesc(C.Structure):
     ]
 
 
+class AttentionBwdDesc(C.Structure):
+    _fields_ = [
+        ("fwd", AttentionDesc),
+        ("dout", C.c_void_p), ("dout_stride", I64x4),
+        ("dq", C.c_void_p), ("dq_stride", I64x4),
+        ("dk", C.c_void_p), ("dk_stride", I64x4),
+        ("dv", C.c_void_p), ("dv_stride", I64x4),
+    ]
+
+
 class DeviceProps(C.Structure):
     _fields_ = [
         ("name", C.c_char * 256),
@@ -207,6 +217,7 @@ def load() -> C.CDLL:
         lib.tvk_reduce_sum.argtypes = [C.POINTER(ReduceDesc)]
         lib.tvk_binary.argtypes = [C.POINTER(BinaryDesc)]
         lib.tvk_attention_fwd.argtypes = [C.POINTER(AttentionDesc)]
+        lib.tvk_attention_bwd.argtypes = [C.POINTER(AttentionBwdDesc)]
         for fn in _ALL_ENTRY_POINTS:
             getattr(lib, fn).restype = C.c_int if fn != "tvk_last_error" else C.c_char_p
         _lib = lib
@@ -221,6 +232,7 @@ _ALL_ENTRY_POINTS = (
     "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan",
     "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad", "tvk_copy", "tvk_copy_plan",
     "tvk_fill", "tvk_reduce_sum", "tvk_binary", "tvk_attention_fwd",
+    "tvk_attention_bwd",
 )
 
 
@@ -401,6 +413,22 @@ def attention_fwd(q, k, v, bias=None, causal=False, scale=None, stream=None):
     d = make_attention_desc(q, k, v, out, lse, bias, causal, scale, _stream_of(q, stream))
     check(load().tvk_attention_fwd(C.byref(d)))
     return out, lse
+
+
+def attention_bwd(q, k, v, out, lse, dout, bias=None, causal=False, scale=None, stream=None):
+    """(dq, dk, dv) of tvk_attention_bwd (new dense tensors) from the forward's out and lse."""
+    import torch
+
+    dq, dk, dv = torch.empty_like(q, memory_format=torch.contiguous_format), \
+        torch.empty_like(k, memory_format=torch.contiguous_format), torch.empty_like(v, memory_format=torch.contiguous_format)
+    d = AttentionBwdDesc()
+    d.fwd = make_attention_desc(q, k, v, out, lse, bias, causal, scale, _stream_of(q, stream))
+    d.dout, d.dout_stride = dout.data_ptr(), I64x4(*dout.stride())
+    d.dq, d.dq_stride = dq.data_ptr(), I64x4(*dq.stride())
+    d.dk, d.dk_stride = dk.data_ptr(), I64x4(*dk.stride())
+    d.dv, d.dv_stride = dv.data_ptr(), I64x4(*dv.stride())
+    check(load().tvk_attention_bwd(C.byref(d)))
+    return dq, dk, dv
 
 
 def _strides3(t) -> tuple[int, int, int]:

@@ -23,6 +23,7 @@
 // log2-scaled arguments.
 #include "gemm_common.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace tvk {
@@ -276,6 +277,376 @@ void launch_attn(const AttnArgs& a, bool causal, bool bias, dim3 grid, hipStream
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+
+struct AttnBwdArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const uint16_t* bias;
+    const uint16_t* out;
+    const uint16_t* dout;
+    const float* lse;
+    float* delta;          // [B][Hq][L], dense
+    uint16_t* dq;
+    uint16_t* dk;
+    uint16_t* dv;
+    int64_t sq[4], sk[4], sv[4], sb[4], so[4], sdo[4], sdq[4], sdk[4], sdv[4], sl[3];
+    int L, S, Hq, group;
+    float scale;
+};
+
+// 64-bit stores of four consecutive elements along the head dimension
+template <int DT>
+__device__ inline void store4(uint16_t* dst, f32x4 v, float mul) {
+    *reinterpret_cast<u32x2*>(dst) = u32x2{pack2<DT>(v[0] * mul, v[1] * mul), pack2<DT>(v[2] * mul, v[3] * mul)};
+}
+
+// Reads, with ds_read_b64_tr_b16, the A operand M^T for M^T X where M is an
+// LDS tile [row][LDK] of 16-bit values: lane c16 of group g gets column
+// 16*i + c16 at rows 32*kk + {4g..4g+3, 16+4g..16+4g+3} (the k-slot order of
+// a transposed-score accumulator).
+template <int LDK>
+__device__ inline u32x4 read_tr(const uint16_t* tile, int kk, int i, int g, int c16) {
+    u32x4 f;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+        const int kr = 32 * kk + 16 * rr + 4 * g + c16 / 4;
+        TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(TVK_LDS const uint16_t*)&tile[kr * LDK + 16 * i + (c16 % 4) * 4];
+        const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+        f[2 * rr] = w.x;
+        f[2 * rr + 1] = w.y;
+    }
+    return f;
+}
+
+// dQ pass (and delta): the forward's orientation. 4 waves x 32 queries of one
+// (batch, head); key tiles of 64 through double-buffered LDS. Per tile:
+// S^T = K Q^T, P^T = exp(s - lse), dP^T = V dO^T, dS^T = P^T (dP^T - delta),
+// dQ^T += K^T dS^T (K read transposed in the dS^T k-slot order). As in the
+// reference's scoreGradients (src/shaders/ops/attention_coop.slang:283-305),
+// P and dS are formed in float32 and rounded to the dtype for their products.
+template <int DT, int D, bool CAUSAL, bool BIAS>
+__global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs p) {
+    constexpr int DS = D / 32, DT16 = D / 16, LDK = D + 8;
+    constexpr int CH = AT_BN * D / 8, CPT = CH / (64 * AT_WAVES);
+    __shared__ __attribute__((aligned(16))) uint16_t ks[2][AT_BN * LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t vs[2][AT_BN * LDK];
+
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int g = lane / 16, c16 = lane % 16;
+    const int b = blockIdx.z, h = blockIdx.y, hk = h / p.group;
+    const int q0 = blockIdx.x * AT_BM + wave * 32;
+    const uint16_t* Q = p.q + (int64_t)b * p.sq[0] + (int64_t)h * p.sq[1];
+    const uint16_t* K = p.k + (int64_t)b * p.sk[0] + (int64_t)hk * p.sk[1];
+    const uint16_t* V = p.v + (int64_t)b * p.sv[0] + (int64_t)hk * p.sv[1];
+    const uint16_t* O = p.out + (int64_t)b * p.so[0] + (int64_t)h * p.so[1];
+    const uint16_t* dO = p.dout + (int64_t)b * p.sdo[0] + (int64_t)h * p.sdo[1];
+
+    u32x4 qf[2][DS], df[2][DS];
+    float lse[2], dlt[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + 16 * qt + c16;
+        const bool in = qi < p.L;
+        float part = 0.0f;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            const int d0 = 32 * ds + 8 * g;
+            qf[qt][ds] = in ? *reinterpret_cast<const u32x4*>(Q + (int64_t)qi * p.sq[2] + d0) : u32x4{0, 0, 0, 0};
+            df[qt][ds] = in ? *reinterpret_cast<const u32x4*>(dO + (int64_t)qi * p.sdo[2] + d0) : u32x4{0, 0, 0, 0};
+            if (in) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint16_t ob = O[(int64_t)qi * p.so[2] + (int64_t)(d0 + e) * p.so[3]];
+                    const uint16_t db = (uint16_t)(df[qt][ds][e / 2] >> (16 * (e % 2)));
+                    part += elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, db)) *
+                            elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, ob));
+                }
+            }
+        }
+        dlt[qt] = xor_sum(xor_sum(part, 16), 32);
+        lse[qt] = in ? p.lse[(int64_t)b * p.sl[0] + (int64_t)h * p.sl[1] + (int64_t)qi * p.sl[2]] : INFINITY;
+        if (in && g == 0) p.delta[((int64_t)b * p.Hq + h) * p.L + qi] = dlt[qt];
+    }
+
+    f32x4 acc[DT16][2];
+#pragma unroll
+    for (int i = 0; i < DT16; ++i)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) acc[i][qt] = f32x4{0, 0, 0, 0};
+
+    int ntiles = (p.S + AT_BN - 1) / AT_BN;
+    if (CAUSAL) {
+        const int last_q = min(p.L, (int)blockIdx.x * AT_BM + AT_BM) - 1;
+        ntiles = min(ntiles, last_q / AT_BN + 1);
+    }
+    u32x4 kreg[CPT], vreg[CPT];
+    auto load_tile = [&](int j) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * 64 * AT_WAVES;
+            const int key = c / (D / 8), d8 = (c % (D / 8)) * 8;
+            const int kj = j * AT_BN + key;
+            kreg[i] = kj < p.S ? *reinterpret_cast<const u32x4*>(K + (int64_t)kj * p.sk[2] + d8) : u32x4{0, 0, 0, 0};
+            vreg[i] = kj < p.S ? *reinterpret_cast<const u32x4*>(V + (int64_t)kj * p.sv[2] + d8) : u32x4{0, 0, 0, 0};
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * 64 * AT_WAVES;
+            const int key = c / (D / 8), d8 = (c % (D / 8)) * 8;
+            *reinterpret_cast<u32x4*>(&ks[buf][key * LDK + d8]) = kreg[i];
+            *reinterpret_cast<u32x4*>(&vs[buf][key * LDK + d8]) = vreg[i];
+        }
+    };
+    if (ntiles > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    for (int j = 0; j < ntiles; ++j) {
+        const int buf = j & 1;
+        if (j + 1 < ntiles) load_tile(j + 1);
+        f32x4 sacc[4][2], pacc[4][2];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                sacc[kt][qt] = f32x4{0, 0, 0, 0};
+                pacc[kt][qt] = f32x4{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) {
+                const u32x4 kf = *reinterpret_cast<const u32x4*>(&ks[buf][(kt * 16 + c16) * LDK + 32 * ds + 8 * g]);
+                const u32x4 vf = *reinterpret_cast<const u32x4*>(&vs[buf][(kt * 16 + c16) * LDK + 32 * ds + 8 * g]);
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    sacc[kt][qt] = mfma16<DT>(kf, qf[qt][ds], sacc[kt][qt]);
+                    pacc[kt][qt] = mfma16<DT>(vf, df[qt][ds], pacc[kt][qt]);
+                }
+            }
+        }
+        // dS^T = P^T (dP^T - delta), P^T = exp(s - lse); masked entries give 0
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            const int qi = q0 + 16 * qt + c16;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int kj = j * AT_BN + kt * 16 + 4 * g + r;
+                    float s = sacc[kt][qt][r] * p.scale;
+                    if (BIAS && kj < p.S && qi < p.L) {
+                        const uint16_t bv = p.bias[(int64_t)b * p.sb[0] + (int64_t)h * p.sb[1] + (int64_t)qi * p.sb[2] + (int64_t)kj * p.sb[3]];
+                        s = s + elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, bv));
+                    }
+                    if (kj >= p.S || (CAUSAL && kj > qi)) s = -INFINITY;
+                    // dS from the float32 P; only dS is rounded to the dtype (when packed)
+                    const float pe = __builtin_amdgcn_exp2f((s - lse[qt]) * AT_LOG2E);
+                    sacc[kt][qt][r] = pe * (pacc[kt][qt][r] - dlt[qt]);
+                }
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            u32x4 sf[2];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                const f32x4 a = sacc[2 * kk][qt], c = sacc[2 * kk + 1][qt];
+                sf[qt] = u32x4{pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]), pack2<DT>(c[2], c[3])};
+            }
+#pragma unroll
+            for (int i = 0; i < DT16; ++i) {
+                const u32x4 kf = read_tr<LDK>(ks[buf], kk, i, g, c16);
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) acc[i][qt] = mfma16<DT>(kf, sf[qt], acc[i][qt]);
+            }
+        }
+        if (j + 1 < ntiles) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    uint16_t* dQ = p.dq + (int64_t)b * p.sdq[0] + (int64_t)h * p.sdq[1];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + 16 * qt + c16;
+        if (qi >= p.L) continue;
+#pragma unroll
+        for (int i = 0; i < DT16; ++i) store4<DT>(dQ + (int64_t)qi * p.sdq[2] + 16 * i + 4 * g, acc[i][qt], p.scale);
+    }
+}
+
+// dK / dV pass: 4 waves x 16 keys of one (batch, kv head); the queries of
+// every head of the group go by tiles of 64 through double-buffered LDS
+// (q, dout, lse, delta). Per tile: S = Q K^T (a lane owns one key),
+// P = exp(s - lse), dP = dO V^T, dS = P (dP - delta), then
+// dV^T += dO^T P and dK^T += Q^T dS with dO and Q read transposed in the
+// k-slot order of the S accumulator.
+template <int DT, int D, bool CAUSAL, bool BIAS>
+__global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dkv_kernel(AttnBwdArgs p) {
+    constexpr int DS = D / 32, DT16 = D / 16, LDK = D + 8;
+    constexpr int QT = 64;   // queries per tile
+    constexpr int CH = QT * D / 8, CPT = CH / (64 * AT_WAVES);
+    __shared__ __attribute__((aligned(16))) uint16_t qs[2][QT * LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t dos[2][QT * LDK];
+    __shared__ float lses[2][QT], dls[2][QT];
+
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int g = lane / 16, c16 = lane % 16;
+    const int b = blockIdx.z, hk = blockIdx.y;
+    const int kb0 = blockIdx.x * 64;
+    const int kj = kb0 + wave * 16 + c16;   // this lane's key
+    const uint16_t* K = p.k + (int64_t)b * p.sk[0] + (int64_t)hk * p.sk[1];
+    const uint16_t* V = p.v + (int64_t)b * p.sv[0] + (int64_t)hk * p.sv[1];
+
+    u32x4 kf[DS], vf[DS];
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+        kf[ds] = kj < p.S ? *reinterpret_cast<const u32x4*>(K + (int64_t)kj * p.sk[2] + 32 * ds + 8 * g) : u32x4{0, 0, 0, 0};
+        vf[ds] = kj < p.S ? *reinterpret_cast<const u32x4*>(V + (int64_t)kj * p.sv[2] + 32 * ds + 8 * g) : u32x4{0, 0, 0, 0};
+    }
+    f32x4 dka[DT16], dva[DT16];
+#pragma unroll
+    for (int i = 0; i < DT16; ++i) {
+        dka[i] = f32x4{0, 0, 0, 0};
+        dva[i] = f32x4{0, 0, 0, 0};
+    }
+
+    // query tiles of all heads of the group; under the causal mask the tiles
+    // wholly before this block's first key see none of its keys
+    const int first_t = CAUSAL ? kb0 / QT : 0;
+    const int per_head = (p.L + QT - 1) / QT;
+    const int ntiles = p.group * max(0, per_head - first_t);
+    u32x4 qreg[CPT], dreg[CPT];
+    float lreg = INFINITY, dreg1 = 0.0f;
+    auto tile_pos = [&](int n, int& hq, int& t) {
+        hq = hk * p.group + n / max(1, per_head - first_t);
+        t = first_t + n % max(1, per_head - first_t);
+    };
+    auto load_tile = [&](int n) {
+        int hq, t;
+        tile_pos(n, hq, t);
+        const uint16_t* Q = p.q + (int64_t)b * p.sq[0] + (int64_t)hq * p.sq[1];
+        const uint16_t* dO = p.dout + (int64_t)b * p.sdo[0] + (int64_t)hq * p.sdo[1];
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * 64 * AT_WAVES;
+            const int row = c / (D / 8), d8 = (c % (D / 8)) * 8;
+            const int qi = t * QT + row;
+            qreg[i] = qi < p.L ? *reinterpret_cast<const u32x4*>(Q + (int64_t)qi * p.sq[2] + d8) : u32x4{0, 0, 0, 0};
+            dreg[i] = qi < p.L ? *reinterpret_cast<const u32x4*>(dO + (int64_t)qi * p.sdo[2] + d8) : u32x4{0, 0, 0, 0};
+        }
+        if (tid < QT) {
+            const int qi = t * QT + tid;
+            lreg = qi < p.L ? p.lse[(int64_t)b * p.sl[0] + (int64_t)hq * p.sl[1] + (int64_t)qi * p.sl[2]] : INFINITY;
+            dreg1 = qi < p.L ? p.delta[((int64_t)b * p.Hq + hq) * p.L + qi] : 0.0f;
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * 64 * AT_WAVES;
+            const int row = c / (D / 8), d8 = (c % (D / 8)) * 8;
+            *reinterpret_cast<u32x4*>(&qs[buf][row * LDK + d8]) = qreg[i];
+            *reinterpret_cast<u32x4*>(&dos[buf][row * LDK + d8]) = dreg[i];
+        }
+        if (tid < QT) {
+            lses[buf][tid] = lreg;
+            dls[buf][tid] = dreg1;
+        }
+    };
+    if (ntiles > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    for (int n = 0; n < ntiles; ++n) {
+        const int buf = n & 1;
+        int hq, t;
+        tile_pos(n, hq, t);
+        if (n + 1 < ntiles) load_tile(n + 1);
+        // S and dP: 4 blocks of 16 queries (rows) x this wave's 16 keys (columns)
+        f32x4 sacc[4], pacc[4];
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+            sacc[qt] = f32x4{0, 0, 0, 0};
+            pacc[qt] = f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) {
+                const u32x4 qa = *reinterpret_cast<const u32x4*>(&qs[buf][(qt * 16 + c16) * LDK + 32 * ds + 8 * g]);
+                const u32x4 da = *reinterpret_cast<const u32x4*>(&dos[buf][(qt * 16 + c16) * LDK + 32 * ds + 8 * g]);
+                sacc[qt] = mfma16<DT>(qa, kf[ds], sacc[qt]);
+                pacc[qt] = mfma16<DT>(da, vf[ds], pacc[qt]);
+            }
+        }
+        // P (rounded to the dtype) into sacc, dS into pacc
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = qt * 16 + 4 * g + r;
+                const int qi = t * QT + row;
+                float s = sacc[qt][r] * p.scale;
+                if (BIAS && kj < p.S && qi < p.L) {
+                    const uint16_t bv = p.bias[(int64_t)b * p.sb[0] + (int64_t)hq * p.sb[1] + (int64_t)qi * p.sb[2] + (int64_t)kj * p.sb[3]];
+                    s = s + elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, bv));
+                }
+                if (kj >= p.S || (CAUSAL && kj > qi)) s = -INFINITY;
+                // P and dS from the float32 P; each is rounded to the dtype when packed
+                const float pe = __builtin_amdgcn_exp2f((s - lses[buf][row]) * AT_LOG2E);
+                sacc[qt][r] = pe;
+                pacc[qt][r] = pe * (pacc[qt][r] - dls[buf][row]);
+            }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const f32x4 a = sacc[2 * kk], c = sacc[2 * kk + 1];
+            const u32x4 pf = u32x4{pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]), pack2<DT>(c[2], c[3])};
+            const f32x4 e = pacc[2 * kk], f = pacc[2 * kk + 1];
+            const u32x4 sf = u32x4{pack2<DT>(e[0], e[1]), pack2<DT>(e[2], e[3]), pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3])};
+#pragma unroll
+            for (int i = 0; i < DT16; ++i) {
+                dva[i] = mfma16<DT>(read_tr<LDK>(dos[buf], kk, i, g, c16), pf, dva[i]);
+                dka[i] = mfma16<DT>(read_tr<LDK>(qs[buf], kk, i, g, c16), sf, dka[i]);
+            }
+        }
+        if (n + 1 < ntiles) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (kj >= p.S) return;
+    uint16_t* dK = p.dk + (int64_t)b * p.sdk[0] + (int64_t)hk * p.sdk[1] + (int64_t)kj * p.sdk[2];
+    uint16_t* dV = p.dv + (int64_t)b * p.sdv[0] + (int64_t)hk * p.sdv[1] + (int64_t)kj * p.sdv[2];
+#pragma unroll
+    for (int i = 0; i < DT16; ++i) {
+        store4<DT>(dK + 16 * i + 4 * g, dka[i], p.scale);
+        store4<DT>(dV + 16 * i + 4 * g, dva[i], 1.0f);
+    }
+}
+
+template <int DT, int D>
+void launch_attn_bwd(const AttnBwdArgs& a, bool causal, bool bias, dim3 gq, dim3 gkv, hipStream_t s) {
+    const dim3 block(64 * AT_WAVES);
+#define TVK_BWD(C, B)                                                                                     \
+    do {                                                                                                  \
+        if (gq.x) hipLaunchKernelGGL((attn_bwd_dq_kernel<DT, D, C, B>), gq, block, 0, s, a);              \
+        if (gkv.x) hipLaunchKernelGGL((attn_bwd_dkv_kernel<DT, D, C, B>), gkv, block, 0, s, a);           \
+    } while (0)
+    if (causal) {
+        if (bias) TVK_BWD(true, true);
+        else TVK_BWD(true, false);
+    } else {
+        if (bias) TVK_BWD(false, true);
+        else TVK_BWD(false, false);
+    }
+#undef TVK_BWD
+}
+
 }  // namespace
 }  // namespace tvk
 
@@ -337,5 +708,88 @@ extern "C" tvk_status tvk_attention_fwd(const tvk_attention_desc* d) {
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_attention_fwd: launch failed: ") + hipGetErrorString(e));
+    return TVK_OK;
+}
+
+namespace {
+
+tvk_status check_attention(const tvk_attention_desc* d, const char* who) {
+    auto bad = [&](tvk_status st, const char* m) { return fail(st, std::string(who) + ": " + m); };
+    if (d->dtype != TVK_F16 && d->dtype != TVK_BF16) return bad(TVK_ERR_UNSUPPORTED, "dtype must be float16 or bfloat16");
+    if (d->batch < 0 || d->heads_q < 0 || d->heads_kv <= 0 || d->len_q < 0 || d->len_kv < 0) return bad(TVK_ERR_INVALID, "negative size");
+    if (d->heads_q % d->heads_kv != 0) return bad(TVK_ERR_INVALID, "heads_q is not a multiple of heads_kv");
+    if (d->head_dim != d->head_dim_v || (d->head_dim != 64 && d->head_dim != 128))
+        return bad(TVK_ERR_UNSUPPORTED, "head_dim == head_dim_v in {64, 128} only");
+    if (d->batch > 65535 || d->heads_q > 65535 || d->len_q > (int64_t)0x7fffffff || d->len_kv > (int64_t)0x7fffffff)
+        return bad(TVK_ERR_UNSUPPORTED, "grid too large");
+    return TVK_OK;
+}
+
+bool rows_ok(const void* ptr, const int64_t* st) {
+    if ((reinterpret_cast<uintptr_t>(ptr) & 15) != 0 || st[3] != 1) return false;
+    for (int i = 0; i < 3; ++i)
+        if (st[i] % 8 != 0) return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc) {
+    if (!desc) return fail(TVK_ERR_INVALID, "tvk_attention_bwd: desc is NULL");
+    const tvk_attention_desc* d = &desc->fwd;
+    tvk_status st = check_attention(d, "tvk_attention_bwd");
+    if (st != TVK_OK) return st;
+    if (d->batch == 0 || d->heads_q == 0 || (d->len_q == 0 && d->len_kv == 0)) return TVK_OK;
+    if (!d->q || !d->k || !d->v || !d->out || !d->lse || !desc->dout || !desc->dq || !desc->dk || !desc->dv)
+        return fail(TVK_ERR_INVALID, "tvk_attention_bwd: NULL tensor");
+    if (!rows_ok(d->q, d->q_stride) || !rows_ok(d->k, d->k_stride) || !rows_ok(d->v, d->v_stride) ||
+        !rows_ok(desc->dout, desc->dout_stride) || !rows_ok(desc->dq, desc->dq_stride) ||
+        !rows_ok(desc->dk, desc->dk_stride) || !rows_ok(desc->dv, desc->dv_stride))
+        return fail(TVK_ERR_UNSUPPORTED, "tvk_attention_bwd: q, k, v, dout, dq, dk, dv need unit stride along the head dimension and 16-byte aligned rows");
+    AttnBwdArgs a{};
+    a.q = static_cast<const uint16_t*>(d->q);
+    a.k = static_cast<const uint16_t*>(d->k);
+    a.v = static_cast<const uint16_t*>(d->v);
+    a.bias = static_cast<const uint16_t*>(d->bias);
+    a.out = static_cast<const uint16_t*>(d->out);
+    a.dout = static_cast<const uint16_t*>(desc->dout);
+    a.lse = d->lse;
+    a.dq = static_cast<uint16_t*>(desc->dq);
+    a.dk = static_cast<uint16_t*>(desc->dk);
+    a.dv = static_cast<uint16_t*>(desc->dv);
+    for (int i = 0; i < 4; ++i) {
+        a.sq[i] = d->q_stride[i];
+        a.sk[i] = d->k_stride[i];
+        a.sv[i] = d->v_stride[i];
+        a.sb[i] = d->bias ? d->bias_stride[i] : 0;
+        a.so[i] = d->out_stride[i];
+        a.sdo[i] = desc->dout_stride[i];
+        a.sdq[i] = desc->dq_stride[i];
+        a.sdk[i] = desc->dk_stride[i];
+        a.sdv[i] = desc->dv_stride[i];
+    }
+    for (int i = 0; i < 3; ++i) a.sl[i] = d->lse_stride[i];
+    a.L = (int)d->len_q;
+    a.S = (int)d->len_kv;
+    a.Hq = (int)d->heads_q;
+    a.group = (int)(d->heads_q / d->heads_kv);
+    a.scale = (float)d->scale;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    a.delta = static_cast<float*>(device_workspace(dev, (size_t)std::max<int64_t>(1, d->batch * d->heads_q * d->len_q) * 4));
+    if (!a.delta) return fail(TVK_ERR_OOM, "tvk_attention_bwd: workspace allocation failed");
+    const dim3 gq((unsigned)((d->len_q + AT_BM - 1) / AT_BM), (unsigned)d->heads_q, (unsigned)d->batch);
+    const dim3 gkv((unsigned)((d->len_kv + 63) / 64), (unsigned)d->heads_kv, (unsigned)d->batch);
+    const hipStream_t s = resolve_stream(d->stream);
+    const bool bias = d->bias != nullptr;
+    if (d->dtype == TVK_F16) {
+        if (d->head_dim == 64) launch_attn_bwd<TVK_F16, 64>(a, d->causal != 0, bias, gq, gkv, s);
+        else launch_attn_bwd<TVK_F16, 128>(a, d->causal != 0, bias, gq, gkv, s);
+    } else {
+        if (d->head_dim == 64) launch_attn_bwd<TVK_BF16, 64>(a, d->causal != 0, bias, gq, gkv, s);
+        else launch_attn_bwd<TVK_BF16, 128>(a, d->causal != 0, bias, gq, gkv, s);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_attention_bwd: launch failed: ") + hipGetErrorString(e));
     return TVK_OK;
 }

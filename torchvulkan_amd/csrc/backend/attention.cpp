@@ -1,9 +1,9 @@
 // Fused scaled dot-product attention on the vulkan device: the overrideable
 // SDPA backend the reference registers (src/api/ops/attention.cpp:667-761).
-// The forward runs tvk_attention_fwd; the backward follows the reference's
-// chunked_backward (attention.cpp:141-199) in float32 on the host until a
-// device kernel takes it, with the fallback warning (an error under
-// TORCHVULKAN_STRICT=1).
+// The forward runs tvk_attention_fwd and the backward tvk_attention_bwd. A
+// requested bias gradient, or a shape the kernels decline, takes the
+// reference's chunked path (attention.cpp:115-199) in float32 on the host,
+// with the fallback warning (an error under TORCHVULKAN_STRICT=1).
 #include "common.h"
 
 #include <ATen/Context.h>
@@ -113,6 +113,40 @@ at::Tensor host_scores(const Attn& a, const at::Tensor& q, const at::Tensor& k, 
     return s;
 }
 
+// The forward descriptor over kernel-layout q, k, v (bias broadcast to [B, Hq, L, S]).
+tvk_attention_desc forward_desc(const Attn& a, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                const at::Tensor& bias, const at::Tensor& out, const at::Tensor& lse) {
+    tvk_attention_desc d;
+    std::memset(&d, 0, sizeof(d));
+    bool ok = false;
+    d.dtype = tvk_dtype_of(a.q.scalar_type(), ok);
+    d.causal = a.causal ? 1 : 0;
+    d.batch = a.B;
+    d.heads_q = a.Hq;
+    d.heads_kv = a.Hk;
+    d.len_q = a.L;
+    d.len_kv = a.S;
+    d.head_dim = a.D;
+    d.head_dim_v = a.Dv;
+    for (int i = 0; i < 4; ++i) {
+        d.q_stride[i] = q.stride(i);
+        d.k_stride[i] = k.stride(i);
+        d.v_stride[i] = v.stride(i);
+        d.bias_stride[i] = bias.defined() ? bias.stride(i) : 0;
+        d.out_stride[i] = out.stride(i);
+    }
+    for (int i = 0; i < 3; ++i) d.lse_stride[i] = lse.stride(i);
+    d.q = q.data_ptr();
+    d.k = k.data_ptr();
+    d.v = v.data_ptr();
+    d.bias = bias.defined() ? bias.data_ptr() : nullptr;
+    d.out = out.data_ptr();
+    d.lse = lse.data_ptr<float>();
+    d.scale = a.scale;
+    d.stream = stream_of(q);
+    return d;
+}
+
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, c10::SymInt, c10::SymInt, at::Tensor, at::Tensor, at::Tensor>
 sdpa_forward(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
              const std::optional<at::Tensor>& attn_bias, double dropout_p, bool is_causal, bool /*return_debug_mask*/,
@@ -125,34 +159,7 @@ sdpa_forward(const at::Tensor& query, const at::Tensor& key, const at::Tensor& v
     if (kernel_takes(a.q.scalar_type(), a.D, a.Dv, a.B, a.Hq) && a.B * a.Hq * a.L > 0) {
         const at::Tensor q = kernel_layout(a.q), k = kernel_layout(a.k), v = kernel_layout(a.v);
         at::Tensor bias = a.bias.defined() ? a.bias.expand({a.B, a.Hq, a.L, a.S}) : at::Tensor();
-        tvk_attention_desc d;
-        std::memset(&d, 0, sizeof(d));
-        bool ok = false;
-        d.dtype = tvk_dtype_of(a.q.scalar_type(), ok);
-        d.causal = a.causal ? 1 : 0;
-        d.batch = a.B;
-        d.heads_q = a.Hq;
-        d.heads_kv = a.Hk;
-        d.len_q = a.L;
-        d.len_kv = a.S;
-        d.head_dim = a.D;
-        d.head_dim_v = a.Dv;
-        for (int i = 0; i < 4; ++i) {
-            d.q_stride[i] = q.stride(i);
-            d.k_stride[i] = k.stride(i);
-            d.v_stride[i] = v.stride(i);
-            d.bias_stride[i] = bias.defined() ? bias.stride(i) : 0;
-            d.out_stride[i] = out.stride(i);
-        }
-        for (int i = 0; i < 3; ++i) d.lse_stride[i] = lse.stride(i);
-        d.q = q.data_ptr();
-        d.k = k.data_ptr();
-        d.v = v.data_ptr();
-        d.bias = bias.defined() ? bias.data_ptr() : nullptr;
-        d.out = out.data_ptr();
-        d.lse = lse.data_ptr<float>();
-        d.scale = a.scale;
-        d.stream = stream_of(query);
+        tvk_attention_desc d = forward_desc(a, q, k, v, bias, out, lse);
         st = tvk_attention_fwd(&d);
         if (st != TVK_ERR_UNSUPPORTED) check_status(st, "tvk_attention_fwd");
     } else if (a.B * a.Hq * a.L == 0) {
@@ -189,9 +196,36 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sdpa_backward(
     TORCH_CHECK(dropout_p == 0.0, "torchvulkan [ERROR]: fused attention doesn't support dropout; it runs on the math backend.");
     Attn a = prepare(query, key, value, attn_bias, is_causal, scale);
     if (!grad_input_mask[0] && !grad_input_mask[1] && !grad_input_mask[2] && !grad_input_mask[3]) return {};
-    TVKB_FALLBACK("The attention backward runs on the CPU.");
-    // chunked_backward (src/api/ops/attention.cpp:141-199) over all rows
     const bool want_bias = grad_input_mask[3] && attn_bias.defined();
+    if (!want_bias && kernel_takes(a.q.scalar_type(), a.D, a.Dv, a.B, a.Hq) && out.scalar_type() == a.q.scalar_type()) {
+        const at::Tensor q = kernel_layout(a.q), k = kernel_layout(a.k), v = kernel_layout(a.v);
+        const at::Tensor dout = kernel_layout(grad_out.scalar_type() == a.q.scalar_type() ? grad_out : grad_out.to(a.q.scalar_type()));
+        at::Tensor bias = a.bias.defined() ? a.bias.expand({a.B, a.Hq, a.L, a.S}) : at::Tensor();
+        const at::Tensor lse = logsumexp.scalar_type() == at::kFloat ? logsumexp : logsumexp.to(at::kFloat);
+        at::Tensor gq = at::empty({a.B, a.Hq, a.L, a.D}, a.q.options());
+        at::Tensor gk = at::empty({a.B, a.Hk, a.S, a.D}, a.q.options());
+        at::Tensor gv = at::empty({a.B, a.Hk, a.S, a.Dv}, a.q.options());
+        tvk_attention_bwd_desc bd;
+        std::memset(&bd, 0, sizeof(bd));
+        bd.fwd = forward_desc(a, q, k, v, bias, out, lse);
+        bd.dout = dout.data_ptr();
+        bd.dq = gq.data_ptr();
+        bd.dk = gk.data_ptr();
+        bd.dv = gv.data_ptr();
+        for (int i = 0; i < 4; ++i) {
+            bd.dout_stride[i] = dout.stride(i);
+            bd.dq_stride[i] = gq.stride(i);
+            bd.dk_stride[i] = gk.stride(i);
+            bd.dv_stride[i] = gv.stride(i);
+        }
+        const tvk_status st = tvk_attention_bwd(&bd);
+        if (st != TVK_ERR_UNSUPPORTED) {
+            check_status(st, "tvk_attention_bwd");
+            return {gq, gk, gv, at::Tensor()};
+        }
+    }
+    TVKB_FALLBACK("This attention backward runs on the CPU.");
+    // chunked_backward (src/api/ops/attention.cpp:141-199) over all rows
     at::Tensor q = a.q.cpu().to(at::kFloat), k = a.k.cpu().to(at::kFloat), v = a.v.cpu().to(at::kFloat);
     at::Tensor dout = grad_out.cpu().to(at::kFloat);
     at::Tensor bias = a.bias.defined() ? a.bias.cpu().to(at::kFloat).expand({a.B, a.Hq, a.L, a.S}) : at::Tensor();
