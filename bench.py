@@ -35,7 +35,7 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 # profiles/gemm_fp16_8192_counters.md. Counters need their own profiler runs, so the figure is
 # recorded here per kernel plan rather than measured inside the timed region.
 MEASURED_TRAFFIC = {
-    "gemm16_dma_256x256": {"bytes": 1.768e9, "fetch_kib": 796263, "write_kib": 133943},
+    "gemm16_dma_256x256": {"bytes": 1.764e9, "fetch_kib": 795667, "write_kib": 131072},
 }
 
 
@@ -360,7 +360,26 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     att_flops = 32 * 8 * (256 * 257 // 2) * 64 * 2 * 2
     out["c3_attention_fwd_us"] = round(ms * 1e3, 2)
     out["c3_attention_fwd_tflops"] = round(att_flops / (ms * 1e-3) / 1e12, 2)
-    del qa, ka, va, oa, la
+    # backward: five products over the unmasked half (S, dP, dV, dQ, dK; S is recomputed in both passes)
+    da = torch.randn(oa.shape, generator=g).to(torch.float16).to(dev)
+    gq, gk, gv = torch.empty_like(qa), torch.empty_like(ka), torch.empty_like(va)
+    bd = _abi.AttentionBwdDesc()
+    bd.fwd = ad
+    bd.dout, bd.dout_stride = da.data_ptr(), _abi.I64x4(*da.stride())
+    bd.dq, bd.dq_stride = gq.data_ptr(), _abi.I64x4(*gq.stride())
+    bd.dk, bd.dk_stride = gk.data_ptr(), _abi.I64x4(*gk.stride())
+    bd.dv, bd.dv_stride = gv.data_ptr(), _abi.I64x4(*gv.stride())
+    br_ = C.byref(bd)
+
+    def attn_bwd_step():
+        st_ = lib.tvk_attention_bwd(br_)
+        if st_:
+            _abi.check(st_)
+
+    ms, _ = timed(attn_bwd_step, steps * 4, warmup, stream)
+    out["c3_attention_bwd_us"] = round(ms * 1e3, 2)
+    out["c3_attention_bwd_tflops"] = round(att_flops * 5 / 2 / (ms * 1e-3) / 1e12, 2)
+    del qa, ka, va, oa, la, da, gq, gk, gv
 
     # ---- C5 ragged [1000,777]x[777,3000] and baddbmm in[64,512,512] + 0.5*bmm ----
     a = torch.randn((1000, 777), generator=g).to(torch.float16).to(dev)
