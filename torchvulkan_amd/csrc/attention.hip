@@ -7,8 +7,8 @@
 // with no unmasked key gives 0 and lse = +inf; the probabilities are staged
 // in the dtype before the product with v (src/shaders/ops/attention_coop.slang).
 //
-// Kernel: one workgroup of 4 waves owns 128 queries of one (batch, head);
-// each wave owns 32 of them as two 16-query columns. Keys go by tiles of 64:
+// Kernel: one workgroup of 4 waves owns 64 or 128 queries of one (batch, head);
+// each wave owns one or two 16-query columns of them. Keys go by tiles of 64:
 // K and V tiles are loaded into registers one tile ahead and parked in a
 // double-buffered LDS pair. Per tile each wave computes the transposed scores
 // S^T = K Q^T with v_mfma_f32_16x16x32 (keys on rows, queries on columns):
@@ -68,8 +68,9 @@ __device__ inline uint32_t pack2(float lo, float hi) {
 __device__ inline float xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m)); }
 __device__ inline float xor_sum(float v, int m) { return v + __shfl_xor(v, m); }
 
-template <int DT, int D, bool CAUSAL, bool BIAS>
+template <int DT, int D, bool CAUSAL, bool BIAS, int QPW>
 __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
+    constexpr int BMQ = 16 * QPW * AT_WAVES;   // queries per workgroup
     constexpr int DS = D / 32;          // 32-wide d steps of the score product
     constexpr int DT16 = D / 16;        // 16-wide dv tiles of the output
     constexpr int LDK = D + 8;          // LDS row pitch (halfs)
@@ -83,16 +84,16 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
     const int g = lane / 16, c16 = lane % 16;
     const int b = blockIdx.z, h = blockIdx.y;
     const int hk = h / p.group;
-    const int q0 = blockIdx.x * AT_BM + wave * 32;   // this wave's first query
+    const int q0 = blockIdx.x * BMQ + wave * 16 * QPW;   // this wave's first query
 
     const uint16_t* Q = p.q + (int64_t)b * p.sq[0] + (int64_t)h * p.sq[1];
     const uint16_t* K = p.k + (int64_t)b * p.sk[0] + (int64_t)hk * p.sk[1];
     const uint16_t* V = p.v + (int64_t)b * p.sv[0] + (int64_t)hk * p.sv[1];
 
     // Q^T as the B operand: lane holds query q0+16qt+c16, d = 32ds + 8g .. +7
-    u32x4 qf[2][DS];
+    u32x4 qf[QPW][DS];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QPW; ++qt) {
         const int qi = q0 + 16 * qt + c16;
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds)
@@ -100,16 +101,21 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
                                   : u32x4{0, 0, 0, 0};
     }
 
-    f32x4 oacc[DT16][2];
+    f32x4 oacc[DT16][QPW];
 #pragma unroll
     for (int i = 0; i < DT16; ++i)
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) oacc[i][qt] = f32x4{0, 0, 0, 0};
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+        for (int qt = 0; qt < QPW; ++qt) oacc[i][qt] = f32x4{0, 0, 0, 0};
+    float m_run[QPW], l_run[QPW];
+#pragma unroll
+    for (int qt = 0; qt < QPW; ++qt) {
+        m_run[qt] = -INFINITY;
+        l_run[qt] = 0.0f;
+    }
 
     int ntiles = (p.S + AT_BN - 1) / AT_BN;
     if (CAUSAL) {
-        const int last_q = min(p.L, (int)blockIdx.x * AT_BM + AT_BM) - 1;   // keys beyond it are masked for the block
+        const int last_q = min(p.L, (int)blockIdx.x * BMQ + BMQ) - 1;   // keys beyond it are masked for the block
         ntiles = min(ntiles, last_q / AT_BN + 1);
     }
 
@@ -150,23 +156,23 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
         if (j + 1 < ntiles) load_tile(j + 1);   // in flight while this tile computes
 
         // ---- S^T = K Q^T over 4 key blocks x 2 query columns
-        f32x4 sacc[4][2];
+        f32x4 sacc[4][QPW];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) sacc[kt][qt] = f32x4{0, 0, 0, 0};
+            for (int qt = 0; qt < QPW; ++qt) sacc[kt][qt] = f32x4{0, 0, 0, 0};
 #pragma unroll
             for (int ds = 0; ds < DS; ++ds) {
                 const u32x4 kf = *reinterpret_cast<const u32x4*>(&ks[buf][(kt * 16 + c16) * LDK + 32 * ds + 8 * g]);
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) sacc[kt][qt] = mfma16<DT>(kf, qf[qt][ds], sacc[kt][qt]);
+                for (int qt = 0; qt < QPW; ++qt) sacc[kt][qt] = mfma16<DT>(kf, qf[qt][ds], sacc[kt][qt]);
             }
         }
 
         // ---- scale, bias, masks; online softmax per query column
-        float alpha[2];
+        float alpha[QPW];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
+        for (int qt = 0; qt < QPW; ++qt) {
             const int qi = q0 + 16 * qt + c16;
             float tmax = -INFINITY;
 #pragma unroll
@@ -203,16 +209,16 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
 #pragma unroll
         for (int i = 0; i < DT16; ++i)
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt)
+            for (int qt = 0; qt < QPW; ++qt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) oacc[i][qt][r] *= alpha[qt];
 
         // ---- O^T += V^T P^T: two 32-key products, k-slots in the S^T lane order
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            u32x4 pf[2];
+            u32x4 pf[QPW];
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+            for (int qt = 0; qt < QPW; ++qt) {
                 const f32x4 a = sacc[2 * kk][qt], c = sacc[2 * kk + 1][qt];
                 pf[qt] = u32x4{pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]), pack2<DT>(c[2], c[3])};
             }
@@ -229,7 +235,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
                     vf[2 * rr + 1] = w.y;
                 }
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) oacc[i][qt] = mfma16<DT>(vf, pf[qt], oacc[i][qt]);
+                for (int qt = 0; qt < QPW; ++qt) oacc[i][qt] = mfma16<DT>(vf, pf[qt], oacc[i][qt]);
             }
         }
 
@@ -242,7 +248,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
     // ---- O = O^T / l; lse = m + log l (+inf for a row that attended to nothing)
     uint16_t* O = p.out + (int64_t)b * p.so[0] + (int64_t)h * p.so[1];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QPW; ++qt) {
         const int qi = q0 + 16 * qt + c16;
         if (qi >= p.L) continue;
         const float inv = l_run[qt] > 0.0f ? 1.0f / l_run[qt] : 0.0f;
@@ -265,15 +271,28 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
     }
 }
 
-template <int DT, int D>
-void launch_attn(const AttnArgs& a, bool causal, bool bias, dim3 grid, hipStream_t s) {
+template <int DT, int D, int QPW>
+void launch_attn_q(const AttnArgs& a, bool causal, bool bias, dim3 grid, hipStream_t s) {
     const dim3 block(64 * AT_WAVES);
     if (causal) {
-        if (bias) hipLaunchKernelGGL((attn_fwd_kernel<DT, D, true, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((attn_fwd_kernel<DT, D, true, false>), grid, block, 0, s, a);
+        if (bias) hipLaunchKernelGGL((attn_fwd_kernel<DT, D, true, true, QPW>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_fwd_kernel<DT, D, true, false, QPW>), grid, block, 0, s, a);
     } else {
-        if (bias) hipLaunchKernelGGL((attn_fwd_kernel<DT, D, false, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((attn_fwd_kernel<DT, D, false, false>), grid, block, 0, s, a);
+        if (bias) hipLaunchKernelGGL((attn_fwd_kernel<DT, D, false, true, QPW>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_fwd_kernel<DT, D, false, false, QPW>), grid, block, 0, s, a);
+    }
+}
+
+// Query columns per wave: two (128 queries per workgroup) when that still gives
+// the device plenty of workgroups, else one (64 per workgroup): more, lighter
+// waves per SIMD to hide the latency of each tile's softmax chain.
+template <int DT, int D>
+void launch_attn(const AttnArgs& a, bool causal, bool bias, int64_t batch, int64_t heads, int64_t L, hipStream_t s) {
+    const int64_t blocks128 = batch * heads * ((L + 127) / 128);
+    if (blocks128 >= 2048) {
+        launch_attn_q<DT, D, 2>(a, causal, bias, dim3((unsigned)((L + 127) / 128), (unsigned)heads, (unsigned)batch), s);
+    } else {
+        launch_attn_q<DT, D, 1>(a, causal, bias, dim3((unsigned)((L + 63) / 64), (unsigned)heads, (unsigned)batch), s);
     }
 }
 
@@ -696,15 +715,14 @@ extern "C" tvk_status tvk_attention_fwd(const tvk_attention_desc* d) {
     a.causal = d->causal != 0;
     a.out_vec = d->out_stride[3] == 1 && (reinterpret_cast<uintptr_t>(d->out) & 7) == 0 && d->out_stride[2] % 4 == 0 &&
                 d->out_stride[1] % 4 == 0 && d->out_stride[0] % 4 == 0;
-    const dim3 grid((unsigned)((d->len_q + AT_BM - 1) / AT_BM), (unsigned)d->heads_q, (unsigned)d->batch);
     const hipStream_t s = resolve_stream(d->stream);
     const bool bias = d->bias != nullptr;
     if (d->dtype == TVK_F16) {
-        if (d->head_dim == 64) launch_attn<TVK_F16, 64>(a, a.causal, bias, grid, s);
-        else launch_attn<TVK_F16, 128>(a, a.causal, bias, grid, s);
+        if (d->head_dim == 64) launch_attn<TVK_F16, 64>(a, a.causal, bias, d->batch, d->heads_q, d->len_q, s);
+        else launch_attn<TVK_F16, 128>(a, a.causal, bias, d->batch, d->heads_q, d->len_q, s);
     } else {
-        if (d->head_dim == 64) launch_attn<TVK_BF16, 64>(a, a.causal, bias, grid, s);
-        else launch_attn<TVK_BF16, 128>(a, a.causal, bias, grid, s);
+        if (d->head_dim == 64) launch_attn<TVK_BF16, 64>(a, a.causal, bias, d->batch, d->heads_q, d->len_q, s);
+        else launch_attn<TVK_BF16, 128>(a, a.causal, bias, d->batch, d->heads_q, d->len_q, s);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_attention_fwd: launch failed: ") + hipGetErrorString(e));

@@ -523,7 +523,7 @@ __global__ __launch_bounds__(256) void repack16_kernel(const uint16_t* src, uint
 // host dispatch
 // ----------------------------------------------------------------------------
 
-enum class Kern { K0, GENERIC, SEQ256, SEQ128, MFMA256, MFMA256W8, MFMA128, SKINNY, DMA256, DMA128 };
+enum class Kern { K0, GENERIC, SEQ256, SEQ128, SEQ64, MFMA256, MFMA256W8, MFMA128, SKINNY, DMA256, DMA128 };
 
 struct Plan {
     Kern kern;
@@ -625,6 +625,12 @@ Plan make_plan(const tvk_gemm_desc& d) {
     if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
         pl.kern = big ? Kern::SEQ256 : Kern::SEQ128;
         pl.name = big ? "gemm_seq_mfma_256x256" : "gemm_seq_mfma_128x128";
+        // fewer 128x128 tiles than half the CUs: 64x128 tiles, twice the workgroups
+        // (the smallest tile of the 2x2 waves of 32x64 rank-1 MFMA; same k order)
+        if (!big && ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch < 128) {
+            pl.kern = Kern::SEQ64;
+            pl.name = "gemm_seq_mfma_64x128";
+        }
     } else if (big && pl.vec && dma_applies(repacked_args(d, pl), a_k, b_k)) {
         pl.kern = Kern::DMA256;
         pl.name = "gemm16_dma_256x256";
@@ -764,13 +770,16 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
             hipLaunchKernelGGL(gemm_generic_kernel<DT>, dim3((unsigned)((d.N + 15) / 16), (unsigned)((d.M + 15) / 16), nb), dim3(256), 0, s, q);
             break;
         case Kern::SEQ256:
-        case Kern::SEQ128: {
-            const int T = pl.kern == Kern::SEQ256 ? 256 : 128;
-            q.tiles_m = (int)((d.M + T - 1) / T);
-            q.tiles_n = (int)((d.N + T - 1) / T);
+        case Kern::SEQ128:
+        case Kern::SEQ64: {
+            const int TM = pl.kern == Kern::SEQ256 ? 256 : pl.kern == Kern::SEQ128 ? 128 : 64;
+            const int TN = pl.kern == Kern::SEQ256 ? 256 : 128;
+            q.tiles_m = (int)((d.M + TM - 1) / TM);
+            q.tiles_n = (int)((d.N + TN - 1) / TN);
             dim3 grid(q.tiles_m * q.tiles_n, nb);
-            if (T == 256) launch_seq<DT, 256, 256>(pl, q, grid, s);
-            else launch_seq<DT, 128, 128>(pl, q, grid, s);
+            if (TM == 256) launch_seq<DT, 256, 256>(pl, q, grid, s);
+            else if (TM == 128) launch_seq<DT, 128, 128>(pl, q, grid, s);
+            else launch_seq<DT, 64, 128>(pl, q, grid, s);
             break;
         }
         case Kern::SKINNY:
