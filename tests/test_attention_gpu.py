@@ -61,6 +61,32 @@ def test_ragged_lengths_and_head_dim_128(gpu, dtype):
     check(q2, k2, v2, causal=True, scale=0.2, what="causal L 300 > S 70")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_wide_grid_two_query_columns_per_wave(gpu, dtype, causal):
+    # batch*heads*ceil(L/128) >= 2048 selects 128-query workgroups (two 16-query
+    # columns per wave); the oracle checks a few (batch, head) slices
+    B, Hq, Hk, L, D = 16, 16, 4, 1024, 64
+    q, k, v = rand((B, Hq, L, D), dtype, 60), rand((B, Hk, L, D), dtype, 61), rand((B, Hk, L, D), dtype, 62)
+    out, lse = _abi.attention_fwd(q.to(DEV), k.to(DEV), v.to(DEV), None, causal)
+    torch.cuda.synchronize()
+    out, lse = f64(out), lse.cpu().double().numpy()
+    for b, h in ((0, 0), (5, 9), (15, 15)):
+        hk = h // (Hq // Hk)
+        ro, rl = orc.attention(f64(q[b:b + 1, h:h + 1]), f64(k[b:b + 1, hk:hk + 1]), f64(v[b:b + 1, hk:hk + 1]),
+                               None, causal)
+        assert_close(out[b:b + 1, h:h + 1], ro, dtype, f"b {b} h {h}: out")
+        assert (np.abs(lse[b:b + 1, h:h + 1] - rl) <= 1e-3 * (np.abs(rl) + 1)).all(), f"b {b} h {h}: lse"
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_negative_and_zero_scale(gpu, causal):
+    dtype = torch.float16
+    q, k, v = rand((2, 4, 130, 64), dtype, 63), rand((2, 4, 130, 64), dtype, 64), rand((2, 4, 130, 64), dtype, 65)
+    check(q, k, v, causal=causal, scale=-0.3, what=f"scale -0.3 causal={causal}")
+    check(q, k, v, causal=causal, scale=0.0, what=f"scale 0 causal={causal}")
+
+
 def test_bias_broadcast_and_masked_rows(gpu):
     dtype = torch.float16
     q, k, v = rand((2, 4, 64, 64), dtype, 10), rand((2, 4, 96, 64), dtype, 11), rand((2, 4, 96, 64), dtype, 12)

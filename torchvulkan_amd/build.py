@@ -50,9 +50,17 @@ def _run(cmd: list[str]) -> None:
         print(out)
 
 
+# The attention kernels keep every MFMA accumulator in VGPRs: their softmax
+# and rescale steps work on the accumulators with ordinary VALU instructions,
+# which the AGPR form would surround with accvgpr copies.
+FILE_FLAGS = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    _run([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
+    _run([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)])
     return obj
 
 

@@ -13,14 +13,23 @@
 // double-buffered LDS pair. Per tile each wave computes the transposed scores
 // S^T = K Q^T with v_mfma_f32_16x16x32 (keys on rows, queries on columns):
 // lane l then holds query l%16 and keys 4(l/16)+r of every 16-key block, so
-// the softmax row statistics need one lane-local pass and two cross-lane
-// steps (xor 16, xor 32). The same accumulator layout is already the B
-// operand of O^T = V^T P^T once rounded to the dtype: the 32 k-slots of one
-// product are keys {4g..4g+3, 16+4g..16+4g+3} of the 16-lane group g, and
-// V^T is read in exactly that key order with ds_read_b64_tr_b16 (four keys
-// of one dv column per lane). Online softmax: the running max m and sum l of
-// each query rescale O by exp(m_old - m_new) per tile; exp is v_exp_f32 on
-// log2-scaled arguments.
+// a query's row statistics are one lane-local pass plus two lane swaps
+// (v_permlane32_swap, v_permlane16_swap). The same accumulator layout is
+// already the B operand of O^T = V^T P^T once rounded to the dtype (one
+// v_cvt_pk per pair): the 32 k-slots of one product are keys
+// {4g..4g+3, 16+4g..16+4g+3} of the 16-lane group g, and V^T is read in
+// exactly that key order with ds_read_b64_tr_b16 (four keys of one dv column
+// per lane).
+//
+// Online softmax in log2 units: with c = |scale|*log2(e) (q negated when the
+// scale is negative, which is exact), the running max m of c*q.k and the
+// probabilities exp2(c*q.k - m) come from the raw accumulators with one fma
+// each. Masks are applied only on the tiles that reach past the last key or
+// cross the causal diagonal; a bias switches every tile to the explicit
+// scale*q.k + bias path. O is rescaled by exp2(m_old - m_new) only when some
+// query's max moved (a factor of exactly 1 otherwise), and each lane keeps
+// its own partial row sum l, reduced across the four lane groups once at the
+// end (l and O share every rescale factor).
 #include "gemm_common.h"
 
 #include <algorithm>
@@ -30,12 +39,16 @@ namespace tvk {
 namespace {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 #define TVK_LDS __attribute__((address_space(3)))
 
 constexpr int AT_WAVES = 4;
-constexpr int AT_BM = 32 * AT_WAVES;   // queries per workgroup
+constexpr int AT_BM = 32 * AT_WAVES;   // queries per workgroup of the dq pass
 constexpr int AT_BN = 64;              // keys per tile
 constexpr float AT_LOG2E = 1.4426950408889634f;
+constexpr float AT_LN2 = 0.6931471805599453f;
 
 struct AttnArgs {
     const uint16_t* q;
@@ -46,9 +59,11 @@ struct AttnArgs {
     float* lse;
     int64_t sq[4], sk[4], sv[4], sb[4], so[4], sl[3];
     int L, S, Hq, group;
-    float scale;
-    int causal;
-    int out_vec;   // out rows 8-byte aligned with unit dv stride
+    int nqb, BH;       // query tiles per (batch, head); batch * heads
+    float scale;       // signed scale (bias path)
+    float c2;          // |scale| * log2(e) (no-bias path)
+    uint32_t qflip;    // sign bits flipped into q on the no-bias path when scale < 0
+    int out_vec;       // out rows 8-byte aligned with unit dv stride
 };
 
 template <int DT>
@@ -59,36 +74,153 @@ __device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Two floats rounded to nearest even into one packed pair (v_cvt_pk_f16_f32 /
+// v_cvt_pk_bf16_f32), lo in the low half.
 template <int DT>
 __device__ inline uint32_t pack2(float lo, float hi) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, elem<DT>::from_f32(lo)) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, elem<DT>::from_f32(hi)) << 16);
+    if constexpr (DT == TVK_F16)
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{lo, hi}, f16x2v));
+    else
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{lo, hi}, bf16x2v));
 }
 
 __device__ inline float xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m)); }
 __device__ inline float xor_sum(float v, int m) { return v + __shfl_xor(v, m); }
 
+// Max / sum over lanes {l, l^16, l^32, l^48}: permlane32_swap of a value with
+// itself hands each lane its partner l^32, permlane16_swap then l^16. Every
+// lane of the four ends with the same bits.
+__device__ inline float lanes4_max(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+    const uint32_t w = __builtin_bit_cast(uint32_t, v);
+    const auto c = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)c[0]), __builtin_bit_cast(float, (uint32_t)c[1]));
+}
+__device__ inline float lanes4_sum(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
+    const uint32_t w = __builtin_bit_cast(uint32_t, v);
+    const auto c = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return __builtin_bit_cast(float, (uint32_t)c[0]) + __builtin_bit_cast(float, (uint32_t)c[1]);
+}
+
+// Workgroup -> (query tile qb, batch*head bh). Workgroups are dealt to the 8
+// XCDs round robin (id % 8); when batch*heads is a multiple of 8 each
+// (batch, head) stays on one XCD, so its K and V tiles are shared in that
+// XCD's L2. Causal rows do work in proportion to their query tile: the
+// heaviest tiles are dealt first, every XCD taking the same mix.
+template <bool CAUSAL>
+__device__ inline void attn_block(const AttnArgs& p, int& qb, int& bh) {
+    const int id = blockIdx.x;
+    if (p.BH % 8 == 0) {
+        const int xcd = id % 8, local = id / 8, per = p.BH / 8;
+        if (CAUSAL) {
+            qb = p.nqb - 1 - local / per;
+            bh = (local % per) * 8 + xcd;
+        } else {
+            qb = local % p.nqb;
+            bh = (local / p.nqb) * 8 + xcd;
+        }
+    } else if (CAUSAL) {
+        qb = p.nqb - 1 - id / p.BH;
+        bh = id % p.BH;
+    } else {
+        qb = id % p.nqb;
+        bh = id / p.nqb;
+    }
+}
+
+// One key tile of the online softmax for QPW query columns: scores from the
+// accumulators (PLAIN: no mask reaches the tile and no bias, so max and
+// exponent work on the raw products), running max m and per-lane sum l
+// updated, probabilities left in sacc, rescale factors in alpha.
+template <int DT, bool PLAIN, bool BIAS, bool CAUSAL, int QPW>
+__device__ inline void softmax_tile(const AttnArgs& p, f32x4 (&sacc)[4][QPW], float (&m_run)[QPW], float (&l_run)[QPW],
+                                    float (&alpha)[QPW], int k0, int q0, int b, int h, int g, int c16) {
+#pragma unroll
+    for (int qt = 0; qt < QPW; ++qt) {
+        float tmax = -INFINITY;
+        if (PLAIN) {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[kt][qt][r]);
+            tmax = lanes4_max(tmax) * p.c2;
+        } else {
+            const int qi = q0 + 16 * qt + c16;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int kj = k0 + kt * 16 + 4 * g + r;
+                    float s;
+                    if (BIAS) {
+                        s = sacc[kt][qt][r] * p.scale;
+                        if (kj < p.S && qi < p.L) {
+                            const uint16_t bv = p.bias[(int64_t)b * p.sb[0] + (int64_t)h * p.sb[1] + (int64_t)qi * p.sb[2] + (int64_t)kj * p.sb[3]];
+                            s = s + elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, bv));
+                        }
+                        s *= AT_LOG2E;
+                    } else {
+                        s = sacc[kt][qt][r] * p.c2;
+                    }
+                    if (kj >= p.S || (CAUSAL && kj > qi)) s = -INFINITY;
+                    sacc[kt][qt][r] = s;
+                    tmax = fmaxf(tmax, s);
+                }
+            tmax = lanes4_max(tmax);
+        }
+        const float m_old = m_run[qt];
+        const float m_new = fmaxf(m_old, tmax);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        // O and l are still 0 while m_old is -inf
+        alpha[qt] = (m_old == m_new || m_old == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_old - m_use);
+        float rsum = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float x = PLAIN ? __builtin_fmaf(sacc[kt][qt][r], p.c2, -m_use) : sacc[kt][qt][r] - m_use;
+                const float e = __builtin_amdgcn_exp2f(x);
+                sacc[kt][qt][r] = e;
+                rsum += e;
+            }
+        l_run[qt] = l_run[qt] * alpha[qt] + rsum;
+        m_run[qt] = m_new;
+    }
+}
+
+// One 16-query column per wave at head_dim 64 without a bias fits 128 VGPRs: four waves per
+// SIMD, the occupancy the 39 KB of LDS per workgroup allows.
 template <int DT, int D, bool CAUSAL, bool BIAS, int QPW>
-__global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
+__global__ __launch_bounds__(64 * AT_WAVES) __attribute__((amdgpu_waves_per_eu(D == 64 && QPW == 1 && !BIAS ? 4 : 1)))
+void attn_fwd_kernel(AttnArgs p) {
     constexpr int BMQ = 16 * QPW * AT_WAVES;   // queries per workgroup
     constexpr int DS = D / 32;          // 32-wide d steps of the score product
     constexpr int DT16 = D / 16;        // 16-wide dv tiles of the output
-    constexpr int LDK = D + 8;          // LDS row pitch (halfs)
+    // LDS row pitches (halfs): K rows step 4 banks (16-byte reads of 8
+    // consecutive rows cover all 32 banks once), V rows step 8 banks (the
+    // transposed 8-byte reads of 4 consecutive rows cover all 32 banks once)
+    constexpr int LDK = D + 8;
+    constexpr int LDV = D + 16;
     constexpr int CH = AT_BN * D / 8;   // 16-byte chunks per K (or V) tile
     constexpr int CPT = CH / (64 * AT_WAVES);
     static_assert(CPT * 64 * AT_WAVES == CH, "whole chunks per thread");
     __shared__ __attribute__((aligned(16))) uint16_t ks[2][AT_BN * LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t vs[2][AT_BN * LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t vs[2][AT_BN * LDV];
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
     const int g = lane / 16, c16 = lane % 16;
-    const int b = blockIdx.z, h = blockIdx.y;
+    int qb, bh;
+    attn_block<CAUSAL>(p, qb, bh);
+    const int b = bh / p.Hq, h = bh % p.Hq;
     const int hk = h / p.group;
-    const int q0 = blockIdx.x * BMQ + wave * 16 * QPW;   // this wave's first query
+    const int q0 = qb * BMQ + wave * 16 * QPW;   // this wave's first query
 
     const uint16_t* Q = p.q + (int64_t)b * p.sq[0] + (int64_t)h * p.sq[1];
-    const uint16_t* K = p.k + (int64_t)b * p.sk[0] + (int64_t)hk * p.sk[1];
-    const uint16_t* V = p.v + (int64_t)b * p.sv[0] + (int64_t)hk * p.sv[1];
 
     // Q^T as the B operand: lane holds query q0+16qt+c16, d = 32ds + 8g .. +7
     u32x4 qf[QPW][DS];
@@ -96,9 +228,12 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
     for (int qt = 0; qt < QPW; ++qt) {
         const int qi = q0 + 16 * qt + c16;
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds)
-            qf[qt][ds] = qi < p.L ? *reinterpret_cast<const u32x4*>(Q + (int64_t)qi * p.sq[2] + 32 * ds + 8 * g)
-                                  : u32x4{0, 0, 0, 0};
+        for (int ds = 0; ds < DS; ++ds) {
+            u32x4 x = qi < p.L ? *reinterpret_cast<const u32x4*>(Q + (int64_t)qi * p.sq[2] + 32 * ds + 8 * g)
+                               : u32x4{0, 0, 0, 0};
+            if (!BIAS) x ^= p.qflip;
+            qf[qt][ds] = x;
+        }
     }
 
     f32x4 oacc[DT16][QPW];
@@ -106,7 +241,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
     for (int i = 0; i < DT16; ++i)
 #pragma unroll
         for (int qt = 0; qt < QPW; ++qt) oacc[i][qt] = f32x4{0, 0, 0, 0};
-    float m_run[QPW], l_run[QPW];
+    float m_run[QPW], l_run[QPW];   // m in log2 units; l a per-lane partial sum
 #pragma unroll
     for (int qt = 0; qt < QPW; ++qt) {
         m_run[qt] = -INFINITY;
@@ -115,47 +250,65 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
 
     int ntiles = (p.S + AT_BN - 1) / AT_BN;
     if (CAUSAL) {
-        const int last_q = min(p.L, (int)blockIdx.x * BMQ + BMQ) - 1;   // keys beyond it are masked for the block
+        const int last_q = min(p.L, qb * BMQ + BMQ) - 1;   // keys beyond it are masked for the block
         ntiles = min(ntiles, last_q / AT_BN + 1);
     }
 
-    u32x4 kreg[CPT], vreg[CPT];
-    auto load_tile = [&](int j) {
+    // K/V tile loads: a uniform base per tile plus a 32-bit byte offset per chunk
+    const char* Kh = reinterpret_cast<const char*>(p.k + (int64_t)b * p.sk[0] + (int64_t)hk * p.sk[1]);
+    const char* Vh = reinterpret_cast<const char*>(p.v + (int64_t)b * p.sv[0] + (int64_t)hk * p.sv[1]);
+    const int64_t kstep = (int64_t)AT_BN * p.sk[2] * 2, vstep = (int64_t)AT_BN * p.sv[2] * 2;
+    uint32_t koff[CPT], voff[CPT];
+    int krow[CPT];
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) {
-            const int c = tid + i * 64 * AT_WAVES;
-            const int key = c / (D / 8), d8 = (c % (D / 8)) * 8;
-            const int kj = j * AT_BN + key;
-            if (kj < p.S) {
-                kreg[i] = *reinterpret_cast<const u32x4*>(K + (int64_t)kj * p.sk[2] + d8);
-                vreg[i] = *reinterpret_cast<const u32x4*>(V + (int64_t)kj * p.sv[2] + d8);
-            } else {
-                kreg[i] = u32x4{0, 0, 0, 0};
-                vreg[i] = u32x4{0, 0, 0, 0};
+    for (int i = 0; i < CPT; ++i) {
+        const int c = tid + i * 64 * AT_WAVES;
+        krow[i] = c / (D / 8);
+        const int d8 = (c % (D / 8)) * 8;
+        koff[i] = (uint32_t)(((int64_t)krow[i] * p.sk[2] + d8) * 2);
+        voff[i] = (uint32_t)(((int64_t)krow[i] * p.sv[2] + d8) * 2);
+    }
+    // two register sets: tile j+2 is in flight while tile j computes and tile
+    // j+1 waits in registers for its LDS buffer
+    u32x4 kra[CPT], vra[CPT], krb[CPT], vrb[CPT];
+    auto load_tile = [&](int j, u32x4 (&kreg)[CPT], u32x4 (&vreg)[CPT]) {
+        const char* kt = Kh + (int64_t)j * kstep;
+        const char* vt = Vh + (int64_t)j * vstep;
+        if (j * AT_BN + AT_BN <= p.S) {
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) {
+                kreg[i] = *reinterpret_cast<const u32x4*>(kt + koff[i]);
+                vreg[i] = *reinterpret_cast<const u32x4*>(vt + voff[i]);
+            }
+        } else {
+            // rows past the last key are zeros: P is 0 there and V must be finite
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) {
+                if (j * AT_BN + krow[i] < p.S) {
+                    kreg[i] = *reinterpret_cast<const u32x4*>(kt + koff[i]);
+                    vreg[i] = *reinterpret_cast<const u32x4*>(vt + voff[i]);
+                } else {
+                    kreg[i] = u32x4{0, 0, 0, 0};
+                    vreg[i] = u32x4{0, 0, 0, 0};
+                }
             }
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](int buf, const u32x4 (&kreg)[CPT], const u32x4 (&vreg)[CPT]) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = tid + i * 64 * AT_WAVES;
             const int key = c / (D / 8), d8 = (c % (D / 8)) * 8;
             *reinterpret_cast<u32x4*>(&ks[buf][key * LDK + d8]) = kreg[i];
-            *reinterpret_cast<u32x4*>(&vs[buf][key * LDK + d8]) = vreg[i];
+            *reinterpret_cast<u32x4*>(&vs[buf][key * LDV + d8]) = vreg[i];
         }
     };
 
-    if (ntiles > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
-    __syncthreads();
-
-    for (int j = 0; j < ntiles; ++j) {
-        const int buf = j & 1;
-        if (j + 1 < ntiles) load_tile(j + 1);   // in flight while this tile computes
-
-        // ---- S^T = K Q^T over 4 key blocks x 2 query columns
+    auto compute_tile = [&](int j, int buf) {
+        const int k0 = j * AT_BN;
+        // a causal wave whose queries all precede the tile has nothing to add
+        if (CAUSAL && k0 > q0 + 16 * QPW - 1) return;
+        // ---- S^T = K Q^T over 4 key blocks x QPW query columns
         f32x4 sacc[4][QPW];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
@@ -169,49 +322,23 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
             }
         }
 
-        // ---- scale, bias, masks; online softmax per query column
+        // ---- online softmax per query column
         float alpha[QPW];
+        if (!BIAS && k0 + AT_BN <= p.S && !(CAUSAL && k0 + AT_BN - 1 > q0))
+            softmax_tile<DT, true, false, CAUSAL, QPW>(p, sacc, m_run, l_run, alpha, k0, q0, b, h, g, c16);
+        else
+            softmax_tile<DT, false, BIAS, CAUSAL, QPW>(p, sacc, m_run, l_run, alpha, k0, q0, b, h, g, c16);
+        bool rescale = false;
 #pragma unroll
-        for (int qt = 0; qt < QPW; ++qt) {
-            const int qi = q0 + 16 * qt + c16;
-            float tmax = -INFINITY;
+        for (int qt = 0; qt < QPW; ++qt) rescale = rescale || alpha[qt] != 1.0f;
+        if (__any(rescale)) {
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+            for (int i = 0; i < DT16; ++i)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int kj = j * AT_BN + kt * 16 + 4 * g + r;
-                    float s = sacc[kt][qt][r] * p.scale;
-                    if (BIAS && kj < p.S && qi < p.L) {
-                        const uint16_t bv = p.bias[(int64_t)b * p.sb[0] + (int64_t)h * p.sb[1] + (int64_t)qi * p.sb[2] + (int64_t)kj * p.sb[3]];
-                        s = s + elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, bv));
-                    }
-                    if (kj >= p.S || (CAUSAL && kj > qi)) s = -INFINITY;
-                    sacc[kt][qt][r] = s;
-                    tmax = fmaxf(tmax, s);
-                }
-            tmax = xor_max(xor_max(tmax, 16), 32);
-            const float m_new = fmaxf(m_run[qt], tmax);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            alpha[qt] = __builtin_amdgcn_exp2f((m_run[qt] - m_use) * AT_LOG2E);
-            float rsum = 0.0f;
+                for (int qt = 0; qt < QPW; ++qt)
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float e = __builtin_amdgcn_exp2f((sacc[kt][qt][r] - m_use) * AT_LOG2E);
-                    sacc[kt][qt][r] = e;
-                    rsum += e;
-                }
-            rsum = xor_sum(xor_sum(rsum, 16), 32);
-            l_run[qt] = l_run[qt] * alpha[qt] + rsum;
-            m_run[qt] = m_new;
+                    for (int r = 0; r < 4; ++r) oacc[i][qt][r] *= alpha[qt];
         }
-#pragma unroll
-        for (int i = 0; i < DT16; ++i)
-#pragma unroll
-            for (int qt = 0; qt < QPW; ++qt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) oacc[i][qt][r] *= alpha[qt];
 
         // ---- O^T += V^T P^T: two 32-key products, k-slots in the S^T lane order
 #pragma unroll
@@ -229,7 +356,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
 #pragma unroll
                 for (int rr = 0; rr < 2; ++rr) {
                     const int kr = 32 * kk + 16 * rr + 4 * g + c16 / 4;
-                    TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(TVK_LDS uint16_t*)&vs[buf][kr * LDK + 16 * i + (c16 % 4) * 4];
+                    TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(TVK_LDS uint16_t*)&vs[buf][kr * LDV + 16 * i + (c16 % 4) * 4];
                     const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
                     vf[2 * rr] = w.x;
                     vf[2 * rr + 1] = w.y;
@@ -238,20 +365,40 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
                 for (int qt = 0; qt < QPW; ++qt) oacc[i][qt] = mfma16<DT>(vf, pf[qt], oacc[i][qt]);
             }
         }
+    };
 
-        // buffer buf^1 was last read in iteration j-1, which every wave left
-        // through the barrier below: it can take tile j+1 now
-        if (j + 1 < ntiles) store_tile(buf ^ 1);
+    if (ntiles > 0) {
+        load_tile(0, kra, vra);
+        if (ntiles > 1) load_tile(1, krb, vrb);
+        store_tile(0, kra, vra);
+    }
+    __syncthreads();
+
+    // Two tiles per trip so the register sets stay fixed: LDS buffer j%2
+    // holds tile j. Each store goes to the buffer that the iteration before
+    // the last barrier finished reading.
+    for (int j = 0; j < ntiles; j += 2) {
+        if (j + 2 < ntiles) load_tile(j + 2, kra, vra);
+        compute_tile(j, 0);
+        if (j + 1 < ntiles) store_tile(1, krb, vrb);
+        __syncthreads();
+        if (j + 1 >= ntiles) break;
+        if (j + 3 < ntiles) load_tile(j + 3, krb, vrb);
+        compute_tile(j + 1, 1);
+        if (j + 2 < ntiles) store_tile(0, kra, vra);
         __syncthreads();
     }
 
-    // ---- O = O^T / l; lse = m + log l (+inf for a row that attended to nothing)
+    // ---- O = O^T / l; lse = m ln2 + log l (+inf for a row that attended to nothing)
+    float l_tot[QPW];
+#pragma unroll
+    for (int qt = 0; qt < QPW; ++qt) l_tot[qt] = lanes4_sum(l_run[qt]);   // every lane, before any divergence
     uint16_t* O = p.out + (int64_t)b * p.so[0] + (int64_t)h * p.so[1];
 #pragma unroll
     for (int qt = 0; qt < QPW; ++qt) {
         const int qi = q0 + 16 * qt + c16;
         if (qi >= p.L) continue;
-        const float inv = l_run[qt] > 0.0f ? 1.0f / l_run[qt] : 0.0f;
+        const float inv = l_tot[qt] > 0.0f ? 1.0f / l_tot[qt] : 0.0f;
 #pragma unroll
         for (int i = 0; i < DT16; ++i) {
             const int dv = 16 * i + 4 * g;   // four consecutive dv of column qi
@@ -267,13 +414,16 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_fwd_kernel(AttnArgs p) {
         }
         if (g == 0)
             p.lse[(int64_t)b * p.sl[0] + (int64_t)h * p.sl[1] + (int64_t)qi * p.sl[2]] =
-                l_run[qt] > 0.0f ? m_run[qt] + logf(l_run[qt]) : INFINITY;
+                l_tot[qt] > 0.0f ? m_run[qt] * AT_LN2 + logf(l_tot[qt]) : INFINITY;
     }
 }
 
 template <int DT, int D, int QPW>
-void launch_attn_q(const AttnArgs& a, bool causal, bool bias, dim3 grid, hipStream_t s) {
-    const dim3 block(64 * AT_WAVES);
+void launch_attn_q(AttnArgs a, bool causal, bool bias, int64_t bh, int64_t L, hipStream_t s) {
+    constexpr int BMQ = 16 * QPW * AT_WAVES;
+    a.nqb = (int)((L + BMQ - 1) / BMQ);
+    a.BH = (int)bh;
+    const dim3 grid((unsigned)(a.nqb * bh)), block(64 * AT_WAVES);
     if (causal) {
         if (bias) hipLaunchKernelGGL((attn_fwd_kernel<DT, D, true, true, QPW>), grid, block, 0, s, a);
         else hipLaunchKernelGGL((attn_fwd_kernel<DT, D, true, false, QPW>), grid, block, 0, s, a);
@@ -283,17 +433,19 @@ void launch_attn_q(const AttnArgs& a, bool causal, bool bias, dim3 grid, hipStre
     }
 }
 
-// Query columns per wave: two (128 queries per workgroup) when that still gives
-// the device plenty of workgroups, else one (64 per workgroup): more, lighter
-// waves per SIMD to hide the latency of each tile's softmax chain.
+// Query columns per wave: at head_dim 64, two (128 queries per workgroup) when
+// that still gives the device plenty of workgroups, else one (64 per
+// workgroup). At head_dim 128 two columns need over 256 VGPRs (one wave per
+// SIMD), so it is always one.
 template <int DT, int D>
 void launch_attn(const AttnArgs& a, bool causal, bool bias, int64_t batch, int64_t heads, int64_t L, hipStream_t s) {
-    const int64_t blocks128 = batch * heads * ((L + 127) / 128);
-    if (blocks128 >= 2048) {
-        launch_attn_q<DT, D, 2>(a, causal, bias, dim3((unsigned)((L + 127) / 128), (unsigned)heads, (unsigned)batch), s);
-    } else {
-        launch_attn_q<DT, D, 1>(a, causal, bias, dim3((unsigned)((L + 63) / 64), (unsigned)heads, (unsigned)batch), s);
+    if constexpr (D == 64) {
+        if (batch * heads * ((L + 127) / 128) >= 2048) {
+            launch_attn_q<DT, D, 2>(a, causal, bias, batch * heads, L, s);
+            return;
+        }
     }
+    launch_attn_q<DT, D, 1>(a, causal, bias, batch * heads, L, s);
 }
 
 
@@ -681,7 +833,8 @@ extern "C" tvk_status tvk_attention_fwd(const tvk_attention_desc* d) {
         return fail(TVK_ERR_INVALID, "tvk_attention_fwd: heads_q is not a multiple of heads_kv");
     if (d->head_dim != d->head_dim_v || (d->head_dim != 64 && d->head_dim != 128))
         return fail(TVK_ERR_UNSUPPORTED, "tvk_attention_fwd: head_dim == head_dim_v in {64, 128} only");
-    if (d->batch > 65535 || d->heads_q > 65535 || d->len_q > (int64_t)0x7fffffff || d->len_kv > (int64_t)0x7fffffff)
+    if (d->len_q > ((int64_t)1 << 30) || d->len_kv > ((int64_t)1 << 30) ||
+        d->batch * d->heads_q * ((d->len_q + 63) / 64) > (int64_t)0x7fffffff)
         return fail(TVK_ERR_UNSUPPORTED, "tvk_attention_fwd: grid too large");
     if (d->batch == 0 || d->heads_q == 0 || d->len_q == 0) return TVK_OK;
     if (!d->q || !d->k || !d->v || !d->out || !d->lse) return fail(TVK_ERR_INVALID, "tvk_attention_fwd: NULL tensor");
@@ -692,6 +845,10 @@ extern "C" tvk_status tvk_attention_fwd(const tvk_attention_desc* d) {
             if (st[i] % 8 != 0) return fail(TVK_ERR_UNSUPPORTED, "tvk_attention_fwd: q, k, v rows must be 16-byte aligned");
     }
     if (!al16(d->q) || !al16(d->k) || !al16(d->v)) return fail(TVK_ERR_UNSUPPORTED, "tvk_attention_fwd: unaligned q, k or v");
+    // a key tile's rows are addressed by 32-bit byte offsets from the tile's first row
+    for (const int64_t row : {d->k_stride[2], d->v_stride[2]})
+        if (row < 0 || (63 * row + d->head_dim) * 2 > (int64_t)0xffffffff)
+            return fail(TVK_ERR_UNSUPPORTED, "tvk_attention_fwd: k or v row stride too large");
     AttnArgs a{};
     a.q = static_cast<const uint16_t*>(d->q);
     a.k = static_cast<const uint16_t*>(d->k);
@@ -712,17 +869,19 @@ extern "C" tvk_status tvk_attention_fwd(const tvk_attention_desc* d) {
     a.Hq = (int)d->heads_q;
     a.group = (int)(d->heads_q / d->heads_kv);
     a.scale = (float)d->scale;
-    a.causal = d->causal != 0;
+    a.c2 = std::fabs(a.scale) * AT_LOG2E;
+    a.qflip = a.scale < 0.0f ? 0x80008000u : 0u;
+    const bool causal = d->causal != 0;
     a.out_vec = d->out_stride[3] == 1 && (reinterpret_cast<uintptr_t>(d->out) & 7) == 0 && d->out_stride[2] % 4 == 0 &&
                 d->out_stride[1] % 4 == 0 && d->out_stride[0] % 4 == 0;
     const hipStream_t s = resolve_stream(d->stream);
     const bool bias = d->bias != nullptr;
     if (d->dtype == TVK_F16) {
-        if (d->head_dim == 64) launch_attn<TVK_F16, 64>(a, a.causal, bias, d->batch, d->heads_q, d->len_q, s);
-        else launch_attn<TVK_F16, 128>(a, a.causal, bias, d->batch, d->heads_q, d->len_q, s);
+        if (d->head_dim == 64) launch_attn<TVK_F16, 64>(a, causal, bias, d->batch, d->heads_q, d->len_q, s);
+        else launch_attn<TVK_F16, 128>(a, causal, bias, d->batch, d->heads_q, d->len_q, s);
     } else {
-        if (d->head_dim == 64) launch_attn<TVK_BF16, 64>(a, a.causal, bias, d->batch, d->heads_q, d->len_q, s);
-        else launch_attn<TVK_BF16, 128>(a, a.causal, bias, d->batch, d->heads_q, d->len_q, s);
+        if (d->head_dim == 64) launch_attn<TVK_BF16, 64>(a, causal, bias, d->batch, d->heads_q, d->len_q, s);
+        else launch_attn<TVK_BF16, 128>(a, causal, bias, d->batch, d->heads_q, d->len_q, s);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_attention_fwd: launch failed: ") + hipGetErrorString(e));
