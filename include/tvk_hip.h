@@ -373,6 +373,46 @@ tvk_status tvk_gemm(const tvk_gemm_desc* desc);
  * choice record (src/vulkan/autotuner.cpp:56-84). */
 tvk_status tvk_gemm_plan(const tvk_gemm_desc* desc, char* name, size_t name_len);
 
+/* ---- kernel-choice table ----------------------------------------------------
+ * tvk_gemm picks its kernel from the shape (the plan above) unless the
+ * kernel-choice table holds another candidate for the product's shape class:
+ * dtype, flags, epilogue, operand layout and alignment, and ceil(log2) of
+ * M, N, K and batch (the reference's matmul tune key,
+ * src/api/ops/matmul.cpp:166-171,541). Candidates are named by their kernel
+ * ("gemm16_dma_128x128"; a split-K plan adds ":<chunks>"). float32 and
+ * TVK_GEMM_EXACT products have only sequential-order candidates, which give
+ * identical bits. The table is read from the tuning file on first use and
+ * persisted one line per result, following the reference's tuning cache
+ * (Autotuner::select/load/save, src/vulkan/autotuner.cpp:56-121; file
+ * location VulkanCache::cachePath, src/vulkan/cache.cpp:181-202):
+ * TORCHVULKAN_PIPELINE_CACHE=0 turns persistence off, the directory is
+ * $TORCHVULKAN_CACHE_DIR, else $XDG_CACHE_HOME/torchvulkan, else
+ * $HOME/.cache/torchvulkan, one file per device model. */
+
+/* Newline-separated names of every kernel that computes `desc`'s product, the
+ * shape-chosen one first ("none" for an empty product). TVK_ERR_INVALID when
+ * names_len is too small. */
+tvk_status tvk_gemm_candidates(const tvk_gemm_desc* desc, char* names, size_t names_len);
+
+/* Records `kernel` (one of the candidates) for `desc`'s shape class, in the
+ * tuning file too when persist != 0. */
+tvk_status tvk_gemm_choose(const tvk_gemm_desc* desc, const char* kernel, int persist);
+
+/* tvk_gemm that first, when the shape class has no recorded choice, times
+ * every candidate (median of five launches after a warm-up) and records and
+ * persists the fastest (Autotuner::fastest, src/vulkan/autotuner.cpp:123-223).
+ * The timed launches write a scratch output when c overlaps an operand. Writes
+ * the kernel used to `name` (may be NULL). Synchronizes the stream when it
+ * times. */
+tvk_status tvk_gemm_tune(const tvk_gemm_desc* desc, char* name, size_t name_len);
+
+/* Forgets every recorded choice; the next use reads the environment and the
+ * tuning file again. */
+tvk_status tvk_tune_reset(void);
+
+/* Path of the tuning file in use ("" when persistence is off). */
+tvk_status tvk_tune_path(char* path, size_t path_len);
+
 /* ------------------------------------------------------------------------- */
 /* Compute: 2-D convolution as implicit GEMM                                  */
 /* ------------------------------------------------------------------------- */

@@ -11,6 +11,11 @@ if str(ROOT) not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")
+    # the kernel-choice table reads its tuning file on first use: the tests get
+    # an empty directory of their own, never a user's tuned choices
+    import tempfile
+
+    os.environ["TORCHVULKAN_CACHE_DIR"] = tempfile.mkdtemp(prefix="tvk-tuning-")
 
 
 def _gpu_available() -> bool:

@@ -24,15 +24,23 @@ F16_TYPES = [torch.float16, torch.bfloat16]
 ALL_TYPES = [torch.float32, torch.float16, torch.bfloat16]
 
 
-def run(abi, a, b, out_shape, dtype, bias=None, alpha=1.0, beta=0.0, act=0, exact=False):
-    """Runs tvk_gemm on device copies of host views a/b (strides kept)."""
+def run(abi, a, b, out_shape, dtype, bias=None, alpha=1.0, beta=0.0, act=0, exact=False, kernel=None):
+    """Runs tvk_gemm on device copies of host views a/b (strides kept); `kernel`
+    records that candidate for the product in the kernel-choice table first."""
     da = a.to(DEV) if a.is_contiguous() else _device_view(a)
     db = b.to(DEV) if b.is_contiguous() else _device_view(b)
     dbias = None if bias is None else bias.to(DEV)
     c = torch.empty(out_shape, dtype=dtype, device=DEV)
-    abi.gemm(da, db, c, bias=dbias, alpha=alpha, beta=beta, activation=act, exact=exact)
-    torch.cuda.synchronize()
-    plan = abi.gemm_plan(da, db, c, bias=dbias, alpha=alpha, beta=beta, activation=act, exact=exact)
+    kw = dict(bias=dbias, alpha=alpha, beta=beta, activation=act, exact=exact)
+    if kernel:
+        abi.gemm_choose(da, db, c, kernel, **kw)
+    try:
+        abi.gemm(da, db, c, **kw)
+        torch.cuda.synchronize()
+        plan = abi.gemm_plan(da, db, c, **kw)
+    finally:
+        if kernel:
+            abi.tune_reset()
     return decode(to_np(c), dtype), plan
 
 
@@ -120,13 +128,14 @@ def test_dma_kernel_integer_exact(gpu, dtype, ta, tb, shape):
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("shape", [(1000, 1024, 96), (8192, 512, 512), (4000, 136, 64)])
 def test_dma_kernel_128_tiles_integer_exact(gpu, dtype, ta, tb, shape):
-    # mid-size products take the same ring on 128x128 tiles
+    # mid-size products take the same ring on 128x128 tiles (recorded in the
+    # kernel-choice table where the shape rule prefers another kernel)
     M, N, K = shape
     a = randint((K, M) if ta else (M, K), dtype, 28, -2, 3)
     b = randint((N, K) if tb else (K, N), dtype, 29, -2, 3)
     a = a.t() if ta else a
     b = b.t() if tb else b
-    got, plan = run(gpu, a, b, (M, N), dtype)
+    got, plan = run(gpu, a, b, (M, N), dtype, kernel="gemm16_dma_128x128")
     assert plan == "gemm16_dma_128x128"
     assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
 

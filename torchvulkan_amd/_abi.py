@@ -197,6 +197,11 @@ def load() -> C.CDLL:
         lib.tvk_last_error.restype = C.c_char_p
         lib.tvk_gemm.argtypes = [C.POINTER(GemmDesc)]
         lib.tvk_gemm_plan.argtypes = [C.POINTER(GemmDesc), C.c_char_p, C.c_size_t]
+        lib.tvk_gemm_candidates.argtypes = [C.POINTER(GemmDesc), C.c_char_p, C.c_size_t]
+        lib.tvk_gemm_choose.argtypes = [C.POINTER(GemmDesc), C.c_char_p, C.c_int]
+        lib.tvk_gemm_tune.argtypes = [C.POINTER(GemmDesc), C.c_char_p, C.c_size_t]
+        lib.tvk_tune_reset.argtypes = []
+        lib.tvk_tune_path.argtypes = [C.c_char_p, C.c_size_t]
         lib.tvk_malloc.argtypes = [C.c_int, C.c_size_t, C.POINTER(C.c_void_p)]
         lib.tvk_free.argtypes = [C.c_void_p]
         lib.tvk_pointer_device.argtypes = [C.c_void_p, C.POINTER(C.c_int)]
@@ -229,7 +234,8 @@ _ALL_ENTRY_POINTS = (
     "tvk_synchronize", "tvk_device_properties", "tvk_malloc", "tvk_free", "tvk_empty_cache",
     "tvk_pointer_device", "tvk_set_memory_limit", "tvk_memory_allocated", "tvk_max_memory_allocated",
     "tvk_memory_reserved", "tvk_reset_peak_memory_stats", "tvk_mem_get_info", "tvk_memcpy_h2d",
-    "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan",
+    "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan", "tvk_gemm_candidates",
+    "tvk_gemm_choose", "tvk_gemm_tune", "tvk_tune_reset", "tvk_tune_path",
     "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad", "tvk_copy", "tvk_copy_plan",
     "tvk_fill", "tvk_reduce_sum", "tvk_binary", "tvk_attention_fwd",
     "tvk_attention_bwd",
@@ -483,6 +489,44 @@ def gemm_plan(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, 
     d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, None, exact)
     buf = C.create_string_buffer(128)
     check(load().tvk_gemm_plan(C.byref(d), buf, 128))
+    return buf.value.decode()
+
+
+def gemm_candidates(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, exact=False) -> list[str]:
+    """Every kernel that computes this product (tvk_gemm_candidates), the shape-chosen one first."""
+    d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, None, exact)
+    buf = C.create_string_buffer(4096)
+    check(load().tvk_gemm_candidates(C.byref(d), buf, 4096))
+    return buf.value.decode().split("\n")
+
+
+def gemm_choose(a, b, c, kernel: str, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, exact=False,
+                persist=False) -> None:
+    """Records `kernel` for this product's shape class in the kernel-choice table (tvk_gemm_choose)."""
+    d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, None, exact)
+    check(load().tvk_gemm_choose(C.byref(d), kernel.encode(), int(persist)))
+
+
+def gemm_tune(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, stream=None, exact=False) -> str:
+    """tvk_gemm_tune: times the candidates when the shape class has no recorded choice, then runs the
+    product; returns the kernel used."""
+    import torch
+
+    if stream is None and c.is_cuda:
+        stream = torch.cuda.current_stream(c.device).cuda_stream
+    d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, stream, exact)
+    buf = C.create_string_buffer(128)
+    check(load().tvk_gemm_tune(C.byref(d), buf, 128))
+    return buf.value.decode()
+
+
+def tune_reset() -> None:
+    check(load().tvk_tune_reset())
+
+
+def tune_path() -> str:
+    buf = C.create_string_buffer(4096)
+    check(load().tvk_tune_path(buf, 4096))
     return buf.value.decode()
 
 

@@ -143,7 +143,15 @@ at::Tensor dispatch_matmul(const at::Tensor& self_, const at::Tensor& other_, co
     d.alpha = alpha.toDouble();
     d.beta = has_bias ? beta.toDouble() : 0.0;
     d.stream = stream_of(out);
-    const tvk_status st = tvk_gemm(&d);
+    // TORCHVULKAN_AUTOTUNE=1: a shape class without a recorded kernel is timed
+    // over every candidate first and the fastest recorded (the reference tunes
+    // every matmul on first sight, src/api/ops/matmul.cpp:538-544); otherwise
+    // the recorded or shape-chosen kernel runs
+    static const bool autotune = [] {
+        const char* e = std::getenv("TORCHVULKAN_AUTOTUNE");
+        return e != nullptr && e[0] && std::strcmp(e, "0") != 0;
+    }();
+    const tvk_status st = autotune ? tvk_gemm_tune(&d, nullptr, 0) : tvk_gemm(&d);
     if (st == TVK_ERR_UNSUPPORTED) {
         TVKB_FALLBACK(tvk_last_error(), ". Falling back to CPU.");
         return fallback();

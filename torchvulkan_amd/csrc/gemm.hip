@@ -22,8 +22,12 @@
 //                v_mfma_f32_32x32x1f32 rank-1 updates (one rounding each).
 //   gemm_generic any strides / dtype, one thread per output, same order.
 #include "gemm_common.h"
+#include "tune_table.h"
 
 #include <algorithm>
+#include <cmath>
+#include <vector>
+#include <string>
 #include <cstring>
 #include <cstdio>
 #include <cstdlib>
@@ -43,7 +47,7 @@ __global__ void gemm_k0_kernel(GemmArgs p) {
     int col = (int)(idx % p.N);
     int row = (int)((idx / p.N) % p.M);
     int b = (int)(idx / ((int64_t)p.N * p.M));
-    store_out<DT>(p, b, row, col, 0.0f);
+    store_out<DT, true>(p, b, row, col, 0.0f);
 }
 
 // One output per thread, sequential k, fmaf accumulate: the reference SIMD
@@ -60,7 +64,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
     float acc = 0.0f;
     for (int k = 0; k < p.K; ++k)
         acc = fmaf(elem<DT>::to_f32(a[(int64_t)k * p.sa[2]]), elem<DT>::to_f32(bm[(int64_t)k * p.sb[1]]), acc);
-    store_out<DT>(p, b, row, col, acc);
+    store_out<DT, true>(p, b, row, col, acc);
 }
 
 // ----------------------------------------------------------------------------
@@ -294,7 +298,7 @@ __global__ __launch_bounds__(128 * WGN) void gemm16_mfma_kernel(GemmArgs p) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-            store_frag16<DT>(p, b, m0 + wm * WM + i * 32 + (lane / 32) * 4, n0 + wn * WN + j * 32 + lane % 32, acc[i][j]);
+            store_frag16<DT, BM <= 128>(p, b, m0 + wm * WM + i * 32 + (lane / 32) * 4, n0 + wn * WN + j * 32 + lane % 32, acc[i][j]);
 }
 
 // ----------------------------------------------------------------------------
@@ -489,8 +493,8 @@ __global__ __launch_bounds__(256) void gemm_seq_mfma_kernel(GemmArgs p) {
         for (int j = 0; j < FN; ++j) {
             const int row0 = m0 + wm * WM + 32 * i + (lane / 32) * 4;
             const int col0 = n0 + wn * WN + 64 * j + lane % 32;
-            store_frag16<DT>(p, b, row0, col0, acc[i][j].lo);
-            store_frag16<DT>(p, b, row0, col0 + 32, acc[i][j].hi);
+            store_frag16<DT, BM <= 128>(p, b, row0, col0, acc[i][j].lo);
+            store_frag16<DT, BM <= 128>(p, b, row0, col0 + 32, acc[i][j].hi);
         }
 }
 
@@ -565,19 +569,21 @@ int64_t pad8(int64_t v) { return (v + 7) / 8 * 8; }
 // are 256-byte aligned).
 GemmArgs repacked_args(const tvk_gemm_desc& d, const struct Plan& pl);
 
-Plan make_plan(const tvk_gemm_desc& d) {
-    Plan pl{Kern::GENERIC, true, true, true, "gemm_generic"};
-    if (d.K == 0) return Plan{Kern::K0, true, true, true, "gemm_k0_fill"};
+// Operand layout facts every tiled kernel shares: which dimension of each
+// operand is contiguous, whether 16-byte loads are legal (vec) and which
+// operands are worth one copy into an aligned layout. False: no tiled kernel
+// applies and the generic kernel runs.
+bool plan_layout(const tvk_gemm_desc& d, Plan& pl) {
     const size_t es = dtype_size(d.dtype);
     // which dimension of each operand is contiguous (size-1 dims have any stride)
     const bool a_k = d.a_stride[2] == 1 || d.K == 1;
     const bool a_m = d.a_stride[1] == 1 || d.M == 1;
     const bool b_k = d.b_stride[1] == 1 || d.K == 1;
     const bool b_n = d.b_stride[2] == 1 || d.N == 1;
-    if (!(a_k || a_m) || !(b_k || b_n)) return pl;
+    if (!(a_k || a_m) || !(b_k || b_n)) return false;
     if (operand_extent_bytes(d.M, d.a_stride[1], d.K, d.a_stride[2], es) >= 0x7fffffff ||
         operand_extent_bytes(d.N, d.b_stride[2], d.K, d.b_stride[1], es) >= 0x7fffffff)
-        return pl;
+        return false;
     pl.ak = a_k;
     pl.bk = b_k;
     // 16-byte chunks need 16-byte aligned rows and whole chunks along the contiguous dimension
@@ -609,17 +615,54 @@ Plan make_plan(const tvk_gemm_desc& d) {
         pl.repack_b = !ok_b();
         pl.vec = true;
     }
-    if (d.dtype != TVK_F32 && !(d.flags & TVK_GEMM_EXACT) && skinny_applies(d.M, d.N, d.K, d.batch)) {
-        // the streaming kernel loads A by rows of k: 16-byte loads need A k-contiguous too
-        bool v = al16(d.a) && al16(d.b) && a_k && d.K % 8 == 0 && (d.M == 1 || d.a_stride[1] % 8 == 0);
-        if (d.batch > 1) v = v && d.a_stride[0] % 8 == 0 && d.b_stride[0] % 8 == 0;
-        if (b_k) v = v && (d.N == 1 || d.b_stride[2] % 8 == 0);
-        else v = v && d.N % 8 == 0 && (d.K == 1 || d.b_stride[1] % 8 == 0);
-        pl.kern = Kern::SKINNY;
-        pl.vec = v;
-        pl.name = skinny_name(make_args(d), b_k, v);
-        return pl;
-    }
+    return true;
+}
+
+Plan with_kern(Plan pl, Kern k, const char* name) {
+    pl.kern = k;
+    pl.name = name;
+    pl.split = 1;
+    pl.k_chunk = 0;
+    return pl;
+}
+
+// The M <= 16 streaming kernel on a laid-out plan (no repacks: the layout
+// never repacks such a product); it loads A by rows of k, so 16-byte loads
+// need A k-contiguous too.
+Plan skinny_plan(const tvk_gemm_desc& d, Plan pl) {
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    bool v = al16(d.a) && al16(d.b) && pl.ak && d.K % 8 == 0 && (d.M == 1 || d.a_stride[1] % 8 == 0);
+    if (d.batch > 1) v = v && d.a_stride[0] % 8 == 0 && d.b_stride[0] % 8 == 0;
+    if (pl.bk) v = v && (d.N == 1 || d.b_stride[2] % 8 == 0);
+    else v = v && d.N % 8 == 0 && (d.K == 1 || d.b_stride[1] % 8 == 0);
+    pl = with_kern(pl, Kern::SKINNY, nullptr);
+    pl.vec = v;
+    pl.name = skinny_name(make_args(d), pl.bk, v);
+    return pl;
+}
+
+// MFMA128 with K split about `want` ways into chunks of whole 64-k steps,
+// float32 partials; false when that would not split or the partials would
+// exceed 512 MB.
+bool split_plan(const tvk_gemm_desc& d, int64_t want, Plan& pl) {
+    if (want < 2) return false;
+    const int64_t chunk = ((d.K + want - 1) / want + 63) / 64 * 64;
+    const int64_t split = (d.K + chunk - 1) / chunk;
+    if (split < 2 || split * d.batch * d.M * d.N * 4 > (int64_t(512) << 20)) return false;
+    pl = with_kern(pl, Kern::MFMA128, "gemm16_mfma_128x128_splitk");
+    pl.split = (int)split;
+    pl.k_chunk = (int)chunk;
+    return true;
+}
+
+// The kernel chosen from the shape alone (used unless the kernel-choice table
+// holds another candidate for the product's shape class).
+Plan make_plan(const tvk_gemm_desc& d) {
+    Plan pl{Kern::GENERIC, true, true, true, "gemm_generic"};
+    if (d.K == 0) return Plan{Kern::K0, true, true, true, "gemm_k0_fill"};
+    if (!plan_layout(d, pl)) return pl;
+    if (d.dtype != TVK_F32 && !(d.flags & TVK_GEMM_EXACT) && skinny_applies(d.M, d.N, d.K, d.batch))
+        return skinny_plan(d, pl);
     const int64_t t256 = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
     const bool big = d.M >= 256 && d.N >= 256 && t256 >= 192;
     if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
@@ -631,7 +674,7 @@ Plan make_plan(const tvk_gemm_desc& d) {
             pl.kern = Kern::SEQ64;
             pl.name = "gemm_seq_mfma_64x128";
         }
-    } else if (big && pl.vec && dma_applies(repacked_args(d, pl), a_k, b_k)) {
+    } else if (big && pl.vec && dma_applies(repacked_args(d, pl), pl.ak, pl.bk)) {
         pl.kern = Kern::DMA256;
         pl.name = "gemm16_dma_256x256";
     } else if (big) {
@@ -642,29 +685,89 @@ Plan make_plan(const tvk_gemm_desc& d) {
         pl.kern = Kern::MFMA128;
         pl.name = "gemm16_mfma_128x128";
         const int64_t t128 = ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
-        // enough 128x128 tiles (or a short K, which split-K cannot help):
-        // the LDS-ring kernel on 128x128 tiles
-        if (pl.vec && (t128 >= 192 || d.K < 1024) && t128 >= 32 && dma_applies(repacked_args(d, pl), a_k, b_k)) {
+        // Few output tiles and a long K (weight gradients, batch-256 layers):
+        // split K into a power of two of chunks so at least one workgroup per
+        // CU runs, chunks of at least 256 k, partials in float32. Below
+        // K = 2048 the partials' round trip costs more than the idle CUs.
+        if (t128 < 192 && d.K >= 2048) {
+            auto pow2_ceil = [](int64_t v) { int64_t r = 1; while (r < v) r *= 2; return r; };
+            auto pow2_floor = [](int64_t v) { int64_t r = 1; while (r * 2 <= v) r *= 2; return r; };
+            if (split_plan(d, std::min<int64_t>({pow2_ceil((256 + t128 - 1) / t128), pow2_floor(d.K / 256), 32}), pl))
+                return pl;
+        }
+        // The LDS-ring kernel on 128x128 tiles, except for two k-contiguous
+        // operands with K <= 1024, where the register-staged kernel is ahead
+        // (measured 4-13% on the transformer and MLP shapes)
+        if (pl.vec && t128 >= 32 && !(pl.ak && pl.bk && d.K <= 1024) && dma_applies(repacked_args(d, pl), pl.ak, pl.bk)) {
             pl.kern = Kern::DMA128;
             pl.name = "gemm16_dma_128x128";
-            return pl;
-        }
-        // Few output tiles and a long K (weight gradients, batch-256 layers):
-        // split K so about one workgroup per CU runs, partials in float32.
-        if (t128 < 192 && d.K >= 1024) {
-            int64_t split = std::min<int64_t>({(256 + t128 - 1) / t128, d.K / 256, 32});
-            if (split >= 2) {
-                const int64_t chunk = ((d.K + split - 1) / split + 63) / 64 * 64;
-                split = (d.K + chunk - 1) / chunk;
-                if (split >= 2 && split * d.batch * d.M * d.N * 4 <= (int64_t(512) << 20)) {
-                    pl.split = (int)split;
-                    pl.k_chunk = (int)chunk;
-                    pl.name = "gemm16_mfma_128x128_splitk";
-                }
-            }
         }
     }
     return pl;
+}
+
+// A candidate's name in the kernel-choice table: the kernel name, and the
+// number of K chunks for a split-K plan.
+std::string plan_id(const Plan& pl) {
+    std::string id = pl.name;
+    if (pl.split > 1) id += ":" + std::to_string(pl.split);
+    return id;
+}
+
+// Every plan that computes this product, make_plan's choice first. float32
+// (and TVK_GEMM_EXACT) offers only the sequential-order kernels, which give
+// identical bits; float16/bfloat16 offer every tiled kernel whose layout
+// conditions hold.
+std::vector<Plan> candidate_plans(const tvk_gemm_desc& d) {
+    std::vector<Plan> out{make_plan(d)};
+    if (out[0].kern == Kern::K0 || out[0].kern == Kern::GENERIC) return out;
+    Plan lay{Kern::GENERIC, true, true, true, "gemm_generic"};
+    plan_layout(d, lay);
+    auto add = [&](const Plan& p) {
+        for (const Plan& q : out)
+            if (q.kern == p.kern && q.split == p.split) return;
+        out.push_back(p);
+    };
+    if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
+        add(with_kern(lay, Kern::SEQ256, "gemm_seq_mfma_256x256"));
+        add(with_kern(lay, Kern::SEQ128, "gemm_seq_mfma_128x128"));
+        add(with_kern(lay, Kern::SEQ64, "gemm_seq_mfma_64x128"));
+        return out;
+    }
+    if (skinny_applies(d.M, d.N, d.K, d.batch)) add(skinny_plan(d, lay));
+    add(with_kern(lay, Kern::MFMA128, "gemm16_mfma_128x128"));
+    for (int64_t want : {2, 4, 8, 16}) {
+        Plan p = lay;
+        if (split_plan(d, want, p)) add(p);
+    }
+    const bool dma = lay.vec && dma_applies(repacked_args(d, lay), lay.ak, lay.bk);
+    if (dma) add(with_kern(lay, Kern::DMA128, "gemm16_dma_128x128"));
+    if (d.M >= 128 && d.N >= 128) {
+        add(with_kern(lay, Kern::MFMA256W8, "gemm16_mfma_256x256_w8"));
+        add(with_kern(lay, Kern::MFMA256, "gemm16_mfma_256x256"));
+        if (dma) add(with_kern(lay, Kern::DMA256, "gemm16_dma_256x256"));
+    }
+    return out;
+}
+
+// Shape class of a product in the kernel-choice table, after the reference's
+// matmul tune key (src/api/ops/matmul.cpp:166-171,541): dtype, flags,
+// epilogue, the operand layout facts that decide which kernels apply, and
+// ceil(log2) of M, N, K and the batch.
+uint64_t tune_key(const tvk_gemm_desc& d) {
+    Plan lay{Kern::GENERIC, true, true, true, "gemm_generic"};
+    const bool tiled = d.K > 0 && plan_layout(d, lay);
+    const bool dma = tiled && lay.vec && dma_applies(repacked_args(d, lay), lay.ak, lay.bk);
+    auto lg = [](int64_t v) {
+        uint64_t r = 0;
+        while (r < 63 && (int64_t(1) << r) < v) ++r;
+        return r;
+    };
+    const bool bias = d.bias != nullptr && d.beta != 0.0;
+    return (uint64_t)(d.dtype & 15) | (uint64_t)(d.flags & 1) << 4 | (uint64_t)(d.activation & 3) << 5 |
+           (uint64_t)bias << 7 | (uint64_t)tiled << 8 | (uint64_t)lay.ak << 9 | (uint64_t)lay.bk << 10 |
+           (uint64_t)lay.vec << 11 | (uint64_t)dma << 12 | (uint64_t)lay.repack_a << 13 | (uint64_t)lay.repack_b << 14 |
+           lg(d.M) << 16 | lg(d.N) << 24 | lg(d.K) << 32 | lg(d.batch) << 40;
 }
 
 GemmArgs repacked_args(const tvk_gemm_desc& d, const Plan& pl) {
@@ -845,6 +948,90 @@ tvk_status validate(const tvk_gemm_desc* d) {
     return TVK_OK;
 }
 
+// make_plan's choice unless the kernel-choice table holds another candidate
+// for the product's shape class (Autotuner::select's lookup,
+// src/vulkan/autotuner.cpp:56-84); a recorded kernel that does not apply to
+// this product is ignored, as the reference ignores a stored config outside
+// the current space (in_space, :20-29).
+Plan choose_plan(const tvk_gemm_desc& d) {
+    std::string id;
+    if (d.K > 0 && tune_lookup("gemm", tune_key(d), id))
+        for (const Plan& p : candidate_plans(d))
+            if (plan_id(p) == id) return p;
+    return make_plan(d);
+}
+
+tvk_status run_plan(const tvk_gemm_desc& d, const Plan& pl) {
+    const hipStream_t s = resolve_stream(d.stream);
+    switch (d.dtype) {
+    case TVK_F32: return run<TVK_F32>(d, pl, s);
+    case TVK_F16: return run<TVK_F16>(d, pl, s);
+    default: return run<TVK_BF16>(d, pl, s);
+    }
+}
+
+// Times every candidate on the product and picks the fastest: one warm-up
+// launch, then the median of five timed launches each (the reference takes
+// the median of five spans per config, src/vulkan/autotuner.cpp:16-18,137-152,
+// and times every config of a space this small, :11-12,194-198). A candidate
+// that fails to launch is skipped. When c shares memory with an operand the
+// timed launches write a scratch output instead, so no input changes.
+tvk_status time_candidates(const tvk_gemm_desc& d, const std::vector<Plan>& cands, Plan& best) {
+    const size_t es = dtype_size(d.dtype);
+    auto extent = [&](const void* base, const int64_t* st, int64_t rows, int64_t cols) {
+        const char* lo = static_cast<const char*>(base);
+        return std::make_pair(lo, lo + es * ((d.batch - 1) * st[0] + (rows - 1) * st[1] + (cols - 1) * st[2] + 1));
+    };
+    const auto c = extent(d.c, d.c_stride, d.M, d.N);
+    auto overlaps = [&](std::pair<const char*, const char*> r) { return r.first < c.second && c.first < r.second; };
+    bool alias = overlaps(extent(d.a, d.a_stride, d.M, d.K)) || overlaps(extent(d.b, d.b_stride, d.K, d.N));
+    if (d.bias && d.beta != 0.0) alias = alias || overlaps(extent(d.bias, d.bias_stride, d.M, d.N));
+    tvk_gemm_desc t = d;
+    void* scratch = nullptr;
+    if (alias) {
+        if (hipMalloc(&scratch, (size_t)(c.second - c.first)) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(TVK_ERR_OOM, "tvk_gemm_tune: no memory for a scratch output");
+        }
+        t.c = scratch;
+    }
+    const hipStream_t s = resolve_stream(d.stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        (void)hipGetLastError();
+        if (e0) (void)hipEventDestroy(e0);
+        if (scratch) (void)hipFree(scratch);
+        return fail(TVK_ERR_DEVICE, "tvk_gemm_tune: hipEventCreate failed");
+    }
+    float best_ms = INFINITY;
+    for (const Plan& pl : cands) {
+        float spans[5];
+        bool ok = run_plan(t, pl) == TVK_OK;
+        for (int i = 0; ok && i < 5; ++i)
+            ok = hipEventRecord(e0, s) == hipSuccess && run_plan(t, pl) == TVK_OK && hipEventRecord(e1, s) == hipSuccess &&
+                 hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&spans[i], e0, e1) == hipSuccess;
+        if (!ok) {
+            (void)hipGetLastError();
+            continue;
+        }
+        std::nth_element(spans, spans + 2, spans + 5);
+        if (spans[2] < best_ms) {
+            best_ms = spans[2];
+            best = pl;
+        }
+    }
+    (void)hipStreamSynchronize(s);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (scratch) (void)hipFree(scratch);
+    if (best_ms == INFINITY) return fail(TVK_ERR_DEVICE, "tvk_gemm_tune: no candidate kernel ran");
+    return TVK_OK;
+}
+
+void put_name(char* name, size_t name_len, const std::string& n) {
+    if (name && name_len) snprintf(name, name_len, "%s", n.c_str());
+}
+
 }  // namespace
 }  // namespace tvk
 
@@ -854,7 +1041,7 @@ extern "C" tvk_status tvk_gemm_plan(const tvk_gemm_desc* desc, char* name, size_
     tvk_status st = validate(desc);
     if (st != TVK_OK) return st;
     if (!name || name_len == 0) return fail(TVK_ERR_INVALID, "tvk_gemm_plan: name buffer is empty");
-    const char* n = (desc->batch == 0 || desc->M == 0 || desc->N == 0) ? "none" : make_plan(*desc).name;
+    const char* n = (desc->batch == 0 || desc->M == 0 || desc->N == 0) ? "none" : choose_plan(*desc).name;
     snprintf(name, name_len, "%s", n);
     return TVK_OK;
 }
@@ -864,11 +1051,79 @@ extern "C" tvk_status tvk_gemm(const tvk_gemm_desc* desc) {
     if (st != TVK_OK) return st;
     const tvk_gemm_desc& d = *desc;
     if (d.batch == 0 || d.M == 0 || d.N == 0) return TVK_OK;
-    Plan pl = make_plan(d);
-    hipStream_t s = resolve_stream(d.stream);
-    switch (d.dtype) {
-    case TVK_F32: return run<TVK_F32>(d, pl, s);
-    case TVK_F16: return run<TVK_F16>(d, pl, s);
-    default: return run<TVK_BF16>(d, pl, s);
+    return run_plan(d, choose_plan(d));
+}
+
+extern "C" tvk_status tvk_gemm_candidates(const tvk_gemm_desc* desc, char* names, size_t names_len) {
+    tvk_status st = validate(desc);
+    if (st != TVK_OK) return st;
+    if (!names || names_len == 0) return fail(TVK_ERR_INVALID, "tvk_gemm_candidates: name buffer is empty");
+    std::string all;
+    if (desc->batch == 0 || desc->M == 0 || desc->N == 0) all = "none";
+    else
+        for (const Plan& p : candidate_plans(*desc)) all += (all.empty() ? "" : "\n") + plan_id(p);
+    if (all.size() + 1 > names_len)
+        return fail(TVK_ERR_INVALID, "tvk_gemm_candidates: the names need " + std::to_string(all.size() + 1) + " bytes");
+    snprintf(names, names_len, "%s", all.c_str());
+    return TVK_OK;
+}
+
+extern "C" tvk_status tvk_gemm_choose(const tvk_gemm_desc* desc, const char* kernel, int persist) {
+    tvk_status st = validate(desc);
+    if (st != TVK_OK) return st;
+    if (!kernel) return fail(TVK_ERR_INVALID, "tvk_gemm_choose: kernel is NULL");
+    if (desc->batch == 0 || desc->M == 0 || desc->N == 0 || desc->K == 0)
+        return fail(TVK_ERR_INVALID, "tvk_gemm_choose: an empty product has no kernel choice");
+    for (const Plan& p : candidate_plans(*desc))
+        if (plan_id(p) == kernel) {
+            tune_record("gemm", tune_key(*desc), plan_id(p), persist != 0);
+            return TVK_OK;
+        }
+    return fail(TVK_ERR_INVALID, std::string("tvk_gemm_choose: ") + kernel + " does not compute this product");
+}
+
+extern "C" tvk_status tvk_gemm_tune(const tvk_gemm_desc* desc, char* name, size_t name_len) {
+    tvk_status st = validate(desc);
+    if (st != TVK_OK) return st;
+    const tvk_gemm_desc& d = *desc;
+    if (d.batch == 0 || d.M == 0 || d.N == 0) {
+        put_name(name, name_len, "none");
+        return TVK_OK;
     }
+    const std::vector<Plan> cands = candidate_plans(d);
+    Plan best = cands[0];
+    if (d.K > 0) {
+        const uint64_t key = tune_key(d);
+        std::string id;
+        bool known = false;
+        if (tune_lookup("gemm", key, id))
+            for (const Plan& p : cands)
+                if (plan_id(p) == id) {
+                    best = p;
+                    known = true;
+                    break;
+                }
+        if (!known) {
+            if (cands.size() > 1) {
+                st = time_candidates(d, cands, best);
+                if (st != TVK_OK) return st;
+            }
+            tune_record("gemm", key, plan_id(best), true);
+        }
+    }
+    put_name(name, name_len, plan_id(best));
+    return run_plan(d, best);
+}
+
+extern "C" tvk_status tvk_tune_reset(void) {
+    tune_reset();
+    return TVK_OK;
+}
+
+extern "C" tvk_status tvk_tune_path(char* path, size_t path_len) {
+    if (!path || path_len == 0) return fail(TVK_ERR_INVALID, "tvk_tune_path: buffer is empty");
+    const std::string p = tune_path();
+    if (p.size() + 1 > path_len) return fail(TVK_ERR_INVALID, "tvk_tune_path: the path needs " + std::to_string(p.size() + 1) + " bytes");
+    snprintf(path, path_len, "%s", p.c_str());
+    return TVK_OK;
 }

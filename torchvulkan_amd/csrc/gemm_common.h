@@ -51,7 +51,28 @@ static __device__ __noinline__ float epilogue_math(float acc, float alpha, int h
     return v;
 }
 
-template <int DT>
+// The same arithmetic inline for every activation but GELU (a few VALU
+// instructions, no call).
+__device__ __forceinline__ float epilogue_linear(float acc, float alpha, int has_bias, float bv, float beta, int act) {
+#pragma clang fp contract(off)
+    float v = acc * alpha;
+    if (has_bias) {
+        float t = bv * beta;
+        v = v + t;
+    }
+    if (act == TVK_ACT_RELU) v = v > 0.0f ? v : (v != v ? v : 0.0f);
+    return v;
+}
+
+__device__ __forceinline__ float epilogue(float acc, float alpha, int has_bias, float bv, float beta, int act) {
+    return act == TVK_ACT_GELU ? epilogue_math(acc, alpha, has_bias, bv, beta, act)
+                               : epilogue_linear(acc, alpha, has_bias, bv, beta, act);
+}
+
+// INL: the arithmetic inline except for GELU, and a row-broadcast bias loaded
+// once per fragment (store_frag16); the 256-wide tiles take neither, their
+// accumulators fill the register file.
+template <int DT, bool INL = false>
 __device__ inline void store_out(const GemmArgs& p, int b, int row, int col, float acc) {
     typedef typename elem<DT>::T T;
     T* c = reinterpret_cast<T*>(p.c);
@@ -65,20 +86,36 @@ __device__ inline void store_out(const GemmArgs& p, int b, int row, int col, flo
             const T* bias = reinterpret_cast<const T*>(p.bias);
             bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2]]);
         }
-        v = epilogue_math(acc, p.alpha, p.has_bias, bv, p.beta, p.act);
+        v = INL ? epilogue(acc, p.alpha, p.has_bias, bv, p.beta, p.act) : epilogue_math(acc, p.alpha, p.has_bias, bv, p.beta, p.act);
     }
     c[(int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2]] = elem<DT>::from_f32(v);
 }
 
 // Epilogue of 16 accumulators of one lane that share a column and sit at
-// rows row0 + (r/4)*8 + r%4 (the 32x32 MFMA accumulator layout).
-template <int DT>
+// rows row0 + (r/4)*8 + r%4 (the 32x32 MFMA accumulator layout). A bias that
+// is constant along the rows (a Linear layer's, broadcast with row stride 0)
+// is loaded once: loaded per element, each load would sit after a store to c
+// (which may be the bias itself) and be waited for on its own.
+template <int DT, bool INL = false>
 __device__ inline void store_frag16(const GemmArgs& p, int b, int row0, int col, const f32x16& v) {
     if (col >= p.N) return;
+    if (INL && p.has_bias && p.sbias[1] == 0) {
+        typedef typename elem<DT>::T T;
+        const float bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[(int64_t)b * p.sbias[0] + (int64_t)col * p.sbias[2]]);
+        T* c = reinterpret_cast<T*>(p.c) + (int64_t)b * p.sc[0] + (int64_t)col * p.sc[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = row0 + (r / 4) * 8 + (r % 4);
+            if (row < p.M)
+                c[(int64_t)row * p.sc[1]] = elem<DT>::from_f32(INL ? epilogue(v[r], p.alpha, 1, bv, p.beta, p.act)
+                                                                   : epilogue_math(v[r], p.alpha, 1, bv, p.beta, p.act));
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int row = row0 + (r / 4) * 8 + (r % 4);
-        if (row < p.M) store_out<DT>(p, b, row, col, v[r]);
+        if (row < p.M) store_out<DT, INL>(p, b, row, col, v[r]);
     }
 }
 

@@ -314,7 +314,7 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
 #pragma clang fp contract(off)
                     v = a8[e] * p.alpha;
                 } else {
-                    v = epilogue_math(a8[e], p.alpha, p.has_bias, bv[e], p.beta, p.act);
+                    v = epilogue(a8[e], p.alpha, p.has_bias, bv[e], p.beta, p.act);
                 }
                 h[e] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
             }

@@ -159,7 +159,7 @@ __global__ __launch_bounds__(64 * SK_NW) void gemm_skinny_kernel(GemmArgs p) {
 #pragma unroll
         for (int w = 1; w < SK_NW; ++w) v += red[(w * 16 + m) * (SK_CW + 4) + cl];
         const int n = n0 + cl;
-        if (m < p.M && n < p.N) store_out<DT>(p, b, m, n, v);
+        if (m < p.M && n < p.N) store_out<DT, true>(p, b, m, n, v);
     }
 }
 
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(64 * SR_NW) void gemm_skinny_ring_kernel(GemmArgs p
         const int m = (lane / 16) * 4 + r;
         if (m >= p.M) continue;
         if (p.split > 1) p.part[(((int64_t)z * p.batch + b) * p.M + m) * p.N + n] = acc[r];
-        else store_out<DT>(p, b, m, n, acc[r]);
+        else store_out<DT, true>(p, b, m, n, acc[r]);
     }
 }
 
