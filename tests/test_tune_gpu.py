@@ -146,3 +146,13 @@ def test_backend_autotune_on_first_sight(gpu, tmp_path):
     assert len(files) == 1
     lines = files[0].read_text().splitlines()
     assert len(lines) == 1 and lines[0].split()[:2] == ["tvk1", "gemm"]   # tuned once, then read from the table
+
+
+def test_ahead_of_time_tuner_records_fastest(gpu, fresh_table, capsys):
+    from torchvulkan_amd import tune
+
+    assert tune.main(["--shape", "512x768x1024:f16:nt", "--shape", "96x96x96:bf16:tn:3:c", "--record"]) == 0
+    out = capsys.readouterr().out
+    assert out.count("| 512x768x1024") == 1 and "recorded in" in out
+    lines = open(_abi.tune_path()).read().splitlines()
+    assert len(lines) == 2 and all(l.startswith("tvk1 gemm ") for l in lines)
