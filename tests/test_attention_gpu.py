@@ -186,3 +186,34 @@ def test_backward_ragged_bias_d128(gpu):
     q2 = rand((1, 2, 200, 64), dtype, 38)
     k2, v2 = rand((1, 2, 40, 64), dtype, 39), rand((1, 2, 40, 64), dtype, 40)
     check_bwd(q2, k2, v2, causal=True, what="causal L 200 > S 40")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_odd_tiles_mha(gpu, causal):
+    # one head per kv head, 3 query tiles (the two dK/dV wave groups take 2 and 1),
+    # batch*heads = 3 (not a multiple of the 8 XCDs), keys past the queries
+    dtype = torch.float16
+    q = rand((1, 3, 130, 64), dtype, 41)
+    k, v = rand((1, 3, 190, 64), dtype, 42), rand((1, 3, 190, 64), dtype, 43)
+    check_bwd(q, k, v, causal=causal, what=f"MHA L 130 S 190 causal={causal}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_backward_wide_grid(gpu, dtype):
+    # batch*heads*ceil(L/128) >= 2048: dQ with two query columns per wave; the
+    # oracle checks two (batch, kv head) slices with all four of their query heads
+    B, Hq, Hk, L, D = 16, 16, 4, 1024, 64
+    q, k, v = rand((B, Hq, L, D), dtype, 44), rand((B, Hk, L, D), dtype, 45), rand((B, Hk, L, D), dtype, 46)
+    dq_, dk_, dv_ = (t.to(DEV) for t in (q, k, v))
+    out, lse = _abi.attention_fwd(dq_, dk_, dv_, None, True)
+    dout = rand(out.shape, dtype, 47)
+    gq, gk, gv = _abi.attention_bwd(dq_, dk_, dv_, out, lse, dout.to(DEV), None, True)
+    torch.cuda.synchronize()
+    rdt = orc.F16 if dtype == torch.float16 else orc.BF16
+    for b, hk in ((0, 0), (11, 3)):
+        hs = slice(4 * hk, 4 * hk + 4)
+        ref = orc.attention_bwd(f64(q[b:b + 1, hs]), f64(k[b:b + 1, hk:hk + 1]), f64(v[b:b + 1, hk:hk + 1]),
+                                f64(dout[b:b + 1, hs]), None, True, None, out=f64(out[b:b + 1, hs]), round_to=rdt)
+        for got, want, name in zip((gq[b:b + 1, hs], gk[b:b + 1, hk:hk + 1], gv[b:b + 1, hk:hk + 1]), ref,
+                                   ("dq", "dk", "dv")):
+            assert_close(f64(got), want, dtype, f"b {b} kv head {hk} {name}")

@@ -45,7 +45,6 @@ typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 #define TVK_LDS __attribute__((address_space(3)))
 
 constexpr int AT_WAVES = 4;
-constexpr int AT_BM = 32 * AT_WAVES;   // queries per workgroup of the dq pass
 constexpr int AT_BN = 64;              // keys per tile
 constexpr float AT_LOG2E = 1.4426950408889634f;
 constexpr float AT_LN2 = 0.6931471805599453f;
@@ -112,8 +111,8 @@ __device__ inline float lanes4_sum(float v) {
 // (batch, head) stays on one XCD, so its K and V tiles are shared in that
 // XCD's L2. Causal rows do work in proportion to their query tile: the
 // heaviest tiles are dealt first, every XCD taking the same mix.
-template <bool CAUSAL>
-__device__ inline void attn_block(const AttnArgs& p, int& qb, int& bh) {
+template <bool CAUSAL, class Args>
+__device__ inline void attn_block(const Args& p, int& qb, int& bh) {
     const int id = blockIdx.x;
     if (p.BH % 8 == 0) {
         const int xcd = id % 8, local = id / 8, per = p.BH / 8;
@@ -467,7 +466,9 @@ struct AttnBwdArgs {
     uint16_t* dv;
     int64_t sq[4], sk[4], sv[4], sb[4], so[4], sdo[4], sdq[4], sdk[4], sdv[4], sl[3];
     int L, S, Hq, group;
+    int nqb, BH;       // dQ pass: query tiles per (batch, head), batch * heads
     float scale;
+    float c2;          // scale * log2(e)
 };
 
 // 64-bit stores of four consecutive elements along the head dimension
@@ -494,14 +495,18 @@ __device__ inline u32x4 read_tr(const uint16_t* tile, int kk, int i, int g, int 
     return f;
 }
 
-// dQ pass (and delta): the forward's orientation. 4 waves x 32 queries of one
-// (batch, head); key tiles of 64 through double-buffered LDS. Per tile:
-// S^T = K Q^T, P^T = exp(s - lse), dP^T = V dO^T, dS^T = P^T (dP^T - delta),
-// dQ^T += K^T dS^T (K read transposed in the dS^T k-slot order). As in the
-// reference's scoreGradients (src/shaders/ops/attention_coop.slang:283-305),
-// P and dS are formed in float32 and rounded to the dtype for their products.
-template <int DT, int D, bool CAUSAL, bool BIAS>
+// dQ pass (and delta): the forward's orientation. 4 waves x 16 or 32 queries
+// of one (batch, head), workgroups dealt as the forward's; key tiles of 64
+// through double-buffered LDS. Per tile: S^T = K Q^T, P^T = exp(s - lse),
+// dP^T = V dO^T, dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T (K read
+// transposed in the dS^T k-slot order). As in the reference's scoreGradients
+// (src/shaders/ops/attention_coop.slang:283-305), P and dS are formed in
+// float32 and rounded to the dtype for their products. Without a bias and away
+// from the sequence end and the causal diagonal, P is one fma and one exp2 of
+// the raw product (scale*log2(e) and lse*log2(e) folded in).
+template <int DT, int D, bool CAUSAL, bool BIAS, int QPW>
 __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs p) {
+    constexpr int BMQ = 16 * QPW * AT_WAVES;
     constexpr int DS = D / 32, DT16 = D / 16, LDK = D + 8;
     constexpr int CH = AT_BN * D / 8, CPT = CH / (64 * AT_WAVES);
     __shared__ __attribute__((aligned(16))) uint16_t ks[2][AT_BN * LDK];
@@ -509,18 +514,20 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs 
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
     const int g = lane / 16, c16 = lane % 16;
-    const int b = blockIdx.z, h = blockIdx.y, hk = h / p.group;
-    const int q0 = blockIdx.x * AT_BM + wave * 32;
+    int qb, bh;
+    attn_block<CAUSAL>(p, qb, bh);
+    const int b = bh / p.Hq, h = bh % p.Hq, hk = h / p.group;
+    const int q0 = qb * BMQ + wave * 16 * QPW;
     const uint16_t* Q = p.q + (int64_t)b * p.sq[0] + (int64_t)h * p.sq[1];
     const uint16_t* K = p.k + (int64_t)b * p.sk[0] + (int64_t)hk * p.sk[1];
     const uint16_t* V = p.v + (int64_t)b * p.sv[0] + (int64_t)hk * p.sv[1];
     const uint16_t* O = p.out + (int64_t)b * p.so[0] + (int64_t)h * p.so[1];
     const uint16_t* dO = p.dout + (int64_t)b * p.sdo[0] + (int64_t)h * p.sdo[1];
 
-    u32x4 qf[2][DS], df[2][DS];
-    float lse[2], dlt[2];
+    u32x4 qf[QPW][DS], df[QPW][DS];
+    float lse[QPW], lse2[QPW], dlt[QPW];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QPW; ++qt) {
         const int qi = q0 + 16 * qt + c16;
         const bool in = qi < p.L;
         float part = 0.0f;
@@ -539,20 +546,21 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs 
                 }
             }
         }
-        dlt[qt] = xor_sum(xor_sum(part, 16), 32);
+        dlt[qt] = lanes4_sum(part);
         lse[qt] = in ? p.lse[(int64_t)b * p.sl[0] + (int64_t)h * p.sl[1] + (int64_t)qi * p.sl[2]] : INFINITY;
+        lse2[qt] = lse[qt] * AT_LOG2E;
         if (in && g == 0) p.delta[((int64_t)b * p.Hq + h) * p.L + qi] = dlt[qt];
     }
 
-    f32x4 acc[DT16][2];
+    f32x4 acc[DT16][QPW];
 #pragma unroll
     for (int i = 0; i < DT16; ++i)
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) acc[i][qt] = f32x4{0, 0, 0, 0};
+        for (int qt = 0; qt < QPW; ++qt) acc[i][qt] = f32x4{0, 0, 0, 0};
 
     int ntiles = (p.S + AT_BN - 1) / AT_BN;
     if (CAUSAL) {
-        const int last_q = min(p.L, (int)blockIdx.x * AT_BM + AT_BM) - 1;
+        const int last_q = min(p.L, qb * BMQ + BMQ) - 1;
         ntiles = min(ntiles, last_q / AT_BN + 1);
     }
     u32x4 kreg[CPT], vreg[CPT];
@@ -583,59 +591,75 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs 
 
     for (int j = 0; j < ntiles; ++j) {
         const int buf = j & 1;
+        const int k0 = j * AT_BN;
         if (j + 1 < ntiles) load_tile(j + 1);
-        f32x4 sacc[4][2], pacc[4][2];
+        // a causal wave whose queries all precede the tile has nothing to add
+        if (!CAUSAL || k0 <= q0 + 16 * QPW - 1) {
+            f32x4 sacc[4][QPW], pacc[4][QPW];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
+            for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
-                sacc[kt][qt] = f32x4{0, 0, 0, 0};
-                pacc[kt][qt] = f32x4{0, 0, 0, 0};
-            }
-#pragma unroll
-            for (int ds = 0; ds < DS; ++ds) {
-                const u32x4 kf = *reinterpret_cast<const u32x4*>(&ks[buf][(kt * 16 + c16) * LDK + 32 * ds + 8 * g]);
-                const u32x4 vf = *reinterpret_cast<const u32x4*>(&vs[buf][(kt * 16 + c16) * LDK + 32 * ds + 8 * g]);
-#pragma unroll
-                for (int qt = 0; qt < 2; ++qt) {
-                    sacc[kt][qt] = mfma16<DT>(kf, qf[qt][ds], sacc[kt][qt]);
-                    pacc[kt][qt] = mfma16<DT>(vf, df[qt][ds], pacc[kt][qt]);
+                for (int qt = 0; qt < QPW; ++qt) {
+                    sacc[kt][qt] = f32x4{0, 0, 0, 0};
+                    pacc[kt][qt] = f32x4{0, 0, 0, 0};
                 }
-            }
-        }
-        // dS^T = P^T (dP^T - delta), P^T = exp(s - lse); masked entries give 0
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-            const int qi = q0 + 16 * qt + c16;
+                for (int ds = 0; ds < DS; ++ds) {
+                    const u32x4 kf = *reinterpret_cast<const u32x4*>(&ks[buf][(kt * 16 + c16) * LDK + 32 * ds + 8 * g]);
+                    const u32x4 vf = *reinterpret_cast<const u32x4*>(&vs[buf][(kt * 16 + c16) * LDK + 32 * ds + 8 * g]);
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int kj = j * AT_BN + kt * 16 + 4 * g + r;
-                    float s = sacc[kt][qt][r] * p.scale;
-                    if (BIAS && kj < p.S && qi < p.L) {
-                        const uint16_t bv = p.bias[(int64_t)b * p.sb[0] + (int64_t)h * p.sb[1] + (int64_t)qi * p.sb[2] + (int64_t)kj * p.sb[3]];
-                        s = s + elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, bv));
+                    for (int qt = 0; qt < QPW; ++qt) {
+                        sacc[kt][qt] = mfma16<DT>(kf, qf[qt][ds], sacc[kt][qt]);
+                        pacc[kt][qt] = mfma16<DT>(vf, df[qt][ds], pacc[kt][qt]);
                     }
-                    if (kj >= p.S || (CAUSAL && kj > qi)) s = -INFINITY;
-                    // dS from the float32 P; only dS is rounded to the dtype (when packed)
-                    const float pe = __builtin_amdgcn_exp2f((s - lse[qt]) * AT_LOG2E);
-                    sacc[kt][qt][r] = pe * (pacc[kt][qt][r] - dlt[qt]);
                 }
-        }
+            }
+            // dS^T = P^T (dP^T - delta), P^T = exp(s - lse); masked entries give 0
+            if (!BIAS && k0 + AT_BN <= p.S && !(CAUSAL && k0 + AT_BN - 1 > q0)) {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            u32x4 sf[2];
+                for (int qt = 0; qt < QPW; ++qt)
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
-                const f32x4 a = sacc[2 * kk][qt], c = sacc[2 * kk + 1][qt];
-                sf[qt] = u32x4{pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]), pack2<DT>(c[2], c[3])};
+                    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][qt][r], p.c2, -lse2[qt]));
+                            sacc[kt][qt][r] = pe * (pacc[kt][qt][r] - dlt[qt]);
+                        }
+            } else {
+#pragma unroll
+                for (int qt = 0; qt < QPW; ++qt) {
+                    const int qi = q0 + 16 * qt + c16;
+#pragma unroll
+                    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int kj = k0 + kt * 16 + 4 * g + r;
+                            float s = sacc[kt][qt][r] * p.scale;
+                            if (BIAS && kj < p.S && qi < p.L) {
+                                const uint16_t bv = p.bias[(int64_t)b * p.sb[0] + (int64_t)h * p.sb[1] + (int64_t)qi * p.sb[2] + (int64_t)kj * p.sb[3]];
+                                s = s + elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, bv));
+                            }
+                            if (kj >= p.S || (CAUSAL && kj > qi)) s = -INFINITY;
+                            // dS from the float32 P; only dS is rounded to the dtype (when packed)
+                            const float pe = __builtin_amdgcn_exp2f((s - lse[qt]) * AT_LOG2E);
+                            sacc[kt][qt][r] = pe * (pacc[kt][qt][r] - dlt[qt]);
+                        }
+                }
             }
 #pragma unroll
-            for (int i = 0; i < DT16; ++i) {
-                const u32x4 kf = read_tr<LDK>(ks[buf], kk, i, g, c16);
+            for (int kk = 0; kk < 2; ++kk) {
+                u32x4 sf[QPW];
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) acc[i][qt] = mfma16<DT>(kf, sf[qt], acc[i][qt]);
+                for (int qt = 0; qt < QPW; ++qt) {
+                    const f32x4 a = sacc[2 * kk][qt], c = sacc[2 * kk + 1][qt];
+                    sf[qt] = u32x4{pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]), pack2<DT>(c[2], c[3])};
+                }
+#pragma unroll
+                for (int i = 0; i < DT16; ++i) {
+                    const u32x4 kf = read_tr<LDK>(ks[buf], kk, i, g, c16);
+#pragma unroll
+                    for (int qt = 0; qt < QPW; ++qt) acc[i][qt] = mfma16<DT>(kf, sf[qt], acc[i][qt]);
+                }
             }
         }
         if (j + 1 < ntiles) store_tile(buf ^ 1);
@@ -644,7 +668,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs 
 
     uint16_t* dQ = p.dq + (int64_t)b * p.sdq[0] + (int64_t)h * p.sdq[1];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QPW; ++qt) {
         const int qi = q0 + 16 * qt + c16;
         if (qi >= p.L) continue;
 #pragma unroll
@@ -652,26 +676,44 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs 
     }
 }
 
-// dK / dV pass: 4 waves x 16 keys of one (batch, kv head); the queries of
-// every head of the group go by tiles of 64 through double-buffered LDS
-// (q, dout, lse, delta). Per tile: S = Q K^T (a lane owns one key),
-// P = exp(s - lse), dP = dO V^T, dS = P (dP - delta), then
-// dV^T += dO^T P and dK^T += Q^T dS with dO and Q read transposed in the
-// k-slot order of the S accumulator.
+// dK / dV pass: one workgroup owns 64 keys of one (batch, kv head); its waves
+// are groups of 4 x 16 keys, two groups at head_dim 64 (one at 128, whose
+// registers a second group would overflow). The query tiles (64 queries) of
+// every head of the group form one list, and the wave groups take alternate
+// entries, each through double-buffered LDS of its own (q, dout, lse, delta).
+// Per tile: S = Q K^T (a lane owns one key), P = exp(s - lse),
+// dP = dO V^T, dS = P (dP - delta), then dV^T += dO^T P and dK^T += Q^T dS
+// with dO and Q read transposed in the k-slot order of the S accumulator. At
+// the end the second group's partial dK and dV go through LDS and are added to
+// the first group's, in that order. Causal workgroups are dealt heaviest
+// first (the first keys see every query tile) with each (batch, kv head) on
+// one XCD, as in the forward.
+template <int D>
+constexpr int dkv_groups() { return D == 64 ? 2 : 1; }
+
 template <int DT, int D, bool CAUSAL, bool BIAS>
-__global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dkv_kernel(AttnBwdArgs p) {
+__global__ __launch_bounds__(64 * AT_WAVES * dkv_groups<D>()) void attn_bwd_dkv_kernel(AttnBwdArgs p) {
+    constexpr int DKV_GROUPS = dkv_groups<D>();
     constexpr int DS = D / 32, DT16 = D / 16, LDK = D + 8;
     constexpr int QT = 64;   // queries per tile
-    constexpr int CH = QT * D / 8, CPT = CH / (64 * AT_WAVES);
-    __shared__ __attribute__((aligned(16))) uint16_t qs[2][QT * LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t dos[2][QT * LDK];
-    __shared__ float lses[2][QT], dls[2][QT];
+    constexpr int NT = 64 * AT_WAVES;   // threads of one wave group
+    constexpr int CH = QT * D / 8, CPT = CH / NT;
+    // tl[group][0 = q, 1 = dout][buffer]: one array, so that a group's tiles are
+    // one contiguous region (the partial exchange below reuses group 1's)
+    __shared__ __attribute__((aligned(16))) uint16_t tl[DKV_GROUPS][2][2][QT * LDK];
+    __shared__ __attribute__((aligned(16))) float lses[DKV_GROUPS][2][QT];
+    __shared__ __attribute__((aligned(16))) float dls[DKV_GROUPS][2][QT];
+    static_assert(sizeof(tl[0]) >= AT_WAVES * DT16 * 2 * 64 * sizeof(f32x4), "partials fit a group's tiles");
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int grp = wave / AT_WAVES, kw = wave % AT_WAVES, tg = tid % NT;
     const int g = lane / 16, c16 = lane % 16;
-    const int b = blockIdx.z, hk = blockIdx.y;
-    const int kb0 = blockIdx.x * 64;
-    const int kj = kb0 + wave * 16 + c16;   // this lane's key
+    int kblk, bhk;
+    attn_block<CAUSAL>(p, kblk, bhk);
+    if (CAUSAL) kblk = p.nqb - 1 - kblk;   // the heaviest key blocks are the first ones
+    const int b = bhk / (p.Hq / p.group), hk = bhk % (p.Hq / p.group);
+    const int kb0 = kblk * 64, kw0 = kb0 + kw * 16;
+    const int kj = kw0 + c16;   // this lane's key
     const uint16_t* K = p.k + (int64_t)b * p.sk[0] + (int64_t)hk * p.sk[1];
     const uint16_t* V = p.v + (int64_t)b * p.sv[0] + (int64_t)hk * p.sv[1];
 
@@ -691,105 +733,141 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dkv_kernel(AttnBwdArgs
     // query tiles of all heads of the group; under the causal mask the tiles
     // wholly before this block's first key see none of its keys
     const int first_t = CAUSAL ? kb0 / QT : 0;
-    const int per_head = (p.L + QT - 1) / QT;
-    const int ntiles = p.group * max(0, per_head - first_t);
+    const int per_head = max(0, (p.L + QT - 1) / QT - first_t);
+    const int ntiles = p.group * per_head;
+    const int nsteps = (ntiles + DKV_GROUPS - 1) / DKV_GROUPS;
     u32x4 qreg[CPT], dreg[CPT];
     float lreg = INFINITY, dreg1 = 0.0f;
     auto tile_pos = [&](int n, int& hq, int& t) {
-        hq = hk * p.group + n / max(1, per_head - first_t);
-        t = first_t + n % max(1, per_head - first_t);
+        hq = hk * p.group + n / max(1, per_head);
+        t = first_t + n % max(1, per_head);
     };
     auto load_tile = [&](int n) {
+        if (n >= ntiles) return;
         int hq, t;
         tile_pos(n, hq, t);
         const uint16_t* Q = p.q + (int64_t)b * p.sq[0] + (int64_t)hq * p.sq[1];
         const uint16_t* dO = p.dout + (int64_t)b * p.sdo[0] + (int64_t)hq * p.sdo[1];
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
-            const int c = tid + i * 64 * AT_WAVES;
+            const int c = tg + i * NT;
             const int row = c / (D / 8), d8 = (c % (D / 8)) * 8;
             const int qi = t * QT + row;
             qreg[i] = qi < p.L ? *reinterpret_cast<const u32x4*>(Q + (int64_t)qi * p.sq[2] + d8) : u32x4{0, 0, 0, 0};
             dreg[i] = qi < p.L ? *reinterpret_cast<const u32x4*>(dO + (int64_t)qi * p.sdo[2] + d8) : u32x4{0, 0, 0, 0};
         }
-        if (tid < QT) {
-            const int qi = t * QT + tid;
-            lreg = qi < p.L ? p.lse[(int64_t)b * p.sl[0] + (int64_t)hq * p.sl[1] + (int64_t)qi * p.sl[2]] : INFINITY;
+        if (tg < QT) {
+            const int qi = t * QT + tg;
+            // lse in log2 units; +inf past the last query gives P = 0 there
+            lreg = qi < p.L ? p.lse[(int64_t)b * p.sl[0] + (int64_t)hq * p.sl[1] + (int64_t)qi * p.sl[2]] * AT_LOG2E : INFINITY;
             dreg1 = qi < p.L ? p.delta[((int64_t)b * p.Hq + hq) * p.L + qi] : 0.0f;
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](int n, int buf) {
+        if (n >= ntiles) return;
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
-            const int c = tid + i * 64 * AT_WAVES;
+            const int c = tg + i * NT;
             const int row = c / (D / 8), d8 = (c % (D / 8)) * 8;
-            *reinterpret_cast<u32x4*>(&qs[buf][row * LDK + d8]) = qreg[i];
-            *reinterpret_cast<u32x4*>(&dos[buf][row * LDK + d8]) = dreg[i];
+            *reinterpret_cast<u32x4*>(&tl[grp][0][buf][row * LDK + d8]) = qreg[i];
+            *reinterpret_cast<u32x4*>(&tl[grp][1][buf][row * LDK + d8]) = dreg[i];
         }
-        if (tid < QT) {
-            lses[buf][tid] = lreg;
-            dls[buf][tid] = dreg1;
+        if (tg < QT) {
+            lses[grp][buf][tg] = lreg;
+            dls[grp][buf][tg] = dreg1;
         }
     };
-    if (ntiles > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
+    load_tile(grp);
+    store_tile(grp, 0);
     __syncthreads();
 
-    for (int n = 0; n < ntiles; ++n) {
-        const int buf = n & 1;
-        int hq, t;
-        tile_pos(n, hq, t);
-        if (n + 1 < ntiles) load_tile(n + 1);
-        // S and dP: 4 blocks of 16 queries (rows) x this wave's 16 keys (columns)
-        f32x4 sacc[4], pacc[4];
+    for (int st = 0; st < nsteps; ++st) {
+        const int buf = st & 1;
+        const int n = st * DKV_GROUPS + grp;   // this group's tile
+        load_tile(n + DKV_GROUPS);
+        int hq = 0, t = 0;
+        if (n < ntiles) tile_pos(n, hq, t);
+        const int qt0 = t * QT;
+        // nothing to add: no tile left for this group, or every key of the wave follows every query
+        if (n < ntiles && !(CAUSAL && kw0 > qt0 + QT - 1)) {
+            // S and dP: 4 blocks of 16 queries (rows) x this wave's 16 keys (columns)
+            f32x4 sacc[4], pacc[4];
 #pragma unroll
-        for (int qt = 0; qt < 4; ++qt) {
-            sacc[qt] = f32x4{0, 0, 0, 0};
-            pacc[qt] = f32x4{0, 0, 0, 0};
+            for (int qt = 0; qt < 4; ++qt) {
+                sacc[qt] = f32x4{0, 0, 0, 0};
+                pacc[qt] = f32x4{0, 0, 0, 0};
 #pragma unroll
-            for (int ds = 0; ds < DS; ++ds) {
-                const u32x4 qa = *reinterpret_cast<const u32x4*>(&qs[buf][(qt * 16 + c16) * LDK + 32 * ds + 8 * g]);
-                const u32x4 da = *reinterpret_cast<const u32x4*>(&dos[buf][(qt * 16 + c16) * LDK + 32 * ds + 8 * g]);
-                sacc[qt] = mfma16<DT>(qa, kf[ds], sacc[qt]);
-                pacc[qt] = mfma16<DT>(da, vf[ds], pacc[qt]);
-            }
-        }
-        // P (rounded to the dtype) into sacc, dS into pacc
-#pragma unroll
-        for (int qt = 0; qt < 4; ++qt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = qt * 16 + 4 * g + r;
-                const int qi = t * QT + row;
-                float s = sacc[qt][r] * p.scale;
-                if (BIAS && kj < p.S && qi < p.L) {
-                    const uint16_t bv = p.bias[(int64_t)b * p.sb[0] + (int64_t)hq * p.sb[1] + (int64_t)qi * p.sb[2] + (int64_t)kj * p.sb[3]];
-                    s = s + elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, bv));
+                for (int ds = 0; ds < DS; ++ds) {
+                    const u32x4 qa = *reinterpret_cast<const u32x4*>(&tl[grp][0][buf][(qt * 16 + c16) * LDK + 32 * ds + 8 * g]);
+                    const u32x4 da = *reinterpret_cast<const u32x4*>(&tl[grp][1][buf][(qt * 16 + c16) * LDK + 32 * ds + 8 * g]);
+                    sacc[qt] = mfma16<DT>(qa, kf[ds], sacc[qt]);
+                    pacc[qt] = mfma16<DT>(da, vf[ds], pacc[qt]);
                 }
-                if (kj >= p.S || (CAUSAL && kj > qi)) s = -INFINITY;
-                // P and dS from the float32 P; each is rounded to the dtype when packed
-                const float pe = __builtin_amdgcn_exp2f((s - lses[buf][row]) * AT_LOG2E);
-                sacc[qt][r] = pe;
-                pacc[qt][r] = pe * (pacc[qt][r] - dls[buf][row]);
+            }
+            // P (rounded to the dtype when packed) into sacc, dS into pacc;
+            // rows 4g..4g+3 of each 16-query block share one 16-byte LDS read
+            const bool plain = !BIAS && kw0 + 15 < p.S && !(CAUSAL && kw0 + 15 > qt0);
+#pragma unroll
+            for (int qt = 0; qt < 4; ++qt) {
+                const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lses[grp][buf][qt * 16 + 4 * g]);
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dls[grp][buf][qt * 16 + 4 * g]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x;
+                    if (plain) {
+                        x = __builtin_fmaf(sacc[qt][r], p.c2, -l4[r]);
+                    } else {
+                        const int qi = qt0 + qt * 16 + 4 * g + r;
+                        float s = sacc[qt][r] * p.scale;
+                        if (BIAS && kj < p.S && qi < p.L) {
+                            const uint16_t bv = p.bias[(int64_t)b * p.sb[0] + (int64_t)hq * p.sb[1] + (int64_t)qi * p.sb[2] + (int64_t)kj * p.sb[3]];
+                            s = s + elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, bv));
+                        }
+                        if (kj >= p.S || (CAUSAL && kj > qi)) s = -INFINITY;
+                        x = s * AT_LOG2E - l4[r];
+                    }
+                    // P and dS from the float32 P; each is rounded to the dtype when packed
+                    const float pe = __builtin_amdgcn_exp2f(x);
+                    sacc[qt][r] = pe;
+                    pacc[qt][r] = pe * (pacc[qt][r] - d4[r]);
+                }
             }
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const f32x4 a = sacc[2 * kk], c = sacc[2 * kk + 1];
-            const u32x4 pf = u32x4{pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]), pack2<DT>(c[2], c[3])};
-            const f32x4 e = pacc[2 * kk], f = pacc[2 * kk + 1];
-            const u32x4 sf = u32x4{pack2<DT>(e[0], e[1]), pack2<DT>(e[2], e[3]), pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3])};
+            for (int kk = 0; kk < 2; ++kk) {
+                const f32x4 a = sacc[2 * kk], c = sacc[2 * kk + 1];
+                const u32x4 pf = u32x4{pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]), pack2<DT>(c[2], c[3])};
+                const f32x4 e = pacc[2 * kk], f = pacc[2 * kk + 1];
+                const u32x4 sf = u32x4{pack2<DT>(e[0], e[1]), pack2<DT>(e[2], e[3]), pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3])};
 #pragma unroll
-            for (int i = 0; i < DT16; ++i) {
-                dva[i] = mfma16<DT>(read_tr<LDK>(dos[buf], kk, i, g, c16), pf, dva[i]);
-                dka[i] = mfma16<DT>(read_tr<LDK>(qs[buf], kk, i, g, c16), sf, dka[i]);
+                for (int i = 0; i < DT16; ++i) {
+                    dva[i] = mfma16<DT>(read_tr<LDK>(tl[grp][1][buf], kk, i, g, c16), pf, dva[i]);
+                    dka[i] = mfma16<DT>(read_tr<LDK>(tl[grp][0][buf], kk, i, g, c16), sf, dka[i]);
+                }
             }
         }
-        if (n + 1 < ntiles) store_tile(buf ^ 1);
+        // buffer buf^1 was last read in step st-1, which every wave left through the barrier below
+        store_tile(n + DKV_GROUPS, buf ^ 1);
         __syncthreads();
     }
 
+    if constexpr (DKV_GROUPS == 2) {
+        // second group's partials through LDS (its tile buffers are free now), added in group order
+        f32x4* part = reinterpret_cast<f32x4*>(&tl[1][0][0][0]);
+        if (grp == 1) {
+#pragma unroll
+            for (int i = 0; i < DT16; ++i) {
+                part[((kw * DT16 + i) * 2 + 0) * 64 + lane] = dka[i];
+                part[((kw * DT16 + i) * 2 + 1) * 64 + lane] = dva[i];
+            }
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int i = 0; i < DT16; ++i) {
+            dka[i] += part[((kw * DT16 + i) * 2 + 0) * 64 + lane];
+            dva[i] += part[((kw * DT16 + i) * 2 + 1) * 64 + lane];
+        }
+    }
     if (kj >= p.S) return;
     uint16_t* dK = p.dk + (int64_t)b * p.sdk[0] + (int64_t)hk * p.sdk[1] + (int64_t)kj * p.sdk[2];
     uint16_t* dV = p.dv + (int64_t)b * p.sdv[0] + (int64_t)hk * p.sdv[1] + (int64_t)kj * p.sdv[2];
@@ -800,22 +878,40 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dkv_kernel(AttnBwdArgs
     }
 }
 
-template <int DT, int D>
-void launch_attn_bwd(const AttnBwdArgs& a, bool causal, bool bias, dim3 gq, dim3 gkv, hipStream_t s) {
+template <int DT, int D, bool C, bool B>
+void launch_attn_bwd_cb(AttnBwdArgs a, int64_t batch, int64_t heads, int64_t L, dim3 gkv, hipStream_t s) {
     const dim3 block(64 * AT_WAVES);
-#define TVK_BWD(C, B)                                                                                     \
-    do {                                                                                                  \
-        if (gq.x) hipLaunchKernelGGL((attn_bwd_dq_kernel<DT, D, C, B>), gq, block, 0, s, a);              \
-        if (gkv.x) hipLaunchKernelGGL((attn_bwd_dkv_kernel<DT, D, C, B>), gkv, block, 0, s, a);           \
-    } while (0)
-    if (causal) {
-        if (bias) TVK_BWD(true, true);
-        else TVK_BWD(true, false);
-    } else {
-        if (bias) TVK_BWD(false, true);
-        else TVK_BWD(false, false);
+    if (L > 0) {
+        a.BH = (int)(batch * heads);
+        // query columns per wave as in the forward: two at head_dim 64 on large grids
+        bool two = false;
+        if constexpr (D == 64) two = batch * heads * ((L + 127) / 128) >= 2048;
+        if (two) {
+            a.nqb = (int)((L + 127) / 128);
+            hipLaunchKernelGGL((attn_bwd_dq_kernel<DT, D, C, B, 2>), dim3((unsigned)(a.nqb * a.BH)), block, 0, s, a);
+        } else {
+            a.nqb = (int)((L + 63) / 64);
+            hipLaunchKernelGGL((attn_bwd_dq_kernel<DT, D, C, B, 1>), dim3((unsigned)(a.nqb * a.BH)), block, 0, s, a);
+        }
     }
-#undef TVK_BWD
+    if (gkv.x) {
+        // workgroups dealt by attn_block: nqb = key blocks per (batch, kv head), BH = batch * kv heads
+        a.nqb = (int)gkv.x;
+        a.BH = (int)(gkv.y * gkv.z);
+        hipLaunchKernelGGL((attn_bwd_dkv_kernel<DT, D, C, B>), dim3(gkv.x * gkv.y * gkv.z), dim3(64 * AT_WAVES * dkv_groups<D>()), 0, s, a);
+    }
+}
+
+template <int DT, int D>
+void launch_attn_bwd(const AttnBwdArgs& a, bool causal, bool bias, int64_t batch, int64_t heads, int64_t L, dim3 gkv,
+                     hipStream_t s) {
+    if (causal) {
+        if (bias) launch_attn_bwd_cb<DT, D, true, true>(a, batch, heads, L, gkv, s);
+        else launch_attn_bwd_cb<DT, D, true, false>(a, batch, heads, L, gkv, s);
+    } else {
+        if (bias) launch_attn_bwd_cb<DT, D, false, true>(a, batch, heads, L, gkv, s);
+        else launch_attn_bwd_cb<DT, D, false, false>(a, batch, heads, L, gkv, s);
+    }
 }
 
 }  // namespace
@@ -897,7 +993,8 @@ tvk_status check_attention(const tvk_attention_desc* d, const char* who) {
     if (d->heads_q % d->heads_kv != 0) return bad(TVK_ERR_INVALID, "heads_q is not a multiple of heads_kv");
     if (d->head_dim != d->head_dim_v || (d->head_dim != 64 && d->head_dim != 128))
         return bad(TVK_ERR_UNSUPPORTED, "head_dim == head_dim_v in {64, 128} only");
-    if (d->batch > 65535 || d->heads_q > 65535 || d->len_q > (int64_t)0x7fffffff || d->len_kv > (int64_t)0x7fffffff)
+    if (d->batch > 65535 || d->heads_q > 65535 || d->len_q > ((int64_t)1 << 30) || d->len_kv > ((int64_t)1 << 30) ||
+        d->batch * d->heads_q * ((d->len_q + 63) / 64) > (int64_t)0x7fffffff)
         return bad(TVK_ERR_UNSUPPORTED, "grid too large");
     return TVK_OK;
 }
@@ -951,20 +1048,20 @@ extern "C" tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc) {
     a.Hq = (int)d->heads_q;
     a.group = (int)(d->heads_q / d->heads_kv);
     a.scale = (float)d->scale;
+    a.c2 = a.scale * AT_LOG2E;
     int dev = 0;
     (void)hipGetDevice(&dev);
     a.delta = static_cast<float*>(device_workspace(dev, (size_t)std::max<int64_t>(1, d->batch * d->heads_q * d->len_q) * 4));
     if (!a.delta) return fail(TVK_ERR_OOM, "tvk_attention_bwd: workspace allocation failed");
-    const dim3 gq((unsigned)((d->len_q + AT_BM - 1) / AT_BM), (unsigned)d->heads_q, (unsigned)d->batch);
     const dim3 gkv((unsigned)((d->len_kv + 63) / 64), (unsigned)d->heads_kv, (unsigned)d->batch);
     const hipStream_t s = resolve_stream(d->stream);
     const bool bias = d->bias != nullptr;
     if (d->dtype == TVK_F16) {
-        if (d->head_dim == 64) launch_attn_bwd<TVK_F16, 64>(a, d->causal != 0, bias, gq, gkv, s);
-        else launch_attn_bwd<TVK_F16, 128>(a, d->causal != 0, bias, gq, gkv, s);
+        if (d->head_dim == 64) launch_attn_bwd<TVK_F16, 64>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, gkv, s);
+        else launch_attn_bwd<TVK_F16, 128>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, gkv, s);
     } else {
-        if (d->head_dim == 64) launch_attn_bwd<TVK_BF16, 64>(a, d->causal != 0, bias, gq, gkv, s);
-        else launch_attn_bwd<TVK_BF16, 128>(a, d->causal != 0, bias, gq, gkv, s);
+        if (d->head_dim == 64) launch_attn_bwd<TVK_BF16, 64>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, gkv, s);
+        else launch_attn_bwd<TVK_BF16, 128>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, gkv, s);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_attention_bwd: launch failed: ") + hipGetErrorString(e));
