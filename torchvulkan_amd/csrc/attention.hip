@@ -676,10 +676,13 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs 
     }
 }
 
-// dK / dV pass: one workgroup owns 64 keys of one (batch, kv head); its waves
-// are groups of 4 x 16 keys, two groups at head_dim 64 (one at 128, whose
-// registers a second group would overflow). The query tiles (64 queries) of
-// every head of the group form one list, and the wave groups take alternate
+// dK / dV pass: one workgroup owns 4 waves x KPW x 16 keys of one (batch, kv
+// head) per wave group. Small grids run two groups of 4 waves on 64 keys
+// (head_dim 64; at 128 a second group would overflow the registers); large
+// ones one group whose waves own two 16-key columns (128 keys), so each q and
+// dout fragment read from LDS feeds twice the MFMAs (one column per wave
+// leaves the pass bound by LDS reads). The query tiles (64 queries) of every
+// head of the group form one list, and the wave groups take alternate
 // entries, each through double-buffered LDS of its own (q, dout, lse, delta).
 // Per tile: S = Q K^T (a lane owns one key), P = exp(s - lse),
 // dP = dO V^T, dS = P (dP - delta), then dV^T += dO^T P and dK^T += Q^T dS
@@ -688,47 +691,55 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs 
 // the first group's, in that order. Causal workgroups are dealt heaviest
 // first (the first keys see every query tile) with each (batch, kv head) on
 // one XCD, as in the forward.
-template <int D>
-constexpr int dkv_groups() { return D == 64 ? 2 : 1; }
+template <int D, int KPW>
+constexpr int dkv_groups() { return D == 64 && KPW == 1 ? 2 : 1; }
 
-template <int DT, int D, bool CAUSAL, bool BIAS>
-__global__ __launch_bounds__(64 * AT_WAVES * dkv_groups<D>()) void attn_bwd_dkv_kernel(AttnBwdArgs p) {
-    constexpr int DKV_GROUPS = dkv_groups<D>();
+template <int DT, int D, bool CAUSAL, bool BIAS, int KPW>
+__global__ __launch_bounds__((64 * AT_WAVES * dkv_groups<D, KPW>())) void attn_bwd_dkv_kernel(AttnBwdArgs p) {
+    constexpr int KW = AT_WAVES;
+    constexpr int DKV_GROUPS = dkv_groups<D, KPW>();
+    constexpr int KB = 16 * KPW * KW;   // keys per workgroup
     constexpr int DS = D / 32, DT16 = D / 16, LDK = D + 8;
     constexpr int QT = 64;   // queries per tile
-    constexpr int NT = 64 * AT_WAVES;   // threads of one wave group
+    constexpr int NT = 64 * KW;   // threads of one wave group
     constexpr int CH = QT * D / 8, CPT = CH / NT;
     // tl[group][0 = q, 1 = dout][buffer]: one array, so that a group's tiles are
     // one contiguous region (the partial exchange below reuses group 1's)
     __shared__ __attribute__((aligned(16))) uint16_t tl[DKV_GROUPS][2][2][QT * LDK];
     __shared__ __attribute__((aligned(16))) float lses[DKV_GROUPS][2][QT];
     __shared__ __attribute__((aligned(16))) float dls[DKV_GROUPS][2][QT];
-    static_assert(sizeof(tl[0]) >= AT_WAVES * DT16 * 2 * 64 * sizeof(f32x4), "partials fit a group's tiles");
+    static_assert(DKV_GROUPS == 1 || sizeof(tl[0]) >= KW * KPW * DT16 * 2 * 64 * sizeof(f32x4), "partials fit a group's tiles");
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-    const int grp = wave / AT_WAVES, kw = wave % AT_WAVES, tg = tid % NT;
+    const int grp = wave / KW, kw = wave % KW, tg = tid % NT;
     const int g = lane / 16, c16 = lane % 16;
     int kblk, bhk;
     attn_block<CAUSAL>(p, kblk, bhk);
     if (CAUSAL) kblk = p.nqb - 1 - kblk;   // the heaviest key blocks are the first ones
     const int b = bhk / (p.Hq / p.group), hk = bhk % (p.Hq / p.group);
-    const int kb0 = kblk * 64, kw0 = kb0 + kw * 16;
-    const int kj = kw0 + c16;   // this lane's key
+    const int kb0 = kblk * KB, kw0 = kb0 + kw * 16 * KPW;   // this wave's first key
     const uint16_t* K = p.k + (int64_t)b * p.sk[0] + (int64_t)hk * p.sk[1];
     const uint16_t* V = p.v + (int64_t)b * p.sv[0] + (int64_t)hk * p.sv[1];
 
-    u32x4 kf[DS], vf[DS];
+    // kc-th 16-key column of the wave: lane key kw0 + 16 kc + c16
+    u32x4 kf[KPW][DS], vf[KPW][DS];
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-        kf[ds] = kj < p.S ? *reinterpret_cast<const u32x4*>(K + (int64_t)kj * p.sk[2] + 32 * ds + 8 * g) : u32x4{0, 0, 0, 0};
-        vf[ds] = kj < p.S ? *reinterpret_cast<const u32x4*>(V + (int64_t)kj * p.sv[2] + 32 * ds + 8 * g) : u32x4{0, 0, 0, 0};
-    }
-    f32x4 dka[DT16], dva[DT16];
+    for (int kc = 0; kc < KPW; ++kc) {
+        const int kj = kw0 + 16 * kc + c16;
 #pragma unroll
-    for (int i = 0; i < DT16; ++i) {
-        dka[i] = f32x4{0, 0, 0, 0};
-        dva[i] = f32x4{0, 0, 0, 0};
+        for (int ds = 0; ds < DS; ++ds) {
+            kf[kc][ds] = kj < p.S ? *reinterpret_cast<const u32x4*>(K + (int64_t)kj * p.sk[2] + 32 * ds + 8 * g) : u32x4{0, 0, 0, 0};
+            vf[kc][ds] = kj < p.S ? *reinterpret_cast<const u32x4*>(V + (int64_t)kj * p.sv[2] + 32 * ds + 8 * g) : u32x4{0, 0, 0, 0};
+        }
     }
+    f32x4 dka[KPW][DT16], dva[KPW][DT16];
+#pragma unroll
+    for (int kc = 0; kc < KPW; ++kc)
+#pragma unroll
+        for (int i = 0; i < DT16; ++i) {
+            dka[kc][i] = f32x4{0, 0, 0, 0};
+            dva[kc][i] = f32x4{0, 0, 0, 0};
+        }
 
     // query tiles of all heads of the group; under the causal mask the tiles
     // wholly before this block's first key see none of its keys
@@ -790,58 +801,77 @@ __global__ __launch_bounds__(64 * AT_WAVES * dkv_groups<D>()) void attn_bwd_dkv_
         const int qt0 = t * QT;
         // nothing to add: no tile left for this group, or every key of the wave follows every query
         if (n < ntiles && !(CAUSAL && kw0 > qt0 + QT - 1)) {
-            // S and dP: 4 blocks of 16 queries (rows) x this wave's 16 keys (columns)
-            f32x4 sacc[4], pacc[4];
+            // S and dP: 4 blocks of 16 queries (rows) x the wave's KPW 16-key columns
+            f32x4 sacc[4][KPW], pacc[4][KPW];
 #pragma unroll
             for (int qt = 0; qt < 4; ++qt) {
-                sacc[qt] = f32x4{0, 0, 0, 0};
-                pacc[qt] = f32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int kc = 0; kc < KPW; ++kc) {
+                    sacc[qt][kc] = f32x4{0, 0, 0, 0};
+                    pacc[qt][kc] = f32x4{0, 0, 0, 0};
+                }
 #pragma unroll
                 for (int ds = 0; ds < DS; ++ds) {
                     const u32x4 qa = *reinterpret_cast<const u32x4*>(&tl[grp][0][buf][(qt * 16 + c16) * LDK + 32 * ds + 8 * g]);
                     const u32x4 da = *reinterpret_cast<const u32x4*>(&tl[grp][1][buf][(qt * 16 + c16) * LDK + 32 * ds + 8 * g]);
-                    sacc[qt] = mfma16<DT>(qa, kf[ds], sacc[qt]);
-                    pacc[qt] = mfma16<DT>(da, vf[ds], pacc[qt]);
+#pragma unroll
+                    for (int kc = 0; kc < KPW; ++kc) {
+                        sacc[qt][kc] = mfma16<DT>(qa, kf[kc][ds], sacc[qt][kc]);
+                        pacc[qt][kc] = mfma16<DT>(da, vf[kc][ds], pacc[qt][kc]);
+                    }
                 }
             }
             // P (rounded to the dtype when packed) into sacc, dS into pacc;
             // rows 4g..4g+3 of each 16-query block share one 16-byte LDS read
-            const bool plain = !BIAS && kw0 + 15 < p.S && !(CAUSAL && kw0 + 15 > qt0);
+            const bool plain = !BIAS && kw0 + 16 * KPW - 1 < p.S && !(CAUSAL && kw0 + 16 * KPW - 1 > qt0);
 #pragma unroll
             for (int qt = 0; qt < 4; ++qt) {
                 const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lses[grp][buf][qt * 16 + 4 * g]);
                 const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dls[grp][buf][qt * 16 + 4 * g]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float x;
-                    if (plain) {
-                        x = __builtin_fmaf(sacc[qt][r], p.c2, -l4[r]);
-                    } else {
-                        const int qi = qt0 + qt * 16 + 4 * g + r;
-                        float s = sacc[qt][r] * p.scale;
-                        if (BIAS && kj < p.S && qi < p.L) {
-                            const uint16_t bv = p.bias[(int64_t)b * p.sb[0] + (int64_t)hq * p.sb[1] + (int64_t)qi * p.sb[2] + (int64_t)kj * p.sb[3]];
-                            s = s + elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, bv));
+                for (int kc = 0; kc < KPW; ++kc) {
+                    const int kj = kw0 + 16 * kc + c16;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float x;
+                        if (plain) {
+                            x = __builtin_fmaf(sacc[qt][kc][r], p.c2, -l4[r]);
+                        } else {
+                            const int qi = qt0 + qt * 16 + 4 * g + r;
+                            float s = sacc[qt][kc][r] * p.scale;
+                            if (BIAS && kj < p.S && qi < p.L) {
+                                const uint16_t bv = p.bias[(int64_t)b * p.sb[0] + (int64_t)hq * p.sb[1] + (int64_t)qi * p.sb[2] + (int64_t)kj * p.sb[3]];
+                                s = s + elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, bv));
+                            }
+                            if (kj >= p.S || (CAUSAL && kj > qi)) s = -INFINITY;
+                            x = s * AT_LOG2E - l4[r];
                         }
-                        if (kj >= p.S || (CAUSAL && kj > qi)) s = -INFINITY;
-                        x = s * AT_LOG2E - l4[r];
+                        // P and dS from the float32 P; each is rounded to the dtype when packed
+                        const float pe = __builtin_amdgcn_exp2f(x);
+                        sacc[qt][kc][r] = pe;
+                        pacc[qt][kc][r] = pe * (pacc[qt][kc][r] - d4[r]);
                     }
-                    // P and dS from the float32 P; each is rounded to the dtype when packed
-                    const float pe = __builtin_amdgcn_exp2f(x);
-                    sacc[qt][r] = pe;
-                    pacc[qt][r] = pe * (pacc[qt][r] - d4[r]);
                 }
             }
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
-                const f32x4 a = sacc[2 * kk], c = sacc[2 * kk + 1];
-                const u32x4 pf = u32x4{pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]), pack2<DT>(c[2], c[3])};
-                const f32x4 e = pacc[2 * kk], f = pacc[2 * kk + 1];
-                const u32x4 sf = u32x4{pack2<DT>(e[0], e[1]), pack2<DT>(e[2], e[3]), pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3])};
+                u32x4 pf[KPW], sf[KPW];
+#pragma unroll
+                for (int kc = 0; kc < KPW; ++kc) {
+                    const f32x4 a = sacc[2 * kk][kc], c = sacc[2 * kk + 1][kc];
+                    pf[kc] = u32x4{pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]), pack2<DT>(c[2], c[3])};
+                    const f32x4 e = pacc[2 * kk][kc], f = pacc[2 * kk + 1][kc];
+                    sf[kc] = u32x4{pack2<DT>(e[0], e[1]), pack2<DT>(e[2], e[3]), pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3])};
+                }
 #pragma unroll
                 for (int i = 0; i < DT16; ++i) {
-                    dva[i] = mfma16<DT>(read_tr<LDK>(tl[grp][1][buf], kk, i, g, c16), pf, dva[i]);
-                    dka[i] = mfma16<DT>(read_tr<LDK>(tl[grp][0][buf], kk, i, g, c16), sf, dka[i]);
+                    const u32x4 dot = read_tr<LDK>(tl[grp][1][buf], kk, i, g, c16);
+                    const u32x4 qtr = read_tr<LDK>(tl[grp][0][buf], kk, i, g, c16);
+#pragma unroll
+                    for (int kc = 0; kc < KPW; ++kc) {
+                        dva[kc][i] = mfma16<DT>(dot, pf[kc], dva[kc][i]);
+                        dka[kc][i] = mfma16<DT>(qtr, sf[kc], dka[kc][i]);
+                    }
                 }
             }
         }
@@ -855,31 +885,40 @@ __global__ __launch_bounds__(64 * AT_WAVES * dkv_groups<D>()) void attn_bwd_dkv_
         f32x4* part = reinterpret_cast<f32x4*>(&tl[1][0][0][0]);
         if (grp == 1) {
 #pragma unroll
-            for (int i = 0; i < DT16; ++i) {
-                part[((kw * DT16 + i) * 2 + 0) * 64 + lane] = dka[i];
-                part[((kw * DT16 + i) * 2 + 1) * 64 + lane] = dva[i];
-            }
+            for (int kc = 0; kc < KPW; ++kc)
+#pragma unroll
+                for (int i = 0; i < DT16; ++i) {
+                    part[(((kw * KPW + kc) * DT16 + i) * 2 + 0) * 64 + lane] = dka[kc][i];
+                    part[(((kw * KPW + kc) * DT16 + i) * 2 + 1) * 64 + lane] = dva[kc][i];
+                }
         }
         __syncthreads();
         if (grp == 1) return;
 #pragma unroll
-        for (int i = 0; i < DT16; ++i) {
-            dka[i] += part[((kw * DT16 + i) * 2 + 0) * 64 + lane];
-            dva[i] += part[((kw * DT16 + i) * 2 + 1) * 64 + lane];
-        }
-    }
-    if (kj >= p.S) return;
-    uint16_t* dK = p.dk + (int64_t)b * p.sdk[0] + (int64_t)hk * p.sdk[1] + (int64_t)kj * p.sdk[2];
-    uint16_t* dV = p.dv + (int64_t)b * p.sdv[0] + (int64_t)hk * p.sdv[1] + (int64_t)kj * p.sdv[2];
+        for (int kc = 0; kc < KPW; ++kc)
 #pragma unroll
-    for (int i = 0; i < DT16; ++i) {
-        store4<DT>(dK + 16 * i + 4 * g, dka[i], p.scale);
-        store4<DT>(dV + 16 * i + 4 * g, dva[i], 1.0f);
+            for (int i = 0; i < DT16; ++i) {
+                dka[kc][i] += part[(((kw * KPW + kc) * DT16 + i) * 2 + 0) * 64 + lane];
+                dva[kc][i] += part[(((kw * KPW + kc) * DT16 + i) * 2 + 1) * 64 + lane];
+            }
+    }
+#pragma unroll
+    for (int kc = 0; kc < KPW; ++kc) {
+        const int kj = kw0 + 16 * kc + c16;
+        if (kj >= p.S) continue;
+        uint16_t* dK = p.dk + (int64_t)b * p.sdk[0] + (int64_t)hk * p.sdk[1] + (int64_t)kj * p.sdk[2];
+        uint16_t* dV = p.dv + (int64_t)b * p.sdv[0] + (int64_t)hk * p.sdv[1] + (int64_t)kj * p.sdv[2];
+#pragma unroll
+        for (int i = 0; i < DT16; ++i) {
+            store4<DT>(dK + 16 * i + 4 * g, dka[kc][i], p.scale);
+            store4<DT>(dV + 16 * i + 4 * g, dva[kc][i], 1.0f);
+        }
     }
 }
 
+
 template <int DT, int D, bool C, bool B>
-void launch_attn_bwd_cb(AttnBwdArgs a, int64_t batch, int64_t heads, int64_t L, dim3 gkv, hipStream_t s) {
+void launch_attn_bwd_cb(AttnBwdArgs a, int64_t batch, int64_t heads, int64_t L, int64_t S, hipStream_t s) {
     const dim3 block(64 * AT_WAVES);
     if (L > 0) {
         a.BH = (int)(batch * heads);
@@ -894,23 +933,34 @@ void launch_attn_bwd_cb(AttnBwdArgs a, int64_t batch, int64_t heads, int64_t L, 
             hipLaunchKernelGGL((attn_bwd_dq_kernel<DT, D, C, B, 1>), dim3((unsigned)(a.nqb * a.BH)), block, 0, s, a);
         }
     }
-    if (gkv.x) {
+    if (S > 0) {
         // workgroups dealt by attn_block: nqb = key blocks per (batch, kv head), BH = batch * kv heads
-        a.nqb = (int)gkv.x;
-        a.BH = (int)(gkv.y * gkv.z);
-        hipLaunchKernelGGL((attn_bwd_dkv_kernel<DT, D, C, B>), dim3(gkv.x * gkv.y * gkv.z), dim3(64 * AT_WAVES * dkv_groups<D>()), 0, s, a);
+        a.BH = (int)(batch * heads / a.group);
+        bool wide = false;
+        if constexpr (D == 64) {
+            if ((int64_t)a.BH * ((S + 127) / 128) >= 512) {
+                wide = true;
+                a.nqb = (int)((S + 127) / 128);
+                hipLaunchKernelGGL((attn_bwd_dkv_kernel<DT, D, C, B, 2>), dim3((unsigned)(a.nqb * a.BH)), dim3(64 * AT_WAVES), 0, s, a);
+            }
+        }
+        if (!wide) {
+            a.nqb = (int)((S + 63) / 64);
+            hipLaunchKernelGGL((attn_bwd_dkv_kernel<DT, D, C, B, 1>), dim3((unsigned)(a.nqb * a.BH)),
+                               dim3(64 * AT_WAVES * dkv_groups<D, 1>()), 0, s, a);
+        }
     }
 }
 
 template <int DT, int D>
-void launch_attn_bwd(const AttnBwdArgs& a, bool causal, bool bias, int64_t batch, int64_t heads, int64_t L, dim3 gkv,
+void launch_attn_bwd(const AttnBwdArgs& a, bool causal, bool bias, int64_t batch, int64_t heads, int64_t L, int64_t S,
                      hipStream_t s) {
     if (causal) {
-        if (bias) launch_attn_bwd_cb<DT, D, true, true>(a, batch, heads, L, gkv, s);
-        else launch_attn_bwd_cb<DT, D, true, false>(a, batch, heads, L, gkv, s);
+        if (bias) launch_attn_bwd_cb<DT, D, true, true>(a, batch, heads, L, S, s);
+        else launch_attn_bwd_cb<DT, D, true, false>(a, batch, heads, L, S, s);
     } else {
-        if (bias) launch_attn_bwd_cb<DT, D, false, true>(a, batch, heads, L, gkv, s);
-        else launch_attn_bwd_cb<DT, D, false, false>(a, batch, heads, L, gkv, s);
+        if (bias) launch_attn_bwd_cb<DT, D, false, true>(a, batch, heads, L, S, s);
+        else launch_attn_bwd_cb<DT, D, false, false>(a, batch, heads, L, S, s);
     }
 }
 
@@ -1053,15 +1103,14 @@ extern "C" tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc) {
     (void)hipGetDevice(&dev);
     a.delta = static_cast<float*>(device_workspace(dev, (size_t)std::max<int64_t>(1, d->batch * d->heads_q * d->len_q) * 4));
     if (!a.delta) return fail(TVK_ERR_OOM, "tvk_attention_bwd: workspace allocation failed");
-    const dim3 gkv((unsigned)((d->len_kv + 63) / 64), (unsigned)d->heads_kv, (unsigned)d->batch);
     const hipStream_t s = resolve_stream(d->stream);
     const bool bias = d->bias != nullptr;
     if (d->dtype == TVK_F16) {
-        if (d->head_dim == 64) launch_attn_bwd<TVK_F16, 64>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, gkv, s);
-        else launch_attn_bwd<TVK_F16, 128>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, gkv, s);
+        if (d->head_dim == 64) launch_attn_bwd<TVK_F16, 64>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, d->len_kv, s);
+        else launch_attn_bwd<TVK_F16, 128>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, d->len_kv, s);
     } else {
-        if (d->head_dim == 64) launch_attn_bwd<TVK_BF16, 64>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, gkv, s);
-        else launch_attn_bwd<TVK_BF16, 128>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, gkv, s);
+        if (d->head_dim == 64) launch_attn_bwd<TVK_BF16, 64>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, d->len_kv, s);
+        else launch_attn_bwd<TVK_BF16, 128>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, d->len_kv, s);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_attention_bwd: launch failed: ") + hipGetErrorString(e));
