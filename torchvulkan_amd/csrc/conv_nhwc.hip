@@ -13,7 +13,10 @@
 //
 // Layouts. The activation that is gathered goes to NHWC in the library
 // workspace first (one transpose pass), so that 8 consecutive channels are one
-// 16-byte load; the weight is permuted to tap-major order.
+// 16-byte load, with a zero border wide enough for every tap of every row
+// pixel: the loads need no bounds checks, and each lane's offsets are set
+// once, a stage adding one uniform tap and channel offset. The weight is
+// permuted to tap-major order.
 //   forward     C[p][co] = sum_{t,c} x_nhwc[pix(p) + off(t)][c] * Wf[co][t][c]
 //               p = output pixel (n, oh, ow); y is written NCHW
 //   grad input  C[p][c]  = sum_{t,co} dy_nhwc[pix(p) + off(t)][co] * Wd[c][t][co]
@@ -26,6 +29,7 @@
 // v_mfma_f32_16x16x32 on 64-column wave tiles.
 #include "tvk_common.h"
 #include "gemm_common.h"
+#include "convert.h"
 
 #include <algorithm>
 #include <cmath>
@@ -44,13 +48,14 @@ constexpr int V_BK = 32, V_NS = 4;
 constexpr int V_MAXTAPS = 16;
 
 struct ConvRing {
-    const void* act;     // gathered activation, NHWC (x, or dy for grad input)
+    const void* act;     // gathered activation, padded NHWC (x, or dy for grad input)
     const void* wt;      // permuted weight [N][T][Cs] (forward / grad input)
     const void* dyc;     // grad weight: dy, NCHW
     const void* bias;    // forward
     void* out;           // y / dx NCHW (forward, grad input); dW (grad weight, no split)
     float* part;         // grad weight partials [split][M][N]
-    // gather geometry: the activation is [n][Hs][Ws][Cs]
+    // gather geometry: the activation is [n][Hs][Ws][Cs], Hs and Ws including the
+    // zero border; every row pixel and tap lands inside it
     int Hs, Ws, Cs;
     // rows: pixels of an [n][Hp][Wp] grid (forward / grad input)
     int Hp, Wp;
@@ -58,7 +63,9 @@ struct ConvRing {
     int ntap;            // taps in this launch (a sub-pixel phase may use a subset)
     int wt_taps;         // taps per row of the permuted weight
     int tap_h[V_MAXTAPS], tap_w[V_MAXTAPS], tap_k[V_MAXTAPS];   // row offsets and weight tap of each k tap
-    int pix_sh, pix_sw, pix_bh, pix_bw;   // row pixel (i, j) -> source origin (i*sh + bh, j*sw + bw)
+    int tap_off[V_MAXTAPS], wt_off[V_MAXTAPS];   // forward / grad input: byte offsets of each k tap in act and wt
+    int pix_sh, pix_sw, pix_bh, pix_bw;   // row pixel (i, j) -> source origin (i*sh + bh, j*sw + bw), border included
+    Div32 wdiv;          // grad weight: division by the output width
     // output placement (forward / grad input): pixel (i, j) -> (i*osh + orh, j*osw + orw) of [n][N][Ho][Wo]
     int Ho, Wo, osh, osw, orh, orw;
     // grad weight: output pixels per image, width; k per split; taps for the dW order
@@ -154,83 +161,76 @@ __global__ __launch_bounds__(64 * ring_waves(BM, BN)) void conv_ring_kernel(Conv
     const i32x4 rb = v_rsrc(MODE == 1 ? p.dyc : p.wt, MODE == 1 ? p.dyc_bytes : p.wt_bytes);
 
     // ---- per-lane, per-load constants ----
-    // A (MODE 0): KM tile, 16 rows per block; row -> pixel (img, i, j) -> source origin
-    // A (MODE 1): MN tile, 2 k-rows per block; column chunk -> (tap, channel)
-    int a_base[DA], a_h[DA], a_w[DA], a_c[DA];
-    bool a_ok[DA];
+    // Rows past M (pixels, or (tap, channel) rows) and columns past N read a
+    // valid row instead; their results are never stored.
+    // A (MODE 0): KM tile, 16 rows per block; a_off = byte offset of the row
+    //   pixel's origin and the lane's 8 channels, a stage adds its tap and channel
+    // A (MODE 1): MN tile, 2 k-rows per block; a_off = element offset of the
+    //   lane's (tap, channel) chunk, a stage adds its output pixel's position
+    int a_off[DA], a_kr[DA];
 #pragma unroll
     for (int q = 0; q < DA; ++q) {
         const int blk = wave * DA + q;
         if constexpr (MODE == 0) {
             const int row = blk * 16 + lane / 4;
-            const int pix = m0 + row;
-            a_ok[q] = pix < p.M;
+            const int pix = min(m0 + row, p.M - 1);
             const int hw = p.Hp * p.Wp;
             const int img = pix / hw, r = pix - img * hw;
             const int i = r / p.Wp, j = r - i * p.Wp;
-            a_base[q] = img * p.Hs * p.Ws;
-            a_h[q] = i * p.pix_sh + p.pix_bh;
-            a_w[q] = j * p.pix_sw + p.pix_bw;
-            a_c[q] = ((lane % 4) ^ swz_km(row)) * 8;
+            const int ih = i * p.pix_sh + p.pix_bh, iw = j * p.pix_sw + p.pix_bw;
+            a_off[q] = (((img * p.Hs + ih) * p.Ws + iw) * p.Cs + ((lane % 4) ^ swz_km(row)) * 8) * 2;
+            a_kr[q] = 0;
         } else {
             const int kr = blk * 2 + lane / 32;
-            const int m = m0 + (((lane % 32) ^ swz_mn(kr)) * 8);
-            a_ok[q] = m < p.M;
+            const int m = min(m0 + (((lane % 32) ^ swz_mn(kr)) * 8), p.M - 8);
             const int t = m / p.Cs, c = m - t * p.Cs;
-            a_base[q] = kr;                       // k-row of the stage
-            a_h[q] = p.tap_h[min(t, V_MAXTAPS - 1)];
-            a_w[q] = p.tap_w[min(t, V_MAXTAPS - 1)];
-            a_c[q] = c;
+            a_off[q] = (p.tap_h[t] * p.Ws + p.tap_w[t]) * p.Cs + c;
+            a_kr[q] = kr;
         }
     }
-    // B: KM tile, 16 rows (output channels) per block
-    int b_row[DB], b_c[DB];
-    bool b_ok[DB];
+    // B: KM tile, 16 rows (output channels) per block; byte offset of the lane's row and chunk
+    int b_off[DB];
 #pragma unroll
     for (int q = 0; q < DB; ++q) {
         const int blk = wave * DB + q;
         const int row = blk * 16 + lane / 4;
-        b_row[q] = n0 + row;
-        b_ok[q] = n0 + row < p.N;
-        b_c[q] = ((lane % 4) ^ swz_km(row)) * 8;
+        const int n = min(n0 + row, p.N - 1);
+        const int bc = ((lane % 4) ^ swz_km(row)) * 8;
+        if constexpr (MODE == 0) b_off[q] = (n * p.wt_taps * p.Cs + bc) * 2;
+        else b_off[q] = (n * p.HWo + bc) * 2;
     }
 
+    // MODE 0: stages run tap-major, channel-minor in issue order
+    int it = 0, ic0 = 0;
     auto issue = [&](int s) {
         if (s >= nk) return;
         const uint32_t slot = lds0 + (uint32_t)((s % V_NS) * STB);
-        const int k0 = kb + s * V_BK;
         if constexpr (MODE == 0) {
-            const int t = k0 / p.Cs, c0 = k0 - t * p.Cs;
-            const int th = p.tap_h[t], tw = p.tap_w[t], tk = p.tap_k[t];
+            const int aoff = p.tap_off[it] + ic0 * 2, woff = p.wt_off[it] + ic0 * 2;
 #pragma unroll
-            for (int q = 0; q < DA; ++q) {
-                const int ih = a_h[q] + th, iw = a_w[q] + tw;
-                const bool ok = a_ok[q] && (unsigned)ih < (unsigned)p.Hs && (unsigned)iw < (unsigned)p.Ws;
-                const uint32_t off = ok ? (uint32_t)(((a_base[q] + ih * p.Ws + iw) * p.Cs + c0 + a_c[q]) * 2) : kOOB;
-                v_dma16(ra, slot + (uint32_t)((wave * DA + q) * 1024), off);
-            }
+            for (int q = 0; q < DA; ++q) v_dma16(ra, slot + (uint32_t)((wave * DA + q) * 1024), (uint32_t)(a_off[q] + aoff));
 #pragma unroll
-            for (int q = 0; q < DB; ++q) {
-                const uint32_t off = b_ok[q] ? (uint32_t)(((b_row[q] * p.wt_taps + tk) * p.Cs + c0 + b_c[q]) * 2) : kOOB;
-                v_dma16(rb, slot + OPA + (uint32_t)((wave * DB + q) * 1024), off);
+            for (int q = 0; q < DB; ++q) v_dma16(rb, slot + OPA + (uint32_t)((wave * DB + q) * 1024), (uint32_t)(b_off[q] + woff));
+            ic0 += V_BK;
+            if (ic0 == p.Cs) {
+                ic0 = 0;
+                ++it;
             }
         } else {
             // the stage's 32 output pixels lie in one image (HWo % 32 == 0)
+            const int k0 = kb + s * V_BK;
             const int img = k0 / p.HWo, o0 = k0 - img * p.HWo;
+            const int ibase = img * p.Hs;
 #pragma unroll
             for (int q = 0; q < DA; ++q) {
-                const int o = o0 + a_base[q];
-                const int oh = o / p.Wd, ow = o - oh * p.Wd;
-                const int ih = oh * p.pix_sh + a_h[q], iw = ow * p.pix_sw + a_w[q];
-                const bool ok = a_ok[q] && (unsigned)ih < (unsigned)p.Hs && (unsigned)iw < (unsigned)p.Ws;
-                const uint32_t off = ok ? (uint32_t)((((img * p.Hs + ih) * p.Ws + iw) * p.Cs + a_c[q]) * 2) : kOOB;
-                v_dma16(ra, slot + (uint32_t)((wave * DA + q) * 1024), off);
+                const int o = o0 + a_kr[q];
+                const int oh = (int)div32((uint32_t)o, p.wdiv), ow = o - oh * p.Wd;
+                const int off = ((ibase + oh * p.pix_sh) * p.Ws + ow * p.pix_sw) * p.Cs + a_off[q];
+                v_dma16(ra, slot + (uint32_t)((wave * DA + q) * 1024), (uint32_t)off * 2);
             }
+            const int dyoff = ((img * p.N) * p.HWo + o0) * 2;
 #pragma unroll
-            for (int q = 0; q < DB; ++q) {
-                const uint32_t off = b_ok[q] ? (uint32_t)((((int64_t)img * p.N + b_row[q]) * p.HWo + o0 + b_c[q]) * 2) : kOOB;
-                v_dma16(rb, slot + OPA + (uint32_t)((wave * DB + q) * 1024), off);
-            }
+            for (int q = 0; q < DB; ++q) v_dma16(rb, slot + OPA + (uint32_t)((wave * DB + q) * 1024), (uint32_t)(b_off[q] + dyoff));
         }
     };
 
@@ -365,15 +365,45 @@ __global__ __launch_bounds__(64 * ring_waves(BM, BN)) void conv_ring_kernel(Conv
     }
 }
 
-// NCHW -> NHWC for 16-bit elements, one block of 64 channels x 64 pixels per
-// workgroup: 16-byte loads along the pixels of a channel, 16-byte stores along
-// the channels of a pixel (when the counts allow; element accesses otherwise)
-__global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint16_t* src, uint16_t* dst, int C, int HW) {
+// NCHW -> zero-bordered NHWC [n][Hs][Ws][C] for 16-bit elements, the image at
+// rows pt.. and columns pl.. of each padded plane. Workgroups x < nblk: one
+// block of 64 channels x 64 source pixels, 16-byte loads along the pixels of
+// a channel and 16-byte stores along the channels of a pixel (when the counts
+// allow; element accesses otherwise). Workgroup x == nblk zeroes the border
+// pixels of the image (the rows above and below, then the columns left and
+// right of each image row).
+__global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint16_t* src, uint16_t* dst, int C, int H, int W, int Hs,
+                                                           int Ws, int pt, int pl, int nblk) {
     __shared__ uint16_t tile[64][72];
-    const int img = blockIdx.z, c0 = blockIdx.y * 64, p0 = blockIdx.x * 64;
-    const uint16_t* s = src + (int64_t)img * C * HW;
-    uint16_t* d = dst + (int64_t)img * C * HW;
+    const int img = blockIdx.z, c0 = blockIdx.y * 64;
+    const int HW = H * W;
+    uint16_t* d = dst + (int64_t)img * Hs * Ws * C;
     const bool vec = HW % 8 == 0 && C % 8 == 0;
+    if ((int)blockIdx.x >= nblk) {
+        const int rows = Hs - H, cols = Ws - W;   // border rows (whole width), border columns per image row
+        const int npix = rows * Ws + H * cols;
+        for (int e = threadIdx.x; e < npix * 8; e += 256) {
+            const int px = e / 8, c = c0 + (e % 8) * 8;
+            if (c >= C) continue;
+            int hp, wp;
+            if (px < rows * Ws) {
+                const int r = px / Ws;
+                hp = r < pt ? r : r + H;
+                wp = px - r * Ws;
+            } else {
+                const int q = px - rows * Ws, r = q / cols, k = q - r * cols;
+                hp = pt + r;
+                wp = k < pl ? k : k + W;
+            }
+            uint16_t* o = d + ((int64_t)hp * Ws + wp) * C + c;
+            if (vec && c + 8 <= C) *reinterpret_cast<u32x4*>(o) = u32x4{0, 0, 0, 0};
+            else
+                for (int k = 0; k < 8 && c + k < C; ++k) o[k] = 0;
+        }
+        return;
+    }
+    const int p0 = blockIdx.x * 64;
+    const uint16_t* s = src + (int64_t)img * C * HW;
 #pragma unroll
     for (int e = threadIdx.x; e < 64 * 8; e += 256) {
         const int c = e / 8, q = (e % 8) * 8;
@@ -389,15 +419,18 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint16_t* src, 
 #pragma unroll
     for (int e = threadIdx.x; e < 64 * 8; e += 256) {
         const int q = e / 8, c = (e % 8) * 8;
-        if (p0 + q >= HW) continue;
+        const int px = p0 + q;
+        if (px >= HW) continue;
+        const int h = px / W, w = px - h * W;
+        uint16_t* o = d + ((int64_t)(h + pt) * Ws + w + pl) * C + c0 + c;
         if (vec && c0 + c + 8 <= C) {
-            uint32_t w[4];
+            uint32_t wv[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) w[k] = (uint32_t)tile[c + 2 * k][q] | ((uint32_t)tile[c + 2 * k + 1][q] << 16);
-            *reinterpret_cast<u32x4*>(d + (int64_t)(p0 + q) * C + c0 + c) = u32x4{w[0], w[1], w[2], w[3]};
+            for (int k = 0; k < 4; ++k) wv[k] = (uint32_t)tile[c + 2 * k][q] | ((uint32_t)tile[c + 2 * k + 1][q] << 16);
+            *reinterpret_cast<u32x4*>(o) = u32x4{wv[0], wv[1], wv[2], wv[3]};
         } else {
             for (int k = 0; k < 8; ++k)
-                if (c0 + c + k < C) d[(int64_t)(p0 + q) * C + c0 + c + k] = tile[c + k][q];
+                if (c0 + c + k < C) o[k] = tile[c + k][q];
         }
     }
 }
@@ -466,9 +499,26 @@ void launch_ring(const ConvRingSet& set, int nph, int splits, hipStream_t s) {
 #undef TVK_RING
 }
 
-void launch_nhwc(const void* src, void* dst, int n, int C, int HW, hipStream_t s) {
-    const dim3 grid((HW + 63) / 64, (C + 63) / 64, n);
-    hipLaunchKernelGGL(nchw_to_nhwc_kernel, grid, dim3(256), 0, s, static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), C, HW);
+// A zero border around each image: pt/pb rows above/below, pl/pr columns left/right.
+struct Border {
+    int pt = 0, pb = 0, pl = 0, pr = 0;
+};
+
+void launch_nhwc(const void* src, void* dst, int n, int C, int H, int W, const Border& bd, hipStream_t s) {
+    const int Hs = H + bd.pt + bd.pb, Ws = W + bd.pl + bd.pr;
+    const int nblk = (H * W + 63) / 64;
+    const bool border = Hs > H || Ws > W;
+    const dim3 grid((unsigned)(nblk + (border ? 1 : 0)), (C + 63) / 64, n);
+    hipLaunchKernelGGL(nchw_to_nhwc_kernel, grid, dim3(256), 0, s, static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), C,
+                       H, W, Hs, Ws, bd.pt, bd.pl, nblk);
+}
+
+// Border that keeps rows lo + i*step + [tap_lo, tap_hi] for i in [0, count)
+// (and likewise columns) inside the image after padding: the amounts by which
+// the lowest index falls below 0 and the highest exceeds size - 1.
+void border_for(int lo, int step, int count, int tap_lo, int tap_hi, int size, int& before, int& after) {
+    before = std::max(before, -(lo + tap_lo));
+    after = std::max(after, lo + (count - 1) * step + tap_hi - (size - 1));
 }
 
 }  // namespace
@@ -509,14 +559,46 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
     auto align = [](size_t v) { return (v + 255) / 256 * 256; };
     const bool f16 = d.dtype == TVK_F16;
     if (mode == 0 || mode == 1) {
-        // gathered activation: x (forward) or dy (grad input), to NHWC
-        const int Cs = mode == 0 ? cin : cout, Hs = mode == 0 ? H : Ho, Ws = mode == 0 ? W : Wo;
+        // gathered activation: x (forward) or dy (grad input), to bordered NHWC
+        const int Cs = mode == 0 ? cin : cout, H0 = mode == 0 ? H : Ho, W0 = mode == 0 ? W : Wo;
         const int Cn = mode == 0 ? cout : cin;   // GEMM columns
+        Border bd;
+        if (mode == 0) {
+            border_for(-ph, sh, Ho, 0, (kh - 1) * dh, H, bd.pt, bd.pb);
+            border_for(-pw, sw, Wo, 0, (kw - 1) * dw, W, bd.pl, bd.pr);
+        } else {
+            // each sub-pixel phase reads dy rows i + nh / sh over its taps (see below)
+            for (int r = 0; r < sh; ++r) {
+                const int Hp = (H - r + sh - 1) / sh;
+                int lo = INT32_MAX, hi = INT32_MIN;
+                for (int a = 0; a < kh; ++a) {
+                    const int nh = r + ph - a * dh;
+                    if (((nh % sh) + sh) % sh != 0) continue;
+                    lo = std::min(lo, nh / sh);
+                    hi = std::max(hi, nh / sh);
+                }
+                if (Hp > 0 && lo <= hi) border_for(0, 1, Hp, lo, hi, Ho, bd.pt, bd.pb);
+            }
+            for (int r = 0; r < sw; ++r) {
+                const int Wp = (W - r + sw - 1) / sw;
+                int lo = INT32_MAX, hi = INT32_MIN;
+                for (int b = 0; b < kw; ++b) {
+                    const int nw = r + pw - b * dw;
+                    if (((nw % sw) + sw) % sw != 0) continue;
+                    lo = std::min(lo, nw / sw);
+                    hi = std::max(hi, nw / sw);
+                }
+                if (Wp > 0 && lo <= hi) border_for(0, 1, Wp, lo, hi, Wo, bd.pl, bd.pr);
+            }
+        }
+        const int Hs = H0 + bd.pt + bd.pb, Ws = W0 + bd.pl + bd.pr;
         const size_t act_b = align((size_t)n * Cs * Hs * Ws * es), wt_b = align((size_t)Cn * T * Cs * es);
+        if ((size_t)n * Cs * Hs * Ws * es >= ((size_t)1 << 31))
+            return fail(TVK_ERR_UNSUPPORTED, std::string(who) + ": the bordered channels-last copy exceeds 2 GiB");
         char* ws = static_cast<char*>(device_workspace(dev, act_b + wt_b));
         if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the channels-last copies");
         const void* src = mode == 0 ? d.x : d.y;
-        launch_nhwc(src, ws, n, Cs, Hs * Ws, s);
+        launch_nhwc(src, ws, n, Cs, H0, W0, bd, s);
         const int64_t wn = (int64_t)cout * cin * T;
         const unsigned wblocks = (unsigned)std::min<int64_t>((wn + 255) / 256, 2048);
         if (mode == 0) hipLaunchKernelGGL((weight_permute_kernel<uint16_t, true>), dim3(wblocks), dim3(256), 0, s, static_cast<const uint16_t*>(d.weight), reinterpret_cast<uint16_t*>(ws + act_b), cout, cin, T);
@@ -527,6 +609,12 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
         p.N = Cn;
         p.act_bytes = (int)((size_t)n * Cs * Hs * Ws * es);
         p.wt_bytes = (int)((size_t)Cn * T * Cs * es);
+        auto set_offsets = [&](ConvRing& q) {
+            for (int t = 0; t < q.ntap; ++t) {
+                q.tap_off[t] = (q.tap_h[t] * Ws + q.tap_w[t]) * Cs * 2;
+                q.wt_off[t] = q.tap_k[t] * Cs * 2;
+            }
+        };
         p.wt_taps = T;
         p.out = mode == 0 ? d.y : d.x;
         p.Ho = mode == 0 ? Ho : H;
@@ -535,7 +623,8 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
             p.ntap = T;
             for (int t = 0; t < T; ++t) { p.tap_h[t] = (t / kw) * dh; p.tap_w[t] = (t % kw) * dw; p.tap_k[t] = t; }
             p.Hp = Ho; p.Wp = Wo;
-            p.pix_sh = sh; p.pix_sw = sw; p.pix_bh = -ph; p.pix_bw = -pw;
+            p.pix_sh = sh; p.pix_sw = sw; p.pix_bh = -ph + bd.pt; p.pix_bw = -pw + bd.pl;
+            set_offsets(p);
             p.osh = 1; p.osw = 1; p.orh = 0; p.orw = 0;
             p.bias = d.bias;
             p.has_bias = d.bias ? 1 : 0;
@@ -576,7 +665,8 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
                         }
                     }
                     q.Hp = Hp; q.Wp = Wp;
-                    q.pix_sh = 1; q.pix_sw = 1; q.pix_bh = 0; q.pix_bw = 0;
+                    q.pix_sh = 1; q.pix_sw = 1; q.pix_bh = bd.pt; q.pix_bw = bd.pl;
+                    set_offsets(q);
                     q.osh = sh; q.osw = sw; q.orh = ry; q.orw = rx;
                     q.M = n * Hp * Wp;
                     q.K = q.ntap * cout;
@@ -587,8 +677,14 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
             flush();
         }
     } else {
-        // grad weight: x to NHWC; dy read NCHW; K = output pixels split into partials
-        const size_t act_b = align((size_t)n * cin * H * W * es);
+        // grad weight: x to bordered NHWC; dy read NCHW; K = output pixels split into partials
+        Border bd;
+        border_for(-ph, sh, Ho, 0, (kh - 1) * dh, H, bd.pt, bd.pb);
+        border_for(-pw, sw, Wo, 0, (kw - 1) * dw, W, bd.pl, bd.pr);
+        const int Hs = H + bd.pt + bd.pb, Ws = W + bd.pl + bd.pr;
+        if ((size_t)n * cin * Hs * Ws * es >= ((size_t)1 << 31))
+            return fail(TVK_ERR_UNSUPPORTED, std::string(who) + ": the bordered channels-last copy exceeds 2 GiB");
+        const size_t act_b = align((size_t)n * cin * Hs * Ws * es);
         p.M = T * cin;
         p.N = cout;
         p.K = n * Ho * Wo;
@@ -607,19 +703,20 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
         const size_t part_b = split > 1 ? (size_t)split * p.M * p.N * 4 : 0;
         char* ws = static_cast<char*>(device_workspace(dev, act_b + part_b));
         if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the channels-last copy");
-        launch_nhwc(d.x, ws, n, cin, H * W, s);
+        launch_nhwc(d.x, ws, n, cin, H, W, bd, s);
         p.act = ws;
         p.dyc = d.y;
         p.part = split > 1 ? reinterpret_cast<float*>(ws + act_b) : nullptr;
         p.out = d.weight;
-        p.Hs = H; p.Ws = W; p.Cs = cin;
+        p.Hs = Hs; p.Ws = Ws; p.Cs = cin;
         p.ntap = T;
         p.wt_taps = T;
-        for (int t = 0; t < T; ++t) { p.tap_h[t] = (t / kw) * dh - ph; p.tap_w[t] = (t % kw) * dw - pw; p.tap_k[t] = t; }
+        for (int t = 0; t < T; ++t) { p.tap_h[t] = (t / kw) * dh - ph + bd.pt; p.tap_w[t] = (t % kw) * dw - pw + bd.pl; p.tap_k[t] = t; }
         p.pix_sh = sh; p.pix_sw = sw;
         p.HWo = Ho * Wo; p.Wd = Wo; p.kh_kw = T;
+        p.wdiv = make_div((uint32_t)Wo);
         p.k_chunk = (int)chunk; p.split = (int)split;
-        p.act_bytes = (int)((size_t)n * cin * H * W * es);
+        p.act_bytes = (int)((size_t)n * cin * Hs * Ws * es);
         p.dyc_bytes = (int)((size_t)n * cout * Ho * Wo * es);
         ConvRingSet set;
         set.ph[0] = p;
