@@ -371,15 +371,38 @@ __global__ __launch_bounds__(64 * ring_waves(BM, BN)) void conv_ring_kernel(Conv
 // a channel and 16-byte stores along the channels of a pixel (when the counts
 // allow; element accesses otherwise). Workgroup x == nblk zeroes the border
 // pixels of the image (the rows above and below, then the columns left and
-// right of each image row).
+// right of each image row). The grid is one-dimensional: workgroup
+// b < nx * cy * n copies column block b % nx of channel block (b / nx) % cy of
+// image b / (nx * cy); the workgroups after those, when the weight is given,
+// permute the weight for the same convolution in the same launch:
+// w[co][c][t] -> wout[co][t][c] (forward) or wout[c][t][co] (grad input).
+struct WeightPermute {
+    const uint16_t* w = nullptr;
+    uint16_t* out = nullptr;
+    int cout = 0, cin = 0, taps = 0, forward = 0;
+};
+
 __global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint16_t* src, uint16_t* dst, int C, int H, int W, int Hs,
-                                                           int Ws, int pt, int pl, int nblk) {
+                                                           int Ws, int pt, int pl, int nblk, int nx, int cy, int copy_blocks,
+                                                           WeightPermute wp) {
     __shared__ uint16_t tile[64][72];
-    const int img = blockIdx.z, c0 = blockIdx.y * 64;
+    const int b = blockIdx.x;
+    if (b >= copy_blocks) {
+        // weight elements number below 2^30 (checked on the host)
+        const int total = wp.cout * wp.cin * wp.taps, nb = (int)gridDim.x - copy_blocks;
+        for (int e = (b - copy_blocks) * 256 + (int)threadIdx.x; e < total; e += nb * 256) {
+            const int t = e % wp.taps, r = e / wp.taps;
+            const int c = r % wp.cin, co = r / wp.cin;
+            const int o = wp.forward ? (co * wp.taps + t) * wp.cin + c : (c * wp.taps + t) * wp.cout + co;
+            wp.out[o] = wp.w[e];
+        }
+        return;
+    }
+    const int bx = b % nx, img = b / (nx * cy), c0 = (b / nx - img * cy) * 64;
     const int HW = H * W;
     uint16_t* d = dst + (int64_t)img * Hs * Ws * C;
     const bool vec = HW % 8 == 0 && C % 8 == 0;
-    if ((int)blockIdx.x >= nblk) {
+    if (bx >= nblk) {
         const int rows = Hs - H, cols = Ws - W;   // border rows (whole width), border columns per image row
         const int npix = rows * Ws + H * cols;
         for (int e = threadIdx.x; e < npix * 8; e += 256) {
@@ -402,7 +425,7 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint16_t* src, 
         }
         return;
     }
-    const int p0 = blockIdx.x * 64;
+    const int p0 = bx * 64;
     const uint16_t* s = src + (int64_t)img * C * HW;
 #pragma unroll
     for (int e = threadIdx.x; e < 64 * 8; e += 256) {
@@ -432,19 +455,6 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint16_t* src, 
             for (int k = 0; k < 8; ++k)
                 if (c0 + c + k < C) o[k] = tile[c + k][q];
         }
-    }
-}
-
-// w[co][c][t] -> out[co][t][c] (forward) or out[c][t][co] (grad input)
-template <typename T, bool FORWARD>
-__global__ __launch_bounds__(256) void weight_permute_kernel(const T* w, T* out, int Cout, int Cin, int taps) {
-    const int64_t total = (int64_t)Cout * Cin * taps;
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-        const int t = (int)(e % taps);
-        const int c = (int)((e / taps) % Cin);
-        const int co = (int)(e / ((int64_t)taps * Cin));
-        const int64_t o = FORWARD ? ((int64_t)co * taps + t) * Cin + c : ((int64_t)c * taps + t) * Cout + co;
-        out[o] = w[e];
     }
 }
 
@@ -504,13 +514,17 @@ struct Border {
     int pt = 0, pb = 0, pl = 0, pr = 0;
 };
 
-void launch_nhwc(const void* src, void* dst, int n, int C, int H, int W, const Border& bd, hipStream_t s) {
+void launch_nhwc(const void* src, void* dst, int n, int C, int H, int W, const Border& bd, hipStream_t s,
+                 const WeightPermute& wp = WeightPermute()) {
     const int Hs = H + bd.pt + bd.pb, Ws = W + bd.pl + bd.pr;
     const int nblk = (H * W + 63) / 64;
     const bool border = Hs > H || Ws > W;
-    const dim3 grid((unsigned)(nblk + (border ? 1 : 0)), (C + 63) / 64, n);
-    hipLaunchKernelGGL(nchw_to_nhwc_kernel, grid, dim3(256), 0, s, static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), C,
-                       H, W, Hs, Ws, bd.pt, bd.pl, nblk);
+    const int nx = nblk + (border ? 1 : 0), cy = (C + 63) / 64, copy_blocks = nx * cy * n;
+    const int64_t wn = (int64_t)wp.cout * wp.cin * wp.taps;
+    const int wblocks = wp.w ? (int)std::min<int64_t>((wn + 255) / 256, 1024) : 0;
+    hipLaunchKernelGGL(nchw_to_nhwc_kernel, dim3((unsigned)(copy_blocks + wblocks)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), C, H, W, Hs, Ws, bd.pt, bd.pl, nblk, nx, cy,
+                       copy_blocks, wp);
 }
 
 // Border that keeps rows lo + i*step + [tap_lo, tap_hi] for i in [0, count)
@@ -598,11 +612,11 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
         char* ws = static_cast<char*>(device_workspace(dev, act_b + wt_b));
         if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the channels-last copies");
         const void* src = mode == 0 ? d.x : d.y;
-        launch_nhwc(src, ws, n, Cs, H0, W0, bd, s);
-        const int64_t wn = (int64_t)cout * cin * T;
-        const unsigned wblocks = (unsigned)std::min<int64_t>((wn + 255) / 256, 2048);
-        if (mode == 0) hipLaunchKernelGGL((weight_permute_kernel<uint16_t, true>), dim3(wblocks), dim3(256), 0, s, static_cast<const uint16_t*>(d.weight), reinterpret_cast<uint16_t*>(ws + act_b), cout, cin, T);
-        else hipLaunchKernelGGL((weight_permute_kernel<uint16_t, false>), dim3(wblocks), dim3(256), 0, s, static_cast<const uint16_t*>(d.weight), reinterpret_cast<uint16_t*>(ws + act_b), cout, cin, T);
+        WeightPermute wp;
+        wp.w = static_cast<const uint16_t*>(d.weight);
+        wp.out = reinterpret_cast<uint16_t*>(ws + act_b);
+        wp.cout = cout; wp.cin = cin; wp.taps = T; wp.forward = mode == 0;
+        launch_nhwc(src, ws, n, Cs, H0, W0, bd, s, wp);
         p.act = ws;
         p.wt = ws + act_b;
         p.Hs = Hs; p.Ws = Ws; p.Cs = Cs;
