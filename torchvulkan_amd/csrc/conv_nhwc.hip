@@ -341,146 +341,184 @@ __global__ __launch_bounds__(64 * ring_waves(BM, BN)) void conv_ring_kernel(Conv
     const int hw = p.Hp * p.Wp;
     const bool dense = p.osh == 1 && p.osw == 1 && p.Hp == p.Ho && p.Wp == p.Wo && hw % 8 == 0;
     constexpr int NT = 64 * NW;
-    for (int idx = tid; idx < BN * (V_BM / 8); idx += NT) {
-        const int ch = idx / (V_BM / 8), pc = idx % (V_BM / 8);
-        const int co = n0 + ch;
-        const int pix = m0 + pc * 8;
-        if (co >= p.N || pix >= p.M) continue;
-        const uint16_t* src = tile + ch * LROW + pc * 8;
-        if (dense && pix + 8 <= p.M) {
+    if (dense) {
+        for (int idx = tid; idx < BN * (V_BM / 8); idx += NT) {
+            const int ch = idx / (V_BM / 8), pc = idx % (V_BM / 8);
+            const int co = n0 + ch;
+            const int pix = m0 + pc * 8;
+            if (co >= p.N || pix >= p.M) continue;
             // 8 pixels of one image row run (hw % 8 == 0): one 16-byte store
             const int img = pix / hw, o = pix - img * hw;
-            *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + co) * hw + o) = *reinterpret_cast<const u32x4*>(src);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int q = pix + e;
-                if (q >= p.M) break;
-                const int img = q / hw, r = q - img * hw;
-                const int i = r / p.Wp, j = r - i * p.Wp;
-                const int oh = i * p.osh + p.orh, ow = j * p.osw + p.orw;
-                out[(((int64_t)img * p.N + co) * p.Ho + oh) * p.Wo + ow] = __builtin_bit_cast(T, src[e]);
-            }
+            *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + co) * hw + o) = *reinterpret_cast<const u32x4*>(tile + ch * LROW + pc * 8);
+        }
+    } else {
+        // sub-pixel phases (or pixel runs that 16-byte stores do not fit): a
+        // thread keeps one pixel (NT is a multiple of the tile's rows) and walks
+        // the channels, so a store's 64 lanes write 64 consecutive row pixels
+        static_assert(NT % V_BM == 0, "one pixel per thread");
+        const int pc = tid % V_BM, pix = m0 + pc;
+        if (pix < p.M) {
+            const int img = pix / hw, r = pix - img * hw;
+            const int i = r / p.Wp, j = r - i * p.Wp;
+            const int plane = p.Ho * p.Wo;
+            T* o = out + ((int64_t)img * p.N + n0) * plane + (i * p.osh + p.orh) * p.Wo + j * p.osw + p.orw;
+            for (int ch = tid / V_BM; ch < BN && n0 + ch < p.N; ch += NT / V_BM)
+                o[(int64_t)ch * plane] = __builtin_bit_cast(T, tile[ch * LROW + pc]);
         }
     }
 }
 
 // NCHW -> zero-bordered NHWC [n][Hs][Ws][C] for 16-bit elements, the image at
-// rows pt.. and columns pl.. of each padded plane. Workgroups x < nblk: one
-// block of 64 channels x 64 source pixels, 16-byte loads along the pixels of
-// a channel and 16-byte stores along the channels of a pixel (when the counts
-// allow; element accesses otherwise). Workgroup x == nblk zeroes the border
-// pixels of the image (the rows above and below, then the columns left and
-// right of each image row). The grid is one-dimensional: workgroup
-// b < nx * cy * n copies column block b % nx of channel block (b / nx) % cy of
-// image b / (nx * cy); the workgroups after those, when the weight is given,
-// permute the weight for the same convolution in the same launch:
-// w[co][c][t] -> wout[co][t][c] (forward) or wout[c][t][co] (grad input).
+// rows pt.. and columns pl.. of each padded plane. The grid is one-dimensional:
+// workgroup b < nx * cy * n takes column block b % nx of channel block
+// (b / nx) % cy of image b / (nx * cy); the workgroups after those, when the
+// weight is given, permute the weight for the same convolution in the same
+// launch: w[co][c][t] -> wout[co][t][c] (forward) or wout[c][t][co] (grad
+// input). Column block nx - 1, when the plane has a border, zeroes the border
+// pixels of its channels (the rows above and below, then the columns left and
+// right of each image row); the others copy 64 channels x PX pixels.
+// VEC (HW % 8 == 0, C % 8 == 0): PX = 256, no LDS. A lane loads 8 pixels of 8
+// channels (eight 16-byte loads; 8 lanes read 128 contiguous bytes of a channel
+// row), transposes the 8x8 block of 16-bit elements in registers and stores 8
+// pixels of 8 channels (8 lanes write 128 contiguous bytes of a pixel).
+// Otherwise PX = 64 through an LDS tile, element accesses where the counts
+// leave no 16-byte run.
 struct WeightPermute {
     const uint16_t* w = nullptr;
     uint16_t* out = nullptr;
     int cout = 0, cin = 0, taps = 0, forward = 0;
 };
 
-__global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint16_t* src, uint16_t* dst, int C, int H, int W, int Hs,
-                                                           int Ws, int pt, int pl, int nblk, int nx, int cy, int copy_blocks,
-                                                           WeightPermute wp) {
-    __shared__ uint16_t tile[64][72];
-    const int b = blockIdx.x;
-    if (b >= copy_blocks) {
-        // weight elements number below 2^30 (checked on the host)
-        const int total = wp.cout * wp.cin * wp.taps, nb = (int)gridDim.x - copy_blocks;
-        for (int e = (b - copy_blocks) * 256 + (int)threadIdx.x; e < total; e += nb * 256) {
-            const int t = e % wp.taps, r = e / wp.taps;
-            const int c = r % wp.cin, co = r / wp.cin;
-            const int o = wp.forward ? (co * wp.taps + t) * wp.cin + c : (c * wp.taps + t) * wp.cout + co;
-            wp.out[o] = wp.w[e];
-        }
-        return;
+struct NhwcArgs {
+    const uint16_t* src;
+    uint16_t* dst;
+    int C, H, W, Hs, Ws, pt, pl;
+    int nblk, nx, cy, copy_blocks;   // copy column blocks per plane (nblk, plus 1 with a border)
+    WeightPermute wp;
+};
+
+__device__ inline void permute_weight(const WeightPermute& wp, int blk, int nb) {
+    // weight elements number below 2^30 (checked on the host)
+    const int total = wp.cout * wp.cin * wp.taps;
+    for (int e = blk * 256 + (int)threadIdx.x; e < total; e += nb * 256) {
+        const int t = e % wp.taps, r = e / wp.taps;
+        const int c = r % wp.cin, co = r / wp.cin;
+        const int o = wp.forward ? (co * wp.taps + t) * wp.cin + c : (c * wp.taps + t) * wp.cout + co;
+        wp.out[o] = wp.w[e];
     }
-    const int bx = b % nx, img = b / (nx * cy), c0 = (b / nx - img * cy) * 64;
-    const int HW = H * W;
-    uint16_t* d = dst + (int64_t)img * Hs * Ws * C;
-    const bool vec = HW % 8 == 0 && C % 8 == 0;
-    if (bx >= nblk) {
-        const int rows = Hs - H, cols = Ws - W;   // border rows (whole width), border columns per image row
-        const int npix = rows * Ws + H * cols;
-        for (int e = threadIdx.x; e < npix * 8; e += 256) {
-            const int px = e / 8, c = c0 + (e % 8) * 8;
-            if (c >= C) continue;
-            int hp, wp;
-            if (px < rows * Ws) {
-                const int r = px / Ws;
-                hp = r < pt ? r : r + H;
-                wp = px - r * Ws;
-            } else {
-                const int q = px - rows * Ws, r = q / cols, k = q - r * cols;
-                hp = pt + r;
-                wp = k < pl ? k : k + W;
-            }
-            uint16_t* o = d + ((int64_t)hp * Ws + wp) * C + c;
-            if (vec && c + 8 <= C) *reinterpret_cast<u32x4*>(o) = u32x4{0, 0, 0, 0};
-            else
-                for (int k = 0; k < 8 && c + k < C; ++k) o[k] = 0;
-        }
-        return;
-    }
-    const int p0 = bx * 64;
-    const uint16_t* s = src + (int64_t)img * C * HW;
-#pragma unroll
-    for (int e = threadIdx.x; e < 64 * 8; e += 256) {
-        const int c = e / 8, q = (e % 8) * 8;
-        if (c0 + c >= C) continue;
-        if (vec && p0 + q + 8 <= HW) {
-            *reinterpret_cast<u32x4*>(&tile[c][q]) = *reinterpret_cast<const u32x4*>(s + (int64_t)(c0 + c) * HW + p0 + q);
+}
+
+__device__ inline void zero_border(const NhwcArgs& a, uint16_t* d, int c0, bool vec) {
+    const int rows = a.Hs - a.H, cols = a.Ws - a.W;   // border rows (whole width), border columns per image row
+    const int npix = rows * a.Ws + a.H * cols;
+    for (int e = threadIdx.x; e < npix * 8; e += 256) {
+        const int px = e / 8, c = c0 + (e % 8) * 8;
+        if (c >= a.C) continue;
+        int hp, wq;
+        if (px < rows * a.Ws) {
+            const int r = px / a.Ws;
+            hp = r < a.pt ? r : r + a.H;
+            wq = px - r * a.Ws;
         } else {
+            const int q = px - rows * a.Ws, r = q / cols, k = q - r * cols;
+            hp = a.pt + r;
+            wq = k < a.pl ? k : k + a.W;
+        }
+        uint16_t* o = d + ((int64_t)hp * a.Ws + wq) * a.C + c;
+        if (vec && c + 8 <= a.C) *reinterpret_cast<u32x4*>(o) = u32x4{0, 0, 0, 0};
+        else
+            for (int k = 0; k < 8 && c + k < a.C; ++k) o[k] = 0;
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(NhwcArgs a) {
+    const int b = blockIdx.x;
+    if (b >= a.copy_blocks) {
+        permute_weight(a.wp, b - a.copy_blocks, (int)gridDim.x - a.copy_blocks);
+        return;
+    }
+    const int bx = b % a.nx, img = b / (a.nx * a.cy), c0 = (b / a.nx - img * a.cy) * 64;
+    const int C = a.C, W = a.W, HW = a.H * a.W;
+    uint16_t* d = a.dst + (int64_t)img * a.Hs * a.Ws * C;
+    if (bx >= a.nblk) {
+        zero_border(a, d, c0, VEC);
+        return;
+    }
+    const uint16_t* s = a.src + (int64_t)img * C * HW;
+    if constexpr (VEC) {
+        const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+        const int c = c0 + (lane % 8) * 8;
+        const int px = bx * 256 + wave * 64 + (lane / 8) * 8;
+        if (c >= C || px >= HW) return;
+        u32x4 r[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = *reinterpret_cast<const u32x4*>(s + (int64_t)(c + i) * HW + px);
+        int h = px / W, w = px - h * W;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // pixel px + j: channel pairs (2k, 2k + 1) packed low/high
+            uint32_t v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t lo = r[2 * k][j / 2], hi = r[2 * k + 1][j / 2];
+                v[k] = (j % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+            }
+            *reinterpret_cast<u32x4*>(d + ((int64_t)(h + a.pt) * a.Ws + w + a.pl) * C + c) = u32x4{v[0], v[1], v[2], v[3]};
+            if (++w == W) {
+                w = 0;
+                ++h;
+            }
+        }
+    } else {
+        __shared__ uint16_t tile[64][72];
+        const int p0 = bx * 64;
+#pragma unroll
+        for (int e = threadIdx.x; e < 64 * 8; e += 256) {
+            const int c = e / 8, q = (e % 8) * 8;
+            if (c0 + c >= C) continue;
             for (int k = 0; k < 8; ++k)
                 if (p0 + q + k < HW) tile[c][q + k] = s[(int64_t)(c0 + c) * HW + p0 + q + k];
         }
-    }
-    __syncthreads();
+        __syncthreads();
 #pragma unroll
-    for (int e = threadIdx.x; e < 64 * 8; e += 256) {
-        const int q = e / 8, c = (e % 8) * 8;
-        const int px = p0 + q;
-        if (px >= HW) continue;
-        const int h = px / W, w = px - h * W;
-        uint16_t* o = d + ((int64_t)(h + pt) * Ws + w + pl) * C + c0 + c;
-        if (vec && c0 + c + 8 <= C) {
-            uint32_t wv[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) wv[k] = (uint32_t)tile[c + 2 * k][q] | ((uint32_t)tile[c + 2 * k + 1][q] << 16);
-            *reinterpret_cast<u32x4*>(o) = u32x4{wv[0], wv[1], wv[2], wv[3]};
-        } else {
+        for (int e = threadIdx.x; e < 64 * 8; e += 256) {
+            const int q = e / 8, c = (e % 8) * 8;
+            const int px = p0 + q;
+            if (px >= HW) continue;
+            const int h = px / W, w = px - h * W;
+            uint16_t* o = d + ((int64_t)(h + a.pt) * a.Ws + w + a.pl) * C + c0 + c;
             for (int k = 0; k < 8; ++k)
                 if (c0 + c + k < C) o[k] = tile[c + k][q];
         }
     }
 }
 
-// grad weight: sums partials [split][(t,c)][co] into dW[co][c][t]. WAVE: one
-// wave per output (lane l sums splits l, l+64, ... in order, then a fixed
-// butterfly), for few outputs with many splits; else one thread per output
-// summing in split order.
-template <int DT, bool WAVE>
-__global__ __launch_bounds__(256) void wgrad_ring_reduce_kernel(const float* part, void* out, int M, int N, int Cs, int taps, int split) {
+// grad weight: sums partials [split][(t,c)][co] into dW[co][c][t]. A
+// workgroup takes E = 1024 / SG consecutive outputs: SG groups of threads each
+// sum every SG-th split with 16-byte loads (group g: splits g, g + SG, ... in
+// order; 4 outputs a thread), then the SG group sums are added in group order
+// through LDS. (M * N % 4 == 0; SG a power of two up to 16.)
+template <int DT>
+__global__ __launch_bounds__(256) void wgrad_ring_reduce_kernel(const float* part, void* out, int M, int N, int Cs, int taps,
+                                                                int split, int sg) {
     typedef typename elem<DT>::T T;
-    const int64_t total = (int64_t)M * N;
-    const int per = WAVE ? 4 : 256;
-    const int lane = threadIdx.x % 64;
-    for (int64_t e = (int64_t)blockIdx.x * per + (WAVE ? threadIdx.x / 64 : threadIdx.x); e < total; e += (int64_t)gridDim.x * per) {
-        float v;
-        if constexpr (WAVE) {
-            v = 0.0f;
-            for (int s = lane; s < split; s += 64) v += part[(int64_t)s * total + e];
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-            if (lane != 0) continue;
-        } else {
-            v = part[e];
-            for (int s = 1; s < split; ++s) v += part[(int64_t)s * total + e];
-        }
-        const int row = (int)(e / N), co = (int)(e % N);
+    __shared__ float red[1024];
+    const int total = M * N;   // below 2^30 (checked on the host)
+    const int L = 256 / sg, E = 1024 / sg;
+    const int g = threadIdx.x / L, l = threadIdx.x % L;
+    const int e0 = blockIdx.x * E + l * 4;
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (e0 < total)
+        for (int s = g; s < split; s += sg) acc += *reinterpret_cast<const f32x4*>(part + (int64_t)s * total + e0);
+    *reinterpret_cast<f32x4*>(red + g * E + l * 4) = acc;
+    __syncthreads();
+    for (int k = threadIdx.x; k < E; k += 256) {
+        const int e = blockIdx.x * E + k;
+        if (e >= total) break;
+        float v = red[k];
+        for (int q = 1; q < sg; ++q) v += red[q * E + k];
+        const int row = e / N, co = e - row * N;
         const int t = row / Cs, c = row - t * Cs;
         reinterpret_cast<T*>(out)[((int64_t)co * Cs + c) * taps + t] = elem<DT>::from_f32(v);
     }
@@ -516,15 +554,27 @@ struct Border {
 
 void launch_nhwc(const void* src, void* dst, int n, int C, int H, int W, const Border& bd, hipStream_t s,
                  const WeightPermute& wp = WeightPermute()) {
-    const int Hs = H + bd.pt + bd.pb, Ws = W + bd.pl + bd.pr;
-    const int nblk = (H * W + 63) / 64;
-    const bool border = Hs > H || Ws > W;
-    const int nx = nblk + (border ? 1 : 0), cy = (C + 63) / 64, copy_blocks = nx * cy * n;
+    NhwcArgs a;
+    a.src = static_cast<const uint16_t*>(src);
+    a.dst = static_cast<uint16_t*>(dst);
+    a.C = C; a.H = H; a.W = W;
+    a.Hs = H + bd.pt + bd.pb; a.Ws = W + bd.pl + bd.pr;
+    a.pt = bd.pt; a.pl = bd.pl;
+    // 16-byte accesses: every channel row and pixel starts 16-byte aligned (the
+    // source is, and the workspace is 256-byte aligned)
+    const bool vec = (H * W) % 8 == 0 && C % 8 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+    const int px = vec ? 256 : 64;
+    a.nblk = (H * W + px - 1) / px;
+    const bool border = a.Hs > H || a.Ws > W;
+    a.nx = a.nblk + (border ? 1 : 0);
+    a.cy = (C + 63) / 64;
+    a.copy_blocks = a.nx * a.cy * n;
+    a.wp = wp;
     const int64_t wn = (int64_t)wp.cout * wp.cin * wp.taps;
     const int wblocks = wp.w ? (int)std::min<int64_t>((wn + 255) / 256, 1024) : 0;
-    hipLaunchKernelGGL(nchw_to_nhwc_kernel, dim3((unsigned)(copy_blocks + wblocks)), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), C, H, W, Hs, Ws, bd.pt, bd.pl, nblk, nx, cy,
-                       copy_blocks, wp);
+    const dim3 grid((unsigned)(a.copy_blocks + wblocks));
+    if (vec) hipLaunchKernelGGL(nchw_to_nhwc_kernel<true>, grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, grid, dim3(256), 0, s, a);
 }
 
 // Border that keeps rows lo + i*step + [tap_lo, tap_hi] for i in [0, count)
@@ -737,16 +787,13 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
         if (f16) launch_ring<TVK_F16, 1>(set, 1, (int)split, s);
         else launch_ring<TVK_BF16, 1>(set, 1, (int)split, s);
         if (split > 1) {
-            const int64_t total = (int64_t)p.M * p.N;
-            if (total < 256 * 1024 && split >= 8) {
-                const unsigned blocks = (unsigned)std::min<int64_t>((total + 3) / 4, 16384);
-                if (f16) hipLaunchKernelGGL((wgrad_ring_reduce_kernel<TVK_F16, true>), dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
-                else hipLaunchKernelGGL((wgrad_ring_reduce_kernel<TVK_BF16, true>), dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
-            } else {
-                const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
-                if (f16) hipLaunchKernelGGL((wgrad_ring_reduce_kernel<TVK_F16, false>), dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
-                else hipLaunchKernelGGL((wgrad_ring_reduce_kernel<TVK_BF16, false>), dim3(blocks), dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split);
-            }
+            // group count: enough workgroups to fill the device, at most the splits
+            const int total = p.M * p.N;
+            int sg = 1;
+            while (sg < 16 && sg * 2 <= split && (int64_t)total * sg / 1024 < 1024) sg *= 2;
+            const dim3 grid((unsigned)((total + 1024 / sg - 1) / (1024 / sg)));
+            if (f16) hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_F16>, grid, dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split, sg);
+            else hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_BF16>, grid, dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split, sg);
         }
     }
     hipError_t e = hipGetLastError();
