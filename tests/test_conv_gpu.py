@@ -146,6 +146,30 @@ def test_ring_geometry(gpu, dtype, case):
                           case.pop("s"), case.pop("p"), case.pop("hw"), seed=40, **case)
 
 
+# few-input-channel kernels (c_in * kh * kw <= 32, c_in < 32): stem shapes with
+# widths that leave idle threads in the grad-input tile (24, 200), stride 2,
+# a 5x5 kernel on one channel, an odd output-channel count (the grad-input
+# pairs), paddings 0 and 2 (halo offsets), dilation, and output tiles past M
+SMALL_CASES = [
+    dict(n=3, cin=3, cout=64, k=3, s=1, p=1, hw=24),
+    dict(n=2, cin=3, cout=96, k=3, s=2, p=1, hw=16),
+    dict(n=2, cin=1, cout=16, k=5, s=1, p=2, hw=16),
+    dict(n=2, cin=4, cout=7, k=3, s=1, p=1, hw=8),
+    dict(n=2, cin=2, cout=40, k=3, s=1, p=0, hw=18),
+    dict(n=2, cin=3, cout=64, k=3, s=1, p=2, hw=14),
+    dict(n=1, cin=3, cout=32, k=3, s=1, p=1, hw=13, dil=2),
+    dict(n=1, cin=3, cout=16, k=3, s=1, p=1, hw=200),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", SMALL_CASES)
+def test_few_input_channels(gpu, dtype, case):
+    case = dict(case)
+    _check_all_directions(gpu, dtype, case.pop("n"), case.pop("cin"), case.pop("cout"), case.pop("k"),
+                          case.pop("s"), case.pop("p"), case.pop("hw"), seed=50, **case)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_exact_mode_bit_identical(gpu, dtype):
     _check_all_directions(gpu, dtype, 4, 16, 32, 3, 2, 1, 12, seed=30, exact=True)

@@ -545,6 +545,8 @@ tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
         if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
         return TVK_OK;
     }
+    // few input channels: one-k-step kernels that gather straight from NCHW (conv_stem.hip)
+    if (conv_small_applies(d, MODE)) return conv_small_run(d, MODE, who);
     // channels-last implicit GEMM on the LDS ring (conv_nhwc.hip) where it applies
     if (conv_ring_applies(d, MODE)) return conv_ring_run(d, MODE, who);
     const bool seq = (d.flags & TVK_GEMM_EXACT) != 0;

@@ -1,0 +1,468 @@
+// 2-D convolution on gfx950 for few input channels (a network's stem: 3
+// colour channels, 3x3 taps), float16/bfloat16, groups == 1. The channel-rich
+// kernels stage 32-channel k stages of a channels-last copy; with 3 channels a
+// whole reduction is one 32-k MFMA step (c, kh, kw <= 32 values), so these
+// kernels gather straight from NCHW and skip the copy:
+//   forward     y[p][co] = sum_k patch(x, p)[k] * W[co][k]: one 16x16x32 MFMA
+//               per 16x16 output block, k = (c, kh, kw) zero-filled past K;
+//               y written NCHW through an LDS tile (16-byte stores)
+//   grad weight dW[co][k] = sum_p dy[co][p] * patch(x, p)[k]: the pixels are
+//               the reduction, 32 a step; dy rows are the A operand read as
+//               16-byte loads, the x patches the B operand; float32 partials
+//               per workgroup, summed in workgroup order by a second kernel
+//   grad input  (stride 1, 3x3, dilation 1, at most 4 input channels)
+//               dx[c][i] = sum_{co,t} dy[co][i + off(t)] * W[co][c][t] with
+//               v_dot2 over output-channel pairs: a workgroup stages a halo of
+//               dy rows (channel pairs interleaved) in LDS and each thread sums
+//               one input pixel for every input channel
+//
+// Reference semantics (file:line under the reference tree): the sums of
+// src/shaders/helpers/conv.slang:198-511 and src/api/ops/conv.cpp:1014-1060
+// (the same as conv.hip's kernels) with another k order inside each output's
+// reduction, which the float16/bfloat16 tolerance allows; bias is added in
+// float32 before the one rounding (src/shaders/conv_simd.slang:8-19).
+#include "tvk_common.h"
+#include "gemm_common.h"
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+
+namespace tvk {
+namespace {
+
+struct SmallArgs {
+    const void* x;
+    const void* w;
+    const void* bias;
+    const void* dy;
+    void* out;        // y (forward), dx (grad input), dW or nothing (grad weight with partials)
+    float* part;      // grad weight: [split][cout * K]
+    int n, cin, H, W, cout, kh, kw, sh, sw, ph, pw, dh, dw, Ho, Wo;
+    int K;            // cin * kh * kw (<= 32)
+    int M;            // forward: output pixels n * Ho * Wo
+    int split;        // grad weight: workgroups along the pixels (partials when > 1)
+    int has_bias;
+    int vec_out;      // forward: Ho * Wo % 8 == 0 and y 16-byte aligned
+    // grad input tile: TR input rows a workgroup, halo HR x HC, ncp output-channel pairs
+    int tr, hr, hc, ncp, row_blocks;
+};
+
+constexpr int S_CP = 16;   // grad input: output-channel pairs per LDS chunk
+
+template <int DT>
+__device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (DT == TVK_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ inline u32x4 pack8(const uint16_t (&v)[8]) {
+    return u32x4{v[0] | ((uint32_t)v[1] << 16), v[2] | ((uint32_t)v[3] << 16), v[4] | ((uint32_t)v[5] << 16),
+                 v[6] | ((uint32_t)v[7] << 16)};
+}
+
+// k -> (channel plane offset, row tap offset, column tap offset); plane -1 past K
+__device__ inline void fill_ktab(const SmallArgs& p, int (*ktab)[32]) {
+    const int k = threadIdx.x;
+    if (k >= 32) return;
+    const int T = p.kh * p.kw;
+    if (k < p.K) {
+        const int c = k / T, t = k - c * T, a = t / p.kw, b = t - a * p.kw;
+        ktab[0][k] = c * p.H * p.W;
+        ktab[1][k] = a * p.dh;
+        ktab[2][k] = b * p.dw;
+    } else {
+        ktab[0][k] = -1;
+        ktab[1][k] = 0;
+        ktab[2][k] = 0;
+    }
+}
+
+// One 256-pixel x 64-channel output tile: 4 waves of 64 pixels, 4x4 MFMAs each.
+template <int DT>
+__global__ __launch_bounds__(256) void conv_small_fwd_kernel(SmallArgs p) {
+    typedef typename elem<DT>::T T;
+    constexpr int LROW = 256 + 8;
+    __shared__ int ktab[3][32];
+    __shared__ __attribute__((aligned(16))) uint16_t tile[64 * LROW];
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16;
+    const int m0 = blockIdx.x * 256, n0 = blockIdx.y * 64;
+    const int HW = p.H * p.W, HWo = p.Ho * p.Wo;
+    fill_ktab(p, ktab);
+    __syncthreads();
+    int kc[8], ka[8], kb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        kc[e] = ktab[0][g * 8 + e];
+        ka[e] = ktab[1][g * 8 + e];
+        kb[e] = ktab[2][g * 8 + e];
+    }
+    const uint16_t* x = static_cast<const uint16_t*>(p.x);
+    const uint16_t* w = static_cast<const uint16_t*>(p.w);
+    // B: W[co][k] is the NCHW weight itself ([co][c][kh][kw] = [co][K])
+    u32x4 fb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int co = n0 + j * 16 + lane % 16;
+        uint16_t v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int k = g * 8 + e;
+            v[e] = (co < p.cout && k < p.K) ? w[co * p.K + k] : (uint16_t)0;
+        }
+        fb[j] = pack8(v);
+    }
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // rows past M gather a valid pixel; they are never stored
+        const int m = min(m0 + wave * 64 + i * 16 + lane % 16, p.M - 1);
+        const int img = m / HWo, o = m - img * HWo;
+        const int oh = o / p.Wo, ow = o - oh * p.Wo;
+        const int ih0 = oh * p.sh - p.ph, iw0 = ow * p.sw - p.pw;
+        const uint16_t* xb = x + img * p.cin * HW;
+        uint16_t v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int ih = ih0 + ka[e], iw = iw0 + kb[e];
+            v[e] = (kc[e] >= 0 && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W) ? xb[kc[e] + ih * p.W + iw]
+                                                                                                  : (uint16_t)0;
+        }
+        const u32x4 fa = pack8(v);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<DT>(fa, fb[j], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+    }
+    // [channel][pixel] tile, then 16-byte stores along each channel plane
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ch = j * 16 + lane % 16;
+        float bv = 0.0f;
+        if (p.has_bias && n0 + ch < p.cout) bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[n0 + ch]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint16_t h[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[i][j][r];
+                if (p.has_bias) {
+#pragma clang fp contract(off)
+                    v = v + bv;
+                }
+                h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
+            }
+            const int px = wave * 64 + i * 16 + g * 4;
+            *reinterpret_cast<u32x2*>(tile + ch * LROW + px) = u32x2{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
+        }
+    }
+    __syncthreads();
+    uint16_t* y = static_cast<uint16_t*>(p.out);
+    for (int idx = tid; idx < 64 * 32; idx += 256) {
+        const int ch = idx / 32, pc = idx % 32;
+        const int co = n0 + ch, pix = m0 + pc * 8;
+        if (co >= p.cout || pix >= p.M) continue;
+        const uint16_t* src = tile + ch * LROW + pc * 8;
+        if (p.vec_out) {
+            // 8 pixels of one image (Ho * Wo % 8 == 0): one 16-byte store
+            const int img = pix / HWo, o = pix - img * HWo;
+            *reinterpret_cast<u32x4*>(y + ((int64_t)img * p.cout + co) * HWo + o) = *reinterpret_cast<const u32x4*>(src);
+        } else {
+            for (int e = 0; e < 8 && pix + e < p.M; ++e) {
+                const int img = (pix + e) / HWo, o = pix + e - img * HWo;
+                y[((int64_t)img * p.cout + co) * HWo + o] = src[e];
+            }
+        }
+    }
+}
+
+// Grad weight: workgroup b sums pixel chunks b, b + split, ... of 512 pixels
+// (4 waves x 4 steps of 32, each wave its own 128 pixels), for 64 output
+// channels (grid y) x the 32 (zero-padded) k. Ho * Wo % 8 == 0 so a lane's 8
+// pixels lie in one image and start 16-byte aligned.
+template <int DT>
+__global__ __launch_bounds__(256) void conv_small_wgrad_kernel(SmallArgs p) {
+    typedef typename elem<DT>::T T;
+    __shared__ int ktab[3][32];
+    __shared__ float red[4][64 * 33];
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16;
+    const int n0 = blockIdx.y * 64;
+    const int HW = p.H * p.W, HWo = p.Ho * p.Wo, P = p.n * HWo;
+    fill_ktab(p, ktab);
+    __syncthreads();
+    // B columns: k = j * 16 + lane % 16
+    int kc[2], ka[2], kb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        kc[j] = ktab[0][j * 16 + lane % 16];
+        ka[j] = ktab[1][j * 16 + lane % 16];
+        kb[j] = ktab[2][j * 16 + lane % 16];
+    }
+    const uint16_t* x = static_cast<const uint16_t*>(p.x);
+    const uint16_t* dy = static_cast<const uint16_t*>(p.dy);
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int base = blockIdx.x * 512; base < P; base += p.split * 512) {
+        u32x4 fa[4][4], fb[4][2];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int p0 = base + wave * 128 + s * 32 + g * 8;
+            const bool live = p0 < P;   // P % 8 == 0: a lane's 8 pixels are all in or all out
+            const int img = live ? p0 / HWo : 0, o = live ? p0 - img * HWo : 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int co = min(n0 + i * 16 + lane % 16, p.cout - 1);
+                fa[s][i] = live ? *reinterpret_cast<const u32x4*>(dy + ((int64_t)img * p.cout + co) * HWo + o)
+                                : u32x4{0u, 0u, 0u, 0u};
+            }
+            int oh = o / p.Wo, ow = o - oh * p.Wo;
+            uint16_t v[2][8];
+            const uint16_t* xb = x + img * p.cin * HW;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int ih0 = oh * p.sh - p.ph, iw0 = ow * p.sw - p.pw;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int ih = ih0 + ka[j], iw = iw0 + kb[j];
+                    v[j][e] = (live && kc[j] >= 0 && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W)
+                                  ? xb[kc[j] + ih * p.W + iw]
+                                  : (uint16_t)0;
+                }
+                if (++ow == p.Wo) {
+                    ow = 0;
+                    ++oh;
+                }
+            }
+            fb[s][0] = pack8(v[0]);
+            fb[s][1] = pack8(v[1]);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = mfma16<DT>(fa[s][i], fb[s][j], acc[i][j]);
+    }
+    // the 4 waves' sums, added in wave order
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][(i * 16 + g * 4 + r) * 33 + j * 16 + lane % 16] = acc[i][j][r];
+    __syncthreads();
+    for (int q = tid; q < 64 * 32; q += 256) {
+        const int cl = q / 32, k = q % 32, co = n0 + cl;
+        if (co >= p.cout || k >= p.K) continue;
+        const int at = cl * 33 + k;
+        const float v = ((red[0][at] + red[1][at]) + red[2][at]) + red[3][at];
+        if (p.split > 1) p.part[(int64_t)blockIdx.x * p.cout * p.K + co * p.K + k] = v;
+        else reinterpret_cast<T*>(p.out)[co * p.K + k] = elem<DT>::from_f32(v);
+    }
+}
+
+// out[e] = sum over s of part[s][e], in s order within each of SG groups
+// (group q: s = q, q + SG, ...), the group sums added in group order.
+template <int DT>
+__global__ __launch_bounds__(256) void small_split_reduce_kernel(const float* part, void* out, int count, int split, int sg) {
+    typedef typename elem<DT>::T T;
+    __shared__ float red[256];
+    const int L = 256 / sg, q = threadIdx.x / L, l = threadIdx.x % L;
+    const int e = blockIdx.x * L + l;
+    float v = 0.0f;
+    if (e < count)
+        for (int s = q; s < split; s += sg) v += part[(int64_t)s * count + e];
+    red[threadIdx.x] = v;
+    __syncthreads();
+    if (threadIdx.x < L && e < count) {
+        float t = red[l];
+        for (int k = 1; k < sg; ++k) t += red[k * L + l];
+        reinterpret_cast<T*>(out)[e] = elem<DT>::from_f32(t);
+    }
+}
+
+// Grad input, stride 1, 3x3 taps, dilation 1: workgroup = TR input rows (all
+// W columns) of one image; threads = pixels. Output-channel pairs are staged
+// S_CP at a time as a halo of dy, [pair][HR][HC] dwords (channel 2q in the low
+// half), zero outside dy; the weights as [pair][tap][4 input channels] dwords.
+template <int DT>
+__global__ __launch_bounds__(256) void conv_small_dgrad_kernel(SmallArgs p) {
+    typedef typename elem<DT>::T T;
+    __shared__ __attribute__((aligned(16))) uint32_t dyh[S_CP * 768];
+    __shared__ __attribute__((aligned(16))) uint32_t wq[128 * 9 * 4];
+    const int tid = threadIdx.x;
+    const int img = blockIdx.x / p.row_blocks, h0 = (blockIdx.x - img * p.row_blocks) * p.tr;
+    const int HR = p.hr, HC = p.hc, HRC = HR * HC;
+    const int r_lo = h0 + p.ph - 2, c_lo = p.pw - 2;   // dy row / column of halo (0, 0)
+    const uint16_t* w = static_cast<const uint16_t*>(p.w);
+    const uint16_t* dy = static_cast<const uint16_t*>(p.dy);
+    const int HWo = p.Ho * p.Wo;
+    // weight pairs: wq[(q * 9 + t) * 4 + c] = W[2q][c][t] | W[2q+1][c][t] << 16
+    for (int e = tid; e < p.ncp * 36; e += 256) {
+        const int c = e % 4, t = (e / 4) % 9, q = e / 36;
+        uint32_t lo = 0, hi = 0;
+        if (c < p.cin) {
+            lo = w[((2 * q) * p.cin + c) * 9 + t];
+            if (2 * q + 1 < p.cout) hi = w[((2 * q + 1) * p.cin + c) * 9 + t];
+        }
+        wq[e] = lo | (hi << 16);
+    }
+    const int tr = tid / p.W, iw = tid - tr * p.W;
+    const bool live = tr < p.tr && h0 + tr < p.H;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int nq = p.Wo / 8;   // 16-byte chunks per dy row
+    for (int q0 = 0; q0 < p.ncp; q0 += S_CP) {
+        // zero the halo, then copy the dy rows that exist
+        for (int e = tid; e < S_CP * HRC / 4; e += 256) reinterpret_cast<u32x4*>(dyh)[e] = u32x4{0u, 0u, 0u, 0u};
+        __syncthreads();
+        for (int e = tid; e < S_CP * HR * nq; e += 256) {
+            const int cq = e % nq, rest = e / nq, hr = rest % HR, cp = rest / HR;
+            const int co = 2 * (q0 + cp), oh = r_lo + hr;
+            if (co >= p.cout || (unsigned)oh >= (unsigned)p.Ho) continue;
+            const int64_t off = ((int64_t)img * p.cout + co) * HWo + oh * p.Wo + cq * 8;
+            const u32x4 lo = *reinterpret_cast<const u32x4*>(dy + off);
+            const u32x4 hi = co + 1 < p.cout ? *reinterpret_cast<const u32x4*>(dy + off + HWo) : u32x4{0u, 0u, 0u, 0u};
+            uint32_t* row = dyh + cp * HRC + hr * HC;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int hc = cq * 8 + k - c_lo;
+                const uint32_t l = lo[k / 2], h = hi[k / 2];
+                const uint32_t v = (k % 2 == 0) ? ((l & 0xffffu) | (h << 16)) : ((l >> 16) | (h & 0xffff0000u));
+                if ((unsigned)hc < (unsigned)HC) row[hc] = v;
+            }
+        }
+        __syncthreads();
+        if (live) {
+            const int ncp = min(S_CP, p.ncp - q0);
+            for (int cp = 0; cp < ncp; ++cp) {
+                const uint32_t* hb = dyh + cp * HRC + tr * HC + iw;
+                const u32x4* wb = reinterpret_cast<const u32x4*>(wq) + (q0 + cp) * 9;
+#pragma unroll
+                for (int a = 0; a < 3; ++a)
+#pragma unroll
+                    for (int b = 0; b < 3; ++b) {
+                        // input (h0 + tr, iw) meets dy (h0 + tr + ph - a, iw + pw - b): halo (tr + 2 - a, iw + 2 - b)
+                        const uint32_t v = hb[(2 - a) * HC + 2 - b];
+                        const u32x4 wv = wb[a * 3 + b];
+                        // scalar copies: hipcc reads element 0 for a bit cast
+                        // of an indexed vector element in this unrolled loop
+                        const uint32_t wc[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            if constexpr (DT == TVK_F16)
+                                acc[c] = __builtin_amdgcn_fdot2(__builtin_bit_cast(_Float16 __attribute__((ext_vector_type(2))), v),
+                                                                __builtin_bit_cast(_Float16 __attribute__((ext_vector_type(2))), wc[c]),
+                                                                acc[c], false);
+                            else
+                                acc[c] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(__bf16 __attribute__((ext_vector_type(2))), v),
+                                                                         __builtin_bit_cast(__bf16 __attribute__((ext_vector_type(2))), wc[c]),
+                                                                         acc[c], false);
+                        }
+                    }
+            }
+        }
+        __syncthreads();
+    }
+    if (!live) return;
+    T* dx = static_cast<T*>(p.out);
+    const int HWi = p.H * p.W;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        if (c < p.cin) dx[((int64_t)img * p.cin + c) * HWi + (h0 + tr) * p.W + iw] = elem<DT>::from_f32(acc[c]);
+}
+
+bool al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+SmallArgs small_args(const tvk_conv_desc& d) {
+    SmallArgs p;
+    memset(&p, 0, sizeof(p));
+    p.x = d.x; p.w = d.weight; p.bias = d.bias; p.dy = d.y;
+    p.n = (int)d.n; p.cin = (int)d.c_in; p.H = (int)d.h; p.W = (int)d.w; p.cout = (int)d.c_out;
+    p.kh = (int)d.kh; p.kw = (int)d.kw; p.sh = (int)d.stride[0]; p.sw = (int)d.stride[1];
+    p.ph = (int)d.padding[0]; p.pw = (int)d.padding[1]; p.dh = (int)d.dilation[0]; p.dw = (int)d.dilation[1];
+    p.Ho = (int)d.h_out; p.Wo = (int)d.w_out;
+    p.K = p.cin * p.kh * p.kw;
+    return p;
+}
+
+// grad input tile: rows per workgroup and the halo it stages
+void dgrad_tile(const tvk_conv_desc& d, int& tr, int& hr, int& hc) {
+    tr = std::max<int>(1, 256 / (int)d.w);
+    hr = tr + 2;
+    hc = (int)d.w + 2;
+}
+
+}  // namespace
+
+bool conv_small_applies(const tvk_conv_desc& d, int mode) {
+    if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return false;
+    if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return false;
+    // channel-rich convolutions keep the channels-last ring
+    if (d.c_in * d.kh * d.kw > 32 || d.c_in >= 32) return false;
+    // 32-bit element offsets
+    const int64_t big = std::max({d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h_out * d.w_out});
+    if (big >= (int64_t(1) << 30)) return false;
+    if (mode == 0) return true;
+    if (mode == 2) return (d.h_out * d.w_out) % 8 == 0 && al16(d.y);
+    // grad input: the stride-1 3x3 halo kernel
+    if (d.kh != 3 || d.kw != 3 || d.stride[0] != 1 || d.stride[1] != 1 || d.dilation[0] != 1 || d.dilation[1] != 1) return false;
+    if (d.c_in > 4 || d.c_out > 256 || d.w > 256 || d.w_out % 8 != 0 || !al16(d.y)) return false;
+    int tr, hr, hc;
+    dgrad_tile(d, tr, hr, hc);
+    return hr * hc <= 768;
+}
+
+tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who) {
+    SmallArgs p = small_args(d);
+    hipStream_t s = resolve_stream(d.stream);
+    const bool f16 = d.dtype == TVK_F16;
+    if (mode == 0) {
+        p.out = d.y;
+        p.M = p.n * p.Ho * p.Wo;
+        p.has_bias = d.bias ? 1 : 0;
+        p.vec_out = (p.Ho * p.Wo) % 8 == 0 && al16(d.y);
+        const dim3 grid((unsigned)((p.M + 255) / 256), (unsigned)((p.cout + 63) / 64));
+        if (f16) hipLaunchKernelGGL(conv_small_fwd_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL(conv_small_fwd_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
+    } else if (mode == 2) {
+        const int64_t P = (int64_t)p.n * p.Ho * p.Wo;
+        const int ny = (p.cout + 63) / 64;
+        // 512-pixel chunks; at most 1024 workgroups along the pixels
+        p.split = (int)std::max<int64_t>(1, std::min<int64_t>((P + 511) / 512, 1024));
+        p.out = d.weight;
+        const int count = p.cout * p.K;
+        if (p.split > 1) {
+            int dev = 0;
+            (void)hipGetDevice(&dev);
+            p.part = static_cast<float*>(device_workspace(dev, (size_t)p.split * count * sizeof(float)));
+            if (!p.part) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
+        }
+        const dim3 grid((unsigned)p.split, (unsigned)ny);
+        if (f16) hipLaunchKernelGGL(conv_small_wgrad_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL(conv_small_wgrad_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
+        if (p.split > 1) {
+            int sg = 1;
+            while (sg < 16 && sg * 2 <= p.split && (int64_t)count * sg / 256 < 512) sg *= 2;
+            const int L = 256 / sg;
+            const dim3 rgrid((unsigned)((count + L - 1) / L));
+            if (f16) hipLaunchKernelGGL(small_split_reduce_kernel<TVK_F16>, rgrid, dim3(256), 0, s, p.part, d.weight, count, p.split, sg);
+            else hipLaunchKernelGGL(small_split_reduce_kernel<TVK_BF16>, rgrid, dim3(256), 0, s, p.part, d.weight, count, p.split, sg);
+        }
+    } else {
+        p.out = d.x;
+        dgrad_tile(d, p.tr, p.hr, p.hc);
+        p.ncp = (p.cout + 1) / 2;
+        p.row_blocks = (p.H + p.tr - 1) / p.tr;
+        const dim3 grid((unsigned)(p.n * p.row_blocks));
+        if (f16) hipLaunchKernelGGL(conv_small_dgrad_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL(conv_small_dgrad_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
+    return TVK_OK;
+}
+
+}  // namespace tvk

@@ -198,6 +198,9 @@ hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, int 
 // 1 grad input, 2 grad weight.
 bool conv_ring_applies(const tvk_conv_desc& d, int mode);
 tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who);
+// Few input channels (conv_stem.hip): cin * kh * kw <= 32; same modes.
+bool conv_small_applies(const tvk_conv_desc& d, int mode);
+tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who);
 
 // M <= 16 streaming kernel (gemm_skinny.hip). b_kmajor: B's k stride is 1.
 // vec: 16-byte loads are legal for A and B. Returns hipSuccess or the launch error.
