@@ -227,6 +227,11 @@ def test_transpose_aligned_vector_path(gpu, dtype):
     check_like_torch(x, cl, "transpose")
     back = torch.empty_like(x)
     check_like_torch(cl, back, "transpose")
+    # several 64 x 256 tiles with edge blocks on both sides (16-bit: the register-transposing kernel), batched
+    for shape in ((520, 776), (3, 264, 136), (1000, 8)):
+        src = (torch.randn(shape, generator=g) * 50).to(dtype).to(DEV)
+        dst = torch.empty(shape[:-2] + (shape[-1], shape[-2]), dtype=dtype, device=DEV)
+        check_like_torch(src.transpose(-1, -2), dst, "transpose")
 
 
 @pytest.mark.parametrize("sdt,ddt", [(orc.F32, orc.F16), (orc.F16, orc.F32), (orc.BF16, orc.F32), (orc.F32, orc.BF16)])

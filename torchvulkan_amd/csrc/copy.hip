@@ -260,6 +260,56 @@ __global__ __launch_bounds__(256) void copy_transpose_vec_kernel(TransposeArgs p
     }
 }
 
+// Same-dtype 16-bit transpose without LDS (the 16-byte conditions of the
+// kernel above). A wave moves 64 (along 0) x 64 (along j) elements: each lane
+// loads an 8x8 block as eight 16-byte rows along j, transposes it in
+// registers and stores eight 16-byte rows along 0; a quarter-wave covers 2 x 8
+// blocks, so its loads and stores each touch whole 128-byte runs. Wave tiles
+// are numbered j first (tilesj counts them along j), then 0, then the batch;
+// a workgroup takes 4 consecutive ones (`total` of them). Blocks that cross
+// the end of either dimension copy element by element.
+__global__ __launch_bounds__(256) void copy_transpose_reg16_kernel(TransposeArgs p, int64_t total) {
+    int64_t bid = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+    if (bid >= total) return;
+    const int64_t tj = bid % p.tilesj;
+    bid /= p.tilesj;
+    const int64_t t0 = bid % p.tiles0;
+    int64_t rest = bid / p.tiles0;
+    int64_t so = 0, dof = 0;
+    for (int k = 0; k < p.nb; ++k) {
+        const int64_t c = rest % p.bsize[k];
+        rest /= p.bsize[k];
+        so += c * p.bss[k];
+        dof += c * p.bds[k];
+    }
+    const int lane = threadIdx.x % 64;
+    const int l = lane % 16, q = lane / 16;
+    const int64_t a = t0 * 64 + (q * 2 + l % 2) * 8;   // 8 rows along 0
+    const int64_t b = tj * 64 + (l / 2) * 8;           // 8 columns along j
+    if (a >= p.n0 || b >= p.nj) return;
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(p.src) + so;
+    uint16_t* dst = reinterpret_cast<uint16_t*>(p.dst) + dof;
+    if (a + 8 <= p.n0 && b + 8 <= p.nj) {
+        u32x4 r[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = *reinterpret_cast<const u32x4*>(src + (a + i) * p.ss0 + b);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // column b + j: rows (2k, 2k + 1) packed low/high
+            uint32_t v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t lo = r[2 * k][j / 2], hi = r[2 * k + 1][j / 2];
+                v[k] = (j % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+            }
+            *reinterpret_cast<u32x4*>(dst + a + (b + j) * p.dsj) = u32x4{v[0], v[1], v[2], v[3]};
+        }
+    } else {
+        for (int i = 0; i < 8 && a + i < p.n0; ++i)
+            for (int j = 0; j < 8 && b + j < p.nj; ++j) dst[a + i + (b + j) * p.dsj] = src[(a + i) * p.ss0 + b + j];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // host plan
 // ---------------------------------------------------------------------------
@@ -483,6 +533,14 @@ void launch_transpose(const Plan& pl, int sdt, int ddt, const void* src, void* d
                              if ((a.bss[k] * a.sb) % 16 != 0 || (a.bds[k] * a.db) % 16 != 0) return false;
                          return true;
                      }();
+    // 16-bit: the register kernel where dimension 0 spans more than one tile
+    // (W.t() of a large matrix: 297 -> 224 us on 16384^2); the LDS kernel kept
+    // its edge on a 64-wide dimension 0 (NCHW -> NHWC of 64 channels: 31 vs 32 us)
+    if (vec && same && a.sb == 2 && a.n0 > TT) {
+        // the tile counts are the 64 x 64 ones of the LDS kernels
+        hipLaunchKernelGGL(copy_transpose_reg16_kernel, dim3((unsigned)((blocks + 3) / 4)), b, 0, st, a, blocks);
+        return;
+    }
     if (vec) {
 #define TVK_TRV(S, D, W) hipLaunchKernelGGL((copy_transpose_vec_kernel<S, D, W>), g, b, 0, st, a)
         if (same) {
