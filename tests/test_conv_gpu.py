@@ -44,7 +44,8 @@ C4 = [
 
 def _check_all_directions(abi, dtype, n, cin, cout, k, s, p, hw, groups=1, dil=1, seed=0, exact=False, sample_n=None):
     kh, kw = (k, k) if isinstance(k, int) else k
-    x = _x((n, cin, hw, hw), dtype, seed)
+    hh, ww = (hw, hw) if isinstance(hw, int) else hw
+    x = _x((n, cin, hh, ww), dtype, seed)
     w = _w((cout, cin // groups, kh, kw), dtype, seed + 1)
     bias = _x((cout,), dtype, seed + 2)
     dx_, dw_, dy_ = x.to(DEV), w.to(DEV), None
@@ -168,6 +169,26 @@ def test_few_input_channels(gpu, dtype, case):
     case = dict(case)
     _check_all_directions(gpu, dtype, case.pop("n"), case.pop("cin"), case.pop("cout"), case.pop("k"),
                           case.pop("s"), case.pop("p"), case.pop("hw"), seed=50, **case)
+
+
+# stride-1 3x3 padding-1 halo kernel (forward and grad input): every tile
+# width (64, 32, 16, 8 pixels; 4, 8, 16, 32 rows a tile), heights that end in
+# a partial tile, one and three 32-channel chunks, output channel counts that
+# leave a partial 64-channel tile, bias
+HALO_CASES = [
+    dict(n=2, cin=32, cout=64, k=3, s=1, p=1, hw=(20, 16)),
+    dict(n=1, cin=96, cout=96, k=3, s=1, p=1, hw=(10, 64)),
+    dict(n=2, cin=64, cout=40, k=3, s=1, p=1, hw=(13, 8)),
+    dict(n=3, cin=32, cout=32, k=3, s=1, p=1, hw=(9, 32)),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", HALO_CASES)
+def test_halo_stride1_3x3(gpu, dtype, case):
+    case = dict(case)
+    _check_all_directions(gpu, dtype, case.pop("n"), case.pop("cin"), case.pop("cout"), case.pop("k"),
+                          case.pop("s"), case.pop("p"), case.pop("hw"), seed=60, **case)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

@@ -547,6 +547,8 @@ tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
     }
     // few input channels: one-k-step kernels that gather straight from NCHW (conv_stem.hip)
     if (conv_small_applies(d, MODE)) return conv_small_run(d, MODE, who);
+    // stride-1 3x3 forward / grad input through an LDS halo of the NCHW source (conv_nhwc.hip)
+    if (conv_halo_applies(d, MODE)) return conv_halo_run(d, MODE, who);
     // channels-last implicit GEMM on the LDS ring (conv_nhwc.hip) where it applies
     if (conv_ring_applies(d, MODE)) return conv_ring_run(d, MODE, who);
     const bool seq = (d.flags & TVK_GEMM_EXACT) != 0;

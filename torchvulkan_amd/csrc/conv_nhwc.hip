@@ -585,6 +585,189 @@ void border_for(int lo, int step, int count, int tap_lo, int tap_hi, int size, i
     after = std::max(after, lo + (count - 1) * step + tap_hi - (size - 1));
 }
 
+// ---------------------------------------------------------------------------
+// Stride-1 3x3 "same" convolution (padding 1) straight from NCHW: forward
+// (source x) and grad input (source dy, taps mirrored). A workgroup computes
+// TR x W output pixels (TR * W = 256, W in 8..64) x 64 output channels. Per
+// 32-channel k chunk it stages the (TR + 2) x (W + 2) source halo in LDS
+// ([pixel][32 channels], 64-byte rows, the 16-byte chunks XOR-swizzled by
+// (pixel >> 2) & 3) and the permuted weight's [9 taps][64 channels][32] rows,
+// then all 9 taps read their A fragments from the halo at a shifted pixel:
+// each source element crosses from L2 once per chunk instead of once per tap.
+// The halo is gathered into registers (a lane: 8 channels x 8 pixels of one
+// row, 16-byte loads, an in-register 8x8 transpose, 16-byte LDS stores); the
+// weight rows go straight to LDS. Two stages: chunk k + 1 loads while k
+// computes.
+// ---------------------------------------------------------------------------
+constexpr int HL_BN = 64;
+constexpr int HL_MAXHP = 396;   // halo pixels (TR + 2) * (W + 2), largest at W = 64
+constexpr int HL_A = 25600;     // HL_MAXHP * 64 bytes, rounded up to 1 KB
+constexpr int HL_B = 9 * HL_BN * 64;
+constexpr int HL_STAGE = HL_A + HL_B;
+
+struct HaloArgs {
+    const uint16_t* src;   // x (forward) or dy (grad input), NCHW [n][Cs][H][W]
+    const void* wt;        // permuted weight [N][9][Cs]
+    const void* bias;      // forward
+    void* out;             // y or dx, NCHW [n][N][H][W]
+    int Cs, N, H, W, tr, row_tiles;
+    int dtap[9];           // halo pixel offset of each tap: hoff * (W + 2) + woff
+    int has_bias;
+    int wt_bytes;
+};
+
+__device__ inline int hl_swz(int row) { return (row >> 2) & 3; }
+
+template <int DT>
+__global__ __launch_bounds__(256) void conv_halo_kernel(HaloArgs p) {
+    __shared__ __attribute__((aligned(1024))) char lds[2 * HL_STAGE];
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
+    const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64), g = lane / 16;
+    const int img = blockIdx.x / p.row_tiles, h0 = (blockIdx.x - img * p.row_tiles) * p.tr;
+    const int n0 = blockIdx.y * HL_BN;
+    const int W = p.W, WP = W + 2, HWs = p.H * W;
+    const int nk = p.Cs / 32;
+
+    // zero halo columns 0 and W + 1 of both stages (no load writes them)
+    for (int e = tid; e < (p.tr + 2) * 8; e += 256) {
+        const int hr = e / 8, hc = (e / 4) % 2 ? W + 1 : 0, ch = e % 4;
+        const int hp = hr * WP + hc;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+            *reinterpret_cast<u32x4*>(lds + st * HL_STAGE + hp * 64 + ch * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+
+    // halo gather: lane -> (column group wq, channel group cg, halo row hr)
+    const int nwq = W / 8;
+    const int wq = tid % nwq, cg = (tid / nwq) % 4, hr = tid / (nwq * 4);
+    const bool a_live = hr < p.tr + 2;
+    const int ih = h0 - 1 + hr;
+    const bool a_row = a_live && ih >= 0 && ih < p.H;
+    const uint16_t* a_src = p.src + ((int64_t)img * p.Cs + cg * 8) * HWs + (int64_t)(a_row ? ih : 0) * W + wq * 8;
+    u32x4 ar[8];
+    auto load_a = [&](int kc) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            ar[i] = a_row ? *reinterpret_cast<const u32x4*>(a_src + (int64_t)(kc * 32 + i) * HWs) : u32x4{0u, 0u, 0u, 0u};
+    };
+    auto store_a = [&](int st) {
+        if (!a_live) return;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t lo = ar[2 * k][j / 2], hi = ar[2 * k + 1][j / 2];
+                v[k] = (j % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+            }
+            const int hp = hr * WP + wq * 8 + j + 1;
+            *reinterpret_cast<u32x4*>(lds + st * HL_STAGE + hp * 64 + ((cg ^ hl_swz(hp)) * 16)) = u32x4{v[0], v[1], v[2], v[3]};
+        }
+    };
+
+    // weight rows: 36 DMA instructions of 16 rows a chunk, 9 per wave; row = tap * 64 + channel
+    const i32x4 rb = v_rsrc(p.wt, p.wt_bytes);
+    int b_off[9];
+#pragma unroll
+    for (int q = 0; q < 9; ++q) {
+        const int row = (wave * 9 + q) * 16 + lane / 4;
+        const int t = row / HL_BN, co = min(n0 + row % HL_BN, p.N - 1);
+        b_off[q] = ((co * 9 + t) * p.Cs + (((lane % 4) ^ hl_swz(row)) * 8)) * 2;
+    }
+    auto issue_b = [&](int kc, int st) {
+        const uint32_t base = lds0 + (uint32_t)(st * HL_STAGE + HL_A);
+#pragma unroll
+        for (int q = 0; q < 9; ++q) v_dma16(rb, base + (uint32_t)((wave * 9 + q) * 1024), (uint32_t)(b_off[q] + kc * 64));
+    };
+
+    // A fragment rows: this wave's 64 pixels of the tile, 16 per fragment
+    int hp0[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = wave * 64 + i * 16 + lane % 16;
+        const int r = q / W, c = q - r * W;
+        hp0[i] = (r + 1) * WP + c + 1;
+    }
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    issue_b(0, 0);
+    load_a(0);
+    store_a(0);
+    v_wait<0>();
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+        const int cur = kc & 1;
+        if (kc + 1 < nk) {
+            issue_b(kc + 1, cur ^ 1);
+            load_a(kc + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const char* sa = lds + cur * HL_STAGE;
+        const char* sb = sa + HL_A;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) {
+            u32x4 fa[4], fb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int hp = hp0[i] + p.dtap[t];
+                fa[i] = *reinterpret_cast<const u32x4*>(sa + hp * 64 + ((g ^ hl_swz(hp)) * 16));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = t * HL_BN + j * 16 + lane % 16;
+                fb[j] = *reinterpret_cast<const u32x4*>(sb + row * 64 + ((g ^ hl_swz(row)) * 16));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (kc + 1 < nk) store_a(cur ^ 1);
+        v_wait<0>();
+        __syncthreads();
+    }
+
+    // [channel][pixel] tile, then 16-byte stores along the output rows
+    typedef typename elem<DT>::T T;
+    constexpr int LROW = 256 + 8;
+    uint16_t* tile = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ch = j * 16 + lane % 16;
+        float bv = 0.0f;
+        if (p.has_bias && n0 + ch < p.N) bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[n0 + ch]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint16_t h[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[i][j][r];
+                if (p.has_bias) {
+#pragma clang fp contract(off)
+                    v = v + bv;
+                }
+                h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
+            }
+            const int px = wave * 64 + i * 16 + g * 4;
+            *reinterpret_cast<u32x2*>(tile + ch * LROW + px) = u32x2{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
+        }
+    }
+    __syncthreads();
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+    for (int idx = tid; idx < HL_BN * 32; idx += 256) {
+        const int ch = idx / 32, px = (idx % 32) * 8;
+        const int r = px / W, c = px - r * W;
+        if (n0 + ch >= p.N || h0 + r >= p.H) continue;
+        *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + n0 + ch) * HWs + (int64_t)(h0 + r) * W + c) =
+            *reinterpret_cast<const u32x4*>(tile + ch * LROW + px);
+    }
+}
+
 }  // namespace
 
 // mode: 0 forward, 1 grad input, 2 grad weight
@@ -796,6 +979,63 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
             else hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_BF16>, grid, dim3(256), 0, s, p.part, d.weight, p.M, p.N, cin, T, (int)split, sg);
         }
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
+    return TVK_OK;
+}
+
+
+// mode 0 forward, 1 grad input: stride 1, 3x3, padding 1, dilation 1, the
+// gathered side in whole 32-channel chunks, widths 8, 16, 32 or 64
+bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
+    if (mode != 0 && mode != 1) return false;
+    if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return false;
+    if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return false;
+    if (d.kh != 3 || d.kw != 3 || d.stride[0] != 1 || d.stride[1] != 1 || d.dilation[0] != 1 || d.dilation[1] != 1) return false;
+    if (d.padding[0] != 1 || d.padding[1] != 1) return false;
+    if (d.w != 8 && d.w != 16 && d.w != 32 && d.w != 64) return false;
+    const int64_t cs = mode == 0 ? d.c_in : d.c_out;
+    if (cs % 32 != 0) return false;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!al16(d.x) || !al16(d.y) || !al16(d.weight)) return false;
+    const int64_t big = std::max({d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h * d.w, d.c_out * d.c_in * 9});
+    return big < (int64_t(1) << 30);
+}
+
+tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
+    const int cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
+    const int Cs = mode == 0 ? cin : cout, N = mode == 0 ? cout : cin;
+    hipStream_t s = resolve_stream(d.stream);
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const size_t wt_b = (size_t)N * 9 * Cs * 2;
+    char* ws = static_cast<char*>(device_workspace(dev, wt_b));
+    if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the permuted weight");
+    WeightPermute wp;
+    wp.w = static_cast<const uint16_t*>(d.weight);
+    wp.out = reinterpret_cast<uint16_t*>(ws);
+    wp.cout = cout; wp.cin = cin; wp.taps = 9; wp.forward = mode == 0;
+    launch_nhwc(nullptr, nullptr, 0, 64, 8, 8, Border(), s, wp);   // no images: the weight alone
+    HaloArgs p;
+    memset(&p, 0, sizeof(p));
+    p.src = static_cast<const uint16_t*>(mode == 0 ? d.x : d.y);
+    p.wt = ws;
+    p.bias = mode == 0 ? d.bias : nullptr;
+    p.has_bias = (mode == 0 && d.bias) ? 1 : 0;
+    p.out = mode == 0 ? d.y : d.x;
+    p.Cs = Cs; p.N = N; p.H = H; p.W = W;
+    p.tr = 256 / W;
+    p.row_tiles = (H + p.tr - 1) / p.tr;
+    p.wt_bytes = (int)wt_b;
+    // forward: tap (a, b) reads source (h + a - 1, w + b - 1); grad input: (h + 1 - a, w + 1 - b)
+    for (int t = 0; t < 9; ++t) {
+        const int a = t / 3, b = t % 3;
+        const int ho = mode == 0 ? a - 1 : 1 - a, wo = mode == 0 ? b - 1 : 1 - b;
+        p.dtap[t] = ho * (W + 2) + wo;
+    }
+    const dim3 grid((unsigned)(d.n * p.row_tiles), (unsigned)((N + HL_BN - 1) / HL_BN));
+    if (d.dtype == TVK_F16) hipLaunchKernelGGL(conv_halo_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(conv_halo_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
     return TVK_OK;

@@ -198,6 +198,10 @@ hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, int 
 // 1 grad input, 2 grad weight.
 bool conv_ring_applies(const tvk_conv_desc& d, int mode);
 tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who);
+// Stride-1 3x3 padding-1 forward / grad input from NCHW through an LDS halo
+// (conv_nhwc.hip); mode 0 or 1.
+bool conv_halo_applies(const tvk_conv_desc& d, int mode);
+tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who);
 // Few input channels (conv_stem.hip): cin * kh * kw <= 32; same modes.
 bool conv_small_applies(const tvk_conv_desc& d, int mode);
 tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who);
