@@ -588,7 +588,9 @@ void border_for(int lo, int step, int count, int tap_lo, int tap_hi, int size, i
 // ---------------------------------------------------------------------------
 // Stride-1 3x3 "same" convolution (padding 1) straight from NCHW: forward
 // (source x) and grad input (source dy, taps mirrored). A workgroup computes
-// TR x W output pixels (TR * W = 256, W in 8..64) x 64 output channels. Per
+// TR x W output pixels (TR * W = 512, W in 8..64) x 64 output channels, 8
+// waves of 64 pixels (two per SIMD, so one wave's LDS waits overlap the
+// other's MFMAs). Per
 // 32-channel k chunk it stages the (TR + 2) x (W + 2) source halo in LDS
 // ([pixel][32 channels], 64-byte rows, the 16-byte chunks XOR-swizzled by
 // (pixel >> 2) & 3) and the permuted weight's [9 taps][64 channels][32] rows,
@@ -600,8 +602,9 @@ void border_for(int lo, int step, int count, int tap_lo, int tap_hi, int size, i
 // computes.
 // ---------------------------------------------------------------------------
 constexpr int HL_BN = 64;
-constexpr int HL_MAXHP = 396;   // halo pixels (TR + 2) * (W + 2), largest at W = 64
-constexpr int HL_A = 25600;     // HL_MAXHP * 64 bytes, rounded up to 1 KB
+constexpr int HL_PX = 512;      // output pixels a tile
+constexpr int HL_MAXHP = 660;   // halo pixels (TR + 2) * (W + 2), largest at W = 8 and 64
+constexpr int HL_A = 43008;     // HL_MAXHP * 64 bytes, rounded up to 1 KB
 constexpr int HL_B = 9 * HL_BN * 64;
 constexpr int HL_STAGE = HL_A + HL_B;
 
@@ -619,7 +622,7 @@ struct HaloArgs {
 __device__ inline int hl_swz(int row) { return (row >> 2) & 3; }
 
 template <int DT>
-__global__ __launch_bounds__(256) void conv_halo_kernel(HaloArgs p) {
+__global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
     __shared__ __attribute__((aligned(1024))) char lds[2 * HL_STAGE];
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
     const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64), g = lane / 16;
@@ -629,7 +632,7 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(HaloArgs p) {
     const int nk = p.Cs / 32;
 
     // zero halo columns 0 and W + 1 of both stages (no load writes them)
-    for (int e = tid; e < (p.tr + 2) * 8; e += 256) {
+    for (int e = tid; e < (p.tr + 2) * 8; e += 512) {
         const int hr = e / 8, hc = (e / 4) % 2 ? W + 1 : 0, ch = e % 4;
         const int hp = hr * WP + hc;
 #pragma unroll
@@ -665,19 +668,21 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(HaloArgs p) {
         }
     };
 
-    // weight rows: 36 DMA instructions of 16 rows a chunk, 9 per wave; row = tap * 64 + channel
+    // weight rows: 36 DMA instructions of 16 rows a chunk, instruction q * 8 + wave
+    // (waves 0-3 issue 5, waves 4-7 issue 4); row = tap * 64 + channel
     const i32x4 rb = v_rsrc(p.wt, p.wt_bytes);
-    int b_off[9];
+    int b_off[5];
 #pragma unroll
-    for (int q = 0; q < 9; ++q) {
-        const int row = (wave * 9 + q) * 16 + lane / 4;
+    for (int q = 0; q < 5; ++q) {
+        const int row = min(q * 8 + wave, 35) * 16 + lane / 4;
         const int t = row / HL_BN, co = min(n0 + row % HL_BN, p.N - 1);
         b_off[q] = ((co * 9 + t) * p.Cs + (((lane % 4) ^ hl_swz(row)) * 8)) * 2;
     }
     auto issue_b = [&](int kc, int st) {
         const uint32_t base = lds0 + (uint32_t)(st * HL_STAGE + HL_A);
 #pragma unroll
-        for (int q = 0; q < 9; ++q) v_dma16(rb, base + (uint32_t)((wave * 9 + q) * 1024), (uint32_t)(b_off[q] + kc * 64));
+        for (int q = 0; q < 5; ++q)
+            if (q * 8 + wave < 36) v_dma16(rb, base + (uint32_t)((q * 8 + wave) * 1024), (uint32_t)(b_off[q] + kc * 64));
     };
 
     // A fragment rows: this wave's 64 pixels of the tile, 16 per fragment
@@ -734,7 +739,7 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(HaloArgs p) {
 
     // [channel][pixel] tile, then 16-byte stores along the output rows
     typedef typename elem<DT>::T T;
-    constexpr int LROW = 256 + 8;
+    constexpr int LROW = HL_PX + 8;
     uint16_t* tile = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -759,8 +764,8 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(HaloArgs p) {
     }
     __syncthreads();
     uint16_t* out = static_cast<uint16_t*>(p.out);
-    for (int idx = tid; idx < HL_BN * 32; idx += 256) {
-        const int ch = idx / 32, px = (idx % 32) * 8;
+    for (int idx = tid; idx < HL_BN * (HL_PX / 8); idx += 512) {
+        const int ch = idx / (HL_PX / 8), px = (idx % (HL_PX / 8)) * 8;
         const int r = px / W, c = px - r * W;
         if (n0 + ch >= p.N || h0 + r >= p.H) continue;
         *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + n0 + ch) * HWs + (int64_t)(h0 + r) * W + c) =
@@ -1024,7 +1029,7 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     p.has_bias = (mode == 0 && d.bias) ? 1 : 0;
     p.out = mode == 0 ? d.y : d.x;
     p.Cs = Cs; p.N = N; p.H = H; p.W = W;
-    p.tr = 256 / W;
+    p.tr = HL_PX / W;
     p.row_tiles = (H + p.tr - 1) / p.tr;
     p.wt_bytes = (int)wt_b;
     // forward: tap (a, b) reads source (h + a - 1, w + b - 1); grad input: (h + 1 - a, w + 1 - b)
@@ -1034,8 +1039,8 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
         p.dtap[t] = ho * (W + 2) + wo;
     }
     const dim3 grid((unsigned)(d.n * p.row_tiles), (unsigned)((N + HL_BN - 1) / HL_BN));
-    if (d.dtype == TVK_F16) hipLaunchKernelGGL(conv_halo_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL(conv_halo_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
+    if (d.dtype == TVK_F16) hipLaunchKernelGGL(conv_halo_kernel<TVK_F16>, grid, dim3(512), 0, s, p);
+    else hipLaunchKernelGGL(conv_halo_kernel<TVK_BF16>, grid, dim3(512), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
     return TVK_OK;
