@@ -621,6 +621,29 @@ struct HaloArgs {
 
 __device__ inline int hl_swz(int row) { return (row >> 2) & 3; }
 
+// 3x3 weight w[co][c][9] -> forward wout[co][t][c] or grad input
+// wout[c][t][co], the reduced channel count a multiple of 8: a thread gathers
+// 8 consecutive reduced channels of one (row, tap) and writes them as one
+// 16-byte store.
+template <bool FWD>
+__global__ __launch_bounds__(256) void weight_permute9_kernel(const uint16_t* w, uint16_t* out, int cout, int cin) {
+    const int rows = FWD ? cout : cin, red = FWD ? cin : cout;
+    const int groups = red / 8, total = rows * 9 * groups;
+    for (int e = blockIdx.x * 256 + (int)threadIdx.x; e < total; e += (int)gridDim.x * 256) {
+        const int gi = e % groups, rest = e / groups;
+        const int t = rest % 9, r = rest / 9;
+        uint32_t v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int c0 = gi * 8 + 2 * k;
+            const uint32_t lo = FWD ? w[(r * cin + c0) * 9 + t] : w[(c0 * cin + r) * 9 + t];
+            const uint32_t hi = FWD ? w[(r * cin + c0 + 1) * 9 + t] : w[((c0 + 1) * cin + r) * 9 + t];
+            v[k] = lo | (hi << 16);
+        }
+        *reinterpret_cast<u32x4*>(out + (r * 9 + t) * red + gi * 8) = u32x4{v[0], v[1], v[2], v[3]};
+    }
+}
+
 template <int DT>
 __global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
     __shared__ __attribute__((aligned(1024))) char lds[2 * HL_STAGE];
@@ -1016,11 +1039,11 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     const size_t wt_b = (size_t)N * 9 * Cs * 2;
     char* ws = static_cast<char*>(device_workspace(dev, wt_b));
     if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the permuted weight");
-    WeightPermute wp;
-    wp.w = static_cast<const uint16_t*>(d.weight);
-    wp.out = reinterpret_cast<uint16_t*>(ws);
-    wp.cout = cout; wp.cin = cin; wp.taps = 9; wp.forward = mode == 0;
-    launch_nhwc(nullptr, nullptr, 0, 64, 8, 8, Border(), s, wp);   // no images: the weight alone
+    const int pgroups = N * 9 * (Cs / 8);
+    const dim3 pgrid((unsigned)std::min((pgroups + 255) / 256, 1024));
+    const uint16_t* w16 = static_cast<const uint16_t*>(d.weight);
+    if (mode == 0) hipLaunchKernelGGL(weight_permute9_kernel<true>, pgrid, dim3(256), 0, s, w16, reinterpret_cast<uint16_t*>(ws), cout, cin);
+    else hipLaunchKernelGGL(weight_permute9_kernel<false>, pgrid, dim3(256), 0, s, w16, reinterpret_cast<uint16_t*>(ws), cout, cin);
     HaloArgs p;
     memset(&p, 0, sizeof(p));
     p.src = static_cast<const uint16_t*>(mode == 0 ? d.x : d.y);
