@@ -171,15 +171,20 @@ def test_few_input_channels(gpu, dtype, case):
                           case.pop("s"), case.pop("p"), case.pop("hw"), seed=50, **case)
 
 
-# stride-1 3x3 padding-1 halo kernel (forward and grad input): every tile
+# stride-1 3x3 padding-1 halo kernels. Forward and grad input: every tile
 # width (64, 32, 16, 8 pixels; 4, 8, 16, 32 rows a tile), heights that end in
 # a partial tile, one and three 32-channel chunks, output channel counts that
-# leave a partial 64-channel tile, bias
+# leave a partial 64-channel tile, bias. Grad weight (64-channel blocks, whole
+# 256-pixel tiles): two input-channel blocks, a partial output-channel block,
+# fewer tiles than the four a workgroup sums
 HALO_CASES = [
     dict(n=2, cin=32, cout=64, k=3, s=1, p=1, hw=(20, 16)),
     dict(n=1, cin=96, cout=96, k=3, s=1, p=1, hw=(10, 64)),
     dict(n=2, cin=64, cout=40, k=3, s=1, p=1, hw=(13, 8)),
     dict(n=3, cin=32, cout=32, k=3, s=1, p=1, hw=(9, 32)),
+    dict(n=2, cin=64, cout=96, k=3, s=1, p=1, hw=(16, 16)),
+    dict(n=1, cin=128, cout=64, k=3, s=1, p=1, hw=(64, 8)),
+    dict(n=3, cin=64, cout=32, k=3, s=1, p=1, hw=(8, 32)),
 ]
 
 

@@ -796,6 +796,191 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
     }
 }
 
+// Grad weight of the same convolution (stride 1, 3x3, padding 1) from NCHW:
+// a workgroup takes 64 input channels x 64 output channels x all 9 taps and
+// sums its share of 256-pixel tiles (TR x W output rows of one image, H % TR
+// == 0) into float32 partials [split][(tap, channel)][output channel]:
+// C[c][co] += sum_p x(p + tap)[c] * dy[co][p]. The 36 row fragments (tap, 16
+// channels) go to 8 waves as w, w + 8, ... (waves 0-3 take five, 4-7 four, so
+// the two waves of each SIMD hold nine), each against all 64 columns. The x
+// halo in LDS as [pixel][64 channels] (128-byte rows, 16-byte chunk c at
+// c ^ (pixel & 3) * 2, so the 16 lanes of a transposed read hit distinct
+// banks) read at the tap's shift by ds_read_b64_tr_b16, and the dy tile as
+// [64 channels][256 pixels] (512-byte rows, chunk c at c ^ (channel & 15))
+// read as 16-byte fragments. Two stages: tile i + 1 loads while i computes.
+constexpr int HG_A = 44032;            // halo pixels (TR + 2) * (W + 2) <= 340 at W <= 32, x 128 bytes, rounded up to 1 KB
+constexpr int HG_B = 64 * 512;
+constexpr int HG_STAGE = HG_A + HG_B;
+
+struct HaloWgArgs {
+    const uint16_t* x;     // [n][cin][H][W]
+    const void* dy;        // [n][cout][H][W]
+    float* part;           // [split][9 * cin][cout]
+    int cin, cout, H, W, wshift, tr, tiles_per_img, ntiles, split;
+    int dy_bytes;
+};
+
+__device__ inline int hg_swz(int hp) { return (hp & 3) * 2; }
+
+template <int DT>
+__global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
+    __shared__ __attribute__((aligned(1024))) char lds[2 * HG_STAGE];
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
+    const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int g = lane / 16, sl = lane % 16;
+    const int c0 = blockIdx.y * 64, n0 = blockIdx.z * 64;
+    const int W = p.W, WP = W + 2, HWs = p.H * W;
+    // row fragment k of this wave: rf = wave + 8k (k < 4, or 5 for waves 0-3), tap rf / 4, channels (rf % 4) * 16
+    const int nrf = wave < 4 ? 5 : 4;
+    const int cf = wave % 4;
+    int dtap[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+        const int t = min((wave + 8 * k) / 4, 8);
+        dtap[k] = (t / 3) * WP + t % 3;
+    }
+
+    // zero halo columns 0 and W + 1 of both stages (no load writes them)
+    for (int e = tid; e < (p.tr + 2) * 16; e += 512) {
+        const int hr = e / 16, hc = (e / 8) % 2 ? W + 1 : 0, ch = e % 8;
+        const int hp = hr * WP + hc;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+            *reinterpret_cast<u32x4*>(lds + st * HG_STAGE + hp * 128 + ch * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+
+    // x halo gather: lane -> (column group wq, channel group cg of 8, halo row hr)
+    const int nwq = W / 8;
+    const int wq = tid % nwq, cg = (tid / nwq) % 8, hr = tid / (nwq * 8);
+    const bool a_live = hr < p.tr + 2;
+    u32x4 ar[8];
+    auto load_a = [&](int tile) {
+        const int img = tile / p.tiles_per_img, h0 = (tile - img * p.tiles_per_img) * p.tr;
+        const int ih = h0 - 1 + hr;
+        const bool row = a_live && ih >= 0 && ih < p.H;
+        const uint16_t* src = p.x + ((int64_t)img * p.cin + c0 + cg * 8) * HWs + (int64_t)(row ? ih : 0) * W + wq * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ar[i] = row ? *reinterpret_cast<const u32x4*>(src + (int64_t)i * HWs) : u32x4{0u, 0u, 0u, 0u};
+    };
+    auto store_a = [&](int st) {
+        if (!a_live) return;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t lo = ar[2 * k][j / 2], hi = ar[2 * k + 1][j / 2];
+                v[k] = (j % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+            }
+            const int hp = hr * WP + wq * 8 + j + 1;
+            *reinterpret_cast<u32x4*>(lds + st * HG_STAGE + hp * 128 + ((cg ^ hg_swz(hp)) * 16)) = u32x4{v[0], v[1], v[2], v[3]};
+        }
+    };
+
+    // dy tile: 32 DMA instructions of two 512-byte channel rows, instruction q * 8 + wave
+    const i32x4 rb = v_rsrc(p.dy, p.dy_bytes);
+    uint32_t b_off[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int pair = q * 8 + wave;
+        const int col = pair * 2 + lane / 32;
+        const int co = min(n0 + col, p.cout - 1);
+        b_off[q] = (uint32_t)((co * HWs + (((lane % 32) ^ (col & 15)) * 8)) * 2);
+    }
+    auto issue_b = [&](int tile, int st) {
+        const int img = tile / p.tiles_per_img, h0 = (tile - img * p.tiles_per_img) * p.tr;
+        const uint32_t toff = (uint32_t)((((int64_t)img * p.cout) * HWs + (int64_t)h0 * W) * 2);
+        const uint32_t base = lds0 + (uint32_t)(st * HG_STAGE + HG_A);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v_dma16(rb, base + (uint32_t)((q * 8 + wave) * 1024), b_off[q] + toff);
+    };
+
+    f32x4 acc[5][4];
+#pragma unroll
+    for (int i = 0; i < 5; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    int tile = blockIdx.x;
+    if (tile < p.ntiles) {
+        issue_b(tile, 0);
+        load_a(tile);
+        store_a(0);
+    }
+    v_wait<0>();
+    __syncthreads();
+    for (int it = 0; tile < p.ntiles; ++it, tile += p.split) {
+        const int cur = it & 1;
+        const int next = tile + p.split;
+        if (next < p.ntiles) {
+            issue_b(next, cur ^ 1);
+            load_a(next);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const char* sa = lds + cur * HG_STAGE;
+        const char* sb = sa + HG_A;
+#pragma unroll 1
+        for (int ks = 0; ks < 8; ++ks) {
+            // A: rows = 16 input channels of one tap, k = this step's 32 pixels (transposed reads)
+            u32x4 fa[5];
+            int hb[2];
+#pragma unroll
+            for (int rr = 0; rr < 2; ++rr) {
+                const int px = ks * 32 + g * 8 + rr * 4 + sl / 4;
+                hb[rr] = (px >> p.wshift) * WP + (px & (W - 1));
+            }
+            const int col = cf * 16 + (sl % 4) * 4;
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                if (i >= nrf) break;
+#pragma unroll
+                for (int rr = 0; rr < 2; ++rr) {
+                    const int hp = hb[rr] + dtap[i];
+                    const char* ptr = sa + hp * 128 + (((col / 8) ^ hg_swz(hp)) * 16) + (col % 8) * 2;
+                    const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((TVK_LDS s16x4*)(uintptr_t)(TVK_LDS const char*)ptr));
+                    fa[i][rr * 2] = w.x;
+                    fa[i][rr * 2 + 1] = w.y;
+                }
+            }
+            // B: columns = 16 output channels, k = the same 32 pixels
+            u32x4 fb[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = j * 16 + sl;
+                fb[j] = *reinterpret_cast<const u32x4*>(sb + col * 512 + (((ks * 4 + g) ^ (col & 15)) * 16));
+            }
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                if (i >= nrf) break;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (next < p.ntiles) store_a(cur ^ 1);
+        v_wait<0>();
+        __syncthreads();
+    }
+
+    // partial rows (tap, channel) of this wave's row fragments, columns = output channels
+    float* part = p.part + (int64_t)blockIdx.x * 9 * p.cin * p.cout;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        if (i >= nrf) break;
+        const int t = (wave + 8 * i) / 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int co = n0 + j * 16 + sl;
+            if (co >= p.cout) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int c = c0 + cf * 16 + g * 4 + r;
+                part[((int64_t)t * p.cin + c) * p.cout + co] = acc[i][j][r];
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // mode: 0 forward, 1 grad input, 2 grad weight
@@ -1013,24 +1198,66 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
 }
 
 
-// mode 0 forward, 1 grad input: stride 1, 3x3, padding 1, dilation 1, the
-// gathered side in whole 32-channel chunks, widths 8, 16, 32 or 64
+// stride 1, 3x3, padding 1, dilation 1. Forward / grad input: the gathered
+// side in whole 32-channel chunks, widths 8, 16, 32 or 64. Grad weight: input
+// channels in 64-channel blocks, widths 8, 16 or 32 with whole 256-pixel tiles.
 bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
-    if (mode != 0 && mode != 1) return false;
     if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return false;
     if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return false;
     if (d.kh != 3 || d.kw != 3 || d.stride[0] != 1 || d.stride[1] != 1 || d.dilation[0] != 1 || d.dilation[1] != 1) return false;
     if (d.padding[0] != 1 || d.padding[1] != 1) return false;
     if (d.w != 8 && d.w != 16 && d.w != 32 && d.w != 64) return false;
-    const int64_t cs = mode == 0 ? d.c_in : d.c_out;
-    if (cs % 32 != 0) return false;
+    if (mode == 2) {
+        if (d.w == 64 || d.c_in % 64 != 0 || d.h % (256 / d.w) != 0) return false;
+    } else if ((mode == 0 ? d.c_in : d.c_out) % 32 != 0) {
+        return false;
+    }
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     if (!al16(d.x) || !al16(d.y) || !al16(d.weight)) return false;
     const int64_t big = std::max({d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h * d.w, d.c_out * d.c_in * 9});
     return big < (int64_t(1) << 30);
 }
 
+tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
+    const int cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
+    hipStream_t s = resolve_stream(d.stream);
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    HaloWgArgs p;
+    memset(&p, 0, sizeof(p));
+    p.x = static_cast<const uint16_t*>(d.x);
+    p.dy = d.y;
+    p.cin = cin; p.cout = cout; p.H = H; p.W = W;
+    p.wshift = W == 8 ? 3 : W == 16 ? 4 : 5;
+    p.tr = 256 / W;
+    p.tiles_per_img = H / p.tr;
+    p.ntiles = (int)d.n * p.tiles_per_img;
+    p.dy_bytes = (int)(d.n * cout * H * W * 2);
+    const int cb = cin / 64, nb = (cout + 63) / 64;
+    // about 256 workgroups, each summing at least 4 tiles (fewer partials to write and add)
+    p.split = std::max(1, std::min(p.ntiles / 4, 256 / (cb * nb)));
+    const size_t part_b = (size_t)p.split * 9 * cin * cout * sizeof(float);
+    char* ws = static_cast<char*>(device_workspace(dev, part_b));
+    if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
+    p.part = reinterpret_cast<float*>(ws);
+    const dim3 grid((unsigned)p.split, (unsigned)cb, (unsigned)nb);
+    const bool f16 = d.dtype == TVK_F16;
+    if (f16) hipLaunchKernelGGL(conv_halo_wgrad_kernel<TVK_F16>, grid, dim3(512), 0, s, p);
+    else hipLaunchKernelGGL(conv_halo_wgrad_kernel<TVK_BF16>, grid, dim3(512), 0, s, p);
+    // partials [split][(tap, channel)][output channel] -> dW[co][c][tap]
+    const int M = 9 * cin, total = M * cout;
+    int sg = 1;
+    while (sg < 16 && sg * 2 <= p.split && (int64_t)total * sg / 1024 < 1024) sg *= 2;
+    const dim3 rgrid((unsigned)((total + 1024 / sg - 1) / (1024 / sg)));
+    if (f16) hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_F16>, rgrid, dim3(256), 0, s, p.part, d.weight, M, cout, cin, 9, p.split, sg);
+    else hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_BF16>, rgrid, dim3(256), 0, s, p.part, d.weight, M, cout, cin, 9, p.split, sg);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
+    return TVK_OK;
+}
+
 tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
+    if (mode == 2) return conv_halo_wgrad_run(d, who);
     const int cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
     const int Cs = mode == 0 ? cin : cout, N = mode == 0 ? cout : cin;
     hipStream_t s = resolve_stream(d.stream);
