@@ -799,49 +799,51 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
 // Grad weight of the same convolution (stride 1, 3x3, padding 1) from NCHW:
 // a workgroup takes 64 input channels x 64 output channels x all 9 taps and
 // sums its share of 256-pixel tiles (TR x W output rows of one image, H % TR
-// == 0) into float32 partials [split][(tap, channel)][output channel]:
-// C[c][co] += sum_p x(p + tap)[c] * dy[co][p]. The 36 row fragments (tap, 16
-// channels) go to 8 waves as w, w + 8, ... (waves 0-3 take five, 4-7 four, so
-// the two waves of each SIMD hold nine), each against all 64 columns. The x
-// halo in LDS as [pixel][64 channels] (128-byte rows, 16-byte chunk c at
-// c ^ (pixel & 3) * 2, so the 16 lanes of a transposed read hit distinct
-// banks) read at the tap's shift by ds_read_b64_tr_b16, and the dy tile as
-// [64 channels][256 pixels] (512-byte rows, chunk c at c ^ (channel & 15))
-// read as 16-byte fragments. Two stages: tile i + 1 loads while i computes.
-constexpr int HG_A = 44032;            // halo pixels (TR + 2) * (W + 2) <= 340 at W <= 32, x 128 bytes, rounded up to 1 KB
-constexpr int HG_B = 64 * 512;
+// == 0, W = 16 or 32) into float32 partials [split][(tap, channel)][output
+// channel]: C[c][co] += sum_p x(p + tap)[c] * dy[co][p]. The 36 row fragments
+// (tap, 16 channels) go to 8 waves as w, w + 8, ... (waves 0-3 take five, 4-7
+// four, so the two waves of each SIMD hold nine), each against all 64 columns.
+// LDS per stage:
+//   x halo [TR + 2][W + 4][64 channels], 128-byte pixel rows, 16-byte chunk c
+//     at c ^ (pixel & 3) * 2 (the 16 lanes of a transposed read hit distinct
+//     banks); the row pitch W + 4 makes a k step (32 pixels) a multiple of 4
+//     pixels, so every fragment address of step s is step 0's plus a constant
+//     (an instruction offset: no address arithmetic in the k loop);
+//   dy [32 pixel chunks][64 output channels][8 pixels]: a fragment is 16 lanes
+//     x 16 contiguous bytes, its offset again linear in the step; one LDS-DMA
+//     instruction loads one pixel chunk of the 64 channels.
+// A fragments are transposed reads (ds_read_b64_tr_b16) at the tap's shift.
+// Two stages: tile i + 1 loads while i computes.
+constexpr int HG_A = 46080;            // (TR + 2) * (W + 4) pixels x 128 bytes: 10 x 36 at W = 32, 18 x 20 at W = 16
+constexpr int HG_B = 32 * 1024;
 constexpr int HG_STAGE = HG_A + HG_B;
 
 struct HaloWgArgs {
     const uint16_t* x;     // [n][cin][H][W]
     const void* dy;        // [n][cout][H][W]
     float* part;           // [split][9 * cin][cout]
-    int cin, cout, H, W, wshift, tr, tiles_per_img, ntiles, split;
+    int cin, cout, H, tiles_per_img, ntiles, split;
     int dy_bytes;
 };
 
 __device__ inline int hg_swz(int hp) { return (hp & 3) * 2; }
 
-template <int DT>
+template <int DT, int W>
 __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
+    constexpr int TR = 256 / W, WP = W + 4, STEP = (32 / W) * WP;   // halo pixels per k step
+    static_assert(STEP % 4 == 0 && (TR + 2) * WP * 128 <= HG_A, "halo layout");
     __shared__ __attribute__((aligned(1024))) char lds[2 * HG_STAGE];
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
     const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const int g = lane / 16, sl = lane % 16;
     const int c0 = blockIdx.y * 64, n0 = blockIdx.z * 64;
-    const int W = p.W, WP = W + 2, HWs = p.H * W;
+    const int HWs = p.H * W;
     // row fragment k of this wave: rf = wave + 8k (k < 4, or 5 for waves 0-3), tap rf / 4, channels (rf % 4) * 16
-    const int nrf = wave < 4 ? 5 : 4;
+    const bool five = wave < 4;
     const int cf = wave % 4;
-    int dtap[5];
-#pragma unroll
-    for (int k = 0; k < 5; ++k) {
-        const int t = min((wave + 8 * k) / 4, 8);
-        dtap[k] = (t / 3) * WP + t % 3;
-    }
 
     // zero halo columns 0 and W + 1 of both stages (no load writes them)
-    for (int e = tid; e < (p.tr + 2) * 16; e += 512) {
+    for (int e = tid; e < (TR + 2) * 16; e += 512) {
         const int hr = e / 16, hc = (e / 8) % 2 ? W + 1 : 0, ch = e % 8;
         const int hp = hr * WP + hc;
 #pragma unroll
@@ -850,12 +852,12 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
     }
 
     // x halo gather: lane -> (column group wq, channel group cg of 8, halo row hr)
-    const int nwq = W / 8;
-    const int wq = tid % nwq, cg = (tid / nwq) % 8, hr = tid / (nwq * 8);
-    const bool a_live = hr < p.tr + 2;
+    constexpr int NWQ = W / 8;
+    const int wq = tid % NWQ, cg = (tid / NWQ) % 8, hr = tid / (NWQ * 8);
+    const bool a_live = hr < TR + 2;
     u32x4 ar[8];
     auto load_a = [&](int tile) {
-        const int img = tile / p.tiles_per_img, h0 = (tile - img * p.tiles_per_img) * p.tr;
+        const int img = tile / p.tiles_per_img, h0 = (tile - img * p.tiles_per_img) * TR;
         const int ih = h0 - 1 + hr;
         const bool row = a_live && ih >= 0 && ih < p.H;
         const uint16_t* src = p.x + ((int64_t)img * p.cin + c0 + cg * 8) * HWs + (int64_t)(row ? ih : 0) * W + wq * 8;
@@ -877,23 +879,35 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
         }
     };
 
-    // dy tile: 32 DMA instructions of two 512-byte channel rows, instruction q * 8 + wave
+    // dy: DMA instruction q (wave * 4 + 0..3) loads pixel chunk q: lane = output channel
     const i32x4 rb = v_rsrc(p.dy, p.dy_bytes);
-    uint32_t b_off[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int pair = q * 8 + wave;
-        const int col = pair * 2 + lane / 32;
-        const int co = min(n0 + col, p.cout - 1);
-        b_off[q] = (uint32_t)((co * HWs + (((lane % 32) ^ (col & 15)) * 8)) * 2);
-    }
+    const uint32_t b_lane = (uint32_t)(min(n0 + lane, p.cout - 1) * HWs * 2);
     auto issue_b = [&](int tile, int st) {
-        const int img = tile / p.tiles_per_img, h0 = (tile - img * p.tiles_per_img) * p.tr;
+        const int img = tile / p.tiles_per_img, h0 = (tile - img * p.tiles_per_img) * TR;
         const uint32_t toff = (uint32_t)((((int64_t)img * p.cout) * HWs + (int64_t)h0 * W) * 2);
         const uint32_t base = lds0 + (uint32_t)(st * HG_STAGE + HG_A);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v_dma16(rb, base + (uint32_t)((q * 8 + wave) * 1024), b_off[q] + toff);
+        for (int q = 0; q < 4; ++q) {
+            const int chunk = wave * 4 + q;
+            v_dma16(rb, base + (uint32_t)(chunk * 1024), b_lane + toff + (uint32_t)(chunk * 16));
+        }
     };
+
+    // fragment offsets at k step 0 (step s adds s * STEP pixels)
+    int a_off[5][2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+        const int px = g * 8 + rr * 4 + sl / 4;
+        const int hb = (px / W) * WP + px % W;
+        const int col = cf * 16 + (sl % 4) * 4;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            const int t = min((wave + 8 * k) / 4, 8);
+            const int hp = hb + (t / 3) * WP + t % 3;
+            a_off[k][rr] = hp * 128 + (((col / 8) ^ hg_swz(hp)) * 16) + (col % 8) * 2;
+        }
+    }
+    const int b_off = g * 1024 + sl * 16;
 
     f32x4 acc[5][4];
 #pragma unroll
@@ -918,25 +932,17 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
         }
         __builtin_amdgcn_sched_barrier(0);
         const char* sa = lds + cur * HG_STAGE;
-        const char* sb = sa + HG_A;
-#pragma unroll 1
+        const char* sb = sa + HG_A + b_off;
+#pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             // A: rows = 16 input channels of one tap, k = this step's 32 pixels (transposed reads)
             u32x4 fa[5];
-            int hb[2];
-#pragma unroll
-            for (int rr = 0; rr < 2; ++rr) {
-                const int px = ks * 32 + g * 8 + rr * 4 + sl / 4;
-                hb[rr] = (px >> p.wshift) * WP + (px & (W - 1));
-            }
-            const int col = cf * 16 + (sl % 4) * 4;
 #pragma unroll
             for (int i = 0; i < 5; ++i) {
-                if (i >= nrf) break;
+                if (i == 4 && !five) break;
 #pragma unroll
                 for (int rr = 0; rr < 2; ++rr) {
-                    const int hp = hb[rr] + dtap[i];
-                    const char* ptr = sa + hp * 128 + (((col / 8) ^ hg_swz(hp)) * 16) + (col % 8) * 2;
+                    const char* ptr = sa + a_off[i][rr] + ks * STEP * 128;
                     const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((TVK_LDS s16x4*)(uintptr_t)(TVK_LDS const char*)ptr));
                     fa[i][rr * 2] = w.x;
                     fa[i][rr * 2 + 1] = w.y;
@@ -945,13 +951,10 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
             // B: columns = 16 output channels, k = the same 32 pixels
             u32x4 fb[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int col = j * 16 + sl;
-                fb[j] = *reinterpret_cast<const u32x4*>(sb + col * 512 + (((ks * 4 + g) ^ (col & 15)) * 16));
-            }
+            for (int j = 0; j < 4; ++j) fb[j] = *reinterpret_cast<const u32x4*>(sb + ks * 4096 + j * 256);
 #pragma unroll
             for (int i = 0; i < 5; ++i) {
-                if (i >= nrf) break;
+                if (i == 4 && !five) break;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
             }
@@ -966,7 +969,7 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
     float* part = p.part + (int64_t)blockIdx.x * 9 * p.cin * p.cout;
 #pragma unroll
     for (int i = 0; i < 5; ++i) {
-        if (i >= nrf) break;
+        if (i == 4 && !five) break;
         const int t = (wave + 8 * i) / 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1200,7 +1203,7 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
 
 // stride 1, 3x3, padding 1, dilation 1. Forward / grad input: the gathered
 // side in whole 32-channel chunks, widths 8, 16, 32 or 64. Grad weight: input
-// channels in 64-channel blocks, widths 8, 16 or 32 with whole 256-pixel tiles.
+// channels in 64-channel blocks, widths 16 or 32 with whole 256-pixel tiles.
 bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
     if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return false;
     if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return false;
@@ -1208,7 +1211,7 @@ bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
     if (d.padding[0] != 1 || d.padding[1] != 1) return false;
     if (d.w != 8 && d.w != 16 && d.w != 32 && d.w != 64) return false;
     if (mode == 2) {
-        if (d.w == 64 || d.c_in % 64 != 0 || d.h % (256 / d.w) != 0) return false;
+        if ((d.w != 16 && d.w != 32) || d.c_in % 64 != 0 || d.h % (256 / d.w) != 0) return false;
     } else if ((mode == 0 ? d.c_in : d.c_out) % 32 != 0) {
         return false;
     }
@@ -1227,23 +1230,26 @@ tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
     memset(&p, 0, sizeof(p));
     p.x = static_cast<const uint16_t*>(d.x);
     p.dy = d.y;
-    p.cin = cin; p.cout = cout; p.H = H; p.W = W;
-    p.wshift = W == 8 ? 3 : W == 16 ? 4 : 5;
-    p.tr = 256 / W;
-    p.tiles_per_img = H / p.tr;
+    p.cin = cin; p.cout = cout; p.H = H;
+    p.tiles_per_img = H / (256 / W);
     p.ntiles = (int)d.n * p.tiles_per_img;
     p.dy_bytes = (int)(d.n * cout * H * W * 2);
     const int cb = cin / 64, nb = (cout + 63) / 64;
-    // about 256 workgroups, each summing at least 4 tiles (fewer partials to write and add)
-    p.split = std::max(1, std::min(p.ntiles / 4, 256 / (cb * nb)));
+    // about 256 workgroups (one a CU), each summing at least 2 tiles
+    p.split = std::max(1, std::min(p.ntiles / 2, 256 / (cb * nb)));
     const size_t part_b = (size_t)p.split * 9 * cin * cout * sizeof(float);
     char* ws = static_cast<char*>(device_workspace(dev, part_b));
     if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
     p.part = reinterpret_cast<float*>(ws);
     const dim3 grid((unsigned)p.split, (unsigned)cb, (unsigned)nb);
     const bool f16 = d.dtype == TVK_F16;
-    if (f16) hipLaunchKernelGGL(conv_halo_wgrad_kernel<TVK_F16>, grid, dim3(512), 0, s, p);
-    else hipLaunchKernelGGL(conv_halo_wgrad_kernel<TVK_BF16>, grid, dim3(512), 0, s, p);
+    if (W == 32) {
+        if (f16) hipLaunchKernelGGL((conv_halo_wgrad_kernel<TVK_F16, 32>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((conv_halo_wgrad_kernel<TVK_BF16, 32>), grid, dim3(512), 0, s, p);
+    } else {
+        if (f16) hipLaunchKernelGGL((conv_halo_wgrad_kernel<TVK_F16, 16>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((conv_halo_wgrad_kernel<TVK_BF16, 16>), grid, dim3(512), 0, s, p);
+    }
     // partials [split][(tap, channel)][output channel] -> dW[co][c][tap]
     const int M = 9 * cin, total = M * cout;
     int sg = 1;
