@@ -526,12 +526,18 @@ __global__ __launch_bounds__(256) void wgrad_ring_reduce_kernel(const float* par
 
 // Launches MODE 0 over set.ph[0..nph) (grid z = phase) or MODE 1 over `splits`
 // k splits. 128-row tiles when 256-row tiles would leave the device under-filled.
+#ifndef TVK_RING_MIN_BN
+#define TVK_RING_MIN_BN 64
+#endif
 template <int DT, int MODE>
 void launch_ring(const ConvRingSet& set, int nph, int splits, hipStream_t s) {
     const ConvRing& p0 = set.ph[0];
-    const int bn = p0.N <= 64 ? 64 : p0.N <= 128 ? 128 : 256;
+    int bn = p0.N <= 64 ? 64 : p0.N <= 128 ? 128 : 256;
     int max_m = 0;
     for (int i = 0; i < nph; ++i) max_m = std::max(max_m, set.ph[i].M);
+    // forward / grad input: narrower columns while 128-row tiles leave the device under-filled
+    if (MODE == 0)
+        while (bn > TVK_RING_MIN_BN && (int64_t)((max_m + 127) / 128) * ((p0.N + bn - 1) / bn) * nph < 192) bn /= 2;
     const int ny = (p0.N + bn - 1) / bn;
     const int64_t t256 = (int64_t)((max_m + 255) / 256) * ny * (MODE == 0 ? nph : splits);
     const int bm = (MODE == 0 && t256 < 192) ? 128 : 256;
