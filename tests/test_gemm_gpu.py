@@ -236,8 +236,15 @@ def test_split_k_integer_exact(gpu, dtype, case):
     a = a.transpose(-1, -2) if ta else a
     b = b.transpose(-1, -2) if tb else b
     got, plan = run(gpu, a, b, lead + (M, N), dtype)
-    assert plan == "gemm16_mfma_128x128_splitk"
+    # the LDS-ring kernel takes the split where it applies (K a multiple of 32)
+    assert plan == ("gemm16_dma_128x128_splitk" if K % 32 == 0 else "gemm16_mfma_128x128_splitk")
     assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
+    if K % 32 == 0:
+        # the register-staged split kernel on the same product, and an odd split count
+        for kernel in ("gemm16_mfma_128x128_splitk:4", "gemm16_dma_128x128_splitk:2"):
+            got, plan = run(gpu, a, b, lead + (M, N), dtype, kernel=kernel)
+            assert plan == kernel.split(":")[0]
+            assert np.array_equal(got, _exact_ref(a, b, dtype)), kernel
 
 
 @pytest.mark.parametrize("dtype", F16_TYPES)
@@ -249,7 +256,7 @@ def test_split_k_epilogue_sampled_rows(gpu, dtype, act):
     b = ((torch.rand((N, K), generator=gen(26)) * 2 - 1) * K ** -0.5).to(dtype).t()
     bias = ((torch.rand((N,), generator=gen(27)) * 2 - 1) * K ** -0.5).to(dtype)
     got, plan = run(gpu, a, b, (M, N), dtype, bias=bias, alpha=1.0, beta=1.0, act=act)
-    assert plan == "gemm16_mfma_128x128_splitk"
+    assert plan == "gemm16_dma_128x128_splitk"
     rows = np.r_[0:4, 127:130, M - 4:M]
     ref = oracle_mm(a[rows], b, dtype, bias=bias, alpha=1.0, beta=1.0, act=act)
     assert_close(got[rows], ref, dtype, plan)

@@ -644,12 +644,12 @@ Plan skinny_plan(const tvk_gemm_desc& d, Plan pl) {
 // MFMA128 with K split about `want` ways into chunks of whole 64-k steps,
 // float32 partials; false when that would not split or the partials would
 // exceed 512 MB.
-bool split_plan(const tvk_gemm_desc& d, int64_t want, Plan& pl) {
+bool split_plan(const tvk_gemm_desc& d, int64_t want, Plan& pl, Kern kern = Kern::MFMA128) {
     if (want < 2) return false;
     const int64_t chunk = ((d.K + want - 1) / want + 63) / 64 * 64;
     const int64_t split = (d.K + chunk - 1) / chunk;
     if (split < 2 || split * d.batch * d.M * d.N * 4 > (int64_t(512) << 20)) return false;
-    pl = with_kern(pl, Kern::MFMA128, "gemm16_mfma_128x128_splitk");
+    pl = with_kern(pl, kern, kern == Kern::DMA128 ? "gemm16_dma_128x128_splitk" : "gemm16_mfma_128x128_splitk");
     pl.split = (int)split;
     pl.k_chunk = (int)chunk;
     return true;
@@ -689,10 +689,16 @@ Plan make_plan(const tvk_gemm_desc& d) {
         // split K into a power of two of chunks so at least one workgroup per
         // CU runs, chunks of at least 256 k, partials in float32. Below
         // K = 2048 the partials' round trip costs more than the idle CUs.
+        // The LDS-ring kernel takes the split where it applies and the tiles are
+        // whole 128-wide ones (measured 1.2-1.7x on the C2/C3 batch-256 and
+        // weight-gradient products); a 10-column output keeps the
+        // register-staged kernel.
         if (t128 < 192 && d.K >= 2048) {
             auto pow2_ceil = [](int64_t v) { int64_t r = 1; while (r < v) r *= 2; return r; };
             auto pow2_floor = [](int64_t v) { int64_t r = 1; while (r * 2 <= v) r *= 2; return r; };
-            if (split_plan(d, std::min<int64_t>({pow2_ceil((256 + t128 - 1) / t128), pow2_floor(d.K / 256), 32}), pl))
+            const bool dma = pl.vec && d.M >= 128 && d.N >= 128 && dma_applies(repacked_args(d, pl), pl.ak, pl.bk);
+            if (split_plan(d, std::min<int64_t>({pow2_ceil((256 + t128 - 1) / t128), pow2_floor(d.K / 256), 32}), pl,
+                           dma ? Kern::DMA128 : Kern::MFMA128))
                 return pl;
         }
         // The LDS-ring kernel on 128x128 tiles, except for two k-contiguous
@@ -741,7 +747,13 @@ std::vector<Plan> candidate_plans(const tvk_gemm_desc& d) {
         if (split_plan(d, want, p)) add(p);
     }
     const bool dma = lay.vec && dma_applies(repacked_args(d, lay), lay.ak, lay.bk);
-    if (dma) add(with_kern(lay, Kern::DMA128, "gemm16_dma_128x128"));
+    if (dma) {
+        add(with_kern(lay, Kern::DMA128, "gemm16_dma_128x128"));
+        for (int64_t want : {2, 4, 8, 16}) {
+            Plan p = lay;
+            if (split_plan(d, want, p, Kern::DMA128)) add(p);
+        }
+    }
     if (d.M >= 128 && d.N >= 128) {
         add(with_kern(lay, Kern::MFMA256W8, "gemm16_mfma_256x256_w8"));
         add(with_kern(lay, Kern::MFMA256, "gemm16_mfma_256x256"));
@@ -831,7 +843,7 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
         const int64_t b_rows = pl.bk ? d.N : d.K, b_ld = pad8(pl.bk ? d.K : d.N);
         const size_t rep_a = pl.repack_a ? al256((size_t)nb * a_rows * a_ld * 2) : 0;
         const size_t rep_b = pl.repack_b ? al256((size_t)nb * b_rows * b_ld * 2) : 0;
-        const size_t part_b = (pl.kern == Kern::MFMA128 && pl.split > 1) ? (size_t)pl.split * nb * d.M * d.N * 4 : 0;
+        const size_t part_b = pl.split > 1 ? (size_t)pl.split * nb * d.M * d.N * 4 : 0;
         char* ws = nullptr;
         if (rep_a + rep_b + part_b > 0) {
             int dev = 0;
@@ -895,8 +907,18 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
         case Kern::DMA256:
         case Kern::DMA128:
             if constexpr (DT != TVK_F32) {
+                if (pl.split > 1) {
+                    q.part = reinterpret_cast<float*>(ws + rep_a + rep_b);
+                    q.split = pl.split;
+                    q.k_chunk = pl.k_chunk;
+                }
                 hipError_t e = launch_dma(DT, q, pl.ak, pl.bk, pl.kern == Kern::DMA256 ? 256 : 128, s);
                 if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_gemm: launch failed: ") + hipGetErrorString(e));
+                if (pl.split > 1) {
+                    const int64_t total = (int64_t)nb * d.M * d.N;
+                    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+                    hipLaunchKernelGGL(gemm_split_reduce_kernel<DT>, dim3(blocks), dim3(256), 0, s, q);
+                }
             }
             break;
         case Kern::MFMA256:

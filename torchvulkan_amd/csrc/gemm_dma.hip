@@ -170,10 +170,13 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     DmaSrc<BK, G::DB, BN> db;
     da.init(p.sa[1], p.sa[2], m0, p.M, wave, lane);
     db.init(p.sb[2], p.sb[1], n0, p.N, wave, lane);
+    // split-K (grid z): this workgroup's k range starts at stage kt0
+    const int kt0 = p.split > 1 ? (int)blockIdx.z * (p.k_chunk / D_BK) : 0;
     auto dma_one = [&](int kt, int q) {   // q-th load (of D_DPS) of this wave for stage kt
         const uint32_t slot = lds0 + (uint32_t)((kt % D_NS) * D_STB);
-        if (q < G::DA) dma16(ra, slot + (uint32_t)((wave * G::DA + q) * 1024), da.off[q] + (uint32_t)kt * da.kstep);
-        else dma16(rb, slot + D_OPB + (uint32_t)((wave * G::DB + q - G::DA) * 1024), db.off[q - G::DA] + (uint32_t)kt * db.kstep);
+        const uint32_t kg = (uint32_t)(kt0 + kt);
+        if (q < G::DA) dma16(ra, slot + (uint32_t)((wave * G::DA + q) * 1024), da.off[q] + kg * da.kstep);
+        else dma16(rb, slot + D_OPB + (uint32_t)((wave * G::DB + q - G::DA) * 1024), db.off[q - G::DA] + kg * db.kstep);
     };
 
     f32x4 acc[D_FM][D_FN];
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
         for (int j = 0; j < D_FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     u32x4 fa[2][D_FM], fb[2][D_FN];
-    const int nk = p.K / D_BK;
+    const int nk = (p.split > 1 ? min(p.k_chunk, p.K - (int)blockIdx.z * p.k_chunk) : p.K) / D_BK;
     // prologue: stages 0..3 in flight; stage 0's fragments in registers once it
     // has landed, stage 1 landed before the loop reads it
 #pragma unroll
@@ -231,6 +234,25 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     // loads of stages past the end are still in flight: drain them before
     // the workgroup's LDS can be handed to another
     wait_vmcnt<0>();
+
+    if (p.split > 1) {
+        // float32 partials part[z][batch][M][N] straight from the accumulators
+        // (lane l: column l % 16, register r: row (l / 16) * 4 + r)
+        float* part = p.part + ((int64_t)blockIdx.z * p.batch + b) * p.M * p.N;
+#pragma unroll
+        for (int i = 0; i < D_FM; ++i)
+#pragma unroll
+            for (int j = 0; j < D_FN; ++j) {
+                const int col = n0 + wn * D_WTN + j * 16 + lane % 16;
+                if (col >= p.N) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = m0 + wm * D_WTM + i * 16 + (lane / 16) * 4 + r;
+                    if (row < p.M) part[(int64_t)row * p.N + col] = acc[i][j][r];
+                }
+            }
+        return;
+    }
 
     __syncthreads();   // every wave is done with the ring: it now holds the output tile
 
@@ -356,7 +378,7 @@ template <int DT, int BM, int BN>
 void launch_dma_tile(GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s) {
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (p.N + BN - 1) / BN;
-    const dim3 grid(p.tiles_m * p.tiles_n, p.batch), block(DCfg<BM, BN>::NT);
+    const dim3 grid(p.tiles_m * p.tiles_n, p.batch, p.split > 1 ? p.split : 1), block(DCfg<BM, BN>::NT);
     if (a_kmajor && b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, true, BM, BN>), grid, block, 0, s, p);
     else if (a_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, false, BM, BN>), grid, block, 0, s, p);
     else if (b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, true, BM, BN>), grid, block, 0, s, p);
