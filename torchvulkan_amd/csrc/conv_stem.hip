@@ -176,6 +176,100 @@ __global__ __launch_bounds__(256) void conv_small_fwd_kernel(SmallArgs p) {
     }
 }
 
+// Forward, stride 1, dilation 1, output width Wo in 8..256 dividing 256: a
+// workgroup computes TR = 256 / Wo whole output rows of one image x 64
+// output channels. The input rows it reads (with zeros for the padding) and
+// the weight block go to LDS with coalesced loads first, so the patch gather
+// is 8 LDS reads a fragment and needs no bounds checks. LDS: x as
+// [c][TR + kh - 1][W + 16] (image column iw at iw + 8), weights as [64][40]
+// (80-byte rows: the 16 lanes of a fragment read hit distinct banks).
+template <int DT>
+__global__ __launch_bounds__(256) void conv_small_fwd_rows_kernel(SmallArgs p) {
+    typedef typename elem<DT>::T T;
+    constexpr int LROW = 256 + 8, WROW = 40;
+    __shared__ int ktab[32];
+    __shared__ __attribute__((aligned(16))) uint16_t ws[64 * WROW];
+    __shared__ __attribute__((aligned(16))) uint16_t xs[8192];
+    __shared__ __attribute__((aligned(16))) uint16_t tile[64 * LROW];
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, sl = lane % 16;
+    const int TR = 256 / p.Wo;
+    const int rt = blockIdx.x % p.row_blocks, img = blockIdx.x / p.row_blocks;
+    const int h0 = rt * TR, n0 = blockIdx.y * 64;
+    const int HR = TR + p.kh - 1, RP = p.W + 16, taps = p.kh * p.kw;
+    const uint16_t* x = static_cast<const uint16_t*>(p.x) + (int64_t)img * p.cin * p.H * p.W;
+    const uint16_t* w = static_cast<const uint16_t*>(p.w);
+    // k -> LDS offset of (c, a, b) from the pixel's row-0 column-0 slot; -1 past K
+    if (tid < 32) {
+        const int k = tid;
+        if (k < p.K) {
+            const int c = k / taps, t = k - c * taps, a = t / p.kw, b = t - a * p.kw;
+            ktab[k] = (c * HR + a) * RP + b - p.pw + 8;
+        } else {
+            ktab[k] = -1;
+        }
+    }
+    for (int e = tid; e < 64 * 32; e += 256) {
+        const int co = e / 32, k = e % 32;
+        ws[co * WROW + k] = (n0 + co < p.cout && k < p.K) ? w[(n0 + co) * p.K + k] : (uint16_t)0;
+    }
+    for (int e = tid; e < p.cin * HR * RP; e += 256) {
+        const int col = e % RP, rest = e / RP;
+        const int hr = rest % HR, c = rest / HR;
+        const int ih = h0 - p.ph + hr, iw = col - 8;
+        xs[e] = ((unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W) ? x[((int64_t)c * p.H + ih) * p.W + iw] : (uint16_t)0;
+    }
+    __syncthreads();
+    int ko[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ko[e] = ktab[g * 8 + e];
+    u32x4 fb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fb[j] = *reinterpret_cast<const u32x4*>(ws + (j * 16 + sl) * WROW + g * 8);
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = wave * 64 + i * 16 + sl;
+        const int base = (q / p.Wo) * RP + q % p.Wo;
+        uint16_t v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = ko[e] >= 0 ? xs[base + ko[e]] : (uint16_t)0;
+        const u32x4 fa = pack8(v);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<DT>(fa, fb[j], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ch = j * 16 + sl;
+        float bv = 0.0f;
+        if (p.has_bias && n0 + ch < p.cout) bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[n0 + ch]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint16_t h[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[i][j][r];
+                if (p.has_bias) {
+#pragma clang fp contract(off)
+                    v = v + bv;
+                }
+                h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
+            }
+            const int px = wave * 64 + i * 16 + g * 4;
+            *reinterpret_cast<u32x2*>(tile + ch * LROW + px) = u32x2{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
+        }
+    }
+    __syncthreads();
+    // the tile's 256 pixels are contiguous in each output plane (whole rows)
+    uint16_t* y = static_cast<uint16_t*>(p.out);
+    const int HWo = p.Ho * p.Wo, pix0 = h0 * p.Wo;
+    for (int idx = tid; idx < 64 * 32; idx += 256) {
+        const int ch = idx / 32, pc = idx % 32;
+        if (n0 + ch >= p.cout || pix0 + pc * 8 >= HWo) continue;
+        *reinterpret_cast<u32x4*>(y + ((int64_t)img * p.cout + n0 + ch) * HWo + pix0 + pc * 8) =
+            *reinterpret_cast<const u32x4*>(tile + ch * LROW + pc * 8);
+    }
+}
+
 // Grad weight: workgroup b sums pixel chunks b, b + split, ... of 512 pixels
 // (4 waves x 4 steps of 32, each wave its own 128 pixels), for 64 output
 // channels (grid y) x the 32 (zero-padded) k. Ho * Wo % 8 == 0 so a lane's 8
@@ -388,6 +482,17 @@ SmallArgs small_args(const tvk_conv_desc& d) {
     return p;
 }
 
+// forward by whole output rows: stride 1, dilation 1, Wo a power of two in
+// 8..256, the padding inside the 8 spare columns each side of a staged row,
+// and the staged rows within 16 KB
+bool fwd_rows_applies(const tvk_conv_desc& d) {
+    if (d.stride[0] != 1 || d.stride[1] != 1 || d.dilation[0] != 1 || d.dilation[1] != 1) return false;
+    const int64_t wo = d.w_out;
+    if (wo < 8 || wo > 256 || (wo & (wo - 1)) != 0 || !al16(d.y)) return false;
+    if (d.padding[1] > 8 || wo - 1 + d.kw - 1 - d.padding[1] >= d.w + 8) return false;
+    return d.c_in * (256 / wo + d.kh - 1) * (d.w + 16) <= 8192;
+}
+
 // grad input tile: rows per workgroup and the halo it stages
 void dgrad_tile(const tvk_conv_desc& d, int& tr, int& hr, int& hc) {
     tr = std::max<int>(1, 256 / (int)d.w);
@@ -424,9 +529,16 @@ tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who) {
         p.M = p.n * p.Ho * p.Wo;
         p.has_bias = d.bias ? 1 : 0;
         p.vec_out = (p.Ho * p.Wo) % 8 == 0 && al16(d.y);
-        const dim3 grid((unsigned)((p.M + 255) / 256), (unsigned)((p.cout + 63) / 64));
-        if (f16) hipLaunchKernelGGL(conv_small_fwd_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL(conv_small_fwd_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
+        if (fwd_rows_applies(d)) {
+            p.row_blocks = (p.Ho + 256 / p.Wo - 1) / (256 / p.Wo);
+            const dim3 grid((unsigned)(p.n * p.row_blocks), (unsigned)((p.cout + 63) / 64));
+            if (f16) hipLaunchKernelGGL(conv_small_fwd_rows_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
+            else hipLaunchKernelGGL(conv_small_fwd_rows_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
+        } else {
+            const dim3 grid((unsigned)((p.M + 255) / 256), (unsigned)((p.cout + 63) / 64));
+            if (f16) hipLaunchKernelGGL(conv_small_fwd_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
+            else hipLaunchKernelGGL(conv_small_fwd_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
+        }
     } else if (mode == 2) {
         const int64_t P = (int64_t)p.n * p.Ho * p.Wo;
         const int ny = (p.cout + 63) / 64;
