@@ -187,6 +187,22 @@ HALO_CASES = [
     dict(n=3, cin=64, cout=32, k=3, s=1, p=1, hw=(8, 32)),
 ]
 
+# 1x1 grad weight from NCHW (stride 1 or 2, 64-channel input blocks): a partial
+# output-channel block, two input blocks, stride 1, non-square images
+POINT_CASES = [
+    dict(n=2, cin=64, cout=40, k=1, s=2, p=0, hw=(16, 32)),
+    dict(n=3, cin=128, cout=96, k=1, s=1, p=0, hw=(4, 16)),
+    dict(n=1, cin=64, cout=64, k=1, s=2, p=0, hw=(8, 16)),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", POINT_CASES)
+def test_pointwise_grad_weight(gpu, dtype, case):
+    case = dict(case)
+    _check_all_directions(gpu, dtype, case.pop("n"), case.pop("cin"), case.pop("cout"), case.pop("k"),
+                          case.pop("s"), case.pop("p"), case.pop("hw"), seed=70, **case)
+
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("case", HALO_CASES)

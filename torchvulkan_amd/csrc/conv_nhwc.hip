@@ -990,6 +990,78 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
     }
 }
 
+// Grad weight of a 1x1 convolution with stride 1 or 2 and no padding,
+// straight from NCHW without LDS: dW[co][c] = sum_p x[c][s*p] * dy[co][p].
+// The output pixels are the reduction, 32 a step (4 groups of 8 in one output
+// row: Wo % 8 == 0, Ho * Wo % 32 == 0). A lane's A fragment is 8 consecutive
+// pixels of one input channel: one 16-byte load at stride 1, or two and the
+// even elements at stride 2; its B fragment is 8 pixels of one output channel,
+// one 16-byte load. Workgroup = 64 input x 64 output channels; its 4 waves
+// take alternate steps of the workgroup's pixel range and add their sums in
+// wave order through LDS into float32 partials [split][c][co].
+struct PointWgArgs {
+    const uint16_t* x;     // [n][cin][H][W]
+    const uint16_t* dy;    // [n][cout][Ho][Wo]
+    float* part;
+    int cin, cout, H, W, Ho, Wo, stride;
+    int steps, steps_per_split, split;   // 32-pixel steps in all; per workgroup
+};
+
+template <int DT, int S>
+__global__ __launch_bounds__(256) void conv1x1_wgrad_kernel(PointWgArgs p) {
+    __shared__ float red[4][64 * 65];
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, sl = lane % 16;
+    const int c0 = blockIdx.y * 64, n0 = blockIdx.z * 64;
+    const int HWo = p.Ho * p.Wo, HW = p.H * p.W;
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int s0 = blockIdx.x * p.steps_per_split, s1 = min(s0 + p.steps_per_split, p.steps);
+#pragma unroll 2
+    for (int st = s0 + wave; st < s1; st += 4) {
+        const int px = st * 32 + g * 8;                 // first of this lane's 8 output pixels
+        const int img = px / HWo, o = px - img * HWo;
+        const int oh = o / p.Wo, ow = o - oh * p.Wo;
+        const uint16_t* xr = p.x + ((int64_t)img * p.cin + c0 + sl) * HW + (int64_t)oh * S * p.W + ow * S;
+        const uint16_t* dr = p.dy + (int64_t)img * p.cout * HWo + o;
+        u32x4 fa[4], fb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint16_t* q = xr + (int64_t)i * 16 * HW;
+            if constexpr (S == 1) {
+                fa[i] = *reinterpret_cast<const u32x4*>(q);
+            } else {
+                const u32x4 lo = *reinterpret_cast<const u32x4*>(q), hi = *reinterpret_cast<const u32x4*>(q + 8);
+                fa[i] = u32x4{(lo.x & 0xffffu) | (lo.y << 16), (lo.z & 0xffffu) | (lo.w << 16),
+                              (hi.x & 0xffffu) | (hi.y << 16), (hi.z & 0xffffu) | (hi.w << 16)};
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fb[j] = *reinterpret_cast<const u32x4*>(dr + (int64_t)min(n0 + j * 16 + sl, p.cout - 1) * HWo);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
+    }
+    // rows = input channels (i * 16 + g * 4 + r), columns = output channels (j * 16 + sl)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][(i * 16 + g * 4 + r) * 65 + j * 16 + sl] = acc[i][j][r];
+    __syncthreads();
+    float* part = p.part + (int64_t)blockIdx.x * p.cin * p.cout;
+    for (int e = tid; e < 64 * 64; e += 256) {
+        const int cl = e / 64, col = e % 64;
+        if (n0 + col >= p.cout) continue;
+        const int at = cl * 65 + col;
+        part[(int64_t)(c0 + cl) * p.cout + n0 + col] = ((red[0][at] + red[1][at]) + red[2][at]) + red[3][at];
+    }
+}
+
 }  // namespace
 
 // mode: 0 forward, 1 grad input, 2 grad weight
@@ -1210,7 +1282,11 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
 // stride 1, 3x3, padding 1, dilation 1. Forward / grad input: the gathered
 // side in whole 32-channel chunks, widths 8, 16, 32 or 64. Grad weight: input
 // channels in 64-channel blocks, widths 16 or 32 with whole 256-pixel tiles.
+bool conv1x1_wgrad_applies(const tvk_conv_desc& d);
+tvk_status conv1x1_wgrad_run(const tvk_conv_desc& d, const char* who);
+
 bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
+    if (mode == 2 && conv1x1_wgrad_applies(d)) return true;
     if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return false;
     if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return false;
     if (d.kh != 3 || d.kw != 3 || d.stride[0] != 1 || d.stride[1] != 1 || d.dilation[0] != 1 || d.dilation[1] != 1) return false;
@@ -1225,6 +1301,61 @@ bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
     if (!al16(d.x) || !al16(d.y) || !al16(d.weight)) return false;
     const int64_t big = std::max({d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h * d.w, d.c_out * d.c_in * 9});
     return big < (int64_t(1) << 30);
+}
+
+// 1x1 grad weight from NCHW: stride 1 or 2 on both axes, no padding, input
+// channels in 64-channel blocks, output rows in 8-pixel groups of 32-pixel steps
+bool conv1x1_wgrad_applies(const tvk_conv_desc& d) {
+    if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return false;
+    if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return false;
+    if (d.kh != 1 || d.kw != 1 || d.padding[0] != 0 || d.padding[1] != 0) return false;
+    if (d.stride[0] != d.stride[1] || (d.stride[0] != 1 && d.stride[0] != 2)) return false;
+    if (d.c_in % 64 != 0 || d.w_out % 8 != 0 || (d.h_out * d.w_out) % 32 != 0) return false;
+    // 16-byte loads: rows and planes of x and dy start 16-byte aligned
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!al16(d.x) || !al16(d.y) || d.w % 8 != 0) return false;
+    // the stride-2 pair of loads reads 16 input pixels from column 2 * ow: inside the row
+    if (d.stride[1] == 2 && 2 * d.w_out > d.w) return false;
+    return std::max(d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h_out * d.w_out) < (int64_t(1) << 30);
+}
+
+tvk_status conv1x1_wgrad_run(const tvk_conv_desc& d, const char* who) {
+    hipStream_t s = resolve_stream(d.stream);
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    PointWgArgs p;
+    memset(&p, 0, sizeof(p));
+    p.x = static_cast<const uint16_t*>(d.x);
+    p.dy = static_cast<const uint16_t*>(d.y);
+    p.cin = (int)d.c_in; p.cout = (int)d.c_out; p.H = (int)d.h; p.W = (int)d.w;
+    p.Ho = (int)d.h_out; p.Wo = (int)d.w_out; p.stride = (int)d.stride[0];
+    p.steps = (int)(d.n * p.Ho * p.Wo / 32);
+    const int cb = p.cin / 64, nb = (p.cout + 63) / 64;
+    // about 256 workgroups, at least 8 steps (two a wave) each
+    p.split = std::max(1, std::min(p.steps / 8, 256 / (cb * nb)));
+    p.steps_per_split = (p.steps + p.split - 1) / p.split;
+    p.split = (p.steps + p.steps_per_split - 1) / p.steps_per_split;
+    const size_t part_b = (size_t)p.split * p.cin * p.cout * sizeof(float);
+    p.part = static_cast<float*>(device_workspace(dev, part_b));
+    if (!p.part) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
+    const dim3 grid((unsigned)p.split, (unsigned)cb, (unsigned)nb);
+    const bool f16 = d.dtype == TVK_F16;
+    if (p.stride == 1) {
+        if (f16) hipLaunchKernelGGL((conv1x1_wgrad_kernel<TVK_F16, 1>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((conv1x1_wgrad_kernel<TVK_BF16, 1>), grid, dim3(256), 0, s, p);
+    } else {
+        if (f16) hipLaunchKernelGGL((conv1x1_wgrad_kernel<TVK_F16, 2>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((conv1x1_wgrad_kernel<TVK_BF16, 2>), grid, dim3(256), 0, s, p);
+    }
+    const int total = p.cin * p.cout;
+    int sg = 1;
+    while (sg < 16 && sg * 2 <= p.split && (int64_t)total * sg / 1024 < 1024) sg *= 2;
+    const dim3 rgrid((unsigned)((total + 1024 / sg - 1) / (1024 / sg)));
+    if (f16) hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_F16>, rgrid, dim3(256), 0, s, p.part, d.weight, p.cin, p.cout, p.cin, 1, p.split, sg);
+    else hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_BF16>, rgrid, dim3(256), 0, s, p.part, d.weight, p.cin, p.cout, p.cin, 1, p.split, sg);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
+    return TVK_OK;
 }
 
 tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
@@ -1269,7 +1400,7 @@ tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
 }
 
 tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
-    if (mode == 2) return conv_halo_wgrad_run(d, who);
+    if (mode == 2) return conv1x1_wgrad_applies(d) ? conv1x1_wgrad_run(d, who) : conv_halo_wgrad_run(d, who);
     const int cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
     const int Cs = mode == 0 ? cin : cout, N = mode == 0 ? cout : cin;
     hipStream_t s = resolve_stream(d.stream);
