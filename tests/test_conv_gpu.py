@@ -187,12 +187,15 @@ HALO_CASES = [
     dict(n=3, cin=64, cout=32, k=3, s=1, p=1, hw=(8, 32)),
 ]
 
-# 1x1 grad weight from NCHW (stride 1 or 2, 64-channel input blocks): a partial
-# output-channel block, two input blocks, stride 1, non-square images
+# 1x1 kernels from NCHW (stride 1 or 2, no padding). Grad weight (64-channel
+# input blocks): a partial output-channel block, two input blocks, stride 1,
+# non-square images. Forward (256- or 64-pixel tiles): both tile sizes, three
+# 32-channel k steps, a plane that takes neither tile (the ring kernel)
 POINT_CASES = [
     dict(n=2, cin=64, cout=40, k=1, s=2, p=0, hw=(16, 32)),
     dict(n=3, cin=128, cout=96, k=1, s=1, p=0, hw=(4, 16)),
     dict(n=1, cin=64, cout=64, k=1, s=2, p=0, hw=(8, 16)),
+    dict(n=2, cin=96, cout=64, k=1, s=1, p=0, hw=(16, 16)),
 ]
 
 

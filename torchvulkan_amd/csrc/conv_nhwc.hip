@@ -1062,6 +1062,113 @@ __global__ __launch_bounds__(256) void conv1x1_wgrad_kernel(PointWgArgs p) {
     }
 }
 
+// Forward of a 1x1 convolution with stride 1 or 2 and no padding, straight
+// from NCHW: a workgroup computes PT consecutive output pixels of one image
+// (whole 8-pixel groups of output rows) x 64 output channels. The input
+// pixels it reads (every channel) go to LDS once as [channel][PT pixels]
+// (one 16-byte load per 8 pixels, or two and their even elements at stride
+// 2; 16-byte chunks XOR-swizzled by (channel & 3) * 2) and the A fragments
+// (pixels x 32 channels) are transposed reads; the B fragments are 16-byte
+// loads of the weight rows. 4 waves of PT / 4 pixels; output through an LDS
+// tile into 16-byte NCHW stores.
+struct PointFwdArgs {
+    const uint16_t* x;     // [n][cin][H][W]
+    const uint16_t* w;     // [cout][cin]
+    const void* bias;
+    void* y;               // [n][cout][Ho][Wo]
+    int cin, cout, H, W, Ho, Wo, tiles_per_img, has_bias;
+};
+
+template <int DT, int S, int PT>
+__global__ __launch_bounds__(256) void conv1x1_fwd_kernel(PointFwdArgs p) {
+    typedef typename elem<DT>::T T;
+    constexpr int FM = PT / 64, RB = PT * 2, LROW = PT + 8;
+    __shared__ __attribute__((aligned(16))) char lds[32768 * 2];
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, sl = lane % 16;
+    const int img = blockIdx.x / p.tiles_per_img, t0 = (blockIdx.x - img * p.tiles_per_img) * PT;
+    const int n0 = blockIdx.y * 64;
+    const int HW = p.H * p.W, HWo = p.Ho * p.Wo;
+    // input tile: chunk q of channel row c holds output pixels t0 + 8q .. + 8
+    const uint16_t* xi = p.x + (int64_t)img * p.cin * HW;
+    for (int e = tid; e < p.cin * (PT / 8); e += 256) {
+        const int c = e / (PT / 8), q = e - c * (PT / 8);
+        const int o = t0 + q * 8, oh = o / p.Wo, ow = o - oh * p.Wo;
+        const uint16_t* src = xi + (int64_t)c * HW + (int64_t)oh * S * p.W + ow * S;
+        u32x4 v;
+        if constexpr (S == 1) {
+            v = *reinterpret_cast<const u32x4*>(src);
+        } else {
+            const u32x4 lo = *reinterpret_cast<const u32x4*>(src), hi = *reinterpret_cast<const u32x4*>(src + 8);
+            v = u32x4{(lo.x & 0xffffu) | (lo.y << 16), (lo.z & 0xffffu) | (lo.w << 16), (hi.x & 0xffffu) | (hi.y << 16),
+                      (hi.z & 0xffffu) | (hi.w << 16)};
+        }
+        *reinterpret_cast<u32x4*>(lds + c * RB + ((q ^ swz_mn(c)) * 16)) = v;
+    }
+    __syncthreads();
+    const uint32_t lbase = (uint32_t)(uintptr_t)(TVK_LDS char*)lds;
+    f32x4 acc[FM][4];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < p.cin; k0 += 32) {
+        u32x4 fb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int co = min(n0 + j * 16 + sl, p.cout - 1);
+            fb[j] = *reinterpret_cast<const u32x4*>(p.w + (int64_t)co * p.cin + k0 + g * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            // A: 16 pixels x 32 channels, transposed reads of channel rows k0 + (g * 8 + rr * 4 + sl / 4)
+            const int col = wave * (PT / 4) + i * 16 + (sl % 4) * 4;
+            u32x4 fa;
+#pragma unroll
+            for (int rr = 0; rr < 2; ++rr) {
+                const int kr = k0 + g * 8 + rr * 4 + sl / 4;
+                TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(lbase + kr * RB + (((col / 8) ^ swz_mn(kr)) * 16) + (col % 8) * 2);
+                const u32x2 w2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+                fa[rr * 2] = w2.x;
+                fa[rr * 2 + 1] = w2.y;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa, fb[j], acc[i][j]);
+        }
+    }
+    __syncthreads();
+    // [channel][pixel] tile, then 16-byte stores along the output plane
+    uint16_t* tile = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ch = j * 16 + sl;
+        float bv = 0.0f;
+        if (p.has_bias && n0 + ch < p.cout) bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[n0 + ch]);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            uint16_t h[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[i][j][r];
+                if (p.has_bias) {
+#pragma clang fp contract(off)
+                    v = v + bv;
+                }
+                h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
+            }
+            const int px = wave * (PT / 4) + i * 16 + g * 4;
+            *reinterpret_cast<u32x2*>(tile + ch * LROW + px) = u32x2{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
+        }
+    }
+    __syncthreads();
+    uint16_t* y = static_cast<uint16_t*>(p.y);
+    for (int idx = tid; idx < 64 * (PT / 8); idx += 256) {
+        const int ch = idx / (PT / 8), pc = idx % (PT / 8);
+        if (n0 + ch >= p.cout) continue;
+        *reinterpret_cast<u32x4*>(y + ((int64_t)img * p.cout + n0 + ch) * HWo + t0 + pc * 8) =
+            *reinterpret_cast<const u32x4*>(tile + ch * LROW + pc * 8);
+    }
+}
+
 }  // namespace
 
 // mode: 0 forward, 1 grad input, 2 grad weight
@@ -1285,8 +1392,57 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
 bool conv1x1_wgrad_applies(const tvk_conv_desc& d);
 tvk_status conv1x1_wgrad_run(const tvk_conv_desc& d, const char* who);
 
+// 1x1 forward from NCHW: stride 1 or 2, no padding, input channels in 32s, the
+// pixel tile (256 or 64 output pixels, whole 8-pixel row groups) and all its
+// input channels within 64 KB of LDS
+int conv1x1_fwd_tile(const tvk_conv_desc& d) {
+    if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return 0;
+    if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return 0;
+    if (d.kh != 1 || d.kw != 1 || d.padding[0] != 0 || d.padding[1] != 0) return 0;
+    if (d.stride[0] != d.stride[1] || (d.stride[0] != 1 && d.stride[0] != 2)) return 0;
+    if (d.c_in % 32 != 0 || d.w_out % 8 != 0 || d.w % 8 != 0) return 0;
+    if (d.stride[1] == 2 && 2 * d.w_out > d.w) return 0;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!al16(d.x) || !al16(d.y) || !al16(d.weight)) return 0;
+    if (std::max(d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h_out * d.w_out) >= (int64_t(1) << 30)) return 0;
+    const int64_t hwo = d.h_out * d.w_out;
+    const int pt = hwo % 256 == 0 ? 256 : hwo % 64 == 0 ? 64 : 0;
+    if (pt == 0 || d.c_in * pt > 32768) return 0;
+    return pt;
+}
+
+tvk_status conv1x1_fwd_run(const tvk_conv_desc& d, const char* who) {
+    const int pt = conv1x1_fwd_tile(d);
+    hipStream_t s = resolve_stream(d.stream);
+    PointFwdArgs p;
+    memset(&p, 0, sizeof(p));
+    p.x = static_cast<const uint16_t*>(d.x);
+    p.w = static_cast<const uint16_t*>(d.weight);
+    p.bias = d.bias;
+    p.has_bias = d.bias ? 1 : 0;
+    p.y = d.y;
+    p.cin = (int)d.c_in; p.cout = (int)d.c_out; p.H = (int)d.h; p.W = (int)d.w;
+    p.Ho = (int)d.h_out; p.Wo = (int)d.w_out;
+    p.tiles_per_img = (int)(d.h_out * d.w_out / pt);
+    const dim3 grid((unsigned)(d.n * p.tiles_per_img), (unsigned)((p.cout + 63) / 64));
+    const bool f16 = d.dtype == TVK_F16, s2 = d.stride[0] == 2;
+#define TVK_PF(DT_, S_, PT_) hipLaunchKernelGGL((conv1x1_fwd_kernel<DT_, S_, PT_>), grid, dim3(256), 0, s, p)
+    if (pt == 256) {
+        if (f16) { if (s2) TVK_PF(TVK_F16, 2, 256); else TVK_PF(TVK_F16, 1, 256); }
+        else { if (s2) TVK_PF(TVK_BF16, 2, 256); else TVK_PF(TVK_BF16, 1, 256); }
+    } else {
+        if (f16) { if (s2) TVK_PF(TVK_F16, 2, 64); else TVK_PF(TVK_F16, 1, 64); }
+        else { if (s2) TVK_PF(TVK_BF16, 2, 64); else TVK_PF(TVK_BF16, 1, 64); }
+    }
+#undef TVK_PF
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
+    return TVK_OK;
+}
+
 bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
     if (mode == 2 && conv1x1_wgrad_applies(d)) return true;
+    if (mode == 0 && conv1x1_fwd_tile(d) != 0) return true;
     if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return false;
     if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return false;
     if (d.kh != 3 || d.kw != 3 || d.stride[0] != 1 || d.stride[1] != 1 || d.dilation[0] != 1 || d.dilation[1] != 1) return false;
@@ -1401,6 +1557,7 @@ tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
 
 tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     if (mode == 2) return conv1x1_wgrad_applies(d) ? conv1x1_wgrad_run(d, who) : conv_halo_wgrad_run(d, who);
+    if (mode == 0 && conv1x1_fwd_tile(d) != 0) return conv1x1_fwd_run(d, who);
     const int cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
     const int Cs = mode == 0 ? cin : cout, N = mode == 0 ? cout : cin;
     hipStream_t s = resolve_stream(d.stream);
