@@ -189,13 +189,15 @@ HALO_CASES = [
 
 # 1x1 kernels from NCHW (stride 1 or 2, no padding). Grad weight (64-channel
 # input blocks): a partial output-channel block, two input blocks, stride 1,
-# non-square images. Forward (256- or 64-pixel tiles): both tile sizes, three
-# 32-channel k steps, a plane that takes neither tile (the ring kernel)
+# non-square images. Forward and grad input (256- or 64-pixel tiles): both
+# tile sizes, three 32-channel k steps, a plane that takes neither tile (the
+# ring kernel), a partial 64-channel block of grad input at stride 2
 POINT_CASES = [
     dict(n=2, cin=64, cout=40, k=1, s=2, p=0, hw=(16, 32)),
     dict(n=3, cin=128, cout=96, k=1, s=1, p=0, hw=(4, 16)),
     dict(n=1, cin=64, cout=64, k=1, s=2, p=0, hw=(8, 16)),
     dict(n=2, cin=96, cout=64, k=1, s=1, p=0, hw=(16, 16)),
+    dict(n=2, cin=40, cout=64, k=1, s=2, p=0, hw=(16, 32)),
 ]
 
 

@@ -1169,6 +1169,112 @@ __global__ __launch_bounds__(256) void conv1x1_fwd_kernel(PointFwdArgs p) {
     }
 }
 
+// Grad input of the same 1x1 convolution: dx[c][s*p] = sum_co W[co][c] *
+// dy[co][p], zero at the pixels no output reaches (odd rows and columns at
+// stride 2). A workgroup takes PT consecutive dy pixels of one image (whole
+// 8-pixel row groups) x 64 input channels: dy[all co][PT] and W[all co][64]
+// go to LDS as k-rows (16-byte chunks XOR-swizzled by (row & 3) * 2), and
+// both fragments are transposed reads. Each 8-pixel dy group becomes 16
+// pixels of dx row s*oh (values and zeros interleaved at stride 2) and, at
+// stride 2, 16 zeros of row s*oh + 1: 16-byte stores.
+struct PointDgArgs {
+    const uint16_t* dy;    // [n][cout][Ho][Wo]
+    const uint16_t* w;     // [cout][cin]
+    void* dx;              // [n][cin][H][W]
+    int cin, cout, H, W, Ho, Wo, tiles_per_img;
+};
+
+template <int DT, int S, int PT>
+__global__ __launch_bounds__(256) void conv1x1_dgrad_kernel(PointDgArgs p) {
+    constexpr int FM = PT / 64, RB = PT * 2, LROW = PT + 8;
+    constexpr int DYB = PT == 256 ? 65536 : 32768;   // dy rows: up to 128 (PT 256) or 256 (PT 64) channels
+    __shared__ __attribute__((aligned(16))) char lds[DYB + 32768];
+    char* wl = lds + DYB;   // W[co][64 channels], 128-byte rows
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, sl = lane % 16;
+    const int img = blockIdx.x / p.tiles_per_img, t0 = (blockIdx.x - img * p.tiles_per_img) * PT;
+    const int c0 = blockIdx.y * 64;
+    const int HWo = p.Ho * p.Wo;
+    const uint16_t* dyi = p.dy + (int64_t)img * p.cout * HWo + t0;
+    for (int e = tid; e < p.cout * (PT / 8); e += 256) {
+        const int co = e / (PT / 8), q = e - co * (PT / 8);
+        *reinterpret_cast<u32x4*>(lds + co * RB + ((q ^ swz_mn(co)) * 16)) =
+            *reinterpret_cast<const u32x4*>(dyi + (int64_t)co * HWo + q * 8);
+    }
+    for (int e = tid; e < p.cout * 8; e += 256) {
+        const int co = e / 8, q = e % 8;
+        const int c = c0 + q * 8;
+        *reinterpret_cast<u32x4*>(wl + co * 128 + ((q ^ swz_mn(co)) * 16)) =
+            c + 8 <= p.cin ? *reinterpret_cast<const u32x4*>(p.w + (int64_t)co * p.cin + c) : u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+    const uint32_t lbase = (uint32_t)(uintptr_t)(TVK_LDS char*)lds, wbase = lbase + DYB;
+    auto tr = [&](uint32_t base, int rb, int kr, int col) {
+        TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(base + kr * rb + (((col / 8) ^ swz_mn(kr)) * 16) + (col % 8) * 2);
+        return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+    };
+    f32x4 acc[FM][4];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < p.cout; k0 += 32) {
+        u32x4 fb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int rr = 0; rr < 2; ++rr) {
+                const u32x2 v = tr(wbase, 128, k0 + g * 8 + rr * 4 + sl / 4, j * 16 + (sl % 4) * 4);
+                fb[j][rr * 2] = v.x;
+                fb[j][rr * 2 + 1] = v.y;
+            }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            u32x4 fa;
+#pragma unroll
+            for (int rr = 0; rr < 2; ++rr) {
+                const u32x2 v = tr(lbase, RB, k0 + g * 8 + rr * 4 + sl / 4, wave * (PT / 4) + i * 16 + (sl % 4) * 4);
+                fa[rr * 2] = v.x;
+                fa[rr * 2 + 1] = v.y;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa, fb[j], acc[i][j]);
+        }
+    }
+    __syncthreads();
+    uint16_t* tile = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ch = j * 16 + sl;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            uint16_t h[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(acc[i][j][r]));
+            const int px = wave * (PT / 4) + i * 16 + g * 4;
+            *reinterpret_cast<u32x2*>(tile + ch * LROW + px) = u32x2{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
+        }
+    }
+    __syncthreads();
+    uint16_t* dx = static_cast<uint16_t*>(p.dx);
+    for (int idx = tid; idx < 64 * (PT / 8); idx += 256) {
+        const int ch = idx / (PT / 8), pc = idx % (PT / 8);
+        if (c0 + ch >= p.cin) continue;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(tile + ch * LROW + pc * 8);
+        uint16_t* plane = dx + ((int64_t)img * p.cin + c0 + ch) * p.H * p.W;
+        const int o = t0 + pc * 8, oh = o / p.Wo, ow = o - oh * p.Wo;
+        if constexpr (S == 1) {
+            *reinterpret_cast<u32x4*>(plane + (int64_t)oh * p.W + ow) = v;
+        } else {
+            // values at even columns, zeros at odd ones; the row below is all zeros
+            uint16_t* row = plane + (int64_t)(2 * oh) * p.W + 2 * ow;
+            *reinterpret_cast<u32x4*>(row) = u32x4{v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16};
+            *reinterpret_cast<u32x4*>(row + 8) = u32x4{v.z & 0xffffu, v.z >> 16, v.w & 0xffffu, v.w >> 16};
+            *reinterpret_cast<u32x4*>(row + p.W) = u32x4{0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(row + p.W + 8) = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+}
+
 }  // namespace
 
 // mode: 0 forward, 1 grad input, 2 grad weight
@@ -1411,6 +1517,53 @@ int conv1x1_fwd_tile(const tvk_conv_desc& d) {
     return pt;
 }
 
+// 1x1 grad input from NCHW: stride 1 or 2 with dx exactly covered (W = s*Wo,
+// H = s*Ho), output channels in 32s, dy tile and the weight rows in LDS
+int conv1x1_dgrad_tile(const tvk_conv_desc& d) {
+    if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return 0;
+    if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return 0;
+    if (d.kh != 1 || d.kw != 1 || d.padding[0] != 0 || d.padding[1] != 0) return 0;
+    if (d.stride[0] != d.stride[1] || (d.stride[0] != 1 && d.stride[0] != 2)) return 0;
+    if (d.w != d.stride[1] * d.w_out || d.h != d.stride[0] * d.h_out) return 0;
+    if (d.c_out % 32 != 0 || d.c_in % 8 != 0 || d.w_out % 8 != 0) return 0;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!al16(d.x) || !al16(d.y) || !al16(d.weight)) return 0;
+    if (std::max(d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h_out * d.w_out) >= (int64_t(1) << 30)) return 0;
+    const int64_t hwo = d.h_out * d.w_out;
+    // 256-pixel tiles only where they still give a workgroup per CU
+    int pt = hwo % 64 == 0 ? 64 : 0;
+    if (hwo % 256 == 0 && d.n * (hwo / 256) * ((d.c_in + 63) / 64) >= 256) pt = 256;
+    if (pt == 0 || d.c_out * pt * 2 > (pt == 256 ? 65536 : 32768) || d.c_out * 128 > 32768) return 0;
+    return pt;
+}
+
+tvk_status conv1x1_dgrad_run(const tvk_conv_desc& d, const char* who) {
+    const int pt = conv1x1_dgrad_tile(d);
+    hipStream_t s = resolve_stream(d.stream);
+    PointDgArgs p;
+    memset(&p, 0, sizeof(p));
+    p.dy = static_cast<const uint16_t*>(d.y);
+    p.w = static_cast<const uint16_t*>(d.weight);
+    p.dx = d.x;
+    p.cin = (int)d.c_in; p.cout = (int)d.c_out; p.H = (int)d.h; p.W = (int)d.w;
+    p.Ho = (int)d.h_out; p.Wo = (int)d.w_out;
+    p.tiles_per_img = (int)(d.h_out * d.w_out / pt);
+    const dim3 grid((unsigned)(d.n * p.tiles_per_img), (unsigned)((p.cin + 63) / 64));
+    const bool f16 = d.dtype == TVK_F16, s2 = d.stride[0] == 2;
+#define TVK_PD(DT_, S_, PT_) hipLaunchKernelGGL((conv1x1_dgrad_kernel<DT_, S_, PT_>), grid, dim3(256), 0, s, p)
+    if (pt == 256) {
+        if (f16) { if (s2) TVK_PD(TVK_F16, 2, 256); else TVK_PD(TVK_F16, 1, 256); }
+        else { if (s2) TVK_PD(TVK_BF16, 2, 256); else TVK_PD(TVK_BF16, 1, 256); }
+    } else {
+        if (f16) { if (s2) TVK_PD(TVK_F16, 2, 64); else TVK_PD(TVK_F16, 1, 64); }
+        else { if (s2) TVK_PD(TVK_BF16, 2, 64); else TVK_PD(TVK_BF16, 1, 64); }
+    }
+#undef TVK_PD
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
+    return TVK_OK;
+}
+
 tvk_status conv1x1_fwd_run(const tvk_conv_desc& d, const char* who) {
     const int pt = conv1x1_fwd_tile(d);
     hipStream_t s = resolve_stream(d.stream);
@@ -1443,6 +1596,7 @@ tvk_status conv1x1_fwd_run(const tvk_conv_desc& d, const char* who) {
 bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
     if (mode == 2 && conv1x1_wgrad_applies(d)) return true;
     if (mode == 0 && conv1x1_fwd_tile(d) != 0) return true;
+    if (mode == 1 && conv1x1_dgrad_tile(d) != 0) return true;
     if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return false;
     if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return false;
     if (d.kh != 3 || d.kw != 3 || d.stride[0] != 1 || d.stride[1] != 1 || d.dilation[0] != 1 || d.dilation[1] != 1) return false;
@@ -1558,6 +1712,7 @@ tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
 tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     if (mode == 2) return conv1x1_wgrad_applies(d) ? conv1x1_wgrad_run(d, who) : conv_halo_wgrad_run(d, who);
     if (mode == 0 && conv1x1_fwd_tile(d) != 0) return conv1x1_fwd_run(d, who);
+    if (mode == 1 && conv1x1_dgrad_tile(d) != 0) return conv1x1_dgrad_run(d, who);
     const int cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
     const int Cs = mode == 0 ? cin : cout, N = mode == 0 ? cout : cin;
     hipStream_t s = resolve_stream(d.stream);
