@@ -802,6 +802,177 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
     }
 }
 
+// Stride-2 3x3 padding-1 forward from NCHW (W = 2 Wo, H = 2 Ho): the same
+// scheme as the stride-1 halo kernel on a 64 * FM output-pixel tile (TR x Wo)
+// x 64 output channels, 4 waves of 16 * FM pixels. The (2 TR + 1)-row input
+// halo is stored with its columns de-interleaved: column hc = iw + 1 goes to
+// slot hc / 2 when even and W / 2 + 1 + hc / 2 when odd, so the 16 output
+// pixels of a fragment read 16 consecutive slots for every tap (tap column b:
+// even slots from c + b / 2, odd slots from W / 2 + 1 + c).
+constexpr int H2_A = 38912;      // (2 TR + 1) x (W + 2) slots x 64 bytes <= 594 x 64, rounded up to 1 KB
+constexpr int H2_STAGE = H2_A + HL_B;
+
+template <int DT, int FM>
+__global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
+    constexpr int TPX = 64 * FM;
+    __shared__ __attribute__((aligned(1024))) char lds[2 * H2_STAGE];
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
+    const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64), g = lane / 16;
+    const int img = blockIdx.x / p.row_tiles, h0 = (blockIdx.x - img * p.row_tiles) * p.tr;   // output rows
+    const int n0 = blockIdx.y * HL_BN;
+    const int W = p.W, RP = W + 2, HWs = p.H * W, Wo = W / 2, Ho = p.H / 2;
+    const int HR = 2 * p.tr + 1, ODD = W / 2 + 1;
+    const int nk = p.Cs / 32;
+
+    // zero halo column hc = 0 (input column -1: even slot 0) of both stages
+    for (int e = tid; e < HR * 4; e += 256) {
+        const int hr = e / 4, ch = e % 4, hp = hr * RP;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+            *reinterpret_cast<u32x4*>(lds + st * H2_STAGE + hp * 64 + ch * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+
+    // halo gather: block b -> (column group wq, channel group cg, halo row hr); up to two a thread
+    const int nwq = W / 8, nblk = HR * nwq * 4;
+    u32x4 ar[2][8];
+    auto load_a = [&](int kc) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int b = tid + u * 256;
+            const int wq = b % nwq, cg = (b / nwq) % 4, hr = b / (nwq * 4);
+            const int ih = 2 * h0 - 1 + hr;
+            const bool row = b < nblk && ih >= 0 && ih < p.H;
+            const uint16_t* src = p.src + ((int64_t)img * p.Cs + kc * 32 + cg * 8) * HWs + (int64_t)(row ? ih : 0) * W + wq * 8;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                ar[u][i] = row ? *reinterpret_cast<const u32x4*>(src + (int64_t)i * HWs) : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto store_a = [&](int st) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int b = tid + u * 256;
+            if (b >= nblk) continue;
+            const int wq = b % nwq, cg = (b / nwq) % 4, hr = b / (nwq * 4);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                uint32_t v[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t lo = ar[u][2 * k][j / 2], hi = ar[u][2 * k + 1][j / 2];
+                    v[k] = (j % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+                }
+                const int hc = wq * 8 + j + 1;
+                const int hp = hr * RP + ((hc & 1) ? ODD + hc / 2 : hc / 2);
+                *reinterpret_cast<u32x4*>(lds + st * H2_STAGE + hp * 64 + ((cg ^ hl_swz(hp)) * 16)) = u32x4{v[0], v[1], v[2], v[3]};
+            }
+        }
+    };
+
+    // weight rows: 36 DMA instructions of 16 rows a chunk, 9 per wave; row = tap * 64 + channel
+    const i32x4 rb = v_rsrc(p.wt, p.wt_bytes);
+    int b_off[9];
+#pragma unroll
+    for (int q = 0; q < 9; ++q) {
+        const int row = (wave * 9 + q) * 16 + lane / 4;
+        const int t = row / HL_BN, co = min(n0 + row % HL_BN, p.N - 1);
+        b_off[q] = ((co * 9 + t) * p.Cs + (((lane % 4) ^ hl_swz(row)) * 8)) * 2;
+    }
+    auto issue_b = [&](int kc, int st) {
+        const uint32_t base = lds0 + (uint32_t)(st * H2_STAGE + H2_A);
+#pragma unroll
+        for (int q = 0; q < 9; ++q) v_dma16(rb, base + (uint32_t)((wave * 9 + q) * 1024), (uint32_t)(b_off[q] + kc * 64));
+    };
+
+    // A fragment rows: this wave's 16 * FM output pixels of the tile
+    int hp0[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int q = wave * 16 * FM + i * 16 + lane % 16;
+        const int r = q / Wo, c = q - r * Wo;
+        hp0[i] = 2 * r * RP + c;
+    }
+    f32x4 acc[FM][4];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    issue_b(0, 0);
+    load_a(0);
+    store_a(0);
+    v_wait<0>();
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+        const int cur = kc & 1;
+        if (kc + 1 < nk) {
+            issue_b(kc + 1, cur ^ 1);
+            load_a(kc + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const char* sa = lds + cur * H2_STAGE;
+        const char* sb = sa + H2_A;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) {
+            u32x4 fa[FM], fb[4];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int hp = hp0[i] + p.dtap[t];
+                fa[i] = *reinterpret_cast<const u32x4*>(sa + hp * 64 + ((g ^ hl_swz(hp)) * 16));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = t * HL_BN + j * 16 + lane % 16;
+                fb[j] = *reinterpret_cast<const u32x4*>(sb + row * 64 + ((g ^ hl_swz(row)) * 16));
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (kc + 1 < nk) store_a(cur ^ 1);
+        v_wait<0>();
+        __syncthreads();
+    }
+
+    // [channel][pixel] tile, then 16-byte stores along the output rows
+    typedef typename elem<DT>::T T;
+    constexpr int LROW = TPX + 8;
+    uint16_t* tile = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ch = j * 16 + lane % 16;
+        float bv = 0.0f;
+        if (p.has_bias && n0 + ch < p.N) bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[n0 + ch]);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            uint16_t h[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[i][j][r];
+                if (p.has_bias) {
+#pragma clang fp contract(off)
+                    v = v + bv;
+                }
+                h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
+            }
+            const int px = wave * 16 * FM + i * 16 + g * 4;
+            *reinterpret_cast<u32x2*>(tile + ch * LROW + px) = u32x2{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
+        }
+    }
+    __syncthreads();
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+    const int HWo = Ho * Wo;
+    for (int idx = tid; idx < HL_BN * (TPX / 8); idx += 256) {
+        const int ch = idx / (TPX / 8), px = (idx % (TPX / 8)) * 8;
+        const int r = px / Wo;
+        if (n0 + ch >= p.N || h0 + r >= Ho) continue;
+        *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + n0 + ch) * HWo + (int64_t)h0 * Wo + px) =
+            *reinterpret_cast<const u32x4*>(tile + ch * LROW + px);
+    }
+}
+
 // Grad weight of the same convolution (stride 1, 3x3, padding 1) from NCHW:
 // a workgroup takes 64 input channels x 64 output channels x all 9 taps and
 // sums its share of 256-pixel tiles (TR x W output rows of one image, H % TR
@@ -1593,7 +1764,23 @@ tvk_status conv1x1_fwd_run(const tvk_conv_desc& d, const char* who) {
     return TVK_OK;
 }
 
+// stride-2 3x3 padding-1 forward: W = 2 Wo in 16..64, H = 2 Ho, input channels in 32s
+int conv_halo_s2_fm(const tvk_conv_desc& d) {
+    if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return 0;
+    if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return 0;
+    if (d.kh != 3 || d.kw != 3 || d.stride[0] != 2 || d.stride[1] != 2 || d.dilation[0] != 1 || d.dilation[1] != 1) return 0;
+    if (d.padding[0] != 1 || d.padding[1] != 1 || d.c_in % 32 != 0) return 0;
+    if ((d.w != 16 && d.w != 32 && d.w != 64) || d.w != 2 * d.w_out || d.h != 2 * d.h_out) return 0;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!al16(d.x) || !al16(d.y) || !al16(d.weight)) return 0;
+    if (std::max({d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h_out * d.w_out, d.c_out * d.c_in * 9}) >= (int64_t(1) << 30)) return 0;
+    // 128-pixel tiles; smaller images (64-pixel tiles) measured no faster than the ring
+    // kernel and its channels-last copy, whose weight rows serve more pixels a workgroup
+    return d.h_out * d.w_out >= 128 ? 2 : 0;
+}
+
 bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
+    if (mode == 0 && conv_halo_s2_fm(d) != 0) return true;
     if (mode == 2 && conv1x1_wgrad_applies(d)) return true;
     if (mode == 0 && conv1x1_fwd_tile(d) != 0) return true;
     if (mode == 1 && conv1x1_dgrad_tile(d) != 0) return true;
@@ -1734,16 +1921,29 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     p.has_bias = (mode == 0 && d.bias) ? 1 : 0;
     p.out = mode == 0 ? d.y : d.x;
     p.Cs = Cs; p.N = N; p.H = H; p.W = W;
-    p.tr = HL_PX / W;
-    p.row_tiles = (H + p.tr - 1) / p.tr;
+    const int fm2 = mode == 0 ? conv_halo_s2_fm(d) : 0;
+    p.tr = fm2 ? 64 * fm2 / (W / 2) : HL_PX / W;
+    p.row_tiles = fm2 ? ((H / 2) + p.tr - 1) / p.tr : (H + p.tr - 1) / p.tr;
     p.wt_bytes = (int)wt_b;
-    // forward: tap (a, b) reads source (h + a - 1, w + b - 1); grad input: (h + 1 - a, w + 1 - b)
+    // forward: tap (a, b) reads source (h + a - 1, w + b - 1); grad input: (h + 1 - a, w + 1 - b);
+    // stride 2: halo row 2r + a, de-interleaved column slot (b == 1 ? W / 2 + 1 + c : c + b / 2)
     for (int t = 0; t < 9; ++t) {
         const int a = t / 3, b = t % 3;
-        const int ho = mode == 0 ? a - 1 : 1 - a, wo = mode == 0 ? b - 1 : 1 - b;
-        p.dtap[t] = ho * (W + 2) + wo;
+        if (fm2) {
+            p.dtap[t] = a * (W + 2) + (b == 1 ? W / 2 + 1 : b / 2);
+        } else {
+            const int ho = mode == 0 ? a - 1 : 1 - a, wo = mode == 0 ? b - 1 : 1 - b;
+            p.dtap[t] = ho * (W + 2) + wo;
+        }
     }
     const dim3 grid((unsigned)(d.n * p.row_tiles), (unsigned)((N + HL_BN - 1) / HL_BN));
+    if (fm2) {
+        if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_s2_kernel<TVK_F16, 2>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((conv_halo_s2_kernel<TVK_BF16, 2>), grid, dim3(256), 0, s, p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
+        return TVK_OK;
+    }
     if (d.dtype == TVK_F16) hipLaunchKernelGGL(conv_halo_kernel<TVK_F16>, grid, dim3(512), 0, s, p);
     else hipLaunchKernelGGL(conv_halo_kernel<TVK_BF16>, grid, dim3(512), 0, s, p);
     hipError_t e = hipGetLastError();
