@@ -1161,6 +1161,173 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
     }
 }
 
+// Grad weight of the stride-2 3x3 padding-1 convolution from NCHW (W = 2 Wo,
+// H = 2 Ho): a workgroup takes 32 input channels x 64 output channels x all 9
+// taps and sums its share of TPX-pixel output tiles (TR x Wo rows of one
+// image) into float32 partials [split][(tap, channel)][output channel]. LDS
+// per stage: the (2 TR + 1)-row x halo with de-interleaved columns (as the
+// stride-2 forward: tap column b of output pixel c is slot c + b / 2, or
+// W / 2 + 1 + c for b = 1), [slot][32 channels] 64-byte rows, so a transposed
+// read's 4 k-rows (output pixels) are 4 consecutive slots; dy as chunk-major
+// [TPX / 8][64 output channels][8 pixels]. The 18 row fragments (tap, 16
+// channels) go to 8 waves as w, w + 8, w + 16. A k step (32 output pixels)
+// moves every fragment address by the same slot count, an instruction offset.
+constexpr int HG2_A = 38912;   // (2 TR + 1) x (W + 2) slots x 64 bytes <= 594 x 64, rounded up to 1 KB
+constexpr int HG2_B = 16 * 1024;
+constexpr int HG2_STAGE = HG2_A + HG2_B;
+
+template <int DT, int WO, int TPX>
+__global__ __launch_bounds__(512) void conv_halo_wgrad_s2_kernel(HaloWgArgs p) {
+    constexpr int W = 2 * WO, RP = W + 2, ODD = WO + 1, TR = TPX / WO, HR = 2 * TR + 1;
+    constexpr int KS = TPX / 32, STEP = 2 * (32 / WO) * RP;   // k steps a tile; slots a k step
+    static_assert(TPX % WO == 0 && 32 % WO == 0 && HR * RP * 64 <= HG2_A, "halo layout");
+    __shared__ __attribute__((aligned(1024))) char lds[2 * HG2_STAGE];
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
+    const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int g = lane / 16, sl = lane % 16;
+    const int c0 = blockIdx.y * 32, n0 = blockIdx.z * 64;
+    const int HWs = p.H * W, HWo = (p.H / 2) * WO;
+    const int nrf = wave < 2 ? 3 : 2;   // row fragments wave + 8k
+
+    // zero slot 0 (input column -1) of every halo row, both stages
+    for (int e = tid; e < HR * 4; e += 512) {
+        const int hr = e / 4, ch = e % 4;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+            *reinterpret_cast<u32x4*>(lds + st * HG2_STAGE + hr * RP * 64 + ch * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+
+    // x halo gather: lane -> (column group wq, channel group cg of 8, halo row hr)
+    constexpr int NWQ = W / 8;
+    const int wq = tid % NWQ, cg = (tid / NWQ) % 4, hr = tid / (NWQ * 4);
+    const bool a_live = hr < HR;
+    u32x4 ar[8];
+    auto load_a = [&](int tile) {
+        const int img = tile / p.tiles_per_img, h0 = (tile - img * p.tiles_per_img) * TR;
+        const int ih = 2 * h0 - 1 + hr;
+        const bool row = a_live && ih >= 0 && ih < p.H;
+        const uint16_t* src = p.x + ((int64_t)img * p.cin + c0 + cg * 8) * HWs + (int64_t)(row ? ih : 0) * W + wq * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ar[i] = row ? *reinterpret_cast<const u32x4*>(src + (int64_t)i * HWs) : u32x4{0u, 0u, 0u, 0u};
+    };
+    auto store_a = [&](int st) {
+        if (!a_live) return;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t lo = ar[2 * k][j / 2], hi = ar[2 * k + 1][j / 2];
+                v[k] = (j % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+            }
+            const int hc = wq * 8 + j + 1;
+            const int slot = (hc & 1) ? ODD + hc / 2 : hc / 2;
+            *reinterpret_cast<u32x4*>(lds + st * HG2_STAGE + (hr * RP + slot) * 64 + cg * 16) = u32x4{v[0], v[1], v[2], v[3]};
+        }
+    };
+
+    // dy: DMA instruction wave + 8q loads output-pixel chunk wave + 8q: lane = output channel
+    const i32x4 rb = v_rsrc(p.dy, p.dy_bytes);
+    const uint32_t b_lane = (uint32_t)(min(n0 + lane, p.cout - 1) * HWo * 2);
+    auto issue_b = [&](int tile, int st) {
+        const int img = tile / p.tiles_per_img, h0 = (tile - img * p.tiles_per_img) * TR;
+        const uint32_t toff = (uint32_t)((((int64_t)img * p.cout) * HWo + (int64_t)h0 * WO) * 2);
+        const uint32_t base = lds0 + (uint32_t)(st * HG2_STAGE + HG2_A);
+#pragma unroll
+        for (int q = 0; q < TPX / 64; ++q) {
+            const int chunk = wave + 8 * q;
+            v_dma16(rb, base + (uint32_t)(chunk * 1024), b_lane + toff + (uint32_t)(chunk * 16));
+        }
+    };
+
+    // fragment offsets at k step 0: row fragment k = wave + 8k -> tap rf / 2, channels (rf % 2) * 16
+    int a_off[3][2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+        const int px = g * 8 + rr * 4 + sl / 4;
+        const int hb = 2 * (px / WO) * RP + px % WO;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int rf = min(wave + 8 * k, 17), t = rf / 2, a = t / 3, b = t % 3;
+            const int col = (rf % 2) * 16 + (sl % 4) * 4;
+            const int hp = hb + a * RP + (b == 1 ? ODD : b / 2);
+            a_off[k][rr] = hp * 64 + col * 2;
+        }
+    }
+    const int b_off = g * 1024 + sl * 16;
+
+    f32x4 acc[3][4];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    int tile = blockIdx.x;
+    if (tile < p.ntiles) {
+        issue_b(tile, 0);
+        load_a(tile);
+        store_a(0);
+    }
+    v_wait<0>();
+    __syncthreads();
+    for (int it = 0; tile < p.ntiles; ++it, tile += p.split) {
+        const int cur = it & 1;
+        const int next = tile + p.split;
+        if (next < p.ntiles) {
+            issue_b(next, cur ^ 1);
+            load_a(next);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const char* sa = lds + cur * HG2_STAGE;
+        const char* sb = sa + HG2_A + b_off;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u32x4 fa[3];
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                if (i == 2 && nrf == 2) break;
+#pragma unroll
+                for (int rr = 0; rr < 2; ++rr) {
+                    const char* ptr = sa + a_off[i][rr] + ks * STEP * 64;
+                    const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((TVK_LDS s16x4*)(uintptr_t)(TVK_LDS const char*)ptr));
+                    fa[i][rr * 2] = w.x;
+                    fa[i][rr * 2 + 1] = w.y;
+                }
+            }
+            u32x4 fb[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fb[j] = *reinterpret_cast<const u32x4*>(sb + ks * 4096 + j * 256);
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                if (i == 2 && nrf == 2) break;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (next < p.ntiles) store_a(cur ^ 1);
+        v_wait<0>();
+        __syncthreads();
+    }
+
+    float* part = p.part + (int64_t)blockIdx.x * 9 * p.cin * p.cout;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        if (i == 2 && nrf == 2) break;
+        const int rf = wave + 8 * i, t = rf / 2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int co = n0 + j * 16 + sl;
+            if (co >= p.cout) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int c = c0 + (rf % 2) * 16 + g * 4 + r;
+                part[((int64_t)t * p.cin + c) * p.cout + co] = acc[i][j][r];
+            }
+        }
+    }
+}
+
 // Grad weight of a 1x1 convolution with stride 1 or 2 and no padding,
 // straight from NCHW without LDS: dW[co][c] = sum_p x[c][s*p] * dy[co][p].
 // The output pixels are the reduction, 32 a step (4 groups of 8 in one output
@@ -1779,8 +1946,12 @@ int conv_halo_s2_fm(const tvk_conv_desc& d) {
     return d.h_out * d.w_out >= 128 ? 2 : 0;
 }
 
+int conv_halo_wgrad_s2_tpx(const tvk_conv_desc& d);
+tvk_status conv_halo_wgrad_s2_run(const tvk_conv_desc& d, const char* who);
+
 bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
     if (mode == 0 && conv_halo_s2_fm(d) != 0) return true;
+    if (mode == 2 && conv_halo_wgrad_s2_tpx(d) != 0) return true;
     if (mode == 2 && conv1x1_wgrad_applies(d)) return true;
     if (mode == 0 && conv1x1_fwd_tile(d) != 0) return true;
     if (mode == 1 && conv1x1_dgrad_tile(d) != 0) return true;
@@ -1855,6 +2026,65 @@ tvk_status conv1x1_wgrad_run(const tvk_conv_desc& d, const char* who) {
     return TVK_OK;
 }
 
+// stride-2 grad weight: W = 2 Wo with Wo in 8..32, H = 2 Ho, output tiles of
+// 128 pixels (64 when Wo = 8), whole tiles per image, input channels in 32s
+int conv_halo_wgrad_s2_tpx(const tvk_conv_desc& d) {
+    if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return 0;
+    if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return 0;
+    if (d.kh != 3 || d.kw != 3 || d.stride[0] != 2 || d.stride[1] != 2 || d.dilation[0] != 1 || d.dilation[1] != 1) return 0;
+    if (d.padding[0] != 1 || d.padding[1] != 1 || d.c_in % 32 != 0) return 0;
+    if ((d.w_out != 8 && d.w_out != 16 && d.w_out != 32) || d.w != 2 * d.w_out || d.h != 2 * d.h_out) return 0;
+    const int tpx = d.w_out == 8 ? 64 : 128;
+    if ((d.h_out * d.w_out) % tpx != 0) return 0;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!al16(d.x) || !al16(d.y)) return 0;
+    if (std::max(d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h_out * d.w_out) >= (int64_t(1) << 30)) return 0;
+    return tpx;
+}
+
+tvk_status conv_halo_wgrad_s2_run(const tvk_conv_desc& d, const char* who) {
+    const int cin = (int)d.c_in, cout = (int)d.c_out, Wo = (int)d.w_out;
+    const int tpx = conv_halo_wgrad_s2_tpx(d);
+    hipStream_t s = resolve_stream(d.stream);
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    HaloWgArgs p;
+    memset(&p, 0, sizeof(p));
+    p.x = static_cast<const uint16_t*>(d.x);
+    p.dy = d.y;
+    p.cin = cin; p.cout = cout; p.H = (int)d.h;
+    p.tiles_per_img = (int)(d.h_out * d.w_out / tpx);
+    p.ntiles = (int)d.n * p.tiles_per_img;
+    p.dy_bytes = (int)(d.n * cout * d.h_out * d.w_out * 2);
+    const int cb = cin / 32, nb = (cout + 63) / 64;
+    // about 256 workgroups, each summing at least 2 tiles
+    p.split = std::max(1, std::min(p.ntiles / 2, 256 / (cb * nb)));
+    const size_t part_b = (size_t)p.split * 9 * cin * cout * sizeof(float);
+    char* ws = static_cast<char*>(device_workspace(dev, part_b));
+    if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
+    p.part = reinterpret_cast<float*>(ws);
+    const dim3 grid((unsigned)p.split, (unsigned)cb, (unsigned)nb);
+    const bool f16 = d.dtype == TVK_F16;
+#define TVK_HW2(WO_, TPX_)                                                                                           \
+    do {                                                                                                             \
+        if (f16) hipLaunchKernelGGL((conv_halo_wgrad_s2_kernel<TVK_F16, WO_, TPX_>), grid, dim3(512), 0, s, p);     \
+        else hipLaunchKernelGGL((conv_halo_wgrad_s2_kernel<TVK_BF16, WO_, TPX_>), grid, dim3(512), 0, s, p);        \
+    } while (0)
+    if (Wo == 8) TVK_HW2(8, 64);
+    else if (Wo == 16) TVK_HW2(16, 128);
+    else TVK_HW2(32, 128);
+#undef TVK_HW2
+    const int M = 9 * cin, total = M * cout;
+    int sg = 1;
+    while (sg < 16 && sg * 2 <= p.split && (int64_t)total * sg / 1024 < 1024) sg *= 2;
+    const dim3 rgrid((unsigned)((total + 1024 / sg - 1) / (1024 / sg)));
+    if (f16) hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_F16>, rgrid, dim3(256), 0, s, p.part, d.weight, M, cout, cin, 9, p.split, sg);
+    else hipLaunchKernelGGL(wgrad_ring_reduce_kernel<TVK_BF16>, rgrid, dim3(256), 0, s, p.part, d.weight, M, cout, cin, 9, p.split, sg);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
+    return TVK_OK;
+}
+
 tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
     const int cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
     hipStream_t s = resolve_stream(d.stream);
@@ -1897,7 +2127,11 @@ tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
 }
 
 tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
-    if (mode == 2) return conv1x1_wgrad_applies(d) ? conv1x1_wgrad_run(d, who) : conv_halo_wgrad_run(d, who);
+    if (mode == 2) {
+        if (conv1x1_wgrad_applies(d)) return conv1x1_wgrad_run(d, who);
+        if (conv_halo_wgrad_s2_tpx(d) != 0) return conv_halo_wgrad_s2_run(d, who);
+        return conv_halo_wgrad_run(d, who);
+    }
     if (mode == 0 && conv1x1_fwd_tile(d) != 0) return conv1x1_fwd_run(d, who);
     if (mode == 1 && conv1x1_dgrad_tile(d) != 0) return conv1x1_dgrad_run(d, who);
     const int cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
