@@ -192,6 +192,13 @@ HALO_CASES = [
     dict(n=1, cin=64, cout=64, k=3, s=2, p=1, hw=(12, 64)),
     dict(n=3, cin=96, cout=32, k=3, s=2, p=1, hw=(16, 32)),
     dict(n=3, cin=96, cout=32, k=3, s=2, p=1, hw=(8, 32)),
+    # stride-2 grad input by phases: 128-position tiles of one image (rows of
+    # 16 and 32 dy columns) and of two images with the batch's last tile half
+    # empty; 64-position tiles holding two images of an odd batch
+    dict(n=256, cin=64, cout=32, k=3, s=2, p=1, hw=(32, 32), sample_n=4),
+    dict(n=32, cin=32, cout=32, k=3, s=2, p=1, hw=(64, 64), sample_n=3),
+    dict(n=511, cin=64, cout=32, k=3, s=2, p=1, hw=(16, 16)),
+    dict(n=5, cin=32, cout=64, k=3, s=2, p=1, hw=(8, 16)),
 ]
 
 # 1x1 kernels from NCHW (stride 1 or 2, no padding). Grad weight (64-channel

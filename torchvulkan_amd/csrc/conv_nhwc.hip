@@ -623,6 +623,7 @@ struct HaloArgs {
     int dtap[9];           // halo pixel offset of each tap: hoff * (W + 2) + woff
     int has_bias;
     int wt_bytes;
+    int ipt, nimg;         // stride-2 grad input: images a tile, batch size
 };
 
 __device__ inline int hl_swz(int row) { return (row >> 2) & 3; }
@@ -969,6 +970,177 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
         const int r = px / Wo;
         if (n0 + ch >= p.N || h0 + r >= Ho) continue;
         *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + n0 + ch) * HWo + (int64_t)h0 * Wo + px) =
+            *reinterpret_cast<const u32x4*>(tile + ch * LROW + px);
+    }
+}
+
+// Stride-2 3x3 padding-1 grad input from NCHW dy (H = 2 Ho, W = 2 Wo). The
+// output splits by pixel parity into four phases (ph, pw) = (h % 2, w % 2):
+// dx(2i + ph, 2j + pw) sums the taps a with (ph + 1 - a) even, reading dy row
+// i + (ph + 1 - a) / 2, and likewise b for the columns, so the phases take 1,
+// 2, 2 and 4 of the 9 taps and no product is a zero of the strided grid. A
+// workgroup takes TP dy positions (ipt images x tr rows x Wo) x 64 input
+// channels. Its 8 waves take one phase and half of the positions each: waves
+// 0-1 phase (0,0), 2-3 (0,1), 4-5 (1,1), 6-7 (1,0), so waves w and w + 4,
+// which share a SIMD, run 5 or 4 taps between them. Per 32-channel chunk the
+// dy halo [ipt][tr + 1][Wo + 1] (the last row and column past the image are
+// zeros) is staged as in the stride-1 kernel, with the permuted weight rows.
+// ---------------------------------------------------------------------------
+constexpr int D2_A = 13312;   // ipt (tr + 1) (Wo + 1) pixels x 64 bytes: 3 x 65 at Wo = 64, 18 x 9 at Wo = 8
+constexpr int D2_STAGE = D2_A + HL_B;
+
+template <int DT, int TP>
+__global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
+    constexpr int FMW = TP / 32;   // A fragments a wave (TP / 2 positions)
+    constexpr int LROW = 4 * TP + 8;
+    static_assert(64 * LROW * 2 <= 2 * D2_STAGE, "output tile fits the stages");
+    __shared__ __attribute__((aligned(1024))) char lds[2 * D2_STAGE];
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
+    const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64), g = lane / 16;
+    const int Wo = p.W / 2, Ho = p.H / 2, TR = p.tr, RP = Wo + 1, HR = p.ipt * (TR + 1), HWo = Ho * Wo;
+    const int img0 = (blockIdx.x / p.row_tiles) * p.ipt, i0 = (blockIdx.x % p.row_tiles) * TR;
+    const int n0 = blockIdx.y * HL_BN;
+    const int nk = p.Cs / 32;
+
+    // zero halo column Wo of every row of both stages (no load writes it)
+    for (int e = tid; e < HR * 4; e += 512) {
+        const int hp = (e / 4) * RP + Wo, ch = e % 4;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+            *reinterpret_cast<u32x4*>(lds + st * D2_STAGE + hp * 64 + ch * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+
+    // halo gather: thread -> (column group wq, channel group cg, halo row hr
+    // = image k of the tile, row r); rows past the image or the batch load zeros
+    const int nwq = Wo / 8, nblk = HR * nwq * 4;
+    const int wq = tid % nwq, cg = (tid / nwq) % 4, hr = tid / (nwq * 4);
+    const int hk = hr / (TR + 1), hi = i0 + hr % (TR + 1);
+    const bool a_live = tid < nblk;
+    const bool a_row = a_live && hi < Ho && img0 + hk < p.nimg;
+    const uint16_t* a_src = p.src + ((int64_t)(a_row ? img0 + hk : 0) * p.Cs + cg * 8) * HWo + (int64_t)(a_row ? hi : 0) * Wo + wq * 8;
+    u32x4 ar[8];
+    auto load_a = [&](int kc) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            ar[i] = a_row ? *reinterpret_cast<const u32x4*>(a_src + (int64_t)(kc * 32 + i) * HWo) : u32x4{0u, 0u, 0u, 0u};
+    };
+    auto store_a = [&](int st) {
+        if (!a_live) return;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t lo = ar[2 * k][j / 2], hi2 = ar[2 * k + 1][j / 2];
+                v[k] = (j % 2 == 0) ? ((lo & 0xffffu) | (hi2 << 16)) : ((lo >> 16) | (hi2 & 0xffff0000u));
+            }
+            const int hp = hr * RP + wq * 8 + j;
+            *reinterpret_cast<u32x4*>(lds + st * D2_STAGE + hp * 64 + ((cg ^ hl_swz(hp)) * 16)) = u32x4{v[0], v[1], v[2], v[3]};
+        }
+    };
+
+    // weight rows: 36 DMA instructions of 16 rows a chunk, instruction q * 8 + wave
+    // (waves 0-3 issue 5, waves 4-7 issue 4); row = tap * 64 + channel
+    const i32x4 rb = v_rsrc(p.wt, p.wt_bytes);
+    int b_off[5];
+#pragma unroll
+    for (int q = 0; q < 5; ++q) {
+        const int row = min(q * 8 + wave, 35) * 16 + lane / 4;
+        const int t = row / HL_BN, co = min(n0 + row % HL_BN, p.N - 1);
+        b_off[q] = ((co * 9 + t) * p.Cs + (((lane % 4) ^ hl_swz(row)) * 8)) * 2;
+    }
+    auto issue_b = [&](int kc, int st) {
+        const uint32_t base = lds0 + (uint32_t)(st * D2_STAGE + D2_A);
+#pragma unroll
+        for (int q = 0; q < 5; ++q)
+            if (q * 8 + wave < 36) v_dma16(rb, base + (uint32_t)((q * 8 + wave) * 1024), (uint32_t)(b_off[q] + kc * 64));
+    };
+
+    // this wave's phase and positions: q = half * TP / 2 + i * 16 + lane % 16
+    const int ph = wave >= 4 ? 1 : 0, pw = (wave >= 2 && wave <= 5) ? 1 : 0, half = wave & 1;
+    const int ppi = TR * Wo;   // positions of one image in the tile
+    int hp0[FMW];
+#pragma unroll
+    for (int i = 0; i < FMW; ++i) {
+        const int q = half * (TP / 2) + i * 16 + lane % 16;
+        const int k = q / ppi, rem = q - k * ppi, r = rem / Wo, c = rem - r * Wo;
+        hp0[i] = (k * (TR + 1) + r) * RP + c;
+    }
+    f32x4 acc[FMW][4];
+#pragma unroll
+    for (int i = 0; i < FMW; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    issue_b(0, 0);
+    load_a(0);
+    store_a(0);
+    v_wait<0>();
+    __syncthreads();
+    const int na = ph ? 2 : 1, nb = pw ? 2 : 1;
+    for (int kc = 0; kc < nk; ++kc) {
+        const int cur = kc & 1;
+        if (kc + 1 < nk) {
+            issue_b(kc + 1, cur ^ 1);
+            load_a(kc + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const char* sa = lds + cur * D2_STAGE;
+        const char* sb = sa + D2_A;
+        for (int ta = 0; ta < na; ++ta) {
+            for (int tb = 0; tb < nb; ++tb) {
+                const int a = ph ? 2 * ta : 1, b = pw ? 2 * tb : 1;
+                const int off = ((ph + 1 - a) / 2) * RP + (pw + 1 - b) / 2, t = a * 3 + b;
+                u32x4 fa[FMW], fb[4];
+#pragma unroll
+                for (int i = 0; i < FMW; ++i) {
+                    const int hp = hp0[i] + off;
+                    fa[i] = *reinterpret_cast<const u32x4*>(sa + hp * 64 + ((g ^ hl_swz(hp)) * 16));
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int row = t * HL_BN + j * 16 + lane % 16;
+                    fb[j] = *reinterpret_cast<const u32x4*>(sb + row * 64 + ((g ^ hl_swz(row)) * 16));
+                }
+#pragma unroll
+                for (int i = 0; i < FMW; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (kc + 1 < nk) store_a(cur ^ 1);
+        v_wait<0>();
+        __syncthreads();
+    }
+
+    // [channel][dx pixel] tile over ipt x 2 tr x W pixels (the phases
+    // interleave along the rows), then 16-byte stores along the dx rows
+    typedef typename elem<DT>::T T;
+    uint16_t* tile = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+    for (int i = 0; i < FMW; ++i) {
+        // accumulator rows g * 4 + r: positions q0 .. q0 + 3 of one dy row (Wo % 8 == 0)
+        const int q0 = half * (TP / 2) + i * 16 + g * 4;
+        const int k = q0 / ppi, rem = q0 - k * ppi, r = rem / Wo, c = rem - r * Wo;
+        const int px0 = k * 4 * ppi + (2 * r + ph) * p.W + 2 * c + pw;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ch = j * 16 + lane % 16;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                tile[ch * LROW + px0 + 2 * rr] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(acc[i][j][rr]));
+        }
+    }
+    __syncthreads();
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+    const int HW = p.H * p.W;
+    for (int idx = tid; idx < HL_BN * (TP / 2); idx += 512) {
+        const int ch = idx / (TP / 2), px = (idx % (TP / 2)) * 8;
+        const int k = px / (4 * ppi), rem = px - k * 4 * ppi;
+        const int h = 2 * i0 + rem / p.W, w = rem % p.W;
+        if (n0 + ch >= p.N || img0 + k >= p.nimg || h >= p.H) continue;
+        *reinterpret_cast<u32x4*>(out + ((int64_t)(img0 + k) * p.N + n0 + ch) * HW + (int64_t)h * p.W + w) =
             *reinterpret_cast<const u32x4*>(tile + ch * LROW + px);
     }
 }
@@ -1946,11 +2118,42 @@ int conv_halo_s2_fm(const tvk_conv_desc& d) {
     return d.h_out * d.w_out >= 128 ? 2 : 0;
 }
 
+// Stride-2 3x3 grad input by phases: TP dy positions a tile (128, or 64 where
+// 128-position tiles would leave the device short of workgroups); tr rows of
+// one image, or ipt whole images where an image has fewer than TP positions.
+// 0 when the kernel does not apply.
+int conv_halo_dgrad_s2_tp(const tvk_conv_desc& d, int* tr = nullptr, int* ipt = nullptr) {
+    if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return 0;
+    if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return 0;
+    if (d.kh != 3 || d.kw != 3 || d.stride[0] != 2 || d.stride[1] != 2 || d.dilation[0] != 1 || d.dilation[1] != 1) return 0;
+    if (d.padding[0] != 1 || d.padding[1] != 1 || d.c_out % 32 != 0) return 0;
+    const int64_t Ho = d.h_out, Wo = d.w_out;
+    if ((Wo != 8 && Wo != 16 && Wo != 32 && Wo != 64) || d.w != 2 * Wo || d.h != 2 * Ho) return 0;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!al16(d.x) || !al16(d.y) || !al16(d.weight)) return 0;
+    if (std::max({d.n * d.c_in * d.h * d.w, d.n * d.c_out * Ho * Wo, d.c_out * d.c_in * 9}) >= (int64_t(1) << 30)) return 0;
+    const int64_t cblk = (d.c_in + HL_BN - 1) / HL_BN;
+    for (int tp : {128, 64}) {
+        const int64_t r = std::min<int64_t>(Ho, tp / Wo);
+        if (r < 1 || tp % (r * Wo) != 0) continue;
+        const int64_t k = tp / (r * Wo);
+        if (k == 1 ? Ho % r != 0 : r != Ho) continue;
+        if (k * (r + 1) * (Wo + 1) * 64 > D2_A) continue;   // the halo fits its LDS stage
+        const int64_t tiles = (d.n + k - 1) / k * (Ho / r);
+        if (tp == 128 && tiles * cblk < 256) continue;
+        if (tr) *tr = (int)r;
+        if (ipt) *ipt = (int)k;
+        return tp;
+    }
+    return 0;
+}
+
 int conv_halo_wgrad_s2_tpx(const tvk_conv_desc& d);
 tvk_status conv_halo_wgrad_s2_run(const tvk_conv_desc& d, const char* who);
 
 bool conv_halo_applies(const tvk_conv_desc& d, int mode) {
     if (mode == 0 && conv_halo_s2_fm(d) != 0) return true;
+    if (mode == 1 && conv_halo_dgrad_s2_tp(d) != 0) return true;
     if (mode == 2 && conv_halo_wgrad_s2_tpx(d) != 0) return true;
     if (mode == 2 && conv1x1_wgrad_applies(d)) return true;
     if (mode == 0 && conv1x1_fwd_tile(d) != 0) return true;
@@ -2155,6 +2358,26 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     p.has_bias = (mode == 0 && d.bias) ? 1 : 0;
     p.out = mode == 0 ? d.y : d.x;
     p.Cs = Cs; p.N = N; p.H = H; p.W = W;
+    int tr2 = 0, ipt2 = 0;
+    const int tp2 = mode == 1 ? conv_halo_dgrad_s2_tp(d, &tr2, &ipt2) : 0;
+    if (tp2) {
+        p.tr = tr2;
+        p.ipt = ipt2;
+        p.nimg = (int)d.n;
+        p.row_tiles = (H / 2) / tr2;
+        p.wt_bytes = (int)wt_b;
+        const dim3 grid((unsigned)((d.n + ipt2 - 1) / ipt2 * p.row_tiles), (unsigned)((N + HL_BN - 1) / HL_BN));
+        if (tp2 == 128) {
+            if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, 128>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, 128>), grid, dim3(512), 0, s, p);
+        } else {
+            if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, 64>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, 64>), grid, dim3(512), 0, s, p);
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
+        return TVK_OK;
+    }
     const int fm2 = mode == 0 ? conv_halo_s2_fm(d) : 0;
     p.tr = fm2 ? 64 * fm2 / (W / 2) : HL_PX / W;
     p.row_tiles = fm2 ? ((H / 2) + p.tr - 1) / p.tr : (H + p.tr - 1) / p.tr;
