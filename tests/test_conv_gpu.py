@@ -186,8 +186,8 @@ HALO_CASES = [
     dict(n=1, cin=128, cout=64, k=3, s=1, p=1, hw=(64, 8)),
     dict(n=3, cin=64, cout=32, k=3, s=1, p=1, hw=(8, 32)),
     # stride-2 forward halo kernel (de-interleaved columns, 128-pixel tiles):
-    # a partial row tile, a partial output-channel tile, three k chunks, and a
-    # 64-pixel image (the ring kernel)
+    # a partial row tile, a partial output-channel tile, three k chunks, and
+    # 64-pixel images two a tile with the batch's last tile half empty
     dict(n=2, cin=32, cout=96, k=3, s=2, p=1, hw=(32, 16)),
     dict(n=1, cin=64, cout=64, k=3, s=2, p=1, hw=(12, 64)),
     dict(n=3, cin=96, cout=32, k=3, s=2, p=1, hw=(16, 32)),
@@ -199,6 +199,8 @@ HALO_CASES = [
     dict(n=32, cin=32, cout=32, k=3, s=2, p=1, hw=(64, 64), sample_n=3),
     dict(n=511, cin=64, cout=32, k=3, s=2, p=1, hw=(16, 16)),
     dict(n=5, cin=32, cout=64, k=3, s=2, p=1, hw=(8, 16)),
+    # forward: 8x8 outputs two images a tile
+    dict(n=3, cin=64, cout=96, k=3, s=2, p=1, hw=(16, 16)),
 ]
 
 # 1x1 kernels from NCHW (stride 1 or 2, no padding). Grad weight (64-channel

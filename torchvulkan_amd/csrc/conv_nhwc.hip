@@ -804,13 +804,14 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
 }
 
 // Stride-2 3x3 padding-1 forward from NCHW (W = 2 Wo, H = 2 Ho): the same
-// scheme as the stride-1 halo kernel on a 64 * FM output-pixel tile (TR x Wo)
-// x 64 output channels, 4 waves of 16 * FM pixels. The (2 TR + 1)-row input
+// scheme as the stride-1 halo kernel on a 64 * FM output-pixel tile (TR x Wo
+// of one image, or ipt whole images of TR = Ho rows where an image has fewer
+// pixels) x 64 output channels, 4 waves of 16 * FM pixels. The (2 TR + 1)-row input
 // halo is stored with its columns de-interleaved: column hc = iw + 1 goes to
 // slot hc / 2 when even and W / 2 + 1 + hc / 2 when odd, so the 16 output
 // pixels of a fragment read 16 consecutive slots for every tap (tap column b:
 // even slots from c + b / 2, odd slots from W / 2 + 1 + c).
-constexpr int H2_A = 38912;      // (2 TR + 1) x (W + 2) slots x 64 bytes <= 594 x 64, rounded up to 1 KB
+constexpr int H2_A = 41984;      // ipt (2 TR + 1) x (W + 2) slots x 64 bytes <= 656 x 64
 constexpr int H2_STAGE = H2_A + HL_B;
 
 template <int DT, int FM>
@@ -819,10 +820,10 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
     __shared__ __attribute__((aligned(1024))) char lds[2 * H2_STAGE];
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
     const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64), g = lane / 16;
-    const int img = blockIdx.x / p.row_tiles, h0 = (blockIdx.x - img * p.row_tiles) * p.tr;   // output rows
+    const int img0 = (blockIdx.x / p.row_tiles) * p.ipt, h0 = (blockIdx.x % p.row_tiles) * p.tr;   // output rows
     const int n0 = blockIdx.y * HL_BN;
     const int W = p.W, RP = W + 2, HWs = p.H * W, Wo = W / 2, Ho = p.H / 2;
-    const int HR = 2 * p.tr + 1, ODD = W / 2 + 1;
+    const int HRI = 2 * p.tr + 1, HR = p.ipt * HRI, ODD = W / 2 + 1, ppi = p.tr * Wo;
     const int nk = p.Cs / 32;
 
     // zero halo column hc = 0 (input column -1: even slot 0) of both stages
@@ -833,7 +834,8 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
             *reinterpret_cast<u32x4*>(lds + st * H2_STAGE + hp * 64 + ch * 16) = u32x4{0u, 0u, 0u, 0u};
     }
 
-    // halo gather: block b -> (column group wq, channel group cg, halo row hr); up to two a thread
+    // halo gather: block b -> (column group wq, channel group cg, halo row hr
+    // = image k of the tile, row 2 h0 - 1 + hr % HRI); up to two a thread
     const int nwq = W / 8, nblk = HR * nwq * 4;
     u32x4 ar[2][8];
     auto load_a = [&](int kc) {
@@ -841,9 +843,9 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
         for (int u = 0; u < 2; ++u) {
             const int b = tid + u * 256;
             const int wq = b % nwq, cg = (b / nwq) % 4, hr = b / (nwq * 4);
-            const int ih = 2 * h0 - 1 + hr;
-            const bool row = b < nblk && ih >= 0 && ih < p.H;
-            const uint16_t* src = p.src + ((int64_t)img * p.Cs + kc * 32 + cg * 8) * HWs + (int64_t)(row ? ih : 0) * W + wq * 8;
+            const int k = hr / HRI, ih = 2 * h0 - 1 + hr % HRI;
+            const bool row = b < nblk && ih >= 0 && ih < p.H && img0 + k < p.nimg;
+            const uint16_t* src = p.src + ((int64_t)(row ? img0 + k : 0) * p.Cs + kc * 32 + cg * 8) * HWs + (int64_t)(row ? ih : 0) * W + wq * 8;
 #pragma unroll
             for (int i = 0; i < 8; ++i)
                 ar[u][i] = row ? *reinterpret_cast<const u32x4*>(src + (int64_t)i * HWs) : u32x4{0u, 0u, 0u, 0u};
@@ -890,8 +892,8 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
         const int q = wave * 16 * FM + i * 16 + lane % 16;
-        const int r = q / Wo, c = q - r * Wo;
-        hp0[i] = 2 * r * RP + c;
+        const int k = q / ppi, rem = q - k * ppi, r = rem / Wo, c = rem - r * Wo;
+        hp0[i] = (k * HRI + 2 * r) * RP + c;
     }
     f32x4 acc[FM][4];
 #pragma unroll
@@ -967,9 +969,9 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
     const int HWo = Ho * Wo;
     for (int idx = tid; idx < HL_BN * (TPX / 8); idx += 256) {
         const int ch = idx / (TPX / 8), px = (idx % (TPX / 8)) * 8;
-        const int r = px / Wo;
-        if (n0 + ch >= p.N || h0 + r >= Ho) continue;
-        *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + n0 + ch) * HWo + (int64_t)h0 * Wo + px) =
+        const int k = px / ppi, rem = px - k * ppi, r = rem / Wo;
+        if (n0 + ch >= p.N || h0 + r >= Ho || img0 + k >= p.nimg) continue;
+        *reinterpret_cast<u32x4*>(out + ((int64_t)(img0 + k) * p.N + n0 + ch) * HWo + (int64_t)h0 * Wo + rem) =
             *reinterpret_cast<const u32x4*>(tile + ch * LROW + px);
     }
 }
@@ -2104,7 +2106,7 @@ tvk_status conv1x1_fwd_run(const tvk_conv_desc& d, const char* who) {
 }
 
 // stride-2 3x3 padding-1 forward: W = 2 Wo in 16..64, H = 2 Ho, input channels in 32s
-int conv_halo_s2_fm(const tvk_conv_desc& d) {
+int conv_halo_s2_fm(const tvk_conv_desc& d, int* ipt = nullptr) {
     if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return 0;
     if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return 0;
     if (d.kh != 3 || d.kw != 3 || d.stride[0] != 2 || d.stride[1] != 2 || d.dilation[0] != 1 || d.dilation[1] != 1) return 0;
@@ -2113,9 +2115,20 @@ int conv_halo_s2_fm(const tvk_conv_desc& d) {
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     if (!al16(d.x) || !al16(d.y) || !al16(d.weight)) return 0;
     if (std::max({d.n * d.c_in * d.h * d.w, d.n * d.c_out * d.h_out * d.w_out, d.c_out * d.c_in * 9}) >= (int64_t(1) << 30)) return 0;
-    // 128-pixel tiles; smaller images (64-pixel tiles) measured no faster than the ring
-    // kernel and its channels-last copy, whose weight rows serve more pixels a workgroup
-    return d.h_out * d.w_out >= 128 ? 2 : 0;
+    // 128-pixel tiles: rows of one image, or whole images where an image has
+    // fewer pixels (64-pixel tiles of one small image measured no faster than
+    // the ring kernel and its channels-last copy: their weight rows serve too
+    // few pixels)
+    const int64_t hw = d.h_out * d.w_out;
+    if (hw >= 128) {
+        if (ipt) *ipt = 1;
+        return 2;
+    }
+    if (128 % hw != 0) return 0;
+    const int64_t k = 128 / hw;
+    if (k * (2 * d.h_out + 1) * (d.w + 2) * 64 > H2_A || k * (2 * d.h_out + 1) * (d.w / 8) * 4 > 512) return 0;
+    if (ipt) *ipt = (int)k;
+    return 2;
 }
 
 // Stride-2 3x3 grad input by phases: TP dy positions a tile (128, or 64 where
@@ -2358,6 +2371,8 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     p.has_bias = (mode == 0 && d.bias) ? 1 : 0;
     p.out = mode == 0 ? d.y : d.x;
     p.Cs = Cs; p.N = N; p.H = H; p.W = W;
+    p.ipt = 1;
+    p.nimg = (int)d.n;
     int tr2 = 0, ipt2 = 0;
     const int tp2 = mode == 1 ? conv_halo_dgrad_s2_tp(d, &tr2, &ipt2) : 0;
     if (tp2) {
@@ -2378,8 +2393,10 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
         if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
         return TVK_OK;
     }
-    const int fm2 = mode == 0 ? conv_halo_s2_fm(d) : 0;
-    p.tr = fm2 ? 64 * fm2 / (W / 2) : HL_PX / W;
+    int ipt_f = 1;
+    const int fm2 = mode == 0 ? conv_halo_s2_fm(d, &ipt_f) : 0;
+    p.ipt = ipt_f;
+    p.tr = fm2 ? (ipt_f > 1 ? H / 2 : 64 * fm2 / (W / 2)) : HL_PX / W;
     p.row_tiles = fm2 ? ((H / 2) + p.tr - 1) / p.tr : (H + p.tr - 1) / p.tr;
     p.wt_bytes = (int)wt_b;
     // forward: tap (a, b) reads source (h + a - 1, w + b - 1); grad input: (h + 1 - a, w + 1 - b);
@@ -2393,7 +2410,7 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
             p.dtap[t] = ho * (W + 2) + wo;
         }
     }
-    const dim3 grid((unsigned)(d.n * p.row_tiles), (unsigned)((N + HL_BN - 1) / HL_BN));
+    const dim3 grid((unsigned)((d.n + p.ipt - 1) / p.ipt * p.row_tiles), (unsigned)((N + HL_BN - 1) / HL_BN));
     if (fm2) {
         if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_s2_kernel<TVK_F16, 2>), grid, dim3(256), 0, s, p);
         else hipLaunchKernelGGL((conv_halo_s2_kernel<TVK_BF16, 2>), grid, dim3(256), 0, s, p);
