@@ -199,6 +199,9 @@ HALO_CASES = [
     dict(n=32, cin=32, cout=32, k=3, s=2, p=1, hw=(64, 64), sample_n=3),
     dict(n=511, cin=64, cout=32, k=3, s=2, p=1, hw=(16, 16)),
     dict(n=5, cin=32, cout=64, k=3, s=2, p=1, hw=(8, 16)),
+    # 128-position tiles of two images x 32-channel blocks, the last block
+    # partial and the batch's last tile half empty
+    dict(n=255, cin=48, cout=32, k=3, s=2, p=1, hw=(16, 16)),
     # forward: 8x8 outputs two images a tile
     dict(n=3, cin=64, cout=96, k=3, s=2, p=1, hw=(16, 16)),
 ]

@@ -981,7 +981,7 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
 // dx(2i + ph, 2j + pw) sums the taps a with (ph + 1 - a) even, reading dy row
 // i + (ph + 1 - a) / 2, and likewise b for the columns, so the phases take 1,
 // 2, 2 and 4 of the 9 taps and no product is a zero of the strided grid. A
-// workgroup takes TP dy positions (ipt images x tr rows x Wo) x 64 input
+// workgroup takes TP dy positions (ipt images x tr rows x Wo) x BN input
 // channels. Its 8 waves take one phase and half of the positions each: waves
 // 0-1 phase (0,0), 2-3 (0,1), 4-5 (1,1), 6-7 (1,0), so waves w and w + 4,
 // which share a SIMD, run 5 or 4 taps between them. Per 32-channel chunk the
@@ -991,17 +991,19 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
 constexpr int D2_A = 13312;   // ipt (tr + 1) (Wo + 1) pixels x 64 bytes: 3 x 65 at Wo = 64, 18 x 9 at Wo = 8
 constexpr int D2_STAGE = D2_A + HL_B;
 
-template <int DT, int TP>
+template <int DT, int TP, int BN>
 __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
     constexpr int FMW = TP / 32;   // A fragments a wave (TP / 2 positions)
+    constexpr int FN = BN / 16;    // B fragments (input-channel columns)
+    constexpr int NBI = 9 * BN / 16, QB = (NBI + 7) / 8;   // weight DMA instructions a chunk; per wave
     constexpr int LROW = 4 * TP + 8;
-    static_assert(64 * LROW * 2 <= 2 * D2_STAGE, "output tile fits the stages");
+    static_assert(BN * LROW * 2 <= 2 * D2_STAGE && 9 * BN * 64 <= HL_B, "tiles fit the stages");
     __shared__ __attribute__((aligned(1024))) char lds[2 * D2_STAGE];
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
     const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64), g = lane / 16;
     const int Wo = p.W / 2, Ho = p.H / 2, TR = p.tr, RP = Wo + 1, HR = p.ipt * (TR + 1), HWo = Ho * Wo;
     const int img0 = (blockIdx.x / p.row_tiles) * p.ipt, i0 = (blockIdx.x % p.row_tiles) * TR;
-    const int n0 = blockIdx.y * HL_BN;
+    const int n0 = blockIdx.y * BN;
     const int nk = p.Cs / 32;
 
     // zero halo column Wo of every row of both stages (no load writes it)
@@ -1041,21 +1043,21 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
         }
     };
 
-    // weight rows: 36 DMA instructions of 16 rows a chunk, instruction q * 8 + wave
-    // (waves 0-3 issue 5, waves 4-7 issue 4); row = tap * 64 + channel
+    // weight rows: NBI DMA instructions of 16 rows a chunk, instruction q * 8 + wave;
+    // row = tap * BN + channel
     const i32x4 rb = v_rsrc(p.wt, p.wt_bytes);
-    int b_off[5];
+    int b_off[QB];
 #pragma unroll
-    for (int q = 0; q < 5; ++q) {
-        const int row = min(q * 8 + wave, 35) * 16 + lane / 4;
-        const int t = row / HL_BN, co = min(n0 + row % HL_BN, p.N - 1);
+    for (int q = 0; q < QB; ++q) {
+        const int row = min(q * 8 + wave, NBI - 1) * 16 + lane / 4;
+        const int t = row / BN, co = min(n0 + row % BN, p.N - 1);
         b_off[q] = ((co * 9 + t) * p.Cs + (((lane % 4) ^ hl_swz(row)) * 8)) * 2;
     }
     auto issue_b = [&](int kc, int st) {
         const uint32_t base = lds0 + (uint32_t)(st * D2_STAGE + D2_A);
 #pragma unroll
-        for (int q = 0; q < 5; ++q)
-            if (q * 8 + wave < 36) v_dma16(rb, base + (uint32_t)((q * 8 + wave) * 1024), (uint32_t)(b_off[q] + kc * 64));
+        for (int q = 0; q < QB; ++q)
+            if (q * 8 + wave < NBI) v_dma16(rb, base + (uint32_t)((q * 8 + wave) * 1024), (uint32_t)(b_off[q] + kc * 64));
     };
 
     // this wave's phase and positions: q = half * TP / 2 + i * 16 + lane % 16
@@ -1068,11 +1070,11 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
         const int k = q / ppi, rem = q - k * ppi, r = rem / Wo, c = rem - r * Wo;
         hp0[i] = (k * (TR + 1) + r) * RP + c;
     }
-    f32x4 acc[FMW][4];
+    f32x4 acc[FMW][FN];
 #pragma unroll
     for (int i = 0; i < FMW; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     issue_b(0, 0);
     load_a(0);
@@ -1093,21 +1095,21 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
             for (int tb = 0; tb < nb; ++tb) {
                 const int a = ph ? 2 * ta : 1, b = pw ? 2 * tb : 1;
                 const int off = ((ph + 1 - a) / 2) * RP + (pw + 1 - b) / 2, t = a * 3 + b;
-                u32x4 fa[FMW], fb[4];
+                u32x4 fa[FMW], fb[FN];
 #pragma unroll
                 for (int i = 0; i < FMW; ++i) {
                     const int hp = hp0[i] + off;
                     fa[i] = *reinterpret_cast<const u32x4*>(sa + hp * 64 + ((g ^ hl_swz(hp)) * 16));
                 }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int row = t * HL_BN + j * 16 + lane % 16;
+                for (int j = 0; j < FN; ++j) {
+                    const int row = t * BN + j * 16 + lane % 16;
                     fb[j] = *reinterpret_cast<const u32x4*>(sb + row * 64 + ((g ^ hl_swz(row)) * 16));
                 }
 #pragma unroll
                 for (int i = 0; i < FMW; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
+                    for (int j = 0; j < FN; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1127,7 +1129,7 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
         const int k = q0 / ppi, rem = q0 - k * ppi, r = rem / Wo, c = rem - r * Wo;
         const int px0 = k * 4 * ppi + (2 * r + ph) * p.W + 2 * c + pw;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < FN; ++j) {
             const int ch = j * 16 + lane % 16;
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr)
@@ -1137,7 +1139,7 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
     __syncthreads();
     uint16_t* out = static_cast<uint16_t*>(p.out);
     const int HW = p.H * p.W;
-    for (int idx = tid; idx < HL_BN * (TP / 2); idx += 512) {
+    for (int idx = tid; idx < BN * (TP / 2); idx += 512) {
         const int ch = idx / (TP / 2), px = (idx % (TP / 2)) * 8;
         const int k = px / (4 * ppi), rem = px - k * 4 * ppi;
         const int h = 2 * i0 + rem / p.W, w = rem % p.W;
@@ -2132,10 +2134,11 @@ int conv_halo_s2_fm(const tvk_conv_desc& d, int* ipt = nullptr) {
 }
 
 // Stride-2 3x3 grad input by phases: TP dy positions a tile (128, or 64 where
-// 128-position tiles would leave the device short of workgroups); tr rows of
-// one image, or ipt whole images where an image has fewer than TP positions.
+// 128-position tiles would leave the device short of workgroups) x BN input
+// channels (64, or 32 where that keeps 128-position tiles); tr rows of one
+// image, or ipt whole images where an image has fewer than TP positions.
 // 0 when the kernel does not apply.
-int conv_halo_dgrad_s2_tp(const tvk_conv_desc& d, int* tr = nullptr, int* ipt = nullptr) {
+int conv_halo_dgrad_s2_tp(const tvk_conv_desc& d, int* tr = nullptr, int* ipt = nullptr, int* bn_out = nullptr) {
     if (d.dtype != TVK_F16 && d.dtype != TVK_BF16) return 0;
     if ((d.flags & TVK_GEMM_EXACT) || d.groups != 1 || d.n <= 0) return 0;
     if (d.kh != 3 || d.kw != 3 || d.stride[0] != 2 || d.stride[1] != 2 || d.dilation[0] != 1 || d.dilation[1] != 1) return 0;
@@ -2145,17 +2148,20 @@ int conv_halo_dgrad_s2_tp(const tvk_conv_desc& d, int* tr = nullptr, int* ipt = 
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     if (!al16(d.x) || !al16(d.y) || !al16(d.weight)) return 0;
     if (std::max({d.n * d.c_in * d.h * d.w, d.n * d.c_out * Ho * Wo, d.c_out * d.c_in * 9}) >= (int64_t(1) << 30)) return 0;
-    const int64_t cblk = (d.c_in + HL_BN - 1) / HL_BN;
-    for (int tp : {128, 64}) {
+    // (TP, BN) in order: (128, 64), (128, 32), (64, 64); the first two only
+    // where they give at least 256 workgroups
+    for (int c = 0; c < 3; ++c) {
+        const int tp = c < 2 ? 128 : 64, bn = c == 1 ? 32 : 64;
         const int64_t r = std::min<int64_t>(Ho, tp / Wo);
         if (r < 1 || tp % (r * Wo) != 0) continue;
         const int64_t k = tp / (r * Wo);
         if (k == 1 ? Ho % r != 0 : r != Ho) continue;
         if (k * (r + 1) * (Wo + 1) * 64 > D2_A) continue;   // the halo fits its LDS stage
-        const int64_t tiles = (d.n + k - 1) / k * (Ho / r);
-        if (tp == 128 && tiles * cblk < 256) continue;
+        const int64_t tiles = (d.n + k - 1) / k * (Ho / r) * ((d.c_in + bn - 1) / bn);
+        if (tp == 128 && tiles < 256) continue;
         if (tr) *tr = (int)r;
         if (ipt) *ipt = (int)k;
+        if (bn_out) *bn_out = bn;
         return tp;
     }
     return 0;
@@ -2373,21 +2379,25 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     p.Cs = Cs; p.N = N; p.H = H; p.W = W;
     p.ipt = 1;
     p.nimg = (int)d.n;
-    int tr2 = 0, ipt2 = 0;
-    const int tp2 = mode == 1 ? conv_halo_dgrad_s2_tp(d, &tr2, &ipt2) : 0;
+    int tr2 = 0, ipt2 = 0, bn2 = 64;
+    const int tp2 = mode == 1 ? conv_halo_dgrad_s2_tp(d, &tr2, &ipt2, &bn2) : 0;
     if (tp2) {
         p.tr = tr2;
         p.ipt = ipt2;
         p.nimg = (int)d.n;
         p.row_tiles = (H / 2) / tr2;
         p.wt_bytes = (int)wt_b;
-        const dim3 grid((unsigned)((d.n + ipt2 - 1) / ipt2 * p.row_tiles), (unsigned)((N + HL_BN - 1) / HL_BN));
-        if (tp2 == 128) {
-            if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, 128>), grid, dim3(512), 0, s, p);
-            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, 128>), grid, dim3(512), 0, s, p);
+        const dim3 grid((unsigned)((d.n + ipt2 - 1) / ipt2 * p.row_tiles), (unsigned)((N + bn2 - 1) / bn2));
+        const bool f16 = d.dtype == TVK_F16;
+        if (tp2 == 128 && bn2 == 64) {
+            if (f16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, 128, 64>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, 128, 64>), grid, dim3(512), 0, s, p);
+        } else if (tp2 == 128) {
+            if (f16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, 128, 32>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, 128, 32>), grid, dim3(512), 0, s, p);
         } else {
-            if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, 64>), grid, dim3(512), 0, s, p);
-            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, 64>), grid, dim3(512), 0, s, p);
+            if (f16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, 64, 64>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, 64, 64>), grid, dim3(512), 0, s, p);
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
