@@ -202,6 +202,9 @@ HALO_CASES = [
     # 128-position tiles of two images x 32-channel blocks, the last block
     # partial and the batch's last tile half empty
     dict(n=255, cin=48, cout=32, k=3, s=2, p=1, hw=(16, 16)),
+    # 64 dy columns: one-row 64-position tiles, and two-row 128-position tiles
+    dict(n=2, cin=32, cout=32, k=3, s=2, p=1, hw=(8, 128)),
+    dict(n=128, cin=32, cout=32, k=3, s=2, p=1, hw=(8, 128), sample_n=2),
     # forward: 8x8 outputs two images a tile
     dict(n=3, cin=64, cout=96, k=3, s=2, p=1, hw=(16, 16)),
 ]
