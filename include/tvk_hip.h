@@ -17,6 +17,15 @@
  *     waits for and the caching allocator's blocks are ordered on.
  *   - strides are in ELEMENTS, not bytes, and may be zero (broadcast) or any
  *     positive value; element offsets must fit in int64.
+ *   - scratch memory: tvk_gemm, tvk_conv2d_*, tvk_reduce_sum and
+ *     tvk_attention_bwd lease library scratch (split-K partials, repacked
+ *     operands, convolution partials, the attention delta) from a per-device
+ *     pool for the kernels they queue on their `stream`. A lease ends when the
+ *     call returns, behind an event recorded on that stream: a later call on
+ *     the same stream reuses the memory in stream order, a call on another
+ *     stream first waits for that event, and no buffer is freed while a call
+ *     holds it or its kernels may still run. Calls may therefore come from any
+ *     thread and any stream; the caller orders only its own tensors.
  */
 #ifndef TVK_HIP_H
 #define TVK_HIP_H
@@ -85,6 +94,24 @@ tvk_status tvk_get_stream(int device, void** stream);
  * Replaces DeviceContext::flush() behind torchvulkan.synchronize
  * (src/api/backend.cpp:32-35). */
 tvk_status tvk_synchronize(int device);
+
+/* Events on a stream, for the device guard's torch.Event API. They replace
+ * the reference's host-timestamp VulkanEvent (src/api/guard.cpp:14-61), which
+ * synchronised the whole queue on every record. `timing` != 0 makes the event
+ * usable by tvk_event_elapsed. A NULL stream is HIP's default stream. */
+tvk_status tvk_event_create(int device, int timing, void** event);
+tvk_status tvk_event_destroy(void* event);
+/* The event completes once the work queued on `stream` so far has run. */
+tvk_status tvk_event_record(void* event, void* stream);
+/* *done = 1 when the event's work has run (or it was never recorded). */
+tvk_status tvk_event_query(void* event, int* done);
+tvk_status tvk_event_synchronize(void* event);
+/* Milliseconds between two recorded timing events (GPU clock). */
+tvk_status tvk_event_elapsed(void* start, void* end, float* ms);
+/* Work queued on `stream` from now on waits for `event`. */
+tvk_status tvk_stream_wait_event(void* stream, void* event);
+/* *done = 1 when every operation queued on `stream` has run. */
+tvk_status tvk_stream_query(void* stream, int* done);
 
 typedef struct {
     char name[256];
@@ -273,11 +300,16 @@ tvk_status tvk_binary(const tvk_binary_desc* desc);
  * dtype before the product with v, as the reference's cooperative-matrix
  * kernel stages them in the dtype (src/shaders/ops/attention_coop.slang;
  * row semantics from chunked_forward, src/api/ops/attention.cpp:115-139).
- * Supported: F16 and BF16; head_dim == head_dim_v in {64, 128}; q, k, v with
- * unit stride along the head dimension and 16-byte aligned rows; bias in the
- * dtype, any strides (zero strides broadcast). Other cases return
- * TVK_ERR_UNSUPPORTED (the caller runs its decomposed path). Replaces
- * fused_forward (src/api/ops/attention.cpp:434-500) behind
+ * Supported: F32, F16 and BF16; head_dim and head_dim_v from 1 to 512 (they
+ * may differ); any element strides for q, k, v, bias (zero strides
+ * broadcast) and out; batch and heads up to 65535, sequences up to 2^30.
+ * float16/bfloat16 with head_dim == head_dim_v in {64, 128}, unit stride along
+ * the head dimension and 16-byte aligned rows run the MFMA kernels; every
+ * other case runs general kernels (float32 dot products over LDS-staged
+ * 64-column chunks of the head dims, the same staging of P in the dtype).
+ * Other cases return TVK_ERR_UNSUPPORTED. Replaces fused_forward
+ * (src/api/ops/attention.cpp:434-500) and, for the shapes it leaves,
+ * chunked_forward (:115-139) behind
  * _scaled_dot_product_fused_attention_overrideable (:697-719). */
 typedef struct {
     int32_t dtype;
@@ -307,17 +339,22 @@ tvk_status tvk_attention_fwd(const tvk_attention_desc* desc);
  * rounded to the dtype before their products, as the reference's
  * scoreGradients stages them (src/shaders/ops/attention_coop.slang:283-305);
  * accumulation is float32, and every output element
- * is written by one workgroup (no atomics: the same bits every run). The
- * gradient of the bias is not produced (the reference computes it on its
- * chunked path). Same support as the forward; dout, dq, dk, dv with unit
- * stride along the head dimension and 16-byte aligned rows. Uses B*Hq*L
- * floats of the library workspace for delta. */
+ * is written by one workgroup (no atomics: the same bits every run). When
+ * `dscores` is not NULL it receives dS (float32, unrounded, [B, Hq, L, S] at
+ * dscores_stride; zero where masked), the gradient of an additive bias before
+ * any broadcast is summed away: the reference computes the bias gradient on
+ * its chunked path (:141-199), here the caller sums dS over the bias's
+ * broadcast dimensions. Same support as the forward (dout, dq, dk, dv any
+ * strides; the MFMA passes need unit stride along the head dimension and
+ * 16-byte aligned rows, and run only without dscores). Uses B*Hq*L floats of
+ * library scratch for delta. */
 typedef struct {
     tvk_attention_desc fwd;
     const void* dout; int64_t dout_stride[4];
     void* dq; int64_t dq_stride[4];
     void* dk; int64_t dk_stride[4];
     void* dv; int64_t dv_stride[4];
+    float* dscores; int64_t dscores_stride[4];   /* NULL: not wanted */
 } tvk_attention_bwd_desc;
 
 tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc);

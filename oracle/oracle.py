@@ -206,7 +206,7 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, bias: np.ndarray | No
     return out, lse
 
 
-def attention_bwd(q, k, v, dout, bias=None, causal=False, scale=None, out=None, round_to=None):
+def attention_bwd(q, k, v, dout, bias=None, causal=False, scale=None, out=None, round_to=None, return_ds=False):
     """(dq, dk, dv) of attention() in float64, as the reference's
     chunked_backward (src/api/ops/attention.cpp:141-199): P = exp(s - lse),
     delta = rowsum(dout*out), dS = P*(dout.v^T - delta), dq = scale*dS.k,
@@ -216,7 +216,10 @@ def attention_bwd(q, k, v, dout, bias=None, causal=False, scale=None, out=None, 
     float64 output is used. round_to (F16/BF16): P and dS are formed in
     float32 and rounded to that dtype before their products, as the
     reference's cooperative-matrix backward stages them
-    (src/shaders/ops/attention_coop.slang:283-305)."""
+    (src/shaders/ops/attention_coop.slang:283-305). return_ds: also the
+    score gradient dS [B,Hq,L,S] before any rounding, the gradient of an
+    additive bias before its broadcast dimensions are summed (the
+    reference's grad_bias is sum_to(ds, bias shape), :187-196)."""
     q, k, v, dout = (np.asarray(t, dtype=np.float64) for t in (q, k, v, dout))
     B, Hq, L, D = q.shape
     Hk, S = k.shape[1], k.shape[2]
@@ -235,12 +238,15 @@ def attention_bwd(q, k, v, dout, bias=None, causal=False, scale=None, out=None, 
     delta = (dout * out).sum(-1, keepdims=True)
     dp = np.einsum("bhld,bhsd->bhls", dout, vv)
     ds = p * (dp - delta)
+    ds_exact = ds
     if round_to is not None:
         rt = lambda x: to_f32(cast(x.astype(np.float32), F32, round_to), round_to).astype(np.float64)
         p, ds = rt(p), rt(ds)
     dq = np.einsum("bhls,bhsd->bhld", ds, kk) * scale
     dk = np.einsum("bhls,bhld->bhsd", ds, q).reshape(B, Hk, g, S, D).sum(2) * scale
     dv = np.einsum("bhls,bhld->bhsd", p, dout).reshape(B, Hk, g, S, v.shape[3]).sum(2)
+    if return_ds:
+        return dq, dk, dv, ds_exact
     return dq, dk, dv
 
 

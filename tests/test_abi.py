@@ -99,6 +99,25 @@ def test_gemm_plan_without_gpu(a_stride, b_stride, dtype, M, N, K, want):
     assert buf.value.decode() == want
 
 
+@pytest.mark.parametrize("a_stride,b_stride,M,N,K,want", [
+    # A spans 4 GiB: tvk_gemm runs it in row blocks below 2 GiB, each on the tiled kernels
+    ((0, 2048, 1), (0, 256, 1), 1 << 20, 256, 2048, "gemm16_dma_256x256"),
+    # just below the boundary: one block
+    ((0, 2048, 1), (0, 256, 1), 524032, 256, 2048, "gemm16_dma_256x256"),
+    # B spans 4 GiB along N with K rows: column blocks
+    ((0, 2048, 1), (0, 1, 2048), 512, 1 << 20, 2048, "gemm16_dma_256x256"),
+    # a single k row of B spans 4 GiB (n-contiguous, k stride 2^20): no block fits, the generic kernel
+    ((0, 2048, 1), (0, 1 << 20, 1), 512, 1 << 20, 2048, "gemm_generic"),
+])
+def test_gemm_plan_past_2gib_operands(a_stride, b_stride, M, N, K, want):
+    lib = _abi.load()
+    d = _desc(a_stride=_abi.I64x3(*a_stride), b_stride=_abi.I64x3(*b_stride), M=M, N=N, K=K)
+    d.a, d.b, d.c = 1 << 12, 1 << 12, 1 << 12
+    buf = C.create_string_buffer(64)
+    assert lib.tvk_gemm_plan(C.byref(d), buf, 64) == _abi.TVK_OK
+    assert buf.value.decode() == want
+
+
 def test_free_rejects_foreign_pointer():
     lib = _abi.load()
     assert lib.tvk_free(C.c_void_p(0x1234)) == _abi.TVK_ERR_INVALID

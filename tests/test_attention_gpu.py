@@ -112,12 +112,77 @@ def test_head_strided_views(gpu):
 
 
 def test_rejects_unsupported(gpu):
-    q = torch.zeros((1, 1, 8, 48), dtype=torch.float16, device=DEV)
+    q = torch.zeros((1, 1, 8, 520), dtype=torch.float16, device=DEV)
     with pytest.raises(_abi.TvkUnsupported):
         _abi.attention_fwd(q, q, q)
-    q32 = torch.zeros((1, 1, 8, 64), device=DEV)
+    q64 = torch.zeros((1, 1, 8, 64), dtype=torch.float64, device=DEV)
     with pytest.raises(_abi.TvkUnsupported):
-        _abi.attention_fwd(q32, q32, q32)
+        _abi.attention_fwd(q64, q64, q64)
+
+
+# The general kernels: float32, head dims other than 64/128 (query/key and value dims may
+# differ), several 64-column chunks of the head dim, GQA, ragged and causal lengths, bias.
+GENERAL_CASES = [
+    # dtype, B, Hq, Hk, L, S, D, Dv, causal, bias
+    (torch.float32, 2, 4, 2, 77, 130, 64, 64, False, False),
+    (torch.float32, 1, 2, 2, 100, 100, 64, 64, True, True),
+    (torch.float16, 1, 4, 1, 129, 65, 80, 80, False, True),
+    (torch.float16, 2, 2, 2, 64, 200, 96, 48, True, False),
+    (torch.bfloat16, 1, 2, 1, 50, 70, 32, 32, False, False),
+    (torch.float16, 1, 2, 2, 40, 90, 200, 320, False, False),
+    (torch.float32, 1, 1, 1, 33, 47, 512, 512, True, False),
+]
+
+
+def general_inputs(case, seed):
+    dt, B, Hq, Hk, L, S, D, Dv, causal, with_bias = case
+    q, k, v = rand((B, Hq, L, D), dt, seed), rand((B, Hk, S, D), dt, seed + 1), rand((B, Hk, S, Dv), dt, seed + 2)
+    bias = rand((B, Hq, L, S), dt, seed + 3) if with_bias else None
+    return q, k, v, bias, causal
+
+
+@pytest.mark.parametrize("case", range(len(GENERAL_CASES)))
+def test_general_forward(gpu, case):
+    q, k, v, bias, causal = general_inputs(GENERAL_CASES[case], 100 + 10 * case)
+    check(q, k, v, bias, causal, what=f"general case {case}")
+
+
+@pytest.mark.parametrize("case", range(len(GENERAL_CASES)))
+def test_general_backward(gpu, case):
+    q, k, v, bias, causal = general_inputs(GENERAL_CASES[case], 200 + 10 * case)
+    check_bwd(q, k, v, bias, causal, what=f"general case {case}")
+
+
+def test_general_strided_views_float32(gpu):
+    # projections split into heads ([B, L, H, D] underneath) and a head dim with stride 2
+    x = rand((2, 96, 4, 128), torch.float32, 300).to(DEV)
+    kv = rand((2, 80, 2, 64), torch.float32, 301).to(DEV)
+    q, k, v = x.transpose(1, 2)[..., ::2], kv.transpose(1, 2), (kv * 0.5).transpose(1, 2)
+    assert q.stride(3) == 2
+    out, lse = _abi.attention_fwd(q, k, v, None, True)
+    torch.cuda.synchronize()
+    ro, rl = orc.attention(f64(q), f64(k), f64(v), None, True)
+    assert_close(f64(out), ro, torch.float32, "strided float32 out")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_score_gradient(gpu, dtype):
+    q, k, v = rand((2, 4, 70, 64), dtype, 400), rand((2, 2, 90, 64), dtype, 401), rand((2, 2, 90, 64), dtype, 402)
+    bias = rand((2, 4, 70, 90), dtype, 403)
+    bias[1, 2, 5] = float("-inf")         # a row that attends to nothing
+    dev = [t.to(DEV) for t in (q, k, v)]
+    out, lse = _abi.attention_fwd(*dev, bias.to(DEV), True)
+    dout = rand(out.shape, dtype, 404)
+    dq, dk, dv, ds = _abi.attention_bwd(*dev, out, lse, dout.to(DEV), bias.to(DEV), True, dscores=True)
+    torch.cuda.synchronize()
+    rdt = {torch.float16: orc.F16, torch.bfloat16: orc.BF16}.get(dtype)
+    *ref, ref_ds = orc.attention_bwd(f64(q), f64(k), f64(v), f64(dout), f64(bias), True, None, out=f64(out),
+                                     round_to=rdt, return_ds=True)
+    for got, want, name in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        assert_close(f64(got), want, dtype, f"{dtype} {name} with the score gradient")
+    # dS is float32 from float32 P and dP: held to the dtype's bound, masked entries exactly 0
+    assert_close(f64(ds), ref_ds, dtype, f"{dtype} dS")
+    assert (f64(ds)[:, :, np.arange(70)[:, None] < np.arange(90)[None, :]] == 0).all()
 
 
 def test_sdpa_on_vulkan_device(gpu):
@@ -161,7 +226,7 @@ def check_bwd(q, k, v, bias=None, causal=False, scale=None, what=""):
     torch.cuda.synchronize()
     # delta from the stored (dtype-rounded) forward output, and P, dS rounded to the dtype
     # before their products: the reference's cooperative-matrix backward
-    rdt = orc.F16 if q.dtype == torch.float16 else orc.BF16
+    rdt = {torch.float16: orc.F16, torch.bfloat16: orc.BF16}.get(q.dtype)
     ref = orc.attention_bwd(f64(q), f64(k), f64(v), f64(dout), None if bias is None else f64(bias), causal, scale,
                             out=f64(out), round_to=rdt)
     for got, want, name in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
@@ -217,3 +282,29 @@ def test_backward_wide_grid(gpu, dtype):
         for got, want, name in zip((gq[b:b + 1, hs], gk[b:b + 1, hk:hk + 1], gv[b:b + 1, hk:hk + 1]), ref,
                                    ("dq", "dk", "dv")):
             assert_close(f64(got), want, dtype, f"b {b} kv head {hk} {name}")
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.float16, 80)])
+def test_sdpa_general_on_vulkan_with_bias_gradient(gpu, monkeypatch, dtype, D):
+    # float32 and head dim 80 run on the device (strict mode raises on any CPU fallback),
+    # and the gradient of a broadcast float mask comes back through the score gradient
+    import torchvulkan_amd  # noqa: F401
+
+    monkeypatch.setenv("TORCHVULKAN_STRICT", "1")
+    V = "vulkan"
+    q, k, v = rand((2, 4, 48, D), dtype, 500), rand((2, 4, 60, D), dtype, 501), rand((2, 4, 60, D), dtype, 502)
+    mask = rand((1, 4, 48, 60), dtype, 503)
+    qv, kv_, vv, mv = (t.to(V).requires_grad_() for t in (q, k, v, mask))
+    out = F.scaled_dot_product_attention(qv, kv_, vv, attn_mask=mv)
+    q64, k64, v64, m64 = (t.double().requires_grad_() for t in (q, k, v, mask))
+    ref = F.scaled_dot_product_attention(q64, k64, v64, attn_mask=m64)
+    assert_close(f64(out), ref.detach().numpy(), dtype, "sdpa out")
+    g = rand(out.shape, dtype, 504)
+    out.backward(g.to(V))
+    ref.backward(g.double())
+    tol = 1e-5 if dtype == torch.float32 else 5e-3
+    for got, want, name in ((qv.grad, q64.grad, "dq"), (kv_.grad, k64.grad, "dk"), (vv.grad, v64.grad, "dv"),
+                            (mv.grad, m64.grad, "dmask")):
+        assert got.shape == want.shape, name
+        err = (got.cpu().double() - want).abs() / (tol * (want.abs() + 1))
+        assert err.max().item() <= 1.0, f"{name}: {err.max().item():.2f}x tolerance"

@@ -75,6 +75,29 @@ def test_backward_matches_torch_autograd_float64():
             np.testing.assert_allclose(got, want.numpy(), rtol=1e-10, atol=1e-12)
 
 
+def test_score_gradient_is_the_bias_gradient():
+    # the oracle's dS, summed over a broadcast bias's dimensions, is torch autograd's bias gradient
+    q, k, v = rnd((2, 4, 11, 8), 30), rnd((2, 2, 13, 8), 31), rnd((2, 2, 13, 8), 32)
+    dout = rnd((2, 4, 11, 8), 33)
+    for shape, causal in (((1, 4, 11, 13), False), ((2, 1, 11, 13), True), ((11, 13), False)):
+        b = rnd(shape, 34)
+        *_, ds = orc.attention_bwd(q, k, v, dout, b, causal, return_ds=True)
+        assert ds.shape == (2, 4, 11, 13)
+        tb = torch.from_numpy(b.copy()).requires_grad_()
+        tq, tk, tv = (torch.from_numpy(x) for x in (q, k, v))
+        mask = tb
+        if causal:
+            # SDPA takes no mask together with is_causal: fold the causal mask into the bias
+            mask = tb + torch.full((11, 13), float("-inf"), dtype=torch.float64).triu(1)
+        o = F.scaled_dot_product_attention(tq, tk.repeat_interleave(2, 1), tv.repeat_interleave(2, 1), attn_mask=mask)
+        o.backward(torch.from_numpy(dout))
+        if len(shape) == 2:
+            got = ds.sum(axis=(0, 1))
+        else:
+            got = ds.sum(axis=tuple(i for i, n in enumerate(shape) if n == 1), keepdims=True)
+        np.testing.assert_allclose(got, tb.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
 def test_backward_rounding_option_changes_only_the_staged_values():
     # round_to rounds P and dS to the dtype: on inputs where both are exact in float16
     # (P in {0, 1} through a dominant key, dS small dyadic values) the rounded and exact results agree

@@ -535,3 +535,26 @@ def test_skinny_exact_mode_uses_sequential_kernel(gpu):
     got, plan = run(gpu, a, b, (16, 2048), torch.float16, exact=True)
     assert plan.startswith("gemm_seq_mfma"), plan
     assert_bit_exact(got, oracle_mm(a, b, torch.float16), plan)
+
+
+# ---------------------------------------------------------------------------
+# an operand past the tiled kernels' 2 GiB buffer range runs in row blocks
+# ---------------------------------------------------------------------------
+
+def test_operand_past_2gib_runs_in_row_blocks(gpu):
+    # A is [2^20, 2048] float16 (4 GiB): three row blocks of 524032, 524032 and 512 rows, each on the ring kernel;
+    # integer operands make every summation order exact, so the rows on both sides of each block edge match bit for bit
+    dtype = torch.float16
+    M, N, K = 1 << 20, 256, 2048
+    a = torch.randint(-2, 3, (M, K), generator=gen(90), dtype=torch.int8).to(DEV).to(dtype)
+    b = randint((K, N), dtype, 91, -2, 3)
+    c = torch.empty((M, N), dtype=dtype, device=DEV)
+    gpu.gemm(a, b.to(DEV), c)
+    torch.cuda.synchronize()
+    assert gpu.gemm_plan(a, b.to(DEV), c) == "gemm16_dma_256x256"
+    rows = np.r_[0:2, 524030:524034, 1048062:1048066, M - 2:M]
+    ah = a[torch.from_numpy(rows).to(DEV)].cpu()
+    ref = oracle_mm(ah, b, dtype)
+    assert_bit_exact(decode(to_np(c[torch.from_numpy(rows).to(DEV)].cpu()), dtype), ref, "row blocks past 2 GiB")
+    del a, c
+    torch.cuda.empty_cache()

@@ -161,6 +161,7 @@ class AttentionBwdDesc(C.Structure):
         ("dq", C.c_void_p), ("dq_stride", I64x4),
         ("dk", C.c_void_p), ("dk_stride", I64x4),
         ("dv", C.c_void_p), ("dv_stride", I64x4),
+        ("dscores", C.c_void_p), ("dscores_stride", I64x4),
     ]
 
 
@@ -421,8 +422,9 @@ def attention_fwd(q, k, v, bias=None, causal=False, scale=None, stream=None):
     return out, lse
 
 
-def attention_bwd(q, k, v, out, lse, dout, bias=None, causal=False, scale=None, stream=None):
-    """(dq, dk, dv) of tvk_attention_bwd (new dense tensors) from the forward's out and lse."""
+def attention_bwd(q, k, v, out, lse, dout, bias=None, causal=False, scale=None, stream=None, dscores=False):
+    """(dq, dk, dv) of tvk_attention_bwd (new dense tensors) from the forward's out and lse; with
+    dscores=True also the float32 score gradient [B, Hq, L, S] as a fourth tensor."""
     import torch
 
     dq, dk, dv = torch.empty_like(q, memory_format=torch.contiguous_format), \
@@ -433,8 +435,12 @@ def attention_bwd(q, k, v, out, lse, dout, bias=None, causal=False, scale=None, 
     d.dq, d.dq_stride = dq.data_ptr(), I64x4(*dq.stride())
     d.dk, d.dk_stride = dk.data_ptr(), I64x4(*dk.stride())
     d.dv, d.dv_stride = dv.data_ptr(), I64x4(*dv.stride())
+    ds = None
+    if dscores:
+        ds = torch.empty((q.shape[0], q.shape[1], q.shape[2], k.shape[2]), dtype=torch.float32, device=q.device)
+        d.dscores, d.dscores_stride = ds.data_ptr(), I64x4(*ds.stride())
     check(load().tvk_attention_bwd(C.byref(d)))
-    return dq, dk, dv
+    return (dq, dk, dv, ds) if dscores else (dq, dk, dv)
 
 
 def _strides3(t) -> tuple[int, int, int]:

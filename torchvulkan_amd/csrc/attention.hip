@@ -31,6 +31,7 @@
 // its own partial row sum l, reduced across the four lane groups once at the
 // end (l and O share every rescale factor).
 #include "gemm_common.h"
+#include "attention_any.h"
 
 #include <algorithm>
 #include <cmath>
@@ -969,8 +970,11 @@ void launch_attn_bwd(const AttnBwdArgs& a, bool causal, bool bias, int64_t batch
 
 using namespace tvk;
 
-extern "C" tvk_status tvk_attention_fwd(const tvk_attention_desc* d) {
-    if (!d) return fail(TVK_ERR_INVALID, "tvk_attention_fwd: desc is NULL");
+namespace {
+
+// The MFMA forward (float16/bfloat16, head dims 64/128, 16-byte rows);
+// TVK_ERR_UNSUPPORTED when the case is not one it takes.
+tvk_status fused_fwd(const tvk_attention_desc* d) {
     if (d->dtype != TVK_F16 && d->dtype != TVK_BF16)
         return fail(TVK_ERR_UNSUPPORTED, "tvk_attention_fwd: dtype must be float16 or bfloat16");
     if (d->batch < 0 || d->heads_q < 0 || d->heads_kv <= 0 || d->len_q < 0 || d->len_kv < 0)
@@ -1034,8 +1038,6 @@ extern "C" tvk_status tvk_attention_fwd(const tvk_attention_desc* d) {
     return TVK_OK;
 }
 
-namespace {
-
 tvk_status check_attention(const tvk_attention_desc* d, const char* who) {
     auto bad = [&](tvk_status st, const char* m) { return fail(st, std::string(who) + ": " + m); };
     if (d->dtype != TVK_F16 && d->dtype != TVK_BF16) return bad(TVK_ERR_UNSUPPORTED, "dtype must be float16 or bfloat16");
@@ -1056,10 +1058,8 @@ bool rows_ok(const void* ptr, const int64_t* st) {
     return true;
 }
 
-}  // namespace
-
-extern "C" tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc) {
-    if (!desc) return fail(TVK_ERR_INVALID, "tvk_attention_bwd: desc is NULL");
+// The MFMA backward passes; TVK_ERR_UNSUPPORTED when the case is not one they take.
+tvk_status fused_bwd(const tvk_attention_bwd_desc* desc) {
     const tvk_attention_desc* d = &desc->fwd;
     tvk_status st = check_attention(d, "tvk_attention_bwd");
     if (st != TVK_OK) return st;
@@ -1099,11 +1099,10 @@ extern "C" tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc) {
     a.group = (int)(d->heads_q / d->heads_kv);
     a.scale = (float)d->scale;
     a.c2 = a.scale * AT_LOG2E;
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    a.delta = static_cast<float*>(device_workspace(dev, (size_t)std::max<int64_t>(1, d->batch * d->heads_q * d->len_q) * 4));
-    if (!a.delta) return fail(TVK_ERR_OOM, "tvk_attention_bwd: workspace allocation failed");
     const hipStream_t s = resolve_stream(d->stream);
+    Scratch scratch;
+    a.delta = static_cast<float*>(scratch.get((size_t)std::max<int64_t>(1, d->batch * d->heads_q * d->len_q) * 4, s));
+    if (!a.delta) return fail(TVK_ERR_OOM, "tvk_attention_bwd: workspace allocation failed");
     const bool bias = d->bias != nullptr;
     if (d->dtype == TVK_F16) {
         if (d->head_dim == 64) launch_attn_bwd<TVK_F16, 64>(a, d->causal != 0, bias, d->batch, d->heads_q, d->len_q, d->len_kv, s);
@@ -1115,4 +1114,56 @@ extern "C" tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_attention_bwd: launch failed: ") + hipGetErrorString(e));
     return TVK_OK;
+}
+
+// Validation shared by both directions: every case that passes runs on the
+// device, in the MFMA kernels when they take it, else in the general kernels
+// of attention_any.hip.
+tvk_status check_any(const tvk_attention_desc* d, const char* who) {
+    auto bad = [&](tvk_status st, const std::string& m) { return fail(st, std::string(who) + ": " + m); };
+    if (d->dtype != TVK_F32 && d->dtype != TVK_F16 && d->dtype != TVK_BF16)
+        return bad(TVK_ERR_UNSUPPORTED, "dtype must be float32, float16 or bfloat16");
+    if (d->batch < 0 || d->heads_q < 0 || d->heads_kv <= 0 || d->len_q < 0 || d->len_kv < 0 || d->head_dim < 0 ||
+        d->head_dim_v < 0)
+        return bad(TVK_ERR_INVALID, "negative size");
+    if (d->heads_q % d->heads_kv != 0) return bad(TVK_ERR_INVALID, "heads_q is not a multiple of heads_kv");
+    if (!attn_any_applies(d))
+        return bad(TVK_ERR_UNSUPPORTED, "head dims above 512, or batch or heads above 65535, or sequences above 2^30");
+    return TVK_OK;
+}
+
+}  // namespace
+
+extern "C" tvk_status tvk_attention_fwd(const tvk_attention_desc* d) {
+    if (!d) return fail(TVK_ERR_INVALID, "tvk_attention_fwd: desc is NULL");
+    tvk_status st = check_any(d, "tvk_attention_fwd");
+    if (st != TVK_OK) return st;
+    if (d->batch == 0 || d->heads_q == 0 || d->len_q == 0) return TVK_OK;
+    if (!d->q || !d->k || !d->v || !d->out || !d->lse) return fail(TVK_ERR_INVALID, "tvk_attention_fwd: NULL tensor");
+    if (d->head_dim == 0 && d->len_kv > 0) return fail(TVK_ERR_UNSUPPORTED, "tvk_attention_fwd: empty head dim");
+    st = fused_fwd(d);
+    if (st != TVK_ERR_UNSUPPORTED) return st;
+    clear_error();
+    return attn_any_fwd(d, resolve_stream(d->stream));
+}
+
+extern "C" tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc) {
+    if (!desc) return fail(TVK_ERR_INVALID, "tvk_attention_bwd: desc is NULL");
+    const tvk_attention_desc* d = &desc->fwd;
+    tvk_status st = check_any(d, "tvk_attention_bwd");
+    if (st != TVK_OK) return st;
+    if (d->batch == 0 || d->heads_q == 0 || (d->len_q == 0 && d->len_kv == 0)) return TVK_OK;
+    if (!d->q || !d->k || !d->v || !d->out || !d->lse || !desc->dout || !desc->dq || !desc->dk || !desc->dv)
+        return fail(TVK_ERR_INVALID, "tvk_attention_bwd: NULL tensor");
+    if (d->head_dim == 0 || d->head_dim_v == 0) return fail(TVK_ERR_UNSUPPORTED, "tvk_attention_bwd: empty head dim");
+    if (!desc->dscores) {
+        st = fused_bwd(desc);
+        if (st != TVK_ERR_UNSUPPORTED) return st;
+        clear_error();
+    }
+    const hipStream_t s = resolve_stream(d->stream);
+    Scratch scratch;
+    float* delta = static_cast<float*>(scratch.get((size_t)std::max<int64_t>(1, d->batch * d->heads_q * d->len_q) * 4, s));
+    if (!delta) return fail(TVK_ERR_OOM, "tvk_attention_bwd: workspace allocation failed");
+    return attn_any_bwd(desc, delta, s);
 }

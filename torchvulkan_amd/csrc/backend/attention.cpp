@@ -1,9 +1,10 @@
-// Fused scaled dot-product attention on the vulkan device: the overrideable
-// SDPA backend the reference registers (src/api/ops/attention.cpp:667-761).
-// The forward runs tvk_attention_fwd and the backward tvk_attention_bwd. A
-// requested bias gradient, or a shape the kernels decline, takes the
-// reference's chunked path (attention.cpp:115-199) in float32 on the host,
-// with the fallback warning (an error under TORCHVULKAN_STRICT=1).
+// Scaled dot-product attention on the vulkan device: the overrideable SDPA
+// backend the reference registers (src/api/ops/attention.cpp:667-761).
+// Every case runs on the device through tvk_attention_fwd / tvk_attention_bwd:
+// the MFMA kernels for float16/bfloat16 with head dims 64/128, the library's
+// general kernels for float32, other head dims, any strides, and the score
+// gradient that gives the bias gradient (summed here over the bias's
+// broadcast dimensions with the device sum).
 #include "common.h"
 
 #include <ATen/Context.h>
@@ -13,67 +14,113 @@
 
 #include <cmath>
 #include <cstring>
-#include <limits>
 
 namespace tvkb {
 namespace {
 
-struct Attn {
+// Sizes of one attention call and its operands in [batch, heads, rows, dim]
+// form (key/value heads may be fewer: grouped-query attention).
+struct Sdpa {
     at::Tensor q, k, v, bias;
-    int64_t B = 0, Hq = 0, Hk = 0, L = 0, S = 0, D = 0, Dv = 0, group = 1;
+    int64_t batch = 0, heads = 0, kv_heads = 0, len_q = 0, len_kv = 0, dim = 0, dim_v = 0;
     bool causal = false;
     double scale = 1.0;
 };
 
-// prepare_attention (src/api/ops/attention.cpp:44-82), with its messages
-Attn prepare(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& bias, bool causal,
-             std::optional<double> scale) {
+// The operands' shape rules and messages are the reference's prepare_attention
+// (src/api/ops/attention.cpp:44-82); the scale defaults to 1/sqrt(head dim).
+Sdpa describe(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& bias, bool causal,
+              std::optional<double> scale) {
     TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4,
                 "torchvulkan [ERROR]: fused attention takes 4D query, key and value, got ", q.sizes(), ", ", k.sizes(),
                 " and ", v.sizes(), ".");
-    Attn a;
-    a.q = q;
-    a.k = k;
-    a.v = v;
-    a.B = q.size(0);
-    a.Hq = q.size(1);
-    a.Hk = k.size(1);
-    a.L = q.size(2);
-    a.S = k.size(2);
-    a.D = q.size(3);
-    a.Dv = v.size(3);
-    TORCH_CHECK(k.size(0) == a.B && v.size(0) == a.B && v.size(1) == a.Hk && v.size(2) == a.S && k.size(3) == a.D,
-                "torchvulkan [ERROR]: attention shapes don't match: query ", q.sizes(), ", key ", k.sizes(), ", value ",
-                v.sizes(), ".");
-    TORCH_CHECK(a.Hk > 0 && a.Hq % a.Hk == 0, "torchvulkan [ERROR]: the number of query heads (", a.Hq,
-                ") must be a multiple of the key/value heads (", a.Hk, ").");
-    a.group = a.Hq / a.Hk;
-    a.causal = causal;
-    a.scale = scale.has_value() ? *scale : 1.0 / std::sqrt(static_cast<double>(a.D));
-    if (bias.defined()) a.bias = bias.scalar_type() == q.scalar_type() ? bias : bias.to(q.scalar_type());
-    return a;
+    Sdpa s;
+    s.batch = q.size(0);
+    s.heads = q.size(1);
+    s.len_q = q.size(2);
+    s.dim = q.size(3);
+    s.kv_heads = k.size(1);
+    s.len_kv = k.size(2);
+    s.dim_v = v.size(3);
+    const bool match = k.size(0) == s.batch && v.size(0) == s.batch && v.size(1) == s.kv_heads && v.size(2) == s.len_kv &&
+                       k.size(3) == s.dim;
+    TORCH_CHECK(match, "torchvulkan [ERROR]: attention shapes don't match: query ", q.sizes(), ", key ", k.sizes(),
+                ", value ", v.sizes(), ".");
+    TORCH_CHECK(s.kv_heads > 0 && s.heads % s.kv_heads == 0, "torchvulkan [ERROR]: the number of query heads (", s.heads,
+                ") must be a multiple of the key/value heads (", s.kv_heads, ").");
+    s.q = q;
+    s.k = k;
+    s.v = v;
+    if (bias.defined()) s.bias = bias.scalar_type() == q.scalar_type() ? bias : bias.to(q.scalar_type());
+    s.causal = causal;
+    s.scale = scale.has_value() ? *scale : 1.0 / std::sqrt((double)s.dim);
+    return s;
 }
 
-bool kernel_takes(at::ScalarType dt, int64_t D, int64_t Dv, int64_t B, int64_t Hq) {
-    return (dt == at::kHalf || dt == at::kBFloat16) && D == Dv && (D == 64 || D == 128) && B <= 65535 && Hq <= 65535;
+bool device_dtype(at::ScalarType dt) { return dt == at::kFloat || dt == at::kHalf || dt == at::kBFloat16; }
+
+// Shapes the library's kernels take (its general kernels: head dims up to 512,
+// batch and heads up to 65535).
+bool library_takes(at::ScalarType dt, int64_t dim, int64_t dim_v, int64_t batch, int64_t heads) {
+    return device_dtype(dt) && dim >= 1 && dim <= 512 && dim_v >= 1 && dim_v <= 512 && batch <= 65535 && heads <= 65535;
 }
 
-// unit stride along the head dimension and 16-byte rows, else a dense copy
-at::Tensor kernel_layout(const at::Tensor& t) {
-    auto ok = [&]() {
-        if (t.stride(3) != 1 || reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 != 0) return false;
-        for (int i = 0; i < 3; ++i)
-            if (t.size(i) > 1 && t.stride(i) % 8 != 0) return false;
-        return true;
-    };
-    return ok() ? t : t.contiguous();
+// The MFMA kernels want unit stride along the head dim and 16-byte rows: for
+// their shapes an operand without that layout is worth one dense copy.
+at::Tensor mfma_layout(const at::Tensor& t, const Sdpa& s) {
+    const bool mfma = (t.scalar_type() == at::kHalf || t.scalar_type() == at::kBFloat16) && s.dim == s.dim_v &&
+                      (s.dim == 64 || s.dim == 128);
+    if (!mfma) return t;
+    bool ok = t.stride(3) == 1 && reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0;
+    for (int i = 0; i < 3; ++i) ok = ok && (t.size(i) <= 1 || t.stride(i) % 8 == 0);
+    return ok ? t : t.contiguous();
 }
 
-// attention_output (src/api/ops/attention.cpp:413-418): [B, L, Hq, Dv]
-// underneath when the query is laid out that way, so merging heads is a view
-at::Tensor attention_output(const Attn& a) {
-    if (a.q.stride(1) < a.q.stride(2)) return at::empty({a.B, a.L, a.Hq, a.Dv}, a.q.options()).transpose(1, 2);
-    return at::empty({a.B, a.Hq, a.L, a.Dv}, a.q.options());
+// The output is laid out [batch, len_q, heads, dim_v] underneath when the
+// query is (the projection's layout), so merging heads afterwards is a view;
+// the reference picks its output the same way (attention.cpp:413-418).
+at::Tensor new_output(const Sdpa& s) {
+    if (s.q.stride(1) < s.q.stride(2))
+        return at::empty({s.batch, s.len_q, s.heads, s.dim_v}, s.q.options()).transpose(1, 2);
+    return at::empty({s.batch, s.heads, s.len_q, s.dim_v}, s.q.options());
+}
+
+void strides4(const at::Tensor& t, int64_t* out) {
+    for (int i = 0; i < 4; ++i) out[i] = t.stride(i);
+}
+
+tvk_attention_desc forward_desc(const Sdpa& s, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                const at::Tensor& out, const at::Tensor& lse) {
+    tvk_attention_desc d;
+    std::memset(&d, 0, sizeof(d));
+    bool ok = false;
+    d.dtype = tvk_dtype_of(q.scalar_type(), ok);
+    d.causal = s.causal ? 1 : 0;
+    d.batch = s.batch;
+    d.heads_q = s.heads;
+    d.heads_kv = s.kv_heads;
+    d.len_q = s.len_q;
+    d.len_kv = s.len_kv;
+    d.head_dim = s.dim;
+    d.head_dim_v = s.dim_v;
+    d.q = q.data_ptr();
+    d.k = k.data_ptr();
+    d.v = v.data_ptr();
+    strides4(q, d.q_stride);
+    strides4(k, d.k_stride);
+    strides4(v, d.v_stride);
+    if (s.bias.defined()) {
+        const at::Tensor b = s.bias.expand({s.batch, s.heads, s.len_q, s.len_kv});
+        d.bias = b.data_ptr();
+        strides4(b, d.bias_stride);
+    }
+    d.out = out.data_ptr();
+    strides4(out, d.out_stride);
+    d.lse = lse.data_ptr<float>();
+    for (int i = 0; i < 3; ++i) d.lse_stride[i] = lse.stride(i);
+    d.scale = s.scale;
+    d.stream = stream_of(q);
+    return d;
 }
 
 int64_t sdp_choice(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
@@ -92,59 +139,16 @@ int64_t sdp_choice(const at::Tensor& query, const at::Tensor& key, const at::Ten
     if (key.size(0) != query.size(0) || value.size(0) != query.size(0) || value.size(1) != kv_heads) return math;
     if (key.size(2) != value.size(2) || key.size(3) != query.size(3)) return math;
     if (heads != kv_heads && !(enable_gqa && kv_heads > 0 && heads % kv_heads == 0)) return math;
-    // the fused kernel's shapes; everything else runs the math decomposition
-    if (!kernel_takes(dt, query.size(3), value.size(3), query.size(0), heads)) return math;
+    if (!library_takes(dt, query.size(3), value.size(3), query.size(0), heads)) return math;
     return static_cast<int64_t>(at::SDPBackend::overrideable);
 }
 
-at::Tensor by_kv_head(const at::Tensor& t, const Attn& a) {
-    return t.reshape({a.B, a.Hk, a.group * t.size(2), t.size(3)});
-}
-
-// chunked_scores (src/api/ops/attention.cpp:101-113) over all rows, float32 on the host
-at::Tensor host_scores(const Attn& a, const at::Tensor& q, const at::Tensor& k, const at::Tensor& bias) {
-    at::Tensor s = at::matmul(by_kv_head(q, a), k.transpose(-2, -1)).reshape({a.B, a.Hq, a.L, a.S}).mul(a.scale);
-    if (bias.defined()) s = s.add(bias);
-    if (a.causal) {
-        at::Tensor row = at::arange(a.L, at::kLong).unsqueeze(1);
-        at::Tensor col = at::arange(a.S, at::kLong).unsqueeze(0);
-        s = at::where(col.gt(row), at::scalar_tensor(-std::numeric_limits<double>::infinity(), s.options()), s);
-    }
-    return s;
-}
-
-// The forward descriptor over kernel-layout q, k, v (bias broadcast to [B, Hq, L, S]).
-tvk_attention_desc forward_desc(const Attn& a, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                                const at::Tensor& bias, const at::Tensor& out, const at::Tensor& lse) {
-    tvk_attention_desc d;
-    std::memset(&d, 0, sizeof(d));
-    bool ok = false;
-    d.dtype = tvk_dtype_of(a.q.scalar_type(), ok);
-    d.causal = a.causal ? 1 : 0;
-    d.batch = a.B;
-    d.heads_q = a.Hq;
-    d.heads_kv = a.Hk;
-    d.len_q = a.L;
-    d.len_kv = a.S;
-    d.head_dim = a.D;
-    d.head_dim_v = a.Dv;
-    for (int i = 0; i < 4; ++i) {
-        d.q_stride[i] = q.stride(i);
-        d.k_stride[i] = k.stride(i);
-        d.v_stride[i] = v.stride(i);
-        d.bias_stride[i] = bias.defined() ? bias.stride(i) : 0;
-        d.out_stride[i] = out.stride(i);
-    }
-    for (int i = 0; i < 3; ++i) d.lse_stride[i] = lse.stride(i);
-    d.q = q.data_ptr();
-    d.k = k.data_ptr();
-    d.v = v.data_ptr();
-    d.bias = bias.defined() ? bias.data_ptr() : nullptr;
-    d.out = out.data_ptr();
-    d.lse = lse.data_ptr<float>();
-    d.scale = a.scale;
-    d.stream = stream_of(q);
-    return d;
+void require_library(const Sdpa& s) {
+    TORCH_CHECK(library_takes(s.q.scalar_type(), s.dim, s.dim_v, s.batch, s.heads),
+                "torchvulkan [ERROR]: fused attention runs float32, float16 and bfloat16 with head dims from 1 to 512 and "
+                "batch and heads up to 65535; got ",
+                s.q.scalar_type(), " with head dims ", s.dim, "/", s.dim_v, ". scaled_dot_product_attention routes "
+                "other cases to its math backend.");
 }
 
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, c10::SymInt, c10::SymInt, at::Tensor, at::Tensor, at::Tensor>
@@ -152,38 +156,17 @@ sdpa_forward(const at::Tensor& query, const at::Tensor& key, const at::Tensor& v
              const std::optional<at::Tensor>& attn_bias, double dropout_p, bool is_causal, bool /*return_debug_mask*/,
              std::optional<double> scale) {
     TORCH_CHECK(dropout_p == 0.0, "torchvulkan [ERROR]: fused attention doesn't support dropout; it runs on the math backend.");
-    Attn a = prepare(query, key, value, attn_bias.has_value() ? *attn_bias : at::Tensor(), is_causal, scale);
-    at::Tensor out = attention_output(a);
-    at::Tensor lse = at::empty({a.B, a.Hq, a.L}, a.q.options().dtype(at::kFloat));
-    tvk_status st = TVK_ERR_UNSUPPORTED;
-    if (kernel_takes(a.q.scalar_type(), a.D, a.Dv, a.B, a.Hq) && a.B * a.Hq * a.L > 0) {
-        const at::Tensor q = kernel_layout(a.q), k = kernel_layout(a.k), v = kernel_layout(a.v);
-        at::Tensor bias = a.bias.defined() ? a.bias.expand({a.B, a.Hq, a.L, a.S}) : at::Tensor();
-        tvk_attention_desc d = forward_desc(a, q, k, v, bias, out, lse);
-        st = tvk_attention_fwd(&d);
-        if (st != TVK_ERR_UNSUPPORTED) check_status(st, "tvk_attention_fwd");
-    } else if (a.B * a.Hq * a.L == 0) {
-        st = TVK_OK;
-    }
-    if (st == TVK_ERR_UNSUPPORTED) {
-        // chunked_forward (src/api/ops/attention.cpp:115-139) in float32 on the host
-        TVKB_FALLBACK("This attention shape can't run on the device kernel. Falling back to CPU.");
-        const double inf = std::numeric_limits<double>::infinity();
-        at::Tensor q = a.q.cpu().to(at::kFloat), k = a.k.cpu().to(at::kFloat), v = a.v.cpu().to(at::kFloat);
-        at::Tensor bias = a.bias.defined() ? a.bias.cpu().to(at::kFloat).expand({a.B, a.Hq, a.L, a.S}) : at::Tensor();
-        at::Tensor s = host_scores(a, q, k, bias);
-        at::Tensor mx = at::amax(s, {-1}, true);
-        at::Tensor safe = at::where(mx.eq(-inf), at::scalar_tensor(0.0, mx.options()), mx);
-        at::Tensor p = at::exp(s.sub(safe));
-        at::Tensor sum = p.sum({-1}, true);
-        at::Tensor empty = sum.eq(0.0);
-        at::Tensor o = at::matmul(by_kv_head(p, a), v).reshape({a.B, a.Hq, a.L, a.Dv});
-        o = o.div(at::where(empty, at::scalar_tensor(1.0, o.options()), sum));
-        out.copy_(o);
-        lse.copy_(at::where(empty, at::scalar_tensor(inf, sum.options()), safe.add(sum.log())).squeeze(-1));
+    Sdpa s = describe(query, key, value, attn_bias.has_value() ? *attn_bias : at::Tensor(), is_causal, scale);
+    at::Tensor out = new_output(s);
+    at::Tensor lse = at::empty({s.batch, s.heads, s.len_q}, s.q.options().dtype(at::kFloat));
+    if (s.batch * s.heads * s.len_q > 0) {
+        require_library(s);
+        const at::Tensor q = mfma_layout(s.q, s), k = mfma_layout(s.k, s), v = mfma_layout(s.v, s);
+        tvk_attention_desc d = forward_desc(s, q, k, v, out, lse);
+        check_status(tvk_attention_fwd(&d), "tvk_attention_fwd");
     }
     at::Tensor philox = at::empty({}, at::TensorOptions().dtype(at::kLong));
-    return {out, lse, at::Tensor(), at::Tensor(), c10::SymInt(a.L), c10::SymInt(a.S), philox, philox.clone(),
+    return {out, lse, at::Tensor(), at::Tensor(), c10::SymInt(s.len_q), c10::SymInt(s.len_kv), philox, philox.clone(),
             at::empty({0}, query.options())};
 }
 
@@ -194,57 +177,43 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> sdpa_backward(
     double dropout_p, bool is_causal, const at::Tensor& /*philox_seed*/, const at::Tensor& /*philox_offset*/,
     std::optional<double> scale) {
     TORCH_CHECK(dropout_p == 0.0, "torchvulkan [ERROR]: fused attention doesn't support dropout; it runs on the math backend.");
-    Attn a = prepare(query, key, value, attn_bias, is_causal, scale);
+    Sdpa s = describe(query, key, value, attn_bias, is_causal, scale);
     if (!grad_input_mask[0] && !grad_input_mask[1] && !grad_input_mask[2] && !grad_input_mask[3]) return {};
+    const at::ScalarType dt = s.q.scalar_type();
+    at::Tensor gq = at::empty({s.batch, s.heads, s.len_q, s.dim}, s.q.options());
+    at::Tensor gk = at::empty({s.batch, s.kv_heads, s.len_kv, s.dim}, s.q.options());
+    at::Tensor gv = at::empty({s.batch, s.kv_heads, s.len_kv, s.dim_v}, s.q.options());
     const bool want_bias = grad_input_mask[3] && attn_bias.defined();
-    if (!want_bias && kernel_takes(a.q.scalar_type(), a.D, a.Dv, a.B, a.Hq) && out.scalar_type() == a.q.scalar_type()) {
-        const at::Tensor q = kernel_layout(a.q), k = kernel_layout(a.k), v = kernel_layout(a.v);
-        const at::Tensor dout = kernel_layout(grad_out.scalar_type() == a.q.scalar_type() ? grad_out : grad_out.to(a.q.scalar_type()));
-        at::Tensor bias = a.bias.defined() ? a.bias.expand({a.B, a.Hq, a.L, a.S}) : at::Tensor();
+    at::Tensor dscores;
+    if (want_bias) dscores = at::empty({s.batch, s.heads, s.len_q, s.len_kv}, s.q.options().dtype(at::kFloat));
+    if (s.batch * s.heads * (s.len_q + s.len_kv) > 0) {
+        require_library(s);
+        const at::Tensor q = mfma_layout(s.q, s), k = mfma_layout(s.k, s), v = mfma_layout(s.v, s);
+        const at::Tensor dout = mfma_layout(grad_out.scalar_type() == dt ? grad_out : grad_out.to(dt), s);
+        const at::Tensor o = out.scalar_type() == dt ? out : out.to(dt);
         const at::Tensor lse = logsumexp.scalar_type() == at::kFloat ? logsumexp : logsumexp.to(at::kFloat);
-        at::Tensor gq = at::empty({a.B, a.Hq, a.L, a.D}, a.q.options());
-        at::Tensor gk = at::empty({a.B, a.Hk, a.S, a.D}, a.q.options());
-        at::Tensor gv = at::empty({a.B, a.Hk, a.S, a.Dv}, a.q.options());
         tvk_attention_bwd_desc bd;
         std::memset(&bd, 0, sizeof(bd));
-        bd.fwd = forward_desc(a, q, k, v, bias, out, lse);
+        bd.fwd = forward_desc(s, q, k, v, o, lse);
         bd.dout = dout.data_ptr();
+        strides4(dout, bd.dout_stride);
         bd.dq = gq.data_ptr();
+        strides4(gq, bd.dq_stride);
         bd.dk = gk.data_ptr();
+        strides4(gk, bd.dk_stride);
         bd.dv = gv.data_ptr();
-        for (int i = 0; i < 4; ++i) {
-            bd.dout_stride[i] = dout.stride(i);
-            bd.dq_stride[i] = gq.stride(i);
-            bd.dk_stride[i] = gk.stride(i);
-            bd.dv_stride[i] = gv.stride(i);
+        strides4(gv, bd.dv_stride);
+        if (want_bias) {
+            bd.dscores = dscores.data_ptr<float>();
+            strides4(dscores, bd.dscores_stride);
         }
-        const tvk_status st = tvk_attention_bwd(&bd);
-        if (st != TVK_ERR_UNSUPPORTED) {
-            check_status(st, "tvk_attention_bwd");
-            return {gq, gk, gv, at::Tensor()};
-        }
+        check_status(tvk_attention_bwd(&bd), "tvk_attention_bwd");
+    } else if (want_bias) {
+        dscores.zero_();
     }
-    TVKB_FALLBACK("This attention backward runs on the CPU.");
-    // chunked_backward (src/api/ops/attention.cpp:141-199) over all rows
-    at::Tensor q = a.q.cpu().to(at::kFloat), k = a.k.cpu().to(at::kFloat), v = a.v.cpu().to(at::kFloat);
-    at::Tensor dout = grad_out.cpu().to(at::kFloat);
-    at::Tensor bias = a.bias.defined() ? a.bias.cpu().to(at::kFloat).expand({a.B, a.Hq, a.L, a.S}) : at::Tensor();
-    at::Tensor delta = at::sum(dout.mul(out.cpu().to(at::kFloat)), {-1}, true);
-    at::Tensor log_sum = logsumexp.cpu().to(at::kFloat).unsqueeze(-1);
-    at::Tensor s = host_scores(a, q, k, bias);
-    at::Tensor p = at::exp(s.sub(log_sum));
-    at::Tensor dout_g = by_kv_head(dout, a);
-    at::Tensor grad_v = at::matmul(by_kv_head(p, a).transpose(-2, -1), dout_g);
-    at::Tensor dp = at::matmul(dout_g, v.transpose(-2, -1)).reshape({a.B, a.Hq, a.L, a.S});
-    at::Tensor ds = p.mul(dp.sub(delta));
-    at::Tensor dsg = by_kv_head(ds, a);
-    at::Tensor grad_q = at::matmul(dsg, k).reshape({a.B, a.Hq, a.L, a.D}).mul(a.scale);
-    at::Tensor grad_k = at::matmul(dsg.transpose(-2, -1), by_kv_head(q, a)).mul(a.scale);
-    at::Tensor grad_bias;
-    if (want_bias) grad_bias = at::sum_to(ds, a.bias.sizes()).to(a.bias.scalar_type()).to(query.device());
-    const at::ScalarType dt = a.q.scalar_type();
-    return {grad_q.to(dt).to(query.device()), grad_k.to(dt).to(query.device()), grad_v.to(dt).to(query.device()),
-            grad_bias};
+    at::Tensor gbias;
+    if (want_bias) gbias = at::sum_to(dscores, s.bias.sizes()).to(attn_bias.scalar_type());
+    return {gq, gk, gv, gbias};
 }
 
 }  // namespace

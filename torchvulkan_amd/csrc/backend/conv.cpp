@@ -11,6 +11,8 @@
 // fallback path with the reference's warning.
 #include "common.h"
 
+#include <ATen/native/Resize.h>
+
 namespace tvkb {
 namespace {
 
@@ -171,10 +173,201 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward(
     return {gi, gw, gb};
 }
 
+// The legacy convolution entry points (slow_conv_transpose2d/3d,
+// slow_conv_dilated2d/3d, _slow_conv2d_forward, slow_conv3d_forward,
+// _conv_depthwise2d, conv_depthwise3d, and their .out forms) carry an explicit
+// kernel_size and some omit dilation, output padding or groups. Each is one
+// convolution() call with the omitted parameters at their neutral values;
+// depthwise means one group per input channel. The reference registers the
+// same set onto its convolution (src/api/ops/conv.cpp:1305-1320).
+struct LegacyConv {
+    bool transposed = false;
+    bool depthwise = false;
+};
+
+at::Tensor legacy_conv(const LegacyConv& kind, const at::Tensor& self, const at::Tensor& weight, c10::SymIntArrayRef kernel_size,
+                       const std::optional<at::Tensor>& bias, c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
+                       c10::SymIntArrayRef dilation, c10::SymIntArrayRef output_padding) {
+    const std::vector<int64_t> ks = ints(kernel_size);
+    const std::vector<int64_t> wk(weight.sizes().begin() + std::min<int64_t>(2, weight.dim()), weight.sizes().end());
+    TORCH_CHECK(ks == wk, "kernel_size ", c10::IntArrayRef(ks), " must match weight spatial dimensions ", c10::IntArrayRef(wk));
+    const size_t nd = ks.size();
+    std::vector<c10::SymInt> ones(nd, c10::SymInt(1)), zeros(nd, c10::SymInt(0));
+    const int64_t groups = kind.depthwise ? self.size(1) : 1;
+    return convolution(self, weight, bias, stride, padding, dilation.empty() ? c10::SymIntArrayRef(ones) : dilation,
+                       kind.transposed, output_padding.empty() ? c10::SymIntArrayRef(zeros) : output_padding, c10::SymInt(groups));
+}
+
+at::Tensor& legacy_out(at::Tensor& out, const at::Tensor& res) {
+    at::native::resize_output(out, res.sizes());
+    out.copy_(res);
+    return out;
+}
+
+// im2col / col2im (the unfold and fold ops; the reference's versions are
+// src/api/ops/conv.cpp:115-185), with torch's CPU checks and messages. Both
+// run on the device with the copy, fill and add kernels: im2col zero-pads the
+// image once and copies the strided window view [n, c, kh, kw, oh, ow] of the
+// padded image into the dense column tensor; col2im adds each tap's column
+// block into the matching strided view of a zeroed padded image (a tap's view
+// holds every output pixel at most once, so each add is one pass with no
+// write collisions) in tap order, then crops the padding.
+void unfold_param_checks(at::IntArrayRef k, at::IntArrayRef d, at::IntArrayRef p, at::IntArrayRef s) {
+    TORCH_CHECK(k.size() == 2, "It is expected kernel_size equals to 2, but got size ", k.size());
+    TORCH_CHECK(d.size() == 2, "It is expected dilation equals to 2, but got size ", d.size());
+    TORCH_CHECK(p.size() == 2, "It is expected padding equals to 2, but got size ", p.size());
+    TORCH_CHECK(s.size() == 2, "It is expected stride equals to 2, but got size ", s.size());
+    TORCH_CHECK(k[0] > 0 && k[1] > 0, "kernel size should be greater than zero, but got kernel_height: ", k[0],
+                " kernel_width: ", k[1]);
+    TORCH_CHECK(s[0] > 0 && s[1] > 0, "stride should be greater than zero, but got stride_height: ", s[0],
+                " stride_width: ", s[1]);
+    TORCH_CHECK(d[0] > 0 && d[1] > 0, "dilation should be greater than zero, but got dilation_height: ", d[0],
+                " dilation_width: ", d[1]);
+    TORCH_CHECK(p[0] >= 0 && p[1] >= 0, "padding should be non-negative, but got pad_height: ", p[0], " pad_width: ", p[1]);
+}
+
+int64_t sliding_blocks(int64_t size, int64_t k, int64_t d, int64_t p, int64_t s) {
+    const int64_t span = size + 2 * p - d * (k - 1) - 1;
+    return (span < 0 ? -((-span + s - 1) / s) : span / s) + 1;   // floor division, as torch's div_rtn
+}
+
+at::Tensor im2col_vk(const at::Tensor& self, at::IntArrayRef k, at::IntArrayRef d, at::IntArrayRef p, at::IntArrayRef s) {
+    unfold_param_checks(k, d, p, s);
+    const int64_t nd = self.dim();
+    const bool valid = (nd == 3 && self.numel() != 0) || (nd == 4 && self.size(1) != 0 && self.size(2) != 0 && self.size(3) != 0);
+    TORCH_CHECK(valid, "Expected 3D or 4D (batch mode) tensor with possibly 0 batch size and other non-zero dimensions for input, but got: ",
+                self.sizes());
+    const at::Tensor x = nd == 4 ? self : self.unsqueeze(0);
+    const int64_t n = x.size(0), c = x.size(1), h = x.size(2), w = x.size(3);
+    const int64_t oh = sliding_blocks(h, k[0], d[0], p[0], s[0]), ow = sliding_blocks(w, k[1], d[1], p[1], s[1]);
+    // (the CPU's message repeats the input height)
+    TORCH_CHECK(oh >= 1 && ow >= 1, "Given input with spatial size (", h, ", ", h, "), kernel_size=(", k[0], ", ", k[1],
+                "), dilation=(", d[0], ", ", d[1], "), padding=(", p[0], ", ", p[1],
+                "), calculated shape of the array of sliding blocks as (", oh, ", ", ow,
+                "), but its components must be at least one.");
+    const int64_t hp = h + 2 * p[0], wp = w + 2 * p[1];
+    at::Tensor padded;
+    if (p[0] == 0 && p[1] == 0) {
+        padded = x.contiguous();
+    } else {
+        padded = at::zeros({n, c, hp, wp}, x.options());
+        padded.narrow(2, p[0], h).narrow(3, p[1], w).copy_(x);
+    }
+    at::Tensor cols = at::empty({n, c * k[0] * k[1], oh * ow}, x.options());
+    if (cols.numel() != 0) {
+        const at::Tensor windows = padded.as_strided({n, c, k[0], k[1], oh, ow},
+                                                     {c * hp * wp, hp * wp, d[0] * wp, d[1], s[0] * wp, s[1]});
+        cols.view({n, c, k[0], k[1], oh, ow}).copy_(windows);
+    }
+    return nd == 4 ? cols : cols.squeeze(0);
+}
+
+at::Tensor col2im_vk(const at::Tensor& self, c10::SymIntArrayRef output_size, at::IntArrayRef k, at::IntArrayRef d,
+                     at::IntArrayRef p, at::IntArrayRef s) {
+    const std::vector<int64_t> os = ints(output_size);
+    TORCH_CHECK(os.size() == 2, "It is expected output_size equals to 2, but got size ", os.size());
+    unfold_param_checks(k, d, p, s);
+    const int64_t nd = self.dim();
+    TORCH_CHECK((nd == 2 && self.size(0) != 0 && self.size(1) != 0) || (nd == 3 && self.size(1) != 0 && self.size(2) != 0),
+                "Expected 2D or 3D (batch mode) tensor for input with possibly 0 batch size and non-zero dimensions for input, but got: ",
+                self.sizes());
+    const at::Tensor cols = nd == 3 ? self : self.unsqueeze(0);
+    const int64_t planes = cols.size(1), length = cols.size(2);
+    TORCH_CHECK(planes % (k[0] * k[1]) == 0,
+                "Expected size of input's dimension 1 to be divisible by the product of kernel_size, but got input.size(1)=",
+                planes, " and kernel_size=(", k[0], ", ", k[1], ").");
+    const int64_t oh = sliding_blocks(os[0], k[0], d[0], p[0], s[0]), ow = sliding_blocks(os[1], k[1], d[1], p[1], s[1]);
+    TORCH_CHECK(length == oh * ow, "Given output_size=(", os[0], ", ", os[1], "), kernel_size=(", k[0], ", ", k[1],
+                "), dilation=(", d[0], ", ", d[1], "), padding=(", p[0], ", ", p[1], "), stride=(", s[0], ", ", s[1],
+                "), expected size of input's dimension 2 to match the calculated number of sliding blocks ", oh, " * ", ow,
+                " = ", oh * ow, ", but got input.size(2)=", length, ".");
+    TORCH_CHECK(oh >= 1 && ow >= 1, "Given output_size=(", os[0], ", ", os[1], "), kernel_size=(", k[0], ", ", k[1],
+                "), dilation=(", d[0], ", ", d[1], "), padding=(", p[0], ", ", p[1], "), stride=(", s[0], ", ", s[1],
+                "), calculated shape of the array of sliding blocks as (", oh, ", ", ow, "), which is too small (non-positive)");
+    TORCH_CHECK(os[0] >= 1 && os[1] >= 1, "Expected output spatial size to be positive, but got: output_size=(", os[0], ", ",
+                os[1], ").");
+    const int64_t n = cols.size(0), c = planes / (k[0] * k[1]);
+    const int64_t hp = os[0] + 2 * p[0], wp = os[1] + 2 * p[1];
+    at::Tensor image = at::zeros({n, c, hp, wp}, cols.options());
+    if (n != 0) {
+        const at::Tensor taps = cols.contiguous().view({n, c, k[0], k[1], oh, ow});
+        for (int64_t i = 0; i < k[0]; ++i)
+            for (int64_t j = 0; j < k[1]; ++j) {
+                at::Tensor dst = image.as_strided({n, c, oh, ow}, {c * hp * wp, hp * wp, s[0] * wp, s[1]},
+                                                  i * d[0] * wp + j * d[1]);
+                dst.add_(taps.select(2, i).select(2, j));
+            }
+    }
+    if (p[0] != 0 || p[1] != 0) image = image.narrow(2, p[0], os[0]).narrow(3, p[1], os[1]).contiguous();
+    return nd == 3 ? image : image.squeeze(0);
+}
+
+at::Tensor& im2col_out_vk(const at::Tensor& self, at::IntArrayRef k, at::IntArrayRef d, at::IntArrayRef p, at::IntArrayRef s,
+                          at::Tensor& out) {
+    return legacy_out(out, im2col_vk(self, k, d, p, s));
+}
+
+at::Tensor& col2im_out_vk(const at::Tensor& self, c10::SymIntArrayRef output_size, at::IntArrayRef k, at::IntArrayRef d,
+                          at::IntArrayRef p, at::IntArrayRef s, at::Tensor& out) {
+    return legacy_out(out, col2im_vk(self, output_size, k, d, p, s));
+}
+
+at::Tensor slow_conv_transpose(const at::Tensor& self, const at::Tensor& weight, c10::SymIntArrayRef kernel_size,
+                               const std::optional<at::Tensor>& bias, c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
+                               c10::SymIntArrayRef output_padding, c10::SymIntArrayRef dilation) {
+    return legacy_conv({true, false}, self, weight, kernel_size, bias, stride, padding, dilation, output_padding);
+}
+at::Tensor& slow_conv_transpose_out(const at::Tensor& self, const at::Tensor& weight, c10::SymIntArrayRef kernel_size,
+                                    const std::optional<at::Tensor>& bias, c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
+                                    c10::SymIntArrayRef output_padding, c10::SymIntArrayRef dilation, at::Tensor& out) {
+    return legacy_out(out, slow_conv_transpose(self, weight, kernel_size, bias, stride, padding, output_padding, dilation));
+}
+at::Tensor slow_conv_dilated(const at::Tensor& self, const at::Tensor& weight, c10::SymIntArrayRef kernel_size,
+                             const std::optional<at::Tensor>& bias, c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
+                             c10::SymIntArrayRef dilation) {
+    return legacy_conv({false, false}, self, weight, kernel_size, bias, stride, padding, dilation, {});
+}
+at::Tensor& slow_conv_dilated_out(const at::Tensor& self, const at::Tensor& weight, c10::SymIntArrayRef kernel_size,
+                                  const std::optional<at::Tensor>& bias, c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
+                                  c10::SymIntArrayRef dilation, at::Tensor& out) {
+    return legacy_out(out, slow_conv_dilated(self, weight, kernel_size, bias, stride, padding, dilation));
+}
+at::Tensor slow_conv_forward(const at::Tensor& self, const at::Tensor& weight, c10::SymIntArrayRef kernel_size,
+                             const std::optional<at::Tensor>& bias, c10::SymIntArrayRef stride, c10::SymIntArrayRef padding) {
+    return legacy_conv({false, false}, self, weight, kernel_size, bias, stride, padding, {}, {});
+}
+at::Tensor& slow_conv_forward_out(const at::Tensor& self, const at::Tensor& weight, c10::SymIntArrayRef kernel_size,
+                                  const std::optional<at::Tensor>& bias, c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
+                                  at::Tensor& out) {
+    return legacy_out(out, slow_conv_forward(self, weight, kernel_size, bias, stride, padding));
+}
+at::Tensor conv_depthwise(const at::Tensor& self, const at::Tensor& weight, c10::SymIntArrayRef kernel_size,
+                          const std::optional<at::Tensor>& bias, c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
+                          c10::SymIntArrayRef dilation) {
+    return legacy_conv({false, true}, self, weight, kernel_size, bias, stride, padding, dilation, {});
+}
+at::Tensor& conv_depthwise_out(const at::Tensor& self, const at::Tensor& weight, c10::SymIntArrayRef kernel_size,
+                               const std::optional<at::Tensor>& bias, c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
+                               c10::SymIntArrayRef dilation, at::Tensor& out) {
+    return legacy_out(out, conv_depthwise(self, weight, kernel_size, bias, stride, padding, dilation));
+}
+
 }  // namespace
 }  // namespace tvkb
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
     m.impl("convolution_overrideable", &tvkb::convolution);
     m.impl("convolution_backward_overrideable", &tvkb::convolution_backward);
+    m.impl("im2col", &tvkb::im2col_vk);
+    m.impl("im2col.out", &tvkb::im2col_out_vk);
+    m.impl("col2im", &tvkb::col2im_vk);
+    m.impl("col2im.out", &tvkb::col2im_out_vk);
+    for (const char* name : {"slow_conv_transpose2d", "slow_conv_transpose3d"}) m.impl(name, &tvkb::slow_conv_transpose);
+    for (const char* name : {"slow_conv_transpose2d.out", "slow_conv_transpose3d.out"}) m.impl(name, &tvkb::slow_conv_transpose_out);
+    for (const char* name : {"slow_conv_dilated2d", "slow_conv_dilated3d"}) m.impl(name, &tvkb::slow_conv_dilated);
+    for (const char* name : {"slow_conv_dilated2d.out", "slow_conv_dilated3d.out"}) m.impl(name, &tvkb::slow_conv_dilated_out);
+    for (const char* name : {"_slow_conv2d_forward", "slow_conv3d_forward"}) m.impl(name, &tvkb::slow_conv_forward);
+    for (const char* name : {"_slow_conv2d_forward.output", "slow_conv3d_forward.output"}) m.impl(name, &tvkb::slow_conv_forward_out);
+    for (const char* name : {"_conv_depthwise2d", "conv_depthwise3d"}) m.impl(name, &tvkb::conv_depthwise);
+    for (const char* name : {"_conv_depthwise2d.out", "conv_depthwise3d.out"}) m.impl(name, &tvkb::conv_depthwise_out);
 }

@@ -23,7 +23,6 @@
 #include <c10/core/impl/DeviceGuardImplInterface.h>
 
 #include <atomic>
-#include <chrono>
 #include <cstdlib>
 #include <cstring>
 #include <unordered_map>
@@ -230,14 +229,13 @@ struct TvkAllocator final : c10::Allocator {
 TvkAllocator g_allocator;
 
 // ---------------------------------------------------------------------------
-// device guard: one stream per device; events are host timestamps taken after
-// synchronizing the stream, as the reference's guard does (guard.cpp:44-61)
+// device guard. Every stream id of a device names the device's one library
+// stream (the reference's guard likewise hands out stream ids over one queue,
+// src/api/guard.cpp:24-33); the current id is kept per thread and device.
+// Events are HIP events recorded on that stream, so torch.Event record, wait,
+// query and elapsed_time are stream-ordered and timed on the GPU clock
+// (the reference stamps host time after draining the queue, guard.cpp:44-61).
 // ---------------------------------------------------------------------------
-
-struct HostEvent {
-    bool recorded = false;
-    std::chrono::steady_clock::time_point time;
-};
 
 struct TvkGuardImpl final : c10::impl::DeviceGuardImplInterface {
     c10::DeviceType type() const override { return c10::DeviceType::PrivateUse1; }
@@ -258,41 +256,72 @@ struct TvkGuardImpl final : c10::impl::DeviceGuardImplInterface {
         if (d.index() >= 0 && tvk_set_device(d.index()) == TVK_OK) g_current = d.index();
     }
     c10::Stream getStream(c10::Device d) const noexcept override {
-        return c10::Stream(c10::Stream::DEFAULT, d.has_index() ? d : getDevice());
+        d = indexed(d);
+        return c10::Stream(c10::Stream::UNSAFE, d, current_ids()[d.index()]);
     }
-    c10::Stream getDefaultStream(c10::Device d) const override {
-        return c10::Stream(c10::Stream::DEFAULT, d.has_index() ? d : getDevice());
+    c10::Stream getDefaultStream(c10::Device d) const override { return c10::Stream(c10::Stream::UNSAFE, indexed(d), 0); }
+    c10::Stream getStreamFromGlobalPool(c10::Device d, bool) const override { return getNewStream(d, 0); }
+    c10::Stream getNewStream(c10::Device d, int) const override {
+        static std::atomic<c10::StreamId> next{0};
+        return c10::Stream(c10::Stream::UNSAFE, indexed(d), ++next);
     }
-    c10::Stream exchangeStream(c10::Stream s) const noexcept override { return s; }
+    c10::Stream exchangeStream(c10::Stream s) const noexcept override {
+        const c10::Device d = indexed(s.device());
+        c10::StreamId& cur = current_ids()[d.index()];
+        c10::Stream prev(c10::Stream::UNSAFE, d, cur);
+        cur = s.id();
+        return prev;
+    }
     c10::DeviceIndex deviceCount() const noexcept override {
         int n = 0;
         (void)tvk_device_count(&n);
         return static_cast<c10::DeviceIndex>(n);
     }
     bool queryStream(const c10::Stream& s) const override {
-        synchronizeStream(s);
-        return true;
+        int done = 0;
+        check_status(tvk_stream_query(stream_of(s.device_index()), &done), "tvk_stream_query");
+        return done != 0;
     }
     void synchronizeStream(const c10::Stream& s) const override { synchronizeDevice(s.device_index()); }
     void synchronizeDevice(const c10::DeviceIndex index) const override {
         check_status(tvk_synchronize(index < 0 ? g_current : index), "tvk_synchronize");
     }
-    void destroyEvent(void* event, const c10::DeviceIndex) const noexcept override { delete static_cast<HostEvent*>(event); }
-    void record(void** event, const c10::Stream& stream, const c10::DeviceIndex, const c10::EventFlag) const override {
-        if (*event == nullptr) *event = new HostEvent();
-        synchronizeStream(stream);
-        auto* e = static_cast<HostEvent*>(*event);
-        e->recorded = true;
-        e->time = std::chrono::steady_clock::now();
+    void destroyEvent(void* event, const c10::DeviceIndex) const noexcept override { (void)tvk_event_destroy(event); }
+    void record(void** event, const c10::Stream& stream, const c10::DeviceIndex device_index,
+                const c10::EventFlag flag) const override {
+        TORCH_CHECK(device_index == -1 || device_index == stream.device_index(), "Event device index ", device_index,
+                    " does not match recording stream's device index ", stream.device_index(), ".");
+        if (*event == nullptr) {
+            // torch's default events do not time (as on CUDA); enable_timing asks for the backend default
+            const int timing = flag == c10::EventFlag::BACKEND_DEFAULT ? 1 : 0;
+            check_status(tvk_event_create(stream.device_index(), timing, event), "tvk_event_create");
+        }
+        check_status(tvk_event_record(*event, stream_of(stream.device_index())), "tvk_event_record");
     }
-    void block(void*, const c10::Stream&) const override {}
-    bool queryEvent(void*) const override { return true; }
-    void synchronizeEvent(void*) const override {}
+    void block(void* event, const c10::Stream& stream) const override {
+        if (event) check_status(tvk_stream_wait_event(stream_of(stream.device_index()), event), "tvk_stream_wait_event");
+    }
+    bool queryEvent(void* event) const override {
+        if (!event) return true;
+        int done = 0;
+        check_status(tvk_event_query(event, &done), "tvk_event_query");
+        return done != 0;
+    }
+    void synchronizeEvent(void* event) const override {
+        if (event) check_status(tvk_event_synchronize(event), "tvk_event_synchronize");
+    }
     double elapsedTime(void* a, void* b, const c10::DeviceIndex) const override {
-        auto* s = static_cast<HostEvent*>(a);
-        auto* e = static_cast<HostEvent*>(b);
-        TORCH_CHECK(s && e && s->recorded && e->recorded, "Both events must be recorded before calculating elapsed time.");
-        return std::chrono::duration<double, std::milli>(e->time - s->time).count();
+        TORCH_CHECK(a && b, "Both events must be recorded before calculating elapsed time.");
+        float ms = 0.0f;
+        check_status(tvk_event_elapsed(a, b, &ms), "tvk_event_elapsed");
+        return ms;
+    }
+
+private:
+    c10::Device indexed(c10::Device d) const { return d.has_index() ? d : getDevice(); }
+    static std::unordered_map<c10::DeviceIndex, c10::StreamId>& current_ids() {
+        thread_local std::unordered_map<c10::DeviceIndex, c10::StreamId> ids;
+        return ids;
     }
 };
 

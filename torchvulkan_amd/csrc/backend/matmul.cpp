@@ -265,12 +265,93 @@ at::Tensor addbmm_vk(const at::Tensor& input, const at::Tensor& b1, const at::Te
                 b2.size(0));
     TORCH_CHECK(b1.size(2) == b2.size(1), "Incompatible matrix sizes for bmm (", b1.size(1), "x", b1.size(2), " and ",
                 b2.size(1), "x", b2.size(2), ")");
+    TORCH_CHECK(input.scalar_type() == b1.scalar_type(), "self and mat2 must have the same dtype, but got ",
+                input.scalar_type(), " and ", b1.scalar_type());
     const int64_t B = b1.size(0), M = b1.size(1), K = b1.size(2), N = b2.size(2);
     at::Tensor a = b1.permute({1, 0, 2}).reshape({M, B * K});
     at::Tensor b = b2.reshape({B * K, N});
     return dispatch_matmul(a, b, input, alpha, beta, ACT_NONE, [&]() {
         return at::addbmm(input.cpu(), b1.cpu(), b2.cpu(), beta, alpha).to(b1.device());
     });
+}
+
+at::Tensor& addbmm_out_vk(const at::Tensor& input, const at::Tensor& b1, const at::Tensor& b2, const at::Scalar& beta,
+                          const at::Scalar& alpha, at::Tensor& out) {
+    return fill_out(out, addbmm_vk(input, b1, b2, beta, alpha));
+}
+
+// in-place variants write the computed result back into self, which must
+// already have the result's shape (src/api/ops/helpers.h:389-397)
+at::Tensor& write_back(at::Tensor& self, const at::Tensor& res) {
+    TORCH_CHECK(at::canCast(res.scalar_type(), self.scalar_type()), "result type ", res.scalar_type(),
+                " can't be cast to the desired output type ", self.scalar_type());
+    TORCH_CHECK(res.sizes() == self.sizes(), "output with shape ", self.sizes(), " doesn't match the broadcast shape ",
+                res.sizes());
+    if (!res.is_same(self)) self.copy_(res);
+    return self;
+}
+
+at::Tensor& addbmm_inplace_vk(at::Tensor& self, const at::Tensor& b1, const at::Tensor& b2, const at::Scalar& beta,
+                              const at::Scalar& alpha) {
+    return write_back(self, addbmm_vk(self, b1, b2, beta, alpha));
+}
+
+// mm.dtype / mm.dtype_out (src/api/decompositions.cpp:1146-1157): the output
+// keeps the inputs' dtype, or is float32 for float16/bfloat16 inputs, which
+// is the float32 product of the widened operands (every float16/bfloat16
+// value is exact in float32, so only the accumulation differs from the
+// inputs' own product: it runs in the float32 kernel's sequential order)
+at::Tensor mm_dtype_vk(const at::Tensor& self, const at::Tensor& mat2, at::ScalarType out_dtype) {
+    const at::ScalarType dt = self.scalar_type();
+    TORCH_CHECK(out_dtype == dt || (out_dtype == at::kFloat && (dt == at::kHalf || dt == at::kBFloat16)),
+                "out_dtype must be the same as input dtype or fp32 for fp16/bf16 inputs");
+    if (out_dtype == dt) return mm_vk(self, mat2);
+    return mm_vk(self.to(at::kFloat), mat2.to(at::kFloat));
+}
+
+at::Tensor& mm_dtype_out_vk(const at::Tensor& self, const at::Tensor& mat2, at::ScalarType out_dtype, at::Tensor& out) {
+    return fill_out(out, mm_dtype_vk(self, mat2, out_dtype));
+}
+
+// addmv: out = beta*self + alpha*(mat @ vec), with torch's addmv meta checks
+// and messages. The product runs as the one-row GEMM
+// out^T[1, M] = vec^T[1, K] . mat^T[K, M] (self broadcast along the row as
+// the bias), the M <= 16 streaming shape of tvk_gemm; no operand is copied.
+// The reference computes it as mm(mat, vec.unsqueeze(1)) in float32 for
+// float16/bfloat16 (src/api/decompositions.cpp:109-124); here the float32
+// accumulation and the epilogue round once to the dtype.
+at::Tensor addmv_vk(const at::Tensor& self, const at::Tensor& mat, const at::Tensor& vec, const at::Scalar& beta,
+                    const at::Scalar& alpha) {
+    TORCH_CHECK(mat.dim() == 2 && vec.dim() == 1 && self.dim() <= 1, "vector + matrix @ vector expected, got ", self.dim(),
+                ", ", mat.dim(), ", ", vec.dim());
+    TORCH_CHECK(mat.size(1) == vec.size(0) && (mat.size(0) == self.numel() || self.numel() == 1),
+                "size mismatch, got input (", self.dim() == 0 ? 1 : self.size(0), "), mat (", mat.size(0), "x", mat.size(1),
+                "), vec (", vec.size(0), ")");
+    TORCH_CHECK(mat.scalar_type() == vec.scalar_type(), "expected scalar type ", mat.scalar_type(), " but found ",
+                vec.scalar_type());
+    for (const at::Tensor* t : {&self, &vec})
+        TORCH_CHECK(t->device() == mat.device(), "Expected all tensors to be on the same device, but found at least two devices, ",
+                    mat.device(), " and ", t->device(), "!");
+    const int64_t M = mat.size(0);
+    at::Tensor bias = self.dim() == 0 ? self.reshape({1}) : self;
+    at::Tensor r = dispatch_matmul(vec.unsqueeze(0), mat.t(), bias, alpha, beta, ACT_NONE, [&]() {
+        return at::addmv(self.cpu(), mat.cpu(), vec.cpu(), beta, alpha).to(mat.device()).unsqueeze(0);
+    });
+    return r.reshape({M});
+}
+
+at::Tensor& addmv_out_vk(const at::Tensor& self, const at::Tensor& mat, const at::Tensor& vec, const at::Scalar& beta,
+                         const at::Scalar& alpha, at::Tensor& out) {
+    TORCH_CHECK(out.scalar_type() == mat.scalar_type(), "Expected out tensor to have dtype ", mat.scalar_type(), ", but got ",
+                out.scalar_type(), " instead");
+    TORCH_CHECK(out.device() == mat.device(), "Expected out tensor to have device ", mat.device(), ", but got ", out.device(),
+                " instead");
+    return fill_out(out, addmv_vk(self, mat, vec, beta, alpha));
+}
+
+at::Tensor& addmv_inplace_vk(at::Tensor& self, const at::Tensor& mat, const at::Tensor& vec, const at::Scalar& beta,
+                             const at::Scalar& alpha) {
+    return write_back(self, addmv_vk(self, mat, vec, beta, alpha));
 }
 
 }  // namespace
@@ -288,4 +369,11 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
     m.impl("_addmm_activation", &tvkb::addmm_activation_vk);
     m.impl("_addmm_activation.out", &tvkb::addmm_activation_out_vk);
     m.impl("addbmm", &tvkb::addbmm_vk);
+    m.impl("addbmm.out", &tvkb::addbmm_out_vk);
+    m.impl("addbmm_", &tvkb::addbmm_inplace_vk);
+    m.impl("mm.dtype", &tvkb::mm_dtype_vk);
+    m.impl("mm.dtype_out", &tvkb::mm_dtype_out_vk);
+    m.impl("addmv", &tvkb::addmv_vk);
+    m.impl("addmv.out", &tvkb::addmv_out_vk);
+    m.impl("addmv_", &tvkb::addmv_inplace_vk);
 }

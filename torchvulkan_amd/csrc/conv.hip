@@ -533,6 +533,7 @@ tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
     else if (MODE == DGRAD) { p.M = p.cx; p.N = p.n * p.h * p.wd; p.K = p.cy * p.taps; }
     else { p.M = p.cy; p.N = p.cx * p.taps; p.K = p.n * p.ho * p.wo; }
     hipStream_t s = resolve_stream(d.stream);
+    Scratch scratch;
     const size_t es = dtype_size(d.dtype);
     if (p.N == 0 || p.M == 0) return TVK_OK;
     if (p.K == 0) {
@@ -565,9 +566,7 @@ tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
         p.split = (int)split;
         p.k_chunk = (int)chunk;
         if (split > 1) {
-            int dev = 0;
-            (void)hipGetDevice(&dev);
-            p.part = static_cast<float*>(device_workspace(dev, (size_t)split * p.cout * p.cx * p.taps * sizeof(float)));
+            p.part = static_cast<float*>(scratch.get((size_t)split * p.cout * p.cx * p.taps * sizeof(float), s));
             if (!p.part) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the split-k partials");
         }
     }

@@ -609,8 +609,7 @@ void border_for(int lo, int step, int count, int tap_lo, int tap_hi, int size, i
 // ---------------------------------------------------------------------------
 constexpr int HL_BN = 64;
 constexpr int HL_PX = 512;      // output pixels a tile
-constexpr int HL_MAXHP = 660;   // halo pixels (TR + 2) * (W + 2), largest at W = 8 and 64
-constexpr int HL_A = 43008;     // HL_MAXHP * 64 bytes, rounded up to 1 KB
+constexpr int HL_A = 43008;     // halo pixels (TR + 2) * (W + 2) <= 660 (largest at W = 8 and 64) * 64 bytes, rounded up to 1 KB
 constexpr int HL_B = 9 * HL_BN * 64;
 constexpr int HL_STAGE = HL_A + HL_B;
 
@@ -1120,7 +1119,6 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
 
     // [channel][dx pixel] tile over ipt x 2 tr x W pixels (the phases
     // interleave along the rows), then 16-byte stores along the dx rows
-    typedef typename elem<DT>::T T;
     uint16_t* tile = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
     for (int i = 0; i < FMW; ++i) {
@@ -1819,8 +1817,7 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
     const int dh = (int)d.dilation[0], dw = (int)d.dilation[1];
     const size_t es = 2;
     hipStream_t s = resolve_stream(d.stream);
-    int dev = 0;
-    (void)hipGetDevice(&dev);
+    Scratch scratch;
 
     ConvRing p;
     memset(&p, 0, sizeof(p));
@@ -1863,7 +1860,7 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
         const size_t act_b = align((size_t)n * Cs * Hs * Ws * es), wt_b = align((size_t)Cn * T * Cs * es);
         if ((size_t)n * Cs * Hs * Ws * es >= ((size_t)1 << 31))
             return fail(TVK_ERR_UNSUPPORTED, std::string(who) + ": the bordered channels-last copy exceeds 2 GiB");
-        char* ws = static_cast<char*>(device_workspace(dev, act_b + wt_b));
+        char* ws = static_cast<char*>(scratch.get(act_b + wt_b, s));
         if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the channels-last copies");
         const void* src = mode == 0 ? d.x : d.y;
         WeightPermute wp;
@@ -1969,7 +1966,7 @@ tvk_status conv_ring_run(const tvk_conv_desc& d, int mode, const char* who) {
         int64_t chunk = ((p.K + split - 1) / split + V_BK - 1) / V_BK * V_BK;
         split = (p.K + chunk - 1) / chunk;
         const size_t part_b = split > 1 ? (size_t)split * p.M * p.N * 4 : 0;
-        char* ws = static_cast<char*>(device_workspace(dev, act_b + part_b));
+        char* ws = static_cast<char*>(scratch.get(act_b + part_b, s));
         if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the channels-last copy");
         launch_nhwc(d.x, ws, n, cin, H, W, bd, s);
         p.act = ws;
@@ -2211,8 +2208,7 @@ bool conv1x1_wgrad_applies(const tvk_conv_desc& d) {
 
 tvk_status conv1x1_wgrad_run(const tvk_conv_desc& d, const char* who) {
     hipStream_t s = resolve_stream(d.stream);
-    int dev = 0;
-    (void)hipGetDevice(&dev);
+    Scratch scratch;
     PointWgArgs p;
     memset(&p, 0, sizeof(p));
     p.x = static_cast<const uint16_t*>(d.x);
@@ -2226,7 +2222,7 @@ tvk_status conv1x1_wgrad_run(const tvk_conv_desc& d, const char* who) {
     p.steps_per_split = (p.steps + p.split - 1) / p.split;
     p.split = (p.steps + p.steps_per_split - 1) / p.steps_per_split;
     const size_t part_b = (size_t)p.split * p.cin * p.cout * sizeof(float);
-    p.part = static_cast<float*>(device_workspace(dev, part_b));
+    p.part = static_cast<float*>(scratch.get(part_b, s));
     if (!p.part) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
     const dim3 grid((unsigned)p.split, (unsigned)cb, (unsigned)nb);
     const bool f16 = d.dtype == TVK_F16;
@@ -2268,8 +2264,7 @@ tvk_status conv_halo_wgrad_s2_run(const tvk_conv_desc& d, const char* who) {
     const int cin = (int)d.c_in, cout = (int)d.c_out, Wo = (int)d.w_out;
     const int tpx = conv_halo_wgrad_s2_tpx(d);
     hipStream_t s = resolve_stream(d.stream);
-    int dev = 0;
-    (void)hipGetDevice(&dev);
+    Scratch scratch;
     HaloWgArgs p;
     memset(&p, 0, sizeof(p));
     p.x = static_cast<const uint16_t*>(d.x);
@@ -2282,7 +2277,7 @@ tvk_status conv_halo_wgrad_s2_run(const tvk_conv_desc& d, const char* who) {
     // about 256 workgroups, each summing at least 2 tiles
     p.split = std::max(1, std::min(p.ntiles / 2, 256 / (cb * nb)));
     const size_t part_b = (size_t)p.split * 9 * cin * cout * sizeof(float);
-    char* ws = static_cast<char*>(device_workspace(dev, part_b));
+    char* ws = static_cast<char*>(scratch.get(part_b, s));
     if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
     p.part = reinterpret_cast<float*>(ws);
     const dim3 grid((unsigned)p.split, (unsigned)cb, (unsigned)nb);
@@ -2310,8 +2305,7 @@ tvk_status conv_halo_wgrad_s2_run(const tvk_conv_desc& d, const char* who) {
 tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
     const int cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
     hipStream_t s = resolve_stream(d.stream);
-    int dev = 0;
-    (void)hipGetDevice(&dev);
+    Scratch scratch;
     HaloWgArgs p;
     memset(&p, 0, sizeof(p));
     p.x = static_cast<const uint16_t*>(d.x);
@@ -2324,7 +2318,7 @@ tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
     // about 256 workgroups (one a CU), each summing at least 2 tiles
     p.split = std::max(1, std::min(p.ntiles / 2, 256 / (cb * nb)));
     const size_t part_b = (size_t)p.split * 9 * cin * cout * sizeof(float);
-    char* ws = static_cast<char*>(device_workspace(dev, part_b));
+    char* ws = static_cast<char*>(scratch.get(part_b, s));
     if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
     p.part = reinterpret_cast<float*>(ws);
     const dim3 grid((unsigned)p.split, (unsigned)cb, (unsigned)nb);
@@ -2359,10 +2353,9 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     const int cin = (int)d.c_in, cout = (int)d.c_out, H = (int)d.h, W = (int)d.w;
     const int Cs = mode == 0 ? cin : cout, N = mode == 0 ? cout : cin;
     hipStream_t s = resolve_stream(d.stream);
-    int dev = 0;
-    (void)hipGetDevice(&dev);
+    Scratch scratch;
     const size_t wt_b = (size_t)N * 9 * Cs * 2;
-    char* ws = static_cast<char*>(device_workspace(dev, wt_b));
+    char* ws = static_cast<char*>(scratch.get(wt_b, s));
     if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the permuted weight");
     const int pgroups = N * 9 * (Cs / 8);
     const dim3 pgrid((unsigned)std::min((pgroups + 255) / 256, 1024));

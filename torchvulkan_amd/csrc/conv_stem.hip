@@ -523,6 +523,7 @@ bool conv_small_applies(const tvk_conv_desc& d, int mode) {
 tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who) {
     SmallArgs p = small_args(d);
     hipStream_t s = resolve_stream(d.stream);
+    Scratch scratch;
     const bool f16 = d.dtype == TVK_F16;
     if (mode == 0) {
         p.out = d.y;
@@ -547,9 +548,7 @@ tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who) {
         p.out = d.weight;
         const int count = p.cout * p.K;
         if (p.split > 1) {
-            int dev = 0;
-            (void)hipGetDevice(&dev);
-            p.part = static_cast<float*>(device_workspace(dev, (size_t)p.split * count * sizeof(float)));
+            p.part = static_cast<float*>(scratch.get((size_t)p.split * count * sizeof(float), s));
             if (!p.part) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
         }
         const dim3 grid((unsigned)p.split, (unsigned)ny);

@@ -52,19 +52,22 @@ __global__ void gemm_k0_kernel(GemmArgs p) {
 
 // One output per thread, sequential k, fmaf accumulate: the reference SIMD
 // tile's per-output order, for operands no tiled kernel accepts.
+// Outputs of one batch matrix (blockIdx.y) are dealt out along x in a
+// grid-stride loop, so any M x N fits the grid.
 template <int DT>
 __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
     typedef typename elem<DT>::T T;
-    int col = blockIdx.x * 16 + (threadIdx.x % 16);
-    int row = blockIdx.y * 16 + (threadIdx.x / 16);
-    int b = blockIdx.z;
-    if (row >= p.M || col >= p.N) return;
-    const T* a = reinterpret_cast<const T*>(p.a) + (int64_t)b * p.sa[0] + (int64_t)row * p.sa[1];
-    const T* bm = reinterpret_cast<const T*>(p.b) + (int64_t)b * p.sb[0] + (int64_t)col * p.sb[2];
-    float acc = 0.0f;
-    for (int k = 0; k < p.K; ++k)
-        acc = fmaf(elem<DT>::to_f32(a[(int64_t)k * p.sa[2]]), elem<DT>::to_f32(bm[(int64_t)k * p.sb[1]]), acc);
-    store_out<DT, true>(p, b, row, col, acc);
+    const int b = blockIdx.y;
+    const int64_t total = (int64_t)p.M * p.N;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+        const int row = (int)(idx / p.N), col = (int)(idx % p.N);
+        const T* a = reinterpret_cast<const T*>(p.a) + (int64_t)b * p.sa[0] + (int64_t)row * p.sa[1];
+        const T* bm = reinterpret_cast<const T*>(p.b) + (int64_t)b * p.sb[0] + (int64_t)col * p.sb[2];
+        float acc = 0.0f;
+        for (int k = 0; k < p.K; ++k)
+            acc = fmaf(elem<DT>::to_f32(a[(int64_t)k * p.sa[2]]), elem<DT>::to_f32(bm[(int64_t)k * p.sb[1]]), acc);
+        store_out<DT, true>(p, b, row, col, acc);
+    }
 }
 
 // ----------------------------------------------------------------------------
@@ -545,6 +548,26 @@ int64_t operand_extent_bytes(int64_t rows, int64_t s_row, int64_t cols, int64_t 
     return (int64_t)es * ((rows - 1) * s_row + (cols - 1) * s_col + 1);
 }
 
+// Row (mc) and column (nc) block sizes that bring A's and B's per-matrix
+// extents below 2 GiB, the tiled kernels' buffer range. Unchanged sizes when
+// they already fit; false when no block of whole rows and columns fits (a
+// single row or column spans 2 GiB), which leaves the product to the generic
+// kernel.
+bool extent_chunks(const tvk_gemm_desc& d, int64_t& mc, int64_t& nc) {
+    const int64_t es = (int64_t)dtype_size(d.dtype), lim = (int64_t(0x7fffffff) - 256) / es;
+    auto rows_fitting = [&](int64_t rows, int64_t s_row, int64_t cols, int64_t s_col) -> int64_t {
+        const int64_t fixed = (cols - 1) * s_col + 1;
+        if (fixed >= lim) return 0;
+        if (s_row == 0 || (rows - 1) * s_row + fixed < lim) return rows;
+        int64_t r = (lim - fixed) / s_row + 1;
+        if (r >= 256) r = r / 256 * 256;   // whole 256-row tiles
+        return std::min(r, rows);
+    };
+    mc = rows_fitting(d.M, d.a_stride[1], d.K, d.a_stride[2]);
+    nc = rows_fitting(d.N, d.b_stride[2], d.K, d.b_stride[1]);
+    return mc > 0 && nc > 0;
+}
+
 GemmArgs make_args(const tvk_gemm_desc& d) {
     GemmArgs p;
     memset(&p, 0, sizeof(p));
@@ -678,9 +701,9 @@ Plan make_plan(const tvk_gemm_desc& d) {
         pl.kern = Kern::DMA256;
         pl.name = "gemm16_dma_256x256";
     } else if (big) {
-        static const bool w8 = getenv("TVK_GEMM_W4") == nullptr;
-        pl.kern = w8 ? Kern::MFMA256W8 : Kern::MFMA256;
-        pl.name = w8 ? "gemm16_mfma_256x256_w8" : "gemm16_mfma_256x256";
+        // 8 waves; the 4-wave form stays a kernel-choice candidate
+        pl.kern = Kern::MFMA256W8;
+        pl.name = "gemm16_mfma_256x256_w8";
     } else {
         pl.kern = Kern::MFMA128;
         pl.name = "gemm16_mfma_128x128";
@@ -845,10 +868,9 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
         const size_t rep_b = pl.repack_b ? al256((size_t)nb * b_rows * b_ld * 2) : 0;
         const size_t part_b = pl.split > 1 ? (size_t)pl.split * nb * d.M * d.N * 4 : 0;
         char* ws = nullptr;
+        Scratch scratch;
         if (rep_a + rep_b + part_b > 0) {
-            int dev = 0;
-            (void)hipGetDevice(&dev);
-            ws = static_cast<char*>(device_workspace(dev, rep_a + rep_b + part_b));
+            ws = static_cast<char*>(scratch.get(rep_a + rep_b + part_b, s));
             if (!ws) return fail(TVK_ERR_OOM, "tvk_gemm: no workspace for repacked operands or split-K partials");
         }
         if constexpr (DT != TVK_F32) {
@@ -882,7 +904,8 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
             break;
         }
         case Kern::GENERIC:
-            hipLaunchKernelGGL(gemm_generic_kernel<DT>, dim3((unsigned)((d.N + 15) / 16), (unsigned)((d.M + 15) / 16), nb), dim3(256), 0, s, q);
+            hipLaunchKernelGGL(gemm_generic_kernel<DT>, dim3((unsigned)std::min<int64_t>(((int64_t)d.M * d.N + 255) / 256, 65536), nb),
+                               dim3(256), 0, s, q);
             break;
         case Kern::SEQ256:
         case Kern::SEQ128:
@@ -1063,8 +1086,18 @@ extern "C" tvk_status tvk_gemm_plan(const tvk_gemm_desc* desc, char* name, size_
     tvk_status st = validate(desc);
     if (st != TVK_OK) return st;
     if (!name || name_len == 0) return fail(TVK_ERR_INVALID, "tvk_gemm_plan: name buffer is empty");
-    const char* n = (desc->batch == 0 || desc->M == 0 || desc->N == 0) ? "none" : choose_plan(*desc).name;
-    snprintf(name, name_len, "%s", n);
+    if (desc->batch == 0 || desc->M == 0 || desc->N == 0) {
+        snprintf(name, name_len, "none");
+        return TVK_OK;
+    }
+    // a product tvk_gemm runs in row/column blocks is named by its first block's kernel
+    tvk_gemm_desc first = *desc;
+    int64_t mc = first.M, nc = first.N;
+    if (first.K > 0 && extent_chunks(first, mc, nc)) {
+        first.M = mc;
+        first.N = nc;
+    }
+    snprintf(name, name_len, "%s", choose_plan(first).name);
     return TVK_OK;
 }
 
@@ -1073,6 +1106,25 @@ extern "C" tvk_status tvk_gemm(const tvk_gemm_desc* desc) {
     if (st != TVK_OK) return st;
     const tvk_gemm_desc& d = *desc;
     if (d.batch == 0 || d.M == 0 || d.N == 0) return TVK_OK;
+    int64_t mc = d.M, nc = d.N;
+    if (d.K > 0 && extent_chunks(d, mc, nc) && (mc < d.M || nc < d.N)) {
+        // row and column blocks whose operand extents fit the tiled kernels'
+        // 32-bit buffer offsets, each its own product
+        const size_t es = dtype_size(d.dtype);
+        for (int64_t m0 = 0; m0 < d.M; m0 += mc)
+            for (int64_t n0 = 0; n0 < d.N; n0 += nc) {
+                tvk_gemm_desc sub = d;
+                sub.M = std::min(mc, d.M - m0);
+                sub.N = std::min(nc, d.N - n0);
+                sub.a = static_cast<const char*>(d.a) + (size_t)(m0 * d.a_stride[1]) * es;
+                sub.b = static_cast<const char*>(d.b) + (size_t)(n0 * d.b_stride[2]) * es;
+                sub.c = static_cast<char*>(d.c) + (size_t)(m0 * d.c_stride[1] + n0 * d.c_stride[2]) * es;
+                if (d.bias) sub.bias = static_cast<const char*>(d.bias) + (size_t)(m0 * d.bias_stride[1] + n0 * d.bias_stride[2]) * es;
+                st = run_plan(sub, choose_plan(sub));
+                if (st != TVK_OK) return st;
+            }
+        return TVK_OK;
+    }
     return run_plan(d, choose_plan(d));
 }
 

@@ -304,10 +304,9 @@ hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, 
         GemmArgs q = p;
         q.split = ring_splits(p);
         q.k_chunk = p.K / q.split;
+        Scratch scratch;
         if (q.split > 1) {
-            int dev = 0;
-            (void)hipGetDevice(&dev);
-            q.part = static_cast<float*>(device_workspace(dev, (size_t)q.split * p.batch * p.M * p.N * 4));
+            q.part = static_cast<float*>(scratch.get((size_t)q.split * p.batch * p.M * p.N * 4, s));
             if (!q.part) return hipErrorOutOfMemory;
         }
         const dim3 grid((p.N + SR_NB - 1) / SR_NB, q.split, p.batch);

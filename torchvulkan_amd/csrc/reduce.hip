@@ -288,8 +288,9 @@ tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
     const int ddt = p.ddt;
     char* final_dst = p.dst;
     Acc* part = nullptr;
+    Scratch scratch;
     if (splits > 1) {
-        part = static_cast<Acc*>(device_workspace(dev, (size_t)(p.nout * splits) * sizeof(Acc)));
+        part = static_cast<Acc*>(scratch.get((size_t)(p.nout * splits) * sizeof(Acc), st));
         if (!part) return fail(TVK_ERR_OOM, "tvk_reduce_sum: workspace allocation failed");
         p.dst = reinterpret_cast<char*>(part);
         p.ddt = -1;

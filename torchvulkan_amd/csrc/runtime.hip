@@ -9,6 +9,7 @@
 // one blocking submit; here every call is enqueued on an in-order HIP stream,
 // so hazards between kernels are ordered by the stream itself.
 #include "tvk_common.h"
+#include "scratch_pool.h"
 
 #include <map>
 #include <mutex>
@@ -29,10 +30,6 @@ constexpr int kMaxDevices = 64;
 
 struct DeviceState {
     hipStream_t stream = nullptr;
-    void* workspace = nullptr;      // library scratch (split-k partials)
-    size_t workspace_bytes = 0;
-    uint32_t* counters = nullptr;   // zeroed arrival counters
-    size_t counter_count = 0;
     // size class -> cached free blocks
     std::map<size_t, std::vector<void*>> free_blocks;
     size_t allocated = 0;   // bytes in live blocks (size-class rounded)
@@ -81,58 +78,74 @@ void release_cached_locked(int device) {
     (void)hipSetDevice(prev);
 }
 
-}  // namespace
+// The scratch pool's operations on one device: hipMalloc'd buffers, events
+// without timing, cross-stream waits (every call makes the device current
+// for its duration).
+struct HipScratchBackend {
+    typedef hipStream_t Stream;
+    typedef hipEvent_t Event;
+    int device = 0;
 
-// Grows the device's scratch area. Growing waits for the whole device first,
-// since kernels still queued on any stream may be using the old area.
-void* device_workspace(int device, size_t bytes) {
-    if (device < 0 || device >= kMaxDevices) return nullptr;
-    std::lock_guard<std::mutex> lk(g_mu);
-    DeviceState& st = g_dev[device];
-    if (bytes > st.workspace_bytes) {
+    struct On {
         int prev = 0;
-        (void)hipGetDevice(&prev);
-        (void)hipSetDevice(device);
-        if (st.workspace) {
-            (void)hipDeviceSynchronize();
-            (void)hipFree(st.workspace);
-        }
-        size_t sz = std::max(bytes, size_t(16) << 20);
-        if (hipMalloc(&st.workspace, sz) != hipSuccess) {
+        explicit On(int d) { (void)hipGetDevice(&prev); (void)hipSetDevice(d); }
+        ~On() { (void)hipSetDevice(prev); }
+    };
+    void* alloc(size_t bytes) {
+        On on(device);
+        void* p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess) {
             (void)hipGetLastError();
-            st.workspace = nullptr;
-            sz = 0;
+            return nullptr;
         }
-        st.workspace_bytes = sz;
-        (void)hipSetDevice(prev);
+        return p;
     }
-    return st.workspace;
+    void free(void* p) { On on(device); (void)hipFree(p); }
+    Event make_event() {
+        On on(device);
+        hipEvent_t e = nullptr;
+        (void)hipEventCreateWithFlags(&e, hipEventDisableTiming);
+        return e;
+    }
+    void destroy_event(Event e) { if (e) (void)hipEventDestroy(e); }
+    void record(Event e, Stream s) { if (e) (void)hipEventRecord(e, s); }
+    void wait(Stream s, Event e) { if (e) (void)hipStreamWaitEvent(s, e, 0); }
+    void sync(Event e) { if (e) (void)hipEventSynchronize(e); }
+};
+
+struct DeviceScratch {
+    HipScratchBackend backend;
+    ScratchPool<HipScratchBackend> pool;
+    explicit DeviceScratch(int d) : pool(backend) { backend.device = d; }
+};
+
+std::mutex g_scratch_mu;
+DeviceScratch* g_scratch[kMaxDevices] = {};
+
+DeviceScratch* device_scratch(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[device]) g_scratch[device] = new DeviceScratch(device);   // lives until the process ends
+    return g_scratch[device];
 }
 
-uint32_t* device_counters(int device, size_t count) {
-    if (device < 0 || device >= kMaxDevices) return nullptr;
-    std::lock_guard<std::mutex> lk(g_mu);
-    DeviceState& st = g_dev[device];
-    if (count > st.counter_count) {
-        int prev = 0;
-        (void)hipGetDevice(&prev);
-        (void)hipSetDevice(device);
-        if (st.counters) {
-            (void)hipDeviceSynchronize();
-            (void)hipFree(st.counters);
-        }
-        size_t n = std::max(count, size_t(65536));
-        if (hipMalloc(&st.counters, n * sizeof(uint32_t)) != hipSuccess ||
-            hipMemset(st.counters, 0, n * sizeof(uint32_t)) != hipSuccess ||
-            hipDeviceSynchronize() != hipSuccess) {
-            (void)hipGetLastError();
-            st.counters = nullptr;
-            n = 0;
-        }
-        st.counter_count = n;
-        (void)hipSetDevice(prev);
-    }
-    return st.counters;
+}  // namespace
+
+void* Scratch::get(size_t bytes, hipStream_t stream) {
+    release();
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    auto* buf = device_scratch(dev)->pool.acquire(bytes, stream);
+    if (!buf) return nullptr;
+    lease_ = buf;
+    device_ = dev;
+    stream_ = stream;
+    return buf->ptr;
+}
+
+void Scratch::release() {
+    if (!lease_) return;
+    device_scratch(device_)->pool.release(static_cast<ScratchPool<HipScratchBackend>::Buffer*>(lease_), stream_);
+    lease_ = nullptr;
 }
 
 hipStream_t device_stream(int device) {
@@ -197,6 +210,74 @@ tvk_status tvk_synchronize(int device) {
     hipError_t e = hipStreamSynchronize(device_stream(device));
     (void)hipSetDevice(prev);
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_synchronize: ") + hipGetErrorString(e));
+    return TVK_OK;
+}
+
+tvk_status tvk_event_create(int device, int timing, void** event) {
+    if (!event) return fail(TVK_ERR_INVALID, "tvk_event_create: event is NULL");
+    *event = nullptr;
+    if (!valid_device(device)) return fail(TVK_ERR_INVALID, "tvk_event_create: invalid device index " + std::to_string(device));
+    int prev = 0;
+    TVK_HIP_CHECK(hipGetDevice(&prev));
+    TVK_HIP_CHECK(hipSetDevice(device));
+    hipEvent_t e = nullptr;
+    const hipError_t r = hipEventCreateWithFlags(&e, timing ? hipEventDefault : hipEventDisableTiming);
+    (void)hipSetDevice(prev);
+    if (r != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_event_create: ") + hipGetErrorString(r));
+    *event = e;
+    return TVK_OK;
+}
+
+tvk_status tvk_event_destroy(void* event) {
+    if (event) TVK_HIP_CHECK(hipEventDestroy(static_cast<hipEvent_t>(event)));
+    return TVK_OK;
+}
+
+tvk_status tvk_event_record(void* event, void* stream) {
+    if (!event) return fail(TVK_ERR_INVALID, "tvk_event_record: event is NULL");
+    TVK_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(event), resolve_stream(stream)));
+    return TVK_OK;
+}
+
+tvk_status tvk_event_query(void* event, int* done) {
+    if (!event || !done) return fail(TVK_ERR_INVALID, "tvk_event_query: NULL argument");
+    const hipError_t r = hipEventQuery(static_cast<hipEvent_t>(event));
+    if (r == hipErrorNotReady) {
+        *done = 0;
+        return TVK_OK;
+    }
+    if (r != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_event_query: ") + hipGetErrorString(r));
+    *done = 1;
+    return TVK_OK;
+}
+
+tvk_status tvk_event_synchronize(void* event) {
+    if (!event) return fail(TVK_ERR_INVALID, "tvk_event_synchronize: event is NULL");
+    TVK_HIP_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(event)));
+    return TVK_OK;
+}
+
+tvk_status tvk_event_elapsed(void* start, void* end, float* ms) {
+    if (!start || !end || !ms) return fail(TVK_ERR_INVALID, "tvk_event_elapsed: NULL argument");
+    TVK_HIP_CHECK(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end)));
+    return TVK_OK;
+}
+
+tvk_status tvk_stream_wait_event(void* stream, void* event) {
+    if (!event) return fail(TVK_ERR_INVALID, "tvk_stream_wait_event: event is NULL");
+    TVK_HIP_CHECK(hipStreamWaitEvent(resolve_stream(stream), static_cast<hipEvent_t>(event), 0));
+    return TVK_OK;
+}
+
+tvk_status tvk_stream_query(void* stream, int* done) {
+    if (!done) return fail(TVK_ERR_INVALID, "tvk_stream_query: done is NULL");
+    const hipError_t r = hipStreamQuery(resolve_stream(stream));
+    if (r == hipErrorNotReady) {
+        *done = 0;
+        return TVK_OK;
+    }
+    if (r != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_stream_query: ") + hipGetErrorString(r));
+    *done = 1;
     return TVK_OK;
 }
 
@@ -276,8 +357,11 @@ tvk_status tvk_free(void* ptr) {
 
 tvk_status tvk_empty_cache(int device) {
     if (!valid_device(device)) return fail(TVK_ERR_INVALID, "tvk_empty_cache: invalid device index " + std::to_string(device));
-    std::lock_guard<std::mutex> lk(g_mu);
-    release_cached_locked(device);
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        release_cached_locked(device);
+    }
+    device_scratch(device)->pool.trim();   // idle scratch buffers, each after its last use
     return TVK_OK;
 }
 

@@ -30,11 +30,31 @@ inline tvk_status fail(tvk_status code, const std::string& msg) {
 
 // Library stream of a device (created lazily); defined in runtime.hip.
 hipStream_t device_stream(int device);
-// Library-owned scratch of a device (defined in runtime.hip). Both grow on
-// demand; the counters are zero between calls (every kernel that increments
-// one resets it before it exits).
-void* device_workspace(int device, size_t bytes);
-uint32_t* device_counters(int device, size_t count);
+
+// A lease of library scratch memory (split-K partials, repacked operands,
+// convolution partials) for the kernels one call queues on one stream of the
+// current device. The lease ends when the object is destroyed, after the
+// call's launches: the buffer then returns to the device's pool behind an
+// event on that stream, so a later call on another stream waits for this
+// call's kernels before it reuses the memory, and no buffer is freed while a
+// lease holds it or its last kernels may still run (scratch_pool.h).
+class Scratch {
+public:
+    Scratch() = default;
+    Scratch(const Scratch&) = delete;
+    Scratch& operator=(const Scratch&) = delete;
+    ~Scratch() { release(); }
+    // At least `bytes` of device memory, 256-byte aligned, for kernels queued
+    // on `stream`; NULL when it cannot be allocated. One lease per object: a
+    // second call ends the first lease.
+    void* get(size_t bytes, hipStream_t stream);
+    void release();
+
+private:
+    void* lease_ = nullptr;
+    int device_ = -1;
+    hipStream_t stream_ = nullptr;
+};
 
 // A NULL stream handle is HIP's default (null) stream, as in every HIP library.
 inline hipStream_t resolve_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
