@@ -112,14 +112,14 @@ def test_addmv_family(tv, strict, dtype, mk):
     # a transposed matrix view is read in place
     matt = randn((K, M), dtype, 9)
     ref_t = oracle_mm(vec.reshape(1, K), matt, dtype).reshape(M)
-    assert_close(decode(to_np(host(torch.mv(matt.to(V).t(), vec.to(V))))), ref_t, dtype, "mv(mat.t())")
+    assert_close(decode(to_np(host(torch.mv(matt.to(V).t(), vec.to(V)))), dtype), ref_t, dtype, "mv(mat.t())")
 
 
 def test_addmv_scalar_self_and_errors(tv, strict):
     mat, vec = randn((70, 90), torch.float32, 10), randn((90,), torch.float32, 11)
     s = torch.tensor(2.0)
     got = torch.addmv(s.to(V), mat.to(V), vec.to(V))
-    ref = oracle_mm(vec.reshape(1, 90), mat.t(), torch.float32, bias=s.expand(1, 70).contiguous()).reshape(70)
+    ref = oracle_mm(vec.reshape(1, 90), mat.t(), torch.float32, bias=s.expand(1, 70).contiguous(), beta=1.0).reshape(70)
     assert_bit_exact(host(got).numpy(), ref, "addmv with a 0-d self")
     cases = [
         lambda d: torch.addmv(torch.zeros(3, device=d), torch.zeros(3, 4, device=d), torch.zeros(5, device=d)),
