@@ -153,6 +153,8 @@ tvk_status tvk_set_memory_limit(int device, size_t bytes);
 
 tvk_status tvk_memory_allocated(int device, size_t* bytes);
 tvk_status tvk_max_memory_allocated(int device, size_t* bytes);
+/* Bytes obtained from hipMalloc and held: the caching allocator's blocks and
+ * the library's scratch buffers. */
 tvk_status tvk_memory_reserved(int device, size_t* bytes);
 tvk_status tvk_reset_peak_memory_stats(int device);
 /* (free, total) as hipMemGetInfo reports them (src/api/backend.cpp:82-85). */
@@ -404,6 +406,19 @@ typedef struct {
 } tvk_gemm_desc;
 
 tvk_status tvk_gemm(const tvk_gemm_desc* desc);
+
+/* tvk_gemm without any allocation: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The product's scratch
+ * (split-K partials, repacked operands) lives in a 32 MiB array the library
+ * holds on each device it runs on until the process ends; a product whose
+ * shape-chosen kernel needs more is rejected with TVK_ERR_INVALID before
+ * anything is queued (tvk_gemm takes it). The kernel is the shape rules'
+ * choice (the kernel-choice table is not consulted). Every call on a device
+ * shares that device's array: calls that overlap on one device (two streams,
+ * or two threads, without ordering between them) race on it; calls ordered on
+ * one stream do not. Results are those of tvk_gemm with the same kernel. */
+tvk_status tvk_gemm_noalloc(const tvk_gemm_desc* desc);
 
 /* Name of the kernel tvk_gemm would launch for `desc` (no launch). Used by
  * tests and the benchmark to state which path ran; replaces the tuner's

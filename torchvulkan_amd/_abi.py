@@ -239,7 +239,8 @@ _ALL_ENTRY_POINTS = (
     "tvk_gemm_choose", "tvk_gemm_tune", "tvk_tune_reset", "tvk_tune_path",
     "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad", "tvk_copy", "tvk_copy_plan",
     "tvk_fill", "tvk_reduce_sum", "tvk_binary", "tvk_attention_fwd",
-    "tvk_attention_bwd",
+    "tvk_attention_bwd", "tvk_gemm_noalloc", "tvk_event_create", "tvk_event_destroy", "tvk_event_record",
+    "tvk_event_query", "tvk_event_synchronize", "tvk_event_elapsed", "tvk_stream_wait_event", "tvk_stream_query",
 )
 
 
@@ -489,6 +490,16 @@ def gemm(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, strea
         stream = torch.cuda.current_stream(c.device).cuda_stream
     d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, stream, exact)
     check(load().tvk_gemm(C.byref(d)))
+
+
+def gemm_noalloc(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, stream=None, exact=False) -> None:
+    """tvk_gemm_noalloc: tvk_gemm with its scratch in the library's fixed per-device array (no allocation)."""
+    import torch
+
+    if stream is None and c.is_cuda:
+        stream = torch.cuda.current_stream(c.device).cuda_stream
+    d = make_gemm_desc(a, b, c, bias, alpha, beta, activation, stream, exact)
+    check(load().tvk_gemm_noalloc(C.byref(d)))
 
 
 def gemm_plan(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, exact=False) -> str:

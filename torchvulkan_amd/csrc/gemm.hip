@@ -22,6 +22,8 @@
 //                v_mfma_f32_32x32x1f32 rank-1 updates (one rounding each).
 //   gemm_generic any strides / dtype, one thread per output, same order.
 #include "gemm_common.h"
+
+#include <mutex>
 #include "tune_table.h"
 
 #include <algorithm>
@@ -846,8 +848,31 @@ void launch_seq(const Plan& pl, GemmArgs& p, dim3 grid, hipStream_t s) {
     TVK_LAYOUT_SWITCH(pl, 256, gemm_seq_mfma_kernel);
 }
 
+// Scratch bytes one batch chunk of `nb` matrices needs under plan pl:
+// repacked operands (256-byte aligned each), then split-K partials, or the
+// streaming kernel's partials. rep_a / rep_b / part_b return the pieces.
+size_t plan_scratch_bytes(const tvk_gemm_desc& d, const Plan& pl, int nb, size_t* rep_a_out = nullptr,
+                          size_t* rep_b_out = nullptr) {
+    auto al256 = [](size_t v) { return (v + 255) / 256 * 256; };
+    const int64_t a_rows = pl.ak ? d.M : d.K, a_ld = pad8(pl.ak ? d.K : d.M);
+    const int64_t b_rows = pl.bk ? d.N : d.K, b_ld = pad8(pl.bk ? d.K : d.N);
+    const size_t rep_a = pl.repack_a ? al256((size_t)nb * a_rows * a_ld * 2) : 0;
+    const size_t rep_b = pl.repack_b ? al256((size_t)nb * b_rows * b_ld * 2) : 0;
+    size_t part_b = pl.split > 1 ? (size_t)pl.split * nb * d.M * d.N * 4 : 0;
+    if (pl.kern == Kern::SKINNY) {
+        GemmArgs q = make_args(d);
+        q.batch = nb;
+        part_b = skinny_scratch_bytes(q, pl.bk, pl.vec);
+    }
+    if (rep_a_out) *rep_a_out = rep_a;
+    if (rep_b_out) *rep_b_out = rep_b;
+    return rep_a + rep_b + part_b;
+}
+
+// Runs one planned product. `fixed` (capacity fixed_cap bytes) replaces the
+// pool lease when the caller brings its own scratch.
 template <int DT>
-tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
+tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixed = nullptr, size_t fixed_cap = 0) {
     const GemmArgs p = make_args(d);
 
     const int64_t max_y = 65535;
@@ -860,17 +885,19 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
         q.b = (const char*)d.b + (size_t)(b0 * d.b_stride[0]) * es;
         if (q.has_bias) q.bias = (const char*)d.bias + (size_t)(b0 * d.bias_stride[0]) * es;
         q.c = (char*)d.c + (size_t)(b0 * d.c_stride[0]) * es;
-        // workspace: repacked operands, then split-K partials
-        auto al256 = [](size_t v) { return (v + 255) / 256 * 256; };
+        // scratch: repacked operands, then split-K partials
         const int64_t a_rows = pl.ak ? d.M : d.K, a_ld = pad8(pl.ak ? d.K : d.M);
         const int64_t b_rows = pl.bk ? d.N : d.K, b_ld = pad8(pl.bk ? d.K : d.N);
-        const size_t rep_a = pl.repack_a ? al256((size_t)nb * a_rows * a_ld * 2) : 0;
-        const size_t rep_b = pl.repack_b ? al256((size_t)nb * b_rows * b_ld * 2) : 0;
-        const size_t part_b = pl.split > 1 ? (size_t)pl.split * nb * d.M * d.N * 4 : 0;
+        size_t rep_a = 0, rep_b = 0;
+        const size_t need = plan_scratch_bytes(d, pl, nb, &rep_a, &rep_b);
         char* ws = nullptr;
         Scratch scratch;
-        if (rep_a + rep_b + part_b > 0) {
-            ws = static_cast<char*>(scratch.get(rep_a + rep_b + part_b, s));
+        if (fixed) {
+            if (need > fixed_cap) return fail(TVK_ERR_INVALID, "tvk_gemm: scratch of " + std::to_string(need) + " bytes exceeds the " +
+                                                                   std::to_string(fixed_cap) + " provided");
+            ws = fixed;
+        } else if (need > 0) {
+            ws = static_cast<char*>(scratch.get(need, s));
             if (!ws) return fail(TVK_ERR_OOM, "tvk_gemm: no workspace for repacked operands or split-K partials");
         }
         if constexpr (DT != TVK_F32) {
@@ -922,7 +949,7 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s) {
         }
         case Kern::SKINNY:
             if constexpr (DT != TVK_F32) {
-                hipError_t e = launch_skinny(DT, q, pl.bk, pl.vec, s);
+                hipError_t e = launch_skinny(DT, q, pl.bk, pl.vec, s, fixed ? reinterpret_cast<float*>(ws) : nullptr);
                 if (e != hipSuccess) return fail(e == hipErrorOutOfMemory ? TVK_ERR_OOM : TVK_ERR_DEVICE,
                                                   std::string("tvk_gemm: skinny launch failed: ") + hipGetErrorString(e));
             }
@@ -1006,12 +1033,12 @@ Plan choose_plan(const tvk_gemm_desc& d) {
     return make_plan(d);
 }
 
-tvk_status run_plan(const tvk_gemm_desc& d, const Plan& pl) {
+tvk_status run_plan(const tvk_gemm_desc& d, const Plan& pl, char* fixed = nullptr, size_t fixed_cap = 0) {
     const hipStream_t s = resolve_stream(d.stream);
     switch (d.dtype) {
-    case TVK_F32: return run<TVK_F32>(d, pl, s);
-    case TVK_F16: return run<TVK_F16>(d, pl, s);
-    default: return run<TVK_BF16>(d, pl, s);
+    case TVK_F32: return run<TVK_F32>(d, pl, s, fixed, fixed_cap);
+    case TVK_F16: return run<TVK_F16>(d, pl, s, fixed, fixed_cap);
+    default: return run<TVK_BF16>(d, pl, s, fixed, fixed_cap);
     }
 }
 
@@ -1101,11 +1128,14 @@ extern "C" tvk_status tvk_gemm_plan(const tvk_gemm_desc* desc, char* name, size_
     return TVK_OK;
 }
 
-extern "C" tvk_status tvk_gemm(const tvk_gemm_desc* desc) {
-    tvk_status st = validate(desc);
-    if (st != TVK_OK) return st;
-    const tvk_gemm_desc& d = *desc;
-    if (d.batch == 0 || d.M == 0 || d.N == 0) return TVK_OK;
+namespace tvk {
+namespace {
+
+// tvk_gemm's body: the product, in row/column blocks when an operand spans
+// 2 GiB. `plan_of` picks each block's kernel; `fixed` as for run().
+template <class PlanOf>
+tvk_status gemm_blocks(const tvk_gemm_desc& d, PlanOf plan_of, char* fixed, size_t fixed_cap) {
+    tvk_status st = TVK_OK;
     int64_t mc = d.M, nc = d.N;
     if (d.K > 0 && extent_chunks(d, mc, nc) && (mc < d.M || nc < d.N)) {
         // row and column blocks whose operand extents fit the tiled kernels'
@@ -1120,12 +1150,76 @@ extern "C" tvk_status tvk_gemm(const tvk_gemm_desc* desc) {
                 sub.b = static_cast<const char*>(d.b) + (size_t)(n0 * d.b_stride[2]) * es;
                 sub.c = static_cast<char*>(d.c) + (size_t)(m0 * d.c_stride[1] + n0 * d.c_stride[2]) * es;
                 if (d.bias) sub.bias = static_cast<const char*>(d.bias) + (size_t)(m0 * d.bias_stride[1] + n0 * d.bias_stride[2]) * es;
-                st = run_plan(sub, choose_plan(sub));
+                st = run_plan(sub, plan_of(sub), fixed, fixed_cap);
                 if (st != TVK_OK) return st;
             }
         return TVK_OK;
     }
-    return run_plan(d, choose_plan(d));
+    return run_plan(d, plan_of(d), fixed, fixed_cap);
+}
+
+// Scratch of the allocation-free entry point: one array per device, in the
+// code object (the runtime places it when the library's module loads on a
+// device and keeps it until the process ends). Host code must not pass the
+// array's name to a kernel: that is a host-side stand-in, not the device
+// address. Each device's address comes from hipGetSymbolAddress, once per
+// device, with that device current.
+constexpr size_t kNoAllocScratch = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratch];
+
+constexpr int kMaxScratchDevices = 64;
+std::once_flag g_scratch_once[kMaxScratchDevices];
+char* g_scratch_ptr[kMaxScratchDevices] = {};
+hipError_t g_scratch_err[kMaxScratchDevices] = {};
+
+// The current device's address of `scratch` (NULL with *err set on failure).
+char* noalloc_scratch(int dev, hipError_t* err) {
+    std::call_once(g_scratch_once[dev], [dev]() {
+        void* ptr = nullptr;
+        g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (g_scratch_err[dev] == hipSuccess) g_scratch_ptr[dev] = static_cast<char*>(ptr);
+        else (void)hipGetLastError();
+    });
+    *err = g_scratch_err[dev];
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace tvk
+
+extern "C" tvk_status tvk_gemm(const tvk_gemm_desc* desc) {
+    tvk_status st = validate(desc);
+    if (st != TVK_OK) return st;
+    const tvk_gemm_desc& d = *desc;
+    if (d.batch == 0 || d.M == 0 || d.N == 0) return TVK_OK;
+    return gemm_blocks(d, [](const tvk_gemm_desc& x) { return choose_plan(x); }, nullptr, 0);
+}
+
+extern "C" tvk_status tvk_gemm_noalloc(const tvk_gemm_desc* desc) {
+    tvk_status st = validate(desc);
+    if (st != TVK_OK) return st;
+    const tvk_gemm_desc& d = *desc;
+    if (d.batch == 0 || d.M == 0 || d.N == 0) return TVK_OK;
+    // every block's scratch must fit the array before anything is queued
+    int64_t mc = d.M, nc = d.N;
+    tvk_gemm_desc first = d;
+    if (d.K > 0 && extent_chunks(d, mc, nc)) {
+        first.M = mc;
+        first.N = nc;
+    }
+    const int nb = (int)std::min<int64_t>(65535, d.batch);
+    const size_t need = plan_scratch_bytes(first, make_plan(first), nb);
+    if (need > kNoAllocScratch)
+        return fail(TVK_ERR_INVALID, "tvk_gemm_noalloc: this product needs " + std::to_string(need) +
+                                         " bytes of scratch (split-K partials or repacked operands), more than the " +
+                                         std::to_string(kNoAllocScratch) + " the entry point holds; use tvk_gemm");
+    int dev = 0;
+    TVK_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxScratchDevices) return fail(TVK_ERR_INVALID, "tvk_gemm_noalloc: device index out of range");
+    hipError_t err = hipSuccess;
+    char* ws = noalloc_scratch(dev, &err);
+    if (!ws) return fail(TVK_ERR_DEVICE, std::string("tvk_gemm_noalloc: hipGetSymbolAddress failed: ") + hipGetErrorString(err));
+    return gemm_blocks(d, [](const tvk_gemm_desc& x) { return make_plan(x); }, ws, kNoAllocScratch);
 }
 
 extern "C" tvk_status tvk_gemm_candidates(const tvk_gemm_desc* desc, char* names, size_t names_len) {

@@ -207,8 +207,12 @@ bool conv_small_applies(const tvk_conv_desc& d, int mode);
 tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who);
 
 // M <= 16 streaming kernel (gemm_skinny.hip). b_kmajor: B's k stride is 1.
-// vec: 16-byte loads are legal for A and B. Returns hipSuccess or the launch error.
-hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, hipStream_t s);
+// vec: 16-byte loads are legal for A and B. `part`: skinny_scratch_bytes of
+// caller-provided scratch for split-K partials, or NULL to lease them from the
+// library's pool. Returns hipSuccess or the launch error.
+hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, hipStream_t s, float* part = nullptr);
+// Scratch bytes launch_skinny needs for this product (0: none).
+size_t skinny_scratch_bytes(const GemmArgs& p, bool b_kmajor, bool vec);
 const char* skinny_name(const GemmArgs& p, bool b_kmajor, bool vec);
 bool skinny_applies(int64_t M, int64_t N, int64_t K, int64_t batch);
 

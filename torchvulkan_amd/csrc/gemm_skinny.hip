@@ -299,14 +299,20 @@ const char* skinny_name(const GemmArgs& p, bool b_kmajor, bool vec) {
     return b_kmajor ? "gemm16_skinny_bk" : "gemm16_skinny_bn";
 }
 
-hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, hipStream_t s) {
+size_t skinny_scratch_bytes(const GemmArgs& p, bool b_kmajor, bool vec) {
+    if (!ring_applies(p, b_kmajor, vec)) return 0;
+    const int split = ring_splits(p);
+    return split > 1 ? (size_t)split * p.batch * p.M * p.N * 4 : 0;
+}
+
+hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, hipStream_t s, float* part) {
     if (ring_applies(p, b_kmajor, vec)) {
         GemmArgs q = p;
         q.split = ring_splits(p);
         q.k_chunk = p.K / q.split;
         Scratch scratch;
         if (q.split > 1) {
-            q.part = static_cast<float*>(scratch.get((size_t)q.split * p.batch * p.M * p.N * 4, s));
+            q.part = part ? part : static_cast<float*>(scratch.get((size_t)q.split * p.batch * p.M * p.N * 4, s));
             if (!q.part) return hipErrorOutOfMemory;
         }
         const dim3 grid((p.N + SR_NB - 1) / SR_NB, q.split, p.batch);

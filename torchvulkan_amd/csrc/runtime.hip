@@ -390,7 +390,20 @@ tvk_status tvk_set_memory_limit(int device, size_t bytes) {
     }
 TVK_STAT_GETTER(tvk_memory_allocated, allocated)
 TVK_STAT_GETTER(tvk_max_memory_allocated, peak)
-TVK_STAT_GETTER(tvk_memory_reserved, reserved)
+
+// The caching allocator's blocks plus the scratch pool's buffers.
+tvk_status tvk_memory_reserved(int device, size_t* bytes) {
+    if (!bytes) return fail(TVK_ERR_INVALID, "tvk_memory_reserved: bytes is NULL");
+    if (device < 0 || device >= kMaxDevices) return fail(TVK_ERR_INVALID, "tvk_memory_reserved: invalid device index");
+    size_t pool = 0;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (g_scratch[device]) pool = g_scratch[device]->pool.total_bytes();
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    *bytes = g_dev[device].reserved + pool;
+    return TVK_OK;
+}
 
 tvk_status tvk_reset_peak_memory_stats(int device) {
     if (device < 0 || device >= kMaxDevices) return fail(TVK_ERR_INVALID, "tvk_reset_peak_memory_stats: invalid device index");

@@ -108,6 +108,14 @@ public:
         return bufs_.size();
     }
 
+    // Bytes of every buffer the pool holds (held or idle).
+    size_t total_bytes() {
+        std::lock_guard<std::mutex> lk(mu_);
+        size_t n = 0;
+        for (auto& b : bufs_) n += b->bytes;
+        return n;
+    }
+
     size_t held_count() {
         std::lock_guard<std::mutex> lk(mu_);
         size_t n = 0;
