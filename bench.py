@@ -89,6 +89,11 @@ def profile_kernel(which, steps):
     print(f"{which}: {steps} launches of {_abi.gemm_plan(a, (bufs[0] if which == 'skinny' else b), c)}", flush=True)
 
 
+def progress(msg: str) -> None:
+    """A progress line on stderr (stdout carries only the result line)."""
+    print(f"bench.py: {msg}", file=sys.stderr, flush=True)
+
+
 def timed(fn, steps, warmup, stream):
     """Runs fn warmup times, then times `steps` calls with events on `stream`.
 
@@ -154,6 +159,7 @@ def main():
             _abi.check(st)
 
     ms, host_ms = timed(step, args.steps, args.warmup, stream)
+    progress(f"headline done: {ms:.4f} ms per step")
     flops = 2.0 * n * n * n
     tflops = flops / (ms * 1e-3) / 1e12
     roofline = {
@@ -204,6 +210,11 @@ def main():
     print(json.dumps(line))
 
 
+def bound_us(flops: float, nbytes: float) -> float:
+    """Roofline time of a launch: the larger of its dense fp16 MFMA time and its HBM time."""
+    return max(flops / (PEAK_F16_TFLOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) * 1e6
+
+
 def run_extra(torch, _abi, dev, stream, steps, warmup):
     out = {}
     # ---- C2 MLP chain fwd+bwd (GEMMs only, fp16) ----------------------------
@@ -241,10 +252,29 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
 
     ms, _ = timed(mlp_step, steps, warmup, stream)
     fl = 0
+    c2_bound = 0.0
     for d in descs:
         fl += 2 * d.M * d.N * d.K
+        c2_bound += bound_us(2 * d.M * d.N * d.K, 2 * (d.M * d.K + d.K * d.N + d.M * d.N + (d.N if d.bias else 0)))
     out["c2_mlp_gemm_fwd_bwd_ms"] = round(ms, 4)
+    progress("C2 chain done")
     out["c2_mlp_gemm_tflops"] = round(fl / (ms * 1e-3) / 1e12, 2)
+    out["c2_bound_ms"] = round(c2_bound / 1e3, 4)
+    out["c2_roofline_frac"] = round(c2_bound / 1e3 / ms, 4)
+    # the batch-256 layers alone: 256x4096x4096 (x W^T and dY W) and 4096x4096x256 (dY^T x)
+    for name, i in (("c2_fwd_256x4096x4096_us", 1), ("c2_dx_256x4096x4096_us", 7), ("c2_dw_4096x4096x256_us", 6)):
+        r = refs[i]
+
+        def one(r=r):
+            st = lib.tvk_gemm(r)
+            if st:
+                _abi.check(st)
+
+        ms1, _ = timed(one, steps * 4, warmup, stream)
+        d = descs[i]
+        b1 = bound_us(2 * d.M * d.N * d.K, 2 * (d.M * d.K + d.K * d.N + d.M * d.N))
+        out[name] = {"us": round(ms1 * 1e3, 2), "bound_us": round(b1, 2), "frac": round(b1 / (ms1 * 1e3), 4),
+                     "kernel": gemm_plan_of(_abi, d)}
 
     # ---- C5 skinny 16x4096x14336 fp16, B rotated past the Infinity Cache ----
     M, K, N = 16, 4096, 14336
@@ -264,6 +294,7 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
 
     ms, _ = timed(skinny_step, steps * 3, warmup, stream)
     byts = 2 * (M * K + K * N + M * N)
+    progress("C5 skinny done")
     out["c5_skinny_kernel"] = _abi.gemm_plan(a, bufs[0], c)
     out["c5_skinny_us"] = round(ms * 1e3, 2)
     out["c5_skinny_GBps"] = round(byts / (ms * 1e-3) / 1e9, 1)
@@ -300,7 +331,34 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
 
     ms, _ = timed(conv_step, steps, warmup, stream)
     out["c4_resnet_conv_fwd_bwd_ms"] = round(ms, 4)
+    progress("C4 chain done")
     out["c4_resnet_conv_tflops"] = round(conv_flops / (ms * 1e-3) / 1e12, 2)
+    # per layer: each direction's time and its roofline (conv flops at the MFMA peak, or the
+    # NCHW bytes it must move: two activations and the weights, at the HBM peak)
+    per_layer = []
+    c4_bound = 0.0
+    for li, (cin, cout, k, st, pd, hw) in enumerate(layers):
+        ho = (hw + 2 * pd - k) // st + 1
+        fl1 = 2 * 128 * cout * ho * ho * cin * k * k
+        by1 = 2 * (128 * cin * hw * hw + 128 * cout * ho * ho + cout * cin * k * k)
+        row = {"layer": f"{cin}->{cout} {k}x{k} s{st}", "bound_us": round(bound_us(fl1, by1), 2)}
+        for j, dirn in enumerate(("fwd", "dgrad", "wgrad")):
+            fn, r = conv_refs[3 * li + j]
+
+            def one(fn=fn, r=r):
+                st_ = fn(r)
+                if st_:
+                    _abi.check(st_)
+
+            ms1, _ = timed(one, steps * 2, warmup, stream)
+            row[f"{dirn}_us"] = round(ms1 * 1e3, 2)
+            row[f"{dirn}_frac"] = round(bound_us(fl1, by1) / (ms1 * 1e3), 4)
+            c4_bound += bound_us(fl1, by1)
+        per_layer.append(row)
+    out["c4_layers"] = per_layer
+    progress("C4 layers done")
+    out["c4_bound_ms"] = round(c4_bound / 1e3, 4)
+    out["c4_roofline_frac"] = round(c4_bound / 1e3 / ms, 4)
     del keep, conv_refs, conv_calls
 
     # ---- C3 transformer layer GEMMs (fp16, tokens 8192): fwd + bwd ----------
@@ -320,14 +378,9 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
         llm_descs += [_abi.make_gemm_desc(x, w.t(), y, stream=s), _abi.make_gemm_desc(dy, w, dx, stream=s),
                       _abi.make_gemm_desc(dy.t(), x, dw, stream=s)]
         llm_flops += 3 * 2 * T * fin * fout
-    # attention products per layer: 256 (batch x heads) of [256,64]x[64,256] and [256,256]x[256,64]
-    q = torch.randn((256, 256, 64), generator=g).to(torch.float16).to(dev)
-    kk = torch.randn((256, 256, 64), generator=g).to(torch.float16).to(dev)
-    sc = torch.empty((256, 256, 256), dtype=torch.float16, device=dev)
-    pv = torch.empty((256, 256, 64), dtype=torch.float16, device=dev)
-    keep += [q, kk, sc, pv]
-    llm_descs += [_abi.make_gemm_desc(q, kk.transpose(1, 2), sc, stream=s), _abi.make_gemm_desc(sc, kk, pv, stream=s)]
-    llm_flops += 2 * 2 * 256 * 256 * 256 * 64
+    llm_bound = 0.0
+    for d in llm_descs:
+        llm_bound += bound_us(2 * d.M * d.N * d.K, 2 * (d.M * d.K + d.K * d.N + d.M * d.N))
     llm_refs = [C.byref(d) for d in llm_descs]
 
     def llm_step():
@@ -338,8 +391,40 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
 
     ms, _ = timed(llm_step, steps, warmup, stream)
     out["c3_llm_layer_gemm_fwd_bwd_ms"] = round(ms, 4)
+    progress("C3 GEMMs done")
     out["c3_llm_layer_gemm_tflops"] = round(llm_flops / (ms * 1e-3) / 1e12, 2)
+    out["c3_llm_layer_gemm_roofline_frac"] = round(llm_bound / 1e3 / ms, 4)
     del keep, llm_refs, llm_descs
+
+    # attention products on head-strided views, as the math path meets them: per sequence,
+    # q [L, H, D] and k, v [S, H, D] from the projections (GQA's kv heads already repeated to H),
+    # S = q k^T and O = P v as batches over the H heads (batch stride D, row stride H*D)
+    Bq, H, L, D = 32, 8, 256, 64
+    qs = torch.randn((Bq, L, H, D), generator=g).to(torch.float16).to(dev)
+    ks = torch.randn((Bq, L, H, D), generator=g).to(torch.float16).to(dev)
+    vs = torch.randn((Bq, L, H, D), generator=g).to(torch.float16).to(dev)
+    ss = torch.empty((Bq, H, L, L), dtype=torch.float16, device=dev)
+    os_ = torch.empty((Bq, L, H, D), dtype=torch.float16, device=dev)
+    hd = []
+    for bi in range(Bq):
+        hd.append(_abi.make_gemm_desc(qs[bi].transpose(0, 1), ks[bi].transpose(0, 1).transpose(1, 2), ss[bi], stream=s))
+        hd.append(_abi.make_gemm_desc(ss[bi], vs[bi].transpose(0, 1), os_[bi].transpose(0, 1), stream=s))
+    hrefs = [C.byref(d) for d in hd]
+
+    def bmm_step():
+        for r in hrefs:
+            st_ = lib.tvk_gemm(r)
+            if st_:
+                _abi.check(st_)
+
+    ms, _ = timed(bmm_step, steps, warmup, stream)
+    bmm_fl = 2 * 2 * Bq * H * L * L * D
+    bmm_by = 2 * (4 * Bq * L * H * D + 2 * Bq * H * L * L)
+    out["c3_head_strided_bmm_us"] = round(ms * 1e3, 2)
+    progress("C3 head-strided bmm done")
+    out["c3_head_strided_bmm_kernels"] = [gemm_plan_of(_abi, hd[0]), gemm_plan_of(_abi, hd[1])]
+    out["c3_head_strided_bmm_roofline_frac"] = round(bound_us(bmm_fl, bmm_by) / (ms * 1e3), 4)
+    del qs, ks, vs, ss, os_, hd, hrefs
 
     # ---- C3 attention: fused forward, batch 32, 8 query / 2 kv heads, seq 256, head_dim 64, causal
     qa = torch.randn((32, 8, 256, 64), generator=g).to(torch.float16).to(dev)
@@ -358,8 +443,10 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     ms, _ = timed(attn_step, steps * 4, warmup, stream)
     # causal: the unmasked half of the L x S scores (i >= j), two products of 2*D flops each
     att_flops = 32 * 8 * (256 * 257 // 2) * 64 * 2 * 2
+    att_bytes = 2 * (2 * 32 * 8 * 256 * 64 + 2 * 32 * 2 * 256 * 64) + 4 * 32 * 8 * 256
     out["c3_attention_fwd_us"] = round(ms * 1e3, 2)
     out["c3_attention_fwd_tflops"] = round(att_flops / (ms * 1e-3) / 1e12, 2)
+    out["c3_attention_fwd_roofline_frac"] = round(bound_us(att_flops, att_bytes) / (ms * 1e3), 4)
     # backward: five products over the unmasked half (S, dP, dV, dQ, dK; S is recomputed in both passes)
     da = torch.randn(oa.shape, generator=g).to(torch.float16).to(dev)
     gq, gk, gv = torch.empty_like(qa), torch.empty_like(ka), torch.empty_like(va)
@@ -378,7 +465,9 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
 
     ms, _ = timed(attn_bwd_step, steps * 4, warmup, stream)
     out["c3_attention_bwd_us"] = round(ms * 1e3, 2)
+    progress("C3 attention done")
     out["c3_attention_bwd_tflops"] = round(att_flops * 5 / 2 / (ms * 1e-3) / 1e12, 2)
+    out["c3_attention_bwd_roofline_frac"] = round(bound_us(att_flops * 5 / 2, 2 * att_bytes) / (ms * 1e3), 4)
     del qa, ka, va, oa, la, da, gq, gk, gv
 
     # ---- C5 ragged [1000,777]x[777,3000] and baddbmm in[64,512,512] + 0.5*bmm ----
@@ -397,6 +486,8 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c5_ragged_kernel"] = _abi.gemm_plan(a, b, c)
     out["c5_ragged_us"] = round(ms * 1e3, 2)
     out["c5_ragged_tflops"] = round(2 * 1000 * 777 * 3000 / (ms * 1e-3) / 1e12, 2)
+    out["c5_ragged_roofline_frac"] = round(bound_us(2 * 1000 * 777 * 3000, 2 * (1000 * 777 + 777 * 3000 + 1000 * 3000))
+                                           / (ms * 1e3), 4)
     x1 = torch.randn((64, 512, 128), generator=g).to(torch.float16).to(dev)
     x2 = torch.randn((64, 128, 512), generator=g).to(torch.float16).to(dev)
     inp = torch.randn((64, 512, 512), generator=g).to(torch.float16).to(dev)
@@ -435,6 +526,8 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     ms, _ = timed(c1_step, steps, warmup, stream)
     out["c1_fp32_mm_1024_us"] = round(ms * 1e3, 2)
     out["c1_fp32_tflops"] = round(2 * 1024 ** 3 / (ms * 1e-3) / 1e12, 2)
+    out["c1_fp32_roofline_frac"] = round(max(2 * 1024 ** 3 / (PEAK_F32_TFLOPS * 1e12), 12 * 1024 ** 2 / (PEAK_HBM_GBS * 1e9))
+                                         * 1e6 / (ms * 1e3), 4)
     out["c1_kernel"] = _abi.gemm_plan(a, b, c)
     return out
 
@@ -453,6 +546,7 @@ def run_memory_ops(torch, _abi, dev, stream, steps, warmup, g):
         ms, _ = timed(call, steps * 2, warmup, stream)
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"us": round(ms * 1e3, 2), "GBps": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 2)}
+        progress(f"{name} done")
 
     def copy_call(src, dst):
         d = _abi.make_copy_desc(src, dst, stream=s)
@@ -499,29 +593,158 @@ def run_memory_ops(torch, _abi, dev, stream, steps, warmup, g):
     return {"memory_ops": res}
 
 
+def gemm_plan_of(_abi, desc) -> str:
+    import ctypes as C
+
+    buf = C.create_string_buffer(128)
+    _abi.check(_abi.load().tvk_gemm_plan(C.byref(desc), buf, 128))
+    return buf.value.decode()
+
+
+def host_info() -> dict:
+    """The host CPU as lscpu reports it, and the cores this process may use."""
+    import subprocess
+
+    model = ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return {"model": model, "cpu_count": os.cpu_count(), "usable_cores": usable}
+
+
+def lavapipe_status() -> str:
+    """The reference's own shaders run on Mesa lavapipe only when its ICD and slangc exist on the host."""
+    import glob
+    import shutil
+
+    icds = [f for d in ("/usr/share/vulkan/icd.d", "/etc/vulkan/icd.d", "/usr/local/share/vulkan/icd.d")
+            for f in glob.glob(os.path.join(d, "lvp_icd*.json"))]
+    if icds and shutil.which("slangc"):
+        return "lavapipe and slangc present; not run (the reference builds against torch 2.15 with CMake and Slang codegen)"
+    return "lavapipe baseline unavailable (no Mesa lavapipe / Slang on host)"
+
+
+def median_ms(fn, reps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def torch_cpu_baselines(cores: int) -> dict:
+    """torch on the host cores, as the reference's benchmark times its CPU
+    device (median of 10 after 3 warm-ups, benchmark/benchmark.py:208-223):
+    rows of the headline product in float32, float16 and bfloat16 (float16 and
+    bfloat16 are the CPU's slow low-precision paths), and the C2 MLP GEMM chain
+    and the C4 convolution layers forward + backward in float32."""
+    import torch
+    import torch.nn.functional as F
+
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    n = 8192
+    out = {}
+    a = torch.randn((1024, n), generator=g)
+    b = torch.randn((n, n), generator=g)
+    samples = []
+    for name, dt in (("f32", torch.float32), ("f16", torch.float16), ("bf16", torch.bfloat16)):
+        bb = b.to(dt)
+        # rows sized so one call takes about 0.25 s (the CPU's low-precision paths can be slow)
+        probe = a[:16].to(dt)
+        t0 = time.perf_counter()
+        torch.mm(probe, bb)
+        t16 = time.perf_counter() - t0
+        rows = int(min(1024, max(16, 16 * 0.25 / max(t16, 1e-6)))) // 16 * 16
+        aa = a[:rows].to(dt)
+        ms = median_ms(lambda: torch.mm(aa, bb), 10, 3)
+        out[f"mm_{name}_tflops"] = round(2.0 * rows * n * n / (ms * 1e-3) / 1e12, 4)
+        samples.append(f"{name} {rows} rows")
+        progress(f"cpu baseline: torch {name} mm done")
+    out["mm_sample"] = "rows of the 8192^3 mm (" + ", ".join(samples) + "), median of 10 after 3 warm-ups"
+    # C2: the MLP's forward and backward GEMMs (784-4096-4096-4096-10, batch 256)
+    dims = [784, 4096, 4096, 4096, 10]
+    xs = [torch.rand((256, dims[0]), generator=g)]
+    ws = [torch.randn((dims[i + 1], dims[i]), generator=g) * dims[i] ** -0.5 for i in range(4)]
+    bs = [torch.randn((dims[i + 1],), generator=g) * 0.01 for i in range(4)]
+    dys = [torch.randn((256, d), generator=g) for d in dims[1:]]
+
+    def c2():
+        x = xs[0]
+        acts = [x]
+        for i in range(4):
+            x = torch.addmm(bs[i], x, ws[i].t())
+            acts.append(x)
+        for i in reversed(range(4)):
+            torch.mm(dys[i].t(), acts[i])
+            if i > 0:
+                torch.mm(dys[i], ws[i])
+
+    out["c2_mlp_gemm_fwd_bwd_ms_f32"] = round(median_ms(c2, 10, 3), 3)
+    progress("cpu baseline: torch C2 chain done")
+    # C4: every layer's forward, grad input and grad weight
+    layers = [(3, 64, 3, 1, 1, 32), (64, 64, 3, 1, 1, 32), (64, 128, 3, 2, 1, 32), (128, 256, 3, 2, 1, 16),
+              (64, 128, 1, 2, 0, 32), (128, 256, 1, 2, 0, 16)]
+    data = []
+    for cin, cout, k, st, pd, hw in layers:
+        x = torch.randn((128, cin, hw, hw), generator=g)
+        w = torch.randn((cout, cin, k, k), generator=g) * (2.0 / (cin * k * k)) ** 0.5
+        ho = (hw + 2 * pd - k) // st + 1
+        dy = torch.randn((128, cout, ho, ho), generator=g)
+        data.append((x, w, dy, st, pd))
+
+    def c4():
+        for x, w, dy, st, pd in data:
+            F.conv2d(x, w, stride=st, padding=pd)
+            torch.ops.aten.convolution_backward(dy, x, w, None, [st, st], [pd, pd], [1, 1], False, [0, 0], 1,
+                                                [True, True, False])
+
+    out["c4_resnet_conv_fwd_bwd_ms_f32"] = round(median_ms(c4, 5, 1), 3)
+    progress("cpu baseline: torch C4 chain done")
+    out["chains_sample"] = "whole C2 and C4 steps (float32); C2 median of 10 after 3, C4 median of 5 after 1"
+    return out
+
+
 def cpu_baseline():
-    """Times the oracle (the reference SIMD tile's algorithm restated in C) on
-    a bounded sample of the headline workload: 32 whole rows of the fp16
-    8192^3 product, on the host's cores."""
+    """The reference path on the host cores. `value`: the oracle (the
+    reference SIMD tile's algorithm restated in C, oracle/gemm_oracle.c,
+    sequential-k float32 FMA per output) on whole rows of the headline fp16
+    8192^3 product; torch's CPU device and the lavapipe probe beside it."""
     import numpy as np
     from oracle import oracle as orc
 
     orc.load()
-    n, rows = 8192, 32
+    host = host_info()
+    cores = max(1, host["usable_cores"])
+    n, rows = 8192, 256
     rng = np.random.default_rng(0)
     a = rng.standard_normal((rows, n)).astype(np.float16).view(np.uint16)
     b = rng.standard_normal((n, n)).astype(np.float16).view(np.uint16)
-    threads = max(1, min(16, os.cpu_count() or 1))
     t0 = time.perf_counter()
-    orc.gemm(a, b, orc.F16, threads=threads)
+    orc.gemm(a, b, orc.F16, threads=cores)
     dt = time.perf_counter() - t0
+    progress(f"cpu baseline: oracle rows done ({dt:.1f} s)")
     tfl = 2.0 * rows * n * n / dt / 1e12
     return {
         "value": round(tfl, 5),
         "unit": "TFLOP/s",
-        "cores": threads,
+        "cores": cores,
         "kind": "port",
-        "sample": f"{rows} of 8192 rows of the fp16 8192^3 mm (oracle/gemm_oracle.c, sequential-k fp32 FMA), {dt:.2f} s",
+        "label": "reference algorithm restated on CPU",
+        "sample": f"{rows} of 8192 rows of the fp16 8192^3 mm (oracle/gemm_oracle.c, sequential-k fp32 FMA), "
+                  f"{dt:.2f} s on {cores} threads",
+        "host": host,
+        "lavapipe": lavapipe_status(),
+        "torch_cpu": torch_cpu_baselines(cores),
     }
 
 

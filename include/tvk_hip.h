@@ -20,12 +20,13 @@
  *   - scratch memory: tvk_gemm, tvk_conv2d_*, tvk_reduce_sum and
  *     tvk_attention_bwd lease library scratch (split-K partials, repacked
  *     operands, convolution partials, the attention delta) from a per-device
- *     pool for the kernels they queue on their `stream`. A lease ends when the
- *     call returns, behind an event recorded on that stream: a later call on
- *     the same stream reuses the memory in stream order, a call on another
- *     stream first waits for that event, and no buffer is freed while a call
- *     holds it or its kernels may still run. Calls may therefore come from any
- *     thread and any stream; the caller orders only its own tensors.
+ *     pool for the kernels they queue on their `stream`. A buffer is leased
+ *     again only for the stream its first lease named, so stream order puts
+ *     each call's kernels after the previous holder's; concurrent calls (other
+ *     threads, other streams) get other buffers; buffers are freed only after
+ *     the device has drained (on growth, allocation failure or
+ *     tvk_empty_cache). Calls may therefore come from any thread and any
+ *     stream; the caller orders only its own tensors.
  */
 #ifndef TVK_HIP_H
 #define TVK_HIP_H

@@ -1,14 +1,15 @@
 // CPU model of the library's scratch pool (torchvulkan_amd/csrc/scratch_pool.h)
 // under a simulated device: streams are queues of operations that run only
-// when the model advances them, events complete when the stream reaches the
-// position they were recorded at, and every use of a buffer is an operation
-// on some stream. The model checks the pool's ownership rules:
+// when the model advances them, and every use of a buffer is an operation on
+// some stream. The model checks the pool's ownership rules:
 //   1. a buffer is never freed while an operation that uses it is pending;
-//   2. a buffer handed to stream s2 after use on stream s1 is used on s2 only
-//      after s2 waits for s1's last use of it (or that use has run);
-//   3. two holders never share a buffer.
-// Scenarios: same-stream reuse, cross-stream reuse, growth while another
-// lease is held, out-of-memory recovery, and a multi-threaded stress run.
+//   2. a buffer is only ever used on one stream (so stream order alone orders
+//      its successive holders);
+//   3. two holders never share a buffer;
+//   4. the hot path (a lease for a stream that has a large enough idle
+//      buffer) neither allocates nor drains the device.
+// Scenarios: same-stream reuse, several streams, growth while another lease is
+// held, out-of-memory recovery, and a multi-threaded stress run.
 // Prints "ok" and exits 0 on success; any violation aborts with a message.
 #include "scratch_pool.h"
 
@@ -29,27 +30,16 @@ namespace {
 }
 #define CHECK(c, msg) do { if (!(c)) die(msg); } while (0)
 
-struct Op {
-    enum Kind { USE, WAIT } kind;
-    void* ptr;         // USE
-    int on_stream;     // WAIT: stream waited for
-    long on_pos;       // WAIT: position (exclusive) it must have run to
-};
-
 struct Model {
     typedef int Stream;
-    typedef int Event;
 
     std::recursive_mutex mu;
-    std::map<int, std::vector<Op>> queue;   // stream -> operations
-    std::map<int, long> ran;                // stream -> operations run so far
-    std::map<int, std::map<int, long>> clock;   // stream -> (stream -> position it is ordered after)
-    std::map<int, std::pair<int, long>> events; // event -> (stream, position) recorded
+    std::map<int, std::vector<void*>> queue;   // stream -> pending uses
+    std::map<void*, int> home;                 // buffer -> the stream it was used on
     std::set<void*> live;
-    size_t budget = size_t(1) << 40, in_use = 0;
     std::map<void*, size_t> sizes;
-    int next_event = 1;
-    long allocs = 0, frees = 0, waits = 0;
+    size_t budget = size_t(1) << 40, in_use = 0;
+    long allocs = 0, frees = 0, drains = 0;
 
     // ---- backend interface ----
     void* alloc(size_t bytes) {
@@ -65,71 +55,33 @@ struct Model {
     void free(void* p) {
         std::lock_guard<std::recursive_mutex> lk(mu);
         for (auto& kv : queue)
-            for (long i = ran[kv.first]; i < (long)kv.second.size(); ++i)
-                if (kv.second[i].kind == Op::USE && kv.second[i].ptr == p) die("a buffer was freed while a use of it was pending");
+            for (void* u : kv.second)
+                if (u == p) die("a buffer was freed while a use of it was pending");
         CHECK(live.erase(p) == 1, "free of an unknown buffer");
         in_use -= sizes[p];
         sizes.erase(p);
+        home.erase(p);
         std::free(p);
         ++frees;
     }
-    Event make_event() {
+    void sync_device() {
         std::lock_guard<std::recursive_mutex> lk(mu);
-        return next_event++;
-    }
-    void destroy_event(Event e) {
-        std::lock_guard<std::recursive_mutex> lk(mu);
-        events.erase(e);
-    }
-    void record(Event e, Stream s) {
-        std::lock_guard<std::recursive_mutex> lk(mu);
-        events[e] = {s, (long)queue[s].size()};
-    }
-    void wait(Stream s, Event e) {
-        std::lock_guard<std::recursive_mutex> lk(mu);
-        auto it = events.find(e);
-        CHECK(it != events.end(), "wait on an event never recorded");
-        queue[s].push_back(Op{Op::WAIT, nullptr, it->second.first, it->second.second});
-        long& c = clock[s][it->second.first];
-        c = std::max(c, it->second.second);
-        ++waits;
-    }
-    void sync(Event e) {
-        std::lock_guard<std::recursive_mutex> lk(mu);
-        auto it = events.find(e);
-        CHECK(it != events.end(), "sync on an event never recorded");
-        run_until(it->second.first, it->second.second);
+        for (auto& kv : queue) kv.second.clear();
+        ++drains;
     }
 
     // ---- simulation ----
-    // Runs stream s up to position pos (exclusive), running what its waits need first.
-    void run_until(int s, long pos) {
-        std::vector<Op>& q = queue[s];
-        long& r = ran[s];
-        while (r < pos && r < (long)q.size()) {
-            const Op& op = q[r];
-            if (op.kind == Op::WAIT) run_until(op.on_stream, op.on_pos);
-            ++r;
-        }
-    }
-    // Queues a use of p on s, checking rule 2 against pending uses on other streams.
     void use(void* p, int s) {
         std::lock_guard<std::recursive_mutex> lk(mu);
         CHECK(live.count(p) == 1, "use of a freed buffer");
-        for (auto& kv : queue) {
-            const int other = kv.first;
-            if (other == s) continue;
-            for (long i = ran[other]; i < (long)kv.second.size(); ++i) {
-                const Op& op = kv.second[i];
-                if (op.kind == Op::USE && op.ptr == p && clock[s][other] <= i)
-                    die("a buffer was used on a stream before that stream waited for its pending use on another stream");
-            }
-        }
-        queue[s].push_back(Op{Op::USE, p, 0, 0});
+        auto it = home.find(p);
+        if (it == home.end()) home[p] = s;
+        else CHECK(it->second == s, "a buffer was used on a second stream");
+        queue[s].push_back(p);
     }
-    void run_all() {
+    void run_stream(int s) {
         std::lock_guard<std::recursive_mutex> lk(mu);
-        for (auto& kv : queue) run_until(kv.first, (long)kv.second.size());
+        queue[s].clear();
     }
 };
 
@@ -140,48 +92,37 @@ void same_stream_reuse() {
     Pool pool(m, 1024);
     auto* a = pool.acquire(100, 1);
     m.use(a->ptr, 1);
-    pool.release(a, 1);
+    pool.release(a);
+    const long allocs = m.allocs, drains = m.drains;
     auto* b = pool.acquire(200, 1);
     CHECK(b == a, "a released buffer big enough is reused on the same stream");
-    CHECK(m.waits == 0, "reuse on the same stream needs no wait");
+    CHECK(m.allocs == allocs && m.drains == drains, "the hot path neither allocates nor drains");
     m.use(b->ptr, 1);
-    pool.release(b, 1);
-    m.run_all();
+    pool.release(b);
     pool.trim();
     CHECK(m.live.empty(), "trim frees every idle buffer");
 }
 
-void cross_stream_reuse() {
+void streams_keep_their_buffers() {
     Model m;
     Pool pool(m, 1024);
     auto* a = pool.acquire(100, 1);
     m.use(a->ptr, 1);
-    pool.release(a, 1);
-    auto* b = pool.acquire(100, 2);   // still pending on stream 1
-    CHECK(b == a, "an idle buffer is reused across streams");
-    CHECK(m.waits == 1, "reuse on another stream waits for the event");
-    m.use(b->ptr, 2);                 // checked against the pending use on stream 1
-    pool.release(b, 2);
-    m.run_all();
-    pool.trim();
-}
-
-void prefer_same_stream() {
-    Model m;
-    Pool pool(m, 1024);
-    auto* a = pool.acquire(100, 1);
-    auto* b = pool.acquire(100, 2);
-    CHECK(a != b, "two holders get two buffers");
-    m.use(a->ptr, 1);
+    pool.release(a);
+    auto* b = pool.acquire(100, 2);   // stream 1's buffer is idle but not stream 2's
+    CHECK(b != a, "another stream gets its own buffer");
     m.use(b->ptr, 2);
-    pool.release(a, 1);
-    pool.release(b, 2);
-    auto* c = pool.acquire(100, 2);
-    CHECK(c == b, "the buffer last used on the acquiring stream is preferred");
-    CHECK(m.waits == 0, "no wait when the same stream's buffer is taken");
-    pool.release(c, 2);
-    m.run_all();
+    pool.release(b);
+    auto* c = pool.acquire(100, 1);
+    CHECK(c == a, "each stream reuses its own buffer");
+    m.use(c->ptr, 1);
+    auto* d = pool.acquire(100, 1);
+    CHECK(d != c, "two holders on one stream get two buffers");
+    m.use(d->ptr, 1);
+    pool.release(c);
+    pool.release(d);
     pool.trim();
+    CHECK(m.live.empty() && m.allocs == m.frees, "every buffer freed once");
 }
 
 void grow_while_held() {
@@ -189,19 +130,18 @@ void grow_while_held() {
     Pool pool(m, 1024);
     auto* small = pool.acquire(100, 1);   // held by "another thread"
     m.use(small->ptr, 1);
-    auto* big = pool.acquire(1 << 20, 2);
+    auto* big = pool.acquire(1 << 20, 1);
     CHECK(big != small && big->bytes >= (1u << 20), "growth allocates beside a held buffer");
     CHECK(m.live.count(small->ptr) == 1, "a held buffer is not freed by growth");
-    m.use(big->ptr, 2);
-    pool.release(big, 2);
-    pool.release(small, 1);               // pending use on stream 1 remains
-    // a request larger than every idle buffer retires the small one: only
-    // after its last use has run (the model aborts otherwise)
-    auto* bigger = pool.acquire(4 << 20, 3);
+    m.use(big->ptr, 1);
+    pool.release(big);
+    pool.release(small);                  // its use is still pending
+    // a request larger than every idle buffer of the stream retires them:
+    // only after the device drained (the model aborts otherwise)
+    auto* bigger = pool.acquire(4 << 20, 1);
     CHECK(m.live.size() == 1, "idle buffers too small for a request are retired");
-    m.use(bigger->ptr, 3);
-    pool.release(bigger, 3);
-    m.run_all();
+    m.use(bigger->ptr, 1);
+    pool.release(bigger);
     pool.trim();
     CHECK(m.live.empty() && m.allocs == m.frees, "every buffer freed once");
 }
@@ -211,18 +151,20 @@ void out_of_memory() {
     m.budget = 3000;
     Pool pool(m, 1024);
     auto* a = pool.acquire(1024, 1);
-    auto* b = pool.acquire(1024, 1);
+    auto* b = pool.acquire(1024, 2);
     m.use(a->ptr, 1);
-    pool.release(a, 1);
-    // 1024 + 1024 in use: a 2000-byte buffer fits only after the idle one is
-    // given back (after its pending use has run)
-    auto* c = pool.acquire(1900, 2);
-    CHECK(c != nullptr, "idle buffers are released to satisfy a request");
-    CHECK(pool.acquire(4096, 2) == nullptr, "a request beyond the budget fails cleanly");
-    pool.release(c, 2);
-    pool.release(b, 1);
-    m.run_all();
+    m.use(b->ptr, 2);
+    pool.release(a);
+    // 2048 in use: a 1900-byte buffer for stream 3 fits only after the idle
+    // one of stream 1 is given back (after the device drained)
+    auto* c = pool.acquire(1900, 3);
+    CHECK(c != nullptr, "idle buffers of any stream are released to satisfy a request");
+    CHECK(pool.acquire(4096, 3) == nullptr, "a request beyond the budget fails cleanly");
+    m.use(c->ptr, 3);
+    pool.release(c);
+    pool.release(b);
     pool.trim();
+    CHECK(m.live.empty(), "every buffer freed");
 }
 
 void threads() {
@@ -246,18 +188,14 @@ void threads() {
                 std::lock_guard<std::mutex> lk(held_mu);
                 held.erase(buf->ptr);
             }
-            pool.release(buf, stream);
-            if (rng() % 64 == 0) {
-                std::lock_guard<std::recursive_mutex> lk(m.mu);
-                m.run_until(stream, (long)m.queue[stream].size());
-            }
+            pool.release(buf);
+            if (rng() % 64 == 0) m.run_stream(stream);
         }
     };
     std::vector<std::thread> ts;
     for (int t = 0; t < 6; ++t) ts.emplace_back(worker, t);
     for (auto& t : ts) t.join();
     CHECK(pool.held_count() == 0, "no lease left held");
-    m.run_all();
     pool.trim();
     CHECK(m.live.empty(), "every buffer freed after trim");
 }
@@ -266,8 +204,7 @@ void threads() {
 
 int main() {
     same_stream_reuse();
-    cross_stream_reuse();
-    prefer_same_stream();
+    streams_keep_their_buffers();
     grow_while_held();
     out_of_memory();
     threads();

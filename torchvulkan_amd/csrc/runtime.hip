@@ -78,12 +78,11 @@ void release_cached_locked(int device) {
     (void)hipSetDevice(prev);
 }
 
-// The scratch pool's operations on one device: hipMalloc'd buffers, events
-// without timing, cross-stream waits (every call makes the device current
-// for its duration).
+// The scratch pool's operations on one device: hipMalloc'd buffers and a
+// device-wide drain before any free (every call makes the device current for
+// its duration).
 struct HipScratchBackend {
     typedef hipStream_t Stream;
-    typedef hipEvent_t Event;
     int device = 0;
 
     struct On {
@@ -101,16 +100,7 @@ struct HipScratchBackend {
         return p;
     }
     void free(void* p) { On on(device); (void)hipFree(p); }
-    Event make_event() {
-        On on(device);
-        hipEvent_t e = nullptr;
-        (void)hipEventCreateWithFlags(&e, hipEventDisableTiming);
-        return e;
-    }
-    void destroy_event(Event e) { if (e) (void)hipEventDestroy(e); }
-    void record(Event e, Stream s) { if (e) (void)hipEventRecord(e, s); }
-    void wait(Stream s, Event e) { if (e) (void)hipStreamWaitEvent(s, e, 0); }
-    void sync(Event e) { if (e) (void)hipEventSynchronize(e); }
+    void sync_device() { On on(device); (void)hipDeviceSynchronize(); }
 };
 
 struct DeviceScratch {
@@ -144,7 +134,7 @@ void* Scratch::get(size_t bytes, hipStream_t stream) {
 
 void Scratch::release() {
     if (!lease_) return;
-    device_scratch(device_)->pool.release(static_cast<ScratchPool<HipScratchBackend>::Buffer*>(lease_), stream_);
+    device_scratch(device_)->pool.release(static_cast<ScratchPool<HipScratchBackend>::Buffer*>(lease_));
     lease_ = nullptr;
 }
 
@@ -361,7 +351,7 @@ tvk_status tvk_empty_cache(int device) {
         std::lock_guard<std::mutex> lk(g_mu);
         release_cached_locked(device);
     }
-    device_scratch(device)->pool.trim();   // idle scratch buffers, each after its last use
+    device_scratch(device)->pool.trim();   // idle scratch buffers, after the device has drained
     return TVK_OK;
 }
 

@@ -1,20 +1,22 @@
-// Stream-ordered pool of library scratch buffers for one device.
+// Pool of library scratch buffers for one device, ordered by streams.
 //
 // Kernels of a call that need scratch memory (split-K partials, repacked
 // operands, convolution partials, the attention delta) lease one buffer for
 // the duration of the call's launches:
 //   - a held buffer belongs to its holder alone: a second acquirer, on any
 //     thread or stream, gets another buffer;
-//   - on release the pool records an event on the holder's stream after the
-//     holder's work; a later lease on the same stream needs nothing more
-//     (stream order), a lease on another stream first makes that stream wait
-//     for the event;
-//   - growing never frees a held buffer: idle buffers too small for a request
-//     are freed only after their last use has completed (their event), and a
-//     new, larger buffer is allocated beside any that are still held.
-// The logic is independent of HIP: the backend supplies the allocation,
-// event and stream-wait operations, so the ownership rules can be exercised
-// on the CPU with a model backend.
+//   - a buffer keeps the stream its first lease named and is only ever leased
+//     again for that stream, where stream order alone puts the next holder's
+//     kernels after the previous holder's. Nothing is recorded on the hot path
+//     (an event per call would put a barrier packet between every pair of
+//     kernels);
+//   - buffers are freed only on a slow path (a request larger than every idle
+//     buffer of its stream, an allocation failure, trim), after the whole
+//     device has drained, so no kernel of any stream can still use them; held
+//     buffers are never freed.
+// The logic is independent of HIP: the backend supplies allocation and the
+// device-wide wait, so the ownership rules can be exercised on the CPU with a
+// model backend.
 #pragma once
 
 #include <cstddef>
@@ -25,25 +27,18 @@
 namespace tvk {
 
 // Backend B provides:
-//   typedef ... Stream; typedef ... Event;
-//   void* alloc(size_t bytes);            nullptr when out of memory
+//   typedef ... Stream;
+//   void* alloc(size_t bytes);    nullptr when out of memory
 //   void free(void* p);
-//   Event make_event();
-//   void destroy_event(Event e);
-//   void record(Event e, Stream s);       e completes after the work queued on s so far
-//   void wait(Stream s, Event e);         work queued on s from now on runs after e
-//   void sync(Event e);                   blocks the host until e has completed
+//   void sync_device();           blocks the host until every stream's work has run
 template <class B>
 class ScratchPool {
 public:
     typedef typename B::Stream Stream;
-    typedef typename B::Event Event;
 
     struct Buffer {
         void* ptr = nullptr;
         size_t bytes = 0;
-        Event done{};            // recorded on `stream` when the last holder released
-        bool recorded = false;
         Stream stream{};
         bool held = false;
     };
@@ -57,50 +52,48 @@ public:
     Buffer* acquire(size_t bytes, Stream s) {
         std::lock_guard<std::mutex> lk(mu_);
         Buffer* pick = nullptr;
+        bool small_idle = false;
         for (auto& up : bufs_) {
             Buffer* b = up.get();
-            if (b->held || b->bytes < bytes) continue;
-            // prefer a buffer last used on this stream (no wait), then the smallest
-            const bool same = b->recorded && b->stream == s, pick_same = pick && pick->recorded && pick->stream == s;
-            if (!pick || (same && !pick_same) || (same == pick_same && b->bytes < pick->bytes)) pick = b;
+            if (b->held || !(b->stream == s)) continue;
+            if (b->bytes < bytes) {
+                small_idle = true;
+                continue;
+            }
+            if (!pick || b->bytes < pick->bytes) pick = b;
         }
         if (!pick) {
-            retire_idle_locked(bytes);
+            // this stream's idle buffers are all too small: replace them
+            if (small_idle) retire_idle_locked([&](const Buffer& b) { return b.stream == s && b.bytes < bytes; });
             const size_t sz = bytes > min_bytes_ ? bytes : min_bytes_;
             void* p = b_.alloc(sz);
             if (!p) {
-                retire_idle_locked(~size_t(0));   // give every idle buffer back and retry once
+                retire_idle_locked([](const Buffer&) { return true; });   // give every idle buffer back, retry once
                 p = b_.alloc(sz);
                 if (!p) return nullptr;
             }
             std::unique_ptr<Buffer> nb(new Buffer());
             nb->ptr = p;
             nb->bytes = sz;
-            nb->done = b_.make_event();
+            nb->stream = s;
             bufs_.push_back(std::move(nb));
             pick = bufs_.back().get();
-        } else if (pick->recorded && !(pick->stream == s)) {
-            b_.wait(s, pick->done);
         }
         pick->held = true;
         return pick;
     }
 
-    // Ends a lease: the buffer is free for others once the work queued on `s`
-    // so far has run.
-    void release(Buffer* buf, Stream s) {
+    // Ends a lease; the next lease for the same stream may take the buffer.
+    void release(Buffer* buf) {
         if (!buf) return;
         std::lock_guard<std::mutex> lk(mu_);
-        b_.record(buf->done, s);
-        buf->recorded = true;
-        buf->stream = s;
         buf->held = false;
     }
 
-    // Frees every idle buffer after its last use (held buffers stay).
+    // Frees every idle buffer (held buffers stay).
     void trim() {
         std::lock_guard<std::mutex> lk(mu_);
-        retire_idle_locked(~size_t(0));
+        retire_idle_locked([](const Buffer&) { return true; });
     }
 
     size_t buffer_count() {
@@ -124,17 +117,20 @@ public:
     }
 
 private:
-    // Frees idle buffers smaller than `below`, each after its last use.
-    void retire_idle_locked(size_t below) {
+    // Frees the idle buffers `which` selects, after the device has drained.
+    template <class Pred>
+    void retire_idle_locked(Pred which) {
+        bool any = false;
+        for (auto& b : bufs_) any = any || (!b->held && which(*b));
+        if (!any) return;
+        b_.sync_device();
         for (size_t i = 0; i < bufs_.size();) {
             Buffer* b = bufs_[i].get();
-            if (b->held || b->bytes >= below) {
+            if (b->held || !which(*b)) {
                 ++i;
                 continue;
             }
-            if (b->recorded) b_.sync(b->done);
             b_.free(b->ptr);
-            b_.destroy_event(b->done);
             bufs_.erase(bufs_.begin() + (std::ptrdiff_t)i);
         }
     }

@@ -34,10 +34,10 @@ hipStream_t device_stream(int device);
 // A lease of library scratch memory (split-K partials, repacked operands,
 // convolution partials) for the kernels one call queues on one stream of the
 // current device. The lease ends when the object is destroyed, after the
-// call's launches: the buffer then returns to the device's pool behind an
-// event on that stream, so a later call on another stream waits for this
-// call's kernels before it reuses the memory, and no buffer is freed while a
-// lease holds it or its last kernels may still run (scratch_pool.h).
+// call's launches. A buffer is only ever leased again for the same stream, so
+// stream order puts this call's kernels before the next holder's; buffers are
+// freed only after the device has drained, never while a lease holds them
+// (scratch_pool.h).
 class Scratch {
 public:
     Scratch() = default;
