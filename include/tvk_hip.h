@@ -49,8 +49,9 @@ typedef enum {
     TVK_ERR_DEVICE = 4
 } tvk_status;
 
-/* Element types. tvk_gemm and tvk_conv2d_* take F32, F16 and BF16; tvk_copy
- * takes every one of them. BOOL is one byte holding 0 or 1. */
+/* Element types. tvk_gemm takes every one but BOOL; tvk_conv2d_* take F32,
+ * F16 and BF16; tvk_copy takes every one of them. BOOL is one byte holding 0
+ * or 1. */
 typedef enum {
     TVK_F32 = 0,
     TVK_F16 = 1,
@@ -373,12 +374,19 @@ tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc);
  * the reference's has_bias rule (src/api/ops/matmul.cpp:259,394). alpha and
  * beta are rounded to float32, the accumulate type the reference pushes them
  * in (src/vulkan/builders.h:119-140, src/api/ops/matmul.cpp:238-239).
- * Accumulation is float32 for every dtype; the result is rounded once to
+ * F32, F16, BF16: accumulation is float32; the result is rounded once to
  * `dtype` (round to nearest even). float32 always accumulates in the
  * reference SIMD tile's order (fmaf over k in sequence per output,
  * src/shaders/helpers/gemm_simd.slang:219-239); float16/bfloat16 use MFMA
  * tiles whose order within 16 k is the hardware's, unless TVK_GEMM_EXACT. K == 0 gives act(beta*bias) or zeros
  * (src/api/ops/matmul.cpp:284-288).
+ * F64 and the integer types accumulate in their own type, as the reference's
+ * device does (src/shaders/core/dtype.slang:117-219): float64 by fma over k in
+ * sequence per output with alpha/beta in float64; integers in two's-complement
+ * with wraparound in the type's width, alpha and beta converted to integers
+ * (truncated), relu = max(v, 0) and no gelu (TVK_ERR_INVALID). These run one
+ * kernel ("gemm_wide_f64" / "gemm_wide_int"), use no scratch, and take any
+ * strides and sizes. TVK_GEMM_EXACT changes nothing for them.
  *
  * Replaces the dispatch in dispatch_matmul_shader
  * (src/api/ops/matmul.cpp:584-597) of matmul_simd_main

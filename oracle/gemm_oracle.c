@@ -171,3 +171,100 @@ int oracle_gemm_rows(int dtype, int act, int fma_mode, int64_t bi, int64_t m_beg
     return oracle_gemm(dtype, act, fma_mode, 1, m_end - m_begin, N, K, a1, sa1, b1, sb1, bias1, sbias1, c1, sc1,
                        alpha_d, beta_d, scratch_row);
 }
+
+/* ---------------------------------------------------------------------------
+ * float64 and integer products.
+ *
+ * The reference runs these on its device too: the accumulate type of a
+ * matmul is the dtype itself for float64 and for every integer type
+ * (Accum = double / int64_t / int32_t / int16_t / int8_t / uint8_t,
+ * src/shaders/core/dtype.slang:117-219), alpha and beta are pushed in that
+ * type (src/vulkan/builders.h:119-140), and the SIMD tile accumulates each
+ * output over k in sequence (src/shaders/helpers/gemm_simd.slang:219-239).
+ *   - float64: fma over k = 0..K-1 per output, then v = acc*alpha;
+ *     v = v + bias*beta (two roundings), act; gelu in its erf form.
+ *   - integers: two's-complement arithmetic in the type's width, so every
+ *     product and sum wraps modulo 2^bits; alpha and beta are integers
+ *     (torch rejects fractional ones for integer inputs) converted to the
+ *     type; relu is max(v, 0) in the type; there is no gelu for integers.
+ * Integer sums modulo 2^bits do not depend on the order of the terms, so the
+ * k order matters only for float64.
+ * Dtype codes follow tvk_dtype: F64 = 3, I64 = 4, I32 = 5, I16 = 6, I8 = 7,
+ * U8 = 8.
+ * ------------------------------------------------------------------------- */
+enum { OR_F64 = 3, OR_I64 = 4, OR_I32 = 5, OR_I16 = 6, OR_I8 = 7, OR_U8 = 8 };
+
+/* an integer element as its two's-complement bits in 64 bits */
+static inline uint64_t load_int(int dt, const void* p, int64_t i) {
+    switch (dt) {
+    case OR_I64: return (uint64_t)((const int64_t*)p)[i];
+    case OR_I32: return (uint64_t)(int64_t)((const int32_t*)p)[i];
+    case OR_I16: return (uint64_t)(int64_t)((const int16_t*)p)[i];
+    case OR_I8: return (uint64_t)(int64_t)((const int8_t*)p)[i];
+    default: return (uint64_t)((const uint8_t*)p)[i];
+    }
+}
+
+/* the value truncated to the type (modulo 2^bits) */
+static inline void store_int(int dt, void* p, int64_t i, uint64_t v) {
+    switch (dt) {
+    case OR_I64: ((int64_t*)p)[i] = (int64_t)v; break;
+    case OR_I32: ((int32_t*)p)[i] = (int32_t)(uint32_t)v; break;
+    case OR_I16: ((int16_t*)p)[i] = (int16_t)(uint16_t)v; break;
+    case OR_I8: ((int8_t*)p)[i] = (int8_t)(uint8_t)v; break;
+    default: ((uint8_t*)p)[i] = (uint8_t)v; break;
+    }
+}
+
+/* relu in the type: negative values of the signed types become 0 */
+static inline uint64_t relu_int(int dt, uint64_t v) {
+    switch (dt) {
+    case OR_I64: return (int64_t)v < 0 ? 0 : v;
+    case OR_I32: return (int32_t)(uint32_t)v < 0 ? 0 : v;
+    case OR_I16: return (int16_t)(uint16_t)v < 0 ? 0 : v;
+    case OR_I8: return (int8_t)(uint8_t)v < 0 ? 0 : v;
+    default: return v;
+    }
+}
+
+double oracle_gelu64(double v) { return 0.5 * v * (1.0 + erf(v * 0.7071067811865476)); }
+
+/* Rows [m_begin, m_end) of batch `bi` of a float64 or integer product
+ * (strides in elements: [batch, row, col]). Returns 0, or -1 on bad input. */
+int oracle_gemm_wide_rows(int dtype, int act, int64_t bi, int64_t m_begin, int64_t m_end, int64_t N, int64_t K,
+                          const void* a, const int64_t* sa, const void* b, const int64_t* sb,
+                          const void* bias, const int64_t* sbias, void* c, const int64_t* sc,
+                          double alpha_d, double beta_d) {
+    if (dtype < OR_F64 || dtype > OR_U8 || act < 0 || act > 2) return -1;
+    if (dtype != OR_F64 && act == OR_ACT_GELU) return -1;
+    if (m_begin < 0 || m_end < m_begin || N < 0 || K < 0) return -1;
+    const int has_bias = bias != 0 && beta_d != 0.0;
+    for (int64_t m = m_begin; m < m_end; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            const int64_t ai = bi * sa[0] + m * sa[1], bj = bi * sb[0] + n * sb[2];
+            const int64_t ci = bi * sc[0] + m * sc[1] + n * sc[2];
+            const int64_t xi = bi * sbias[0] + m * sbias[1] + n * sbias[2];
+            if (dtype == OR_F64) {
+                double acc = 0.0;
+                for (int64_t k = 0; k < K; ++k)
+                    acc = fma(((const double*)a)[ai + k * sa[2]], ((const double*)b)[bj + k * sb[1]], acc);
+                double v = acc * alpha_d;
+                if (has_bias) {
+                    double t = ((const double*)bias)[xi] * beta_d;
+                    v = v + t;
+                }
+                if (act == OR_ACT_RELU) v = v > 0.0 ? v : (isnan(v) ? v : 0.0);
+                else if (act == OR_ACT_GELU) v = oracle_gelu64(v);
+                ((double*)c)[ci] = v;
+            } else {
+                uint64_t acc = 0;
+                for (int64_t k = 0; k < K; ++k) acc += load_int(dtype, a, ai + k * sa[2]) * load_int(dtype, b, bj + k * sb[1]);
+                uint64_t v = acc * (uint64_t)(int64_t)alpha_d;
+                if (has_bias) v += load_int(dtype, bias, xi) * (uint64_t)(int64_t)beta_d;
+                if (act == OR_ACT_RELU) v = relu_int(dtype, v);
+                store_int(dtype, c, ci, v);
+            }
+        }
+    }
+    return 0;
+}

@@ -56,6 +56,11 @@ def load() -> C.CDLL:
             C.c_double, C.c_double, C.POINTER(C.c_float),
         ]
         lib.oracle_gemm_rows.restype = C.c_int
+        lib.oracle_gemm_wide_rows.argtypes = [
+            C.c_int, C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
+            C.c_void_p, C.POINTER(C.c_int64), C.c_void_p, C.POINTER(C.c_int64), C.c_void_p, C.POINTER(C.c_int64),
+            C.c_void_p, C.POINTER(C.c_int64), C.c_double, C.c_double]
+        lib.oracle_gemm_wide_rows.restype = C.c_int
         lib.oracle_cast.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int64]
         lib.oracle_cast.restype = C.c_int
         lib.oracle_f64_to_f16.argtypes = [C.c_double]
@@ -264,13 +269,18 @@ def _estrides3(x: np.ndarray) -> tuple[int, int, int]:
     raise ValueError("expected 2-D or 3-D")
 
 
+# element storage of the float64 and integer products (oracle_gemm_wide_rows)
+WIDE_STORE = {F64: np.float64, I64: np.int64, I32: np.int32, I16: np.int16, I8: np.int8, U8: np.uint8}
+
+
 def gemm(a: np.ndarray, b: np.ndarray, dtype: int, bias: np.ndarray | None = None, alpha: float = 1.0,
          beta: float = 0.0, act: int = ACT_NONE, fma: bool = True, threads: int | None = None) -> np.ndarray:
     """C = act(alpha*A@B + beta*bias) in the reference SIMD tile's order.
 
     a: [M,K] or [B,M,K]; b: [K,N] or [B,K,N] (any strides, including
     broadcast); bias broadcasts to C. Returns a contiguous array of the same
-    element storage (float32, or uint16 bit patterns for float16/bfloat16).
+    element storage (float32, uint16 bit patterns for float16/bfloat16, the
+    numpy type itself for float64 and the integer types).
     """
     lib = load()
     batched = a.ndim == 3 or b.ndim == 3
@@ -286,7 +296,7 @@ def gemm(a: np.ndarray, b: np.ndarray, dtype: int, bias: np.ndarray | None = Non
     K2, N = b.shape[-2], b.shape[-1]
     if K != K2:
         raise ValueError(f"shapes cannot be multiplied ({M}x{K} and {K2}x{N})")
-    store = np.float32 if dtype == F32 else np.uint16
+    store = WIDE_STORE.get(dtype, np.float32 if dtype == F32 else np.uint16)
     out_shape = (nb, M, N) if batched else (M, N)
     c = np.zeros(out_shape, dtype=store)
     if c.size == 0:
@@ -312,6 +322,12 @@ def gemm(a: np.ndarray, b: np.ndarray, dtype: int, bias: np.ndarray | None = Non
 
     def run(job):
         bi, m0, m1 = job
+        if dtype in WIDE_STORE:
+            rc = lib.oracle_gemm_wide_rows(dtype, act, bi, m0, m1, N, K, a_p, sa, b_p, sb, bias_p, sbias, c.ctypes.data,
+                                           sc, float(alpha), float(beta))
+            if rc != 0:
+                raise ValueError("oracle_gemm_wide_rows rejected its arguments")
+            return
         scratch = (C.c_float * max(1, N))()
         rc = lib.oracle_gemm_rows(dtype, act, 1 if fma else 0, bi, m0, m1, N, K, a_p, sa, b_p, sb, bias_p, sbias,
                                   c.ctypes.data, sc, float(alpha), float(beta), scratch)

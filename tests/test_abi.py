@@ -53,7 +53,7 @@ def _desc(**kw):
 
 
 @pytest.mark.parametrize("field,value,status", [
-    ("dtype", 7, _abi.TVK_ERR_UNSUPPORTED),
+    ("dtype", 9, _abi.TVK_ERR_UNSUPPORTED),   # BOOL: every other dtype has a kernel
     ("activation", 9, _abi.TVK_ERR_INVALID),
     ("M", -1, _abi.TVK_ERR_INVALID),
     ("K", 1 << 40, _abi.TVK_ERR_UNSUPPORTED),

@@ -199,3 +199,100 @@ def test_relu_and_gelu():
     gelu = orc.gemm(a, b, orc.F32, act=orc.ACT_GELU)
     want = torch.nn.functional.gelu(torch.from_numpy(plain).double()).numpy()
     assert np.all(np.abs(gelu - want) <= 1e-6 * (np.abs(want) + 1))
+
+
+# ---------------------------------------------------------------------------
+# float64 and integer products (oracle_gemm_wide_rows)
+# ---------------------------------------------------------------------------
+
+INT_TYPES = [(orc.I64, np.int64), (orc.I32, np.int32), (orc.I16, np.int16), (orc.I8, np.int8), (orc.U8, np.uint8)]
+
+
+@pytest.mark.parametrize("dt,npt", INT_TYPES)
+def test_integer_products_wrap_like_numpy(dt, npt):
+    # numpy's integer matmul accumulates in the type and wraps: the reference's accumulate type
+    rng = np.random.default_rng(10 + dt)
+    info = np.iinfo(npt)
+    a = rng.integers(info.min, info.max, (3, 17, 29), endpoint=True, dtype=npt)
+    b = rng.integers(info.min, info.max, (3, 29, 11), endpoint=True, dtype=npt)
+    got = orc.gemm(a, b, dt)
+    assert got.dtype == npt
+    assert np.array_equal(got, np.matmul(a, b))
+    # transposed views, broadcast B, bias with integer alpha and beta
+    bt = np.ascontiguousarray(b[0].T).T
+    bias = rng.integers(info.min, info.max, (11,), endpoint=True, dtype=npt)
+    got = orc.gemm(a[1], bt, dt, bias=bias, alpha=3.0, beta=-2.0)
+    with np.errstate(over="ignore"):
+        want = (np.matmul(a[1], bt) * npt(3) + bias * (npt(-2) if info.min < 0 else npt(-2 % (info.max + 1)))).astype(npt)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("dt,npt", INT_TYPES)
+def test_integer_products_brute_force_modular(dt, npt):
+    # Python integers reduced modulo 2^bits at the end: a different route to the same bits
+    rng = np.random.default_rng(20 + dt)
+    info = np.iinfo(npt)
+    bits = info.bits
+    a = rng.integers(info.min, info.max, (4, 9), endpoint=True, dtype=npt)
+    b = rng.integers(info.min, info.max, (9, 5), endpoint=True, dtype=npt)
+    bias = rng.integers(info.min, info.max, (4, 5), endpoint=True, dtype=npt)
+    got = orc.gemm(a, b, dt, bias=bias, alpha=5.0, beta=7.0, act=orc.ACT_RELU)
+    for i in range(4):
+        for j in range(5):
+            v = 5 * sum(int(a[i, k]) * int(b[k, j]) for k in range(9)) + 7 * int(bias[i, j])
+            v %= 1 << bits
+            if info.min < 0 and v >= 1 << (bits - 1):
+                v -= 1 << bits
+            if v < 0:
+                v = 0
+            assert int(got[i, j]) == v, (i, j)
+
+
+def test_float64_sequential_fma_order():
+    # exact-rational fma recurrence per output (fma = the exact a*b + acc, rounded once);
+    # the inputs span many magnitudes so that other orders land on other doubles
+    rng = np.random.default_rng(30)
+    M, N, K = 5, 6, 40
+    a = rng.standard_normal((M, K)) * np.exp2(rng.integers(-30, 30, (M, K)))
+    b = rng.standard_normal((K, N)) * np.exp2(rng.integers(-30, 30, (K, N)))
+    bias = rng.standard_normal((N,))
+    got = orc.gemm(a, b, orc.F64, bias=bias, alpha=0.3, beta=-1.7)
+    differs = 0
+    for i in range(M):
+        for j in range(N):
+            acc = 0.0
+            for k in range(K):
+                acc = float(Fraction(a[i, k]) * Fraction(b[k, j]) + Fraction(acc))
+            v = float(Fraction(acc) * Fraction(0.3))
+            t = float(Fraction(bias[j]) * Fraction(-1.7))
+            v = float(Fraction(v) + Fraction(t))
+            assert got[i, j] == v, (i, j)
+            differs += float(np.dot(a[i], b[:, j])) * 0.3 + bias[j] * -1.7 != v
+    assert differs > 0   # the order is visible on these inputs
+
+
+def test_float64_integer_valued_exact_and_activations():
+    rng = np.random.default_rng(31)
+    a = rng.integers(-8, 9, (2, 33, 70)).astype(np.float64)
+    b = rng.integers(-8, 9, (2, 70, 21)).astype(np.float64)
+    assert np.array_equal(orc.gemm(a, b, orc.F64), a @ b)
+    x = rng.standard_normal((9, 13))
+    y = rng.standard_normal((13, 7))
+    r = orc.gemm(x, y, orc.F64)
+    assert np.array_equal(orc.gemm(x, y, orc.F64, act=orc.ACT_RELU), np.maximum(r, 0.0))
+    g = torch.nn.functional.gelu(torch.from_numpy(r)).numpy()
+    np.testing.assert_allclose(orc.gemm(x, y, orc.F64, act=orc.ACT_GELU), g, rtol=1e-15, atol=1e-15)
+
+
+def test_wide_k_zero_and_beta_zero():
+    a = np.zeros((3, 0))
+    b = np.zeros((0, 4))
+    bias = np.arange(4, dtype=np.float64)
+    assert np.array_equal(orc.gemm(a, b, orc.F64, bias=bias, beta=2.0), np.tile(bias * 2.0, (3, 1)))
+    nanb = np.full((4,), np.nan)
+    x = np.ones((3, 5))
+    assert np.array_equal(orc.gemm(x, np.ones((5, 4)), orc.F64, bias=nanb, beta=0.0), np.full((3, 4), 5.0))
+    ai = np.ones((3, 0), dtype=np.int32)
+    bi = np.ones((0, 4), dtype=np.int32)
+    assert np.array_equal(orc.gemm(ai, bi, orc.I32, bias=np.int32([1, 2, 3, 4]), beta=3.0),
+                          np.tile(np.int32([3, 6, 9, 12]), (3, 1)))

@@ -265,6 +265,12 @@ def device_count() -> int:
 # torch-tensor helpers (torch supplies device memory and the stream)
 # ---------------------------------------------------------------------------
 
+def _torch():
+    import torch
+
+    return torch
+
+
 def _dtype_code(dtype) -> int:
     import torch
 
@@ -462,7 +468,8 @@ def make_gemm_desc(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_N
     M, N = c.shape[-2], c.shape[-1]
     K = a.shape[-1]
     d = GemmDesc()
-    d.dtype = _dtype_code(c.dtype)
+    d.dtype = copy_dtype_code(c.dtype) if c.dtype not in (_torch().float32, _torch().float16, _torch().bfloat16) \
+        else _dtype_code(c.dtype)
     d.activation = activation
     d.flags = TVK_GEMM_EXACT if exact else 0
     d.batch, d.M, d.N, d.K = batch, M, N, K

@@ -112,12 +112,60 @@ at::Tensor conv_wgrad_impl(const at::Tensor& x, const at::Tensor& dy, c10::IntAr
     return dw;
 }
 
+// float64 and integer convolutions: no implicit-GEMM kernel takes them (the
+// reference gates those to float dtypes too, conv.cpp:295-311, and runs the
+// rest through im2col + matmul, :32-58,200-216). Here the columns come from the
+// device im2col and the products from tvk_gemm's float64 / integer kernel, so
+// the whole convolution stays on the device.
+bool unfold_dtype(at::ScalarType t) {
+    return t == at::kDouble || t == at::kLong || t == at::kInt || t == at::kShort || t == at::kChar || t == at::kByte;
+}
+
+// y[n, g*co + o, ...] = sum over (c, kh, kw) of the group's weights x columns
+at::Tensor unfold_forward(const at::Tensor& x, const at::Tensor& w, const at::Tensor& b, const std::vector<int64_t>& s,
+                          const std::vector<int64_t>& p, const std::vector<int64_t>& dl, int64_t groups) {
+    const int64_t n = x.size(0), cout = w.size(0), kk = w.size(1) * w.size(2) * w.size(3);
+    const int64_t ho = out_size(x.size(2), w.size(2), s[0], p[0], dl[0]);
+    const int64_t wo = out_size(x.size(3), w.size(3), s[1], p[1], dl[1]);
+    const at::Tensor cols = at::im2col(x, {w.size(2), w.size(3)}, dl, p, s);                    // [n, c*kh*kw, ho*wo]
+    at::Tensor y = at::matmul(w.reshape({groups, cout / groups, kk}), cols.view({n, groups, kk, ho * wo}));
+    y = y.reshape({n, cout, ho, wo});
+    if (b.defined()) y = y + b.view({1, cout, 1, 1});
+    return y;
+}
+
+// the transposed convolution of x (the input gradient of a forward one):
+// columns = w^T x per group, folded back by col2im
+at::Tensor unfold_transposed(const at::Tensor& x, const at::Tensor& w, int64_t h, int64_t wd, const std::vector<int64_t>& s,
+                             const std::vector<int64_t>& p, const std::vector<int64_t>& dl, int64_t groups) {
+    const int64_t n = x.size(0), cin_g = x.size(1) / groups, cout = w.size(1) * groups;
+    const int64_t kk = w.size(2) * w.size(3), l = x.size(2) * x.size(3);
+    const at::Tensor wg = w.reshape({groups, cin_g, (cout / groups) * kk}).transpose(1, 2);      // [g, co*kk, ci]
+    const at::Tensor cols = at::matmul(wg, x.reshape({n, groups, cin_g, l})).reshape({n, cout * kk, l});
+    return at::col2im(cols, {h, wd}, {w.size(2), w.size(3)}, dl, p, s);
+}
+
 at::Tensor convolution(const at::Tensor& input, const at::Tensor& weight, const std::optional<at::Tensor>& bias,
                        c10::SymIntArrayRef stride_, c10::SymIntArrayRef padding_, c10::SymIntArrayRef dilation_,
                        bool transposed, c10::SymIntArrayRef output_padding_, c10::SymInt groups_) {
     const int64_t groups = groups_.guard_int(__FILE__, __LINE__);
     auto s = expand2(ints(stride_)), p = expand2(ints(padding_)), dl = expand2(ints(dilation_)), op = expand2(ints(output_padding_));
     const at::MemoryFormat format = conv_memory_format(input, weight);
+    if (unfold_dtype(weight.scalar_type()) && input.scalar_type() == weight.scalar_type() && input.dim() == 4 &&
+        weight.dim() == 4 && s.size() == 2) {
+        const at::Tensor x = input.contiguous(), w = weight.contiguous();
+        const at::Tensor b = bias.has_value() && bias->defined() ? bias->to(w.scalar_type()) : at::Tensor();
+        at::Tensor y;
+        if (!transposed) {
+            y = unfold_forward(x, w, b, s, p, dl, groups);
+        } else {
+            const int64_t h = (x.size(2) - 1) * s[0] - 2 * p[0] + dl[0] * (w.size(2) - 1) + op[0] + 1;
+            const int64_t wd = (x.size(3) - 1) * s[1] - 2 * p[1] + dl[1] * (w.size(3) - 1) + op[1] + 1;
+            y = unfold_transposed(x, w, h, wd, s, p, dl, groups);
+            if (b.defined()) y = y + b.view({1, -1, 1, 1});
+        }
+        return y.contiguous(format);
+    }
     if (!supported(input, weight) || s.size() != 2) {
         TVKB_FALLBACK("A ", weight.scalar_type(), " ", weight.dim() - 2, "-d convolution can't run on the Vulkan device. Falling back to CPU.");
         std::optional<at::Tensor> bc = bias.has_value() && bias->defined() ? std::optional<at::Tensor>(bias->cpu()) : std::nullopt;
@@ -148,6 +196,24 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward(
     auto s = expand2(ints(stride_)), p = expand2(ints(padding_)), dl = expand2(ints(dilation_)), op = expand2(ints(output_padding_));
     const at::MemoryFormat format = conv_memory_format(input, weight);
     at::Tensor gi, gw, gb;
+    if (weight.scalar_type() == at::kDouble && input.scalar_type() == at::kDouble && grad_output.scalar_type() == at::kDouble &&
+        input.dim() == 4 && weight.dim() == 4 && s.size() == 2 && !transposed) {
+        // float64 (the only unfold dtype with gradients): the input gradient is
+        // the transposed convolution of dy, the weight gradient dy times the
+        // columns summed over the batch
+        const at::Tensor go = grad_output.contiguous(), in = input.contiguous(), w = weight.contiguous();
+        if (mask[0]) gi = unfold_transposed(go, w, in.size(2), in.size(3), s, p, dl, groups).contiguous(format);
+        if (mask[1]) {
+            const int64_t n = in.size(0), cout = w.size(0), kk = w.size(1) * w.size(2) * w.size(3), l = go.size(2) * go.size(3);
+            const at::Tensor cols = at::im2col(in, {w.size(2), w.size(3)}, dl, p, s);
+            gw = at::matmul(go.reshape({n, groups, cout / groups, l}), cols.view({n, groups, kk, l}).transpose(-1, -2))
+                     .sum(0)
+                     .reshape(w.sizes())
+                     .contiguous(format);
+        }
+        if (mask[2]) gb = at::sum(grad_output, {0, 2, 3});
+        return {gi, gw, gb};
+    }
     if (!supported(input, weight) || s.size() != 2 || grad_output.scalar_type() != weight.scalar_type() ||
         input.scalar_type() != weight.scalar_type()) {
         TVKB_FALLBACK("A ", weight.scalar_type(), " ", weight.dim() - 2, "-d convolution backward can't run on the Vulkan device. Falling back to CPU.");

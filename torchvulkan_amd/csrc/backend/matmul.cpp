@@ -17,6 +17,23 @@ namespace {
 
 enum Activation { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
 
+// dtypes tvk_gemm computes: float32/16, bfloat16 on the MFMA kernels, float64
+// and the integer types (accumulating in their own type, as the reference's
+// device does, src/api/ops/helpers.h:59-82) on the wide kernel. bool stays on
+// the CPU, which rejects it too.
+int32_t gemm_dtype_of(c10::ScalarType t, bool& ok) {
+    ok = true;
+    switch (t) {
+    case at::kDouble: return TVK_F64;
+    case at::kLong: return TVK_I64;
+    case at::kInt: return TVK_I32;
+    case at::kShort: return TVK_I16;
+    case at::kChar: return TVK_I8;
+    case at::kByte: return TVK_U8;
+    default: return tvk_dtype_of(t, ok);
+    }
+}
+
 struct Shape {
     at::Tensor self, other;
     bool self_unsqueezed = false, other_unsqueezed = false;
@@ -93,7 +110,7 @@ at::Tensor dispatch_matmul(const at::Tensor& self_, const at::Tensor& other_, co
     Shape s = matmul_shape(self_, other_);
     const c10::ScalarType dtype = at::result_type(s.self, s.other);
     bool ok = false;
-    const int32_t tdt = tvk_dtype_of(dtype, ok);
+    const int32_t tdt = gemm_dtype_of(dtype, ok);
     if (!ok) {
         TVKB_FALLBACK("A ", dtype, " matmul can't run on the Vulkan device. Falling back to CPU.");
         return fallback();

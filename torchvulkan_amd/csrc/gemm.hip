@@ -532,7 +532,7 @@ __global__ __launch_bounds__(256) void repack16_kernel(const uint16_t* src, uint
 // host dispatch
 // ----------------------------------------------------------------------------
 
-enum class Kern { K0, GENERIC, SEQ256, SEQ128, SEQ64, MFMA256, MFMA256W8, MFMA128, SKINNY, DMA256, DMA128 };
+enum class Kern { K0, GENERIC, SEQ256, SEQ128, SEQ64, MFMA256, MFMA256W8, MFMA128, SKINNY, DMA256, DMA128, DMA128R8 };
 
 struct Plan {
     Kern kern;
@@ -674,7 +674,8 @@ bool split_plan(const tvk_gemm_desc& d, int64_t want, Plan& pl, Kern kern = Kern
     const int64_t chunk = ((d.K + want - 1) / want + 63) / 64 * 64;
     const int64_t split = (d.K + chunk - 1) / chunk;
     if (split < 2 || split * d.batch * d.M * d.N * 4 > (int64_t(512) << 20)) return false;
-    pl = with_kern(pl, kern, kern == Kern::DMA128 ? "gemm16_dma_128x128_splitk" : "gemm16_mfma_128x128_splitk");
+    pl = with_kern(pl, kern, kern == Kern::DMA128 ? "gemm16_dma_128x128_splitk"
+                             : kern == Kern::DMA128R8 ? "gemm16_dma_128x128_ring8_splitk" : "gemm16_mfma_128x128_splitk");
     pl.split = (int)split;
     pl.k_chunk = (int)chunk;
     return true;
@@ -774,9 +775,12 @@ std::vector<Plan> candidate_plans(const tvk_gemm_desc& d) {
     const bool dma = lay.vec && dma_applies(repacked_args(d, lay), lay.ak, lay.bk);
     if (dma) {
         add(with_kern(lay, Kern::DMA128, "gemm16_dma_128x128"));
+        add(with_kern(lay, Kern::DMA128R8, "gemm16_dma_128x128_ring8"));
         for (int64_t want : {2, 4, 8, 16}) {
             Plan p = lay;
             if (split_plan(d, want, p, Kern::DMA128)) add(p);
+            p = lay;
+            if (split_plan(d, want, p, Kern::DMA128R8)) add(p);
         }
     }
     if (d.M >= 128 && d.N >= 128) {
@@ -956,13 +960,15 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixe
             break;
         case Kern::DMA256:
         case Kern::DMA128:
+        case Kern::DMA128R8:
             if constexpr (DT != TVK_F32) {
                 if (pl.split > 1) {
                     q.part = reinterpret_cast<float*>(ws + rep_a + rep_b);
                     q.split = pl.split;
                     q.k_chunk = pl.k_chunk;
                 }
-                hipError_t e = launch_dma(DT, q, pl.ak, pl.bk, pl.kern == Kern::DMA256 ? 256 : 128, s);
+                hipError_t e = launch_dma(DT, q, pl.ak, pl.bk, pl.kern == Kern::DMA256 ? 256 : 128, s,
+                                          pl.kern == Kern::DMA128R8 ? 8 : 4);
                 if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_gemm: launch failed: ") + hipGetErrorString(e));
                 if (pl.split > 1) {
                     const int64_t total = (int64_t)nb * d.M * d.N;
@@ -1002,7 +1008,7 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixe
 
 tvk_status validate(const tvk_gemm_desc* d) {
     if (!d) return fail(TVK_ERR_INVALID, "tvk_gemm: desc is NULL");
-    if (d->dtype != TVK_F32 && d->dtype != TVK_F16 && d->dtype != TVK_BF16)
+    if (d->dtype != TVK_F32 && d->dtype != TVK_F16 && d->dtype != TVK_BF16 && !gemm_wide_dtype(d->dtype))
         return fail(TVK_ERR_UNSUPPORTED, "tvk_gemm: unsupported dtype " + std::to_string(d->dtype));
     if ((d->flags & ~TVK_GEMM_EXACT) != 0 || d->reserved != 0)
         return fail(TVK_ERR_INVALID, "tvk_gemm: unknown flags or nonzero reserved field");
@@ -1117,6 +1123,10 @@ extern "C" tvk_status tvk_gemm_plan(const tvk_gemm_desc* desc, char* name, size_
         snprintf(name, name_len, "none");
         return TVK_OK;
     }
+    if (gemm_wide_dtype(desc->dtype)) {
+        snprintf(name, name_len, "%s", gemm_wide_name(desc->dtype));
+        return TVK_OK;
+    }
     // a product tvk_gemm runs in row/column blocks is named by its first block's kernel
     tvk_gemm_desc first = *desc;
     int64_t mc = first.M, nc = first.N;
@@ -1192,6 +1202,7 @@ extern "C" tvk_status tvk_gemm(const tvk_gemm_desc* desc) {
     if (st != TVK_OK) return st;
     const tvk_gemm_desc& d = *desc;
     if (d.batch == 0 || d.M == 0 || d.N == 0) return TVK_OK;
+    if (gemm_wide_dtype(d.dtype)) return gemm_wide_run(d);
     return gemm_blocks(d, [](const tvk_gemm_desc& x) { return choose_plan(x); }, nullptr, 0);
 }
 
@@ -1200,6 +1211,7 @@ extern "C" tvk_status tvk_gemm_noalloc(const tvk_gemm_desc* desc) {
     if (st != TVK_OK) return st;
     const tvk_gemm_desc& d = *desc;
     if (d.batch == 0 || d.M == 0 || d.N == 0) return TVK_OK;
+    if (gemm_wide_dtype(d.dtype)) return gemm_wide_run(d);   // no scratch
     // every block's scratch must fit the array before anything is queued
     int64_t mc = d.M, nc = d.N;
     tvk_gemm_desc first = d;
@@ -1228,6 +1240,7 @@ extern "C" tvk_status tvk_gemm_candidates(const tvk_gemm_desc* desc, char* names
     if (!names || names_len == 0) return fail(TVK_ERR_INVALID, "tvk_gemm_candidates: name buffer is empty");
     std::string all;
     if (desc->batch == 0 || desc->M == 0 || desc->N == 0) all = "none";
+    else if (gemm_wide_dtype(desc->dtype)) all = gemm_wide_name(desc->dtype);
     else
         for (const Plan& p : candidate_plans(*desc)) all += (all.empty() ? "" : "\n") + plan_id(p);
     if (all.size() + 1 > names_len)
@@ -1242,6 +1255,11 @@ extern "C" tvk_status tvk_gemm_choose(const tvk_gemm_desc* desc, const char* ker
     if (!kernel) return fail(TVK_ERR_INVALID, "tvk_gemm_choose: kernel is NULL");
     if (desc->batch == 0 || desc->M == 0 || desc->N == 0 || desc->K == 0)
         return fail(TVK_ERR_INVALID, "tvk_gemm_choose: an empty product has no kernel choice");
+    if (gemm_wide_dtype(desc->dtype)) {
+        // one kernel: nothing to record
+        if (std::string(kernel) == gemm_wide_name(desc->dtype)) return TVK_OK;
+        return fail(TVK_ERR_INVALID, std::string("tvk_gemm_choose: ") + kernel + " does not compute this product");
+    }
     for (const Plan& p : candidate_plans(*desc))
         if (plan_id(p) == kernel) {
             tune_record("gemm", tune_key(*desc), plan_id(p), persist != 0);
@@ -1257,6 +1275,10 @@ extern "C" tvk_status tvk_gemm_tune(const tvk_gemm_desc* desc, char* name, size_
     if (d.batch == 0 || d.M == 0 || d.N == 0) {
         put_name(name, name_len, "none");
         return TVK_OK;
+    }
+    if (gemm_wide_dtype(d.dtype)) {
+        put_name(name, name_len, gemm_wide_name(d.dtype));
+        return gemm_wide_run(d);
     }
     const std::vector<Plan> cands = candidate_plans(d);
     Plan best = cands[0];

@@ -192,7 +192,7 @@ __device__ inline u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, bool row_ok, int64_
 // returns hipSuccess or the launch error.
 bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor);
 // tile: 256 (256x256) or 128 (128x128)
-hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, int tile, hipStream_t s);
+hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, int tile, hipStream_t s, int stages = 4);
 
 // Channels-last convolution on the LDS ring (conv_nhwc.hip); mode 0 forward,
 // 1 grad input, 2 grad weight.
@@ -205,6 +205,12 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who);
 // Few input channels (conv_stem.hip): cin * kh * kw <= 32; same modes.
 bool conv_small_applies(const tvk_conv_desc& d, int mode);
 tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who);
+
+// float64 and integer products (gemm_wide.hip): one kernel, any strides, no
+// scratch; the dtype's own accumulate type, float64 in k order.
+bool gemm_wide_dtype(int dtype);
+const char* gemm_wide_name(int dtype);
+tvk_status gemm_wide_run(const tvk_gemm_desc& d);
 
 // M <= 16 streaming kernel (gemm_skinny.hip). b_kmajor: B's k stride is 1.
 // vec: 16-byte loads are legal for A and B. `part`: skinny_scratch_bytes of

@@ -37,7 +37,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 #define TVK_LDS __attribute__((address_space(3)))
 
-constexpr int D_BK = 32, D_NS = 4;
+constexpr int D_BK = 32;
 
 // Tile configurations: 256x256 runs 8 waves of 128x64; the others 64x64 wave
 // tiles (128x128: 4 waves, 256x128 and 128x256: 8 waves).
@@ -146,8 +146,11 @@ __device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 
 constexpr int dma_threads(int bm, int bn) { return 64 * ((bm == 256 && bn == 256) ? 8 : (bm / 64) * (bn / 64)); }
 
-template <int DT, bool AK, bool BK, int BM, int BN>
+// NS: stages in the ring (4, or 8 for 128x128 tiles whose loads need more
+// lookahead to cover memory latency: short K, one workgroup per CU).
+template <int DT, bool AK, bool BK, int BM, int BN, int NS>
 __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArgs p) {
+    constexpr int D_NS = NS;
     typedef DCfg<BM, BN> G;
     constexpr int D_BM = BM, D_BN = BN, D_NT = G::NT, D_FM = G::FM, D_FN = G::FN, D_WTM = G::WTM, D_WTN = G::WTN;
     constexpr int D_OPB = G::OPA, D_STB = G::STB, D_DPS = G::DS;
@@ -374,24 +377,26 @@ bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor) {
     return true;
 }
 
-template <int DT, int BM, int BN>
+template <int DT, int BM, int BN, int NS>
 void launch_dma_tile(GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s) {
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (p.N + BN - 1) / BN;
     const dim3 grid(p.tiles_m * p.tiles_n, p.batch, p.split > 1 ? p.split : 1), block(DCfg<BM, BN>::NT);
-    if (a_kmajor && b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, true, BM, BN>), grid, block, 0, s, p);
-    else if (a_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, false, BM, BN>), grid, block, 0, s, p);
-    else if (b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, true, BM, BN>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, false, BM, BN>), grid, block, 0, s, p);
+    if (a_kmajor && b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, true, BM, BN, NS>), grid, block, 0, s, p);
+    else if (a_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, false, BM, BN, NS>), grid, block, 0, s, p);
+    else if (b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, true, BM, BN, NS>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, false, BM, BN, NS>), grid, block, 0, s, p);
 }
 
-hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, int tile, hipStream_t s) {
+hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, int tile, hipStream_t s, int stages) {
     if (dtype == TVK_F16) {
-        if (tile == 256) launch_dma_tile<TVK_F16, 256, 256>(p, a_kmajor, b_kmajor, s);
-        else launch_dma_tile<TVK_F16, 128, 128>(p, a_kmajor, b_kmajor, s);
+        if (tile == 256) launch_dma_tile<TVK_F16, 256, 256, 4>(p, a_kmajor, b_kmajor, s);
+        else if (stages == 8) launch_dma_tile<TVK_F16, 128, 128, 8>(p, a_kmajor, b_kmajor, s);
+        else launch_dma_tile<TVK_F16, 128, 128, 4>(p, a_kmajor, b_kmajor, s);
     } else {
-        if (tile == 256) launch_dma_tile<TVK_BF16, 256, 256>(p, a_kmajor, b_kmajor, s);
-        else launch_dma_tile<TVK_BF16, 128, 128>(p, a_kmajor, b_kmajor, s);
+        if (tile == 256) launch_dma_tile<TVK_BF16, 256, 256, 4>(p, a_kmajor, b_kmajor, s);
+        else if (stages == 8) launch_dma_tile<TVK_BF16, 128, 128, 8>(p, a_kmajor, b_kmajor, s);
+        else launch_dma_tile<TVK_BF16, 128, 128, 4>(p, a_kmajor, b_kmajor, s);
     }
     return hipGetLastError();
 }
