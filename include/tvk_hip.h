@@ -49,9 +49,11 @@ typedef enum {
     TVK_ERR_DEVICE = 4
 } tvk_status;
 
-/* Element types. tvk_gemm takes every one but BOOL; tvk_conv2d_* take F32,
- * F16 and BF16; tvk_copy takes every one of them. BOOL is one byte holding 0
- * or 1. */
+/* Element types. tvk_gemm takes F32 through U8; tvk_conv2d_* take F32, F16
+ * and BF16; tvk_copy takes every one of them. BOOL is one byte holding 0 or
+ * 1. F8E4M3FN and F8E5M2 are torch's float8_e4m3fn and float8_e5m2 (OCP 8-bit
+ * floats: e4m3 with no infinities and NaN = S.1111.111, e5m2 IEEE-like);
+ * only tvk_copy takes them. */
 typedef enum {
     TVK_F32 = 0,
     TVK_F16 = 1,
@@ -62,7 +64,9 @@ typedef enum {
     TVK_I16 = 6,
     TVK_I8 = 7,
     TVK_U8 = 8,
-    TVK_BOOL = 9
+    TVK_BOOL = 9,
+    TVK_F8E4M3FN = 10,
+    TVK_F8E5M2 = 11
 } tvk_dtype;
 
 /* Epilogue activation, the reference's MatmulActivation
@@ -191,6 +195,15 @@ tvk_status tvk_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream
  *   - to BF16: BFloat16(float(v)), so F64 rounds to float first.
  * With BOOL on either side the value is (src != 0) ? 1 : 0 (IS_BOOL_CAST,
  * src/shaders/ops/cast.slang:29-33).
+ * The float8 types have no shader type in the reference, which converts them
+ * through float32 with c10's own conversions (copy_float8_vulkan_to_vulkan,
+ * src/api/tensor/transfer.cpp:129-226), so they match the CPU bit for bit:
+ *   - from F8: the exact value as a float (then the float rules above);
+ *   - to F8: the value converted to float first (the rules above), then
+ *     rounded to nearest even onto the 8-bit grid, subnormals included.
+ *     F8E4M3FN: NaN, infinities and magnitudes that round past 448 become
+ *     NaN (S.1111.111, sign kept). F8E5M2: NaN becomes S.11111.11, infinities
+ *     and magnitudes that round past 57344 become infinity.
  *
  * Replaces dispatch_copy_shader (src/api/tensor/transfer.cpp:16-56) and
  * dispatch_cast_shader (src/api/tensor/cast.cpp:8-56). Dimensions are merged
@@ -262,13 +275,16 @@ tvk_status tvk_reduce_sum(const tvk_reduce_desc* desc);
 typedef enum {
     TVK_BIN_ADD = 0,        /* out = a + alpha*b */
     TVK_BIN_SUB = 1,        /* out = a - alpha*b */
-    TVK_BIN_MUL = 2         /* out = a * b (alpha unused) */
+    TVK_BIN_MUL = 2,        /* out = a * b (alpha unused) */
+    TVK_BIN_DIV = 3         /* out = a / b (alpha unused; F32, F16, BF16, F64) */
 } tvk_binary_op;
 
 /* Element-wise out = op(a, b) over `sizes`, every operand strided (zero
  * strides broadcast a and b). One dtype for all three: F32, F16, BF16, F64,
- * I64, I32, I16, I8, U8. As the reference's binary shader
- * (src/shaders/ops/binary.slang:39-55): alpha is converted to the dtype;
+ * I64, I32, I16, I8, U8 (DIV: the float types only, IEEE division rounded to
+ * nearest even, the reference's DivOp, binary.slang:57-60). As the
+ * reference's binary shader (src/shaders/ops/binary.slang:39-55): alpha is
+ * converted to the dtype;
  * with alpha != 1, add/sub compute T(a op T(alpha*b)), otherwise T(a op b);
  * every operation rounds to the dtype (float16/bfloat16 compute in float32
  * and round after each operation, dtype.slang:911-913), float32 products are

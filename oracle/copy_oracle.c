@@ -21,12 +21,26 @@
  * The float64 -> float16 rounding here works on the bits of the double
  * directly (not through float32), so it checks the device's round-to-odd
  * route independently.
+ *
+ * float8 (torch's float8_e4m3fn and float8_e5m2): the reference has no shader
+ * type for them and converts through float32 with c10's own conversions
+ * (float8_tables / copy_float8_vulkan_to_vulkan,
+ * src/api/tensor/transfer.cpp:129-226), so the semantics are the CPU's: the
+ * code's exact value as a float, and from a float (other types convert to
+ * float first) the nearest code, ties to the even code, with e4m3fn's NaN
+ * for NaN, infinities and |x| >= 480 (or a rounding onto the 0x7F slot past
+ * 448), and e5m2's infinity for |x| >= 65536 (or a rounding onto the 0x7C
+ * slot past 57344), NaN -> 0x7F. This restatement decodes from the fields
+ * with ldexp and encodes by searching every code's value for the nearest one
+ * (a different method from the device's bit arithmetic); the tests pin both
+ * against torch's own CPU conversion.
  */
 #include <math.h>
 #include <stdint.h>
 #include <string.h>
 
-enum { C_F32 = 0, C_F16 = 1, C_BF16 = 2, C_F64 = 3, C_I64 = 4, C_I32 = 5, C_I16 = 6, C_I8 = 7, C_U8 = 8, C_BOOL = 9 };
+enum { C_F32 = 0, C_F16 = 1, C_BF16 = 2, C_F64 = 3, C_I64 = 4, C_I32 = 5, C_I16 = 6, C_I8 = 7, C_U8 = 8, C_BOOL = 9,
+       C_F8E4M3FN = 10, C_F8E5M2 = 11 };
 enum { W_I = 0, W_U = 1, W_F = 2, W_D = 3 };
 
 /* shared with gemm_oracle.c */
@@ -52,6 +66,58 @@ static int elem_size(int dt) {
     }
 }
 
+/* The value of a float8 code (NaN payloads as the CPU's conversion leaves
+ * them: e4m3fn 0x7FF00000; e5m2 goes through float16, payload m << 21 with
+ * the quiet bit set). */
+float oracle_f8_decode(int dt, uint8_t c) {
+    int neg = (c & 0x80) != 0;
+    int e4 = dt == C_F8E4M3FN;
+    int eb = e4 ? 4 : 5, mb = e4 ? 3 : 2, bias = e4 ? 7 : 15;
+    int e = (c & 0x7f) >> mb, m = c & ((1 << mb) - 1);
+    double v;
+    if (e4 && e == 15 && m == 7) {
+        uint32_t bits = 0x7FF00000u | (neg ? 0x80000000u : 0u);
+        float f;
+        memcpy(&f, &bits, 4);
+        return f;
+    }
+    if (!e4 && e == 31) {
+        /* the float16 route quiets a signaling NaN: the quiet bit is set */
+        uint32_t bits = (m ? 0x7FC00000u : 0x7F800000u) | ((uint32_t)m << 21) | (neg ? 0x80000000u : 0u);
+        float f;
+        memcpy(&f, &bits, 4);
+        return f;
+    }
+    (void)eb;
+    if (e == 0) v = ldexp((double)m, 1 - bias - mb);
+    else v = ldexp((double)((1 << mb) + m), e - bias - mb);
+    return (float)(neg ? -v : v);
+}
+
+/* The float8 code of a float: the nearest of the codes 0..top (top being the
+ * slot past the largest finite value: e4m3fn's NaN code 0x7F, valued 480 for
+ * the search, e5m2's infinity 0x7C, valued 65536), ties to the even code. */
+uint8_t oracle_f8_encode(int dt, float f) {
+    int e4 = dt == C_F8E4M3FN;
+    uint8_t sign = signbit(f) ? 0x80 : 0x00;
+    if (f != f) return sign | 0x7f;
+    double a = fabs((double)f);
+    if (e4 && a >= 480.0) return sign | 0x7f;
+    if (!e4 && a >= 65536.0) return sign | 0x7c;
+    int top = e4 ? 0x7f : 0x7c;
+    int best = 0;
+    double best_d = a;
+    for (int k = 1; k <= top; ++k) {
+        double v = k == top ? (e4 ? 480.0 : 65536.0) : (double)oracle_f8_decode(dt, (uint8_t)k);
+        double dd = fabs(a - v);
+        if (dd < best_d || (dd == best_d && (k & 1) == 0)) {
+            best = k;
+            best_d = dd;
+        }
+    }
+    return sign | (uint8_t)best;
+}
+
 static wide_t widen(int dt, const unsigned char* p) {
     wide_t w;
     memset(&w, 0, sizeof(w));
@@ -64,6 +130,7 @@ static wide_t widen(int dt, const unsigned char* p) {
     case C_I32: { int32_t v; memcpy(&v, p, 4); w.fam = W_I; w.i = v; break; }
     case C_I16: { int16_t v; memcpy(&v, p, 2); w.fam = W_I; w.i = v; break; }
     case C_I8: { int8_t v; memcpy(&v, p, 1); w.fam = W_I; w.i = v; break; }
+    case C_F8E4M3FN: case C_F8E5M2: w.fam = W_F; w.f = oracle_f8_decode(dt, p[0]); break;
     default: w.fam = W_U; w.u = p[0]; break; /* U8, BOOL */
     }
     return w;
@@ -172,13 +239,14 @@ static void narrow(int dt, const wide_t* w, unsigned char* p) {
         p[0] = t;
         break;
     }
+    case C_F8E4M3FN: case C_F8E5M2: p[0] = oracle_f8_encode(dt, as_float(w)); break;
     default: p[0] = (unsigned char)is_nonzero(w); break; /* BOOL */
     }
 }
 
 /* dst[i] = castValue(src[i]) for i < n, both arrays dense. */
 int oracle_cast(int sdt, const void* src, int ddt, void* dst, int64_t n) {
-    if (sdt < C_F32 || sdt > C_BOOL || ddt < C_F32 || ddt > C_BOOL) return 1;
+    if (sdt < C_F32 || sdt > C_F8E5M2 || ddt < C_F32 || ddt > C_F8E5M2) return 1;
     const unsigned char* s = (const unsigned char*)src;
     unsigned char* d = (unsigned char*)dst;
     int ss = elem_size(sdt), ds = elem_size(ddt);

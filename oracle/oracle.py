@@ -21,7 +21,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "build" / "liboracle.so"
 
-F32, F16, BF16, F64, I64, I32, I16, I8, U8, BOOL = range(10)
+F32, F16, BF16, F64, I64, I32, I16, I8, U8, BOOL, F8E4M3FN, F8E5M2 = range(12)
 ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
 
 _lib = None
@@ -106,7 +106,7 @@ def to_f32(bits_or_f32: np.ndarray, dtype: int) -> np.ndarray:
 
 # numpy storage of each code; float16/bfloat16 travel as raw uint16 patterns
 STORAGE = {F32: np.float32, F16: np.uint16, BF16: np.uint16, F64: np.float64, I64: np.int64, I32: np.int32,
-           I16: np.int16, I8: np.int8, U8: np.uint8, BOOL: np.uint8}
+           I16: np.int16, I8: np.int8, U8: np.uint8, BOOL: np.uint8, F8E4M3FN: np.uint8, F8E5M2: np.uint8}
 
 
 def cast(src: np.ndarray, sdt: int, ddt: int) -> np.ndarray:
@@ -122,7 +122,7 @@ def cast(src: np.ndarray, sdt: int, ddt: int) -> np.ndarray:
 # element-wise add / sub / mul of tvk_binary
 # ---------------------------------------------------------------------------
 
-BIN_ADD, BIN_SUB, BIN_MUL = 0, 1, 2
+BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = 0, 1, 2, 3
 _NP_INT = {I64: np.int64, I32: np.int32, I16: np.int16, I8: np.int8, U8: np.uint8}
 
 
@@ -136,14 +136,16 @@ def _round_to(x32: np.ndarray, dt: int) -> np.ndarray:
 
 
 def binary(a: np.ndarray, b: np.ndarray, dt: int, op: int, alpha: float = 1.0) -> np.ndarray:
-    """AddOp / SubOp / MulOp of the reference's binary shader in dtype dt
-    (src/shaders/ops/binary.slang:39-55): alpha converted to dt; with
+    """AddOp / SubOp / MulOp / DivOp of the reference's binary shader in dtype dt
+    (src/shaders/ops/binary.slang:39-60): alpha converted to dt; with
     alpha != 1, T(a op T(alpha*b)); float16/bfloat16 compute each operation
     in float32 and round back (src/shaders/core/dtype.slang:911-913); float32
     and float64 round every operation (no fused multiply-add); integers wrap.
     a, b: storage arrays (uint16 patterns for float16/bfloat16), broadcast."""
     a, b = np.broadcast_arrays(np.asarray(a, dtype=STORAGE[dt]), np.asarray(b, dtype=STORAGE[dt]))
-    has_alpha = op != BIN_MUL and alpha != 1.0
+    has_alpha = op in (BIN_ADD, BIN_SUB) and alpha != 1.0
+    if op == BIN_DIV and dt in _NP_INT:
+        raise ValueError("division is defined for the float dtypes only")
     if dt in _NP_INT:
         t = _NP_INT[dt]
         with np.errstate(over="ignore"):
@@ -159,12 +161,18 @@ def binary(a: np.ndarray, b: np.ndarray, dt: int, op: int, alpha: float = 1.0) -
         a64, b64, al = a.astype(np.float64), b.astype(np.float64), np.float64(alpha)
         if op == BIN_MUL:
             return a64 * b64
+        if op == BIN_DIV:
+            with np.errstate(divide="ignore", invalid="ignore"):
+                return a64 / b64
         t = al * b64 if has_alpha else b64
         return a64 + t if op == BIN_ADD else a64 - t
     fa, fb = to_f32(a, dt), to_f32(b, dt)
     al = _round_to(np.array([alpha], dtype=np.float32), dt)[0]
     if op == BIN_MUL:
         r = _round_to(fa * fb, dt)
+    elif op == BIN_DIV:
+        with np.errstate(divide="ignore", invalid="ignore"):
+            r = _round_to(fa / fb, dt)
     else:
         t = _round_to(al * fb, dt) if has_alpha else fb
         r = _round_to(fa + t if op == BIN_ADD else fa - t, dt)
@@ -340,6 +348,63 @@ def gemm(a: np.ndarray, b: np.ndarray, dtype: int, bias: np.ndarray | None = Non
         with cf.ThreadPoolExecutor(max_workers=threads) as ex:
             list(ex.map(run, jobs))
     return c
+
+
+def complex_gemm(a: np.ndarray, b: np.ndarray, bias: np.ndarray | None = None, alpha: complex = 1.0,
+                 beta: complex = 0.0) -> np.ndarray:
+    """complex_matmul (src/api/ops/matmul.cpp:355-371) of complex64 or
+    complex128 operands ([M,K]/[B,M,K] and [K,N]/[B,K,N], bias broadcasting
+    to the result): the real and imaginary parts multiplied by the real
+    product (gemm above, in the real type), re = T(re.re) - T(im.im) and
+    im = T(re.im) + T(im.re) each rounded in the real type; then, when
+    alpha != 1, r = r * alpha and, when a bias is given with beta != 0,
+    r = r + bias * beta, as complex_mul (src/api/ops/complex.cpp:43-46):
+    (x.re*s.re - x.im*s.im, x.re*s.im + x.im*s.re), every operation rounded
+    in the real type. complex32 operands compute as complex64 (the caller
+    widens them and rounds the result)."""
+    real = np.float64 if a.dtype == np.complex128 else np.float32
+    dt = F64 if real == np.float64 else F32
+
+    def parts(z):
+        z = np.asarray(z)
+        return np.ascontiguousarray(z.real, dtype=real), np.ascontiguousarray(z.imag, dtype=real)
+
+    def cmul(xr, xi, s):
+        sr, si = real(complex(s).real), real(complex(s).imag)
+        return (xr * sr - xi * si).astype(real), (xr * si + xi * sr).astype(real)
+
+    ar, ai = parts(a)
+    br, bi = parts(b)
+    re = (gemm(ar, br, dt) - gemm(ai, bi, dt)).astype(real)
+    im = (gemm(ar, bi, dt) + gemm(ai, br, dt)).astype(real)
+    if complex(alpha) != 1:
+        re, im = cmul(re, im, alpha)
+    if bias is not None and complex(beta) != 0:
+        cr, ci = parts(np.broadcast_to(bias, re.shape))
+        cr, ci = cmul(cr, ci, beta)
+        re, im = (re + cr).astype(real), (im + ci).astype(real)
+    out = np.empty(re.shape, dtype=np.complex128 if real == np.float64 else np.complex64)
+    out.real, out.imag = re, im
+    return out
+
+
+def scaled_mm(a_codes: np.ndarray, a_dt: int, b_codes: np.ndarray, b_dt: int, scale_a, scale_b, out_dt: int,
+              bias: np.ndarray | None = None, bias_dt: int = F32, scale_result: float | None = None) -> np.ndarray:
+    """torch's emulated _scaled_mm as the reference computes it
+    (scaled_mm_out_vulkan, src/api/ops/matmul.cpp:706-747): float8 codes
+    decoded to float32 and multiplied by their scale (one each, or a [M,1]
+    column for A and a [1,N] row for B) in float32; the float32 product
+    (gemm above); the bias (storage of bias_dt, [N]) added in float32; times
+    the float32 1 / scale_result when out_dt is a float8 type; rounded to
+    out_dt (cast above). Returns out_dt storage."""
+    fa = cast(a_codes, a_dt, F32) * np.asarray(scale_a, dtype=np.float32)
+    fb = cast(b_codes, b_dt, F32) * np.asarray(scale_b, dtype=np.float32)
+    p = gemm(fa.astype(np.float32), fb.astype(np.float32), F32)
+    if bias is not None:
+        p = (p + cast(np.asarray(bias), bias_dt, F32)).astype(np.float32)
+    if scale_result is not None and out_dt in (F8E4M3FN, F8E5M2):
+        p = (p * (np.float32(1.0) / np.float32(scale_result))).astype(np.float32)
+    return cast(p, F32, out_dt)
 
 
 # ---------------------------------------------------------------------------

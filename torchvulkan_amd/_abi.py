@@ -14,7 +14,7 @@ _LIB_PATH = Path(__file__).resolve().parent / "libtvk_hip.so"
 
 TVK_OK, TVK_ERR_UNSUPPORTED, TVK_ERR_OOM, TVK_ERR_INVALID, TVK_ERR_DEVICE = range(5)
 (TVK_F32, TVK_F16, TVK_BF16, TVK_F64, TVK_I64, TVK_I32, TVK_I16, TVK_I8, TVK_U8,
- TVK_BOOL) = range(10)
+ TVK_BOOL, TVK_F8E4M3FN, TVK_F8E5M2) = range(12)
 TVK_COPY_MAX_DIMS = 16
 TVK_ACT_NONE, TVK_ACT_RELU, TVK_ACT_GELU = range(3)
 TVK_GEMM_EXACT = 1
@@ -116,7 +116,7 @@ class ReduceDesc(C.Structure):
     ]
 
 
-TVK_BIN_ADD, TVK_BIN_SUB, TVK_BIN_MUL = range(3)
+TVK_BIN_ADD, TVK_BIN_SUB, TVK_BIN_MUL, TVK_BIN_DIV = range(4)
 
 
 class BinaryDesc(C.Structure):
@@ -286,7 +286,8 @@ def copy_dtype_code(dtype) -> int:
 
     codes = {torch.float32: TVK_F32, torch.float16: TVK_F16, torch.bfloat16: TVK_BF16, torch.float64: TVK_F64,
              torch.int64: TVK_I64, torch.int32: TVK_I32, torch.int16: TVK_I16, torch.int8: TVK_I8,
-             torch.uint8: TVK_U8, torch.bool: TVK_BOOL}
+             torch.uint8: TVK_U8, torch.bool: TVK_BOOL, torch.float8_e4m3fn: TVK_F8E4M3FN,
+             torch.float8_e5m2: TVK_F8E5M2}
     if dtype not in codes:
         raise TvkUnsupported(TVK_ERR_UNSUPPORTED, f"dtype {dtype} has no device copy")
     return codes[dtype]

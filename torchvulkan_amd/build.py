@@ -28,7 +28,9 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # Packed FP32 instructions are disabled for every device pass; the host pass
-# warns that it does not know the feature, which is harmless.
+# warns that it does not know the feature, which is harmless. float32 division
+# and square root are the correctly rounded ones (hipcc's default, stated so
+# that no later flag can change it silently).
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -36,6 +38,7 @@ HIP_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}",
 ]

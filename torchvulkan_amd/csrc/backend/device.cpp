@@ -18,6 +18,8 @@
 #include <ATen/ops/_reshape_alias_native.h>
 #include <ATen/ops/as_strided_native.h>
 #include <ATen/ops/set_native.h>
+#include <ATen/ops/view_as_complex_native.h>
+#include <ATen/ops/view_as_real_native.h>
 #include <ATen/ops/view_native.h>
 #include <c10/core/Allocator.h>
 #include <c10/core/impl/DeviceGuardImplInterface.h>
@@ -82,6 +84,8 @@ int32_t copy_dtype_of(c10::ScalarType t, bool& ok) {
     case at::kChar: return TVK_I8;
     case at::kByte: return TVK_U8;
     case at::kBool: return TVK_BOOL;
+    case at::kFloat8_e4m3fn: return TVK_F8E4M3FN;
+    case at::kFloat8_e5m2: return TVK_F8E5M2;
     default: ok = false; return -1;
     }
 }
@@ -397,6 +401,58 @@ at::Tensor empty_strided(c10::IntArrayRef size, c10::IntArrayRef stride, std::op
     return at::detail::empty_strided_generic(size, stride, &g_allocator, ks, c10::dtype_or_default(dtype));
 }
 
+// Copies with a complex side, on one device, as copies of the (real,
+// imaginary) pairs (copy_complex_vulkan_to_vulkan,
+// src/api/tensor/transfer.cpp:228-244): complex to complex casts the pairs;
+// real to complex writes the real parts and zeroes the imaginary ones;
+// complex to real keeps the real parts (the caller warned). False when not
+// applicable (the caller resolves conjugate and negative views first).
+bool complex_copy(const at::Tensor& src, const at::Tensor& dst) {
+    if (!src.is_complex() && !dst.is_complex()) return false;
+    if (src.device() != dst.device() || src.is_conj() || src.is_neg() || dst.is_conj() || dst.is_neg()) return false;
+    if (dst.dim() + 1 > TVK_COPY_MAX_DIMS) return false;
+    bool ok_s = false, ok_d = false;
+    copy_dtype_of(c10::toRealValueType(src.scalar_type()), ok_s);
+    copy_dtype_of(c10::toRealValueType(dst.scalar_type()), ok_d);
+    if (!ok_s || !ok_d) return false;
+    if (src.is_complex() && dst.is_complex()) {
+        at::Tensor d = at::view_as_real(dst);
+        d.copy_(at::view_as_real(src));
+    } else if (dst.is_complex()) {
+        at::Tensor pairs = at::view_as_real(dst);
+        pairs.select(-1, 0).copy_(src);
+        pairs.select(-1, 1).zero_();
+    } else {
+        at::Tensor d = dst;
+        d.copy_(at::view_as_real(src).select(-1, 0));
+    }
+    return true;
+}
+
+// A copy with a pending conjugation or negation on either side
+// (copy_vulkan's lazily conjugated / negated cases, transfer.cpp:306-331).
+// A tensor's values are (neg ? -1 : 1) * (conj ? conj(stored) : stored), so
+// dst's stored values become the source's stored values, negated where
+// exactly one side is negative and with the imaginary parts negated where
+// exactly one side is conjugate: a plain copy of the stored values, then
+// those sign flips on dst's side (on the device for a vulkan dst).
+at::Tensor copy_math_bits(const at::Tensor& self, const at::Tensor& dst) {
+    at::Tensor s = self, d = dst;
+    if (s.is_conj()) s = at::_conj(s);        // the same storage without the pending conjugation
+    if (s.is_neg()) s = at::_neg_view(s);
+    if (d.is_conj()) d = at::_conj(d);
+    if (d.is_neg()) d = at::_neg_view(d);
+    d.copy_(s);
+    const bool flip_all = self.is_neg() != dst.is_neg();
+    const bool flip_im = self.is_conj() != dst.is_conj() && d.is_complex();
+    if (flip_all || flip_im) {
+        at::Tensor pairs = d.is_complex() ? at::view_as_real(d) : d;
+        if (flip_all) pairs.mul_(-1);
+        if (flip_im) pairs.select(-1, 1).mul_(-1);
+    }
+    return dst;
+}
+
 // _copy_from: torch routes copy_ here whenever one side is a vulkan tensor
 // (torchvulkan::copy_vulkan, src/api/tensor/transfer.cpp:292-397). Device to
 // device copies, casts and layout changes run on the device (tvk_copy);
@@ -408,6 +464,7 @@ at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool non_blo
         self.strides().equals(dst.strides()) && self.scalar_type() == dst.scalar_type() &&
         self.is_conj() == dst.is_conj() && self.is_neg() == dst.is_neg())
         return dst;
+    if (self.is_conj() || self.is_neg() || dst.is_conj() || dst.is_neg()) return copy_math_bits(self, dst);
     at::Tensor src = self;
     if (src.sizes() != dst.sizes()) {
         if (at::is_expandable_to(src.sizes(), dst.sizes())) src = src.expand(dst.sizes());
@@ -434,6 +491,7 @@ at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool non_blo
             }
             return dst;
         }
+        if (complex_copy(src, dst)) return dst;
         TVKB_FALLBACK("A copy from ", src.scalar_type(), " to ", dst.scalar_type(), " can't run on the device. Falling back to CPU.");
         from_host(to_host(src), dst);
         return dst;
@@ -518,6 +576,19 @@ const at::Tensor& resize_(const at::Tensor& self, c10::IntArrayRef size, std::op
 }  // namespace
 }  // namespace tvkb
 
+// _copy_from sees conjugate and negative views itself (copy_math_bits): the
+// generic math-bit fallback would resolve them by a clone, which is a copy_
+// and so another _copy_from of the same view, without end.
+TORCH_LIBRARY_IMPL(aten, Conjugate, m) {
+    m.impl("_copy_from", torch::CppFunction::makeFallthrough());
+    m.impl("_copy_from_and_resize", torch::CppFunction::makeFallthrough());
+}
+
+TORCH_LIBRARY_IMPL(aten, Negative, m) {
+    m.impl("_copy_from", torch::CppFunction::makeFallthrough());
+    m.impl("_copy_from_and_resize", torch::CppFunction::makeFallthrough());
+}
+
 TORCH_LIBRARY_IMPL(_, PrivateUse1, m) {
     m.fallback(torch::CppFunction::makeFromBoxedFunction<&tvkb::cpu_fallback>());
 }
@@ -526,6 +597,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
     m.impl("empty.memory_format", &tvkb::empty_memory_format);
     m.impl("empty_strided", &tvkb::empty_strided);
     m.impl("as_strided", &at::native::as_strided_tensorimpl);
+    m.impl("view_as_real", &at::native::view_as_real);
+    m.impl("view_as_complex", &at::native::view_as_complex);
     m.impl("view", &at::native::view);
     m.impl("_reshape_alias", &at::native::_reshape_alias);
     m.impl("resize_", &tvkb::resize_);

@@ -35,7 +35,8 @@ bool sum_on_device(const at::Tensor& self, at::ScalarType out) {
     bool ok = false;
     copy_dtype_of(self.scalar_type(), ok);
     const bool out_ok = out == at::kFloat || out == at::kHalf || out == at::kBFloat16 || out == at::kDouble || out == at::kLong;
-    return ok && out_ok && self.dim() <= TVK_COPY_MAX_DIMS && !self.is_conj() && !self.is_neg();
+    return ok && out_ok && !at::isFloat8Type(self.scalar_type()) && self.dim() <= TVK_COPY_MAX_DIMS && !self.is_conj() &&
+           !self.is_neg();
 }
 
 at::Tensor sum_dim(const at::Tensor& self, at::OptionalIntArrayRef dim, bool keepdim, std::optional<at::ScalarType> dtype) {

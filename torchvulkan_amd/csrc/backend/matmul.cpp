@@ -1,5 +1,6 @@
-// aten::mm / bmm / addmm / baddbmm / _addmm_activation (+ .out) for the
-// vulkan (PrivateUse1) device, computed by tvk_gemm.
+// aten::mm / bmm / addmm / baddbmm / _addmm_activation (+ .out), addbmm,
+// addmv, mm.dtype and _scaled_mm for the vulkan (PrivateUse1) device,
+// computed by tvk_gemm (complex operands as products of their real parts).
 //
 // Follows src/api/ops/matmul.cpp: operand preparation and broadcasting
 // (prepare_matmul_operands :27-78, get_matmul_shape :108-140,
@@ -104,11 +105,165 @@ at::Tensor batched_view(const at::Tensor& t, const std::vector<int64_t>& batch_s
     return e.reshape({B, rows, cols});  // materialises a contiguous copy
 }
 
+// One tvk_gemm: out[B, M, N] = act(alpha * a[B, M, K] . b[B, K, N] + beta * bias)
+// on 3-D views (bias undefined: none). False when the library declines the
+// shape (the caller falls back); other failures throw.
+bool run_gemm(const at::Tensor& a, const at::Tensor& b, const at::Tensor& bias, double alpha, double beta, Activation act,
+              int32_t tdt, const at::Tensor& out) {
+    tvk_gemm_desc d;
+    std::memset(&d, 0, sizeof(d));
+    d.dtype = tdt;
+    d.activation = act;
+    d.flags = 0;
+    if (const char* e = std::getenv("TORCHVULKAN_EXACT")) {
+        if (e[0] && std::strcmp(e, "0") != 0) d.flags = TVK_GEMM_EXACT;
+    }
+    d.batch = out.size(0); d.M = out.size(1); d.N = out.size(2); d.K = a.size(2);
+    d.a = a.data_ptr();
+    d.b = b.data_ptr();
+    d.c = out.data_ptr();
+    for (int i = 0; i < 3; ++i) {
+        d.a_stride[i] = a.stride(i);
+        d.b_stride[i] = b.stride(i);
+        d.c_stride[i] = out.stride(i);
+    }
+    if (bias.defined()) {
+        d.bias = bias.data_ptr();
+        for (int i = 0; i < 3; ++i) d.bias_stride[i] = bias.stride(i);
+    }
+    d.alpha = alpha;
+    d.beta = bias.defined() ? beta : 0.0;
+    d.stream = stream_of(out);
+    // TORCHVULKAN_AUTOTUNE=1: a shape class without a recorded kernel is timed
+    // over every candidate first and the fastest recorded (the reference tunes
+    // every matmul on first sight, src/api/ops/matmul.cpp:538-544); otherwise
+    // the recorded or shape-chosen kernel runs
+    static const bool autotune = [] {
+        const char* e = std::getenv("TORCHVULKAN_AUTOTUNE");
+        return e != nullptr && e[0] && std::strcmp(e, "0") != 0;
+    }();
+    const tvk_status st = autotune ? tvk_gemm_tune(&d, nullptr, 0) : tvk_gemm(&d);
+    if (st == TVK_ERR_UNSUPPORTED) {
+        TVKB_FALLBACK(tvk_last_error(), ". Falling back to CPU.");
+        return false;
+    }
+    check_status(st, "tvk_gemm");
+    return true;
+}
+
+bool negative_strides(std::initializer_list<const at::Tensor*> ts) {
+    for (const at::Tensor* t : ts) {
+        if (!t->defined()) continue;
+        for (int64_t d = 0; d < t->dim(); ++d)
+            if (t->stride(d) < 0) return true;
+    }
+    return false;
+}
+
+// ---- complex operands ------------------------------------------------------
+// complex_matmul (src/api/ops/matmul.cpp:355-371): four real products of the
+// (real, imaginary) parts, in the real type (float32 for complex32),
+//   re = A.re B.re - A.im B.im,  im = A.re B.im + A.im B.re,
+// each product rounded to the real type and the pair then combined in one
+// more rounding. Here the second product of each pair takes the first as its
+// bias with beta = 1 and alpha = -1 or 1, which is that same rounding
+// (acc * -1 is exact and the epilogue's one sum is the subtraction). Then
+// r *= alpha and r += beta * bias as complex multiplications of the parts
+// (complex_mul, src/api/ops/complex.cpp:43-46), when alpha != 1 and when a
+// bias is given with beta != 0. Conjugate and negative views are not
+// materialised: their signs fold into the products' alphas and the scalars.
+
+// The parts of a complex tensor as dense real tensors, and the sign each one
+// carries (conjugate view: imaginary negated; negative view: both).
+struct Parts {
+    at::Tensor re, im;
+    double sre = 1.0, sim = 1.0;
+};
+
+Parts parts_of(const at::Tensor& z, c10::ScalarType real) {
+    Parts p;
+    at::Tensor w = z;
+    if (w.is_neg()) {
+        w = w._neg_view();
+        p.sre = -p.sre;
+        p.sim = -p.sim;
+    }
+    if (w.is_conj()) {
+        w = w.conj();
+        p.sim = -p.sim;
+    }
+    at::Tensor pairs = at::view_as_real(w);
+    if (pairs.scalar_type() != real) pairs = pairs.to(real);
+    p.re = pairs.select(-1, 0).contiguous();
+    p.im = pairs.select(-1, 1).contiguous();
+    return p;
+}
+
+// (re, im) * (s.re, s.im) with the parts' signs folded into the scalar:
+// the reference's complex_mul of resolved parts, whose products differ from
+// these only by exact sign flips.
+void complex_scale(at::Tensor& re, at::Tensor& im, double sre, double sim, c10::complex<double> s) {
+    auto sc = [&](double v) { return at::scalar_tensor(v, re.options()); };
+    at::Tensor r = at::sub(at::mul(re, sc(sre * s.real())), at::mul(im, sc(sim * s.imag())));
+    at::Tensor i = at::add(at::mul(re, sc(sre * s.imag())), at::mul(im, sc(sim * s.real())));
+    re = r;
+    im = i;
+}
+
+at::Tensor complex_product(const Shape& s, const at::Tensor& bias_, const at::Scalar& alpha, const at::Scalar& beta,
+                           c10::ScalarType dtype, const std::function<at::Tensor()>& fallback) {
+    const c10::ScalarType real = c10::toRealValueType(dtype == at::kComplexHalf ? at::kComplexFloat : dtype);
+    bool ok = false;
+    const int32_t tdt = gemm_dtype_of(real, ok);
+    at::Tensor a3 = batched_view(s.self, s.batch_shape, s.M, s.K, s.B);
+    at::Tensor b3 = batched_view(s.other, s.batch_shape, s.K, s.N, s.B);
+    at::Tensor out = at::empty({s.B, s.M, s.N}, a3.options().dtype(dtype));
+    if (s.M == 0 || s.N == 0 || s.B == 0) return out;
+    const at::TensorOptions ro = a3.options().dtype(real);
+    at::Tensor re, im;
+    if (s.K == 0) {
+        re = at::zeros({s.B, s.M, s.N}, ro);
+        im = at::zeros({s.B, s.M, s.N}, ro);
+    } else {
+        const Parts A = parts_of(a3, real), B = parts_of(b3, real);
+        at::Tensor t1 = at::empty({s.B, s.M, s.N}, ro), t3 = at::empty({s.B, s.M, s.N}, ro);
+        re = at::empty({s.B, s.M, s.N}, ro);
+        im = at::empty({s.B, s.M, s.N}, ro);
+        if (!run_gemm(A.re, B.re, {}, A.sre * B.sre, 0.0, ACT_NONE, tdt, t1) ||
+            !run_gemm(A.im, B.im, t1, -A.sim * B.sim, 1.0, ACT_NONE, tdt, re) ||
+            !run_gemm(A.re, B.im, {}, A.sre * B.sim, 0.0, ACT_NONE, tdt, t3) ||
+            !run_gemm(A.im, B.re, t3, A.sim * B.sre, 1.0, ACT_NONE, tdt, im))
+            return fallback();
+    }
+    const c10::complex<double> al = alpha.toComplexDouble(), be = beta.toComplexDouble();
+    if (al != c10::complex<double>(1.0)) complex_scale(re, im, 1.0, 1.0, al);
+    if (bias_.defined() && be != c10::complex<double>(0.0)) {
+        at::Tensor c3 = batched_view(bias_, s.batch_shape, s.M, s.N, s.B);
+        Parts C = parts_of(c3.scalar_type() == dtype ? c3 : c3.to(dtype), real);
+        complex_scale(C.re, C.im, C.sre, C.sim, be);
+        re = at::add(re, C.re);
+        im = at::add(im, C.im);
+    }
+    at::Tensor pairs = at::view_as_real(out);
+    pairs.select(-1, 0).copy_(re);
+    pairs.select(-1, 1).copy_(im);
+    return out;
+}
+
 at::Tensor dispatch_matmul(const at::Tensor& self_, const at::Tensor& other_, const at::Tensor& bias_, const at::Scalar& alpha,
                            const at::Scalar& beta, Activation act, const std::function<at::Tensor()>& fallback) {
-    const bool has_bias = bias_.defined() && beta.toDouble() != 0.0;
     Shape s = matmul_shape(self_, other_);
-    const c10::ScalarType dtype = at::result_type(s.self, s.other);
+    // matmul_shape checked that both have one dtype (at::result_type would
+    // first resolve a conjugate view through the math-bit fallback)
+    const c10::ScalarType dtype = s.self.scalar_type();
+    if (at::isComplexType(dtype)) {
+        if (act != ACT_NONE || negative_strides({&s.self, &s.other, &bias_})) {
+            TVKB_FALLBACK("A ", dtype, " matmul with an activation or negative strides. Falling back to CPU.");
+            return fallback();
+        }
+        return finish(complex_product(s, bias_, alpha, beta, dtype, fallback), s);
+    }
+    const bool has_bias = bias_.defined() && beta.toDouble() != 0.0;
     bool ok = false;
     const int32_t tdt = gemm_dtype_of(dtype, ok);
     if (!ok) {
@@ -127,53 +282,11 @@ at::Tensor dispatch_matmul(const at::Tensor& self_, const at::Tensor& other_, co
         at::Tensor r = has_bias ? (bias * beta) : out.zero_();
         return finish(apply_activation(r, act), s);
     }
-    for (const at::Tensor* t : {&a, &b, &bias}) {
-        if (!t->defined()) continue;
-        for (int64_t d = 0; d < 3; ++d)
-            if (t->stride(d) < 0) {
-                TVKB_FALLBACK("A matmul operand with negative strides. Falling back to CPU.");
-                return fallback();
-            }
-    }
-
-    tvk_gemm_desc d;
-    std::memset(&d, 0, sizeof(d));
-    d.dtype = tdt;
-    d.activation = act;
-    d.flags = 0;
-    if (const char* e = std::getenv("TORCHVULKAN_EXACT")) {
-        if (e[0] && std::strcmp(e, "0") != 0) d.flags = TVK_GEMM_EXACT;
-    }
-    d.batch = s.B; d.M = s.M; d.N = s.N; d.K = s.K;
-    d.a = a.data_ptr();
-    d.b = b.data_ptr();
-    d.c = out.data_ptr();
-    for (int i = 0; i < 3; ++i) {
-        d.a_stride[i] = a.stride(i);
-        d.b_stride[i] = b.stride(i);
-        d.c_stride[i] = out.stride(i);
-    }
-    if (has_bias) {
-        d.bias = bias.data_ptr();
-        for (int i = 0; i < 3; ++i) d.bias_stride[i] = bias.stride(i);
-    }
-    d.alpha = alpha.toDouble();
-    d.beta = has_bias ? beta.toDouble() : 0.0;
-    d.stream = stream_of(out);
-    // TORCHVULKAN_AUTOTUNE=1: a shape class without a recorded kernel is timed
-    // over every candidate first and the fastest recorded (the reference tunes
-    // every matmul on first sight, src/api/ops/matmul.cpp:538-544); otherwise
-    // the recorded or shape-chosen kernel runs
-    static const bool autotune = [] {
-        const char* e = std::getenv("TORCHVULKAN_AUTOTUNE");
-        return e != nullptr && e[0] && std::strcmp(e, "0") != 0;
-    }();
-    const tvk_status st = autotune ? tvk_gemm_tune(&d, nullptr, 0) : tvk_gemm(&d);
-    if (st == TVK_ERR_UNSUPPORTED) {
-        TVKB_FALLBACK(tvk_last_error(), ". Falling back to CPU.");
+    if (negative_strides({&a, &b, &bias})) {
+        TVKB_FALLBACK("A matmul operand with negative strides. Falling back to CPU.");
         return fallback();
     }
-    check_status(st, "tvk_gemm");
+    if (!run_gemm(a, b, bias, alpha.toDouble(), has_bias ? beta.toDouble() : 0.0, act, tdt, out)) return fallback();
     return finish(out, s);
 }
 
@@ -371,6 +484,87 @@ at::Tensor& addmv_inplace_vk(at::Tensor& self, const at::Tensor& mat, const at::
     return write_back(self, addmv_vk(self, mat, vec, beta, alpha));
 }
 
+// 1 / x of a float32 scalar on the device (tvk_binary's IEEE division).
+at::Tensor device_reciprocal(const at::Tensor& x) {
+    at::Tensor one = at::scalar_tensor(1.0, x.options().dtype(at::kFloat));
+    at::Tensor v = x.reshape({}).to(at::kFloat);
+    at::Tensor out = at::empty({}, one.options());
+    tvk_binary_desc d;
+    std::memset(&d, 0, sizeof(d));
+    d.op = TVK_BIN_DIV;
+    d.dtype = TVK_F32;
+    d.ndim = 0;
+    d.a = one.data_ptr();
+    d.b = v.data_ptr();
+    d.out = out.data_ptr();
+    d.alpha = 1.0;
+    d.stream = stream_of(out);
+    check_status(tvk_binary(&d), "tvk_binary");
+    return out;
+}
+
+// _scaled_mm (+ .out): torch's emulated float8 product, as the reference
+// computes it on its device (scaled_mm_out_vulkan, src/api/ops/matmul.cpp:706-747,
+// torch's own checks and messages): the float8 operands are decoded to
+// float32 and multiplied by their scales (one scale each, or a row of A by a
+// column of B), multiplied in float32, the bias added, the product
+// multiplied by 1 / scale_result when the target is a float8 type, and
+// rounded to the output's dtype. Every step runs on the device.
+at::Tensor& scaled_mm_out_vk(const at::Tensor& mat1, const at::Tensor& mat2, const at::Tensor& scale_a,
+                             const at::Tensor& scale_b, const std::optional<at::Tensor>& bias,
+                             const std::optional<at::Tensor>& scale_result, std::optional<at::ScalarType> out_dtype,
+                             bool /* use_fast_accum */, at::Tensor& out) {
+    TORCH_CHECK_VALUE(!out_dtype || *out_dtype == out.scalar_type(), "out_dtype must match output matrix type");
+    TORCH_CHECK(mat1.dim() == 2, "mat1 must be a matrix");
+    TORCH_CHECK(mat2.dim() == 2, "mat2 must be a matrix");
+    TORCH_CHECK(mat1.size(1) == mat2.size(0), "mat_a and mat_b shapes cannot be multiplied (", mat1.size(0), "x",
+                mat1.size(1), " and ", mat2.size(0), "x", mat2.size(1), ")");
+    TORCH_CHECK_VALUE(at::isFloat8Type(mat1.scalar_type()) && at::isFloat8Type(mat2.scalar_type()),
+                      "mat1 and mat2 must be fp8 types, got: ", mat1.scalar_type(), mat2.scalar_type());
+    const bool tensorwise = scale_a.numel() == 1 && scale_b.numel() == 1;
+    const bool rowwise = scale_a.dim() == 2 && scale_b.dim() == 2 && scale_a.size(0) == mat1.size(0) &&
+                         scale_a.size(1) == 1 && scale_b.size(0) == 1 && scale_b.size(1) == mat2.size(1);
+    TORCH_CHECK_VALUE(tensorwise || rowwise, "Invalid scaling configuration");
+    TORCH_CHECK_VALUE(scale_a.scalar_type() == at::kFloat, "scale_a must have Float elements");
+    TORCH_CHECK_VALUE(scale_b.scalar_type() == at::kFloat, "scale_b must have Float elements");
+    TORCH_CHECK(!scale_result || (scale_result->numel() == 1 && scale_result->scalar_type() == at::kFloat),
+                "scale_result must be a float scalar");
+    TORCH_CHECK(!bias || bias->numel() == mat2.size(1), "Bias must be size ", mat2.size(1), " but got ", bias->numel());
+    bool ok8 = false;
+    copy_dtype_of(mat1.scalar_type(), ok8);
+    bool ok8b = false;
+    copy_dtype_of(mat2.scalar_type(), ok8b);
+    auto on_dev = [&](const at::Tensor& t) { return t.device() == mat1.device(); };
+    if (!ok8 || !ok8b || !on_dev(mat2) || !on_dev(scale_a) || !on_dev(scale_b) || (bias && !on_dev(*bias)) ||
+        (scale_result && !on_dev(*scale_result))) {
+        TVKB_FALLBACK("A _scaled_mm of ", mat1.scalar_type(), " operands or with host tensors. Falling back to CPU.");
+        std::optional<at::Tensor> bc, rc;
+        if (bias) bc = bias->cpu();
+        if (scale_result) rc = scale_result->cpu();
+        at::Tensor r = at::_scaled_mm(mat1.cpu(), mat2.cpu(), scale_a.cpu(), scale_b.cpu(), bc, rc, out_dtype, false);
+        at::native::resize_output(out, r.sizes());
+        out.copy_(r);
+        return out;
+    }
+    at::native::resize_output(out, {mat1.size(0), mat2.size(1)});
+    const at::ScalarType target = out_dtype.value_or(at::kBFloat16);
+    at::Tensor a = at::mul(mat1.to(at::kFloat), tensorwise ? scale_a.reshape({}) : scale_a);
+    at::Tensor b = at::mul(mat2.to(at::kFloat), tensorwise ? scale_b.reshape({}) : scale_b);
+    at::Tensor product = at::mm(a, b);
+    if (bias) product = at::add(product, *bias);
+    if (scale_result && (target == at::kFloat8_e4m3fn || target == at::kFloat8_e5m2))
+        product = at::mul(product, device_reciprocal(*scale_result));
+    out.copy_(product);
+    return out;
+}
+
+at::Tensor scaled_mm_vk(const at::Tensor& mat1, const at::Tensor& mat2, const at::Tensor& scale_a, const at::Tensor& scale_b,
+                        const std::optional<at::Tensor>& bias, const std::optional<at::Tensor>& scale_result,
+                        std::optional<at::ScalarType> out_dtype, bool use_fast_accum) {
+    at::Tensor out = at::empty({0}, mat1.options().dtype(out_dtype.value_or(mat1.scalar_type())));
+    return scaled_mm_out_vk(mat1, mat2, scale_a, scale_b, bias, scale_result, out_dtype, use_fast_accum, out);
+}
+
 }  // namespace
 }  // namespace tvkb
 
@@ -393,4 +587,6 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
     m.impl("addmv", &tvkb::addmv_vk);
     m.impl("addmv.out", &tvkb::addmv_out_vk);
     m.impl("addmv_", &tvkb::addmv_inplace_vk);
+    m.impl("_scaled_mm", &tvkb::scaled_mm_vk);
+    m.impl("_scaled_mm.out", &tvkb::scaled_mm_out_vk);
 }

@@ -2,7 +2,7 @@
 // element-wise kernels: the reference's castValue
 // (src/shaders/core/cast.slang:49-52, src/shaders/core/dtype.slang:122-282).
 // The source widens to int64 (signed integers), uint64 (U8, BOOL), float
-// (F16, BF16, F32) or double (F64); the destination is built from that one
+// (F16, BF16, F32, the float8 types) or double (F64); the destination is built from that one
 // wide value. With a bool on either side the value is (src != 0) ? 1 : 0
 // (src/shaders/ops/cast.slang:29-33).
 #pragma once
@@ -19,9 +19,11 @@ constexpr int DYN = -1;   // dtype taken from the kernel arguments
 
 enum { FAM_I = 0, FAM_U = 1, FAM_F = 2, FAM_D = 3 };
 
+__host__ __device__ constexpr bool is_f8(int dt) { return dt == TVK_F8E4M3FN || dt == TVK_F8E5M2; }
+
 __host__ __device__ constexpr int family(int dt) {
     return dt == TVK_F64 ? FAM_D
-         : (dt == TVK_F32 || dt == TVK_F16 || dt == TVK_BF16) ? FAM_F
+         : (dt == TVK_F32 || dt == TVK_F16 || dt == TVK_BF16 || is_f8(dt)) ? FAM_F
          : (dt == TVK_U8 || dt == TVK_BOOL) ? FAM_U
          : FAM_I;
 }
@@ -32,6 +34,67 @@ struct Wide {
     float f;
     double d;
 };
+
+// float8 (torch's float8_e4m3fn and float8_e5m2). The reference converts
+// them with c10's own routines, through float32 (transfer.cpp:129-226), so
+// these match the CPU bit for bit.
+//
+// Decoding is exact: the code's fields placed into a float32. NaN codes get
+// the payload the CPU's conversion gives them: e5m2 goes through float16 on
+// the CPU, which widens the payload (m << 21) and sets the quiet bit;
+// e4m3fn's single NaN per sign becomes 0x7FF00000.
+__device__ __forceinline__ float f8_to_f32(uint8_t c, int dt) {
+    const uint32_t sign = (uint32_t)(c & 0x80) << 24;
+    uint32_t bits;
+    if (dt == TVK_F8E4M3FN) {
+        const uint32_t e = (c >> 3) & 15, m = c & 7;
+        if (e == 15 && m == 7) bits = 0x7FF00000u;
+        else if (e == 0) return __builtin_bit_cast(float, sign | __builtin_bit_cast(uint32_t, (float)m * 0x1p-9f));
+        else bits = ((e + 120) << 23) | (m << 20);
+    } else {
+        const uint32_t e = (c >> 2) & 31, m = c & 3;
+        if (e == 31) bits = (m ? 0x7FC00000u : 0x7F800000u) | (m << 21);
+        else if (e == 0) return __builtin_bit_cast(float, sign | __builtin_bit_cast(uint32_t, (float)m * 0x1p-16f));
+        else bits = ((e + 112) << 23) | (m << 21);
+    }
+    return __builtin_bit_cast(float, sign | bits);
+}
+
+// Encoding: round to nearest even onto the 8-bit grid, on the float's bits
+// (integer arithmetic only, so no flush of float32 subnormals can interfere).
+//   e4m3fn: |x| >= 480 (NaN and infinities included) is NaN; below that a
+//           magnitude rounding past 448 lands on the NaN code 0x7F too.
+//   e5m2:   NaN is 0x7F; |x| >= 65536 is infinity; below that a magnitude
+//           rounding past 57344 lands on the infinity code 0x7C.
+__device__ __forceinline__ uint8_t f32_to_f8(float x, int dt) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const uint8_t sign = (uint8_t)((u >> 24) & 0x80);
+    const uint32_t a = u & 0x7FFFFFFFu;
+    const bool e4 = dt == TVK_F8E4M3FN;
+    if (e4) {
+        if (a >= 0x43F00000u) return sign | 0x7F;
+    } else {
+        if (a > 0x7F800000u) return sign | 0x7F;
+        if (a >= 0x47800000u) return sign | 0x7C;
+    }
+    const int bias = e4 ? 7 : 15, mb = e4 ? 3 : 2;
+    const int e = (int)(a >> 23);
+    if (e >= 128 - bias) {   // a normal 8-bit value: rebias, round the mantissa
+        const int sh = 23 - mb;
+        uint32_t t = a - ((uint32_t)(127 - bias) << 23);
+        t += ((1u << (sh - 1)) - 1) + ((t >> sh) & 1);
+        return sign | (uint8_t)(t >> sh);
+    }
+    // subnormal 8-bit range: a / 2^(1 - bias - mb) rounded to an integer
+    // (reaching 2^mb gives the smallest normal code, as it should)
+    const int s = 151 - bias - mb - e;
+    if (e == 0 || s > 24) return sign;   // below half the smallest step
+    const uint32_t mant = (a & 0x7FFFFFu) | 0x800000u;
+    uint32_t q = mant >> s;
+    const uint32_t r = mant & ((1u << s) - 1), h = 1u << (s - 1);
+    if (r > h || (r == h && (q & 1))) ++q;
+    return sign | (uint8_t)q;
+}
 
 __device__ __forceinline__ Wide load_wide(const char* p, int dt) {
     Wide w{0, 0, 0.0f, 0.0};
@@ -44,6 +107,7 @@ __device__ __forceinline__ Wide load_wide(const char* p, int dt) {
         case TVK_I32: w.i = *reinterpret_cast<const int32_t*>(p); break;
         case TVK_I16: w.i = *reinterpret_cast<const int16_t*>(p); break;
         case TVK_I8: w.i = *reinterpret_cast<const int8_t*>(p); break;
+        case TVK_F8E4M3FN: case TVK_F8E5M2: w.f = f8_to_f32(*reinterpret_cast<const uint8_t*>(p), dt); break;
         default: w.u = *reinterpret_cast<const uint8_t*>(p); break;   // U8, BOOL
     }
     return w;
@@ -141,6 +205,7 @@ __device__ __forceinline__ void store_narrow(char* p, int dt, const Wide& w, int
         case TVK_I16: *reinterpret_cast<int16_t*>(p) = wide_to_int<int16_t>(w, fam); break;
         case TVK_I8: *reinterpret_cast<int8_t*>(p) = wide_to_int<int8_t>(w, fam); break;
         case TVK_U8: *reinterpret_cast<uint8_t*>(p) = wide_to_u8(w, fam); break;
+        case TVK_F8E4M3FN: case TVK_F8E5M2: *reinterpret_cast<uint8_t*>(p) = f32_to_f8(wide_to_f32(w, fam), dt); break;
         default: *reinterpret_cast<uint8_t*>(p) = nonzero(w, fam) ? 1 : 0; break;   // BOOL
     }
 }

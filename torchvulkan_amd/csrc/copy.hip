@@ -323,7 +323,7 @@ struct Plan {
     int j;   // transpose: the source's contiguous dimension
 };
 
-bool valid_dtype(int dt) { return dt >= TVK_F32 && dt <= TVK_BOOL; }
+bool valid_dtype(int dt) { return dt >= TVK_F32 && dt <= TVK_F8E5M2; }
 
 tvk_status make_plan(const tvk_copy_desc* d, Plan& pl, const char* who) {
     if (!d) return fail(TVK_ERR_INVALID, std::string(who) + ": desc is NULL");

@@ -321,7 +321,7 @@ tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
-// element-wise add / sub / mul
+// element-wise add / sub / mul / div
 // ---------------------------------------------------------------------------
 
 template <typename T> struct BinT;   // storage type -> arithmetic
@@ -329,6 +329,7 @@ template <> struct BinT<float> {
     __device__ static inline float op(int o, float a, float b, float al, bool has_alpha) {
 #pragma clang fp contract(off)
         if (o == TVK_BIN_MUL) return a * b;
+        if (o == TVK_BIN_DIV) return a / b;
         const float t = has_alpha ? al * b : b;
         return o == TVK_BIN_ADD ? a + t : a - t;
     }
@@ -337,6 +338,7 @@ template <> struct BinT<double> {
     __device__ static inline double op(int o, double a, double b, double al, bool has_alpha) {
 #pragma clang fp contract(off)
         if (o == TVK_BIN_MUL) return a * b;
+        if (o == TVK_BIN_DIV) return a / b;
         const double t = has_alpha ? al * b : b;
         return o == TVK_BIN_ADD ? a + t : a - t;
     }
@@ -353,6 +355,7 @@ __device__ __forceinline__ uint16_t bin16(int o, uint16_t a, uint16_t b, uint16_
         return DT == TVK_F16 ? __builtin_bit_cast(uint16_t, (_Float16)v) : f32_to_bf16_bits(v);
     };
     if (o == TVK_BIN_MUL) return fromf(tof(a) * tof(b));
+    if (o == TVK_BIN_DIV) return fromf(tof(a) / tof(b));
     const uint16_t t = has_alpha ? fromf(tof(al) * tof(b)) : b;
     return fromf(o == TVK_BIN_ADD ? tof(a) + tof(t) : tof(a) - tof(t));
 }
@@ -576,8 +579,10 @@ extern "C" tvk_status tvk_reduce_sum(const tvk_reduce_desc* d) {
 
 extern "C" tvk_status tvk_binary(const tvk_binary_desc* d) {
     if (!d) return fail(TVK_ERR_INVALID, "tvk_binary: desc is NULL");
-    if (d->op < TVK_BIN_ADD || d->op > TVK_BIN_MUL) return fail(TVK_ERR_INVALID, "tvk_binary: unknown op");
+    if (d->op < TVK_BIN_ADD || d->op > TVK_BIN_DIV) return fail(TVK_ERR_INVALID, "tvk_binary: unknown op");
     if (d->dtype < TVK_F32 || d->dtype > TVK_U8) return fail(TVK_ERR_UNSUPPORTED, "tvk_binary: unsupported dtype");
+    if (d->op == TVK_BIN_DIV && d->dtype != TVK_F32 && d->dtype != TVK_F16 && d->dtype != TVK_BF16 && d->dtype != TVK_F64)
+        return fail(TVK_ERR_UNSUPPORTED, "tvk_binary: division takes floating point dtypes only");
     if (d->reserved != 0) return fail(TVK_ERR_INVALID, "tvk_binary: nonzero reserved field");
     if (d->ndim < 0 || d->ndim > kMaxDims) return fail(TVK_ERR_UNSUPPORTED, "tvk_binary: too many dimensions");
     BinArgs p{};
@@ -625,7 +630,7 @@ extern "C" tvk_status tvk_binary(const tvk_binary_desc* d) {
     p.a = static_cast<const char*>(d->a);
     p.b = static_cast<const char*>(d->b);
     p.out = static_cast<char*>(d->out);
-    p.has_alpha = d->op != TVK_BIN_MUL && d->alpha != 1.0;
+    p.has_alpha = (d->op == TVK_BIN_ADD || d->op == TVK_BIN_SUB) && d->alpha != 1.0;
     p.alpha_bits = alpha_bits_of(d->dtype, d->alpha);
     const size_t es = dtype_size(d->dtype);
     auto al = [&](const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % (es * 8) == 0; };
