@@ -53,11 +53,19 @@ def _run(cmd: list[str]) -> None:
         print(out)
 
 
-# The attention kernels keep every MFMA accumulator in VGPRs: their softmax
-# and rescale steps work on the accumulators with ordinary VALU instructions,
-# which the AGPR form would surround with accvgpr copies.
+# MFMA results in VGPRs for these files: the attention kernels' softmax and
+# rescale steps work on the accumulators with ordinary VALU instructions, and
+# in the AGPR form hipcc rotates the GEMM and convolution kernels'
+# accumulators through AGPR copies inside their k loops (the 256x256 ring
+# GEMM, gemm_dma.hip, and gemm.hip allocate cleanly in the default form).
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 FILE_FLAGS = {
-    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "attention.hip": VGPR_FORM,
+    "gemm_dma128.hip": VGPR_FORM,
+    "gemm_skinny.hip": VGPR_FORM,
+    "conv.hip": VGPR_FORM,
+    "conv_nhwc.hip": VGPR_FORM,
+    "conv_stem.hip": VGPR_FORM,
 }
 
 

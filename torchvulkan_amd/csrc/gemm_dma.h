@@ -1,0 +1,400 @@
+// float16/bfloat16 GEMM for large problems on gfx950: 256x256 workgroup tiles,
+// 8 waves (two per SIMD), v_mfma_f32_16x16x32, operands fetched from global
+// memory straight into LDS by buffer loads (no register staging) through a
+// ring of four 32-k stages.
+//
+// Reference semantics: the same operand model and epilogue as the other
+// tvk_gemm kernels (src/shaders/helpers/gemm.slang:3-9,
+// src/shaders/helpers/gemm_simd.slang:67-99); only the summation order inside
+// a 32-k step differs (the MFMA's), as with the reference's coop-matrix path
+// (src/shaders/ops/matmul_coop.slang:172-222).
+//
+// LDS layouts (per stage, per operand, 16 KB). gfx950's LDS has 64 banks of
+// 4 bytes; a ds_read_b128 is served 16 lanes a cycle, in the lane groups
+// {0-3, 12-15, 20-27}, {16-19, 28-31, 4-11} and the same two shifted by 32
+// (measured: bank-conflict counters over address patterns that tell the
+// groupings apart); a ds_read_b64 (also the transposing one) 32 lanes a
+// cycle. A read is conflict-free when each group's 16-byte (8-byte) units
+// fall on distinct banks.
+//   k-contiguous operand ("KM"): BM or BN rows x 32 k, 64 B per row. Row r's
+//     16-byte chunk c sits at slot c ^ swz_km(r). With the wide swizzle,
+//     (r >> 1) & 3, each lane group of a fragment read (16 rows x one chunk)
+//     lands on 16 distinct 16-byte bank slots; the narrow one,
+//     ((r >> 1) ^ (r >> 3)) & 3, puts two units of a group on one slot.
+//   m/n-contiguous operand ("MN"): 32 k-rows x W columns (W >= 128), 2W bytes
+//     per row, chunk slot c ^ swz_mn(k). Fragments are read with
+//     ds_read_b64_tr_b16, which transposes 4 k-rows x 16 columns across each
+//     16-lane group; the 32 lanes served together read k-rows 8g + 0..3 and
+//     8(g+1) + 0..3. The wide swizzle spreads them over all 64 banks (bit 3
+//     of the k-row selects the other half of the bank window); the narrow one
+//     leaves the two row groups on the same banks (two cycles a read).
+// The 128x128 tiles use the wide swizzles; the 256x256 tile the narrow ones,
+// measured 1 % faster there (its LDS reads are not what limits it, and the
+// wide MN swizzle spills registers when A is the MN operand).
+// Each buffer load writes one contiguous 1 KB block of LDS (lane l's 16 bytes
+// at offset 16*l), so every block is 16 KM rows or 2 MN rows.
+//
+// Pipeline, per 32-k stage kt (each wave: 32 MFMAs of 16x16x32 on a 128x64
+// wave tile): the MFMAs use fragments already in registers; between them the
+// wave reads the next stage's fragments and issues its share of the loads of
+// stage kt+4 into the slot stage kt occupied (free: every wave read it before
+// the previous barrier). One barrier per stage, after waiting until stage kt+2
+// has landed. The loads are issued from inline assembly: a compiler-visible
+// LDS-DMA would make every later LDS read wait for all of them.
+#pragma once
+
+#include "gemm_common.h"
+
+#include <type_traits>
+
+namespace tvk {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define TVK_LDS __attribute__((address_space(3)))
+
+constexpr int D_BK = 32;
+
+// Tile configurations: 256x256 runs 8 waves of 128x64; the others 64x64 wave
+// tiles (128x128: 4 waves, 256x128 and 128x256: 8 waves).
+template <int BM_, int BN_>
+struct DCfg {
+    static constexpr int BM = BM_, BN = BN_;
+    static constexpr bool BIG = BM == 256 && BN == 256;
+    static constexpr int NW = BIG ? 8 : (BM / 64) * (BN / 64);
+    static constexpr int NT = 64 * NW;
+    static constexpr int WN = BIG ? 4 : BN / 64;           // waves along N
+    static constexpr int WMW = NW / WN;                     // waves along M
+    static constexpr int WTM = BM / WMW, WTN = BN / WN;     // wave tile
+    static constexpr int FM = WTM / 16, FN = WTN / 16;
+    static constexpr int OPA = BM * D_BK * 2, OPB = BN * D_BK * 2;   // bytes per operand per stage
+    static constexpr int STB = OPA + OPB;
+    static constexpr int DA = OPA / 1024 / NW, DB = OPB / 1024 / NW; // loads per wave per stage
+    static constexpr int DS = DA + DB;
+    static_assert(DA >= 1 && DB >= 1 && WTN == 64, "tile configuration");
+};
+
+// Buffer resource over [p, p + bytes): loads past the end return zeros.
+__device__ inline i32x4 dma_rsrc(const void* p, int64_t bytes) {
+    const uint64_t a = (uint64_t)p;
+    return i32x4{(int)(uint32_t)a, (int)((a >> 32) & 0xffff), (int)min(bytes, (int64_t)0x7fffffff), 0x00020000};
+}
+
+// 16 bytes per lane from r + voff into LDS at lds_addr + 16 * lane (lds_addr
+// is wave-uniform; it travels in M0).
+__device__ inline void dma16(i32x4 r, uint32_t lds_addr, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(lds_addr), "v"(voff), "s"(r) : "memory");
+}
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+template <bool WIDE>
+__device__ inline int swz_km(int row) { return WIDE ? (row >> 1) & 3 : ((row >> 1) ^ (row >> 3)) & 3; }
+template <bool WIDE>
+__device__ inline int swz_mn(int kr) { return WIDE ? ((kr & 3) | (((kr >> 3) & 1) << 2)) * 2 : (kr & 3) * 2; }
+
+// Per-lane source offsets (bytes, at k = 0) of one operand's loads. Rows or
+// columns outside the matrix start at kOOB, so with the k advance added they
+// stay past the buffer's end and load zeros.
+// D loads per wave; W = the tile's extent along this operand's rows (m or n):
+// an MN tile has k-rows of 2W bytes, 1024 / (2W) of them per 1 KB load; XS:
+// the wide swizzles.
+template <bool KM, int D, int W, bool XS>
+struct DmaSrc {
+    static_assert(KM || W >= 128, "the MN swizzle moves chunks within 16-chunk blocks");
+    uint32_t off[D];
+    uint32_t kstep;   // bytes per stage along k
+    __device__ inline void init(int64_t s_row, int64_t s_k, int row0, int rows, int wave, int lane) {
+        constexpr int CPR = 2 * W / 16;   // 16-byte chunks per MN k-row
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const int blk = wave * D + i;
+            if constexpr (KM) {
+                const int row = blk * 16 + lane / 4;
+                const int c = (lane % 4) ^ swz_km<XS>(row);
+                const int gr = row0 + row;
+                off[i] = gr < rows ? (uint32_t)(((int64_t)gr * s_row + c * 8) * 2) : kOOB;
+            } else {
+                const int kr = blk * (64 / CPR) + lane / CPR;
+                const int c = (lane % CPR) ^ swz_mn<XS>(kr);
+                const int gc = row0 + c * 8;
+                off[i] = gc < rows ? (uint32_t)(((int64_t)kr * s_k + gc) * 2) : kOOB;
+            }
+        }
+        kstep = KM ? (uint32_t)(D_BK * 2) : (uint32_t)(D_BK * s_k * 2);
+    }
+};
+
+// One 16x16x32 operand fragment: lane l holds row (or column) l % 16 and
+// k = (l / 16) * 8 .. + 7 of the stage.
+template <bool KM, int W, bool XS>
+__device__ inline u32x4 read_frag(uint32_t base, int row_base, int lane) {
+    if constexpr (KM) {
+        const int row = row_base + lane % 16;
+        const int chunk = lane / 16;
+        return *(const TVK_LDS u32x4*)(uintptr_t)(base + row * (2 * D_BK) + ((chunk ^ swz_km<XS>(row)) * 16));
+    } else {
+        // source lane s of group g points at k-row 8g + 4rr + s/4, columns 4(s%4)..+3;
+        // the transpose hands lane s the four k values of column s
+        const int g = lane / 16, s = lane % 16;
+        const int col = row_base + (s % 4) * 4;
+        const int chunk = col / 8, within = (col % 8) * 2;
+        u32x4 out;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int kr = g * 8 + rr * 4 + s / 4;
+            TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(base + kr * (2 * W) + ((chunk ^ swz_mn<XS>(kr)) * 16) + within);
+            const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+            out[rr * 2] = w.x;
+            out[rr * 2 + 1] = w.y;
+        }
+        return out;
+    }
+}
+
+template <int DT>
+__device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (DT == TVK_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+constexpr int dma_threads(int bm, int bn) { return 64 * ((bm == 256 && bn == 256) ? 8 : (bm / 64) * (bn / 64)); }
+
+// NS: stages in the ring (4, or 8 for 128x128 tiles whose loads need more
+// lookahead to cover memory latency: short K, one workgroup per CU).
+template <int DT, bool AK, bool BK, int BM, int BN, int NS>
+__global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArgs p) {
+    constexpr int D_NS = NS;
+    typedef DCfg<BM, BN> G;
+    constexpr int D_BM = BM, D_BN = BN, D_NT = G::NT, D_FM = G::FM, D_FN = G::FN, D_WTM = G::WTM, D_WTN = G::WTN;
+    constexpr int D_OPB = G::OPA, D_STB = G::STB, D_DPS = G::DS;
+    static_assert(dma_threads(BM, BN) == G::NT, "thread count");
+    __shared__ __attribute__((aligned(1024))) char lds_raw[D_NS * D_STB];
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds_raw);
+    const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int wm = wave / G::WN, wn = wave % G::WN;
+    const int b = blockIdx.y;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * D_BM, n0 = tn * D_BN;
+
+    // A: (m, k) at m*sa[1] + k*sa[2]; B: (k, n) at k*sb[1] + n*sb[2]
+    const char* A = reinterpret_cast<const char*>(p.a) + (int64_t)b * p.sa[0] * 2;
+    const char* B = reinterpret_cast<const char*>(p.b) + (int64_t)b * p.sb[0] * 2;
+    const i32x4 ra = dma_rsrc(A, 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1));
+    const i32x4 rb = dma_rsrc(B, 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1));
+    constexpr bool XS = !G::BIG;   // the wide (conflict-free) swizzles
+    DmaSrc<AK, G::DA, BM, XS> da;
+    DmaSrc<BK, G::DB, BN, XS> db;
+    da.init(p.sa[1], p.sa[2], m0, p.M, wave, lane);
+    db.init(p.sb[2], p.sb[1], n0, p.N, wave, lane);
+    // split-K (grid z): this workgroup's k range starts at stage kt0
+    const int kt0 = p.split > 1 ? (int)blockIdx.z * (p.k_chunk / D_BK) : 0;
+    auto dma_one = [&](int kt, int q) {   // q-th load (of D_DPS) of this wave for stage kt
+        const uint32_t slot = lds0 + (uint32_t)((kt % D_NS) * D_STB);
+        const uint32_t kg = (uint32_t)(kt0 + kt);
+        if (q < G::DA) dma16(ra, slot + (uint32_t)((wave * G::DA + q) * 1024), da.off[q] + kg * da.kstep);
+        else dma16(rb, slot + D_OPB + (uint32_t)((wave * G::DB + q - G::DA) * 1024), db.off[q - G::DA] + kg * db.kstep);
+    };
+
+    f32x4 acc[D_FM][D_FN];
+#pragma unroll
+    for (int i = 0; i < D_FM; ++i)
+#pragma unroll
+        for (int j = 0; j < D_FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    u32x4 fa[2][D_FM], fb[2][D_FN];
+    const int nk = (p.split > 1 ? min(p.k_chunk, p.K - (int)blockIdx.z * p.k_chunk) : p.K) / D_BK;
+    // prologue: stages 0..3 in flight; stage 0's fragments in registers once it
+    // has landed, stage 1 landed before the loop reads it
+#pragma unroll
+    for (int s = 0; s < D_NS; ++s)
+#pragma unroll
+        for (int q = 0; q < D_DPS; ++q) dma_one(s, q);
+    wait_vmcnt<D_DPS * (D_NS - 1)>();
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < D_FM; ++i) fa[0][i] = read_frag<AK, BM, XS>(lds0, wm * D_WTM + i * 16, lane);
+#pragma unroll
+    for (int j = 0; j < D_FN; ++j) fb[0][j] = read_frag<BK, BN, XS>(lds0 + D_OPB, wn * D_WTN + j * 16, lane);
+    wait_vmcnt<D_DPS * (D_NS - 2)>();
+    __syncthreads();
+
+    // Stage kt: MFMAs from register set `cur`; in between, one fragment read
+    // of stage kt+1 (into set cur^1) after each even MFMA and one load of
+    // stage kt+4 after each odd one, in this exact order (sched_barrier).
+    auto body = [&](int kt, auto cur_c) {
+        constexpr int cur = decltype(cur_c)::value;
+        const uint32_t st_next = lds0 + (uint32_t)(((kt + 1) % D_NS) * D_STB);
+#pragma unroll
+        for (int q = 0; q < D_FM * D_FN; ++q) {
+            const int i = q / D_FN, j = q % D_FN;
+            acc[i][j] = mfma16<DT>(fa[cur][i], fb[cur][j], acc[i][j]);
+            if (q % 2 == 0) {
+                const int r = q / 2;
+                if (r < D_FM) fa[cur ^ 1][r] = read_frag<AK, BM, XS>(st_next, wm * D_WTM + r * 16, lane);
+                else if (r < D_FM + D_FN) fb[cur ^ 1][r - D_FM] = read_frag<BK, BN, XS>(st_next + D_OPB, wn * D_WTN + (r - D_FM) * 16, lane);
+            } else if (q / 2 < D_DPS) {
+                dma_one(kt + D_NS, q / 2);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // stage kt+2 landed for this wave; after the barrier, for all waves
+        wait_vmcnt<D_DPS * (D_NS - 2)>();
+        __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        body(kt, std::integral_constant<int, 0>{});
+        body(kt + 1, std::integral_constant<int, 1>{});
+    }
+    if (kt < nk) body(kt, std::integral_constant<int, 0>{});
+    // loads of stages past the end are still in flight: drain them before
+    // the workgroup's LDS can be handed to another
+    wait_vmcnt<0>();
+
+    if (p.split > 1) {
+        // float32 partials part[z][batch][M][N] straight from the accumulators
+        // (lane l: column l % 16, register r: row (l / 16) * 4 + r)
+        float* part = p.part + ((int64_t)blockIdx.z * p.batch + b) * p.M * p.N;
+#pragma unroll
+        for (int i = 0; i < D_FM; ++i)
+#pragma unroll
+            for (int j = 0; j < D_FN; ++j) {
+                const int col = n0 + wn * D_WTN + j * 16 + lane % 16;
+                if (col >= p.N) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = m0 + wm * D_WTM + i * 16 + (lane / 16) * 4 + r;
+                    if (row < p.M) part[(int64_t)row * p.N + col] = acc[i][j][r];
+                }
+            }
+        return;
+    }
+
+    __syncthreads();   // every wave is done with the ring: it now holds the output tile
+
+    // Output through LDS, 64 rows at a time. The waves write their float32
+    // accumulators (layout of v_mfma_f32_16x16x32: lane l holds column l % 16,
+    // register r row (l / 16) * 4 + r); then each thread finishes 8 consecutive
+    // columns of one row (alpha, bias, activation, one rounding) and stores
+    // them with a single 16-byte store where the output rows allow it.
+    typedef typename elem<DT>::T T;
+    constexpr int E_LD = D_BN + 4;   // floats per LDS row
+    float* et = reinterpret_cast<float*>(lds_raw);
+    T* Cb = reinterpret_cast<T*>(p.c) + (int64_t)b * p.sc[0];
+    const T* Bb = p.has_bias ? reinterpret_cast<const T*>(p.bias) + (int64_t)b * p.sbias[0] : nullptr;
+    auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    const bool vec_c = p.sc[2] == 1 && p.sc[1] % 8 == 0 && al16(Cb);
+    const bool vec_b = p.has_bias && p.sbias[2] == 1 && p.sbias[1] % 8 == 0 && al16(Bb);
+    const bool plain = !p.has_bias && p.act == TVK_ACT_NONE;
+    // thread tid finishes chunk q = tid + j * D_NT (j < 4) of each 64-row pass:
+    // row q / 32, columns 8 * (q % 32); the bias chunks of all four passes are
+    // requested up front so their latency overlaps
+    constexpr int NPASS = D_BM / 64, CPT = 64 * (D_BN / 8) / D_NT;   // passes; chunks per thread per pass
+    static_assert(CPT * D_NT == 64 * (D_BN / 8), "whole chunks per thread");
+    static_assert(64 * (D_BN + 4) * 4 <= D_NS * D_STB, "epilogue tile fits the ring");
+    u32x4 bpre[NPASS][CPT];
+    if (vec_b) {
+#pragma unroll
+        for (int pass = 0; pass < NPASS; ++pass)
+#pragma unroll
+            for (int j = 0; j < CPT; ++j) {
+                const int q = tid + j * D_NT;
+                const int row = m0 + pass * 64 + q / (D_BN / 8), col = n0 + (q % (D_BN / 8)) * 8;
+                bpre[pass][j] = u32x4{0, 0, 0, 0};
+                if (row < p.M && col + 8 <= p.N)
+                    bpre[pass][j] = *reinterpret_cast<const u32x4*>(Bb + (int64_t)row * p.sbias[1] + col);
+            }
+    }
+#pragma unroll
+    for (int pass = 0; pass < NPASS; ++pass) {
+        if (wm == pass * 64 / D_WTM) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const int i = (pass * 64 % D_WTM) / 16 + ii;
+#pragma unroll
+                for (int j = 0; j < D_FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        et[(ii * 16 + (lane / 16) * 4 + r) * E_LD + wn * D_WTN + j * 16 + lane % 16] = acc[i][j][r];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int q = tid + j * D_NT;
+            const int rl = q / (D_BN / 8), cc = (q % (D_BN / 8)) * 8;
+            const int row = m0 + pass * 64 + rl, col = n0 + cc;
+            if (row >= p.M || col >= p.N) continue;
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(et + rl * E_LD + cc);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(et + rl * E_LD + cc + 4);
+            const float a8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            const bool full = col + 8 <= p.N;
+            float bv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (p.has_bias) {
+                if (vec_b && full) {
+                    const u32x4 w = bpre[pass][j];
+                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        bv[2 * e] = elem<DT>::to_f32(__builtin_bit_cast(T, (uint16_t)(ww[e] & 0xffffu)));
+                        bv[2 * e + 1] = elem<DT>::to_f32(__builtin_bit_cast(T, (uint16_t)(ww[e] >> 16)));
+                    }
+                } else {
+                    const T* bp = Bb + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2];
+                    for (int e = 0; e < 8 && col + e < p.N; ++e) bv[e] = elem<DT>::to_f32(bp[(int64_t)e * p.sbias[2]]);
+                }
+            }
+            uint16_t h[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float v;
+                if (plain) {
+#pragma clang fp contract(off)
+                    v = a8[e] * p.alpha;
+                } else {
+                    v = epilogue(a8[e], p.alpha, p.has_bias, bv[e], p.beta, p.act);
+                }
+                h[e] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
+            }
+            T* cp = Cb + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2];
+            if (vec_c && full) {
+                *reinterpret_cast<u32x4*>(cp) = u32x4{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
+                                                      (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16)};
+            } else {
+                for (int e = 0; e < 8 && col + e < p.N; ++e) cp[(int64_t)e * p.sc[2]] = __builtin_bit_cast(T, h[e]);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+// Launches the kernel on BM x BN tiles for the operand layout (any split).
+template <int DT, int BM, int BN, int NS>
+void launch_dma_tile(GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s) {
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + BN - 1) / BN;
+    const dim3 grid(p.tiles_m * p.tiles_n, p.batch, p.split > 1 ? p.split : 1), block(DCfg<BM, BN>::NT);
+    if (a_kmajor && b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, true, BM, BN, NS>), grid, block, 0, s, p);
+    else if (a_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, false, BM, BN, NS>), grid, block, 0, s, p);
+    else if (b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, true, BM, BN, NS>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, false, BM, BN, NS>), grid, block, 0, s, p);
+}
+
+// The 128x128 instantiations live in gemm_dma128.hip, compiled with the MFMA
+// results in VGPRs (in the AGPR form hipcc rotates their accumulators through
+// AGPR copies inside the k loop); the 256x256 ones keep the default form,
+// in which they allocate cleanly while the VGPR form spills.
+void launch_dma128(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s, int stages);
+
+}  // namespace tvk
