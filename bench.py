@@ -37,6 +37,12 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 MEASURED_TRAFFIC = {
     "gemm16_dma_256x256": {"bytes": 1.764e9, "fetch_kib": 795667, "write_kib": 131072},
 }
+# the headline kernel under counters (profiles/mfma_ceiling_calibration.md)
+MEASURED_COUNTERS = {
+    "gemm16_dma_256x256": {"mfma_busy_pct": [70.6, 74.0], "shader_clock_ghz": [1.28, 1.70],
+                           "ceiling_loop_mfma_busy_pct": [77.6, 78.8], "ceiling_loop_clock_ghz": [1.90, 1.93],
+                           "source": "profiles/mfma_ceiling_calibration.md"},
+}
 
 
 def parse():
@@ -46,9 +52,10 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-extra", action="store_true", help="headline only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--profile-kernel", choices=["gemm", "skinny", "copy"],
+    p.add_argument("--profile-kernel", choices=["gemm", "skinny", "copy", "ceiling"],
                    help="launch only this kernel --steps times and exit (for rocprofv3 counter passes); "
-                        "'copy' is torch's copy of a 1 GiB buffer, the calibration for FETCH_SIZE/WRITE_SIZE")
+                        "'copy' is torch's copy of a 1 GiB buffer, the calibration for FETCH_SIZE/WRITE_SIZE; "
+                        "'ceiling' the random-operand MFMA loop of tvk_calibrate_mfma (two waves per SIMD)")
     return p.parse_args()
 
 
@@ -63,6 +70,11 @@ def profile_kernel(which, steps):
     lib = _abi.load()
     dev = torch.device("cuda:0")
     s = torch.cuda.current_stream(dev).cuda_stream
+    if which == "ceiling":
+        for _ in range(steps):
+            tf, _ = _abi.calibrate_mfma(0, 2, 40000)
+        print(f"ceiling: {steps} launches, last {tf:.1f} TFLOP/s", flush=True)
+        return
     if which == "copy":
         x = torch.ones((1 << 29,), dtype=torch.float16, device=dev)   # 1 GiB
         y = torch.empty_like(x)
@@ -175,6 +187,22 @@ def main():
         "algorithmic_bytes": 3 * n * n * 2,
         "avg_kernel_ms": round(ms, 5),
     }
+    # the power-limited ceiling on this box: the MFMA rate with random fp16
+    # operands (tvk_calibrate_mfma), at one and two waves per SIMD (the
+    # headline kernel runs two); the dense peak needs operands that barely toggle
+    ceiling = {}
+    _abi.calibrate_mfma(0, 2, 40000)   # the clock settles under the load first
+    for w in (1, 2, 4):
+        tf, _ = _abi.calibrate_mfma(0, w, 40000)
+        ceiling[f"waves_per_simd_{w}"] = round(tf, 1)
+    top = max(ceiling.values())
+    roofline["ceiling"] = {
+        "what": "v_mfma_f32_16x16x32_f16 loop, random fp16 operands, no memory traffic (tvk_calibrate_mfma)",
+        "unit": "TFLOP/s", **ceiling, "max": top,
+        "frac_of_ceiling": round(tflops / top, 4),
+    }
+    roofline["counters"] = MEASURED_COUNTERS.get(plan)
+    progress("MFMA ceiling done")
 
     extra = {}
     if not args.no_extra:

@@ -134,6 +134,16 @@ typedef struct {
 /* Replaces _device_properties (src/api/backend.cpp:104-124). */
 tvk_status tvk_device_properties(int device, tvk_device_props* out);
 
+/* Measurement aid with no counterpart in the reference: the sustained float16
+ * MFMA rate of `device` with random operands (v_mfma_f32_16x16x32_f16 over
+ * eight independent accumulators, `waves_per_simd` waves on every SIMD, 1-4),
+ * timed with HIP events over one launch of `iterations` steps on a stream of
+ * its own. The dense-peak figure assumes operands that barely toggle; with
+ * random data the part is power-limited, and this rate is the ceiling a GEMM's
+ * MFMA pipe can reach. *tflops and the launch's *ms on return. Allocates and
+ * synchronises: not for hot paths. */
+tvk_status tvk_calibrate_mfma(int device, int waves_per_simd, int iterations, double* tflops, double* ms);
+
 /* ------------------------------------------------------------------------- */
 /* Memory: a hipMalloc-backed caching allocator, stream-ordered on the        */
 /* library stream. Replaces VulkanAllocator + DeviceContext buffer pools      */

@@ -558,3 +558,16 @@ def test_operand_past_2gib_runs_in_row_blocks(gpu):
     assert_bit_exact(decode(to_np(c[torch.from_numpy(rows).to(DEV)].cpu()), dtype), ref, "row blocks past 2 GiB")
     del a, c
     torch.cuda.empty_cache()
+
+
+def test_calibrate_mfma_reports_a_plausible_rate(gpu):
+    # the random-operand MFMA loop: positive, below the dense peak, and more
+    # waves per SIMD never slower than one by much; bad arguments are rejected
+    rates = {w: gpu.calibrate_mfma(0, w, 4000)[0] for w in (1, 2, 4)}
+    for w, tf in rates.items():
+        assert 50.0 < tf < 2600.0, (w, tf)
+    assert rates[4] > 0.8 * rates[1]
+    with pytest.raises(gpu.TvkError):
+        gpu.calibrate_mfma(0, 0, 100)
+    with pytest.raises(gpu.TvkError):
+        gpu.calibrate_mfma(0, 2, 0)
