@@ -971,9 +971,7 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixe
                                           pl.kern == Kern::DMA128R8 ? 8 : 4);
                 if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_gemm: launch failed: ") + hipGetErrorString(e));
                 if (pl.split > 1) {
-                    const int64_t total = (int64_t)nb * d.M * d.N;
-                    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
-                    hipLaunchKernelGGL(gemm_split_reduce_kernel<DT>, dim3(blocks), dim3(256), 0, s, q);
+                    launch_split_reduce<DT>(q, s);
                 }
             }
             break;
@@ -993,9 +991,7 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixe
                     q.k_chunk = pl.k_chunk;
                     grid.z = pl.split;
                     launch_mfma<DT, 128, 128, 2>(pl, q, grid, s);
-                    const int64_t total = (int64_t)nb * d.M * d.N;
-                    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
-                    hipLaunchKernelGGL(gemm_split_reduce_kernel<DT>, dim3(blocks), dim3(256), 0, s, q);
+                    launch_split_reduce<DT>(q, s);
                 } else launch_mfma<DT, 128, 128, 2>(pl, q, grid, s);
             }
             break;

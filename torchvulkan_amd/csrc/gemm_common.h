@@ -153,7 +153,68 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmArgs p) {
     }
 }
 
+// The same sum, four consecutive outputs of one row a thread (N % 4 == 0, so
+// a group never straddles two rows): 16-byte loads from each partial plane,
+// added in split order, the epilogue inline, and one 8-byte store where the
+// output rows are contiguous and 8-byte aligned (VEC).
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(GemmArgs p) {
+    typedef typename elem<DT>::T T;
+    const int64_t mn = (int64_t)p.M * p.N;
+    const int64_t total = (int64_t)p.batch * mn;
+    const int64_t groups = total / 4;
+    T* c = reinterpret_cast<T*>(p.c);
+    const T* bias = reinterpret_cast<const T*>(p.bias);
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < groups; q += (int64_t)gridDim.x * 256) {
+        const int64_t idx = q * 4;
+        f32x4 v = *reinterpret_cast<const f32x4*>(p.part + idx);
+#pragma unroll 4
+        for (int z = 1; z < p.split; ++z) {
+#pragma clang fp contract(off)
+            const f32x4 w = *reinterpret_cast<const f32x4*>(p.part + (int64_t)z * total + idx);
+            v = f32x4{v[0] + w[0], v[1] + w[1], v[2] + w[2], v[3] + w[3]};
+        }
+        const int b = (int)(idx / mn);
+        const int64_t e = idx - (int64_t)b * mn;
+        const int row = (int)(e / p.N), col = (int)(e - (int64_t)row * p.N);
+        uint16_t h[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float bv = 0.0f;
+            if (p.has_bias)
+                bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)(col + r) * p.sbias[2]]);
+            h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(epilogue(v[r], p.alpha, p.has_bias, bv, p.beta, p.act)));
+        }
+        T* cp = c + (int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2];
+        if constexpr (VEC) {
+            *reinterpret_cast<u32x2*>(cp) = u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cp[(int64_t)r * p.sc[2]] = __builtin_bit_cast(T, h[r]);
+        }
+    }
+}
+
 }  // namespace
+
+// The split-K reduction for a float16/bfloat16 output: the four-wide kernel
+// where N is a multiple of 4 and the output fills at least 256 of its
+// workgroups (smaller outputs, such as the M <= 16 products', keep more
+// workgroups with one output a thread: measured 0.2 us faster there).
+template <int DT>
+inline void launch_split_reduce(const GemmArgs& q, hipStream_t s) {
+    const int64_t total = (int64_t)q.batch * q.M * q.N;
+    if (q.N % 4 == 0 && total >= 4 * 256 * 256) {
+        const bool vec = q.sc[2] == 1 && q.sc[1] % 4 == 0 && (q.batch == 1 || q.sc[0] % 4 == 0) &&
+                         (reinterpret_cast<uintptr_t>(q.c) & 7) == 0;
+        const unsigned blocks = (unsigned)std::min<int64_t>((total / 4 + 255) / 256, 8192);
+        if (vec) hipLaunchKernelGGL((gemm_split_reduce4_kernel<DT, true>), dim3(blocks), dim3(256), 0, s, q);
+        else hipLaunchKernelGGL((gemm_split_reduce4_kernel<DT, false>), dim3(blocks), dim3(256), 0, s, q);
+        return;
+    }
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+    hipLaunchKernelGGL(gemm_split_reduce_kernel<DT>, dim3(blocks), dim3(256), 0, s, q);
+}
 
 // Out-of-range buffer offset: the hardware returns zeros for it.
 constexpr uint32_t kOOB = 0x80000000u;

@@ -319,10 +319,8 @@ hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, 
         if (dtype == TVK_F16) hipLaunchKernelGGL(gemm_skinny_ring_kernel<TVK_F16>, grid, dim3(64 * SR_NW), 0, s, q);
         else hipLaunchKernelGGL(gemm_skinny_ring_kernel<TVK_BF16>, grid, dim3(64 * SR_NW), 0, s, q);
         if (q.split > 1) {
-            const int64_t total = (int64_t)p.batch * p.M * p.N;
-            const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
-            if (dtype == TVK_F16) hipLaunchKernelGGL(gemm_split_reduce_kernel<TVK_F16>, dim3(blocks), dim3(256), 0, s, q);
-            else hipLaunchKernelGGL(gemm_split_reduce_kernel<TVK_BF16>, dim3(blocks), dim3(256), 0, s, q);
+            if (dtype == TVK_F16) launch_split_reduce<TVK_F16>(q, s);
+            else launch_split_reduce<TVK_BF16>(q, s);
         }
         return hipGetLastError();
     }
