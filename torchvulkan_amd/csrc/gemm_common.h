@@ -199,12 +199,13 @@ __global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(GemmArgs p) {
 
 // The split-K reduction for a float16/bfloat16 output: the four-wide kernel
 // where N is a multiple of 4 and the output fills at least 256 of its
-// workgroups (smaller outputs, such as the M <= 16 products', keep more
-// workgroups with one output a thread: measured 0.2 us faster there).
+// workgroups or there are 8 or more partial planes (smaller outputs of few
+// planes, such as the M <= 16 products', keep more workgroups with one output
+// a thread: measured 0.2 us faster there).
 template <int DT>
 inline void launch_split_reduce(const GemmArgs& q, hipStream_t s) {
     const int64_t total = (int64_t)q.batch * q.M * q.N;
-    if (q.N % 4 == 0 && total >= 4 * 256 * 256) {
+    if (q.N % 4 == 0 && (total >= 4 * 256 * 256 || q.split >= 8)) {
         const bool vec = q.sc[2] == 1 && q.sc[1] % 4 == 0 && (q.batch == 1 || q.sc[0] % 4 == 0) &&
                          (reinterpret_cast<uintptr_t>(q.c) & 7) == 0;
         const unsigned blocks = (unsigned)std::min<int64_t>((total / 4 + 255) / 256, 8192);
