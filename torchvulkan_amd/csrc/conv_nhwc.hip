@@ -611,7 +611,22 @@ constexpr int HL_BN = 64;
 constexpr int HL_PX = 512;      // output pixels a tile
 constexpr int HL_A = 43008;     // halo pixels (TR + 2) * (W + 2) <= 660 (largest at W = 8 and 64) * 64 bytes, rounded up to 1 KB
 constexpr int HL_B = 9 * HL_BN * 64;
-constexpr int HL_STAGE = HL_A + HL_B;
+
+// The stride-1 kernel's two tile sizes: 512 output pixels on 8 waves with
+// two LDS stages (156 KB: one workgroup a CU), or 256 pixels on 4 waves with
+// one stage (61 KB: two workgroups a CU, which overlap each other's loads,
+// prologue and epilogue), for grids that would leave the CUs one 512-pixel
+// workgroup or less each.
+template <int PX>
+struct HaloCfg {
+    static constexpr int NT = PX, NW = PX / 64;
+    static constexpr int NS = PX == 512 ? 2 : 1;
+    static constexpr int A = PX == 512 ? HL_A : 25600;   // (TR + 2) * (W + 2) <= 396 pixels x 64 bytes at 256
+    static constexpr int STAGE = A + HL_B;
+    static constexpr int NQ = (36 + NW - 1) / NW;       // weight-row loads per wave
+    static_assert(PX == 512 || PX == 256, "tile");
+    static_assert(HL_BN * (PX + 8) * 2 <= NS * STAGE, "the epilogue tile fits the stages");
+};
 
 struct HaloArgs {
     const uint16_t* src;   // x (forward) or dy (grad input), NCHW [n][Cs][H][W]
@@ -650,9 +665,11 @@ __global__ __launch_bounds__(256) void weight_permute9_kernel(const uint16_t* w,
     }
 }
 
-template <int DT>
-__global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
-    __shared__ __attribute__((aligned(1024))) char lds[2 * HL_STAGE];
+template <int DT, int PX>
+__global__ __launch_bounds__(PX) void conv_halo_kernel(HaloArgs p) {
+    typedef HaloCfg<PX> G;
+    constexpr int NT = G::NT, NS = G::NS, STG = G::STAGE, A_BYTES = G::A, NQ = G::NQ, NW = G::NW;
+    __shared__ __attribute__((aligned(1024))) char lds[NS * STG];
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
     const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64), g = lane / 16;
     const int img = blockIdx.x / p.row_tiles, h0 = (blockIdx.x - img * p.row_tiles) * p.tr;
@@ -660,13 +677,13 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
     const int W = p.W, WP = W + 2, HWs = p.H * W;
     const int nk = p.Cs / 32;
 
-    // zero halo columns 0 and W + 1 of both stages (no load writes them)
-    for (int e = tid; e < (p.tr + 2) * 8; e += 512) {
+    // zero halo columns 0 and W + 1 of every stage (no load writes them)
+    for (int e = tid; e < (p.tr + 2) * 8; e += NT) {
         const int hr = e / 8, hc = (e / 4) % 2 ? W + 1 : 0, ch = e % 4;
         const int hp = hr * WP + hc;
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
-            *reinterpret_cast<u32x4*>(lds + st * HL_STAGE + hp * 64 + ch * 16) = u32x4{0u, 0u, 0u, 0u};
+        for (int st = 0; st < NS; ++st)
+            *reinterpret_cast<u32x4*>(lds + st * STG + hp * 64 + ch * 16) = u32x4{0u, 0u, 0u, 0u};
     }
 
     // halo gather: lane -> (column group wq, channel group cg, halo row hr)
@@ -693,25 +710,25 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
                 v[k] = (j % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
             }
             const int hp = hr * WP + wq * 8 + j + 1;
-            *reinterpret_cast<u32x4*>(lds + st * HL_STAGE + hp * 64 + ((cg ^ hl_swz(hp)) * 16)) = u32x4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<u32x4*>(lds + st * STG + hp * 64 + ((cg ^ hl_swz(hp)) * 16)) = u32x4{v[0], v[1], v[2], v[3]};
         }
     };
 
-    // weight rows: 36 DMA instructions of 16 rows a chunk, instruction q * 8 + wave
-    // (waves 0-3 issue 5, waves 4-7 issue 4); row = tap * 64 + channel
+    // weight rows: 36 DMA instructions of 16 rows a chunk, instruction q * NW + wave
+    // (at 8 waves, waves 0-3 issue 5 and waves 4-7 issue 4); row = tap * 64 + channel
     const i32x4 rb = v_rsrc(p.wt, p.wt_bytes);
-    int b_off[5];
+    int b_off[NQ];
 #pragma unroll
-    for (int q = 0; q < 5; ++q) {
-        const int row = min(q * 8 + wave, 35) * 16 + lane / 4;
+    for (int q = 0; q < NQ; ++q) {
+        const int row = min(q * NW + wave, 35) * 16 + lane / 4;
         const int t = row / HL_BN, co = min(n0 + row % HL_BN, p.N - 1);
         b_off[q] = ((co * 9 + t) * p.Cs + (((lane % 4) ^ hl_swz(row)) * 8)) * 2;
     }
     auto issue_b = [&](int kc, int st) {
-        const uint32_t base = lds0 + (uint32_t)(st * HL_STAGE + HL_A);
+        const uint32_t base = lds0 + (uint32_t)(st * STG + A_BYTES);
 #pragma unroll
-        for (int q = 0; q < 5; ++q)
-            if (q * 8 + wave < 36) v_dma16(rb, base + (uint32_t)((q * 8 + wave) * 1024), (uint32_t)(b_off[q] + kc * 64));
+        for (int q = 0; q < NQ; ++q)
+            if (q * NW + wave < 36) v_dma16(rb, base + (uint32_t)((q * NW + wave) * 1024), (uint32_t)(b_off[q] + kc * 64));
     };
 
     // A fragment rows: this wave's 64 pixels of the tile, 16 per fragment
@@ -728,20 +745,10 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    issue_b(0, 0);
-    load_a(0);
-    store_a(0);
-    v_wait<0>();
-    __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
-        const int cur = kc & 1;
-        if (kc + 1 < nk) {
-            issue_b(kc + 1, cur ^ 1);
-            load_a(kc + 1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        const char* sa = lds + cur * HL_STAGE;
-        const char* sb = sa + HL_A;
+    // the nine taps of one chunk from stage `cur`
+    auto compute = [&](int cur) {
+        const char* sa = lds + cur * STG;
+        const char* sb = sa + A_BYTES;
 #pragma unroll
         for (int t = 0; t < 9; ++t) {
             u32x4 fa[4], fb[4];
@@ -760,15 +767,44 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        if (kc + 1 < nk) store_a(cur ^ 1);
+    };
+
+    if constexpr (NS == 2) {
+        issue_b(0, 0);
+        load_a(0);
+        store_a(0);
         v_wait<0>();
+        __syncthreads();
+        for (int kc = 0; kc < nk; ++kc) {
+            const int cur = kc & 1;
+            if (kc + 1 < nk) {
+                issue_b(kc + 1, cur ^ 1);
+                load_a(kc + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            compute(cur);
+            __builtin_amdgcn_sched_barrier(0);
+            if (kc + 1 < nk) store_a(cur ^ 1);
+            v_wait<0>();
+            __syncthreads();
+        }
+    } else {
+        // one stage: each chunk loads after every wave has read the previous one
+        for (int kc = 0; kc < nk; ++kc) {
+            if (kc > 0) __syncthreads();
+            issue_b(kc, 0);
+            load_a(kc);
+            store_a(0);
+            v_wait<0>();
+            __syncthreads();
+            compute(0);
+        }
         __syncthreads();
     }
 
     // [channel][pixel] tile, then 16-byte stores along the output rows
     typedef typename elem<DT>::T T;
-    constexpr int LROW = HL_PX + 8;
+    constexpr int LROW = PX + 8;
     uint16_t* tile = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -793,8 +829,8 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(HaloArgs p) {
     }
     __syncthreads();
     uint16_t* out = static_cast<uint16_t*>(p.out);
-    for (int idx = tid; idx < HL_BN * (HL_PX / 8); idx += 512) {
-        const int ch = idx / (HL_PX / 8), px = (idx % (HL_PX / 8)) * 8;
+    for (int idx = tid; idx < HL_BN * (PX / 8); idx += NT) {
+        const int ch = idx / (PX / 8), px = (idx % (PX / 8)) * 8;
         const int r = px / W, c = px - r * W;
         if (n0 + ch >= p.N || h0 + r >= p.H) continue;
         *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + n0 + ch) * HWs + (int64_t)(h0 + r) * W + c) =
@@ -2399,7 +2435,11 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     int ipt_f = 1;
     const int fm2 = mode == 0 ? conv_halo_s2_fm(d, &ipt_f) : 0;
     p.ipt = ipt_f;
-    p.tr = fm2 ? (ipt_f > 1 ? H / 2 : 64 * fm2 / (W / 2)) : HL_PX / W;
+    // stride 1: 256-pixel tiles (two workgroups a CU) where 512-pixel ones would
+    // give the 256 CUs fewer than two workgroups each
+    const int64_t wg512 = d.n * ((H + HL_PX / W - 1) / (HL_PX / W)) * ((N + HL_BN - 1) / HL_BN);
+    const int px = !fm2 && wg512 < 512 ? 256 : HL_PX;
+    p.tr = fm2 ? (ipt_f > 1 ? H / 2 : 64 * fm2 / (W / 2)) : px / W;
     p.row_tiles = fm2 ? ((H / 2) + p.tr - 1) / p.tr : (H + p.tr - 1) / p.tr;
     p.wt_bytes = (int)wt_b;
     // forward: tap (a, b) reads source (h + a - 1, w + b - 1); grad input: (h + 1 - a, w + 1 - b);
@@ -2421,8 +2461,13 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
         if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
         return TVK_OK;
     }
-    if (d.dtype == TVK_F16) hipLaunchKernelGGL(conv_halo_kernel<TVK_F16>, grid, dim3(512), 0, s, p);
-    else hipLaunchKernelGGL(conv_halo_kernel<TVK_BF16>, grid, dim3(512), 0, s, p);
+    if (px == 256) {
+        if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_kernel<TVK_F16, 256>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((conv_halo_kernel<TVK_BF16, 256>), grid, dim3(256), 0, s, p);
+    } else {
+        if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_kernel<TVK_F16, 512>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((conv_halo_kernel<TVK_BF16, 512>), grid, dim3(512), 0, s, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
     return TVK_OK;
