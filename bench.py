@@ -327,6 +327,12 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c5_skinny_us"] = round(ms * 1e3, 2)
     out["c5_skinny_GBps"] = round(byts / (ms * 1e-3) / 1e9, 1)
     out["c5_skinny_pct_hbm"] = round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)
+    # the practical read ceiling on this box: a plain streaming read of the same
+    # B size over three rotating windows (tvk_calibrate_hbm)
+    rd_gbps, rd_ms = _abi.calibrate_hbm(0, K * N * 2, 60)
+    out["c5_read_ceiling"] = {"what": "plain streaming read, 512 workgroups, three rotating windows of B's size "
+                                      "(tvk_calibrate_hbm)", "GBps": round(rd_gbps, 1), "us_for_B": round(rd_ms * 1e3, 2),
+                              "skinny_frac_of_ceiling": round(byts / (ms * 1e-3) / 1e9 / rd_gbps, 4)}
     del bufs
 
     # ---- C4 ResNet convs: fwd + dgrad + wgrad of each layer, fp16, batch 128 -

@@ -144,6 +144,16 @@ tvk_status tvk_device_properties(int device, tvk_device_props* out);
  * synchronises: not for hot paths. */
 tvk_status tvk_calibrate_mfma(int device, int waves_per_simd, int iterations, double* tflops, double* ms);
 
+/* Measurement aid with no counterpart in the reference: the read bandwidth of
+ * a plain streaming kernel on `device` (512 workgroups, four 16-byte loads in
+ * flight a thread), the practical ceiling of a kernel that reads each byte of
+ * HBM once. Three windows of `window_bytes` (a multiple of 16, 4 KiB to 8 GiB)
+ * are read in rotation, one a launch; `iterations` launches are timed with HIP
+ * events on a stream of its own. *gbps (window bytes / launch time, 1e9 B/s)
+ * and the average launch *ms on return. Allocates 3 x window_bytes and
+ * synchronises: not for hot paths. */
+tvk_status tvk_calibrate_hbm(int device, size_t window_bytes, int iterations, double* gbps, double* ms);
+
 /* ------------------------------------------------------------------------- */
 /* Memory: a hipMalloc-backed caching allocator, stream-ordered on the        */
 /* library stream. Replaces VulkanAllocator + DeviceContext buffer pools      */

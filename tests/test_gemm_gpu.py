@@ -571,3 +571,15 @@ def test_calibrate_mfma_reports_a_plausible_rate(gpu):
         gpu.calibrate_mfma(0, 0, 100)
     with pytest.raises(gpu.TvkError):
         gpu.calibrate_mfma(0, 2, 0)
+
+
+def test_calibrate_hbm_reports_a_plausible_rate(gpu):
+    # the streaming read: positive and below the 8 TB/s HBM peak (windows of
+    # 128 MiB, three in rotation, so the 256 MB Infinity Cache cannot hold the
+    # next one); bad arguments are rejected
+    gbps, ms = gpu.calibrate_hbm(0, 128 << 20, 20)
+    assert 1000.0 < gbps < 8000.0 and ms > 0.0, (gbps, ms)
+    with pytest.raises(gpu.TvkError):
+        gpu.calibrate_hbm(0, 100, 10)
+    with pytest.raises(gpu.TvkError):
+        gpu.calibrate_hbm(0, 1 << 20, 0)

@@ -225,6 +225,7 @@ def load() -> C.CDLL:
         lib.tvk_attention_fwd.argtypes = [C.POINTER(AttentionDesc)]
         lib.tvk_attention_bwd.argtypes = [C.POINTER(AttentionBwdDesc)]
         lib.tvk_calibrate_mfma.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        lib.tvk_calibrate_hbm.argtypes = [C.c_int, C.c_size_t, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]
         for fn in _ALL_ENTRY_POINTS:
             getattr(lib, fn).restype = C.c_int if fn != "tvk_last_error" else C.c_char_p
         _lib = lib
@@ -243,6 +244,7 @@ _ALL_ENTRY_POINTS = (
     "tvk_attention_bwd", "tvk_gemm_noalloc", "tvk_event_create", "tvk_event_destroy", "tvk_event_record",
     "tvk_event_query", "tvk_event_synchronize", "tvk_event_elapsed", "tvk_stream_wait_event", "tvk_stream_query",
     "tvk_calibrate_mfma",
+    "tvk_calibrate_hbm",
 )
 
 
@@ -271,6 +273,13 @@ def _torch():
     import torch
 
     return torch
+
+
+def calibrate_hbm(device: int = 0, window_bytes: int = 4096 * 14336 * 2, iterations: int = 60) -> tuple[float, float]:
+    """(GB/s, ms per launch) of tvk_calibrate_hbm: a plain streaming read over three rotating windows."""
+    gb, ms = C.c_double(), C.c_double()
+    check(load().tvk_calibrate_hbm(device, window_bytes, iterations, C.byref(gb), C.byref(ms)))
+    return gb.value, ms.value
 
 
 def calibrate_mfma(device: int = 0, waves_per_simd: int = 2, iterations: int = 20000) -> tuple[float, float]:

@@ -1,4 +1,6 @@
-// Measurement aid: the sustained float16 MFMA rate of this device with data
+// Measurement aids (no counterpart in the reference).
+//
+// tvk_calibrate_mfma: the sustained float16 MFMA rate of this device with data
 // that toggles like a GEMM's (tvk_calibrate_mfma). The dense-peak figure
 // (2.5 PFLOP/s) assumes operands that barely toggle; with random operands the
 // part is power-limited, and that lower ceiling is what a GEMM's MFMA pipe
@@ -12,6 +14,16 @@
 // and stored at the end so nothing is removed. A grid of 256 CUs x 4 SIMDs x
 // `waves_per_simd` waves (`waves_per_simd` workgroups of 256 threads per CU),
 // timed with HIP events around the launch.
+//
+// tvk_calibrate_hbm: the read bandwidth a plain streaming kernel reaches, the
+// practical ceiling of an HBM-bound kernel that reads each byte once (the
+// M <= 16 GEMM streaming B). Three windows of `window_bytes` are read in
+// rotation, one a launch, so that with windows above ~90 MB the window read
+// next has left the 256 MB Infinity Cache since it was last read (the same
+// rotation the skinny-GEMM benchmark uses for its B operands). Kernel: 512
+// workgroups of 256 threads (two a CU), each thread four 16-byte loads in
+// flight, grid-strided; the loaded words are folded into one value that is
+// stored only if it matches a constant, so nothing is removed.
 #include "tvk_common.h"
 
 #include <string>
@@ -65,10 +77,70 @@ __global__ __launch_bounds__(256) void mfma_ceiling_kernel(int iterations, float
     out[id] = s;
 }
 
+__global__ __launch_bounds__(256) void hbm_read_kernel(const u32x4* p, int64_t n16, uint32_t* out) {
+    uint32_t acc = 0;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const u32x4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
+        acc ^= a.x ^ b.y ^ c.z ^ d.w;
+    }
+    for (; i < n16; i += stride) acc ^= p[i].x;
+    if (acc == 0x9e3779b9u) out[0] = acc;
+}
+
 }  // namespace
 }  // namespace tvk
 
 using namespace tvk;
+
+extern "C" tvk_status tvk_calibrate_hbm(int device, size_t window_bytes, int iterations, double* gbps, double* ms) {
+    if (!gbps || !ms) return fail(TVK_ERR_INVALID, "tvk_calibrate_hbm: gbps or ms is NULL");
+    if (window_bytes < 4096 || window_bytes % 16 != 0 || window_bytes > (size_t(8) << 30) || iterations < 1)
+        return fail(TVK_ERR_INVALID, "tvk_calibrate_hbm: window_bytes must be a multiple of 16 in [4 KiB, 8 GiB] and iterations positive");
+    int cur = 0;
+    TVK_HIP_CHECK(hipGetDevice(&cur));
+    TVK_HIP_CHECK(hipSetDevice(device));
+    tvk_status st = TVK_OK;
+    char* buf = nullptr;
+    uint32_t* out = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipStream_t s = nullptr;
+    do {
+        if (hipMalloc(&buf, 3 * window_bytes) != hipSuccess || hipMalloc(&out, 16) != hipSuccess) {
+            st = fail(TVK_ERR_OOM, "tvk_calibrate_hbm: out of memory");
+            break;
+        }
+        if (hipStreamCreate(&s) != hipSuccess || hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+            st = fail(TVK_ERR_DEVICE, "tvk_calibrate_hbm: stream or event creation failed");
+            break;
+        }
+        if (hipMemsetAsync(buf, 0x3c, 3 * window_bytes, s) != hipSuccess) { st = fail(TVK_ERR_DEVICE, "tvk_calibrate_hbm: fill failed"); break; }
+        const int64_t n16 = (int64_t)(window_bytes / 16);
+        auto window = [&](int i) { return reinterpret_cast<const u32x4*>(buf + (size_t)(i % 3) * window_bytes); };
+        for (int i = 0; i < 6; ++i) hipLaunchKernelGGL(hbm_read_kernel, dim3(512), dim3(256), 0, s, window(i), n16, out);   // warm-up
+        if (hipEventRecord(e0, s) != hipSuccess) { st = fail(TVK_ERR_DEVICE, "tvk_calibrate_hbm: event record failed"); break; }
+        for (int i = 0; i < iterations; ++i) hipLaunchKernelGGL(hbm_read_kernel, dim3(512), dim3(256), 0, s, window(i), n16, out);
+        if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) {
+            st = fail(TVK_ERR_DEVICE, std::string("tvk_calibrate_hbm: ") + hipGetErrorString(hipGetLastError()));
+            break;
+        }
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, e0, e1) != hipSuccess) { st = fail(TVK_ERR_DEVICE, "tvk_calibrate_hbm: elapsed time failed"); break; }
+        *ms = t / iterations;
+        *gbps = (double)window_bytes / ((double)*ms * 1e-3) / 1e9;
+    } while (false);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) {
+        (void)hipStreamSynchronize(s);
+        (void)hipStreamDestroy(s);
+    }
+    if (out) (void)hipFree(out);
+    if (buf) (void)hipFree(buf);
+    (void)hipSetDevice(cur);
+    return st;
+}
 
 extern "C" tvk_status tvk_calibrate_mfma(int device, int waves_per_simd, int iterations, double* tflops, double* ms) {
     if (!tflops || !ms) return fail(TVK_ERR_INVALID, "tvk_calibrate_mfma: tflops or ms is NULL");

@@ -197,11 +197,19 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     db.init(p.sb[2], p.sb[1], n0, p.N, wave, lane);
     // split-K (grid z): this workgroup's k range starts at stage kt0
     const int kt0 = p.split > 1 ? (int)blockIdx.z * (p.k_chunk / D_BK) : 0;
+    const int nk = (p.split > 1 ? min(p.k_chunk, p.K - (int)blockIdx.z * p.k_chunk) : p.K) / D_BK;
+    // The ring issues the same loads every stage, also for the NS stages past
+    // this workgroup's k range (the waits count on them). Those go through
+    // resources of no records: out of range, so they return zeros without
+    // reading memory (past the end of K, a k-contiguous operand's addresses
+    // run into its next row, and a split's into the next split's range).
+    const i32x4 ra_none = dma_rsrc(A, 0), rb_none = dma_rsrc(B, 0);
     auto dma_one = [&](int kt, int q) {   // q-th load (of D_DPS) of this wave for stage kt
         const uint32_t slot = lds0 + (uint32_t)((kt % D_NS) * D_STB);
         const uint32_t kg = (uint32_t)(kt0 + kt);
-        if (q < G::DA) dma16(ra, slot + (uint32_t)((wave * G::DA + q) * 1024), da.off[q] + kg * da.kstep);
-        else dma16(rb, slot + D_OPB + (uint32_t)((wave * G::DB + q - G::DA) * 1024), db.off[q - G::DA] + kg * db.kstep);
+        const bool live = kt < nk;
+        if (q < G::DA) dma16(live ? ra : ra_none, slot + (uint32_t)((wave * G::DA + q) * 1024), da.off[q] + kg * da.kstep);
+        else dma16(live ? rb : rb_none, slot + D_OPB + (uint32_t)((wave * G::DB + q - G::DA) * 1024), db.off[q - G::DA] + kg * db.kstep);
     };
 
     f32x4 acc[D_FM][D_FN];
@@ -211,7 +219,6 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
         for (int j = 0; j < D_FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     u32x4 fa[2][D_FM], fb[2][D_FN];
-    const int nk = (p.split > 1 ? min(p.k_chunk, p.K - (int)blockIdx.z * p.k_chunk) : p.K) / D_BK;
     // prologue: stages 0..3 in flight; stage 0's fragments in registers once it
     // has landed, stage 1 landed before the loop reads it
 #pragma unroll
@@ -256,8 +263,8 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
         body(kt + 1, std::integral_constant<int, 1>{});
     }
     if (kt < nk) body(kt, std::integral_constant<int, 0>{});
-    // loads of stages past the end are still in flight: drain them before
-    // the workgroup's LDS can be handed to another
+    // the (empty) loads of stages past the end are still in flight: drain
+    // them before the workgroup's LDS can be handed to another
     wait_vmcnt<0>();
 
     if (p.split > 1) {
