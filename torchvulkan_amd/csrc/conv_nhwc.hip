@@ -599,7 +599,7 @@ void border_for(int lo, int step, int count, int tap_lo, int tap_hi, int size, i
 // other's MFMAs). Per
 // 32-channel k chunk it stages the (TR + 2) x (W + 2) source halo in LDS
 // ([pixel][32 channels], 64-byte rows, the 16-byte chunks XOR-swizzled by
-// (pixel >> 2) & 3) and the permuted weight's [9 taps][64 channels][32] rows,
+// hl_swz(pixel)) and the permuted weight's [9 taps][64 channels][32] rows,
 // then all 9 taps read their A fragments from the halo at a shifted pixel:
 // each source element crosses from L2 once per chunk instead of once per tap.
 // The halo is gathered into registers (a lane: 8 channels x 8 pixels of one
@@ -640,7 +640,13 @@ struct HaloArgs {
     int ipt, nimg;         // stride-2 grad input: images a tile, batch size
 };
 
-__device__ inline int hl_swz(int row) { return (row >> 2) & 3; }
+// 16-byte chunk swizzle of the 64-byte LDS rows (halo pixels and weight rows):
+// chunk c of row r sits at c ^ hl_swz(r). A fragment read takes 16
+// consecutive rows, chunk g = lane / 16; with gfx950's ds_read_b128 lane
+// groups ({0-3, 12-15} of one 16 and {4-11} of the other, served together)
+// flipping bit 1 of the chunk every 4 rows spreads every group over the 64
+// banks for any first row, where a 4-row rotation left 2-way conflicts.
+__device__ inline int hl_swz(int row) { return ((row >> 2) & 1) * 2; }
 
 // 3x3 weight w[co][c][9] -> forward wout[co][t][c] or grad input
 // wout[c][t][co], the reduced channel count a multiple of 8: a thread gathers
