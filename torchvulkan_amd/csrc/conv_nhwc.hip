@@ -509,8 +509,19 @@ __global__ __launch_bounds__(256) void wgrad_ring_reduce_kernel(const float* par
     const int g = threadIdx.x / L, l = threadIdx.x % L;
     const int e0 = blockIdx.x * E + l * 4;
     f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (e0 < total)
-        for (int s = g; s < split; s += sg) acc += *reinterpret_cast<const f32x4*>(part + (int64_t)s * total + e0);
+    if (e0 < total) {
+        // eight planes' loads in flight before their adds (still in split order)
+        const float* src = part + e0;
+        int s = g;
+        for (; s + 7 * sg < split; s += 8 * sg) {
+            f32x4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)(s + u * sg) * total);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; s < split; s += sg) acc += *reinterpret_cast<const f32x4*>(src + (int64_t)s * total);
+    }
     *reinterpret_cast<f32x4*>(red + g * E + l * 4) = acc;
     __syncthreads();
     for (int k = threadIdx.x; k < E; k += 256) {

@@ -367,8 +367,18 @@ __global__ __launch_bounds__(256) void small_split_reduce_kernel(const float* pa
     const int L = 256 / sg, q = threadIdx.x / L, l = threadIdx.x % L;
     const int e = blockIdx.x * L + l;
     float v = 0.0f;
-    if (e < count)
-        for (int s = q; s < split; s += sg) v += part[(int64_t)s * count + e];
+    if (e < count) {
+        // eight planes' loads in flight before their adds (still in split order)
+        int s = q;
+        for (; s + 7 * sg < split; s += 8 * sg) {
+            float w[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[u] = part[(int64_t)(s + u * sg) * count + e];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += w[u];
+        }
+        for (; s < split; s += sg) v += part[(int64_t)s * count + e];
+    }
     red[threadIdx.x] = v;
     __syncthreads();
     if (threadIdx.x < L && e < count) {

@@ -148,7 +148,16 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmArgs p) {
         const int b = (int)(idx / mn);
         const int64_t e = idx - (int64_t)b * mn;
         float v = p.part[idx];
-        for (int z = 1; z < p.split; ++z) v += p.part[(int64_t)z * total + idx];
+        // eight planes' loads in flight before their adds (still in split order)
+        int z = 1;
+        for (; z + 7 < p.split; z += 8) {
+            float w[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[u] = p.part[(int64_t)(z + u) * total + idx];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += w[u];
+        }
+        for (; z < p.split; ++z) v += p.part[(int64_t)z * total + idx];
         store_out<DT>(p, b, (int)(e / p.N), (int)(e % p.N), v);
     }
 }
@@ -168,8 +177,17 @@ __global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(GemmArgs p) {
     for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < groups; q += (int64_t)gridDim.x * 256) {
         const int64_t idx = q * 4;
         f32x4 v = *reinterpret_cast<const f32x4*>(p.part + idx);
-#pragma unroll 4
-        for (int z = 1; z < p.split; ++z) {
+        // eight planes' loads in flight before their adds (still in split order)
+        int z = 1;
+        for (; z + 7 < p.split; z += 8) {
+#pragma clang fp contract(off)
+            f32x4 w[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[u] = *reinterpret_cast<const f32x4*>(p.part + (int64_t)(z + u) * total + idx);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v = f32x4{v[0] + w[u][0], v[1] + w[u][1], v[2] + w[u][2], v[3] + w[u][3]};
+        }
+        for (; z < p.split; ++z) {
 #pragma clang fp contract(off)
             const f32x4 w = *reinterpret_cast<const f32x4*>(p.part + (int64_t)z * total + idx);
             v = f32x4{v[0] + w[0], v[1] + w[1], v[2] + w[2], v[3] + w[3]};
