@@ -160,6 +160,12 @@ SMALL_CASES = [
     dict(n=2, cin=3, cout=64, k=3, s=1, p=2, hw=14),
     dict(n=1, cin=3, cout=32, k=3, s=1, p=1, hw=13, dil=2),
     dict(n=1, cin=3, cout=16, k=3, s=1, p=1, hw=200),
+    # the MFMA grad-input kernel (64 output channels, padding 1, W 8/16/32/64):
+    # 1-3 input channels, heights that end in a partial row tile
+    dict(n=3, cin=1, cout=64, k=3, s=1, p=1, hw=(20, 8)),
+    dict(n=2, cin=2, cout=64, k=3, s=1, p=1, hw=(7, 64)),
+    dict(n=2, cin=3, cout=64, k=3, s=1, p=1, hw=(12, 32)),
+    dict(n=2, cin=3, cout=64, k=3, s=1, p=1, hw=(16, 16)),
 ]
 
 

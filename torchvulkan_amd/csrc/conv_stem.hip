@@ -208,15 +208,50 @@ __global__ __launch_bounds__(256) void conv_small_fwd_rows_kernel(SmallArgs p) {
             ktab[k] = -1;
         }
     }
-    for (int e = tid; e < 64 * 32; e += 256) {
-        const int co = e / 32, k = e % 32;
-        ws[co * WROW + k] = (n0 + co < p.cout && k < p.K) ? w[(n0 + co) * p.K + k] : (uint16_t)0;
+    // every load of a phase is issued before its LDS stores (a loop that
+    // stored each load as it arrived waited on every load in turn)
+    {
+        uint16_t wv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = tid + i * 256, co = e / 32, k = e % 32;
+            const bool ok = n0 + co < p.cout && k < p.K;
+            const uint16_t v = w[ok ? (n0 + co) * p.K + k : 0];
+            wv[i] = ok ? v : (uint16_t)0;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = tid + i * 256;
+            ws[(e / 32) * WROW + e % 32] = wv[i];
+        }
     }
-    for (int e = tid; e < p.cin * HR * RP; e += 256) {
-        const int col = e % RP, rest = e / RP;
-        const int hr = rest % HR, c = rest / HR;
-        const int ih = h0 - p.ph + hr, iw = col - 8;
-        xs[e] = ((unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W) ? x[((int64_t)c * p.H + ih) * p.W + iw] : (uint16_t)0;
+    const int nx = p.cin * HR * RP;
+    for (int e0 = 0; e0 < nx; e0 += 8 * 256) {
+        uint16_t xv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = e0 + tid + i * 256;
+            const int col = e % RP, rest = e / RP;
+            const int hr = rest % HR, c = rest / HR;
+            const int ih = h0 - p.ph + hr, iw = col - 8;
+            const bool ok = e < nx && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
+            const uint16_t v = x[ok ? ((int64_t)c * p.H + ih) * p.W + iw : 0];
+            xv[i] = ok ? v : (uint16_t)0;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = e0 + tid + i * 256;
+            if (e < nx) xs[e] = xv[i];
+        }
+    }
+    float bvs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (p.has_bias) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int co = n0 + j * 16 + sl;
+            const float v = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[min(co, p.cout - 1)]);
+            bvs[j] = co < p.cout ? v : 0.0f;
+        }
     }
     __syncthreads();
     int ko[8];
@@ -240,8 +275,7 @@ __global__ __launch_bounds__(256) void conv_small_fwd_rows_kernel(SmallArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int ch = j * 16 + sl;
-        float bv = 0.0f;
-        if (p.has_bias && n0 + ch < p.cout) bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[n0 + ch]);
+        const float bv = bvs[j];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             uint16_t h[4];
@@ -271,16 +305,19 @@ __global__ __launch_bounds__(256) void conv_small_fwd_rows_kernel(SmallArgs p) {
 }
 
 // Grad weight: workgroup b sums pixel chunks b, b + split, ... of 512 pixels
-// (4 waves x 4 steps of 32, each wave its own 128 pixels), for 64 output
-// channels (grid y) x the 32 (zero-padded) k. Ho * Wo % 8 == 0 so a lane's 8
-// pixels lie in one image and start 16-byte aligned.
-template <int DT>
+// (4 waves x 4 steps of 32, each wave its own 128 pixels), for 16 * NI (64)
+// output channels (grid y) x the 32 (zero-padded) k. Ho * Wo % 8 == 0 so a
+// lane's 8 pixels lie in one image and start 16-byte aligned. (32-channel
+// blocks, twice the workgroups, measured slower on the C4 stem: 12.8 against
+// 10.7 us.)
+template <int DT, int NI = 4>
 __global__ __launch_bounds__(256) void conv_small_wgrad_kernel(SmallArgs p) {
     typedef typename elem<DT>::T T;
+    constexpr int CB = 16 * NI;
     __shared__ int ktab[3][32];
-    __shared__ float red[4][64 * 33];
+    __shared__ float red[4][CB * 33];
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16;
-    const int n0 = blockIdx.y * 64;
+    const int n0 = blockIdx.y * CB;
     const int HW = p.H * p.W, HWo = p.Ho * p.Wo, P = p.n * HWo;
     fill_ktab(p, ktab);
     __syncthreads();
@@ -294,20 +331,20 @@ __global__ __launch_bounds__(256) void conv_small_wgrad_kernel(SmallArgs p) {
     }
     const uint16_t* x = static_cast<const uint16_t*>(p.x);
     const uint16_t* dy = static_cast<const uint16_t*>(p.dy);
-    f32x4 acc[4][2];
+    f32x4 acc[NI][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int base = blockIdx.x * 512; base < P; base += p.split * 512) {
-        u32x4 fa[4][4], fb[4][2];
+        u32x4 fa[4][NI], fb[4][2];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int p0 = base + wave * 128 + s * 32 + g * 8;
             const bool live = p0 < P;   // P % 8 == 0: a lane's 8 pixels are all in or all out
             const int img = live ? p0 / HWo : 0, o = live ? p0 - img * HWo : 0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < NI; ++i) {
                 const int co = min(n0 + i * 16 + lane % 16, p.cout - 1);
                 fa[s][i] = live ? *reinterpret_cast<const u32x4*>(dy + ((int64_t)img * p.cout + co) * HWo + o)
                                 : u32x4{0u, 0u, 0u, 0u};
@@ -336,19 +373,19 @@ __global__ __launch_bounds__(256) void conv_small_wgrad_kernel(SmallArgs p) {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < NI; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j] = mfma16<DT>(fa[s][i], fb[s][j], acc[i][j]);
     }
     // the 4 waves' sums, added in wave order
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[wave][(i * 16 + g * 4 + r) * 33 + j * 16 + lane % 16] = acc[i][j][r];
     __syncthreads();
-    for (int q = tid; q < 64 * 32; q += 256) {
+    for (int q = tid; q < CB * 32; q += 256) {
         const int cl = q / 32, k = q % 32, co = n0 + cl;
         if (co >= p.cout || k >= p.K) continue;
         const int at = cl * 33 + k;
@@ -391,8 +428,14 @@ __global__ __launch_bounds__(256) void small_split_reduce_kernel(const float* pa
 // Grad input, stride 1, 3x3 taps, dilation 1: workgroup = TR input rows (all
 // W columns) of one image; threads = pixels. Output-channel pairs are staged
 // S_CP at a time as a halo of dy, [pair][HR][HC] dwords (channel 2q in the low
-// half), zero outside dy; the weights as [pair][tap][4 input channels] dwords.
-template <int DT>
+// half, zero outside dy); the weights as [pair][tap][4 input channels] dwords.
+// Every global load of a phase is issued before its LDS stores (a loop that
+// stored each load as it arrived waited on every load in turn), and each halo
+// element is written exactly once per chunk (rows outside dy and the columns
+// left and right of it as zeros), so no separate clearing pass is needed.
+constexpr int S_DT = 4;   // grad input: dy copy tasks a thread per batch of loads
+
+template <int DT, int NC>
 __global__ __launch_bounds__(256) void conv_small_dgrad_kernel(SmallArgs p) {
     typedef typename elem<DT>::T T;
     __shared__ __attribute__((aligned(16))) uint32_t dyh[S_CP * 768];
@@ -405,38 +448,79 @@ __global__ __launch_bounds__(256) void conv_small_dgrad_kernel(SmallArgs p) {
     const uint16_t* dy = static_cast<const uint16_t*>(p.dy);
     const int HWo = p.Ho * p.Wo;
     // weight pairs: wq[(q * 9 + t) * 4 + c] = W[2q][c][t] | W[2q+1][c][t] << 16
-    for (int e = tid; e < p.ncp * 36; e += 256) {
-        const int c = e % 4, t = (e / 4) % 9, q = e / 36;
-        uint32_t lo = 0, hi = 0;
-        if (c < p.cin) {
-            lo = w[((2 * q) * p.cin + c) * 9 + t];
-            if (2 * q + 1 < p.cout) hi = w[((2 * q + 1) * p.cin + c) * 9 + t];
+    const int nw = p.ncp * 36;
+    for (int e0 = 0; e0 < nw; e0 += 8 * 256) {
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = e0 + tid + i * 256;
+            const int c = e % 4, t = (e / 4) % 9, q = e / 36;
+            const bool ok = e < nw && c < p.cin, okh = ok && 2 * q + 1 < p.cout;
+            const uint16_t l = w[ok ? ((2 * q) * p.cin + c) * 9 + t : 0];
+            const uint16_t h = w[okh ? ((2 * q + 1) * p.cin + c) * 9 + t : 0];
+            lo[i] = ok ? l : 0u;
+            hi[i] = okh ? h : 0u;
         }
-        wq[e] = lo | (hi << 16);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = e0 + tid + i * 256;
+            if (e < nw) wq[e] = lo[i] | (hi[i] << 16);
+        }
     }
     const int tr = tid / p.W, iw = tid - tr * p.W;
     const bool live = tr < p.tr && h0 + tr < p.H;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int nq = p.Wo / 8;   // 16-byte chunks per dy row
-    for (int q0 = 0; q0 < p.ncp; q0 += S_CP) {
-        // zero the halo, then copy the dy rows that exist
-        for (int e = tid; e < S_CP * HRC / 4; e += 256) reinterpret_cast<u32x4*>(dyh)[e] = u32x4{0u, 0u, 0u, 0u};
-        __syncthreads();
-        for (int e = tid; e < S_CP * HR * nq; e += 256) {
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
+    const int nq = p.Wo / 8;                              // 16-byte chunks per dy row
+    const int left = max(0, -c_lo), right = max(0, HC - (p.Wo - c_lo));   // zero columns either side of dy
+    const int ncopy = S_CP * HR * nq, nedge = S_CP * HR;
+    u32x4 lo[S_DT], hi[S_DT];
+    // loads of copy tasks e0 + tid + i * 256 of the chunk at pair q0
+    auto load = [&](int q0, int e0) {
+#pragma unroll
+        for (int i = 0; i < S_DT; ++i) {
+            const int e = e0 + tid + i * 256;
             const int cq = e % nq, rest = e / nq, hr = rest % HR, cp = rest / HR;
             const int co = 2 * (q0 + cp), oh = r_lo + hr;
-            if (co >= p.cout || (unsigned)oh >= (unsigned)p.Ho) continue;
+            const bool ok = e < ncopy && co < p.cout && (unsigned)oh < (unsigned)p.Ho;
+            const bool okh = ok && co + 1 < p.cout;
             const int64_t off = ((int64_t)img * p.cout + co) * HWo + oh * p.Wo + cq * 8;
-            const u32x4 lo = *reinterpret_cast<const u32x4*>(dy + off);
-            const u32x4 hi = co + 1 < p.cout ? *reinterpret_cast<const u32x4*>(dy + off + HWo) : u32x4{0u, 0u, 0u, 0u};
+            lo[i] = *reinterpret_cast<const u32x4*>(dy + (ok ? off : 0));
+            hi[i] = *reinterpret_cast<const u32x4*>(dy + (okh ? off + HWo : 0));
+            if (!ok) lo[i] = u32x4{0u, 0u, 0u, 0u};
+            if (!okh) hi[i] = u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto store = [&](int e0) {
+#pragma unroll
+        for (int i = 0; i < S_DT; ++i) {
+            const int e = e0 + tid + i * 256;
+            if (e >= ncopy) break;
+            const int cq = e % nq, rest = e / nq, hr = rest % HR, cp = rest / HR;
             uint32_t* row = dyh + cp * HRC + hr * HC;
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 const int hc = cq * 8 + k - c_lo;
-                const uint32_t l = lo[k / 2], h = hi[k / 2];
+                const uint32_t l = lo[i][k / 2], h = hi[i][k / 2];
                 const uint32_t v = (k % 2 == 0) ? ((l & 0xffffu) | (h << 16)) : ((l >> 16) | (h & 0xffff0000u));
                 if ((unsigned)hc < (unsigned)HC) row[hc] = v;
             }
+        }
+    };
+    for (int q0 = 0; q0 < p.ncp; q0 += S_CP) {
+        // halo rows of 8 dy columns (rows outside dy as zeros); keeping the
+        // next chunk's loads in flight during this one's products measured
+        // slower (16.4 -> 18.3 us on the C4 stem)
+        for (int e0 = 0; e0 < ncopy; e0 += S_DT * 256) {
+            load(q0, e0);
+            store(e0);
+        }
+        // the columns left and right of dy
+        for (int e = tid; e < nedge; e += 256) {
+            uint32_t* row = dyh + (e / HR) * HRC + (e % HR) * HC;
+            for (int k = 0; k < left; ++k) row[k] = 0u;
+            for (int k = HC - right; k < HC; ++k) row[k] = 0u;
         }
         __syncthreads();
         if (live) {
@@ -455,7 +539,7 @@ __global__ __launch_bounds__(256) void conv_small_dgrad_kernel(SmallArgs p) {
                         // of an indexed vector element in this unrolled loop
                         const uint32_t wc[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
-                        for (int c = 0; c < 4; ++c) {
+                        for (int c = 0; c < NC; ++c) {
                             if constexpr (DT == TVK_F16)
                                 acc[c] = __builtin_amdgcn_fdot2(__builtin_bit_cast(_Float16 __attribute__((ext_vector_type(2))), v),
                                                                 __builtin_bit_cast(_Float16 __attribute__((ext_vector_type(2))), wc[c]),
@@ -474,8 +558,140 @@ __global__ __launch_bounds__(256) void conv_small_dgrad_kernel(SmallArgs p) {
     T* dx = static_cast<T*>(p.out);
     const int HWi = p.H * p.W;
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-        if (c < p.cin) dx[((int64_t)img * p.cin + c) * HWi + (h0 + tr) * p.W + iw] = elem<DT>::from_f32(acc[c]);
+    for (int c = 0; c < NC; ++c) dx[((int64_t)img * p.cin + c) * HWi + (h0 + tr) * p.W + iw] = elem<DT>::from_f32(acc[c]);
+}
+
+// Grad input, stride 1, 3x3, padding 1, 64 output channels, at most 16 input
+// channels, as a product on the MFMA pipe: dx[c][p] = sum over k = (tap,
+// output channel) of W[k][c] * dy[k][p + shift(tap)], one 16x16x32 MFMA per
+// 16 pixels and 32 k (the c rows past c_in are zero). A workgroup takes
+// TR = 256 / W whole input rows of one image. The dy halo [TR + 2][W + 2]
+// [64 channels] is staged once in LDS (NCHW rows loaded 16 bytes at a time and
+// transposed in registers, 128-byte pixel rows); each pixel-fragment read is
+// one ds_read_b128. The 18 A fragments (the weights of all k) stay in
+// registers for the whole tile. Lane column j of a fragment takes pixel
+// pi(j): {0-3} -> 0-3, {4-11} -> 8-15, {12-15} -> 4-7, so the 16 lanes that
+// gfx950 serves together (j {0-3, 12-15} of one lane group and j {4-11} of
+// the next) read pixels 0-7 at one chunk and 8-15 at the next; with the
+// chunk XOR 2 * ((pixel >> 1) & 3) they cover the 64 banks for any shift.
+constexpr int SM_HALO = 396 * 128;   // (TR + 2) * (W + 2) pixels <= 396 (W = 64) x 128 bytes
+
+__device__ inline int sm_swz(int hp) { return ((hp >> 1) & 3) * 2; }
+
+template <int DT>
+__global__ __launch_bounds__(256) void conv_small_dgrad_mfma_kernel(SmallArgs p) {
+    typedef typename elem<DT>::T T;
+    __shared__ __attribute__((aligned(16))) char halo[SM_HALO];
+    __shared__ __attribute__((aligned(16))) uint16_t ws[64 * 16 * 9];
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, j = lane % 16;
+    const int W = p.W, TR = 256 / W, HC = W + 2, HR = TR + 2;
+    const int img = blockIdx.x / p.row_blocks, h0 = (blockIdx.x - img * p.row_blocks) * TR;
+    const uint16_t* w = static_cast<const uint16_t*>(p.w);
+    const uint16_t* dy = static_cast<const uint16_t*>(p.dy);
+    const int HW = p.H * W;
+
+    // weights [64][cin][9] as they are, eight loads a thread in flight
+    const int nw = 64 * p.cin * 9;
+    for (int e0 = 0; e0 < nw; e0 += 8 * 256) {
+        uint16_t v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = e0 + tid + i * 256;
+            v[i] = w[e < nw ? e : 0];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = e0 + tid + i * 256;
+            if (e < nw) ws[e] = v[i];
+        }
+    }
+
+    // dy halo: task = (8 columns, 8 channels, halo row): eight 16-byte loads
+    // (one per channel), an 8x8 transpose, eight 16-byte stores (one per
+    // pixel). (Rows before channels, so that a load instruction reads a
+    // channel's rows as one run, measured the same.)
+    const int ncq = W / 8, ntask = HR * ncq * 8;
+    u32x4 ld[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int e = tid + u * 256;
+        const int cq = e % ncq, rest = e / ncq, cg = rest % 8, hr = rest / 8;
+        const int oh = h0 - 1 + hr;
+        const bool ok = e < ntask && (unsigned)oh < (unsigned)p.H;
+        const int64_t off = ((int64_t)img * 64 + cg * 8) * HW + (int64_t)(ok ? oh : 0) * W + cq * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            ld[u][i] = ok ? *reinterpret_cast<const u32x4*>(dy + off + (int64_t)i * HW) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int e = tid + u * 256;
+        if (e >= ntask) break;
+        const int cq = e % ncq, rest = e / ncq, cg = rest % 8, hr = rest / 8;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            uint32_t v[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const uint32_t lo = ld[u][2 * m][k / 2], hi = ld[u][2 * m + 1][k / 2];
+                v[m] = (k % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+            }
+            const int hp = hr * HC + cq * 8 + k + 1;
+            *reinterpret_cast<u32x4*>(halo + hp * 128 + ((cg ^ sm_swz(hp)) * 16)) = u32x4{v[0], v[1], v[2], v[3]};
+        }
+    }
+    // halo columns 0 and W + 1 (outside dy) are zero
+    for (int e = tid; e < HR * 2 * 8; e += 256) {
+        const int hp = (e / 16) * HC + ((e / 8) % 2 ? W + 1 : 0);
+        *reinterpret_cast<u32x4*>(halo + hp * 128 + (e % 8) * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+
+    // A fragments: k step s = tap * 2 + cb; lane: c = j, channels cb * 32 + 8g .. + 7
+    u32x4 af[18];
+#pragma unroll
+    for (int s = 0; s < 18; ++s) {
+        const int t = s / 2, cb = s % 2;
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int co = cb * 32 + g * 8 + e;
+            h[e] = j < p.cin ? ws[(co * p.cin + j) * 9 + t] : 0u;
+        }
+        af[s] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    }
+    const int pj = j < 4 ? j : (j < 12 ? j + 4 : j - 8);
+    int hb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = wave * 64 + i * 16 + pj, r = q / W, col = q - r * W;
+        hb[i] = (r + 2) * HC + col + 2;   // halo pixel of tap (0, 0): input (r, col) meets dy (r + 1 - a, col + 1 - b)
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 18; ++s) {
+        const int t = s / 2, cb = s % 2, a = t / 3, b = t % 3;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int hp = hb[i] - a * HC - b;
+            const u32x4 bf = *reinterpret_cast<const u32x4*>(halo + hp * 128 + (((cb * 4 + g) ^ sm_swz(hp)) * 16));
+            acc[i] = mfma16<DT>(af[s], bf, acc[i]);
+        }
+    }
+    // lane: pixel pi(j) of each block, channels 4g .. 4g + 3
+    T* dx = static_cast<T*>(p.out);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = wave * 64 + i * 16 + pj, r = q / W, col = q - r * W;
+        if (h0 + r >= p.H) continue;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int c = g * 4 + m;
+            if (c < p.cin) dx[((int64_t)img * p.cin + c) * HW + (int64_t)(h0 + r) * W + col] = elem<DT>::from_f32(acc[i][m]);
+        }
+    }
 }
 
 bool al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
@@ -503,6 +719,14 @@ bool fwd_rows_applies(const tvk_conv_desc& d) {
     return d.c_in * (256 / wo + d.kh - 1) * (d.w + 16) <= 8192;
 }
 
+// grad input on the MFMA pipe: 3x3 stride 1 padding 1, 64 output channels,
+// W in {8, 16, 32, 64}, dy 16-byte aligned
+bool dgrad_mfma_applies(const tvk_conv_desc& d) {
+    if (d.kh != 3 || d.kw != 3 || d.stride[0] != 1 || d.stride[1] != 1 || d.dilation[0] != 1 || d.dilation[1] != 1) return false;
+    if (d.padding[0] != 1 || d.padding[1] != 1 || d.c_out != 64 || d.c_in > 16) return false;
+    return (d.w == 8 || d.w == 16 || d.w == 32 || d.w == 64) && al16(d.y);
+}
+
 // grad input tile: rows per workgroup and the halo it stages
 void dgrad_tile(const tvk_conv_desc& d, int& tr, int& hr, int& hc) {
     tr = std::max<int>(1, 256 / (int)d.w);
@@ -522,8 +746,9 @@ bool conv_small_applies(const tvk_conv_desc& d, int mode) {
     if (big >= (int64_t(1) << 30)) return false;
     if (mode == 0) return true;
     if (mode == 2) return (d.h_out * d.w_out) % 8 == 0 && al16(d.y);
-    // grad input: the stride-1 3x3 halo kernel
+    // grad input: the stride-1 3x3 kernels
     if (d.kh != 3 || d.kw != 3 || d.stride[0] != 1 || d.stride[1] != 1 || d.dilation[0] != 1 || d.dilation[1] != 1) return false;
+    if (dgrad_mfma_applies(d)) return true;
     if (d.c_in > 4 || d.c_out > 256 || d.w > 256 || d.w_out % 8 != 0 || !al16(d.y)) return false;
     int tr, hr, hc;
     dgrad_tile(d, tr, hr, hc);
@@ -562,8 +787,8 @@ tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who) {
             if (!p.part) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
         }
         const dim3 grid((unsigned)p.split, (unsigned)ny);
-        if (f16) hipLaunchKernelGGL(conv_small_wgrad_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL(conv_small_wgrad_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
+        if (f16) hipLaunchKernelGGL((conv_small_wgrad_kernel<TVK_F16, 4>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((conv_small_wgrad_kernel<TVK_BF16, 4>), grid, dim3(256), 0, s, p);
         if (p.split > 1) {
             int sg = 1;
             while (sg < 16 && sg * 2 <= p.split && (int64_t)count * sg / 256 < 512) sg *= 2;
@@ -572,14 +797,31 @@ tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who) {
             if (f16) hipLaunchKernelGGL(small_split_reduce_kernel<TVK_F16>, rgrid, dim3(256), 0, s, p.part, d.weight, count, p.split, sg);
             else hipLaunchKernelGGL(small_split_reduce_kernel<TVK_BF16>, rgrid, dim3(256), 0, s, p.part, d.weight, count, p.split, sg);
         }
+    } else if (dgrad_mfma_applies(d)) {
+        p.out = d.x;
+        p.tr = 256 / p.W;
+        p.row_blocks = (p.H + p.tr - 1) / p.tr;
+        const dim3 grid((unsigned)(p.n * p.row_blocks));
+        if (f16) hipLaunchKernelGGL(conv_small_dgrad_mfma_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL(conv_small_dgrad_mfma_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
     } else {
         p.out = d.x;
         dgrad_tile(d, p.tr, p.hr, p.hc);
         p.ncp = (p.cout + 1) / 2;
         p.row_blocks = (p.H + p.tr - 1) / p.tr;
         const dim3 grid((unsigned)(p.n * p.row_blocks));
-        if (f16) hipLaunchKernelGGL(conv_small_dgrad_kernel<TVK_F16>, grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL(conv_small_dgrad_kernel<TVK_BF16>, grid, dim3(256), 0, s, p);
+#define TVK_SD(NC_)                                                                                 \
+    do {                                                                                          \
+        if (f16) hipLaunchKernelGGL((conv_small_dgrad_kernel<TVK_F16, NC_>), grid, dim3(256), 0, s, p);  \
+        else hipLaunchKernelGGL((conv_small_dgrad_kernel<TVK_BF16, NC_>), grid, dim3(256), 0, s, p);     \
+    } while (0)
+        switch (p.cin) {
+        case 1: TVK_SD(1); break;
+        case 2: TVK_SD(2); break;
+        case 3: TVK_SD(3); break;
+        default: TVK_SD(4); break;
+        }
+#undef TVK_SD
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
