@@ -56,7 +56,83 @@ def parse():
                    help="launch only this kernel --steps times and exit (for rocprofv3 counter passes); "
                         "'copy' is torch's copy of a 1 GiB buffer, the calibration for FETCH_SIZE/WRITE_SIZE; "
                         "'ceiling' the random-operand MFMA loop of tvk_calibrate_mfma (two waves per SIMD)")
+    p.add_argument("--vendor", action="store_true",
+                   help="time the C2 GEMM chain and the C4 conv layers through torch on this GPU (hipBLASLt, "
+                        "MIOpen) with the same shapes and data, print one JSON line and exit")
     return p.parse_args()
+
+
+def vendor_baseline():
+    """The vendor libraries on the same workloads, for calibration: torch's
+    fp16 addmm/mm (hipBLASLt) on the C2 MLP chain and its 256x4096x4096
+    products, and aten.convolution / convolution_backward (MIOpen) on the C4
+    layers, all on torch's stream with HIP events (the mean of N launches
+    after a warm-up)."""
+    import json
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    f16 = torch.float16
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def us(fn, n=50, w=10):
+        for _ in range(w):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(e0.elapsed_time(e1) / n * 1e3, 2)
+
+    g = torch.Generator().manual_seed(1)
+    out = {"what": "torch on this GPU: hipBLASLt (fp16 addmm/mm), MIOpen (fp16 convolution)"}
+    B, dims = 256, [784, 4096, 4096, 4096, 10]
+    xs = [torch.rand((B, dims[0]), generator=g).to(f16).to(dev)]
+    ws = [((torch.rand((dims[i + 1], dims[i]), generator=g) * 2 - 1) * dims[i] ** -0.5).to(f16).to(dev) for i in range(4)]
+    bs = [((torch.rand((dims[i + 1],), generator=g) * 2 - 1) * dims[i] ** -0.5).to(f16).to(dev) for i in range(4)]
+    dys = [torch.randn((B, d), generator=g).to(f16).to(dev) for d in dims[1:]]
+    h1 = torch.randn((B, 4096), generator=g).to(f16).to(dev)
+    out["c2_fwd_256x4096x4096_us"] = us(lambda: torch.addmm(bs[1], h1, ws[1].t()))
+    out["c2_dx_256x4096x4096_us"] = us(lambda: torch.mm(dys[1], ws[1]))
+    out["c2_dw_4096x4096x256_us"] = us(lambda: torch.mm(dys[1].t(), h1))
+
+    def chain():
+        h, acts = xs[0], [xs[0]]
+        for i in range(4):
+            h = torch.addmm(bs[i], h, ws[i].t())
+            acts.append(h)
+        for i in reversed(range(4)):
+            torch.mm(dys[i].t(), acts[i])
+            if i > 0:
+                torch.mm(dys[i], ws[i])
+
+    out["c2_mlp_gemm_fwd_bwd_us"] = us(chain, 20, 5)
+    progress("vendor: C2 done")
+    layers = [(3, 64, 3, 1, 1, 32), (64, 64, 3, 1, 1, 32), (64, 128, 3, 2, 1, 32), (128, 256, 3, 2, 1, 16),
+              (64, 128, 1, 2, 0, 32), (128, 256, 1, 2, 0, 16)]
+    calls, per = [], []
+    for cin, cout, k, st, pd, hw in layers:
+        x = torch.randn((128, cin, hw, hw), generator=g).to(f16).to(dev)
+        w = (torch.randn((cout, cin, k, k), generator=g) * (2.0 / (cin * k * k)) ** 0.5).to(f16).to(dev)
+        ho = (hw + 2 * pd - k) // st + 1
+        dy = torch.randn((128, cout, ho, ho), generator=g).to(f16).to(dev)
+        fwd = lambda x=x, w=w, st=st, pd=pd: torch.ops.aten.convolution(x, w, None, [st, st], [pd, pd], [1, 1], False, [0, 0], 1)
+        bwd = lambda x=x, w=w, dy=dy, st=st, pd=pd: torch.ops.aten.convolution_backward(
+            dy, x, w, None, [st, st], [pd, pd], [1, 1], False, [0, 0], 1, [True, True, False])
+        per.append({"layer": f"{cin}->{cout} {k}x{k} s{st}", "fwd_us": us(fwd, 20, 3), "dgrad_wgrad_us": us(bwd, 20, 3)})
+        calls += [fwd, bwd]
+
+    def c4():
+        for c in calls:
+            c()
+
+    out["c4_layers"] = per
+    out["c4_resnet_conv_fwd_bwd_us"] = us(c4, 10, 2)
+    progress("vendor: C4 done")
+    print(json.dumps(out), flush=True)
 
 
 def profile_kernel(which, steps):
@@ -137,6 +213,9 @@ def main():
 
     if args.profile_kernel:
         profile_kernel(args.profile_kernel, args.steps)
+        return
+    if args.vendor:
+        vendor_baseline()
         return
 
     import torch
