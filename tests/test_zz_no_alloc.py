@@ -43,7 +43,7 @@ def bits(t: torch.Tensor) -> np.ndarray:
 # an operand repack, the streaming kernel's split partials, batches, and float32 (no scratch)
 CASES = [
     ((256, 4096, 4096, torch.float16, True, 1, True), "gemm16_dma_128x128_splitk"),
-    ((1000, 3000, 777, torch.float16, False, 1, False), "gemm16_mfma_128x128"),
+    ((1000, 3000, 777, torch.float16, False, 1, False), "gemm16_dma_128x128"),
     ((16, 14336, 4096, torch.bfloat16, False, 1, False), "gemm16_skinny_ring_splitk"),
     ((512, 512, 8192, torch.bfloat16, True, 2, True), "gemm16_dma_128x128_splitk"),
     ((300, 260, 200, torch.float32, False, 1, True), "gemm_seq_mfma_64x128"),

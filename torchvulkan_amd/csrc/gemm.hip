@@ -586,8 +586,17 @@ GemmArgs make_args(const tvk_gemm_desc& d) {
     return p;
 }
 
-// Leading dimension of a repacked operand: its contiguous dimension padded to 8.
+// Leading dimension of a repacked operand: its contiguous dimension padded to
+// 8, or to 32 when that dimension is K (the padding is zeros, so the
+// LDS-ring kernels can run a last k step of 32 past K).
 int64_t pad8(int64_t v) { return (v + 7) / 8 * 8; }
+int64_t repack_ld(int64_t v, bool kdim) { return kdim ? (v + 31) / 32 * 32 : pad8(v); }
+
+// Whether every load of k in [K, K rounded up to 32) returns zero under plan
+// pl: each k-contiguous operand is repacked (zero-padded rows), and each
+// m/n-contiguous one has rows at least as long as its extent, so row K and
+// beyond lie past its buffer range.
+bool k_tail_zero(const tvk_gemm_desc& d, const struct Plan& pl);
 
 // Arguments as the kernels see them once the planned repacks are done (the
 // pointers of repacked operands only matter for alignment: workspace offsets
@@ -816,15 +825,25 @@ GemmArgs repacked_args(const tvk_gemm_desc& d, const Plan& pl) {
     static const char aligned_dummy[16] __attribute__((aligned(256))) = {0};
     if (pl.repack_a) {
         p.a = aligned_dummy;
-        if (pl.ak) { const int64_t ld = pad8(d.K); p.sa[0] = d.M * ld; p.sa[1] = ld; p.sa[2] = 1; }
+        if (pl.ak) { const int64_t ld = repack_ld(d.K, true); p.sa[0] = d.M * ld; p.sa[1] = ld; p.sa[2] = 1; }
         else { const int64_t ld = pad8(d.M); p.sa[0] = d.K * ld; p.sa[1] = 1; p.sa[2] = ld; }
+        p.a_ext = 2 * p.sa[0];
     }
     if (pl.repack_b) {
         p.b = aligned_dummy;
-        if (pl.bk) { const int64_t ld = pad8(d.K); p.sb[0] = d.N * ld; p.sb[1] = 1; p.sb[2] = ld; }
+        if (pl.bk) { const int64_t ld = repack_ld(d.K, true); p.sb[0] = d.N * ld; p.sb[1] = 1; p.sb[2] = ld; }
         else { const int64_t ld = pad8(d.N); p.sb[0] = d.K * ld; p.sb[1] = ld; p.sb[2] = 1; }
+        p.b_ext = 2 * p.sb[0];
     }
+    p.kzero = k_tail_zero(d, pl) ? 1 : 0;
     return p;
+}
+
+bool k_tail_zero(const tvk_gemm_desc& d, const Plan& pl) {
+    if (d.K % 32 == 0) return true;
+    const bool a_ok = pl.ak ? pl.repack_a : (pl.repack_a || d.a_stride[2] >= d.M);
+    const bool b_ok = pl.bk ? pl.repack_b : (pl.repack_b || d.b_stride[1] >= d.N);
+    return a_ok && b_ok;
 }
 
 #define TVK_LAYOUT_SWITCH(PL, NTHR, KERNEL, ...)                                            \
@@ -858,8 +877,8 @@ void launch_seq(const Plan& pl, GemmArgs& p, dim3 grid, hipStream_t s) {
 size_t plan_scratch_bytes(const tvk_gemm_desc& d, const Plan& pl, int nb, size_t* rep_a_out = nullptr,
                           size_t* rep_b_out = nullptr) {
     auto al256 = [](size_t v) { return (v + 255) / 256 * 256; };
-    const int64_t a_rows = pl.ak ? d.M : d.K, a_ld = pad8(pl.ak ? d.K : d.M);
-    const int64_t b_rows = pl.bk ? d.N : d.K, b_ld = pad8(pl.bk ? d.K : d.N);
+    const int64_t a_rows = pl.ak ? d.M : d.K, a_ld = repack_ld(pl.ak ? d.K : d.M, pl.ak);
+    const int64_t b_rows = pl.bk ? d.N : d.K, b_ld = repack_ld(pl.bk ? d.K : d.N, pl.bk);
     const size_t rep_a = pl.repack_a ? al256((size_t)nb * a_rows * a_ld * 2) : 0;
     const size_t rep_b = pl.repack_b ? al256((size_t)nb * b_rows * b_ld * 2) : 0;
     size_t part_b = pl.split > 1 ? (size_t)pl.split * nb * d.M * d.N * 4 : 0;
@@ -890,8 +909,8 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixe
         if (q.has_bias) q.bias = (const char*)d.bias + (size_t)(b0 * d.bias_stride[0]) * es;
         q.c = (char*)d.c + (size_t)(b0 * d.c_stride[0]) * es;
         // scratch: repacked operands, then split-K partials
-        const int64_t a_rows = pl.ak ? d.M : d.K, a_ld = pad8(pl.ak ? d.K : d.M);
-        const int64_t b_rows = pl.bk ? d.N : d.K, b_ld = pad8(pl.bk ? d.K : d.N);
+        const int64_t a_rows = pl.ak ? d.M : d.K, a_ld = repack_ld(pl.ak ? d.K : d.M, pl.ak);
+        const int64_t b_rows = pl.bk ? d.N : d.K, b_ld = repack_ld(pl.bk ? d.K : d.N, pl.bk);
         size_t rep_a = 0, rep_b = 0;
         const size_t need = plan_scratch_bytes(d, pl, nb, &rep_a, &rep_b);
         char* ws = nullptr;
@@ -918,6 +937,7 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixe
                 q.sa[0] = a_rows * a_ld;
                 q.sa[1] = pl.ak ? a_ld : 1;
                 q.sa[2] = pl.ak ? 1 : a_ld;
+                q.a_ext = 2 * q.sa[0];
             }
             if (pl.repack_b) {
                 if (pl.bk) repack(q.b, d.b_stride[0], d.b_stride[2], d.b_stride[1], d.N, d.K, b_ld, ws + rep_a);
@@ -926,6 +946,7 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixe
                 q.sb[0] = b_rows * b_ld;
                 q.sb[1] = pl.bk ? 1 : b_ld;
                 q.sb[2] = pl.bk ? b_ld : 1;
+                q.b_ext = 2 * q.sb[0];
             }
         }
         switch (pl.kern) {

@@ -24,6 +24,15 @@ struct GemmArgs {
     float* part;
     int k_chunk;
     int split;
+    // 1: loads of k in [K, K rounded up to 32) return zeros for both operands
+    // (a k-contiguous operand was copied with zero-padded rows; rows past K of
+    // an m/n-contiguous one lie outside its buffer range), so the LDS-ring
+    // kernels may run the last k step whole
+    int kzero;
+    // bytes of one matrix of a repacked operand (the whole zero-padded
+    // [rows][ld] copy, which the LDS-ring kernels' buffer ranges then cover);
+    // 0: the range ends at the operand's last element
+    int64_t a_ext, b_ext;
 };
 
 // ----------------------------------------------------------------------------

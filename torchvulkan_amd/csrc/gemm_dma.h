@@ -188,8 +188,8 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     // A: (m, k) at m*sa[1] + k*sa[2]; B: (k, n) at k*sb[1] + n*sb[2]
     const char* A = reinterpret_cast<const char*>(p.a) + (int64_t)b * p.sa[0] * 2;
     const char* B = reinterpret_cast<const char*>(p.b) + (int64_t)b * p.sb[0] * 2;
-    const i32x4 ra = dma_rsrc(A, 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1));
-    const i32x4 rb = dma_rsrc(B, 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1));
+    const i32x4 ra = dma_rsrc(A, p.a_ext ? p.a_ext : 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1));
+    const i32x4 rb = dma_rsrc(B, p.b_ext ? p.b_ext : 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1));
     constexpr bool XS = !G::BIG;   // the wide (conflict-free) swizzles
     DmaSrc<AK, G::DA, BM, XS> da;
     DmaSrc<BK, G::DB, BN, XS> db;
@@ -197,7 +197,9 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     db.init(p.sb[2], p.sb[1], n0, p.N, wave, lane);
     // split-K (grid z): this workgroup's k range starts at stage kt0
     const int kt0 = p.split > 1 ? (int)blockIdx.z * (p.k_chunk / D_BK) : 0;
-    const int nk = (p.split > 1 ? min(p.k_chunk, p.K - (int)blockIdx.z * p.k_chunk) : p.K) / D_BK;
+    // (a K off the 32 grid runs its last step whole: split chunks are whole
+    // multiples of 64, and the loads past K return zeros, kzero)
+    const int nk = ((p.split > 1 ? min(p.k_chunk, p.K - (int)blockIdx.z * p.k_chunk) : p.K) + D_BK - 1) / D_BK;
     // The ring issues the same loads every stage, also for the NS stages past
     // this workgroup's k range (the waits count on them). Those go through
     // resources of no records: out of range, so they return zeros without

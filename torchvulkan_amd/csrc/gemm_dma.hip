@@ -5,7 +5,8 @@
 namespace tvk {
 
 bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor) {
-    if (p.K < D_BK || p.K % D_BK != 0) return false;
+    // K off the 32 grid: the last k step runs whole, so its loads past K must read zeros
+    if (p.K < D_BK || (p.K % D_BK != 0 && !p.kzero)) return false;
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     if (!al16(p.a) || !al16(p.b)) return false;
     if (p.batch > 1 && (p.sa[0] % 8 != 0 || p.sb[0] % 8 != 0)) return false;
