@@ -57,17 +57,17 @@ def parse():
                         "'copy' is torch's copy of a 1 GiB buffer, the calibration for FETCH_SIZE/WRITE_SIZE; "
                         "'ceiling' the random-operand MFMA loop of tvk_calibrate_mfma (two waves per SIMD)")
     p.add_argument("--vendor", action="store_true",
-                   help="time the C2 GEMM chain and the C4 conv layers through torch on this GPU (hipBLASLt, "
-                        "MIOpen) with the same shapes and data, print one JSON line and exit")
+                   help="time the C2 GEMM chain, the C4 conv layers and the C5 products through torch on this "
+                        "GPU (hipBLASLt, MIOpen) with the same shapes and data, print one JSON line and exit")
     return p.parse_args()
 
 
 def vendor_baseline():
     """The vendor libraries on the same workloads, for calibration: torch's
     fp16 addmm/mm (hipBLASLt) on the C2 MLP chain and its 256x4096x4096
-    products, and aten.convolution / convolution_backward (MIOpen) on the C4
-    layers, all on torch's stream with HIP events (the mean of N launches
-    after a warm-up)."""
+    products, aten.convolution / convolution_backward (MIOpen) on the C4
+    layers, and mm / baddbmm on the C5 products, all on torch's stream with
+    HIP events (the mean of N launches after a warm-up)."""
     import json
 
     import torch
@@ -132,6 +132,37 @@ def vendor_baseline():
     out["c4_layers"] = per
     out["c4_resnet_conv_fwd_bwd_us"] = us(c4, 10, 2)
     progress("vendor: C4 done")
+    del calls, per
+    # C5: the headline square product, the skinny one (B rotated over three
+    # buffers past the 256 MB Infinity Cache), the ragged one and baddbmm
+    n = 8192
+    a = torch.randn((n, n), generator=g).to(f16).to(dev)
+    b = torch.randn((n, n), generator=g).to(f16).to(dev)
+    c = torch.empty((n, n), dtype=f16, device=dev)
+    t = us(lambda: torch.mm(a, b, out=c), 20, 5)
+    out["c5_square_8192_us"] = t
+    out["c5_square_8192_tflops"] = round(2 * n ** 3 / (t * 1e-6) / 1e12, 1)
+    del a, b, c
+    M, K, N = 16, 4096, 14336
+    a = torch.randn((M, K), generator=g).to(f16).to(dev)
+    bufs = [torch.randn((K, N), generator=g).to(f16).to(dev) for _ in range(3)]
+    c = torch.empty((M, N), dtype=f16, device=dev)
+    idx = [0]
+
+    def skinny():
+        torch.mm(a, bufs[idx[0] % 3], out=c)
+        idx[0] += 1
+
+    out["c5_skinny_us"] = us(skinny, 150, 30)
+    del bufs
+    a = torch.randn((1000, 777), generator=g).to(f16).to(dev)
+    b = torch.randn((777, 3000), generator=g).to(f16).to(dev)
+    out["c5_ragged_us"] = us(lambda: torch.mm(a, b))
+    x1 = torch.randn((64, 512, 128), generator=g).to(f16).to(dev)
+    x2 = torch.randn((64, 128, 512), generator=g).to(f16).to(dev)
+    inp = torch.randn((64, 512, 512), generator=g).to(f16).to(dev)
+    out["c5_baddbmm_us"] = us(lambda: torch.baddbmm(inp, x1, x2, beta=1.0, alpha=0.5))
+    progress("vendor: C5 done")
     print(json.dumps(out), flush=True)
 
 
