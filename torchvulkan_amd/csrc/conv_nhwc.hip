@@ -349,7 +349,7 @@ __global__ __launch_bounds__(64 * ring_waves(BM, BN)) void conv_ring_kernel(Conv
             if (co >= p.N || pix >= p.M) continue;
             // 8 pixels of one image row run (hw % 8 == 0): one 16-byte store
             const int img = pix / hw, o = pix - img * hw;
-            *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + co) * hw + o) = *reinterpret_cast<const u32x4*>(tile + ch * LROW + pc * 8);
+            st_nt(reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + co) * hw + o), *reinterpret_cast<const u32x4*>(tile + ch * LROW + pc * 8));
         }
     } else {
         // sub-pixel phases (or pixel runs that 16-byte stores do not fit): a
@@ -850,8 +850,7 @@ __global__ __launch_bounds__(PX) void conv_halo_kernel(HaloArgs p) {
         const int ch = idx / (PX / 8), px = (idx % (PX / 8)) * 8;
         const int r = px / W, c = px - r * W;
         if (n0 + ch >= p.N || h0 + r >= p.H) continue;
-        *reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + n0 + ch) * HWs + (int64_t)(h0 + r) * W + c) =
-            *reinterpret_cast<const u32x4*>(tile + ch * LROW + px);
+        st_nt(reinterpret_cast<u32x4*>(out + ((int64_t)img * p.N + n0 + ch) * HWs + (int64_t)(h0 + r) * W + c), *reinterpret_cast<const u32x4*>(tile + ch * LROW + px));
     }
 }
 
@@ -1023,8 +1022,7 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
         const int ch = idx / (TPX / 8), px = (idx % (TPX / 8)) * 8;
         const int k = px / ppi, rem = px - k * ppi, r = rem / Wo;
         if (n0 + ch >= p.N || h0 + r >= Ho || img0 + k >= p.nimg) continue;
-        *reinterpret_cast<u32x4*>(out + ((int64_t)(img0 + k) * p.N + n0 + ch) * HWo + (int64_t)h0 * Wo + rem) =
-            *reinterpret_cast<const u32x4*>(tile + ch * LROW + px);
+        st_nt(reinterpret_cast<u32x4*>(out + ((int64_t)(img0 + k) * p.N + n0 + ch) * HWo + (int64_t)h0 * Wo + rem), *reinterpret_cast<const u32x4*>(tile + ch * LROW + px));
     }
 }
 
@@ -1195,8 +1193,7 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
         const int k = px / (4 * ppi), rem = px - k * 4 * ppi;
         const int h = 2 * i0 + rem / p.W, w = rem % p.W;
         if (n0 + ch >= p.N || img0 + k >= p.nimg || h >= p.H) continue;
-        *reinterpret_cast<u32x4*>(out + ((int64_t)(img0 + k) * p.N + n0 + ch) * HW + (int64_t)h * p.W + w) =
-            *reinterpret_cast<const u32x4*>(tile + ch * LROW + px);
+        st_nt(reinterpret_cast<u32x4*>(out + ((int64_t)(img0 + k) * p.N + n0 + ch) * HW + (int64_t)h * p.W + w), *reinterpret_cast<const u32x4*>(tile + ch * LROW + px));
     }
 }
 
@@ -1729,8 +1726,7 @@ __global__ __launch_bounds__(256) void conv1x1_fwd_kernel(PointFwdArgs p) {
     for (int idx = tid; idx < 64 * (PT / 8); idx += 256) {
         const int ch = idx / (PT / 8), pc = idx % (PT / 8);
         if (n0 + ch >= p.cout) continue;
-        *reinterpret_cast<u32x4*>(y + ((int64_t)img * p.cout + n0 + ch) * HWo + t0 + pc * 8) =
-            *reinterpret_cast<const u32x4*>(tile + ch * LROW + pc * 8);
+        st_nt(reinterpret_cast<u32x4*>(y + ((int64_t)img * p.cout + n0 + ch) * HWo + t0 + pc * 8), *reinterpret_cast<const u32x4*>(tile + ch * LROW + pc * 8));
     }
 }
 

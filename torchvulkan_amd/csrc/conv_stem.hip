@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256) void conv_small_fwd_kernel(SmallArgs p) {
         if (p.vec_out) {
             // 8 pixels of one image (Ho * Wo % 8 == 0): one 16-byte store
             const int img = pix / HWo, o = pix - img * HWo;
-            *reinterpret_cast<u32x4*>(y + ((int64_t)img * p.cout + co) * HWo + o) = *reinterpret_cast<const u32x4*>(src);
+            st_nt(reinterpret_cast<u32x4*>(y + ((int64_t)img * p.cout + co) * HWo + o), *reinterpret_cast<const u32x4*>(src));
         } else {
             for (int e = 0; e < 8 && pix + e < p.M; ++e) {
                 const int img = (pix + e) / HWo, o = pix + e - img * HWo;
@@ -299,8 +299,7 @@ __global__ __launch_bounds__(256) void conv_small_fwd_rows_kernel(SmallArgs p) {
     for (int idx = tid; idx < 64 * 32; idx += 256) {
         const int ch = idx / 32, pc = idx % 32;
         if (n0 + ch >= p.cout || pix0 + pc * 8 >= HWo) continue;
-        *reinterpret_cast<u32x4*>(y + ((int64_t)img * p.cout + n0 + ch) * HWo + pix0 + pc * 8) =
-            *reinterpret_cast<const u32x4*>(tile + ch * LROW + pc * 8);
+        st_nt(reinterpret_cast<u32x4*>(y + ((int64_t)img * p.cout + n0 + ch) * HWo + pix0 + pc * 8), *reinterpret_cast<const u32x4*>(tile + ch * LROW + pc * 8));
     }
 }
 

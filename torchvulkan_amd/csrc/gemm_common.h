@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(GemmArgs p) {
         }
         T* cp = c + (int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2];
         if constexpr (VEC) {
-            *reinterpret_cast<u32x2*>(cp) = u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+            st_nt(reinterpret_cast<u32x2*>(cp), u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)});
         } else {
 #pragma unroll
             for (int r = 0; r < 4; ++r) cp[(int64_t)r * p.sc[2]] = __builtin_bit_cast(T, h[r]);

@@ -376,8 +376,8 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
             }
             T* cp = Cb + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2];
             if (vec_c && full) {
-                *reinterpret_cast<u32x4*>(cp) = u32x4{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
-                                                      (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16)};
+                st_nt(reinterpret_cast<u32x4*>(cp), u32x4{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
+                                                      (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16)});
             } else {
                 for (int e = 0; e < 8 && col + e < p.N; ++e) cp[(int64_t)e * p.sc[2]] = __builtin_bit_cast(T, h[e]);
             }
