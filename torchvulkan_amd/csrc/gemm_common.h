@@ -97,7 +97,7 @@ __device__ inline void store_out(const GemmArgs& p, int b, int row, int col, flo
         }
         v = INL ? epilogue(acc, p.alpha, p.has_bias, bv, p.beta, p.act) : epilogue_math(acc, p.alpha, p.has_bias, bv, p.beta, p.act);
     }
-    st_nt(&c[(int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2]], elem<DT>::from_f32(v));
+    c[(int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2]] = elem<DT>::from_f32(v);
 }
 
 // Epilogue of 16 accumulators of one lane that share a column and sit at
@@ -116,8 +116,8 @@ __device__ inline void store_frag16(const GemmArgs& p, int b, int row0, int col,
         for (int r = 0; r < 16; ++r) {
             const int row = row0 + (r / 4) * 8 + (r % 4);
             if (row < p.M)
-                st_nt(&c[(int64_t)row * p.sc[1]], elem<DT>::from_f32(INL ? epilogue(v[r], p.alpha, 1, bv, p.beta, p.act)
-                                                                        : epilogue_math(v[r], p.alpha, 1, bv, p.beta, p.act)));
+                c[(int64_t)row * p.sc[1]] = elem<DT>::from_f32(INL ? epilogue(v[r], p.alpha, 1, bv, p.beta, p.act)
+                                                                   : epilogue_math(v[r], p.alpha, 1, bv, p.beta, p.act));
         }
         return;
     }
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(GemmArgs p) {
             st_nt(reinterpret_cast<u32x2*>(cp), u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)});
         } else {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) st_nt(&cp[(int64_t)r * p.sc[2]], __builtin_bit_cast(T, h[r]));
+            for (int r = 0; r < 4; ++r) cp[(int64_t)r * p.sc[2]] = __builtin_bit_cast(T, h[r]);
         }
     }
 }
