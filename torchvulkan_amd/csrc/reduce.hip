@@ -243,6 +243,40 @@ __global__ __launch_bounds__(256) void reduce_fold_kernel(const Acc* part, RedAr
     }
 }
 
+// The same sum for many splits: a workgroup takes 32 consecutive outputs,
+// its 8 thread groups sum the splits z = g, g + 8, ... (eight loads in flight
+// a thread), and the group sums are added in group order through LDS. (One
+// thread an output left a 3072-output, 256-split fold to 12 workgroups and
+// 32 dependent rounds of loads.)
+template <typename Acc>
+__global__ __launch_bounds__(256) void reduce_fold8_kernel(const Acc* part, RedArgs p) {
+    __shared__ Acc red[8][32];
+    const int l = threadIdx.x % 32, g = threadIdx.x / 32;
+    const int64_t o = (int64_t)blockIdx.x * 32 + l;
+    Acc v = 0;
+    if (o < p.nout) {
+        int z = g;
+        for (; z + 56 < p.splits; z += 64) {
+            Acc w[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[u] = part[(int64_t)(z + 8 * u) * p.nout + o];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += w[u];
+        }
+        for (; z < p.splits; z += 8) v += part[(int64_t)z * p.nout + o];
+    }
+    red[g][l] = v;
+    __syncthreads();
+    if (g == 0 && o < p.nout) {
+        Acc t = red[0][l];
+#pragma unroll
+        for (int q = 1; q < 8; ++q) t += red[q][l];
+        int64_t so, dof;
+        kept_offsets(p, o, so, dof);
+        store_acc<Acc>(p.dst + dof * p.db, p.ddt, t);
+    }
+}
+
 // An empty sum: every output is castValue(0), all-zero bytes in every dtype.
 __global__ __launch_bounds__(256) void reduce_zero_kernel(RedArgs p) {
     for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < p.nout; o += (int64_t)gridDim.x * 256) {
@@ -315,7 +349,8 @@ tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
     if (splits > 1) {
         p.dst = final_dst;
         p.ddt = ddt;
-        hipLaunchKernelGGL(reduce_fold_kernel<Acc>, dim3(blocks_for(p.nout, 256)), dim3(256), 0, st, part, p);
+        if (splits >= 32) hipLaunchKernelGGL(reduce_fold8_kernel<Acc>, dim3((unsigned)((p.nout + 31) / 32)), dim3(256), 0, st, part, p);
+        else hipLaunchKernelGGL(reduce_fold_kernel<Acc>, dim3(blocks_for(p.nout, 256)), dim3(256), 0, st, part, p);
     }
     return TVK_OK;
 }
