@@ -649,6 +649,7 @@ struct HaloArgs {
     int has_bias;
     int wt_bytes;
     int ipt, nimg;         // stride-2 grad input: images a tile, batch size
+    const uint16_t* wraw;  // forward on 256 threads: the weight as given, [N][Cs][3][3] (no permuted copy)
 };
 
 // 16-byte chunk swizzle of the 64-byte LDS rows (halo pixels and weight rows):
@@ -658,6 +659,37 @@ struct HaloArgs {
 // flipping bit 1 of the chunk every 4 rows spreads every group over the 64
 // banks for any first row, where a 4-row rotation left 2-way conflicts.
 __device__ inline int hl_swz(int row) { return ((row >> 2) & 1) * 2; }
+
+// Forward weight rows of one 32-channel chunk gathered by the conv kernel
+// itself from the weight as given ([N][Cs][3][3]), in place of the permuted
+// copy's LDS-DMA: thread t of 256 takes output channel t / 4 of the tile's 64
+// and input channels 8 * (t % 4) .. + 7 of the chunk, whose 72 halves (8
+// channels x 9 taps) are one contiguous, 16-byte aligned run: nine 16-byte
+// loads, then the 8 x 9 transpose in registers (two halves a dword) and nine
+// 16-byte LDS stores, one per tap row (tap * 64 + channel, the permuted
+// layout's rows). Saves the permute launch of every forward call.
+struct RawWeights {
+    u32x4 v[9];
+    __device__ inline void load(const uint16_t* w, int co, int Cs, int kc, int cg) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(w + ((int64_t)co * Cs + kc * 32 + cg * 8) * 9);
+#pragma unroll
+        for (int j = 0; j < 9; ++j) v[j] = src[j];
+    }
+    __device__ inline uint32_t half_at(int a) const {   // half a of the 72-half run, in the low 16 bits
+        const uint32_t d = v[a / 8][(a / 2) % 4];
+        return (a % 2) ? (d >> 16) : (d & 0xffffu);
+    }
+    __device__ inline void store(char* rows, int col, int cg) const {
+#pragma unroll
+        for (int t = 0; t < 9; ++t) {
+            uint32_t o[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) o[m] = half_at(2 * m * 9 + t) | (half_at((2 * m + 1) * 9 + t) << 16);
+            const int row = t * 64 + col;
+            *reinterpret_cast<u32x4*>(rows + row * 64 + ((cg ^ hl_swz(row)) * 16)) = u32x4{o[0], o[1], o[2], o[3]};
+        }
+    }
+};
 
 // 3x3 weight w[co][c][9] -> forward wout[co][t][c] or grad input
 // wout[c][t][co], the reduced channel count a multiple of 8: a thread gathers
@@ -807,11 +839,15 @@ __global__ __launch_bounds__(PX) void conv_halo_kernel(HaloArgs p) {
         }
     } else {
         // one stage: each chunk loads after every wave has read the previous one
+        RawWeights rw;
+        const int rw_co = min(n0 + tid / 4, p.N - 1), rw_cg = tid % 4;
         for (int kc = 0; kc < nk; ++kc) {
             if (kc > 0) __syncthreads();
-            issue_b(kc, 0);
+            if (p.wraw) rw.load(p.wraw, rw_co, p.Cs, kc, rw_cg);
+            else issue_b(kc, 0);
             load_a(kc);
             store_a(0);
+            if (p.wraw) rw.store(lds + A_BYTES, tid / 4, rw_cg);
             v_wait<0>();
             __syncthreads();
             compute(0);
@@ -952,15 +988,20 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    issue_b(0, 0);
+    RawWeights rw;
+    const int rw_co = min(n0 + tid / 4, p.N - 1), rw_cg = tid % 4;
+    if (p.wraw) rw.load(p.wraw, rw_co, p.Cs, 0, rw_cg);
+    else issue_b(0, 0);
     load_a(0);
     store_a(0);
+    if (p.wraw) rw.store(lds + H2_A, tid / 4, rw_cg);
     v_wait<0>();
     __syncthreads();
     for (int kc = 0; kc < nk; ++kc) {
         const int cur = kc & 1;
         if (kc + 1 < nk) {
-            issue_b(kc + 1, cur ^ 1);
+            if (p.wraw) rw.load(p.wraw, rw_co, p.Cs, kc + 1, rw_cg);
+            else issue_b(kc + 1, cur ^ 1);
             load_a(kc + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -985,7 +1026,10 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
                 for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (kc + 1 < nk) store_a(cur ^ 1);
+        if (kc + 1 < nk) {
+            store_a(cur ^ 1);
+            if (p.wraw) rw.store(lds + (cur ^ 1) * H2_STAGE + H2_A, tid / 4, rw_cg);
+        }
         v_wait<0>();
         __syncthreads();
     }
@@ -2391,6 +2435,15 @@ tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
     return TVK_OK;
 }
 
+// Stride-1 halo tile: 256 pixels (two workgroups a CU) where 512-pixel tiles
+// would give the 256 CUs fewer than two workgroups each. N: the output's
+// channels (forward c_out, grad input c_in).
+int halo_s1_px(const tvk_conv_desc& d, int N) {
+    const int H = (int)d.h, W = (int)d.w;
+    const int64_t wg512 = d.n * ((H + HL_PX / W - 1) / (HL_PX / W)) * ((N + HL_BN - 1) / HL_BN);
+    return wg512 < 512 ? 256 : HL_PX;
+}
+
 tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     if (mode == 2) {
         if (conv1x1_wgrad_applies(d)) return conv1x1_wgrad_run(d, who);
@@ -2404,15 +2457,23 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     hipStream_t s = resolve_stream(d.stream);
     Scratch scratch;
     const size_t wt_b = (size_t)N * 9 * Cs * 2;
-    char* ws = static_cast<char*>(scratch.get(wt_b, s));
-    if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the permuted weight");
-    const int pgroups = N * 9 * (Cs / 8);
-    const dim3 pgrid((unsigned)std::min((pgroups + 255) / 256, 1024));
     const uint16_t* w16 = static_cast<const uint16_t*>(d.weight);
-    if (mode == 0) hipLaunchKernelGGL(weight_permute9_kernel<true>, pgrid, dim3(256), 0, s, w16, reinterpret_cast<uint16_t*>(ws), cout, cin);
-    else hipLaunchKernelGGL(weight_permute9_kernel<false>, pgrid, dim3(256), 0, s, w16, reinterpret_cast<uint16_t*>(ws), cout, cin);
+    // the forward kernels on 256 threads (the stride-2 one, and the stride-1 one
+    // on 256-pixel tiles) gather their weight rows from the weight as given
+    const bool raw = mode == 0 && (reinterpret_cast<uintptr_t>(w16) & 15) == 0 &&
+                     (conv_halo_s2_fm(d, nullptr) != 0 || halo_s1_px(d, N) == 256);
+    char* ws = nullptr;
+    if (!raw) {
+        ws = static_cast<char*>(scratch.get(wt_b, s));
+        if (!ws) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the permuted weight");
+        const int pgroups = N * 9 * (Cs / 8);
+        const dim3 pgrid((unsigned)std::min((pgroups + 255) / 256, 1024));
+        if (mode == 0) hipLaunchKernelGGL(weight_permute9_kernel<true>, pgrid, dim3(256), 0, s, w16, reinterpret_cast<uint16_t*>(ws), cout, cin);
+        else hipLaunchKernelGGL(weight_permute9_kernel<false>, pgrid, dim3(256), 0, s, w16, reinterpret_cast<uint16_t*>(ws), cout, cin);
+    }
     HaloArgs p;
     memset(&p, 0, sizeof(p));
+    p.wraw = raw ? w16 : nullptr;
     p.src = static_cast<const uint16_t*>(mode == 0 ? d.x : d.y);
     p.wt = ws;
     p.bias = mode == 0 ? d.bias : nullptr;
@@ -2448,10 +2509,7 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     int ipt_f = 1;
     const int fm2 = mode == 0 ? conv_halo_s2_fm(d, &ipt_f) : 0;
     p.ipt = ipt_f;
-    // stride 1: 256-pixel tiles (two workgroups a CU) where 512-pixel ones would
-    // give the 256 CUs fewer than two workgroups each
-    const int64_t wg512 = d.n * ((H + HL_PX / W - 1) / (HL_PX / W)) * ((N + HL_BN - 1) / HL_BN);
-    const int px = !fm2 && wg512 < 512 ? 256 : HL_PX;
+    const int px = fm2 ? HL_PX : halo_s1_px(d, N);
     p.tr = fm2 ? (ipt_f > 1 ? H / 2 : 64 * fm2 / (W / 2)) : px / W;
     p.row_tiles = fm2 ? ((H / 2) + p.tr - 1) / p.tr : (H + p.tr - 1) / p.tr;
     p.wt_bytes = (int)wt_b;
