@@ -71,7 +71,7 @@ def test_gemm_validation_codes(field, value, status):
     ((0, 1, 8192), (0, 1, 8192), _abi.TVK_BF16, 8192, 8192, 4096, "gemm16_dma_256x256"),
     ((0, 8200, 1), (0, 8192, 1), _abi.TVK_F16, 8192, 8192, 8200, "gemm16_mfma_256x256_w8"),   # K % 32 != 0
     ((0, 8193, 1), (0, 8192, 1), _abi.TVK_F16, 8192, 8192, 8192, "gemm16_dma_256x256"),   # rows not 16 B aligned: A repacked
-    ((0, 777, 1), (0, 3000, 1), _abi.TVK_F16, 1000, 3000, 777, "gemm16_mfma_128x128"),      # C5 ragged, A repacked
+    ((0, 777, 1), (0, 3000, 1), _abi.TVK_F16, 1000, 3000, 777, "gemm16_dma_128x128"),       # C5 ragged, A repacked (rows padded to 32 with zeros)
     ((0, 1000, 1), (0, 1000, 1), _abi.TVK_F16, 1000, 1000, 1000, "gemm16_mfma_128x128"),
     ((0, 4096, 1), (0, 1, 4096), _abi.TVK_F16, 256, 4096, 4096, "gemm16_dma_128x128_splitk"),
     ((0, 1, 512), (0, 512, 1), _abi.TVK_BF16, 512, 512, 8192, "gemm16_dma_128x128_splitk"),
