@@ -57,15 +57,17 @@ def parse():
                         "'copy' is torch's copy of a 1 GiB buffer, the calibration for FETCH_SIZE/WRITE_SIZE; "
                         "'ceiling' the random-operand MFMA loop of tvk_calibrate_mfma (two waves per SIMD)")
     p.add_argument("--vendor", action="store_true",
-                   help="time the C2 GEMM chain, the C4 conv layers and the C5 products through torch on this "
-                        "GPU (hipBLASLt, MIOpen) with the same shapes and data, print one JSON line and exit")
+                   help="time the C2 GEMM chain, the C3 layer GEMMs, the C4 conv layers and the C5 products "
+                        "through torch on this GPU (hipBLASLt, MIOpen) with the same shapes and data, print one "
+                        "JSON line and exit")
     return p.parse_args()
 
 
 def vendor_baseline():
     """The vendor libraries on the same workloads, for calibration: torch's
     fp16 addmm/mm (hipBLASLt) on the C2 MLP chain and its 256x4096x4096
-    products, aten.convolution / convolution_backward (MIOpen) on the C4
+    products and on the C3 layer GEMMs, aten.convolution /
+    convolution_backward (MIOpen) on the C4
     layers, and mm / baddbmm on the C5 products, all on torch's stream with
     HIP events (the mean of N launches after a warm-up)."""
     import json
@@ -111,6 +113,22 @@ def vendor_baseline():
 
     out["c2_mlp_gemm_fwd_bwd_us"] = us(chain, 20, 5)
     progress("vendor: C2 done")
+    # C3: the transformer layer's six projections, forward and both gradients
+    T, calls3 = 8192, []
+    for fin, fout in [(512, 512), (512, 256), (512, 256), (512, 512), (512, 3072), (1536, 512)]:
+        x = torch.randn((T, fin), generator=g).to(f16).to(dev)
+        w = (torch.randn((fout, fin), generator=g) * 0.02).to(f16).to(dev)
+        dy = torch.randn((T, fout), generator=g).to(f16).to(dev)
+        calls3 += [lambda x=x, w=w: torch.mm(x, w.t()), lambda dy=dy, w=w: torch.mm(dy, w),
+                   lambda dy=dy, x=x: torch.mm(dy.t(), x)]
+
+    def c3():
+        for c in calls3:
+            c()
+
+    out["c3_llm_layer_gemm_fwd_bwd_us"] = us(c3, 20, 5)
+    del calls3
+    progress("vendor: C3 done")
     layers = [(3, 64, 3, 1, 1, 32), (64, 64, 3, 1, 1, 32), (64, 128, 3, 2, 1, 32), (128, 256, 3, 2, 1, 16),
               (64, 128, 1, 2, 0, 32), (128, 256, 1, 2, 0, 16)]
     calls, per = [], []
