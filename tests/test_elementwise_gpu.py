@@ -122,6 +122,12 @@ def test_sum_integer_valued_is_exact(gpu, dtype):
     z = torch.randint(-3, 4, (4096, 1024), generator=g).to(dtype).to(DEV)
     reduce_check(z, [0], out_dtype=out, exact=True)
     reduce_check(z, [1], out_dtype=out, exact=True)
+    # 32 or more splits: the grouped fold (32 outputs a workgroup, 8 thread
+    # groups over the splits), for a column sum and a row sum
+    w = torch.randint(-3, 4, (65536, 384), generator=g).to(dtype).to(DEV)
+    reduce_check(w, [0], out_dtype=out, exact=True)
+    r = torch.randint(-3, 4, (4, 1 << 20), generator=g).to(dtype).to(DEV)
+    reduce_check(r, [1], out_dtype=out, exact=True)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float64])

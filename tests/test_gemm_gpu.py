@@ -198,6 +198,12 @@ def test_dma_kernel_epilogue_sampled_rows(gpu, dtype, act):
     ((777, 1000), True, (777, 3001), False, None),     # A m-contiguous view, B rows of 3001
     ((3000, 777), False, (3000, 777), True, None),     # B = W^T with K = 777
     ((600, 333), False, (333, 700), False, 3),         # batched, both repacked
+    # K off the 32 grid on the LDS-ring split-K kernel (its last k step runs
+    # whole, reading zeros past K): A repacked with zero-padded rows, both
+    # repacked, and no repack at all (rows past K outside both buffer ranges)
+    ((512, 8190), False, (8190, 512), False, None),
+    ((512, 8190), False, (512, 8190), True, None),
+    ((8190, 512), True, (8190, 512), False, None),
 ])
 def test_repacked_operands_integer_exact(gpu, dtype, case):
     ashape, ta, bshape, tb, batch = case
