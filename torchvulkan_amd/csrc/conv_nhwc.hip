@@ -901,10 +901,13 @@ __global__ __launch_bounds__(PX) void conv_halo_kernel(HaloArgs p) {
 constexpr int H2_A = 41984;      // ipt (2 TR + 1) x (W + 2) slots x 64 bytes <= 656 x 64
 constexpr int H2_STAGE = H2_A + HL_B;
 
-template <int DT, int FM>
+// NS: LDS stages, 2 (chunk k + 1 loads while k computes; 157 KB, one
+// workgroup a CU) or 1 (78 KB: two workgroups a CU, for grids of more
+// workgroups than CUs, which would otherwise run in two rounds).
+template <int DT, int FM, int NS>
 __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
     constexpr int TPX = 64 * FM;
-    __shared__ __attribute__((aligned(1024))) char lds[2 * H2_STAGE];
+    __shared__ __attribute__((aligned(1024))) char lds[NS * H2_STAGE];
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
     const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64), g = lane / 16;
     const int img0 = (blockIdx.x / p.row_tiles) * p.ipt, h0 = (blockIdx.x % p.row_tiles) * p.tr;   // output rows
@@ -913,11 +916,11 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
     const int HRI = 2 * p.tr + 1, HR = p.ipt * HRI, ODD = W / 2 + 1, ppi = p.tr * Wo;
     const int nk = p.Cs / 32;
 
-    // zero halo column hc = 0 (input column -1: even slot 0) of both stages
+    // zero halo column hc = 0 (input column -1: even slot 0) of every stage
     for (int e = tid; e < HR * 4; e += 256) {
         const int hr = e / 4, ch = e % 4, hp = hr * RP;
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+        for (int st = 0; st < NS; ++st)
             *reinterpret_cast<u32x4*>(lds + st * H2_STAGE + hp * 64 + ch * 16) = u32x4{0u, 0u, 0u, 0u};
     }
 
@@ -988,23 +991,8 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    RawWeights rw;
-    const int rw_co = min(n0 + tid / 4, p.N - 1), rw_cg = tid % 4;
-    if (p.wraw) rw.load(p.wraw, rw_co, p.Cs, 0, rw_cg);
-    else issue_b(0, 0);
-    load_a(0);
-    store_a(0);
-    if (p.wraw) rw.store(lds + H2_A, tid / 4, rw_cg);
-    v_wait<0>();
-    __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
-        const int cur = kc & 1;
-        if (kc + 1 < nk) {
-            if (p.wraw) rw.load(p.wraw, rw_co, p.Cs, kc + 1, rw_cg);
-            else issue_b(kc + 1, cur ^ 1);
-            load_a(kc + 1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+    // the nine taps of one chunk from stage `cur`
+    auto compute = [&](int cur) {
         const char* sa = lds + cur * H2_STAGE;
         const char* sb = sa + H2_A;
 #pragma unroll
@@ -1025,12 +1013,48 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        if (kc + 1 < nk) {
-            store_a(cur ^ 1);
-            if (p.wraw) rw.store(lds + (cur ^ 1) * H2_STAGE + H2_A, tid / 4, rw_cg);
-        }
+    };
+
+    RawWeights rw;
+    const int rw_co = min(n0 + tid / 4, p.N - 1), rw_cg = tid % 4;
+    if constexpr (NS == 2) {
+        if (p.wraw) rw.load(p.wraw, rw_co, p.Cs, 0, rw_cg);
+        else issue_b(0, 0);
+        load_a(0);
+        store_a(0);
+        if (p.wraw) rw.store(lds + H2_A, tid / 4, rw_cg);
         v_wait<0>();
+        __syncthreads();
+        for (int kc = 0; kc < nk; ++kc) {
+            const int cur = kc & 1;
+            if (kc + 1 < nk) {
+                if (p.wraw) rw.load(p.wraw, rw_co, p.Cs, kc + 1, rw_cg);
+                else issue_b(kc + 1, cur ^ 1);
+                load_a(kc + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            compute(cur);
+            __builtin_amdgcn_sched_barrier(0);
+            if (kc + 1 < nk) {
+                store_a(cur ^ 1);
+                if (p.wraw) rw.store(lds + (cur ^ 1) * H2_STAGE + H2_A, tid / 4, rw_cg);
+            }
+            v_wait<0>();
+            __syncthreads();
+        }
+    } else {
+        // one stage: each chunk loads after every wave has read the previous one
+        for (int kc = 0; kc < nk; ++kc) {
+            if (kc > 0) __syncthreads();
+            if (p.wraw) rw.load(p.wraw, rw_co, p.Cs, kc, rw_cg);
+            else issue_b(kc, 0);
+            load_a(kc);
+            store_a(0);
+            if (p.wraw) rw.store(lds + H2_A, tid / 4, rw_cg);
+            v_wait<0>();
+            __syncthreads();
+            compute(0);
+        }
         __syncthreads();
     }
 
@@ -2526,8 +2550,15 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     }
     const dim3 grid((unsigned)((d.n + p.ipt - 1) / p.ipt * p.row_tiles), (unsigned)((N + HL_BN - 1) / HL_BN));
     if (fm2) {
-        if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_s2_kernel<TVK_F16, 2>), grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL((conv_halo_s2_kernel<TVK_BF16, 2>), grid, dim3(256), 0, s, p);
+        // one LDS stage (two workgroups a CU) where the grid has more workgroups than CUs
+        const bool one = (int64_t)grid.x * grid.y > 256;
+        if (one) {
+            if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_s2_kernel<TVK_F16, 2, 1>), grid, dim3(256), 0, s, p);
+            else hipLaunchKernelGGL((conv_halo_s2_kernel<TVK_BF16, 2, 1>), grid, dim3(256), 0, s, p);
+        } else {
+            if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_s2_kernel<TVK_F16, 2, 2>), grid, dim3(256), 0, s, p);
+            else hipLaunchKernelGGL((conv_halo_s2_kernel<TVK_BF16, 2, 2>), grid, dim3(256), 0, s, p);
+        }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
         return TVK_OK;
