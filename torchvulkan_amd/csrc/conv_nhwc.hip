@@ -671,7 +671,10 @@ __device__ inline int hl_swz(int row) { return ((row >> 2) & 1) * 2; }
 struct RawWeights {
     u32x4 v[9];
     __device__ inline void load(const uint16_t* w, int co, int Cs, int kc, int cg) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(w + ((int64_t)co * Cs + kc * 32 + cg * 8) * 9);
+        load_at(w + ((int64_t)co * Cs + kc * 32 + cg * 8) * 9);
+    }
+    __device__ inline void load_at(const uint16_t* run) {   // the 72-half run (16-byte aligned)
+        const u32x4* src = reinterpret_cast<const u32x4*>(run);
 #pragma unroll
         for (int j = 0; j < 9; ++j) v[j] = src[j];
     }
@@ -689,7 +692,27 @@ struct RawWeights {
             *reinterpret_cast<u32x4*>(rows + row * 64 + ((cg ^ hl_swz(row)) * 16)) = u32x4{o[0], o[1], o[2], o[3]};
         }
     }
+    // Grad input: the run holds 8 input channels (its output columns) of one
+    // output channel (a k row), and the B tile is kept k-major, [tap][32 k
+    // rows][64 columns], 128-byte rows read back with transposed reads
+    // (ds_read_b64_tr_b16); k row kr, 16-byte chunk cg at cg ^ hl_swz_t(kr)
+    __device__ inline void store_t(char* rows, int kr, int cg) const;
 };
+
+// Chunk swizzle of the grad input's k-major weight rows (128 bytes, 8 chunks):
+// a transposed fragment read takes k rows {0-3, 8-11} (+ 4) at one chunk pair,
+// which this spreads over the 8 32-byte bank groups of a 256-byte window.
+__device__ inline int hl_swz_t(int kr) { return (((kr >> 1) & 1) | ((kr >> 2) & 2)) * 2; }
+
+__device__ inline void RawWeights::store_t(char* rows, int kr, int cg) const {
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+        uint32_t o[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) o[m] = half_at(2 * m * 9 + t) | (half_at((2 * m + 1) * 9 + t) << 16);
+        *reinterpret_cast<u32x4*>(rows + (t * 32 + kr) * 128 + ((cg ^ hl_swz_t(kr)) * 16)) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+}
 
 // 3x3 weight w[co][c][9] -> forward wout[co][t][c] or grad input
 // wout[c][t][co], the reduced channel count a multiple of 8: a thread gathers
@@ -714,7 +737,9 @@ __global__ __launch_bounds__(256) void weight_permute9_kernel(const uint16_t* w,
     }
 }
 
-template <int DT, int PX>
+// TB: grad input with its weight rows gathered from the weight as given
+// (k-major B tile, transposed fragment reads); 256-pixel tiles only.
+template <int DT, int PX, bool TB = false>
 __global__ __launch_bounds__(PX) void conv_halo_kernel(HaloArgs p) {
     typedef HaloCfg<PX> G;
     constexpr int NT = G::NT, NS = G::NS, STG = G::STAGE, A_BYTES = G::A, NQ = G::NQ, NW = G::NW;
@@ -808,8 +833,24 @@ __global__ __launch_bounds__(PX) void conv_halo_kernel(HaloArgs p) {
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int row = t * HL_BN + j * 16 + lane % 16;
-                fb[j] = *reinterpret_cast<const u32x4*>(sb + row * 64 + ((g ^ hl_swz(row)) * 16));
+                if constexpr (TB) {
+                    // source lane s of group g points at k row 8g + 4rr + s/4, columns
+                    // 4(s%4)..+3 of this fragment; the transpose hands lane s the four
+                    // k values of its column
+                    const int sl = lane % 16, col = j * 16 + (sl % 4) * 4;
+#pragma unroll
+                    for (int rr = 0; rr < 2; ++rr) {
+                        const int kr = g * 8 + rr * 4 + sl / 4;
+                        TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(TVK_LDS const char*)(
+                            sb + (t * 32 + kr) * 128 + (((col / 8) ^ hl_swz_t(kr)) * 16) + (col % 8) * 2);
+                        const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+                        fb[j][rr * 2] = w.x;
+                        fb[j][rr * 2 + 1] = w.y;
+                    }
+                } else {
+                    const int row = t * HL_BN + j * 16 + lane % 16;
+                    fb[j] = *reinterpret_cast<const u32x4*>(sb + row * 64 + ((g ^ hl_swz(row)) * 16));
+                }
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -818,6 +859,7 @@ __global__ __launch_bounds__(PX) void conv_halo_kernel(HaloArgs p) {
         }
     };
 
+    static_assert(!TB || PX == 256, "the k-major weight tile is gathered on 256 threads");
     if constexpr (NS == 2) {
         issue_b(0, 0);
         load_a(0);
@@ -841,13 +883,17 @@ __global__ __launch_bounds__(PX) void conv_halo_kernel(HaloArgs p) {
         // one stage: each chunk loads after every wave has read the previous one
         RawWeights rw;
         const int rw_co = min(n0 + tid / 4, p.N - 1), rw_cg = tid % 4;
+        // grad input: k row tid / 8 of the chunk, input channels 8 (tid % 8) .. + 7 of the tile
+        const int rt_kr = tid / 8, rt_cg = tid % 8, rt_c0 = min(n0 + rt_cg * 8, p.N - 8);
         for (int kc = 0; kc < nk; ++kc) {
             if (kc > 0) __syncthreads();
-            if (p.wraw) rw.load(p.wraw, rw_co, p.Cs, kc, rw_cg);
+            if constexpr (TB) rw.load_at(p.wraw + ((int64_t)(kc * 32 + rt_kr) * p.N + rt_c0) * 9);
+            else if (p.wraw) rw.load(p.wraw, rw_co, p.Cs, kc, rw_cg);
             else issue_b(kc, 0);
             load_a(kc);
             store_a(0);
-            if (p.wraw) rw.store(lds + A_BYTES, tid / 4, rw_cg);
+            if constexpr (TB) rw.store_t(lds + A_BYTES, rt_kr, rt_cg);
+            else if (p.wraw) rw.store(lds + A_BYTES, tid / 4, rw_cg);
             v_wait<0>();
             __syncthreads();
             compute(0);
@@ -2484,8 +2530,11 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     const uint16_t* w16 = static_cast<const uint16_t*>(d.weight);
     // the forward kernels on 256 threads (the stride-2 one, and the stride-1 one
     // on 256-pixel tiles) gather their weight rows from the weight as given
-    const bool raw = mode == 0 && (reinterpret_cast<uintptr_t>(w16) & 15) == 0 &&
-                     (conv_halo_s2_fm(d, nullptr) != 0 || halo_s1_px(d, N) == 256);
+    // and so does the stride-1 grad input on 256-pixel tiles (k-major tile)
+    const bool tb = mode == 1 && conv_halo_dgrad_s2_tp(d, nullptr, nullptr, nullptr) == 0 && halo_s1_px(d, N) == 256 &&
+                    N % 8 == 0 && (reinterpret_cast<uintptr_t>(w16) & 15) == 0;
+    const bool raw = tb || (mode == 0 && (reinterpret_cast<uintptr_t>(w16) & 15) == 0 &&
+                            (conv_halo_s2_fm(d, nullptr) != 0 || halo_s1_px(d, N) == 256));
     char* ws = nullptr;
     if (!raw) {
         ws = static_cast<char*>(scratch.get(wt_b, s));
@@ -2563,7 +2612,10 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
         if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
         return TVK_OK;
     }
-    if (px == 256) {
+    if (px == 256 && tb) {
+        if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_kernel<TVK_F16, 256, true>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((conv_halo_kernel<TVK_BF16, 256, true>), grid, dim3(256), 0, s, p);
+    } else if (px == 256) {
         if (d.dtype == TVK_F16) hipLaunchKernelGGL((conv_halo_kernel<TVK_F16, 256>), grid, dim3(256), 0, s, p);
         else hipLaunchKernelGGL((conv_halo_kernel<TVK_BF16, 256>), grid, dim3(256), 0, s, p);
     } else {
