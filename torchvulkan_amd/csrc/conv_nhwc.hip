@@ -697,12 +697,29 @@ struct RawWeights {
     // rows][64 columns], 128-byte rows read back with transposed reads
     // (ds_read_b64_tr_b16); k row kr, 16-byte chunk cg at cg ^ hl_swz_t(kr)
     __device__ inline void store_t(char* rows, int kr, int cg) const;
+    // the same with 64-byte rows (32 columns)
+    __device__ inline void store_t64(char* rows, int kr, int cg) const;
 };
 
 // Chunk swizzle of the grad input's k-major weight rows (128 bytes, 8 chunks):
 // a transposed fragment read takes k rows {0-3, 8-11} (+ 4) at one chunk pair,
 // which this spreads over the 8 32-byte bank groups of a 256-byte window.
 __device__ inline int hl_swz_t(int kr) { return (((kr >> 1) & 1) | ((kr >> 2) & 2)) * 2; }
+
+// With 64-byte rows (four per 256-byte window) the pair of k rows kr and
+// kr + 8 of a transposed read shares a window position; flipping the chunk
+// pair for kr & 8 separates them.
+__device__ inline int hl_swz_t64(int kr) { return ((kr >> 3) & 1) * 2; }
+
+__device__ inline void RawWeights::store_t64(char* rows, int kr, int cg) const {
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+        uint32_t o[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) o[m] = half_at(2 * m * 9 + t) | (half_at((2 * m + 1) * 9 + t) << 16);
+        *reinterpret_cast<u32x4*>(rows + (t * 32 + kr) * 64 + ((cg ^ hl_swz_t64(kr)) * 16)) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+}
 
 __device__ inline void RawWeights::store_t(char* rows, int kr, int cg) const {
 #pragma unroll
@@ -1155,7 +1172,9 @@ __global__ __launch_bounds__(256) void conv_halo_s2_kernel(HaloArgs p) {
 constexpr int D2_A = 13312;   // ipt (tr + 1) (Wo + 1) pixels x 64 bytes: 3 x 65 at Wo = 64, 18 x 9 at Wo = 8
 constexpr int D2_STAGE = D2_A + HL_B;
 
-template <int DT, int TP, int BN>
+// TB: weight rows gathered from the weight as given into a k-major tile
+// ([tap][32 k rows][BN columns]) read by transposed fragment reads.
+template <int DT, int TP, int BN, bool TB = false>
 __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
     constexpr int FMW = TP / 32;   // A fragments a wave (TP / 2 positions)
     constexpr int FN = BN / 16;    // B fragments (input-channel columns)
@@ -1240,16 +1259,32 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    issue_b(0, 0);
+    // k-major tile: task tid (< 32 BN / 8) = k row tid / (BN / 8), input channels 8 (tid % (BN / 8)) .. + 7
+    constexpr int RTASKS = 32 * BN / 8;
+    RawWeights rw;
+    const int rt_kr = tid / (BN / 8), rt_cg = tid % (BN / 8), rt_c0 = min(n0 + rt_cg * 8, p.N - 8);
+    auto raw_load = [&](int kc) {
+        if (tid < RTASKS) rw.load_at(p.wraw + ((int64_t)(kc * 32 + rt_kr) * p.N + rt_c0) * 9);
+    };
+    auto raw_store = [&](int st) {
+        if (tid >= RTASKS) return;
+        char* rows = lds + st * D2_STAGE + D2_A;
+        if constexpr (BN == 64) rw.store_t(rows, rt_kr, rt_cg);
+        else rw.store_t64(rows, rt_kr, rt_cg);
+    };
+    if constexpr (TB) raw_load(0);
+    else issue_b(0, 0);
     load_a(0);
     store_a(0);
+    if constexpr (TB) raw_store(0);
     v_wait<0>();
     __syncthreads();
     const int na = ph ? 2 : 1, nb = pw ? 2 : 1;
     for (int kc = 0; kc < nk; ++kc) {
         const int cur = kc & 1;
         if (kc + 1 < nk) {
-            issue_b(kc + 1, cur ^ 1);
+            if constexpr (TB) raw_load(kc + 1);
+            else issue_b(kc + 1, cur ^ 1);
             load_a(kc + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1267,8 +1302,23 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
                 }
 #pragma unroll
                 for (int j = 0; j < FN; ++j) {
-                    const int row = t * BN + j * 16 + lane % 16;
-                    fb[j] = *reinterpret_cast<const u32x4*>(sb + row * 64 + ((g ^ hl_swz(row)) * 16));
+                    if constexpr (TB) {
+                        // lane s of group g points at k row 8g + 4rr + s/4, columns 4(s%4)..+3
+                        const int sl = lane % 16, col = j * 16 + (sl % 4) * 4;
+#pragma unroll
+                        for (int rr = 0; rr < 2; ++rr) {
+                            const int kr = g * 8 + rr * 4 + sl / 4;
+                            const int sw = BN == 64 ? hl_swz_t(kr) : hl_swz_t64(kr);
+                            TVK_LDS s16x4* ptr = (TVK_LDS s16x4*)(uintptr_t)(TVK_LDS const char*)(
+                                sb + (t * 32 + kr) * (2 * BN) + (((col / 8) ^ sw) * 16) + (col % 8) * 2);
+                            const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+                            fb[j][rr * 2] = w.x;
+                            fb[j][rr * 2 + 1] = w.y;
+                        }
+                    } else {
+                        const int row = t * BN + j * 16 + lane % 16;
+                        fb[j] = *reinterpret_cast<const u32x4*>(sb + row * 64 + ((g ^ hl_swz(row)) * 16));
+                    }
                 }
 #pragma unroll
                 for (int i = 0; i < FMW; ++i)
@@ -1277,7 +1327,10 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (kc + 1 < nk) store_a(cur ^ 1);
+        if (kc + 1 < nk) {
+            store_a(cur ^ 1);
+            if constexpr (TB) raw_store(cur ^ 1);
+        }
         v_wait<0>();
         __syncthreads();
     }
@@ -2530,9 +2583,10 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
     const uint16_t* w16 = static_cast<const uint16_t*>(d.weight);
     // the forward kernels on 256 threads (the stride-2 one, and the stride-1 one
     // on 256-pixel tiles) gather their weight rows from the weight as given
-    // and so does the stride-1 grad input on 256-pixel tiles (k-major tile)
-    const bool tb = mode == 1 && conv_halo_dgrad_s2_tp(d, nullptr, nullptr, nullptr) == 0 && halo_s1_px(d, N) == 256 &&
-                    N % 8 == 0 && (reinterpret_cast<uintptr_t>(w16) & 15) == 0;
+    // and so do the grad inputs (stride 2, and stride 1 on 256-pixel tiles)
+    // into a k-major tile
+    const bool tb = mode == 1 && N % 8 == 0 && (reinterpret_cast<uintptr_t>(w16) & 15) == 0 &&
+                    (conv_halo_dgrad_s2_tp(d, nullptr, nullptr, nullptr) != 0 || halo_s1_px(d, N) == 256);
     const bool raw = tb || (mode == 0 && (reinterpret_cast<uintptr_t>(w16) & 15) == 0 &&
                             (conv_halo_s2_fm(d, nullptr) != 0 || halo_s1_px(d, N) == 256));
     char* ws = nullptr;
@@ -2565,16 +2619,20 @@ tvk_status conv_halo_run(const tvk_conv_desc& d, int mode, const char* who) {
         p.wt_bytes = (int)wt_b;
         const dim3 grid((unsigned)((d.n + ipt2 - 1) / ipt2 * p.row_tiles), (unsigned)((N + bn2 - 1) / bn2));
         const bool f16 = d.dtype == TVK_F16;
-        if (tp2 == 128 && bn2 == 64) {
-            if (f16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, 128, 64>), grid, dim3(512), 0, s, p);
-            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, 128, 64>), grid, dim3(512), 0, s, p);
-        } else if (tp2 == 128) {
-            if (f16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, 128, 32>), grid, dim3(512), 0, s, p);
-            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, 128, 32>), grid, dim3(512), 0, s, p);
-        } else {
-            if (f16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, 64, 64>), grid, dim3(512), 0, s, p);
-            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, 64, 64>), grid, dim3(512), 0, s, p);
-        }
+#define TVK_D2(TP_, BN_)                                                                                        \
+    do {                                                                                                        \
+        if (tb) {                                                                                               \
+            if (f16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, TP_, BN_, true>), grid, dim3(512), 0, s, p);   \
+            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, TP_, BN_, true>), grid, dim3(512), 0, s, p);      \
+        } else {                                                                                                \
+            if (f16) hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_F16, TP_, BN_>), grid, dim3(512), 0, s, p);         \
+            else hipLaunchKernelGGL((conv_halo_dgrad_s2_kernel<TVK_BF16, TP_, BN_>), grid, dim3(512), 0, s, p);            \
+        }                                                                                                       \
+    } while (0)
+        if (tp2 == 128 && bn2 == 64) TVK_D2(128, 64);
+        else if (tp2 == 128) TVK_D2(128, 32);
+        else TVK_D2(64, 64);
+#undef TVK_D2
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
         return TVK_OK;
