@@ -582,11 +582,43 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     ms, _ = timed(bmm_step, steps, warmup, stream)
     bmm_fl = 2 * 2 * Bq * H * L * L * D
     bmm_by = 2 * (4 * Bq * L * H * D + 2 * Bq * H * L * L)
+    out["c3_head_strided_bmm_per_sequence_us"] = round(ms * 1e3, 2)
+    out["c3_head_strided_bmm_per_sequence_kernels"] = [gemm_plan_of(_abi, hd[0]), gemm_plan_of(_abi, hd[1])]
+    out["c3_head_strided_bmm_per_sequence_roofline_frac"] = round(bound_us(bmm_fl, bmm_by) / (ms * 1e3), 4)
+    del hd, hrefs
+
+    # the same products as torch.matmul runs them on the 4-D views [B, H, L, D] (the math SDPA):
+    # batch and head do not merge into one stride, so matmul's reshape to [B*H, ., .] copies q,
+    # k^T and v (the scores are already contiguous), then one bmm of batch B*H each
+    qc = torch.empty((Bq * H, L, D), dtype=torch.float16, device=dev)
+    ktc = torch.empty((Bq * H, D, L), dtype=torch.float16, device=dev)
+    vc = torch.empty((Bq * H, L, D), dtype=torch.float16, device=dev)
+    sc = torch.empty((Bq * H, L, L), dtype=torch.float16, device=dev)
+    oc = torch.empty((Bq * H, L, D), dtype=torch.float16, device=dev)
+    cds = [_abi.make_copy_desc(qs.transpose(1, 2), qc.view(Bq, H, L, D), stream=s),
+           _abi.make_copy_desc(ks.permute(0, 2, 3, 1), ktc.view(Bq, H, D, L), stream=s),
+           _abi.make_copy_desc(vs.transpose(1, 2), vc.view(Bq, H, L, D), stream=s)]
+    gds = [_abi.make_gemm_desc(qc, ktc, sc, stream=s), _abi.make_gemm_desc(sc, vc, oc, stream=s)]
+    crefs, grefs = [C.byref(d) for d in cds], [C.byref(d) for d in gds]
+
+    def matmul_step():
+        for r in crefs:
+            st_ = lib.tvk_copy(r)
+            if st_:
+                _abi.check(st_)
+        for r in grefs:
+            st_ = lib.tvk_gemm(r)
+            if st_:
+                _abi.check(st_)
+
+    ms, _ = timed(matmul_step, steps, warmup, stream)
+    copy_by = 3 * 2 * 2 * Bq * L * H * D
     out["c3_head_strided_bmm_us"] = round(ms * 1e3, 2)
+    out["c3_head_strided_bmm_path"] = "torch.matmul on [B, H, L, D] views: 3 reshape copies + 2 bmm of batch B*H"
+    out["c3_head_strided_bmm_kernels"] = [gemm_plan_of(_abi, gds[0]), gemm_plan_of(_abi, gds[1])]
+    out["c3_head_strided_bmm_roofline_frac"] = round(bound_us(bmm_fl, bmm_by + copy_by) / (ms * 1e3), 4)
     progress("C3 head-strided bmm done")
-    out["c3_head_strided_bmm_kernels"] = [gemm_plan_of(_abi, hd[0]), gemm_plan_of(_abi, hd[1])]
-    out["c3_head_strided_bmm_roofline_frac"] = round(bound_us(bmm_fl, bmm_by) / (ms * 1e3), 4)
-    del qs, ks, vs, ss, os_, hd, hrefs
+    del qs, ks, vs, ss, os_, qc, ktc, vc, sc, oc, cds, gds, crefs, grefs
 
     # ---- C3 attention: fused forward, batch 32, 8 query / 2 kv heads, seq 256, head_dim 64, causal
     qa = torch.randn((32, 8, 256, 64), generator=g).to(torch.float16).to(dev)

@@ -68,9 +68,11 @@ def test_c1_fp32_mm_1024_bit_exact(gpu):
 
 @pytest.mark.parametrize("dtype", F16_TYPES)
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
-@pytest.mark.parametrize("shape", [(256, 256, 256), (300, 520, 136), (64, 80, 24)])
+@pytest.mark.parametrize("shape", [(256, 256, 256), (300, 520, 136), (64, 80, 24), (1024, 1024, 160)])
 def test_integer_exact_all_layouts(gpu, dtype, ta, tb, shape):
-    # integer operands: every summation order gives identical bits
+    # integer operands: every summation order gives identical bits. The first
+    # three have fewer 128x128 tiles than a quarter of the CUs (64x64 tiles);
+    # the last takes the 128x128 kernels
     M, N, K = shape
     a = randint((K, M) if ta else (M, K), dtype, 10)
     b = randint((N, K) if tb else (K, N), dtype, 11)
@@ -325,6 +327,7 @@ def test_c3_head_strided_bmm(gpu, dtype):
     qh = q.view(256, 8, 64).transpose(0, 1)            # [8, 256, 64] strides (64, 512, 1)
     kt = k.view(256, 8, 64).transpose(0, 1).transpose(1, 2)  # [8, 64, 256] strides (64, 1, 512)
     got, plan = run(gpu, qh, kt, (8, 256, 256), dtype)
+    assert plan == "gemm16_mfma_64x64"
     assert_close(got, oracle_mm(qh, kt, dtype), dtype, "QK^T " + plan)
     p = randn((8, 256, 256), dtype, 52, std=0.1)
     v = randn((256, 8 * 64), dtype, 53)
