@@ -191,6 +191,10 @@ HALO_CASES = [
     dict(n=2, cin=64, cout=96, k=3, s=1, p=1, hw=(16, 16)),
     dict(n=1, cin=128, cout=64, k=3, s=1, p=1, hw=(64, 8)),
     dict(n=3, cin=64, cout=32, k=3, s=1, p=1, hw=(8, 32)),
+    # grad weight in 32-output-channel blocks (one 64-channel input block and
+    # at most 64 output channels): a partial second block, and 16-wide rows
+    dict(n=3, cin=64, cout=48, k=3, s=1, p=1, hw=(16, 32)),
+    dict(n=2, cin=64, cout=64, k=3, s=1, p=1, hw=(32, 16)),
     # stride-2 forward halo kernel (de-interleaved columns, 128-pixel tiles):
     # a partial row tile, a partial output-channel tile, three k chunks, and
     # 64-pixel images two a tile with the batch's last tile half empty

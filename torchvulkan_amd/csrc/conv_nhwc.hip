@@ -1365,7 +1365,7 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
 }
 
 // Grad weight of the same convolution (stride 1, 3x3, padding 1) from NCHW:
-// a workgroup takes 64 input channels x 64 output channels x all 9 taps and
+// a workgroup takes 64 input channels x BN (64 or 32) output channels x all 9 taps and
 // sums its share of 256-pixel tiles (TR x W output rows of one image, H % TR
 // == 0, W = 16 or 32) into float32 partials [split][(tap, channel)][output
 // channel]: C[c][co] += sum_p x(p + tap)[c] * dy[co][p]. The 36 row fragments
@@ -1377,9 +1377,12 @@ __global__ __launch_bounds__(512) void conv_halo_dgrad_s2_kernel(HaloArgs p) {
 //     banks); the row pitch W + 4 makes a k step (32 pixels) a multiple of 4
 //     pixels, so every fragment address of step s is step 0's plus a constant
 //     (an instruction offset: no address arithmetic in the k loop);
-//   dy [32 pixel chunks][64 output channels][8 pixels]: a fragment is 16 lanes
+//   dy [32 pixel chunks][BN output channels][8 pixels]: a fragment is 16 lanes
 //     x 16 contiguous bytes, its offset again linear in the step; one LDS-DMA
-//     instruction loads one pixel chunk of the 64 channels.
+//     instruction loads 1 KB, one pixel chunk of 64 channels or two of 32.
+// With 32 output channels a workgroup sums twice the tiles of the 64-channel
+// form for the same grid, which halves the float32 partials (the 64 -> 64
+// layer's are otherwise 256 planes of 147 KB, written and read back once).
 // A fragments are transposed reads (ds_read_b64_tr_b16) at the tap's shift.
 // Two stages: tile i + 1 loads while i computes.
 constexpr int HG_A = 46080;            // (TR + 2) * (W + 4) pixels x 128 bytes: 10 x 36 at W = 32, 18 x 20 at W = 16
@@ -1396,15 +1399,16 @@ struct HaloWgArgs {
 
 __device__ inline int hg_swz(int hp) { return (hp & 3) * 2; }
 
-template <int DT, int W>
+template <int DT, int W, int BN = 64>
 __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
+    constexpr int FNB = BN / 16;   // column fragments; also the dy DMA instructions a wave
     constexpr int TR = 256 / W, WP = W + 4, STEP = (32 / W) * WP;   // halo pixels per k step
     static_assert(STEP % 4 == 0 && (TR + 2) * WP * 128 <= HG_A, "halo layout");
     __shared__ __attribute__((aligned(1024))) char lds[2 * HG_STAGE];
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds);
     const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const int g = lane / 16, sl = lane % 16;
-    const int c0 = blockIdx.y * 64, n0 = blockIdx.z * 64;
+    const int c0 = blockIdx.y * 64, n0 = blockIdx.z * BN;
     const int HWs = p.H * W;
     // row fragment k of this wave: rf = wave + 8k (k < 4, or 5 for waves 0-3), tap rf / 4, channels (rf % 4) * 16
     const bool five = wave < 4;
@@ -1447,17 +1451,20 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
         }
     };
 
-    // dy: DMA instruction q (wave * 4 + 0..3) loads pixel chunk q: lane = output channel
+    // dy: DMA instruction u = wave * FNB + q loads 1 KB: pixel chunk u with lane =
+    // output channel (BN = 64), or chunks 2u, 2u + 1 with lane = chunk half x 32
+    // + output channel (BN = 32)
     const i32x4 rb = v_rsrc(p.dy, p.dy_bytes);
-    const uint32_t b_lane = (uint32_t)(min(n0 + lane, p.cout - 1) * HWs * 2);
+    const uint32_t b_lane = BN == 64 ? (uint32_t)(min(n0 + lane, p.cout - 1) * HWs * 2)
+                                     : (uint32_t)(min(n0 + lane % 32, p.cout - 1) * HWs * 2 + (lane / 32) * 16);
     auto issue_b = [&](int tile, int st) {
         const int img = tile / p.tiles_per_img, h0 = (tile - img * p.tiles_per_img) * TR;
         const uint32_t toff = (uint32_t)((((int64_t)img * p.cout) * HWs + (int64_t)h0 * W) * 2);
         const uint32_t base = lds0 + (uint32_t)(st * HG_STAGE + HG_A);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int chunk = wave * 4 + q;
-            v_dma16(rb, base + (uint32_t)(chunk * 1024), b_lane + toff + (uint32_t)(chunk * 16));
+        for (int q = 0; q < FNB; ++q) {
+            const int u = wave * FNB + q;
+            v_dma16(rb, base + (uint32_t)(u * 1024), b_lane + toff + (uint32_t)(u * (1024 / BN)));
         }
     };
 
@@ -1475,13 +1482,13 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
             a_off[k][rr] = hp * 128 + (((col / 8) ^ hg_swz(hp)) * 16) + (col % 8) * 2;
         }
     }
-    const int b_off = g * 1024 + sl * 16;
+    const int b_off = g * (BN * 16) + sl * 16;
 
-    f32x4 acc[5][4];
+    f32x4 acc[5][FNB];
 #pragma unroll
     for (int i = 0; i < 5; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < FNB; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     int tile = blockIdx.x;
     if (tile < p.ntiles) {
@@ -1517,14 +1524,14 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
                 }
             }
             // B: columns = 16 output channels, k = the same 32 pixels
-            u32x4 fb[4];
+            u32x4 fb[FNB];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) fb[j] = *reinterpret_cast<const u32x4*>(sb + ks * 4096 + j * 256);
+            for (int j = 0; j < FNB; ++j) fb[j] = *reinterpret_cast<const u32x4*>(sb + ks * (64 * BN) + j * 256);
 #pragma unroll
             for (int i = 0; i < 5; ++i) {
                 if (i == 4 && !five) break;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
+                for (int j = 0; j < FNB; ++j) acc[i][j] = vmfma<DT>(fa[i], fb[j], acc[i][j]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1540,7 +1547,7 @@ __global__ __launch_bounds__(512) void conv_halo_wgrad_kernel(HaloWgArgs p) {
         if (i == 4 && !five) break;
         const int t = (wave + 8 * i) / 4;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < FNB; ++j) {
             const int co = n0 + j * 16 + sl;
             if (co >= p.cout) continue;
 #pragma unroll
@@ -2530,7 +2537,11 @@ tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
     p.tiles_per_img = H / (256 / W);
     p.ntiles = (int)d.n * p.tiles_per_img;
     p.dy_bytes = (int)(d.n * cout * H * W * 2);
-    const int cb = cin / 64, nb = (cout + 63) / 64;
+    const int cb = cin / 64;
+    // 32 output channels a workgroup where one 64 x 64 block covers the weight
+    // (half the partials for the same grid); 64 otherwise
+    const int bn = (cb * ((cout + 63) / 64) == 1 && cout > 32) ? 32 : 64;
+    const int nb = (cout + bn - 1) / bn;
     // about 256 workgroups (one a CU), each summing at least 2 tiles
     p.split = std::max(1, std::min(p.ntiles / 2, 256 / (cb * nb)));
     const size_t part_b = (size_t)p.split * 9 * cin * cout * sizeof(float);
@@ -2539,13 +2550,16 @@ tvk_status conv_halo_wgrad_run(const tvk_conv_desc& d, const char* who) {
     p.part = reinterpret_cast<float*>(ws);
     const dim3 grid((unsigned)p.split, (unsigned)cb, (unsigned)nb);
     const bool f16 = d.dtype == TVK_F16;
-    if (W == 32) {
-        if (f16) hipLaunchKernelGGL((conv_halo_wgrad_kernel<TVK_F16, 32>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((conv_halo_wgrad_kernel<TVK_BF16, 32>), grid, dim3(512), 0, s, p);
-    } else {
-        if (f16) hipLaunchKernelGGL((conv_halo_wgrad_kernel<TVK_F16, 16>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((conv_halo_wgrad_kernel<TVK_BF16, 16>), grid, dim3(512), 0, s, p);
-    }
+#define TVK_HW1(W_, BN_)                                                                                          \
+    do {                                                                                                          \
+        if (f16) hipLaunchKernelGGL((conv_halo_wgrad_kernel<TVK_F16, W_, BN_>), grid, dim3(512), 0, s, p);       \
+        else hipLaunchKernelGGL((conv_halo_wgrad_kernel<TVK_BF16, W_, BN_>), grid, dim3(512), 0, s, p);          \
+    } while (0)
+    if (W == 32 && bn == 32) TVK_HW1(32, 32);
+    else if (W == 32) TVK_HW1(32, 64);
+    else if (bn == 32) TVK_HW1(16, 32);
+    else TVK_HW1(16, 64);
+#undef TVK_HW1
     // partials [split][(tap, channel)][output channel] -> dW[co][c][tap]
     const int M = 9 * cin, total = M * cout;
     int sg = 1;
