@@ -142,6 +142,58 @@ def test_dma_kernel_128_tiles_integer_exact(gpu, dtype, ta, tb, shape):
     assert np.array_equal(got, _exact_ref(a, b, dtype)), plan
 
 
+# C-in through the 256x256 kernel's epilogue (16-byte bias chunks requested
+# before the first pass): K of 3, 4 and 32 ring stages; ragged M, a partial
+# 8-column N tile, bias broadcast over the batch or over the rows, a bias of
+# padded rows, relu
+BIAS_RING_CASES = [
+    # batch, M, N, K, bias kind, activation
+    (3, 300, 520, 96, "full", 0),
+    (2, 512, 512, 128, "batch_broadcast", 0),
+    (1, 1000, 776, 1024, "row_broadcast", 1),
+    (2, 256, 264, 256, "padded_rows", 0),
+]
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("case", BIAS_RING_CASES, ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}x{c[3]}-{c[4]}")
+def test_dma256_c_in_epilogue(gpu, dtype, case):
+    B, M, N, K, kind, act = case
+    a = randint((B, M, K), dtype, 33, -3, 4)
+    b = randint((B, K, N), dtype, 34, -3, 4)
+    if kind == "full":
+        bias_h = randint((B, M, N), dtype, 35)
+        bias = bias_h.to(DEV)
+    elif kind == "batch_broadcast":
+        bias_h = randint((M, N), dtype, 35).expand(B, M, N)
+        bias = bias_h[0].to(DEV).expand(B, M, N)
+    elif kind == "row_broadcast":
+        bias_h = randint((N,), dtype, 35).expand(B, M, N)
+        bias = bias_h[0, 0].to(DEV).expand(B, M, N)
+    else:
+        full = randint((B, M, N + 8), dtype, 35)
+        bias_h = full[:, :, :N]
+        bias = full.to(DEV)[:, :, :N]
+    da, db = a.to(DEV), b.to(DEV)
+    c = torch.empty((B, M, N), dtype=dtype, device=DEV)
+    kw = dict(bias=bias, alpha=0.5, beta=2.0, activation=act)
+    gpu.gemm_choose(da, db, c, "gemm16_dma_256x256", **kw)
+    try:
+        c.fill_(float("nan"))
+        gpu.gemm(da, db, c, **kw)
+        torch.cuda.synchronize()
+        assert gpu.gemm_plan(da, db, c, **kw) == "gemm16_dma_256x256"
+    finally:
+        gpu.tune_reset()
+    # integer operands: the product, alpha * it + beta * bias and relu are exact
+    # in float32, so the one rounding to the dtype gives the reference's bits
+    r = 0.5 * (a.double().numpy() @ b.double().numpy()) + 2.0 * bias_h.double().numpy()
+    if act == 1:
+        r = np.maximum(r, 0.0)
+    want = decode(to_np(torch.from_numpy(r).to(dtype)), dtype)
+    assert np.array_equal(decode(to_np(c), dtype), want)
+
+
 @pytest.mark.parametrize("dtype", F16_TYPES)
 def test_dma_kernel_128_tiles_batched_epilogue(gpu, dtype):
     # baddbmm-like: batched, C-in through the fused epilogue, alpha and beta

@@ -169,14 +169,17 @@ constexpr int dma_threads(int bm, int bn) { return 64 * ((bm == 256 && bn == 256
 
 // NS: stages in the ring (4, or 8 for 128x128 tiles whose loads need more
 // lookahead to cover memory latency: short K, one workgroup per CU).
-template <int DT, bool AK, bool BK, int BM, int BN, int NS>
+// BL: C-in staged through the ring (256x256 tiles with a bias; a variant of
+// its own because the bias loads' offsets cost the k loop registers).
+template <int DT, bool AK, bool BK, int BM, int BN, int NS, bool BL = false>
 __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArgs p) {
     constexpr int D_NS = NS;
     typedef DCfg<BM, BN> G;
     constexpr int D_BM = BM, D_BN = BN, D_NT = G::NT, D_FM = G::FM, D_FN = G::FN, D_WTM = G::WTM, D_WTN = G::WTN;
     constexpr int D_OPB = G::OPA, D_STB = G::STB, D_DPS = G::DS;
     static_assert(dma_threads(BM, BN) == G::NT, "thread count");
-    __shared__ __attribute__((aligned(1024))) char lds_raw[D_NS * D_STB];
+    // BL: 32 KB past the ring for the epilogue's float32 staging
+    __shared__ __attribute__((aligned(1024))) char lds_raw[D_NS * D_STB + (G::BIG && BL ? 32768 : 0)];
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(TVK_LDS char*)lds_raw);
     const int tid = threadIdx.x, lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const int wm = wave / G::WN, wn = wave % G::WN;
@@ -206,10 +209,34 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     // reading memory (past the end of K, a k-contiguous operand's addresses
     // run into its next row, and a split's into the next split's range).
     const i32x4 ra_none = dma_rsrc(A, 0), rb_none = dma_rsrc(B, 0);
+    // C-in through the ring (BL: 256x256 tiles; 16-byte bias and output rows,
+    // N a multiple of 8): the loads of stages nk .. nk + 3 bring the bias
+    // tile, 64 rows of 512 bytes a slot, instead of nothing, so it arrives
+    // with the operands rather than after the k loop
+    bool bias_lds = false;
+    i32x4 rbias{0, 0, 0, 0};
+    uint32_t bias_lane = 0;
+    if constexpr (G::BIG && BL) {
+        const char* Bias = reinterpret_cast<const char*>(p.bias) + (int64_t)b * p.sbias[0] * 2;
+        auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+        bias_lds = p.split <= 1 && p.has_bias && p.sbias[2] == 1 && p.sbias[1] % 8 == 0 && al16(Bias) && p.sc[2] == 1 &&
+                   p.sc[1] % 8 == 0 && al16(reinterpret_cast<const char*>(p.c) + (int64_t)b * p.sc[0] * 2) && p.N % 8 == 0 &&
+                   2 * ((int64_t)(p.M + 256) * p.sbias[1] + p.N) < (int64_t(1) << 31);
+        // an instruction's two rows start 2 u rows past its quarter's first: lane -> row lane / 32, chunk lane % 32
+        rbias = dma_rsrc(Bias + ((int64_t)m0 * p.sbias[1] + n0) * 2, bias_lds ? 2 * ((int64_t)(p.M - 1 - m0) * p.sbias[1] + p.N - n0) : 0);
+        bias_lane = (uint32_t)((lane / 32) * p.sbias[1] * 2 + (lane % 32) * 16);
+    }
     auto dma_one = [&](int kt, int q) {   // q-th load (of D_DPS) of this wave for stage kt
         const uint32_t slot = lds0 + (uint32_t)((kt % D_NS) * D_STB);
         const uint32_t kg = (uint32_t)(kt0 + kt);
         const bool live = kt < nk;
+        if constexpr (G::BIG && BL) {
+            if (!live && bias_lds) {
+                const int u = wave * D_DPS + q;
+                dma16(rbias, slot + (uint32_t)(u * 1024), bias_lane + (uint32_t)(((kt - nk) * 64 + 2 * u) * p.sbias[1] * 2));
+                return;
+            }
+        }
         if (q < G::DA) dma16(live ? ra : ra_none, slot + (uint32_t)((wave * G::DA + q) * 1024), da.off[q] + kg * da.kstep);
         else dma16(live ? rb : rb_none, slot + D_OPB + (uint32_t)((wave * G::DB + q - G::DA) * 1024), db.off[q - G::DA] + kg * db.kstep);
     };
@@ -289,6 +316,57 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     }
 
     __syncthreads();   // every wave is done with the ring: it now holds the output tile
+    if constexpr (G::BIG && BL) {
+        typedef typename elem<DT>::T T;
+        if (bias_lds) {
+            // 32 rows a pass: the waves holding them write their accumulators
+            // into a float32 tile past the ring ([32][256], 16-byte chunk c of
+            // row r at c ^ ((r >> 2) & 3) * 4: the four row groups of a write
+            // meet on distinct banks); then each thread finishes 8 columns of a
+            // row against its bias chunk from the ring and stores 16 bytes
+            float* et = reinterpret_cast<float*>(lds_raw + D_NS * D_STB);
+            T* Cb = reinterpret_cast<T*>(p.c) + (int64_t)b * p.sc[0];
+            auto et_at = [](int r, int col) { return r * 256 + (((col / 4) ^ (((r >> 2) & 3) * 4)) * 4) + col % 4; };
+#pragma unroll
+            for (int pass = 0; pass < 8; ++pass) {
+                if (wm == pass / 4) {
+#pragma unroll
+                    for (int ii = 0; ii < 2; ++ii) {
+                        const int i = (pass % 4) * 2 + ii;
+#pragma unroll
+                        for (int j = 0; j < D_FN; ++j)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                et[et_at(ii * 16 + (lane / 16) * 4 + r, wn * D_WTN + j * 16 + lane % 16)] = acc[i][j][r];
+                    }
+                }
+                __syncthreads();
+#pragma unroll
+                for (int jj = 0; jj < 32 * 32 / D_NT; ++jj) {
+                    const int q = tid + jj * D_NT, rl = q / 32, cc = (q % 32) * 8;
+                    const int rt = pass * 32 + rl, row = m0 + rt, col = n0 + cc;
+                    if (row >= p.M || col >= p.N) continue;
+                    const f32x4 lo = *reinterpret_cast<const f32x4*>(et + et_at(rl, cc));
+                    const f32x4 hi = *reinterpret_cast<const f32x4*>(et + et_at(rl, cc + 4));
+                    const u32x4 w = *reinterpret_cast<const u32x4*>(lds_raw + ((nk + rt / 64) % D_NS) * D_STB + (rt % 64) * 512 + cc * 2);
+                    const float a8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+                    uint32_t o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float b0 = elem<DT>::to_f32(__builtin_bit_cast(T, (uint16_t)(ww[e] & 0xffffu)));
+                        const float b1 = elem<DT>::to_f32(__builtin_bit_cast(T, (uint16_t)(ww[e] >> 16)));
+                        const uint16_t h0 = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(epilogue(a8[2 * e], p.alpha, 1, b0, p.beta, p.act)));
+                        const uint16_t h1 = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(epilogue(a8[2 * e + 1], p.alpha, 1, b1, p.beta, p.act)));
+                        o[e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    }
+                    st_nt(reinterpret_cast<u32x4*>(Cb + (int64_t)row * p.sc[1] + col), u32x4{o[0], o[1], o[2], o[3]});
+                }
+                __syncthreads();
+            }
+            return;
+        }
+    }
 
     // Output through LDS, 64 rows at a time. The waves write their float32
     // accumulators (layout of v_mfma_f32_16x16x32: lane l holds column l % 16,
@@ -394,6 +472,15 @@ void launch_dma_tile(GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s) {
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (p.N + BN - 1) / BN;
     const dim3 grid(p.tiles_m * p.tiles_n, p.batch, p.split > 1 ? p.split : 1), block(DCfg<BM, BN>::NT);
+    if constexpr (DCfg<BM, BN>::BIG) {
+        if (p.has_bias && p.split <= 1) {
+            if (a_kmajor && b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, true, BM, BN, NS, true>), grid, block, 0, s, p);
+            else if (a_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, false, BM, BN, NS, true>), grid, block, 0, s, p);
+            else if (b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, true, BM, BN, NS, true>), grid, block, 0, s, p);
+            else hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, false, BM, BN, NS, true>), grid, block, 0, s, p);
+            return;
+        }
+    }
     if (a_kmajor && b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, true, BM, BN, NS>), grid, block, 0, s, p);
     else if (a_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, true, false, BM, BN, NS>), grid, block, 0, s, p);
     else if (b_kmajor) hipLaunchKernelGGL((gemm16_dma_kernel<DT, false, true, BM, BN, NS>), grid, block, 0, s, p);
