@@ -532,7 +532,7 @@ __global__ __launch_bounds__(256) void repack16_kernel(const uint16_t* src, uint
 // host dispatch
 // ----------------------------------------------------------------------------
 
-enum class Kern { K0, GENERIC, SEQ256, SEQ128, SEQ64, MFMA256, MFMA256W8, MFMA128, MFMA64, SKINNY, DMA256, DMA128, DMA128R8 };
+enum class Kern { K0, GENERIC, SEQ256, SEQ128, SEQ64, MFMA256, MFMA256W8, MFMA128, MFMA64, SKINNY, DMA256, DMA128, DMA128R8, DMA128X256, DMA256X128 };
 
 struct Plan {
     Kern kern;
@@ -736,10 +736,11 @@ Plan make_plan(const tvk_gemm_desc& d) {
                            dma ? Kern::DMA128 : Kern::MFMA128))
                 return pl;
         }
-        // The LDS-ring kernel on 128x128 tiles, except for two k-contiguous
-        // operands with K <= 1024, where the register-staged kernel is ahead
-        // (measured 4-13% on the transformer and MLP shapes)
-        if (pl.vec && t128 >= 32 && !(pl.ak && pl.bk && d.K <= 1024) && dma_applies(repacked_args(d, pl), pl.ak, pl.bk)) {
+        // The LDS-ring kernel on 128x128 tiles; with two k-contiguous operands
+        // from 64 tiles up (13-18 % ahead of the register-staged kernel on
+        // 8192 x {512, 256, 96} x 512; on 8 x 256x256x64, 32 tiles, the 64x64
+        // tiles below are ahead of both)
+        if (pl.vec && t128 >= ((pl.ak && pl.bk) ? 64 : 32) && dma_applies(repacked_args(d, pl), pl.ak, pl.bk)) {
             pl.kern = Kern::DMA128;
             pl.name = "gemm16_dma_128x128";
         } else if (t128 < 64) {
@@ -803,7 +804,11 @@ std::vector<Plan> candidate_plans(const tvk_gemm_desc& d) {
     if (d.M >= 128 && d.N >= 128) {
         add(with_kern(lay, Kern::MFMA256W8, "gemm16_mfma_256x256_w8"));
         add(with_kern(lay, Kern::MFMA256, "gemm16_mfma_256x256"));
-        if (dma) add(with_kern(lay, Kern::DMA256, "gemm16_dma_256x256"));
+        if (dma) {
+            add(with_kern(lay, Kern::DMA256, "gemm16_dma_256x256"));
+            add(with_kern(lay, Kern::DMA128X256, "gemm16_dma_128x256"));
+            add(with_kern(lay, Kern::DMA256X128, "gemm16_dma_256x128"));
+        }
     }
     return out;
 }
@@ -990,14 +995,17 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixe
         case Kern::DMA256:
         case Kern::DMA128:
         case Kern::DMA128R8:
+        case Kern::DMA128X256:
+        case Kern::DMA256X128:
             if constexpr (DT != TVK_F32) {
                 if (pl.split > 1) {
                     q.part = reinterpret_cast<float*>(ws + rep_a + rep_b);
                     q.split = pl.split;
                     q.k_chunk = pl.k_chunk;
                 }
-                hipError_t e = launch_dma(DT, q, pl.ak, pl.bk, pl.kern == Kern::DMA256 ? 256 : 128, s,
-                                          pl.kern == Kern::DMA128R8 ? 8 : 4);
+                const int tile = pl.kern == Kern::DMA256 ? 256 : pl.kern == Kern::DMA128X256 ? DMA_TILE_128X256
+                                 : pl.kern == Kern::DMA256X128 ? DMA_TILE_256X128 : 128;
+                hipError_t e = launch_dma(DT, q, pl.ak, pl.bk, tile, s, pl.kern == Kern::DMA128R8 ? 8 : 4);
                 if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string("tvk_gemm: launch failed: ") + hipGetErrorString(e));
                 if (pl.split > 1) {
                     launch_split_reduce<DT>(q, s);

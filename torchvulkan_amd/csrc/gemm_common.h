@@ -280,7 +280,8 @@ __device__ inline u32x4 load_chunk(__amdgpu_buffer_rsrc_t r, bool row_ok, int64_
 // dma_applies: the operands meet its alignment and K granularity; launch_dma
 // returns hipSuccess or the launch error.
 bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor);
-// tile: 256 (256x256) or 128 (128x128)
+// tile: 256 (256x256), 128 (128x128), DMA_TILE_128X256 or DMA_TILE_256X128
+constexpr int DMA_TILE_128X256 = 1, DMA_TILE_256X128 = 2;
 hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, int tile, hipStream_t s, int stages = 4);
 
 // Channels-last convolution on the LDS ring (conv_nhwc.hip); mode 0 forward,

@@ -492,5 +492,7 @@ void launch_dma_tile(GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s) {
 // AGPR copies inside the k loop); the 256x256 ones keep the default form,
 // in which they allocate cleanly while the VGPR form spills.
 void launch_dma128(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s, int stages);
+// 128x256 (wide) and 256x128 tiles, 8 waves of 64x64 (gemm_dma128.hip, the same form)
+void launch_dma_rect(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, hipStream_t s, bool wide);
 
 }  // namespace tvk

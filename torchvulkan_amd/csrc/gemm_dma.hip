@@ -26,6 +26,10 @@ bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor) {
 }
 
 hipError_t launch_dma(int dtype, GemmArgs& p, bool a_kmajor, bool b_kmajor, int tile, hipStream_t s, int stages) {
+    if (tile == DMA_TILE_128X256 || tile == DMA_TILE_256X128) {
+        launch_dma_rect(dtype, p, a_kmajor, b_kmajor, s, tile == DMA_TILE_128X256);
+        return hipGetLastError();
+    }
     if (dtype == TVK_F16) {
         if (tile == 256) launch_dma_tile<TVK_F16, 256, 256, 4>(p, a_kmajor, b_kmajor, s);
         else launch_dma128(dtype, p, a_kmajor, b_kmajor, s, stages);
