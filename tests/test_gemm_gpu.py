@@ -68,11 +68,11 @@ def test_c1_fp32_mm_1024_bit_exact(gpu):
 
 @pytest.mark.parametrize("dtype", F16_TYPES)
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
-@pytest.mark.parametrize("shape", [(256, 256, 256), (300, 520, 136), (64, 80, 24), (1024, 1024, 160)])
+@pytest.mark.parametrize("shape", [(256, 256, 256), (300, 520, 136), (64, 80, 24), (1024, 1024, 160), (2048, 1024, 160)])
 def test_integer_exact_all_layouts(gpu, dtype, ta, tb, shape):
     # integer operands: every summation order gives identical bits. The first
-    # three have fewer 128x128 tiles than a quarter of the CUs (64x64 tiles);
-    # the last takes the 128x128 kernels
+    # four have fewer 128x128 tiles than half the CUs (64x64 tiles); the last
+    # takes the 128x128 ring
     M, N, K = shape
     a = randint((K, M) if ta else (M, K), dtype, 10)
     b = randint((N, K) if tb else (K, N), dtype, 11)
@@ -200,7 +200,7 @@ def test_dma_kernel_128_tiles_batched_epilogue(gpu, dtype):
     a = randn((4, 512, 512), dtype, 30)
     b = randn((4, 512, 384), dtype, 31)
     inp = randn((4, 512, 384), dtype, 32)
-    got, plan = run(gpu, a, b, (4, 512, 384), dtype, bias=inp, alpha=0.5, beta=1.0)
+    got, plan = run(gpu, a, b, (4, 512, 384), dtype, bias=inp, alpha=0.5, beta=1.0, kernel="gemm16_dma_128x128")
     assert plan == "gemm16_dma_128x128"
     assert_close(got, oracle_mm(a, b, dtype, bias=inp, alpha=0.5, beta=1.0), dtype, plan)
 

@@ -709,10 +709,18 @@ Plan make_plan(const tvk_gemm_desc& d) {
             pl.kern = Kern::SEQ64;
             pl.name = "gemm_seq_mfma_64x128";
         }
-    } else if (big && pl.vec && dma_applies(repacked_args(d, pl), pl.ak, pl.bk)) {
+        return pl;
+    }
+    const bool dma_ok = pl.vec && dma_applies(repacked_args(d, pl), pl.ak, pl.bk);
+    // 256x256 tiles whose last round on the 256 CUs is at most half full, with
+    // few rounds (the transformer's gate_up, 8192x3072x512: 384 tiles, one and
+    // a half rounds) leave the 128x128 ring ahead, four times the tiles
+    // (measured 1.14x)
+    const bool half_round = t256 < 1024 && t256 % 256 != 0 && t256 % 256 <= 128;
+    if (big && dma_ok && !half_round) {
         pl.kern = Kern::DMA256;
         pl.name = "gemm16_dma_256x256";
-    } else if (big) {
+    } else if (big && !dma_ok) {
         // 8 waves; the 4-wave form stays a kernel-choice candidate
         pl.kern = Kern::MFMA256W8;
         pl.name = "gemm16_mfma_256x256_w8";
@@ -736,20 +744,22 @@ Plan make_plan(const tvk_gemm_desc& d) {
                            dma ? Kern::DMA128 : Kern::MFMA128))
                 return pl;
         }
-        // The LDS-ring kernel on 128x128 tiles; with two k-contiguous operands
-        // from 64 tiles up (13-18 % ahead of the register-staged kernel on
-        // 8192 x {512, 256, 96} x 512; on 8 x 256x256x64, 32 tiles, the 64x64
-        // tiles below are ahead of both)
-        if (pl.vec && t128 >= ((pl.ak && pl.bk) ? 64 : 32) && dma_applies(repacked_args(d, pl), pl.ak, pl.bk)) {
-            pl.kern = Kern::DMA128;
-            pl.name = "gemm16_dma_128x128";
-        } else if (t128 < 64) {
-            // fewer 128x128 tiles than a quarter of the CUs (the per-head
-            // attention products, small batches): 64x64 tiles on two waves,
-            // four times the workgroups (measured 30 % ahead of 128x128 on
-            // 8 x 256x256x64 and 8 x 256x64x256)
+        if (t128 < 128) {
+            // fewer 128x128 tiles than half the CUs: 64x64 tiles on two waves,
+            // four times the workgroups (measured ahead of both 128x128 kernels:
+            // 1.27-1.49x on 256x4096x784 and 8192x96x512, 64 tiles; 1.3x on
+            // the per-head attention products, 16 and 32 tiles)
             pl.kern = Kern::MFMA64;
             pl.name = "gemm16_mfma_64x64";
+        } else if (dma_ok) {
+            // the LDS-ring kernel on 128x128 tiles (13-18 % ahead of the
+            // register-staged one on 8192 x {512, 256} x 512); with a long K
+            // and at most a round of tiles on the 8-stage ring, whose deeper
+            // lookahead covers the loads of one workgroup a CU (1.07x on
+            // 8192x512x3072)
+            const bool r8 = d.K >= 2048 && t128 <= 256;
+            pl.kern = r8 ? Kern::DMA128R8 : Kern::DMA128;
+            pl.name = r8 ? "gemm16_dma_128x128_ring8" : "gemm16_dma_128x128";
         }
     }
     return pl;
