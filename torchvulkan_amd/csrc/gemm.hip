@@ -753,9 +753,13 @@ Plan make_plan(const tvk_gemm_desc& d) {
             pl.name = "gemm16_mfma_64x64";
         } else if (dma_ok) {
             // the LDS-ring kernel on 128x128 tiles (13-18 % ahead of the
-            // register-staged one on 8192 x {512, 256} x 512)
-            pl.kern = Kern::DMA128;
-            pl.name = "gemm16_dma_128x128";
+            // register-staged one on 8192 x {512, 256} x 512); with a long K
+            // and at most one round of tiles, its 8-stage ring, whose deeper
+            // lookahead covers the loads of one workgroup a CU (8192x512x3072:
+            // 33.9-37.9 us on three boxes, against 33.0-43.0 with 4 stages)
+            const bool r8 = d.K >= 2048 && t128 <= 256;
+            pl.kern = r8 ? Kern::DMA128R8 : Kern::DMA128;
+            pl.name = r8 ? "gemm16_dma_128x128_ring8" : "gemm16_dma_128x128";
         }
     }
     return pl;
