@@ -714,12 +714,12 @@ Plan make_plan(const tvk_gemm_desc& d) {
     const bool dma_ok = pl.vec && dma_applies(repacked_args(d, pl), pl.ak, pl.bk);
     // 256x256 tiles whose last round on the 256 CUs is at most half full, with
     // few rounds (the transformer's gate_up, 8192x3072x512: 384 tiles, one and
-    // a half rounds): 128x256 tiles, twice as many, whole rounds (39.8-41.6 us
-    // on three boxes, against 41.9-45.8 for 256x256 and 40.1-45.5 for 128x128)
+    // a half rounds): 256x128 tiles, twice as many, whole rounds (38.2-40.5 us
+    // on four boxes, against 41.9-45.8 for 256x256 and 40.1-45.5 for 128x128)
     const bool half_round = t256 < 1024 && t256 % 256 != 0 && t256 % 256 <= 128;
     if (big && dma_ok) {
-        pl.kern = half_round ? Kern::DMA128X256 : Kern::DMA256;
-        pl.name = half_round ? "gemm16_dma_128x256" : "gemm16_dma_256x256";
+        pl.kern = half_round ? Kern::DMA256X128 : Kern::DMA256;
+        pl.name = half_round ? "gemm16_dma_256x128" : "gemm16_dma_256x256";
     } else if (big) {
         // 8 waves; the 4-wave form stays a kernel-choice candidate
         pl.kern = Kern::MFMA256W8;
@@ -753,13 +753,9 @@ Plan make_plan(const tvk_gemm_desc& d) {
             pl.name = "gemm16_mfma_64x64";
         } else if (dma_ok) {
             // the LDS-ring kernel on 128x128 tiles (13-18 % ahead of the
-            // register-staged one on 8192 x {512, 256} x 512); with a long K
-            // and at most one round of tiles, its 8-stage ring, whose deeper
-            // lookahead covers the loads of one workgroup a CU (8192x512x3072:
-            // 33.9-37.9 us on three boxes, against 33.0-43.0 with 4 stages)
-            const bool r8 = d.K >= 2048 && t128 <= 256;
-            pl.kern = r8 ? Kern::DMA128R8 : Kern::DMA128;
-            pl.name = r8 ? "gemm16_dma_128x128_ring8" : "gemm16_dma_128x128";
+            // register-staged one on 8192 x {512, 256} x 512)
+            pl.kern = Kern::DMA128;
+            pl.name = "gemm16_dma_128x128";
         }
     }
     return pl;
