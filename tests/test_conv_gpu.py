@@ -166,6 +166,11 @@ SMALL_CASES = [
     dict(n=2, cin=2, cout=64, k=3, s=1, p=1, hw=(7, 64)),
     dict(n=2, cin=3, cout=64, k=3, s=1, p=1, hw=(12, 32)),
     dict(n=2, cin=3, cout=64, k=3, s=1, p=1, hw=(16, 16)),
+    # grad weight with the input rows staged in LDS (whole-row 512-pixel
+    # chunks, W 16/32/64): 1-3 input channels, partial output-channel blocks
+    dict(n=3, cin=3, cout=64, k=3, s=1, p=1, hw=(16, 32)),
+    dict(n=2, cin=1, cout=48, k=3, s=1, p=1, hw=(64, 16)),
+    dict(n=2, cin=2, cout=80, k=3, s=1, p=1, hw=(8, 64)),
 ]
 
 

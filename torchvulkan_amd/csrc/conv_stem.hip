@@ -394,6 +394,112 @@ __global__ __launch_bounds__(256) void conv_small_wgrad_kernel(SmallArgs p) {
     }
 }
 
+// The same grad weight where each 512-pixel chunk is whole rows of one image
+// (stride 1, padding 1, 3x3, at most 3 input channels, W = 16, 32 or 64): the
+// chunk's TR + 2 input rows of every channel go to LDS first (one aligned
+// 16-byte load a thread, rows padded by 8 zero columns each side), and a
+// lane's 8 pixels of one (channel, tap) come back as one 16-byte LDS read,
+// shifted by one element with its neighbour for the side taps, instead of 8
+// bounds-checked 2-byte global gathers. Same products, sums and partials as
+// conv_small_wgrad_kernel.
+__device__ inline u32x4 shift_in_low(u32x4 a, uint32_t prev) {   // {prev, a0 .. a6}
+    return u32x4{(prev & 0xffffu) | (a.x << 16), (a.x >> 16) | (a.y << 16), (a.y >> 16) | (a.z << 16), (a.z >> 16) | (a.w << 16)};
+}
+__device__ inline u32x4 shift_in_high(u32x4 a, uint32_t next) {  // {a1 .. a7, next}
+    return u32x4{(a.x >> 16) | (a.y << 16), (a.y >> 16) | (a.z << 16), (a.z >> 16) | (a.w << 16), (a.w >> 16) | (next << 16)};
+}
+
+template <int DT, int W>
+__global__ __launch_bounds__(256) void conv_small_wgrad_rows_kernel(SmallArgs p) {
+    typedef typename elem<DT>::T T;
+    constexpr int NI = 4, CB = 16 * NI, TR = 512 / W, PITCH = W + 16, ROWS = 3 * (TR + 2);
+    __shared__ __attribute__((aligned(16))) uint16_t xs[ROWS * PITCH];
+    __shared__ float red[4][CB * 33];
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16;
+    const int n0 = blockIdx.y * CB;
+    const int HW = p.H * W, P = p.n * HW;
+    // this lane's B columns k = j * 16 + lane % 16: channel c, tap (a, b); k >= K are zeros
+    int krow[2], kb[2];
+    bool kon[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int k = j * 16 + lane % 16, c = k / 9, t = k % 9;
+        kon[j] = k < p.K;
+        krow[j] = kon[j] ? c * (TR + 2) + t / 3 : 0;   // (k >= K: an in-range row, the value is dropped)
+        kb[j] = kon[j] ? t % 3 : 1;
+    }
+    // the column pads of every row, once (the fills write only the data columns)
+    for (int e = tid; e < ROWS * 16; e += 256) {
+        const int r = e / 16, q = e % 16;
+        xs[r * PITCH + (q < 8 ? q : W + q)] = 0;
+    }
+    const uint16_t* x = static_cast<const uint16_t*>(p.x);
+    const uint16_t* dy = static_cast<const uint16_t*>(p.dy);
+    f32x4 acc[NI][2];
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int base = blockIdx.x * 512; base < P; base += p.split * 512) {
+        const int img = base / HW, oh0 = (base - img * HW) / W;
+        // dy of the chunk first, so its latency overlaps the row fill
+        u32x4 fa[4][NI];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int o = base - img * HW + wave * 128 + s * 32 + g * 8;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int co = min(n0 + i * 16 + lane % 16, p.cout - 1);
+                fa[s][i] = *reinterpret_cast<const u32x4*>(dy + ((int64_t)img * p.cout + co) * HW + o);
+            }
+        }
+        __syncthreads();   // the previous chunk's LDS reads are done
+        for (int e = tid; e < p.cin * (TR + 2) * (W / 8); e += 256) {
+            const int q = e % (W / 8), r = e / (W / 8), c = r / (TR + 2), ih = oh0 - 1 + r % (TR + 2);
+            u32x4 v = u32x4{0u, 0u, 0u, 0u};
+            if (ih >= 0 && ih < p.H) v = *reinterpret_cast<const u32x4*>(x + ((int64_t)img * p.cin + c) * HW + ih * W + q * 8);
+            *reinterpret_cast<u32x4*>(xs + r * PITCH + 8 + q * 8) = v;
+        }
+        __syncthreads();
+        u32x4 fb[4][2];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int o = base - img * HW + wave * 128 + s * 32 + g * 8, oh = o / W, ow = o - oh * W;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint16_t* rp = xs + (krow[j] + oh - oh0) * PITCH + 8 + ow;
+                const u32x4 a = *reinterpret_cast<const u32x4*>(rp);
+                u32x4 v = a;
+                if (kb[j] == 0) v = shift_in_low(a, rp[-1]);
+                else if (kb[j] == 2) v = shift_in_high(a, rp[8]);
+                fb[s][j] = kon[j] ? v : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = mfma16<DT>(fa[s][i], fb[s][j], acc[i][j]);
+    }
+    // the 4 waves' sums, added in wave order
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][(i * 16 + g * 4 + r) * 33 + j * 16 + lane % 16] = acc[i][j][r];
+    __syncthreads();
+    for (int q = tid; q < CB * 32; q += 256) {
+        const int cl = q / 32, k = q % 32, co = n0 + cl;
+        if (co >= p.cout || k >= p.K) continue;
+        const int at = cl * 33 + k;
+        const float v = ((red[0][at] + red[1][at]) + red[2][at]) + red[3][at];
+        if (p.split > 1) p.part[(int64_t)blockIdx.x * p.cout * p.K + co * p.K + k] = v;
+        else reinterpret_cast<T*>(p.out)[co * p.K + k] = elem<DT>::from_f32(v);
+    }
+}
+
 // out[e] = sum over s of part[s][e], in s order within each of SG groups
 // (group q: s = q, q + SG, ...), the group sums added in group order.
 template <int DT>
@@ -786,8 +892,21 @@ tvk_status conv_small_run(const tvk_conv_desc& d, int mode, const char* who) {
             if (!p.part) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the grad-weight partials");
         }
         const dim3 grid((unsigned)p.split, (unsigned)ny);
-        if (f16) hipLaunchKernelGGL((conv_small_wgrad_kernel<TVK_F16, 4>), grid, dim3(256), 0, s, p);
+        // whole-row chunks of a stride-1 3x3 padding-1 stem: input rows staged in LDS
+        const bool rows = d.kh == 3 && d.kw == 3 && d.stride[0] == 1 && d.stride[1] == 1 && d.padding[0] == 1 &&
+                          d.padding[1] == 1 && d.dilation[0] == 1 && d.dilation[1] == 1 && d.c_in <= 3 &&
+                          (p.W == 16 || p.W == 32 || p.W == 64) && p.H % (512 / p.W) == 0 && al16(d.x);
+#define TVK_SWR(W_)                                                                                          \
+    do {                                                                                                     \
+        if (f16) hipLaunchKernelGGL((conv_small_wgrad_rows_kernel<TVK_F16, W_>), grid, dim3(256), 0, s, p); \
+        else hipLaunchKernelGGL((conv_small_wgrad_rows_kernel<TVK_BF16, W_>), grid, dim3(256), 0, s, p);    \
+    } while (0)
+        if (rows && p.W == 16) TVK_SWR(16);
+        else if (rows && p.W == 32) TVK_SWR(32);
+        else if (rows) TVK_SWR(64);
+        else if (f16) hipLaunchKernelGGL((conv_small_wgrad_kernel<TVK_F16, 4>), grid, dim3(256), 0, s, p);
         else hipLaunchKernelGGL((conv_small_wgrad_kernel<TVK_BF16, 4>), grid, dim3(256), 0, s, p);
+#undef TVK_SWR
         if (p.split > 1) {
             int sg = 1;
             while (sg < 16 && sg * 2 <= p.split && (int64_t)count * sg / 256 < 512) sg *= 2;
