@@ -68,7 +68,7 @@ def test_c1_fp32_mm_1024_bit_exact(gpu):
 
 @pytest.mark.parametrize("dtype", F16_TYPES)
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
-@pytest.mark.parametrize("shape", [(256, 256, 256), (300, 520, 136), (64, 80, 24), (1024, 1024, 160), (2048, 1024, 160)])
+@pytest.mark.parametrize("shape", [(256, 256, 256), (300, 520, 136), (64, 80, 24), (1024, 1024, 160), (4096, 1024, 160)])
 def test_integer_exact_all_layouts(gpu, dtype, ta, tb, shape):
     # integer operands: every summation order gives identical bits. The first
     # four have fewer 128x128 tiles than half the CUs (64x64 tiles); the last

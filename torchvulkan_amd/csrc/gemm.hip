@@ -744,10 +744,11 @@ Plan make_plan(const tvk_gemm_desc& d) {
                            dma ? Kern::DMA128 : Kern::MFMA128))
                 return pl;
         }
-        if (t128 < 128) {
-            // fewer 128x128 tiles than half the CUs: 64x64 tiles on two waves,
-            // four times the workgroups (measured ahead of both 128x128 kernels:
-            // 1.27-1.49x on 256x4096x784 and 8192x96x512, 64 tiles; 1.3x on
+        if (t128 <= 128) {
+            // at most half as many 128x128 tiles as CUs: 64x64 tiles on two
+            // waves, four times the workgroups (measured ahead of both 128x128
+            // kernels: 1.27-1.49x on 256x4096x784 and 8192x96x512, 64 tiles;
+            // 1.05-1.08x on 8192x256x512, 128 tiles, on three boxes; 1.3x on
             // the per-head attention products, 16 and 32 tiles)
             pl.kern = Kern::MFMA64;
             pl.name = "gemm16_mfma_64x64";
