@@ -1123,6 +1123,19 @@ tvk_status time_candidates(const tvk_gemm_desc& d, const std::vector<Plan>& cand
         if (scratch) (void)hipFree(scratch);
         return fail(TVK_ERR_DEVICE, "tvk_gemm_tune: hipEventCreate failed");
     }
+    // The shader clock ramps up over the first milliseconds of work after an
+    // idle spell, which would count against whichever candidate is timed
+    // first: run the first one for about 2 ms (at most 200 launches) first.
+    if (!cands.empty() && hipEventRecord(e0, s) == hipSuccess) {
+        for (int i = 0; i < 200; ++i) {
+            if (run_plan(t, cands[0]) != TVK_OK) break;
+            float ms = 0.0f;
+            if (i % 8 == 7 && (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                               hipEventElapsedTime(&ms, e0, e1) != hipSuccess || ms > 2.0f))
+                break;
+        }
+        (void)hipGetLastError();
+    }
     float best_ms = INFINITY;
     for (const Plan& pl : cands) {
         float spans[5];
