@@ -33,6 +33,10 @@ struct GemmArgs {
     // [rows][ld] copy, which the LDS-ring kernels' buffer ranges then cover);
     // 0: the range ends at the operand's last element
     int64_t a_ext, b_ext;
+    // split-K with the reduction in the same launch (split_fixup, the M <= 16
+    // streaming kernel): one counter per output tile, zero before the launch
+    // and left zero after it; NULL: the partials are summed by a second kernel
+    unsigned* tile_count;
 };
 
 // ----------------------------------------------------------------------------
@@ -146,6 +150,105 @@ __device__ inline void tile_of(int bid, int nblocks, int tiles_m, int tiles_n, i
     tn = in / gm;
 }
 
+// Finishes four consecutive outputs (row, col .. col + 3) of matrix b from
+// their float32 sums: the epilogue, one rounding to the output type, and one
+// 8-byte store where the output rows are contiguous and 8-byte aligned (vec).
+template <int DT>
+__device__ __forceinline__ void finish4(const GemmArgs& p, int b, int row, int col, f32x4 v, bool vec) {
+    typedef typename elem<DT>::T T;
+    T* c = reinterpret_cast<T*>(p.c);
+    const T* bias = reinterpret_cast<const T*>(p.bias);
+    uint16_t h[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float bv = 0.0f;
+        if (p.has_bias)
+            bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)(col + r) * p.sbias[2]]);
+        h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(epilogue(v[r], p.alpha, p.has_bias, bv, p.beta, p.act)));
+    }
+    T* cp = c + (int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2];
+    if (vec) {
+        st_nt(reinterpret_cast<u32x2*>(cp), u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)});
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cp[(int64_t)r * p.sc[2]] = __builtin_bit_cast(T, h[r]);
+    }
+}
+
+// Whether finish4 may store four outputs as one 8-byte write.
+__device__ __forceinline__ bool finish4_vec(const GemmArgs& p) {
+    return p.sc[2] == 1 && p.sc[1] % 4 == 0 && (p.batch == 1 || p.sc[0] % 4 == 0) && (reinterpret_cast<uintptr_t>(p.c) & 7) == 0;
+}
+
+// Split-K without a second launch. The float32 partial planes of such a
+// launch are written through to memory (stores at system coherence: the L2 of
+// each XCD is private, and a device-scope fence would write back and
+// invalidate whole L2s under every other workgroup's loads) and read back
+// with loads that miss in L2. Buffer offsets are 32-bit: the host keeps the
+// partials under 2 GiB.
+constexpr int kCoherent = 1 | 16;   // sc0 | sc1 cache-policy bits
+
+__device__ inline __amdgpu_buffer_rsrc_t part_rsrc(const GemmArgs& p) {
+    const int64_t bytes = (int64_t)p.split * p.batch * p.M * p.N * 4;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)p.part, 0, (int)bytes, 0x00020000);
+}
+
+__device__ inline void part_store(__amdgpu_buffer_rsrc_t r, int64_t idx, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)(idx * 4), 0, kCoherent);
+}
+
+// Each workgroup of an output tile has stored its plane with part_store; it
+// waits for its stores and counts itself in on the tile's counter `cnt`
+// (a system-scope atomic, performed in memory). The workgroup that brings
+// the count to `split` resets the counter for the next launch and sums the
+// tile's planes in split order with the additions and rounding of
+// gemm_split_reduce4_kernel, so both paths give the same bits. No workgroup
+// waits on another. Tile: rows m0 .. m0 + BM - 1, columns n0 .. n0 + BN - 1
+// of matrix b (N % 4 == 0: 16-byte partial rows). `flag`: one word of LDS
+// that no wave reads, nor loads into, any more.
+template <int DT, int NT, int BM, int BN>
+__device__ void split_fixup(const GemmArgs& p, int b, int m0, int n0, unsigned* cnt, int* flag) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's plane stores are complete
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned old = atomicAdd_system(cnt, 1u);
+        const int last = old + 1 == (unsigned)p.split;
+        if (last) atomicExch_system(cnt, 0u);
+        *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    const __amdgpu_buffer_rsrc_t r = part_rsrc(p);
+    const int64_t mn = (int64_t)p.M * p.N, total = (int64_t)p.batch * mn;
+    auto ld = [&](int64_t idx) {
+        return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(idx * 4), 0, kCoherent));
+    };
+    const bool vec = finish4_vec(p);
+    constexpr int G4 = BN / 4;
+    for (int g = threadIdx.x; g < BM * G4; g += NT) {
+        const int row = m0 + g / G4, col = n0 + (g % G4) * 4;
+        if (row >= p.M || col >= p.N) continue;
+        const int64_t e = (int64_t)b * mn + (int64_t)row * p.N + col;
+        f32x4 v = ld(e);
+        // four planes' loads in flight before their adds (still in split order)
+        int z = 1;
+        for (; z + 3 < p.split; z += 4) {
+#pragma clang fp contract(off)
+            f32x4 w[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) w[u] = ld((int64_t)(z + u) * total + e);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v = f32x4{v[0] + w[u][0], v[1] + w[u][1], v[2] + w[u][2], v[3] + w[u][3]};
+        }
+        for (; z < p.split; ++z) {
+#pragma clang fp contract(off)
+            const f32x4 w = ld((int64_t)z * total + e);
+            v = f32x4{v[0] + w[0], v[1] + w[1], v[2] + w[2], v[3] + w[3]};
+        }
+        finish4<DT>(p, b, row, col, v, vec);
+    }
+}
+
 namespace {
 // Sums the split-K partials of one output in split order, then applies the
 // epilogue and rounds once to the output type.
@@ -177,12 +280,9 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmArgs p) {
 // output rows are contiguous and 8-byte aligned (VEC).
 template <int DT, bool VEC>
 __global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(GemmArgs p) {
-    typedef typename elem<DT>::T T;
     const int64_t mn = (int64_t)p.M * p.N;
     const int64_t total = (int64_t)p.batch * mn;
     const int64_t groups = total / 4;
-    T* c = reinterpret_cast<T*>(p.c);
-    const T* bias = reinterpret_cast<const T*>(p.bias);
     for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < groups; q += (int64_t)gridDim.x * 256) {
         const int64_t idx = q * 4;
         f32x4 v = *reinterpret_cast<const f32x4*>(p.part + idx);
@@ -204,21 +304,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(GemmArgs p) {
         const int b = (int)(idx / mn);
         const int64_t e = idx - (int64_t)b * mn;
         const int row = (int)(e / p.N), col = (int)(e - (int64_t)row * p.N);
-        uint16_t h[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float bv = 0.0f;
-            if (p.has_bias)
-                bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)(col + r) * p.sbias[2]]);
-            h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(epilogue(v[r], p.alpha, p.has_bias, bv, p.beta, p.act)));
-        }
-        T* cp = c + (int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2];
-        if constexpr (VEC) {
-            st_nt(reinterpret_cast<u32x2*>(cp), u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)});
-        } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) cp[(int64_t)r * p.sc[2]] = __builtin_bit_cast(T, h[r]);
-        }
+        finish4<DT>(p, b, row, col, v, VEC);
     }
 }
 

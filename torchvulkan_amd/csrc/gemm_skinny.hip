@@ -261,14 +261,22 @@ __global__ __launch_bounds__(64 * SR_NW) void gemm_skinny_ring_kernel(GemmArgs p
 
     // lane l holds column l % 16 of the wave's 16, rows (l / 16) * 4 + r
     const int n = n0 + wave * 16 + lane % 16;
-    if (n >= p.N) return;
+    if (n < p.N) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int m = (lane / 16) * 4 + r;
-        if (m >= p.M) continue;
-        if (p.split > 1) p.part[(((int64_t)z * p.batch + b) * p.M + m) * p.N + n] = acc[r];
-        else store_out<DT, true>(p, b, m, n, acc[r]);
+        for (int r = 0; r < 4; ++r) {
+            const int m = (lane / 16) * 4 + r;
+            if (m >= p.M) continue;
+            const int64_t pi = (((int64_t)z * p.batch + b) * p.M + m) * p.N + n;
+            if (p.split > 1 && p.tile_count) part_store(part_rsrc(p), pi, acc[r]);   // written through (split_fixup)
+            else if (p.split > 1) p.part[pi] = acc[r];
+            else store_out<DT, true>(p, b, m, n, acc[r]);
+        }
     }
+    // every wave has drained its loads into the ring: its first word serves
+    // as the fixup's flag (the fixup's first barrier orders that)
+    if (p.split > 1 && p.tile_count)
+        split_fixup<DT, 64 * SR_NW, 16, SR_NB>(p, b, 0, n0, p.tile_count + (int64_t)b * gridDim.x + blockIdx.x,
+                                               reinterpret_cast<int*>(lds_raw));
 }
 
 // Splits of K for the ring kernel: powers of two while the grid stays within
@@ -316,9 +324,13 @@ hipError_t launch_skinny(int dtype, const GemmArgs& p, bool b_kmajor, bool vec, 
             if (!q.part) return hipErrorOutOfMemory;
         }
         const dim3 grid((p.N + SR_NB - 1) / SR_NB, q.split, p.batch);
+        // the reduction in the same launch, except on caller-provided scratch
+        // (the allocation-free entry point keeps its second launch)
+        if (q.split > 1 && !part && (int64_t)q.split * p.batch * p.M * p.N * 4 < (int64_t(1) << 31))
+            q.tile_count = split_counters(s, (int64_t)grid.x * p.batch);
         if (dtype == TVK_F16) hipLaunchKernelGGL(gemm_skinny_ring_kernel<TVK_F16>, grid, dim3(64 * SR_NW), 0, s, q);
         else hipLaunchKernelGGL(gemm_skinny_ring_kernel<TVK_BF16>, grid, dim3(64 * SR_NW), 0, s, q);
-        if (q.split > 1) {
+        if (q.split > 1 && !q.tile_count) {
             if (dtype == TVK_F16) launch_split_reduce<TVK_F16>(q, s);
             else launch_split_reduce<TVK_BF16>(q, s);
         }

@@ -138,6 +138,38 @@ void Scratch::release() {
     lease_ = nullptr;
 }
 
+namespace {
+constexpr int64_t kSplitCounters = 16384;   // 64 KB a stream: 16384 output tiles
+std::mutex g_counter_mu;
+std::map<std::pair<int, hipStream_t>, unsigned*> g_counters;
+}  // namespace
+
+unsigned* split_counters(hipStream_t stream, int64_t count) {
+    if (count <= 0 || count > kSplitCounters) return nullptr;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g_counter_mu);
+    auto it = g_counters.find({dev, stream});
+    if (it != g_counters.end()) return it->second;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    unsigned* p = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&p), kSplitCounters * sizeof(unsigned)) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (hipMemsetAsync(p, 0, kSplitCounters * sizeof(unsigned), stream) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(p);
+        return nullptr;
+    }
+    g_counters[{dev, stream}] = p;
+    return p;
+}
+
 hipStream_t device_stream(int device) {
     if (device < 0 || device >= kMaxDevices) return nullptr;
     std::lock_guard<std::mutex> lk(g_mu);

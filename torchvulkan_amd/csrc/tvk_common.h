@@ -56,6 +56,15 @@ private:
     hipStream_t stream_ = nullptr;
 };
 
+// Split-K tile counters for kernels queued on `stream` of the current device:
+// `count` words, zero now and left zero by every kernel that uses them (the
+// last workgroup of a tile resets its counter). One array per stream, so
+// stream order alone separates two launches' use of it; allocated and zeroed
+// on the stream at its first use and kept until the process ends. NULL when
+// count exceeds the array, the allocation fails, or the stream is being
+// captured before its first use (callers then reduce in a second launch).
+unsigned* split_counters(hipStream_t stream, int64_t count);
+
 // A NULL stream handle is HIP's default (null) stream, as in every HIP library.
 inline hipStream_t resolve_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
