@@ -36,3 +36,12 @@ def test_import_alias():
     import torchvulkan
 
     assert torchvulkan.is_available is tv.is_available
+
+
+def test_autocast_registered():
+    # the AutocastPrivateUse1 kernels of the reference (src/api/registration.cpp:4-21)
+    for op in ("aten::mm", "aten::addmm", "aten::bmm", "aten::baddbmm", "aten::linear", "aten::conv2d",
+               "aten::conv3d", "aten::matmul"):
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(op, "AutocastPrivateUse1"), op
+    assert torch.amp.is_autocast_available("vulkan")
+    assert torch.get_autocast_dtype("vulkan") == torch.float16
