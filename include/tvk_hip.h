@@ -549,6 +549,47 @@ tvk_status tvk_conv2d_dgrad(const tvk_conv_desc* desc);
 /* Replaces implicit_grad_weight (src/api/ops/conv.cpp:1034-1060). */
 tvk_status tvk_conv2d_wgrad(const tvk_conv_desc* desc);
 
+/* ------------------------------------------------------------------------- */
+/* Compute: convolution with 1, 2 or 3 spatial dimensions                     */
+/* ------------------------------------------------------------------------- */
+
+/* One convolution problem with `spatial_dims` spatial dimensions (1, 2 or 3),
+ * the reference's ConvProblem (src/api/ops/conv.cpp:247-255), which takes up
+ * to three (implicit_gemm_supported, conv.cpp:295-311). Tensors are
+ * contiguous NC[D][H]W, weights [c_out][c_in/groups][kernel...]. The spatial
+ * arrays list the dimensions outermost first (D, H, W); only the first
+ * `spatial_dims` entries are read. out_size[i] must equal
+ * floor((in_size[i] + 2 padding[i] - dilation[i] (kernel[i] - 1) - 1) / stride[i]) + 1.
+ * Directions, pointers and accumulation as tvk_conv_desc. One and two spatial
+ * dimensions run the 2-D kernels (one as a height of 1); three run the 3-D
+ * implicit-GEMM kernels, k = (channel, kd, kh, kw). */
+typedef struct {
+    int32_t dtype;
+    uint32_t flags;          /* TVK_GEMM_EXACT */
+    int32_t spatial_dims;    /* 1, 2 or 3 */
+    int32_t reserved;        /* 0 */
+    int64_t n, c_in, c_out, groups;
+    int64_t in_size[3];
+    int64_t kernel[3];
+    int64_t stride[3], padding[3], dilation[3];
+    int64_t out_size[3];
+    void* x;
+    void* weight;
+    const void* bias;        /* fwd only; NULL: none */
+    void* y;
+    void* stream;
+} tvk_convnd_desc;
+
+/* Replaces implicit_forward (src/api/ops/conv.cpp:1014-1022) for 1-3 spatial
+ * dimensions, with the N-d gathers of src/shaders/helpers/conv.slang:93-117. */
+tvk_status tvk_conv_fwd(const tvk_convnd_desc* desc);
+/* Replaces implicit_grad_input (src/api/ops/conv.cpp:1024-1032) for 1-3
+ * spatial dimensions (and the transposed forward that reuses it, :1105). */
+tvk_status tvk_conv_dgrad(const tvk_convnd_desc* desc);
+/* Replaces implicit_grad_weight (src/api/ops/conv.cpp:1034-1060) for 1-3
+ * spatial dimensions. */
+tvk_status tvk_conv_wgrad(const tvk_convnd_desc* desc);
+
 #ifdef __cplusplus
 }
 #endif

@@ -247,3 +247,124 @@ int oracle_winograd_fwd(int dt, const conv_geom* g, int64_t nb, int64_t ne, cons
     free(U); free(V); free(M);
     return 0;
 }
+
+/* ------------------------------------------------------------------------- */
+/* 3-D convolution: the reference's implicit GEMM takes up to three spatial   */
+/* dimensions (src/api/ops/conv.cpp:295-311; geometry padded to three,        */
+/* conv.cpp:313-343; N-d gathers src/shaders/helpers/conv.slang:93-117).       */
+/* Tensors NCDHW, weights [Cout][Cin/groups][KD][KH][KW]; k runs over          */
+/* (c, kd, kh, kw) in that order, as in 2-D with the depth tap outermost.      */
+/* ------------------------------------------------------------------------- */
+
+typedef struct {
+    int64_t n, cin, cout, groups;
+    int64_t in[3], k[3], s[3], p[3], d[3], out[3];   /* (D, H, W) */
+} conv3_geom;
+
+static int geom3_ok(const conv3_geom* g) {
+    if (g->n < 0 || g->cin <= 0 || g->cout <= 0 || g->groups <= 0) return 0;
+    if (g->cin % g->groups || g->cout % g->groups) return 0;
+    for (int i = 0; i < 3; ++i)
+        if (g->in[i] <= 0 || g->k[i] <= 0 || g->s[i] <= 0 || g->d[i] <= 0 || g->p[i] < 0 || g->out[i] < 0) return 0;
+    return 1;
+}
+
+static inline int64_t vol3(const int64_t* v) { return v[0] * v[1] * v[2]; }
+
+/* samples [nb, ne) */
+int oracle_conv3d_fwd(int dt, const conv3_geom* g, int64_t nb, int64_t ne, const void* x, const void* wt, const void* bias,
+                      void* y) {
+    if (!geom3_ok(g)) return -1;
+    const int64_t cx = g->cin / g->groups, cy = g->cout / g->groups;
+    const int64_t si = vol3(g->in), so = vol3(g->out), taps = vol3(g->k);
+    for (int64_t n = nb; n < ne; ++n)
+        for (int64_t oc = 0; oc < g->cout; ++oc) {
+            const int64_t grp = oc / cy;
+            for (int64_t od = 0; od < g->out[0]; ++od)
+                for (int64_t oh = 0; oh < g->out[1]; ++oh)
+                    for (int64_t ow = 0; ow < g->out[2]; ++ow) {
+                        float acc = 0.0f;
+                        for (int64_t c = 0; c < cx; ++c)
+                            for (int64_t a = 0; a < g->k[0]; ++a)
+                                for (int64_t b = 0; b < g->k[1]; ++b)
+                                    for (int64_t e = 0; e < g->k[2]; ++e) {
+                                        const int64_t id = od * g->s[0] - g->p[0] + a * g->d[0];
+                                        const int64_t ih = oh * g->s[1] - g->p[1] + b * g->d[1];
+                                        const int64_t iw = ow * g->s[2] - g->p[2] + e * g->d[2];
+                                        float xv = 0.0f;
+                                        if (id >= 0 && id < g->in[0] && ih >= 0 && ih < g->in[1] && iw >= 0 && iw < g->in[2])
+                                            xv = ld(dt, x, (n * g->cin + grp * cx + c) * si + (id * g->in[1] + ih) * g->in[2] + iw);
+                                        const float wv = ld(dt, wt, (oc * cx + c) * taps + (a * g->k[1] + b) * g->k[2] + e);
+                                        acc = fmaf(wv, xv, acc);
+                                    }
+                        if (bias) acc = acc + ld(dt, bias, oc);
+                        st(dt, y, (n * g->cout + oc) * so + (od * g->out[1] + oh) * g->out[2] + ow, acc);
+                    }
+        }
+    return 0;
+}
+
+int oracle_conv3d_dgrad(int dt, const conv3_geom* g, int64_t nb, int64_t ne, const void* dy, const void* wt, void* dx) {
+    if (!geom3_ok(g)) return -1;
+    const int64_t cx = g->cin / g->groups, cy = g->cout / g->groups;
+    const int64_t si = vol3(g->in), so = vol3(g->out), taps = vol3(g->k);
+    for (int64_t n = nb; n < ne; ++n)
+        for (int64_t ic = 0; ic < g->cin; ++ic) {
+            const int64_t grp = ic / cx, c = ic % cx;
+            for (int64_t id = 0; id < g->in[0]; ++id)
+                for (int64_t ih = 0; ih < g->in[1]; ++ih)
+                    for (int64_t iw = 0; iw < g->in[2]; ++iw) {
+                        float acc = 0.0f;
+                        for (int64_t m = 0; m < cy; ++m)
+                            for (int64_t a = 0; a < g->k[0]; ++a)
+                                for (int64_t b = 0; b < g->k[1]; ++b)
+                                    for (int64_t e = 0; e < g->k[2]; ++e) {
+                                        const int64_t td = id + g->p[0] - a * g->d[0];
+                                        const int64_t th = ih + g->p[1] - b * g->d[1];
+                                        const int64_t tw = iw + g->p[2] - e * g->d[2];
+                                        if (td < 0 || th < 0 || tw < 0 || td % g->s[0] || th % g->s[1] || tw % g->s[2]) continue;
+                                        const int64_t od = td / g->s[0], oh = th / g->s[1], ow = tw / g->s[2];
+                                        if (od >= g->out[0] || oh >= g->out[1] || ow >= g->out[2]) continue;
+                                        const int64_t oc = grp * cy + m;
+                                        acc = fmaf(ld(dt, wt, (oc * cx + c) * taps + (a * g->k[1] + b) * g->k[2] + e),
+                                                   ld(dt, dy, (n * g->cout + oc) * so + (od * g->out[1] + oh) * g->out[2] + ow), acc);
+                                    }
+                        st(dt, dx, (n * g->cin + ic) * si + (id * g->in[1] + ih) * g->in[2] + iw, acc);
+                    }
+        }
+    return 0;
+}
+
+/* output channels [ob, oe) */
+int oracle_conv3d_wgrad(int dt, const conv3_geom* g, int64_t ob, int64_t oe, const void* x, const void* dy, void* dw,
+                        int acc64) {
+    if (!geom3_ok(g)) return -1;
+    const int64_t cx = g->cin / g->groups, cy = g->cout / g->groups;
+    const int64_t si = vol3(g->in), so = vol3(g->out), taps = vol3(g->k);
+    for (int64_t oc = ob; oc < oe; ++oc) {
+        const int64_t grp = oc / cy;
+        for (int64_t c = 0; c < cx; ++c)
+            for (int64_t a = 0; a < g->k[0]; ++a)
+                for (int64_t b = 0; b < g->k[1]; ++b)
+                    for (int64_t e = 0; e < g->k[2]; ++e) {
+                        float acc = 0.0f;
+                        double acc_d = 0.0;
+                        for (int64_t n = 0; n < g->n; ++n)
+                            for (int64_t od = 0; od < g->out[0]; ++od)
+                                for (int64_t oh = 0; oh < g->out[1]; ++oh)
+                                    for (int64_t ow = 0; ow < g->out[2]; ++ow) {
+                                        const int64_t id = od * g->s[0] - g->p[0] + a * g->d[0];
+                                        const int64_t ih = oh * g->s[1] - g->p[1] + b * g->d[1];
+                                        const int64_t iw = ow * g->s[2] - g->p[2] + e * g->d[2];
+                                        if (id < 0 || id >= g->in[0] || ih < 0 || ih >= g->in[1] || iw < 0 || iw >= g->in[2])
+                                            continue;
+                                        const float yv = ld(dt, dy, (n * g->cout + oc) * so + (od * g->out[1] + oh) * g->out[2] + ow);
+                                        const float xv = ld(dt, x, (n * g->cin + grp * cx + c) * si + (id * g->in[1] + ih) * g->in[2] + iw);
+                                        if (acc64) acc_d += (double)yv * (double)xv;
+                                        else acc = fmaf(yv, xv, acc);
+                                    }
+                        st(dt, dw, (oc * cx + c) * taps + (a * g->k[1] + b) * g->k[2] + e, acc64 ? (float)acc_d : acc);
+                    }
+    }
+    return 0;
+}

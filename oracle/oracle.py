@@ -510,3 +510,73 @@ def winograd_conv2d(x, w, dtype: int, bias=None, padding=(1, 1), threads=None) -
     _parallel(g.n, lambda s, e: lib.oracle_winograd_fwd(dtype, C.byref(g), s, e, x.ctypes.data, w.ctypes.data,
                                                         None if b is None else b.ctypes.data, y.ctypes.data), threads)
     return y
+
+
+# ---------------------------------------------------------------------------
+# 3-D convolution (conv_oracle.c, oracle_conv3d_*)
+# ---------------------------------------------------------------------------
+
+class Conv3Geom(C.Structure):
+    _fields_ = [("n", C.c_int64), ("cin", C.c_int64), ("cout", C.c_int64), ("groups", C.c_int64)] + \
+               [(f, C.c_int64 * 3) for f in ("inn", "k", "s", "p", "d", "out")]
+
+
+def _triple(v):
+    return tuple(v) if isinstance(v, (tuple, list)) else (v, v, v)
+
+
+def make_geom3(x_shape, w_shape, stride=1, padding=0, dilation=1, groups=1, out=None) -> Conv3Geom:
+    n, cin = x_shape[:2]
+    cout = w_shape[0]
+    s, p, d = _triple(stride), _triple(padding), _triple(dilation)
+    k = tuple(w_shape[2:])
+    if out is None:
+        out = tuple(conv_out_size(x_shape[2 + i], k[i], s[i], p[i], d[i]) for i in range(3))
+    A = C.c_int64 * 3
+    return Conv3Geom(n, cin, cout, groups, A(*x_shape[2:]), A(*k), A(*s), A(*p), A(*d), A(*out))
+
+
+def _conv3_lib():
+    lib = load()
+    if not getattr(lib, "_conv3_ready", False):
+        P = C.POINTER(Conv3Geom)
+        lib.oracle_conv3d_fwd.argtypes = [C.c_int, P, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        lib.oracle_conv3d_dgrad.argtypes = [C.c_int, P, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]
+        lib.oracle_conv3d_wgrad.argtypes = [C.c_int, P, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+        for f in ("oracle_conv3d_fwd", "oracle_conv3d_dgrad", "oracle_conv3d_wgrad"):
+            getattr(lib, f).restype = C.c_int
+        lib._conv3_ready = True
+    return lib
+
+
+def conv3d(x, w, dtype: int, bias=None, stride=1, padding=0, dilation=1, groups=1, threads=None) -> np.ndarray:
+    """Forward 3-D implicit-GEMM convolution in the reference's k order (c, kd, kh, kw)."""
+    lib = _conv3_lib()
+    x, w = _c(x), _c(w)
+    g = make_geom3(x.shape, w.shape, stride, padding, dilation, groups)
+    y = np.zeros((g.n, g.cout) + tuple(g.out), dtype=x.dtype)
+    b = None if bias is None else _c(bias)
+    _parallel(g.n, lambda s, e: lib.oracle_conv3d_fwd(dtype, C.byref(g), s, e, x.ctypes.data, w.ctypes.data,
+                                                      None if b is None else b.ctypes.data, y.ctypes.data), threads)
+    return y
+
+
+def conv3d_dgrad(dy, w, x_shape, dtype: int, stride=1, padding=0, dilation=1, groups=1, threads=None) -> np.ndarray:
+    lib = _conv3_lib()
+    dy, w = _c(dy), _c(w)
+    g = make_geom3(x_shape, w.shape, stride, padding, dilation, groups, out=dy.shape[2:])
+    dx = np.zeros(tuple(x_shape), dtype=dy.dtype)
+    _parallel(g.n, lambda s, e: lib.oracle_conv3d_dgrad(dtype, C.byref(g), s, e, dy.ctypes.data, w.ctypes.data,
+                                                        dx.ctypes.data), threads)
+    return dx
+
+
+def conv3d_wgrad(x, dy, w_shape, dtype: int, stride=1, padding=0, dilation=1, groups=1, acc64=True,
+                 threads=None) -> np.ndarray:
+    lib = _conv3_lib()
+    x, dy = _c(x), _c(dy)
+    g = make_geom3(x.shape, w_shape, stride, padding, dilation, groups, out=dy.shape[2:])
+    dw = np.zeros(tuple(w_shape), dtype=x.dtype)
+    _parallel(g.cout, lambda s, e: lib.oracle_conv3d_wgrad(dtype, C.byref(g), s, e, x.ctypes.data, dy.ctypes.data,
+                                                           dw.ctypes.data, 1 if acc64 else 0), threads)
+    return dw

@@ -125,3 +125,36 @@ def test_free_rejects_foreign_pointer():
     lib = _abi.load()
     assert lib.tvk_free(C.c_void_p(0x1234)) == _abi.TVK_ERR_INVALID
     assert lib.tvk_free(None) == _abi.TVK_OK
+
+
+def _convnd(**kw):
+    import torch
+
+    d = _abi.make_convnd_desc((2, 4, 5, 6, 7), (8, 4, 3, 3, 3), torch.float16, stride=1, padding=1)
+    d.x = d.weight = d.y = 16   # never dereferenced by validation
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("spatial_dims", 4, _abi.TVK_ERR_UNSUPPORTED),
+    ("spatial_dims", 0, _abi.TVK_ERR_UNSUPPORTED),
+    ("dtype", 3, _abi.TVK_ERR_UNSUPPORTED),   # float64 convolutions run as im2col + GEMM in the backend
+    ("groups", 3, _abi.TVK_ERR_INVALID),
+    ("c_in", 0, _abi.TVK_ERR_INVALID),
+])
+def test_convnd_validation(field, value, status):
+    lib = _abi.load()
+    d = _convnd(**{field: value})
+    for fn in (lib.tvk_conv_fwd, lib.tvk_conv_dgrad, lib.tvk_conv_wgrad):
+        assert fn(C.byref(d)) == status, (field, value, lib.tvk_last_error())
+
+
+def test_convnd_rejects_wrong_output_size():
+    lib = _abi.load()
+    d = _convnd()
+    d.out_size[1] = 99
+    assert lib.tvk_conv_fwd(C.byref(d)) == _abi.TVK_ERR_INVALID
+    assert b"out_size[1]" in lib.tvk_last_error()
+    assert lib.tvk_conv_fwd(None) == _abi.TVK_ERR_INVALID

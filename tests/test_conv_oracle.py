@@ -78,3 +78,82 @@ def test_winograd_restatement_close_to_direct(dtype, tol):
     if dtype == orc.F16:
         # the rounded intermediates do change the result (the check has teeth)
         assert not np.array_equal(wino, direct)
+
+
+# ---------------------------------------------------------------------------
+# 3-D restatement (oracle_conv3d_*): the reference takes up to three spatial
+# dimensions (src/api/ops/conv.cpp:295-311)
+# ---------------------------------------------------------------------------
+
+GEOMS3 = [
+    # x shape, w shape, stride, padding, dilation, groups
+    ((2, 3, 5, 6, 7), (4, 3, 3, 3, 3), (1, 1, 1), (1, 1, 1), (1, 1, 1), 1),
+    ((1, 4, 7, 6, 9), (6, 4, 3, 3, 3), (2, 2, 2), (1, 1, 1), (1, 1, 1), 1),
+    ((2, 4, 6, 5, 8), (6, 2, 3, 2, 3), (2, 1, 3), (1, 0, 2), (2, 1, 1), 2),
+    ((1, 6, 4, 6, 6), (3, 6, 1, 1, 1), (1, 2, 2), (0, 0, 0), (1, 1, 1), 1),
+    ((2, 3, 5, 5, 5), (3, 1, 3, 3, 3), (1, 1, 1), (1, 1, 1), (1, 2, 1), 3),   # depthwise, dilated
+]
+
+
+@pytest.mark.parametrize("geom", GEOMS3)
+def test_conv3d_forward_exact(geom):
+    xs, ws, s, p, d, g = geom
+    x, w, b = _ints(xs, 11), _ints(ws, 12), _ints((ws[0],), 13)
+    got = orc.conv3d(x, w, orc.F32, bias=b, stride=s, padding=p, dilation=d, groups=g)
+    want = torch.nn.functional.conv3d(torch.from_numpy(x).double(), torch.from_numpy(w).double(),
+                                      torch.from_numpy(b).double(), s, p, d, g).numpy()
+    assert got.shape == want.shape
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("geom", GEOMS3)
+def test_conv3d_gradients_exact(geom):
+    xs, ws, s, p, d, g = geom
+    x = torch.from_numpy(_ints(xs, 14)).double().requires_grad_()
+    w = torch.from_numpy(_ints(ws, 15)).double().requires_grad_()
+    y = torch.nn.functional.conv3d(x, w, None, s, p, d, g)
+    dy = torch.from_numpy(_ints(tuple(y.shape), 16)).double()
+    y.backward(dy)
+    dx = orc.conv3d_dgrad(dy.float().numpy(), w.detach().float().numpy(), xs, orc.F32, s, p, d, g)
+    dw = orc.conv3d_wgrad(x.detach().float().numpy(), dy.float().numpy(), ws, orc.F32, s, p, d, g)
+    dw32 = orc.conv3d_wgrad(x.detach().float().numpy(), dy.float().numpy(), ws, orc.F32, s, p, d, g, acc64=False)
+    assert np.array_equal(dx, x.grad.numpy().astype(np.float32))
+    assert np.array_equal(dw, w.grad.numpy().astype(np.float32))
+    assert np.array_equal(dw32, w.grad.numpy().astype(np.float32))
+
+
+def _columns(x, kernel, stride, padding, dilation):
+    """im2col by numpy windows: [c * prod(kernel), n * prod(out)], rows in (c, kd, kh, kw) order."""
+    nd = len(kernel)
+    pad = [(0, 0), (0, 0)] + [(p, p) for p in padding]
+    xp = np.pad(x, pad)
+    span = [(k - 1) * d + 1 for k, d in zip(kernel, dilation)]
+    win = np.lib.stride_tricks.sliding_window_view(xp, span, axis=tuple(range(2, 2 + nd)))
+    idx = (slice(None), slice(None)) + tuple(slice(None, None, s) for s in stride) + tuple(slice(None, None, d) for d in dilation)
+    win = win[idx]   # [n, c, out..., kernel...]
+    n, c = x.shape[:2]
+    out = win.shape[2:2 + nd]
+    perm = (1,) + tuple(range(2 + nd, 2 + 2 * nd)) + (0,) + tuple(range(2, 2 + nd))
+    return np.ascontiguousarray(win.transpose(perm)).reshape(c * int(np.prod(kernel)), n * int(np.prod(out))), out
+
+
+@pytest.mark.parametrize("nd", [2, 3])
+def test_conv_k_order_is_the_gemm_order(nd):
+    """The conv oracle accumulates in the k order (c, [kd,] kh, kw): on random float32 data (where the order
+    shows in the last bits) it is bit-identical to the GEMM oracle, whose fused-multiply-add order is pinned by
+    test_oracle.py, applied to the im2col columns."""
+    rng = np.random.default_rng(20 + nd)
+    if nd == 2:
+        xs, ws, s, p, d = (2, 5, 9, 8), (6, 5, 3, 2), (2, 1), (1, 1), (1, 2)
+    else:
+        xs, ws, s, p, d = (2, 4, 5, 6, 7), (6, 4, 3, 2, 3), (1, 2, 2), (1, 0, 1), (2, 1, 1)
+    x = rng.standard_normal(xs).astype(np.float32)
+    w = rng.standard_normal(ws).astype(np.float32)
+    cols, out = _columns(x, ws[2:], s, p, d)
+    prod = orc.gemm(w.reshape(ws[0], -1), cols, orc.F32)                       # [cout, n * prod(out)]
+    want = prod.reshape((ws[0], xs[0]) + tuple(out)).swapaxes(0, 1)
+    got = (orc.conv2d if nd == 2 else orc.conv3d)(x, w, orc.F32, stride=s, padding=p, dilation=d)
+    assert np.array_equal(got, want)
+    # the order matters on these data: summing the taps in reverse gives other bits somewhere
+    rev = orc.gemm(w.reshape(ws[0], -1)[:, ::-1], cols[::-1], orc.F32)
+    assert not np.array_equal(prod, rev)

@@ -76,6 +76,26 @@ class ConvDesc(C.Structure):
     ]
 
 
+I64x3s = C.c_int64 * 3
+
+
+class ConvNdDesc(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int32),
+        ("flags", C.c_uint32),
+        ("spatial_dims", C.c_int32),
+        ("reserved", C.c_int32),
+        ("n", C.c_int64), ("c_in", C.c_int64), ("c_out", C.c_int64), ("groups", C.c_int64),
+        ("in_size", I64x3s), ("kernel", I64x3s), ("stride", I64x3s), ("padding", I64x3s), ("dilation", I64x3s),
+        ("out_size", I64x3s),
+        ("x", C.c_void_p),
+        ("weight", C.c_void_p),
+        ("bias", C.c_void_p),
+        ("y", C.c_void_p),
+        ("stream", C.c_void_p),
+    ]
+
+
 I64xD = C.c_int64 * TVK_COPY_MAX_DIMS
 
 
@@ -217,6 +237,8 @@ def load() -> C.CDLL:
         lib.tvk_device_properties.argtypes = [C.c_int, C.POINTER(DeviceProps)]
         for fn in ("tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad"):
             getattr(lib, fn).argtypes = [C.POINTER(ConvDesc)]
+        for fn in ("tvk_conv_fwd", "tvk_conv_dgrad", "tvk_conv_wgrad"):
+            getattr(lib, fn).argtypes = [C.POINTER(ConvNdDesc)]
         lib.tvk_copy.argtypes = [C.POINTER(CopyDesc)]
         lib.tvk_copy_plan.argtypes = [C.POINTER(CopyDesc), C.c_char_p, C.c_size_t]
         lib.tvk_fill.argtypes = [C.POINTER(FillDesc)]
@@ -239,7 +261,8 @@ _ALL_ENTRY_POINTS = (
     "tvk_memory_reserved", "tvk_reset_peak_memory_stats", "tvk_mem_get_info", "tvk_memcpy_h2d",
     "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan", "tvk_gemm_candidates",
     "tvk_gemm_choose", "tvk_gemm_tune", "tvk_tune_reset", "tvk_tune_path",
-    "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad", "tvk_copy", "tvk_copy_plan",
+    "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad", "tvk_conv_fwd", "tvk_conv_dgrad", "tvk_conv_wgrad",
+    "tvk_copy", "tvk_copy_plan",
     "tvk_fill", "tvk_reduce_sum", "tvk_binary", "tvk_attention_fwd",
     "tvk_attention_bwd", "tvk_gemm_noalloc", "tvk_event_create", "tvk_event_destroy", "tvk_event_record",
     "tvk_event_query", "tvk_event_synchronize", "tvk_event_elapsed", "tvk_stream_wait_event", "tvk_stream_query",
@@ -636,4 +659,62 @@ def conv2d_wgrad(x, dy, w_shape, stride=1, padding=0, dilation=1, groups=1, exac
     d.x, d.weight, d.y = x.data_ptr(), dw.data_ptr(), dy.data_ptr()
     d.stream = torch.cuda.current_stream(x.device).cuda_stream
     _conv_call("tvk_conv2d_wgrad", d)
+    return dw
+
+
+def _nd(v, nd):
+    return (v,) * nd if isinstance(v, int) else tuple(v)
+
+
+def make_convnd_desc(x_shape, w_shape, dtype, stride=1, padding=0, dilation=1, groups=1, exact=False) -> ConvNdDesc:
+    """Describes a convolution with 1-3 spatial dimensions over contiguous NC[D][H]W tensors."""
+    nd = len(x_shape) - 2
+    if nd < 1 or nd > 3 or len(w_shape) != nd + 2:
+        raise ValueError(f"shapes {tuple(x_shape)} / {tuple(w_shape)} are not a 1-3 spatial-dimension convolution")
+    s, p, dl = _nd(stride, nd), _nd(padding, nd), _nd(dilation, nd)
+    k = tuple(w_shape[2:])
+    o = tuple((x_shape[2 + i] + 2 * p[i] - dl[i] * (k[i] - 1) - 1) // s[i] + 1 for i in range(nd))
+    pad3 = lambda v, fill: I64x3s(*(tuple(v) + (fill,) * (3 - nd)))
+    d = ConvNdDesc()
+    d.dtype = _dtype_code(dtype)
+    d.flags = TVK_GEMM_EXACT if exact else 0
+    d.spatial_dims = nd
+    d.n, d.c_in, d.c_out, d.groups = x_shape[0], x_shape[1], w_shape[0], groups
+    d.in_size, d.kernel, d.out_size = pad3(x_shape[2:], 1), pad3(k, 1), pad3(o, 1)
+    d.stride, d.padding, d.dilation = pad3(s, 1), pad3(p, 0), pad3(dl, 1)
+    return d
+
+
+def conv_fwd(x, weight, bias=None, stride=1, padding=0, dilation=1, groups=1, exact=False):
+    """y = conv(x, weight) + bias with 1-3 spatial dimensions through tvk_conv_fwd (contiguous device tensors)."""
+    import torch
+
+    d = make_convnd_desc(x.shape, weight.shape, x.dtype, stride, padding, dilation, groups, exact=exact)
+    y = torch.empty((d.n, d.c_out) + tuple(d.out_size[:d.spatial_dims]), dtype=x.dtype, device=x.device)
+    d.x, d.weight, d.y = x.data_ptr(), weight.data_ptr(), y.data_ptr()
+    d.bias = None if bias is None else bias.data_ptr()
+    d.stream = torch.cuda.current_stream(x.device).cuda_stream
+    _conv_call("tvk_conv_fwd", d)
+    return y
+
+
+def conv_dgrad(dy, weight, x_shape, stride=1, padding=0, dilation=1, groups=1, exact=False):
+    import torch
+
+    d = make_convnd_desc(x_shape, weight.shape, dy.dtype, stride, padding, dilation, groups, exact=exact)
+    dx = torch.empty(tuple(x_shape), dtype=dy.dtype, device=dy.device)
+    d.x, d.weight, d.y = dx.data_ptr(), weight.data_ptr(), dy.data_ptr()
+    d.stream = torch.cuda.current_stream(dy.device).cuda_stream
+    _conv_call("tvk_conv_dgrad", d)
+    return dx
+
+
+def conv_wgrad(x, dy, w_shape, stride=1, padding=0, dilation=1, groups=1, exact=False):
+    import torch
+
+    d = make_convnd_desc(x.shape, w_shape, x.dtype, stride, padding, dilation, groups, exact=exact)
+    dw = torch.empty(tuple(w_shape), dtype=x.dtype, device=x.device)
+    d.x, d.weight, d.y = x.data_ptr(), dw.data_ptr(), dy.data_ptr()
+    d.stream = torch.cuda.current_stream(x.device).cuda_stream
+    _conv_call("tvk_conv_wgrad", d)
     return dw

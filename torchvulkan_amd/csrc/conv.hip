@@ -1,26 +1,32 @@
-// 2-D convolution as implicit GEMM on gfx950: forward, grad-input and
-// grad-weight, NCHW, any stride / padding / dilation / groups.
+// Convolution as implicit GEMM on gfx950: forward, grad-input and
+// grad-weight, NC(D)HW, 2 or 3 spatial dimensions, any stride / padding /
+// dilation / groups.
 //
 // Reference semantics (file:line under the reference tree):
 //   forward     y[n, g*Cy+m, o] = sum_{c,tap} W[g*Cy+m, c, tap] x[n, g*Cx+c, o*s-p+tap*d]
-//               + bias, zero padding; GEMM M = Cy, N = n*Ho*Wo, K = Cx*taps with
-//               k = (c, kh, kw) (src/shaders/helpers/conv.slang:198-207,280-312,
-//               src/api/ops/conv.cpp:1014-1022, bias epilogue conv_simd.slang:8-19)
+//               + bias, zero padding; GEMM M = Cy, N = n*prod(out), K = Cx*taps with
+//               k = (c, [kd,] kh, kw) (src/shaders/helpers/conv.slang:93-117,198-207,
+//               280-312, src/api/ops/conv.cpp:1014-1022, bias epilogue conv_simd.slang:8-19)
 //   grad input  dx[n, g*Cx+c, i] = sum_{m,tap} W[g*Cy+m, c, tap] dy[n, g*Cy+m, (i+p-tap*d)/s]
-//               where the division is exact and in range; M = Cx, N = n*H*W,
+//               where the division is exact and in range; M = Cx, N = n*prod(in),
 //               K = Cy*taps (conv.slang:320-362, conv.cpp:1024-1032)
 //   grad weight dW[g*Cy+m, c, tap] = sum_{n,o} dy[n, g*Cy+m, o] x[n, g*Cx+c, o*s-p+tap*d];
-//               M = Cy, N = Cx*taps, K = n*Ho*Wo, K split into float32 partials that
+//               M = Cy, N = Cx*taps, K = n*prod(out), K split into float32 partials that
 //               are summed and cast to the storage type (conv.cpp:1034-1060)
+// The reference takes up to three spatial dimensions (conv.cpp:295-311); its
+// geometry block pads the shapes to three (conv.cpp:313-343). Here the 2-D and
+// 3-D kernels are separate instantiations (ND), so the 2-D gathers carry no
+// depth arithmetic; one spatial dimension runs as 2-D with a height of 1.
 //
 // Both operands of every mode are gathered element by element (buffer loads
 // whose out-of-range offset reads zero, which is the padding) into LDS tiles
 // laid out k-contiguous, the layout the GEMM kernels' MFMA fragments read.
 // Each thread gathers 8 consecutive k of one GEMM row or column; the column
 // decompositions are computed once per tile and the k decompositions are
-// wave-uniform, so the inner gather is an add, two range tests and a load.
-// float16/bfloat16 use v_mfma_f32_32x32x16; float32 (and TVK_GEMM_EXACT) use
-// the rank-1 v_mfma_f32_32x32x1f32 so every output accumulates in k order.
+// wave-uniform, so the inner gather is an add, two (three) range tests and a
+// load. float16/bfloat16 use v_mfma_f32_32x32x16; float32 (and
+// TVK_GEMM_EXACT) use the rank-1 v_mfma_f32_32x32x1f32 so every output
+// accumulates in k order.
 #include "gemm_common.h"
 
 #include <algorithm>
@@ -40,6 +46,8 @@ struct ConvArgs {
     void* out;      // y (FWD), x (DGRAD), w (WGRAD)
     float* part;    // WGRAD float32 partials [split][Cout][Cx*taps] when split > 1
     int n, cin, h, wd, cout, kh, kw, sh, sw, ph, pw, dh, dw, groups, ho, wo;
+    int dp, kd, sd, pd, dd, dop;   // depth: input, kernel, stride, padding, dilation, output (3-D only)
+    int si, so;                    // spatial elements per channel: input, output
     int cx, cy, taps;
     int M, N, K;
     int k_chunk;    // WGRAD: k per split
@@ -57,73 +65,103 @@ constexpr int C_BN = 128;  // GEMM columns per block
 
 // Per-row (A) or per-column (B) part of an element address, fixed for the tile.
 struct Lane {
-    int base;   // element offset of the (row, k = 0) origin
-    int hb, wb; // spatial offsets (meaning depends on mode)
-    bool ok;    // the row/column exists
+    int base;       // element offset of the (row, k = 0) origin
+    int db, hb, wb; // spatial offsets (meaning depends on mode; db only in 3-D)
+    bool ok;        // the row/column exists
 };
 
 // k decomposition, wave-uniform; advanced by one k at a time.
 struct KPos {
-    int a, b, c;   // FWD B / DGRAD A,B: (channel, kh, kw); WGRAD A,B: (n, oh, ow)
+    int a, z, b, c;   // FWD B / DGRAD A,B: (channel, kd, kh, kw); WGRAD A,B: (n, od, oh, ow)
 };
 
-template <int MODE, bool IS_A>
+template <int ND, int MODE, bool IS_A>
 __device__ inline Lane lane_info(const ConvArgs& p, int g, int idx) {
-    Lane L{0, 0, 0, false};
+    Lane L{0, 0, 0, 0, false};
     if constexpr (IS_A) {
         if (idx >= p.M) return L;
         L.ok = true;
         if constexpr (MODE == FWD) L.base = (g * p.cy + idx) * p.cx * p.taps;                 // W row
         else if constexpr (MODE == DGRAD) L.base = (g * p.cy * p.cx + idx) * p.taps;         // W[g*Cy][c]
-        else L.base = (g * p.cy + idx) * p.ho * p.wo;                                        // dy[0][g*Cy+m]
+        else L.base = (g * p.cy + idx) * p.so;                                               // dy[0][g*Cy+m]
     } else {
         if (idx >= p.N) return L;
         L.ok = true;
         if constexpr (MODE == FWD) {
-            const int o = idx % (p.ho * p.wo), n = idx / (p.ho * p.wo);
-            L.base = (n * p.cin + g * p.cx) * p.h * p.wd;
-            L.hb = (o / p.wo) * p.sh - p.ph;
-            L.wb = (o % p.wo) * p.sw - p.pw;
+            const int o = idx % p.so, n = idx / p.so;
+            const int plane = ND == 3 ? o % (p.ho * p.wo) : o;
+            L.base = (n * p.cin + g * p.cx) * p.si;
+            if constexpr (ND == 3) L.db = (o / (p.ho * p.wo)) * p.sd - p.pd;
+            L.hb = (plane / p.wo) * p.sh - p.ph;
+            L.wb = (plane % p.wo) * p.sw - p.pw;
         } else if constexpr (MODE == DGRAD) {
-            const int o = idx % (p.h * p.wd), n = idx / (p.h * p.wd);
-            L.base = (n * p.cout + g * p.cy) * p.ho * p.wo;
-            L.hb = o / p.wd + p.ph;
-            L.wb = o % p.wd + p.pw;
+            const int o = idx % p.si, n = idx / p.si;
+            const int plane = ND == 3 ? o % (p.h * p.wd) : o;
+            L.base = (n * p.cout + g * p.cy) * p.so;
+            if constexpr (ND == 3) L.db = o / (p.h * p.wd) + p.pd;
+            L.hb = plane / p.wd + p.ph;
+            L.wb = plane % p.wd + p.pw;
         } else {
             const int t = idx % p.taps, c = idx / p.taps;
-            L.base = (g * p.cx + c) * p.h * p.wd;
-            L.hb = (t / p.kw) * p.dh - p.ph;
-            L.wb = (t % p.kw) * p.dw - p.pw;
+            const int tp = ND == 3 ? t % (p.kh * p.kw) : t;
+            L.base = (g * p.cx + c) * p.si;
+            if constexpr (ND == 3) L.db = (t / (p.kh * p.kw)) * p.dd - p.pd;
+            L.hb = (tp / p.kw) * p.dh - p.ph;
+            L.wb = (tp % p.kw) * p.dw - p.pw;
         }
     }
     return L;
 }
 
-template <int MODE, bool IS_A>
+template <int ND, int MODE, bool IS_A>
 __device__ inline KPos kpos_of(const ConvArgs& p, int k) {
-    KPos q{0, 0, 0};
+    KPos q{0, 0, 0, 0};
     if constexpr (MODE == WGRAD) {
-        const int o = k % (p.ho * p.wo);
-        q.a = k / (p.ho * p.wo);
-        q.b = o / p.wo;
-        q.c = o % p.wo;
+        const int o = k % p.so;
+        const int plane = ND == 3 ? o % (p.ho * p.wo) : o;
+        q.a = k / p.so;
+        if constexpr (ND == 3) q.z = o / (p.ho * p.wo);
+        q.b = plane / p.wo;
+        q.c = plane % p.wo;
     } else if constexpr (!(IS_A && MODE == FWD)) {
         const int t = k % p.taps;
+        const int tp = ND == 3 ? t % (p.kh * p.kw) : t;
         q.a = k / p.taps;
-        q.b = t / p.kw;
-        q.c = t % p.kw;
+        if constexpr (ND == 3) q.z = t / (p.kh * p.kw);
+        q.b = tp / p.kw;
+        q.c = tp % p.kw;
     } else {
         q.a = k;
     }
     return q;
 }
 
-template <int MODE, bool IS_A>
+template <int ND, int MODE, bool IS_A>
 __device__ inline void kpos_next(const ConvArgs& p, KPos& q) {
     if constexpr (MODE == WGRAD) {
-        if (++q.c == p.wo) { q.c = 0; if (++q.b == p.ho) { q.b = 0; ++q.a; } }
+        if (++q.c == p.wo) {
+            q.c = 0;
+            if (++q.b == p.ho) {
+                q.b = 0;
+                if constexpr (ND == 3) {
+                    if (++q.z == p.dop) { q.z = 0; ++q.a; }
+                } else {
+                    ++q.a;
+                }
+            }
+        }
     } else if constexpr (!(IS_A && MODE == FWD)) {
-        if (++q.c == p.kw) { q.c = 0; if (++q.b == p.kh) { q.b = 0; ++q.a; } }
+        if (++q.c == p.kw) {
+            q.c = 0;
+            if (++q.b == p.kh) {
+                q.b = 0;
+                if constexpr (ND == 3) {
+                    if (++q.z == p.kd) { q.z = 0; ++q.a; }
+                } else {
+                    ++q.a;
+                }
+            }
+        }
     } else {
         ++q.a;
     }
@@ -131,28 +169,47 @@ __device__ inline void kpos_next(const ConvArgs& p, KPos& q) {
 
 // Element offset (in elements) of operand element (row/col lane L, k = q), or
 // -1 when it is padding / out of range.
-template <int MODE, bool IS_A>
+template <int ND, int MODE, bool IS_A>
 __device__ inline int elem_offset(const ConvArgs& p, const Lane& L, const KPos& q, bool kvalid) {
     if (!L.ok || !kvalid) return -1;
     if constexpr (IS_A) {
+        const int tap = ND == 3 ? (q.z * p.kh + q.b) * p.kw + q.c : q.b * p.kw + q.c;
+        const int opix = ND == 3 ? (q.z * p.ho + q.b) * p.wo + q.c : q.b * p.wo + q.c;
         if constexpr (MODE == FWD) return L.base + q.a;
-        else if constexpr (MODE == DGRAD) return L.base + q.a * p.cx * p.taps + q.b * p.kw + q.c;
-        else return L.base + q.a * p.cout * p.ho * p.wo + q.b * p.wo + q.c;
+        else if constexpr (MODE == DGRAD) return L.base + q.a * p.cx * p.taps + tap;
+        else return L.base + q.a * p.cout * p.so + opix;
     } else {
         if constexpr (MODE == FWD) {
             const int ih = L.hb + q.b * p.dh, iw = L.wb + q.c * p.dw;
             if ((unsigned)ih >= (unsigned)p.h || (unsigned)iw >= (unsigned)p.wd) return -1;
-            return L.base + q.a * p.h * p.wd + ih * p.wd + iw;
+            if constexpr (ND == 3) {
+                const int id = L.db + q.z * p.dd;
+                if ((unsigned)id >= (unsigned)p.dp) return -1;
+                return L.base + q.a * p.si + (id * p.h + ih) * p.wd + iw;
+            }
+            return L.base + q.a * p.si + ih * p.wd + iw;
         } else if constexpr (MODE == DGRAD) {
             const int th = L.hb - q.b * p.dh, tw = L.wb - q.c * p.dw;
             if (th < 0 || tw < 0) return -1;
             const int oh = th / p.sh, ow = tw / p.sw;
             if (oh * p.sh != th || ow * p.sw != tw || oh >= p.ho || ow >= p.wo) return -1;
-            return L.base + q.a * p.ho * p.wo + oh * p.wo + ow;
+            if constexpr (ND == 3) {
+                const int td = L.db - q.z * p.dd;
+                if (td < 0) return -1;
+                const int od = td / p.sd;
+                if (od * p.sd != td || od >= p.dop) return -1;
+                return L.base + q.a * p.so + (od * p.ho + oh) * p.wo + ow;
+            }
+            return L.base + q.a * p.so + oh * p.wo + ow;
         } else {
             const int ih = q.b * p.sh + L.hb, iw = q.c * p.sw + L.wb;
             if ((unsigned)ih >= (unsigned)p.h || (unsigned)iw >= (unsigned)p.wd) return -1;
-            return L.base + q.a * p.cin * p.h * p.wd + ih * p.wd + iw;
+            if constexpr (ND == 3) {
+                const int id = q.z * p.sd + L.db;
+                if ((unsigned)id >= (unsigned)p.dp) return -1;
+                return L.base + q.a * p.cin * p.si + (id * p.h + ih) * p.wd + iw;
+            }
+            return L.base + q.a * p.cin * p.si + ih * p.wd + iw;
         }
     }
 }
@@ -160,7 +217,7 @@ __device__ inline int elem_offset(const ConvArgs& p, const Lane& L, const KPos& 
 // Gathers operand tiles of R rows x C_BK k: thread t owns row t % R and the
 // k chunks (t / R) + (256 / R) * i of 8 elements each; the chunk index is
 // wave-uniform (R is 64 or 128).
-template <int DT, int MODE, bool IS_A, int R>
+template <int DT, int ND, int MODE, bool IS_A, int R>
 struct Gather {
     static constexpr int ES = DT == TVK_F32 ? 4 : 2;
     static constexpr int NCH = R * (C_BK / 8) / 256;
@@ -168,7 +225,7 @@ struct Gather {
     uint32_t raw[NCH][8];
 
     __device__ inline void init(const ConvArgs& p, int g, int row0, int tid) {
-        lane = lane_info<MODE, IS_A>(p, g, row0 + tid % R);
+        lane = lane_info<ND, MODE, IS_A>(p, g, row0 + tid % R);
     }
 
     __device__ inline void load(const ConvArgs& p, __amdgpu_buffer_rsrc_t rsrc, int k0, int kend, int tid) {
@@ -176,14 +233,14 @@ struct Gather {
         for (int i = 0; i < NCH; ++i) {
             const int kc = __builtin_amdgcn_readfirstlane(tid / R + (256 / R) * i);
             const int kb = k0 + kc * 8;
-            KPos q = kpos_of<MODE, IS_A>(p, kb);
+            KPos q = kpos_of<ND, MODE, IS_A>(p, kb);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int off = elem_offset<MODE, IS_A>(p, lane, q, kb + e < kend);
+                const int off = elem_offset<ND, MODE, IS_A>(p, lane, q, kb + e < kend);
                 const uint32_t bo = off < 0 ? kOOB : (uint32_t)off * ES;
                 if constexpr (ES == 4) raw[i][e] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsrc, (int)bo, 0, 0);
                 else raw[i][e] = buf_load2(rsrc, bo);
-                kpos_next<MODE, IS_A>(p, q);
+                kpos_next<ND, MODE, IS_A>(p, q);
             }
         }
     }
@@ -229,17 +286,17 @@ __device__ inline void conv_store(const ConvArgs& p, int g, int split, int row, 
     if (row >= p.M || col >= p.N) return;
     typedef typename elem<DT>::T T;
     if constexpr (MODE == FWD) {
-        const int o = col % (p.ho * p.wo), n = col / (p.ho * p.wo);
+        const int o = col % p.so, n = col / p.so;
         const int ch = g * p.cy + row;
         float v = acc;
         if (p.has_bias) {
 #pragma clang fp contract(off)
             v = v + elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[ch]);
         }
-        reinterpret_cast<T*>(p.out)[(int64_t)(n * p.cout + ch) * p.ho * p.wo + o] = elem<DT>::from_f32(v);
+        reinterpret_cast<T*>(p.out)[(int64_t)(n * p.cout + ch) * p.so + o] = elem<DT>::from_f32(v);
     } else if constexpr (MODE == DGRAD) {
-        const int o = col % (p.h * p.wd), n = col / (p.h * p.wd);
-        reinterpret_cast<T*>(p.out)[(int64_t)(n * p.cin + g * p.cx + row) * p.h * p.wd + o] = elem<DT>::from_f32(acc);
+        const int o = col % p.si, n = col / p.si;
+        reinterpret_cast<T*>(p.out)[(int64_t)(n * p.cin + g * p.cx + row) * p.si + o] = elem<DT>::from_f32(acc);
     } else {
         const int64_t idx = (int64_t)(g * p.cy + row) * p.cx * p.taps + col;
         if (p.split > 1) p.part[(int64_t)split * p.cout * p.cx * p.taps + idx] = acc;
@@ -282,7 +339,7 @@ __device__ inline f32x16 cmfma32(u32x4 a, u32x4 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-template <int DT, int MODE, int BM>
+template <int DT, int ND, int MODE, int BM>
 __global__ __launch_bounds__(256) void conv16_kernel(ConvArgs p) {
     constexpr int WGM = BM / 64;                 // waves along M (1 or 2)
     constexpr int WGN = 4 / WGM;                 // waves along N
@@ -298,8 +355,8 @@ __global__ __launch_bounds__(256) void conv16_kernel(ConvArgs p) {
     __amdgpu_buffer_rsrc_t ra, rb;
     operand_rsrc<MODE>(p, ra, rb);
 
-    Gather<DT, MODE, true, BM> ga;
-    Gather<DT, MODE, false, C_BN> gb;
+    Gather<DT, ND, MODE, true, BM> ga;
+    Gather<DT, ND, MODE, false, C_BN> gb;
     ga.init(p, g, m0, tid);
     gb.init(p, g, n0, tid);
 
@@ -365,7 +422,7 @@ __global__ __launch_bounds__(256) void conv16_kernel(ConvArgs p) {
 
 constexpr int S_LDK = C_BK + 4;   // float rows of 144 bytes
 
-template <int DT, int MODE>
+template <int DT, int ND, int MODE>
 __global__ __launch_bounds__(256) void conv_seq_kernel(ConvArgs p) {
     constexpr int BM = 128;
     __shared__ __attribute__((aligned(16))) float lds[2][(BM + C_BN) * S_LDK];
@@ -377,8 +434,8 @@ __global__ __launch_bounds__(256) void conv_seq_kernel(ConvArgs p) {
     __amdgpu_buffer_rsrc_t ra, rb;
     operand_rsrc<MODE>(p, ra, rb);
 
-    Gather<DT, MODE, true, BM> ga;
-    Gather<DT, MODE, false, C_BN> gb;
+    Gather<DT, ND, MODE, true, BM> ga;
+    Gather<DT, ND, MODE, false, C_BN> gb;
     ga.init(p, g, m0, tid);
     gb.init(p, g, n0, tid);
 
@@ -459,12 +516,18 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* part, vo
 // host side
 // ---------------------------------------------------------------------------
 
+tvk_status check_dtype_flags(int32_t dtype, uint32_t flags, const std::string& w) {
+    if (dtype != TVK_F32 && dtype != TVK_F16 && dtype != TVK_BF16)
+        return fail(TVK_ERR_UNSUPPORTED, w + ": unsupported dtype " + std::to_string(dtype));
+    if (flags & ~TVK_GEMM_EXACT) return fail(TVK_ERR_INVALID, w + ": unknown flags");
+    return TVK_OK;
+}
+
 tvk_status conv_validate(const tvk_conv_desc* d, const char* who) {
     const std::string w(who);
     if (!d) return fail(TVK_ERR_INVALID, w + ": desc is NULL");
-    if (d->dtype != TVK_F32 && d->dtype != TVK_F16 && d->dtype != TVK_BF16)
-        return fail(TVK_ERR_UNSUPPORTED, w + ": unsupported dtype " + std::to_string(d->dtype));
-    if (d->flags & ~TVK_GEMM_EXACT) return fail(TVK_ERR_INVALID, w + ": unknown flags");
+    tvk_status st = check_dtype_flags(d->dtype, d->flags, w);
+    if (st != TVK_OK) return st;
     if (d->n < 0 || d->c_in <= 0 || d->c_out <= 0 || d->h <= 0 || d->w <= 0 || d->kh <= 0 || d->kw <= 0 || d->groups <= 0)
         return fail(TVK_ERR_INVALID, w + ": sizes must be positive");
     if (d->c_in % d->groups || d->c_out % d->groups)
@@ -494,6 +557,8 @@ ConvArgs make_args(const tvk_conv_desc& d) {
     p.sh = (int)d.stride[0]; p.sw = (int)d.stride[1]; p.ph = (int)d.padding[0]; p.pw = (int)d.padding[1];
     p.dh = (int)d.dilation[0]; p.dw = (int)d.dilation[1]; p.groups = (int)d.groups;
     p.ho = (int)d.h_out; p.wo = (int)d.w_out;
+    p.dp = 1; p.kd = 1; p.sd = 1; p.pd = 0; p.dd = 1; p.dop = 1;
+    p.si = p.h * p.wd; p.so = p.ho * p.wo;
     p.cx = p.cin / p.groups; p.cy = p.cout / p.groups; p.taps = p.kh * p.kw;
     const int64_t es = dtype_size(d.dtype);
     p.x_bytes = (int)(d.n * d.c_in * d.h * d.w * es);
@@ -503,38 +568,34 @@ ConvArgs make_args(const tvk_conv_desc& d) {
     return p;
 }
 
-template <int DT, int MODE>
+template <int DT, int ND, int MODE>
 void launch(const ConvArgs& p, bool seq, hipStream_t s) {
     if (seq || DT == TVK_F32) {
         dim3 grid((p.N + C_BN - 1) / C_BN, (p.M + 127) / 128, p.groups * p.split);
-        hipLaunchKernelGGL((conv_seq_kernel<DT, MODE>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((conv_seq_kernel<DT, ND, MODE>), grid, dim3(256), 0, s, p);
     } else if constexpr (DT != TVK_F32) {
         if (p.M <= 64) {
             dim3 grid((p.N + C_BN - 1) / C_BN, (p.M + 63) / 64, p.groups * p.split);
-            hipLaunchKernelGGL((conv16_kernel<DT, MODE, 64>), grid, dim3(256), 0, s, p);
+            hipLaunchKernelGGL((conv16_kernel<DT, ND, MODE, 64>), grid, dim3(256), 0, s, p);
         } else {
             dim3 grid((p.N + C_BN - 1) / C_BN, (p.M + 127) / 128, p.groups * p.split);
-            hipLaunchKernelGGL((conv16_kernel<DT, MODE, 128>), grid, dim3(256), 0, s, p);
+            hipLaunchKernelGGL((conv16_kernel<DT, ND, MODE, 128>), grid, dim3(256), 0, s, p);
         }
     }
 }
 
 template <int MODE>
-tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
-    tvk_status st = conv_validate(desc, who);
-    if (st != TVK_OK) return st;
-    const tvk_conv_desc& d = *desc;
-    void* out = MODE == FWD ? d.y : MODE == DGRAD ? d.x : d.weight;
-    if (!out) return fail(TVK_ERR_INVALID, std::string(who) + ": output pointer is NULL");
-    ConvArgs p = make_args(d);
-    p.out = out;
-    p.has_bias = (MODE == FWD && d.bias) ? 1 : 0;
-    if (MODE == FWD) { p.M = p.cy; p.N = p.n * p.ho * p.wo; p.K = p.cx * p.taps; }
-    else if (MODE == DGRAD) { p.M = p.cx; p.N = p.n * p.h * p.wd; p.K = p.cy * p.taps; }
-    else { p.M = p.cy; p.N = p.cx * p.taps; p.K = p.n * p.ho * p.wo; }
-    hipStream_t s = resolve_stream(d.stream);
-    Scratch scratch;
-    const size_t es = dtype_size(d.dtype);
+void set_gemm_shape(ConvArgs& p) {
+    if (MODE == FWD) { p.M = p.cy; p.N = p.n * p.so; p.K = p.cx * p.taps; }
+    else if (MODE == DGRAD) { p.M = p.cx; p.N = p.n * p.si; p.K = p.cy * p.taps; }
+    else { p.M = p.cy; p.N = p.cx * p.taps; p.K = p.n * p.so; }
+}
+
+// The generic implicit-GEMM kernels: the grad-weight split, the launch, and
+// the split reduction. p carries the geometry and the GEMM shape.
+template <int ND, int MODE>
+tvk_status run_generic(ConvArgs& p, int32_t dtype, bool seq, void* out, hipStream_t s, const char* who) {
+    const size_t es = dtype_size(dtype);
     if (p.N == 0 || p.M == 0) return TVK_OK;
     if (p.K == 0) {
         // empty reduction (grad weight of an empty batch): zeros, written by a
@@ -546,17 +607,11 @@ tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
         if (e != hipSuccess) return fail(TVK_ERR_DEVICE, std::string(who) + ": launch failed: " + hipGetErrorString(e));
         return TVK_OK;
     }
-    // few input channels: one-k-step kernels that gather straight from NCHW (conv_stem.hip)
-    if (conv_small_applies(d, MODE)) return conv_small_run(d, MODE, who);
-    // stride-1 3x3 forward / grad input through an LDS halo of the NCHW source (conv_nhwc.hip)
-    if (conv_halo_applies(d, MODE)) return conv_halo_run(d, MODE, who);
-    // channels-last implicit GEMM on the LDS ring (conv_nhwc.hip) where it applies
-    if (conv_ring_applies(d, MODE)) return conv_ring_run(d, MODE, who);
-    const bool seq = (d.flags & TVK_GEMM_EXACT) != 0;
+    Scratch scratch;
     if (MODE == WGRAD) {
         // split the long reduction so the grid covers the device: about 512
         // blocks, each with at least 8 k stages
-        const int bm = (seq || d.dtype == TVK_F32 || p.M > 64) ? 128 : 64;
+        const int bm = (seq || dtype == TVK_F32 || p.M > 64) ? 128 : 64;
         const int64_t tiles = (int64_t)((p.M + bm - 1) / bm) * ((p.N + C_BN - 1) / C_BN) * p.groups;
         int64_t split = std::max<int64_t>(1, std::min<int64_t>(512 / std::max<int64_t>(1, tiles), p.K / (8 * C_BK)));
         split = std::min<int64_t>(split, 65535 / p.groups);
@@ -570,15 +625,15 @@ tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
             if (!p.part) return fail(TVK_ERR_OOM, std::string(who) + ": no workspace for the split-k partials");
         }
     }
-    switch (d.dtype) {
-    case TVK_F32: launch<TVK_F32, MODE>(p, true, s); break;
-    case TVK_F16: launch<TVK_F16, MODE>(p, seq, s); break;
-    default: launch<TVK_BF16, MODE>(p, seq, s); break;
+    switch (dtype) {
+    case TVK_F32: launch<TVK_F32, ND, MODE>(p, true, s); break;
+    case TVK_F16: launch<TVK_F16, ND, MODE>(p, seq, s); break;
+    default: launch<TVK_BF16, ND, MODE>(p, seq, s); break;
     }
     if (MODE == WGRAD && p.split > 1) {
         const int64_t count = (int64_t)p.cout * p.cx * p.taps;
         const unsigned blocks = (unsigned)std::min<int64_t>((count + 3) / 4, 8192);
-        switch (d.dtype) {
+        switch (dtype) {
         case TVK_F32: hipLaunchKernelGGL(wgrad_reduce_kernel<TVK_F32>, dim3(blocks), dim3(256), 0, s, p.part, out, count, p.split); break;
         case TVK_F16: hipLaunchKernelGGL(wgrad_reduce_kernel<TVK_F16>, dim3(blocks), dim3(256), 0, s, p.part, out, count, p.split); break;
         default: hipLaunchKernelGGL(wgrad_reduce_kernel<TVK_BF16>, dim3(blocks), dim3(256), 0, s, p.part, out, count, p.split); break;
@@ -589,6 +644,123 @@ tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
     return TVK_OK;
 }
 
+template <int MODE>
+tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
+    tvk_status st = conv_validate(desc, who);
+    if (st != TVK_OK) return st;
+    const tvk_conv_desc& d = *desc;
+    void* out = MODE == FWD ? d.y : MODE == DGRAD ? d.x : d.weight;
+    if (!out) return fail(TVK_ERR_INVALID, std::string(who) + ": output pointer is NULL");
+    ConvArgs p = make_args(d);
+    p.out = out;
+    p.has_bias = (MODE == FWD && d.bias) ? 1 : 0;
+    set_gemm_shape<MODE>(p);
+    if (p.N != 0 && p.M != 0 && p.K != 0) {
+        // few input channels: one-k-step kernels that gather straight from NCHW (conv_stem.hip)
+        if (conv_small_applies(d, MODE)) return conv_small_run(d, MODE, who);
+        // stride-1 3x3 forward / grad input through an LDS halo of the NCHW source (conv_nhwc.hip)
+        if (conv_halo_applies(d, MODE)) return conv_halo_run(d, MODE, who);
+        // channels-last implicit GEMM on the LDS ring (conv_nhwc.hip) where it applies
+        if (conv_ring_applies(d, MODE)) return conv_ring_run(d, MODE, who);
+    }
+    return run_generic<2, MODE>(p, d.dtype, (d.flags & TVK_GEMM_EXACT) != 0, out, resolve_stream(d.stream), who);
+}
+
+// ---------------------------------------------------------------------------
+// N-d entry points: 1 and 2 spatial dimensions run the 2-D dispatch (1-D as a
+// height of 1), 3 run the 3-D generic kernels
+// ---------------------------------------------------------------------------
+
+tvk_status convnd_validate(const tvk_convnd_desc* d, const char* who) {
+    const std::string w(who);
+    if (!d) return fail(TVK_ERR_INVALID, w + ": desc is NULL");
+    if (d->spatial_dims < 1 || d->spatial_dims > 3)
+        return fail(TVK_ERR_UNSUPPORTED, w + ": spatial_dims must be 1, 2 or 3 (got " + std::to_string(d->spatial_dims) + ")");
+    tvk_status st = check_dtype_flags(d->dtype, d->flags, w);
+    if (st != TVK_OK) return st;
+    if (d->n < 0 || d->c_in <= 0 || d->c_out <= 0 || d->groups <= 0)
+        return fail(TVK_ERR_INVALID, w + ": sizes must be positive");
+    if (d->c_in % d->groups || d->c_out % d->groups)
+        return fail(TVK_ERR_INVALID, w + ": channels must be divisible by groups");
+    int64_t si = 1, so = 1, taps = 1;
+    for (int i = 0; i < d->spatial_dims; ++i) {
+        if (d->in_size[i] <= 0 || d->kernel[i] <= 0) return fail(TVK_ERR_INVALID, w + ": sizes must be positive");
+        if (d->stride[i] <= 0 || d->dilation[i] <= 0 || d->padding[i] < 0)
+            return fail(TVK_ERR_INVALID, w + ": stride and dilation must be positive, padding non-negative");
+        const int64_t o = (d->in_size[i] + 2 * d->padding[i] - d->dilation[i] * (d->kernel[i] - 1) - 1) / d->stride[i] + 1;
+        if (o <= 0 || o != d->out_size[i])
+            return fail(TVK_ERR_INVALID, w + ": out_size[" + std::to_string(i) + "] does not match the geometry (expected " +
+                                             std::to_string(o) + ")");
+        si *= d->in_size[i];
+        so *= o;
+        taps *= d->kernel[i];
+    }
+    const int64_t es = dtype_size(d->dtype);
+    const int64_t xb = d->n * d->c_in * si * es, yb = d->n * d->c_out * so * es, wb = d->c_out * (d->c_in / d->groups) * taps * es;
+    if (xb >= 0x7fffffff || yb >= 0x7fffffff || wb >= 0x7fffffff)
+        return fail(TVK_ERR_UNSUPPORTED, w + ": an operand exceeds 2 GiB (32-bit buffer offsets)");
+    return TVK_OK;
+}
+
+// The 2-D descriptor of a 1-D or 2-D problem (1-D: height 1, kernel height 1).
+tvk_conv_desc as_2d(const tvk_convnd_desc& d) {
+    tvk_conv_desc c;
+    memset(&c, 0, sizeof(c));
+    c.dtype = d.dtype; c.flags = d.flags;
+    c.n = d.n; c.c_in = d.c_in; c.c_out = d.c_out; c.groups = d.groups;
+    const int o = d.spatial_dims == 1 ? 1 : 0;   // first 2-D slot taken from the descriptor
+    c.h = o ? 1 : d.in_size[0];
+    c.kh = o ? 1 : d.kernel[0];
+    c.stride[0] = o ? 1 : d.stride[0];
+    c.padding[0] = o ? 0 : d.padding[0];
+    c.dilation[0] = o ? 1 : d.dilation[0];
+    c.h_out = o ? 1 : d.out_size[0];
+    const int j = d.spatial_dims - 1;
+    c.w = d.in_size[j]; c.kw = d.kernel[j]; c.stride[1] = d.stride[j]; c.padding[1] = d.padding[j];
+    c.dilation[1] = d.dilation[j]; c.w_out = d.out_size[j];
+    c.x = d.x; c.weight = d.weight; c.bias = d.bias; c.y = d.y; c.stream = d.stream;
+    return c;
+}
+
+ConvArgs make_args3(const tvk_convnd_desc& d) {
+    ConvArgs p;
+    memset(&p, 0, sizeof(p));
+    p.x = d.x; p.w = d.weight; p.bias = d.bias; p.y = d.y;
+    p.n = (int)d.n; p.cin = (int)d.c_in; p.cout = (int)d.c_out; p.groups = (int)d.groups;
+    p.dp = (int)d.in_size[0]; p.h = (int)d.in_size[1]; p.wd = (int)d.in_size[2];
+    p.kd = (int)d.kernel[0]; p.kh = (int)d.kernel[1]; p.kw = (int)d.kernel[2];
+    p.sd = (int)d.stride[0]; p.sh = (int)d.stride[1]; p.sw = (int)d.stride[2];
+    p.pd = (int)d.padding[0]; p.ph = (int)d.padding[1]; p.pw = (int)d.padding[2];
+    p.dd = (int)d.dilation[0]; p.dh = (int)d.dilation[1]; p.dw = (int)d.dilation[2];
+    p.dop = (int)d.out_size[0]; p.ho = (int)d.out_size[1]; p.wo = (int)d.out_size[2];
+    p.si = p.dp * p.h * p.wd; p.so = p.dop * p.ho * p.wo;
+    p.cx = p.cin / p.groups; p.cy = p.cout / p.groups; p.taps = p.kd * p.kh * p.kw;
+    const int64_t es = dtype_size(d.dtype);
+    p.x_bytes = (int)(d.n * d.c_in * p.si * es);
+    p.y_bytes = (int)(d.n * d.c_out * p.so * es);
+    p.w_bytes = (int)(d.c_out * p.cx * p.taps * es);
+    p.split = 1;
+    return p;
+}
+
+template <int MODE>
+tvk_status run_convnd(const tvk_convnd_desc* desc, const char* who) {
+    tvk_status st = convnd_validate(desc, who);
+    if (st != TVK_OK) return st;
+    const tvk_convnd_desc& d = *desc;
+    if (d.spatial_dims < 3) {
+        const tvk_conv_desc c = as_2d(d);
+        return run_conv<MODE>(&c, who);
+    }
+    void* out = MODE == FWD ? d.y : MODE == DGRAD ? d.x : d.weight;
+    if (!out) return fail(TVK_ERR_INVALID, std::string(who) + ": output pointer is NULL");
+    ConvArgs p = make_args3(d);
+    p.out = out;
+    p.has_bias = (MODE == FWD && d.bias) ? 1 : 0;
+    set_gemm_shape<MODE>(p);
+    return run_generic<3, MODE>(p, d.dtype, (d.flags & TVK_GEMM_EXACT) != 0, out, resolve_stream(d.stream), who);
+}
+
 }  // namespace
 }  // namespace tvk
 
@@ -597,3 +769,6 @@ using namespace tvk;
 extern "C" tvk_status tvk_conv2d_fwd(const tvk_conv_desc* desc) { return run_conv<FWD>(desc, "tvk_conv2d_fwd"); }
 extern "C" tvk_status tvk_conv2d_dgrad(const tvk_conv_desc* desc) { return run_conv<DGRAD>(desc, "tvk_conv2d_dgrad"); }
 extern "C" tvk_status tvk_conv2d_wgrad(const tvk_conv_desc* desc) { return run_conv<WGRAD>(desc, "tvk_conv2d_wgrad"); }
+extern "C" tvk_status tvk_conv_fwd(const tvk_convnd_desc* desc) { return run_convnd<FWD>(desc, "tvk_conv_fwd"); }
+extern "C" tvk_status tvk_conv_dgrad(const tvk_convnd_desc* desc) { return run_convnd<DGRAD>(desc, "tvk_conv_dgrad"); }
+extern "C" tvk_status tvk_conv_wgrad(const tvk_convnd_desc* desc) { return run_convnd<WGRAD>(desc, "tvk_conv_wgrad"); }
