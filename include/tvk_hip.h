@@ -17,7 +17,7 @@
  *     waits for and the caching allocator's blocks are ordered on.
  *   - strides are in ELEMENTS, not bytes, and may be zero (broadcast) or any
  *     positive value; element offsets must fit in int64.
- *   - scratch memory: tvk_gemm, tvk_conv2d_*, tvk_reduce_sum and
+ *   - scratch memory: tvk_gemm, tvk_conv2d_*, tvk_conv_*, tvk_reduce_sum and
  *     tvk_attention_bwd lease library scratch (split-K partials, repacked
  *     operands, convolution partials, the attention delta) from a per-device
  *     pool for the kernels they queue on their `stream`. A buffer is leased
@@ -49,8 +49,8 @@ typedef enum {
     TVK_ERR_DEVICE = 4
 } tvk_status;
 
-/* Element types. tvk_gemm takes F32 through U8; tvk_conv2d_* take F32, F16
- * and BF16; tvk_copy takes every one of them. BOOL is one byte holding 0 or
+/* Element types. tvk_gemm takes F32 through U8; tvk_conv2d_* and tvk_conv_*
+ * take F32, F16 and BF16; tvk_copy takes every one of them. BOOL is one byte holding 0 or
  * 1. F8E4M3FN and F8E5M2 are torch's float8_e4m3fn and float8_e5m2 (OCP 8-bit
  * floats: e4m3 with no infinities and NaN = S.1111.111, e5m2 IEEE-like);
  * only tvk_copy takes them. */
@@ -161,13 +161,37 @@ tvk_status tvk_calibrate_hbm(int device, size_t window_bytes, int iterations, do
 /* ------------------------------------------------------------------------- */
 
 /* Allocates `bytes` (rounded up to a size class) on `device`. bytes==0 gives
- * *out==NULL and TVK_OK. Over the budget set by tvk_set_memory_limit this
- * returns TVK_ERR_OOM, the reference's TORCHVULKAN_STRICT_ALLOCATION
- * behaviour (src/vulkan/allocator.cpp:171-200). */
+ * *out==NULL and TVK_OK. A request past the budget set by
+ * tvk_set_memory_limit, or one hipMalloc cannot serve after the cache is
+ * released, follows the reference's allocateBuffer
+ * (src/vulkan/allocator.cpp:171-200): with strict allocation off (the
+ * default) it is served from pinned host memory, which kernels read and write
+ * over the host link (slower; tvk_last_malloc_spilled then reports 1); with
+ * strict allocation on it returns TVK_ERR_OOM. */
 tvk_status tvk_malloc(int device, size_t bytes, void** out);
 /* Returns a block to its size-class cache. NULL is a no-op. Freeing a pointer
- * the allocator did not hand out is TVK_ERR_INVALID. */
+ * the allocator did not hand out is TVK_ERR_INVALID. A block served from host
+ * memory is freed at once, after the device has drained. */
 tvk_status tvk_free(void* ptr);
+/* Strict allocation, the reference's TORCHVULKAN_STRICT_ALLOCATION
+ * (src/vulkan/vulkan_context.cpp:248, read at start-up): on when that
+ * variable is set to a non-empty value other than "0" when the library loads;
+ * this call changes it for the process. */
+tvk_status tvk_set_strict_allocation(int strict);
+tvk_status tvk_get_strict_allocation(int* strict);
+/* *spilled = 1 when this thread's last successful tvk_malloc was served from
+ * host memory (the caller's cue for the reference's one-time warning). */
+tvk_status tvk_last_malloc_spilled(int* spilled);
+/* Pinned (page-locked) host memory for tensor.pin_memory(): the reference's
+ * pinned allocator with its block registry (src/api/hook.cpp:14-51). Pinned
+ * blocks let host <-> device copies run as direct DMA. tvk_host_free takes
+ * only pointers tvk_host_malloc returned, and the caller must not free a block
+ * an asynchronous copy still reads. */
+tvk_status tvk_host_malloc(size_t bytes, void** out);
+tvk_status tvk_host_free(void* ptr);
+/* *pinned = 1 when ptr lies inside a live tvk_host_malloc block
+ * (isPinnedPtr, src/api/hook.cpp:24-31,69). */
+tvk_status tvk_host_pointer_pinned(const void* ptr, int* pinned);
 /* Releases every cached (unused) block of `device` back to HIP
  * (torchvulkan.empty_cache, src/api/backend.cpp:52-54). */
 tvk_status tvk_empty_cache(int device);
@@ -428,7 +452,15 @@ tvk_status tvk_attention_bwd(const tvk_attention_bwd_desc* desc);
  * (src/api/ops/matmul.cpp:584-597) of matmul_simd_main
  * (src/shaders/ops/matmul_simd.slang:23-44) and matmul_coop_main
  * (src/shaders/ops/matmul_coop.slang:443-452), with the same 4-stride operand
- * model as TensorStrides (src/shaders/helpers/gemm.slang:3-9). */
+ * model as TensorStrides (src/shaders/helpers/gemm.slang:3-9).
+ *
+ * Scratch: split-K partials and repacked operands come from a per-device pool
+ * of stream-affine buffers (freed by tvk_empty_cache after a drain). The
+ * M <= 16 streaming kernel reduces its split-K partials in the same launch,
+ * counting finished workgroups in a 64 KB array per stream (allocated at the
+ * stream's first such product, kept until the process ends, at most 32
+ * streams a device); launches under graph capture, on hipStreamPerThread and
+ * on further streams use a second reduction launch instead. */
 /* tvk_gemm_desc.flags */
 #define TVK_GEMM_EXACT 1u   /* every dtype in the reference SIMD tile's order:
                                float32 operands, fmaf over k = 0..K-1 in
@@ -455,8 +487,10 @@ tvk_status tvk_gemm(const tvk_gemm_desc* desc);
 /* tvk_gemm without any allocation: no counterpart in the reference. For
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). The product's scratch
- * (split-K partials, repacked operands) lives in a 32 MiB array the library
- * holds on each device it runs on until the process ends; a product whose
+ * (split-K partials, repacked operands) lives in a 32 MiB `__device__` array
+ * that is part of the library's code object: every device the library is
+ * loaded on holds those 32 MiB from load until the process ends, whether or
+ * not this entry point is ever called. A product whose
  * shape-chosen kernel needs more is rejected with TVK_ERR_INVALID before
  * anything is queued (tvk_gemm takes it). The kernel is the shape rules'
  * choice (the kernel-choice table is not consulted). Every call on a device

@@ -158,3 +158,20 @@ def test_convnd_rejects_wrong_output_size():
     assert lib.tvk_conv_fwd(C.byref(d)) == _abi.TVK_ERR_INVALID
     assert b"out_size[1]" in lib.tvk_last_error()
     assert lib.tvk_conv_fwd(None) == _abi.TVK_ERR_INVALID
+
+
+def test_strict_allocation_switch():
+    # the reference's TORCHVULKAN_STRICT_ALLOCATION (src/vulkan/vulkan_context.cpp:248), switchable for the process
+    lib = _abi.load()
+    v = C.c_int(-1)
+    assert lib.tvk_get_strict_allocation(C.byref(v)) == _abi.TVK_OK
+    old = v.value
+    try:
+        for on in (1, 0):
+            assert lib.tvk_set_strict_allocation(on) == _abi.TVK_OK
+            assert lib.tvk_get_strict_allocation(C.byref(v)) == _abi.TVK_OK and v.value == on
+    finally:
+        lib.tvk_set_strict_allocation(old)
+    assert lib.tvk_host_free(C.c_void_p(16)) == _abi.TVK_ERR_INVALID   # not a tvk_host_malloc block
+    p = C.c_int(7)
+    assert lib.tvk_host_pointer_pinned(C.c_void_p(16), C.byref(p)) == _abi.TVK_OK and p.value == 0

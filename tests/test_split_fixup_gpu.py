@@ -80,3 +80,34 @@ def test_fused_two_streams_and_strided_output():
     assert np.array_equal(bits(got_t), bits(want))
     for i, o in enumerate(outs):
         assert np.array_equal(bits(o), bits(want)), f"call {i} on a side stream differs"
+
+
+def test_fused_after_cached_split_reduction_on_one_stream():
+    """A two-launch split-K product on the 128x128 ring (its reduction reads the partials with ordinary cached
+    loads, from the stream's pool buffer) alternates on one stream with the fused skinny product, which writes its
+    partials through to the same pool buffer and reads them back at system scope. Any stale L2 line left by the
+    cached reads would change the fused result's bits."""
+    s = torch.cuda.Stream()
+    ring_a = randn((256, 4096), torch.float16, 60).to(DEV)
+    ring_b = randn((4096, 2048), torch.float16, 61).to(DEV)
+    ring_c = torch.empty((256, 2048), dtype=torch.float16, device=DEV)
+    assert _abi.gemm_plan(ring_a, ring_b, ring_c) == "gemm16_dma_128x128_splitk"
+    M, N, K = 16, 14336, 4096
+    ops = [operands(M, N, K, 1, torch.float16, True, 70 + i) for i in range(3)]
+    wants = []
+    for a, b, bias in ops:
+        w = torch.empty((M, N), dtype=torch.float16, device=DEV)
+        two_launch(a, b, w, bias, 1.0)
+        wants.append(w)
+    ring_want = torch.empty_like(ring_c)
+    _abi.gemm_noalloc(ring_a, ring_b, ring_want)
+    torch.cuda.synchronize()
+    for it in range(6):
+        a, b, bias = ops[it % 3]
+        _abi.gemm(ring_a, ring_b, ring_c, stream=s.cuda_stream)            # partials through the pool, cached reads
+        got = torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV)
+        torch.cuda.synchronize()
+        _abi.gemm(a, b, got, bias=bias, beta=1.0, stream=s.cuda_stream)   # fused, same stream, same pool buffer
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(ring_c), bits(ring_want)), f"iteration {it}: ring split-K differs"
+        assert np.array_equal(bits(got), bits(wants[it % 3])), f"iteration {it}: fused split-K differs"

@@ -3,7 +3,8 @@
 results bit for bit on products that use scratch (split-K partials, repacked
 operands, the streaming kernel's partials) and on one that uses none, on two
 calls in a row with the second smaller (the array keeps the first call's
-contents), allocates no device memory, and rejects a product whose scratch
+contents), allocates no device memory (checked against an emptied scratch
+pool, where tvk_gemm's lease of the same product does allocate), and rejects a product whose scratch
 exceeds the array before queuing anything."""
 from __future__ import annotations
 
@@ -80,12 +81,21 @@ def test_noalloc_matches_tvk_gemm_twice(gpu, case):
         if step == 0:
             assert _abi.gemm_plan(a, b, c, **kw) == kernel
         torch.cuda.synchronize()
+        # drop every idle scratch-pool buffer and cached block first: a lease from the pool would
+        # then have to allocate a new buffer, which the reserved bytes would show
+        assert _abi.load().tvk_empty_cache(torch.cuda.current_device()) == _abi.TVK_OK
         held0 = reserved()
         assert noalloc(a, b, c, **kw) == _abi.TVK_OK, _abi.load().tvk_last_error()
         torch.cuda.synchronize()
         # no device memory was taken: the library's reserved bytes (allocator blocks and the
         # scratch pool's buffers) are unchanged
         assert reserved() == held0
+        # the check has teeth: tvk_gemm of a product that needs scratch leases a pool buffer,
+        # which the emptied pool must allocate
+        if step == 0 and kernel != "gemm_seq_mfma_64x128":
+            _abi.gemm(a, b, torch.empty_like(c), **kw)
+            torch.cuda.synchronize()
+            assert reserved() > held0
         _abi.gemm(a, b, c_ref, **kw)
         torch.cuda.synchronize()
         assert np.array_equal(bits(c), bits(c_ref)), f"case {case} step {step}: differs from tvk_gemm"

@@ -233,6 +233,12 @@ def load() -> C.CDLL:
         for fn in ("tvk_memory_allocated", "tvk_max_memory_allocated", "tvk_memory_reserved"):
             getattr(lib, fn).argtypes = [C.c_int, C.POINTER(C.c_size_t)]
         lib.tvk_set_memory_limit.argtypes = [C.c_int, C.c_size_t]
+        lib.tvk_set_strict_allocation.argtypes = [C.c_int]
+        lib.tvk_get_strict_allocation.argtypes = [C.POINTER(C.c_int)]
+        lib.tvk_last_malloc_spilled.argtypes = [C.POINTER(C.c_int)]
+        lib.tvk_host_malloc.argtypes = [C.c_size_t, C.POINTER(C.c_void_p)]
+        lib.tvk_host_free.argtypes = [C.c_void_p]
+        lib.tvk_host_pointer_pinned.argtypes = [C.c_void_p, C.POINTER(C.c_int)]
         lib.tvk_mem_get_info.argtypes = [C.c_int, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
         lib.tvk_device_properties.argtypes = [C.c_int, C.POINTER(DeviceProps)]
         for fn in ("tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad"):
@@ -257,7 +263,8 @@ def load() -> C.CDLL:
 _ALL_ENTRY_POINTS = (
     "tvk_last_error", "tvk_device_count", "tvk_set_device", "tvk_get_device", "tvk_get_stream",
     "tvk_synchronize", "tvk_device_properties", "tvk_malloc", "tvk_free", "tvk_empty_cache",
-    "tvk_pointer_device", "tvk_set_memory_limit", "tvk_memory_allocated", "tvk_max_memory_allocated",
+    "tvk_pointer_device", "tvk_set_memory_limit", "tvk_set_strict_allocation", "tvk_get_strict_allocation",
+    "tvk_last_malloc_spilled", "tvk_host_malloc", "tvk_host_free", "tvk_host_pointer_pinned", "tvk_memory_allocated", "tvk_max_memory_allocated",
     "tvk_memory_reserved", "tvk_reset_peak_memory_stats", "tvk_mem_get_info", "tvk_memcpy_h2d",
     "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan", "tvk_gemm_candidates",
     "tvk_gemm_choose", "tvk_gemm_tune", "tvk_tune_reset", "tvk_tune_path",

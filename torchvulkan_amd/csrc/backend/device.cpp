@@ -221,7 +221,16 @@ struct TvkAllocator final : c10::Allocator {
     c10::DataPtr allocate(size_t nbytes) override {
         const c10::DeviceIndex dev = g_current;
         void* p = nullptr;
-        if (nbytes) check_status(tvk_malloc(dev, nbytes, &p), "tvk_malloc");
+        if (nbytes) {
+            check_status(tvk_malloc(dev, nbytes, &p), "tvk_malloc");
+            int spilled = 0;
+            (void)tvk_last_malloc_spilled(&spilled);
+            // the reference's warning (src/vulkan/allocator.cpp:189-195)
+            if (spilled)
+                TORCH_WARN_ONCE("torchvulkan [WARNING]: Vulkan memory may be allocated using host memory, which may cause "
+                                "performance degradation. Set TORCHVULKAN_STRICT_ALLOCATION=1 to raise an out-of-memory "
+                                "error instead.");
+        }
         return {p, p, &free_fn, c10::Device(c10::DeviceType::PrivateUse1, dev)};
     }
     c10::DeleterFnPtr raw_deleter() const override { return &free_fn; }
@@ -231,6 +240,24 @@ struct TvkAllocator final : c10::Allocator {
 };
 
 TvkAllocator g_allocator;
+
+// Pinned host memory for tensor.pin_memory() (src/api/hook.cpp:14-51): page-
+// locked blocks from tvk_host_malloc, which the device's copies reach by DMA.
+void pinned_free_fn(void* p) {
+    if (p) (void)tvk_host_free(p);
+}
+
+struct TvkPinnedAllocator final : c10::Allocator {
+    c10::DataPtr allocate(size_t nbytes) override {
+        void* p = nullptr;
+        if (nbytes) check_status(tvk_host_malloc(nbytes, &p), "tvk_host_malloc");
+        return {p, p, &pinned_free_fn, c10::Device(c10::DeviceType::CPU)};
+    }
+    c10::DeleterFnPtr raw_deleter() const override { return &pinned_free_fn; }
+    void copy_data(void* dest, const void* src, std::size_t count) const override { std::memcpy(dest, src, count); }
+};
+
+TvkPinnedAllocator g_pinned_allocator;
 
 // ---------------------------------------------------------------------------
 // device guard. Every stream id of a device names the device's one library
@@ -351,8 +378,11 @@ struct TvkHooks final : at::PrivateUse1HooksInterface {
         TORCH_CHECK(dev >= 0, "torchvulkan [ERROR]: pointer was not allocated by the vulkan allocator");
         return at::Device(at::DeviceType::PrivateUse1, static_cast<c10::DeviceIndex>(dev));
     }
-    bool isPinnedPtr(const void*) const override { return false; }
-    at::Allocator* getPinnedMemoryAllocator() const override { return at::getCPUAllocator(); }
+    bool isPinnedPtr(const void* p) const override {
+        int pinned = 0;
+        return tvk_host_pointer_pinned(p, &pinned) == TVK_OK && pinned != 0;
+    }
+    at::Allocator* getPinnedMemoryAllocator() const override { return &g_pinned_allocator; }
     bool hasPrimaryContext(c10::DeviceIndex) const override { return true; }
     void resizePrivateUse1Bytes(const c10::Storage& storage, size_t newsize) const override {
         c10::StorageImpl* impl = storage.unsafeGetStorageImpl();
@@ -649,6 +679,12 @@ PYBIND11_MODULE(_C, m) {
     m.def("_memory_reserved", [](int64_t d) { return stat(tvk_memory_reserved, d); });
     m.def("_reset_peak_memory_stats", [](int64_t d) { tvkb::check_status(tvk_reset_peak_memory_stats((int)d), "reset_peak"); });
     m.def("_set_memory_limit", [](int64_t d, size_t bytes) { tvkb::check_status(tvk_set_memory_limit((int)d, bytes), "limit"); });
+    m.def("_set_strict_allocation", [](bool on) { tvkb::check_status(tvk_set_strict_allocation(on ? 1 : 0), "strict allocation"); });
+    m.def("_strict_allocation", []() {
+        int on = 0;
+        tvkb::check_status(tvk_get_strict_allocation(&on), "strict allocation");
+        return on != 0;
+    });
     m.def("_mem_get_info", [](int64_t d) {
         size_t f = 0, t = 0;
         tvkb::check_status(tvk_mem_get_info((int)d, &f, &t), "mem_get_info");

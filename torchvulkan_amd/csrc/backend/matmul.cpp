@@ -114,10 +114,12 @@ bool run_gemm(const at::Tensor& a, const at::Tensor& b, const at::Tensor& bias, 
     std::memset(&d, 0, sizeof(d));
     d.dtype = tdt;
     d.activation = act;
-    d.flags = 0;
-    if (const char* e = std::getenv("TORCHVULKAN_EXACT")) {
-        if (e[0] && std::strcmp(e, "0") != 0) d.flags = TVK_GEMM_EXACT;
-    }
+    // TORCHVULKAN_EXACT is read once, at the first product
+    static const bool exact = [] {
+        const char* e = std::getenv("TORCHVULKAN_EXACT");
+        return e && e[0] && std::strcmp(e, "0") != 0;
+    }();
+    d.flags = exact ? TVK_GEMM_EXACT : 0;
     d.batch = out.size(0); d.M = out.size(1); d.N = out.size(2); d.K = a.size(2);
     d.a = a.data_ptr();
     d.b = b.data_ptr();

@@ -181,12 +181,21 @@ __device__ __forceinline__ bool finish4_vec(const GemmArgs& p) {
 }
 
 // Split-K without a second launch. The float32 partial planes of such a
-// launch are written through to memory (stores at system coherence: the L2 of
-// each XCD is private, and a device-scope fence would write back and
-// invalidate whole L2s under every other workgroup's loads) and read back
-// with loads that miss in L2. Buffer offsets are 32-bit: the host keeps the
+// launch are written through to memory and read back coherently, without a
+// fence: the L2 of each XCD is private, and a device-scope fence would write
+// back and invalidate whole L2s under every other workgroup's loads.
+// The cache-policy operand's SC1:SC0 bits select the scope of a vector memory
+// instruction on gfx942/gfx950 (AMD CDNA3 ISA reference, "Memory Scope and
+// Temporal Controls": 0 wave, 1 workgroup, 2 device, 3 system). At system
+// scope a store writes through the L2 to memory and a load is coherent at
+// that scope, so it cannot return a line another XCD's L2 held from before
+// the write; the LLVM AMDGPU memory model for GFX942 (AMDGPUUsage, "Memory
+// Model GFX942") emits the same sc0=1 sc1=1 bits for system-scope atomic
+// loads and stores. tests/test_split_fixup_gpu.py alternates these launches
+// with a two-launch split-K whose reduction reads the same pool buffer with
+// ordinary cached loads. Buffer offsets are 32-bit: the host keeps the
 // partials under 2 GiB.
-constexpr int kCoherent = 1 | 16;   // sc0 | sc1 cache-policy bits
+constexpr int kCoherent = 1 | 16;   // sc0 | sc1: system scope
 
 __device__ inline __amdgpu_buffer_rsrc_t part_rsrc(const GemmArgs& p) {
     const int64_t bytes = (int64_t)p.split * p.batch * p.M * p.N * 4;

@@ -11,6 +11,8 @@
 #include "tvk_common.h"
 #include "scratch_pool.h"
 
+#include <atomic>
+#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <unordered_map>
@@ -41,6 +43,7 @@ struct DeviceState {
 struct Block {
     size_t size;
     int device;
+    bool host;   // served from pinned host memory (past the device's memory, strict allocation off)
 };
 
 std::mutex g_mu;
@@ -54,6 +57,17 @@ size_t size_class(size_t bytes) {
     const size_t g = size_t(2) << 20;
     return (bytes + g - 1) / g * g;
 }
+
+// TORCHVULKAN_STRICT_ALLOCATION, read when the library loads; tvk_set_strict_allocation changes it
+std::atomic<int> g_strict_alloc{[] {
+    const char* e = std::getenv("TORCHVULKAN_STRICT_ALLOCATION");
+    return (e && e[0] && std::strcmp(e, "0") != 0) ? 1 : 0;
+}()};
+thread_local int g_last_spilled = 0;
+
+// Pinned host blocks of tvk_host_malloc: start -> bytes
+std::mutex g_host_mu;
+std::map<uintptr_t, size_t> g_host_blocks;
 
 bool valid_device(int d) {
     int n = 0;
@@ -140,22 +154,34 @@ void Scratch::release() {
 
 namespace {
 constexpr int64_t kSplitCounters = 16384;   // 64 KB a stream: 16384 output tiles
+// Counter arrays are never freed (a launch may hold one it looked up before a
+// free could run); instead at most this many streams a device get one, 2 MB in
+// all. Launches on further streams take the two-launch reduction.
+constexpr int kMaxCounterStreams = 32;
 std::mutex g_counter_mu;
 std::map<std::pair<int, hipStream_t>, unsigned*> g_counters;
+int g_counter_streams[kMaxDevices] = {};
 }  // namespace
 
 unsigned* split_counters(hipStream_t stream, int64_t count) {
     if (count <= 0 || count > kSplitCounters) return nullptr;
+    // One handle that stands for every thread's own stream: launches from two
+    // threads could overlap on one counter array.
+    if (stream == hipStreamPerThread) return nullptr;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lk(g_counter_mu);
-    auto it = g_counters.find({dev, stream});
-    if (it != g_counters.end()) return it->second;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    // Under capture the graph could be replayed on another stream, concurrently
+    // with launches on this one, so captured launches never take the array
+    // (checked before the lookup: the stream may have used it before capture).
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
         (void)hipGetLastError();
         return nullptr;
     }
+    std::lock_guard<std::mutex> lk(g_counter_mu);
+    auto it = g_counters.find({dev, stream});
+    if (it != g_counters.end()) return it->second;
+    if (g_counter_streams[dev] >= kMaxCounterStreams) return nullptr;
     unsigned* p = nullptr;
     if (hipMalloc(reinterpret_cast<void**>(&p), kSplitCounters * sizeof(unsigned)) != hipSuccess) {
         (void)hipGetLastError();
@@ -167,6 +193,7 @@ unsigned* split_counters(hipStream_t stream, int64_t count) {
         return nullptr;
     }
     g_counters[{dev, stream}] = p;
+    ++g_counter_streams[dev];
     return p;
 }
 
@@ -326,39 +353,72 @@ tvk_status tvk_device_properties(int device, tvk_device_props* out) {
 tvk_status tvk_malloc(int device, size_t bytes, void** out) {
     if (!out) return fail(TVK_ERR_INVALID, "tvk_malloc: out is NULL");
     *out = nullptr;
+    g_last_spilled = 0;
     if (!valid_device(device)) return fail(TVK_ERR_INVALID, "tvk_malloc: invalid device index " + std::to_string(device));
     if (bytes == 0) return TVK_OK;
     const size_t sz = size_class(bytes);
     std::lock_guard<std::mutex> lk(g_mu);
     DeviceState& st = g_dev[device];
-    if (st.limit && st.allocated + sz > st.limit)
-        return fail(TVK_ERR_OOM, "tvk_malloc: allocating " + std::to_string(bytes) + " bytes would exceed the memory limit of " +
-                                     std::to_string(st.limit) + " bytes (" + std::to_string(st.allocated) + " in use)");
     void* p = nullptr;
-    auto it = st.free_blocks.find(sz);
-    if (it != st.free_blocks.end() && !it->second.empty()) {
-        p = it->second.back();
-        it->second.pop_back();
+    bool host = false;
+    hipError_t e = hipSuccess;
+    if (st.limit && st.allocated + sz > st.limit) {
+        e = hipErrorOutOfMemory;   // past the budget: spill or fail, as when the device is full
     } else {
+        auto it = st.free_blocks.find(sz);
+        if (it != st.free_blocks.end() && !it->second.empty()) {
+            p = it->second.back();
+            it->second.pop_back();
+        } else {
+            int prev = 0;
+            (void)hipGetDevice(&prev);
+            (void)hipSetDevice(device);
+            e = hipMalloc(&p, sz);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                // give the cache back and retry once
+                release_cached_locked(device);
+                (void)hipSetDevice(device);
+                e = hipMalloc(&p, sz);
+            }
+            (void)hipSetDevice(prev);
+            if (e == hipSuccess) st.reserved += sz;
+            else (void)hipGetLastError();
+        }
+    }
+    if (!p) {
+        // The reference's allocateBuffer (src/vulkan/allocator.cpp:171-200): past
+        // the budget it allocates anyway unless strict allocation is on. Here the
+        // memory then comes from pinned host memory, which kernels reach over the
+        // host link.
+        const std::string what = "tvk_malloc: out of memory on device " + std::to_string(device) + ". Tried to allocate " +
+                                 std::to_string(bytes) + " bytes with " + std::to_string(st.allocated) + " bytes in use" +
+                                 (st.limit ? " (limit " + std::to_string(st.limit) + ")" : std::string());
+        if (g_strict_alloc.load()) return fail(TVK_ERR_OOM, what + ".");
         int prev = 0;
         (void)hipGetDevice(&prev);
         (void)hipSetDevice(device);
-        hipError_t e = hipMalloc(&p, sz);
-        if (e != hipSuccess) {
-            (void)hipGetLastError();
-            // give the cache back and retry once
-            release_cached_locked(device);
-            (void)hipSetDevice(device);
-            e = hipMalloc(&p, sz);
+        e = hipHostMalloc(&p, sz, hipHostMallocMapped | hipHostMallocPortable);
+        if (e == hipSuccess) {
+            // kernels take the pointer as a device address: only a block the
+            // device sees at the same address is handed out
+            void* dp = nullptr;
+            if (hipHostGetDevicePointer(&dp, p, 0) != hipSuccess || dp != p) {
+                (void)hipGetLastError();
+                (void)hipHostFree(p);
+                p = nullptr;
+                e = hipErrorOutOfMemory;
+            }
         }
         (void)hipSetDevice(prev);
         if (e != hipSuccess) {
             (void)hipGetLastError();
-            return fail(TVK_ERR_OOM, "tvk_malloc: out of device memory allocating " + std::to_string(bytes) + " bytes");
+            return fail(TVK_ERR_OOM, what + ", and pinned host memory could not hold it either.");
         }
-        st.reserved += sz;
+        host = true;
+        g_last_spilled = 1;
     }
-    g_live[p] = Block{sz, device};
+    g_live[p] = Block{sz, device, host};
     st.allocated += sz;
     if (st.allocated > st.peak) st.peak = st.allocated;
     *out = p;
@@ -372,8 +432,75 @@ tvk_status tvk_free(void* ptr) {
     if (it == g_live.end()) return fail(TVK_ERR_INVALID, "tvk_free: pointer was not allocated by tvk_malloc");
     DeviceState& st = g_dev[it->second.device];
     st.allocated -= it->second.size;
-    st.free_blocks[it->second.size].push_back(ptr);
+    if (it->second.host) {
+        // spilled blocks are not cached: freed once the device has drained the
+        // work that may still read or write them
+        int prev = 0;
+        (void)hipGetDevice(&prev);
+        (void)hipSetDevice(it->second.device);
+        (void)hipDeviceSynchronize();
+        (void)hipHostFree(ptr);
+        (void)hipSetDevice(prev);
+    } else {
+        st.free_blocks[it->second.size].push_back(ptr);
+    }
     g_live.erase(it);
+    return TVK_OK;
+}
+
+tvk_status tvk_set_strict_allocation(int strict) {
+    g_strict_alloc.store(strict ? 1 : 0);
+    return TVK_OK;
+}
+
+tvk_status tvk_get_strict_allocation(int* strict) {
+    if (!strict) return fail(TVK_ERR_INVALID, "tvk_get_strict_allocation: strict is NULL");
+    *strict = g_strict_alloc.load();
+    return TVK_OK;
+}
+
+tvk_status tvk_last_malloc_spilled(int* spilled) {
+    if (!spilled) return fail(TVK_ERR_INVALID, "tvk_last_malloc_spilled: spilled is NULL");
+    *spilled = g_last_spilled;
+    return TVK_OK;
+}
+
+tvk_status tvk_host_malloc(size_t bytes, void** out) {
+    if (!out) return fail(TVK_ERR_INVALID, "tvk_host_malloc: out is NULL");
+    *out = nullptr;
+    if (bytes == 0) return TVK_OK;
+    void* p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(TVK_ERR_OOM, "tvk_host_malloc: could not pin " + std::to_string(bytes) + " bytes of host memory");
+    }
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    g_host_blocks[reinterpret_cast<uintptr_t>(p)] = bytes;
+    *out = p;
+    return TVK_OK;
+}
+
+tvk_status tvk_host_free(void* ptr) {
+    if (!ptr) return TVK_OK;
+    {
+        std::lock_guard<std::mutex> lk(g_host_mu);
+        auto it = g_host_blocks.find(reinterpret_cast<uintptr_t>(ptr));
+        if (it == g_host_blocks.end()) return fail(TVK_ERR_INVALID, "tvk_host_free: pointer was not allocated by tvk_host_malloc");
+        g_host_blocks.erase(it);
+    }
+    TVK_HIP_CHECK(hipHostFree(ptr));
+    return TVK_OK;
+}
+
+tvk_status tvk_host_pointer_pinned(const void* ptr, int* pinned) {
+    if (!pinned) return fail(TVK_ERR_INVALID, "tvk_host_pointer_pinned: pinned is NULL");
+    *pinned = 0;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(ptr);
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    auto it = g_host_blocks.upper_bound(a);
+    if (it == g_host_blocks.begin()) return TVK_OK;
+    --it;
+    *pinned = a < it->first + std::max<size_t>(it->second, 1) ? 1 : 0;
     return TVK_OK;
 }
 
