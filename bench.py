@@ -37,11 +37,13 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 MEASURED_TRAFFIC = {
     "gemm16_dma_256x256": {"bytes": 1.764e9, "fetch_kib": 795667, "write_kib": 131072},
 }
-# the headline kernel under counters (profiles/mfma_ceiling_calibration.md)
+# the headline kernel and the MFMA ceiling loop under counters
 MEASURED_COUNTERS = {
     "gemm16_dma_256x256": {"mfma_busy_pct": [70.6, 74.0], "shader_clock_ghz": [1.28, 1.70],
-                           "ceiling_loop_mfma_busy_pct": [77.6, 78.8], "ceiling_loop_clock_ghz": [1.90, 1.93],
-                           "source": "profiles/mfma_ceiling_calibration.md"},
+                           "source": "profiles/gemm_fp16_8192_counters.md",
+                           "ceiling_loop_random": {"mfma_busy_pct": [95.1, 97.2], "shader_clock_ghz": [1.83, 1.90]},
+                           "ceiling_loop_zero": {"mfma_busy_pct": [98.6, 98.7], "shader_clock_ghz": [2.30, 2.39]},
+                           "ceiling_source": "profiles/mfma_ceiling_calibration.md"},
 }
 
 
@@ -52,10 +54,11 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-extra", action="store_true", help="headline only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--profile-kernel", choices=["gemm", "skinny", "copy", "ceiling"],
+    p.add_argument("--profile-kernel", choices=["gemm", "skinny", "copy", "ceiling", "ceiling_zero"],
                    help="launch only this kernel --steps times and exit (for rocprofv3 counter passes); "
                         "'copy' is torch's copy of a 1 GiB buffer, the calibration for FETCH_SIZE/WRITE_SIZE; "
-                        "'ceiling' the random-operand MFMA loop of tvk_calibrate_mfma (two waves per SIMD)")
+                        "'ceiling' the random-operand MFMA loop of tvk_calibrate_mfma (two waves per SIMD), "
+                        "'ceiling_zero' the same loop on all-zero operands")
     p.add_argument("--vendor", action="store_true",
                    help="time the C2 GEMM chain, the C3 layer GEMMs, the C4 conv layers and the C5 products "
                         "through torch on this GPU (hipBLASLt, MIOpen) with the same shapes and data, print one "
@@ -195,10 +198,10 @@ def profile_kernel(which, steps):
     lib = _abi.load()
     dev = torch.device("cuda:0")
     s = torch.cuda.current_stream(dev).cuda_stream
-    if which == "ceiling":
+    if which in ("ceiling", "ceiling_zero"):
         for _ in range(steps):
-            tf, _ = _abi.calibrate_mfma(0, 2, 40000)
-        print(f"ceiling: {steps} launches, last {tf:.1f} TFLOP/s", flush=True)
+            tf, _ = _abi.calibrate_mfma(0, 2, 40000, zeros=which == "ceiling_zero")
+        print(f"{which}: {steps} launches, last {tf:.1f} TFLOP/s", flush=True)
         return
     if which == "copy":
         x = torch.ones((1 << 29,), dtype=torch.float16, device=dev)   # 1 GiB
@@ -315,18 +318,20 @@ def main():
         "algorithmic_bytes": 3 * n * n * 2,
         "avg_kernel_ms": round(ms, 5),
     }
-    # the power-limited ceiling on this box: the MFMA rate with random fp16
-    # operands (tvk_calibrate_mfma), at one and two waves per SIMD (the
-    # headline kernel runs two); the dense peak needs operands that barely toggle
+    # the ceiling on this box: the issue-saturated MFMA loop of tvk_calibrate_mfma
+    # with random fp16 operands (the power-limited rate a GEMM on random data can
+    # reach) and with all-zero operands (the pipe's issue rate at the full clock)
     ceiling = {}
     _abi.calibrate_mfma(0, 2, 40000)   # the clock settles under the load first
     for w in (1, 2, 4):
         tf, _ = _abi.calibrate_mfma(0, w, 40000)
         ceiling[f"waves_per_simd_{w}"] = round(tf, 1)
     top = max(ceiling.values())
+    zero_tf = max(_abi.calibrate_mfma(0, 2, 40000, zeros=True)[0] for _ in range(2))
     roofline["ceiling"] = {
-        "what": "v_mfma_f32_16x16x32_f16 loop, random fp16 operands, no memory traffic (tvk_calibrate_mfma)",
-        "unit": "TFLOP/s", **ceiling, "max": top,
+        "what": "v_mfma_f32_16x16x32_f16 loop, 16 accumulators, no memory traffic (tvk_calibrate_mfma): random fp16 "
+                "operands; zero_operands is the same loop on all-zero operands",
+        "unit": "TFLOP/s", **ceiling, "max": top, "zero_operands": round(zero_tf, 1),
         "frac_of_ceiling": round(tflops / top, 4),
     }
     roofline["counters"] = MEASURED_COUNTERS.get(plan)

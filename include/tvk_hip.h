@@ -136,13 +136,18 @@ tvk_status tvk_device_properties(int device, tvk_device_props* out);
 
 /* Measurement aid with no counterpart in the reference: the sustained float16
  * MFMA rate of `device` with random operands (v_mfma_f32_16x16x32_f16 over
- * eight independent accumulators, `waves_per_simd` waves on every SIMD, 1-4),
+ * sixteen independent accumulators, 64 a loop trip, `waves_per_simd` waves on every SIMD, 1-4),
  * timed with HIP events over one launch of `iterations` steps on a stream of
  * its own. The dense-peak figure assumes operands that barely toggle; with
  * random data the part is power-limited, and this rate is the ceiling a GEMM's
  * MFMA pipe can reach. *tflops and the launch's *ms on return. Allocates and
  * synchronises: not for hot paths. */
 tvk_status tvk_calibrate_mfma(int device, int waves_per_simd, int iterations, double* tflops, double* ms);
+/* The same loop with `operands` 0 (random, as tvk_calibrate_mfma) or 1 (all
+ * zeros: operands that toggle nothing, which shows the pipe's issue limit
+ * apart from the part's power limit). */
+tvk_status tvk_calibrate_mfma_operands(int device, int waves_per_simd, int iterations, int operands, double* tflops,
+                                       double* ms);
 
 /* Measurement aid with no counterpart in the reference: the read bandwidth of
  * a plain streaming kernel on `device` (512 workgroups, four 16-byte loads in

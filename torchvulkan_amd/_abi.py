@@ -253,6 +253,8 @@ def load() -> C.CDLL:
         lib.tvk_attention_fwd.argtypes = [C.POINTER(AttentionDesc)]
         lib.tvk_attention_bwd.argtypes = [C.POINTER(AttentionBwdDesc)]
         lib.tvk_calibrate_mfma.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        lib.tvk_calibrate_mfma_operands.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double),
+                                                    C.POINTER(C.c_double)]
         lib.tvk_calibrate_hbm.argtypes = [C.c_int, C.c_size_t, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]
         for fn in _ALL_ENTRY_POINTS:
             getattr(lib, fn).restype = C.c_int if fn != "tvk_last_error" else C.c_char_p
@@ -273,7 +275,7 @@ _ALL_ENTRY_POINTS = (
     "tvk_fill", "tvk_reduce_sum", "tvk_binary", "tvk_attention_fwd",
     "tvk_attention_bwd", "tvk_gemm_noalloc", "tvk_event_create", "tvk_event_destroy", "tvk_event_record",
     "tvk_event_query", "tvk_event_synchronize", "tvk_event_elapsed", "tvk_stream_wait_event", "tvk_stream_query",
-    "tvk_calibrate_mfma",
+    "tvk_calibrate_mfma", "tvk_calibrate_mfma_operands",
     "tvk_calibrate_hbm",
 )
 
@@ -312,10 +314,12 @@ def calibrate_hbm(device: int = 0, window_bytes: int = 4096 * 14336 * 2, iterati
     return gb.value, ms.value
 
 
-def calibrate_mfma(device: int = 0, waves_per_simd: int = 2, iterations: int = 20000) -> tuple[float, float]:
-    """(TFLOP/s, ms) of tvk_calibrate_mfma: the float16 MFMA rate with random operands."""
+def calibrate_mfma(device: int = 0, waves_per_simd: int = 2, iterations: int = 20000,
+                   zeros: bool = False) -> tuple[float, float]:
+    """(TFLOP/s, ms) of tvk_calibrate_mfma_operands: the float16 MFMA rate with random (or all-zero) operands."""
     tf, ms = C.c_double(), C.c_double()
-    check(load().tvk_calibrate_mfma(device, waves_per_simd, iterations, C.byref(tf), C.byref(ms)))
+    check(load().tvk_calibrate_mfma_operands(device, waves_per_simd, iterations, 1 if zeros else 0, C.byref(tf),
+                                             C.byref(ms)))
     return tf.value, ms.value
 
 

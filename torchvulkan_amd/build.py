@@ -57,10 +57,13 @@ def _run(cmd: list[str]) -> None:
 # rescale steps work on the accumulators with ordinary VALU instructions, and
 # in the AGPR form hipcc rotates the GEMM and convolution kernels'
 # accumulators through AGPR copies inside their k loops (the 256x256 ring
-# GEMM, gemm_dma.hip, and gemm.hip allocate cleanly in the default form).
+# GEMM, gemm_dma.hip, and gemm.hip allocate cleanly in the default form). The
+# MFMA calibration loop rotates its sixteen accumulators through 88 AGPR
+# copies a trip in the AGPR form and issues only MFMAs in the VGPR form.
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 FILE_FLAGS = {
     "attention.hip": VGPR_FORM,
+    "calibrate.hip": VGPR_FORM,
     "gemm_dma128.hip": VGPR_FORM,
     "gemm_skinny.hip": VGPR_FORM,
     "conv.hip": VGPR_FORM,

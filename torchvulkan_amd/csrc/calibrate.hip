@@ -6,14 +6,16 @@
 // part is power-limited, and that lower ceiling is what a GEMM's MFMA pipe
 // can reach at all. The GEMM kernels' roofline reports carry both.
 //
-// Kernel: every wave holds four pairs of random float16 A/B fragments
-// (uniform in [-1, 1), from a per-lane hash) and issues
-// v_mfma_f32_16x16x32_f16 in a loop over eight independent accumulators,
-// cycling through the fragment pairs so consecutive MFMAs see different
-// operands. No memory traffic inside the loop; the accumulators are summed
-// and stored at the end so nothing is removed. A grid of 256 CUs x 4 SIMDs x
-// `waves_per_simd` waves (`waves_per_simd` workgroups of 256 threads per CU),
-// timed with HIP events around the launch.
+// Kernel: every wave holds four pairs of float16 A/B fragments (random:
+// uniform in [-1, 1) from a per-lane hash; or all zeros, the operands that
+// toggle nothing) and issues v_mfma_f32_16x16x32_f16 over sixteen independent
+// accumulators, 64 MFMAs per loop trip (one scalar add, compare and branch per
+// 64 MFMAs), cycling through the fragment pairs so consecutive MFMAs see
+// different operands. No memory traffic inside the loop; the accumulators are
+// summed and stored at the end so nothing is removed. A grid of 256 CUs x 4
+// SIMDs x `waves_per_simd` waves (`waves_per_simd` workgroups of 256 threads
+// per CU), timed with HIP events around the launch. Random against zero
+// operands separates the pipe's issue limit from the part's power limit.
 //
 // tvk_calibrate_hbm: the read bandwidth a plain streaming kernel reaches, the
 // practical ceiling of an HBM-bound kernel that reads each byte once (the
@@ -51,29 +53,33 @@ __device__ inline half8 rand_frag(uint32_t seed) {
     return v;
 }
 
-__global__ __launch_bounds__(256) void mfma_ceiling_kernel(int iterations, float* out) {
+__global__ __launch_bounds__(256) void mfma_ceiling_kernel(int iterations, int zeros, float* out) {
     const uint32_t id = blockIdx.x * 256u + threadIdx.x;
     half8 a[4], b[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         a[i] = rand_frag(id * 16u + (uint32_t)i);
         b[i] = rand_frag(id * 16u + 8u + (uint32_t)i);
-    }
-    f32x4 acc[8];
+        if (zeros) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // four steps a trip, so every fragment index is a constant (the fragments
-    // stay in registers)
+            for (int e = 0; e < 8; ++e) a[i][e] = b[i][e] = (_Float16)0.0f;
+        }
+    }
+    f32x4 acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // 64 MFMAs a trip, four per accumulator; every fragment index is a
+    // constant, so the fragments stay in registers
     for (int it = 0; it < iterations; it += 4) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j % 4], b[(j + r) % 4], acc[j], 0, 0, 0);
+            for (int j = 0; j < 16; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j % 4], b[(j / 4 + r) % 4], acc[j], 0, 0, 0);
     }
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+    for (int j = 0; j < 16; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
     out[id] = s;
 }
 
@@ -142,8 +148,10 @@ extern "C" tvk_status tvk_calibrate_hbm(int device, size_t window_bytes, int ite
     return st;
 }
 
-extern "C" tvk_status tvk_calibrate_mfma(int device, int waves_per_simd, int iterations, double* tflops, double* ms) {
+extern "C" tvk_status tvk_calibrate_mfma_operands(int device, int waves_per_simd, int iterations, int operands, double* tflops,
+                                                  double* ms) {
     if (!tflops || !ms) return fail(TVK_ERR_INVALID, "tvk_calibrate_mfma: tflops or ms is NULL");
+    if (operands != 0 && operands != 1) return fail(TVK_ERR_INVALID, "tvk_calibrate_mfma: operands must be 0 (random) or 1 (zeros)");
     if (waves_per_simd < 1 || waves_per_simd > 4 || iterations < 1)
         return fail(TVK_ERR_INVALID, "tvk_calibrate_mfma: waves_per_simd must be 1..4 and iterations positive");
     int cur = 0;
@@ -162,9 +170,9 @@ extern "C" tvk_status tvk_calibrate_mfma(int device, int waves_per_simd, int ite
             st = fail(TVK_ERR_DEVICE, "tvk_calibrate_mfma: stream or event creation failed");
             break;
         }
-        hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(blocks), dim3(256), 0, s, iterations / 8 + 4, out);   // warm-up
+        hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(blocks), dim3(256), 0, s, iterations / 8 + 4, operands, out);   // warm-up
         if (hipEventRecord(e0, s) != hipSuccess) { st = fail(TVK_ERR_DEVICE, "tvk_calibrate_mfma: event record failed"); break; }
-        hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(blocks), dim3(256), 0, s, iterations, out);
+        hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(blocks), dim3(256), 0, s, iterations, operands, out);
         if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) {
             st = fail(TVK_ERR_DEVICE, std::string("tvk_calibrate_mfma: ") + hipGetErrorString(hipGetLastError()));
             break;
@@ -172,7 +180,7 @@ extern "C" tvk_status tvk_calibrate_mfma(int device, int waves_per_simd, int ite
         float t = 0.0f;
         if (hipEventElapsedTime(&t, e0, e1) != hipSuccess) { st = fail(TVK_ERR_DEVICE, "tvk_calibrate_mfma: elapsed time failed"); break; }
         const double steps = (double)((iterations + 3) / 4 * 4);
-        const double flops = (double)blocks * 4.0 * 8.0 * steps * 16.0 * 16.0 * 32.0 * 2.0;
+        const double flops = (double)blocks * 4.0 * 16.0 * steps * 16.0 * 16.0 * 32.0 * 2.0;
         *ms = t;
         *tflops = flops / ((double)t * 1e-3) / 1e12;
     } while (false);
@@ -182,4 +190,8 @@ extern "C" tvk_status tvk_calibrate_mfma(int device, int waves_per_simd, int ite
     if (out) (void)hipFree(out);
     (void)hipSetDevice(cur);
     return st;
+}
+
+extern "C" tvk_status tvk_calibrate_mfma(int device, int waves_per_simd, int iterations, double* tflops, double* ms) {
+    return tvk_calibrate_mfma_operands(device, waves_per_simd, iterations, 0, tflops, ms);
 }
