@@ -618,12 +618,31 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
 
     ms, _ = timed(matmul_step, steps, warmup, stream)
     copy_by = 3 * 2 * 2 * Bq * L * H * D
+    out["c3_head_strided_bmm_reshape_copies_us"] = round(ms * 1e3, 2)
+    out["c3_head_strided_bmm_reshape_copies_path"] = "3 reshape copies to [B*H, ., .] + 2 bmm of batch B*H (torch's composite matmul)"
+
+    # the same products as the device's matmul runs them: the [B, H, L, D] views as
+    # they are, one product each over two batch dimensions (B, and H with its own stride)
+    q4, k4t, v4 = qs.permute(0, 2, 1, 3), ks.permute(0, 2, 3, 1), vs.permute(0, 2, 1, 3)
+    s4 = torch.empty((Bq, H, L, L), dtype=torch.float16, device=dev)
+    o4 = torch.empty((Bq, H, L, D), dtype=torch.float16, device=dev)
+    g2 = [_abi.make_gemm_desc(q4, k4t, s4, stream=s), _abi.make_gemm_desc(s4, v4, o4, stream=s)]
+    g2refs = [C.byref(d) for d in g2]
+
+    def two_level_step():
+        for r in g2refs:
+            st_ = lib.tvk_gemm(r)
+            if st_:
+                _abi.check(st_)
+
+    ms, _ = timed(two_level_step, steps, warmup, stream)
     out["c3_head_strided_bmm_us"] = round(ms * 1e3, 2)
-    out["c3_head_strided_bmm_path"] = "torch.matmul on [B, H, L, D] views: 3 reshape copies + 2 bmm of batch B*H"
-    out["c3_head_strided_bmm_kernels"] = [gemm_plan_of(_abi, gds[0]), gemm_plan_of(_abi, gds[1])]
-    out["c3_head_strided_bmm_roofline_frac"] = round(bound_us(bmm_fl, bmm_by + copy_by) / (ms * 1e3), 4)
+    out["c3_head_strided_bmm_path"] = ("torch.matmul on [B, H, L, D] views on the vulkan device: one product each over two "
+                                       "batch dimensions (tvk_gemm_desc.batch_inner), no copies")
+    out["c3_head_strided_bmm_kernels"] = [gemm_plan_of(_abi, g2[0]), gemm_plan_of(_abi, g2[1])]
+    out["c3_head_strided_bmm_roofline_frac"] = round(bound_us(bmm_fl, bmm_by) / (ms * 1e3), 4)
     progress("C3 head-strided bmm done")
-    del qs, ks, vs, ss, os_, qc, ktc, vc, sc, oc, cds, gds, crefs, grefs
+    del qs, ks, vs, ss, os_, qc, ktc, vc, sc, oc, cds, gds, crefs, grefs, s4, o4, g2, g2refs
 
     # ---- C3 attention: fused forward, batch 32, 8 query / 2 kv heads, seq 256, head_dim 64, causal
     qa = torch.randn((32, 8, 256, 64), generator=g).to(torch.float16).to(dev)
@@ -728,7 +747,96 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c1_fp32_roofline_frac"] = round(max(2 * 1024 ** 3 / (PEAK_F32_TFLOPS * 1e12), 12 * 1024 ** 2 / (PEAK_HBM_GBS * 1e9))
                                          * 1e6 / (ms * 1e3), 4)
     out["c1_kernel"] = _abi.gemm_plan(a, b, c)
+
+    # ---- the drop-in path: whole fwd+bwd steps through autograd on "vulkan" ----
+    out["dropin_steps"] = run_dropin(torch, out)
+    progress("drop-in steps done")
     return out
+
+
+def run_dropin(torch, chains):
+    """Whole training steps through the vulkan device, timed as the reference's
+    benchmark times them (benchmark/benchmark.py:208-223): zero_grad, then
+    synchronize, loss.backward() over the forward, synchronize, and the median
+    over 10 steps after 3 warm-ups. Everything between the two synchronizes
+    counts: dispatch, autograd, the allocator, casts and the bias and loss sums,
+    besides the products the C-ABI chains time alone. The models hold only ops
+    on the path (no activations: ops outside it run on the CPU fallback), and
+    strict mode is on while they run, so any fallback would fail the run."""
+    import statistics
+
+    import torchvulkan_amd as tv
+
+    V = "vulkan"
+    g = torch.Generator().manual_seed(3)
+    res = {}
+
+    def median_step(params, loss_fn, iters=10, warm=3):
+        times = []
+        for i in range(warm + iters):
+            for q in params:
+                q.grad = None
+            tv.synchronize()
+            t0 = time.perf_counter()
+            loss_fn().backward()
+            tv.synchronize()
+            t1 = time.perf_counter()
+            if i >= warm:
+                times.append((t1 - t0) * 1e3)
+        return statistics.median(times)
+
+    old = os.environ.get("TORCHVULKAN_STRICT")
+    os.environ["TORCHVULKAN_STRICT"] = "1"
+    try:
+        # C2: the MLP 784-4096-4096-4096-10, fp16, batch 256, inputs U(0,1), nn.Linear's initialisation
+        dims = [784, 4096, 4096, 4096, 10]
+        torch.manual_seed(3)
+        layers = [torch.nn.Linear(dims[i], dims[i + 1]).to(torch.float16).to(V) for i in range(4)]
+        params = [q for lay in layers for q in lay.parameters()]
+        x = torch.rand((256, dims[0]), generator=g).to(torch.float16).to(V)
+
+        def mlp_loss():
+            y = x
+            for lay in layers:
+                y = lay(y)
+            return y.sum()
+
+        ms = median_step(params, mlp_loss)
+        res["c2_mlp_fwd_bwd_ms"] = round(ms, 4)
+        res["c2_vs_gemm_chain"] = round(ms / chains["c2_mlp_gemm_fwd_bwd_ms"], 2) if chains.get("c2_mlp_gemm_fwd_bwd_ms") else None
+        del layers, params, x
+        # C4: the ResNet layers as one block chain, fp16, batch 128, 32x32, Kaiming-normal weights: stem 3->64,
+        # 3x3 64->64, then two stride-2 stages whose 1x1 downsample convs are added to the 3x3 ones
+        def kconv(cin, cout, k):
+            w = torch.randn((cout, cin, k, k), generator=g) * (2.0 / (cin * k * k)) ** 0.5
+            return w.to(torch.float16).to(V).requires_grad_()
+
+        ws = {"stem": kconv(3, 64, 3), "c64": kconv(64, 64, 3), "c128": kconv(64, 128, 3), "d128": kconv(64, 128, 1),
+              "c256": kconv(128, 256, 3), "d256": kconv(128, 256, 1)}
+        xi = torch.randn((128, 3, 32, 32), generator=g).to(torch.float16).to(V)
+        F = torch.nn.functional
+
+        def block_loss():
+            h1 = F.conv2d(xi, ws["stem"], padding=1)
+            h2 = F.conv2d(h1, ws["c64"], padding=1)
+            h3 = F.conv2d(h2, ws["c128"], stride=2, padding=1) + F.conv2d(h2, ws["d128"], stride=2)
+            h4 = F.conv2d(h3, ws["c256"], stride=2, padding=1) + F.conv2d(h3, ws["d256"], stride=2)
+            return h4.sum()
+
+        ms = median_step(list(ws.values()), block_loss)
+        res["c4_block_fwd_bwd_ms"] = round(ms, 4)
+        res["c4_vs_conv_chain"] = (round(ms / chains["c4_resnet_conv_fwd_bwd_ms"], 2)
+                                   if chains.get("c4_resnet_conv_fwd_bwd_ms") else None)
+        res["fallbacks"] = 0
+        res["note"] = ("median of 10 after 3 (zero_grad, sync, loss.backward(), sync; the reference's time_pass); "
+                       "strict mode on, so no op left the device; the C4 block's input needs no gradient, so the "
+                       "stem's grad input is not computed")
+    finally:
+        if old is None:
+            del os.environ["TORCHVULKAN_STRICT"]
+        else:
+            os.environ["TORCHVULKAN_STRICT"] = old
+    return res
 
 
 def run_memory_ops(torch, _abi, dev, stream, steps, warmup, g):

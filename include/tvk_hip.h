@@ -485,6 +485,16 @@ typedef struct {
     void* c; int64_t c_stride[3];
     double alpha, beta;
     void* stream;           /* hipStream_t or NULL */
+    /* An optional second batch dimension. With batch_inner > 1 (it must
+     * divide batch), batch index b addresses every operand at
+     *   (b / batch_inner) * stride[0] + (b % batch_inner) * stride_inner,
+     * so a [B, H, rows, cols] view whose B and H strides do not merge into
+     * one (head-strided q, k, v: [B, L, H, D] underneath) runs as one product
+     * of batch B*H without a copy; the batch dimensions of
+     * prepare_matmul_operands / batched matmul (src/api/ops/matmul.cpp:27-78)
+     * collapse into these two. 0 or 1: one batch dimension, stride[0]. */
+    int64_t batch_inner;
+    int64_t a_stride_inner, b_stride_inner, bias_stride_inner, c_stride_inner;
 } tvk_gemm_desc;
 
 tvk_status tvk_gemm(const tvk_gemm_desc* desc);

@@ -56,6 +56,9 @@ class GemmDesc(C.Structure):
         ("alpha", C.c_double),
         ("beta", C.c_double),
         ("stream", C.c_void_p),
+        ("batch_inner", C.c_int64),
+        ("a_stride_inner", C.c_int64), ("b_stride_inner", C.c_int64),
+        ("bias_stride_inner", C.c_int64), ("c_stride_inner", C.c_int64),
     ]
 
 
@@ -506,18 +509,20 @@ def attention_bwd(q, k, v, out, lse, dout, bias=None, causal=False, scale=None, 
 def _strides3(t) -> tuple[int, int, int]:
     if t.dim() == 2:
         return (0, t.stride(0), t.stride(1))
-    if t.dim() == 3:
-        return (t.stride(0), t.stride(1), t.stride(2))
-    raise ValueError("expected a 2-D or 3-D tensor")
+    if t.dim() in (3, 4):
+        return (t.stride(0), t.stride(-2), t.stride(-1))
+    raise ValueError("expected a 2-D, 3-D or 4-D tensor")
 
 
 def make_gemm_desc(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_NONE, stream=None, exact=False) -> GemmDesc:
-    """Describes C = act(alpha*A@B + beta*bias) over 2-D or batched 3-D tensors.
+    """Describes C = act(alpha*A@B + beta*bias) over 2-D, batched 3-D or 4-D tensors.
 
     `bias` may be any tensor that broadcasts to C's shape (it is expanded with
-    stride-0 views, as the reference's prepare_matmul_operands does).
+    stride-0 views, as the reference's prepare_matmul_operands does). 4-D
+    operands [B, H, rows, cols] use the descriptor's second batch dimension
+    (batch_inner = H, the H strides), so head-strided views need no copy.
     """
-    batch = c.shape[0] if c.dim() == 3 else 1
+    batch = c.shape[0] if c.dim() == 3 else (c.shape[0] * c.shape[1] if c.dim() == 4 else 1)
     M, N = c.shape[-2], c.shape[-1]
     K = a.shape[-1]
     d = GemmDesc()
@@ -536,6 +541,13 @@ def make_gemm_desc(a, b, c, bias=None, alpha=1.0, beta=0.0, activation=TVK_ACT_N
         d.bias_stride = I64x3(*_strides3(bias_e))
     d.c = c.data_ptr() if c.numel() else None
     d.c_stride = I64x3(*_strides3(c))
+    if c.dim() == 4:
+        if a.dim() != 4 or b.dim() != 4:
+            raise ValueError("a 4-D output needs 4-D operands")
+        d.batch_inner = c.shape[1]
+        d.a_stride_inner, d.b_stride_inner, d.c_stride_inner = a.stride(1), b.stride(1), c.stride(1)
+        if bias is not None:
+            d.bias_stride_inner = bias.expand(c.shape).stride(1)
     d.alpha = float(alpha)
     d.beta = float(beta)
     d.stream = stream

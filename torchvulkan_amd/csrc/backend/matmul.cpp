@@ -12,6 +12,7 @@
 #include "common.h"
 
 #include <ATen/native/Resize.h>
+#include <ATen/ops/matmul_native.h>
 
 namespace tvkb {
 namespace {
@@ -105,9 +106,60 @@ at::Tensor batched_view(const at::Tensor& t, const std::vector<int64_t>& batch_s
     return e.reshape({B, rows, cols});  // materialises a contiguous copy
 }
 
+// Whether batch dims [lo, hi) of an expanded operand collapse into one
+// stride (returned in `stride`; 0 when every dim there is 1 or broadcast).
+bool batch_range_collapses(const at::Tensor& e, const std::vector<int64_t>& batch_shape, int64_t lo, int64_t hi, int64_t& stride) {
+    int64_t s = -1, prod = 1;
+    for (int64_t d = hi - 1; d >= lo; --d) {
+        if (batch_shape[d] == 1) continue;
+        const int64_t st = e.stride(d);
+        if (s < 0) s = st;
+        else if (st != s * prod) return false;
+        prod *= batch_shape[d];
+    }
+    stride = s < 0 ? 0 : s;
+    return true;
+}
+
+// Two batch dimensions for operands whose batch dims do not collapse into
+// one (head-strided [B, H, L, D] views): the first batch dims [0, split)
+// and the rest [split, n) each collapse into one stride, for every operand.
+// Returns the split (0: none found) and the 4-D views [B1, B2, rows, cols].
+int64_t batched_views2(const std::vector<const at::Tensor*>& ops, const std::vector<std::pair<int64_t, int64_t>>& mats,
+                       const std::vector<int64_t>& batch_shape, std::vector<at::Tensor>& views) {
+    const int64_t n = (int64_t)batch_shape.size();
+    for (int64_t split = n - 1; split >= 1; --split) {
+        int64_t b1 = 1, b2 = 1;
+        for (int64_t d = 0; d < split; ++d) b1 *= batch_shape[d];
+        for (int64_t d = split; d < n; ++d) b2 *= batch_shape[d];
+        if (b1 == 1 || b2 == 1) continue;
+        std::vector<at::Tensor> vs;
+        bool ok = true;
+        for (size_t i = 0; i < ops.size() && ok; ++i) {
+            if (!ops[i]->defined()) {
+                vs.emplace_back();
+                continue;
+            }
+            std::vector<int64_t> shape(batch_shape);
+            shape.push_back(mats[i].first);
+            shape.push_back(mats[i].second);
+            const at::Tensor e = ops[i]->expand(shape);
+            int64_t s0 = 0, s1 = 0;
+            ok = batch_range_collapses(e, batch_shape, 0, split, s0) && batch_range_collapses(e, batch_shape, split, n, s1);
+            if (ok) vs.push_back(e.as_strided({b1, b2, mats[i].first, mats[i].second}, {s0, s1, e.stride(-2), e.stride(-1)}));
+        }
+        if (ok) {
+            views = vs;
+            return split;
+        }
+    }
+    return 0;
+}
+
 // One tvk_gemm: out[B, M, N] = act(alpha * a[B, M, K] . b[B, K, N] + beta * bias)
-// on 3-D views (bias undefined: none). False when the library declines the
-// shape (the caller falls back); other failures throw.
+// on 3-D views, or on 4-D views [B1, B2, ., .] with two batch dimensions
+// (bias undefined: none). False when the library declines the shape (the
+// caller falls back); other failures throw.
 bool run_gemm(const at::Tensor& a, const at::Tensor& b, const at::Tensor& bias, double alpha, double beta, Activation act,
               int32_t tdt, const at::Tensor& out) {
     tvk_gemm_desc d;
@@ -120,18 +172,31 @@ bool run_gemm(const at::Tensor& a, const at::Tensor& b, const at::Tensor& bias, 
         return e && e[0] && std::strcmp(e, "0") != 0;
     }();
     d.flags = exact ? TVK_GEMM_EXACT : 0;
-    d.batch = out.size(0); d.M = out.size(1); d.N = out.size(2); d.K = a.size(2);
+    const bool two = out.dim() == 4;
+    d.batch = two ? out.size(0) * out.size(1) : out.size(0);
+    d.M = out.size(-2); d.N = out.size(-1); d.K = a.size(-1);
     d.a = a.data_ptr();
     d.b = b.data_ptr();
     d.c = out.data_ptr();
-    for (int i = 0; i < 3; ++i) {
-        d.a_stride[i] = a.stride(i);
-        d.b_stride[i] = b.stride(i);
-        d.c_stride[i] = out.stride(i);
-    }
+    // (batch, row, col) element strides; with two batch dims the inner one's separately
+    auto st3 = [&](const at::Tensor& t, int64_t* dst) {
+        dst[0] = t.stride(0);
+        dst[1] = t.stride(-2);
+        dst[2] = t.stride(-1);
+    };
+    st3(a, d.a_stride);
+    st3(b, d.b_stride);
+    st3(out, d.c_stride);
     if (bias.defined()) {
         d.bias = bias.data_ptr();
-        for (int i = 0; i < 3; ++i) d.bias_stride[i] = bias.stride(i);
+        st3(bias, d.bias_stride);
+    }
+    if (two) {
+        d.batch_inner = out.size(1);
+        d.a_stride_inner = a.stride(1);
+        d.b_stride_inner = b.stride(1);
+        d.c_stride_inner = out.stride(1);
+        d.bias_stride_inner = bias.defined() ? bias.stride(1) : 0;
     }
     d.alpha = alpha;
     d.beta = bias.defined() ? beta : 0.0;
@@ -274,12 +339,36 @@ at::Tensor dispatch_matmul(const at::Tensor& self_, const at::Tensor& other_, co
     }
     TORCH_CHECK(act != ACT_GELU || at::isFloatingType(dtype), "torchvulkan [ERROR]: gelu is only defined for floating point matmuls, not ", dtype);
 
-    at::Tensor a = batched_view(s.self.to(dtype), s.batch_shape, s.M, s.K, s.B);
-    at::Tensor b = batched_view(s.other.to(dtype), s.batch_shape, s.K, s.N, s.B);
+    const at::Tensor self_t = s.self.to(dtype), other_t = s.other.to(dtype);
+    const at::Tensor bias_t = has_bias ? bias_.to(self_t.options()) : at::Tensor();
+    if (s.M != 0 && s.N != 0 && s.B != 0 && s.K != 0 && s.batch_shape.size() >= 2) {
+        // operands whose batch dims do not collapse into one stride (head-strided
+        // [B, H, L, D] views): two batch dimensions instead of a reshape copy
+        auto collapses = [&](const at::Tensor& t, int64_t r, int64_t c) {
+            if (!t.defined()) return true;
+            std::vector<int64_t> shape(s.batch_shape);
+            shape.push_back(r);
+            shape.push_back(c);
+            int64_t st = 0;
+            return batch_range_collapses(t.expand(shape), s.batch_shape, 0, (int64_t)s.batch_shape.size(), st);
+        };
+        if (!collapses(self_t, s.M, s.K) || !collapses(other_t, s.K, s.N) || !collapses(bias_t, s.M, s.N)) {
+            std::vector<at::Tensor> v;
+            if (batched_views2({&self_t, &other_t, &bias_t}, {{s.M, s.K}, {s.K, s.N}, {s.M, s.N}}, s.batch_shape, v) &&
+                !negative_strides({&v[0], &v[1], &v[2]})) {
+                at::Tensor out4 = at::empty({v[0].size(0), v[0].size(1), s.M, s.N}, self_t.options());
+                if (run_gemm(v[0], v[1], v[2], alpha.toDouble(), has_bias ? beta.toDouble() : 0.0, act, tdt, out4))
+                    return finish(out4.view({s.B, s.M, s.N}), s);
+                return fallback();
+            }
+        }
+    }
+    at::Tensor a = batched_view(self_t, s.batch_shape, s.M, s.K, s.B);
+    at::Tensor b = batched_view(other_t, s.batch_shape, s.K, s.N, s.B);
     at::Tensor out = at::empty({s.B, s.M, s.N}, a.options());
     if (s.M == 0 || s.N == 0 || s.B == 0) return finish(out, s);
     at::Tensor bias;
-    if (has_bias) bias = batched_view(bias_.to(a.options()), s.batch_shape, s.M, s.N, s.B);
+    if (has_bias) bias = batched_view(bias_t, s.batch_shape, s.M, s.N, s.B);
     if (s.K == 0) {
         at::Tensor r = has_bias ? (bias * beta) : out.zero_();
         return finish(apply_activation(r, act), s);
@@ -311,6 +400,25 @@ at::Tensor mm_vk(const at::Tensor& self, const at::Tensor& other) {
     check_matrix_product("mm", self, other);
     return dispatch_matmul(self, other, {}, 1, 0, ACT_NONE,
                            [&]() { return at::mm(self.cpu(), other.cpu()).to(self.device()); });
+}
+
+// aten::matmul on the device: torch's composite reshapes batched operands to
+// [B, M, K] first, which copies views whose batch dims do not merge
+// (head-strided q/k/v); here they keep their strides (two batch dimensions).
+// Broadcasting, 1-D operands and the result shape follow torch.matmul.
+at::Tensor matmul_vk(const at::Tensor& self, const at::Tensor& other) {
+    TORCH_CHECK(self.dim() != 0 && other.dim() != 0, "both arguments to matmul need to be at least 1D, but they are ",
+                self.dim(), "D and ", other.dim(), "D");
+    return dispatch_matmul(self, other, {}, 1, 0, ACT_NONE,
+                           [&]() { return at::matmul(self.cpu(), other.cpu()).to(self.device()); });
+}
+
+// Autograd: the composite (whose reshape and bmm record their own backward)
+// whenever a gradient is needed; the device kernel otherwise.
+at::Tensor matmul_autograd_vk(const at::Tensor& self, const at::Tensor& other) {
+    if (at::GradMode::is_enabled() && (self.requires_grad() || other.requires_grad())) return at::native::matmul(self, other);
+    at::AutoDispatchBelowADInplaceOrView guard;
+    return matmul_vk(self, other);
 }
 
 at::Tensor bmm_vk(const at::Tensor& self, const at::Tensor& other) {
@@ -571,6 +679,7 @@ at::Tensor scaled_mm_vk(const at::Tensor& mat1, const at::Tensor& mat2, const at
 }  // namespace tvkb
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+    m.impl("matmul", &tvkb::matmul_vk);
     m.impl("mm", &tvkb::mm_vk);
     m.impl("mm.out", &tvkb::mm_out_vk);
     m.impl("bmm", &tvkb::bmm_vk);
@@ -591,4 +700,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
     m.impl("addmv_", &tvkb::addmv_inplace_vk);
     m.impl("_scaled_mm", &tvkb::scaled_mm_vk);
     m.impl("_scaled_mm.out", &tvkb::scaled_mm_out_vk);
+}
+
+TORCH_LIBRARY_IMPL(aten, AutogradPrivateUse1, m) {
+    m.impl("matmul", &tvkb::matmul_autograd_vk);
 }

@@ -63,8 +63,8 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
     const int64_t total = (int64_t)p.M * p.N;
     for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
         const int row = (int)(idx / p.N), col = (int)(idx % p.N);
-        const T* a = reinterpret_cast<const T*>(p.a) + (int64_t)b * p.sa[0] + (int64_t)row * p.sa[1];
-        const T* bm = reinterpret_cast<const T*>(p.b) + (int64_t)b * p.sb[0] + (int64_t)col * p.sb[2];
+        const T* a = reinterpret_cast<const T*>(p.a) + a_boff(p, b) + (int64_t)row * p.sa[1];
+        const T* bm = reinterpret_cast<const T*>(p.b) + b_boff(p, b) + (int64_t)col * p.sb[2];
         float acc = 0.0f;
         for (int k = 0; k < p.K; ++k)
             acc = fmaf(elem<DT>::to_f32(a[(int64_t)k * p.sa[2]]), elem<DT>::to_f32(bm[(int64_t)k * p.sb[1]]), acc);
@@ -177,8 +177,8 @@ __global__ __launch_bounds__(128 * WGN) void gemm16_mfma_kernel(GemmArgs p) {
     const int m0 = tm * BM, n0 = tn * BN;
 
     // operand buffers of this batch (and of this k split): A rows are M, B rows are N
-    const uint16_t* A = reinterpret_cast<const uint16_t*>(p.a) + (int64_t)b * p.sa[0];
-    const uint16_t* B = reinterpret_cast<const uint16_t*>(p.b) + (int64_t)b * p.sb[0];
+    const uint16_t* A = reinterpret_cast<const uint16_t*>(p.a) + a_boff(p, b);
+    const uint16_t* B = reinterpret_cast<const uint16_t*>(p.b) + b_boff(p, b);
     int K = p.K;
     if (p.split > 1) {
         const int kb = blockIdx.z * p.k_chunk;
@@ -418,8 +418,8 @@ __global__ __launch_bounds__(256) void gemm_seq_mfma_kernel(GemmArgs p) {
     tile_of(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     constexpr int ES = DT == TVK_F32 ? 4 : 2;
-    const char* A = reinterpret_cast<const char*>(p.a) + (int64_t)b * p.sa[0] * ES;
-    const char* B = reinterpret_cast<const char*>(p.b) + (int64_t)b * p.sb[0] * ES;
+    const char* A = reinterpret_cast<const char*>(p.a) + a_boff(p, b) * ES;
+    const char* B = reinterpret_cast<const char*>(p.b) + b_boff(p, b) * ES;
     const int64_t a_bytes = ES * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1);
     const int64_t b_bytes = ES * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1);
     __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)min(a_bytes, (int64_t)0x7fffffff), 0x00020000);
@@ -583,6 +583,10 @@ GemmArgs make_args(const tvk_gemm_desc& d) {
     p.beta = (float)d.beta;
     p.has_bias = (d.bias != nullptr && d.beta != 0.0) ? 1 : 0;
     p.act = d.activation;
+    p.bh = d.batch_inner > 1 ? (int)d.batch_inner : 1;
+    if (p.bh > 1) {
+        p.sa_h = d.a_stride_inner; p.sb_h = d.b_stride_inner; p.sbias_h = d.bias_stride_inner; p.sc_h = d.c_stride_inner;
+    }
     return p;
 }
 
@@ -625,6 +629,7 @@ bool plan_layout(const tvk_gemm_desc& d, Plan& pl) {
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     bool vec = al16(d.a) && al16(d.b);
     if (d.batch > 1) vec = vec && d.a_stride[0] % ce == 0 && d.b_stride[0] % ce == 0;
+    if (d.batch_inner > 1) vec = vec && d.a_stride_inner % ce == 0 && d.b_stride_inner % ce == 0;
     if (pl.ak) vec = vec && d.K % ce == 0 && (d.M == 1 || d.a_stride[1] % ce == 0);
     else vec = vec && d.M % ce == 0 && (d.K == 1 || d.a_stride[2] % ce == 0);
     if (pl.bk) vec = vec && d.K % ce == 0 && (d.N == 1 || d.b_stride[2] % ce == 0);
@@ -633,8 +638,9 @@ bool plan_layout(const tvk_gemm_desc& d, Plan& pl) {
     // A sizeable fp16/bf16 product whose operands miss the 16-byte layout
     // (rows not 8-element multiples, as [1000,777] or a sliced view) is worth
     // one copy of the offending operands into an aligned layout
+    // (the repack copies address one batch dimension: a two-level batch is not repacked)
     if (!vec && d.dtype != TVK_F32 && !(d.flags & TVK_GEMM_EXACT) && !skinny_applies(d.M, d.N, d.K, d.batch) &&
-        (double)d.M * d.N * d.K * d.batch >= double(1 << 28)) {
+        d.batch_inner <= 1 && (double)d.M * d.N * d.K * d.batch >= double(1 << 28)) {
         auto ok_a = [&]() {
             bool v = al16(d.a) && (d.batch == 1 || d.a_stride[0] % ce == 0);
             if (pl.ak) return v && d.K % ce == 0 && (d.M == 1 || d.a_stride[1] % ce == 0);
@@ -667,6 +673,7 @@ Plan skinny_plan(const tvk_gemm_desc& d, Plan pl) {
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     bool v = al16(d.a) && al16(d.b) && pl.ak && d.K % 8 == 0 && (d.M == 1 || d.a_stride[1] % 8 == 0);
     if (d.batch > 1) v = v && d.a_stride[0] % 8 == 0 && d.b_stride[0] % 8 == 0;
+    if (d.batch_inner > 1) v = v && d.a_stride_inner % 8 == 0 && d.b_stride_inner % 8 == 0;
     if (pl.bk) v = v && (d.N == 1 || d.b_stride[2] % 8 == 0);
     else v = v && d.N % 8 == 0 && (d.K == 1 || d.b_stride[1] % 8 == 0);
     pl = with_kern(pl, Kern::SKINNY, nullptr);
@@ -918,16 +925,19 @@ template <int DT>
 tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixed = nullptr, size_t fixed_cap = 0) {
     const GemmArgs p = make_args(d);
 
-    const int64_t max_y = 65535;
+    // batch chunks within the grid's y limit, of whole inner batches when there
+    // are two batch dimensions (each chunk then starts at an outer index bo)
+    const int64_t max_y = 65535 / p.bh * p.bh;
     for (int64_t b0 = 0; b0 < d.batch; b0 += max_y) {
         const int nb = (int)std::min<int64_t>(max_y, d.batch - b0);
+        const int64_t bo = b0 / p.bh;
         GemmArgs q = p;
         q.batch = nb;
         const size_t es = dtype_size(d.dtype);
-        q.a = (const char*)d.a + (size_t)(b0 * d.a_stride[0]) * es;
-        q.b = (const char*)d.b + (size_t)(b0 * d.b_stride[0]) * es;
-        if (q.has_bias) q.bias = (const char*)d.bias + (size_t)(b0 * d.bias_stride[0]) * es;
-        q.c = (char*)d.c + (size_t)(b0 * d.c_stride[0]) * es;
+        q.a = (const char*)d.a + (size_t)(bo * d.a_stride[0]) * es;
+        q.b = (const char*)d.b + (size_t)(bo * d.b_stride[0]) * es;
+        if (q.has_bias) q.bias = (const char*)d.bias + (size_t)(bo * d.bias_stride[0]) * es;
+        q.c = (char*)d.c + (size_t)(bo * d.c_stride[0]) * es;
         // scratch: repacked operands, then split-K partials
         const int64_t a_rows = pl.ak ? d.M : d.K, a_ld = repack_ld(pl.ak ? d.K : d.M, pl.ak);
         const int64_t b_rows = pl.bk ? d.N : d.K, b_ld = repack_ld(pl.bk ? d.K : d.N, pl.bk);
@@ -1062,6 +1072,11 @@ tvk_status validate(const tvk_gemm_desc* d) {
     for (int i = 0; i < 3; ++i)
         if (d->a_stride[i] < 0 || d->b_stride[i] < 0 || d->c_stride[i] < 0 || d->bias_stride[i] < 0)
             return fail(TVK_ERR_UNSUPPORTED, "tvk_gemm: negative strides are not supported");
+    if (d->batch_inner < 0 || (d->batch_inner > 1 && d->batch % d->batch_inner != 0))
+        return fail(TVK_ERR_INVALID, "tvk_gemm: batch_inner must divide batch");
+    if (d->batch_inner > 1 &&
+        (d->a_stride_inner < 0 || d->b_stride_inner < 0 || d->c_stride_inner < 0 || d->bias_stride_inner < 0))
+        return fail(TVK_ERR_UNSUPPORTED, "tvk_gemm: negative strides are not supported");
     if (d->batch == 0 || d->M == 0 || d->N == 0) return TVK_OK;
     if (!d->c) return fail(TVK_ERR_INVALID, "tvk_gemm: c is NULL");
     if (d->K > 0 && (!d->a || !d->b)) return fail(TVK_ERR_INVALID, "tvk_gemm: a or b is NULL");
@@ -1098,14 +1113,17 @@ tvk_status run_plan(const tvk_gemm_desc& d, const Plan& pl, char* fixed = nullpt
 // timed launches write a scratch output instead, so no input changes.
 tvk_status time_candidates(const tvk_gemm_desc& d, const std::vector<Plan>& cands, Plan& best) {
     const size_t es = dtype_size(d.dtype);
-    auto extent = [&](const void* base, const int64_t* st, int64_t rows, int64_t cols) {
+    const int64_t bh = d.batch_inner > 1 ? d.batch_inner : 1;
+    auto extent = [&](const void* base, const int64_t* st, int64_t sh, int64_t rows, int64_t cols) {
         const char* lo = static_cast<const char*>(base);
-        return std::make_pair(lo, lo + es * ((d.batch - 1) * st[0] + (rows - 1) * st[1] + (cols - 1) * st[2] + 1));
+        return std::make_pair(lo, lo + es * ((d.batch / bh - 1) * st[0] + (bh - 1) * sh + (rows - 1) * st[1] +
+                                             (cols - 1) * st[2] + 1));
     };
-    const auto c = extent(d.c, d.c_stride, d.M, d.N);
+    const auto c = extent(d.c, d.c_stride, d.c_stride_inner, d.M, d.N);
     auto overlaps = [&](std::pair<const char*, const char*> r) { return r.first < c.second && c.first < r.second; };
-    bool alias = overlaps(extent(d.a, d.a_stride, d.M, d.K)) || overlaps(extent(d.b, d.b_stride, d.K, d.N));
-    if (d.bias && d.beta != 0.0) alias = alias || overlaps(extent(d.bias, d.bias_stride, d.M, d.N));
+    bool alias = overlaps(extent(d.a, d.a_stride, d.a_stride_inner, d.M, d.K)) ||
+                 overlaps(extent(d.b, d.b_stride, d.b_stride_inner, d.K, d.N));
+    if (d.bias && d.beta != 0.0) alias = alias || overlaps(extent(d.bias, d.bias_stride, d.bias_stride_inner, d.M, d.N));
     tvk_gemm_desc t = d;
     void* scratch = nullptr;
     if (alias) {

@@ -37,7 +37,23 @@ struct GemmArgs {
     // streaming kernel): one counter per output tile, zero before the launch
     // and left zero after it; NULL: the partials are summed by a second kernel
     unsigned* tile_count;
+    // a second batch dimension (bh > 1): batch index b is (b / bh, b % bh),
+    // addressed with stride [0] and the *_h stride (batch_off)
+    int bh;
+    int64_t sa_h, sb_h, sbias_h, sc_h;
 };
+
+// Element offset of batch b of an operand with outer stride s0 and inner
+// stride sh (tvk_gemm_desc.batch_inner).
+__host__ __device__ __forceinline__ int64_t batch_off(const GemmArgs& p, int b, int64_t s0, int64_t sh) {
+    if (p.bh <= 1) return (int64_t)b * s0;
+    const int bo = b / p.bh;
+    return (int64_t)bo * s0 + (int64_t)(b - bo * p.bh) * sh;
+}
+__host__ __device__ __forceinline__ int64_t a_boff(const GemmArgs& p, int b) { return batch_off(p, b, p.sa[0], p.sa_h); }
+__host__ __device__ __forceinline__ int64_t b_boff(const GemmArgs& p, int b) { return batch_off(p, b, p.sb[0], p.sb_h); }
+__host__ __device__ __forceinline__ int64_t c_boff(const GemmArgs& p, int b) { return batch_off(p, b, p.sc[0], p.sc_h); }
+__host__ __device__ __forceinline__ int64_t bias_boff(const GemmArgs& p, int b) { return batch_off(p, b, p.sbias[0], p.sbias_h); }
 
 // ----------------------------------------------------------------------------
 // epilogue (shared by all kernels)
@@ -97,11 +113,11 @@ __device__ inline void store_out(const GemmArgs& p, int b, int row, int col, flo
         float bv = 0.0f;
         if (p.has_bias) {
             const T* bias = reinterpret_cast<const T*>(p.bias);
-            bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2]]);
+            bv = elem<DT>::to_f32(bias[bias_boff(p, b) + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2]]);
         }
         v = INL ? epilogue(acc, p.alpha, p.has_bias, bv, p.beta, p.act) : epilogue_math(acc, p.alpha, p.has_bias, bv, p.beta, p.act);
     }
-    c[(int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2]] = elem<DT>::from_f32(v);
+    c[c_boff(p, b) + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2]] = elem<DT>::from_f32(v);
 }
 
 // Epilogue of 16 accumulators of one lane that share a column and sit at
@@ -114,8 +130,8 @@ __device__ inline void store_frag16(const GemmArgs& p, int b, int row0, int col,
     if (col >= p.N) return;
     if (INL && p.has_bias && p.sbias[1] == 0) {
         typedef typename elem<DT>::T T;
-        const float bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[(int64_t)b * p.sbias[0] + (int64_t)col * p.sbias[2]]);
-        T* c = reinterpret_cast<T*>(p.c) + (int64_t)b * p.sc[0] + (int64_t)col * p.sc[2];
+        const float bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[bias_boff(p, b) + (int64_t)col * p.sbias[2]]);
+        T* c = reinterpret_cast<T*>(p.c) + c_boff(p, b) + (int64_t)col * p.sc[2];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = row0 + (r / 4) * 8 + (r % 4);
@@ -163,10 +179,10 @@ __device__ __forceinline__ void finish4(const GemmArgs& p, int b, int row, int c
     for (int r = 0; r < 4; ++r) {
         float bv = 0.0f;
         if (p.has_bias)
-            bv = elem<DT>::to_f32(bias[(int64_t)b * p.sbias[0] + (int64_t)row * p.sbias[1] + (int64_t)(col + r) * p.sbias[2]]);
+            bv = elem<DT>::to_f32(bias[bias_boff(p, b) + (int64_t)row * p.sbias[1] + (int64_t)(col + r) * p.sbias[2]]);
         h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(epilogue(v[r], p.alpha, p.has_bias, bv, p.beta, p.act)));
     }
-    T* cp = c + (int64_t)b * p.sc[0] + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2];
+    T* cp = c + c_boff(p, b) + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2];
     if (vec) {
         st_nt(reinterpret_cast<u32x2*>(cp), u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)});
     } else {
@@ -177,7 +193,8 @@ __device__ __forceinline__ void finish4(const GemmArgs& p, int b, int row, int c
 
 // Whether finish4 may store four outputs as one 8-byte write.
 __device__ __forceinline__ bool finish4_vec(const GemmArgs& p) {
-    return p.sc[2] == 1 && p.sc[1] % 4 == 0 && (p.batch == 1 || p.sc[0] % 4 == 0) && (reinterpret_cast<uintptr_t>(p.c) & 7) == 0;
+    return p.sc[2] == 1 && p.sc[1] % 4 == 0 && (p.batch == 1 || (p.sc[0] % 4 == 0 && (p.bh <= 1 || p.sc_h % 4 == 0))) &&
+           (reinterpret_cast<uintptr_t>(p.c) & 7) == 0;
 }
 
 // Split-K without a second launch. The float32 partial planes of such a
@@ -328,7 +345,7 @@ template <int DT>
 inline void launch_split_reduce(const GemmArgs& q, hipStream_t s) {
     const int64_t total = (int64_t)q.batch * q.M * q.N;
     if (q.N % 4 == 0 && (total >= 4 * 256 * 256 || q.split >= 8)) {
-        const bool vec = q.sc[2] == 1 && q.sc[1] % 4 == 0 && (q.batch == 1 || q.sc[0] % 4 == 0) &&
+        const bool vec = q.sc[2] == 1 && q.sc[1] % 4 == 0 && (q.batch == 1 || (q.sc[0] % 4 == 0 && (q.bh <= 1 || q.sc_h % 4 == 0))) &&
                          (reinterpret_cast<uintptr_t>(q.c) & 7) == 0;
         const unsigned blocks = (unsigned)std::min<int64_t>((total / 4 + 255) / 256, 8192);
         if (vec) hipLaunchKernelGGL((gemm_split_reduce4_kernel<DT, true>), dim3(blocks), dim3(256), 0, s, q);

@@ -189,8 +189,8 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     const int m0 = tm * D_BM, n0 = tn * D_BN;
 
     // A: (m, k) at m*sa[1] + k*sa[2]; B: (k, n) at k*sb[1] + n*sb[2]
-    const char* A = reinterpret_cast<const char*>(p.a) + (int64_t)b * p.sa[0] * 2;
-    const char* B = reinterpret_cast<const char*>(p.b) + (int64_t)b * p.sb[0] * 2;
+    const char* A = reinterpret_cast<const char*>(p.a) + a_boff(p, b) * 2;
+    const char* B = reinterpret_cast<const char*>(p.b) + b_boff(p, b) * 2;
     const i32x4 ra = dma_rsrc(A, p.a_ext ? p.a_ext : 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1));
     const i32x4 rb = dma_rsrc(B, p.b_ext ? p.b_ext : 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1));
     constexpr bool XS = !G::BIG;   // the wide (conflict-free) swizzles
@@ -217,10 +217,10 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     i32x4 rbias{0, 0, 0, 0};
     uint32_t bias_lane = 0;
     if constexpr (G::BIG && BL) {
-        const char* Bias = reinterpret_cast<const char*>(p.bias) + (int64_t)b * p.sbias[0] * 2;
+        const char* Bias = reinterpret_cast<const char*>(p.bias) + bias_boff(p, b) * 2;
         auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
         bias_lds = p.split <= 1 && p.has_bias && p.sbias[2] == 1 && p.sbias[1] % 8 == 0 && al16(Bias) && p.sc[2] == 1 &&
-                   p.sc[1] % 8 == 0 && al16(reinterpret_cast<const char*>(p.c) + (int64_t)b * p.sc[0] * 2) && p.N % 8 == 0 &&
+                   p.sc[1] % 8 == 0 && al16(reinterpret_cast<const char*>(p.c) + c_boff(p, b) * 2) && p.N % 8 == 0 &&
                    2 * ((int64_t)(p.M + 256) * p.sbias[1] + p.N) < (int64_t(1) << 31);
         // an instruction's two rows start 2 u rows past its quarter's first: lane -> row lane / 32, chunk lane % 32
         rbias = dma_rsrc(Bias + ((int64_t)m0 * p.sbias[1] + n0) * 2, bias_lds ? 2 * ((int64_t)(p.M - 1 - m0) * p.sbias[1] + p.N - n0) : 0);
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
             // meet on distinct banks); then each thread finishes 8 columns of a
             // row against its bias chunk from the ring and stores 16 bytes
             float* et = reinterpret_cast<float*>(lds_raw + D_NS * D_STB);
-            T* Cb = reinterpret_cast<T*>(p.c) + (int64_t)b * p.sc[0];
+            T* Cb = reinterpret_cast<T*>(p.c) + c_boff(p, b);
             auto et_at = [](int r, int col) { return r * 256 + (((col / 4) ^ (((r >> 2) & 3) * 4)) * 4) + col % 4; };
 #pragma unroll
             for (int pass = 0; pass < 8; ++pass) {
@@ -376,8 +376,8 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     typedef typename elem<DT>::T T;
     constexpr int E_LD = D_BN + 4;   // floats per LDS row
     float* et = reinterpret_cast<float*>(lds_raw);
-    T* Cb = reinterpret_cast<T*>(p.c) + (int64_t)b * p.sc[0];
-    const T* Bb = p.has_bias ? reinterpret_cast<const T*>(p.bias) + (int64_t)b * p.sbias[0] : nullptr;
+    T* Cb = reinterpret_cast<T*>(p.c) + c_boff(p, b);
+    const T* Bb = p.has_bias ? reinterpret_cast<const T*>(p.bias) + bias_boff(p, b) : nullptr;
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     const bool vec_c = p.sc[2] == 1 && p.sc[1] % 8 == 0 && al16(Cb);
     const bool vec_b = p.has_bias && p.sbias[2] == 1 && p.sbias[1] % 8 == 0 && al16(Bb);

@@ -10,6 +10,7 @@ bool dma_applies(const GemmArgs& p, bool a_kmajor, bool b_kmajor) {
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     if (!al16(p.a) || !al16(p.b)) return false;
     if (p.batch > 1 && (p.sa[0] % 8 != 0 || p.sb[0] % 8 != 0)) return false;
+    if (p.bh > 1 && (p.sa_h % 8 != 0 || p.sb_h % 8 != 0)) return false;
     // every 16-byte chunk starts 16-byte aligned: the stride between the rows
     // of the contiguous dimension is a multiple of 8 elements
     const int64_t a_rows = a_kmajor ? p.sa[1] : p.sa[2];

@@ -60,8 +60,8 @@ __global__ __launch_bounds__(64 * SK_NW) void gemm_skinny_kernel(GemmArgs p) {
     if (gridDim.x % 8 == 0) strip = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
     const int n0 = strip * SK_CW, b = blockIdx.z;
 
-    const uint16_t* A = reinterpret_cast<const uint16_t*>(p.a) + (int64_t)b * p.sa[0];
-    const uint16_t* B = reinterpret_cast<const uint16_t*>(p.b) + (int64_t)b * p.sb[0];
+    const uint16_t* A = reinterpret_cast<const uint16_t*>(p.a) + a_boff(p, b);
+    const uint16_t* B = reinterpret_cast<const uint16_t*>(p.b) + b_boff(p, b);
     const int64_t a_bytes = 2 * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1);
     const int64_t b_bytes = 2 * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1);
     __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)min(a_bytes, (int64_t)0x7fffffff), 0x00020000);
@@ -208,8 +208,8 @@ __global__ __launch_bounds__(64 * SR_NW) void gemm_skinny_ring_kernel(GemmArgs p
     const int klen = p.split > 1 ? p.k_chunk : p.K;
     const int nk = klen / 32;
 
-    const char* A = reinterpret_cast<const char*>(p.a) + (int64_t)b * p.sa[0] * 2;
-    const char* B = reinterpret_cast<const char*>(p.b) + (int64_t)b * p.sb[0] * 2;
+    const char* A = reinterpret_cast<const char*>(p.a) + a_boff(p, b) * 2;
+    const char* B = reinterpret_cast<const char*>(p.b) + b_boff(p, b) * 2;
     const i32x4 ra = sr_rsrc(A, 2 * ((int64_t)(p.M - 1) * p.sa[1] + p.K));
     const i32x4 rb = sr_rsrc(B, 2 * ((int64_t)(p.K - 1) * p.sb[1] + p.N));
     // wave w loads B block w (k-rows 4w..4w+3 of the stage); wave 0 also loads A
@@ -294,6 +294,7 @@ bool ring_applies(const GemmArgs& p, bool b_kmajor, bool vec) {
     if (!al16(p.a) || !al16(p.b) || p.sa[2] != 1 || p.sb[2] != 1) return false;
     if (p.K % 32 != 0 || p.N % 8 != 0 || (p.M > 1 && p.sa[1] % 8 != 0) || (p.K > 1 && p.sb[1] % 8 != 0)) return false;
     if (p.batch > 1 && (p.sa[0] % 8 != 0 || p.sb[0] % 8 != 0)) return false;
+    if (p.bh > 1 && (p.sa_h % 8 != 0 || p.sb_h % 8 != 0)) return false;
     return true;
 }
 }  // namespace

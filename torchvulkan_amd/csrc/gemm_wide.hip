@@ -48,7 +48,14 @@ struct WideArgs {
     int has_bias, act;
     double alpha_f, beta_f;      // float64
     uint64_t alpha_i, beta_i;    // integers: the scalars as two's-complement bits
+    int64_t bh;                  // second batch dimension (tvk_gemm_desc.batch_inner), > 1 when present
+    int64_t sa_h, sb_h, sbias_h, sc_h;
 };
+
+// Element offset of batch bz with outer stride s0 and inner stride sh.
+__device__ inline int64_t wide_boff(const WideArgs& p, int64_t bz, int64_t s0, int64_t sh) {
+    return p.bh > 1 ? (bz / p.bh) * s0 + (bz % p.bh) * sh : bz * s0;
+}
 
 // An element in the accumulate type: signed types sign-extend, so the low
 // bits of every product and sum are the type's own.
@@ -95,8 +102,8 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(WideArgs p) {
     const int64_t tm = blockIdx.x / p.tiles_n, tn = blockIdx.x % p.tiles_n;
     const int64_t m0 = tm * W_T, n0 = tn * W_T;
     const int64_t bz = blockIdx.y;
-    const char* A = static_cast<const char*>(p.a) + bz * p.sa[0] * (int64_t)sizeof(T);
-    const char* B = static_cast<const char*>(p.b) + bz * p.sb[0] * (int64_t)sizeof(T);
+    const char* A = static_cast<const char*>(p.a) + wide_boff(p, bz, p.sa[0], p.sa_h) * (int64_t)sizeof(T);
+    const char* B = static_cast<const char*>(p.b) + wide_boff(p, bz, p.sb[0], p.sb_h) * (int64_t)sizeof(T);
 
     Acc acc[4][4];
 #pragma unroll
@@ -138,8 +145,8 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(WideArgs p) {
         __syncthreads();
     }
 
-    T* C = static_cast<T*>(p.c) + bz * p.sc[0];
-    const char* X = p.has_bias ? static_cast<const char*>(p.bias) + bz * p.sbias[0] * (int64_t)sizeof(T) : nullptr;
+    T* C = static_cast<T*>(p.c) + wide_boff(p, bz, p.sc[0], p.sc_h);
+    const char* X = p.has_bias ? static_cast<const char*>(p.bias) + wide_boff(p, bz, p.sbias[0], p.sbias_h) * (int64_t)sizeof(T) : nullptr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t m = m0 + ty + 16 * i;
@@ -161,13 +168,16 @@ tvk_status launch_wide(const tvk_gemm_desc& d, WideArgs w) {
     w.tiles_n = (int)tiles_n;
     const hipStream_t s = resolve_stream(d.stream);
     const size_t es = sizeof(typename wide<DT>::T);
-    for (int64_t b0 = 0; b0 < d.batch; b0 += 65535) {
-        const int nb = (int)std::min<int64_t>(65535, d.batch - b0);
+    // batch chunks of whole inner batches, so each chunk starts at an outer index
+    const int64_t bh = w.bh > 1 ? w.bh : 1, step = 65535 / bh * bh;
+    for (int64_t b0 = 0; b0 < d.batch; b0 += step) {
+        const int nb = (int)std::min<int64_t>(step, d.batch - b0);
+        const int64_t bo = b0 / bh;
         WideArgs q = w;
-        q.a = static_cast<const char*>(d.a) + (size_t)(b0 * d.a_stride[0]) * es;
-        q.b = static_cast<const char*>(d.b) + (size_t)(b0 * d.b_stride[0]) * es;
-        q.c = static_cast<char*>(d.c) + (size_t)(b0 * d.c_stride[0]) * es;
-        if (q.has_bias) q.bias = static_cast<const char*>(d.bias) + (size_t)(b0 * d.bias_stride[0]) * es;
+        q.a = static_cast<const char*>(d.a) + (size_t)(bo * d.a_stride[0]) * es;
+        q.b = static_cast<const char*>(d.b) + (size_t)(bo * d.b_stride[0]) * es;
+        q.c = static_cast<char*>(d.c) + (size_t)(bo * d.c_stride[0]) * es;
+        if (q.has_bias) q.bias = static_cast<const char*>(d.bias) + (size_t)(bo * d.bias_stride[0]) * es;
         hipLaunchKernelGGL(gemm_wide_kernel<DT>, dim3((unsigned)(tiles_m * tiles_n), (unsigned)nb), dim3(256), 0, s, q);
     }
     const hipError_t e = hipGetLastError();
@@ -197,6 +207,9 @@ tvk_status gemm_wide_run(const tvk_gemm_desc& d) {
         w.sbias[i] = w.has_bias ? d.bias_stride[i] : 0;
     }
     w.M = d.M; w.N = d.N; w.K = d.K;
+    w.bh = d.batch_inner > 1 ? d.batch_inner : 1;
+    w.sa_h = d.a_stride_inner; w.sb_h = d.b_stride_inner; w.sc_h = d.c_stride_inner;
+    w.sbias_h = w.has_bias ? d.bias_stride_inner : 0;
     w.a_kfast = d.a_stride[2] == 1 && !(d.a_stride[1] == 1 && d.M > 1 && d.K == 1);
     w.b_kfast = d.b_stride[1] == 1 && !(d.b_stride[2] == 1 && d.N > 1 && d.K == 1);
     w.act = d.activation;
