@@ -37,6 +37,21 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 MEASURED_TRAFFIC = {
     "gemm16_dma_256x256": {"bytes": 1.764e9, "fetch_kib": 795667, "write_kib": 131072},
 }
+# HBM bytes per step of the other bench rows (FETCH_SIZE x 2 + WRITE_SIZE, summed over
+# each step's kernels; profiles/bench_rows_counters.md)
+MEASURED_ROW_TRAFFIC = {
+    "source": "profiles/bench_rows_counters.md",
+    "c2_mlp_gemm_step": {"bytes": 4.717e8, "algorithmic": 2.5e8},
+    "c2_256x4096x4096_product_with_reduce": {"bytes": 8.624e7, "algorithmic": 3.77e7},
+    "c2_dw_4096x4096x256": {"bytes": 4.683e7, "algorithmic": 3.77e7},
+    "c3_dx_8192x512x3072": {"bytes": 1.731e8, "algorithmic": 6.13e7},
+    "c4_conv_step": {"bytes": 5.64e8, "algorithmic": 2.76e8},
+    "c5_ragged_with_repack": {"bytes": 2.834e7, "algorithmic": 1.22e7},
+    "c5_baddbmm": {"bytes": 1.033e8, "algorithmic": 8.39e7},
+    "c3_attention_fwd": {"bytes": 3.397e7},
+    "c3_attention_bwd": {"bytes": 7.689e7},
+}
+
 # the headline kernel and the MFMA ceiling loop under counters
 MEASURED_COUNTERS = {
     "gemm16_dma_256x256": {"mfma_busy_pct": [70.6, 74.0], "shader_clock_ghz": [1.28, 1.70],
@@ -59,6 +74,9 @@ def parse():
                         "'copy' is torch's copy of a 1 GiB buffer, the calibration for FETCH_SIZE/WRITE_SIZE; "
                         "'ceiling' the random-operand MFMA loop of tvk_calibrate_mfma (two waves per SIMD), "
                         "'ceiling_zero' the same loop on all-zero operands")
+    p.add_argument("--only", default=None,
+                   help="comma-separated run_extra sections to run alone (c2, skinny, c4, c3, c3_bmm, attn, ragged, "
+                        "baddbmm, memops, c1, dropin), printing their results; for rocprofv3 passes over one workload")
     p.add_argument("--vendor", action="store_true",
                    help="time the C2 GEMM chain, the C3 layer GEMMs, the C4 conv layers and the C5 products "
                         "through torch on this GPU (hipBLASLt, MIOpen) with the same shapes and data, print one "
@@ -229,6 +247,19 @@ def profile_kernel(which, steps):
     print(f"{which}: {steps} launches of {_abi.gemm_plan(a, (bufs[0] if which == 'skinny' else b), c)}", flush=True)
 
 
+# --only: the run_extra sections that launch anything (for rocprofv3 passes over
+# one workload); the others build their inputs but time nothing
+_ONLY = None
+_SECTION = None
+
+
+def section(name: str) -> bool:
+    """Enters a run_extra section; True when it runs its kernels."""
+    global _SECTION
+    _SECTION = name
+    return _ONLY is None or name in _ONLY
+
+
 def progress(msg: str) -> None:
     """A progress line on stderr (stdout carries only the result line)."""
     print(f"bench.py: {msg}", file=sys.stderr, flush=True)
@@ -240,6 +271,8 @@ def timed(fn, steps, warmup, stream):
     Returns (ms per step from events, ms per step from the host clock)."""
     import torch
 
+    if _ONLY is not None and _SECTION not in _ONLY:
+        return 1.0, 1.0
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -283,6 +316,14 @@ def main():
 
     props = _abi.DeviceProps()
     _abi.check(_abi.load().tvk_device_properties(0, props))
+
+    if args.only:
+        global _ONLY
+        _ONLY = set(args.only.split(","))
+        res = run_extra(torch, _abi, dev, stream, args.steps, args.warmup)
+        keep = {k: v for k, v in res.items() if any(k.startswith(x) for x in ("c1", "c2", "c3", "c4", "c5", "dropin"))}
+        print(json.dumps({"only": sorted(_ONLY), "extra": keep}, default=str), flush=True)
+        return
 
     # ---- headline: fp16 8192^3 --------------------------------------------
     n = 8192
@@ -379,6 +420,7 @@ def bound_us(flops: float, nbytes: float) -> float:
 def run_extra(torch, _abi, dev, stream, steps, warmup):
     out = {}
     # ---- C2 MLP chain fwd+bwd (GEMMs only, fp16) ----------------------------
+    section("c2")
     dims = [784, 4096, 4096, 4096, 10]
     g = torch.Generator().manual_seed(1)
     B = 256
@@ -438,6 +480,7 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
                      "kernel": gemm_plan_of(_abi, d)}
 
     # ---- C5 skinny 16x4096x14336 fp16, B rotated past the Infinity Cache ----
+    section("skinny")
     M, K, N = 16, 4096, 14336
     a = torch.randn((M, K), generator=g).to(torch.float16).to(dev)
     bufs = [torch.randn((K, N), generator=g).to(torch.float16).to(dev) for _ in range(3)]
@@ -462,13 +505,14 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c5_skinny_pct_hbm"] = round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)
     # the practical read ceiling on this box: a plain streaming read of the same
     # B size over three rotating windows (tvk_calibrate_hbm)
-    rd_gbps, rd_ms = _abi.calibrate_hbm(0, K * N * 2, 60)
+    rd_gbps, rd_ms = _abi.calibrate_hbm(0, K * N * 2, 60) if section("skinny") else (1.0, 1.0)
     out["c5_read_ceiling"] = {"what": "plain streaming read, 512 workgroups, three rotating windows of B's size "
                                       "(tvk_calibrate_hbm)", "GBps": round(rd_gbps, 1), "us_for_B": round(rd_ms * 1e3, 2),
                               "skinny_frac_of_ceiling": round(byts / (ms * 1e-3) / 1e9 / rd_gbps, 4)}
     del bufs
 
     # ---- C4 ResNet convs: fwd + dgrad + wgrad of each layer, fp16, batch 128 -
+    section("c4")
     layers = [(3, 64, 3, 1, 1, 32), (64, 64, 3, 1, 1, 32), (64, 128, 3, 2, 1, 32), (128, 256, 3, 2, 1, 16),
               (64, 128, 1, 2, 0, 32), (128, 256, 1, 2, 0, 16)]
     conv_calls = []
@@ -529,6 +573,7 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     del keep, conv_refs, conv_calls
 
     # ---- C3 transformer layer GEMMs (fp16, tokens 8192): fwd + bwd ----------
+    section("c3")
     T = 8192
     shapes = [(512, 512), (512, 256), (512, 256), (512, 512), (512, 3072), (1536, 512)]  # q, k, v, out, gate_up, down
     llm_descs = []
@@ -563,6 +608,7 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c3_llm_layer_gemm_roofline_frac"] = round(llm_bound / 1e3 / ms, 4)
     del keep, llm_refs, llm_descs
 
+    section("c3_bmm")
     # attention products on head-strided views, as the math path meets them: per sequence,
     # q [L, H, D] and k, v [S, H, D] from the projections (GQA's kv heads already repeated to H),
     # S = q k^T and O = P v as batches over the H heads (batch stride D, row stride H*D)
@@ -645,6 +691,7 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     del qs, ks, vs, ss, os_, qc, ktc, vc, sc, oc, cds, gds, crefs, grefs, s4, o4, g2, g2refs
 
     # ---- C3 attention: fused forward, batch 32, 8 query / 2 kv heads, seq 256, head_dim 64, causal
+    section("attn")
     qa = torch.randn((32, 8, 256, 64), generator=g).to(torch.float16).to(dev)
     ka = torch.randn((32, 2, 256, 64), generator=g).to(torch.float16).to(dev)
     va = torch.randn((32, 2, 256, 64), generator=g).to(torch.float16).to(dev)
@@ -689,6 +736,7 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     del qa, ka, va, oa, la, da, gq, gk, gv
 
     # ---- C5 ragged [1000,777]x[777,3000] and baddbmm in[64,512,512] + 0.5*bmm ----
+    section("ragged")
     a = torch.randn((1000, 777), generator=g).to(torch.float16).to(dev)
     b = torch.randn((777, 3000), generator=g).to(torch.float16).to(dev)
     c = torch.empty((1000, 3000), dtype=torch.float16, device=dev)
@@ -706,6 +754,7 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     out["c5_ragged_tflops"] = round(2 * 1000 * 777 * 3000 / (ms * 1e-3) / 1e12, 2)
     out["c5_ragged_roofline_frac"] = round(bound_us(2 * 1000 * 777 * 3000, 2 * (1000 * 777 + 777 * 3000 + 1000 * 3000))
                                            / (ms * 1e3), 4)
+    section("baddbmm")
     x1 = torch.randn((64, 512, 128), generator=g).to(torch.float16).to(dev)
     x2 = torch.randn((64, 128, 512), generator=g).to(torch.float16).to(dev)
     inp = torch.randn((64, 512, 512), generator=g).to(torch.float16).to(dev)
@@ -727,9 +776,11 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
     del a, b, c, x1, x2, inp, cb
 
     # ---- copies, casts, sums and adds on both sides of the contractions ----
-    out.update(run_memory_ops(torch, _abi, dev, stream, steps, warmup, g))
+    if section("memops"):
+        out.update(run_memory_ops(torch, _abi, dev, stream, steps, warmup, g))
 
     # ---- C1 fp32 1024^3 ----------------------------------------------------
+    section("c1")
     a = torch.randn((1024, 1024), generator=g).to(dev)
     b = torch.randn((1024, 1024), generator=g).to(dev)
     c = torch.empty((1024, 1024), device=dev)
@@ -748,9 +799,12 @@ def run_extra(torch, _abi, dev, stream, steps, warmup):
                                          * 1e6 / (ms * 1e3), 4)
     out["c1_kernel"] = _abi.gemm_plan(a, b, c)
 
+    out["measured_traffic"] = MEASURED_ROW_TRAFFIC
+
     # ---- the drop-in path: whole fwd+bwd steps through autograd on "vulkan" ----
-    out["dropin_steps"] = run_dropin(torch, out)
-    progress("drop-in steps done")
+    if section("dropin"):
+        out["dropin_steps"] = run_dropin(torch, out)
+        progress("drop-in steps done")
     return out
 
 
