@@ -226,10 +226,11 @@ struct TvkAllocator final : c10::Allocator {
             int spilled = 0;
             (void)tvk_last_malloc_spilled(&spilled);
             // the reference's warning (src/vulkan/allocator.cpp:189-195)
-            if (spilled)
+            if (spilled) {
                 TORCH_WARN_ONCE("torchvulkan [WARNING]: Vulkan memory may be allocated using host memory, which may cause "
                                 "performance degradation. Set TORCHVULKAN_STRICT_ALLOCATION=1 to raise an out-of-memory "
                                 "error instead.");
+            }
         }
         return {p, p, &free_fn, c10::Device(c10::DeviceType::PrivateUse1, dev)};
     }

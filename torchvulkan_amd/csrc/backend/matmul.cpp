@@ -160,8 +160,7 @@ int64_t batched_views2(const std::vector<const at::Tensor*>& ops, const std::vec
 // on 3-D views, or on 4-D views [B1, B2, ., .] with two batch dimensions
 // (bias undefined: none). False when the library declines the shape (the
 // caller falls back); other failures throw.
-bool run_gemm(const at::Tensor& a, const at::Tensor& b, const at::Tensor& bias, double alpha, double beta, Activation act,
-              int32_t tdt, const at::Tensor& out) {
+tvk_gemm_desc base_desc(int32_t tdt, Activation act) {
     tvk_gemm_desc d;
     std::memset(&d, 0, sizeof(d));
     d.dtype = tdt;
@@ -172,6 +171,33 @@ bool run_gemm(const at::Tensor& a, const at::Tensor& b, const at::Tensor& bias, 
         return e && e[0] && std::strcmp(e, "0") != 0;
     }();
     d.flags = exact ? TVK_GEMM_EXACT : 0;
+    return d;
+}
+
+// Runs a filled descriptor; false when the library declines it (the caller
+// falls back), other failures throw.
+bool launch_desc(tvk_gemm_desc& d, const at::Tensor& out) {
+    d.stream = stream_of(out);
+    // TORCHVULKAN_AUTOTUNE=1: a shape class without a recorded kernel is timed
+    // over every candidate first and the fastest recorded (the reference tunes
+    // every matmul on first sight, src/api/ops/matmul.cpp:538-544); otherwise
+    // the recorded or shape-chosen kernel runs
+    static const bool autotune = [] {
+        const char* e = std::getenv("TORCHVULKAN_AUTOTUNE");
+        return e != nullptr && e[0] && std::strcmp(e, "0") != 0;
+    }();
+    const tvk_status st = autotune ? tvk_gemm_tune(&d, nullptr, 0) : tvk_gemm(&d);
+    if (st == TVK_ERR_UNSUPPORTED) {
+        TVKB_FALLBACK(tvk_last_error(), ". Falling back to CPU.");
+        return false;
+    }
+    check_status(st, "tvk_gemm");
+    return true;
+}
+
+bool run_gemm(const at::Tensor& a, const at::Tensor& b, const at::Tensor& bias, double alpha, double beta, Activation act,
+              int32_t tdt, const at::Tensor& out) {
+    tvk_gemm_desc d = base_desc(tdt, act);
     const bool two = out.dim() == 4;
     d.batch = two ? out.size(0) * out.size(1) : out.size(0);
     d.M = out.size(-2); d.N = out.size(-1); d.K = a.size(-1);
@@ -200,22 +226,60 @@ bool run_gemm(const at::Tensor& a, const at::Tensor& b, const at::Tensor& bias, 
     }
     d.alpha = alpha;
     d.beta = bias.defined() ? beta : 0.0;
-    d.stream = stream_of(out);
-    // TORCHVULKAN_AUTOTUNE=1: a shape class without a recorded kernel is timed
-    // over every candidate first and the fastest recorded (the reference tunes
-    // every matmul on first sight, src/api/ops/matmul.cpp:538-544); otherwise
-    // the recorded or shape-chosen kernel runs
-    static const bool autotune = [] {
-        const char* e = std::getenv("TORCHVULKAN_AUTOTUNE");
-        return e != nullptr && e[0] && std::strcmp(e, "0") != 0;
-    }();
-    const tvk_status st = autotune ? tvk_gemm_tune(&d, nullptr, 0) : tvk_gemm(&d);
-    if (st == TVK_ERR_UNSUPPORTED) {
-        TVKB_FALLBACK(tvk_last_error(), ". Falling back to CPU.");
-        return false;
+    return launch_desc(d, out);
+}
+
+// The 2-D products (mm, addmm, _addmm_activation: every nn.Linear layer and its
+// gradients) with operands of one real dtype, a unit stride in each operand's
+// matrix dims and a bias that broadcasts to [M, N] in at most two dims: the
+// sizes and strides go straight into the descriptor, without the expand /
+// as_strided / reshape views of the general path (each a dispatcher call).
+// Returns an undefined tensor when the product is not of this kind.
+at::Tensor gemm2d_direct(const at::Tensor& a, const at::Tensor& b, const at::Tensor& bias_, const at::Scalar& alpha,
+                         const at::Scalar& beta, Activation act, bool& declined) {
+    declined = false;
+    if (a.dim() != 2 || b.dim() != 2 || a.scalar_type() != b.scalar_type() || a.is_conj() || b.is_conj() || a.is_neg() ||
+        b.is_neg())
+        return {};
+    bool ok = false;
+    const int32_t tdt = gemm_dtype_of(a.scalar_type(), ok);
+    if (!ok) return {};
+    const int64_t M = a.size(0), K = a.size(1), N = b.size(1);
+    if (M == 0 || N == 0 || K == 0 || b.size(0) != K) return {};
+    auto unit = [](const at::Tensor& t) {
+        return (t.size(1) <= 1 || t.stride(1) == 1) || (t.size(0) <= 1 || t.stride(0) == 1);
+    };
+    if (!unit(a) || !unit(b) || a.stride(0) < 0 || a.stride(1) < 0 || b.stride(0) < 0 || b.stride(1) < 0) return {};
+    const double be = beta.toDouble();
+    const bool has_bias = bias_.defined() && be != 0.0;
+    int64_t bs_row = 0, bs_col = 0;
+    if (has_bias) {
+        if (bias_.scalar_type() != a.scalar_type() || bias_.dim() > 2 || bias_.is_conj() || bias_.is_neg()) return {};
+        // right-aligned broadcast of the bias to [M, N]
+        const int64_t bn = bias_.dim() >= 1 ? bias_.size(-1) : 1, bm = bias_.dim() == 2 ? bias_.size(0) : 1;
+        if ((bn != N && bn != 1) || (bm != M && bm != 1)) return {};
+        bs_col = (bias_.dim() >= 1 && bn != 1) ? bias_.stride(-1) : 0;
+        bs_row = (bias_.dim() == 2 && bm != 1) ? bias_.stride(0) : 0;
+        if (bs_col < 0 || bs_row < 0) return {};
     }
-    check_status(st, "tvk_gemm");
-    return true;
+    at::Tensor out = at::empty({M, N}, a.options());
+    tvk_gemm_desc d = base_desc(tdt, act);
+    d.batch = 1; d.M = M; d.N = N; d.K = K;
+    d.a = a.data_ptr(); d.a_stride[1] = a.stride(0); d.a_stride[2] = a.stride(1);
+    d.b = b.data_ptr(); d.b_stride[1] = b.stride(0); d.b_stride[2] = b.stride(1);
+    d.c = out.data_ptr(); d.c_stride[1] = N; d.c_stride[2] = 1;
+    if (has_bias) {
+        d.bias = bias_.data_ptr();
+        d.bias_stride[1] = bs_row;
+        d.bias_stride[2] = bs_col;
+    }
+    d.alpha = alpha.toDouble();
+    d.beta = has_bias ? be : 0.0;
+    if (!launch_desc(d, out)) {
+        declined = true;
+        return {};
+    }
+    return out;
 }
 
 bool negative_strides(std::initializer_list<const at::Tensor*> ts) {
@@ -338,8 +402,21 @@ at::Tensor dispatch_matmul(const at::Tensor& self_, const at::Tensor& other_, co
         return fallback();
     }
     TORCH_CHECK(act != ACT_GELU || at::isFloatingType(dtype), "torchvulkan [ERROR]: gelu is only defined for floating point matmuls, not ", dtype);
+    {
+        bool declined = false;
+        at::Tensor r = gemm2d_direct(self_, other_, bias_, alpha, beta, act, declined);
+        if (declined) return fallback();
+        if (r.defined()) return r;
+    }
 
-    const at::Tensor self_t = s.self.to(dtype), other_t = s.other.to(dtype);
+    // an operand with no unit stride in its matrix dims (a broadcast gradient, such
+    // as sum()'s, arrives with stride 0 in both) would take the one-thread-per-
+    // output kernel: one dense copy of it is far cheaper
+    auto dense_rows = [](const at::Tensor& t) {
+        const bool unit = (t.size(-1) <= 1 || t.stride(-1) == 1) || (t.size(-2) <= 1 || t.stride(-2) == 1);
+        return unit ? t : t.contiguous();
+    };
+    const at::Tensor self_t = dense_rows(s.self.to(dtype)), other_t = dense_rows(s.other.to(dtype));
     const at::Tensor bias_t = has_bias ? bias_.to(self_t.options()) : at::Tensor();
     if (s.M != 0 && s.N != 0 && s.B != 0 && s.K != 0 && s.batch_shape.size() >= 2) {
         // operands whose batch dims do not collapse into one stride (head-strided

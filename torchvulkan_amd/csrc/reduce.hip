@@ -312,8 +312,13 @@ tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
     const int64_t out_blocks = row ? p.nout : (p.nout / per_thread + 255) / 256;
     int64_t splits = 1;
     if (out_blocks < 1024 && p.nred > 1) {
+        const int64_t want = (1024 + out_blocks - 1) / out_blocks;
         const int64_t min_chunk = row ? 4096 : 256;
-        splits = std::min<int64_t>((1024 + out_blocks - 1) / out_blocks, (p.nred + min_chunk - 1) / min_chunk);
+        splits = std::min<int64_t>(want, (p.nred + min_chunk - 1) / min_chunk);
+        // a short column reduction over few outputs (a bias gradient, [256, 4096]
+        // summed over dim 0: two workgroups) takes chunks of 16 rows instead, so
+        // more workgroups read it; long ones keep the 256-row chunks
+        if (!row && splits < 8 && p.nred >= 32) splits = std::min<int64_t>(want, p.nred / 16);
         splits = std::max<int64_t>(1, std::min<int64_t>(splits, 65535));
     }
     p.chunk = (p.nred + splits - 1) / splits;
