@@ -369,10 +369,12 @@ def main():
         ceiling[f"waves_per_simd_{w}"] = round(tf, 1)
     top = max(ceiling.values())
     zero_tf = max(_abi.calibrate_mfma(0, 2, 40000, zeros=True)[0] for _ in range(2))
+    m32_tf = max(_abi.calibrate_mfma(0, 2, 40000, mfma32=True)[0] for _ in range(2))
     roofline["ceiling"] = {
         "what": "v_mfma_f32_16x16x32_f16 loop, 16 accumulators, no memory traffic (tvk_calibrate_mfma): random fp16 "
-                "operands; zero_operands is the same loop on all-zero operands",
-        "unit": "TFLOP/s", **ceiling, "max": top, "zero_operands": round(zero_tf, 1),
+                "operands; zero_operands is the same loop on all-zero operands; mfma32_random the same flops on "
+                "v_mfma_f32_32x32x16_f16 with random operands",
+        "unit": "TFLOP/s", **ceiling, "max": top, "zero_operands": round(zero_tf, 1), "mfma32_random": round(m32_tf, 1),
         "frac_of_ceiling": round(tflops / top, 4),
     }
     roofline["counters"] = MEASURED_COUNTERS.get(plan)

@@ -145,7 +145,9 @@ tvk_status tvk_device_properties(int device, tvk_device_props* out);
 tvk_status tvk_calibrate_mfma(int device, int waves_per_simd, int iterations, double* tflops, double* ms);
 /* The same loop with `operands` 0 (random, as tvk_calibrate_mfma) or 1 (all
  * zeros: operands that toggle nothing, which shows the pipe's issue limit
- * apart from the part's power limit). */
+ * apart from the part's power limit); 2 and 3 are the same two operand sets
+ * on v_mfma_f32_32x32x16_f16 (eight 32x32 accumulators, 32 MFMAs a trip: the
+ * same flops). */
 tvk_status tvk_calibrate_mfma_operands(int device, int waves_per_simd, int iterations, int operands, double* tflops,
                                        double* ms);
 

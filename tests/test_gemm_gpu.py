@@ -628,8 +628,13 @@ def test_calibrate_mfma_reports_a_plausible_rate(gpu):
     for w, tf in rates.items():
         assert 50.0 < tf < 2600.0, (w, tf)
     assert rates[4] > 0.8 * rates[1]
+    # the 32x32x16 form and the zero operands run the same flops
+    for zeros in (False, True):
+        assert 50.0 < gpu.calibrate_mfma(0, 2, 4000, zeros=zeros, mfma32=True)[0] < 2600.0
     with pytest.raises(gpu.TvkError):
         gpu.calibrate_mfma(0, 0, 100)
+    tf, ms = gpu.C.c_double(), gpu.C.c_double()
+    assert gpu.load().tvk_calibrate_mfma_operands(0, 2, 100, 4, gpu.C.byref(tf), gpu.C.byref(ms)) == gpu.TVK_ERR_INVALID
     with pytest.raises(gpu.TvkError):
         gpu.calibrate_mfma(0, 2, 0)
 

@@ -318,11 +318,12 @@ def calibrate_hbm(device: int = 0, window_bytes: int = 4096 * 14336 * 2, iterati
 
 
 def calibrate_mfma(device: int = 0, waves_per_simd: int = 2, iterations: int = 20000,
-                   zeros: bool = False) -> tuple[float, float]:
-    """(TFLOP/s, ms) of tvk_calibrate_mfma_operands: the float16 MFMA rate with random (or all-zero) operands."""
+                   zeros: bool = False, mfma32: bool = False) -> tuple[float, float]:
+    """(TFLOP/s, ms) of tvk_calibrate_mfma_operands: the float16 MFMA rate with random (or all-zero) operands,
+    on v_mfma_f32_16x16x32_f16 (or v_mfma_f32_32x32x16_f16 with mfma32)."""
     tf, ms = C.c_double(), C.c_double()
-    check(load().tvk_calibrate_mfma_operands(device, waves_per_simd, iterations, 1 if zeros else 0, C.byref(tf),
-                                             C.byref(ms)))
+    operands = (1 if zeros else 0) + (2 if mfma32 else 0)
+    check(load().tvk_calibrate_mfma_operands(device, waves_per_simd, iterations, operands, C.byref(tf), C.byref(ms)))
     return tf.value, ms.value
 
 

@@ -83,6 +83,42 @@ __global__ __launch_bounds__(256) void mfma_ceiling_kernel(int iterations, int z
     out[id] = s;
 }
 
+// The same flops a trip on v_mfma_f32_32x32x16_f16: 32 MFMAs over eight
+// 32x32 accumulators (the larger instruction reads half the A/B register
+// bytes per flop; whether that buys clock under the power limit is what this
+// form measures).
+__global__ __launch_bounds__(256) void mfma32_ceiling_kernel(int iterations, int zeros, float* out) {
+    const uint32_t id = blockIdx.x * 256u + threadIdx.x;
+    half8 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a[i] = rand_frag(id * 16u + (uint32_t)i);
+        b[i] = rand_frag(id * 16u + 8u + (uint32_t)i);
+        if (zeros) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[i][e] = b[i][e] = (_Float16)0.0f;
+        }
+    }
+    f32x16 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+    for (int it = 0; it < iterations; it += 4) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[j % 4], b[(j / 4 + r) % 4], acc[j], 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[j][r];
+    out[id] = s;
+}
+
 __global__ __launch_bounds__(256) void hbm_read_kernel(const u32x4* p, int64_t n16, uint32_t* out) {
     uint32_t acc = 0;
     const int64_t stride = (int64_t)gridDim.x * 256;
@@ -151,7 +187,8 @@ extern "C" tvk_status tvk_calibrate_hbm(int device, size_t window_bytes, int ite
 extern "C" tvk_status tvk_calibrate_mfma_operands(int device, int waves_per_simd, int iterations, int operands, double* tflops,
                                                   double* ms) {
     if (!tflops || !ms) return fail(TVK_ERR_INVALID, "tvk_calibrate_mfma: tflops or ms is NULL");
-    if (operands != 0 && operands != 1) return fail(TVK_ERR_INVALID, "tvk_calibrate_mfma: operands must be 0 (random) or 1 (zeros)");
+    if (operands < 0 || operands > 3)
+        return fail(TVK_ERR_INVALID, "tvk_calibrate_mfma: operands must be 0 (random) or 1 (zeros), +2 for the 32x32x16 form");
     if (waves_per_simd < 1 || waves_per_simd > 4 || iterations < 1)
         return fail(TVK_ERR_INVALID, "tvk_calibrate_mfma: waves_per_simd must be 1..4 and iterations positive");
     int cur = 0;
@@ -170,9 +207,11 @@ extern "C" tvk_status tvk_calibrate_mfma_operands(int device, int waves_per_simd
             st = fail(TVK_ERR_DEVICE, "tvk_calibrate_mfma: stream or event creation failed");
             break;
         }
-        hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(blocks), dim3(256), 0, s, iterations / 8 + 4, operands, out);   // warm-up
+        auto kern = operands >= 2 ? mfma32_ceiling_kernel : mfma_ceiling_kernel;
+        const int zeros = operands & 1;
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, iterations / 8 + 4, zeros, out);   // warm-up
         if (hipEventRecord(e0, s) != hipSuccess) { st = fail(TVK_ERR_DEVICE, "tvk_calibrate_mfma: event record failed"); break; }
-        hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(blocks), dim3(256), 0, s, iterations, operands, out);
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, iterations, zeros, out);
         if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) {
             st = fail(TVK_ERR_DEVICE, std::string("tvk_calibrate_mfma: ") + hipGetErrorString(hipGetLastError()));
             break;
