@@ -641,6 +641,31 @@ tvk_status tvk_conv_dgrad(const tvk_convnd_desc* desc);
  * spatial dimensions. */
 tvk_status tvk_conv_wgrad(const tvk_convnd_desc* desc);
 
+/* Kernel choice for convolutions: the reference tunes its conv tilings per
+ * problem through the matmul autotuner (dispatch_conv_coop_shader,
+ * src/api/ops/conv.cpp:499-659, keyed by mode and the log2 problem sizes,
+ * :643-644). Here a 2-D problem (one or two spatial dimensions) can run on up
+ * to four kernel families, "conv_stem", "conv_halo", "conv_ring" and
+ * "conv_implicit_gemm"; the shape rule takes the first that applies, unless
+ * the kernel-choice table (the one tvk_gemm_* use, same tuning file) records
+ * another for the problem's shape class. float32, TVK_GEMM_EXACT and three
+ * spatial dimensions have one family, "conv_implicit_gemm". `mode` is one of: */
+#define TVK_CONV_FWD 0
+#define TVK_CONV_DGRAD 1
+#define TVK_CONV_WGRAD 2
+/* Newline-separated names of every family that computes the problem, the
+ * shape-chosen one first. TVK_ERR_INVALID when names_len is too small. */
+tvk_status tvk_conv_candidates(const tvk_convnd_desc* desc, int mode, char* names, size_t names_len);
+/* Records `kernel` (one of the candidates) for the problem's shape class, in
+ * the tuning file too when persist != 0. */
+tvk_status tvk_conv_choose(const tvk_convnd_desc* desc, int mode, const char* kernel, int persist);
+/* The convolution of `mode`, first timing every candidate (median of five
+ * calls after a warm-up) and recording and persisting the fastest when the
+ * shape class has no recorded choice. The timed calls write the problem's own
+ * output. Writes the family used to `name` (may be NULL). Synchronizes the
+ * stream when it times. */
+tvk_status tvk_conv_tune(const tvk_convnd_desc* desc, int mode, char* name, size_t name_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -248,6 +248,9 @@ def load() -> C.CDLL:
             getattr(lib, fn).argtypes = [C.POINTER(ConvDesc)]
         for fn in ("tvk_conv_fwd", "tvk_conv_dgrad", "tvk_conv_wgrad"):
             getattr(lib, fn).argtypes = [C.POINTER(ConvNdDesc)]
+        lib.tvk_conv_candidates.argtypes = [C.POINTER(ConvNdDesc), C.c_int, C.c_char_p, C.c_size_t]
+        lib.tvk_conv_choose.argtypes = [C.POINTER(ConvNdDesc), C.c_int, C.c_char_p, C.c_int]
+        lib.tvk_conv_tune.argtypes = [C.POINTER(ConvNdDesc), C.c_int, C.c_char_p, C.c_size_t]
         lib.tvk_copy.argtypes = [C.POINTER(CopyDesc)]
         lib.tvk_copy_plan.argtypes = [C.POINTER(CopyDesc), C.c_char_p, C.c_size_t]
         lib.tvk_fill.argtypes = [C.POINTER(FillDesc)]
@@ -274,6 +277,7 @@ _ALL_ENTRY_POINTS = (
     "tvk_memcpy_d2h", "tvk_memcpy_d2d", "tvk_gemm", "tvk_gemm_plan", "tvk_gemm_candidates",
     "tvk_gemm_choose", "tvk_gemm_tune", "tvk_tune_reset", "tvk_tune_path",
     "tvk_conv2d_fwd", "tvk_conv2d_dgrad", "tvk_conv2d_wgrad", "tvk_conv_fwd", "tvk_conv_dgrad", "tvk_conv_wgrad",
+    "tvk_conv_candidates", "tvk_conv_choose", "tvk_conv_tune",
     "tvk_copy", "tvk_copy_plan",
     "tvk_fill", "tvk_reduce_sum", "tvk_binary", "tvk_attention_fwd",
     "tvk_attention_bwd", "tvk_gemm_noalloc", "tvk_event_create", "tvk_event_destroy", "tvk_event_record",
@@ -742,3 +746,46 @@ def conv_wgrad(x, dy, w_shape, stride=1, padding=0, dilation=1, groups=1, exact=
     d.stream = torch.cuda.current_stream(x.device).cuda_stream
     _conv_call("tvk_conv_wgrad", d)
     return dw
+
+
+TVK_CONV_FWD, TVK_CONV_DGRAD, TVK_CONV_WGRAD = 0, 1, 2
+_CONV_ENTRY = {TVK_CONV_FWD: "tvk_conv_fwd", TVK_CONV_DGRAD: "tvk_conv_dgrad", TVK_CONV_WGRAD: "tvk_conv_wgrad"}
+
+
+def conv_problem(x, weight, y, bias=None, stride=1, padding=0, dilation=1, groups=1, exact=False,
+                 stream=None) -> ConvNdDesc:
+    """The descriptor of one convolution over existing contiguous device tensors: x [N, C, ...], weight,
+    y [N, C_out, ...] (which one a call writes depends on its mode)."""
+    import torch
+
+    d = make_convnd_desc(x.shape, weight.shape, x.dtype, stride, padding, dilation, groups, exact=exact)
+    if tuple(y.shape) != (d.n, d.c_out) + tuple(d.out_size[:d.spatial_dims]):
+        raise ValueError(f"y has shape {tuple(y.shape)}; the geometry gives {(d.n, d.c_out) + tuple(d.out_size[:d.spatial_dims])}")
+    d.x, d.weight, d.y = x.data_ptr(), weight.data_ptr(), y.data_ptr()
+    d.bias = None if bias is None else bias.data_ptr()
+    d.stream = stream if stream is not None else torch.cuda.current_stream(x.device).cuda_stream
+    return d
+
+
+def conv_run(d: ConvNdDesc, mode: int) -> None:
+    _conv_call(_CONV_ENTRY[mode], d)
+
+
+def conv_candidates(d: ConvNdDesc, mode: int) -> list[str]:
+    """Kernel families that compute the convolution (tvk_conv_candidates), the shape-chosen one first."""
+    buf = C.create_string_buffer(256)
+    check(load().tvk_conv_candidates(C.byref(d), mode, buf, len(buf)))
+    return buf.value.decode().split("\n")
+
+
+def conv_choose(d: ConvNdDesc, mode: int, kernel: str, persist: bool = False) -> None:
+    """Records `kernel` for the convolution's shape class (tvk_conv_choose)."""
+    check(load().tvk_conv_choose(C.byref(d), mode, kernel.encode(), 1 if persist else 0))
+
+
+def conv_tune(d: ConvNdDesc, mode: int) -> str:
+    """Runs the convolution through tvk_conv_tune; returns the family used."""
+    buf = C.create_string_buffer(64)
+    check(load().tvk_conv_tune(C.byref(d), mode, buf, len(buf)))
+    return buf.value.decode()
+

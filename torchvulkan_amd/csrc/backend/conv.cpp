@@ -57,6 +57,18 @@ bool exact_env() {
     return exact;
 }
 
+// TORCHVULKAN_AUTOTUNE=1: a convolution whose shape class has no recorded
+// kernel family times every candidate first and records the fastest (the
+// reference tunes its conv tilings on first sight, src/api/ops/conv.cpp:643-651)
+tvk_status run_conv_mode(tvk_convnd_desc& d, int mode) {
+    static const bool autotune = [] {
+        const char* e = std::getenv("TORCHVULKAN_AUTOTUNE");
+        return e != nullptr && e[0] && std::strcmp(e, "0") != 0;
+    }();
+    if (autotune) return tvk_conv_tune(&d, mode, nullptr, 0);
+    return mode == TVK_CONV_FWD ? tvk_conv_fwd(&d) : mode == TVK_CONV_DGRAD ? tvk_conv_dgrad(&d) : tvk_conv_wgrad(&d);
+}
+
 int64_t out_size(int64_t in, int64_t k, int64_t s, int64_t p, int64_t d) { return (in + 2 * p - d * (k - 1) - 1) / s + 1; }
 
 std::vector<int64_t> out_sizes(c10::IntArrayRef in_sp, c10::IntArrayRef k, const std::vector<int64_t>& s,
@@ -117,7 +129,7 @@ at::Tensor conv_forward_impl(const at::Tensor& x, const at::Tensor& w, const at:
     d.weight = w.data_ptr();
     d.bias = b.defined() ? b.data_ptr() : nullptr;
     d.y = y.data_ptr();
-    check_status(tvk_conv_fwd(&d), "tvk_conv_fwd");
+    check_status(run_conv_mode(d, TVK_CONV_FWD), "tvk_conv_fwd");
     return y;
 }
 
@@ -130,7 +142,7 @@ at::Tensor conv_dgrad_impl(const at::Tensor& dy, const at::Tensor& w, int64_t c_
     d.x = dx.data_ptr();
     d.weight = w.data_ptr();
     d.y = dy.data_ptr();
-    check_status(tvk_conv_dgrad(&d), "tvk_conv_dgrad");
+    check_status(run_conv_mode(d, TVK_CONV_DGRAD), "tvk_conv_dgrad");
     return dx;
 }
 
@@ -141,7 +153,7 @@ at::Tensor conv_wgrad_impl(const at::Tensor& x, const at::Tensor& dy, c10::IntAr
     d.x = x.data_ptr();
     d.weight = dw.data_ptr();
     d.y = dy.data_ptr();
-    check_status(tvk_conv_wgrad(&d), "tvk_conv_wgrad");
+    check_status(run_conv_mode(d, TVK_CONV_WGRAD), "tvk_conv_wgrad");
     return dw;
 }
 

@@ -28,9 +28,13 @@
 // TVK_GEMM_EXACT) use the rank-1 v_mfma_f32_32x32x1f32 so every output
 // accumulates in k order.
 #include "gemm_common.h"
+#include "tune_table.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
+#include <string>
+#include <vector>
 
 namespace tvk {
 namespace {
@@ -644,26 +648,157 @@ tvk_status run_generic(ConvArgs& p, int32_t dtype, bool seq, void* out, hipStrea
     return TVK_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Kernel choice. A 2-D problem can run on up to four kernel families:
+//   conv_stem           few input channels, one k step, straight from NCHW (conv_stem.hip)
+//   conv_halo           3x3 (stride 1 and 2) and 1x1 kernels through an LDS halo of the
+//                       NCHW source (conv_nhwc.hip)
+//   conv_ring           channels-last implicit GEMM on the LDS ring (conv_nhwc.hip)
+//   conv_implicit_gemm  the element-gathering implicit GEMM here, every problem
+// The shape rule takes the first that applies in that order; the kernel-choice
+// table (the GEMMs' table, kind "conv") may record another candidate for the
+// problem's shape class, as the reference tunes its conv tilings per problem
+// through the matmul autotuner (src/api/ops/conv.cpp:499-659). Only the
+// implicit GEMM runs float32 and TVK_GEMM_EXACT (the others are float16 /
+// bfloat16 kernels of another summation order), so a recorded choice never
+// changes an exact result.
+// ---------------------------------------------------------------------------
+
+enum class ConvFamily { SMALL, HALO, RING, GENERIC };
+
+const char* family_name(ConvFamily f) {
+    switch (f) {
+    case ConvFamily::SMALL: return "conv_stem";
+    case ConvFamily::HALO: return "conv_halo";
+    case ConvFamily::RING: return "conv_ring";
+    default: return "conv_implicit_gemm";
+    }
+}
+
+template <int MODE>
+ConvArgs gemm_args(const tvk_conv_desc& d) {
+    ConvArgs p = make_args(d);
+    p.out = MODE == FWD ? d.y : MODE == DGRAD ? d.x : d.weight;
+    p.has_bias = (MODE == FWD && d.bias) ? 1 : 0;
+    set_gemm_shape<MODE>(p);
+    return p;
+}
+
+// Every family that computes the (validated) problem, the shape rule's first.
+template <int MODE>
+std::vector<ConvFamily> conv_candidates(const tvk_conv_desc& d) {
+    std::vector<ConvFamily> out;
+    const ConvArgs p = gemm_args<MODE>(d);
+    if (p.N != 0 && p.M != 0 && p.K != 0) {
+        if (conv_small_applies(d, MODE)) out.push_back(ConvFamily::SMALL);
+        if (conv_halo_applies(d, MODE)) out.push_back(ConvFamily::HALO);
+        if (conv_ring_applies(d, MODE)) out.push_back(ConvFamily::RING);
+    }
+    out.push_back(ConvFamily::GENERIC);
+    return out;
+}
+
+// Shape class, after the reference's conv tune key (conv.cpp:643-644: mode,
+// ceil(log2) of the GEMM rows, columns, depth and planes, of the taps, padding,
+// unit stride): here mode, dtype, exact flag, bias, grouping, which families
+// apply, ceil(log2) of the GEMM M, N, K and of the taps, padding, unit stride
+// and unit dilation.
+template <int MODE>
+uint64_t conv_tune_key(const tvk_conv_desc& d, const std::vector<ConvFamily>& cands) {
+    const ConvArgs p = gemm_args<MODE>(d);
+    auto lg = [](int64_t v) {
+        uint64_t r = 0;
+        while (r < 63 && (int64_t(1) << r) < v) ++r;
+        return r;
+    };
+    uint64_t fam = 0;
+    for (ConvFamily f : cands) fam |= uint64_t(1) << (int)f;
+    const bool padded = d.padding[0] != 0 || d.padding[1] != 0;
+    const bool unit_stride = d.stride[0] == 1 && d.stride[1] == 1;
+    const bool unit_dil = d.dilation[0] == 1 && d.dilation[1] == 1;
+    return (uint64_t)MODE | (uint64_t)(d.dtype & 15) << 2 | (uint64_t)(d.flags & 1) << 6 | (uint64_t)(p.has_bias & 1) << 7 |
+           (uint64_t)(d.groups > 1) << 8 | fam << 9 | (uint64_t)padded << 13 | (uint64_t)unit_stride << 14 |
+           (uint64_t)unit_dil << 15 | lg(p.M) << 16 | lg(p.N) << 24 | lg(p.K) << 32 | lg(p.taps) << 40;
+}
+
+template <int MODE>
+tvk_status run_family(const tvk_conv_desc& d, ConvFamily f, const char* who) {
+    ConvArgs p = gemm_args<MODE>(d);
+    if (!p.out) return fail(TVK_ERR_INVALID, std::string(who) + ": output pointer is NULL");
+    if (p.N != 0 && p.M != 0 && p.K != 0) {
+        if (f == ConvFamily::SMALL) return conv_small_run(d, MODE, who);
+        if (f == ConvFamily::HALO) return conv_halo_run(d, MODE, who);
+        if (f == ConvFamily::RING) return conv_ring_run(d, MODE, who);
+    }
+    return run_generic<2, MODE>(p, d.dtype, (d.flags & TVK_GEMM_EXACT) != 0, p.out, resolve_stream(d.stream), who);
+}
+
+// The shape rule's family unless the table records another candidate for the
+// shape class (a recorded family that does not apply is ignored).
+template <int MODE>
+ConvFamily choose_family(const tvk_conv_desc& d, const std::vector<ConvFamily>& cands) {
+    std::string id;
+    if (cands.size() > 1 && tune_lookup("conv", conv_tune_key<MODE>(d, cands), id))
+        for (ConvFamily f : cands)
+            if (id == family_name(f)) return f;
+    return cands[0];
+}
+
 template <int MODE>
 tvk_status run_conv(const tvk_conv_desc* desc, const char* who) {
     tvk_status st = conv_validate(desc, who);
     if (st != TVK_OK) return st;
     const tvk_conv_desc& d = *desc;
-    void* out = MODE == FWD ? d.y : MODE == DGRAD ? d.x : d.weight;
-    if (!out) return fail(TVK_ERR_INVALID, std::string(who) + ": output pointer is NULL");
-    ConvArgs p = make_args(d);
-    p.out = out;
-    p.has_bias = (MODE == FWD && d.bias) ? 1 : 0;
-    set_gemm_shape<MODE>(p);
-    if (p.N != 0 && p.M != 0 && p.K != 0) {
-        // few input channels: one-k-step kernels that gather straight from NCHW (conv_stem.hip)
-        if (conv_small_applies(d, MODE)) return conv_small_run(d, MODE, who);
-        // stride-1 3x3 forward / grad input through an LDS halo of the NCHW source (conv_nhwc.hip)
-        if (conv_halo_applies(d, MODE)) return conv_halo_run(d, MODE, who);
-        // channels-last implicit GEMM on the LDS ring (conv_nhwc.hip) where it applies
-        if (conv_ring_applies(d, MODE)) return conv_ring_run(d, MODE, who);
+    const std::vector<ConvFamily> cands = conv_candidates<MODE>(d);
+    return run_family<MODE>(d, choose_family<MODE>(d, cands), who);
+}
+
+// Times every candidate and returns the fastest: the first candidate runs for
+// about 2 ms first (the clock ramps up after an idle spell), then each takes
+// the median of five timed calls after one untimed call, as tvk_gemm_tune
+// does. The timed calls write the problem's own output.
+template <int MODE>
+tvk_status time_families(const tvk_conv_desc& d, const std::vector<ConvFamily>& cands, ConvFamily& best, const char* who) {
+    const hipStream_t s = resolve_stream(d.stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        (void)hipGetLastError();
+        if (e0) (void)hipEventDestroy(e0);
+        return fail(TVK_ERR_DEVICE, std::string(who) + ": hipEventCreate failed");
     }
-    return run_generic<2, MODE>(p, d.dtype, (d.flags & TVK_GEMM_EXACT) != 0, out, resolve_stream(d.stream), who);
+    if (hipEventRecord(e0, s) == hipSuccess) {
+        for (int i = 0; i < 200; ++i) {
+            if (run_family<MODE>(d, cands[0], who) != TVK_OK) break;
+            float ms = 0.0f;
+            if (i % 8 == 7 && (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                               hipEventElapsedTime(&ms, e0, e1) != hipSuccess || ms > 2.0f))
+                break;
+        }
+        (void)hipGetLastError();
+    }
+    float best_ms = INFINITY;
+    best = cands[0];
+    for (ConvFamily f : cands) {
+        float spans[5];
+        bool ok = run_family<MODE>(d, f, who) == TVK_OK;
+        for (int i = 0; ok && i < 5; ++i)
+            ok = hipEventRecord(e0, s) == hipSuccess && run_family<MODE>(d, f, who) == TVK_OK &&
+                 hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+                 hipEventElapsedTime(&spans[i], e0, e1) == hipSuccess;
+        if (!ok) {
+            (void)hipGetLastError();
+            continue;
+        }
+        std::nth_element(spans, spans + 2, spans + 5);
+        if (spans[2] < best_ms) {
+            best_ms = spans[2];
+            best = f;
+        }
+    }
+    (void)hipStreamSynchronize(s);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return TVK_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -765,6 +900,115 @@ tvk_status run_convnd(const tvk_convnd_desc* desc, const char* who) {
 }  // namespace tvk
 
 using namespace tvk;
+
+namespace tvk {
+namespace {
+
+void put_conv_name(char* name, size_t name_len, const std::string& n) {
+    if (name && name_len) snprintf(name, name_len, "%s", n.c_str());
+}
+
+// The 2-D view of a validated N-d problem, or false for three spatial
+// dimensions (one family: the 3-D implicit GEMM).
+bool nd_as_2d(const tvk_convnd_desc& d, tvk_conv_desc& c) {
+    if (d.spatial_dims >= 3) return false;
+    c = as_2d(d);
+    return true;
+}
+
+template <int MODE>
+tvk_status conv_candidates_nd(const tvk_convnd_desc* desc, char* names, size_t names_len, const char* who) {
+    tvk_status st = convnd_validate(desc, who);
+    if (st != TVK_OK) return st;
+    if (!names || names_len == 0) return fail(TVK_ERR_INVALID, std::string(who) + ": name buffer is empty");
+    std::string all;
+    tvk_conv_desc c;
+    if (!nd_as_2d(*desc, c)) all = family_name(ConvFamily::GENERIC);
+    else
+        for (ConvFamily f : conv_candidates<MODE>(c)) all += (all.empty() ? "" : "\n") + std::string(family_name(f));
+    if (all.size() + 1 > names_len)
+        return fail(TVK_ERR_INVALID, std::string(who) + ": the names need " + std::to_string(all.size() + 1) + " bytes");
+    snprintf(names, names_len, "%s", all.c_str());
+    return TVK_OK;
+}
+
+template <int MODE>
+tvk_status conv_choose_nd(const tvk_convnd_desc* desc, const char* kernel, int persist, const char* who) {
+    tvk_status st = convnd_validate(desc, who);
+    if (st != TVK_OK) return st;
+    if (!kernel) return fail(TVK_ERR_INVALID, std::string(who) + ": kernel is NULL");
+    tvk_conv_desc c;
+    if (!nd_as_2d(*desc, c)) {
+        // one family: nothing to record
+        if (std::string(kernel) == family_name(ConvFamily::GENERIC)) return TVK_OK;
+        return fail(TVK_ERR_INVALID, std::string(who) + ": " + kernel + " does not compute this convolution");
+    }
+    const std::vector<ConvFamily> cands = conv_candidates<MODE>(c);
+    for (ConvFamily f : cands)
+        if (std::string(kernel) == family_name(f)) {
+            tune_record("conv", conv_tune_key<MODE>(c, cands), family_name(f), persist != 0);
+            return TVK_OK;
+        }
+    return fail(TVK_ERR_INVALID, std::string(who) + ": " + kernel + " does not compute this convolution");
+}
+
+template <int MODE>
+tvk_status conv_tune_nd(const tvk_convnd_desc* desc, char* name, size_t name_len, const char* who) {
+    tvk_status st = convnd_validate(desc, who);
+    if (st != TVK_OK) return st;
+    tvk_conv_desc c;
+    if (!nd_as_2d(*desc, c)) {
+        put_conv_name(name, name_len, family_name(ConvFamily::GENERIC));
+        return run_convnd<MODE>(desc, who);
+    }
+    const std::vector<ConvFamily> cands = conv_candidates<MODE>(c);
+    ConvFamily best = cands[0];
+    if (cands.size() > 1) {
+        const uint64_t key = conv_tune_key<MODE>(c, cands);
+        std::string id;
+        bool known = false;
+        if (tune_lookup("conv", key, id))
+            for (ConvFamily f : cands)
+                if (id == family_name(f)) {
+                    best = f;
+                    known = true;
+                    break;
+                }
+        if (!known) {
+            st = time_families<MODE>(c, cands, best, who);
+            if (st != TVK_OK) return st;
+            tune_record("conv", key, family_name(best), true);
+        }
+    }
+    put_conv_name(name, name_len, family_name(best));
+    return run_family<MODE>(c, best, who);
+}
+
+int conv_mode_ok(int mode) { return mode == FWD || mode == DGRAD || mode == WGRAD; }
+
+}  // namespace
+}  // namespace tvk
+
+extern "C" tvk_status tvk_conv_candidates(const tvk_convnd_desc* desc, int mode, char* names, size_t names_len) {
+    if (!conv_mode_ok(mode)) return fail(TVK_ERR_INVALID, "tvk_conv_candidates: mode must be TVK_CONV_FWD, _DGRAD or _WGRAD");
+    if (mode == FWD) return conv_candidates_nd<FWD>(desc, names, names_len, "tvk_conv_candidates");
+    if (mode == DGRAD) return conv_candidates_nd<DGRAD>(desc, names, names_len, "tvk_conv_candidates");
+    return conv_candidates_nd<WGRAD>(desc, names, names_len, "tvk_conv_candidates");
+}
+
+extern "C" tvk_status tvk_conv_choose(const tvk_convnd_desc* desc, int mode, const char* kernel, int persist) {
+    if (!conv_mode_ok(mode)) return fail(TVK_ERR_INVALID, "tvk_conv_choose: mode must be TVK_CONV_FWD, _DGRAD or _WGRAD");
+    if (mode == FWD) return conv_choose_nd<FWD>(desc, kernel, persist, "tvk_conv_choose");
+    if (mode == DGRAD) return conv_choose_nd<DGRAD>(desc, kernel, persist, "tvk_conv_choose");
+    return conv_choose_nd<WGRAD>(desc, kernel, persist, "tvk_conv_choose");
+}
+
+extern "C" tvk_status tvk_conv_tune(const tvk_convnd_desc* desc, int mode, char* name, size_t name_len) {
+    if (!conv_mode_ok(mode)) return fail(TVK_ERR_INVALID, "tvk_conv_tune: mode must be TVK_CONV_FWD, _DGRAD or _WGRAD");
+    if (mode == FWD) return conv_tune_nd<FWD>(desc, name, name_len, "tvk_conv_tune");
+    if (mode == DGRAD) return conv_tune_nd<DGRAD>(desc, name, name_len, "tvk_conv_tune");
+    return conv_tune_nd<WGRAD>(desc, name, name_len, "tvk_conv_tune");
+}
 
 extern "C" tvk_status tvk_conv2d_fwd(const tvk_conv_desc* desc) { return run_conv<FWD>(desc, "tvk_conv2d_fwd"); }
 extern "C" tvk_status tvk_conv2d_dgrad(const tvk_conv_desc* desc) { return run_conv<DGRAD>(desc, "tvk_conv2d_dgrad"); }

@@ -3,6 +3,7 @@
     python -m torchvulkan_amd.tune                 # the benchmark configs' products, a table on stdout
     python -m torchvulkan_amd.tune --record        # and record each product's fastest kernel in the tuning file
     python -m torchvulkan_amd.tune --shape 4096x1024x512:f16:nt ...
+    python -m torchvulkan_amd.tune --conv [--record]   # the C4 convolutions' kernel families, each direction
 
 For each product it lists tvk_gemm_candidates, records one candidate at a
 time with tvk_gemm_choose (memory only), times tvk_gemm over 7 spans of 10
@@ -88,21 +89,29 @@ def operands(M, N, K, dt, lay, batch, bias, gen):
     return a, b, c, kw
 
 
-def time_launches(lib, desc, spans=7, per_span=10) -> float:
-    """Median over spans of the average launch time (us)."""
+def time_calls(call, spans=7, per_span=10) -> float:
+    """Median over spans of the average time of `call` (us). Each span starts behind a short GPU wait
+    (torch.cuda._sleep, on the same stream), so the host has queued the whole span before the GPU reaches
+    it and the span measures the kernels back to back rather than the host's launch rate."""
     for _ in range(3):
-        _abi.check(lib.tvk_gemm(C.byref(desc)))
+        _abi.check(call())
     torch.cuda.synchronize()
     out = []
     for _ in range(spans):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(200_000)
         e0.record()
         for _ in range(per_span):
-            lib.tvk_gemm(C.byref(desc))
+            call()
         e1.record()
         torch.cuda.synchronize()
         out.append(e0.elapsed_time(e1) * 1e3 / per_span)
     return statistics.median(out)
+
+
+def time_launches(lib, desc, spans=7, per_span=10) -> float:
+    """Median over spans of the average tvk_gemm launch time (us)."""
+    return time_calls(lambda: lib.tvk_gemm(C.byref(desc)), spans, per_span)
 
 
 def tune_product(lib, spec, gen, record: bool):
@@ -129,15 +138,73 @@ def tune_product(lib, spec, gen, record: bool):
     return name, names[0], times[names[0]], best, times[best], flops, times
 
 
+# (name, c_in, c_out, kernel, stride, padding, input size): the C4 ResNet convolutions at batch 128
+CONV_LAYERS = [
+    ("3->64 3x3 s1", 3, 64, 3, 1, 1, 32),
+    ("64->64 3x3 s1", 64, 64, 3, 1, 1, 32),
+    ("64->128 3x3 s2", 64, 128, 3, 2, 1, 32),
+    ("128->256 3x3 s2", 128, 256, 3, 2, 1, 16),
+    ("64->128 1x1 s2", 64, 128, 1, 2, 0, 32),
+    ("128->256 1x1 s2", 128, 256, 1, 2, 0, 16),
+]
+CONV_MODES = (("fwd", _abi.TVK_CONV_FWD), ("dgrad", _abi.TVK_CONV_DGRAD), ("wgrad", _abi.TVK_CONV_WGRAD))
+
+
+def tune_conv(lib, layer, gen, record: bool, batch: int = 128):
+    """Every kernel family of the layer's three directions (tvk_conv_candidates), each recorded in turn
+    (tvk_conv_choose, memory only) and timed through the ordinary entry point; two passes, the faster
+    median kept."""
+    name, cin, cout, k, s, p, hw = layer
+    f16 = torch.float16
+    ho = (hw + 2 * p - k) // s + 1
+    x = torch.randn((batch, cin, hw, hw), generator=gen).to(f16).to("cuda")
+    w = (torch.randn((cout, cin, k, k), generator=gen) * (2.0 / (cin * k * k)) ** 0.5).to(f16).to("cuda")
+    y = torch.randn((batch, cout, ho, ho), generator=gen).to(f16).to("cuda")
+    dx, dw = torch.empty_like(x), torch.empty_like(w)
+    rows = []
+    for mode_name, mode in CONV_MODES:
+        d = _abi.conv_problem(*((x, w, y) if mode == _abi.TVK_CONV_FWD else (dx, w, y) if mode == _abi.TVK_CONV_DGRAD
+                                else (x, dw, y)), stride=s, padding=p)
+        entry = getattr(lib, _abi._CONV_ENTRY[mode])
+        names = _abi.conv_candidates(d, mode)
+        times = {}
+        for _ in range(2):
+            for n in names:
+                _abi.tune_reset()
+                _abi.conv_choose(d, mode, n)
+                t = time_calls(lambda: entry(C.byref(d)))
+                times[n] = min(times.get(n, t), t)
+        _abi.tune_reset()
+        best = min(times, key=times.get)
+        if record:
+            _abi.conv_choose(d, mode, best, persist=True)
+        rows.append((name, mode_name, names[0], times[names[0]], best, times[best], times))
+    return rows
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--shape", action="append", default=[], help="MxNxK[:dtype[:layout[:batch[:bias]]]]")
     ap.add_argument("--record", action="store_true", help="persist each product's fastest kernel")
     ap.add_argument("--all", action="store_true", help="print every candidate's time")
+    ap.add_argument("--conv", action="store_true", help="the C4 convolutions' kernel families instead of products")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         raise SystemExit("torchvulkan_amd.tune needs a GPU")
     lib = _abi.load()
+    if args.conv:
+        gen = torch.Generator().manual_seed(0)
+        print("| layer (batch 128, fp16) | direction | shape rule's family | us | fastest family | us | ratio |")
+        print("|---|---|---|---|---|---|---|")
+        for layer in CONV_LAYERS:
+            for name, mode, chosen, t0, best, t1, times in tune_conv(lib, layer, gen, args.record):
+                print(f"| {name} | {mode} | `{chosen}` | {t0:.2f} | `{best}` | {t1:.2f} | {t0 / t1:.2f} |", flush=True)
+                if args.all:
+                    print("|  |  | " + ", ".join(f"`{n}` {t:.1f}" for n, t in sorted(times.items(), key=lambda x: x[1]))
+                          + " | | | | |")
+        if args.record:
+            print(f"recorded in {_abi.tune_path()}")
+        return 0
     specs = [parse_shape(s) for s in args.shape] or CONFIG_PRODUCTS
     gen = torch.Generator().manual_seed(0)
     print("| product | shape rule's kernel | us | fastest kernel | us | ratio | TFLOP/s (fastest) |")
