@@ -80,6 +80,26 @@ def test_winograd_restatement_close_to_direct(dtype, tol):
         assert not np.array_equal(wino, direct)
 
 
+@pytest.mark.parametrize("dtype", [orc.F32, orc.F16])
+def test_winograd_transforms_exact_on_integers(dtype):
+    # Weights in multiples of 4 and small integer inputs keep every intermediate of F(2x2, 3x3) an
+    # integer far inside float16's exact range: the filter transform's halvings divide sums of
+    # multiples of 4, the input transform and the products add integers (|M| < 2048 here). The
+    # staged roundings are then all exact and Winograd equals direct convolution bit for bit; a wrong
+    # coefficient, sign or index in G, B^T or A^T (or a mis-tiled output) breaks the equality.
+    rng = np.random.default_rng(11)
+    x = rng.integers(-2, 3, size=(2, 4, 7, 9)).astype(np.float32)
+    w = (4 * rng.integers(-1, 2, size=(5, 4, 3, 3))).astype(np.float32)
+    b = rng.integers(-3, 4, size=5).astype(np.float32)
+    direct64 = torch.nn.functional.conv2d(torch.from_numpy(x).double(), torch.from_numpy(w).double(),
+                                          torch.from_numpy(b).double(), padding=1).numpy()
+    assert np.abs(direct64).max() < 2048
+    if dtype == orc.F16:
+        x, w, b = (v.astype(np.float16).view(np.uint16) for v in (x, w, b))
+    wino = orc.to_f32(orc.winograd_conv2d(x, w, dtype, bias=b, padding=(1, 1)), dtype)
+    assert np.array_equal(wino, direct64.astype(np.float32))
+
+
 # ---------------------------------------------------------------------------
 # 3-D restatement (oracle_conv3d_*): the reference takes up to three spatial
 # dimensions (src/api/ops/conv.cpp:295-311)

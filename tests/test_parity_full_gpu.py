@@ -10,6 +10,13 @@
 - float16 autograd through the vulkan device at C2 and C4 shapes: nn.Linear
   (256 x 4096 -> 4096) and F.conv2d (64 -> 64, 3x3, batch 128) forward and
   backward against the oracle (and, for the bias gradient, a float64 sum).
+- The C3 layer's backward products at full size (8192 tokens), as nn.Linear's
+  backward forms them: dX = dY.W and dW = dY^T.X for every projection, every
+  element against float64, rows spread over every 128-row tile against the
+  oracle.
+- The C2 10-output layer's backward: dX with K = 10, dW on the M <= 16
+  streaming kernel, every element against the oracle; and the same layer
+  under autograd with loss sum() (a gradient with stride 0 in both dims).
 
 Tolerances are the ones gemm_cases.py states: |got - ref| <= 5e-3 (|ref| + 1)
 for float16. Against float64 the float16 result also carries its own
@@ -168,3 +175,66 @@ def test_c4_conv_autograd_fp16(gpu, strict):
     assert_close(wv.grad.cpu().float().numpy(), ogw, F16, "conv2d grad weight vs oracle")
     db = dy.double().sum((0, 2, 3)).numpy()
     assert_close(bv.grad.cpu().float().numpy(), db, F16, "conv2d grad bias vs float64 sum")
+
+
+C3_LINEARS = [(512, 512), (512, 256), (512, 3072), (1536, 512), (512, 96)]   # (in, out): q, kv, gate_up, down, head
+
+
+@pytest.mark.parametrize("fin,fout", C3_LINEARS, ids=[f"{a}to{b}" for a, b in C3_LINEARS])
+def test_c3_backward_products_full(gpu, fin, fout):
+    T = 8192
+    dy = _rand((T, fout), 100 + fout)
+    x = _rand((T, fin), 200 + fin)
+    w = _rand((fout, fin), 300 + fin + fout, std=0.02)
+    dyd, wd, xd = dy.to(DEV), w.to(DEV), x.to(DEV)
+    dx = torch.empty((T, fin), dtype=F16, device=DEV)
+    dw = torch.empty((fout, fin), dtype=F16, device=DEV)
+    gpu.gemm(dyd, wd, dx)            # dX = dY . W: B [out, in] row-major (n-contiguous), K = out
+    gpu.gemm(dyd.t(), xd, dw)        # dW = dY^T . X: A an m-contiguous view, K = 8192 tokens
+    torch.cuda.synchronize()
+    plans = (gpu.gemm_plan(dyd, wd, dx), gpu.gemm_plan(dyd.t(), xd, dw))
+    got_dx, got_dw = dx.cpu().float().numpy(), dw.cpu().float().numpy()
+    assert_close(got_dx, (dy.double() @ w.double()).numpy(), F16, f"dX {plans[0]} vs float64")
+    assert_close(got_dw, (dy.double().t() @ x.double()).numpy(), F16, f"dW {plans[1]} vs float64")
+    rows = np.r_[0:T:97, T - 1]        # at least one row of every 128-row tile, and the last
+    assert_close(got_dx[rows], oracle_mm(dy[rows], w, F16), F16, f"dX {plans[0]} vs oracle")
+    wrows = np.r_[0:fout:7, fout - 1]
+    assert_close(got_dw[wrows], oracle_mm(dy.t()[wrows], x, F16), F16, f"dW {plans[1]} vs oracle")
+
+
+def test_c2_last_layer_backward(gpu):
+    g = torch.Generator().manual_seed(120)
+    dy = torch.randn((256, 10), generator=g).to(F16)
+    w = (torch.randn((10, 4096), generator=g) * 0.02).to(F16)
+    x = torch.rand((256, 4096), generator=g).to(F16)
+    dyd, wd, xd = dy.to(DEV), w.to(DEV), x.to(DEV)
+    dx = torch.empty((256, 4096), dtype=F16, device=DEV)
+    dw = torch.empty((10, 4096), dtype=F16, device=DEV)
+    gpu.gemm(dyd, wd, dx)            # K = 10: one partial k step
+    gpu.gemm(dyd.t(), xd, dw)        # M = 10: the streaming kernel
+    torch.cuda.synchronize()
+    assert gpu.gemm_plan(dyd.t(), xd, dw).startswith("gemm16_skinny"), gpu.gemm_plan(dyd.t(), xd, dw)
+    assert_close(dx.cpu().float().numpy(), oracle_mm(dy, w, F16), F16, "dX, K = 10")
+    assert_close(dw.cpu().float().numpy(), oracle_mm(dy.t(), x, F16), F16, "dW, M = 10")
+
+
+def test_c2_last_layer_autograd_sum_loss(gpu, strict):
+    import torchvulkan_amd  # noqa: F401
+
+    torch.manual_seed(1)
+    lin = torch.nn.Linear(4096, 10).to(F16)
+    x = torch.rand((256, 4096), generator=gen(121)).to(F16)
+    lv = torch.nn.Linear(4096, 10).to(F16).to(V)
+    with torch.no_grad():
+        lv.weight.copy_(lin.weight.to(V))
+        lv.bias.copy_(lin.bias.to(V))
+    xv = x.to(V).requires_grad_()
+    y = lv(xv)
+    y.sum().backward()               # the gradient reaches the products as ones expanded with stride 0
+    W, b = lin.weight.detach(), lin.bias.detach()
+    ones = torch.ones((256, 10), dtype=F16)
+    assert_close(y.detach().cpu().float().numpy(), oracle_mm(x, W.t(), F16, bias=b, beta=1.0), F16, "forward")
+    assert_close(xv.grad.cpu().float().numpy(), oracle_mm(ones, W, F16), F16, "grad input")
+    assert_close(lv.weight.grad.cpu().float().numpy(), oracle_mm(ones.t(), x, F16), F16, "grad weight")
+    assert torch.equal(lv.bias.grad.cpu(), torch.full((10,), 256.0, dtype=F16)), "grad bias"
+
