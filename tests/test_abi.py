@@ -90,7 +90,7 @@ def test_gemm_validation_codes(field, value, status):
     ((0, 2000, 1), (0, 1000, 1), _abi.TVK_F16, 7, 1000, 2000, "gemm16_skinny_bn"),
     ((0, 4096, 1), (0, 1, 4096), _abi.TVK_BF16, 8, 4096, 4096, "gemm16_skinny_bk"),
     ((0, 3, 5), (0, 4, 1), _abi.TVK_F16, 8, 4, 4, "gemm_generic"),
-    ((0, 1024, 1), (0, 1024, 1), _abi.TVK_F32, 1024, 1024, 1024, "gemm_seq_mfma_64x128"),
+    ((0, 1024, 1), (0, 1024, 1), _abi.TVK_F32, 1024, 1024, 1024, "gemm_seq_mfma_64x64"),
     ((0, 2048, 1), (0, 2048, 1), _abi.TVK_F32, 2048, 2048, 2048, "gemm_seq_mfma_128x128"),
     ((0, 4, 1), (0, 4, 1), _abi.TVK_BF16, 4, 4, 0, "gemm_k0_fill"),
 ])

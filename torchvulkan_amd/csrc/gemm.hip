@@ -503,6 +503,95 @@ __global__ __launch_bounds__(256) void gemm_seq_mfma_kernel(GemmArgs p) {
         }
 }
 
+// The same order on 64x64 tiles for products with few tiles (1024^2 float32:
+// 256 tiles against 128 of 64x128): each of the four waves owns 16 rows x 64
+// columns and issues v_mfma_f32_16x16x1_4b_f32 with its row's A value in all
+// four blocks, so one instruction is a 16x64 rank-1 update (block q: columns
+// 16q .. 16q+15), at the matrix core's float32 rate like the 32x32x1 form.
+// Every output again accumulates fmaf(a_k, b_k, acc) for k = 0, 1, 2, ...
+template <int DT, bool AK, bool BK, int BM, int BN, bool VEC>
+__global__ __launch_bounds__(256) void gemm_seq16_kernel(GemmArgs p) {
+    static_assert(BM == 64 && BN == 64, "64x64 tiles of four 16x64 waves");
+    typedef SeqLoader<DT, AK ? BM : Q_BK, AK ? Q_BK : BM, VEC> LA;
+    typedef SeqLoader<DT, BK ? BN : Q_BK, BK ? Q_BK : BN, VEC> LB;
+    constexpr int A_FL = (AK ? BM : Q_BK) * LA::LD;
+    constexpr int B_FL = (BK ? BN : Q_BK) * LB::LD;
+    __shared__ float lds[2][A_FL + B_FL];
+
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int b = blockIdx.y;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    constexpr int ES = DT == TVK_F32 ? 4 : 2;
+    const char* A = reinterpret_cast<const char*>(p.a) + a_boff(p, b) * ES;
+    const char* B = reinterpret_cast<const char*>(p.b) + b_boff(p, b) * ES;
+    const int64_t a_bytes = ES * ((int64_t)(p.M - 1) * p.sa[1] + (int64_t)(p.K - 1) * p.sa[2] + 1);
+    const int64_t b_bytes = ES * ((int64_t)(p.N - 1) * p.sb[2] + (int64_t)(p.K - 1) * p.sb[1] + 1);
+    __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)min(a_bytes, (int64_t)0x7fffffff), 0x00020000);
+    __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)B, 0, (int)min(b_bytes, (int64_t)0x7fffffff), 0x00020000);
+
+    LA la;
+    LB lb;
+    auto load = [&](int k0) {
+        if constexpr (AK) la.load(ra, p.sa[1], p.sa[2], m0, p.M, k0, p.K, tid);
+        else la.load(ra, p.sa[2], p.sa[1], k0, p.K, m0, p.M, tid);
+        if constexpr (BK) lb.load(rb, p.sb[2], p.sb[1], n0, p.N, k0, p.K, tid);
+        else lb.load(rb, p.sb[1], p.sb[2], k0, p.K, n0, p.N, tid);
+    };
+
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+
+    const int nk = (p.K + Q_BK - 1) / Q_BK;
+    load(0);
+    la.store(lds[0], tid);
+    lb.store(lds[0] + A_FL, tid);
+    __syncthreads();
+    const int arow = wave * 16 + lane % 16;   // the same row in all four blocks
+    const int bcol = lane;                    // block lane / 16, column lane % 16
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load((kt + 1) * Q_BK);
+        const float* As = lds[buf];
+        const float* Bs = lds[buf] + A_FL;
+#pragma unroll
+        for (int k4 = 0; k4 < Q_BK; k4 += 4) {
+            float av[4], bv[4];
+            if constexpr (AK) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(As + arow * LA::LD + k4);
+                av[0] = v.x; av[1] = v.y; av[2] = v.z; av[3] = v.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) av[q] = As[(k4 + q) * LA::LD + arow];
+            }
+            if constexpr (BK) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(Bs + bcol * LB::LD + k4);
+                bv[0] = v.x; bv[1] = v.y; bv[2] = v.z; bv[3] = v.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) bv[q] = Bs[(k4 + q) * LB::LD + bcol];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x1f32(av[q], bv[q], acc, 0, 0, 0);
+        }
+        if (kt + 1 < nk) {
+            la.store(lds[buf ^ 1], tid);
+            lb.store(lds[buf ^ 1] + A_FL, tid);
+        }
+        __syncthreads();
+    }
+
+    // register r: block r / 4 (columns 16 (r / 4) ..), row (lane / 16) * 4 + r % 4, column lane % 16
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wave * 16 + (lane / 16) * 4 + r % 4;
+        const int col = n0 + (r / 4) * 16 + lane % 16;
+        if (row < p.M && col < p.N) store_out<DT, true>(p, b, row, col, acc[r]);
+    }
+}
+
 // ----------------------------------------------------------------------------
 // operand repack: dst[b][r][c] = src(b, r, c) for c < C, 0 for C <= c < Cp
 // (c is the operand's contiguous dimension; rows are Cp elements apart)
@@ -532,7 +621,7 @@ __global__ __launch_bounds__(256) void repack16_kernel(const uint16_t* src, uint
 // host dispatch
 // ----------------------------------------------------------------------------
 
-enum class Kern { K0, GENERIC, SEQ256, SEQ128, SEQ64, MFMA256, MFMA256W8, MFMA128, MFMA64, SKINNY, DMA256, DMA128, DMA128R8, DMA128X256, DMA256X128 };
+enum class Kern { K0, GENERIC, SEQ256, SEQ128, SEQ64, SEQ16, MFMA256, MFMA256W8, MFMA128, MFMA64, SKINNY, DMA256, DMA128, DMA128R8, DMA128X256, DMA256X128 };
 
 struct Plan {
     Kern kern;
@@ -710,11 +799,12 @@ Plan make_plan(const tvk_gemm_desc& d) {
     if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
         pl.kern = big ? Kern::SEQ256 : Kern::SEQ128;
         pl.name = big ? "gemm_seq_mfma_256x256" : "gemm_seq_mfma_128x128";
-        // fewer 128x128 tiles than half the CUs: 64x128 tiles, twice the workgroups
-        // (the smallest tile of the 2x2 waves of 32x64 rank-1 MFMA; same k order)
+        // fewer 128x128 tiles than half the CUs: 64x64 tiles of four 16x64 waves,
+        // four times the workgroups (same k order; the 64x128 tiles of 2x2 waves
+        // of 32x64 stay a kernel-choice candidate)
         if (!big && ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch < 128) {
-            pl.kern = Kern::SEQ64;
-            pl.name = "gemm_seq_mfma_64x128";
+            pl.kern = Kern::SEQ16;
+            pl.name = "gemm_seq_mfma_64x64";
         }
         return pl;
     }
@@ -795,6 +885,7 @@ std::vector<Plan> candidate_plans(const tvk_gemm_desc& d) {
         add(with_kern(lay, Kern::SEQ256, "gemm_seq_mfma_256x256"));
         add(with_kern(lay, Kern::SEQ128, "gemm_seq_mfma_128x128"));
         add(with_kern(lay, Kern::SEQ64, "gemm_seq_mfma_64x128"));
+        add(with_kern(lay, Kern::SEQ16, "gemm_seq_mfma_64x64"));
         return out;
     }
     if (skinny_applies(d.M, d.N, d.K, d.batch)) add(skinny_plan(d, lay));
@@ -898,6 +989,12 @@ void launch_seq(const Plan& pl, GemmArgs& p, dim3 grid, hipStream_t s) {
     TVK_LAYOUT_SWITCH(pl, 256, gemm_seq_mfma_kernel);
 }
 
+template <int DT>
+void launch_seq16(const Plan& pl, GemmArgs& p, dim3 grid, hipStream_t s) {
+    constexpr int BM = 64, BN = 64;
+    TVK_LAYOUT_SWITCH(pl, 256, gemm_seq16_kernel);
+}
+
 // Scratch bytes one batch chunk of `nb` matrices needs under plan pl:
 // repacked operands (256-byte aligned each), then split-K partials, or the
 // streaming kernel's partials. rep_a / rep_b / part_b return the pieces.
@@ -989,6 +1086,13 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixe
             hipLaunchKernelGGL(gemm_generic_kernel<DT>, dim3((unsigned)std::min<int64_t>(((int64_t)d.M * d.N + 255) / 256, 65536), nb),
                                dim3(256), 0, s, q);
             break;
+        case Kern::SEQ16: {
+            q.tiles_m = (int)((d.M + 63) / 64);
+            q.tiles_n = (int)((d.N + 63) / 64);
+            dim3 grid(q.tiles_m * q.tiles_n, nb);
+            launch_seq16<DT>(pl, q, grid, s);
+            break;
+        }
         case Kern::SEQ256:
         case Kern::SEQ128:
         case Kern::SEQ64: {
