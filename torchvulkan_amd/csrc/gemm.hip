@@ -779,8 +779,16 @@ bool split_plan(const tvk_gemm_desc& d, int64_t want, Plan& pl, Kern kern = Kern
     const int64_t chunk = ((d.K + want - 1) / want + 63) / 64 * 64;
     const int64_t split = (d.K + chunk - 1) / chunk;
     if (split < 2 || split * d.batch * d.M * d.N * 4 > (int64_t(512) << 20)) return false;
-    pl = with_kern(pl, kern, kern == Kern::DMA128 ? "gemm16_dma_128x128_splitk"
-                             : kern == Kern::DMA128R8 ? "gemm16_dma_128x128_ring8_splitk" : "gemm16_mfma_128x128_splitk");
+    const char* name = "gemm16_mfma_128x128_splitk";
+    switch (kern) {
+    case Kern::DMA128: name = "gemm16_dma_128x128_splitk"; break;
+    case Kern::DMA128R8: name = "gemm16_dma_128x128_ring8_splitk"; break;
+    case Kern::DMA256X128: name = "gemm16_dma_256x128_splitk"; break;
+    case Kern::DMA128X256: name = "gemm16_dma_128x256_splitk"; break;
+    case Kern::DMA256: name = "gemm16_dma_256x256_splitk"; break;
+    default: break;
+    }
+    pl = with_kern(pl, kern, name);
     pl.split = (int)split;
     pl.k_chunk = (int)chunk;
     return true;
@@ -913,6 +921,13 @@ std::vector<Plan> candidate_plans(const tvk_gemm_desc& d) {
             add(with_kern(lay, Kern::DMA256, "gemm16_dma_256x256"));
             add(with_kern(lay, Kern::DMA128X256, "gemm16_dma_128x256"));
             add(with_kern(lay, Kern::DMA256X128, "gemm16_dma_256x128"));
+            // the larger ring tiles split along K too (fewer workgroups fetch each
+            // operand block; more float32 partials)
+            for (Kern k : {Kern::DMA256X128, Kern::DMA128X256, Kern::DMA256})
+                for (int64_t want : {2, 4, 8, 16}) {
+                    Plan p = lay;
+                    if (split_plan(d, want, p, k)) add(p);
+                }
         }
     }
     return out;
