@@ -470,6 +470,7 @@ struct AttnBwdArgs {
     int nqb, BH;       // dQ pass: query tiles per (batch, head), batch * heads
     float scale;
     float c2;          // scale * log2(e)
+    int o_vec;         // out: unit stride along the head dim and 16-byte aligned rows
 };
 
 // 64-bit stores of four consecutive elements along the head dimension
@@ -525,40 +526,6 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs 
     const uint16_t* O = p.out + (int64_t)b * p.so[0] + (int64_t)h * p.so[1];
     const uint16_t* dO = p.dout + (int64_t)b * p.sdo[0] + (int64_t)h * p.sdo[1];
 
-    u32x4 qf[QPW][DS], df[QPW][DS];
-    float lse[QPW], lse2[QPW], dlt[QPW];
-#pragma unroll
-    for (int qt = 0; qt < QPW; ++qt) {
-        const int qi = q0 + 16 * qt + c16;
-        const bool in = qi < p.L;
-        float part = 0.0f;
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-            const int d0 = 32 * ds + 8 * g;
-            qf[qt][ds] = in ? *reinterpret_cast<const u32x4*>(Q + (int64_t)qi * p.sq[2] + d0) : u32x4{0, 0, 0, 0};
-            df[qt][ds] = in ? *reinterpret_cast<const u32x4*>(dO + (int64_t)qi * p.sdo[2] + d0) : u32x4{0, 0, 0, 0};
-            if (in) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint16_t ob = O[(int64_t)qi * p.so[2] + (int64_t)(d0 + e) * p.so[3]];
-                    const uint16_t db = (uint16_t)(df[qt][ds][e / 2] >> (16 * (e % 2)));
-                    part += elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, db)) *
-                            elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, ob));
-                }
-            }
-        }
-        dlt[qt] = lanes4_sum(part);
-        lse[qt] = in ? p.lse[(int64_t)b * p.sl[0] + (int64_t)h * p.sl[1] + (int64_t)qi * p.sl[2]] : INFINITY;
-        lse2[qt] = lse[qt] * AT_LOG2E;
-        if (in && g == 0) p.delta[((int64_t)b * p.Hq + h) * p.L + qi] = dlt[qt];
-    }
-
-    f32x4 acc[DT16][QPW];
-#pragma unroll
-    for (int i = 0; i < DT16; ++i)
-#pragma unroll
-        for (int qt = 0; qt < QPW; ++qt) acc[i][qt] = f32x4{0, 0, 0, 0};
-
     int ntiles = (p.S + AT_BN - 1) / AT_BN;
     if (CAUSAL) {
         const int last_q = min(p.L, qb * BMQ + BMQ) - 1;
@@ -575,6 +542,53 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs 
             vreg[i] = kj < p.S ? *reinterpret_cast<const u32x4*>(V + (int64_t)kj * p.sv[2] + d8) : u32x4{0, 0, 0, 0};
         }
     };
+    // the first key tile is requested before the query side: its latency then
+    // overlaps the q / dout / out loads and delta (the delta store would
+    // otherwise keep the compiler from issuing these loads earlier)
+    if (ntiles > 0) load_tile(0);
+
+    u32x4 qf[QPW][DS], df[QPW][DS];
+    float lse[QPW], lse2[QPW], dlt[QPW];
+#pragma unroll
+    for (int qt = 0; qt < QPW; ++qt) {
+        const int qi = q0 + 16 * qt + c16;
+        const bool in = qi < p.L;
+        float part = 0.0f;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            const int d0 = 32 * ds + 8 * g;
+            qf[qt][ds] = in ? *reinterpret_cast<const u32x4*>(Q + (int64_t)qi * p.sq[2] + d0) : u32x4{0, 0, 0, 0};
+            df[qt][ds] = in ? *reinterpret_cast<const u32x4*>(dO + (int64_t)qi * p.sdo[2] + d0) : u32x4{0, 0, 0, 0};
+            if (in) {
+                uint16_t ob[8];
+                if (p.o_vec) {
+                    const u32x4 ow = *reinterpret_cast<const u32x4*>(O + (int64_t)qi * p.so[2] + d0);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ob[e] = (uint16_t)(ow[e / 2] >> (16 * (e % 2)));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ob[e] = O[(int64_t)qi * p.so[2] + (int64_t)(d0 + e) * p.so[3]];
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint16_t db = (uint16_t)(df[qt][ds][e / 2] >> (16 * (e % 2)));
+                    part += elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, db)) *
+                            elem<DT>::to_f32(__builtin_bit_cast(typename elem<DT>::T, ob[e]));
+                }
+            }
+        }
+        dlt[qt] = lanes4_sum(part);
+        lse[qt] = in ? p.lse[(int64_t)b * p.sl[0] + (int64_t)h * p.sl[1] + (int64_t)qi * p.sl[2]] : INFINITY;
+        lse2[qt] = lse[qt] * AT_LOG2E;
+        if (in && g == 0) p.delta[((int64_t)b * p.Hq + h) * p.L + qi] = dlt[qt];
+    }
+
+    f32x4 acc[DT16][QPW];
+#pragma unroll
+    for (int i = 0; i < DT16; ++i)
+#pragma unroll
+        for (int qt = 0; qt < QPW; ++qt) acc[i][qt] = f32x4{0, 0, 0, 0};
+
     auto store_tile = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
@@ -584,10 +598,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_bwd_dq_kernel(AttnBwdArgs 
             *reinterpret_cast<u32x4*>(&vs[buf][key * LDK + d8]) = vreg[i];
         }
     };
-    if (ntiles > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
+    if (ntiles > 0) store_tile(0);
     __syncthreads();
 
     for (int j = 0; j < ntiles; ++j) {
@@ -1099,6 +1110,7 @@ tvk_status fused_bwd(const tvk_attention_bwd_desc* desc) {
     a.group = (int)(d->heads_q / d->heads_kv);
     a.scale = (float)d->scale;
     a.c2 = a.scale * AT_LOG2E;
+    a.o_vec = rows_ok(d->out, d->out_stride) ? 1 : 0;
     const hipStream_t s = resolve_stream(d->stream);
     Scratch scratch;
     a.delta = static_cast<float*>(scratch.get((size_t)std::max<int64_t>(1, d->batch * d->heads_q * d->len_q) * 4, s));
