@@ -883,6 +883,35 @@ def run_dropin(torch, chains):
         res["c4_block_fwd_bwd_ms"] = round(ms, 4)
         res["c4_vs_conv_chain"] = (round(ms / chains["c4_resnet_conv_fwd_bwd_ms"], 2)
                                    if chains.get("c4_resnet_conv_fwd_bwd_ms") else None)
+        del ws, xi
+        # C3: one transformer layer, 8192 tokens (32 sequences x 256), d 512, 8 query and 2 key/value heads of 64,
+        # fp16, N(0, 0.02) weights: q, k, v projections, causal GQA attention (the fused SDPA), out projection and
+        # residual, gate and up projections multiplied (SwiGLU without its SiLU: no activation is on the path),
+        # down projection and residual; loss = sum in float32. No norms (off the path)
+        Bs, Ls, dm, Hq, Hkv, Dh, Ff = 32, 256, 512, 8, 2, 64, 1536
+
+        def lin(fin, fout):
+            return (torch.randn((fout, fin), generator=g) * 0.02).to(torch.float16).to(V).requires_grad_()
+
+        lw = {"q": lin(dm, Hq * Dh), "k": lin(dm, Hkv * Dh), "v": lin(dm, Hkv * Dh), "o": lin(Hq * Dh, dm),
+              "gate": lin(dm, Ff), "up": lin(dm, Ff), "down": lin(Ff, dm)}
+        xt = torch.randn((Bs * Ls, dm), generator=g).to(torch.float16).to(V)
+
+        def layer_loss():
+            q = F.linear(xt, lw["q"]).view(Bs, Ls, Hq, Dh).transpose(1, 2)
+            k = F.linear(xt, lw["k"]).view(Bs, Ls, Hkv, Dh).transpose(1, 2)
+            v = F.linear(xt, lw["v"]).view(Bs, Ls, Hkv, Dh).transpose(1, 2)
+            a = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+            h = xt + F.linear(a.transpose(1, 2).reshape(Bs * Ls, Hq * Dh), lw["o"])
+            y = h + F.linear(F.linear(h, lw["gate"]) * F.linear(h, lw["up"]), lw["down"])
+            return y.float().sum()
+
+        ms = median_step(list(lw.values()), layer_loss)
+        res["c3_layer_fwd_bwd_ms"] = round(ms, 4)
+        c3_chain = chains.get("c3_llm_layer_gemm_fwd_bwd_ms")
+        res["c3_layer_note"] = ("q/k/v/out/gate/up/down products (k, v at 128 columns each: 2 kv heads) plus the "
+                                "fused causal GQA attention forward and backward; the C-ABI GEMM chain beside it "
+                                f"(c3_llm_layer_gemm_fwd_bwd_ms, k and v at 256 columns) took {c3_chain} ms")
         res["fallbacks"] = 0
         res["note"] = ("median of 10 after 3 (zero_grad, sync, loss.backward(), sync; the reference's time_pass); "
                        "strict mode on, so no op left the device; the C4 block's input needs no gradient, so the "
