@@ -160,6 +160,48 @@ def test_convnd_rejects_wrong_output_size():
     assert lib.tvk_conv_fwd(None) == _abi.TVK_ERR_INVALID
 
 
+@pytest.mark.parametrize("mode,missing", [(0, "x"), (0, "weight"), (1, "y"), (1, "weight"), (2, "x"), (2, "y")])
+def test_conv_rejects_null_inputs(mode, missing):
+    # a direction's inputs must be given: checked before any launch (no GPU needed)
+    lib = _abi.load()
+    fn = (lib.tvk_conv_fwd, lib.tvk_conv_dgrad, lib.tvk_conv_wgrad)[mode]
+    for d in (_convnd(), _conv2(**{})):
+        setattr(d, missing, None)
+        assert fn(C.byref(d)) == _abi.TVK_ERR_INVALID
+        assert b"input pointer is NULL" in lib.tvk_last_error()
+
+
+def _conv2(**kw):
+    import torch
+
+    d = _abi.make_convnd_desc((8, 64, 32, 32), (64, 64, 3, 3), torch.float16, stride=1, padding=1)
+    d.x = d.weight = d.y = 256   # 16-byte aligned, never dereferenced here
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+def test_conv_candidates_without_gpu():
+    import torch
+
+    lib = _abi.load()
+    d = _conv2()
+    for mode in (_abi.TVK_CONV_FWD, _abi.TVK_CONV_DGRAD, _abi.TVK_CONV_WGRAD):
+        names = _abi.conv_candidates(d, mode)
+        # the 3x3 stride-1 layer: the halo kernels first, the implicit GEMM (every problem) last
+        assert names[0] == "conv_halo" and names[-1] == "conv_implicit_gemm" and len(names) >= 2, names
+    f32 = _abi.make_convnd_desc((8, 64, 32, 32), (64, 64, 3, 3), torch.float32, stride=1, padding=1)
+    f32.x = f32.weight = f32.y = 256
+    assert _abi.conv_candidates(f32, _abi.TVK_CONV_FWD) == ["conv_implicit_gemm"]
+    exact = _conv2(flags=_abi.TVK_GEMM_EXACT)
+    assert _abi.conv_candidates(exact, _abi.TVK_CONV_WGRAD) == ["conv_implicit_gemm"]
+    assert _abi.conv_candidates(_convnd(), _abi.TVK_CONV_FWD) == ["conv_implicit_gemm"]   # 3-D
+    buf = C.create_string_buffer(64)
+    assert lib.tvk_conv_candidates(C.byref(d), 3, buf, 64) == _abi.TVK_ERR_INVALID
+    assert lib.tvk_conv_candidates(C.byref(d), 0, buf, 4) == _abi.TVK_ERR_INVALID   # names do not fit
+    assert lib.tvk_conv_choose(C.byref(d), 0, b"no_such_family", 0) == _abi.TVK_ERR_INVALID
+
+
 def test_strict_allocation_switch():
     # the reference's TORCHVULKAN_STRICT_ALLOCATION (src/vulkan/vulkan_context.cpp:248), switchable for the process
     lib = _abi.load()

@@ -721,10 +721,19 @@ uint64_t conv_tune_key(const tvk_conv_desc& d, const std::vector<ConvFamily>& ca
            (uint64_t)unit_dil << 15 | lg(p.M) << 16 | lg(p.N) << 24 | lg(p.K) << 32 | lg(p.taps) << 40;
 }
 
+// The tensors a direction reads must be given (an empty batch reads no x or y).
+template <int MODE>
+bool inputs_given(int64_t n, const void* x, const void* weight, const void* y) {
+    if (MODE == FWD) return (n == 0 || x) && weight;
+    if (MODE == DGRAD) return (n == 0 || y) && weight;
+    return n == 0 || (x && y);
+}
+
 template <int MODE>
 tvk_status run_family(const tvk_conv_desc& d, ConvFamily f, const char* who) {
     ConvArgs p = gemm_args<MODE>(d);
     if (!p.out) return fail(TVK_ERR_INVALID, std::string(who) + ": output pointer is NULL");
+    if (!inputs_given<MODE>(d.n, d.x, d.weight, d.y)) return fail(TVK_ERR_INVALID, std::string(who) + ": an input pointer is NULL");
     if (p.N != 0 && p.M != 0 && p.K != 0) {
         if (f == ConvFamily::SMALL) return conv_small_run(d, MODE, who);
         if (f == ConvFamily::HALO) return conv_halo_run(d, MODE, who);
@@ -889,6 +898,7 @@ tvk_status run_convnd(const tvk_convnd_desc* desc, const char* who) {
     }
     void* out = MODE == FWD ? d.y : MODE == DGRAD ? d.x : d.weight;
     if (!out) return fail(TVK_ERR_INVALID, std::string(who) + ": output pointer is NULL");
+    if (!inputs_given<MODE>(d.n, d.x, d.weight, d.y)) return fail(TVK_ERR_INVALID, std::string(who) + ": an input pointer is NULL");
     ConvArgs p = make_args3(d);
     p.out = out;
     p.has_bias = (MODE == FWD && d.bias) ? 1 : 0;
