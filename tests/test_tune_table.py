@@ -57,9 +57,9 @@ def test_candidate_sets():
     assert "gemm16_mfma_128x128_splitk:16" in candidates(_desc(1024, 1024, 8192))
     # float32 (and exact mode): only the sequential-order kernels
     assert candidates(_desc(1024, 1024, 1024, _abi.TVK_F32)) == [
-        "gemm_seq_mfma_64x64", "gemm_seq_mfma_256x256", "gemm_seq_mfma_128x128", "gemm_seq_mfma_64x128"]
+        "gemm_seq_mfma_64x64", "gemm_seq_mfma_128x128", "gemm_seq_mfma_64x128"]
     assert set(candidates(_desc(512, 512, 512, flags=_abi.TVK_GEMM_EXACT))) == {
-        "gemm_seq_mfma_256x256", "gemm_seq_mfma_128x128", "gemm_seq_mfma_64x128", "gemm_seq_mfma_64x64"}
+        "gemm_seq_mfma_128x128", "gemm_seq_mfma_64x128", "gemm_seq_mfma_64x64"}
     # M <= 16: the streaming kernel first, the tiled kernels after it
     sk = candidates(_desc(16, 14336, 4096))
     assert sk[0] == "gemm16_skinny_ring_splitk" and "gemm16_mfma_128x128" in sk

@@ -621,7 +621,7 @@ __global__ __launch_bounds__(256) void repack16_kernel(const uint16_t* src, uint
 // host dispatch
 // ----------------------------------------------------------------------------
 
-enum class Kern { K0, GENERIC, SEQ256, SEQ128, SEQ64, SEQ16, MFMA256, MFMA256W8, MFMA128, MFMA64, SKINNY, DMA256, DMA128, DMA128R8, DMA128X256, DMA256X128 };
+enum class Kern { K0, GENERIC, SEQ128, SEQ64, SEQ16, MFMA256, MFMA256W8, MFMA128, MFMA64, SKINNY, DMA256, DMA128, DMA128R8, DMA128X256, DMA256X128 };
 
 struct Plan {
     Kern kern;
@@ -805,8 +805,10 @@ Plan make_plan(const tvk_gemm_desc& d) {
     const int64_t t256 = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
     const bool big = d.M >= 256 && d.N >= 256 && t256 >= 192;
     if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
-        pl.kern = big ? Kern::SEQ256 : Kern::SEQ128;
-        pl.name = big ? "gemm_seq_mfma_256x256" : "gemm_seq_mfma_128x128";
+        // 128x128 tiles at every size (a 256x256 variant, four waves of 128x128
+        // float32 accumulators, ran 2.3-8x slower from 2048^3 to 8192^3)
+        pl.kern = Kern::SEQ128;
+        pl.name = "gemm_seq_mfma_128x128";
         // fewer 128x128 tiles than half the CUs: 64x64 tiles of four 16x64 waves,
         // four times the workgroups (same k order; the 64x128 tiles of 2x2 waves
         // of 32x64 stay a kernel-choice candidate)
@@ -890,7 +892,6 @@ std::vector<Plan> candidate_plans(const tvk_gemm_desc& d) {
         out.push_back(p);
     };
     if (d.dtype == TVK_F32 || (d.flags & TVK_GEMM_EXACT)) {
-        add(with_kern(lay, Kern::SEQ256, "gemm_seq_mfma_256x256"));
         add(with_kern(lay, Kern::SEQ128, "gemm_seq_mfma_128x128"));
         add(with_kern(lay, Kern::SEQ64, "gemm_seq_mfma_64x128"));
         add(with_kern(lay, Kern::SEQ16, "gemm_seq_mfma_64x64"));
@@ -1108,16 +1109,14 @@ tvk_status run(const tvk_gemm_desc& d, const Plan& pl, hipStream_t s, char* fixe
             launch_seq16<DT>(pl, q, grid, s);
             break;
         }
-        case Kern::SEQ256:
         case Kern::SEQ128:
         case Kern::SEQ64: {
-            const int TM = pl.kern == Kern::SEQ256 ? 256 : pl.kern == Kern::SEQ128 ? 128 : 64;
-            const int TN = pl.kern == Kern::SEQ256 ? 256 : 128;
+            const int TM = pl.kern == Kern::SEQ128 ? 128 : 64;
+            const int TN = 128;
             q.tiles_m = (int)((d.M + TM - 1) / TM);
             q.tiles_n = (int)((d.N + TN - 1) / TN);
             dim3 grid(q.tiles_m * q.tiles_n, nb);
-            if (TM == 256) launch_seq<DT, 256, 256>(pl, q, grid, s);
-            else if (TM == 128) launch_seq<DT, 128, 128>(pl, q, grid, s);
+            if (TM == 128) launch_seq<DT, 128, 128>(pl, q, grid, s);
             else launch_seq<DT, 64, 128>(pl, q, grid, s);
             break;
         }
