@@ -75,12 +75,12 @@ def test_gemm_validation_codes(field, value, status):
     ((0, 1000, 1), (0, 1000, 1), _abi.TVK_F16, 1000, 1000, 1000, "gemm16_mfma_64x64"),    # 64 tiles of 128^2
     ((0, 4096, 1), (0, 1, 4096), _abi.TVK_F16, 256, 4096, 4096, "gemm16_dma_128x128_splitk"),
     ((0, 1, 512), (0, 512, 1), _abi.TVK_BF16, 512, 512, 8192, "gemm16_dma_128x128_splitk"),
-    ((0, 4096, 1), (0, 1, 4096), _abi.TVK_F16, 256, 10, 4096, "gemm16_mfma_128x128_splitk"),   # 10 columns
+    ((0, 4096, 1), (0, 1, 4096), _abi.TVK_F16, 256, 10, 4096, "gemm16_dma_128x128_splitk"),   # 10 columns
     ((0, 5000, 1), (0, 320, 1), _abi.TVK_F16, 384, 320, 5000, "gemm16_mfma_128x128_splitk"),    # K % 32 != 0
     ((0, 512, 1), (0, 1, 512), _abi.TVK_F16, 4096, 1024, 512, "gemm16_dma_128x128"),      # both k-contiguous, short K
     ((0, 512, 1), (0, 1024, 1), _abi.TVK_F16, 4096, 1024, 512, "gemm16_dma_128x128"),
     ((0, 512, 1), (0, 1024, 1), _abi.TVK_F16, 1024, 1024, 512, "gemm16_mfma_64x64"),      # 64 tiles of 128^2
-    ((0, 512, 1), (0, 1, 512), _abi.TVK_F16, 8192, 3072, 512, "gemm16_dma_256x128"),     # 384 tiles of 256^2: 1.5 rounds
+    ((0, 512, 1), (0, 1, 512), _abi.TVK_F16, 8192, 3072, 512, "gemm16_dma_128x256"),     # 384 tiles of 256^2: 1.5 rounds
     ((0, 3072, 1), (0, 512, 1), _abi.TVK_F16, 8192, 512, 3072, "gemm16_dma_128x128"),
     ((0, 1024, 1), (0, 4096, 1), _abi.TVK_F16, 1024, 4096, 1024, "gemm16_dma_128x128"),   # K < 2048: no split
     ((0, 1, 768), (0, 768, 1), _abi.TVK_F16, 768, 768, 4096, "gemm16_dma_128x128_splitk"),

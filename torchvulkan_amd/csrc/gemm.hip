@@ -821,12 +821,13 @@ Plan make_plan(const tvk_gemm_desc& d) {
     const bool dma_ok = pl.vec && dma_applies(repacked_args(d, pl), pl.ak, pl.bk);
     // 256x256 tiles whose last round on the 256 CUs is at most half full, with
     // few rounds (the transformer's gate_up, 8192x3072x512: 384 tiles, one and
-    // a half rounds): 256x128 tiles, twice as many, whole rounds (38.2-40.5 us
-    // on four boxes, against 41.9-45.8 for 256x256 and 40.1-45.5 for 128x128)
+    // a half rounds; 6144^3: 576 tiles): 128x256 tiles, twice as many, whole
+    // rounds (gate_up 38.2-40.7 us against 41.9-45.8 for 256x256; 6144^3 409
+    // against 449 for 256x128 tiles)
     const bool half_round = t256 < 1024 && t256 % 256 != 0 && t256 % 256 <= 128;
     if (big && dma_ok) {
-        pl.kern = half_round ? Kern::DMA256X128 : Kern::DMA256;
-        pl.name = half_round ? "gemm16_dma_256x128" : "gemm16_dma_256x256";
+        pl.kern = half_round ? Kern::DMA128X256 : Kern::DMA256;
+        pl.name = half_round ? "gemm16_dma_128x256" : "gemm16_dma_256x256";
     } else if (big) {
         // 8 waves; the 4-wave form stays a kernel-choice candidate
         pl.kern = Kern::MFMA256W8;
@@ -839,24 +840,24 @@ Plan make_plan(const tvk_gemm_desc& d) {
         // split K into a power of two of chunks so at least one workgroup per
         // CU runs, chunks of at least 256 k, partials in float32. Below
         // K = 2048 the partials' round trip costs more than the idle CUs.
-        // The LDS-ring kernel takes the split where it applies and the tiles are
-        // whole 128-wide ones (measured 1.2-1.7x on the C2/C3 batch-256 and
-        // weight-gradient products); a 10-column output keeps the
-        // register-staged kernel.
+        // The LDS-ring kernel takes the split where it applies (measured
+        // 1.2-1.7x on the C2/C3 batch-256 and weight-gradient products, 1.08-1.2x
+        // on 10-column, 32-row and 64-row outputs).
         if (t128 < 192 && d.K >= 2048) {
             auto pow2_ceil = [](int64_t v) { int64_t r = 1; while (r < v) r *= 2; return r; };
             auto pow2_floor = [](int64_t v) { int64_t r = 1; while (r * 2 <= v) r *= 2; return r; };
-            const bool dma = pl.vec && d.M >= 128 && d.N >= 128 && dma_applies(repacked_args(d, pl), pl.ak, pl.bk);
+            const bool dma = pl.vec && dma_applies(repacked_args(d, pl), pl.ak, pl.bk);
             if (split_plan(d, std::min<int64_t>({pow2_ceil((256 + t128 - 1) / t128), pow2_floor(d.K / 256), 32}), pl,
                            dma ? Kern::DMA128 : Kern::MFMA128))
                 return pl;
         }
-        if (t128 <= 128) {
+        if (t128 <= 128 && !(dma_ok && d.K >= 1024)) {
             // at most half as many 128x128 tiles as CUs: 64x64 tiles on two
             // waves, four times the workgroups (measured ahead of both 128x128
             // kernels: 1.27-1.49x on 256x4096x784 and 8192x96x512, 64 tiles;
             // 1.05-1.08x on 8192x256x512, 128 tiles, on three boxes; 1.3x on
-            // the per-head attention products, 16 and 32 tiles)
+            // the per-head attention products, 16 and 32 tiles). From K = 1024
+            // the ring's 128x128 tiles lead again (1024^3: 14.4 against 16.0 us)
             pl.kern = Kern::MFMA64;
             pl.name = "gemm16_mfma_64x64";
         } else if (dma_ok) {
@@ -864,6 +865,22 @@ Plan make_plan(const tvk_gemm_desc& d) {
             // register-staged one on 8192 x {512, 256} x 512)
             pl.kern = Kern::DMA128;
             pl.name = "gemm16_dma_128x128";
+            // More than one round of 128x128 tiles at K >= 1024: the tile whose
+            // rounds of 256 workgroups cost least, a 128x128 / 128x256 / 256x256
+            // tile costing 1 : 1.6 : 2.4 (measured at 2560^3, 3072^3, 4096x2048x4096
+            // and 2048x4096x2048: 1.10-1.24x over 128x128 tiles)
+            if (t128 > 256 && d.K >= 1024) {
+                const int64_t t12 = ((d.M + 127) / 128) * ((d.N + 255) / 256) * d.batch;
+                auto rounds = [](int64_t t) { return (double)((t + 255) / 256); };
+                const double c128 = rounds(t128), c12 = 1.6 * rounds(t12), c256 = 2.4 * rounds(t256);
+                if (c256 < c128 && c256 < c12 && d.M >= 256 && d.N >= 256) {
+                    pl.kern = Kern::DMA256;
+                    pl.name = "gemm16_dma_256x256";
+                } else if (c12 < c128 && d.N >= 256) {
+                    pl.kern = Kern::DMA128X256;
+                    pl.name = "gemm16_dma_128x256";
+                }
+            }
         }
     }
     return pl;
