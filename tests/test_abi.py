@@ -91,7 +91,8 @@ def test_gemm_validation_codes(field, value, status):
     ((0, 4096, 1), (0, 1, 4096), _abi.TVK_BF16, 8, 4096, 4096, "gemm16_skinny_bk"),
     ((0, 3, 5), (0, 4, 1), _abi.TVK_F16, 8, 4, 4, "gemm_generic"),
     ((0, 1024, 1), (0, 1024, 1), _abi.TVK_F32, 1024, 1024, 1024, "gemm_seq_mfma_64x64"),
-    ((0, 2048, 1), (0, 2048, 1), _abi.TVK_F32, 2048, 2048, 2048, "gemm_seq_mfma_128x128"),
+    ((0, 2048, 1), (0, 2048, 1), _abi.TVK_F32, 2048, 2048, 2048, "gemm_seq_mfma_64x64"),
+    ((0, 4096, 1), (0, 4096, 1), _abi.TVK_F32, 4096, 4096, 4096, "gemm_seq_mfma_128x128"),
     ((0, 4, 1), (0, 4, 1), _abi.TVK_BF16, 4, 4, 0, "gemm_k0_fill"),
 ])
 def test_gemm_plan_without_gpu(a_stride, b_stride, dtype, M, N, K, want):

@@ -809,10 +809,11 @@ Plan make_plan(const tvk_gemm_desc& d) {
         // float32 accumulators, ran 2.3-8x slower from 2048^3 to 8192^3)
         pl.kern = Kern::SEQ128;
         pl.name = "gemm_seq_mfma_128x128";
-        // fewer 128x128 tiles than half the CUs: 64x64 tiles of four 16x64 waves,
-        // four times the workgroups (same k order; the 64x128 tiles of 2x2 waves
-        // of 32x64 stay a kernel-choice candidate)
-        if (!big && ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch < 128) {
+        // at most one round of 128x128 tiles: 64x64 tiles of four 16x64 waves,
+        // four times the workgroups (same k order; 1024^3 53.7 -> 40.0 us,
+        // 512^3 x 16 53.3 -> 48.2, 4096x1024x1024 91.1 -> 87.4; 2048^3 within 1 %;
+        // the 64x128 tiles of 2x2 waves of 32x64 stay a kernel-choice candidate)
+        if (((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch <= 256) {
             pl.kern = Kern::SEQ16;
             pl.name = "gemm_seq_mfma_64x64";
         }
