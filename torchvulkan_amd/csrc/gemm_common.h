@@ -266,10 +266,16 @@ __device__ void split_fixup(const GemmArgs& p, int b, int m0, int n0, unsigned* 
 #pragma unroll
             for (int u = 0; u < 4; ++u) v = f32x4{v[0] + w[u][0], v[1] + w[u][1], v[2] + w[u][2], v[3] + w[u][3]};
         }
-        for (; z < p.split; ++z) {
+        {
 #pragma clang fp contract(off)
-            const f32x4 w = ld((int64_t)z * total + e);
-            v = f32x4{v[0] + w[0], v[1] + w[1], v[2] + w[2], v[3] + w[3]};
+            f32x4 w[3];
+            const int rem = p.split - z;
+#pragma unroll
+            for (int u = 0; u < 3; ++u)
+                if (u < rem) w[u] = ld((int64_t)(z + u) * total + e);
+#pragma unroll
+            for (int u = 0; u < 3; ++u)
+                if (u < rem) v = f32x4{v[0] + w[u][0], v[1] + w[u][1], v[2] + w[u][2], v[3] + w[u][3]};
         }
         finish4<DT>(p, b, row, col, v, vec);
     }
@@ -295,7 +301,17 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmArgs p) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) v += w[u];
         }
-        for (; z < p.split; ++z) v += p.part[(int64_t)z * total + idx];
+        {
+            // the last planes (fewer than eight): every load issued before the first add
+            float w[7];
+            const int rem = p.split - z;
+#pragma unroll
+            for (int u = 0; u < 7; ++u)
+                if (u < rem) w[u] = p.part[(int64_t)(z + u) * total + idx];
+#pragma unroll
+            for (int u = 0; u < 7; ++u)
+                if (u < rem) v += w[u];
+        }
         store_out<DT>(p, b, (int)(e / p.N), (int)(e % p.N), v);
     }
 }
@@ -322,10 +338,17 @@ __global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(GemmArgs p) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) v = f32x4{v[0] + w[u][0], v[1] + w[u][1], v[2] + w[u][2], v[3] + w[u][3]};
         }
-        for (; z < p.split; ++z) {
+        {
+            // the last planes (fewer than eight): every load issued before the first add
 #pragma clang fp contract(off)
-            const f32x4 w = *reinterpret_cast<const f32x4*>(p.part + (int64_t)z * total + idx);
-            v = f32x4{v[0] + w[0], v[1] + w[1], v[2] + w[2], v[3] + w[3]};
+            f32x4 w[7];
+            const int rem = p.split - z;
+#pragma unroll
+            for (int u = 0; u < 7; ++u)
+                if (u < rem) w[u] = *reinterpret_cast<const f32x4*>(p.part + (int64_t)(z + u) * total + idx);
+#pragma unroll
+            for (int u = 0; u < 7; ++u)
+                if (u < rem) v = f32x4{v[0] + w[u][0], v[1] + w[u][1], v[2] + w[u][2], v[3] + w[u][3]};
         }
         const int b = (int)(idx / mn);
         const int64_t e = idx - (int64_t)b * mn;
