@@ -238,7 +238,17 @@ __global__ __launch_bounds__(256) void reduce_fold_kernel(const Acc* part, RedAr
 #pragma unroll
             for (int u = 0; u < 8; ++u) v += w[u];
         }
-        for (; z < p.splits; ++z) v += part[(int64_t)z * p.nout + o];
+        {
+            // the last chunks (fewer than eight): every load issued before the first add
+            Acc w[7];
+            const int rem = p.splits - z;
+#pragma unroll
+            for (int u = 0; u < 7; ++u)
+                if (u < rem) w[u] = part[(int64_t)(z + u) * p.nout + o];
+#pragma unroll
+            for (int u = 0; u < 7; ++u)
+                if (u < rem) v += w[u];
+        }
         store_acc<Acc>(p.dst + dof * p.db, p.ddt, v);
     }
 }
@@ -263,7 +273,14 @@ __global__ __launch_bounds__(256) void reduce_fold8_kernel(const Acc* part, RedA
 #pragma unroll
             for (int u = 0; u < 8; ++u) v += w[u];
         }
-        for (; z < p.splits; z += 8) v += part[(int64_t)z * p.nout + o];
+        // the last chunks of this group (fewer than eight): every load issued before the first add
+        Acc w[7];
+#pragma unroll
+        for (int u = 0; u < 7; ++u)
+            if (z + 8 * u < p.splits) w[u] = part[(int64_t)(z + 8 * u) * p.nout + o];
+#pragma unroll
+        for (int u = 0; u < 7; ++u)
+            if (z + 8 * u < p.splits) v += w[u];
     }
     red[g][l] = v;
     __syncthreads();
