@@ -520,14 +520,7 @@ __global__ __launch_bounds__(256) void wgrad_ring_reduce_kernel(const float* par
 #pragma unroll
             for (int u = 0; u < 8; ++u) acc += v[u];
         }
-        // the last planes (fewer than eight): every load issued before the first add
-        f32x4 w[7];
-#pragma unroll
-        for (int u = 0; u < 7; ++u)
-            if (s + u * sg < split) w[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)(s + u * sg) * total);
-#pragma unroll
-        for (int u = 0; u < 7; ++u)
-            if (s + u * sg < split) acc += w[u];
+        for (; s < split; s += sg) acc += *reinterpret_cast<const f32x4*>(src + (int64_t)s * total);
     }
     *reinterpret_cast<f32x4*>(red + g * E + l * 4) = acc;
     __syncthreads();

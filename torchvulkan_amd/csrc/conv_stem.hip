@@ -519,14 +519,7 @@ __global__ __launch_bounds__(256) void small_split_reduce_kernel(const float* pa
 #pragma unroll
             for (int u = 0; u < 8; ++u) v += w[u];
         }
-        // the last planes (fewer than eight): every load issued before the first add
-        float w[7];
-#pragma unroll
-        for (int u = 0; u < 7; ++u)
-            if (s + u * sg < split) w[u] = part[(int64_t)(s + u * sg) * count + e];
-#pragma unroll
-        for (int u = 0; u < 7; ++u)
-            if (s + u * sg < split) v += w[u];
+        for (; s < split; s += sg) v += part[(int64_t)s * count + e];
     }
     red[threadIdx.x] = v;
     __syncthreads();
