@@ -274,7 +274,8 @@ typedef struct {
 tvk_status tvk_copy(const tvk_copy_desc* desc);
 
 /* Name of the kernel tvk_copy would launch for `desc` ("memcpy", "cast_contig",
- * "transpose", "strided", or "none" for an empty copy); no launch. */
+ * "transpose", "broadcast" for one source element repeated into a dense
+ * destination, "strided", or "none" for an empty copy); no launch. */
 tvk_status tvk_copy_plan(const tvk_copy_desc* desc, char* name, size_t name_len);
 
 /* Fills every element of a strided destination with one element value.

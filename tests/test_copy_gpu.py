@@ -138,6 +138,29 @@ def test_slices_expands_and_strided_destinations(gpu):
     check_like_torch(torch.randn(64, generator=g).to(DEV), x[:, 7])
 
 
+@pytest.mark.parametrize("sdt", ALL)
+def test_broadcast_scalar_all_pairs(gpu, sdt):
+    """An expanded scalar (stride 0 everywhere) into a dense destination: the broadcast kernel, every dtype
+    pair bit-exact against the cast oracle, with destinations starting off 16-byte alignment and lengths
+    that leave a head and a tail outside the 16-byte stores."""
+    vals = source_values(sdt, 16, 40 + sdt)
+    for i in (2, 5, 14):
+        src_cpu = vals[i:i + 1].reshape(())
+        src = src_cpu.to(DEV)
+        for ddt in ALL:
+            want = orc.cast(storage_np(src_cpu.reshape(1)), sdt, ddt)[0]
+            for n, off in ((37, 0), (37, 3), (4099, 1), (3 * 1024 * 1024 + 5, 0)):
+                if n > 4099 and i != 2:
+                    continue
+                buf = torch.zeros(n + off + 2, dtype=TORCH_OF[ddt], device=DEV)
+                dst = buf[off:off + n].view(n // 1, 1) if n % 2 else buf[off:off + n].view(n // 2, 2)
+                assert run_copy(src.expand(dst.shape), dst) == "broadcast"
+                got = storage_np(buf)
+                assert_bits_equal(got[off:off + n], np.full(n, want, dtype=got.dtype), ddt,
+                                  f"{TORCH_OF[sdt]}->{TORCH_OF[ddt]} n={n} off={off}")
+                assert (got[:off] == 0).all() and (got[off + n:] == 0).all(), "wrote outside the destination"
+
+
 def test_many_dims_empty_and_single(gpu):
     g = torch.Generator().manual_seed(6)
     x = torch.randn((2, 3, 2, 3, 2, 3, 2, 3), generator=g).to(DEV)

@@ -130,6 +130,28 @@ def test_sum_integer_valued_is_exact(gpu, dtype):
     reduce_check(r, [1], out_dtype=out, exact=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_sum_whole_tensor_paths(gpu, dtype):
+    """Whole-tensor sums (a training loss): the 16-byte row kernel over many chunks and the wide fold
+    (one workgroup an output), exact on integers and within the tree bound on random data; and the
+    element-wise row kernel where the 16-byte one does not apply (a source off 16-byte alignment, a row
+    length that is not whole vectors)."""
+    g = torch.Generator().manual_seed(17)
+    out = torch.float32
+    for shape in ((8192, 512), (128, 256, 8, 8), (3, 1 << 21), (16 * 1024 + 8,)):
+        xi = torch.randint(-3, 4, shape, generator=g).to(dtype).to(DEV)
+        reduce_check(xi, list(range(len(shape))), out_dtype=out, exact=True)
+        reduce_check(xi, [len(shape) - 1], out_dtype=out, exact=True)
+    xr = values(dtype, (8192, 512), 18).to(DEV)
+    reduce_check(xr, [0, 1], out_dtype=out)
+    reduce_check(xr, [0, 1])                       # the result in the source dtype
+    base = torch.randint(-3, 4, ((1 << 20) + 1,), generator=g).to(dtype).to(DEV)
+    reduce_check(base[1:], [0], out_dtype=out, exact=True)           # 2 bytes off alignment
+    odd = torch.randint(-3, 4, (5, 100003), generator=g).to(dtype).to(DEV)
+    reduce_check(odd, [1], out_dtype=out, exact=True)                # rows of a partial vector
+    reduce_check(odd, [0, 1], out_dtype=out, exact=True)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
 def test_sum_random_within_bound(gpu, dtype):
     x = values(dtype, (128, 64, 16, 16), 8).to(DEV)

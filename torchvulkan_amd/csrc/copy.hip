@@ -11,8 +11,11 @@
 // value is (src != 0) ? 1 : 0 (src/shaders/ops/cast.slang:29-33).
 //
 // The host plan merges dimensions the way TensorIterator coalesces them
-// (innermost first, by destination strides), then picks one of three kernels:
+// (innermost first, by destination strides), then picks one of four kernels:
 //   cast_contig: both sides dense: 8 elements per thread, vector loads/stores;
+//   broadcast:   a dense destination from one source element (an expanded
+//                scalar, stride 0 everywhere): converted once per thread and
+//                stored 16 bytes at a time;
 //   transpose:   destination contiguous along a dimension the source is not,
 //                source contiguous along another: 64x64 tiles through LDS, so
 //                both the loads and the stores are coalesced (W.t().contiguous(),
@@ -314,7 +317,7 @@ __global__ __launch_bounds__(256) void copy_transpose_reg16_kernel(TransposeArgs
 // host plan
 // ---------------------------------------------------------------------------
 
-enum PlanKind { PK_NONE = 0, PK_MEMCPY, PK_CAST_CONTIG, PK_TRANSPOSE, PK_STRIDED };
+enum PlanKind { PK_NONE = 0, PK_MEMCPY, PK_CAST_CONTIG, PK_TRANSPOSE, PK_STRIDED, PK_BROADCAST };
 
 struct Plan {
     PlanKind kind;
@@ -390,6 +393,11 @@ tvk_status make_plan(const tvk_copy_desc* d, Plan& pl, const char* who) {
         return TVK_OK;
     }
     pl.kind = PK_STRIDED;
+    // one source element repeated into a dense destination (an expanded scalar)
+    if (sh.nd == 1 && sh.ss[0] == 0 && sh.ds[0] == 1 && reinterpret_cast<uintptr_t>(d->dst) % dtype_size(d->dst_dtype) == 0) {
+        pl.kind = PK_BROADCAST;
+        return TVK_OK;
+    }
     if (sh.ds[0] == 1 && sh.ss[0] != 1 && sh.size[0] >= 8) {
         for (int k = 1; k < sh.nd; ++k)
             if (sh.ss[k] == 1 && sh.size[k] >= 8) {
@@ -407,6 +415,7 @@ const char* plan_name(PlanKind k) {
         case PK_MEMCPY: return "memcpy";
         case PK_CAST_CONTIG: return "cast_contig";
         case PK_TRANSPOSE: return "transpose";
+        case PK_BROADCAST: return "broadcast";
         default: return "strided";
     }
 }
@@ -580,7 +589,7 @@ void launch_transpose(const Plan& pl, int sdt, int ddt, const void* src, void* d
 // Dense fill: 16-byte stores of the repeated pattern; the elements before the
 // first 16-byte boundary and after the last are stored one by one.
 template <typename E>
-__global__ __launch_bounds__(256) void fill_contig_kernel(E* dst, int64_t n, int64_t head, E v) {
+__device__ __forceinline__ void fill_body(E* dst, int64_t n, int64_t head, E v) {
     constexpr int PER = 16 / sizeof(E);
     const int64_t step = (int64_t)gridDim.x * 256;
     const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -594,6 +603,53 @@ __global__ __launch_bounds__(256) void fill_contig_kernel(E* dst, int64_t n, int
     for (int64_t i = tid; i < body; i += step) vd[i] = vv;
     const int64_t tail0 = head + body * PER;
     if (tail0 + tid < n) dst[tail0 + tid] = v;
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void fill_contig_kernel(E* dst, int64_t n, int64_t head, E v) {
+    fill_body<E>(dst, n, head, v);
+}
+
+// A copy whose source is one element (stride 0 along every dimension, an
+// expanded scalar) into a dense destination: every thread converts the
+// element and stores it as the fill kernel does.
+template <typename E>
+__global__ __launch_bounds__(256) void broadcast_contig_kernel(const char* src, int sdt, int ddt, E* dst, int64_t n,
+                                                               int64_t head) {
+    alignas(8) char tmp[8];
+    convert(src, sdt, tmp, ddt);
+    E v;
+    __builtin_memcpy(&v, tmp, sizeof(E));
+    fill_body<E>(dst, n, head, v);
+}
+
+// Elements before dst's first 16-byte boundary, and the threads that cover
+// the 16-byte body, the head and the tail.
+template <typename E>
+void dense_fill_geometry(const void* dst, int64_t numel, int64_t& head, int64_t& threads) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(dst);
+    head = std::min<int64_t>((int64_t)(((16 - a % 16) % 16) / sizeof(E)), numel);
+    threads = std::max<int64_t>((numel - head) / (16 / sizeof(E)), std::max<int64_t>(head, 16));
+}
+
+template <typename E>
+void launch_broadcast_t(const char* src, int sdt, int ddt, void* dst, int64_t numel, hipStream_t st) {
+    int64_t head, threads;
+    dense_fill_geometry<E>(dst, numel, head, threads);
+    hipLaunchKernelGGL(broadcast_contig_kernel<E>, dim3(grid_for(threads)), dim3(256), 0, st, src, sdt, ddt,
+                       static_cast<E*>(dst), numel, head);
+}
+
+void launch_broadcast(const Plan& pl, int sdt, int ddt, const void* src, void* dst, hipStream_t st) {
+    const bool same = sdt == ddt && sdt != TVK_BOOL;
+    const int s = same ? raw_dtype(sdt) : sdt, d = same ? raw_dtype(ddt) : ddt;
+    const char* sp = static_cast<const char*>(src);
+    switch (dtype_size(ddt)) {
+        case 8: launch_broadcast_t<uint64_t>(sp, s, d, dst, pl.numel, st); break;
+        case 4: launch_broadcast_t<uint32_t>(sp, s, d, dst, pl.numel, st); break;
+        case 2: launch_broadcast_t<uint16_t>(sp, s, d, dst, pl.numel, st); break;
+        default: launch_broadcast_t<uint8_t>(sp, s, d, dst, pl.numel, st); break;
+    }
 }
 
 template <typename E>
@@ -716,6 +772,9 @@ extern "C" tvk_status tvk_copy(const tvk_copy_desc* desc) {
             break;
         case PK_TRANSPOSE:
             launch_transpose(pl, sdt, ddt, desc->src, desc->dst, s);
+            break;
+        case PK_BROADCAST:
+            launch_broadcast(pl, sdt, ddt, desc->src, desc->dst, s);
             break;
         default:
             launch_strided(pl, sdt, ddt, desc->src, desc->dst, s);

@@ -16,13 +16,15 @@
 // source stride and merged where contiguous, then:
 //   row mode (the source's innermost dimension is reduced): one 256-thread
 //     block per output and K chunk; the threads walk the chunk in memory order,
-//     then a fixed-shape tree in LDS adds their 256 partial sums;
+//     then a fixed-shape tree in LDS adds their 256 partial sums (a float
+//     source over one contiguous dimension: 16-byte loads, four in flight);
 //   column mode (the innermost dimension is kept): one thread per output,
 //     neighbouring threads on neighbouring outputs (coalesced), each adding
 //     its K chunk in order.
 // When the outputs alone cannot fill the device, K is cut into chunks whose
 // partial sums (in the accumulate type) are added by a second pass in chunk
-// order. Every order is fixed, so a sum gives the same bits on every run.
+// order (for a few outputs of many chunks, 256 threads an output and a tree).
+// Every order is fixed, so a sum gives the same bits on every run.
 #include "convert.h"
 
 #include <algorithm>
@@ -169,6 +171,58 @@ __global__ __launch_bounds__(256) void reduce_row_kernel(RedArgs p) {
     }
 }
 
+// Row mode over one contiguous reduced dimension, V = 16/sb elements a
+// 16-byte load: thread t adds vectors t, t + 256, ... of its chunk (four
+// loads in flight), each vector's elements in order; then the same tree as
+// reduce_row_kernel. The chunk and nred are whole vectors.
+template <typename Acc, int SDT>
+__global__ __launch_bounds__(256) void reduce_rowv_kernel(RedArgs p) {
+    constexpr int SB = (int)dtype_size(SDT), V = 16 / SB;
+    struct alignas(16) V16 { char c[16]; };
+    __shared__ Acc red[256];
+    const int z = blockIdx.y;
+    const int64_t r0 = (int64_t)z * p.chunk;
+    const int64_t r1 = r0 + p.chunk < p.nred ? r0 + p.chunk : p.nred;
+    const int64_t nv = (r1 - r0) / V;
+    for (int64_t o = blockIdx.x; o < p.nout; o += gridDim.x) {
+        int64_t so, dof;
+        kept_offsets(p, o, so, dof);
+        const V16* src = reinterpret_cast<const V16*>(p.src + (so + r0) * SB);
+        Acc acc = 0;
+        int64_t v = threadIdx.x;
+        for (; v + 3 * 256 < nv; v += 4 * 256) {
+            V16 w[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) w[u] = src[v + u * 256];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int e = 0; e < V; ++e) acc += load_acc<Acc>(w[u].c + e * SB, SDT);
+        }
+        {
+            // the last vectors (fewer than four): every load issued before the first add
+            V16 w[3];
+#pragma unroll
+            for (int u = 0; u < 3; ++u)
+                if (v + u * 256 < nv) w[u] = src[v + u * 256];
+#pragma unroll
+            for (int u = 0; u < 3; ++u)
+                if (v + u * 256 < nv)
+#pragma unroll
+                    for (int e = 0; e < V; ++e) acc += load_acc<Acc>(w[u].c + e * SB, SDT);
+        }
+        red[threadIdx.x] = acc;
+        __syncthreads();
+#pragma unroll
+        for (int w = 128; w > 0; w >>= 1) {
+            if ((int)threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) put<Acc>(p, o, dof, z, red[0]);
+        __syncthreads();
+    }
+}
+
 template <typename Acc, int SDT>
 __global__ __launch_bounds__(256) void reduce_col_kernel(RedArgs p) {
     const int sdt = SDT == DYN ? p.sdt : SDT;
@@ -294,6 +348,46 @@ __global__ __launch_bounds__(256) void reduce_fold8_kernel(const Acc* part, RedA
     }
 }
 
+// The same sum for few outputs and many splits (a whole tensor summed to one
+// value): one workgroup an output; thread t adds splits t, t + 256, ...
+// (eight loads in flight), then a tree over the 256 thread sums in a fixed
+// order. (The 32-output fold left such a sum to eight threads.)
+template <typename Acc>
+__global__ __launch_bounds__(256) void reduce_foldw_kernel(const Acc* part, RedArgs p) {
+    __shared__ Acc red[256];
+    const int64_t o = blockIdx.x;
+    Acc v = 0;
+    int z = threadIdx.x;
+    for (; z + 7 * 256 < p.splits; z += 8 * 256) {
+        Acc w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w[u] = part[(int64_t)(z + u * 256) * p.nout + o];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v += w[u];
+    }
+    {
+        Acc w[7];
+#pragma unroll
+        for (int u = 0; u < 7; ++u)
+            if (z + u * 256 < p.splits) w[u] = part[(int64_t)(z + u * 256) * p.nout + o];
+#pragma unroll
+        for (int u = 0; u < 7; ++u)
+            if (z + u * 256 < p.splits) v += w[u];
+    }
+    red[threadIdx.x] = v;
+    __syncthreads();
+#pragma unroll
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        int64_t so, dof;
+        kept_offsets(p, o, so, dof);
+        store_acc<Acc>(p.dst + dof * p.db, p.ddt, red[0]);
+    }
+}
+
 // An empty sum: every output is castValue(0), all-zero bytes in every dtype.
 __global__ __launch_bounds__(256) void reduce_zero_kernel(RedArgs p) {
     for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < p.nout; o += (int64_t)gridDim.x * 256) {
@@ -321,16 +415,29 @@ bool colv_applies(const RedArgs& p) {
     return true;
 }
 
+// row mode with 16-byte loads: a float source reduced over one contiguous
+// dimension of whole vectors, every output's row start 16-byte aligned
+bool rowv_applies(const RedArgs& p) {
+    if (p.sdt != TVK_F32 && p.sdt != TVK_F16 && p.sdt != TVK_BF16) return false;
+    const int v = 16 / p.sb;
+    if (p.nr != 1 || p.rss[0] != 1 || p.nred % v != 0 || reinterpret_cast<uintptr_t>(p.src) % 16 != 0) return false;
+    for (int k = 0; k < p.nk; ++k)
+        if ((p.kss[k] * p.sb) % 16 != 0) return false;
+    return true;
+}
+
 template <typename Acc>
 tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
     const bool colv = !row && colv_applies(p);
+    const bool rowv = row && rowv_applies(p);
     const int64_t per_thread = colv ? 16 / p.sb : 1;
     // split K when the outputs alone would leave the device short of blocks
     const int64_t out_blocks = row ? p.nout : (p.nout / per_thread + 255) / 256;
     int64_t splits = 1;
     if (out_blocks < 1024 && p.nred > 1) {
         const int64_t want = (1024 + out_blocks - 1) / out_blocks;
-        const int64_t min_chunk = row ? 4096 : 256;
+        // rowv: four 16-byte loads a thread per chunk
+        const int64_t min_chunk = rowv ? 1024 * (16 / p.sb) : row ? 4096 : 256;
         splits = std::min<int64_t>(want, (p.nred + min_chunk - 1) / min_chunk);
         // a short column reduction over few outputs (a bias gradient, [256, 4096]
         // summed over dim 0: two workgroups) takes chunks of 16 rows instead, so
@@ -339,6 +446,10 @@ tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
         splits = std::max<int64_t>(1, std::min<int64_t>(splits, 65535));
     }
     p.chunk = (p.nred + splits - 1) / splits;
+    if (rowv) {   // whole vectors a chunk
+        const int64_t v = 16 / p.sb;
+        p.chunk = (p.chunk + v - 1) / v * v;
+    }
     splits = (p.nred + p.chunk - 1) / p.chunk;
     p.splits = (int)splits;
     const int ddt = p.ddt;
@@ -357,7 +468,11 @@ tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
         if (row) hipLaunchKernelGGL((reduce_row_kernel<Acc, S>), grid, dim3(256), 0, st, p); \
         else hipLaunchKernelGGL((reduce_col_kernel<Acc, S>), grid, dim3(256), 0, st, p);     \
     } while (0)
-    if (colv) {
+    if (rowv) {
+        if (p.sdt == TVK_F32) hipLaunchKernelGGL((reduce_rowv_kernel<Acc, TVK_F32>), grid, dim3(256), 0, st, p);
+        else if (p.sdt == TVK_F16) hipLaunchKernelGGL((reduce_rowv_kernel<Acc, TVK_F16>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((reduce_rowv_kernel<Acc, TVK_BF16>), grid, dim3(256), 0, st, p);
+    } else if (colv) {
         if (p.sdt == TVK_F32) hipLaunchKernelGGL((reduce_colv_kernel<Acc, TVK_F32>), grid, dim3(256), 0, st, p);
         else if (p.sdt == TVK_F16) hipLaunchKernelGGL((reduce_colv_kernel<Acc, TVK_F16>), grid, dim3(256), 0, st, p);
         else hipLaunchKernelGGL((reduce_colv_kernel<Acc, TVK_BF16>), grid, dim3(256), 0, st, p);
@@ -371,7 +486,8 @@ tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
     if (splits > 1) {
         p.dst = final_dst;
         p.ddt = ddt;
-        if (splits >= 32) hipLaunchKernelGGL(reduce_fold8_kernel<Acc>, dim3((unsigned)((p.nout + 31) / 32)), dim3(256), 0, st, part, p);
+        if (splits >= 256 && p.nout <= 64) hipLaunchKernelGGL(reduce_foldw_kernel<Acc>, dim3((unsigned)p.nout), dim3(256), 0, st, part, p);
+        else if (splits >= 32) hipLaunchKernelGGL(reduce_fold8_kernel<Acc>, dim3((unsigned)((p.nout + 31) / 32)), dim3(256), 0, st, part, p);
         else hipLaunchKernelGGL(reduce_fold_kernel<Acc>, dim3(blocks_for(p.nout, 256)), dim3(256), 0, st, part, p);
     }
     return TVK_OK;
