@@ -388,6 +388,58 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     constexpr int NPASS = D_BM / 64, CPT = 64 * (D_BN / 8) / D_NT;   // passes; chunks per thread per pass
     static_assert(CPT * D_NT == 64 * (D_BN / 8), "whole chunks per thread");
     static_assert(64 * (D_BN + 4) * 4 <= D_NS * D_STB, "epilogue tile fits the ring");
+    // pass `pass`: the waves holding its 64 rows write their accumulators to the LDS tile
+    auto stage_pass = [&](int pass) {
+        if (wm == pass * 64 / D_WTM) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const int i = (pass * 64 % D_WTM) / 16 + ii;
+#pragma unroll
+                for (int j = 0; j < D_FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        et[(ii * 16 + (lane / 16) * 4 + r) * E_LD + wn * D_WTN + j * 16 + lane % 16] = acc[i][j][r];
+            }
+        }
+    };
+    if (plain && vec_c) {
+        // No bias, no activation, 16-byte output rows (the common product):
+        // each element is its sum times alpha, rounded once, as below, in a
+        // loop with no per-element branches. (The general loop spends about
+        // 500 instructions a chunk on the bias and activation variants, and
+        // its code is fetched cold by every workgroup.)
+#pragma unroll
+        for (int pass = 0; pass < NPASS; ++pass) {
+            stage_pass(pass);
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < CPT; ++j) {
+                const int q = tid + j * D_NT;
+                const int rl = q / (D_BN / 8), cc = (q % (D_BN / 8)) * 8;
+                const int row = m0 + pass * 64 + rl, col = n0 + cc;
+                if (row >= p.M || col >= p.N) continue;
+                const f32x4 lo = *reinterpret_cast<const f32x4*>(et + rl * E_LD + cc);
+                const f32x4 hi = *reinterpret_cast<const f32x4*>(et + rl * E_LD + cc + 4);
+                const float a8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                uint16_t h[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+#pragma clang fp contract(off)
+                    const float v = a8[e] * p.alpha;
+                    h[e] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
+                }
+                T* cp = Cb + (int64_t)row * p.sc[1] + col;
+                if (col + 8 <= p.N) {
+                    st_nt(reinterpret_cast<u32x4*>(cp), u32x4{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
+                                                          (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16)});
+                } else {
+                    for (int e = 0; e < 8 && col + e < p.N; ++e) cp[e] = __builtin_bit_cast(T, h[e]);
+                }
+            }
+            __syncthreads();
+        }
+        return;
+    }
     u32x4 bpre[NPASS][CPT];
     if (vec_b) {
 #pragma unroll
@@ -403,17 +455,7 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     }
 #pragma unroll
     for (int pass = 0; pass < NPASS; ++pass) {
-        if (wm == pass * 64 / D_WTM) {
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-                const int i = (pass * 64 % D_WTM) / 16 + ii;
-#pragma unroll
-                for (int j = 0; j < D_FN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        et[(ii * 16 + (lane / 16) * 4 + r) * E_LD + wn * D_WTN + j * 16 + lane % 16] = acc[i][j][r];
-            }
-        }
+        stage_pass(pass);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
