@@ -206,6 +206,45 @@ def test_dma_kernel_128_tiles_batched_epilogue(gpu, dtype):
 
 
 @pytest.mark.parametrize("dtype", F16_TYPES)
+@pytest.mark.parametrize("kernel", ["gemm16_dma_128x128", "gemm16_dma_128x256", "gemm16_dma_256x128", "gemm16_dma_256x256"])
+def test_dma_epilogue_variants_exact(gpu, dtype, kernel):
+    """The LDS-ring kernels' epilogue on integer-valued data, where every result is exact: no bias, a row
+    bias, a full C-in, ReLU and none, alpha 0.5 and beta 2. The output rows hold 256 elements of which
+    N = 250 are the product (a last chunk of two columns), and one C-in has an odd row stride (the
+    per-element path) while the others have 16-byte rows (the select path). Elements past N stay zero."""
+    from torchvulkan_amd import _abi
+    M, N, K = 300, 250, 32
+    a = randint((M, K), dtype, 60, lo=-2, hi=3).to(DEV)
+    w = randint((N, K), dtype, 61, lo=-2, hi=3).to(DEV)
+    cbuf = torch.zeros((M, 256), dtype=dtype, device=DEV)
+    c = cbuf[:, :N]
+    if kernel not in _abi.gemm_candidates(a, w.t(), c):
+        pytest.skip(f"{kernel} is not a candidate for {M}x{N}x{K}")
+    exact = a.double().cpu() @ w.double().cpu().t()
+    biases = [None, randint((N,), dtype, 62, lo=-2, hi=3), randint((M, N), dtype, 63, lo=-2, hi=3),
+              randint((M, N + 1), dtype, 64, lo=-2, hi=3)[:, :N]]
+    for bi, bias in enumerate(biases):
+        for act in (orc.ACT_NONE, orc.ACT_RELU):
+            dbias = None if bias is None else (bias.to(DEV) if bias.is_contiguous() else _device_view(bias))
+            kw = dict(bias=dbias, alpha=0.5, beta=2.0 if bias is not None else 0.0, activation=act)
+            cbuf.zero_()
+            _abi.gemm_choose(a, w.t(), c, kernel, **kw)
+            try:
+                _abi.gemm(a, w.t(), c, **kw)
+                torch.cuda.synchronize()
+                plan = _abi.gemm_plan(a, w.t(), c, **kw)
+            finally:
+                _abi.tune_reset()
+            assert plan == kernel
+            ref = exact * 0.5 + (0.0 if bias is None else 2.0 * bias.double())
+            if act == orc.ACT_RELU:
+                ref = ref.clamp(min=0.0)
+            got = cbuf.cpu()
+            assert torch.equal(got[:, :N].double(), ref.to(dtype).double()), f"bias case {bi}, act {act}"
+            assert (got[:, N:] == 0).all(), "wrote past N"
+
+
+@pytest.mark.parametrize("dtype", F16_TYPES)
 def test_dma_kernel_column_edge_inside_a_chunk(gpu, dtype):
     # N = 3001 of rows strided 3008: the last 16-byte chunk of a B row would
     # straddle N, so the ring kernel declines and another kernel runs
