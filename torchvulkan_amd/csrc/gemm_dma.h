@@ -296,10 +296,54 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     // them before the workgroup's LDS can be handed to another
     wait_vmcnt<0>();
 
+    // The output tile goes through LDS 64 rows a pass (once the ring is free):
+    // the waves holding a pass's rows write their float32 accumulators there
+    // (layout of v_mfma_f32_16x16x32: lane l holds column l % 16, register r
+    // row (l / 16) * 4 + r), E_LD floats a row, and the threads read it back
+    // along the rows.
+    constexpr int E_LD = D_BN + 4;
+    float* const et = reinterpret_cast<float*>(lds_raw);
+    auto stage_pass = [&](int pass) {
+        if (wm == pass * 64 / D_WTM) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const int i = (pass * 64 % D_WTM) / 16 + ii;
+#pragma unroll
+                for (int j = 0; j < D_FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        et[(ii * 16 + (lane / 16) * 4 + r) * E_LD + wn * D_WTN + j * 16 + lane % 16] = acc[i][j][r];
+            }
+        }
+    };
+
     if (p.split > 1) {
-        // float32 partials part[z][batch][M][N] straight from the accumulators
-        // (lane l: column l % 16, register r: row (l / 16) * 4 + r)
+        // float32 partials part[z][batch][M][N]
         float* part = p.part + ((int64_t)blockIdx.z * p.batch + b) * p.M * p.N;
+        if (p.N % 4 == 0 && (reinterpret_cast<uintptr_t>(p.part) & 15) == 0) {
+            // through the LDS tile: 16-byte row chunks a thread (a lane's
+            // accumulators hold four rows of one column; stored directly they
+            // are 4-byte stores, which took 2.1 us a workgroup at 128x128)
+            constexpr int SPASS = D_BM / 64, SCH = 64 * (D_BN / 4) / D_NT;
+            static_assert(SCH * D_NT == 64 * (D_BN / 4), "whole chunks per thread");
+            __syncthreads();   // every wave is done with the ring
+#pragma unroll
+            for (int pass = 0; pass < SPASS; ++pass) {
+                stage_pass(pass);
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < SCH; ++j) {
+                    const int q = tid + j * D_NT;
+                    const int rl = q / (D_BN / 4), cc = (q % (D_BN / 4)) * 4;
+                    const int row = m0 + pass * 64 + rl, col = n0 + cc;
+                    if (row < p.M && col < p.N)
+                        *reinterpret_cast<f32x4*>(part + (int64_t)row * p.N + col) = *reinterpret_cast<const f32x4*>(et + rl * E_LD + cc);
+                }
+                __syncthreads();
+            }
+            return;
+        }
+        // straight from the accumulators
 #pragma unroll
         for (int i = 0; i < D_FM; ++i)
 #pragma unroll
@@ -374,8 +418,6 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     // columns of one row (alpha, bias, activation, one rounding) and stores
     // them with a single 16-byte store where the output rows allow it.
     typedef typename elem<DT>::T T;
-    constexpr int E_LD = D_BN + 4;   // floats per LDS row
-    float* et = reinterpret_cast<float*>(lds_raw);
     T* Cb = reinterpret_cast<T*>(p.c) + c_boff(p, b);
     const T* Bb = p.has_bias ? reinterpret_cast<const T*>(p.bias) + bias_boff(p, b) : nullptr;
     auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
@@ -388,20 +430,6 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     constexpr int NPASS = D_BM / 64, CPT = 64 * (D_BN / 8) / D_NT;   // passes; chunks per thread per pass
     static_assert(CPT * D_NT == 64 * (D_BN / 8), "whole chunks per thread");
     static_assert(64 * (D_BN + 4) * 4 <= D_NS * D_STB, "epilogue tile fits the ring");
-    // pass `pass`: the waves holding its 64 rows write their accumulators to the LDS tile
-    auto stage_pass = [&](int pass) {
-        if (wm == pass * 64 / D_WTM) {
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-                const int i = (pass * 64 % D_WTM) / 16 + ii;
-#pragma unroll
-                for (int j = 0; j < D_FN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        et[(ii * 16 + (lane / 16) * 4 + r) * E_LD + wn * D_WTN + j * 16 + lane % 16] = acc[i][j][r];
-            }
-        }
-    };
     u32x4 bpre[NPASS][CPT];
     if (vec_b) {
 #pragma unroll
