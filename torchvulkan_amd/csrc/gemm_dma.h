@@ -430,6 +430,44 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
     constexpr int NPASS = D_BM / 64, CPT = 64 * (D_BN / 8) / D_NT;   // passes; chunks per thread per pass
     static_assert(CPT * D_NT == 64 * (D_BN / 8), "whole chunks per thread");
     static_assert(64 * (D_BN + 4) * 4 <= D_NS * D_STB, "epilogue tile fits the ring");
+    if (plain && vec_c) {
+        // No bias, no activation, 16-byte output rows (most products): each
+        // element is its sum times alpha, rounded once, as in the general loop
+        // below, with no per-element branches and no bias registers live.
+        // (The general loop spends about 500 instructions a chunk on its
+        // variants, and its code is fetched cold by every workgroup.)
+#pragma unroll
+        for (int pass = 0; pass < NPASS; ++pass) {
+            stage_pass(pass);
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < CPT; ++j) {
+                const int q = tid + j * D_NT;
+                const int rl = q / (D_BN / 8), cc = (q % (D_BN / 8)) * 8;
+                const int row = m0 + pass * 64 + rl, col = n0 + cc;
+                if (row >= p.M || col >= p.N) continue;
+                const f32x4 lo = *reinterpret_cast<const f32x4*>(et + rl * E_LD + cc);
+                const f32x4 hi = *reinterpret_cast<const f32x4*>(et + rl * E_LD + cc + 4);
+                const float a8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                uint16_t h[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+#pragma clang fp contract(off)
+                    const float v = a8[e] * p.alpha;
+                    h[e] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(v));
+                }
+                T* cp = Cb + (int64_t)row * p.sc[1] + col;
+                if (col + 8 <= p.N) {
+                    st_nt(reinterpret_cast<u32x4*>(cp), u32x4{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
+                                                          (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16)});
+                } else {
+                    for (int e = 0; e < 8 && col + e < p.N; ++e) cp[e] = __builtin_bit_cast(T, h[e]);
+                }
+            }
+            __syncthreads();
+        }
+        return;
+    }
     u32x4 bpre[NPASS][CPT];
     if (vec_b) {
 #pragma unroll
@@ -444,12 +482,10 @@ __global__ __launch_bounds__(dma_threads(BM, BN)) void gemm16_dma_kernel(GemmArg
             }
     }
     if (vec_c && p.act != TVK_ACT_GELU && (!p.has_bias || vec_b)) {
-        // 16-byte output rows, no GELU, and no bias or one with 16-byte rows
-        // (the common products): the epilogue of the general loop below
-        // (sum times alpha, plus bias times beta, ReLU, one rounding) with
-        // selects in place of its per-element branches. (The general loop
-        // spends about 500 instructions a chunk on its variants, and its
-        // code is fetched cold by every workgroup.)
+        // 16-byte output rows, no GELU, and a bias with 16-byte rows or ReLU:
+        // the epilogue of the general loop below (sum times alpha, plus bias
+        // times beta, ReLU, one rounding) with selects in place of its
+        // per-element branches
         const bool hb = p.has_bias, relu = p.act == TVK_ACT_RELU;
 #pragma unroll
         for (int pass = 0; pass < NPASS; ++pass) {
