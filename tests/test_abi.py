@@ -218,3 +218,23 @@ def test_strict_allocation_switch():
     assert lib.tvk_host_free(C.c_void_p(16)) == _abi.TVK_ERR_INVALID   # not a tvk_host_malloc block
     p = C.c_int(7)
     assert lib.tvk_host_pointer_pinned(C.c_void_p(16), C.byref(p)) == _abi.TVK_OK and p.value == 0
+
+
+def test_copy_plans_without_gpu():
+    """tvk_copy_plan names the kernel a copy would take (no launch): dense same-dtype and cast copies,
+    a transpose, an expanded scalar into a dense destination (the broadcast fill), and an expanded row
+    (still the strided kernel: its source is not one element)."""
+    import torch
+
+    x = torch.zeros((64, 48), dtype=torch.float16)
+    assert _abi.copy_plan(x, torch.empty((64, 48), dtype=torch.float16)) == "memcpy"
+    assert _abi.copy_plan(x, torch.empty((64, 48), dtype=torch.float32)) == "cast_contig"
+    assert _abi.copy_plan(x.t(), torch.empty((48, 64), dtype=torch.float16)) == "transpose"
+    s = torch.tensor(1.5, dtype=torch.float32)
+    for dt in (torch.float16, torch.float32, torch.bfloat16, torch.int64, torch.bool, torch.uint8):
+        assert _abi.copy_plan(s.expand(300, 7), torch.empty((300, 7), dtype=dt)) == "broadcast", dt
+    wide = torch.empty((300, 8), dtype=torch.float16)
+    assert _abi.copy_plan(s.expand(300, 7), wide[:, :7]) == "strided"      # destination not dense
+    row = torch.zeros((1, 7), dtype=torch.float32)
+    assert _abi.copy_plan(row.expand(300, 7), torch.empty((300, 7))) == "strided"
+    assert _abi.copy_plan(s.expand(0, 7), torch.empty((0, 7))) == "none"
