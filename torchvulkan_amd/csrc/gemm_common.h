@@ -128,6 +128,23 @@ __device__ inline void store_out(const GemmArgs& p, int b, int row, int col, flo
 template <int DT, bool INL = false>
 __device__ inline void store_frag16(const GemmArgs& p, int b, int row0, int col, const f32x16& v) {
     if (col >= p.N) return;
+    if (!p.has_bias && p.act == TVK_ACT_NONE) {
+        // no bias, no activation: each element is its sum times alpha, as in
+        // store_out, with the batch offset computed once for the 16 elements
+        // (per element it cost a scalar division sequence where bh > 1)
+        typedef typename elem<DT>::T T;
+        T* c = reinterpret_cast<T*>(p.c) + c_boff(p, b) + (int64_t)col * p.sc[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = row0 + (r / 4) * 8 + (r % 4);
+            if (row < p.M) {
+#pragma clang fp contract(off)
+                const float o = v[r] * p.alpha;
+                c[(int64_t)row * p.sc[1]] = elem<DT>::from_f32(o);
+            }
+        }
+        return;
+    }
     if (INL && p.has_bias && p.sbias[1] == 0) {
         typedef typename elem<DT>::T T;
         const float bv = elem<DT>::to_f32(reinterpret_cast<const T*>(p.bias)[bias_boff(p, b) + (int64_t)col * p.sbias[2]]);
