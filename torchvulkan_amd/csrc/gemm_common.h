@@ -190,13 +190,14 @@ template <int DT>
 __device__ __forceinline__ void finish4(const GemmArgs& p, int b, int row, int col, f32x4 v, bool vec) {
     typedef typename elem<DT>::T T;
     T* c = reinterpret_cast<T*>(p.c);
-    const T* bias = reinterpret_cast<const T*>(p.bias);
+    // the bias row's address once for the four outputs
+    const T* bp = p.has_bias ? reinterpret_cast<const T*>(p.bias) + bias_boff(p, b) + (int64_t)row * p.sbias[1] + (int64_t)col * p.sbias[2]
+                             : nullptr;
     uint16_t h[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         float bv = 0.0f;
-        if (p.has_bias)
-            bv = elem<DT>::to_f32(bias[bias_boff(p, b) + (int64_t)row * p.sbias[1] + (int64_t)(col + r) * p.sbias[2]]);
+        if (p.has_bias) bv = elem<DT>::to_f32(bp[(int64_t)r * p.sbias[2]]);
         h[r] = __builtin_bit_cast(uint16_t, elem<DT>::from_f32(epilogue(v[r], p.alpha, p.has_bias, bv, p.beta, p.act)));
     }
     T* cp = c + c_boff(p, b) + (int64_t)row * p.sc[1] + (int64_t)col * p.sc[2];
