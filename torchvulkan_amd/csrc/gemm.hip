@@ -584,6 +584,23 @@ __global__ __launch_bounds__(256) void gemm_seq16_kernel(GemmArgs p) {
     }
 
     // register r: block r / 4 (columns 16 (r / 4) ..), row (lane / 16) * 4 + r % 4, column lane % 16
+    if (!p.has_bias && p.act == TVK_ACT_NONE) {
+        // no bias, no activation: alpha times the sum, as store_out computes it,
+        // with the batch offset once for the lane's 16 outputs
+        typedef typename elem<DT>::T T;
+        T* c = reinterpret_cast<T*>(p.c) + c_boff(p, b);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wave * 16 + (lane / 16) * 4 + r % 4;
+            const int col = n0 + (r / 4) * 16 + lane % 16;
+            if (row < p.M && col < p.N) {
+#pragma clang fp contract(off)
+                const float o = acc[r] * p.alpha;
+                c[(int64_t)row * p.sc[1] + (int64_t)col * p.sc[2]] = elem<DT>::from_f32(o);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int row = m0 + wave * 16 + (lane / 16) * 4 + r % 4;
