@@ -152,6 +152,23 @@ def test_sum_whole_tensor_paths(gpu, dtype):
     reduce_check(odd, [0, 1], out_dtype=out, exact=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_sum_short_columns_one_launch(gpu, dtype):
+    """Column sums of at most 1024 rows over few outputs (bias gradients): the one-launch kernel with
+    row groups and a tree, exact on integers and within the tree bound on random data; one reduced
+    dimension made of two merged ones, keepdim, and the result in the source dtype."""
+    g = torch.Generator().manual_seed(19)
+    out = torch.float32
+    for shape, dims in (((256, 4096), [0]), ((1000, 3000), [0]), ((7, 64), [0]), ((3, 256, 40), [0, 1]),
+                        ((1024, 8), [0]), ((33, 520), [0])):
+        xi = torch.randint(-3, 4, shape, generator=g).to(dtype).to(DEV)
+        reduce_check(xi, dims, out_dtype=out, exact=True)
+        reduce_check(xi, dims, keepdim=True, out_dtype=out, exact=True)
+        xr = values(dtype, shape, 20).to(DEV)
+        reduce_check(xr, dims, out_dtype=out)
+        reduce_check(xr, dims)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
 def test_sum_random_within_bound(gpu, dtype):
     x = values(dtype, (128, 64, 16, 16), 8).to(DEV)

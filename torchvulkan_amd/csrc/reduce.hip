@@ -24,11 +24,14 @@
 // When the outputs alone cannot fill the device, K is cut into chunks whose
 // partial sums (in the accumulate type) are added by a second pass in chunk
 // order (for a few outputs of many chunks, 256 threads an output and a tree).
+// A column sum of at most 1024 rows that would be chunked runs in one launch
+// instead: row groups of one workgroup, then a tree over the groups.
 // Every order is fixed, so a sum gives the same bits on every run.
 #include "convert.h"
 
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 
 namespace tvk {
 namespace {
@@ -276,6 +279,64 @@ __global__ __launch_bounds__(256) void reduce_colv_kernel(RedArgs p) {
     }
 }
 
+// Column mode for short reductions (a bias gradient: [256, 4096] summed over
+// the rows) in one launch: a workgroup takes CV = 256 / RG consecutive
+// 16-byte column vectors; thread group g adds rows g, g + RG, ... of its
+// vector in order (eight loads in flight), then the RG group sums are added
+// in a fixed tree through LDS. (The chunked form ran a column kernel over 16
+// row chunks and a second launch to fold them.)
+template <typename Acc, int SDT, int RG>
+__global__ __launch_bounds__(256) void reduce_colw_kernel(RedArgs p) {
+    constexpr int SB = (int)dtype_size(SDT), V = 16 / SB, CV = 256 / RG;
+    struct alignas(16) V16 { char c[16]; };
+    __shared__ Acc red[RG][CV * V + 1];   // + 1: a row's groups on different banks
+    const int v = threadIdx.x % CV, g = threadIdx.x / CV;
+    const int64_t ov = (int64_t)blockIdx.x * CV + v;
+    const bool live = ov < p.nout / V;
+    int64_t so = 0, dof = 0;
+    Acc acc[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[e] = 0;
+    if (live) {
+        kept_offsets(p, ov * V, so, dof);
+        int64_t r = g;
+        for (; r + 7 * RG < p.nred; r += 8 * RG) {
+            V16 w[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[u] = *reinterpret_cast<const V16*>(p.src + (so + red_offset(p, r + u * RG)) * SB);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int e = 0; e < V; ++e) acc[e] += load_acc<Acc>(w[u].c + e * SB, SDT);
+        }
+        {
+            // the last rows (fewer than eight): every load issued before the first add
+            V16 w[7];
+#pragma unroll
+            for (int u = 0; u < 7; ++u)
+                if (r + u * RG < p.nred) w[u] = *reinterpret_cast<const V16*>(p.src + (so + red_offset(p, r + u * RG)) * SB);
+#pragma unroll
+            for (int u = 0; u < 7; ++u)
+                if (r + u * RG < p.nred)
+#pragma unroll
+                    for (int e = 0; e < V; ++e) acc[e] += load_acc<Acc>(w[u].c + e * SB, SDT);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < V; ++e) red[g][v * V + e] = acc[e];
+    __syncthreads();
+#pragma unroll
+    for (int w = RG / 2; w > 0; w >>= 1) {
+        if (g < w)
+#pragma unroll
+            for (int e = 0; e < V; ++e) red[g][v * V + e] = red[g][v * V + e] + red[g + w][v * V + e];
+        __syncthreads();
+    }
+    if (g == 0 && live)
+#pragma unroll
+        for (int e = 0; e < V; ++e) store_acc<Acc>(p.dst + (dof + e * p.kds[0]) * p.db, p.ddt, red[0][v * V + e]);
+}
+
 // dst[o] = sum over z of part[z][o], in z order; neighbouring threads read
 // neighbouring partials, eight chunks in flight per thread
 template <typename Acc>
@@ -433,6 +494,23 @@ tvk_status run_sum(RedArgs& p, bool row, int dev, hipStream_t st) {
     const int64_t per_thread = colv ? 16 / p.sb : 1;
     // split K when the outputs alone would leave the device short of blocks
     const int64_t out_blocks = row ? p.nout : (p.nout / per_thread + 255) / 256;
+    if (colv && out_blocks < 1024 && p.nred <= 1024) {
+        // a short column sum over few outputs: one launch, row groups of a
+        // workgroup (about four rows a thread: 64 groups up to 256 rows)
+        p.splits = 1;
+        p.chunk = p.nred;
+        const int64_t nvec = p.nout / per_thread;
+        auto go = [&](auto rg_c) {
+            constexpr int RG = decltype(rg_c)::value;
+            const dim3 grid((unsigned)((nvec + 256 / RG - 1) / (256 / RG)));
+            if (p.sdt == TVK_F32) hipLaunchKernelGGL((reduce_colw_kernel<Acc, TVK_F32, RG>), grid, dim3(256), 0, st, p);
+            else if (p.sdt == TVK_F16) hipLaunchKernelGGL((reduce_colw_kernel<Acc, TVK_F16, RG>), grid, dim3(256), 0, st, p);
+            else hipLaunchKernelGGL((reduce_colw_kernel<Acc, TVK_BF16, RG>), grid, dim3(256), 0, st, p);
+        };
+        if (p.nred <= 256) go(std::integral_constant<int, 64>{});
+        else go(std::integral_constant<int, 128>{});
+        return TVK_OK;
+    }
     int64_t splits = 1;
     if (out_blocks < 1024 && p.nred > 1) {
         const int64_t want = (1024 + out_blocks - 1) / out_blocks;
