@@ -222,8 +222,8 @@ def test_strict_allocation_switch():
 
 def test_copy_plans_without_gpu():
     """tvk_copy_plan names the kernel a copy would take (no launch): dense same-dtype and cast copies,
-    a transpose, an expanded scalar into a dense destination (the broadcast fill), and an expanded row
-    (still the strided kernel: its source is not one element)."""
+    a transpose, an expanded scalar into a dense destination (the broadcast fill), a permute of outer
+    dimensions with whole 16-byte rows (the rows kernel), and an expanded row of 28 bytes (strided)."""
     import torch
 
     x = torch.zeros((64, 48), dtype=torch.float16)
@@ -236,5 +236,8 @@ def test_copy_plans_without_gpu():
     wide = torch.empty((300, 8), dtype=torch.float16)
     assert _abi.copy_plan(s.expand(300, 7), wide[:, :7]) == "strided"      # destination not dense
     row = torch.zeros((1, 7), dtype=torch.float32)
-    assert _abi.copy_plan(row.expand(300, 7), torch.empty((300, 7))) == "strided"
+    assert _abi.copy_plan(row.expand(300, 7), torch.empty((300, 7))) == "strided"   # 28-byte runs
+    y = torch.zeros((4, 33, 8, 64), dtype=torch.float16)
+    assert _abi.copy_plan(y.transpose(1, 2), torch.empty((4, 8, 33, 64), dtype=torch.float16)) == "rows"
+    assert _abi.copy_plan(y.transpose(1, 2), torch.empty((4, 8, 33, 64), dtype=torch.float32)) != "rows"
     assert _abi.copy_plan(s.expand(0, 7), torch.empty((0, 7))) == "none"

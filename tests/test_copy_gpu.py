@@ -138,6 +138,28 @@ def test_slices_expands_and_strided_destinations(gpu):
     check_like_torch(torch.randn(64, generator=g).to(DEV), x[:, 7])
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32, torch.float64, torch.uint8, torch.int64])
+def test_rows_permute_outer_dimensions(gpu, dtype):
+    """Same-dtype copies whose innermost dimension is contiguous on both sides in whole 16-byte vectors
+    take the rows kernel (a permute of the outer dimensions, an expanded row, a sliced batch, a strided
+    destination), bit-exact against torch's CPU copy_; runs that are not whole vectors, and casts, do
+    not."""
+    g = torch.Generator().manual_seed(21)
+    x = (torch.randn((4, 33, 8, 64), generator=g) * 50).to(dtype).to(DEV)
+    check_like_torch(x.transpose(1, 2), torch.empty((4, 8, 33, 64), dtype=dtype, device=DEV), "rows")
+    check_like_torch(x.permute(2, 0, 1, 3), torch.empty((8, 4, 33, 64), dtype=dtype, device=DEV), "rows")
+    check_like_torch(x[::2].transpose(1, 2), torch.empty((2, 8, 33, 64), dtype=dtype, device=DEV), "rows")
+    row = (torch.randn((1, 128), generator=g) * 50).to(dtype).to(DEV)
+    check_like_torch(row.expand(300, 128), torch.empty((300, 128), dtype=dtype, device=DEV), "rows")
+    big = torch.zeros((33, 4, 8, 2, 64), dtype=dtype, device=DEV)
+    check_like_torch(x.permute(1, 0, 2, 3), big[:, :, :, 0, :], "rows")
+    assert (big[:, :, :, 1, :].cpu() == 0).all(), "wrote outside the view"
+    y = (torch.randn((4, 33, 8, 3), generator=g) * 50).to(dtype).to(DEV)   # 3-element runs
+    check_like_torch(y.transpose(1, 2), torch.empty((4, 8, 33, 3), dtype=dtype, device=DEV), "strided")
+    if dtype != torch.float32:
+        check_like_torch(x.transpose(1, 2), torch.empty((4, 8, 33, 64), dtype=torch.float32, device=DEV))
+
+
 @pytest.mark.parametrize("sdt", ALL)
 def test_broadcast_scalar_all_pairs(gpu, sdt):
     """An expanded scalar (stride 0 everywhere) into a dense destination: the broadcast kernel, every dtype

@@ -11,11 +11,14 @@
 // value is (src != 0) ? 1 : 0 (src/shaders/ops/cast.slang:29-33).
 //
 // The host plan merges dimensions the way TensorIterator coalesces them
-// (innermost first, by destination strides), then picks one of four kernels:
+// (innermost first, by destination strides), then picks one of five kernels:
 //   cast_contig: both sides dense: 8 elements per thread, vector loads/stores;
 //   broadcast:   a dense destination from one source element (an expanded
 //                scalar, stride 0 everywhere): converted once per thread and
 //                stored 16 bytes at a time;
+//   rows:        same dtype, the innermost dimension contiguous on both sides
+//                in whole 16-byte vectors (a permute of outer dimensions): one
+//                16-byte vector per thread;
 //   transpose:   destination contiguous along a dimension the source is not,
 //                source contiguous along another: 64x64 tiles through LDS, so
 //                both the loads and the stores are coalesced (W.t().contiguous(),
@@ -90,6 +93,41 @@ __global__ __launch_bounds__(256) void copy_strided_kernel(StridedArgs p) {
             dof += rem * p.ds[p.nd - 1];
         }
         convert(p.src + so * p.ss_bytes, t.s, p.dst + dof * p.ds_bytes, t.d);
+    }
+}
+
+// Same-dtype copies whose innermost dimension is contiguous on both sides in
+// whole 16-byte vectors (a permute of the outer dimensions, such as
+// [B, L, H, D] -> [B, H, L, D]): one 16-byte vector per thread; the vector
+// index is split into the position inside its run and the run's outer
+// coordinates, whose offsets are in bytes.
+struct RowsArgs {
+    const char* src;
+    char* dst;
+    int nd;                   // outer dimensions (the run dimension excluded)
+    int64_t nvec;             // 16-byte vectors in all
+    Div32 vdiv;               // vectors per run
+    Div32 div[kMaxDims];
+    int64_t size[kMaxDims], ss[kMaxDims], ds[kMaxDims];   // outer extents; strides in bytes
+};
+
+__global__ __launch_bounds__(256) void copy_rows_kernel(RowsArgs p) {
+    const int64_t step = (int64_t)gridDim.x * 256;
+    for (int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x; v < p.nvec; v += step) {
+        uint32_t run = div32((uint32_t)v, p.vdiv);
+        const uint32_t w = (uint32_t)v - run * p.vdiv.d;
+        int64_t so = (int64_t)w * 16, dof = (int64_t)w * 16;
+#pragma unroll 1
+        for (int k = 0; k < p.nd - 1; ++k) {
+            const uint32_t q = div32(run, p.div[k]);
+            const uint32_t c = run - q * p.div[k].d;
+            so += (int64_t)c * p.ss[k];
+            dof += (int64_t)c * p.ds[k];
+            run = q;
+        }
+        so += (int64_t)run * p.ss[p.nd - 1];
+        dof += (int64_t)run * p.ds[p.nd - 1];
+        *reinterpret_cast<u32x4*>(p.dst + dof) = *reinterpret_cast<const u32x4*>(p.src + so);
     }
 }
 
@@ -317,7 +355,7 @@ __global__ __launch_bounds__(256) void copy_transpose_reg16_kernel(TransposeArgs
 // host plan
 // ---------------------------------------------------------------------------
 
-enum PlanKind { PK_NONE = 0, PK_MEMCPY, PK_CAST_CONTIG, PK_TRANSPOSE, PK_STRIDED, PK_BROADCAST };
+enum PlanKind { PK_NONE = 0, PK_MEMCPY, PK_CAST_CONTIG, PK_TRANSPOSE, PK_STRIDED, PK_BROADCAST, PK_ROWS };
 
 struct Plan {
     PlanKind kind;
@@ -398,6 +436,18 @@ tvk_status make_plan(const tvk_copy_desc* d, Plan& pl, const char* who) {
         pl.kind = PK_BROADCAST;
         return TVK_OK;
     }
+    // same dtype, the innermost dimension contiguous on both sides in whole 16-byte vectors,
+    // every run start 16-byte aligned, and a vector index that fits 32 bits
+    if (same && sh.nd >= 2 && sh.ss[0] == 1 && sh.ds[0] == 1) {
+        const int64_t es = (int64_t)dtype_size(d->src_dtype);
+        bool ok = (sh.size[0] * es) % 16 == 0 && reinterpret_cast<uintptr_t>(d->src) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(d->dst) % 16 == 0 && numel * es / 16 < (int64_t(1) << 32);
+        for (int k = 1; k < sh.nd && ok; ++k) ok = (sh.ss[k] * es) % 16 == 0 && (sh.ds[k] * es) % 16 == 0;
+        if (ok) {
+            pl.kind = PK_ROWS;
+            return TVK_OK;
+        }
+    }
     if (sh.ds[0] == 1 && sh.ss[0] != 1 && sh.size[0] >= 8) {
         for (int k = 1; k < sh.nd; ++k)
             if (sh.ss[k] == 1 && sh.size[k] >= 8) {
@@ -416,6 +466,7 @@ const char* plan_name(PlanKind k) {
         case PK_CAST_CONTIG: return "cast_contig";
         case PK_TRANSPOSE: return "transpose";
         case PK_BROADCAST: return "broadcast";
+        case PK_ROWS: return "rows";
         default: return "strided";
     }
 }
@@ -505,6 +556,23 @@ void launch_strided(const Plan& pl, int sdt, int ddt, const void* src, void* dst
         TVK_STRIDED(DYN, DYN);
     }
 #undef TVK_STRIDED
+}
+
+void launch_rows(const Plan& pl, int dt, const void* src, void* dst, hipStream_t st) {
+    const int64_t es = (int64_t)dtype_size(dt);
+    RowsArgs a{};
+    a.src = static_cast<const char*>(src);
+    a.dst = static_cast<char*>(dst);
+    a.nd = pl.sh.nd - 1;
+    a.nvec = pl.numel * es / 16;
+    a.vdiv = make_div((uint32_t)(pl.sh.size[0] * es / 16));
+    for (int k = 0; k < a.nd; ++k) {
+        a.size[k] = pl.sh.size[k + 1];
+        a.ss[k] = pl.sh.ss[k + 1] * es;
+        a.ds[k] = pl.sh.ds[k + 1] * es;
+        a.div[k] = make_div((uint32_t)pl.sh.size[k + 1]);
+    }
+    hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(a.nvec)), dim3(256), 0, st, a);
 }
 
 void launch_transpose(const Plan& pl, int sdt, int ddt, const void* src, void* dst, hipStream_t st) {
@@ -775,6 +843,9 @@ extern "C" tvk_status tvk_copy(const tvk_copy_desc* desc) {
             break;
         case PK_BROADCAST:
             launch_broadcast(pl, sdt, ddt, desc->src, desc->dst, s);
+            break;
+        case PK_ROWS:
+            launch_rows(pl, sdt, desc->src, desc->dst, s);
             break;
         default:
             launch_strided(pl, sdt, ddt, desc->src, desc->dst, s);
